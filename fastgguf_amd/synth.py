@@ -1,0 +1,134 @@
+"""Seeded synthetic GGUF weight blocks and activations, in the reference's file layout.
+
+Byte layouts follow fastgguf.c (lawnak/FastGGUF):
+  Q8_0  34 B / 32 weights   fp16 d @0, int8 q[32] @2                       (fastgguf.c:552-562)
+  Q4_K 144 B / 256 weights  fp16 d @0, fp16 dmin @2, 12 B scales @4, 128 B nibbles @16
+                            (fastgguf.c:622-643; scale unpack scale_min_k4 466-472)
+  Q6_K 210 B / 256 weights  ql[128] @0, qh[64] @128, int8 sc[16] @192, fp16 d @208
+                            (fastgguf.c:669-693)
+Value distributions are the benchmark's: Q4_K nibbles uniform, 6-bit scales and mins uniform in
+[0, 63], d and dmin = fp16(|N(0,1)| * 0.005); Q6_K quant bytes uniform, int8 scales uniform in
+[-64, 63], d = fp16(|N(0,1)| * 0.002); Q8_0 quants uniform in [-127, 127], d = fp16(|N(0,1)| * 0.01).
+fp16 conversion rounds to nearest even (numpy astype).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+T_F32 = 0
+T_Q8_0 = 8
+T_Q4_K = 12
+T_Q6_K = 14
+
+#: (elements per block, bytes per block), block_size_of (fastgguf.c:235-253)
+BLOCK = {T_Q8_0: (32, 34), T_Q4_K: (256, 144), T_Q6_K: (256, 210)}
+TYPE_NAME = {T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q6_K: "Q6_K"}
+
+#: activation blocks, the reference's structs q8_blk_t (743) and q8k_blk_t (771)
+Q8_BLK = np.dtype([("d", "<f4"), ("qs", "i1", 32), ("s16", "<i2", 2)])
+Q8K_BLK = np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bsums", "<i2", 16)])
+assert Q8_BLK.itemsize == 40 and Q8K_BLK.itemsize == 292
+
+
+def row_bytes(type_: int, cols: int) -> int:
+    eb, bb = BLOCK[type_]
+    if cols % eb:
+        raise ValueError(f"{TYPE_NAME[type_]}: cols {cols} is not a multiple of {eb}")
+    return cols // eb * bb
+
+
+def _fp16_abs_normal(rng: np.random.Generator, n: int, scale: float) -> np.ndarray:
+    return (np.abs(rng.standard_normal(n)) * scale).astype(np.float16)
+
+
+def pack_q4k_scales(sc: np.ndarray, mn: np.ndarray) -> np.ndarray:
+    """Inverse of scale_min_k4 (fastgguf.c:466-472): 8 six-bit scales and mins -> 12 bytes."""
+    sc = sc.astype(np.uint8)
+    mn = mn.astype(np.uint8)
+    out = np.empty(sc.shape[:-1] + (12,), np.uint8)
+    for j in range(4):
+        out[..., j] = sc[..., j] | ((sc[..., j + 4] >> 4) << 6)
+        out[..., 4 + j] = mn[..., j] | ((mn[..., j + 4] >> 4) << 6)
+        out[..., 8 + j] = (sc[..., j + 4] & 15) | ((mn[..., j + 4] & 15) << 4)
+    return out
+
+
+def q4_k_weights(rows: int, cols: int, seed: int) -> np.ndarray:
+    """rows x cols Q4_K matrix, returned as uint8 [rows, cols/256*144]."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    nb = rows * (cols // 256)
+    if cols % 256:
+        raise ValueError("Q4_K needs cols % 256 == 0")
+    blk = np.empty((nb, 144), np.uint8)
+    blk[:, 0:2] = _fp16_abs_normal(rng, nb, 0.005).view(np.uint8).reshape(nb, 2)
+    blk[:, 2:4] = _fp16_abs_normal(rng, nb, 0.005).view(np.uint8).reshape(nb, 2)
+    sc = rng.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+    mn = rng.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+    blk[:, 4:16] = pack_q4k_scales(sc, mn)
+    blk[:, 16:144] = rng.integers(0, 256, size=(nb, 128), dtype=np.uint8)
+    return blk.reshape(rows, -1)
+
+
+def q6_k_weights(rows: int, cols: int, seed: int) -> np.ndarray:
+    """rows x cols Q6_K matrix, returned as uint8 [rows, cols/256*210]."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    if cols % 256:
+        raise ValueError("Q6_K needs cols % 256 == 0")
+    nb = rows * (cols // 256)
+    blk = np.empty((nb, 210), np.uint8)
+    blk[:, 0:192] = rng.integers(0, 256, size=(nb, 192), dtype=np.uint8)
+    blk[:, 192:208] = rng.integers(-64, 64, size=(nb, 16), dtype=np.int8).view(np.uint8)
+    blk[:, 208:210] = _fp16_abs_normal(rng, nb, 0.002).view(np.uint8).reshape(nb, 2)
+    return blk.reshape(rows, -1)
+
+
+def q8_0_weights(rows: int, cols: int, seed: int) -> np.ndarray:
+    """rows x cols Q8_0 matrix, returned as uint8 [rows, cols/32*34]."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    if cols % 32:
+        raise ValueError("Q8_0 needs cols % 32 == 0")
+    nb = rows * (cols // 32)
+    blk = np.empty((nb, 34), np.uint8)
+    blk[:, 0:2] = _fp16_abs_normal(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)
+    blk[:, 2:34] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
+    return blk.reshape(rows, -1)
+
+
+def weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    if type_ == T_Q4_K:
+        return q4_k_weights(rows, cols, seed)
+    if type_ == T_Q6_K:
+        return q6_k_weights(rows, cols, seed)
+    if type_ == T_Q8_0:
+        return q8_0_weights(rows, cols, seed)
+    raise ValueError(f"unsupported type {type_}")
+
+
+def random_bytes_weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """Uniform random bytes with sane fp16 scales, as the reference selftest builds its rows
+    (fastgguf.c:5701-5710): d in 0x2C00..0x2FFF, dmin in 0x2400..0x27FF."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    eb, bb = BLOCK[type_]
+    nb = rows * (cols // eb)
+    blk = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    d = (0x2C00 + rng.integers(0, 0x400, size=nb)).astype(np.uint16)
+    dm = (0x2400 + rng.integers(0, 0x400, size=nb)).astype(np.uint16)
+    if type_ == T_Q6_K:
+        blk[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    else:
+        blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        if type_ == T_Q4_K:
+            blk[:, 2:4] = dm.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(rows, -1)
+
+
+def activations(n: int, seed: int, rows: int | None = None) -> np.ndarray:
+    """fp32 N(0, 1) activations: shape [n] or [rows, n]."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    shape = (n,) if rows is None else (rows, n)
+    return rng.standard_normal(shape).astype(np.float32)
+
+
+def router_logits(n_tok: int, n_expert: int, seed: int) -> np.ndarray:
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return rng.standard_normal((n_tok, n_expert)).astype(np.float32)

@@ -1,0 +1,593 @@
+/*
+ * fg_oracle.c - CPU restatement of fastgguf's quantized weight x Q8-activation hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker for the HIP backend (see fg_oracle.h). It is
+ * never linked into, called by, or used as a fallback of the product library.
+ *
+ * Written from the reference's formulas; each function cites the fastgguf.c lines it restates.
+ * The reference's SIMD kernels keep several fp32 accumulator lanes; this file keeps the same
+ * lanes as plain arrays and combines them in the same order, so results are bit-identical to
+ * the reference's AVX2 / AVX-VNNI / AVX-512-VNNI builds:
+ *   hsum8(v) = ((v0+v4)+(v1+v5)) + ((v2+v6)+(v3+v7))   (hsum_ps, fastgguf.c:797-806)
+ *   hsum4(v) = (v0+v1) + (v2+v3)                         (hsum128_ps, fastgguf.c:1089-1095)
+ * Compile with -ffp-contract=off: every fused multiply-add below is an explicit fmaf, exactly
+ * where the reference uses _mm256_fmadd_ps / _mm256_fnmadd_ps.
+ *
+ * Parity pins (tests/test_oracle.py): golden vectors written by the compiled reference
+ * (tests/golden/), closed-form checks of the quantizers (IEEE division, round-half-even), brute
+ * force integer sums over dequantized codes, and the reference selftest relations.
+ */
+#include "fg_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- fp16 -> fp32, exact including subnormals (fp16_to_float_sw, fastgguf.c:96-117) ---- */
+float fgo_fp16(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t ex = (h >> 10) & 0x1fu, man = h & 0x3ffu, f;
+    if (ex == 0) {
+        if (man == 0) {
+            f = sign;
+        } else { /* subnormal: renormalise */
+            int e = -1;
+            do { man <<= 1; e++; } while (!(man & 0x400u));
+            f = sign | ((uint32_t)(127 - 15 - e) << 23) | ((man & 0x3ffu) << 13);
+        }
+    } else if (ex == 31) {
+        f = sign | 0x7f800000u | (man << 13);
+    } else {
+        f = sign | ((ex + 127 - 15) << 23) | (man << 13);
+    }
+    float out;
+    memcpy(&out, &f, 4);
+    return out;
+}
+
+static inline uint16_t rd16(const uint8_t *p) { uint16_t v; memcpy(&v, p, 2); return v; }
+
+static inline float hsum8(const float v[8]) {
+    return ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+}
+static inline float hsum4(const float v[4]) { return (v[0] + v[1]) + (v[2] + v[3]); }
+
+/* ---- activation quantizers ---- */
+
+/* quantize_q8 (fastgguf.c:746-768): per 32 values d = amax/127, q = lrintf(x/d), two 16-sums */
+void fgo_quantize_q8(const float *x, fgo_q8_blk *out, int n) {
+    for (int b = 0; b < n / 32; b++) {
+        const float *xb = x + b * 32;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; j++) {
+            float a = fabsf(xb[j]);
+            if (a > amax) amax = a;
+        }
+        float d = amax / 127.0f;
+        float id = d > 0.0f ? 1.0f / d : 0.0f;
+        out[b].d = d;
+        int s0 = 0, s1 = 0;
+        for (int j = 0; j < 32; j++) {
+            int8_t q = (int8_t)lrintf(xb[j] * id);
+            out[b].qs[j] = q;
+            if (j < 16) s0 += q; else s1 += q;
+        }
+        out[b].s16[0] = (int16_t)s0;
+        out[b].s16[1] = (int16_t)s1;
+    }
+}
+
+/* quantize_q8k (fastgguf.c:773-793): one d per 256 values, sums of every 16 quants */
+void fgo_quantize_q8k(const float *x, fgo_q8k_blk *out, int n) {
+    for (int b = 0; b < n / 256; b++) {
+        const float *xb = x + b * 256;
+        float amax = 0.0f;
+        for (int j = 0; j < 256; j++) {
+            float a = fabsf(xb[j]);
+            if (a > amax) amax = a;
+        }
+        float d = amax / 127.0f, id = d > 0.0f ? 1.0f / d : 0.0f;
+        out[b].d = d;
+        for (int g = 0; g < 16; g++) {
+            int s = 0;
+            for (int j = 0; j < 16; j++) {
+                int v = (int)lrintf(xb[16 * g + j] * id);
+                out[b].qs[16 * g + j] = (int8_t)v;
+                s += v;
+            }
+            out[b].bsums[g] = (int16_t)s;
+        }
+    }
+}
+
+/* ---- Q4_K scale/min unpack (scale_min_k4, fastgguf.c:466-472) ---- */
+static inline void q4k_scales(const uint8_t *s12, uint8_t sc[8], uint8_t mn[8]) {
+    for (int j = 0; j < 8; j++) {
+        if (j < 4) {
+            sc[j] = s12[j] & 63;
+            mn[j] = s12[j + 4] & 63;
+        } else {
+            sc[j] = (uint8_t)((s12[j + 4] & 0x0F) | ((s12[j - 4] >> 6) << 4));
+            mn[j] = (uint8_t)((s12[j + 4] >> 4) | ((s12[j] >> 6) << 4));
+        }
+    }
+}
+
+/* Q6_K value of element e (0..255) of a block (fastgguf.c:676-690); 0..63, offset 32 not removed */
+static inline int q6k_val(const uint8_t *p, int e) {
+    int h = e >> 7, r = e & 127, k = r >> 5, l = r & 31;
+    const uint8_t *ql = p + 64 * h, *qh = p + 128 + 32 * h;
+    int lo = (k & 1) ? ql[l + 32] : ql[l];
+    lo = (k & 2) ? (lo >> 4) : (lo & 0x0F);
+    int hi = (qh[l] >> (2 * k)) & 3;
+    return lo | (hi << 4);
+}
+
+/* ---- B-1: dot_q8_0_q8 (fastgguf.c:891-902) ----
+ * lane i of block b: s_i = sum_{t=4i}^{4i+3} w_t x_t;  acc_i = fma(FP16(d)*xd, s_i, acc_i) */
+float fgo_dot_q8_0(const uint8_t *row, const fgo_q8_blk *xq, int nb) {
+    float acc[8] = {0};
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *p = row + (size_t)b * 34;
+        const int8_t *w = (const int8_t *)(p + 2);
+        float d = fgo_fp16(rd16(p)) * xq[b].d;
+        for (int i = 0; i < 8; i++) {
+            int s = 0;
+            for (int t = 4 * i; t < 4 * i + 4; t++) s += (int)w[t] * xq[b].qs[t];
+            acc[i] = fmaf(d, (float)s, acc[i]);
+        }
+    }
+    return hsum8(acc);
+}
+
+/* ---- B-2: dot_q4_K_q8k (fastgguf.c:1118-1153) ----
+ * lane i: sum_j [sc_2j * sum_{t=4i}^{4i+3} lo(32j+t) y(64j+t) + sc_2j+1 * sum hi(32j+t) y(64j+32+t)]
+ * min lane p: m_2p (bs_4p + bs_4p+1) + m_2p+1 (bs_4p+2 + bs_4p+3)   (k4_min_vec, 1078-1082) */
+float fgo_dot_q4_K(const uint8_t *row, const fgo_q8k_blk *y, int nb) {
+    float acc[8] = {0}, macc[4] = {0};
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *p = row + (size_t)b * 144, *qs = p + 16;
+        const int8_t *q8 = y[b].qs;
+        uint8_t sc[8], mn[8];
+        q4k_scales(p + 4, sc, mn);
+        float yd = y[b].d;
+        float dd = fgo_fp16(rd16(p)) * yd, dm = fgo_fp16(rd16(p + 2)) * yd;
+        for (int i = 0; i < 8; i++) {
+            int lane = 0;
+            for (int j = 0; j < 4; j++) {
+                int il = 0, ih = 0;
+                for (int t = 4 * i; t < 4 * i + 4; t++) {
+                    il += (qs[32 * j + t] & 0x0F) * q8[64 * j + t];
+                    ih += (qs[32 * j + t] >> 4) * q8[64 * j + 32 + t];
+                }
+                lane += sc[2 * j] * il + sc[2 * j + 1] * ih;
+            }
+            acc[i] = fmaf(dd, (float)lane, acc[i]);
+        }
+        for (int pp = 0; pp < 4; pp++) {
+            const int16_t *bs = y[b].bsums;
+            int s0 = bs[4 * pp] + bs[4 * pp + 1], s1 = bs[4 * pp + 2] + bs[4 * pp + 3];
+            int ml = mn[2 * pp] * s0 + mn[2 * pp + 1] * s1;
+            macc[pp] = fmaf(dm, (float)ml, macc[pp]);
+        }
+    }
+    return hsum8(acc) - hsum4(macc);
+}
+
+/* per-block Q4_K integers */
+static void q4k_block_ints(const uint8_t *p, const fgo_q8k_blk *yb, int32_t *sumi, int32_t *msum) {
+    const uint8_t *qs = p + 16;
+    uint8_t sc[8], mn[8];
+    q4k_scales(p + 4, sc, mn);
+    int s = 0, m = 0;
+    for (int j = 0; j < 4; j++) {
+        int il = 0, ih = 0;
+        for (int l = 0; l < 32; l++) {
+            il += (qs[32 * j + l] & 0x0F) * yb->qs[64 * j + l];
+            ih += (qs[32 * j + l] >> 4) * yb->qs[64 * j + 32 + l];
+        }
+        s += sc[2 * j] * il + sc[2 * j + 1] * ih;
+    }
+    for (int j = 0; j < 8; j++) m += mn[j] * (yb->bsums[2 * j] + yb->bsums[2 * j + 1]);
+    *sumi = s;
+    *msum = m;
+}
+
+/* ---- B-3: dot_q4Kx8 (fastgguf.c:2322-2358), the 8-row repacked kernel, one row of it ----
+ * per block: sumi, msum (whole-block integers); acc = fma(d*yd, sumi, acc);
+ * macc = fma(dmin*yd, msum, macc); result acc - macc. The repack (2268-2282) moves bytes only. */
+float fgo_dot_q4_K_rp(const uint8_t *row, const fgo_q8k_blk *y, int nb) {
+    float acc = 0.0f, macc = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *p = row + (size_t)b * 144;
+        int32_t sumi, msum;
+        q4k_block_ints(p, &y[b], &sumi, &msum);
+        float yd = y[b].d;
+        acc = fmaf(fgo_fp16(rd16(p)) * yd, (float)sumi, acc);
+        macc = fmaf(fgo_fp16(rd16(p + 2)) * yd, (float)msum, macc);
+    }
+    return acc - macc;
+}
+
+/* ---- B-4: dot_q6_K_q8k (fastgguf.c:1232-1264) ----
+ * lane i: sum_{h,k} sc[8h+2k+(i>=4)] * sum_{t=4i}^{4i+3} q(128h+32k+t) y(128h+32k+t)
+ * correction lane p (q6_corr_vec, 1085-1088):
+ *   (sc_2p bs_2p + sc_2p+1 bs_2p+1) + (sc_2p+8 bs_2p+8 + sc_2p+9 bs_2p+9)
+ * acc_i = fma(dd, lane_i, acc_i); cacc_p = fma(32*dd, corr_p, cacc_p); hsum8(acc) - hsum4(cacc) */
+float fgo_dot_q6_K(const uint8_t *row, const fgo_q8k_blk *y, int nb) {
+    float acc[8] = {0}, cacc[4] = {0};
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *p = row + (size_t)b * 210;
+        const int8_t *sc = (const int8_t *)(p + 192);
+        float dd = fgo_fp16(rd16(p + 208)) * y[b].d;
+        const int8_t *q8 = y[b].qs;
+        for (int i = 0; i < 8; i++) {
+            int lane = 0;
+            for (int h = 0; h < 2; h++)
+                for (int k = 0; k < 4; k++) {
+                    int s = 0;
+                    for (int t = 4 * i; t < 4 * i + 4; t++) {
+                        int e = 128 * h + 32 * k + t;
+                        s += q6k_val(p, e) * q8[e];
+                    }
+                    lane += sc[8 * h + 2 * k + (i >= 4)] * s;
+                }
+            acc[i] = fmaf(dd, (float)lane, acc[i]);
+        }
+        const int16_t *bs = y[b].bsums;
+        for (int pp = 0; pp < 4; pp++) {
+            int c = (sc[2 * pp] * bs[2 * pp] + sc[2 * pp + 1] * bs[2 * pp + 1]) +
+                    (sc[2 * pp + 8] * bs[2 * pp + 8] + sc[2 * pp + 9] * bs[2 * pp + 9]);
+            cacc[pp] = fmaf(dd * 32.0f, (float)c, cacc[pp]);
+        }
+    }
+    return hsum8(acc) - hsum4(cacc);
+}
+
+void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
+                    int32_t *sumi, int32_t *msum) {
+    for (int b = 0; b < nb; b++) {
+        if (type == FGO_T_Q4_K) {
+            q4k_block_ints(row + (size_t)b * 144, (const fgo_q8k_blk *)act + b, &sumi[b], &msum[b]);
+        } else if (type == FGO_T_Q6_K) {
+            const uint8_t *p = row + (size_t)b * 210;
+            const int8_t *sc = (const int8_t *)(p + 192);
+            const fgo_q8k_blk *yb = (const fgo_q8k_blk *)act + b;
+            int s = 0, m = 0;
+            for (int g = 0; g < 16; g++) {
+                int ig = 0;
+                for (int l = 0; l < 16; l++) ig += q6k_val(p, 16 * g + l) * yb->qs[16 * g + l];
+                s += sc[g] * ig;
+                m += sc[g] * yb->bsums[g];
+            }
+            sumi[b] = s;
+            msum[b] = m;
+        } else { /* Q8_0 */
+            const uint8_t *p = row + (size_t)b * 34;
+            const fgo_q8_blk *xb = (const fgo_q8_blk *)act + b;
+            int s = 0;
+            for (int t = 0; t < 32; t++) s += (int)(int8_t)p[2 + t] * xb->qs[t];
+            sumi[b] = s;
+            msum[b] = 0;
+        }
+    }
+}
+
+/* ---- dequantize_row (fastgguf.c:552-562, 622-643, 669-693) ---- */
+int fgo_dequantize_row(uint32_t type, const uint8_t *raw, float *out, int n) {
+    if (type == FGO_T_Q8_0) {
+        for (int b = 0; b < n / 32; b++) {
+            const uint8_t *p = raw + (size_t)b * 34;
+            float d = fgo_fp16(rd16(p));
+            for (int j = 0; j < 32; j++) out[32 * b + j] = d * (float)(int8_t)p[2 + j];
+        }
+        return 0;
+    }
+    if (type == FGO_T_Q4_K) {
+        for (int b = 0; b < n / 256; b++) {
+            const uint8_t *p = raw + (size_t)b * 144;
+            float d = fgo_fp16(rd16(p)), dmin = fgo_fp16(rd16(p + 2));
+            uint8_t sc[8], mn[8];
+            q4k_scales(p + 4, sc, mn);
+            for (int j = 0; j < 4; j++) {
+                float d1 = d * sc[2 * j], m1 = dmin * mn[2 * j];
+                float d2 = d * sc[2 * j + 1], m2 = dmin * mn[2 * j + 1];
+                for (int l = 0; l < 32; l++) {
+                    uint8_t q = p[16 + 32 * j + l];
+                    out[256 * b + 64 * j + l] = d1 * (float)(q & 0x0F) - m1;
+                    out[256 * b + 64 * j + 32 + l] = d2 * (float)(q >> 4) - m2;
+                }
+            }
+        }
+        return 0;
+    }
+    if (type == FGO_T_Q6_K) {
+        for (int b = 0; b < n / 256; b++) {
+            const uint8_t *p = raw + (size_t)b * 210;
+            const int8_t *sc = (const int8_t *)(p + 192);
+            float d = fgo_fp16(rd16(p + 208));
+            for (int e = 0; e < 256; e++)
+                out[256 * b + e] = d * (float)sc[e / 16] * (float)(q6k_val(p, e) - 32);
+        }
+        return 0;
+    }
+    return -1;
+}
+
+int fgo_block_size(uint32_t type, int *elems, int *bytes) {
+    switch (type) {
+    case FGO_T_Q8_0: *elems = 32; *bytes = 34; return 0;
+    case FGO_T_Q4_K: *elems = 256; *bytes = 144; return 0;
+    case FGO_T_Q6_K: *elems = 256; *bytes = 210; return 0;
+    default: return -1;
+    }
+}
+
+/* ---- dot_row dispatch for the three types (fastgguf.c:2183-2201) ---- */
+static float dot_row3(uint32_t type, int order, const uint8_t *rb, const void *act, int cols) {
+    if (type == FGO_T_Q4_K)
+        return order == FGO_ORDER_REPACKED ? fgo_dot_q4_K_rp(rb, (const fgo_q8k_blk *)act, cols / 256)
+                                           : fgo_dot_q4_K(rb, (const fgo_q8k_blk *)act, cols / 256);
+    if (type == FGO_T_Q6_K) return fgo_dot_q6_K(rb, (const fgo_q8k_blk *)act, cols / 256);
+    return fgo_dot_q8_0(rb, (const fgo_q8_blk *)act, cols / 32);
+}
+
+static int type_ok(uint32_t type, int cols) {
+    if (type == FGO_T_Q4_K || type == FGO_T_Q6_K) return cols > 0 && cols % 256 == 0;
+    if (type == FGO_T_Q8_0) return cols > 0 && cols % 32 == 0;
+    return 0;
+}
+
+/* quantize one activation vector for the type (type_uses_q8 2167 + quantize_act 2176);
+ * returns a malloc'd buffer, NULL on failure */
+static void *quantize_for(uint32_t type, const float *x, int cols) {
+    if (type == FGO_T_Q8_0) {
+        fgo_q8_blk *q = (fgo_q8_blk *)malloc((size_t)(cols / 32) * sizeof(fgo_q8_blk));
+        if (q) fgo_quantize_q8(x, q, cols);
+        return q;
+    }
+    fgo_q8k_blk *q = (fgo_q8k_blk *)malloc((size_t)(cols / 256) * sizeof(fgo_q8k_blk));
+    if (q) fgo_quantize_q8k(x, q, cols);
+    return q;
+}
+
+static size_t act_bytes(uint32_t type, int cols) {
+    return type == FGO_T_Q8_0 ? (size_t)(cols / 32) * sizeof(fgo_q8_blk)
+                              : (size_t)(cols / 256) * sizeof(fgo_q8k_blk);
+}
+
+/* matvec (fastgguf.c:2575-2622) and matvec_rp (2540-2545): rows are independent, so the row
+ * order of the OpenMP loop does not change any value */
+int fgo_matvec(uint32_t type, int order, const uint8_t *w, int64_t rows, int cols,
+               const float *x, float *y) {
+    if (!type_ok(type, cols)) return -1;
+    int eb, bb;
+    fgo_block_size(type, &eb, &bb);
+    size_t stride = (size_t)(cols / eb) * bb;
+    void *act = quantize_for(type, x, cols);
+    if (!act) return -1;
+#pragma omp parallel for schedule(guided, 32)
+    for (int64_t r = 0; r < rows; r++) y[r] = dot_row3(type, order, w + (size_t)r * stride, act, cols);
+    free(act);
+    return 0;
+}
+
+/* ---- B-5: gemmk_kern (fastgguf.c:2756-2797) for Q4_K (GS = MS = 32) and Q6_K (16/16) ----
+ * per (row, token) and block b:  a = 0
+ *   for g: a = fma(wsc_g, ia_g, a)          wsc_g = FP16(d)*sc_g  (Q6_K: FP16(d)*sc_g)
+ *   for g: a = fnmadd(wmn_g, bs_g, a)       wmn_g = FP16(dmin)*m_g (Q6_K: 32*FP16(d)*sc_g)
+ *   f = fma(a, yd_b, f)
+ * ---- and gemm32_kern (2909-2937) for Q8_0 (unpack_row_q32 2876-2894, gemm_pack_q8 2897-2913):
+ *   per 32-block g: a = fma(d*xd, ia'_g, a); a = fnmadd(128*d, xd*(s16_0+s16_1), a)
+ *   with ia' = sum (w+128)*x (the unsigned weight the VNNI kernel multiplies) */
+static void gemm_row_token(uint32_t type, const uint8_t *rb, const void *act, int cols, float *out) {
+    if (type == FGO_T_Q8_0) {
+        const fgo_q8_blk *xq = (const fgo_q8_blk *)act;
+        float acc = 0.0f;
+        for (int g = 0; g < cols / 32; g++) {
+            const uint8_t *p = rb + (size_t)g * 34;
+            float d = fgo_fp16(rd16(p));
+            int ia = 0;
+            for (int t = 0; t < 32; t++) ia += ((int)(int8_t)p[2 + t] + 128) * xq[g].qs[t];
+            float ws = d * xq[g].d;
+            float ys = xq[g].d * (float)(xq[g].s16[0] + xq[g].s16[1]);
+            acc = fmaf(ws, (float)ia, acc);
+            acc = fmaf(-(128.0f * d), ys, acc);
+        }
+        *out = acc;
+        return;
+    }
+    const fgo_q8k_blk *y = (const fgo_q8k_blk *)act;
+    float f = 0.0f;
+    for (int b = 0; b < cols / 256; b++) {
+        float a = 0.0f;
+        if (type == FGO_T_Q4_K) {
+            const uint8_t *p = rb + (size_t)b * 144;
+            uint8_t sc[8], mn[8];
+            q4k_scales(p + 4, sc, mn);
+            float d = fgo_fp16(rd16(p)), dmin = fgo_fp16(rd16(p + 2));
+            for (int g = 0; g < 8; g++) {
+                int ia = 0;
+                for (int l = 0; l < 32; l++) {
+                    int e = 32 * g + l; /* element e: sub-block g = pair j = g/2, nibble g&1 */
+                    uint8_t q = p[16 + 32 * (g >> 1) + l];
+                    ia += ((g & 1) ? (q >> 4) : (q & 0x0F)) * y[b].qs[e];
+                }
+                a = fmaf(d * (float)sc[g], (float)ia, a);
+            }
+            for (int g = 0; g < 8; g++) {
+                float bs = (float)(y[b].bsums[2 * g] + y[b].bsums[2 * g + 1]);
+                a = fmaf(-(dmin * (float)mn[g]), bs, a);
+            }
+        } else { /* Q6_K */
+            const uint8_t *p = rb + (size_t)b * 210;
+            const int8_t *sc = (const int8_t *)(p + 192);
+            float d = fgo_fp16(rd16(p + 208));
+            for (int g = 0; g < 16; g++) {
+                int ia = 0;
+                for (int l = 0; l < 16; l++) ia += q6k_val(p, 16 * g + l) * y[b].qs[16 * g + l];
+                a = fmaf(d * (float)sc[g], (float)ia, a);
+            }
+            for (int g = 0; g < 16; g++)
+                a = fmaf(-(32.0f * d * (float)sc[g]), (float)y[b].bsums[g], a);
+        }
+        f = fmaf(a, y[b].d, f);
+    }
+    *out = f;
+}
+
+int fgo_gemm(uint32_t type, const uint8_t *w, int64_t rows, int cols, const void *act,
+             int act_stride_blocks, float *Y, int ldy, int nb) {
+    if (!type_ok(type, cols)) return -1;
+    int eb, bb;
+    fgo_block_size(type, &eb, &bb);
+    size_t stride = (size_t)(cols / eb) * bb;
+    size_t ablk = type == FGO_T_Q8_0 ? sizeof(fgo_q8_blk) : sizeof(fgo_q8k_blk);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++)
+        for (int t = 0; t < nb; t++)
+            gemm_row_token(type, w + (size_t)r * stride,
+                           (const uint8_t *)act + (size_t)t * act_stride_blocks * ablk, cols,
+                           &Y[(size_t)t * ldy + r]);
+    return 0;
+}
+
+/* matmul (fastgguf.c:3004-3093) restricted to Q4_K / Q6_K / Q8_0, as built for a VNNI CPU:
+ *   nb == 1: matvec;  repacked and nb < 8: per-token matvec;  nb >= 8: the prompt GEMM
+ *   (gemm_kquant, or gemm_q32 for Q8_0 - VNNI builds only, GEMM_Q8_0 at 2864-2868);
+ *   otherwise the x4 tiles, which equal the single-row kernels bit for bit (selftest 5871-5916). */
+int fgo_matmul(uint32_t type, int order, const uint8_t *w, int64_t rows, int cols,
+               const float *X, int ldx, float *Y, int ldy, int nb) {
+    if (!type_ok(type, cols) || nb < 1) return -1;
+    if (nb == 1) return fgo_matvec(type, order, w, rows, cols, X, Y);
+    int repacked = type == FGO_T_Q4_K && order == FGO_ORDER_REPACKED;
+    if (repacked && nb < 8) {
+        for (int t = 0; t < nb; t++)
+            if (fgo_matvec(type, order, w, rows, cols, X + (size_t)t * ldx, Y + (size_t)t * ldy) != 0)
+                return -1;
+        return 0;
+    }
+    size_t ab = act_bytes(type, cols);
+    uint8_t *act = (uint8_t *)malloc(ab * (size_t)nb);
+    if (!act) return -1;
+    for (int t = 0; t < nb; t++) {
+        if (type == FGO_T_Q8_0) fgo_quantize_q8(X + (size_t)t * ldx, (fgo_q8_blk *)(act + ab * t), cols);
+        else fgo_quantize_q8k(X + (size_t)t * ldx, (fgo_q8k_blk *)(act + ab * t), cols);
+    }
+    int eb, bb;
+    fgo_block_size(type, &eb, &bb);
+    int sblocks = cols / eb;
+    if (nb >= 8) {
+        int rc = fgo_gemm(type, w, rows, cols, act, sblocks, Y, ldy, nb);
+        free(act);
+        return rc;
+    }
+    size_t stride = (size_t)(cols / eb) * bb;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++)
+        for (int t = 0; t < nb; t++)
+            Y[(size_t)t * ldy + r] = dot_row3(type, FGO_ORDER_ROW, w + (size_t)r * stride, act + ab * t, cols);
+    free(act);
+    return 0;
+}
+
+/* ---- MoE (moe_ffn, fastgguf.c:4588-4642) ---- */
+
+/* silu_f (fastgguf.c:3118) */
+float fgo_silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* softmax_inplace (3147-3156), argmax_f (3328-3332), selection and renormalisation (4594-4604) */
+void fgo_moe_route(const float *logits, int n_expert, int k, int32_t *sel, float *w) {
+    float *p = (float *)malloc((size_t)n_expert * sizeof(float));
+    memcpy(p, logits, (size_t)n_expert * sizeof(float));
+    float mx = -INFINITY;
+    for (int i = 0; i < n_expert; i++) if (p[i] > mx) mx = p[i];
+    float sum = 0.0f;
+    for (int i = 0; i < n_expert; i++) { p[i] = expf(p[i] - mx); sum += p[i]; }
+    if (sum > 0.0f) {
+        float inv = 1.0f / sum;
+        for (int i = 0; i < n_expert; i++) p[i] *= inv;
+    }
+    float wsum = 0.0f;
+    for (int j = 0; j < k; j++) {
+        int best = 0;
+        float bv = -INFINITY;
+        for (int i = 0; i < n_expert; i++) if (p[i] > bv) { bv = p[i]; best = i; }
+        sel[j] = best;
+        w[j] = p[best];
+        wsum += p[best];
+        p[best] = -1.0f;
+    }
+    if (wsum < 6.103515625e-5f) wsum = 6.103515625e-5f;
+    for (int j = 0; j < k; j++) w[j] /= wsum;
+    free(p);
+}
+
+/* the reference's down loop: s = s + w_j * dot (4626-4635). gcc contracts this statement to a
+ * fused multiply-add under -O3 -march=native (fp-contract=fast, the GNU C default); the golden
+ * vectors written by the compiled reference fix which form is used. */
+static float moe_accum(float s, float wj, float dot) { return fmaf(wj, dot, s); }
+
+int fgo_moe_down(uint32_t type_down, const uint8_t *down, int n_embd, int ff, int k,
+                 const int32_t *sel, const float *w, const float *h, float *out) {
+    if (!type_ok(type_down, ff)) return -1;
+    int eb, bb;
+    fgo_block_size(type_down, &eb, &bb);
+    size_t sd = (size_t)(ff / eb) * bb, ab = act_bytes(type_down, ff);
+    uint8_t *act = (uint8_t *)malloc(ab * (size_t)k);
+    if (!act) return -1;
+    for (int j = 0; j < k; j++) {
+        if (type_down == FGO_T_Q8_0) fgo_quantize_q8(h + (size_t)j * ff, (fgo_q8_blk *)(act + ab * j), ff);
+        else fgo_quantize_q8k(h + (size_t)j * ff, (fgo_q8k_blk *)(act + ab * j), ff);
+    }
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < n_embd; i++) {
+        float s = 0.0f;
+        for (int j = 0; j < k; j++) {
+            size_t row = (size_t)sel[j] * n_embd + i;
+            s = moe_accum(s, w[j], dot_row3(type_down, FGO_ORDER_ROW, down + row * sd, act + ab * j, ff));
+        }
+        out[i] = s;
+    }
+    free(act);
+    return 0;
+}
+
+int fgo_moe_ffn(uint32_t type_gate, uint32_t type_up, uint32_t type_down,
+                const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                int n_expert, int k, int n_embd, int ff, const float *logits,
+                const float *X, float *Y, int n_tok, int32_t *sel_out, float *w_out,
+                float *h_out) {
+    if (!type_ok(type_gate, n_embd) || !type_ok(type_up, n_embd) || !type_ok(type_down, ff)) return -1;
+    if (k < 1 || k > n_expert) return -1;
+    int eg, bg, eu, bu;
+    fgo_block_size(type_gate, &eg, &bg);
+    fgo_block_size(type_up, &eu, &bu);
+    size_t sg = (size_t)(n_embd / eg) * bg, su = (size_t)(n_embd / eu) * bu;
+    int32_t *sel = (int32_t *)malloc((size_t)k * sizeof(int32_t));
+    float *w = (float *)malloc((size_t)k * sizeof(float));
+    float *h = (float *)malloc((size_t)k * ff * sizeof(float));
+    if (!sel || !w || !h) { free(sel); free(w); free(h); return -1; }
+    int rc = 0;
+    for (int t = 0; t < n_tok && rc == 0; t++) {
+        const float *x = X + (size_t)t * n_embd;
+        fgo_moe_route(logits + (size_t)t * n_expert, n_expert, k, sel, w);
+        void *ag = quantize_for(type_gate, x, n_embd);
+        void *au = type_up == type_gate ? ag : quantize_for(type_up, x, n_embd);
+#pragma omp parallel for schedule(static)
+        for (int r = 0; r < k * ff; r++) {
+            size_t row = (size_t)sel[r / ff] * ff + r % ff;
+            float gv = dot_row3(type_gate, FGO_ORDER_ROW, gate + row * sg, ag, n_embd);
+            float uv = dot_row3(type_up, FGO_ORDER_ROW, up + row * su, au, n_embd);
+            h[r] = fgo_silu(gv) * uv;
+        }
+        if (au != ag) free(au);
+        free(ag);
+        rc = fgo_moe_down(type_down, down, n_embd, ff, k, sel, w, h, Y + (size_t)t * n_embd);
+        if (sel_out) memcpy(sel_out + (size_t)t * k, sel, (size_t)k * sizeof(int32_t));
+        if (w_out) memcpy(w_out + (size_t)t * k, w, (size_t)k * sizeof(float));
+        if (h_out) memcpy(h_out + (size_t)t * k * ff, h, (size_t)k * ff * sizeof(float));
+    }
+    free(sel); free(w); free(h);
+    return rc;
+}

@@ -1,0 +1,93 @@
+/*
+ * fg_oracle.h - CPU restatement of fastgguf's quantized weight x Q8-activation kernels.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the parity checker for the HIP backend in
+ * fastgguf_amd/: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * it. Nothing in the product path calls it, and the HIP backend never falls back to it.
+ *
+ * Every function restates one reference function (file:line into lawnak/FastGGUF fastgguf.c) and
+ * reproduces the fp32 evaluation order of the reference's AVX2 / AVX-VNNI / AVX-512-VNNI builds,
+ * lane by lane, so that results are bit-identical to the compiled reference.
+ *
+ * Activation block layouts are the reference's C structs (little-endian, no padding):
+ *   q8_blk  (fastgguf.c:743) = { float d; int8 qs[32]; int16 s16[2]; }        40 bytes
+ *   q8k_blk (fastgguf.c:771) = { float d; int8 qs[256]; int16 bsums[16]; }   292 bytes
+ */
+#ifndef FG_ORACLE_H
+#define FG_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { FGO_T_F32 = 0, FGO_T_Q8_0 = 8, FGO_T_Q4_K = 12, FGO_T_Q6_K = 14 };
+
+/* fp32 evaluation order a kernel follows (which reference kernel the call restates) */
+enum {
+    FGO_ORDER_ROW = 0,      /* dot_q4_K_q8k / dot_q6_K_q8k / dot_q8_0_q8 (file layout) */
+    FGO_ORDER_REPACKED = 1, /* dot_q4Kx8 (8-row repacked Q4_K, fastgguf.c:2322) */
+};
+
+typedef struct { float d; int8_t qs[32]; int16_t s16[2]; } fgo_q8_blk;
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } fgo_q8k_blk;
+
+float fgo_fp16(uint16_t h);
+void fgo_quantize_q8(const float *x, fgo_q8_blk *out, int n);
+void fgo_quantize_q8k(const float *x, fgo_q8k_blk *out, int n);
+
+float fgo_dot_q8_0(const uint8_t *row, const fgo_q8_blk *xq, int nb);
+float fgo_dot_q4_K(const uint8_t *row, const fgo_q8k_blk *y, int nb);
+float fgo_dot_q4_K_rp(const uint8_t *row, const fgo_q8k_blk *y, int nb);
+float fgo_dot_q6_K(const uint8_t *row, const fgo_q8k_blk *y, int nb);
+
+/* per-block integer parts (the bit-exact targets):
+ *   Q4_K: sumi[b] = sum_s sc_s * sum_32 q*y,   msum[b] = sum_s m_s * (bs_2s + bs_2s+1)
+ *   Q6_K: sumi[b] = sum_g sc_g * sum_16 q*y,   msum[b] = sum_g sc_g * bs_g      (q in 0..63)
+ *   Q8_0: sumi[b] = sum_32 w*x,                msum[b] = 0                    */
+void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
+                    int32_t *sumi, int32_t *msum);
+
+/* y[r] = dot(W[r], Q8(x)) for r < rows: quantize once, then the row kernel (matvec 2575) */
+int fgo_matvec(uint32_t type, int order, const uint8_t *w, int64_t rows, int cols,
+               const float *x, float *y);
+
+/* Y[t*ldy + r] for t < nb tokens, with the kernel choice of matmul (fastgguf.c:3004) */
+int fgo_matmul(uint32_t type, int order, const uint8_t *w, int64_t rows, int cols,
+               const float *X, int ldx, float *Y, int ldy, int nb);
+
+/* the prompt GEMM on pre-quantized activations (gemm_kquant 2818 / gemm_q32 2981) */
+int fgo_gemm(uint32_t type, const uint8_t *w, int64_t rows, int cols, const void *act,
+             int act_stride_blocks, float *Y, int ldy, int nb);
+
+/* moe_ffn (fastgguf.c:4588) for n_tok independent tokens, router logits given:
+ *   logits [n_tok][n_expert], X [n_tok][n_embd], Y [n_tok][n_embd]
+ *   gate/up: [n_expert][ff][n_embd] expert rows, down: [n_expert][n_embd][ff]
+ *   sel_out [n_tok][k] and w_out [n_tok][k] (optional, may be NULL) receive the routing.
+ *   h_out [n_tok][k][ff] (optional) receives silu(gate)*up before its quantization. */
+int fgo_moe_ffn(uint32_t type_gate, uint32_t type_up, uint32_t type_down,
+                const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                int n_expert, int k, int n_embd, int ff, const float *logits,
+                const float *X, float *Y, int n_tok, int32_t *sel_out, float *w_out,
+                float *h_out);
+
+/* the MoE down-projection stage alone, with h given: out = sum_j w_j * dot(down_j, Q8K(h_j)) */
+int fgo_moe_down(uint32_t type_down, const uint8_t *down, int n_embd, int ff, int k,
+                 const int32_t *sel, const float *w, const float *h, float *out);
+
+/* reference order for the router: softmax (3147), top-k by argmax (3328), renormalise (4603) */
+void fgo_moe_route(const float *logits, int n_expert, int k, int32_t *sel, float *w);
+
+/* silu_f (fastgguf.c:3118) with the C library's expf */
+float fgo_silu(float x);
+
+/* dequantize_row for the three types (fastgguf.c:552, 622, 669): textbook value decode */
+int fgo_dequantize_row(uint32_t type, const uint8_t *raw, float *out, int n);
+
+/* block geometry: elements and bytes per block (block_size_of, fastgguf.c:235) */
+int fgo_block_size(uint32_t type, int *elems, int *bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

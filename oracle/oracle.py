@@ -1,0 +1,266 @@
+"""ctypes loader for the CPU parity oracle (test infrastructure only).
+
+`Oracle` wraps liboracle.so, the clean-room C restatement of the reference kernels (fg_oracle.c).
+`Reference` wraps oracle/_ref/libfgref_*.so, the reference's own kernels compiled from
+/root/reference (built only where the reference is present; the built .so travels with the repo).
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(HERE))
+from fastgguf_amd.synth import BLOCK, Q8_BLK, Q8K_BLK, T_Q8_0  # noqa: E402
+
+ORDER_ROW = 0
+ORDER_REPACKED = 1
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def act_dtype(type_: int):
+    return Q8_BLK if type_ == T_Q8_0 else Q8K_BLK
+
+
+class Oracle:
+    """The restatement (fg_oracle.c)."""
+
+    def __init__(self, path: str | None = None):
+        path = path or os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (run make -C oracle)")
+        L = self.lib = C.CDLL(path)
+        L.fgo_fp16.restype = C.c_float
+        L.fgo_fp16.argtypes = [C.c_uint16]
+        for n in ("fgo_quantize_q8", "fgo_quantize_q8k"):
+            getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+            getattr(L, n).restype = None
+        for n in ("fgo_dot_q8_0", "fgo_dot_q4_K", "fgo_dot_q4_K_rp", "fgo_dot_q6_K"):
+            getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+            getattr(L, n).restype = C.c_float
+        L.fgo_block_ints.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+        L.fgo_matvec.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
+        L.fgo_matmul.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_int,
+                                 C.c_void_p, C.c_int, C.c_int]
+        L.fgo_gemm.argtypes = [C.c_uint32, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
+                               C.c_int, C.c_int]
+        L.fgo_moe_ffn.argtypes = [C.c_uint32] * 3 + [C.c_void_p] * 3 + [C.c_int] * 4 + \
+            [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.fgo_moe_down.argtypes = [C.c_uint32, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                   C.c_void_p, C.c_void_p]
+        L.fgo_moe_route.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        L.fgo_moe_route.restype = None
+        L.fgo_silu.argtypes = [C.c_float]
+        L.fgo_silu.restype = C.c_float
+        L.fgo_dequantize_row.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
+
+    # -- quantizers
+    def quantize_q8(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size // 32, Q8_BLK)
+        self.lib.fgo_quantize_q8(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def quantize_q8k(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size // 256, Q8K_BLK)
+        self.lib.fgo_quantize_q8k(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def quantize_for(self, type_: int, x: np.ndarray) -> np.ndarray:
+        return self.quantize_q8(x) if type_ == T_Q8_0 else self.quantize_q8k(x)
+
+    # -- row kernels
+    def dot(self, type_: int, row: np.ndarray, act: np.ndarray, order: int = ORDER_ROW) -> float:
+        row = np.ascontiguousarray(row, np.uint8)
+        eb, _ = BLOCK[type_]
+        nb = act.size
+        name = {8: "fgo_dot_q8_0", 12: "fgo_dot_q4_K_rp" if order == ORDER_REPACKED else "fgo_dot_q4_K",
+                14: "fgo_dot_q6_K"}[type_]
+        return getattr(self.lib, name)(_ptr(row), _ptr(act), nb)
+
+    def block_ints(self, type_: int, row: np.ndarray, act: np.ndarray):
+        row = np.ascontiguousarray(row, np.uint8)
+        nb = act.size
+        s = np.zeros(nb, np.int32)
+        m = np.zeros(nb, np.int32)
+        self.lib.fgo_block_ints(type_, _ptr(row), _ptr(act), nb, _ptr(s), _ptr(m))
+        return s, m
+
+    def dequantize_row(self, type_: int, raw: np.ndarray, n: int) -> np.ndarray:
+        out = np.zeros(n, np.float32)
+        raw = np.ascontiguousarray(raw, np.uint8)
+        if self.lib.fgo_dequantize_row(type_, _ptr(raw), _ptr(out), n) != 0:
+            raise ValueError("dequantize_row failed")
+        return out
+
+    # -- drivers
+    def matvec(self, type_: int, w: np.ndarray, cols: int, x: np.ndarray, order: int = ORDER_ROW) -> np.ndarray:
+        w = np.ascontiguousarray(w, np.uint8)
+        x = np.ascontiguousarray(x, np.float32)
+        rows = w.shape[0]
+        y = np.zeros(rows, np.float32)
+        if self.lib.fgo_matvec(type_, order, _ptr(w), rows, cols, _ptr(x), _ptr(y)) != 0:
+            raise ValueError("fgo_matvec failed")
+        return y
+
+    def matmul(self, type_: int, w: np.ndarray, cols: int, X: np.ndarray, order: int = ORDER_ROW) -> np.ndarray:
+        w = np.ascontiguousarray(w, np.uint8)
+        X = np.ascontiguousarray(X, np.float32)
+        rows, nb = w.shape[0], X.shape[0]
+        Y = np.zeros((nb, rows), np.float32)
+        if self.lib.fgo_matmul(type_, order, _ptr(w), rows, cols, _ptr(X), cols, _ptr(Y), rows, nb) != 0:
+            raise ValueError("fgo_matmul failed")
+        return Y
+
+    def gemm(self, type_: int, w: np.ndarray, cols: int, act: np.ndarray) -> np.ndarray:
+        """act: [nb, blocks] structured activation blocks."""
+        w = np.ascontiguousarray(w, np.uint8)
+        act = np.ascontiguousarray(act)
+        rows, nb = w.shape[0], act.shape[0]
+        Y = np.zeros((nb, rows), np.float32)
+        if self.lib.fgo_gemm(type_, _ptr(w), rows, cols, _ptr(act), act.shape[1], _ptr(Y), rows, nb) != 0:
+            raise ValueError("fgo_gemm failed")
+        return Y
+
+    def moe_route(self, logits: np.ndarray, k: int):
+        logits = np.ascontiguousarray(logits, np.float32)
+        sel = np.zeros(k, np.int32)
+        w = np.zeros(k, np.float32)
+        self.lib.fgo_moe_route(_ptr(logits), logits.size, k, _ptr(sel), _ptr(w))
+        return sel, w
+
+    def silu(self, x: float) -> float:
+        return self.lib.fgo_silu(x)
+
+    def moe_ffn(self, types, gate, up, down, n_expert, k, n_embd, ff, logits, X, want_h=False):
+        X = np.ascontiguousarray(X, np.float32)
+        logits = np.ascontiguousarray(logits, np.float32)
+        n_tok = X.shape[0]
+        Y = np.zeros((n_tok, n_embd), np.float32)
+        sel = np.zeros((n_tok, k), np.int32)
+        w = np.zeros((n_tok, k), np.float32)
+        h = np.zeros((n_tok, k, ff), np.float32) if want_h else None
+        g, u, d = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
+        rc = self.lib.fgo_moe_ffn(types[0], types[1], types[2], _ptr(g), _ptr(u), _ptr(d), n_expert, k, n_embd,
+                                  ff, _ptr(logits), _ptr(X), _ptr(Y), n_tok, _ptr(sel), _ptr(w),
+                                  _ptr(h) if want_h else None)
+        if rc != 0:
+            raise ValueError("fgo_moe_ffn failed")
+        return (Y, sel, w, h) if want_h else (Y, sel, w)
+
+    def moe_down(self, type_down, down, n_embd, ff, sel, w, h):
+        sel = np.ascontiguousarray(sel, np.int32)
+        w = np.ascontiguousarray(w, np.float32)
+        h = np.ascontiguousarray(h, np.float32)
+        out = np.zeros(n_embd, np.float32)
+        d = np.ascontiguousarray(down, np.uint8)
+        if self.lib.fgo_moe_down(type_down, _ptr(d), n_embd, ff, sel.size, _ptr(sel), _ptr(w), _ptr(h),
+                                 _ptr(out)) != 0:
+            raise ValueError("fgo_moe_down failed")
+        return out
+
+
+def _cpu_has_vnni() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            flags = f.read()
+        return " avx512_vnni" in flags and " avx512vl" in flags
+    except OSError:
+        return False
+
+
+class Reference:
+    """The reference's own kernels, compiled from /root/reference (oracle/_ref)."""
+
+    def __init__(self, variant: str | None = None):
+        if variant is None:
+            variant = "vnni" if _cpu_has_vnni() else "avx2"
+        path = os.path.join(HERE, "_ref", f"libfgref_{variant}.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.variant = variant
+        L = self.lib = C.CDLL(path)
+        L.fgr_build.restype = C.c_char_p
+        L.fgr_init.argtypes = [C.c_int]
+        L.fgr_threads.restype = C.c_int
+        for n in ("fgr_quantize_q8", "fgr_quantize_q8k"):
+            getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+            getattr(L, n).restype = None
+        for n in ("fgr_dot_q8_0", "fgr_dot_q4_K", "fgr_dot_q6_K"):
+            getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+            getattr(L, n).restype = C.c_float
+        L.fgr_matvec.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
+        L.fgr_matvec_multi.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                       C.c_void_p, C.c_void_p]
+        L.fgr_matmul.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_int,
+                                 C.c_void_p, C.c_int, C.c_int]
+        L.fgr_moe_ffn.argtypes = [C.c_uint32] * 3 + [C.c_void_p] * 3 + [C.c_int] * 4 + \
+            [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+        L.fgr_init(256)
+
+    @property
+    def build(self) -> str:
+        return self.lib.fgr_build().decode()
+
+    def threads(self) -> int:
+        return self.lib.fgr_threads()
+
+    def quantize_q8(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size // 32, Q8_BLK)
+        self.lib.fgr_quantize_q8(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def quantize_q8k(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size // 256, Q8K_BLK)
+        self.lib.fgr_quantize_q8k(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def dot(self, type_, row, act):
+        row = np.ascontiguousarray(row, np.uint8)
+        name = {8: "fgr_dot_q8_0", 12: "fgr_dot_q4_K", 14: "fgr_dot_q6_K"}[type_]
+        return getattr(self.lib, name)(_ptr(row), _ptr(act), act.size)
+
+    def matvec(self, type_, w, cols, x, repack=False):
+        w = np.ascontiguousarray(w, np.uint8)
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(w.shape[0], np.float32)
+        if self.lib.fgr_matvec(type_, int(repack), _ptr(w), w.shape[0], cols, _ptr(x), _ptr(y)) != 0:
+            raise ValueError("fgr_matvec failed")
+        return y
+
+    def matmul(self, type_, w, cols, X, repack=False):
+        w = np.ascontiguousarray(w, np.uint8)
+        X = np.ascontiguousarray(X, np.float32)
+        rows, nb = w.shape[0], X.shape[0]
+        Y = np.zeros((nb, rows), np.float32)
+        if self.lib.fgr_matmul(type_, int(repack), _ptr(w), rows, cols, _ptr(X), cols, _ptr(Y), rows, nb) != 0:
+            raise ValueError("fgr_matmul failed")
+        return Y
+
+    def moe_ffn(self, types, gate, up, down, n_expert, k, n_embd, ff, logits, X):
+        X = np.ascontiguousarray(X, np.float32)
+        logits = np.ascontiguousarray(logits, np.float32)
+        n_tok = X.shape[0]
+        Y = np.zeros((n_tok, n_embd), np.float32)
+        sel = np.zeros((n_tok, k), np.int32)
+        w = np.zeros((n_tok, k), np.float32)
+        g, u, d = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
+        rc = self.lib.fgr_moe_ffn(types[0], types[1], types[2], _ptr(g), _ptr(u), _ptr(d), n_expert, k, n_embd,
+                                  ff, _ptr(logits), _ptr(X), _ptr(Y), n_tok, _ptr(sel), _ptr(w))
+        if rc != 0:
+            raise ValueError(f"fgr_moe_ffn failed ({rc})")
+        return Y, sel, w

@@ -1,0 +1,147 @@
+/*
+ * ref_harness.c - exports the reference's own CPU kernels (lawnak/FastGGUF fastgguf.c, compiled
+ * from where it lies under /root/reference) as plain C entry points, so the test suite can write
+ * golden vectors with them and bench.py can time them as the CPU baseline.
+ *
+ * TEST INFRASTRUCTURE ONLY. Built by oracle/Makefile into oracle/_ref/ (git-ignored); never
+ * linked into the product library. The reference source is #included, not copied: compiling it
+ * with FG_VARIANT set renames its main() functions (fastgguf.c:51-59) so this file can add its own
+ * exported wrappers around the `static` kernels.
+ */
+#define FG_VARIANT ref
+#include FG_REF_SOURCE
+
+#define FGR_EXPORT __attribute__((visibility("default")))
+
+FGR_EXPORT const char *fgr_build(void) { return FG_CPU_BUILD; }
+
+FGR_EXPORT void fgr_init(int max_cols) {
+    static int fp16_ready;
+    if (!fp16_ready) { fp16_init(); fp16_ready = 1; }
+    matvec_init_scratch(max_cols);
+}
+
+FGR_EXPORT int fgr_threads(void) { return omp_get_max_threads(); }
+
+FGR_EXPORT void fgr_quantize_q8(const float *x, void *out, int n) { quantize_q8(x, (q8_blk_t *)out, n); }
+FGR_EXPORT void fgr_quantize_q8k(const float *x, void *out, int n) { quantize_q8k(x, (q8k_blk_t *)out, n); }
+
+FGR_EXPORT float fgr_dot_q8_0(const uint8_t *row, const void *xq, int nb) { return dot_q8_0_q8(row, (const q8_blk_t *)xq, nb); }
+FGR_EXPORT float fgr_dot_q4_K(const uint8_t *row, const void *y, int nb) { return dot_q4_K_q8k(row, (const q8k_blk_t *)y, nb); }
+FGR_EXPORT float fgr_dot_q6_K(const uint8_t *row, const void *y, int nb) { return dot_q6_K_q8k(row, (const q8k_blk_t *)y, nb); }
+
+/* a tensor view over caller memory; `repack` asks for the 8-row layout the reference builds at
+ * load time (repack_tensor, 2486). repack_tensor drops the source pages with MADV_DONTNEED, so
+ * it is given a private copy of the weights. */
+static int make_tensor(tensor_t *t, uint32_t type, int repack, const uint8_t *w, int64_t rows, int cols,
+                       uint8_t **copy) {
+    memset(t, 0, sizeof(*t));
+    snprintf(t->name, sizeof(t->name), "harness");
+    t->type = type;
+    t->n_dims = 2;
+    t->ne[0] = (uint64_t)cols;
+    t->ne[1] = (uint64_t)rows;
+    t->data = w;
+    t->nbytes = row_stride(type, (uint64_t)cols) * (uint64_t)rows;
+    *copy = NULL;
+    if (repack) {
+        *copy = (uint8_t *)malloc(t->nbytes);
+        if (!*copy) return -1;
+        memcpy(*copy, w, t->nbytes);
+        t->data = *copy;
+        if (repack_tensor(t) == 0) return -1;
+    }
+    return 0;
+}
+
+static void drop_tensor(tensor_t *t, uint8_t *copy) {
+    free((void *)t->rp);
+    free(copy);
+}
+
+FGR_EXPORT int fgr_matvec(uint32_t type, int repack, const uint8_t *w, int64_t rows, int cols,
+                          const float *x, float *y) {
+    tensor_t t;
+    uint8_t *copy;
+    fgr_init(cols);
+    if (make_tensor(&t, type, repack, w, rows, cols, &copy) != 0) return -1;
+    int rc = matvec(&t, x, y);
+    drop_tensor(&t, copy);
+    return rc;
+}
+
+/* matvec_multi over n <= 4 tensors with the same x (2552) */
+FGR_EXPORT int fgr_matvec_multi(int n, const uint32_t *types, const int *repack, const uint8_t *const *w,
+                                const int64_t *rows, int cols, const float *x, float *const *y) {
+    tensor_t t[4], *tp[4];
+    uint8_t *copy[4] = {0};
+    if (n < 1 || n > 4) return -1;
+    fgr_init(cols);
+    for (int i = 0; i < n; i++) {
+        if (make_tensor(&t[i], types[i], repack[i], w[i], rows[i], cols, &copy[i]) != 0) return -1;
+        tp[i] = &t[i];
+    }
+    int rc = matvec_multi(n, tp, x, y);
+    for (int i = 0; i < n; i++) drop_tensor(&t[i], copy[i]);
+    return rc;
+}
+
+FGR_EXPORT int fgr_matmul(uint32_t type, int repack, const uint8_t *w, int64_t rows, int cols,
+                          const float *X, int ldx, float *Y, int ldy, int nb) {
+    tensor_t t;
+    uint8_t *copy;
+    if (nb < 1 || nb > FG_BATCH) return -1;
+    fgr_init(cols);
+    if (make_tensor(&t, type, repack, w, rows, cols, &copy) != 0) return -1;
+    int rc = matmul(&t, X, ldx, Y, ldy, nb);
+    drop_tensor(&t, copy);
+    return rc;
+}
+
+/* moe_ffn (4588) for n_tok tokens, one call per token as forward_chunk does (5089-5091).
+ * The router is an F32 tensor whose row e is (logit_e, 0, ..., 0); with X[t][0] == 1 the
+ * reference's own router matvec then reproduces the given logits exactly. */
+FGR_EXPORT int fgr_moe_ffn(uint32_t tg_type, uint32_t tu_type, uint32_t td_type,
+                           const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                           int n_expert, int k, int n_embd, int ff, const float *logits,
+                           const float *X, float *Y, int n_tok, int32_t *sel_out, float *w_out) {
+    fgr_init(n_embd > ff ? n_embd : ff);
+    model_t *mm = (model_t *)calloc(1, sizeof(model_t));
+    float *router = (float *)calloc((size_t)n_expert * n_embd, sizeof(float));
+    if (!mm || !router) { free(mm); free(router); return -1; }
+    mm->n_embd = n_embd; mm->ff_exp = ff; mm->n_expert = n_expert; mm->n_expert_used = k;
+    mm->moe_probs = (float *)malloc((size_t)n_expert * sizeof(float));
+    mm->moe_w = (float *)malloc((size_t)k * sizeof(float));
+    mm->moe_sel = (int *)malloc((size_t)k * sizeof(int));
+    mm->moe_h = (float *)malloc((size_t)k * ff * sizeof(float));
+    mm->moe_xq = (q8_blk_t *)malloc(((size_t)k * ff / 32 + 1) * sizeof(q8_blk_t));
+    mm->moe_xk = (q8k_blk_t *)malloc(((size_t)k * ff / 256 + 1) * sizeof(q8k_blk_t));
+    tensor_t ti, tg, tu, td;
+    memset(&ti, 0, sizeof(ti));
+    ti.type = T_F32; ti.n_dims = 2; ti.ne[0] = (uint64_t)n_embd; ti.ne[1] = (uint64_t)n_expert;
+    ti.data = (const uint8_t *)router;
+    tg = tu = td = ti;
+    tg.type = tg_type; tu.type = tu_type; td.type = td_type;
+    tg.n_dims = tu.n_dims = td.n_dims = 3;
+    tg.ne[0] = tu.ne[0] = (uint64_t)n_embd; tg.ne[1] = tu.ne[1] = (uint64_t)ff;
+    tg.ne[2] = tu.ne[2] = (uint64_t)n_expert;
+    td.ne[0] = (uint64_t)ff; td.ne[1] = (uint64_t)n_embd; td.ne[2] = (uint64_t)n_expert;
+    tg.data = gate; tu.data = up; td.data = down;
+    layer_t LL;
+    memset(&LL, 0, sizeof(LL));
+    LL.ffn_gate_inp = &ti; LL.ffn_gate_exps = &tg; LL.ffn_up_exps = &tu; LL.ffn_down_exps = &td;
+    int rc = 0;
+    for (int t = 0; t < n_tok && rc == 0; t++) {
+        const float *x = X + (size_t)t * n_embd;
+        if (x[0] != 1.0f) { rc = -2; break; }
+        for (int e = 0; e < n_expert; e++) router[(size_t)e * n_embd] = logits[(size_t)t * n_expert + e];
+        rc = moe_ffn(mm, &LL, x, Y + (size_t)t * n_embd);
+        for (int j = 0; j < k; j++) {
+            if (sel_out) sel_out[(size_t)t * k + j] = mm->moe_sel[j];
+            if (w_out) w_out[(size_t)t * k + j] = mm->moe_w[j];
+        }
+    }
+    free(mm->moe_probs); free(mm->moe_w); free(mm->moe_sel); free(mm->moe_h);
+    free(mm->moe_xq); free(mm->moe_xk); free(mm); free(router);
+    return rc;
+}
