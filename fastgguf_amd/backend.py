@@ -1,0 +1,289 @@
+"""Python binding of the C ABI in include/fastgguf_hip.h (ctypes; no torch).
+
+The class and method names mirror the reference engine's offload and dispatch surface
+(fastgguf.c): `Backend` plays g_gpu (fg_gpu_init 2057, gpu_upload_tensor 2060), and
+`matvec` / `matvec_multi` / `matmul` / `moe_ffn` take the arguments of the reference functions
+of the same names (2575, 2552, 3004, 4588). Every method raises `BackendError` carrying the
+library's status and message when the device call fails; nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from .synth import BLOCK, Q8_BLK, Q8K_BLK, T_Q4_K, T_Q6_K, T_Q8_0, row_bytes
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfastgguf_hip.so")
+
+OK, ERR, ERR_ARG, SKIP_TYPE, SKIP_MEM, ERR_DEVICE = 0, -1, -2, -3, -4, -5
+ORDER_AUTO, ORDER_ROW, ORDER_REPACKED = -1, 0, 1
+ACT_Q8, ACT_Q8K = 1, 2
+
+#: every symbol include/fastgguf_hip.h declares
+EXPORTS = (
+    "fgh_open", "fgh_close", "fgh_info", "fgh_last_error", "fgh_upload", "fgh_tensor_free",
+    "fgh_matvec", "fgh_matvec_multi", "fgh_matmul", "fgh_moe_ffn",
+    "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matmul_dev", "fgh_moe_ffn_dev",
+    "fgh_act_quantize_dev", "fgh_matvec_act_dev",
+    "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_sync",
+    "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
+    "fgh_quantize", "fgh_block_ints", "fgh_fp16_to_f32",
+)
+
+
+class BackendError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"fastgguf_hip status {status}: {msg}")
+        self.status = status
+
+
+class InfoT(C.Structure):
+    _fields_ = [("vram", C.c_uint64), ("budget", C.c_uint64), ("used", C.c_uint64),
+                ("n_offloaded", C.c_int32), ("n_skip_type", C.c_int32), ("n_skip_mem", C.c_int32),
+                ("device", C.c_int32), ("name", C.c_char * 96)]
+
+
+_LIB = None
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    """Loads the built HIP library. Raises if it is missing: there is no fallback path."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built; run `python -m fastgguf_amd.build`")
+    L = C.CDLL(path)
+    vp, i32, i64, u32, u64, f32p = C.c_void_p, C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_void_p
+    sig = {
+        "fgh_open": (i32, [i32, u64, C.POINTER(vp)]),
+        "fgh_close": (None, [vp]),
+        "fgh_info": (i32, [vp, C.POINTER(InfoT)]),
+        "fgh_last_error": (C.c_char_p, [vp]),
+        "fgh_upload": (i32, [vp, u32, i64, i64, i64, i32, vp, u64, C.POINTER(vp)]),
+        "fgh_tensor_free": (None, [vp]),
+        "fgh_matvec": (i32, [vp, vp, f32p, f32p]),
+        "fgh_matvec_multi": (i32, [vp, i32, vp, f32p, vp]),
+        "fgh_matmul": (i32, [vp, vp, f32p, i32, f32p, i32, i32]),
+        "fgh_moe_ffn": (i32, [vp, vp, vp, vp, i32, f32p, f32p, f32p, i32, vp, vp]),
+        "fgh_matvec_dev": (i32, [vp, vp, vp, vp]),
+        "fgh_matvec_multi_dev": (i32, [vp, i32, vp, vp, vp]),
+        "fgh_matmul_dev": (i32, [vp, vp, vp, i32, vp, i32, i32]),
+        "fgh_moe_ffn_dev": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, i32]),
+        "fgh_act_quantize_dev": (i32, [vp, u32, i64, vp, i32]),
+        "fgh_matvec_act_dev": (i32, [vp, vp, vp]),
+        "fgh_dev_alloc": (i32, [vp, u64, C.POINTER(vp)]),
+        "fgh_dev_free": (i32, [vp, vp]),
+        "fgh_copy_h2d": (i32, [vp, vp, vp, u64]),
+        "fgh_copy_d2h": (i32, [vp, vp, vp, u64]),
+        "fgh_sync": (i32, [vp]),
+        "fgh_event_create": (i32, [vp, C.POINTER(vp)]),
+        "fgh_event_record": (i32, [vp, vp]),
+        "fgh_event_elapsed_ms": (i32, [vp, vp, vp, C.POINTER(C.c_float)]),
+        "fgh_event_destroy": (i32, [vp, vp]),
+        "fgh_quantize": (i32, [vp, i32, f32p, i32, vp]),
+        "fgh_block_ints": (i32, [vp, vp, f32p, vp, vp]),
+        "fgh_fp16_to_f32": (i32, [vp, vp, i32, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = L
+    return L
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Tensor:
+    """A device copy of one GGUF tensor (the reference's tensor_t.gpu, fastgguf.c:274)."""
+
+    def __init__(self, backend: "Backend", handle: int, type_: int, cols: int, rows: int, n_mats: int):
+        self.backend, self.handle = backend, handle
+        self.type, self.cols, self.rows, self.n_mats = type_, cols, rows, n_mats
+
+    @property
+    def nout(self) -> int:
+        return self.rows * self.n_mats
+
+    @property
+    def nblocks(self) -> int:
+        return self.cols // BLOCK[self.type][0]
+
+    def free(self):
+        if self.handle:
+            self.backend.lib.fgh_tensor_free(self.handle)
+            self.handle = None
+
+
+class Backend:
+    """One device context (fg_gpu_init, fastgguf.c:1968-2057)."""
+
+    def __init__(self, device: int = 0, budget_bytes: int = 0):
+        self.lib = load_library()
+        h = C.c_void_p()
+        rc = self.lib.fgh_open(device, budget_bytes, C.byref(h))
+        if rc != OK:
+            raise BackendError(rc, "fgh_open failed (no usable gfx950 device)")
+        self.ctx = h
+
+    def close(self):
+        if self.ctx:
+            self.lib.fgh_close(self.ctx)
+            self.ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, rc: int):
+        if rc != OK:
+            raise BackendError(rc, self.lib.fgh_last_error(self.ctx).decode())
+
+    def info(self) -> dict:
+        i = InfoT()
+        self._check(self.lib.fgh_info(self.ctx, C.byref(i)))
+        return {f: (getattr(i, f).decode() if f == "name" else getattr(i, f)) for f, _ in InfoT._fields_}
+
+    # -- gpu_upload_tensor (2060)
+    def upload(self, type_: int, cols: int, data: np.ndarray, rows: int | None = None, n_mats: int = 1,
+               order: int = ORDER_AUTO) -> Tensor:
+        data = np.ascontiguousarray(data, np.uint8)
+        if rows is None:
+            rows = data.size // (row_bytes(type_, cols) * n_mats)
+        h = C.c_void_p()
+        self._check(self.lib.fgh_upload(self.ctx, type_, cols, rows, n_mats, order, _p(data), data.size,
+                                        C.byref(h)))
+        return Tensor(self, h.value, type_, cols, rows, n_mats)
+
+    # -- matvec (2575)
+    def matvec(self, t: Tensor, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        if x.size != t.cols:
+            raise ValueError("x length != cols")
+        y = np.empty(t.nout, np.float32)
+        self._check(self.lib.fgh_matvec(self.ctx, t.handle, _p(x), _p(y)))
+        return y
+
+    # -- matvec_multi (2552)
+    def matvec_multi(self, ts: list[Tensor], x: np.ndarray) -> list[np.ndarray]:
+        x = np.ascontiguousarray(x, np.float32)
+        ys = [np.empty(t.nout, np.float32) for t in ts]
+        th = (C.c_void_p * len(ts))(*[t.handle for t in ts])
+        yp = (C.c_void_p * len(ts))(*[y.ctypes.data for y in ys])
+        self._check(self.lib.fgh_matvec_multi(self.ctx, len(ts), th, _p(x), yp))
+        return ys
+
+    # -- matmul (3004): X [nb, cols] -> Y [nb, rows]
+    def matmul(self, t: Tensor, X: np.ndarray) -> np.ndarray:
+        X = np.ascontiguousarray(X, np.float32)
+        nb = X.shape[0]
+        Y = np.empty((nb, t.nout), np.float32)
+        self._check(self.lib.fgh_matmul(self.ctx, t.handle, _p(X), t.cols, _p(Y), t.nout, nb))
+        return Y
+
+    # -- moe_ffn (4588) for n_tok tokens
+    def moe_ffn(self, gate: Tensor, up: Tensor, down: Tensor, k: int, logits: np.ndarray, X: np.ndarray):
+        X = np.ascontiguousarray(X, np.float32)
+        logits = np.ascontiguousarray(logits, np.float32)
+        n_tok = X.shape[0]
+        Y = np.empty((n_tok, down.rows), np.float32)
+        sel = np.empty((n_tok, k), np.int32)
+        w = np.empty((n_tok, k), np.float32)
+        self._check(self.lib.fgh_moe_ffn(self.ctx, gate.handle, up.handle, down.handle, k, _p(logits), _p(X),
+                                         _p(Y), n_tok, _p(sel), _p(w)))
+        return Y, sel, w
+
+    # -- test hooks
+    def quantize_q8(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size // 32, Q8_BLK)
+        self._check(self.lib.fgh_quantize(self.ctx, ACT_Q8, _p(x), x.size, _p(out)))
+        return out
+
+    def quantize_q8k(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size // 256, Q8K_BLK)
+        self._check(self.lib.fgh_quantize(self.ctx, ACT_Q8K, _p(x), x.size, _p(out)))
+        return out
+
+    def block_ints(self, t: Tensor, x: np.ndarray):
+        x = np.ascontiguousarray(x, np.float32)
+        s = np.empty((t.nout, t.nblocks), np.int32)
+        m = np.empty((t.nout, t.nblocks), np.int32)
+        self._check(self.lib.fgh_block_ints(self.ctx, t.handle, _p(x), _p(s), _p(m)))
+        return s, m
+
+    def fp16_to_f32(self, h: np.ndarray) -> np.ndarray:
+        h = np.ascontiguousarray(h, np.uint16)
+        out = np.empty(h.size, np.float32)
+        self._check(self.lib.fgh_fp16_to_f32(self.ctx, _p(h), h.size, _p(out)))
+        return out
+
+    # -- device memory / events (device-resident callers, benchmarks)
+    def dev_alloc(self, nbytes: int) -> int:
+        p = C.c_void_p()
+        self._check(self.lib.fgh_dev_alloc(self.ctx, nbytes, C.byref(p)))
+        return p.value
+
+    def dev_free(self, p: int):
+        self._check(self.lib.fgh_dev_free(self.ctx, p))
+
+    def h2d(self, dst: int, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        self._check(self.lib.fgh_copy_h2d(self.ctx, dst, _p(a), a.nbytes))
+
+    def d2h(self, a: np.ndarray, src: int):
+        self._check(self.lib.fgh_copy_d2h(self.ctx, _p(a), src, a.nbytes))
+
+    def sync(self):
+        self._check(self.lib.fgh_sync(self.ctx))
+
+    def event(self) -> int:
+        e = C.c_void_p()
+        self._check(self.lib.fgh_event_create(self.ctx, C.byref(e)))
+        return e.value
+
+    def record(self, ev: int):
+        self._check(self.lib.fgh_event_record(self.ctx, ev))
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        ms = C.c_float()
+        self._check(self.lib.fgh_event_elapsed_ms(self.ctx, a, b, C.byref(ms)))
+        return ms.value
+
+    def event_destroy(self, ev: int):
+        self._check(self.lib.fgh_event_destroy(self.ctx, ev))
+
+    def matvec_dev(self, t: Tensor, x_dev: int, y_dev: int):
+        self._check(self.lib.fgh_matvec_dev(self.ctx, t.handle, x_dev, y_dev))
+
+    def matvec_multi_dev(self, ts: list[Tensor], x_dev: int, y_devs: list[int]):
+        th = (C.c_void_p * len(ts))(*[t.handle for t in ts])
+        yp = (C.c_void_p * len(ts))(*y_devs)
+        self._check(self.lib.fgh_matvec_multi_dev(self.ctx, len(ts), th, x_dev, yp))
+
+    def act_quantize_dev(self, type_: int, cols: int, x_dev: int, ntok: int = 1):
+        self._check(self.lib.fgh_act_quantize_dev(self.ctx, type_, cols, x_dev, ntok))
+
+    def matvec_act_dev(self, t: Tensor, y_dev: int):
+        self._check(self.lib.fgh_matvec_act_dev(self.ctx, t.handle, y_dev))
+
+    def matmul_dev(self, t: Tensor, X_dev: int, Y_dev: int, nb: int):
+        self._check(self.lib.fgh_matmul_dev(self.ctx, t.handle, X_dev, t.cols, Y_dev, t.nout, nb))
+
+    def moe_ffn_dev(self, gate: Tensor, up: Tensor, down: Tensor, k: int, logits_dev: int, X_dev: int,
+                    Y_dev: int, n_tok: int):
+        self._check(self.lib.fgh_moe_ffn_dev(self.ctx, gate.handle, up.handle, down.handle, k, logits_dev, X_dev,
+                                             Y_dev, n_tok))
+
+
+__all__ = ["Backend", "BackendError", "Tensor", "load_library", "EXPORTS", "T_Q4_K", "T_Q6_K", "T_Q8_0",
+           "ORDER_AUTO", "ORDER_ROW", "ORDER_REPACKED"]

@@ -1,0 +1,66 @@
+"""Builds the gfx950 HIP library of the backend in-tree (fastgguf_amd/libfastgguf_hip.so).
+
+    python -m fastgguf_amd.build          # or __graft_entry__.build()
+
+hipcc cross-compiles for gfx950 without a GPU. Flags that matter for results:
+  -ffp-contract=off   no fused multiply-add except where written (__builtin_fmaf), so the fp32
+                      chains match the reference's evaluation order
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                      no packed fp32 instructions (the host pass warns it does not know the
+                      feature; that is expected)
+Division and square root stay IEEE-correct (hipcc's default), which the bit-exact quantizers need.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libfastgguf_hip.so")
+SOURCES = ["fgh_api.hip", "fgh_kernels.hip"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+
+def hipcc_cmd(out: str = LIB) -> list[str]:
+    return [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+            "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-Wall", "-Wno-unused-function", "-fvisibility=hidden",
+            "-I", os.path.join(ROOT, "include"),
+            "-o", out] + [os.path.join(CSRC, s) for s in SOURCES]
+
+
+def build(verbose: bool = True) -> str:
+    tmp = LIB + ".tmp"
+    cmd = hipcc_cmd(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip())
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
+    if verbose and err:
+        print(err, file=sys.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle(verbose: bool = True) -> None:
+    """Builds oracle/liboracle.so (the CPU parity checker) and, where /root/reference exists, the
+    reference kernels into oracle/_ref/."""
+    odir = os.path.join(ROOT, "oracle")
+    targets = ["all"]
+    if os.path.exists("/root/reference/fastgguf.c"):
+        targets.append("ref")
+    r = subprocess.run(["make", "-C", odir, "-B"] + targets, capture_output=True, text=True)
+    if verbose:
+        print(r.stdout[-2000:], flush=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{r.stderr[-4000:]}")
+
+
+if __name__ == "__main__":
+    build()
+    build_oracle()

@@ -1,0 +1,507 @@
+// fgh_api.hip - the C ABI (include/fastgguf_hip.h): context, upload, dispatch and helpers.
+// No entry point aborts or falls back to a CPU computation: failures return a negative status and
+// leave a message in the context, and the caller decides (fastgguf.c:2577-2581 recomputes on its
+// own CPU kernels).
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+
+#include "../../include/fastgguf_hip.h"
+#include "fgh_internal.h"
+
+static const int FG_BATCH = 64;  // prompt batch limit (fastgguf.c:2139)
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+struct fgh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint64_t vram = 0, budget = 0, used = 0;
+    int n_offloaded = 0, n_skip_type = 0, n_skip_mem = 0;
+    char name[96] = {0};
+    std::string err = "ok";
+    // scratch, grown on demand (gpu_grow_buf, fastgguf.c:2083-2091)
+    DevBuf x, y, aqs, ad, abs;
+    // what the activation buffers currently hold (fgh_act_quantize_dev)
+    bool act_q8 = false;
+    int64_t act_cols = 0;
+};
+
+struct fgh_tensor {
+    fgh_ctx *ctx;
+    uint32_t type;
+    int64_t cols, rows, n_mats;
+    int order;     // FGH_ORDER_ROW / FGH_ORDER_REPACKED (Q4_K); ROW otherwise
+    int nb;        // blocks per row (256-blocks for K-quants, 32-blocks for Q8_0)
+    int ntile;     // tiles per row group
+    int64_t gpm;   // row groups per matrix
+    int64_t groups;
+    uint8_t *dev;
+    uint64_t dev_bytes;
+};
+
+static int fail(fgh_ctx *c, int code, const char *fmt, ...) {
+    if (c) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof(buf), fmt, ap);
+        va_end(ap);
+        c->err = buf;
+    }
+    return code;
+}
+
+#define HIP_TRY(ctx, call)                                                                        \
+    do {                                                                                          \
+        hipError_t e_ = (call);                                                                   \
+        if (e_ != hipSuccess) return fail((ctx), FGH_ERR_DEVICE, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+static int grow(fgh_ctx *c, DevBuf &b, size_t need) {
+    if (need <= b.cap) return FGH_OK;
+    if (b.p) {
+        HIP_TRY(c, hipStreamSynchronize(c->stream));
+        HIP_TRY(c, hipFree(b.p));
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    size_t cap = std::max(need, (size_t)1 << 16);
+    HIP_TRY(c, hipMalloc(&b.p, cap));
+    b.cap = cap;
+    return FGH_OK;
+}
+
+static bool type_supported(uint32_t t) { return t == FGH_T_Q8_0 || t == FGH_T_Q4_K || t == FGH_T_Q6_K; }
+static int block_elems(uint32_t t) { return t == FGH_T_Q8_0 ? 32 : 256; }
+static int block_bytes(uint32_t t) { return t == FGH_T_Q8_0 ? 34 : t == FGH_T_Q4_K ? 144 : 210; }
+static int tile_bytes(uint32_t t) { return t == FGH_T_Q8_0 ? fgh::Q80_TILE : t == FGH_T_Q4_K ? fgh::Q4K_TILE : fgh::Q6K_TILE; }
+
+// activation buffers for ntok tokens of `cols` values, for the tensor's type
+static int ensure_act(fgh_ctx *c, uint32_t type, int64_t cols, int ntok) {
+    const int64_t nbk = cols / block_elems(type);
+    int rc;
+    if (type == FGH_T_Q8_0) {
+        if ((rc = grow(c, c->aqs, (size_t)ntok * nbk * 32)) || (rc = grow(c, c->ad, (size_t)ntok * nbk * 4)) ||
+            (rc = grow(c, c->abs, (size_t)ntok * nbk * 4)))
+            return rc;
+    } else {
+        if ((rc = grow(c, c->aqs, (size_t)ntok * nbk * 256)) || (rc = grow(c, c->ad, (size_t)ntok * nbk * 4)) ||
+            (rc = grow(c, c->abs, (size_t)ntok * nbk * 32)))
+            return rc;
+    }
+    return FGH_OK;
+}
+
+// quantize ntok rows of x (device, row stride ldx) for the type into the context's buffers
+static int quantize_dev(fgh_ctx *c, uint32_t type, int64_t cols, const float *x, int64_t ldx, int ntok) {
+    int rc = ensure_act(c, type, cols, ntok);
+    if (rc) return rc;
+    if (type == FGH_T_Q8_0) {
+        fgh::ActQ8 a{(int8_t *)c->aqs.p, (float *)c->ad.p, (int16_t *)c->abs.p};
+        HIP_TRY(c, fgh::launch_quant_q8(x, ldx, (int)(cols / 32), ntok, a, c->stream));
+    } else {
+        fgh::ActQ8K a{(int8_t *)c->aqs.p, (float *)c->ad.p, (int16_t *)c->abs.p};
+        HIP_TRY(c, fgh::launch_quant_q8k(x, ldx, (int)(cols / 256), ntok, a, c->stream));
+    }
+    c->act_q8 = type == FGH_T_Q8_0;
+    c->act_cols = cols;
+    return FGH_OK;
+}
+
+// decode kernel over the activations already in the context buffers (ntok tokens)
+static int matvec_launch(fgh_ctx *c, const fgh_tensor *t, float *y, int64_t ldy, int ntok, int32_t *ds, int32_t *dm) {
+    fgh::MvOut out{y, ldy, t->rows, t->gpm, ds, dm};
+    fgh::ActQ8K ak{(int8_t *)c->aqs.p, (float *)c->ad.p, (int16_t *)c->abs.p};
+    fgh::ActQ8 a8{(int8_t *)c->aqs.p, (float *)c->ad.p, (int16_t *)c->abs.p};
+    const void *act = t->type == FGH_T_Q8_0 ? (const void *)&a8 : (const void *)&ak;
+    HIP_TRY(c, fgh::launch_matvec((int)t->type, t->order, t->dev, t->nb, t->groups, ntok, act, out,
+                                  ds != nullptr, c->stream));
+    return FGH_OK;
+}
+
+static int check_tensor(fgh_ctx *c, const fgh_tensor *t) {
+    if (!c) return FGH_ERR_ARG;
+    if (!t || t->ctx != c || !t->dev) return fail(c, FGH_ERR_ARG, "invalid tensor handle");
+    return FGH_OK;
+}
+
+extern "C" {
+
+int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out) {
+    if (!out) return FGH_ERR_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return FGH_ERR_DEVICE;
+    if (device < 0) device = 0;
+    if (device >= n) return FGH_ERR_ARG;
+    if (hipSetDevice(device) != hipSuccess) return FGH_ERR_DEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return FGH_ERR_DEVICE;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return FGH_ERR_DEVICE;  // kernels are built for gfx950 only
+    fgh_ctx *c = new fgh_ctx();
+    c->device = device;
+    snprintf(c->name, sizeof(c->name), "%s (%s)", prop.name, prop.gcnArchName);
+    c->vram = prop.totalGlobalMem;
+    c->budget = budget_bytes ? budget_bytes : c->vram - c->vram / 8;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return FGH_ERR_DEVICE;
+    }
+    *out = c;
+    return FGH_OK;
+}
+
+void fgh_close(fgh_ctx *c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs})
+        if (b->p) hipFree(b->p);
+    hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int fgh_info(const fgh_ctx *c, fgh_info_t *out) {
+    if (!c || !out) return FGH_ERR_ARG;
+    memset(out, 0, sizeof(*out));
+    out->vram = c->vram;
+    out->budget = c->budget;
+    out->used = c->used;
+    out->n_offloaded = c->n_offloaded;
+    out->n_skip_type = c->n_skip_type;
+    out->n_skip_mem = c->n_skip_mem;
+    out->device = c->device;
+    snprintf(out->name, sizeof(out->name), "%s", c->name);
+    return FGH_OK;
+}
+
+const char *fgh_last_error(const fgh_ctx *c) { return c ? c->err.c_str() : "no context"; }
+
+int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_mats, int order,
+               const void *host, uint64_t nbytes, fgh_tensor **out) {
+    if (!c || !out) return FGH_ERR_ARG;
+    *out = nullptr;
+    if (!host || rows <= 0 || n_mats <= 0 || cols <= 0) return fail(c, FGH_ERR_ARG, "upload: bad shape");
+    if (!type_supported(type) || cols % block_elems(type) != 0 || cols / block_elems(type) > (1 << 24)) {
+        c->n_skip_type++;
+        return fail(c, FGH_SKIP_TYPE, "upload: type %u with %lld cols is not supported", type, (long long)cols);
+    }
+    const int64_t row_bytes = cols / block_elems(type) * block_bytes(type);
+    if ((uint64_t)(row_bytes * rows * n_mats) != nbytes)
+        return fail(c, FGH_ERR_ARG, "upload: nbytes %llu != %lld", (unsigned long long)nbytes,
+                    (long long)(row_bytes * rows * n_mats));
+    HIP_TRY(c, hipSetDevice(c->device));
+    fgh_tensor *t = new fgh_tensor();
+    t->ctx = c;
+    t->type = type;
+    t->cols = cols;
+    t->rows = rows;
+    t->n_mats = n_mats;
+    t->nb = (int)(cols / block_elems(type));
+    t->ntile = type == FGH_T_Q8_0 ? (t->nb + 3) / 4 : t->nb;
+    t->gpm = (rows + 7) / 8;
+    t->groups = t->gpm * n_mats;
+    if (type == FGH_T_Q4_K) {
+        // the reference repacks 2-D Q4_K matrices with rows % 8 == 0 (repack_tensor, 2486-2488)
+        t->order = order == FGH_ORDER_AUTO ? ((n_mats == 1 && rows % 8 == 0) ? FGH_ORDER_REPACKED : FGH_ORDER_ROW)
+                                           : (order == FGH_ORDER_REPACKED ? FGH_ORDER_REPACKED : FGH_ORDER_ROW);
+    } else {
+        t->order = FGH_ORDER_ROW;
+    }
+    t->dev_bytes = (uint64_t)t->groups * t->ntile * tile_bytes(type);
+    if (c->used + t->dev_bytes > c->budget) {
+        delete t;
+        c->n_skip_mem++;
+        return fail(c, FGH_SKIP_MEM, "upload: budget exceeded");
+    }
+    void *stage = nullptr;
+    if (hipMalloc(&t->dev, t->dev_bytes) != hipSuccess || hipMalloc(&stage, nbytes) != hipSuccess) {
+        if (t->dev) hipFree(t->dev);
+        delete t;
+        c->n_skip_mem++;
+        (void)hipGetLastError();
+        return fail(c, FGH_SKIP_MEM, "upload: device allocation failed");
+    }
+    hipError_t e = hipMemcpy(stage, host, nbytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = fgh::launch_relayout((const uint8_t *)stage, t->dev, (int)type, rows, t->nb, t->ntile, t->gpm,
+                                 (int64_t)t->dev_bytes, row_bytes, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    (void)hipFree(stage);
+    if (e != hipSuccess) {
+        (void)hipFree(t->dev);
+        delete t;
+        return fail(c, FGH_ERR_DEVICE, "upload: %s", hipGetErrorString(e));
+    }
+    c->used += t->dev_bytes;
+    c->n_offloaded++;
+    *out = t;
+    return FGH_OK;
+}
+
+void fgh_tensor_free(fgh_tensor *t) {
+    if (!t) return;
+    if (t->dev) {
+        (void)hipSetDevice(t->ctx->device);
+        (void)hipStreamSynchronize(t->ctx->stream);
+        (void)hipFree(t->dev);
+        t->ctx->used -= t->dev_bytes;
+    }
+    delete t;
+}
+
+// ---- device-resident entry points ----
+
+int fgh_matvec_multi_dev(fgh_ctx *c, int n, const fgh_tensor *const *t, const float *x, float *const *y) {
+    if (!c || !t || !x || !y || n < 1 || n > 4) return fail(c, FGH_ERR_ARG, "matvec_multi: bad arguments");
+    int rc;
+    for (int i = 0; i < n; i++) {
+        if ((rc = check_tensor(c, t[i]))) return rc;
+        if (!y[i]) return fail(c, FGH_ERR_ARG, "matvec_multi: null output");
+        if (t[i]->cols != t[0]->cols || (t[i]->type == FGH_T_Q8_0) != (t[0]->type == FGH_T_Q8_0))
+            return fail(c, FGH_ERR_ARG, "matvec_multi: tensors differ in cols or activation kind");
+    }
+    HIP_TRY(c, hipSetDevice(c->device));
+    if ((rc = quantize_dev(c, t[0]->type, t[0]->cols, x, t[0]->cols, 1))) return rc;
+    for (int i = 0; i < n; i++)
+        if ((rc = matvec_launch(c, t[i], y[i], 0, 1, nullptr, nullptr))) return rc;
+    return FGH_OK;
+}
+
+int fgh_act_quantize_dev(fgh_ctx *c, uint32_t type, int64_t cols, const float *x, int ntok) {
+    if (!c) return FGH_ERR_ARG;
+    if (!x || !type_supported(type) || cols <= 0 || cols % block_elems(type) || ntok < 1 || ntok > FG_BATCH)
+        return fail(c, FGH_ERR_ARG, "act_quantize: bad arguments");
+    HIP_TRY(c, hipSetDevice(c->device));
+    return quantize_dev(c, type, cols, x, cols, ntok);
+}
+
+int fgh_matvec_act_dev(fgh_ctx *c, const fgh_tensor *t, float *y) {
+    int rc = check_tensor(c, t);
+    if (rc) return rc;
+    if (!y) return fail(c, FGH_ERR_ARG, "matvec_act: null output");
+    if (c->act_cols != t->cols || c->act_q8 != (t->type == FGH_T_Q8_0))
+        return fail(c, FGH_ERR_ARG, "matvec_act: the prepared activation does not match the tensor");
+    HIP_TRY(c, hipSetDevice(c->device));
+    return matvec_launch(c, t, y, 0, 1, nullptr, nullptr);
+}
+
+int fgh_matvec_dev(fgh_ctx *c, const fgh_tensor *t, const float *x, float *y) {
+    const fgh_tensor *tt[1] = {t};
+    float *yy[1] = {y};
+    return fgh_matvec_multi_dev(c, 1, tt, x, yy);
+}
+
+int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, float *Y, int ldy, int nb) {
+    int rc = check_tensor(c, t);
+    if (rc) return rc;
+    if (!X || !Y || nb < 1 || nb > FG_BATCH || ldx < t->cols || ldy < t->rows * t->n_mats)
+        return fail(c, FGH_ERR_ARG, "matmul: bad arguments");
+    HIP_TRY(c, hipSetDevice(c->device));
+    if (nb >= 8) return fail(c, FGH_ERR, "matmul: the prompt GEMM for nb >= 8 is not available in this build");
+    if ((rc = quantize_dev(c, t->type, t->cols, X, ldx, nb))) return rc;
+    return matvec_launch(c, t, Y, ldy, nb, nullptr, nullptr);
+}
+
+int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *, const fgh_tensor *, const fgh_tensor *, int,
+                    const float *, const float *, float *, int) {
+    return fail(c, FGH_ERR, "moe_ffn: not available in this build");
+}
+
+// ---- host-pointer entry points (synchronous) ----
+
+int fgh_matvec_multi(fgh_ctx *c, int n, const fgh_tensor *const *t, const float *x, float *const *y) {
+    if (!c || !t || !x || !y || n < 1 || n > 4) return fail(c, FGH_ERR_ARG, "matvec_multi: bad arguments");
+    int rc;
+    int64_t total = 0;
+    for (int i = 0; i < n; i++) {
+        if ((rc = check_tensor(c, t[i]))) return rc;
+        total += t[i]->rows * t[i]->n_mats;
+    }
+    HIP_TRY(c, hipSetDevice(c->device));
+    if ((rc = grow(c, c->x, (size_t)t[0]->cols * 4)) || (rc = grow(c, c->y, (size_t)total * 4))) return rc;
+    HIP_TRY(c, hipMemcpyAsync(c->x.p, x, (size_t)t[0]->cols * 4, hipMemcpyHostToDevice, c->stream));
+    float *yd[4];
+    int64_t off = 0;
+    for (int i = 0; i < n; i++) {
+        yd[i] = (float *)c->y.p + off;
+        off += t[i]->rows * t[i]->n_mats;
+    }
+    if ((rc = fgh_matvec_multi_dev(c, n, t, (const float *)c->x.p, yd))) return rc;
+    for (int i = 0; i < n; i++)
+        HIP_TRY(c, hipMemcpyAsync(y[i], yd[i], (size_t)(t[i]->rows * t[i]->n_mats) * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return FGH_OK;
+}
+
+int fgh_matvec(fgh_ctx *c, const fgh_tensor *t, const float *x, float *y) {
+    const fgh_tensor *tt[1] = {t};
+    float *yy[1] = {y};
+    return fgh_matvec_multi(c, 1, tt, x, yy);
+}
+
+int fgh_matmul(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, float *Y, int ldy, int nb) {
+    int rc = check_tensor(c, t);
+    if (rc) return rc;
+    const int64_t nout = t->rows * t->n_mats;
+    if (!X || !Y || nb < 1 || nb > FG_BATCH || ldx < t->cols || ldy < nout)
+        return fail(c, FGH_ERR_ARG, "matmul: bad arguments");
+    HIP_TRY(c, hipSetDevice(c->device));
+    if ((rc = grow(c, c->x, (size_t)nb * t->cols * 4)) || (rc = grow(c, c->y, (size_t)nb * nout * 4))) return rc;
+    HIP_TRY(c, hipMemcpy2DAsync(c->x.p, (size_t)t->cols * 4, X, (size_t)ldx * 4, (size_t)t->cols * 4, nb,
+                                hipMemcpyHostToDevice, c->stream));
+    if ((rc = fgh_matmul_dev(c, t, (const float *)c->x.p, (int)t->cols, (float *)c->y.p, (int)nout, nb))) return rc;
+    HIP_TRY(c, hipMemcpy2DAsync(Y, (size_t)ldy * 4, c->y.p, (size_t)nout * 4, (size_t)nout * 4, nb,
+                                hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return FGH_OK;
+}
+
+int fgh_moe_ffn(fgh_ctx *c, const fgh_tensor *, const fgh_tensor *, const fgh_tensor *, int, const float *,
+                const float *, float *, int, int32_t *, float *) {
+    return fail(c, FGH_ERR, "moe_ffn: not available in this build");
+}
+
+// ---- memory, stream, events ----
+
+int fgh_dev_alloc(fgh_ctx *c, uint64_t bytes, void **ptr) {
+    if (!c || !ptr) return FGH_ERR_ARG;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipMalloc(ptr, bytes ? bytes : 1));
+    return FGH_OK;
+}
+int fgh_dev_free(fgh_ctx *c, void *p) {
+    if (!c) return FGH_ERR_ARG;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    HIP_TRY(c, hipFree(p));
+    return FGH_OK;
+}
+int fgh_copy_h2d(fgh_ctx *c, void *dst, const void *src, uint64_t bytes) {
+    if (!c) return FGH_ERR_ARG;
+    HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return FGH_OK;
+}
+int fgh_copy_d2h(fgh_ctx *c, void *dst, const void *src, uint64_t bytes) {
+    if (!c) return FGH_ERR_ARG;
+    HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return FGH_OK;
+}
+int fgh_sync(fgh_ctx *c) {
+    if (!c) return FGH_ERR_ARG;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return FGH_OK;
+}
+int fgh_event_create(fgh_ctx *c, void **ev) {
+    if (!c || !ev) return FGH_ERR_ARG;
+    HIP_TRY(c, hipEventCreate((hipEvent_t *)ev));
+    return FGH_OK;
+}
+int fgh_event_record(fgh_ctx *c, void *ev) {
+    if (!c || !ev) return FGH_ERR_ARG;
+    HIP_TRY(c, hipEventRecord((hipEvent_t)ev, c->stream));
+    return FGH_OK;
+}
+int fgh_event_elapsed_ms(fgh_ctx *c, void *a, void *b, float *ms) {
+    if (!c || !a || !b || !ms) return FGH_ERR_ARG;
+    HIP_TRY(c, hipEventSynchronize((hipEvent_t)b));
+    HIP_TRY(c, hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+    return FGH_OK;
+}
+int fgh_event_destroy(fgh_ctx *c, void *ev) {
+    if (!c || !ev) return FGH_ERR_ARG;
+    HIP_TRY(c, hipEventDestroy((hipEvent_t)ev));
+    return FGH_OK;
+}
+
+// ---- test hooks ----
+
+int fgh_quantize(fgh_ctx *c, int kind, const float *x, int n, void *out_blocks) {
+    if (!c || !x || !out_blocks || n <= 0) return FGH_ERR_ARG;
+    const uint32_t type = kind == FGH_ACT_Q8 ? FGH_T_Q8_0 : kind == FGH_ACT_Q8K ? FGH_T_Q4_K : 0;
+    if (!type) return fail(c, FGH_ERR_ARG, "quantize: bad kind");
+    const int be = block_elems(type), nbk = n / be;
+    if (nbk == 0) return FGH_OK;  // tails shorter than a block are ignored (n/32, n/256)
+    int rc;
+    HIP_TRY(c, hipSetDevice(c->device));
+    if ((rc = grow(c, c->x, (size_t)nbk * be * 4))) return rc;
+    HIP_TRY(c, hipMemcpyAsync(c->x.p, x, (size_t)nbk * be * 4, hipMemcpyHostToDevice, c->stream));
+    if ((rc = quantize_dev(c, type, (int64_t)nbk * be, (const float *)c->x.p, (int64_t)nbk * be, 1))) return rc;
+    const size_t qb = (size_t)nbk * (kind == FGH_ACT_Q8 ? 32 : 256), sb = (size_t)nbk * (kind == FGH_ACT_Q8 ? 2 : 16);
+    std::string qs(qb, '\0'), bs(sb * 2, '\0');
+    std::string d((size_t)nbk * 4, '\0');
+    HIP_TRY(c, hipMemcpyAsync(&qs[0], c->aqs.p, qb, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(&d[0], c->ad.p, (size_t)nbk * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(&bs[0], c->abs.p, sb * 2, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    uint8_t *o = (uint8_t *)out_blocks;
+    for (int b = 0; b < nbk; b++) {
+        if (kind == FGH_ACT_Q8) {  // {f32 d; i8 qs[32]; i16 s16[2]}
+            uint8_t *blk = o + (size_t)b * 40;
+            memcpy(blk, &d[(size_t)b * 4], 4);
+            memcpy(blk + 4, &qs[(size_t)b * 32], 32);
+            memcpy(blk + 36, &bs[(size_t)b * 4], 4);
+        } else {  // {f32 d; i8 qs[256]; i16 bsums[16]}, undoing the lane permutation
+            uint8_t *blk = o + (size_t)b * 292;
+            memcpy(blk, &d[(size_t)b * 4], 4);
+            for (int e = 0; e < 256; e++) {
+                const int cc = e >> 5, i = (e >> 2) & 7, k = e & 3;
+                blk[4 + e] = (uint8_t)qs[(size_t)b * 256 + 32 * i + 4 * cc + k];
+            }
+            memcpy(blk + 260, &bs[(size_t)b * 32], 32);
+        }
+    }
+    return FGH_OK;
+}
+
+int fgh_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *x, int32_t *sumi, int32_t *msum) {
+    int rc = check_tensor(c, t);
+    if (rc) return rc;
+    if (!x || !sumi || !msum) return fail(c, FGH_ERR_ARG, "block_ints: null pointer");
+    const int64_t nout = t->rows * t->n_mats;
+    const size_t nint = (size_t)nout * t->nb;
+    HIP_TRY(c, hipSetDevice(c->device));
+    void *ds = nullptr;
+    if ((rc = grow(c, c->x, (size_t)t->cols * 4)) || (rc = grow(c, c->y, (size_t)nout * 4))) return rc;
+    HIP_TRY(c, hipMalloc(&ds, nint * 8));
+    int32_t *dsi = (int32_t *)ds, *dmi = dsi + nint;
+    hipError_t e = hipMemcpyAsync(c->x.p, x, (size_t)t->cols * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        rc = quantize_dev(c, t->type, t->cols, (const float *)c->x.p, t->cols, 1);
+        if (!rc) rc = matvec_launch(c, t, (float *)c->y.p, 0, 1, dsi, dmi);
+        if (!rc) {
+            e = hipMemcpyAsync(sumi, dsi, nint * 4, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipMemcpyAsync(msum, dmi, nint * 4, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        }
+    }
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(ds);
+    if (rc) return rc;
+    if (e != hipSuccess) return fail(c, FGH_ERR_DEVICE, "block_ints: %s", hipGetErrorString(e));
+    return FGH_OK;
+}
+
+int fgh_fp16_to_f32(fgh_ctx *c, const uint16_t *h, int n, float *out) {
+    if (!c || !h || !out || n <= 0) return FGH_ERR_ARG;
+    HIP_TRY(c, hipSetDevice(c->device));
+    int rc;
+    if ((rc = grow(c, c->x, (size_t)n * 2)) || (rc = grow(c, c->y, (size_t)n * 4))) return rc;
+    HIP_TRY(c, hipMemcpyAsync(c->x.p, h, (size_t)n * 2, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, fgh::launch_fp16((const uint16_t *)c->x.p, (float *)c->y.p, n, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(out, c->y.p, (size_t)n * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return FGH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,136 @@
+// fgh_internal.h - device layouts and helpers shared by the gfx950 kernels of the fastgguf
+// backend. Internal: the public surface is include/fastgguf_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fgh {
+
+// ---------------------------------------------------------------------------------------------
+// Device weight layouts ("tiles"). Rows are interleaved in groups of 8, as the reference's CPU
+// repack does for Q4_K (q4kx8_t, fastgguf.c:2260-2266), so one wavefront of 64 lanes = 8 rows x 8
+// slices reads one contiguous tile per block with 16-byte loads. Lane (r, i) holds slice i of row
+// r; slice i of a 256-weight block is exactly the part of the block the reference's AVX2 fp32
+// accumulator lane i sums (its bytes 4i..4i+3 of every 32-byte chunk), so the per-lane integer
+// partials are the reference's lane partials, and the fp32 chains can follow its order.
+// Rows past the end of a matrix are zero-filled (d = 0) and never stored.
+//
+//   Q4_K tile, one block of 8 rows, 1152 B (= 8 x 144):
+//     [0, 128)     meta: row r at 16r = the block's first 16 bytes (fp16 d, fp16 dmin, scales12)
+//     [128, 1152)  quants: slice (r, i) at 128 + 16(8r + i); dword j = file bytes 16+32j+4i..+3
+//   Q6_K tile, one block of 8 rows, 1680 B (= 8 x 210):
+//     [0, 128)     int8 scales, row r at 16r (file bytes 192..207)
+//     [128, 144)   fp16 d, row r at 128 + 2r (file bytes 208..209)
+//     [144, 1168)  ql words, slice (r,i) at 144 + 16(8r+i): dword 2h+s = file bytes 64h+32s+4i..+3
+//     [1168, 1680) qh words, slice (r,i) at 1168 + 8(8r+i): dword h = file bytes 128+32h+4i..+3
+//   Q8_0 tile, 4 blocks of 8 rows, 1088 B (= 8 x 4 x 34):
+//     [0, 64)      fp16 d of row r, block bb at 8r + 2bb
+//     [64, 1088)   quants: slice (r, i) at 64 + 16(8r + i); dword bb = block bb's bytes 2+4i..+3
+// ---------------------------------------------------------------------------------------------
+constexpr int T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14;
+constexpr int Q4K_TILE = 1152, Q6K_TILE = 1680, Q80_TILE = 1088;
+
+// Device activation layouts. Q8_K (for Q4_K / Q6_K): per token, nb blocks of
+//   qs [nb][256] int8, permuted so lane i's 32 bytes are contiguous: position 32i + 4c + k holds
+//                 element 32c + 4i + k (an 8x8 transpose of the block's dwords)
+//   d  [nb] fp32, bs [nb][16] int16 (the reference's bsums)
+// Q8 (for Q8_0): per token, nb32 blocks of qs [nb32][32] int8 (natural order), d [nb32] fp32,
+//   s16 [nb32][2] int16.
+struct ActQ8K {
+    int8_t *qs;
+    float *d;
+    int16_t *bs;
+};
+struct ActQ8 {
+    int8_t *qs;
+    float *d;
+    int16_t *s16;
+};
+
+// ---- cross-lane helpers (DPP: no LDS traffic) ----
+__device__ __forceinline__ int dpp_xor1(int v) {  // quad_perm [1,0,3,2]
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+}
+__device__ __forceinline__ int dpp_xor2(int v) {  // quad_perm [2,3,0,1]
+    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+}
+__device__ __forceinline__ int dpp_half_mirror(int v) {  // lane j <-> 7-j within 8 lanes
+    return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+}
+// exact integer sum over the 8 lanes of a row group; every lane of the group gets the total
+__device__ __forceinline__ int sum8_i32(int v) {
+    v += dpp_xor1(v);
+    v += dpp_xor2(v);
+    v += dpp_half_mirror(v);
+    return v;
+}
+__device__ __forceinline__ int sum4_i32(int v) {
+    v += dpp_xor1(v);
+    v += dpp_xor2(v);
+    return v;
+}
+
+__device__ __forceinline__ float fp16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// sum of four int8 x int8 products plus c (v_dot4_i32_i8)
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+__device__ __forceinline__ int sbyte(uint32_t w, int k) {  // signed byte k of a dword
+    return (int)(int8_t)(w >> (8 * k));
+}
+__device__ __forceinline__ int ubyte(uint32_t w, int k) { return (int)((w >> (8 * k)) & 0xFF); }
+
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *(const uint4 *)p; }
+__device__ __forceinline__ uint2 ld8(const uint8_t *p) { return *(const uint2 *)p; }
+
+// Q4_K 12-byte scales -> sc (4 bytes each in lo/hi words) and mins, the word form of
+// scale_min_k4 (fastgguf.c:466-472) that unpack_scales_k4 (1057-1067) also uses
+struct Q4KScales {
+    uint32_t sc_lo, sc_hi, mn_lo, mn_hi;  // bytes: sc0..3, sc4..7, m0..3, m4..7
+};
+__device__ __forceinline__ Q4KScales q4k_scales(uint32_t u0, uint32_t u1, uint32_t u2) {
+    const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
+    Q4KScales s;
+    s.sc_lo = u0 & k1;
+    s.sc_hi = (u2 & k2) | (((u0 >> 6) & k3) << 4);
+    s.mn_lo = u1 & k1;
+    s.mn_hi = ((u2 >> 4) & k2) | (((u1 >> 6) & k3) << 4);
+    return s;
+}
+__device__ __forceinline__ int q4k_sc(const Q4KScales &s, int j) {
+    return ubyte(j < 4 ? s.sc_lo : s.sc_hi, j & 3);
+}
+__device__ __forceinline__ int q4k_mn(const Q4KScales &s, int j) {
+    return ubyte(j < 4 ? s.mn_lo : s.mn_hi, j & 3);
+}
+
+// output side of a decode matvec: row r of group g is row m * rows + gl * 8 + r of y, with
+// g = m * gpm + gl; dump_s / dump_m (test hook only) receive per (row, block) integers
+struct MvOut {
+    float *y;
+    int64_t ldy;   // token stride of y
+    int64_t rows;  // rows per matrix
+    int64_t gpm;   // row groups per matrix
+    int32_t *dump_s, *dump_m;
+    __device__ __forceinline__ int64_t row_of(int64_t g, int r, bool &ok) const {
+        const int64_t m = g / gpm, gl = g - m * gpm, lr = gl * 8 + r;
+        ok = lr < rows;
+        return m * rows + lr;
+    }
+};
+
+// host-side launchers (fgh_kernels.hip)
+hipError_t launch_quant_q8k(const float *x, int64_t ldx, int nb, int ntok, ActQ8K act, hipStream_t s);
+hipError_t launch_quant_q8(const float *x, int64_t ldx, int nb, int ntok, ActQ8 act, hipStream_t s);
+hipError_t launch_relayout(const uint8_t *src, uint8_t *dst, int type, int64_t rows, int nb, int ntile,
+                           int64_t gpm, int64_t total, int64_t row_bytes, hipStream_t s);
+hipError_t launch_fp16(const uint16_t *h, float *out, int n, hipStream_t s);
+hipError_t launch_matvec(int type, int order, const uint8_t *W, int nb, int64_t groups, int ntok,
+                         const void *act, MvOut out, bool dump, hipStream_t s);
+
+}  // namespace fgh

@@ -1,0 +1,171 @@
+/*
+ * fastgguf_hip.h - C ABI of the MI355X (gfx950) backend for fastgguf's quantized
+ * weight x Q8-activation hot path: GGUF Q4_K / Q6_K / Q8_0 weights multiplied by activations
+ * quantized to the reference's Q8 / Q8_K blocks, as a decode matvec, a <=64-token prompt matmul
+ * and a mixture-of-experts FFN over the router-selected experts.
+ *
+ * The ABI is plain C: fixed-width integers, plain pointers and sizes, opaque handles, no
+ * callbacks, no varargs, no C++ or torch types. A Rust `extern "C"` block or a C caller binds it
+ * directly. Every entry point returns FGH_OK (0) or a negative FGH_* status and never aborts; a
+ * caller treats any non-zero status the way fastgguf.c treats a failed fg_gpu_matvec
+ * (fastgguf.c:2577-2581): report it and recompute on its own CPU kernels.
+ *
+ * Results are those of the reference's CPU kernels (the ones `fastgguf selftest` checks), not of
+ * its OpenCL kernels: activations are quantized exactly as quantize_q8 / quantize_q8k
+ * (fastgguf.c:746-793) do, per-block integer dot products are exact, and the fp32 outputs follow
+ * the reference's accumulation order for matvec and MoE (bit-identical) and agree to within
+ * 1e-5 relative per output vector for the MFMA prompt GEMM.
+ *
+ * Threading: a context is used by one host thread at a time, like the reference's g_gpu state
+ * (fastgguf.c:1845-1857). Host-pointer calls are synchronous: outputs are valid on return, as
+ * with fg_gpu_matvec_raw's blocking read (fastgguf.c:2110). *_dev calls take device pointers and
+ * are asynchronous on the context's stream.
+ */
+#ifndef FASTGGUF_HIP_H
+#define FASTGGUF_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FGH_ABI_VERSION 1
+
+/* exported from the shared library (built with -fvisibility=hidden) */
+#if defined(__GNUC__) || defined(__clang__)
+#define FGH_API __attribute__((visibility("default")))
+#else
+#define FGH_API
+#endif
+
+/* GGML tensor types handled here (the reference's enum, fastgguf.c:215-221) */
+#define FGH_T_Q8_0 8u
+#define FGH_T_Q4_K 12u
+#define FGH_T_Q6_K 14u
+
+/* status codes */
+#define FGH_OK 0
+#define FGH_ERR (-1)           /* operation failed (the reference's -1 from fg_gpu_matvec) */
+#define FGH_ERR_ARG (-2)       /* bad argument or shape mismatch */
+#define FGH_SKIP_TYPE (-3)     /* upload: unsupported type or cols not a block multiple */
+#define FGH_SKIP_MEM (-4)      /* upload: over the memory budget, or device allocation failed */
+#define FGH_ERR_DEVICE (-5)    /* no usable device, or a HIP runtime error */
+
+/* fp32 accumulation order of a Q4_K tensor's matvec: which reference kernel it reproduces */
+#define FGH_ORDER_AUTO (-1)    /* what the reference CPU path would pick (repack_tensor, 2486) */
+#define FGH_ORDER_ROW 0        /* dot_q4_K_q8k (fastgguf.c:1118), file-layout rows */
+#define FGH_ORDER_REPACKED 1   /* dot_q4Kx8 (fastgguf.c:2322), the 8-row repacked layout */
+
+/* activation block kinds for the quantizer test hook (type_uses_q8, fastgguf.c:2167) */
+#define FGH_ACT_Q8 1           /* q8_blk_t  {f32 d; i8 qs[32];  i16 s16[2];}    40 bytes */
+#define FGH_ACT_Q8K 2          /* q8k_blk_t {f32 d; i8 qs[256]; i16 bsums[16];} 292 bytes */
+
+typedef struct fgh_ctx fgh_ctx;
+typedef struct fgh_tensor fgh_tensor;
+
+/* counters mirroring g_gpu (fastgguf.c:1845-1857) */
+typedef struct {
+    uint64_t vram;          /* device memory in bytes */
+    uint64_t budget;        /* weight memory budget in bytes */
+    uint64_t used;          /* bytes held by uploaded tensors */
+    int32_t n_offloaded;    /* tensors uploaded */
+    int32_t n_skip_type;    /* uploads refused: unsupported type / shape */
+    int32_t n_skip_mem;     /* uploads refused: over budget / allocation failed */
+    int32_t device;         /* HIP device index */
+    char name[96];          /* device name */
+} fgh_info_t;
+
+/* ---- context: replaces fg_gpu_init / fg_gpu_init_ex (fastgguf.c:1968-2057) ----
+ * device < 0 picks device 0 (the reference's FASTGGUF_GPU_DEVICE default is the largest discrete
+ * GPU; on a one-GPU MI355X box that is device 0). budget_bytes == 0 means 87.5 % of device memory
+ * (fastgguf.c:2045). Runs a self-check of every kernel against exact integer results on a small
+ * seeded case (the role of gpu_selfcheck, 1898-1965); on any failure returns < 0 and *out = NULL,
+ * and the caller stays on the CPU. */
+FGH_API int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out);
+FGH_API void fgh_close(fgh_ctx *ctx);
+FGH_API int fgh_info(const fgh_ctx *ctx, fgh_info_t *out);
+/* message for the last failing call on this context (never NULL) */
+FGH_API const char *fgh_last_error(const fgh_ctx *ctx);
+
+/* ---- upload: replaces gpu_upload_tensor (fastgguf.c:2060-2081) ----
+ * host_data holds n_mats x rows x row_bytes(type, cols) bytes in the GGUF file layout (a 2-D
+ * tensor has n_mats = 1; a 3-D MoE expert tensor [n_mats][rows][cols] has n_mats = n_expert).
+ * The copy is synchronous; the device copy is re-laid out for the kernels (rows interleaved in
+ * groups of 8, as the reference's CPU repack does, fastgguf.c:2237-2282). Returns FGH_SKIP_TYPE /
+ * FGH_SKIP_MEM like the reference's n_skip_type / n_skip_mem paths, with *out = NULL. */
+FGH_API int fgh_upload(fgh_ctx *ctx, uint32_t ggml_type, int64_t cols, int64_t rows, int64_t n_mats,
+               int order, const void *host_data, uint64_t nbytes, fgh_tensor **out);
+FGH_API void fgh_tensor_free(fgh_tensor *t);
+
+/* ---- matvec: replaces fg_gpu_matvec (fastgguf.c:2114) and the CPU matvec (2575) ----
+ * y[r] = dot(W[r], Q8(x)) for all rows of all matrices (rows * n_mats outputs); x has cols
+ * floats. Host pointers, synchronous. */
+FGH_API int fgh_matvec(fgh_ctx *ctx, const fgh_tensor *t, const float *x, float *y);
+
+/* ---- matvec_multi: replaces matvec_multi (fastgguf.c:2552) ----
+ * n <= 4 tensors with the same cols read the same x, which is quantized once. */
+FGH_API int fgh_matvec_multi(fgh_ctx *ctx, int n, const fgh_tensor *const *t, const float *x, float *const *y);
+
+/* ---- matmul: replaces matmul (fastgguf.c:3004) for nb <= 64 tokens ----
+ * Y[tok * ldy + r] = dot(W[r], Q8(X[tok * ldx ...])). nb >= 8 runs the int8 MFMA prompt GEMM
+ * (the role of gemm_kquant 2818 / gemm_q32 2981); nb < 8 runs the decode kernel per token, as the
+ * reference does for repacked tensors (3006-3009). */
+FGH_API int fgh_matmul(fgh_ctx *ctx, const fgh_tensor *t, const float *X, int ldx, float *Y, int ldy, int nb);
+
+/* ---- MoE FFN: replaces moe_ffn (fastgguf.c:4588) for n_tok tokens ----
+ * gate, up: 3-D tensors [n_expert][ff][n_embd]; down: [n_expert][n_embd][ff].
+ * logits: [n_tok][n_expert] router outputs (the reference's matvec(ffn_gate_inp), 4593).
+ * X, Y: [n_tok][n_embd]. Each token is routed independently (softmax, top-k, renormalise,
+ * 4594-4604); tokens are grouped by expert on the device. sel_out / w_out ([n_tok][k], optional,
+ * may be NULL) receive the selected experts and their weights. */
+FGH_API int fgh_moe_ffn(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tensor *up, const fgh_tensor *down,
+                int k, const float *logits, const float *X, float *Y, int n_tok,
+                int32_t *sel_out, float *w_out);
+
+/* ---- device-resident variants: device pointers, asynchronous on the context stream ----
+ * These skip the host<->device copies of the synchronous calls above (the copies fastgguf.c
+ * makes at 2102 and 2110), for callers that keep activations in device memory. */
+FGH_API int fgh_matvec_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *x_dev, float *y_dev);
+FGH_API int fgh_matvec_multi_dev(fgh_ctx *ctx, int n, const fgh_tensor *const *t, const float *x_dev,
+                         float *const *y_dev);
+FGH_API int fgh_matmul_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *X_dev, int ldx, float *Y_dev,
+                   int ldy, int nb);
+FGH_API int fgh_moe_ffn_dev(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tensor *up,
+                    const fgh_tensor *down, int k, const float *logits_dev, const float *X_dev,
+                    float *Y_dev, int n_tok);
+
+/* The two halves of a device-resident matvec, for callers that quantize one activation once and
+ * multiply it with several tensors at different times (the reference's quantize_act, 2176, and
+ * its row loop, 2612). fgh_act_quantize_dev quantizes ntok vectors of cols floats (row stride
+ * cols) for ggml_type's activation kind into the context; fgh_matvec_act_dev multiplies the
+ * context's current activation (token 0) with t, which must match its kind and cols. */
+FGH_API int fgh_act_quantize_dev(fgh_ctx *ctx, uint32_t ggml_type, int64_t cols, const float *x_dev, int ntok);
+FGH_API int fgh_matvec_act_dev(fgh_ctx *ctx, const fgh_tensor *t, float *y_dev);
+
+/* ---- device memory, stream and timing helpers (for device-resident callers and benchmarks) */
+FGH_API int fgh_dev_alloc(fgh_ctx *ctx, uint64_t bytes, void **ptr);
+FGH_API int fgh_dev_free(fgh_ctx *ctx, void *ptr);
+FGH_API int fgh_copy_h2d(fgh_ctx *ctx, void *dst_dev, const void *src_host, uint64_t bytes);
+FGH_API int fgh_copy_d2h(fgh_ctx *ctx, void *dst_host, const void *src_dev, uint64_t bytes);
+FGH_API int fgh_sync(fgh_ctx *ctx);
+/* HIP events recorded on the context stream */
+FGH_API int fgh_event_create(fgh_ctx *ctx, void **ev);
+FGH_API int fgh_event_record(fgh_ctx *ctx, void *ev);
+FGH_API int fgh_event_elapsed_ms(fgh_ctx *ctx, void *ev_start, void *ev_stop, float *ms);
+FGH_API int fgh_event_destroy(fgh_ctx *ctx, void *ev);
+
+/* ---- test hooks (bit-exactness checks; not needed by a production caller) ----
+ * fgh_quantize: the device quantizer's output in the reference struct layout (kind FGH_ACT_Q8:
+ * n/32 blocks of 40 bytes; FGH_ACT_Q8K: n/256 blocks of 292 bytes), from host x.
+ * fgh_block_ints: per (row, block) integer parts of dot(W[r], Q8(x)) as the device kernels
+ * compute them: sumi / msum [rows * n_mats][blocks per row] (see the oracle's fgo_block_ints).
+ * fgh_fp16_to_f32: the device's fp16 -> fp32 decode of n codes. */
+FGH_API int fgh_quantize(fgh_ctx *ctx, int kind, const float *x, int n, void *out_blocks);
+FGH_API int fgh_block_ints(fgh_ctx *ctx, const fgh_tensor *t, const float *x, int32_t *sumi, int32_t *msum);
+FGH_API int fgh_fp16_to_f32(fgh_ctx *ctx, const uint16_t *h, int n, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

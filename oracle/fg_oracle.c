@@ -47,8 +47,18 @@ float fgo_fp16(uint16_t h) {
 
 static inline uint16_t rd16(const uint8_t *p) { uint16_t v; memcpy(&v, p, 2); return v; }
 
+/* FGO_MUTATE (tests only, tests/test_oracle.py) builds a copy of this oracle with one planted
+ * mistake, to show that the golden vectors catch it. 0 = the real oracle. */
+#ifndef FGO_MUTATE
+#define FGO_MUTATE 0
+#endif
+
 static inline float hsum8(const float v[8]) {
+#if FGO_MUTATE == 1 /* sequential lane sum instead of the hsum_ps tree */
+    return ((((((v[0] + v[1]) + v[2]) + v[3]) + v[4]) + v[5]) + v[6]) + v[7];
+#else
     return ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+#endif
 }
 static inline float hsum4(const float v[4]) { return (v[0] + v[1]) + (v[2] + v[3]); }
 
@@ -63,7 +73,11 @@ void fgo_quantize_q8(const float *x, fgo_q8_blk *out, int n) {
             float a = fabsf(xb[j]);
             if (a > amax) amax = a;
         }
+#if FGO_MUTATE == 3 /* reciprocal multiply instead of the IEEE division */
+        float d = amax * (1.0f / 127.0f);
+#else
         float d = amax / 127.0f;
+#endif
         float id = d > 0.0f ? 1.0f / d : 0.0f;
         out[b].d = d;
         int s0 = 0, s1 = 0;
@@ -203,8 +217,13 @@ float fgo_dot_q4_K_rp(const uint8_t *row, const fgo_q8k_blk *y, int nb) {
         int32_t sumi, msum;
         q4k_block_ints(p, &y[b], &sumi, &msum);
         float yd = y[b].d;
+#if FGO_MUTATE == 5 /* one chain: the min term subtracted block by block */
+        acc = fmaf(fgo_fp16(rd16(p)) * yd, (float)sumi, acc);
+        acc = fmaf(-(fgo_fp16(rd16(p + 2)) * yd), (float)msum, acc);
+#else
         acc = fmaf(fgo_fp16(rd16(p)) * yd, (float)sumi, acc);
         macc = fmaf(fgo_fp16(rd16(p + 2)) * yd, (float)msum, macc);
+#endif
     }
     return acc - macc;
 }
@@ -230,7 +249,11 @@ float fgo_dot_q6_K(const uint8_t *row, const fgo_q8k_blk *y, int nb) {
                         int e = 128 * h + 32 * k + t;
                         s += q6k_val(p, e) * q8[e];
                     }
+#if FGO_MUTATE == 4 /* the per-16 scale of the upper half-lane dropped */
+                    lane += sc[8 * h + 2 * k] * s;
+#else
                     lane += sc[8 * h + 2 * k + (i >= 4)] * s;
+#endif
                 }
             acc[i] = fmaf(dd, (float)lane, acc[i]);
         }
@@ -413,8 +436,25 @@ static void gemm_row_token(uint32_t type, const uint8_t *rb, const void *act, in
                     uint8_t q = p[16 + 32 * (g >> 1) + l];
                     ia += ((g & 1) ? (q >> 4) : (q & 0x0F)) * y[b].qs[e];
                 }
+#if FGO_MUTATE == 6 /* integer scale sum first, one conversion per block (not the GEMM order) */
+                a += 0.0f * (float)ia;
+            }
+            {
+                int isum = 0;
+                for (int g = 0; g < 8; g++) {
+                    int ia = 0;
+                    for (int l = 0; l < 32; l++) {
+                        uint8_t q = p[16 + 32 * (g >> 1) + l];
+                        ia += ((g & 1) ? (q >> 4) : (q & 0x0F)) * y[b].qs[32 * g + l];
+                    }
+                    isum += sc[g] * ia;
+                }
+                a = d * (float)isum;
+            }
+#else
                 a = fmaf(d * (float)sc[g], (float)ia, a);
             }
+#endif
             for (int g = 0; g < 8; g++) {
                 float bs = (float)(y[b].bsums[2 * g] + y[b].bsums[2 * g + 1]);
                 a = fmaf(-(dmin * (float)mn[g]), bs, a);
@@ -526,7 +566,14 @@ void fgo_moe_route(const float *logits, int n_expert, int k, int32_t *sel, float
 /* the reference's down loop: s = s + w_j * dot (4626-4635). gcc contracts this statement to a
  * fused multiply-add under -O3 -march=native (fp-contract=fast, the GNU C default); the golden
  * vectors written by the compiled reference fix which form is used. */
-static float moe_accum(float s, float wj, float dot) { return fmaf(wj, dot, s); }
+static float moe_accum(float s, float wj, float dot) {
+#if FGO_MUTATE == 2 /* separately rounded multiply and add */
+    volatile float p = wj * dot;
+    return s + p;
+#else
+    return fmaf(wj, dot, s);
+#endif
+}
 
 int fgo_moe_down(uint32_t type_down, const uint8_t *down, int n_embd, int ff, int k,
                  const int32_t *sel, const float *w, const float *h, float *out) {

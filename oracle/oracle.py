@@ -208,6 +208,11 @@ class Reference:
                                  C.c_void_p, C.c_int, C.c_int]
         L.fgr_moe_ffn.argtypes = [C.c_uint32] * 3 + [C.c_void_p] * 3 + [C.c_int] * 4 + \
             [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+        L.fgr_tensor_new.restype = C.c_void_p
+        L.fgr_tensor_new.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int]
+        L.fgr_tensor_free.argtypes = [C.c_void_p]
+        L.fgr_tensor_free.restype = None
+        L.fgr_tensor_matvec_multi.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
         L.fgr_init(256)
 
     @property
@@ -250,6 +255,23 @@ class Reference:
         if self.lib.fgr_matmul(type_, int(repack), _ptr(w), rows, cols, _ptr(X), cols, _ptr(Y), rows, nb) != 0:
             raise ValueError("fgr_matmul failed")
         return Y
+
+    def tensor(self, type_, w, cols, repack=False):
+        """A persistent reference tensor (repacked once); returns an opaque handle."""
+        w = np.ascontiguousarray(w, np.uint8)
+        h = self.lib.fgr_tensor_new(type_, int(repack), _ptr(w), w.shape[0], cols)
+        if not h:
+            raise ValueError("fgr_tensor_new failed")
+        return h
+
+    def tensor_free(self, h):
+        self.lib.fgr_tensor_free(h)
+
+    def tensor_matvec_multi(self, hs, x, ys):
+        arr = (C.c_void_p * len(hs))(*hs)
+        yp = (C.c_void_p * len(ys))(*[y.ctypes.data for y in ys])
+        if self.lib.fgr_tensor_matvec_multi(len(hs), arr, _ptr(x), yp) != 0:
+            raise ValueError("fgr_tensor_matvec_multi failed")
 
     def moe_ffn(self, types, gate, up, down, n_expert, k, n_embd, ff, logits, X):
         X = np.ascontiguousarray(X, np.float32)

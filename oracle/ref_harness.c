@@ -145,3 +145,29 @@ FGR_EXPORT int fgr_moe_ffn(uint32_t tg_type, uint32_t tu_type, uint32_t td_type,
     free(mm->moe_xq); free(mm->moe_xk); free(mm); free(router);
     return rc;
 }
+
+/* persistent tensors for timing the reference's CPU path (bench.py cpu_baseline): the 8-row
+ * repack happens once, as at model load (4542-4557), and each call is one matvec / matvec_multi */
+typedef struct { tensor_t t; uint8_t *copy; } fgr_tensor;
+
+FGR_EXPORT void *fgr_tensor_new(uint32_t type, int repack, const uint8_t *w, int64_t rows, int cols) {
+    fgr_tensor *h = (fgr_tensor *)calloc(1, sizeof(fgr_tensor));
+    if (!h) return NULL;
+    fgr_init(cols);
+    if (make_tensor(&h->t, type, repack, w, rows, cols, &h->copy) != 0) { free(h); return NULL; }
+    return h;
+}
+
+FGR_EXPORT void fgr_tensor_free(void *p) {
+    fgr_tensor *h = (fgr_tensor *)p;
+    if (!h) return;
+    drop_tensor(&h->t, h->copy);
+    free(h);
+}
+
+FGR_EXPORT int fgr_tensor_matvec_multi(int n, void *const *hs, const float *x, float *const *y) {
+    tensor_t *tp[4];
+    if (n < 1 || n > 4) return -1;
+    for (int i = 0; i < n; i++) tp[i] = &((fgr_tensor *)hs[i])->t;
+    return n == 1 ? matvec(tp[0], x, y[0]) : matvec_multi(n, tp, x, y);
+}

@@ -1,0 +1,106 @@
+"""Writes the golden vectors in tests/golden/*.npz with the reference's own kernels.
+
+Run in a container where lawnak/FastGGUF is mounted at /root/reference:
+
+    make -C oracle ref && python tests/golden/make_golden.py
+
+It loads oracle/_ref/libfgref_vnni.so (fastgguf.c compiled from where it lies, AVX-512-VNNI
+build; ref_harness.c exports its static kernels) and records inputs and outputs only: weight
+bytes, activations, quantized blocks, outputs. The fixtures are data; no reference source or
+binary is stored. Seeds are fixed, so re-running reproduces the same files.
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+from fastgguf_amd import synth as S  # noqa: E402
+from oracle import Reference  # noqa: E402
+
+
+def quant_inputs() -> np.ndarray:
+    """Activation rows for the quantizer fixtures: normal values plus the edge cases the
+    quantizers must get right (all-zero block, exact .5 ties after scaling, a single huge value,
+    negative-zero, subnormals)."""
+    rng = np.random.Generator(np.random.PCG64(101))
+    x = rng.standard_normal((6, 1024)).astype(np.float32)
+    x[1, :256] = 0.0                          # all-zero Q8_K block -> d = id = 0, q = 0
+    x[1, 256:288] = 0.0                       # all-zero Q8 block
+    x[2, :256] = np.arange(256) - 127.5       # amax 128 -> halfway cases
+    x[2, 256:512] = (np.arange(256) % 64 - 32) * 0.5 + 0.25
+    x[3, :] *= 1e3
+    x[3, 5] = 3e4                             # one dominant value per block
+    x[4, :] = -0.0
+    x[4, 512:] = rng.standard_normal(512).astype(np.float32) * 1e-39  # subnormals
+    x[5, :] = np.float32(127.0) * (rng.integers(-3, 4, 1024) / 2.0)   # exact ties x*id = k + .5
+    return x
+
+
+def main() -> None:
+    ref = Reference("vnni")
+    print("reference build:", ref.build, "threads:", ref.threads())
+    out = {}
+
+    x = quant_inputs()
+    out["quant_x"] = x
+    out["quant_q8"] = np.stack([ref.quantize_q8(r) for r in x]).view(np.uint8)
+    out["quant_q8k"] = np.stack([ref.quantize_q8k(r) for r in x]).view(np.uint8)
+    np.savez_compressed(os.path.join(HERE, "quantize.npz"), **out)
+
+    # single-token matvecs: per type, synthetic (benchmark distributions) and random-byte rows
+    mv = {}
+    cases = [("q8_0", S.T_Q8_0, 24, 512), ("q4_k", S.T_Q4_K, 24, 768), ("q6_k", S.T_Q6_K, 24, 512)]
+    for name, t, rows, cols in cases:
+        for gname, gen in (("synth", S.weights), ("bytes", S.random_bytes_weights)):
+            w = gen(t, rows, cols, 200 + t)
+            xv = S.activations(cols, 300 + t)
+            key = f"{name}_{gname}"
+            mv[f"{key}_w"] = w
+            mv[f"{key}_x"] = xv
+            mv[f"{key}_y"] = ref.matvec(t, w, cols, xv)
+            if t == S.T_Q4_K:
+                mv[f"{key}_y_rp"] = ref.matvec(t, w, cols, xv, repack=True)
+    np.savez_compressed(os.path.join(HERE, "matvec.npz"), **mv)
+
+    # prompt batches through matmul: 3 tokens (x4 tiles / repacked per-token) and 8, 45 (GEMM)
+    mm = {}
+    for name, t, rows, cols in [("q8_0", S.T_Q8_0, 20, 512), ("q4_k", S.T_Q4_K, 24, 512), ("q6_k", S.T_Q6_K, 20, 512)]:
+        w = S.weights(t, rows, cols, 400 + t)
+        mm[f"{name}_w"] = w
+        for nb in (3, 8, 45):
+            X = S.activations(cols, 500 + nb, rows=nb)
+            mm[f"{name}_X{nb}"] = X
+            mm[f"{name}_Y{nb}"] = ref.matmul(t, w, cols, X)
+            if t == S.T_Q4_K:
+                mm[f"{name}_Y{nb}_rp"] = ref.matmul(t, w, cols, X, repack=True)
+    np.savez_compressed(os.path.join(HERE, "matmul.npz"), **mm)
+
+    # MoE: 8 experts, top-3 (the reference selftest's shape, 5938-6020), n_embd 256, ff 256,
+    # 4 tokens, Q4_K experts. X[:, 0] = 1 lets the harness reproduce the given router logits
+    # through the reference's own router matvec.
+    E, K, D, F, T = 8, 3, 256, 256, 4
+    g = S.weights(S.T_Q4_K, E * F, D, 601)
+    u = S.weights(S.T_Q4_K, E * F, D, 602)
+    d = S.weights(S.T_Q4_K, E * D, F, 603)
+    X = S.activations(D, 604, rows=T)
+    X[:, 0] = 1.0
+    L = S.router_logits(T, E, 605)
+    L[2, 3] = L[2, 7] = L[2].max() + 1.0     # a tie on top: argmax keeps the lower index
+    L[3, :] = 0.0                            # all equal: selection 0, 1, 2
+    Y, sel, w = ref.moe_ffn((S.T_Q4_K,) * 3, g, u, d, E, K, D, F, L, X)
+    np.savez_compressed(os.path.join(HERE, "moe.npz"), gate=g, up=u, down=d, X=X, logits=L, Y=Y, sel=sel, w=w,
+                        dims=np.array([E, K, D, F, T]))
+    for f in sorted(os.listdir(HERE)):
+        if f.endswith(".npz"):
+            print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
+
+
+if __name__ == "__main__":
+    main()

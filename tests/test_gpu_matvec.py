@@ -1,0 +1,162 @@
+"""GPU parity of the decode path: device quantizers, per-block integers and matvec outputs against
+the oracle (and the reference's golden vectors), through the C ABI.
+
+Bar: bit-exact. Activation quants, scales and sums, and per-block integer dot products are
+integer work; the fp32 matvec outputs reproduce the reference kernels' accumulation order
+(dot_q8_0_q8 / dot_q4_K_q8k / dot_q4Kx8 / dot_q6_K_q8k), so they are compared bit for bit too
+(stronger than the 1e-5 per-vector tolerance the north star allows, which is also checked).
+"""
+import numpy as np
+import pytest
+from conftest import bits_equal, golden, rel_err
+
+from fastgguf_amd import synth as S
+from fastgguf_amd.backend import ORDER_REPACKED, ORDER_ROW, SKIP_MEM, SKIP_TYPE, BackendError
+from oracle import ORDER_REPACKED as O_RP
+from oracle import ORDER_ROW as O_ROW
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5  # max|y - y_ref| / max|y_ref| per output vector (fastgguf.c:5723-5733)
+
+
+def check_vec(y, ref):
+    assert rel_err(y, ref) <= TOL
+    assert bits_equal(y, ref), f"not bit-exact: rel {rel_err(y, ref):.3e}"
+
+
+def test_fp16_decode_exhaustive(backend, oracle):
+    """fp16 -> fp32 of all 65536 codes (the reference selftest's table check, fastgguf.c:6022-6031)."""
+    h = np.arange(65536, dtype=np.uint16)
+    got = backend.fp16_to_f32(h)
+    want = np.array([oracle.lib.fgo_fp16(int(v)) for v in h], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_quantizers_match_golden(backend):
+    g = golden("quantize.npz")
+    for r, x in enumerate(g["quant_x"]):
+        assert backend.quantize_q8(x).view(np.uint8).tobytes() == g["quant_q8"][r].tobytes(), f"q8 row {r}"
+        assert backend.quantize_q8k(x).view(np.uint8).tobytes() == g["quant_q8k"][r].tobytes(), f"q8k row {r}"
+
+
+@pytest.mark.parametrize("n", [256, 4096, 14336, 768, 2048, 4096 + 100])
+def test_quantizers_bit_exact(backend, oracle, n):
+    x = S.activations(n, 40 + n) * np.float32(3.0)
+    assert backend.quantize_q8(x).tobytes() == oracle.quantize_q8(x).tobytes()
+    assert backend.quantize_q8k(x).tobytes() == oracle.quantize_q8k(x).tobytes()
+
+
+@pytest.mark.parametrize("name,t", [("q8_0", S.T_Q8_0), ("q4_k", S.T_Q4_K), ("q6_k", S.T_Q6_K)])
+@pytest.mark.parametrize("gen", ["synth", "bytes"])
+def test_matvec_matches_golden(backend, name, t, gen):
+    g = golden("matvec.npz")
+    w, x = g[f"{name}_{gen}_w"], g[f"{name}_{gen}_x"]
+    tt = backend.upload(t, x.size, w, order=ORDER_ROW)
+    check_vec(backend.matvec(tt, x), g[f"{name}_{gen}_y"])
+    tt.free()
+    if t == S.T_Q4_K:
+        tt = backend.upload(t, x.size, w, order=ORDER_REPACKED)
+        check_vec(backend.matvec(tt, x), g[f"{name}_{gen}_y_rp"])
+        tt.free()
+
+
+CASES = [  # (type, rows, cols, n_mats, order)
+    (S.T_Q8_0, 64, 512, 1, ORDER_ROW),
+    (S.T_Q8_0, 20, 96, 1, ORDER_ROW),          # 3 blocks: a tile with a padding block
+    (S.T_Q8_0, 37, 4096 + 32, 2, ORDER_ROW),   # ragged rows, 3-D
+    (S.T_Q4_K, 64, 768, 1, ORDER_REPACKED),
+    (S.T_Q4_K, 64, 768, 1, ORDER_ROW),
+    (S.T_Q4_K, 21, 256, 3, ORDER_ROW),         # ragged rows, 3-D, one block
+    (S.T_Q4_K, 16, 14336, 1, ORDER_REPACKED),  # many chunks
+    (S.T_Q4_K, 16, 14336, 1, ORDER_ROW),
+    (S.T_Q6_K, 64, 512, 1, ORDER_ROW),
+    (S.T_Q6_K, 13, 4608, 2, ORDER_ROW),        # ragged rows, 18 blocks (2 chunks)
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"t{c[0]}_{c[1]}x{c[2]}x{c[3]}_o{c[4]}")
+def test_block_ints_and_matvec_exact(backend, oracle, case):
+    t, rows, cols, n_mats, order = case
+    w = S.random_bytes_weights(t, rows * n_mats, cols, 5 + rows)
+    x = S.activations(cols, 6 + rows)
+    tt = backend.upload(t, cols, w, rows=rows, n_mats=n_mats, order=order)
+    act = oracle.quantize_for(t, x)
+    s, m = backend.block_ints(tt, x)
+    for r in range(rows * n_mats):
+        os_, om = oracle.block_ints(t, w[r], act)
+        assert np.array_equal(s[r], os_), f"sumi row {r}"
+        assert np.array_equal(m[r], om), f"msum row {r}"
+    check_vec(backend.matvec(tt, x), oracle.matvec(t, w, cols, x, O_RP if order == ORDER_REPACKED else O_ROW))
+    tt.free()
+
+
+@pytest.mark.parametrize("cfg", ["cfg1_q8_0", "gate_q4k_rp", "gate_q4k_row", "down_q4k_rp", "lmhead_q6k"])
+def test_matvec_config_shapes(backend, oracle, cfg):
+    """BASELINE.json shapes with the benchmark's weight distributions."""
+    t, rows, cols, order = {
+        "cfg1_q8_0": (S.T_Q8_0, 4096, 4096, ORDER_ROW),
+        "gate_q4k_rp": (S.T_Q4_K, 14336, 4096, ORDER_REPACKED),
+        "gate_q4k_row": (S.T_Q4_K, 14336, 4096, ORDER_ROW),
+        "down_q4k_rp": (S.T_Q4_K, 4096, 14336, ORDER_REPACKED),
+        "lmhead_q6k": (S.T_Q6_K, 128256, 4096, ORDER_ROW),
+    }[cfg]
+    w = S.weights(t, rows, cols, 11)
+    x = S.activations(cols, 12)
+    tt = backend.upload(t, cols, w, order=order)
+    y = backend.matvec(tt, x)
+    check_vec(y, oracle.matvec(t, w, cols, x, O_RP if order == ORDER_REPACKED else O_ROW))
+    # a second call on the same tensor with another x (buffers reused)
+    x2 = S.activations(cols, 13)
+    check_vec(backend.matvec(tt, x2), oracle.matvec(t, w, cols, x2, O_RP if order == ORDER_REPACKED else O_ROW))
+    tt.free()
+
+
+def test_matvec_multi_qkv(backend, oracle):
+    """matvec_multi (fastgguf.c:2552): Q, K, V of one layer read one quantized x."""
+    cols = 4096
+    ws = [S.weights(S.T_Q4_K, r, cols, 20 + i) for i, r in enumerate((4096, 1024, 1024))]
+    ts = [backend.upload(S.T_Q4_K, cols, w) for w in ws]
+    x = S.activations(cols, 23)
+    ys = backend.matvec_multi(ts, x)
+    for w, y in zip(ws, ys):
+        check_vec(y, oracle.matvec(S.T_Q4_K, w, cols, x, O_RP))
+    for t in ts:
+        t.free()
+
+
+@pytest.mark.parametrize("t", [S.T_Q8_0, S.T_Q4_K, S.T_Q6_K])
+@pytest.mark.parametrize("nb", [2, 3, 7])
+def test_matmul_small_batch(backend, oracle, t, nb):
+    """nb < 8: the per-token decode kernel (matmul 3006-3009 for repacked tensors; the x4 tiles
+    otherwise, which equal the single-row kernels)."""
+    cols, rows = 1024, 72
+    w = S.weights(t, rows, cols, 30 + nb)
+    X = S.activations(cols, 31 + nb, rows=nb)
+    tt = backend.upload(t, cols, w)
+    Y = backend.matmul(tt, X)
+    order = O_RP if t == S.T_Q4_K else O_ROW
+    Yo = oracle.matmul(t, w, cols, X, order)
+    for b in range(nb):
+        check_vec(Y[b], Yo[b])
+    tt.free()
+
+
+def test_upload_refusals(backend):
+    info0 = backend.info()
+    with pytest.raises(BackendError) as e:
+        backend.upload(S.T_Q4_K, 300, np.zeros(8 * 144 * 2, np.uint8), rows=8)  # cols % 256 != 0
+    assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:
+        backend.upload(2, 256, np.zeros(8 * 144, np.uint8), rows=8)  # Q4_0: not on this path
+    assert e.value.status == SKIP_TYPE
+    info1 = backend.info()
+    assert info1["n_skip_type"] == info0["n_skip_type"] + 2
+    from fastgguf_amd.backend import Backend
+    small = Backend(0, budget_bytes=1 << 20)
+    with pytest.raises(BackendError) as e:
+        small.upload(S.T_Q4_K, 4096, S.weights(S.T_Q4_K, 512, 4096, 1))  # 1.2 MB > 1 MB budget
+    assert e.value.status == SKIP_MEM and small.info()["n_skip_mem"] == 1
+    small.close()

@@ -1,0 +1,252 @@
+"""Pins the CPU oracle (oracle/fg_oracle.c) before it is trusted as the GPU parity checker.
+
+* golden vectors written by the reference's own compiled kernels (tests/golden/make_golden.py):
+  the restatement must reproduce them bit for bit;
+* what the mathematics fixes independently of the reference code: quantizer special cases and
+  invariants, integer block sums against brute force over independently decoded codes
+  (numpy, from the byte layouts), and the dequantized-float relation of the reference selftest;
+* the reference selftest's relations between kernels (batch GEMM vs single kernel, repacked vs
+  row kernel: rel < 1e-5, fastgguf.c:5690-5785);
+* planted mistakes: the oracle rebuilt with one mistake (FGO_MUTATE) must fail the golden vectors.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+from conftest import ROOT, bits_equal, golden, rel_err
+
+from fastgguf_amd import synth as S
+from oracle import ORDER_REPACKED, ORDER_ROW, Oracle
+
+TYPES = {"q8_0": S.T_Q8_0, "q4_k": S.T_Q4_K, "q6_k": S.T_Q6_K}
+
+
+# ---------------------------------------------------------------- golden vectors (reference)
+
+def test_quantizers_match_golden(oracle):
+    g = golden("quantize.npz")
+    for r, x in enumerate(g["quant_x"]):
+        assert oracle.quantize_q8(x).view(np.uint8).tobytes() == g["quant_q8"][r].tobytes(), f"q8 row {r}"
+        assert oracle.quantize_q8k(x).view(np.uint8).tobytes() == g["quant_q8k"][r].tobytes(), f"q8k row {r}"
+
+
+@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("gen", ["synth", "bytes"])
+def test_matvec_matches_golden(oracle, name, gen):
+    g = golden("matvec.npz")
+    t = TYPES[name]
+    w, x = g[f"{name}_{gen}_w"], g[f"{name}_{gen}_x"]
+    cols = x.size
+    assert bits_equal(oracle.matvec(t, w, cols, x, ORDER_ROW), g[f"{name}_{gen}_y"])
+    if t == S.T_Q4_K:
+        assert bits_equal(oracle.matvec(t, w, cols, x, ORDER_REPACKED), g[f"{name}_{gen}_y_rp"])
+
+
+@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("nb", [3, 8, 45])
+def test_matmul_matches_golden(oracle, name, nb):
+    g = golden("matmul.npz")
+    t = TYPES[name]
+    w, X = g[f"{name}_w"], g[f"{name}_X{nb}"]
+    cols = X.shape[1]
+    assert bits_equal(oracle.matmul(t, w, cols, X, ORDER_ROW), g[f"{name}_Y{nb}"])
+    if t == S.T_Q4_K:
+        assert bits_equal(oracle.matmul(t, w, cols, X, ORDER_REPACKED), g[f"{name}_Y{nb}_rp"])
+
+
+def test_moe_matches_golden(oracle):
+    g = golden("moe.npz")
+    E, K, D, F, T = (int(v) for v in g["dims"])
+    Y, sel, w = oracle.moe_ffn((S.T_Q4_K,) * 3, g["gate"], g["up"], g["down"], E, K, D, F, g["logits"], g["X"])
+    assert np.array_equal(sel, g["sel"])
+    assert bits_equal(w, g["w"])
+    assert bits_equal(Y, g["Y"])
+    assert list(g["sel"][2][:2]) == [3, 7]      # tie on top keeps the lower index first
+    assert list(g["sel"][3]) == [0, 1, 2]       # all-equal logits
+
+
+def test_oracle_matches_compiled_reference_random(oracle, reference):
+    """Fresh random shapes and seeds against the reference's kernels (where oracle/_ref is built)."""
+    rng = np.random.Generator(np.random.PCG64(7))
+    for case in range(6):
+        t = [S.T_Q8_0, S.T_Q4_K, S.T_Q6_K][case % 3]
+        cols = int(rng.integers(1, 5)) * 256
+        rows = 8 * int(rng.integers(1, 5))
+        w = (S.weights if case % 2 else S.random_bytes_weights)(t, rows, cols, 1000 + case)
+        x = S.activations(cols, 2000 + case)
+        assert bits_equal(oracle.matvec(t, w, cols, x), reference.matvec(t, w, cols, x))
+        if t == S.T_Q4_K:
+            assert bits_equal(oracle.matvec(t, w, cols, x, ORDER_REPACKED), reference.matvec(t, w, cols, x, True))
+        nb = int(rng.integers(8, 20))
+        X = S.activations(cols, 3000 + case, rows=nb)
+        if reference.variant == "vnni" or t != S.T_Q8_0:  # AVX2 builds have no Q8_0 GEMM
+            assert bits_equal(oracle.matmul(t, w, cols, X), reference.matmul(t, w, cols, X))
+
+
+# ---------------------------------------------------------------- what the mathematics fixes
+
+def test_quantizer_invariants(oracle):
+    x = S.activations(4096, 11)
+    x[:256] = 0.0
+    for blocks, bsz, sums in ((oracle.quantize_q8k(x), 256, "bsums"), (oracle.quantize_q8(x), 32, "s16")):
+        xb = x[: blocks.size * bsz].reshape(blocks.size, bsz)
+        amax = np.abs(xb).max(axis=1)
+        # d is the IEEE quotient amax / 127 (numpy float32 division is correctly rounded)
+        assert np.array_equal(blocks["d"], (amax / np.float32(127)).astype(np.float32))
+        q = blocks["qs"].astype(np.int32)
+        assert np.abs(q).max() <= 127
+        nz = amax > 0
+        # the largest magnitude maps to +-127 exactly
+        assert np.all(np.abs(q[nz]).max(axis=1) == 127)
+        assert np.all(q[~nz] == 0) and np.all(blocks["d"][~nz] == 0)
+        # sums of every 16 quants
+        s = q.reshape(blocks.size, -1, 16).sum(axis=2)
+        assert np.array_equal(blocks[sums].astype(np.int32), s)
+        # dequantized values within half a step of x
+        err = np.abs(q * blocks["d"][:, None] - xb)
+        assert np.all(err <= blocks["d"][:, None] * 0.5 * (1 + 1e-5) + 1e-30)
+    # a tail shorter than a block is ignored (n / 32, n / 256)
+    assert oracle.quantize_q8(x[:63]).size == 1 and oracle.quantize_q8k(x[:511]).size == 1
+
+
+def test_quantizer_rounds_half_to_even(oracle):
+    # amax = 127 -> d = 1, id = 1: x * id = x exactly, so the .5 cases must round to even
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 126.5]
+    q = oracle.quantize_q8(x)["qs"][0][:9]
+    assert list(q) == [127, 0, 2, 2, 0, -2, -2, 4, 126]
+
+
+def _decode_codes(t, w_row, cols):
+    """Independent numpy decode of one row into (integer codes, integer scale per element,
+    integer min per element, block index); from the byte layouts, not from the oracle."""
+    nb = cols // S.BLOCK[t][0]
+    blk = w_row.reshape(nb, S.BLOCK[t][1])
+    if t == S.T_Q8_0:
+        q = blk[:, 2:34].view(np.int8).astype(np.int64).reshape(-1)
+        return q, np.ones_like(q), np.zeros_like(q)
+    if t == S.T_Q4_K:
+        s12 = blk[:, 4:16].astype(np.int64)
+        sc = np.zeros((nb, 8), np.int64)
+        mn = np.zeros((nb, 8), np.int64)
+        for j in range(4):
+            sc[:, j] = s12[:, j] & 63
+            mn[:, j] = s12[:, j + 4] & 63
+            sc[:, j + 4] = (s12[:, j + 8] & 15) | ((s12[:, j] >> 6) << 4)
+            mn[:, j + 4] = (s12[:, j + 8] >> 4) | ((s12[:, j + 4] >> 6) << 4)
+        qs = blk[:, 16:144].astype(np.int64).reshape(nb, 4, 32)
+        q = np.stack([qs & 15, qs >> 4], axis=2).reshape(nb, 256)  # [j][lo/hi][32]
+        sub = np.arange(256) // 32
+        return q.reshape(-1), sc[:, sub].reshape(-1), mn[:, sub].reshape(-1)
+    ql = blk[:, 0:128].astype(np.int64).reshape(nb, 2, 64)
+    qh = blk[:, 128:192].astype(np.int64).reshape(nb, 2, 32)
+    sc = blk[:, 192:208].view(np.int8).astype(np.int64)
+    q = np.zeros((nb, 2, 4, 32), np.int64)
+    q[:, :, 0] = (ql[:, :, :32] & 15) | ((qh & 3) << 4)
+    q[:, :, 1] = (ql[:, :, 32:] & 15) | (((qh >> 2) & 3) << 4)
+    q[:, :, 2] = (ql[:, :, :32] >> 4) | (((qh >> 4) & 3) << 4)
+    q[:, :, 3] = (ql[:, :, 32:] >> 4) | (((qh >> 6) & 3) << 4)
+    return q.reshape(-1), sc[:, np.arange(256) // 16].reshape(-1), np.zeros(nb * 256, np.int64)
+
+
+@pytest.mark.parametrize("t", [S.T_Q8_0, S.T_Q4_K, S.T_Q6_K])
+def test_block_ints_brute_force(oracle, t):
+    cols = 1024
+    w = S.random_bytes_weights(t, 4, cols, 77)
+    x = S.activations(cols, 78)
+    act = oracle.quantize_for(t, x)
+    y = act["qs"].astype(np.int64).reshape(-1)
+    bsz = S.BLOCK[t][0]
+    for r in range(4):
+        q, sc, mn = _decode_codes(t, w[r], cols)
+        s, m = oracle.block_ints(t, w[r], act)
+        if t == S.T_Q6_K:
+            want_s = (sc * q * y).reshape(-1, bsz).sum(1)
+            want_m = (sc * y).reshape(-1, bsz).sum(1)
+        else:
+            want_s = (sc * q * y).reshape(-1, bsz).sum(1)
+            want_m = (mn * y).reshape(-1, bsz).sum(1)
+        assert np.array_equal(s, want_s) and np.array_equal(m, want_m)
+
+
+@pytest.mark.parametrize("t", [S.T_Q4_K, S.T_Q6_K, S.T_Q8_0])
+def test_dot_vs_dequantized_double(oracle, t):
+    """test_kquant (fastgguf.c:5379-5411): kernel vs double sum of dequantized weights times
+    dequantized activations, relative to sum |term| < 1e-4."""
+    n = 1024
+    for seed in range(4):
+        w = S.random_bytes_weights(t, 1, n, 90 + seed)[0]
+        x = S.activations(n, 95 + seed) * 2.0
+        act = oracle.quantize_for(t, x)
+        fast = oracle.dot(t, w, act)
+        dq = oracle.dequantize_row(t, w, n).astype(np.float64)
+        xd = (act["qs"].astype(np.float64) * act["d"][:, None].astype(np.float64)).reshape(-1)
+        terms = dq * xd
+        assert abs(fast - terms.sum()) / (np.abs(terms).sum() + 1e-9) < 1e-4
+
+
+@pytest.mark.parametrize("t", [S.T_Q4_K, S.T_Q6_K, S.T_Q8_0])
+def test_selftest_relations(oracle, t):
+    """matmul vs the single-row kernel and repacked vs row (fastgguf.c:5690-5785): < 1e-5."""
+    cols, rows, nbt = 512, 37, 45
+    w = S.random_bytes_weights(t, rows, cols, 55)
+    X = S.activations(cols, 56, rows=nbt)
+    Y = oracle.matmul(t, w, cols, X)
+    for b in range(nbt):
+        act = oracle.quantize_for(t, X[b])
+        ref = np.array([oracle.dot(t, w[r], act) for r in range(rows)], np.float32)
+        assert rel_err(Y[b], ref) < 1e-5
+    if t == S.T_Q4_K:
+        w = S.random_bytes_weights(t, 16, 768, 57)
+        x = S.activations(768, 58)
+        assert rel_err(oracle.matvec(t, w, 768, x, ORDER_REPACKED), oracle.matvec(t, w, 768, x, ORDER_ROW)) < 1e-5
+
+
+# ---------------------------------------------------------------- planted mistakes
+
+MUTANTS = {1: "hsum8 order", 2: "MoE accumulate without fma", 3: "reciprocal instead of division",
+           4: "Q6_K half-lane scale", 5: "Q4_K repacked single chain", 6: "Q4_K GEMM integer epilogue"}
+
+
+@pytest.fixture(scope="module")
+def mutant_dir(tmp_path_factory):
+    return tmp_path_factory.mktemp("mutants")
+
+
+def _golden_failures(o: Oracle) -> int:
+    fails = 0
+    g = golden("quantize.npz")
+    for r, x in enumerate(g["quant_x"]):
+        fails += o.quantize_q8(x).view(np.uint8).tobytes() != g["quant_q8"][r].tobytes()
+    g = golden("matvec.npz")
+    for name, t in TYPES.items():
+        for gen in ("synth", "bytes"):
+            x = g[f"{name}_{gen}_x"]
+            fails += not bits_equal(o.matvec(t, g[f"{name}_{gen}_w"], x.size, x), g[f"{name}_{gen}_y"])
+            if t == S.T_Q4_K:
+                fails += not bits_equal(o.matvec(t, g[f"{name}_{gen}_w"], x.size, x, ORDER_REPACKED),
+                                        g[f"{name}_{gen}_y_rp"])
+    g = golden("matmul.npz")
+    for name, t in TYPES.items():
+        X = g[f"{name}_X45"]
+        fails += not bits_equal(o.matmul(t, g[f"{name}_w"], X.shape[1], X), g[f"{name}_Y45"])
+    g = golden("moe.npz")
+    E, K, D, F, T = (int(v) for v in g["dims"])
+    Y, _, _ = o.moe_ffn((S.T_Q4_K,) * 3, g["gate"], g["up"], g["down"], E, K, D, F, g["logits"], g["X"])
+    fails += not bits_equal(Y, g["Y"])
+    return fails
+
+
+@pytest.mark.parametrize("mutant", sorted(MUTANTS))
+def test_planted_mistake_is_caught(mutant, mutant_dir):
+    so = os.path.join(str(mutant_dir), f"liboracle_m{mutant}.so")
+    src = os.path.join(ROOT, "oracle", "fg_oracle.c")
+    subprocess.run(["gcc", "-O2", "-march=x86-64-v3", "-ffp-contract=off", "-fPIC", "-fopenmp", "-std=c11",
+                    f"-DFGO_MUTATE={mutant}", "-shared", "-o", so, src, "-lm"], check=True)
+    assert _golden_failures(Oracle(so)) > 0, f"golden vectors did not catch: {MUTANTS[mutant]}"
+
+
+def test_real_oracle_passes_golden_check(oracle):
+    assert _golden_failures(oracle) == 0
