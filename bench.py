@@ -10,7 +10,8 @@ steps rotate over COPIES distinct device copies of the layer (>= 512 MB in total
 
 value  = whole-layer algorithmic bytes (weights + fp32 x in + fp32 y out) / step time, in GB/s.
 roofline: the dominant kernel is the Q4_K decode matvec at the gate shape (4096->14336); its
-         launches are timed one by one with HIP events on the library's stream.
+         launches are timed one by one with HIP events on the library's stream. A step replays
+         one HIP graph of the layer's launches (one per weight copy).
 cpu_baseline: the reference's own CPU kernels (oracle/_ref, compiled from fastgguf.c) on the same
          layer with its default repacked Q4_K path, on this host's cores, for a bounded sample.
 Prints one JSON line.
@@ -118,17 +119,22 @@ def main() -> int:
         be.h2d(xd[k], v)
     yd = {n: be.dev_alloc(4 * r) for n, r, c in LAYER}
 
+    def record_layer(t):
+        be.matvec_dev(t["qkv"], xd["x"], yd["qkv"])
+        be.matvec_dev(t["o"], xd["a"], yd["o"])
+        be.matvec_multi_dev([t["gate"], t["up"]], xd["x2"], [yd["gate"], yd["up"]])  # forward 4870-4872
+        be.matvec_dev(t["down"], xd["h"], yd["down"])
+
+    # one HIP graph per weight copy: a step is one graph replay (5 matvecs in 4 launches, each
+    # quantizing its input on the device)
+    graphs = []
+    for t in tensors:
+        be.graph_begin()
+        record_layer(t)
+        graphs.append(be.graph_end())
+
     def step(k: int):
-        t = tensors[k % args.copies]
-        be.act_quantize_dev(S.T_Q4_K, 4096, xd["x"])
-        be.matvec_act_dev(t["qkv"], yd["qkv"])
-        be.act_quantize_dev(S.T_Q4_K, 4096, xd["a"])
-        be.matvec_act_dev(t["o"], yd["o"])
-        be.act_quantize_dev(S.T_Q4_K, 4096, xd["x2"])
-        be.matvec_act_dev(t["gate"], yd["gate"])
-        be.matvec_act_dev(t["up"], yd["up"])
-        be.act_quantize_dev(S.T_Q4_K, 14336, xd["h"])
-        be.matvec_act_dev(t["down"], yd["down"])
+        be.graph_launch(graphs[k % args.copies])
 
     for k in range(args.warmup):
         step(k)
@@ -145,13 +151,12 @@ def main() -> int:
     layer_bytes = sum(algo_bytes(r, c) for _, r, c in LAYER)
     value = layer_bytes / (ms_step * 1e-3) / 1e9
 
-    # dominant kernel: the gate-shaped Q4_K matvec, each launch timed alone (x already quantized)
-    def kernel_time(name: str, cols: int, xkey: str, reps: int) -> float:
-        be.act_quantize_dev(S.T_Q4_K, cols, xd[xkey])
+    # per-kernel durations: each launch timed alone with HIP events on the library's stream
+    def kernel_time(launch, reps: int) -> float:
         evs = [(be.event(), be.event()) for _ in range(reps)]
         for i, (a, b) in enumerate(evs):
             be.record(a)
-            be.matvec_act_dev(tensors[i % args.copies][name], yd[name])
+            launch(i % args.copies)
             be.record(b)
         be.sync()
         t = [be.elapsed_ms(a, b) for a, b in evs]
@@ -160,14 +165,22 @@ def main() -> int:
             be.event_destroy(b)
         return float(np.mean(t)) * 1e3  # us
 
+    launches = {
+        "qkv": (lambda c: be.matvec_dev(tensors[c]["qkv"], xd["x"], yd["qkv"]), algo_bytes(6144, 4096)),
+        "o": (lambda c: be.matvec_dev(tensors[c]["o"], xd["a"], yd["o"]), algo_bytes(4096, 4096)),
+        "gate": (lambda c: be.matvec_dev(tensors[c]["gate"], xd["x2"], yd["gate"]), algo_bytes(14336, 4096)),
+        "gate+up": (lambda c: be.matvec_multi_dev([tensors[c]["gate"], tensors[c]["up"]], xd["x2"],
+                                                 [yd["gate"], yd["up"]]), 2 * algo_bytes(14336, 4096) - 4 * 4096),
+        "down": (lambda c: be.matvec_dev(tensors[c]["down"], xd["h"], yd["down"]), algo_bytes(4096, 14336)),
+    }
     kernels = {}
-    for n, r, c in LAYER:
-        us = kernel_time(n, c, {"qkv": "x", "o": "a", "gate": "x2", "up": "x2", "down": "h"}[n], args.kernel_reps)
-        gbs = algo_bytes(r, c) / (us * 1e-6) / 1e9
+    for n, (fn, nbytes) in launches.items():
+        us = kernel_time(fn, args.kernel_reps)
+        gbs = nbytes / (us * 1e-6) / 1e9
         kernels[n] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
     g = kernels["gate"]
     roofline = {"bound": "hbm", "achieved": g["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g["frac"],
-                "traffic": None, "kernel": "mv_q4k_rp_kernel (Q4_K decode matvec, gate 4096->14336)",
+                "traffic": None, "kernel": "mv_kernel<Q4_K, repacked> (Q4_K decode matvec, gate 4096->14336)",
                 "bytes_per_launch": algo_bytes(14336, 4096), "us_per_launch": g["us"]}
 
     cpu = cpu_baseline(layer_w, xs, args.cpu_seconds) if args.cpu_seconds > 0 else None

@@ -27,7 +27,7 @@ EXPORTS = (
     "fgh_open", "fgh_close", "fgh_info", "fgh_last_error", "fgh_upload", "fgh_tensor_free",
     "fgh_matvec", "fgh_matvec_multi", "fgh_matmul", "fgh_moe_ffn",
     "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matmul_dev", "fgh_moe_ffn_dev",
-    "fgh_act_quantize_dev", "fgh_matvec_act_dev",
+    "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
     "fgh_quantize", "fgh_block_ints", "fgh_fp16_to_f32",
@@ -73,8 +73,10 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_matvec_multi_dev": (i32, [vp, i32, vp, vp, vp]),
         "fgh_matmul_dev": (i32, [vp, vp, vp, i32, vp, i32, i32]),
         "fgh_moe_ffn_dev": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, i32]),
-        "fgh_act_quantize_dev": (i32, [vp, u32, i64, vp, i32]),
-        "fgh_matvec_act_dev": (i32, [vp, vp, vp]),
+        "fgh_graph_begin": (i32, [vp]),
+        "fgh_graph_end": (i32, [vp, C.POINTER(vp)]),
+        "fgh_graph_launch": (i32, [vp, vp]),
+        "fgh_graph_destroy": (i32, [vp, vp]),
         "fgh_dev_alloc": (i32, [vp, u64, C.POINTER(vp)]),
         "fgh_dev_free": (i32, [vp, vp]),
         "fgh_copy_h2d": (i32, [vp, vp, vp, u64]),
@@ -270,11 +272,19 @@ class Backend:
         yp = (C.c_void_p * len(ts))(*y_devs)
         self._check(self.lib.fgh_matvec_multi_dev(self.ctx, len(ts), th, x_dev, yp))
 
-    def act_quantize_dev(self, type_: int, cols: int, x_dev: int, ntok: int = 1):
-        self._check(self.lib.fgh_act_quantize_dev(self.ctx, type_, cols, x_dev, ntok))
+    def graph_begin(self):
+        self._check(self.lib.fgh_graph_begin(self.ctx))
 
-    def matvec_act_dev(self, t: Tensor, y_dev: int):
-        self._check(self.lib.fgh_matvec_act_dev(self.ctx, t.handle, y_dev))
+    def graph_end(self) -> int:
+        g = C.c_void_p()
+        self._check(self.lib.fgh_graph_end(self.ctx, C.byref(g)))
+        return g.value
+
+    def graph_launch(self, g: int):
+        self._check(self.lib.fgh_graph_launch(self.ctx, g))
+
+    def graph_destroy(self, g: int):
+        self._check(self.lib.fgh_graph_destroy(self.ctx, g))
 
     def matmul_dev(self, t: Tensor, X_dev: int, Y_dev: int, nb: int):
         self._check(self.lib.fgh_matmul_dev(self.ctx, t.handle, X_dev, t.cols, Y_dev, t.nout, nb))

@@ -30,9 +30,8 @@ struct fgh_ctx {
     std::string err = "ok";
     // scratch, grown on demand (gpu_grow_buf, fastgguf.c:2083-2091)
     DevBuf x, y, aqs, ad, abs;
-    // what the activation buffers currently hold (fgh_act_quantize_dev)
-    bool act_q8 = false;
-    int64_t act_cols = 0;
+    int num_cu = 256;         // compute units (sizes the persistent decode grid)
+    bool capturing = false;   // inside fgh_graph_begin / fgh_graph_end
 };
 
 struct fgh_tensor {
@@ -68,6 +67,7 @@ static int fail(fgh_ctx *c, int code, const char *fmt, ...) {
 
 static int grow(fgh_ctx *c, DevBuf &b, size_t need) {
     if (need <= b.cap) return FGH_OK;
+    if (c->capturing) return fail(c, FGH_ERR, "a scratch buffer would grow during graph capture");
     if (b.p) {
         HIP_TRY(c, hipStreamSynchronize(c->stream));
         HIP_TRY(c, hipFree(b.p));
@@ -112,21 +112,38 @@ static int quantize_dev(fgh_ctx *c, uint32_t type, int64_t cols, const float *x,
         fgh::ActQ8K a{(int8_t *)c->aqs.p, (float *)c->ad.p, (int16_t *)c->abs.p};
         HIP_TRY(c, fgh::launch_quant_q8k(x, ldx, (int)(cols / 256), ntok, a, c->stream));
     }
-    c->act_q8 = type == FGH_T_Q8_0;
-    c->act_cols = cols;
     return FGH_OK;
 }
 
-// decode kernel over the activations already in the context buffers (ntok tokens)
-static int matvec_launch(fgh_ctx *c, const fgh_tensor *t, float *y, int64_t ldy, int ntok, int32_t *ds, int32_t *dm) {
-    fgh::MvOut out{y, ldy, t->rows, t->gpm, ds, dm};
-    fgh::ActQ8K ak{(int8_t *)c->aqs.p, (float *)c->ad.p, (int16_t *)c->abs.p};
-    fgh::ActQ8 a8{(int8_t *)c->aqs.p, (float *)c->ad.p, (int16_t *)c->abs.p};
-    const void *act = t->type == FGH_T_Q8_0 ? (const void *)&a8 : (const void *)&ak;
-    HIP_TRY(c, fgh::launch_matvec((int)t->type, t->order, t->dev, t->nb, t->groups, ntok, act, out,
-                                  ds != nullptr, c->stream));
+// one decode launch over n tensors that share type, order and width; x: ntok fp32 vectors
+// (device, stride ldx); y[i]: outputs of tensor i (token stride ldy)
+static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const float *x, int64_t ldx,
+                         float *const *y, int64_t ldy, int ntok, int32_t *ds, int32_t *dm) {
+    fgh::MvArgs a;
+    memset(&a, 0, sizeof(a));
+    int64_t g = 0;
+    for (int i = 0; i < n; i++) {
+        a.t[i] = fgh::MvT{t[i]->dev, y[i], t[i]->rows, t[i]->gpm, g};
+        g += t[i]->groups;
+    }
+    a.nt = n;
+    a.groups = g;
+    a.x = x;
+    a.ldx = ldx;
+    a.ldy = ldy;
+    a.nb = t[0]->nb;
+    a.ntile = t[0]->ntile;
+    a.dump_s = ds;
+    a.dump_m = dm;
+    HIP_TRY(c, fgh::launch_matvec2((int)t[0]->type, t[0]->order, a, ntok, c->num_cu, c->stream));
     return FGH_OK;
 }
+
+// host-synchronous and allocating calls cannot be recorded into a graph
+#define NO_CAPTURE(c) \
+    do { \
+        if ((c)->capturing) return fail((c), FGH_ERR, "%s: not allowed while capturing a graph", __func__); \
+    } while (0)
 
 static int check_tensor(fgh_ctx *c, const fgh_tensor *t) {
     if (!c) return FGH_ERR_ARG;
@@ -152,6 +169,7 @@ int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out) {
     snprintf(c->name, sizeof(c->name), "%s (%s)", prop.name, prop.gcnArchName);
     c->vram = prop.totalGlobalMem;
     c->budget = budget_bytes ? budget_bytes : c->vram - c->vram / 8;
+    c->num_cu = std::max(1, prop.multiProcessorCount);
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return FGH_ERR_DEVICE;
@@ -162,11 +180,11 @@ int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out) {
 
 void fgh_close(fgh_ctx *c) {
     if (!c) return;
-    hipSetDevice(c->device);
+    (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs})
-        if (b->p) hipFree(b->p);
-    hipStreamDestroy(c->stream);
+        if (b->p) (void)hipFree(b->p);
+    (void)hipStreamDestroy(c->stream);
     delete c;
 }
 
@@ -189,9 +207,12 @@ const char *fgh_last_error(const fgh_ctx *c) { return c ? c->err.c_str() : "no c
 int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_mats, int order,
                const void *host, uint64_t nbytes, fgh_tensor **out) {
     if (!c || !out) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
     *out = nullptr;
     if (!host || rows <= 0 || n_mats <= 0 || cols <= 0) return fail(c, FGH_ERR_ARG, "upload: bad shape");
-    if (!type_supported(type) || cols % block_elems(type) != 0 || cols / block_elems(type) > (1 << 24)) {
+    if (!type_supported(type) || cols % block_elems(type) != 0 ||
+        fgh::matvec_lds_bytes((int)type, 0, (int)std::min<int64_t>(cols / block_elems(type), 1 << 20)) > 65536 ||
+        fgh::matvec_lds_bytes((int)type, 1, (int)std::min<int64_t>(cols / block_elems(type), 1 << 20)) > 65536) {
         c->n_skip_type++;
         return fail(c, FGH_SKIP_TYPE, "upload: type %u with %lld cols is not supported", type, (long long)cols);
     }
@@ -225,7 +246,7 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     }
     void *stage = nullptr;
     if (hipMalloc(&t->dev, t->dev_bytes) != hipSuccess || hipMalloc(&stage, nbytes) != hipSuccess) {
-        if (t->dev) hipFree(t->dev);
+        if (t->dev) (void)hipFree(t->dev);
         delete t;
         c->n_skip_mem++;
         (void)hipGetLastError();
@@ -267,32 +288,25 @@ int fgh_matvec_multi_dev(fgh_ctx *c, int n, const fgh_tensor *const *t, const fl
     for (int i = 0; i < n; i++) {
         if ((rc = check_tensor(c, t[i]))) return rc;
         if (!y[i]) return fail(c, FGH_ERR_ARG, "matvec_multi: null output");
-        if (t[i]->cols != t[0]->cols || (t[i]->type == FGH_T_Q8_0) != (t[0]->type == FGH_T_Q8_0))
-            return fail(c, FGH_ERR_ARG, "matvec_multi: tensors differ in cols or activation kind");
+        if (t[i]->cols != t[0]->cols) return fail(c, FGH_ERR_ARG, "matvec_multi: tensors differ in cols");
     }
     HIP_TRY(c, hipSetDevice(c->device));
-    if ((rc = quantize_dev(c, t[0]->type, t[0]->cols, x, t[0]->cols, 1))) return rc;
-    for (int i = 0; i < n; i++)
-        if ((rc = matvec_launch(c, t[i], y[i], 0, 1, nullptr, nullptr))) return rc;
+    // tensors of the same type and order run in one launch (matvec_multi, fastgguf.c:2552-2572)
+    bool done[4] = {false, false, false, false};
+    for (int i = 0; i < n; i++) {
+        if (done[i]) continue;
+        const fgh_tensor *grp[4];
+        float *ys[4];
+        int m = 0;
+        for (int j = i; j < n; j++)
+            if (!done[j] && t[j]->type == t[i]->type && t[j]->order == t[i]->order) {
+                grp[m] = t[j];
+                ys[m++] = y[j];
+                done[j] = true;
+            }
+        if ((rc = matvec_launch(c, m, grp, x, t[0]->cols, ys, 0, 1, nullptr, nullptr))) return rc;
+    }
     return FGH_OK;
-}
-
-int fgh_act_quantize_dev(fgh_ctx *c, uint32_t type, int64_t cols, const float *x, int ntok) {
-    if (!c) return FGH_ERR_ARG;
-    if (!x || !type_supported(type) || cols <= 0 || cols % block_elems(type) || ntok < 1 || ntok > FG_BATCH)
-        return fail(c, FGH_ERR_ARG, "act_quantize: bad arguments");
-    HIP_TRY(c, hipSetDevice(c->device));
-    return quantize_dev(c, type, cols, x, cols, ntok);
-}
-
-int fgh_matvec_act_dev(fgh_ctx *c, const fgh_tensor *t, float *y) {
-    int rc = check_tensor(c, t);
-    if (rc) return rc;
-    if (!y) return fail(c, FGH_ERR_ARG, "matvec_act: null output");
-    if (c->act_cols != t->cols || c->act_q8 != (t->type == FGH_T_Q8_0))
-        return fail(c, FGH_ERR_ARG, "matvec_act: the prepared activation does not match the tensor");
-    HIP_TRY(c, hipSetDevice(c->device));
-    return matvec_launch(c, t, y, 0, 1, nullptr, nullptr);
 }
 
 int fgh_matvec_dev(fgh_ctx *c, const fgh_tensor *t, const float *x, float *y) {
@@ -308,8 +322,8 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
         return fail(c, FGH_ERR_ARG, "matmul: bad arguments");
     HIP_TRY(c, hipSetDevice(c->device));
     if (nb >= 8) return fail(c, FGH_ERR, "matmul: the prompt GEMM for nb >= 8 is not available in this build");
-    if ((rc = quantize_dev(c, t->type, t->cols, X, ldx, nb))) return rc;
-    return matvec_launch(c, t, Y, ldy, nb, nullptr, nullptr);
+    float *ys[1] = {Y};
+    return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
 }
 
 int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *, const fgh_tensor *, const fgh_tensor *, int,
@@ -321,6 +335,7 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *, const fgh_tensor *, const fg
 
 int fgh_matvec_multi(fgh_ctx *c, int n, const fgh_tensor *const *t, const float *x, float *const *y) {
     if (!c || !t || !x || !y || n < 1 || n > 4) return fail(c, FGH_ERR_ARG, "matvec_multi: bad arguments");
+    NO_CAPTURE(c);
     int rc;
     int64_t total = 0;
     for (int i = 0; i < n; i++) {
@@ -352,6 +367,7 @@ int fgh_matvec(fgh_ctx *c, const fgh_tensor *t, const float *x, float *y) {
 int fgh_matmul(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, float *Y, int ldy, int nb) {
     int rc = check_tensor(c, t);
     if (rc) return rc;
+    NO_CAPTURE(c);
     const int64_t nout = t->rows * t->n_mats;
     if (!X || !Y || nb < 1 || nb > FG_BATCH || ldx < t->cols || ldy < nout)
         return fail(c, FGH_ERR_ARG, "matmul: bad arguments");
@@ -375,30 +391,35 @@ int fgh_moe_ffn(fgh_ctx *c, const fgh_tensor *, const fgh_tensor *, const fgh_te
 
 int fgh_dev_alloc(fgh_ctx *c, uint64_t bytes, void **ptr) {
     if (!c || !ptr) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
     HIP_TRY(c, hipSetDevice(c->device));
     HIP_TRY(c, hipMalloc(ptr, bytes ? bytes : 1));
     return FGH_OK;
 }
 int fgh_dev_free(fgh_ctx *c, void *p) {
     if (!c) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     HIP_TRY(c, hipFree(p));
     return FGH_OK;
 }
 int fgh_copy_h2d(fgh_ctx *c, void *dst, const void *src, uint64_t bytes) {
     if (!c) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
     HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     return FGH_OK;
 }
 int fgh_copy_d2h(fgh_ctx *c, void *dst, const void *src, uint64_t bytes) {
     if (!c) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
     HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     return FGH_OK;
 }
 int fgh_sync(fgh_ctx *c) {
     if (!c) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     return FGH_OK;
 }
@@ -414,6 +435,7 @@ int fgh_event_record(fgh_ctx *c, void *ev) {
 }
 int fgh_event_elapsed_ms(fgh_ctx *c, void *a, void *b, float *ms) {
     if (!c || !a || !b || !ms) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
     HIP_TRY(c, hipEventSynchronize((hipEvent_t)b));
     HIP_TRY(c, hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
     return FGH_OK;
@@ -424,10 +446,50 @@ int fgh_event_destroy(fgh_ctx *c, void *ev) {
     return FGH_OK;
 }
 
+// ---- graphs ----
+
+int fgh_graph_begin(fgh_ctx *c) {
+    if (!c) return FGH_ERR_ARG;
+    if (c->capturing) return fail(c, FGH_ERR, "graph_begin: already capturing");
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;
+    return FGH_OK;
+}
+
+int fgh_graph_end(fgh_ctx *c, void **graph) {
+    if (!c || !graph) return FGH_ERR_ARG;
+    *graph = nullptr;
+    if (!c->capturing) return fail(c, FGH_ERR, "graph_end: not capturing");
+    c->capturing = false;
+    hipGraph_t g = nullptr;
+    HIP_TRY(c, hipStreamEndCapture(c->stream, &g));
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail(c, FGH_ERR_DEVICE, "graph instantiate: %s", hipGetErrorString(e));
+    *graph = ge;
+    return FGH_OK;
+}
+
+int fgh_graph_launch(fgh_ctx *c, void *graph) {
+    if (!c || !graph) return FGH_ERR_ARG;
+    if (c->capturing) return fail(c, FGH_ERR, "graph_launch: capturing");
+    HIP_TRY(c, hipGraphLaunch((hipGraphExec_t)graph, c->stream));
+    return FGH_OK;
+}
+
+int fgh_graph_destroy(fgh_ctx *c, void *graph) {
+    if (!c || !graph) return FGH_ERR_ARG;
+    HIP_TRY(c, hipGraphExecDestroy((hipGraphExec_t)graph));
+    return FGH_OK;
+}
+
 // ---- test hooks ----
 
 int fgh_quantize(fgh_ctx *c, int kind, const float *x, int n, void *out_blocks) {
     if (!c || !x || !out_blocks || n <= 0) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
     const uint32_t type = kind == FGH_ACT_Q8 ? FGH_T_Q8_0 : kind == FGH_ACT_Q8K ? FGH_T_Q4_K : 0;
     if (!type) return fail(c, FGH_ERR_ARG, "quantize: bad kind");
     const int be = block_elems(type), nbk = n / be;
@@ -467,6 +529,7 @@ int fgh_quantize(fgh_ctx *c, int kind, const float *x, int n, void *out_blocks) 
 int fgh_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *x, int32_t *sumi, int32_t *msum) {
     int rc = check_tensor(c, t);
     if (rc) return rc;
+    NO_CAPTURE(c);
     if (!x || !sumi || !msum) return fail(c, FGH_ERR_ARG, "block_ints: null pointer");
     const int64_t nout = t->rows * t->n_mats;
     const size_t nint = (size_t)nout * t->nb;
@@ -477,8 +540,8 @@ int fgh_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *x, int32_t *sum
     int32_t *dsi = (int32_t *)ds, *dmi = dsi + nint;
     hipError_t e = hipMemcpyAsync(c->x.p, x, (size_t)t->cols * 4, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) {
-        rc = quantize_dev(c, t->type, t->cols, (const float *)c->x.p, t->cols, 1);
-        if (!rc) rc = matvec_launch(c, t, (float *)c->y.p, 0, 1, dsi, dmi);
+        float *ys[1] = {(float *)c->y.p};
+        rc = matvec_launch(c, 1, &t, (const float *)c->x.p, t->cols, ys, 0, 1, dsi, dmi);
         if (!rc) {
             e = hipMemcpyAsync(sumi, dsi, nint * 4, hipMemcpyDeviceToHost, c->stream);
             if (e == hipSuccess) e = hipMemcpyAsync(msum, dmi, nint * 4, hipMemcpyDeviceToHost, c->stream);
@@ -494,6 +557,7 @@ int fgh_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *x, int32_t *sum
 
 int fgh_fp16_to_f32(fgh_ctx *c, const uint16_t *h, int n, float *out) {
     if (!c || !h || !out || n <= 0) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
     HIP_TRY(c, hipSetDevice(c->device));
     int rc;
     if ((rc = grow(c, c->x, (size_t)n * 2)) || (rc = grow(c, c->y, (size_t)n * 4))) return rc;

@@ -109,20 +109,6 @@ __device__ __forceinline__ int q4k_mn(const Q4KScales &s, int j) {
     return ubyte(j < 4 ? s.mn_lo : s.mn_hi, j & 3);
 }
 
-// output side of a decode matvec: row r of group g is row m * rows + gl * 8 + r of y, with
-// g = m * gpm + gl; dump_s / dump_m (test hook only) receive per (row, block) integers
-struct MvOut {
-    float *y;
-    int64_t ldy;   // token stride of y
-    int64_t rows;  // rows per matrix
-    int64_t gpm;   // row groups per matrix
-    int32_t *dump_s, *dump_m;
-    __device__ __forceinline__ int64_t row_of(int64_t g, int r, bool &ok) const {
-        const int64_t m = g / gpm, gl = g - m * gpm, lr = gl * 8 + r;
-        ok = lr < rows;
-        return m * rows + lr;
-    }
-};
 
 // host-side launchers (fgh_kernels.hip)
 hipError_t launch_quant_q8k(const float *x, int64_t ldx, int nb, int ntok, ActQ8K act, hipStream_t s);
@@ -130,7 +116,25 @@ hipError_t launch_quant_q8(const float *x, int64_t ldx, int nb, int ntok, ActQ8 
 hipError_t launch_relayout(const uint8_t *src, uint8_t *dst, int type, int64_t rows, int nb, int ntile,
                            int64_t gpm, int64_t total, int64_t row_bytes, hipStream_t s);
 hipError_t launch_fp16(const uint16_t *h, float *out, int n, hipStream_t s);
-hipError_t launch_matvec(int type, int order, const uint8_t *W, int nb, int64_t groups, int ntok,
-                         const void *act, MvOut out, bool dump, hipStream_t s);
+
+// decode matvec (fgh_matvec.hip): up to 4 tensors of one type, order and width in one launch
+struct MvT {
+    const uint8_t *W;
+    float *y;
+    int64_t rows;    // rows per matrix
+    int64_t gpm;     // row groups per matrix
+    int64_t gfirst;  // first global group index of this tensor
+};
+struct MvArgs {
+    MvT t[4];
+    int nt;
+    int64_t groups;    // row groups over all the tensors
+    const float *x;    // fp32 activations, quantized inside the kernel
+    int64_t ldx, ldy;  // token strides of x and of every y
+    int nb, ntile;     // blocks and tiles per row
+    int32_t *dump_s, *dump_m;  // test hook: per (row, block) integers of tensor 0, or null
+};
+size_t matvec_lds_bytes(int type, int order, int nb);
+hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
 
 }  // namespace fgh

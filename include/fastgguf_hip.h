@@ -135,13 +135,15 @@ FGH_API int fgh_moe_ffn_dev(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tens
                     const fgh_tensor *down, int k, const float *logits_dev, const float *X_dev,
                     float *Y_dev, int n_tok);
 
-/* The two halves of a device-resident matvec, for callers that quantize one activation once and
- * multiply it with several tensors at different times (the reference's quantize_act, 2176, and
- * its row loop, 2612). fgh_act_quantize_dev quantizes ntok vectors of cols floats (row stride
- * cols) for ggml_type's activation kind into the context; fgh_matvec_act_dev multiplies the
- * context's current activation (token 0) with t, which must match its kind and cols. */
-FGH_API int fgh_act_quantize_dev(fgh_ctx *ctx, uint32_t ggml_type, int64_t cols, const float *x_dev, int ntok);
-FGH_API int fgh_matvec_act_dev(fgh_ctx *ctx, const fgh_tensor *t, float *y_dev);
+/* ---- HIP graphs of device-resident calls (launch-bound decode loops) ----
+ * fgh_graph_begin starts capturing the context stream; the *_dev calls that follow are recorded,
+ * not run; fgh_graph_end instantiates them as one executable graph that fgh_graph_launch replays
+ * on the context stream. While capturing, calls that would allocate or synchronize fail with
+ * FGH_ERR. No entry point records a memset, so replays are safe to repeat. */
+FGH_API int fgh_graph_begin(fgh_ctx *ctx);
+FGH_API int fgh_graph_end(fgh_ctx *ctx, void **graph);
+FGH_API int fgh_graph_launch(fgh_ctx *ctx, void *graph);
+FGH_API int fgh_graph_destroy(fgh_ctx *ctx, void *graph);
 
 /* ---- device memory, stream and timing helpers (for device-resident callers and benchmarks) */
 FGH_API int fgh_dev_alloc(fgh_ctx *ctx, uint64_t bytes, void **ptr);

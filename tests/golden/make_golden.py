@@ -28,9 +28,9 @@ from oracle import Reference  # noqa: E402
 def quant_inputs() -> np.ndarray:
     """Activation rows for the quantizer fixtures: normal values plus the edge cases the
     quantizers must get right (all-zero block, exact .5 ties after scaling, a single huge value,
-    negative-zero, subnormals)."""
+    negative-zero, subnormals where 1/d overflows, infinities and NaN)."""
     rng = np.random.Generator(np.random.PCG64(101))
-    x = rng.standard_normal((6, 1024)).astype(np.float32)
+    x = rng.standard_normal((7, 1024)).astype(np.float32)
     x[1, :256] = 0.0                          # all-zero Q8_K block -> d = id = 0, q = 0
     x[1, 256:288] = 0.0                       # all-zero Q8 block
     x[2, :256] = np.arange(256) - 127.5       # amax 128 -> halfway cases
@@ -40,6 +40,10 @@ def quant_inputs() -> np.ndarray:
     x[4, :] = -0.0
     x[4, 512:] = rng.standard_normal(512).astype(np.float32) * 1e-39  # subnormals
     x[5, :] = np.float32(127.0) * (rng.integers(-3, 4, 1024) / 2.0)   # exact ties x*id = k + .5
+    x[6, 3] = np.inf                          # non-finite inputs: d = inf, id = 0
+    x[6, 300] = -np.inf
+    x[6, 600] = np.nan                        # NaN is skipped by the amax compare, quantizes to 0
+    x[6, 900] = 3.4e38                        # near the top of the range
     return x
 
 

@@ -160,3 +160,41 @@ def test_upload_refusals(backend):
         small.upload(S.T_Q4_K, 4096, S.weights(S.T_Q4_K, 512, 4096, 1))  # 1.2 MB > 1 MB budget
     assert e.value.status == SKIP_MEM and small.info()["n_skip_mem"] == 1
     small.close()
+
+
+def test_graph_replay_matches_eager(backend, oracle):
+    """A captured layer (QKV, gate+up in one launch) replayed several times, with eager work and
+    synchronizations between replays: every replay equals the eager result and the oracle."""
+    cols = 4096
+    ws = {n: S.weights(S.T_Q4_K, r, cols, 60 + i) for i, (n, r) in enumerate((("qkv", 1536), ("gate", 2048), ("up", 2048)))}
+    ts = {n: backend.upload(S.T_Q4_K, cols, w) for n, w in ws.items()}
+    x = S.activations(cols, 64)
+    xd = backend.dev_alloc(4 * cols)
+    backend.h2d(xd, x)
+    yd = {n: backend.dev_alloc(4 * w.shape[0]) for n, w in ws.items()}
+    backend.graph_begin()
+    backend.matvec_dev(ts["qkv"], xd, yd["qkv"])
+    backend.matvec_multi_dev([ts["gate"], ts["up"]], xd, [yd["gate"], yd["up"]])
+    g = backend.graph_end()
+    want = {n: oracle.matvec(S.T_Q4_K, w, cols, x, O_RP) for n, w in ws.items()}
+    for rep in range(4):
+        for n in yd:  # clobber the outputs eagerly between replays
+            backend.h2d(yd[n], np.full(ws[n].shape[0], np.nan, np.float32))
+        backend.graph_launch(g)
+        backend.sync()
+        for n in yd:
+            got = np.empty(ws[n].shape[0], np.float32)
+            backend.d2h(got, yd[n])
+            check_vec(got, want[n])
+        check_vec(backend.matvec(ts["qkv"], x), want["qkv"])  # eager call between replays
+    backend.graph_destroy(g)
+    with pytest.raises(BackendError):  # host-synchronous calls are refused while capturing
+        backend.graph_begin()
+        try:
+            backend.matvec(ts["qkv"], x)
+        finally:
+            backend.graph_destroy(backend.graph_end())
+    for p in list(yd.values()) + [xd]:
+        backend.dev_free(p)
+    for t in ts.values():
+        t.free()
