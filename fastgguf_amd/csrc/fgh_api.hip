@@ -254,8 +254,11 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     }
     hipError_t e = hipMemcpy(stage, host, nbytes, hipMemcpyHostToDevice);
     if (e == hipSuccess)
-        e = fgh::launch_relayout((const uint8_t *)stage, t->dev, (int)type, rows, t->nb, t->ntile, t->gpm,
-                                 (int64_t)t->dev_bytes, row_bytes, c->stream);
+        e = type == FGH_T_Q4_K
+                ? fgh::launch_q4k_relayout((const uint8_t *)stage, t->dev, rows, t->nb, t->gpm, (int64_t)t->dev_bytes,
+                                           row_bytes, c->stream)
+                : fgh::launch_relayout((const uint8_t *)stage, t->dev, (int)type, rows, t->nb, t->ntile, t->gpm,
+                                       (int64_t)t->dev_bytes, row_bytes, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     (void)hipFree(stage);
     if (e != hipSuccess) {

@@ -16,9 +16,7 @@ namespace fgh {
 // partials are the reference's lane partials, and the fp32 chains can follow its order.
 // Rows past the end of a matrix are zero-filled (d = 0) and never stored.
 //
-//   Q4_K tile, one block of 8 rows, 1152 B (= 8 x 144):
-//     [0, 128)     meta: row r at 16r = the block's first 16 bytes (fp16 d, fp16 dmin, scales12)
-//     [128, 1152)  quants: slice (r, i) at 128 + 16(8r + i); dword j = file bytes 16+32j+4i..+3
+//   (Q4_K uses its own group layout, described in fgh_q4k.hip)
 //   Q6_K tile, one block of 8 rows, 1680 B (= 8 x 210):
 //     [0, 128)     int8 scales, row r at 16r (file bytes 192..207)
 //     [128, 144)   fp16 d, row r at 128 + 2r (file bytes 208..209)
@@ -80,6 +78,16 @@ __device__ __forceinline__ int dot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
+// (lo & 0xFFFF) | (hi << 16): two int16 values packed for dot2_i16 (v_perm_b32)
+__device__ __forceinline__ uint32_t pack_i16(int lo, int hi) {
+    return __builtin_amdgcn_perm((uint32_t)hi, (uint32_t)lo, 0x05040100u);
+}
+// dot product of two packed int16 pairs plus c (v_dot2_i32_i16)
+typedef short fgh_short2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ int dot2_i16(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(fgh_short2, a), __builtin_bit_cast(fgh_short2, b), c, false);
+}
+
 __device__ __forceinline__ int sbyte(uint32_t w, int k) {  // signed byte k of a dword
     return (int)(int8_t)(w >> (8 * k));
 }
@@ -134,7 +142,12 @@ struct MvArgs {
     int nb, ntile;     // blocks and tiles per row
     int32_t *dump_s, *dump_m;  // test hook: per (row, block) integers of tensor 0, or null
 };
-size_t matvec_lds_bytes(int type, int order, int nb);
+size_t matvec_lds_bytes(int type, int order, int nb);  // Q6_K / Q8_0 (fgh_matvec.hip)
+// Q4_K (fgh_q4k.hip): its own group layout and kernel
+size_t q4k_lds_bytes(int order, int nb);
+hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, hipStream_t s);
+hipError_t launch_q4k_relayout(const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t gpm, int64_t total,
+                               int64_t row_bytes, hipStream_t s);
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
 
 }  // namespace fgh

@@ -200,10 +200,12 @@ __global__ __launch_bounds__(256) void mv_kernel(MvArgs a) {
         int ti;
         const int64_t lg = tensor_of(g, ti);
         const uint8_t *Wg = a.t[ti].W + (size_t)lg * ntile * TILE;
+        // unconditional loads (slots past the end re-read the last tile and are not used), so
+        // the compiler can count outstanding loads and wait only for the chunk it computes
 #pragma unroll
         for (int k = 0; k < CS; ++k) {
-            const int tile = c * CT + 4 * k + slot;
-            if (tile < ntile) load_step<TYPE>(Wg, tile, 8 * r + i, r, sw[k]);
+            const int tile = min(c * CT + 4 * k + slot, ntile - 1);
+            load_step<TYPE>(Wg, tile, 8 * r + i, r, sw[k]);
         }
     };
 
@@ -369,29 +371,59 @@ __global__ __launch_bounds__(256) void mv_kernel(MvArgs a) {
 
         // ---- chain phase: ascending tiles of this chunk ----
         const int nct = min(CT, ntile - c * CT);
+        // (all reads first, then the ordered fused multiply-adds; records past nct are skipped)
         if (TYPE == T_Q4_K && ORDER == 1) {
             if (slot == 0 && i == 0) {
                 const float *rec = wrec + (size_t)r2 * CT * RN;
-                for (int tl = 0; tl < nct; ++tl) {
-                    const float4 p = *(const float4 *)(rec + tl * RN);
-                    acc = __builtin_fmaf(p.x, p.y, acc);
-                    macc = __builtin_fmaf(p.z, p.w, macc);
+#pragma unroll
+                for (int t0 = 0; t0 < CT; t0 += 4) {
+                    float4 p[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) p[u] = *(const float4 *)(rec + (t0 + u) * RN);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (t0 + u < nct) {
+                            acc = __builtin_fmaf(p[u].x, p[u].y, acc);
+                            macc = __builtin_fmaf(p[u].z, p[u].w, macc);
+                        }
                 }
             }
         } else if (TYPE == T_Q8_0) {
             if (slot == 0) {
                 const float *rec = wrec + (size_t)r2 * CT * RN;
                 const int nblk = min(4 * nct, nb - 4 * c * CT);
-                for (int bl = 0; bl < nblk; ++bl)
-                    acc = __builtin_fmaf(rec[(bl >> 2) * RN + 32 + (bl & 3)], rec[(bl >> 2) * RN + 8 * (bl & 3) + i], acc);
+#pragma unroll
+                for (int tl = 0; tl < CT; ++tl) {
+                    float lv[4], dv[4];
+#pragma unroll
+                    for (int bb = 0; bb < 4; ++bb) {
+                        lv[bb] = rec[tl * RN + 8 * bb + i];
+                        dv[bb] = rec[tl * RN + 32 + bb];
+                    }
+#pragma unroll
+                    for (int bb = 0; bb < 4; ++bb)
+                        if (4 * tl + bb < nblk) acc = __builtin_fmaf(dv[bb], lv[bb], acc);
+                }
             }
         } else {
             if (slot == 0) {
                 const float *rec = wrec + (size_t)r2 * CT * RN;
-                for (int tl = 0; tl < nct; ++tl) {
-                    const float *p = rec + tl * RN;
-                    acc = __builtin_fmaf(p[12], p[i], acc);
-                    if (i < 4) macc = __builtin_fmaf(p[13], p[8 + i], macc);
+#pragma unroll
+                for (int t0 = 0; t0 < CT; t0 += 4) {
+                    float lv[4], mv[4], dv[4], mdv[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        lv[u] = rec[(t0 + u) * RN + i];
+                        mv[u] = rec[(t0 + u) * RN + 8 + (i & 3)];
+                        dv[u] = rec[(t0 + u) * RN + 12];
+                        mdv[u] = rec[(t0 + u) * RN + 13];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (t0 + u < nct) {
+                            acc = __builtin_fmaf(dv[u], lv[u], acc);
+                            macc = __builtin_fmaf(mdv[u], mv[u], macc);
+                        }
                 }
             }
         }
@@ -442,7 +474,7 @@ static size_t mv_lds_bytes(int nb) {
 }
 
 size_t matvec_lds_bytes(int type, int order, int nb) {
-    if (type == T_Q4_K) return order == 1 ? mv_lds_bytes<T_Q4_K, 1>(nb) : mv_lds_bytes<T_Q4_K, 0>(nb);
+    if (type == T_Q4_K) return q4k_lds_bytes(order, nb);
     if (type == T_Q6_K) return mv_lds_bytes<T_Q6_K, 0>(nb);
     return mv_lds_bytes<T_Q8_0, 0>(nb);
 }
@@ -468,10 +500,7 @@ static hipError_t launch_t(const MvArgs &a, int ntok, int num_cu, hipStream_t s)
 
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
     const bool dump = a.dump_s != nullptr;
-    if (type == T_Q4_K && order == 1)
-        return dump ? launch_t<T_Q4_K, 1, true>(a, ntok, num_cu, s) : launch_t<T_Q4_K, 1, false>(a, ntok, num_cu, s);
-    if (type == T_Q4_K)
-        return dump ? launch_t<T_Q4_K, 0, true>(a, ntok, num_cu, s) : launch_t<T_Q4_K, 0, false>(a, ntok, num_cu, s);
+    if (type == T_Q4_K) return launch_q4k_matvec(order, a, ntok, s);
     if (type == T_Q6_K)
         return dump ? launch_t<T_Q6_K, 0, true>(a, ntok, num_cu, s) : launch_t<T_Q6_K, 0, false>(a, ntok, num_cu, s);
     if (type == T_Q8_0)
