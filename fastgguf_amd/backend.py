@@ -30,7 +30,7 @@ EXPORTS = (
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
-    "fgh_quantize", "fgh_block_ints", "fgh_fp16_to_f32",
+    "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_fp16_to_f32",
 )
 
 
@@ -88,6 +88,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_event_destroy": (i32, [vp, vp]),
         "fgh_quantize": (i32, [vp, i32, f32p, i32, vp]),
         "fgh_block_ints": (i32, [vp, vp, f32p, vp, vp]),
+        "fgh_gemm_block_ints": (i32, [vp, vp, f32p, i32, i32, vp, vp]),
         "fgh_fp16_to_f32": (i32, [vp, vp, i32, vp]),
     }
     for name, (res, args) in sig.items():
@@ -221,6 +222,15 @@ class Backend:
         s = np.empty((t.nout, t.nblocks), np.int32)
         m = np.empty((t.nout, t.nblocks), np.int32)
         self._check(self.lib.fgh_block_ints(self.ctx, t.handle, _p(x), _p(s), _p(m)))
+        return s, m
+
+    def gemm_block_ints(self, t: Tensor, X: np.ndarray):
+        """Per (token, row, block) integers of the prompt GEMM (Q4_K): sumi, msum [nb][nout][blocks]."""
+        X = np.ascontiguousarray(X, np.float32)
+        nb = X.shape[0]
+        s = np.empty((nb, t.nout, t.nblocks), np.int32)
+        m = np.empty((nb, t.nout, t.nblocks), np.int32)
+        self._check(self.lib.fgh_gemm_block_ints(self.ctx, t.handle, _p(X), t.cols, nb, _p(s), _p(m)))
         return s, m
 
     def fp16_to_f32(self, h: np.ndarray) -> np.ndarray:

@@ -30,6 +30,7 @@ struct fgh_ctx {
     std::string err = "ok";
     // scratch, grown on demand (gpu_grow_buf, fastgguf.c:2083-2091)
     DevBuf x, y, aqs, ad, abs;
+    DevBuf gq, gy, gb;  // prompt-GEMM activations (launch_gemm_quant layout)
     int num_cu = 256;         // compute units (sizes the persistent decode grid)
     bool capturing = false;   // inside fgh_graph_begin / fgh_graph_end
 };
@@ -139,6 +140,37 @@ static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const fl
     return FGH_OK;
 }
 
+// the prompt GEMM for a Q4_K tensor: quantize T tokens (device X, stride ldx) into the GEMM
+// layout, then one MFMA launch; ds / dm: optional [T][rows * n_mats][nb] integer dump
+static int gemm_q4k(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
+                    int32_t *ds, int32_t *dm) {
+    const int Tp = T > 32 ? 64 : 32;
+    int rc;
+    if ((rc = grow(c, c->gq, (size_t)Tp * t->cols)) || (rc = grow(c, c->gy, (size_t)Tp * t->nb * 4)) ||
+        (rc = grow(c, c->gb, (size_t)Tp * t->nb * 16)))
+        return rc;
+    HIP_TRY(c, fgh::launch_gemm_quant(X, ldx, t->nb, T, Tp, (int8_t *)c->gq.p, (float *)c->gy.p, (int8_t *)c->gb.p,
+                                      c->stream));
+    fgh::GemmArgs a;
+    memset(&a, 0, sizeof(a));
+    a.W = t->dev;
+    a.Y = Y;
+    a.rows = t->rows;
+    a.gpm = t->gpm;
+    a.nrows = t->rows * t->n_mats;
+    a.nb = t->nb;
+    a.qs = (const int8_t *)c->gq.p;
+    a.ydT = (const float *)c->gy.p;
+    a.bsp = (const int8_t *)c->gb.p;
+    a.Tp = Tp;
+    a.T = T;
+    a.ldy = ldy;
+    a.dump_s = ds;
+    a.dump_m = dm;
+    HIP_TRY(c, fgh::launch_q4k_gemm(a, c->stream));
+    return FGH_OK;
+}
+
 // host-synchronous and allocating calls cannot be recorded into a graph
 #define NO_CAPTURE(c) \
     do { \
@@ -182,7 +214,7 @@ void fgh_close(fgh_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
-    for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs})
+    for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->gy, &c->gb})
         if (b->p) (void)hipFree(b->p);
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -324,7 +356,9 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
     if (!X || !Y || nb < 1 || nb > FG_BATCH || ldx < t->cols || ldy < t->rows * t->n_mats)
         return fail(c, FGH_ERR_ARG, "matmul: bad arguments");
     HIP_TRY(c, hipSetDevice(c->device));
-    if (nb >= 8) return fail(c, FGH_ERR, "matmul: the prompt GEMM for nb >= 8 is not available in this build");
+    // nb >= 8: the prompt GEMM (matmul 3018-3031) on int8 MFMA for Q4_K; Q6_K and Q8_0 run the
+    // per-token decode kernels (their fp32 orders differ from gemm_kquant's only by rounding)
+    if (nb >= 8 && t->type == FGH_T_Q4_K) return gemm_q4k(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
     float *ys[1] = {Y};
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
 }
@@ -555,6 +589,38 @@ int fgh_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *x, int32_t *sum
     (void)hipFree(ds);
     if (rc) return rc;
     if (e != hipSuccess) return fail(c, FGH_ERR_DEVICE, "block_ints: %s", hipGetErrorString(e));
+    return FGH_OK;
+}
+
+int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, int nb, int32_t *sumi,
+                        int32_t *msum) {
+    int rc = check_tensor(c, t);
+    if (rc) return rc;
+    NO_CAPTURE(c);
+    if (!X || !sumi || !msum || nb < 1 || nb > FG_BATCH || ldx < t->cols)
+        return fail(c, FGH_ERR_ARG, "gemm_block_ints: bad arguments");
+    if (t->type != FGH_T_Q4_K) return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMM is for Q4_K tensors");
+    const int64_t nout = t->rows * t->n_mats;
+    const size_t nint = (size_t)nb * nout * t->nb;
+    HIP_TRY(c, hipSetDevice(c->device));
+    if ((rc = grow(c, c->x, (size_t)nb * t->cols * 4)) || (rc = grow(c, c->y, (size_t)nb * nout * 4))) return rc;
+    void *ds = nullptr;
+    HIP_TRY(c, hipMalloc(&ds, nint * 8));
+    int32_t *dsi = (int32_t *)ds, *dmi = dsi + nint;
+    hipError_t e = hipMemcpy2DAsync(c->x.p, (size_t)t->cols * 4, X, (size_t)ldx * 4, (size_t)t->cols * 4, nb,
+                                    hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        rc = gemm_q4k(c, t, (const float *)c->x.p, t->cols, (float *)c->y.p, nout, nb, dsi, dmi);
+        if (!rc) {
+            e = hipMemcpyAsync(sumi, dsi, nint * 4, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipMemcpyAsync(msum, dmi, nint * 4, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        }
+    }
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(ds);
+    if (rc) return rc;
+    if (e != hipSuccess) return fail(c, FGH_ERR_DEVICE, "gemm_block_ints: %s", hipGetErrorString(e));
     return FGH_OK;
 }
 

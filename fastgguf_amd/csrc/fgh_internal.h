@@ -46,6 +46,16 @@ struct ActQ8 {
     int16_t *s16;
 };
 
+// (int)lrintf(v) as the reference computes it on x86 (fastgguf.c:762, 786): round half to even;
+// a NaN or infinite v (id = 1/d overflows when amax is subnormal) gives the "integer indefinite"
+// value, whose low byte is 0. A finite id keeps |v| <= 127, so no other case arises.
+__device__ __forceinline__ int q8_round(float v) {
+    return fabsf(v) < 2147483648.0f ? (int)rintf(v) : 0;
+}
+__device__ __forceinline__ uint32_t pack_q(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);
+}
+
 // ---- cross-lane helpers (DPP: no LDS traffic) ----
 __device__ __forceinline__ int dpp_xor1(int v) {  // quad_perm [1,0,3,2]
     return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
@@ -149,5 +159,23 @@ hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, hipStream_t s
 hipError_t launch_q4k_relayout(const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t gpm, int64_t total,
                                int64_t row_bytes, hipStream_t s);
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
+
+// prompt-batch Q4_K GEMM (fgh_gemm.hip): 1..64 tokens, weights in the Q4_K decode layout
+struct GemmArgs {
+    const uint8_t *W;   // Q4_K tensor (group layout)
+    float *Y;           // Y[tok * ldy + row]
+    int64_t rows, gpm;  // rows and row groups per matrix
+    int64_t nrows;      // rows over all matrices (outputs per token)
+    int nb;             // 256-blocks per row
+    const int8_t *qs;   // activations from launch_gemm_quant
+    const float *ydT;
+    const int8_t *bsp;
+    int Tp, T;          // padded token count (32 or 64), tokens
+    int64_t ldy;
+    int32_t *dump_s, *dump_m;  // test hook: [T][nrows][nb] integers, or null
+};
+hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, int8_t *qs, float *ydT, int8_t *bsp,
+                             hipStream_t s);
+hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s);
 
 }  // namespace fgh

@@ -41,14 +41,6 @@ __device__ __forceinline__ float dpp_ror_f32(float v, int ctrl_n) {
     return __builtin_bit_cast(float, r);
 }
 
-__device__ __forceinline__ int q8_round(float v) {  // (int)lrintf(v) as on x86
-    return fabsf(v) < 2147483648.0f ? (int)rintf(v) : 0;
-}
-
-__device__ __forceinline__ uint32_t pack_q(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);
-}
-
 // LDS: natural-order Q8_K blocks: qs [nb][256] at 0, d [nb] at 256 nb, bsums [nb][16] at
 // align16(260 nb); then 4 wavefront record areas
 __host__ __device__ constexpr size_t q4_off_d(int nb) { return (size_t)nb * 256; }

@@ -162,9 +162,13 @@ FGH_API int fgh_event_destroy(fgh_ctx *ctx, void *ev);
  * n/32 blocks of 40 bytes; FGH_ACT_Q8K: n/256 blocks of 292 bytes), from host x.
  * fgh_block_ints: per (row, block) integer parts of dot(W[r], Q8(x)) as the device kernels
  * compute them: sumi / msum [rows * n_mats][blocks per row] (see the oracle's fgo_block_ints).
+ * fgh_gemm_block_ints: the same integers as the prompt GEMM (Q4_K, nb tokens, 1..64) computes
+ * them: sumi / msum [nb][rows * n_mats][blocks per row], token t from row t of X (stride ldx).
  * fgh_fp16_to_f32: the device's fp16 -> fp32 decode of n codes. */
 FGH_API int fgh_quantize(fgh_ctx *ctx, int kind, const float *x, int n, void *out_blocks);
 FGH_API int fgh_block_ints(fgh_ctx *ctx, const fgh_tensor *t, const float *x, int32_t *sumi, int32_t *msum);
+FGH_API int fgh_gemm_block_ints(fgh_ctx *ctx, const fgh_tensor *t, const float *X, int ldx, int nb,
+                                int32_t *sumi, int32_t *msum);
 FGH_API int fgh_fp16_to_f32(fgh_ctx *ctx, const uint16_t *h, int n, float *out);
 
 #ifdef __cplusplus
