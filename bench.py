@@ -10,8 +10,11 @@ steps rotate over COPIES distinct device copies of the layer (>= 512 MB in total
 
 value  = whole-layer algorithmic bytes (weights + fp32 x in + fp32 y out) / step time, in GB/s.
 roofline: the dominant kernel is the Q4_K decode matvec at the gate shape (4096->14336); its
-         launches are timed one by one with HIP events on the library's stream. A step replays
-         one HIP graph of the layer's launches (one per weight copy).
+         duration is the mean over back-to-back launches captured in one HIP graph and timed with
+         HIP events on the library's stream. A step replays one HIP graph of the layer's launches
+         (one per weight copy).
+prefill: BASELINE config 4 (64 tokens x 4096 -> 14336, Q4_K) on the int8 MFMA GEMM, timed the
+         same way, cold (rotating weights) and Infinity-Cache hot, as TOPS and fraction of 5 POPS.
 cpu_baseline: the reference's own CPU kernels (oracle/_ref, compiled from fastgguf.c) on the same
          layer with its default repacked Q4_K path, on this host's cores, for a bounded sample.
 Prints one JSON line.
@@ -29,6 +32,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Q4_K decode matvec HBM GB/s (%peak); 64-tok prefill int8 TOPS (%MFMA peak)"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
 LAYER = [  # name, rows (outputs), cols (inputs)
     ("qkv", 6144, 4096),
     ("o", 4096, 4096),
@@ -151,27 +155,40 @@ def main() -> int:
     layer_bytes = sum(algo_bytes(r, c) for _, r, c in LAYER)
     value = layer_bytes / (ms_step * 1e-3) / 1e9
 
-    # per-kernel durations: each launch timed alone with HIP events on the library's stream
-    def kernel_time(launch, reps: int) -> float:
-        evs = [(be.event(), be.event()) for _ in range(reps)]
-        for i, (a, b) in enumerate(evs):
-            be.record(a)
-            launch(i % args.copies)
-            be.record(b)
-        be.sync()
-        t = [be.elapsed_ms(a, b) for a, b in evs]
-        for a, b in evs:
-            be.event_destroy(a)
-            be.event_destroy(b)
-        return float(np.mean(t)) * 1e3  # us
+    # per-kernel durations: GRAPH_LAUNCHES back-to-back launches of one kernel (rotating over the
+    # weight copies) captured in one HIP graph, replayed and timed with HIP events on the library's
+    # stream; time / launches = the kernel's duration plus the in-graph gap between launches
+    GRAPH_LAUNCHES = 50
 
+    def kernel_time(launch, reps: int) -> float:
+        launch(0)  # grows any scratch before capture
+        be.graph_begin()
+        for i in range(GRAPH_LAUNCHES):
+            launch(i)
+        gr = be.graph_end()
+        be.graph_launch(gr)
+        be.sync()
+        a, b = be.event(), be.event()
+        n = max(1, reps // GRAPH_LAUNCHES)
+        be.record(a)
+        for _ in range(n):
+            be.graph_launch(gr)
+        be.record(b)
+        be.sync()
+        t = be.elapsed_ms(a, b)
+        be.event_destroy(a)
+        be.event_destroy(b)
+        be.graph_destroy(gr)
+        return t * 1e3 / (n * GRAPH_LAUNCHES)  # us
+
+    nc = args.copies
     launches = {
-        "qkv": (lambda c: be.matvec_dev(tensors[c]["qkv"], xd["x"], yd["qkv"]), algo_bytes(6144, 4096)),
-        "o": (lambda c: be.matvec_dev(tensors[c]["o"], xd["a"], yd["o"]), algo_bytes(4096, 4096)),
-        "gate": (lambda c: be.matvec_dev(tensors[c]["gate"], xd["x2"], yd["gate"]), algo_bytes(14336, 4096)),
-        "gate+up": (lambda c: be.matvec_multi_dev([tensors[c]["gate"], tensors[c]["up"]], xd["x2"],
+        "qkv": (lambda i: be.matvec_dev(tensors[i % nc]["qkv"], xd["x"], yd["qkv"]), algo_bytes(6144, 4096)),
+        "o": (lambda i: be.matvec_dev(tensors[i % nc]["o"], xd["a"], yd["o"]), algo_bytes(4096, 4096)),
+        "gate": (lambda i: be.matvec_dev(tensors[i % nc]["gate"], xd["x2"], yd["gate"]), algo_bytes(14336, 4096)),
+        "gate+up": (lambda i: be.matvec_multi_dev([tensors[i % nc]["gate"], tensors[i % nc]["up"]], xd["x2"],
                                                  [yd["gate"], yd["up"]]), 2 * algo_bytes(14336, 4096) - 4 * 4096),
-        "down": (lambda c: be.matvec_dev(tensors[c]["down"], xd["h"], yd["down"]), algo_bytes(4096, 14336)),
+        "down": (lambda i: be.matvec_dev(tensors[i % nc]["down"], xd["h"], yd["down"]), algo_bytes(4096, 14336)),
     }
     kernels = {}
     for n, (fn, nbytes) in launches.items():
@@ -180,8 +197,29 @@ def main() -> int:
         kernels[n] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
     g = kernels["gate"]
     roofline = {"bound": "hbm", "achieved": g["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g["frac"],
-                "traffic": None, "kernel": "mv_kernel<Q4_K, repacked> (Q4_K decode matvec, gate 4096->14336)",
+                "traffic": None, "kernel": "q4k_mv_kernel<repacked> (Q4_K decode matvec, gate 4096->14336)",
                 "bytes_per_launch": algo_bytes(14336, 4096), "us_per_launch": g["us"]}
+
+    # prefill: 64 tokens x 4096 -> 14336 Q4_K on the int8 MFMA GEMM; one launch
+    # = device Q8_K quantization of X + the GEMM. Cold: rotating over the 2 * COPIES distinct
+    # gate/up matrices; hot: one matrix (Infinity-Cache resident).
+    T = 64
+    Xp = S.activations(4096, 5, rows=T)
+    xpd = be.dev_alloc(Xp.nbytes)
+    be.h2d(xpd, Xp)
+    ypd = be.dev_alloc(4 * T * 14336)
+    mats = [t[n] for t in tensors for n in ("gate", "up")]
+    ops = 2.0 * T * 4096 * 14336
+    prefill = {}
+    for kind, pick in (("cold", lambda i: mats[i % len(mats)]), ("hot", lambda i: mats[0])):
+        us = kernel_time(lambda i: be.matmul_dev(pick(i), xpd, ypd, T), args.kernel_reps)
+        tops = ops / (us * 1e-6) / 1e12
+        prefill[kind] = {"us": round(us, 3), "TOPS": round(tops, 2), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+    prefill.update({"workload": "cfg4: 64 tokens x K=4096 -> N=14336, Q4_K x Q8_K (quantization of X included)",
+                    "ops_per_launch": ops, "peak_TOPS": INT8_PEAK_TOPS,
+                    "kernel": "q4k_gemm_kernel (int8 MFMA 32x32x32, split sub-block scales)"})
+    be.dev_free(xpd)
+    be.dev_free(ypd)
 
     cpu = cpu_baseline(layer_w, xs, args.cpu_seconds) if args.cpu_seconds > 0 else None
     info = be.info()
@@ -199,6 +237,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -27,7 +27,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 def hipcc_cmd(out: str = LIB) -> list[str]:
     return [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
             "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            "-Wall", "-Wno-unused-function", "-fvisibility=hidden",
+            "-Wall", "-Wno-unused-function", "-fvisibility=hidden", "-Wl,-z,defs",
             "-I", os.path.join(ROOT, "include"),
             "-o", out] + [os.path.join(CSRC, s) for s in SOURCES]
 

@@ -19,10 +19,13 @@
 // values 32 g + 16 (l / 32) + i of a group, so the products pair up whatever order the hardware
 // uses inside one K step.
 //
-// Weights are read in the decode layout (fgh_q4k.hip): the GEMM needs no second copy.
-// Workgroup: 4 wavefronts = 2 slices of 32 rows x 2 halves of the blocks (b even / b odd); each
-// wavefront covers all tokens (one or two 32-token tiles) and keeps the next block's operands in
-// flight while it computes the current one. The two halves are added at the end through LDS.
+// Weights are read in the decode layout (fgh_q4k.hip): the GEMM needs no second copy. A
+// workgroup owns 64 rows and all tokens: 4 * NTW wavefronts = 2 slices of 32 rows x 2 halves of
+// the blocks (even / odd) x NTW tiles of 32 tokens. It walks the blocks in steps of two: the
+// step's weights for all 64 rows (18 KB) are staged in LDS by the whole workgroup with coalesced
+// loads (128 contiguous bytes per row half) and read back as MFMA fragments; activations are read
+// straight from global memory in a fragment-ordered layout (1 KB contiguous per load). Both are
+// double-buffered one step ahead. The two halves of the blocks are added at the end through LDS.
 //
 // fp32 order: per (row, token) and block t = d * float(isum) - dmin * float(msum) (one fma),
 // acc = fma(yd, t, acc) over the wavefront's blocks, out = acc_even + acc_odd. The integers are
@@ -38,9 +41,10 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 // ---------------------------------------------------------------------------------------------
 // Activation quantizer for the GEMM (quantize_q8k, fastgguf.c:773-793, bit-exact): one wavefront
 // per (token, 256-block); lane l holds values 4l..4l+3. Writes
-//   qs  [Tp][K]      int8, natural order
+//   qs  [nb][8][Tp][32] int8: group g of block b of token t at ((8 b + g) Tp + t) * 32, so the 32
+//                    tokens of one MFMA fragment are 1 KB contiguous
 //   ydT [nb][Tp]     fp32 block scales, token-minor (one float4 = 4 consecutive tokens)
-//   bsp [Tp][nb][16] int8: the 32-value sums bs_g = bsums[2g] + bsums[2g+1] as bl_g (bytes 0..7,
+//   bsp [nb][Tp][16] int8: the 32-value sums bs_g = bsums[2g] + bsums[2g+1] as bl_g (bytes 0..7,
 //                    bs & 127) and bh_g (bytes 8..15, bs >> 7)
 // Tokens T..Tp-1 are written as zeros.
 // ---------------------------------------------------------------------------------------------
@@ -60,14 +64,13 @@ __global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict
     const float id = d > 0.0f ? 1.0f / d : 0.0f;
     const int q0 = q8_round(v.x * id), q1 = q8_round(v.y * id);
     const int q2 = q8_round(v.z * id), q3 = q8_round(v.w * id);
-    const size_t K = (size_t)nb * 256;
-    *(uint32_t *)(qs + (size_t)tok * K + (size_t)b * 256 + 4 * lane) = pack_q(q0, q1, q2, q3);
+    *(uint32_t *)(qs + (((size_t)b * 8 + (lane >> 3)) * Tp + tok) * 32 + 4 * (lane & 7)) = pack_q(q0, q1, q2, q3);
     int s = q0 + q1 + q2 + q3;  // 32-value group g = lanes 8g..8g+7
     s += __shfl_xor(s, 1, 64);
     s += __shfl_xor(s, 2, 64);
     s += __shfl_xor(s, 4, 64);
     if ((lane & 7) == 0) {
-        int8_t *p = bsp + ((size_t)tok * nb + b) * 16;
+        int8_t *p = bsp + ((size_t)b * Tp + tok) * 16;
         p[lane >> 3] = (int8_t)(s & 127);
         p[8 + (lane >> 3)] = (int8_t)(s >> 7);
     }
@@ -77,34 +80,85 @@ __global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict
 // ---------------------------------------------------------------------------------------------
 // The GEMM kernel
 // ---------------------------------------------------------------------------------------------
-struct BlockOps {
-    uint4 meta;      // fp16 d, fp16 dmin, 12 bytes of packed scales / mins
-    uint4 pc[4];     // chunk j (sub-blocks 2j, 2j+1): 16 bytes, piece l / 32
-    uint4 a[2][8];   // activations: token tile t, group g
-    uint2 am[2];     // activation group sums as bytes, token tile t
-    float4 yd[2][4]; // block scales of tokens 8k + 4 (l / 32) + 0..3 of tile t
+constexpr int GW_STAGE = 18432;  // LDS bytes of one weight stage: quants 16 KB + meta 2 KB
+
+// the decode-layout address of one 16-byte piece: piece h of chunk j of block b of a row, given
+// the row's wavefront region base (group + 128 nb + 256 nb * w') and its index r2 in the region
+__device__ __forceinline__ const uint8_t *q4_piece(const uint8_t *region, int nb, int r2, int b, int h, int j) {
+    const int q = r2 * nb + b;
+    const int st = q >> 4, p = q & 15, np = min(16, 2 * nb - 16 * st);
+    return region + 2048 * st + h * 64 * np + 64 * p + 16 * j;
+}
+
+// One workgroup's share of a weight stage (blocks 2s and 2s+1 of its 64 rows), held by thread tid:
+// quant units u = tid + k * NT (u = 16 row + 8 h + 4 blk + j: eight consecutive threads read 128
+// contiguous bytes) and, for tid < 128, the meta of (row tid / 2, blk tid % 2).
+template <int NT>
+struct WStage {
+    static constexpr int NU = 1024 / NT;
+    const uint8_t *region[NU];  // per unit: the row's wavefront region in the decode layout
+    int r2[NU];
+    const uint8_t *mregion;      // meta: group base + 16 * 2 nb * w'
+    int mr2;
+    uint4 q[NU], m;
 };
 
-template <int NTT>
-__device__ __forceinline__ void gemm_load(BlockOps &o, const uint8_t *G, int nb, int rr, int b, int h, int n,
-                                          const GemmArgs &a) {
-    const int q = (rr & 1) * nb + b;
-    const int w = rr >> 1;
-    o.meta = ld16(G + 16 * ((size_t)2 * nb * w + q));
-    const int s = q >> 4, p = q & 15, np = min(16, 2 * nb - 16 * s);
-    const uint8_t *qb = G + (size_t)128 * nb + (size_t)256 * nb * w + 2048 * s + h * 64 * np + 64 * p;
+template <int NT>
+__device__ __forceinline__ void wstage_init(WStage<NT> &w, const GemmArgs &a, int64_t row0, int tid) {
+    const int nb = a.nb;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o.pc[j] = ld16(qb + 16 * j);
-    const size_t K = (size_t)nb * 256;
-#pragma unroll
-    for (int t = 0; t < NTT; ++t) {
-        const int8_t *yq = a.qs + (size_t)(32 * t + n) * K + (size_t)b * 256 + 16 * h;
-#pragma unroll
-        for (int g = 0; g < 8; ++g) o.a[t][g] = *(const uint4 *)(yq + 32 * g);
-        o.am[t] = *(const uint2 *)(a.bsp + ((size_t)(32 * t + n) * nb + b) * 16 + 8 * h);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) o.yd[t][k] = *(const float4 *)(a.ydT + (size_t)b * a.Tp + 32 * t + 8 * k + 4 * h);
+    for (int k = 0; k <= WStage<NT>::NU; ++k) {
+        const int u = k < WStage<NT>::NU ? tid + k * NT : 16 * (tid >> 1);  // k == NU: the meta row
+        int64_t R = row0 + (u >> 4);
+        R = R < a.nrows ? R : a.nrows - 1;
+        const int64_t mat = R / a.rows, r = R - mat * a.rows;
+        const int rr = (int)(r & 7);
+        const uint8_t *G = a.W + (size_t)(mat * a.gpm + (r >> 3)) * 1152 * nb;
+        if (k < WStage<NT>::NU) {
+            w.region[k] = G + (size_t)128 * nb + (size_t)256 * nb * (rr >> 1);
+            w.r2[k] = rr & 1;
+        } else {
+            w.mregion = G + (size_t)32 * nb * (rr >> 1);
+            w.mr2 = rr & 1;
+        }
     }
+}
+
+template <int NT>
+__device__ __forceinline__ void wstage_load(WStage<NT> &w, int nb, int s, int tid) {
+#pragma unroll
+    for (int k = 0; k < WStage<NT>::NU; ++k) {
+        const int u = tid + k * NT;
+        const int b = min(2 * s + ((u >> 2) & 1), nb - 1);
+        w.q[k] = ld16(q4_piece(w.region[k], nb, w.r2[k], b, (u >> 3) & 1, u & 3));
+    }
+    if (tid < 128) w.m = ld16(w.mregion + 16 * (w.mr2 * nb + min(2 * s + (tid & 1), nb - 1)));
+}
+
+// LDS stage layout: quants [blk][j][h][row 0..63] x 16 B (a fragment = 512 B contiguous per h),
+// meta at 16 KB: [blk][row] x 16 B
+template <int NT>
+__device__ __forceinline__ void wstage_store(const WStage<NT> &w, uint8_t *buf, int tid) {
+#pragma unroll
+    for (int k = 0; k < WStage<NT>::NU; ++k) {
+        const int u = tid + k * NT;
+        const int j = u & 3, blk = (u >> 2) & 1, h = (u >> 3) & 1, row = u >> 4;
+        *(uint4 *)(buf + ((blk * 4 + j) * 2 + h) * 1024 + row * 16) = w.q[k];
+    }
+    if (tid < 128) *(uint4 *)(buf + 16384 + ((tid & 1) * 64 + (tid >> 1)) * 16) = w.m;
+}
+
+// one lane's activation operands of one block: group g (16 values of token 32 tt + l % 32) and
+// the token's 32-value sums as bytes (bl_0..7 or bh_0..7)
+struct ActOps {
+    uint4 av[8];
+    uint2 am;
+};
+
+__device__ __forceinline__ void act_load(ActOps &o, const GemmArgs &a, int b, int tok, int h) {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) o.av[g] = *(const uint4 *)(a.qs + (((size_t)b * 8 + g) * a.Tp + tok) * 32 + 16 * h);
+    o.am = *(const uint2 *)(a.bsp + ((size_t)b * a.Tp + tok) * 16 + 8 * h);
 }
 
 __device__ __forceinline__ v4i u4v(uint4 u) { return v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w}; }
@@ -115,40 +169,46 @@ __device__ __forceinline__ uint32_t bmul(uint32_t q, uint32_t f2) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
-template <int NTT, bool DUMP>
-__device__ __forceinline__ void gemm_block(const BlockOps &o, float (&acc)[NTT][16], int h, int b, int64_t R,
-                                           const GemmArgs &a) {
-    const float d = fp16_bits_to_f32(o.meta.x & 0xFFFF);
-    const float dmin = fp16_bits_to_f32(o.meta.x >> 16);
-    const Q4KScales sc = q4k_scales(o.meta.y, o.meta.z, o.meta.w);
-    v16i chi[NTT], clo[NTT];
+// One 256-block of one wavefront: weights from the LDS stage (slice blk of the step), activations
+// from registers. live == false: a padding block (odd block counts): computed, weighted by zero,
+// not dumped.
+template <bool DUMP>
+__device__ __forceinline__ void gemm_block(const ActOps &o, const uint8_t *stage, int blk, int rs, int n, int h,
+                                           int tt, float (&acc)[16], const float *__restrict__ yds, int b, bool live,
+                                           int64_t row, const GemmArgs &a) {
+    const uint4 meta = *(const uint4 *)(stage + 16384 + (blk * 64 + rs * 32 + n) * 16);
+    uint4 pc[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t P[4] = {o.pc[j].x, o.pc[j].y, o.pc[j].z, o.pc[j].w};
+    for (int j = 0; j < 4; ++j) pc[j] = *(const uint4 *)(stage + ((blk * 4 + j) * 2 + h) * 1024 + (rs * 32 + n) * 16);
+    const Q4KScales sc = q4k_scales(meta.y, meta.z, meta.w);
+    const float d = fp16_bits_to_f32(meta.x & 0xFFFF);
+    const float dmin = fp16_bits_to_f32(meta.x >> 16);
+    // pass 0: q * sh over the block's 8 groups; pass 1 continues from 8 * Chi with q * sl
+    v16i ai;
 #pragma unroll
-        for (int hn = 0; hn < 2; ++hn) {
-            const int g = 2 * j + hn;
-            const uint32_t s6 = (uint32_t)q4k_sc(sc, g);
-            const uint32_t fh = (s6 >> 3) * 0x00010001u, fl = (s6 & 7) * 0x00010001u;
-            v4i bh, bl;
+    for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t qn = hn ? ((P[k] >> 4) & 0x0F0F0F0Fu) : (P[k] & 0x0F0F0F0Fu);
-                bh[k] = (int)bmul(qn, fh);
-                bl[k] = (int)bmul(qn, fl);
-            }
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t P[4] = {pc[j].x, pc[j].y, pc[j].z, pc[j].w};
 #pragma unroll
-            for (int t = 0; t < NTT; ++t) {
-                const v4i av = u4v(o.a[t][g]);
-                if (g == 0) {
+            for (int hn = 0; hn < 2; ++hn) {
+                const int g = 2 * j + hn;
+                const uint32_t s6 = (uint32_t)q4k_sc(sc, g);
+                const uint32_t f = (pass == 0 ? (s6 >> 3) : (s6 & 7)) * 0x00010001u;
+                v4i bw;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) bw[k] = (int)bmul(hn ? ((P[k] >> 4) & 0x0F0F0F0Fu) : (P[k] & 0x0F0F0F0Fu), f);
+                if (pass == 0 && g == 0) {
                     const v16i z = {};
-                    chi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bh, z, 0, 0, 0);
-                    clo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bl, z, 0, 0, 0);
+                    ai = __builtin_amdgcn_mfma_i32_32x32x32_i8(u4v(o.av[g]), bw, z, 0, 0, 0);
                 } else {
-                    chi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bh, chi[t], 0, 0, 0);
-                    clo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bl, clo[t], 0, 0, 0);
+                    ai = __builtin_amdgcn_mfma_i32_32x32x32_i8(u4v(o.av[g]), bw, ai, 0, 0, 0);
                 }
             }
+        }
+        if (pass == 0) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) ai[v] <<= 3;
         }
     }
     // the row's eight mins as bytes; lanes 0-31 feed K slots 0..7 (bl), lanes 32-63 slots 8..15 (bh)
@@ -160,85 +220,101 @@ __device__ __forceinline__ void gemm_block(const BlockOps &o, float (&acc)[NTT][
     }
     const long mp = (long)(((uint64_t)m1 << 32) | m0);
     const long b1 = h == 0 ? mp : 0L, b2 = h == 0 ? 0L : mp;
+    const v16i z = {};
+    const long ab = (long)(((uint64_t)o.am.y << 32) | o.am.x);
+    v16i ms = __builtin_amdgcn_mfma_i32_32x32x16_i8(ab, b2, z, 0, 0, 0);
 #pragma unroll
-    for (int t = 0; t < NTT; ++t) {
-        const v16i z = {};
-        const long av = (long)(((uint64_t)o.am[t].y << 32) | o.am[t].x);
-        const v16i c1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, b1, z, 0, 0, 0);
-        const v16i c2 = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, b2, z, 0, 0, 0);
+    for (int v = 0; v < 16; ++v) ms[v] <<= 7;
+    ms = __builtin_amdgcn_mfma_i32_32x32x16_i8(ab, b1, ms, 0, 0, 0);
+    float4 yd[4];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int isum = (chi[t][v] << 3) + clo[t][v];
-            const int msum = c1[v] + (c2[v] << 7);
-            const float4 y4 = o.yd[t][v >> 2];
-            const float yd = (v & 3) == 0 ? y4.x : (v & 3) == 1 ? y4.y : (v & 3) == 2 ? y4.z : y4.w;
-            const float tt = __builtin_fmaf(-dmin, (float)msum, d * (float)isum);
-            acc[t][v] = __builtin_fmaf(yd, tt, acc[t][v]);
-            if (DUMP) {
-                const int tok = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (tok < a.T && R < a.nrows) {
-                    const size_t i = ((size_t)tok * a.nrows + R) * a.nb + b;
-                    a.dump_s[i] = isum;
-                    a.dump_m[i] = msum;
-                }
+    for (int k = 0; k < 4; ++k) yd[k] = *(const float4 *)(yds + b * a.Tp + 32 * tt + 8 * k + 4 * h);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int isum = ai[v], msum = ms[v];
+        const float4 q4 = yd[v >> 2];
+        float ydv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+        ydv = live ? ydv : 0.0f;
+        const float t = __builtin_fmaf(-dmin, (float)msum, d * (float)isum);
+        acc[v] = __builtin_fmaf(ydv, t, acc[v]);
+        if (DUMP) {
+            const int tok = 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (live && tok < a.T && row < a.nrows) {
+                const size_t i = ((size_t)tok * a.nrows + row) * a.nb + b;
+                a.dump_s[i] = isum;
+                a.dump_m[i] = msum;
             }
         }
     }
 }
 
-template <int NTT, bool DUMP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void q4k_gemm_kernel(GemmArgs a) {
-    __shared__ float red[2][NTT][16][64];
+// NTW = token tiles (1 or 2). Wavefront w: rs = w & 1 (32-row slice), kh = (w >> 1) & 1 (even /
+// odd blocks), tt = w >> 2 (32-token tile). Step s covers blocks 2s (kh 0) and 2s + 1 (kh 1).
+template <int NTW, bool DUMP>
+__global__ __launch_bounds__(256 * NTW) void q4k_gemm_kernel(GemmArgs a) {
+    constexpr int NT = 256 * NTW;
+    // LDS: the block scales of every token (ydT, nb x Tp floats), then two weight stages (the
+    // reduction area reuses the first after the loop)
+    extern __shared__ __align__(16) float lds_g[];
+    float *yds = lds_g;
+    uint8_t *stage0 = (uint8_t *)(lds_g + (size_t)a.nb * a.Tp);
+    uint8_t *stage1 = stage0 + GW_STAGE;
     const int tid = threadIdx.x, l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rs = wave & 1, kh = wave >> 1;
+    const int rs = wave & 1, kh = (wave >> 1) & 1, tt = wave >> 2;
     const int n = l & 31, h = l >> 5;
-    const int nb = a.nb;
-    const int64_t row = (int64_t)blockIdx.x * 64 + 32 * rs + n;
-    const int64_t R = row < a.nrows ? row : a.nrows - 1;  // rows past the end re-read the last one
-    const int64_t mat = R / a.rows, r = R - mat * a.rows;
-    const int rr = (int)(r & 7);
-    const uint8_t *G = a.W + (size_t)(mat * a.gpm + (r >> 3)) * 1152 * nb;
+    const int nb = a.nb, nsteps = (nb + 1) >> 1;
+    const int64_t row0 = (int64_t)blockIdx.x * 64;
+    const int64_t row = row0 + 32 * rs + n;
+    const int tok = 32 * tt + n;
 
-    float acc[NTT][16];
-#pragma unroll
-    for (int t = 0; t < NTT; ++t)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[t][v] = 0.0f;
+    WStage<NT> ws;
+    wstage_init(ws, a, row0, tid);
+    wstage_load(ws, nb, 0, tid);
+    ActOps A, B;
+    act_load(A, a, min(kh, nb - 1), tok, h);
+    for (int i = tid; i < nb * a.Tp / 4; i += NT) ((float4 *)yds)[i] = ((const float4 *)a.ydT)[i];
+    wstage_store(ws, stage0, tid);
+    __syncthreads();
 
-    // blocks kh, kh + 2, ...: two operand sets alternate, the next block's loads in flight while
-    // the current one computes (loads past the end repeat the wavefront's last block)
-    const int cnt = (nb - kh + 1) >> 1;
-    const int last = kh + 2 * (cnt - 1);
-    BlockOps o0, o1;
-    if (cnt > 0) {
-        gemm_load<NTT>(o0, G, nb, rr, kh, h, n, a);
-        for (int i = 0; i < cnt; i += 2) {
-            const int b0 = kh + 2 * i, b1 = min(b0 + 2, last), b2 = min(b0 + 4, last);
-            gemm_load<NTT>(o1, G, nb, rr, b1, h, n, a);
-            gemm_block<NTT, DUMP>(o0, acc, h, b0, row, a);
-            if (i + 1 < cnt) {
-                gemm_load<NTT>(o0, G, nb, rr, b2, h, n, a);
-                gemm_block<NTT, DUMP>(o1, acc, h, b1, row, a);
-            }
+    float acc[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    for (int s = 0; s < nsteps; s += 2) {
+        // step s: stage0, set A; loads of step s + 1 (stage1, set B) in flight
+        wstage_load(ws, nb, min(s + 1, nsteps - 1), tid);
+        act_load(B, a, min(2 * (s + 1) + kh, nb - 1), tok, h);
+        __builtin_amdgcn_sched_barrier(0);
+        gemm_block<DUMP>(A, stage0, kh, rs, n, h, tt, acc, yds, min(2 * s + kh, nb - 1), 2 * s + kh < nb, row, a);
+        __builtin_amdgcn_sched_barrier(0);
+        wstage_store(ws, stage1, tid);
+        __syncthreads();
+        if (s + 1 < nsteps) {  // uniform
+            // step s + 1: stage1, set B; loads of step s + 2 (stage0, set A) in flight
+            wstage_load(ws, nb, min(s + 2, nsteps - 1), tid);
+            act_load(A, a, min(2 * (s + 2) + kh, nb - 1), tok, h);
+            __builtin_amdgcn_sched_barrier(0);
+            gemm_block<DUMP>(B, stage1, kh, rs, n, h, tt, acc, yds, min(2 * (s + 1) + kh, nb - 1),
+                             2 * (s + 1) + kh < nb, row, a);
+            __builtin_amdgcn_sched_barrier(0);
+            wstage_store(ws, stage0, tid);
+            __syncthreads();
         }
     }
-    // odd-block half -> LDS; the even half adds it (fixed order) and stores
+    // odd-block half -> LDS (over the first stage: every wavefront is past its last read of it);
+    // the even half adds it (fixed order) and stores
+    float(*red)[2][16][64] = (float(*)[2][16][64])stage0;
     if (kh == 1) {
 #pragma unroll
-        for (int t = 0; t < NTT; ++t)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) red[rs][t][v][l] = acc[t][v];
+        for (int v = 0; v < 16; ++v) red[tt][rs][v][l] = acc[v];
     }
     __syncthreads();
     if (kh == 0 && row < a.nrows) {
 #pragma unroll
-        for (int t = 0; t < NTT; ++t)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int tok = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (tok < a.T) a.Y[(size_t)tok * a.ldy + row] = acc[t][v] + red[rs][t][v][l];
-            }
+        for (int v = 0; v < 16; ++v) {
+            const int tk = 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (tk < a.T) a.Y[(size_t)tk * a.ldy + row] = acc[v] + red[tt][rs][v][l];
+        }
     }
 }
 
@@ -249,15 +325,19 @@ hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp,
     return hipGetLastError();
 }
 
+size_t q4k_gemm_lds_bytes(int nb, int Tp) { return (size_t)nb * Tp * 4 + 2 * (size_t)GW_STAGE; }
+
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > 64 || a.Tp != (a.T > 32 ? 64 : 32) || a.nb < 1 || a.nrows < 1) return hipErrorInvalidValue;
+    const size_t lds = q4k_gemm_lds_bytes(a.nb, a.Tp);
+    if (lds > 65536) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.nrows + 63) / 64));
     if (a.Tp == 64) {
-        if (a.dump_s) q4k_gemm_kernel<2, true><<<grid, 256, 0, s>>>(a);
-        else q4k_gemm_kernel<2, false><<<grid, 256, 0, s>>>(a);
+        if (a.dump_s) q4k_gemm_kernel<2, true><<<grid, 512, lds, s>>>(a);
+        else q4k_gemm_kernel<2, false><<<grid, 512, lds, s>>>(a);
     } else {
-        if (a.dump_s) q4k_gemm_kernel<1, true><<<grid, 256, 0, s>>>(a);
-        else q4k_gemm_kernel<1, false><<<grid, 256, 0, s>>>(a);
+        if (a.dump_s) q4k_gemm_kernel<1, true><<<grid, 256, lds, s>>>(a);
+        else q4k_gemm_kernel<1, false><<<grid, 256, lds, s>>>(a);
     }
     return hipGetLastError();
 }

@@ -176,6 +176,7 @@ struct GemmArgs {
 };
 hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, int8_t *qs, float *ydT, int8_t *bsp,
                              hipStream_t s);
+size_t q4k_gemm_lds_bytes(int nb, int Tp);  // <= 65536 for the GEMM to run
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s);
 
 }  // namespace fgh
