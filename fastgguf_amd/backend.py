@@ -30,7 +30,7 @@ EXPORTS = (
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
-    "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_fp16_to_f32",
+    "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_expf", "fgh_fp16_to_f32",
 )
 
 
@@ -90,6 +90,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_block_ints": (i32, [vp, vp, f32p, vp, vp]),
         "fgh_gemm_block_ints": (i32, [vp, vp, f32p, i32, i32, vp, vp]),
         "fgh_fp16_to_f32": (i32, [vp, vp, i32, vp]),
+        "fgh_expf": (i32, [vp, f32p, i32, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -232,6 +233,13 @@ class Backend:
         m = np.empty((nb, t.nout, t.nblocks), np.int32)
         self._check(self.lib.fgh_gemm_block_ints(self.ctx, t.handle, _p(X), t.cols, nb, _p(s), _p(m)))
         return s, m
+
+    def expf(self, x: np.ndarray) -> np.ndarray:
+        """The device's expf (MoE softmax and silu) of every value of x."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.size, np.float32)
+        self._check(self.lib.fgh_expf(self.ctx, _p(x), x.size, _p(out)))
+        return out
 
     def fp16_to_f32(self, h: np.ndarray) -> np.ndarray:
         h = np.ascontiguousarray(h, np.uint16)

@@ -31,6 +31,7 @@ struct fgh_ctx {
     // scratch, grown on demand (gpu_grow_buf, fastgguf.c:2083-2091)
     DevBuf x, y, aqs, ad, abs;
     DevBuf gq, gy, gb;  // prompt-GEMM activations (launch_gemm_quant layout)
+    DevBuf msel, mw, mg, mu, mh, md, mlog;  // MoE: selection, weights, gate / up / h / down outputs
     int num_cu = 256;         // compute units (sizes the persistent decode grid)
     bool capturing = false;   // inside fgh_graph_begin / fgh_graph_end
 };
@@ -119,14 +120,17 @@ static int quantize_dev(fgh_ctx *c, uint32_t type, int64_t cols, const float *x,
 // one decode launch over n tensors that share type, order and width; x: ntok fp32 vectors
 // (device, stride ldx); y[i]: outputs of tensor i (token stride ldy)
 static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const float *x, int64_t ldx,
-                         float *const *y, int64_t ldy, int ntok, int32_t *ds, int32_t *dm) {
+                         float *const *y, int64_t ldy, int ntok, int32_t *ds, int32_t *dm,
+                         const int32_t *sel = nullptr, int xdiv = 1) {
     fgh::MvArgs a;
     memset(&a, 0, sizeof(a));
     int64_t g = 0;
     for (int i = 0; i < n; i++) {
         a.t[i] = fgh::MvT{t[i]->dev, y[i], t[i]->rows, t[i]->gpm, g};
-        g += t[i]->groups;
+        g += sel ? t[i]->gpm : t[i]->groups;  // with an expert index: the groups of one matrix
     }
+    a.sel = sel;
+    a.xdiv = xdiv;
     a.nt = n;
     a.groups = g;
     a.x = x;
@@ -214,7 +218,8 @@ void fgh_close(fgh_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
-    for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->gy, &c->gb})
+    for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->gy, &c->gb, &c->msel, &c->mw, &c->mg,
+                      &c->mu, &c->mh, &c->md, &c->mlog})
         if (b->p) (void)hipFree(b->p);
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -363,9 +368,42 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
 }
 
-int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *, const fgh_tensor *, const fgh_tensor *, int,
-                    const float *, const float *, float *, int) {
-    return fail(c, FGH_ERR, "moe_ffn: not available in this build");
+int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, const fgh_tensor *down, int k,
+                    const float *logits, const float *X, float *Y, int n_tok) {
+    int rc;
+    if ((rc = check_tensor(c, gate)) || (rc = check_tensor(c, up)) || (rc = check_tensor(c, down))) return rc;
+    const int64_t E = gate->n_mats, n_embd = gate->cols, ff = gate->rows;
+    if (up->n_mats != E || up->cols != n_embd || up->rows != ff || down->n_mats != E || down->cols != ff ||
+        down->rows != n_embd)
+        return fail(c, FGH_ERR_ARG, "moe_ffn: gate/up must be [E][ff][n_embd] and down [E][n_embd][ff]");
+    if (!logits || !X || !Y || n_tok < 1 || n_tok > FG_BATCH || k < 1 || k > E || k > 64 || E > 512)
+        return fail(c, FGH_ERR_ARG, "moe_ffn: bad arguments (k %d, experts %lld, tokens %d)", k, (long long)E, n_tok);
+    HIP_TRY(c, hipSetDevice(c->device));
+    const int64_t np = (int64_t)n_tok * k;  // (token, selected expert) slots
+    if ((rc = grow(c, c->msel, (size_t)np * 4)) || (rc = grow(c, c->mw, (size_t)np * 4)) ||
+        (rc = grow(c, c->mg, (size_t)np * ff * 4)) || (rc = grow(c, c->mu, (size_t)np * ff * 4)) ||
+        (rc = grow(c, c->mh, (size_t)np * ff * 4)) || (rc = grow(c, c->md, (size_t)np * n_embd * 4)))
+        return rc;
+    int32_t *sel = (int32_t *)c->msel.p;
+    float *w = (float *)c->mw.p, *G = (float *)c->mg.p, *U = (float *)c->mu.p, *H = (float *)c->mh.p,
+          *D = (float *)c->md.p;
+    HIP_TRY(c, fgh::launch_moe_route(logits, (int)E, k, n_tok, sel, w, c->stream));
+    // gate and up: one launch when their type and order agree (both read the same x row)
+    if (gate->type == up->type && gate->order == up->order) {
+        const fgh_tensor *gu[2] = {gate, up};
+        float *ys[2] = {G, U};
+        if ((rc = matvec_launch(c, 2, gu, X, n_embd, ys, ff, (int)np, nullptr, nullptr, sel, k))) return rc;
+    } else {
+        float *yg[1] = {G}, *yu[1] = {U};
+        if ((rc = matvec_launch(c, 1, &gate, X, n_embd, yg, ff, (int)np, nullptr, nullptr, sel, k)) ||
+            (rc = matvec_launch(c, 1, &up, X, n_embd, yu, ff, (int)np, nullptr, nullptr, sel, k)))
+            return rc;
+    }
+    HIP_TRY(c, fgh::launch_moe_silu_mul(G, U, H, np * ff, c->stream));
+    float *yd[1] = {D};
+    if ((rc = matvec_launch(c, 1, &down, H, ff, yd, n_embd, (int)np, nullptr, nullptr, sel, 1))) return rc;
+    HIP_TRY(c, fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, c->stream));
+    return FGH_OK;
 }
 
 // ---- host-pointer entry points (synchronous) ----
@@ -419,9 +457,27 @@ int fgh_matmul(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, float *
     return FGH_OK;
 }
 
-int fgh_moe_ffn(fgh_ctx *c, const fgh_tensor *, const fgh_tensor *, const fgh_tensor *, int, const float *,
-                const float *, float *, int, int32_t *, float *) {
-    return fail(c, FGH_ERR, "moe_ffn: not available in this build");
+int fgh_moe_ffn(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, const fgh_tensor *down, int k,
+                const float *logits, const float *X, float *Y, int n_tok, int32_t *sel_out, float *w_out) {
+    int rc = check_tensor(c, gate);
+    if (rc) return rc;
+    NO_CAPTURE(c);
+    if (!logits || !X || !Y || n_tok < 1 || n_tok > FG_BATCH) return fail(c, FGH_ERR_ARG, "moe_ffn: bad arguments");
+    const int64_t E = gate->n_mats, n_embd = gate->cols;
+    HIP_TRY(c, hipSetDevice(c->device));
+    if ((rc = grow(c, c->x, (size_t)n_tok * n_embd * 4)) || (rc = grow(c, c->y, (size_t)n_tok * n_embd * 4)) ||
+        (rc = grow(c, c->mlog, (size_t)n_tok * E * 4)))
+        return rc;
+    HIP_TRY(c, hipMemcpyAsync(c->x.p, X, (size_t)n_tok * n_embd * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(c->mlog.p, logits, (size_t)n_tok * E * 4, hipMemcpyHostToDevice, c->stream));
+    if ((rc = fgh_moe_ffn_dev(c, gate, up, down, k, (const float *)c->mlog.p, (const float *)c->x.p, (float *)c->y.p,
+                              n_tok)))
+        return rc;
+    HIP_TRY(c, hipMemcpyAsync(Y, c->y.p, (size_t)n_tok * n_embd * 4, hipMemcpyDeviceToHost, c->stream));
+    if (sel_out) HIP_TRY(c, hipMemcpyAsync(sel_out, c->msel.p, (size_t)n_tok * k * 4, hipMemcpyDeviceToHost, c->stream));
+    if (w_out) HIP_TRY(c, hipMemcpyAsync(w_out, c->mw.p, (size_t)n_tok * k * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return FGH_OK;
 }
 
 // ---- memory, stream, events ----
@@ -621,6 +677,19 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     (void)hipFree(ds);
     if (rc) return rc;
     if (e != hipSuccess) return fail(c, FGH_ERR_DEVICE, "gemm_block_ints: %s", hipGetErrorString(e));
+    return FGH_OK;
+}
+
+int fgh_expf(fgh_ctx *c, const float *x, int n, float *out) {
+    if (!c || !x || !out || n <= 0) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
+    HIP_TRY(c, hipSetDevice(c->device));
+    int rc;
+    if ((rc = grow(c, c->x, (size_t)n * 4)) || (rc = grow(c, c->y, (size_t)n * 4))) return rc;
+    HIP_TRY(c, hipMemcpyAsync(c->x.p, x, (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, fgh::launch_expf((const float *)c->x.p, (float *)c->y.p, n, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(out, c->y.p, (size_t)n * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
     return FGH_OK;
 }
 

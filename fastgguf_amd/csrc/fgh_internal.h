@@ -151,6 +151,10 @@ struct MvArgs {
     int64_t ldx, ldy;  // token strides of x and of every y
     int nb, ntile;     // blocks and tiles per row
     int32_t *dump_s, *dump_m;  // test hook: per (row, block) integers of tensor 0, or null
+    // expert indirection (MoE): when sel is set, token slot y (blockIdx.y) uses matrix sel[y] of
+    // every tensor (launched with the groups of one matrix) and activation row y / xdiv
+    const int32_t *sel;
+    int xdiv;
 };
 size_t matvec_lds_bytes(int type, int order, int nb);  // Q6_K / Q8_0 (fgh_matvec.hip)
 // Q4_K (fgh_q4k.hip): its own group layout and kernel
@@ -159,6 +163,52 @@ hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, hipStream_t s
 hipError_t launch_q4k_relayout(const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t gpm, int64_t total,
                                int64_t row_bytes, hipStream_t s);
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
+
+// MoE around the expert matvecs (fgh_moe.hip)
+// expf as glibc >= 2.27 computes it (the method of ARM's optimized-routines expf), in double:
+// with N = 32, z = x N / ln 2, k = round(z), r = fma(N / ln 2, x, -k) (glibc's x86-64 FMA build
+// fuses it), exp(x) = 2^(k / N) * 2^(r / N), where
+// 2^(k / N) = table[k mod N] (the correctly rounded 2^(i / N), i < N, stored with i << 47
+// subtracted) with k << 47 added to its bits, and 2^(r / N) ~ (c0 r + c1) r^2 + (c2 r + 1)
+// (fused multiply-adds);
+// one rounding to float at the end. Matches the host libm bit for bit (the oracle tests sweep the
+// floats); the reference calls expf in softmax and silu (fastgguf.c:3118, 3151).
+__host__ __device__ inline float expf_ref(float x) {
+    constexpr uint64_t tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
+    };
+    const double invln2n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    if (!(x < 128.0f)) return x > 0.0f ? __builtin_inff() : x;  // +inf, NaN; overflow below
+    if (!(x > -128.0f)) return 0.0f;
+    const double xd = x;
+    const double z = invln2n * xd;
+    double kd = z + shift;
+    uint64_t ki;
+    __builtin_memcpy(&ki, &kd, 8);
+    kd -= shift;
+    const double r = __builtin_fma(invln2n, xd, -kd);  // fused, as glibc's FMA build (x86-64)
+    const uint64_t t = tab[ki % 32] + (ki << 47);
+    double s;
+    __builtin_memcpy(&s, &t, 8);
+    const double p = __builtin_fma(c0, r, c1), r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(p, r2, y);
+    return (float)(y * s);
+}
+hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s);  // test hook
+hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok, int32_t *sel, float *w, hipStream_t s);
+hipError_t launch_moe_silu_mul(const float *g, const float *u, float *h, int64_t n, hipStream_t s);
+hipError_t launch_moe_combine(const float *d, const float *w, float *y, int n_embd, int k, int n_tok, int64_t ldy,
+                              hipStream_t s);
 
 // prompt-batch Q4_K GEMM (fgh_gemm.hip): 1..64 tokens, weights in the Q4_K decode layout
 struct GemmArgs {

@@ -199,7 +199,8 @@ __global__ __launch_bounds__(256) void mv_kernel(MvArgs a) {
         const int c = (int)(it % nchunk);
         int ti;
         const int64_t lg = tensor_of(g, ti);
-        const uint8_t *Wg = a.t[ti].W + (size_t)lg * ntile * TILE;
+        const int64_t mg = a.sel ? (int64_t)a.sel[tok] * a.t[ti].gpm : 0;  // selected matrix (MoE)
+        const uint8_t *Wg = a.t[ti].W + (size_t)(mg + lg) * ntile * TILE;
         // unconditional loads (slots past the end re-read the last tile and are not used), so
         // the compiler can count outstanding loads and wait only for the chunk it computes
 #pragma unroll
@@ -212,7 +213,7 @@ __global__ __launch_bounds__(256) void mv_kernel(MvArgs a) {
     StepW bufA[CS], bufB[CS];
     if (nitems > 0) load_item(0, bufA);  // first weights in flight during quantization
 
-    quantize_to_lds<TYPE>(a.x + (size_t)tok * a.ldx, nb, act);
+    quantize_to_lds<TYPE>(a.x + (size_t)(tok / a.xdiv) * a.ldx, nb, act);
     __syncthreads();
 
     const int8_t *aqs = (const int8_t *)act;

@@ -1,0 +1,126 @@
+// fgh_moe.hip - the MoE FFN around the expert matvecs (moe_ffn, fastgguf.c:4588-4642), per token:
+//   route:    p = softmax(logits) (softmax_inplace 3147-3156), top-k by repeated argmax (3328-3332,
+//             first index on ties), w_j = p_j / max(sum_j p_j, 2^-14) (4594-4604)
+//   gate, up: expert sel_j's rows of gate / up times Q8_K(x) (the decode kernels with an expert
+//             index read on the device)
+//   h_j     = silu(g_j) * u_j, silu(x) = x / (1 + expf(-x)) (silu_f 3118)
+//   down:     d_j = expert sel_j's rows of down times Q8_K(h_j)
+//   y_i     = sum over j in order of fma(w_j, d_j[i], s)  (4626-4635; gcc contracts s += w*dot)
+// Every dot product runs the reference's own per-row order (dot_q4_K_q8k and friends), so the
+// integers are bit-exact and, given the same expf, so is everything else.
+#include "fgh_internal.h"
+
+namespace fgh {
+
+// one wavefront per token; n_expert <= 64 * MOE_EPL
+constexpr int MOE_EPL = 8;
+
+__global__ __launch_bounds__(64) void moe_route_kernel(const float *__restrict__ logits, int n_expert, int k,
+                                                       int32_t *__restrict__ sel, float *__restrict__ w) {
+    __shared__ float p[64 * MOE_EPL];
+    __shared__ float wl[64];
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float *lg = logits + (size_t)t * n_expert;
+    // max (order-independent, exact)
+    float mx = -INFINITY;
+    for (int i = lane; i < n_expert; i += 64) mx = fmaxf(mx, lg[i]);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    for (int i = lane; i < n_expert; i += 64) p[i] = expf_ref(lg[i] - mx);
+    __syncthreads();
+    // the reference's sequential sum, then its scaling by the reciprocal
+    __shared__ float inv_s;
+    if (lane == 0) {
+        float sum = 0.0f;
+        for (int i = 0; i < n_expert; ++i) sum += p[i];
+        inv_s = sum > 0.0f ? 1.0f / sum : 0.0f;
+        if (!(sum > 0.0f)) inv_s = -1.0f;  // marker: leave p unscaled
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    if (inv >= 0.0f)
+        for (int i = lane; i < n_expert; i += 64) p[i] *= inv;
+    __syncthreads();
+    // top-k by repeated argmax: the first index holding the largest value (v > best, scanning up)
+    float wsum = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int i = lane; i < n_expert; i += 64)
+            if (p[i] > bv) {  // per lane: ascending indices, so the first maximum is kept
+                bv = p[i];
+                bi = i;
+            }
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (bi == 0x7fffffff) bi = 0;  // every value -inf or NaN: argmax_f returns 0
+        const float pv = p[bi];
+        __syncthreads();
+        if (lane == 0) {
+            sel[(size_t)t * k + j] = bi;
+            wl[j] = pv;
+            p[bi] = -1.0f;
+        }
+        wsum += pv;  // every lane keeps the same sequential sum
+        __syncthreads();
+    }
+    if (wsum < 6.103515625e-5f) wsum = 6.103515625e-5f;
+    if (lane < k) w[(size_t)t * k + lane] = wl[lane] / wsum;
+}
+
+__global__ void moe_silu_mul_kernel(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ h,
+                                    int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float x = g[i];
+        h[i] = x / (1.0f + expf_ref(-x)) * u[i];
+    }
+}
+
+// y[t][i] = sum_j fma(w[t][j], d[t k + j][i], s), j ascending
+__global__ void moe_combine_kernel(const float *__restrict__ d, const float *__restrict__ w, float *__restrict__ y,
+                                   int n_embd, int k, int64_t ldy) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_embd) return;
+    float s = 0.0f;
+    for (int j = 0; j < k; ++j) s = __builtin_fmaf(w[(size_t)t * k + j], d[((size_t)t * k + j) * n_embd + i], s);
+    y[(size_t)t * ldy + i] = s;
+}
+
+__global__ void expf_kernel(const float *__restrict__ x, float *__restrict__ y, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = expf_ref(x[i]);
+}
+
+hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s) {
+    expf_kernel<<<(n + 255) / 256, 256, 0, s>>>(x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok, int32_t *sel, float *w,
+                            hipStream_t s) {
+    if (n_expert < 1 || n_expert > 64 * MOE_EPL || k < 1 || k > n_expert || k > 64) return hipErrorInvalidValue;
+    moe_route_kernel<<<n_tok, 64, 0, s>>>(logits, n_expert, k, sel, w);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_silu_mul(const float *g, const float *u, float *h, int64_t n, hipStream_t s) {
+    const int64_t want = (n + 255) / 256;
+    moe_silu_mul_kernel<<<(unsigned)(want < 4096 ? want : 4096), 256, 0, s>>>(g, u, h, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const float *d, const float *w, float *y, int n_embd, int k, int n_tok, int64_t ldy,
+                              hipStream_t s) {
+    moe_combine_kernel<<<dim3((n_embd + 255) / 256, n_tok), 256, 0, s>>>(d, w, y, n_embd, k, ldy);
+    return hipGetLastError();
+}
+
+}  // namespace fgh

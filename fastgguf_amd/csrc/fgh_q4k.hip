@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256 * GPW) void q4k_mv_kernel(MvArgs a) {
     const int tok = blockIdx.y;
     const int64_t g = (int64_t)blockIdx.x * GPW + gsub;
     if (g >= a.groups) {  // a trailing workgroup's spare group: only help quantize
-        const float *xs = a.x + (size_t)blockIdx.y * a.ldx;
+        const float *xs = a.x + (size_t)(blockIdx.y / a.xdiv) * a.ldx;
         for (int rb = 0; rb < nb; rb += 16 * GPW) {
             XRound xr;
             q8k_load(xs, nb, rb, xr);
@@ -136,7 +136,8 @@ __global__ __launch_bounds__(256 * GPW) void q4k_mv_kernel(MvArgs a) {
     for (int k = 1; k < 4; ++k)
         if (k < a.nt && g >= a.t[k].gfirst) ti = k;
     const int64_t lg = g - a.t[ti].gfirst;
-    const uint8_t *G = a.t[ti].W + (size_t)lg * 1152 * nb;
+    const int64_t mg = a.sel ? (int64_t)a.sel[tok] * a.t[ti].gpm : 0;  // selected matrix (MoE)
+    const uint8_t *G = a.t[ti].W + (size_t)(mg + lg) * 1152 * nb;
     const uint8_t *meta = G + (size_t)16 * P * wave;
     const uint8_t *quant = G + (size_t)128 * nb + (size_t)256 * nb * wave;
 
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(256 * GPW) void q4k_mv_kernel(MvArgs a) {
     float *fin = rec + (size_t)2 * nb * (ORDER == 1 ? 4 : 16);
 
     // (1) x for the first quantization round, then (2) every weight load of the first chunk
-    const float *x = a.x + (size_t)tok * a.ldx;
+    const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
     XRound xr;
     q8k_load(x, nb, 0, xr);
     Q4Step st[MAXS];

@@ -164,11 +164,13 @@ FGH_API int fgh_event_destroy(fgh_ctx *ctx, void *ev);
  * compute them: sumi / msum [rows * n_mats][blocks per row] (see the oracle's fgo_block_ints).
  * fgh_gemm_block_ints: the same integers as the prompt GEMM (Q4_K, nb tokens, 1..64) computes
  * them: sumi / msum [nb][rows * n_mats][blocks per row], token t from row t of X (stride ldx).
- * fgh_fp16_to_f32: the device's fp16 -> fp32 decode of n codes. */
+ * fgh_fp16_to_f32: the device's fp16 -> fp32 decode of n codes.
+ * fgh_expf: the device's expf (the MoE softmax and silu) of n values. */
 FGH_API int fgh_quantize(fgh_ctx *ctx, int kind, const float *x, int n, void *out_blocks);
 FGH_API int fgh_block_ints(fgh_ctx *ctx, const fgh_tensor *t, const float *x, int32_t *sumi, int32_t *msum);
 FGH_API int fgh_gemm_block_ints(fgh_ctx *ctx, const fgh_tensor *t, const float *X, int ldx, int nb,
                                 int32_t *sumi, int32_t *msum);
+FGH_API int fgh_expf(fgh_ctx *ctx, const float *x, int n, float *out);
 FGH_API int fgh_fp16_to_f32(fgh_ctx *ctx, const uint16_t *h, int n, float *out);
 
 #ifdef __cplusplus

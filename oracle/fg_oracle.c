@@ -536,6 +536,71 @@ int fgo_matmul(uint32_t type, int order, const uint8_t *w, int64_t rows, int col
 /* silu_f (fastgguf.c:3118) */
 float fgo_silu(float x) { return x / (1.0f + expf(-x)); }
 
+/* the method of ARM optimized-routines' expf (glibc >= 2.27, built with FMA on x86-64): N = 32,
+ * z = x N / ln 2, k = round(z) (by adding 1.5 * 2^52), r = fma(N / ln 2, x, -k), 2^(k/N) from a table of the correctly rounded
+ * 2^(i/N) with the exponent bits of k/N added, 2^(r/N) ~ (c0 r + c1) r^2 + (c2 r + 1), all in
+ * double, one rounding to float. The table is 2^(i/32) rounded to nearest double (computed from
+ * the mathematics), stored minus i << 47 as the method stores it. */
+static const uint64_t EXP2_TAB[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
+};
+
+float fgo_expf_restated(float x) {
+    if (!(x < 128.0f)) return x > 0.0f ? INFINITY : x;
+    if (!(x > -128.0f)) return 0.0f;
+    const double invln2n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    double xd = x, z = invln2n * xd, kd = z + shift;
+    uint64_t ki, t;
+    memcpy(&ki, &kd, 8);
+    kd -= shift;
+    double r = fma(invln2n, xd, -kd), s; /* fused as in glibc's FMA build (x86-64 with FMA) */
+    t = EXP2_TAB[ki % 32] + (ki << 47);
+    memcpy(&s, &t, 8);
+    double p = fma(c0, r, c1), r2 = r * r, y = fma(c2, r, 1.0);
+    y = fma(p, r2, y);
+    return (float)(y * s);
+}
+
+void fgo_expf_n(const float *x, int n, float *out) {
+    for (int i = 0; i < n; i++) out[i] = expf(x[i]);
+}
+
+static int64_t f32_key(float f) { /* monotone integer key of a float */
+    int32_t i;
+    memcpy(&i, &f, 4);
+    return i < 0 ? -(int64_t)(i & 0x7fffffff) : (int64_t)i;
+}
+
+uint64_t fgo_expf_compare(float lo, float hi, uint32_t stride, uint64_t *n_checked, int *max_ulp) {
+    uint64_t bad = 0, n = 0;
+    int mu = 0;
+    for (int64_t k = f32_key(lo); k <= f32_key(hi); k += stride) {
+        int32_t i = k < 0 ? (int32_t)((uint32_t)(-k) | 0x80000000u) : (int32_t)k;
+        float x;
+        memcpy(&x, &i, 4);
+        float a = expf(x), b = fgo_expf_restated(x);
+        if (isnan(a) && isnan(b)) continue;
+        n++;
+        if (memcmp(&a, &b, 4) != 0) {
+            bad++;
+            int d = (int)llabs(f32_key(a) - f32_key(b));
+            if (d > mu) mu = d;
+        }
+    }
+    if (n_checked) *n_checked = n;
+    if (max_ulp) *max_ulp = mu;
+    return bad;
+}
+
 /* softmax_inplace (3147-3156), argmax_f (3328-3332), selection and renormalisation (4594-4604) */
 void fgo_moe_route(const float *logits, int n_expert, int k, int32_t *sel, float *w) {
     float *p = (float *)malloc((size_t)n_expert * sizeof(float));

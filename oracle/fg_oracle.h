@@ -81,6 +81,14 @@ void fgo_moe_route(const float *logits, int n_expert, int k, int32_t *sel, float
 /* silu_f (fastgguf.c:3118) with the C library's expf */
 float fgo_silu(float x);
 
+/* expf restated from its published method (ARM optimized-routines, glibc >= 2.27), as the GPU
+ * backend computes it. fgo_expf_compare counts the float inputs x (every stride-th bit pattern of
+ * [lo, hi]) where it differs from this libm's expf, and the largest difference in ulps; the
+ * reference's softmax and silu call expf (fastgguf.c:3118, 3151). */
+float fgo_expf_restated(float x);
+void fgo_expf_n(const float *x, int n, float *out); /* this libm's expf of n values */
+uint64_t fgo_expf_compare(float lo, float hi, uint32_t stride, uint64_t *n_checked, int *max_ulp);
+
 /* dequantize_row for the three types (fastgguf.c:552, 622, 669): textbook value decode */
 int fgo_dequantize_row(uint32_t type, const uint8_t *raw, float *out, int n);
 

@@ -63,6 +63,10 @@ class Oracle:
         L.fgo_moe_route.restype = None
         L.fgo_silu.argtypes = [C.c_float]
         L.fgo_silu.restype = C.c_float
+        L.fgo_expf_restated.argtypes = [C.c_float]
+        L.fgo_expf_restated.restype = C.c_float
+        L.fgo_expf_compare.argtypes = [C.c_float, C.c_float, C.c_uint32, C.POINTER(C.c_uint64), C.POINTER(C.c_int)]
+        L.fgo_expf_compare.restype = C.c_uint64
         L.fgo_dequantize_row.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
 
     # -- quantizers
@@ -143,6 +147,22 @@ class Oracle:
 
     def silu(self, x: float) -> float:
         return self.lib.fgo_silu(x)
+
+    def expf(self, x: float) -> float:
+        return self.lib.fgo_expf_restated(x)
+
+    def libm_expf(self, x: np.ndarray) -> np.ndarray:
+        """This host's libm expf of every value (what the reference's softmax and silu call)."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.size, np.float32)
+        self.lib.fgo_expf_n(_ptr(x), x.size, _ptr(out))
+        return out
+
+    def expf_compare(self, lo: float, hi: float, stride: int):
+        """(mismatches, checked, max ulps) of the restated expf against libm's expf."""
+        n, mu = C.c_uint64(), C.c_int()
+        bad = self.lib.fgo_expf_compare(lo, hi, stride, C.byref(n), C.byref(mu))
+        return int(bad), int(n.value), int(mu.value)
 
     def moe_ffn(self, types, gate, up, down, n_expert, k, n_embd, ff, logits, X, want_h=False):
         X = np.ascontiguousarray(X, np.float32)

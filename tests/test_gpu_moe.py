@@ -1,0 +1,92 @@
+"""GPU parity of the MoE FFN (moe_ffn, fastgguf.c:4588-4642) through the C ABI.
+
+Every dot product runs the reference's own per-row order, so expert selection, weights and outputs
+are compared bit for bit: against the reference's golden outputs (including tied router logits)
+and against the oracle on random and BASELINE config-5 shapes. The one function outside the
+integer and IEEE-basic arithmetic is expf (softmax and silu): the device restates glibc's expf
+method, checked bit for bit against the host libm here and over every float in test_oracle.
+"""
+import numpy as np
+import pytest
+from conftest import bits_equal, golden, rel_err
+
+from fastgguf_amd import synth as S
+
+pytestmark = pytest.mark.gpu
+
+
+def test_device_expf_matches_libm(backend, oracle):
+    """The device expf (softmax, silu) against this host's libm expf, bit for bit: the inputs where
+    only a fused evaluation rounds as glibc does, special values, and 4M float bit patterns across
+    the range where expf is neither 0 nor infinite."""
+    from test_oracle import EXPF_HARD, EXPF_SPECIAL
+    rng = np.random.default_rng(7)
+    lo = np.float32(-104.0).view(np.uint32)
+    bits_pos = rng.integers(0, np.float32(89.0).view(np.uint32), 2_000_000, dtype=np.uint32)
+    bits_neg = rng.integers(0x80000000, lo, 2_000_000, dtype=np.uint32)
+    xs = np.concatenate([np.array(EXPF_HARD + EXPF_SPECIAL, np.float32), bits_pos.view(np.float32),
+                         bits_neg.view(np.float32)])
+    got = backend.expf(xs)
+    want = oracle.libm_expf(xs)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def upload_experts(backend, w, cols, rows, n_exp):
+    return backend.upload(S.T_Q4_K, cols, w, rows=rows, n_mats=n_exp)
+
+
+def test_moe_matches_golden(backend):
+    g = golden("moe.npz")
+    E, K, D, F, T = (int(v) for v in g["dims"])
+    gate = upload_experts(backend, g["gate"], D, F, E)
+    up = upload_experts(backend, g["up"], D, F, E)
+    down = upload_experts(backend, g["down"], F, D, E)
+    Y, sel, w = backend.moe_ffn(gate, up, down, K, g["logits"], g["X"])
+    assert np.array_equal(sel, g["sel"])  # ties on token 2 (experts 3, 7) and token 3 (all equal)
+    assert bits_equal(w, g["w"])
+    assert bits_equal(Y, g["Y"])
+    for t in (gate, up, down):
+        t.free()
+
+
+@pytest.mark.parametrize("E,K,D,F,T", [(16, 4, 512, 256, 1), (16, 4, 512, 256, 5), (32, 8, 768, 512, 9)])
+def test_moe_matches_oracle(backend, oracle, E, K, D, F, T):
+    gw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 200 + E)
+    uw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 201 + E)
+    dw = S.random_bytes_weights(S.T_Q4_K, E * D, F, 202 + E)
+    X = S.activations(D, 203 + T, rows=T)
+    logits = S.router_logits(T, E, 204 + T)
+    Yo, so, wo = oracle.moe_ffn((S.T_Q4_K,) * 3, gw, uw, dw, E, K, D, F, logits, X)
+    gate, up, down = (upload_experts(backend, a, c, r, E) for a, c, r in ((gw, D, F), (uw, D, F), (dw, F, D)))
+    Y, sel, w = backend.moe_ffn(gate, up, down, K, logits, X)
+    assert np.array_equal(sel, so)
+    assert bits_equal(w, wo)
+    for t in range(T):
+        assert rel_err(Y[t], Yo[t]) <= 1e-5
+    assert bits_equal(Y, Yo)
+    for t in (gate, up, down):
+        t.free()
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_moe_config5(backend, oracle, T):
+    """Qwen3-30B-A3B-shaped layer, 128 experts, top-8, hidden 2048, ff 768."""
+    E, K, D, F = 128, 8, 2048, 768
+    gw = S.q4_k_weights(E * F, D, seed=300)
+    uw = S.q4_k_weights(E * F, D, seed=301)
+    dw = S.q4_k_weights(E * D, F, seed=302)
+    X = S.activations(D, 303, rows=T)
+    logits = S.router_logits(T, E, 304)
+    Yo, so, wo = oracle.moe_ffn((S.T_Q4_K,) * 3, gw, uw, dw, E, K, D, F, logits, X)
+    gate, up, down = (upload_experts(backend, a, c, r, E) for a, c, r in ((gw, D, F), (uw, D, F), (dw, F, D)))
+    Y, sel, w = backend.moe_ffn(gate, up, down, K, logits, X)
+    assert np.array_equal(sel, so)
+    assert bits_equal(w, wo)
+    for t in range(T):
+        assert rel_err(Y[t], Yo[t]) <= 1e-5
+    assert bits_equal(Y, Yo)
+    # repeated call (scratch reuse) gives the same bits
+    Y2, _, _ = backend.moe_ffn(gate, up, down, K, logits, X)
+    assert bits_equal(Y2, Y)
+    for t in (gate, up, down):
+        t.free()

@@ -66,6 +66,26 @@ def test_moe_matches_golden(oracle):
     assert list(g["sel"][3]) == [0, 1, 2]       # all-equal logits
 
 
+# expf inputs where a separately rounded r = x N / ln 2 - k gives another float than glibc's
+# fused evaluation (found by sweeping every float); and special values
+EXPF_HARD = [float.fromhex("0x1.04845ep+5"), float.fromhex("-0x1.f8cbb2p+5")]
+EXPF_SPECIAL = [0.0, -0.0, 1.0, -1.0, 88.72283, 88.72284, 100.0, -87.33654, -103.97207, -103.97208, -150.0,
+                float("inf"), float("-inf"), 1e-30, -1e-30]
+
+
+def test_expf_restatement_matches_libm(oracle):
+    """The MoE's expf, restated from its published method and run by the GPU: equal to this host's
+    libm expf on every 31st float bit pattern (the full sweep of all 2^32 also passes), on the two
+    inputs that only the fused evaluation rounds right, and on special values."""
+    bad, n, max_ulp = oracle.expf_compare(float("-inf"), float("inf"), 31)
+    assert n > 130_000_000
+    assert bad == 0, f"{bad} of {n} differ (max {max_ulp} ulp)"
+    xs = np.array(EXPF_HARD + EXPF_SPECIAL, np.float32)
+    want = oracle.libm_expf(xs)
+    got = np.array([oracle.expf(float(x)) for x in xs], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_oracle_matches_compiled_reference_random(oracle, reference):
     """Fresh random shapes and seeds against the reference's kernels (where oracle/_ref is built)."""
     rng = np.random.Generator(np.random.PCG64(7))
