@@ -247,9 +247,14 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     NO_CAPTURE(c);
     *out = nullptr;
     if (!host || rows <= 0 || n_mats <= 0 || cols <= 0) return fail(c, FGH_ERR_ARG, "upload: bad shape");
+    // the order the tensor will use: the reference repacks 2-D Q4_K matrices with rows % 8 == 0
+    // (repack_tensor, 2486-2488)
+    const int ord = type == FGH_T_Q4_K && (order == FGH_ORDER_REPACKED ||
+                                           (order == FGH_ORDER_AUTO && n_mats == 1 && rows % 8 == 0))
+                        ? FGH_ORDER_REPACKED
+                        : FGH_ORDER_ROW;
     if (!type_supported(type) || cols % block_elems(type) != 0 ||
-        fgh::matvec_lds_bytes((int)type, 0, (int)std::min<int64_t>(cols / block_elems(type), 1 << 20)) > 65536 ||
-        fgh::matvec_lds_bytes((int)type, 1, (int)std::min<int64_t>(cols / block_elems(type), 1 << 20)) > 65536) {
+        fgh::matvec_lds_bytes((int)type, ord, (int)std::min<int64_t>(cols / block_elems(type), 1 << 20)) > 65536) {
         c->n_skip_type++;
         return fail(c, FGH_SKIP_TYPE, "upload: type %u with %lld cols is not supported", type, (long long)cols);
     }
@@ -268,13 +273,7 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     t->ntile = type == FGH_T_Q8_0 ? (t->nb + 3) / 4 : t->nb;
     t->gpm = (rows + 7) / 8;
     t->groups = t->gpm * n_mats;
-    if (type == FGH_T_Q4_K) {
-        // the reference repacks 2-D Q4_K matrices with rows % 8 == 0 (repack_tensor, 2486-2488)
-        t->order = order == FGH_ORDER_AUTO ? ((n_mats == 1 && rows % 8 == 0) ? FGH_ORDER_REPACKED : FGH_ORDER_ROW)
-                                           : (order == FGH_ORDER_REPACKED ? FGH_ORDER_REPACKED : FGH_ORDER_ROW);
-    } else {
-        t->order = FGH_ORDER_ROW;
-    }
+    t->order = ord;
     t->dev_bytes = (uint64_t)t->groups * t->ntile * tile_bytes(type);
     if (c->used + t->dev_bytes > c->budget) {
         delete t;
@@ -363,7 +362,8 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
     HIP_TRY(c, hipSetDevice(c->device));
     // nb >= 8: the prompt GEMM (matmul 3018-3031) on int8 MFMA for Q4_K; Q6_K and Q8_0 run the
     // per-token decode kernels (their fp32 orders differ from gemm_kquant's only by rounding)
-    if (nb >= 8 && t->type == FGH_T_Q4_K) return gemm_q4k(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
+    if (nb >= 8 && t->type == FGH_T_Q4_K && fgh::q4k_gemm_lds_bytes(t->nb, nb > 32 ? 64 : 32) <= 65536)
+        return gemm_q4k(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
     float *ys[1] = {Y};
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
 }
@@ -655,7 +655,8 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     NO_CAPTURE(c);
     if (!X || !sumi || !msum || nb < 1 || nb > FG_BATCH || ldx < t->cols)
         return fail(c, FGH_ERR_ARG, "gemm_block_ints: bad arguments");
-    if (t->type != FGH_T_Q4_K) return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMM is for Q4_K tensors");
+    if (t->type != FGH_T_Q4_K || fgh::q4k_gemm_lds_bytes(t->nb, nb > 32 ? 64 : 32) > 65536)
+        return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMM runs Q4_K tensors with K <= 28672");
     const int64_t nout = t->rows * t->n_mats;
     const size_t nint = (size_t)nb * nout * t->nb;
     HIP_TRY(c, hipSetDevice(c->device));

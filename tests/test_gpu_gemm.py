@@ -97,3 +97,17 @@ def test_prefill_config_shape(backend, oracle):
     Y2 = backend.matmul(tt, X[:9])
     check_tokens(Y2, oracle.matmul(S.T_Q4_K, w, cols, X[:9], O_RP))
     tt.free()
+
+
+def test_matmul_wide_q4k_runs_decode_kernels(backend, oracle):
+    """K beyond the GEMM's LDS (116 blocks): the per-token decode kernels run instead, bit-exact with
+    the repacked single-row order."""
+    rows, cols, T = 16, 256 * 116, 9
+    w = S.random_bytes_weights(S.T_Q4_K, rows, cols, 95)
+    X = S.activations(cols, 96, rows=T)
+    tt = backend.upload(S.T_Q4_K, cols, w)
+    Y = backend.matmul(tt, X)
+    for t in range(T):
+        ref = oracle.matvec(S.T_Q4_K, w, cols, X[t], O_RP)
+        assert np.array_equal(Y[t].view(np.uint32), ref.view(np.uint32))
+    tt.free()
