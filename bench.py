@@ -47,6 +47,20 @@ def algo_bytes(rows: int, cols: int) -> int:
     return rows * (cols // 256) * 144 + 4 * cols + 4 * rows
 
 
+def counted_traffic(kernel: str):
+    """HBM bytes per launch measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
+    profiles/ (scaled by a plain copy kernel of known size), or None if not recorded."""
+    path = os.path.join(ROOT, "profiles", "q4k_gate_decode_prefill_gemm_hbm_counters.md")
+    try:
+        for line in open(path):
+            f = line.split()
+            if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == kernel:
+                return int(f[2])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(layer_w: dict, xs: dict, budget_s: float) -> dict | None:
     """The reference's CPU path on the same layer (oracle/_ref), median over a bounded sample."""
     try:
@@ -99,6 +113,9 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=5, help="distinct device copies of the layer")
     ap.add_argument("--kernel-reps", type=int, default=200, help="individually timed gate matvecs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget (0 = skip)")
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="only run 20 gate matvecs, 20 copies of the same byte count by a plain copy kernel, "
+                         "and 20 prefill GEMMs, eagerly (for rocprofv3 --pmc counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build has no multi-GPU "
@@ -122,6 +139,25 @@ def main() -> int:
     for k, v in xs.items():
         be.h2d(xd[k], v)
     yd = {n: be.dev_alloc(4 * r) for n, r, c in LAYER}
+
+    if args.profile_kernels:
+        gate_bytes = algo_bytes(14336, 4096)
+        cbytes = (gate_bytes + 15) // 16 * 16
+        src, dst = be.dev_alloc(cbytes), be.dev_alloc(cbytes)
+        Xp = S.activations(4096, 5, rows=64)
+        xpd, ypd = be.dev_alloc(Xp.nbytes), be.dev_alloc(4 * 64 * 14336)
+        be.h2d(xpd, Xp)
+        for i in range(20):
+            be.matvec_dev(tensors[i % args.copies]["gate"], xd["x2"], yd["gate"])
+        for i in range(20):
+            be.d2d(dst, src, cbytes)
+        for i in range(20):
+            be.matmul_dev(tensors[i % args.copies]["up"], xpd, ypd, 64)
+        be.sync()
+        print(json.dumps({"profile_kernels": True, "gate_bytes": gate_bytes, "copy_bytes": cbytes,
+                          "gemm_ops": 2 * 64 * 4096 * 14336}), flush=True)
+        be.close()
+        return 0
 
     def record_layer(t):
         be.matvec_dev(t["qkv"], xd["x"], yd["qkv"])
@@ -197,7 +233,8 @@ def main() -> int:
         kernels[n] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
     g = kernels["gate"]
     roofline = {"bound": "hbm", "achieved": g["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g["frac"],
-                "traffic": None, "kernel": "q4k_mv_kernel<repacked> (Q4_K decode matvec, gate 4096->14336)",
+                "traffic": counted_traffic("gate"),
+                "kernel": "q4k_mv_kernel<repacked> (Q4_K decode matvec, gate 4096->14336)",
                 "bytes_per_launch": algo_bytes(14336, 4096), "us_per_launch": g["us"]}
 
     # prefill: 64 tokens x 4096 -> 14336 Q4_K on the int8 MFMA GEMM; one launch
@@ -217,7 +254,8 @@ def main() -> int:
         prefill[kind] = {"us": round(us, 3), "TOPS": round(tops, 2), "frac": round(tops / INT8_PEAK_TOPS, 4)}
     prefill.update({"workload": "cfg4: 64 tokens x K=4096 -> N=14336, Q4_K x Q8_K (quantization of X included)",
                     "ops_per_launch": ops, "peak_TOPS": INT8_PEAK_TOPS,
-                    "kernel": "q4k_gemm_kernel (int8 MFMA 32x32x32, split sub-block scales)"})
+                    "kernel": "q4k_gemm_kernel (int8 MFMA 32x32x32, split sub-block scales)",
+                    "traffic": counted_traffic("prefill_gemm")})
     be.dev_free(xpd)
     be.dev_free(ypd)
 

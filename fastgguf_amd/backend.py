@@ -28,7 +28,7 @@ EXPORTS = (
     "fgh_matvec", "fgh_matvec_multi", "fgh_matmul", "fgh_moe_ffn",
     "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matmul_dev", "fgh_moe_ffn_dev",
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
-    "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_sync",
+    "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
     "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_expf", "fgh_fp16_to_f32",
 )
@@ -81,6 +81,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_dev_free": (i32, [vp, vp]),
         "fgh_copy_h2d": (i32, [vp, vp, vp, u64]),
         "fgh_copy_d2h": (i32, [vp, vp, vp, u64]),
+        "fgh_copy_d2d": (i32, [vp, vp, vp, u64]),
         "fgh_sync": (i32, [vp]),
         "fgh_event_create": (i32, [vp, C.POINTER(vp)]),
         "fgh_event_record": (i32, [vp, vp]),
@@ -262,6 +263,9 @@ class Backend:
 
     def d2h(self, a: np.ndarray, src: int):
         self._check(self.lib.fgh_copy_d2h(self.ctx, _p(a), src, a.nbytes))
+
+    def d2d(self, dst: int, src: int, nbytes: int):
+        self._check(self.lib.fgh_copy_d2d(self.ctx, dst, src, nbytes))
 
     def sync(self):
         self._check(self.lib.fgh_sync(self.ctx))

@@ -510,6 +510,13 @@ int fgh_copy_d2h(fgh_ctx *c, void *dst, const void *src, uint64_t bytes) {
     HIP_TRY(c, hipStreamSynchronize(c->stream));
     return FGH_OK;
 }
+int fgh_copy_d2d(fgh_ctx *c, void *dst, const void *src, uint64_t bytes) {
+    if (!c) return FGH_ERR_ARG;
+    if (!dst || !src || bytes % 16 != 0) return fail(c, FGH_ERR_ARG, "copy_d2d: null pointer or bytes % 16 != 0");
+    HIP_TRY(c, hipSetDevice(c->device));
+    if (bytes) HIP_TRY(c, fgh::launch_copy16(src, dst, (int64_t)(bytes / 16), c->stream));
+    return FGH_OK;
+}
 int fgh_sync(fgh_ctx *c) {
     if (!c) return FGH_ERR_ARG;
     NO_CAPTURE(c);

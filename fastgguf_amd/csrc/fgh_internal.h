@@ -134,6 +134,7 @@ hipError_t launch_quant_q8(const float *x, int64_t ldx, int nb, int ntok, ActQ8 
 hipError_t launch_relayout(const uint8_t *src, uint8_t *dst, int type, int64_t rows, int nb, int ntile,
                            int64_t gpm, int64_t total, int64_t row_bytes, hipStream_t s);
 hipError_t launch_fp16(const uint16_t *h, float *out, int n, hipStream_t s);
+hipError_t launch_copy16(const void *src, void *dst, int64_t n16, hipStream_t s);
 
 // decode matvec (fgh_matvec.hip): up to 4 tensors of one type, order and width in one launch
 struct MvT {

@@ -167,6 +167,17 @@ hipError_t launch_relayout(const uint8_t *src, uint8_t *dst, int type, int64_t r
     return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void copy16_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+hipError_t launch_copy16(const void *src, void *dst, int64_t n16, hipStream_t s) {
+    const int64_t want = (n16 + 255) / 256;
+    copy16_kernel<<<(unsigned)(want < 8192 ? want : 8192), 256, 0, s>>>((const uint4 *)src, (uint4 *)dst, n16);
+    return hipGetLastError();
+}
+
 hipError_t launch_fp16(const uint16_t *h, float *out, int n, hipStream_t s) {
     fp16_kernel<<<(n + 255) / 256, 256, 0, s>>>(h, out, n);
     return hipGetLastError();

@@ -150,6 +150,9 @@ FGH_API int fgh_dev_alloc(fgh_ctx *ctx, uint64_t bytes, void **ptr);
 FGH_API int fgh_dev_free(fgh_ctx *ctx, void *ptr);
 FGH_API int fgh_copy_h2d(fgh_ctx *ctx, void *dst_dev, const void *src_host, uint64_t bytes);
 FGH_API int fgh_copy_d2h(fgh_ctx *ctx, void *dst_host, const void *src_dev, uint64_t bytes);
+/* device-to-device copy by a plain streaming kernel (16-byte loads and stores), asynchronous on
+ * the context stream; bytes % 16 == 0. Also the known-size kernel that calibrates HBM counters. */
+FGH_API int fgh_copy_d2d(fgh_ctx *ctx, void *dst_dev, const void *src_dev, uint64_t bytes);
 FGH_API int fgh_sync(fgh_ctx *ctx);
 /* HIP events recorded on the context stream */
 FGH_API int fgh_event_create(fgh_ctx *ctx, void **ev);

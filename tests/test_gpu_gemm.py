@@ -99,15 +99,17 @@ def test_prefill_config_shape(backend, oracle):
     tt.free()
 
 
-def test_matmul_wide_q4k_runs_decode_kernels(backend, oracle):
-    """K beyond the GEMM's LDS (116 blocks): the per-token decode kernels run instead, bit-exact with
-    the repacked single-row order."""
-    rows, cols, T = 16, 256 * 116, 9
+def test_matmul_wide_q4k(backend, oracle):
+    """K = 116 blocks: with 40 tokens (a 64-token tile) the GEMM's LDS does not fit and the per-token
+    decode kernels run, bit-exact with the repacked single-row order; with 9 tokens (a 32-token
+    tile) the GEMM runs, within tolerance of gemm_kquant."""
+    rows, cols = 16, 256 * 116
     w = S.random_bytes_weights(S.T_Q4_K, rows, cols, 95)
-    X = S.activations(cols, 96, rows=T)
     tt = backend.upload(S.T_Q4_K, cols, w)
+    X = S.activations(cols, 96, rows=40)
     Y = backend.matmul(tt, X)
-    for t in range(T):
+    for t in range(40):
         ref = oracle.matvec(S.T_Q4_K, w, cols, X[t], O_RP)
-        assert np.array_equal(Y[t].view(np.uint32), ref.view(np.uint32))
+        assert np.array_equal(Y[t].view(np.uint32), ref.view(np.uint32)), f"token {t}"
+    check_tokens(backend.matmul(tt, X[:9]), oracle.matmul(S.T_Q4_K, w, cols, X[:9], O_RP))
     tt.free()

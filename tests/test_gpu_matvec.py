@@ -198,3 +198,16 @@ def test_graph_replay_matches_eager(backend, oracle):
         backend.dev_free(p)
     for t in ts.values():
         t.free()
+
+
+def test_copy_d2d(backend):
+    """The plain copy kernel (device-to-device; also the HBM-counter calibration kernel)."""
+    a = np.arange(1 << 20, dtype=np.uint32)
+    src, dst = backend.dev_alloc(a.nbytes), backend.dev_alloc(a.nbytes)
+    backend.h2d(src, a)
+    backend.d2d(dst, src, a.nbytes)
+    b = np.empty_like(a)
+    backend.d2h(b, dst)
+    assert np.array_equal(a, b)
+    backend.dev_free(src)
+    backend.dev_free(dst)
