@@ -61,6 +61,72 @@ def counted_traffic(kernel: str):
     return None
 
 
+def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
+    """BASELINE configs 1 (Q8_0 4096^2 matvec), 3 (Q6_K LM head 128256 x 4096) and 5 (MoE, 128
+    experts, top-8, hidden 2048, ff 768: batch 1 and 64 tokens), each timed like the kernels above.
+    Weight sets rotate where one copy would stay in the Infinity Cache."""
+    if not enabled:
+        return None
+    import numpy as np
+    out = {}
+    # config 1: Q8_0 4096 x 4096, 32 copies (571 MB)
+    w = S.q8_0_weights(4096, 4096, seed=110)
+    ts = [be.upload(S.T_Q8_0, 4096, w) for _ in range(32)]
+    x, y = be.dev_alloc(4 * 4096), be.dev_alloc(4 * 4096)
+    be.h2d(x, S.activations(4096, 111))
+    us = kernel_time(lambda i: be.matvec_dev(ts[i % 32], x, y), 200)
+    nbytes = 4096 * 128 * 34 + 4 * 8192
+    out["cfg1_q8_0_matvec"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                               "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    for t in ts:
+        t.free()
+    be.dev_free(y)
+    # config 3: Q6_K LM head, one copy (431 MB: beyond the Infinity Cache by itself)
+    w = S.q6_k_weights(128256, 4096, seed=120)
+    t = be.upload(S.T_Q6_K, 4096, w)
+    del w
+    y = be.dev_alloc(4 * 128256)
+    us = kernel_time(lambda i: be.matvec_dev(t, x, y), 50)
+    nbytes = 128256 * 16 * 210 + 4 * (4096 + 128256)
+    out["cfg3_q6_k_lm_head"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                                "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    t.free()
+    be.dev_free(y)
+    be.dev_free(x)
+    # config 5: MoE FFN, 2 expert sets (531 MB)
+    E, K, D, F = 128, 8, 2048, 768
+    sets = []
+    for c in range(2):
+        g = be.upload(S.T_Q4_K, D, S.q4_k_weights(E * F, D, seed=300 + 3 * c), rows=F, n_mats=E)
+        u = be.upload(S.T_Q4_K, D, S.q4_k_weights(E * F, D, seed=301 + 3 * c), rows=F, n_mats=E)
+        d = be.upload(S.T_Q4_K, F, S.q4_k_weights(E * D, F, seed=302 + 3 * c), rows=D, n_mats=E)
+        sets.append((g, u, d))
+    expert_bytes = 2 * F * (D // 256) * 144 + D * (F // 256) * 144
+    for T in (1, 64):
+        X = S.activations(D, 310, rows=T)
+        L = S.router_logits(T, E, 311)
+        xd, ld, yd = be.dev_alloc(X.nbytes), be.dev_alloc(L.nbytes), be.dev_alloc(X.nbytes)
+        be.h2d(xd, X)
+        be.h2d(ld, L)
+        us = kernel_time(lambda i: be.moe_ffn_dev(*sets[i % 2], K, ld, xd, yd, T), 100)
+        # distinct experts the tokens select (the oracle's routing, same as the device's)
+        sel = set()
+        for r in range(T):
+            p = np.exp(L[r] - L[r].max())
+            sel.update(np.argsort(-p, kind="stable")[:K].tolist())
+        nbytes = len(sel) * expert_bytes + 4 * T * (2 * D + E)
+        ops = 2.0 * T * K * (2 * F * D + D * F)
+        out[f"cfg5_moe_{T}tok"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                                   "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+                                   "distinct_experts": len(sel), "TOPS": round(ops / us / 1e6, 3)}
+        for p_ in (xd, ld, yd):
+            be.dev_free(p_)
+    for st in sets:
+        for t in st:
+            t.free()
+    return out
+
+
 def cpu_baseline(layer_w: dict, xs: dict, budget_s: float) -> dict | None:
     """The reference's CPU path on the same layer (oracle/_ref), median over a bounded sample."""
     try:
@@ -113,6 +179,7 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=5, help="distinct device copies of the layer")
     ap.add_argument("--kernel-reps", type=int, default=200, help="individually timed gate matvecs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget (0 = skip)")
+    ap.add_argument("--configs", type=int, default=1, help="also time BASELINE configs 1, 3 and 5 (0 = skip)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run 20 gate matvecs, 20 copies of the same byte count by a plain copy kernel, "
                          "and 20 prefill GEMMs, eagerly (for rocprofv3 --pmc counter passes)")
@@ -259,6 +326,8 @@ def main() -> int:
     be.dev_free(xpd)
     be.dev_free(ypd)
 
+    others = other_configs(be, S, kernel_time, args.configs)
+
     cpu = cpu_baseline(layer_w, xs, args.cpu_seconds) if args.cpu_seconds > 0 else None
     info = be.info()
     be.close()
@@ -276,6 +345,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "kernels": kernels,
         "prefill": prefill,
+        "other_configs": others,
     }
     print(json.dumps(out), flush=True)
     return 0

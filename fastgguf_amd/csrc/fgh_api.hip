@@ -362,7 +362,7 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
     HIP_TRY(c, hipSetDevice(c->device));
     // nb >= 8: the prompt GEMM (matmul 3018-3031) on int8 MFMA for Q4_K; Q6_K and Q8_0 run the
     // per-token decode kernels (their fp32 orders differ from gemm_kquant's only by rounding)
-    if (nb >= 8 && t->type == FGH_T_Q4_K && fgh::q4k_gemm_lds_bytes(t->nb, nb > 32 ? 64 : 32) <= 65536)
+    if (nb >= 8 && t->type == FGH_T_Q4_K && fgh::q4k_gemm_lds_bytes(t->nb, nb > 32 ? 64 : 32) <= fgh::GEMM_LDS_MAX)
         return gemm_q4k(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
     float *ys[1] = {Y};
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
@@ -662,8 +662,8 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     NO_CAPTURE(c);
     if (!X || !sumi || !msum || nb < 1 || nb > FG_BATCH || ldx < t->cols)
         return fail(c, FGH_ERR_ARG, "gemm_block_ints: bad arguments");
-    if (t->type != FGH_T_Q4_K || fgh::q4k_gemm_lds_bytes(t->nb, nb > 32 ? 64 : 32) > 65536)
-        return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMM runs Q4_K tensors with K <= 28672");
+    if (t->type != FGH_T_Q4_K || fgh::q4k_gemm_lds_bytes(t->nb, nb > 32 ? 64 : 32) > fgh::GEMM_LDS_MAX)
+        return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMM's LDS does not fit this K");
     const int64_t nout = t->rows * t->n_mats;
     const size_t nint = (size_t)nb * nout * t->nb;
     HIP_TRY(c, hipSetDevice(c->device));

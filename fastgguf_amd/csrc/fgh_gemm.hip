@@ -41,8 +41,9 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 // ---------------------------------------------------------------------------------------------
 // Activation quantizer for the GEMM (quantize_q8k, fastgguf.c:773-793, bit-exact): one wavefront
 // per (token, 256-block); lane l holds values 4l..4l+3. Writes
-//   qs  [nb][8][Tp][32] int8: group g of block b of token t at ((8 b + g) Tp + t) * 32, so the 32
-//                    tokens of one MFMA fragment are 1 KB contiguous
+//   qs  [nb][Tp/32][8][32][32] int8: group g of block b of token t = 32 tt + n at
+//                    (((b Tp/32 + tt) 8 + g) 32 + n) 32, so one MFMA fragment (32 tokens x 32
+//                    values) is 1 KB contiguous and a block's 8 fragments of one token tile 8 KB
 //   ydT [nb][Tp]     fp32 block scales, token-minor (one float4 = 4 consecutive tokens)
 //   bsp [nb][Tp][16] int8: the 32-value sums bs_g = bsums[2g] + bsums[2g+1] as bl_g (bytes 0..7,
 //                    bs & 127) and bh_g (bytes 8..15, bs >> 7)
@@ -64,7 +65,8 @@ __global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict
     const float id = d > 0.0f ? 1.0f / d : 0.0f;
     const int q0 = q8_round(v.x * id), q1 = q8_round(v.y * id);
     const int q2 = q8_round(v.z * id), q3 = q8_round(v.w * id);
-    *(uint32_t *)(qs + (((size_t)b * 8 + (lane >> 3)) * Tp + tok) * 32 + 4 * (lane & 7)) = pack_q(q0, q1, q2, q3);
+    *(uint32_t *)(qs + ((((size_t)b * (Tp >> 5) + (tok >> 5)) * 8 + (lane >> 3)) * 32 + (tok & 31)) * 32 +
+                  4 * (lane & 7)) = pack_q(q0, q1, q2, q3);
     int s = q0 + q1 + q2 + q3;  // 32-value group g = lanes 8g..8g+7
     s += __shfl_xor(s, 1, 64);
     s += __shfl_xor(s, 2, 64);
@@ -136,16 +138,23 @@ __device__ __forceinline__ void wstage_load(WStage<NT> &w, int nb, int s, int ti
 }
 
 // LDS stage layout: quants [blk][j][h][row 0..63] x 16 B (a fragment = 512 B contiguous per h),
-// meta at 16 KB: [blk][row] x 16 B
+// meta at 16 KB: [blk][row] x 16 B. Row slots are XOR-swizzled with (j, blk) (quants) and blk
+// (meta): the eight threads of one 128-byte write phase hold eight (j, blk) of one row, and the
+// swizzle sends them to eight different bank quads; a fragment read stays a permutation of 32
+// consecutive slots.
+__device__ __forceinline__ int gq_slot(int blk, int j, int h, int row) {
+    return ((blk * 4 + j) * 2 + h) * 64 + (row ^ (j | (blk << 2)));
+}
+__device__ __forceinline__ int gm_slot(int blk, int row) { return 1024 + blk * 64 + (row ^ (blk << 2)); }
+
 template <int NT>
 __device__ __forceinline__ void wstage_store(const WStage<NT> &w, uint8_t *buf, int tid) {
 #pragma unroll
     for (int k = 0; k < WStage<NT>::NU; ++k) {
         const int u = tid + k * NT;
-        const int j = u & 3, blk = (u >> 2) & 1, h = (u >> 3) & 1, row = u >> 4;
-        *(uint4 *)(buf + ((blk * 4 + j) * 2 + h) * 1024 + row * 16) = w.q[k];
+        *(uint4 *)(buf + 16 * gq_slot((u >> 2) & 1, u & 3, (u >> 3) & 1, u >> 4)) = w.q[k];
     }
-    if (tid < 128) *(uint4 *)(buf + 16384 + ((tid & 1) * 64 + (tid >> 1)) * 16) = w.m;
+    if (tid < 128) *(uint4 *)(buf + 16 * gm_slot(tid & 1, tid >> 1)) = w.m;
 }
 
 // one lane's activation operands of one block: group g (16 values of token 32 tt + l % 32) and
@@ -156,8 +165,10 @@ struct ActOps {
 };
 
 __device__ __forceinline__ void act_load(ActOps &o, const GemmArgs &a, int b, int tok, int h) {
+    // the block's 8 fragments of this token tile are 8 KB contiguous: two bases, immediate offsets
+    const int8_t *p = a.qs + (((size_t)b * (a.Tp >> 5) + (tok >> 5)) * 8 * 32 + (tok & 31)) * 32 + 16 * h;
 #pragma unroll
-    for (int g = 0; g < 8; ++g) o.av[g] = *(const uint4 *)(a.qs + (((size_t)b * 8 + g) * a.Tp + tok) * 32 + 16 * h);
+    for (int g = 0; g < 8; ++g) o.av[g] = *(const uint4 *)(p + 1024 * g);
     o.am = *(const uint2 *)(a.bsp + ((size_t)b * a.Tp + tok) * 16 + 8 * h);
 }
 
@@ -176,13 +187,18 @@ template <bool DUMP>
 __device__ __forceinline__ void gemm_block(const ActOps &o, const uint8_t *stage, int blk, int rs, int n, int h,
                                            int tt, float (&acc)[16], const float *__restrict__ yds, int b, bool live,
                                            int64_t row, const GemmArgs &a) {
-    const uint4 meta = *(const uint4 *)(stage + 16384 + (blk * 64 + rs * 32 + n) * 16);
+    const int row32 = rs * 32 + n;
+    const uint4 meta = *(const uint4 *)(stage + 16 * gm_slot(blk, row32));
     uint4 pc[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pc[j] = *(const uint4 *)(stage + ((blk * 4 + j) * 2 + h) * 1024 + (rs * 32 + n) * 16);
+    for (int j = 0; j < 4; ++j) pc[j] = *(const uint4 *)(stage + 16 * gq_slot(blk, j, h, row32));
     const Q4KScales sc = q4k_scales(meta.y, meta.z, meta.w);
-    const float d = fp16_bits_to_f32(meta.x & 0xFFFF);
-    const float dmin = fp16_bits_to_f32(meta.x >> 16);
+    // a padding block contributes zero: its scales are zeroed once here
+    const float d = live ? fp16_bits_to_f32(meta.x & 0xFFFF) : 0.0f;
+    const float dmin = live ? fp16_bits_to_f32(meta.x >> 16) : 0.0f;
+    // the split scale factors of the 8 groups as bytes: sh = sc >> 3, sl = sc & 7
+    const uint32_t shb[2] = {(sc.sc_lo >> 3) & 0x07070707u, (sc.sc_hi >> 3) & 0x07070707u};
+    const uint32_t slb[2] = {sc.sc_lo & 0x07070707u, sc.sc_hi & 0x07070707u};
     // pass 0: q * sh over the block's 8 groups; pass 1 continues from 8 * Chi with q * sl
     v16i ai;
 #pragma unroll
@@ -193,8 +209,9 @@ __device__ __forceinline__ void gemm_block(const ActOps &o, const uint8_t *stage
 #pragma unroll
             for (int hn = 0; hn < 2; ++hn) {
                 const int g = 2 * j + hn;
-                const uint32_t s6 = (uint32_t)q4k_sc(sc, g);
-                const uint32_t f = (pass == 0 ? (s6 >> 3) : (s6 & 7)) * 0x00010001u;
+                // byte g of the factors into both 16-bit lanes (v_perm_b32; selector 0x0C = zero)
+                const uint32_t f = __builtin_amdgcn_perm(0u, pass == 0 ? shb[g >> 2] : slb[g >> 2],
+                                                         0x0C000C00u | (uint32_t)((g & 3) * 0x00010001));
                 v4i bw;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) bw[k] = (int)bmul(hn ? ((P[k] >> 4) & 0x0F0F0F0Fu) : (P[k] & 0x0F0F0F0Fu), f);
@@ -212,13 +229,7 @@ __device__ __forceinline__ void gemm_block(const ActOps &o, const uint8_t *stage
         }
     }
     // the row's eight mins as bytes; lanes 0-31 feed K slots 0..7 (bl), lanes 32-63 slots 8..15 (bh)
-    uint32_t m0 = 0, m1 = 0;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        m0 |= (uint32_t)q4k_mn(sc, g) << (8 * g);
-        m1 |= (uint32_t)q4k_mn(sc, g + 4) << (8 * g);
-    }
-    const long mp = (long)(((uint64_t)m1 << 32) | m0);
+    const long mp = (long)(((uint64_t)sc.mn_hi << 32) | sc.mn_lo);
     const long b1 = h == 0 ? mp : 0L, b2 = h == 0 ? 0L : mp;
     const v16i z = {};
     const long ab = (long)(((uint64_t)o.am.y << 32) | o.am.x);
@@ -233,8 +244,7 @@ __device__ __forceinline__ void gemm_block(const ActOps &o, const uint8_t *stage
     for (int v = 0; v < 16; ++v) {
         const int isum = ai[v], msum = ms[v];
         const float4 q4 = yd[v >> 2];
-        float ydv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
-        ydv = live ? ydv : 0.0f;
+        const float ydv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
         const float t = __builtin_fmaf(-dmin, (float)msum, d * (float)isum);
         acc[v] = __builtin_fmaf(ydv, t, acc[v]);
         if (DUMP) {
@@ -330,7 +340,7 @@ size_t q4k_gemm_lds_bytes(int nb, int Tp) { return (size_t)nb * Tp * 4 + 2 * (si
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > 64 || a.Tp != (a.T > 32 ? 64 : 32) || a.nb < 1 || a.nrows < 1) return hipErrorInvalidValue;
     const size_t lds = q4k_gemm_lds_bytes(a.nb, a.Tp);
-    if (lds > 65536) return hipErrorInvalidValue;
+    if (lds > GEMM_LDS_MAX) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.nrows + 63) / 64));
     if (a.Tp == 64) {
         if (a.dump_s) q4k_gemm_kernel<2, true><<<grid, 512, lds, s>>>(a);

@@ -160,7 +160,7 @@ struct MvArgs {
 size_t matvec_lds_bytes(int type, int order, int nb);  // Q6_K / Q8_0 (fgh_matvec.hip)
 // Q4_K (fgh_q4k.hip): its own group layout and kernel
 size_t q4k_lds_bytes(int order, int nb);
-hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, hipStream_t s);
+hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
 hipError_t launch_q4k_relayout(const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t gpm, int64_t total,
                                int64_t row_bytes, hipStream_t s);
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
@@ -227,7 +227,8 @@ struct GemmArgs {
 };
 hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, int8_t *qs, float *ydT, int8_t *bsp,
                              hipStream_t s);
-size_t q4k_gemm_lds_bytes(int nb, int Tp);  // <= 65536 for the GEMM to run
+constexpr size_t GEMM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
+size_t q4k_gemm_lds_bytes(int nb, int Tp);  // <= GEMM_LDS_MAX for the GEMM to run
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s);
 
 }  // namespace fgh

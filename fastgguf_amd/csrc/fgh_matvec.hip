@@ -501,7 +501,7 @@ static hipError_t launch_t(const MvArgs &a, int ntok, int num_cu, hipStream_t s)
 
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
     const bool dump = a.dump_s != nullptr;
-    if (type == T_Q4_K) return launch_q4k_matvec(order, a, ntok, s);
+    if (type == T_Q4_K) return launch_q4k_matvec(order, a, ntok, num_cu, s);
     if (type == T_Q6_K)
         return dump ? launch_t<T_Q6_K, 0, true>(a, ntok, num_cu, s) : launch_t<T_Q6_K, 0, false>(a, ntok, num_cu, s);
     if (type == T_Q8_0)

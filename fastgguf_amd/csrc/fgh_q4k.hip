@@ -108,6 +108,172 @@ struct Q4Step {
     uint4 p0, p1, m;
 };
 
+// what one wavefront needs to compute its steps: the quantized x and its record area (LDS)
+struct Q4Ctx {
+    const uint8_t *act;
+    const float *ad;
+    const int16_t *abs16;
+    float *rec;
+    int nb, P, j, pl;
+};
+
+// where the per-(row, block) integers of the test hook go: rows dbase + r2 if r2 < dleft
+struct Q4Dump {
+    int32_t *s, *m;
+    int64_t base;
+    int64_t left;
+};
+
+// One step (16 (row, block) pairs) of one wavefront from its registers: the exact integers of the
+// lane's chunk (v_dot4_i32_i8), reduced over the pair's 4 lanes, and the pair's fp32 record in LDS
+//   repacked: float4 {d*yd, sumi, dmin*yd, msum} at pair q
+//   row:      16 floats at pair q: the 8 lane partials (dword i = the reference's lane i), the 4
+//             min partials at 8 + j, d*yd at 12, dmin*yd at 13
+template <int ORDER, bool DUMP>
+__device__ __forceinline__ void q4_step(const Q4Step &st, int s, const Q4Ctx &c, const Q4Dump &dump) {
+    const int nb = c.nb, j = c.j, pl = c.pl;
+    const int np = min(16, c.P - 16 * s);
+    const bool live = pl < np;
+    const int q = 16 * s + min(pl, np - 1);
+    const int r2 = q >= nb, b = q - r2 * nb;
+    const uint8_t *yb = c.act + (size_t)b * 256 + 64 * j;
+    const uint4 ylo0 = *(const uint4 *)yb, ylo1 = *(const uint4 *)(yb + 16);
+    const uint4 yhi0 = *(const uint4 *)(yb + 32), yhi1 = *(const uint4 *)(yb + 48);
+    const uint32_t qd[8] = {st.p0.x, st.p0.y, st.p0.z, st.p0.w, st.p1.x, st.p1.y, st.p1.z, st.p1.w};
+    const uint32_t ylo[8] = {ylo0.x, ylo0.y, ylo0.z, ylo0.w, ylo1.x, ylo1.y, ylo1.z, ylo1.w};
+    const uint32_t yhi[8] = {yhi0.x, yhi0.y, yhi0.z, yhi0.w, yhi1.x, yhi1.y, yhi1.z, yhi1.w};
+    // scales and mins of sub-blocks 2j (low nibbles) and 2j+1 (high nibbles) of this chunk,
+    // straight from the packed words u0..u2 (scale_min_k4, fastgguf.c:466-472): for j < 2 the low
+    // 6 bits of bytes 2j, 2j+1 of u0 (scales) and u1 (mins); for j >= 2 the nibbles of bytes
+    // 2j-4, 2j-3 of u2 with the top 2 bits of the same bytes of u0 / u1
+    const int sh = 16 * (j & 1);
+    const uint32_t A = st.m.y >> sh, B = st.m.z >> sh, C = st.m.w >> sh;
+    const uint32_t scp = j < 2 ? (A & 0x3f3fu) : ((C & 0x0f0fu) | ((A & 0xc0c0u) >> 2));
+    const uint32_t mnp = j < 2 ? (B & 0x3f3fu) : (((C >> 4) & 0x0f0fu) | ((B & 0xc0c0u) >> 2));
+    // (s_lo, s_hi) as an int16 pair for the packed dots below; m_lo, m_hi as bytes
+    const uint32_t sc2 = __builtin_amdgcn_perm(0u, scp, 0x0C010C00u);
+    const int m_lo = (int)(mnp & 0x3F), m_hi = (int)((mnp >> 8) & 0x3F);
+    // min term m_2j (bs[4j] + bs[4j+1]) + m_2j+1 (bs[4j+2] + bs[4j+3]): two packed int16 dots on
+    // the activation sums as stored (all values fit int16)
+    const uint2 bq = *(const uint2 *)(c.abs16 + 16 * b + 4 * j);
+    const int mterm = dot2_i16((uint32_t)m_lo | ((uint32_t)m_lo << 16), bq.x,
+                               dot2_i16((uint32_t)m_hi | ((uint32_t)m_hi << 16), bq.y, 0));
+    const float yd = c.ad[b];
+    const float fd = fp16_bits_to_f32(st.m.x & 0xFFFF) * yd;
+    const float fdm = fp16_bits_to_f32(st.m.x >> 16) * yd;
+    if (ORDER == 1) {
+        // integer dots of the low / high nibbles in two halves of 16 values each: every partial is
+        // at most 16 * 15 * 127 = 30480 in magnitude, so fits int16, and the scale products are
+        // two packed int16 dots
+        int il0 = 0, il1 = 0, ih0 = 0, ih1 = 0;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            il0 = dot4((int)(qd[d] & 0x0F0F0F0Fu), (int)ylo[d], il0);
+            ih0 = dot4((int)((qd[d] >> 4) & 0x0F0F0F0Fu), (int)yhi[d], ih0);
+            il1 = dot4((int)(qd[d + 4] & 0x0F0F0F0Fu), (int)ylo[d + 4], il1);
+            ih1 = dot4((int)((qd[d + 4] >> 4) & 0x0F0F0F0Fu), (int)yhi[d + 4], ih1);
+        }
+        const int sumi = sum4_i32(dot2_i16(sc2, pack_i16(il0, ih0), dot2_i16(sc2, pack_i16(il1, ih1), 0)));
+        const int msum = sum4_i32(mterm);
+        if (live && j == 0) {
+            *(float4 *)(c.rec + 4 * q) = make_float4(fd, (float)sumi, fdm, (float)msum);
+            if (DUMP && r2 < dump.left) {
+                dump.s[(dump.base + r2) * nb + b] = sumi;
+                dump.m[(dump.base + r2) * nb + b] = msum;
+            }
+        }
+    } else {
+        // the reference's lane i sums bytes 4i..4i+3 of every chunk: dword i here
+        int lv[8];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            // each dot4 is at most 4 * 15 * 127 = 7620 in magnitude: an int16 pair
+            lv[d] = dot2_i16(sc2, pack_i16(dot4((int)(qd[d] & 0x0F0F0F0Fu), (int)ylo[d], 0),
+                                           dot4((int)((qd[d] >> 4) & 0x0F0F0F0Fu), (int)yhi[d], 0)), 0);
+            lv[d] = sum4_i32(lv[d]);
+        }
+        float *rq = c.rec + 16 * q;
+        if (live) {
+            rq[8 + j] = (float)mterm;  // min lane p = j
+            if (j == 0) {
+#pragma unroll
+                for (int d = 0; d < 8; ++d) rq[d] = (float)lv[d];
+                rq[12] = fd;
+                rq[13] = fdm;
+            }
+        }
+        if (DUMP) {
+            int ts = 0;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) ts += lv[d];
+            const int tm = sum4_i32(mterm);
+            if (live && j == 0 && r2 < dump.left) {
+                dump.s[(dump.base + r2) * nb + b] = ts;
+                dump.m[(dump.base + r2) * nb + b] = tm;
+            }
+        }
+    }
+}
+
+// The reference's fp32 chain over the wavefront's records, in ascending block order, and its
+// final combination; rows ybase[0], ybase[1] (if r2 < left). Call after a wave_sync.
+template <int ORDER>
+__device__ __forceinline__ void q4_chain(const Q4Ctx &c, int lane, float *__restrict__ ybase, int64_t left) {
+    const int nb = c.nb;
+    if (ORDER == 1) {
+        if (lane < 2) {
+            const float *rr = c.rec + 4 * (size_t)lane * nb;
+            float acc = 0.0f, macc = 0.0f;
+            int b = 0;
+            for (; b + 4 <= nb; b += 4) {
+                float4 p[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) p[u] = *(const float4 *)(rr + 4 * (b + u));
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    acc = __builtin_fmaf(p[u].x, p[u].y, acc);
+                    macc = __builtin_fmaf(p[u].z, p[u].w, macc);
+                }
+            }
+            for (; b < nb; ++b) {
+                const float4 p = *(const float4 *)(rr + 4 * b);
+                acc = __builtin_fmaf(p.x, p.y, acc);
+                macc = __builtin_fmaf(p.z, p.w, macc);
+            }
+            if (lane < left) ybase[lane] = acc - macc;
+        }
+    } else {
+        float *fin = c.rec + (size_t)2 * nb * 16;
+        if (lane < 16) {
+            const int r2 = lane >> 3, i = lane & 7;
+            const float *rr = c.rec + 16 * (size_t)r2 * nb;
+            float acc = 0.0f, macc = 0.0f;
+            for (int b = 0; b < nb; ++b) {
+                const float *p = rr + 16 * b;
+                acc = __builtin_fmaf(p[12], p[i], acc);
+                macc = __builtin_fmaf(p[13], p[8 + (i & 3)], macc);
+            }
+            fin[12 * r2 + i] = acc;
+            if (i < 4) fin[12 * r2 + 8 + i] = macc;
+        }
+        wave_sync();
+        if (lane < 2 && lane < left) {
+            const float *v = fin + 12 * lane;
+            const float h8 = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+            ybase[lane] = h8 - ((v[8] + v[9]) + (v[10] + v[11]));
+        }
+    }
+}
+
+// the tensor of global group g in a multi-tensor launch
+__device__ __forceinline__ int q4_tensor_of(const MvArgs &a, int64_t g) {
+    int ti = 0;
+#pragma unroll
+    for (int k = 1; k < 4; ++k)
+        if (k < a.nt && g >= a.t[k].gfirst) ti = k;
+    return ti;
+}
+
 template <int ORDER, int MAXS, int GPW, bool DUMP>
 __global__ __launch_bounds__(256 * GPW) void q4k_mv_kernel(MvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -131,10 +297,7 @@ __global__ __launch_bounds__(256 * GPW) void q4k_mv_kernel(MvArgs a) {
         __syncthreads();
         return;
     }
-    int ti = 0;
-#pragma unroll
-    for (int k = 1; k < 4; ++k)
-        if (k < a.nt && g >= a.t[k].gfirst) ti = k;
+    const int ti = q4_tensor_of(a, g);
     const int64_t lg = g - a.t[ti].gfirst;
     const int64_t mg = a.sel ? (int64_t)a.sel[tok] * a.t[ti].gpm : 0;  // selected matrix (MoE)
     const uint8_t *G = a.t[ti].W + (size_t)(mg + lg) * 1152 * nb;
@@ -142,8 +305,18 @@ __global__ __launch_bounds__(256 * GPW) void q4k_mv_kernel(MvArgs a) {
     const uint8_t *quant = G + (size_t)128 * nb + (size_t)256 * nb * wave;
 
     uint8_t *act = smem;
-    float *rec = (float *)(smem + q4_act_bytes(nb) + (size_t)(4 * gsub + wave) * q4_wave_bytes(ORDER, nb));
-    float *fin = rec + (size_t)2 * nb * (ORDER == 1 ? 4 : 16);
+    Q4Ctx c;
+    c.act = act;
+    c.ad = (const float *)(act + q4_off_d(nb));
+    c.abs16 = (const int16_t *)(act + q4_off_s(nb));
+    c.rec = (float *)(smem + q4_act_bytes(nb) + (size_t)(4 * gsub + wave) * q4_wave_bytes(ORDER, nb));
+    c.nb = nb;
+    c.P = P;
+    c.j = j;
+    c.pl = pl;
+    const int64_t lr0 = (lg % a.t[ti].gpm) * 8 + 2 * wave;
+    const int64_t obase = (lg / a.t[ti].gpm) * a.t[ti].rows;
+    Q4Dump dump{a.dump_s, a.dump_m, obase + lr0, a.t[ti].rows - lr0};
 
     // (1) x for the first quantization round, then (2) every weight load of the first chunk
     const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
@@ -172,157 +345,118 @@ __global__ __launch_bounds__(256 * GPW) void q4k_mv_kernel(MvArgs a) {
     }
     __syncthreads();
 
-    const float *ad = (const float *)(act + q4_off_d(nb));
-    const int16_t *abs16 = (const int16_t *)(act + q4_off_s(nb));
-
     for (int s0 = 0; s0 < nsteps; s0 += MAXS) {
         if (s0 > 0) load_steps(s0);
 #pragma unroll
         for (int k = 0; k < MAXS; ++k) {
             const int s = s0 + k;
             if (s >= nsteps) break;  // uniform
-            const int np = min(16, P - 16 * s);
-            const bool live = pl < np;
-            const int q = 16 * s + min(pl, np - 1);
-            const int r2 = q >= nb, b = q - r2 * nb;
-            const uint8_t *yb = act + (size_t)b * 256 + 64 * j;
-            const uint4 ylo0 = *(const uint4 *)yb, ylo1 = *(const uint4 *)(yb + 16);
-            const uint4 yhi0 = *(const uint4 *)(yb + 32), yhi1 = *(const uint4 *)(yb + 48);
-            const uint32_t qd[8] = {st[k].p0.x, st[k].p0.y, st[k].p0.z, st[k].p0.w,
-                                    st[k].p1.x, st[k].p1.y, st[k].p1.z, st[k].p1.w};
-            const uint32_t ylo[8] = {ylo0.x, ylo0.y, ylo0.z, ylo0.w, ylo1.x, ylo1.y, ylo1.z, ylo1.w};
-            const uint32_t yhi[8] = {yhi0.x, yhi0.y, yhi0.z, yhi0.w, yhi1.x, yhi1.y, yhi1.z, yhi1.w};
-            // scales and mins of sub-blocks 2j (low nibbles) and 2j+1 (high nibbles) of this chunk,
-            // straight from the packed words u0..u2 (scale_min_k4, fastgguf.c:466-472): for j < 2
-            // the low 6 bits of bytes 2j, 2j+1 of u0 (scales) and u1 (mins); for j >= 2 the nibbles
-            // of bytes 2j-4, 2j-3 of u2 with the top 2 bits of the same bytes of u0 / u1
-            const int sh = 16 * (j & 1);
-            const uint32_t A = st[k].m.y >> sh, B = st[k].m.z >> sh, C = st[k].m.w >> sh;
-            const uint32_t scp = j < 2 ? (A & 0x3f3fu) : ((C & 0x0f0fu) | ((A & 0xc0c0u) >> 2));
-            const uint32_t mnp = j < 2 ? (B & 0x3f3fu) : (((C >> 4) & 0x0f0fu) | ((B & 0xc0c0u) >> 2));
-            // (s_lo, s_hi) as an int16 pair for the packed dots below; m_lo, m_hi as bytes
-            const uint32_t sc2 = __builtin_amdgcn_perm(0u, scp, 0x0C010C00u);
-            const int m_lo = (int)(mnp & 0x3F), m_hi = (int)((mnp >> 8) & 0x3F);
-            // min term m_2j (bs[4j] + bs[4j+1]) + m_2j+1 (bs[4j+2] + bs[4j+3]): two packed int16 dots
-            // on the activation sums as stored (all values fit int16)
-            const uint2 bq = *(const uint2 *)(abs16 + 16 * b + 4 * j);
-            const int mterm = dot2_i16((uint32_t)m_lo | ((uint32_t)m_lo << 16), bq.x,
-                                       dot2_i16((uint32_t)m_hi | ((uint32_t)m_hi << 16), bq.y, 0));
-            const float yd = ad[b];
-            const float fd = fp16_bits_to_f32(st[k].m.x & 0xFFFF) * yd;
-            const float fdm = fp16_bits_to_f32(st[k].m.x >> 16) * yd;
-            if (ORDER == 1) {
-                // integer dots of the low / high nibbles in two halves of 16 values each: every
-                // partial is at most 16 * 15 * 127 = 30480 in magnitude, so fits int16, and the
-                // scale products are two packed int16 dots
-                int il0 = 0, il1 = 0, ih0 = 0, ih1 = 0;
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    il0 = dot4((int)(qd[d] & 0x0F0F0F0Fu), (int)ylo[d], il0);
-                    ih0 = dot4((int)((qd[d] >> 4) & 0x0F0F0F0Fu), (int)yhi[d], ih0);
-                    il1 = dot4((int)(qd[d + 4] & 0x0F0F0F0Fu), (int)ylo[d + 4], il1);
-                    ih1 = dot4((int)((qd[d + 4] >> 4) & 0x0F0F0F0Fu), (int)yhi[d + 4], ih1);
-                }
-                const int sumi = sum4_i32(dot2_i16(sc2, pack_i16(il0, ih0), dot2_i16(sc2, pack_i16(il1, ih1), 0)));
-                const int msum = sum4_i32(mterm);
-                if (live && j == 0) {
-                    *(float4 *)(rec + 4 * q) = make_float4(fd, (float)sumi, fdm, (float)msum);
-                    if (DUMP) {
-                        const int64_t lr = (lg % a.t[ti].gpm) * 8 + 2 * wave + r2;
-                        if (lr < a.t[ti].rows) {
-                            const int64_t orow = (lg / a.t[ti].gpm) * a.t[ti].rows + lr;
-                            a.dump_s[orow * nb + b] = sumi;
-                            a.dump_m[orow * nb + b] = msum;
-                        }
-                    }
-                }
-            } else {
-                // the reference's lane i sums bytes 4i..4i+3 of every chunk: dword i here
-                int lv[8];
-#pragma unroll
-                for (int d = 0; d < 8; ++d) {
-                    // each dot4 is at most 4 * 15 * 127 = 7620 in magnitude: an int16 pair
-                    lv[d] = dot2_i16(sc2, pack_i16(dot4((int)(qd[d] & 0x0F0F0F0Fu), (int)ylo[d], 0),
-                                                   dot4((int)((qd[d] >> 4) & 0x0F0F0F0Fu), (int)yhi[d], 0)), 0);
-                    lv[d] = sum4_i32(lv[d]);
-                }
-                float *rq = rec + 16 * q;
-                if (live) {
-                    rq[8 + j] = (float)mterm;  // min lane p = j
-                    if (j == 0) {
-#pragma unroll
-                        for (int d = 0; d < 8; ++d) rq[d] = (float)lv[d];
-                        rq[12] = fd;
-                        rq[13] = fdm;
-                    }
-                }
-                if (DUMP) {
-                    int ts = 0;
-#pragma unroll
-                    for (int d = 0; d < 8; ++d) ts += lv[d];
-                    const int tm = sum4_i32(mterm);
-                    if (live && j == 0) {
-                        const int64_t lr = (lg % a.t[ti].gpm) * 8 + 2 * wave + r2;
-                        if (lr < a.t[ti].rows) {
-                            const int64_t orow = (lg / a.t[ti].gpm) * a.t[ti].rows + lr;
-                            a.dump_s[orow * nb + b] = ts;
-                            a.dump_m[orow * nb + b] = tm;
-                        }
-                    }
-                }
-            }
+            q4_step<ORDER, DUMP>(st[k], s, c, dump);
         }
     }
     wave_sync();
+    q4_chain<ORDER>(c, lane, a.t[ti].y + (size_t)tok * a.ldy + obase + lr0, a.t[ti].rows - lr0);
+}
 
-    // chain in ascending block order, then the reference's final combination
-    const int64_t lr0 = (lg % a.t[ti].gpm) * 8 + 2 * wave;
-    const int64_t obase = (lg / a.t[ti].gpm) * a.t[ti].rows;
-    float *y = a.t[ti].y + (size_t)tok * a.ldy;
-    if (ORDER == 1) {
-        if (lane < 2) {
-            const float *rr = rec + 4 * (size_t)lane * nb;
-            float acc = 0.0f, macc = 0.0f;
-            int b = 0;
-            for (; b + 4 <= nb; b += 4) {
-                float4 p[4];
+// Persistent, software-pipelined variant: workgroup blockIdx.x walks the groups
+// [G * x / gridDim.x, G * (x + 1) / gridDim.x) with 4 wavefronts (rows 2w, 2w + 1 of each group).
+// A wavefront's steps form one sequence over its groups; D steps are in flight in a ring of
+// registers, each reloaded with the step D later right after it is computed (the scheduling
+// barrier keeps the loads in issue order, so waiting for one step never waits for a later one).
+// x is quantized once per workgroup while the first D steps load.
+template <int ORDER, int D, bool DUMP>
+__global__ __launch_bounds__(256) void q4k_pipe_kernel(MvArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 3, pl = lane >> 2;
+    const int nb = a.nb, P = 2 * nb;
+    const int NS = (P + 15) >> 4;
+    const int tok = blockIdx.y;
+    const int64_t g0 = a.groups * blockIdx.x / gridDim.x, g1 = a.groups * (blockIdx.x + 1) / gridDim.x;
+    if (g0 >= g1) return;  // whole workgroup
+    const int64_t S = (g1 - g0) * NS;
+    const int64_t mgsel = a.sel ? (int64_t)a.sel[tok] : 0;  // selected matrix (MoE)
+
+    Q4Ctx c;
+    c.act = smem;
+    c.ad = (const float *)(smem + q4_off_d(nb));
+    c.abs16 = (const int16_t *)(smem + q4_off_s(nb));
+    c.rec = (float *)(smem + q4_act_bytes(nb) + (size_t)wave * q4_wave_bytes(ORDER, nb));
+    c.nb = nb;
+    c.P = P;
+    c.j = j;
+    c.pl = pl;
+
+    // loads of step s of the sequence (clamped to the last one)
+    int64_t lg_g = g0;  // group of the next load
+    int lg_s = 0;       // its step
+    auto load_next = [&](Q4Step &st) {
+        const int ti = q4_tensor_of(a, lg_g);
+        const uint8_t *G = a.t[ti].W + (size_t)(mgsel * a.t[ti].gpm + lg_g - a.t[ti].gfirst) * 1152 * nb;
+        const int np = min(16, P - 16 * lg_s);
+        const int pc = min(pl, np - 1);
+        const uint8_t *qb = G + (size_t)128 * nb + (size_t)256 * nb * wave + (size_t)2048 * lg_s + 16 * (4 * pc + j);
+        st.p0 = ld16(qb);
+        st.p1 = ld16(qb + 64 * np);
+        st.m = ld16(G + (size_t)16 * P * wave + 16 * (16 * lg_s + pc));
+        if (lg_s + 1 < NS) {
+            ++lg_s;
+        } else if (lg_g + 1 < g1) {
+            lg_s = 0;
+            ++lg_g;
+        }  // else: stay on the last step (re-reads)
+    };
+
+    const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
+    XRound xr;
+    q8k_load(x, nb, 0, xr);
+    Q4Step ring[D];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) p[u] = *(const float4 *)(rr + 4 * (b + u));
+    for (int k = 0; k < D; ++k) load_next(ring[k]);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int rb = 0; rb < nb; rb += 16) {
+        if (rb > 0) q8k_load(x, nb, rb, xr);
+        q8k_store(nb, rb, xr, smem);
+    }
+    __syncthreads();
+
+    int64_t cg = g0;  // group being computed
+    int cs = 0;       // its step
+    for (int64_t s0 = 0; s0 < S; s0 += D) {
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    acc = __builtin_fmaf(p[u].x, p[u].y, acc);
-                    macc = __builtin_fmaf(p[u].z, p[u].w, macc);
+        for (int k = 0; k < D; ++k) {
+            if (s0 + k < S) {  // uniform
+                if (DUMP || cs == NS - 1) {
+                    const int ti = q4_tensor_of(a, cg);
+                    const int64_t lg = cg - a.t[ti].gfirst;
+                    const int64_t lr0 = (lg % a.t[ti].gpm) * 8 + 2 * wave;
+                    const int64_t obase = (lg / a.t[ti].gpm) * a.t[ti].rows;
+                    Q4Dump dump{a.dump_s, a.dump_m, obase + lr0, a.t[ti].rows - lr0};
+                    q4_step<ORDER, DUMP>(ring[k], cs, c, dump);
+                    if (cs == NS - 1) {
+                        wave_sync();
+                        q4_chain<ORDER>(c, lane, a.t[ti].y + (size_t)tok * a.ldy + obase + lr0, a.t[ti].rows - lr0);
+                        wave_sync();  // the next group's records reuse the area
+                    }
+                } else {
+                    Q4Dump none{nullptr, nullptr, 0, 0};
+                    q4_step<ORDER, false>(ring[k], cs, c, none);
+                }
+                if (++cs == NS) {
+                    cs = 0;
+                    ++cg;
                 }
             }
-            for (; b < nb; ++b) {
-                const float4 p = *(const float4 *)(rr + 4 * b);
-                acc = __builtin_fmaf(p.x, p.y, acc);
-                macc = __builtin_fmaf(p.z, p.w, macc);
-            }
-            if (lr0 + lane < a.t[ti].rows) y[obase + lr0 + lane] = acc - macc;
-        }
-    } else {
-        if (lane < 16) {
-            const int r2 = lane >> 3, i = lane & 7;
-            const float *rr = rec + 16 * (size_t)r2 * nb;
-            float acc = 0.0f, macc = 0.0f;
-            for (int b = 0; b < nb; ++b) {
-                const float *p = rr + 16 * b;
-                acc = __builtin_fmaf(p[12], p[i], acc);
-                macc = __builtin_fmaf(p[13], p[8 + (i & 3)], macc);
-            }
-            fin[12 * r2 + i] = acc;
-            if (i < 4) fin[12 * r2 + 8 + i] = macc;
-        }
-        wave_sync();
-        if (lane < 2 && lr0 + lane < a.t[ti].rows) {
-            const float *v = fin + 12 * lane;
-            const float h8 = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
-            y[obase + lr0 + lane] = h8 - ((v[8] + v[9]) + (v[10] + v[11]));
+            load_next(ring[k]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
 
+#ifndef FGH_Q4_KERNEL
+#define FGH_Q4_KERNEL 0
+#endif
 #ifndef FGH_Q4_GPW
 #define FGH_Q4_GPW 2
 #endif
@@ -331,8 +465,12 @@ constexpr int Q4_GPW = FGH_Q4_GPW;  // 8-row groups per workgroup (sharing one q
 // groups per workgroup for a row length: Q4_GPW when its LDS fits 64 KiB, else 1
 static int q4_gpw(int order, int nb) { return q4k_lds_bytes(order, nb, Q4_GPW) <= 65536 ? Q4_GPW : 1; }
 
+#ifndef FGH_Q4_LDS_MIN
+#define FGH_Q4_LDS_MIN 0
+#endif
 template <int ORDER, int MAXS, int GPW>
 static hipError_t q4_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
+    if (lds < FGH_Q4_LDS_MIN) lds = FGH_Q4_LDS_MIN;
     const unsigned wg = (unsigned)((a.groups + GPW - 1) / GPW);
     if (a.dump_s) q4k_mv_kernel<ORDER, MAXS, GPW, true><<<dim3(wg, ntok), 256 * GPW, lds, s>>>(a);
     else q4k_mv_kernel<ORDER, MAXS, GPW, false><<<dim3(wg, ntok), 256 * GPW, lds, s>>>(a);
@@ -349,9 +487,35 @@ static hipError_t q4_launch_steps(const MvArgs &a, int ntok, size_t lds, hipStre
     return q4_launch<ORDER, Q4_MAXS, GPW>(a, ntok, lds, s);
 }
 
-size_t q4k_lds_bytes(int order, int nb) { return q4k_lds_bytes(order, nb, q4_gpw(order, nb)); }
+size_t q4k_lds_bytes(int order, int nb) {
+    return FGH_Q4_KERNEL == 1 ? q4k_lds_bytes(order, nb, 1) : q4k_lds_bytes(order, nb, q4_gpw(order, nb));
+}
 
-hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, hipStream_t s) {
+#ifndef FGH_Q4_PIPE_D
+#define FGH_Q4_PIPE_D 4
+#endif
+#ifndef FGH_Q4_PIPE_WGCU
+#define FGH_Q4_PIPE_WGCU 2
+#endif
+
+template <int ORDER, int D>
+static hipError_t q4_pipe_launch(const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
+    const size_t lds = q4k_lds_bytes(ORDER, a.nb, 1);
+    if (lds > 65536) return hipErrorInvalidValue;
+    // persistent grid: FGH_Q4_PIPE_WGCU workgroups per compute unit per token, at most one per group
+    int64_t wg = (int64_t)num_cu * FGH_Q4_PIPE_WGCU;
+    if (ntok > 1) wg = (wg + ntok - 1) / ntok;
+    if (wg > a.groups) wg = a.groups;
+    if (wg < 1) wg = 1;
+    if (a.dump_s) q4k_pipe_kernel<ORDER, D, true><<<dim3((unsigned)wg, ntok), 256, lds, s>>>(a);
+    else q4k_pipe_kernel<ORDER, D, false><<<dim3((unsigned)wg, ntok), 256, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
+    if (FGH_Q4_KERNEL == 1)
+        return order == 1 ? q4_pipe_launch<1, FGH_Q4_PIPE_D>(a, ntok, num_cu, s)
+                          : q4_pipe_launch<0, FGH_Q4_PIPE_D>(a, ntok, num_cu, s);
     const int gpw = q4_gpw(order, a.nb);
     const size_t lds = q4k_lds_bytes(order, a.nb, gpw);
     if (lds > 65536) return hipErrorInvalidValue;

@@ -100,16 +100,19 @@ def test_prefill_config_shape(backend, oracle):
 
 
 def test_matmul_wide_q4k(backend, oracle):
-    """K = 116 blocks: with 40 tokens (a 64-token tile) the GEMM's LDS does not fit and the per-token
-    decode kernels run, bit-exact with the repacked single-row order; with 9 tokens (a 32-token
-    tile) the GEMM runs, within tolerance of gemm_kquant."""
+    """K = 116 blocks (29696), the widest Q4_K rows in use (Llama-70B-like FFN down projections are
+    28672): the GEMM with 40 tokens (two token tiles) and 9 tokens, within tolerance of gemm_kquant,
+    and its integers exact."""
     rows, cols = 16, 256 * 116
     w = S.random_bytes_weights(S.T_Q4_K, rows, cols, 95)
     tt = backend.upload(S.T_Q4_K, cols, w)
     X = S.activations(cols, 96, rows=40)
-    Y = backend.matmul(tt, X)
-    for t in range(40):
-        ref = oracle.matvec(S.T_Q4_K, w, cols, X[t], O_RP)
-        assert np.array_equal(Y[t].view(np.uint32), ref.view(np.uint32)), f"token {t}"
+    check_tokens(backend.matmul(tt, X), oracle.matmul(S.T_Q4_K, w, cols, X, O_RP))
     check_tokens(backend.matmul(tt, X[:9]), oracle.matmul(S.T_Q4_K, w, cols, X[:9], O_RP))
+    s_, m_ = backend.gemm_block_ints(tt, X[:33])
+    for tok in (0, 32):
+        act = oracle.quantize_for(S.T_Q4_K, X[tok])
+        for r in range(rows):
+            os_, om = oracle.block_ints(S.T_Q4_K, w[r], act)
+            assert np.array_equal(s_[tok, r], os_) and np.array_equal(m_[tok, r], om), f"token {tok} row {r}"
     tt.free()
