@@ -32,6 +32,7 @@ struct fgh_ctx {
     DevBuf x, y, aqs, ad, abs;
     DevBuf gq, gy, gb;  // prompt-GEMM activations (launch_gemm_quant layout)
     DevBuf msel, mw, mg, mu, mh, md, mlog;  // MoE: selection, weights, gate / up / h / down outputs
+    DevBuf mseg, mslot, mimx, mimh;         // MoE: slots grouped by expert, Q8_K images of x and h
     int num_cu = 256;         // compute units (sizes the persistent decode grid)
     bool capturing = false;   // inside fgh_graph_begin / fgh_graph_end
 };
@@ -219,7 +220,7 @@ void fgh_close(fgh_ctx *c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->gy, &c->gb, &c->msel, &c->mw, &c->mg,
-                      &c->mu, &c->mh, &c->md, &c->mlog})
+                      &c->mu, &c->mh, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh})
         if (b->p) (void)hipFree(b->p);
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -388,6 +389,46 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
     float *w = (float *)c->mw.p, *G = (float *)c->mg.p, *U = (float *)c->mu.p, *H = (float *)c->mh.p,
           *D = (float *)c->md.p;
     HIP_TRY(c, fgh::launch_moe_route(logits, (int)E, k, n_tok, sel, w, c->stream));
+    // several tokens, Q4_K experts: the slots grouped by expert, each expert's rows read once
+    const bool grouped = n_tok > 1 && gate->type == FGH_T_Q4_K && up->type == FGH_T_Q4_K && down->type == FGH_T_Q4_K &&
+                         gate->order == FGH_ORDER_ROW && up->order == FGH_ORDER_ROW && down->order == FGH_ORDER_ROW &&
+                         (2 * gate->nb + 15) / 16 <= 4 && (2 * down->nb + 15) / 16 <= 4 &&
+                         fgh::q4k_moe_lds_bytes(gate->nb) <= 65536 && fgh::q4k_moe_lds_bytes(down->nb) <= 65536;
+    if (grouped) {
+        const size_t ibx = fgh::q4_image_bytes(gate->nb), ibh = fgh::q4_image_bytes(down->nb);
+        if ((rc = grow(c, c->mseg, (size_t)(1 + 3 * E) * 4)) || (rc = grow(c, c->mslot, (size_t)np * 4)) ||
+            (rc = grow(c, c->mimx, (size_t)n_tok * ibx)) || (rc = grow(c, c->mimh, (size_t)np * ibh)))
+            return rc;
+        int32_t *seg = (int32_t *)c->mseg.p, *slots = (int32_t *)c->mslot.p;
+        uint8_t *imx = (uint8_t *)c->mimx.p, *imh = (uint8_t *)c->mimh.p;
+        HIP_TRY(c, fgh::launch_moe_group(sel, (int)np, (int)E, seg, slots, c->stream));
+        HIP_TRY(c, fgh::launch_q4_image(X, nullptr, n_embd, gate->nb, n_tok, imx, c->stream));
+        const int maxseg = (int)std::min<int64_t>(E, np);
+        fgh::MvArgs a;
+        memset(&a, 0, sizeof(a));
+        a.t[0] = fgh::MvT{gate->dev, G, gate->rows, gate->gpm, 0};
+        a.t[1] = fgh::MvT{up->dev, U, up->rows, up->gpm, gate->gpm};
+        a.nt = 2;
+        a.groups = gate->gpm + up->gpm;
+        a.x = X;
+        a.ldx = n_embd;
+        a.ldy = ff;
+        a.nb = gate->nb;
+        a.xdiv = k;
+        HIP_TRY(c, fgh::launch_q4k_moe(a, seg, slots, imx, maxseg, c->stream));
+        // h = silu(g) * u, quantized straight into its images (never stored as fp32)
+        HIP_TRY(c, fgh::launch_q4_image(G, U, ff, down->nb, np, imh, c->stream));
+        a.t[0] = fgh::MvT{down->dev, D, down->rows, down->gpm, 0};
+        a.nt = 1;
+        a.groups = down->gpm;
+        a.x = nullptr;
+        a.ldy = n_embd;
+        a.nb = down->nb;
+        a.xdiv = 1;
+        HIP_TRY(c, fgh::launch_q4k_moe(a, seg, slots, imh, maxseg, c->stream));
+        HIP_TRY(c, fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, c->stream));
+        return FGH_OK;
+    }
     // gate and up: one launch when their type and order agree (both read the same x row)
     if (gate->type == up->type && gate->order == up->order) {
         const fgh_tensor *gu[2] = {gate, up};

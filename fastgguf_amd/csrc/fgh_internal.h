@@ -207,6 +207,15 @@ __host__ __device__ inline float expf_ref(float x) {
 }
 hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s);  // test hook
 hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok, int32_t *sel, float *w, hipStream_t s);
+hipError_t launch_moe_group(const int32_t *sel, int np, int n_expert, int32_t *seg, int32_t *slots, hipStream_t s);
+// grouped Q4_K row-order expert matvecs (fgh_q4k.hip): a.groups = groups of one matrix over a.t
+size_t q4k_moe_lds_bytes(int nb);
+hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *seg, const int32_t *slots, const uint8_t *img,
+                          int max_segments, hipStream_t s);
+// Q8_K images of rows in the decode kernels' LDS layout; u != null: the rows are silu(x) * u
+size_t q4_image_bytes(int nb);
+hipError_t launch_q4_image(const float *x, const float *u, int64_t ldx, int nb, int64_t rows, uint8_t *img,
+                           hipStream_t s);
 hipError_t launch_moe_silu_mul(const float *g, const float *u, float *h, int64_t n, hipStream_t s);
 hipError_t launch_moe_combine(const float *d, const float *w, float *y, int n_embd, int k, int n_tok, int64_t ldy,
                               hipStream_t s);

@@ -57,16 +57,20 @@ size_t q4k_lds_bytes(int order, int nb, int gpw) { return q4_act_bytes(nb) + 4 *
 struct XRound {
     float4 v[4];
 };
-__device__ __forceinline__ void q8k_load(const float *__restrict__ x, int nb, int rb, XRound &xr) {
-    const int b = rb + (threadIdx.x >> 4), tl = threadIdx.x & 15;
-    const bool live = b < nb;
-    const float *p = x + (size_t)(live ? b : 0) * 256 + 16 * tl;
+// block b of x (thread's 16 values: tl = threadIdx.x % 16); blocks past the end read block 0
+__device__ __forceinline__ void q8k_load_b(const float *__restrict__ x, int b, bool live, XRound &xr) {
+    const float *p = x + (size_t)(live ? b : 0) * 256 + 16 * (threadIdx.x & 15);
 #pragma unroll
     for (int u = 0; u < 4; ++u) xr.v[u] = *(const float4 *)(p + 4 * u);
 }
-__device__ __forceinline__ void q8k_store(int nb, int rb, const XRound &xr, uint8_t *act) {
-    const int b = rb + (threadIdx.x >> 4), tl = threadIdx.x & 15;
-    const bool live = b < nb;
+__device__ __forceinline__ void q8k_load(const float *__restrict__ x, int nb, int rb, XRound &xr) {
+    const int b = rb + (threadIdx.x >> 4);
+    q8k_load_b(x, b, b < nb, xr);
+}
+// quantizes the 16 threads' block b into act (stored only if live); the 16 threads of a block
+// are one DPP row, so a row is either wholly live or wholly not
+__device__ __forceinline__ void q8k_store_b(int nb, int b, bool live, const XRound &xr, uint8_t *act) {
+    const int tl = threadIdx.x & 15;
     float v[16];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -95,6 +99,10 @@ __device__ __forceinline__ void q8k_store(int nb, int rb, const XRound &xr, uint
         ((int16_t *)(act + q4_off_s(nb)))[16 * b + tl] = (int16_t)s;
         if (tl == 0) ((float *)(act + q4_off_d(nb)))[b] = d;
     }
+}
+__device__ __forceinline__ void q8k_store(int nb, int rb, const XRound &xr, uint8_t *act) {
+    const int b = rb + (threadIdx.x >> 4);
+    q8k_store_b(nb, b, b < nb, xr, act);
 }
 
 __device__ __forceinline__ void wave_sync() {
@@ -358,105 +366,6 @@ __global__ __launch_bounds__(256 * GPW) void q4k_mv_kernel(MvArgs a) {
     q4_chain<ORDER>(c, lane, a.t[ti].y + (size_t)tok * a.ldy + obase + lr0, a.t[ti].rows - lr0);
 }
 
-// Persistent, software-pipelined variant: workgroup blockIdx.x walks the groups
-// [G * x / gridDim.x, G * (x + 1) / gridDim.x) with 4 wavefronts (rows 2w, 2w + 1 of each group).
-// A wavefront's steps form one sequence over its groups; D steps are in flight in a ring of
-// registers, each reloaded with the step D later right after it is computed (the scheduling
-// barrier keeps the loads in issue order, so waiting for one step never waits for a later one).
-// x is quantized once per workgroup while the first D steps load.
-template <int ORDER, int D, bool DUMP>
-__global__ __launch_bounds__(256) void q4k_pipe_kernel(MvArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j = lane & 3, pl = lane >> 2;
-    const int nb = a.nb, P = 2 * nb;
-    const int NS = (P + 15) >> 4;
-    const int tok = blockIdx.y;
-    const int64_t g0 = a.groups * blockIdx.x / gridDim.x, g1 = a.groups * (blockIdx.x + 1) / gridDim.x;
-    if (g0 >= g1) return;  // whole workgroup
-    const int64_t S = (g1 - g0) * NS;
-    const int64_t mgsel = a.sel ? (int64_t)a.sel[tok] : 0;  // selected matrix (MoE)
-
-    Q4Ctx c;
-    c.act = smem;
-    c.ad = (const float *)(smem + q4_off_d(nb));
-    c.abs16 = (const int16_t *)(smem + q4_off_s(nb));
-    c.rec = (float *)(smem + q4_act_bytes(nb) + (size_t)wave * q4_wave_bytes(ORDER, nb));
-    c.nb = nb;
-    c.P = P;
-    c.j = j;
-    c.pl = pl;
-
-    // loads of step s of the sequence (clamped to the last one)
-    int64_t lg_g = g0;  // group of the next load
-    int lg_s = 0;       // its step
-    auto load_next = [&](Q4Step &st) {
-        const int ti = q4_tensor_of(a, lg_g);
-        const uint8_t *G = a.t[ti].W + (size_t)(mgsel * a.t[ti].gpm + lg_g - a.t[ti].gfirst) * 1152 * nb;
-        const int np = min(16, P - 16 * lg_s);
-        const int pc = min(pl, np - 1);
-        const uint8_t *qb = G + (size_t)128 * nb + (size_t)256 * nb * wave + (size_t)2048 * lg_s + 16 * (4 * pc + j);
-        st.p0 = ld16(qb);
-        st.p1 = ld16(qb + 64 * np);
-        st.m = ld16(G + (size_t)16 * P * wave + 16 * (16 * lg_s + pc));
-        if (lg_s + 1 < NS) {
-            ++lg_s;
-        } else if (lg_g + 1 < g1) {
-            lg_s = 0;
-            ++lg_g;
-        }  // else: stay on the last step (re-reads)
-    };
-
-    const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
-    XRound xr;
-    q8k_load(x, nb, 0, xr);
-    Q4Step ring[D];
-#pragma unroll
-    for (int k = 0; k < D; ++k) load_next(ring[k]);
-    __builtin_amdgcn_sched_barrier(0);
-    for (int rb = 0; rb < nb; rb += 16) {
-        if (rb > 0) q8k_load(x, nb, rb, xr);
-        q8k_store(nb, rb, xr, smem);
-    }
-    __syncthreads();
-
-    int64_t cg = g0;  // group being computed
-    int cs = 0;       // its step
-    for (int64_t s0 = 0; s0 < S; s0 += D) {
-#pragma unroll
-        for (int k = 0; k < D; ++k) {
-            if (s0 + k < S) {  // uniform
-                if (DUMP || cs == NS - 1) {
-                    const int ti = q4_tensor_of(a, cg);
-                    const int64_t lg = cg - a.t[ti].gfirst;
-                    const int64_t lr0 = (lg % a.t[ti].gpm) * 8 + 2 * wave;
-                    const int64_t obase = (lg / a.t[ti].gpm) * a.t[ti].rows;
-                    Q4Dump dump{a.dump_s, a.dump_m, obase + lr0, a.t[ti].rows - lr0};
-                    q4_step<ORDER, DUMP>(ring[k], cs, c, dump);
-                    if (cs == NS - 1) {
-                        wave_sync();
-                        q4_chain<ORDER>(c, lane, a.t[ti].y + (size_t)tok * a.ldy + obase + lr0, a.t[ti].rows - lr0);
-                        wave_sync();  // the next group's records reuse the area
-                    }
-                } else {
-                    Q4Dump none{nullptr, nullptr, 0, 0};
-                    q4_step<ORDER, false>(ring[k], cs, c, none);
-                }
-                if (++cs == NS) {
-                    cs = 0;
-                    ++cg;
-                }
-            }
-            load_next(ring[k]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-}
-
-#ifndef FGH_Q4_KERNEL
-#define FGH_Q4_KERNEL 0
-#endif
 #ifndef FGH_Q4_GPW
 #define FGH_Q4_GPW 2
 #endif
@@ -465,12 +374,8 @@ constexpr int Q4_GPW = FGH_Q4_GPW;  // 8-row groups per workgroup (sharing one q
 // groups per workgroup for a row length: Q4_GPW when its LDS fits 64 KiB, else 1
 static int q4_gpw(int order, int nb) { return q4k_lds_bytes(order, nb, Q4_GPW) <= 65536 ? Q4_GPW : 1; }
 
-#ifndef FGH_Q4_LDS_MIN
-#define FGH_Q4_LDS_MIN 0
-#endif
 template <int ORDER, int MAXS, int GPW>
 static hipError_t q4_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
-    if (lds < FGH_Q4_LDS_MIN) lds = FGH_Q4_LDS_MIN;
     const unsigned wg = (unsigned)((a.groups + GPW - 1) / GPW);
     if (a.dump_s) q4k_mv_kernel<ORDER, MAXS, GPW, true><<<dim3(wg, ntok), 256 * GPW, lds, s>>>(a);
     else q4k_mv_kernel<ORDER, MAXS, GPW, false><<<dim3(wg, ntok), 256 * GPW, lds, s>>>(a);
@@ -487,40 +392,141 @@ static hipError_t q4_launch_steps(const MvArgs &a, int ntok, size_t lds, hipStre
     return q4_launch<ORDER, Q4_MAXS, GPW>(a, ntok, lds, s);
 }
 
-size_t q4k_lds_bytes(int order, int nb) {
-    return FGH_Q4_KERNEL == 1 ? q4k_lds_bytes(order, nb, 1) : q4k_lds_bytes(order, nb, q4_gpw(order, nb));
-}
+size_t q4k_lds_bytes(int order, int nb) { return q4k_lds_bytes(order, nb, q4_gpw(order, nb)); }
 
-#ifndef FGH_Q4_PIPE_D
-#define FGH_Q4_PIPE_D 4
-#endif
-#ifndef FGH_Q4_PIPE_WGCU
-#define FGH_Q4_PIPE_WGCU 2
-#endif
-
-template <int ORDER, int D>
-static hipError_t q4_pipe_launch(const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
-    const size_t lds = q4k_lds_bytes(ORDER, a.nb, 1);
-    if (lds > 65536) return hipErrorInvalidValue;
-    // persistent grid: FGH_Q4_PIPE_WGCU workgroups per compute unit per token, at most one per group
-    int64_t wg = (int64_t)num_cu * FGH_Q4_PIPE_WGCU;
-    if (ntok > 1) wg = (wg + ntok - 1) / ntok;
-    if (wg > a.groups) wg = a.groups;
-    if (wg < 1) wg = 1;
-    if (a.dump_s) q4k_pipe_kernel<ORDER, D, true><<<dim3((unsigned)wg, ntok), 256, lds, s>>>(a);
-    else q4k_pipe_kernel<ORDER, D, false><<<dim3((unsigned)wg, ntok), 256, lds, s>>>(a);
-    return hipGetLastError();
-}
-
-hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
-    if (FGH_Q4_KERNEL == 1)
-        return order == 1 ? q4_pipe_launch<1, FGH_Q4_PIPE_D>(a, ntok, num_cu, s)
-                          : q4_pipe_launch<0, FGH_Q4_PIPE_D>(a, ntok, num_cu, s);
+hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int, hipStream_t s) {
     const int gpw = q4_gpw(order, a.nb);
     const size_t lds = q4k_lds_bytes(order, a.nb, gpw);
     if (lds > 65536) return hipErrorInvalidValue;
     if (order == 1) return gpw == 1 ? q4_launch_steps<1, 1>(a, ntok, lds, s) : q4_launch_steps<1, Q4_GPW>(a, ntok, lds, s);
     return gpw == 1 ? q4_launch_steps<0, 1>(a, ntok, lds, s) : q4_launch_steps<0, Q4_GPW>(a, ntok, lds, s);
+}
+
+// Q8_K images of activation rows, in the kernels' LDS layout (q4_act_bytes(nb) bytes per row): row
+// r of x (stride ldx) -> img + r * q4_act_bytes(nb). SILU: the row is silu(g) * u of two fp32
+// arrays (silu_f, fastgguf.c:3118: x / (1 + expf(-x))), quantized without being stored.
+// 16 threads per 256-value block, 16 blocks per workgroup.
+template <bool SILU>
+__global__ __launch_bounds__(256) void q4_image_kernel(const float *__restrict__ x, const float *__restrict__ u,
+                                                       int64_t ldx, int nb, int64_t rows, uint8_t *__restrict__ img) {
+    const int64_t cb = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);  // (row, block)
+    const bool live = cb < rows * nb;
+    const int64_t r = live ? cb / nb : 0;
+    const int b = live ? (int)(cb - r * nb) : 0;
+    XRound xr;
+    q8k_load_b(x + (size_t)r * ldx, b, true, xr);
+    if (SILU) {
+        XRound ur;
+        q8k_load_b(u + (size_t)r * ldx, b, true, ur);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float4 &g = xr.v[q];
+            const float4 uu = ur.v[q];
+            g.x = g.x / (1.0f + expf_ref(-g.x)) * uu.x;
+            g.y = g.y / (1.0f + expf_ref(-g.y)) * uu.y;
+            g.z = g.z / (1.0f + expf_ref(-g.z)) * uu.z;
+            g.w = g.w / (1.0f + expf_ref(-g.w)) * uu.w;
+        }
+    }
+    q8k_store_b(nb, b, live, xr, img + (size_t)r * q4_act_bytes(nb));
+}
+
+hipError_t launch_q4_image(const float *x, const float *u, int64_t ldx, int nb, int64_t rows, uint8_t *img,
+                           hipStream_t s) {
+    const int64_t wg = (rows * nb + 15) / 16;
+    if (u) q4_image_kernel<true><<<(unsigned)wg, 256, 0, s>>>(x, u, ldx, nb, rows, img);
+    else q4_image_kernel<false><<<(unsigned)wg, 256, 0, s>>>(x, u, ldx, nb, rows, img);
+    return hipGetLastError();
+}
+size_t q4_image_bytes(int nb) { return q4_act_bytes(nb); }
+
+// MoE expert matvecs grouped by expert (row order, dot_q4_K_q8k): workgroup (x, y) takes 8-row group
+// x of the matrix of segment y (one selected expert with its token slots, from moe_group_kernel)
+// and every slot of that segment. Each wavefront loads its two rows' weights into registers once,
+// then for every chunk of MOE_TC slots copies their activation images (q4_image_kernel, row
+// slot / a.xdiv) into LDS and runs the same steps and chain as q4k_mv_kernel, once per slot.
+// Tensor i of a.t: output rows y_i[slot * ldy]. seg: [0] = number of segments, then per segment
+// {expert, first, count}.
+constexpr int MOE_TC = 4;
+template <int MAXS>
+__global__ __launch_bounds__(256) void q4k_moe_kernel(MvArgs a, const int32_t *__restrict__ seg,
+                                                      const int32_t *__restrict__ slots, const uint8_t *__restrict__ img) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 3, pl = lane >> 2;
+    const int nb = a.nb, P = 2 * nb;
+    const int nsteps = (P + 15) >> 4;
+    const int sidx = blockIdx.y;
+    if (sidx >= seg[0]) return;  // whole workgroup: fewer segments than the grid allows
+    const int expert = seg[1 + 3 * sidx], first = seg[2 + 3 * sidx], count = seg[3 + 3 * sidx];
+    const int64_t g = blockIdx.x;
+    const int ti = q4_tensor_of(a, g);
+    const int64_t lg = g - a.t[ti].gfirst;  // group within the matrix
+    const uint8_t *G = a.t[ti].W + (size_t)((int64_t)expert * a.t[ti].gpm + lg) * 1152 * nb;
+    const uint8_t *meta = G + (size_t)16 * P * wave;
+    const uint8_t *quant = G + (size_t)128 * nb + (size_t)256 * nb * wave;
+    Q4Step st[MAXS];
+#pragma unroll
+    for (int k = 0; k < MAXS; ++k) {
+        const int s = k < nsteps ? k : nsteps - 1;
+        const int np = min(16, P - 16 * s);
+        const int pc = min(pl, np - 1);
+        const uint8_t *qb = quant + (size_t)2048 * s + 16 * (4 * pc + j);
+        st[k].p0 = ld16(qb);
+        st[k].p1 = ld16(qb + 64 * np);
+        st[k].m = ld16(meta + 16 * (16 * s + pc));
+    }
+    const size_t actb = q4_act_bytes(nb), waveb = q4_wave_bytes(0, nb);
+    const int units = (int)(actb / 16);
+    const int64_t lr0 = lg * 8 + 2 * wave;
+    const int64_t left = a.t[ti].rows - lr0;
+    float *rec0 = (float *)(smem + MOE_TC * actb + (size_t)wave * waveb);
+    for (int c0 = 0; c0 < count; c0 += MOE_TC) {
+        const int nc = min(MOE_TC, count - c0);
+        // the chunk's activation images (rows slot / xdiv) into LDS
+        for (int i = tid; i < nc * units; i += 256) {
+            const int c = i / units, o = i - c * units;
+            const int slot = slots[first + c0 + c];
+            ((uint4 *)(smem + (size_t)c * actb))[o] = ((const uint4 *)(img + (size_t)(slot / a.xdiv) * actb))[o];
+        }
+        __syncthreads();
+        for (int c = 0; c < nc; ++c) {
+            const uint8_t *act = smem + (size_t)c * actb;
+            Q4Ctx cx;
+            cx.act = act;
+            cx.ad = (const float *)(act + q4_off_d(nb));
+            cx.abs16 = (const int16_t *)(act + q4_off_s(nb));
+            cx.rec = rec0;
+            cx.nb = nb;
+            cx.P = P;
+            cx.j = j;
+            cx.pl = pl;
+            Q4Dump none{nullptr, nullptr, 0, 0};
+#pragma unroll
+            for (int k = 0; k < MAXS; ++k)
+                if (k < nsteps) q4_step<0, false>(st[k], k, cx, none);
+            wave_sync();
+            q4_chain<0>(cx, lane, a.t[ti].y + (size_t)slots[first + c0 + c] * a.ldy + lr0, left);
+            wave_sync();  // the next slot's records reuse the area
+        }
+        __syncthreads();  // the next chunk reuses the activations
+    }
+}
+
+size_t q4k_moe_lds_bytes(int nb) { return MOE_TC * q4_act_bytes(nb) + 4 * q4_wave_bytes(0, nb); }
+
+// a.groups = groups of one matrix over all tensors (the launch's x extent); grid.y = max_segments
+hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *seg, const int32_t *slots, const uint8_t *img,
+                          int max_segments, hipStream_t s) {
+    const int nsteps = (2 * a.nb + 15) / 16;
+    const size_t lds = q4k_moe_lds_bytes(a.nb);
+    if (nsteps > 4 || lds > 65536) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)a.groups, (unsigned)max_segments);
+    if (nsteps <= 1) q4k_moe_kernel<1><<<grid, 256, lds, s>>>(a, seg, slots, img);
+    else if (nsteps <= 2) q4k_moe_kernel<2><<<grid, 256, lds, s>>>(a, seg, slots, img);
+    else q4k_moe_kernel<4><<<grid, 256, lds, s>>>(a, seg, slots, img);
+    return hipGetLastError();
 }
 
 // upload-time re-layout of Q4_K rows into the group layout above; one thread per destination byte
