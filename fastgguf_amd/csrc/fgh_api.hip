@@ -44,7 +44,7 @@ struct fgh_tensor {
     int order;     // FGH_ORDER_ROW / FGH_ORDER_REPACKED (Q4_K); ROW otherwise
     int nb;        // blocks per row (256-blocks for K-quants, 32-blocks for Q8_0)
     int ntile;     // tiles per row group
-    int64_t gpm;   // row groups per matrix
+    int64_t gpm;   // row tiles per matrix (16 rows for Q4_K, 8 otherwise)
     int64_t groups;
     uint8_t *dev;
     uint64_t dev_bytes;
@@ -128,7 +128,7 @@ static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const fl
     int64_t g = 0;
     for (int i = 0; i < n; i++) {
         a.t[i] = fgh::MvT{t[i]->dev, y[i], t[i]->rows, t[i]->gpm, g};
-        g += sel ? t[i]->gpm : t[i]->groups;  // with an expert index: the groups of one matrix
+        g += sel ? t[i]->gpm : t[i]->groups;  // with an expert index: the tiles of one matrix
     }
     a.sel = sel;
     a.xdiv = xdiv;
@@ -272,7 +272,8 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     t->n_mats = n_mats;
     t->nb = (int)(cols / block_elems(type));
     t->ntile = type == FGH_T_Q8_0 ? (t->nb + 3) / 4 : t->nb;
-    t->gpm = (rows + 7) / 8;
+    const int tile_rows = type == FGH_T_Q4_K ? fgh::Q4K_TILE_ROWS : 8;
+    t->gpm = (rows + tile_rows - 1) / tile_rows;
     t->groups = t->gpm * n_mats;
     t->order = ord;
     t->dev_bytes = (uint64_t)t->groups * t->ntile * tile_bytes(type);
@@ -392,7 +393,7 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
     // several tokens, Q4_K experts: the slots grouped by expert, each expert's rows read once
     const bool grouped = n_tok > 1 && gate->type == FGH_T_Q4_K && up->type == FGH_T_Q4_K && down->type == FGH_T_Q4_K &&
                          gate->order == FGH_ORDER_ROW && up->order == FGH_ORDER_ROW && down->order == FGH_ORDER_ROW &&
-                         (2 * gate->nb + 15) / 16 <= 4 && (2 * down->nb + 15) / 16 <= 4 &&
+                         gate->nb <= fgh::q4k_moe_max_blocks() && down->nb <= fgh::q4k_moe_max_blocks() &&
                          fgh::q4k_moe_lds_bytes(gate->nb) <= 65536 && fgh::q4k_moe_lds_bytes(down->nb) <= 65536;
     if (grouped) {
         const size_t ibx = fgh::q4_image_bytes(gate->nb), ibh = fgh::q4_image_bytes(down->nb);

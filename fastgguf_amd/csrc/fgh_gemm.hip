@@ -20,10 +20,10 @@
 // uses inside one K step.
 //
 // Weights are read in the decode layout (fgh_q4k.hip): the GEMM needs no second copy. A
-// workgroup owns 64 rows and all tokens: 4 * NTW wavefronts = 2 slices of 32 rows x 2 halves of
-// the blocks (even / odd) x NTW tiles of 32 tokens. It walks the blocks in steps of two: the
-// step's weights for all 64 rows (18 KB) are staged in LDS by the whole workgroup with coalesced
-// loads (128 contiguous bytes per row half) and read back as MFMA fragments; activations are read
+// workgroup owns 64 rows (4 tiles) and all tokens: 4 * NTW wavefronts = 2 slices of 32 rows x 2
+// halves of the blocks (even / odd) x NTW tiles of 32 tokens. It walks the blocks in steps of two:
+// the step's weights for all 64 rows (18 KB) are staged in LDS by the whole workgroup with
+// coalesced loads (1 KB contiguous per wavefront load) and read back as MFMA fragments; activations are read
 // straight from global memory in a fragment-ordered layout (1 KB contiguous per load). Both are
 // double-buffered one step ahead. The two halves of the blocks are added at the end through LDS.
 //
@@ -84,77 +84,69 @@ __global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict
 // ---------------------------------------------------------------------------------------------
 constexpr int GW_STAGE = 18432;  // LDS bytes of one weight stage: quants 16 KB + meta 2 KB
 
-// the decode-layout address of one 16-byte piece: piece h of chunk j of block b of a row, given
-// the row's wavefront region base (group + 128 nb + 256 nb * w') and its index r2 in the region
-__device__ __forceinline__ const uint8_t *q4_piece(const uint8_t *region, int nb, int r2, int b, int h, int j) {
-    const int q = r2 * nb + b;
-    const int st = q >> 4, p = q & 15, np = min(16, 2 * nb - 16 * st);
-    return region + 2048 * st + h * 64 * np + 64 * p + 16 * j;
-}
-
-// One workgroup's share of a weight stage (blocks 2s and 2s+1 of its 64 rows), held by thread tid:
-// quant units u = tid + k * NT (u = 16 row + 8 h + 4 blk + j: eight consecutive threads read 128
-// contiguous bytes) and, for tid < 128, the meta of (row tid / 2, blk tid % 2).
+// One workgroup's share of a weight stage (blocks 2s and 2s+1 of its 64 rows = 4 tiles), held by
+// thread tid: quant units u = tid + k * NT, u = ((blk * 4 + tile) * 2 + hh) * 64 + L, i.e. slot
+// (hh, L) of the tile layout (64 consecutive units read 1 KB contiguous), and for tid < 128 the
+// meta of (row tid % 64, blk tid / 64).
 template <int NT>
 struct WStage {
     static constexpr int NU = 1024 / NT;
-    const uint8_t *region[NU];  // per unit: the row's wavefront region in the decode layout
-    int r2[NU];
-    const uint8_t *mregion;      // meta: group base + 16 * 2 nb * w'
-    int mr2;
+    const uint8_t *src[NU];  // per unit: its address in block 0 of its tile
+    int slot[NU];            // per unit: its LDS slot
+    const uint8_t *msrc;     // the meta row's address in block 0 of its tile
     uint4 q[NU], m;
 };
 
+// LDS stage layout: quants [blk][j][h][row 0..63] x 16 B (a fragment = 512 B contiguous per h),
+// meta at 16 KB: [blk][row] x 16 B. Row slots are XOR-swizzled with 2j (quants) and 4 blk (meta):
+// the eight threads of one 128-byte write phase hold rows 2m, 2m+1 x chunks j = 0..3 of one tile,
+// and the swizzle sends them to eight different bank quads; a fragment read stays a permutation
+// of 32 consecutive slots.
+__device__ __forceinline__ int gq_slot(int blk, int j, int h, int row) {
+    return ((blk * 4 + j) * 2 + h) * 64 + (row ^ (2 * j));
+}
+__device__ __forceinline__ int gm_slot(int blk, int row) { return 1024 + blk * 64 + (row ^ (blk << 2)); }
+
+// the tile-layout address of (row R over all matrices, block 0): its tile and its row in the tile
+__device__ __forceinline__ const uint8_t *gemm_tile(const GemmArgs &a, int64_t R, int &rr) {
+    R = R < a.nrows ? R : a.nrows - 1;
+    const int64_t mat = R / a.rows, r = R - mat * a.rows;
+    rr = (int)(r & 15);
+    return a.W + (size_t)(mat * a.gpm + (r >> 4)) * a.nb * 2304;
+}
+
 template <int NT>
 __device__ __forceinline__ void wstage_init(WStage<NT> &w, const GemmArgs &a, int64_t row0, int tid) {
-    const int nb = a.nb;
 #pragma unroll
-    for (int k = 0; k <= WStage<NT>::NU; ++k) {
-        const int u = k < WStage<NT>::NU ? tid + k * NT : 16 * (tid >> 1);  // k == NU: the meta row
-        int64_t R = row0 + (u >> 4);
-        R = R < a.nrows ? R : a.nrows - 1;
-        const int64_t mat = R / a.rows, r = R - mat * a.rows;
-        const int rr = (int)(r & 7);
-        const uint8_t *G = a.W + (size_t)(mat * a.gpm + (r >> 3)) * 1152 * nb;
-        if (k < WStage<NT>::NU) {
-            w.region[k] = G + (size_t)128 * nb + (size_t)256 * nb * (rr >> 1);
-            w.r2[k] = rr & 1;
-        } else {
-            w.mregion = G + (size_t)32 * nb * (rr >> 1);
-            w.mr2 = rr & 1;
-        }
+    for (int k = 0; k < WStage<NT>::NU; ++k) {
+        const int u = tid + k * NT;
+        const int L = u & 63, hh = (u >> 6) & 1, tl = (u >> 7) & 3, blk = u >> 9, j = L & 3;
+        const int row = 16 * tl + (L >> 2);
+        int rr;
+        const uint8_t *T = gemm_tile(a, row0 + row, rr);
+        w.src[k] = T + 256 + 1024 * hh + 16 * (4 * rr + j);
+        w.slot[k] = gq_slot(blk, j, hh ^ (j >> 1), row);  // slot hh holds piece hh ^ (j >> 1)
     }
+    int rr;
+    const uint8_t *T = gemm_tile(a, row0 + (tid & 63), rr);
+    w.msrc = T + 16 * rr;
 }
 
 template <int NT>
 __device__ __forceinline__ void wstage_load(WStage<NT> &w, int nb, int s, int tid) {
 #pragma unroll
     for (int k = 0; k < WStage<NT>::NU; ++k) {
-        const int u = tid + k * NT;
-        const int b = min(2 * s + ((u >> 2) & 1), nb - 1);
-        w.q[k] = ld16(q4_piece(w.region[k], nb, w.r2[k], b, (u >> 3) & 1, u & 3));
+        const int blk = (tid + k * NT) >> 9;
+        w.q[k] = ld16(w.src[k] + (size_t)min(2 * s + blk, nb - 1) * 2304);
     }
-    if (tid < 128) w.m = ld16(w.mregion + 16 * (w.mr2 * nb + min(2 * s + (tid & 1), nb - 1)));
+    if (tid < 128) w.m = ld16(w.msrc + (size_t)min(2 * s + (tid >> 6), nb - 1) * 2304);
 }
-
-// LDS stage layout: quants [blk][j][h][row 0..63] x 16 B (a fragment = 512 B contiguous per h),
-// meta at 16 KB: [blk][row] x 16 B. Row slots are XOR-swizzled with (j, blk) (quants) and blk
-// (meta): the eight threads of one 128-byte write phase hold eight (j, blk) of one row, and the
-// swizzle sends them to eight different bank quads; a fragment read stays a permutation of 32
-// consecutive slots.
-__device__ __forceinline__ int gq_slot(int blk, int j, int h, int row) {
-    return ((blk * 4 + j) * 2 + h) * 64 + (row ^ (j | (blk << 2)));
-}
-__device__ __forceinline__ int gm_slot(int blk, int row) { return 1024 + blk * 64 + (row ^ (blk << 2)); }
 
 template <int NT>
 __device__ __forceinline__ void wstage_store(const WStage<NT> &w, uint8_t *buf, int tid) {
 #pragma unroll
-    for (int k = 0; k < WStage<NT>::NU; ++k) {
-        const int u = tid + k * NT;
-        *(uint4 *)(buf + 16 * gq_slot((u >> 2) & 1, u & 3, (u >> 3) & 1, u >> 4)) = w.q[k];
-    }
-    if (tid < 128) *(uint4 *)(buf + 16 * gm_slot(tid & 1, tid >> 1)) = w.m;
+    for (int k = 0; k < WStage<NT>::NU; ++k) *(uint4 *)(buf + 16 * w.slot[k]) = w.q[k];
+    if (tid < 128) *(uint4 *)(buf + 16 * gm_slot(tid >> 6, tid & 63)) = w.m;
 }
 
 // one lane's activation operands of one block: group g (16 values of token 32 tt + l % 32) and

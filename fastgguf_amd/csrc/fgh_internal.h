@@ -16,7 +16,7 @@ namespace fgh {
 // partials are the reference's lane partials, and the fp32 chains can follow its order.
 // Rows past the end of a matrix are zero-filled (d = 0) and never stored.
 //
-//   (Q4_K uses its own group layout, described in fgh_q4k.hip)
+//   (Q4_K uses its own layout of 16-row tiles, 2304 B per (tile, block), described in fgh_q4k.hip)
 //   Q6_K tile, one block of 8 rows, 1680 B (= 8 x 210):
 //     [0, 128)     int8 scales, row r at 16r (file bytes 192..207)
 //     [128, 144)   fp16 d, row r at 128 + 2r (file bytes 208..209)
@@ -27,7 +27,8 @@ namespace fgh {
 //     [64, 1088)   quants: slice (r, i) at 64 + 16(8r + i); dword bb = block bb's bytes 2+4i..+3
 // ---------------------------------------------------------------------------------------------
 constexpr int T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14;
-constexpr int Q4K_TILE = 1152, Q6K_TILE = 1680, Q80_TILE = 1088;
+constexpr int Q4K_TILE = 2304, Q6K_TILE = 1680, Q80_TILE = 1088;
+constexpr int Q4K_TILE_ROWS = 16;  // rows per Q4_K tile (8 for the other types)
 
 // Device activation layouts. Q8_K (for Q4_K / Q6_K): per token, nb blocks of
 //   qs [nb][256] int8, permuted so lane i's 32 bytes are contiguous: position 32i + 4c + k holds
@@ -141,27 +142,27 @@ struct MvT {
     const uint8_t *W;
     float *y;
     int64_t rows;    // rows per matrix
-    int64_t gpm;     // row groups per matrix
-    int64_t gfirst;  // first global group index of this tensor
+    int64_t gpm;     // row tiles per matrix (16 rows for Q4_K, 8 otherwise)
+    int64_t gfirst;  // first global tile index of this tensor
 };
 struct MvArgs {
     MvT t[4];
     int nt;
-    int64_t groups;    // row groups over all the tensors
+    int64_t groups;    // row tiles over all the tensors
     const float *x;    // fp32 activations, quantized inside the kernel
     int64_t ldx, ldy;  // token strides of x and of every y
     int nb, ntile;     // blocks and tiles per row
     int32_t *dump_s, *dump_m;  // test hook: per (row, block) integers of tensor 0, or null
     // expert indirection (MoE): when sel is set, token slot y (blockIdx.y) uses matrix sel[y] of
-    // every tensor (launched with the groups of one matrix) and activation row y / xdiv
+    // every tensor (launched with the tiles of one matrix) and activation row y / xdiv
     const int32_t *sel;
     int xdiv;
 };
 size_t matvec_lds_bytes(int type, int order, int nb);  // Q6_K / Q8_0 (fgh_matvec.hip)
-// Q4_K (fgh_q4k.hip): its own group layout and kernel
+// Q4_K (fgh_q4k.hip): its own tile layout and kernel
 size_t q4k_lds_bytes(int order, int nb);
 hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
-hipError_t launch_q4k_relayout(const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t gpm, int64_t total,
+hipError_t launch_q4k_relayout(const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t tpm, int64_t total,
                                int64_t row_bytes, hipStream_t s);
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
 
@@ -208,8 +209,10 @@ __host__ __device__ inline float expf_ref(float x) {
 hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s);  // test hook
 hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok, int32_t *sel, float *w, hipStream_t s);
 hipError_t launch_moe_group(const int32_t *sel, int np, int n_expert, int32_t *seg, int32_t *slots, hipStream_t s);
-// grouped Q4_K row-order expert matvecs (fgh_q4k.hip): a.groups = groups of one matrix over a.t
+// grouped Q4_K row-order expert matvecs (fgh_q4k.hip): a.groups = tiles of one matrix over a.t;
+// rows of at most q4k_moe_max_blocks() blocks
 size_t q4k_moe_lds_bytes(int nb);
+int q4k_moe_max_blocks();
 hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *seg, const int32_t *slots, const uint8_t *img,
                           int max_segments, hipStream_t s);
 // Q8_K images of rows in the decode kernels' LDS layout; u != null: the rows are silu(x) * u
@@ -222,9 +225,9 @@ hipError_t launch_moe_combine(const float *d, const float *w, float *y, int n_em
 
 // prompt-batch Q4_K GEMM (fgh_gemm.hip): 1..64 tokens, weights in the Q4_K decode layout
 struct GemmArgs {
-    const uint8_t *W;   // Q4_K tensor (group layout)
+    const uint8_t *W;   // Q4_K tensor (tile layout)
     float *Y;           // Y[tok * ldy + row]
-    int64_t rows, gpm;  // rows and row groups per matrix
+    int64_t rows, gpm;  // rows and 16-row tiles per matrix
     int64_t nrows;      // rows over all matrices (outputs per token)
     int nb;             // 256-blocks per row
     const int8_t *qs;   // activations from launch_gemm_quant

@@ -78,12 +78,13 @@ __global__ __launch_bounds__(256) void quant_q8_kernel(const float *__restrict__
 }
 
 // =============================================================================================
-// Upload-time re-layout: file-layout rows (n_mats x rows x row_bytes) -> tiles. One thread per
-// destination byte; padding rows and padding blocks are zero.
+// Upload-time re-layout of Q6_K / Q8_0: file-layout rows (n_mats x rows x row_bytes) -> tiles (Q4_K
+// has its own, fgh_q4k.hip). One thread per destination byte; padding rows and padding blocks are
+// zero.
 // =============================================================================================
 __global__ void relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int type,
                                 int64_t rows, int nb, int ntile, int64_t gpm, int64_t total, int64_t row_bytes) {
-    const int tile_bytes = type == T_Q4_K ? Q4K_TILE : type == T_Q6_K ? Q6K_TILE : Q80_TILE;
+    const int tile_bytes = type == T_Q6_K ? Q6K_TILE : Q80_TILE;
     for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
          o += (int64_t)gridDim.x * blockDim.x) {
         const int64_t t = o / tile_bytes;
@@ -92,17 +93,7 @@ __global__ void relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__rest
         const int tb = (int)(t - g * ntile);
         const int64_t m = g / gpm, gl = g - m * gpm;
         int r, blk, byte;  // source row in group, block in row, byte in block
-        if (type == T_Q4_K) {
-            blk = tb;
-            if (ob < 128) {
-                r = ob >> 4;
-                byte = ob & 15;
-            } else {
-                const int q = ob - 128, i = (q & 127) >> 4, j = (q & 15) >> 2, k = q & 3;
-                r = q >> 7;
-                byte = 16 + 32 * j + 4 * i + k;
-            }
-        } else if (type == T_Q6_K) {
+        if (type == T_Q6_K) {
             blk = tb;
             if (ob < 128) {
                 r = ob >> 4;
@@ -132,7 +123,7 @@ __global__ void relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__rest
             }
         }
         const int64_t row = gl * 8 + r;
-        const int bb = type == T_Q8_0 ? 34 : type == T_Q4_K ? 144 : 210;
+        const int bb = type == T_Q8_0 ? 34 : 210;
         uint8_t v = 0;
         if (row < rows && blk < nb) v = src[(m * rows + row) * row_bytes + (int64_t)blk * bb + byte];
         dst[o] = v;

@@ -1,5 +1,5 @@
-// fgh_matvec.hip - the decode matvec for Q4_K / Q6_K / Q8_0 on gfx950: one persistent kernel
-// per call that quantizes x itself and streams the weights.
+// fgh_matvec.hip - the decode matvec for Q6_K / Q8_0 on gfx950 (Q4_K has its own kernel in
+// fgh_q4k.hip): one persistent kernel per call that quantizes x itself and streams the weights.
 //
 //  * Quantization (once per workgroup and token): x (fp32, device) -> Q8_K or Q8 blocks in LDS,
 //    bit-exact with the reference's quantize_q8k / quantize_q8 (fastgguf.c:746-793). 16 lanes
@@ -25,9 +25,9 @@ constexpr int CT = 4 * CS;       // tiles per chunk
 // per (row, tile) record in wavefront LDS, in floats
 template <int TYPE, int ORDER>
 struct Rec {
-    // Q4_K repacked: {d*yd, sumi, dmin*yd, msum}; lanes orders: 8 lane partials, 4 min lanes,
-    // d*yd, dmin*yd (16 with padding); Q8_0: 4 blocks x 8 lane partials + 4 d*xd
-    static constexpr int N = TYPE == T_Q8_0 ? 36 : (TYPE == T_Q4_K && ORDER == 1) ? 4 : 16;
+    // Q6_K: 8 lane partials, 4 correction lanes, d*yd (16 with padding); Q8_0: 4 blocks x 8 lane
+    // partials + 4 d*xd
+    static constexpr int N = TYPE == T_Q8_0 ? 36 : 16;
 };
 
 // LDS activation region, each array 16-byte aligned: qs at 0, d at act_off_d, sums at act_off_s
@@ -144,7 +144,7 @@ __device__ void quantize_to_lds(const float *__restrict__ x, int nb, uint8_t *sm
 }
 
 // weights of one step for one lane: q = 16 quant bytes of its slice; m = the row's 16 meta bytes
-// (Q4_K: d, dmin, scales; Q6_K: int8 scales); h = Q6_K qh words, or the row's 4 fp16 d (Q8_0);
+// (Q6_K: int8 scales); h = Q6_K qh words, or the row's 4 fp16 d (Q8_0);
 // e = Q6_K fp16 d of the row
 struct StepW {
     uint4 q, m;
@@ -154,12 +154,9 @@ struct StepW {
 
 template <int TYPE>
 __device__ __forceinline__ void load_step(const uint8_t *__restrict__ Wg, int tile, int slice, int r, StepW &s) {
-    constexpr int TILE = TYPE == T_Q4_K ? Q4K_TILE : TYPE == T_Q6_K ? Q6K_TILE : Q80_TILE;
+    constexpr int TILE = TYPE == T_Q6_K ? Q6K_TILE : Q80_TILE;
     const uint8_t *t = Wg + (size_t)tile * TILE;
-    if (TYPE == T_Q4_K) {
-        s.q = ld16(t + 128 + 16 * slice);
-        s.m = ld16(t + 16 * r);
-    } else if (TYPE == T_Q6_K) {
+    if (TYPE == T_Q6_K) {
         s.q = ld16(t + 144 + 16 * slice);
         s.h = ld8(t + 1168 + 8 * slice);
         s.m = ld16(t + 16 * r);
@@ -174,7 +171,7 @@ template <int TYPE, int ORDER, bool DUMP>
 __global__ __launch_bounds__(256) void mv_kernel(MvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int RN = Rec<TYPE, ORDER>::N;
-    constexpr int TILE = TYPE == T_Q4_K ? Q4K_TILE : TYPE == T_Q6_K ? Q6K_TILE : Q80_TILE;
+    constexpr int TILE = TYPE == T_Q6_K ? Q6K_TILE : Q80_TILE;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int slot = lane >> 4, r2 = (lane >> 3) & 1, i = lane & 7;
     const int r = 2 * wave + r2;  // row within the 8-row group
@@ -220,7 +217,7 @@ __global__ __launch_bounds__(256) void mv_kernel(MvArgs a) {
     const float *ad = (const float *)(act + act_off_d(TYPE, nb));
     const int16_t *abs16 = (const int16_t *)(act + act_off_s(TYPE, nb));
 
-    // chain state: Q4_K repacked uses lanes 0 and 8 (r2 = 0, 1); the others lanes 0..15 (r2, i)
+    // chain state: lanes 0..15 (r2, i)
     float acc = 0.0f, macc = 0.0f;
 
     auto process = [&](int64_t it, const StepW (&cur)[CS]) {
@@ -238,59 +235,7 @@ __global__ __launch_bounds__(256) void mv_kernel(MvArgs a) {
             const int tile = c * CT + 4 * k + slot;
             const int tl = 4 * k + slot;  // tile within the chunk
             float *rec = wrec + ((size_t)r2 * CT + tl) * RN;
-            if (TYPE == T_Q4_K) {
-                if (c * CT + 4 * k < ntile) {  // the wavefront has at least one live slot
-                    const bool live = tile < ntile;
-                    const int b = live ? tile : 0;
-                    const uint4 yv0 = *(const uint4 *)(aqs + (size_t)b * 256 + 32 * i);
-                    const uint4 yv1 = *(const uint4 *)(aqs + (size_t)b * 256 + 32 * i + 16);
-                    const int yv[8] = {(int)yv0.x, (int)yv0.y, (int)yv0.z, (int)yv0.w,
-                                       (int)yv1.x, (int)yv1.y, (int)yv1.z, (int)yv1.w};
-                    const StepW &s = cur[k];
-                    const Q4KScales sc = q4k_scales(s.m.y, s.m.z, s.m.w);
-                    const uint32_t qw[4] = {s.q.x, s.q.y, s.q.z, s.q.w};
-                    int sum = 0;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int lo = (int)(qw[j] & 0x0F0F0F0Fu), hi = (int)((qw[j] >> 4) & 0x0F0F0F0Fu);
-                        sum += q4k_sc(sc, 2 * j) * dot4(lo, yv[2 * j], 0) + q4k_sc(sc, 2 * j + 1) * dot4(hi, yv[2 * j + 1], 0);
-                    }
-                    const float yd = ad[b];
-                    const float fd = fp16_bits_to_f32(s.m.x & 0xFFFF) * yd, fdm = fp16_bits_to_f32(s.m.x >> 16) * yd;
-                    if (ORDER == 1) {
-                        const uint32_t bp = *(const uint32_t *)(abs16 + 16 * b + 2 * i);
-                        const int bs2 = (int)(int16_t)(bp & 0xFFFF) + (int)(int16_t)(bp >> 16);
-                        const int mterm = ubyte(i < 4 ? sc.mn_lo : sc.mn_hi, i & 3) * bs2;
-                        const int sumi = sum8_i32(sum), msum = sum8_i32(mterm);
-                        if (live && i == 0) {
-                            *(float4 *)rec = make_float4(fd, (float)sumi, fdm, (float)msum);
-                            if (DUMP && row_ok) {
-                                a.dump_s[orow * nb + b] = sumi;
-                                a.dump_m[orow * nb + b] = msum;
-                            }
-                        }
-                    } else {
-                        const int p = i & 3;
-                        const uint2 bq = *(const uint2 *)(abs16 + 16 * b + 4 * p);
-                        const int bs_lo = (int)(int16_t)(bq.x & 0xFFFF) + (int)(int16_t)(bq.x >> 16);
-                        const int bs_hi = (int)(int16_t)(bq.y & 0xFFFF) + (int)(int16_t)(bq.y >> 16);
-                        const uint32_t mw = p < 2 ? sc.mn_lo : sc.mn_hi;
-                        const int mterm = ubyte(mw, 2 * (p & 1)) * bs_lo + ubyte(mw, 2 * (p & 1) + 1) * bs_hi;
-                        if (live) {
-                            rec[i] = (float)sum;
-                            if (i < 4) rec[8 + i] = (float)mterm;
-                            if (i == 0) { rec[12] = fd; rec[13] = fdm; }
-                        }
-                        if (DUMP) {
-                            const int ts = sum8_i32(sum), tm = sum4_i32(mterm);
-                            if (live && i == 0 && row_ok) {
-                                a.dump_s[orow * nb + b] = ts;
-                                a.dump_m[orow * nb + b] = tm;
-                            }
-                        }
-                    }
-                }
-            } else if (TYPE == T_Q6_K) {
+            if (TYPE == T_Q6_K) {
                 if (c * CT + 4 * k < ntile) {
                     const bool live = tile < ntile;
                     const int b = live ? tile : 0;
@@ -373,23 +318,7 @@ __global__ __launch_bounds__(256) void mv_kernel(MvArgs a) {
         // ---- chain phase: ascending tiles of this chunk ----
         const int nct = min(CT, ntile - c * CT);
         // (all reads first, then the ordered fused multiply-adds; records past nct are skipped)
-        if (TYPE == T_Q4_K && ORDER == 1) {
-            if (slot == 0 && i == 0) {
-                const float *rec = wrec + (size_t)r2 * CT * RN;
-#pragma unroll
-                for (int t0 = 0; t0 < CT; t0 += 4) {
-                    float4 p[4];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) p[u] = *(const float4 *)(rec + (t0 + u) * RN);
-#pragma unroll
-                    for (int u = 0; u < 4; ++u)
-                        if (t0 + u < nct) {
-                            acc = __builtin_fmaf(p[u].x, p[u].y, acc);
-                            macc = __builtin_fmaf(p[u].z, p[u].w, macc);
-                        }
-                }
-            }
-        } else if (TYPE == T_Q8_0) {
+        if (TYPE == T_Q8_0) {
             if (slot == 0) {
                 const float *rec = wrec + (size_t)r2 * CT * RN;
                 const int nblk = min(4 * nct, nb - 4 * c * CT);
@@ -435,24 +364,20 @@ __global__ __launch_bounds__(256) void mv_kernel(MvArgs a) {
         // ---- end of a group: combine the lanes in the reference's order and store ----
         if (c == nchunk - 1) {
             float *y = a.t[ti].y + (size_t)tok * a.ldy;
-            if (TYPE == T_Q4_K && ORDER == 1) {
-                if (slot == 0 && i == 0 && row_ok) y[orow] = acc - macc;
-            } else {
-                if (slot == 0) {
-                    wfin[12 * r2 + i] = acc;
-                    if (i < 4) wfin[12 * r2 + 8 + i] = macc;
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                if (slot == 0 && i == 0 && row_ok) {
-                    const float *v = wfin + 12 * r2;
-                    const float h8 = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
-                    y[orow] = TYPE == T_Q8_0 ? h8 : h8 - ((v[8] + v[9]) + (v[10] + v[11]));
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
+            if (slot == 0) {
+                wfin[12 * r2 + i] = acc;
+                if (i < 4) wfin[12 * r2 + 8 + i] = macc;
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (slot == 0 && i == 0 && row_ok) {
+                const float *v = wfin + 12 * r2;
+                const float h8 = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+                y[orow] = TYPE == T_Q8_0 ? h8 : h8 - ((v[8] + v[9]) + (v[10] + v[11]));
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
             acc = 0.0f;
             macc = 0.0f;
         }
@@ -484,7 +409,7 @@ size_t matvec_lds_bytes(int type, int order, int nb) {
 // this LDS size), balanced so that every workgroup gets the same number of row groups (+-1)
 template <int TYPE, int ORDER, bool DUMP>
 static hipError_t launch_t(const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
-    const size_t lds = matvec_lds_bytes(TYPE == T_Q4_K ? T_Q4_K : TYPE, ORDER, a.nb);
+    const size_t lds = matvec_lds_bytes(TYPE, ORDER, a.nb);
     if (lds > 65536) return hipErrorInvalidValue;
     int per_cu = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_kernel<TYPE, ORDER, DUMP>, 256, lds);

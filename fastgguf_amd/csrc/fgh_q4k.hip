@@ -1,57 +1,44 @@
-// fgh_q4k.hip - Q4_K decode matvec for gfx950 (the dominant kernel of a Q4_K_M decode layer).
+// fgh_q4k.hip - Q4_K decode matvec for gfx950 (the dominant kernel of a Q4_K_M decode layer), the
+// MoE expert kernel over the same layout, and the layout's upload transform.
 //
-// Device layout of a Q4_K tensor (written at upload by q4k_relayout_kernel): rows in groups of
-// 8, each group 1152 * nb bytes (the same bytes as the file: 8 rows x nb blocks x 144 B).
-// Wavefront w of a group's workgroup owns rows 2w and 2w+1; its P = 2 * nb (row, block) "pairs"
-// are numbered q = r2 * nb + b. Inside the group:
-//   meta   [0, 128 nb):        pair q of wavefront w at 16 * (P * w + q): the block's first 16
-//                              bytes (fp16 d, fp16 dmin, 12 bytes of 6-bit scales and mins)
-//   quants [128 nb, 1152 nb):  wavefront w at + 256 nb * w, in steps of 16 pairs (2 KB each);
-//                              lane L = 4 * (q % 16) + j holds chunk j (32 bytes = sub-blocks 2j
-//                              and 2j+1) of pair q as two 16-byte pieces: piece h at
-//                              + 2048 * step + h * 64 * np + 16 * L (np = pairs in the step)
-// so every load instruction of a wavefront reads one contiguous span and the layout is dense
-// for any nb.
+// Device layout of a Q4_K tensor (written at upload by q4k_relayout_kernel): rows in tiles of 16
+// per matrix (tpm = ceil(rows / 16) tiles, the last one zero-padded). Tile t of matrix m, block b,
+// is 2304 bytes (the file's 16 x 144 bytes, rearranged) at ((m * tpm + t) * nb + b) * 2304:
+//   [0, 256)     meta: row r at 16 r, the block's first 16 bytes (fp16 d, fp16 dmin, 12 bytes of
+//                6-bit scales and mins)
+//   [256, 2304)  quants: slot (h, L) at 256 + 1024 h + 16 L, L = 4 r + j, holds 16-byte piece
+//                h ^ (j >> 1) of chunk j of row r (block bytes 16 + 32 j + 16 (h ^ (j >> 1)) ...)
+// Lane L = 4 r + j of a wavefront owns chunk j of row r (32 bytes: sub-block 2j in the low nibbles,
+// 2j + 1 in the high nibbles): one step of a wavefront is one block of 16 rows, three 16-byte loads
+// per lane (1 KB contiguous per quant load, 256 B for the meta). Lanes j >= 2 receive the second
+// half of their chunk first and read their activation halves swapped the same way, so register k
+// of the lane holds the reference's AVX2 lane k (j < 2) or lane 4 + k (j >= 2) of the block: the
+// row-order reduction below needs no lane-dependent selects for that half.
 //
-// One workgroup per 8-row group (grid.y = token). It issues the loads of x (to quantize it) and
-// then every weight load of its group, quantizes x into LDS (Q8_K, bit-exact with quantize_q8k,
-// fastgguf.c:773-793) while the weights are in flight, and then computes: each lane the exact
-// integer dot products of its chunk (v_dot4_i32_i8), a quad reduction per (row, block), fp32
-// records in wavefront LDS, and the reference's fused multiply-add chain in block order by one
-// lane per row:
+// Decode (q4k_mv_kernel): every workgroup quantizes x into LDS (Q8_K, bit-exact with
+// quantize_q8k, fastgguf.c:773-793) while its first weight steps are in flight. A wavefront walks
+// the blocks of its 16-row tile through a ring of R steps in registers; the activations of a step
+// are LDS broadcasts (the 4 chunks of one block: no bank conflicts). Per (row, block) the exact
+// integers come from v_dot4_i32_i8 and a quad reduction; the fp32 chain runs in registers in block
+// order:
 //   repacked order, dot_q4Kx8 (fastgguf.c:2322-2358): acc = fma(d*yd, sumi, acc),
 //                   macc = fma(dmin*yd, msum, macc), out = acc - macc
-//   row order, dot_q4_K_q8k (fastgguf.c:1118-1153): 8 lane chains and 4 min chains, out =
-//                   hsum8(acc) - hsum4(macc)
+//   row order, dot_q4_K_q8k (fastgguf.c:1118-1153): lane j of a row carries the reference's lane
+//                   chains 2j, 2j+1 and min chain j; out = hsum8(acc) - hsum4(macc)
+// Short matrices split the blocks of a tile over S wavefronts (repacked order): each writes fp32
+// records {d*yd, sumi, dmin*yd, msum} to LDS and one wavefront runs the chain.
 #include "fgh_internal.h"
 
 namespace fgh {
 
-constexpr int Q4_MAXS = 8;  // steps (16 pairs each) of one wavefront held in registers at once
+constexpr int RB_ROWS = 16;     // rows per tile
+constexpr int RB_BYTES = 2304;  // one (tile, block): 16 x 144
 
-__device__ __forceinline__ float dpp_ror_f32(float v, int ctrl_n) {
-    const int iv = __builtin_bit_cast(int, v);
-    int r;
-    switch (ctrl_n) {
-    case 8: r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false); break;
-    case 4: r = __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false); break;
-    case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x122, 0xF, 0xF, false); break;
-    default: r = __builtin_amdgcn_update_dpp(0, iv, 0x121, 0xF, 0xF, false); break;
-    }
-    return __builtin_bit_cast(float, r);
-}
-
-// LDS: natural-order Q8_K blocks: qs [nb][256] at 0, d [nb] at 256 nb, bsums [nb][16] at
-// align16(260 nb); then 4 wavefront record areas
+// LDS activations: natural-order Q8_K blocks: qs [nb][256] at 0, d [nb] at 256 nb, bsums [nb][16]
+// at align16(260 nb)
 __host__ __device__ constexpr size_t q4_off_d(int nb) { return (size_t)nb * 256; }
 __host__ __device__ constexpr size_t q4_off_s(int nb) { return ((size_t)nb * 260 + 15) & ~(size_t)15; }
 __host__ __device__ constexpr size_t q4_act_bytes(int nb) { return (q4_off_s(nb) + (size_t)nb * 32 + 15) & ~(size_t)15; }
-template <int ORDER>
-__host__ __device__ constexpr size_t q4_rec_floats() { return ORDER == 1 ? 4 : 16; }
-__host__ __device__ inline size_t q4_wave_bytes(int order, int nb) {
-    return (size_t)2 * nb * (order == 1 ? 4 : 16) * 4 + 2 * 12 * 4;
-}
-size_t q4k_lds_bytes(int order, int nb, int gpw) { return q4_act_bytes(nb) + 4 * (size_t)gpw * q4_wave_bytes(order, nb); }
 
 // 16 threads per 256-value block; thread tl holds values 16tl..16tl+15 (4 float4 loads)
 struct XRound {
@@ -67,6 +54,21 @@ __device__ __forceinline__ void q8k_load(const float *__restrict__ x, int nb, in
     const int b = rb + (threadIdx.x >> 4);
     q8k_load_b(x, b, b < nb, xr);
 }
+
+__device__ __forceinline__ float dpp_ror_f32(float v, int ctrl_n) {
+    const int iv = __builtin_bit_cast(int, v);
+    int r;
+    switch (ctrl_n) {
+    case 8: r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false); break;
+    case 4: r = __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false); break;
+    case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x122, 0xF, 0xF, false); break;
+    default: r = __builtin_amdgcn_update_dpp(0, iv, 0x121, 0xF, 0xF, false); break;
+    }
+    return __builtin_bit_cast(float, r);
+}
+__device__ __forceinline__ float dppf_xor1(float v) { return __builtin_bit_cast(float, dpp_xor1(__builtin_bit_cast(int, v))); }
+__device__ __forceinline__ float dppf_xor2(float v) { return __builtin_bit_cast(float, dpp_xor2(__builtin_bit_cast(int, v))); }
+
 // quantizes the 16 threads' block b into act (stored only if live); the 16 threads of a block
 // are one DPP row, so a row is either wholly live or wholly not
 __device__ __forceinline__ void q8k_store_b(int nb, int b, bool live, const XRound &xr, uint8_t *act) {
@@ -105,175 +107,122 @@ __device__ __forceinline__ void q8k_store(int nb, int rb, const XRound &xr, uint
     q8k_store_b(nb, b, b < nb, xr, act);
 }
 
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+// Quantizes x (nb blocks) into act with all 64 * WPG threads: q8k_begin issues the loads of the
+// first two rounds (before the caller's weight loads), q8k_finish the rest and the stores.
+template <int WPG>
+struct XQuant {
+    static constexpr int XB = 4 * WPG;  // blocks per round
+    XRound r0, r1;
+};
+template <int WPG>
+__device__ __forceinline__ void q8k_begin(XQuant<WPG> &q, const float *x, int nb) {
+    q8k_load(x, nb, 0, q.r0);
+    if (nb > XQuant<WPG>::XB) q8k_load(x, nb, XQuant<WPG>::XB, q.r1);  // uniform
+}
+template <int WPG>
+__device__ __forceinline__ void q8k_finish(XQuant<WPG> &q, const float *x, int nb, uint8_t *act) {
+    constexpr int XB = XQuant<WPG>::XB;
+    q8k_store(nb, 0, q.r0, act);
+    if (nb > XB) q8k_store(nb, XB, q.r1, act);
+    for (int rb = 2 * XB; rb < nb; rb += XB) {  // rows longer than 2 * XB blocks
+        q8k_load(x, nb, rb, q.r0);
+        q8k_store(nb, rb, q.r0, act);
+    }
 }
 
-// one step's registers: two 16-byte pieces of the lane's chunk and the pair's 16 meta bytes
-struct Q4Step {
+// one step of a lane: two 16-byte pieces of its chunk (register order) and its row's meta
+struct RbW {
     uint4 p0, p1, m;
 };
+__device__ __forceinline__ void rb_load(const uint8_t *T, int lane, RbW &w) {
+    w.p0 = ld16(T + 256 + 16 * lane);
+    w.p1 = ld16(T + 1280 + 16 * lane);
+    w.m = ld16(T + 16 * (lane >> 2));
+}
 
-// what one wavefront needs to compute its steps: the quantized x and its record area (LDS)
-struct Q4Ctx {
-    const uint8_t *act;
-    const float *ad;
-    const int16_t *abs16;
-    float *rec;
-    int nb, P, j, pl;
+// What every order needs of one lane's chunk j of one block: its activations (register order),
+// the chunk's two sub-block scales as an int16 pair, the min partial of chunk j,
+// m_2j (bs_4j + bs_4j+1) + m_2j+1 (bs_4j+2 + bs_4j+3) (the reference's min lane p = j), and yd.
+struct RbIn {
+    uint32_t ylo[8], yhi[8];
+    uint32_t sc2;
+    int mt;
+    float yd;
 };
-
-// where the per-(row, block) integers of the test hook go: rows dbase + r2 if r2 < dleft
-struct Q4Dump {
-    int32_t *s, *m;
-    int64_t base;
-    int64_t left;
-};
-
-// One step (16 (row, block) pairs) of one wavefront from its registers: the exact integers of the
-// lane's chunk (v_dot4_i32_i8), reduced over the pair's 4 lanes, and the pair's fp32 record in LDS
-//   repacked: float4 {d*yd, sumi, dmin*yd, msum} at pair q
-//   row:      16 floats at pair q: the 8 lane partials (dword i = the reference's lane i), the 4
-//             min partials at 8 + j, d*yd at 12, dmin*yd at 13
-template <int ORDER, bool DUMP>
-__device__ __forceinline__ void q4_step(const Q4Step &st, int s, const Q4Ctx &c, const Q4Dump &dump) {
-    const int nb = c.nb, j = c.j, pl = c.pl;
-    const int np = min(16, c.P - 16 * s);
-    const bool live = pl < np;
-    const int q = 16 * s + min(pl, np - 1);
-    const int r2 = q >= nb, b = q - r2 * nb;
-    const uint8_t *yb = c.act + (size_t)b * 256 + 64 * j;
-    const uint4 ylo0 = *(const uint4 *)yb, ylo1 = *(const uint4 *)(yb + 16);
-    const uint4 yhi0 = *(const uint4 *)(yb + 32), yhi1 = *(const uint4 *)(yb + 48);
-    const uint32_t qd[8] = {st.p0.x, st.p0.y, st.p0.z, st.p0.w, st.p1.x, st.p1.y, st.p1.z, st.p1.w};
-    const uint32_t ylo[8] = {ylo0.x, ylo0.y, ylo0.z, ylo0.w, ylo1.x, ylo1.y, ylo1.z, ylo1.w};
-    const uint32_t yhi[8] = {yhi0.x, yhi0.y, yhi0.z, yhi0.w, yhi1.x, yhi1.y, yhi1.z, yhi1.w};
-    // scales and mins of sub-blocks 2j (low nibbles) and 2j+1 (high nibbles) of this chunk,
-    // straight from the packed words u0..u2 (scale_min_k4, fastgguf.c:466-472): for j < 2 the low
-    // 6 bits of bytes 2j, 2j+1 of u0 (scales) and u1 (mins); for j >= 2 the nibbles of bytes
-    // 2j-4, 2j-3 of u2 with the top 2 bits of the same bytes of u0 / u1
+__device__ __forceinline__ void rb_in(const RbW &w, const uint8_t *act, int nb, int b, int j, RbIn &in) {
+    const int hs = 16 * (j >> 1);  // lanes j >= 2: second half first
+    const uint8_t *yb = act + (size_t)b * 256 + 64 * j;
+    const uint4 l0 = *(const uint4 *)(yb + hs), l1 = *(const uint4 *)(yb + 16 - hs);
+    const uint4 h0 = *(const uint4 *)(yb + 32 + hs), h1 = *(const uint4 *)(yb + 48 - hs);
+    in.ylo[0] = l0.x; in.ylo[1] = l0.y; in.ylo[2] = l0.z; in.ylo[3] = l0.w;
+    in.ylo[4] = l1.x; in.ylo[5] = l1.y; in.ylo[6] = l1.z; in.ylo[7] = l1.w;
+    in.yhi[0] = h0.x; in.yhi[1] = h0.y; in.yhi[2] = h0.z; in.yhi[3] = h0.w;
+    in.yhi[4] = h1.x; in.yhi[5] = h1.y; in.yhi[6] = h1.z; in.yhi[7] = h1.w;
+    // scales and mins of sub-blocks 2j (low nibbles) and 2j+1 (high nibbles) straight from the
+    // packed words u0..u2 (scale_min_k4, fastgguf.c:466-472): for j < 2 the low 6 bits of bytes 2j,
+    // 2j+1 of u0 (scales) and u1 (mins); for j >= 2 the nibbles of bytes 2j-4, 2j-3 of u2 with the
+    // top 2 bits of the same bytes of u0 / u1
     const int sh = 16 * (j & 1);
-    const uint32_t A = st.m.y >> sh, B = st.m.z >> sh, C = st.m.w >> sh;
+    const uint32_t A = w.m.y >> sh, B = w.m.z >> sh, C = w.m.w >> sh;
     const uint32_t scp = j < 2 ? (A & 0x3f3fu) : ((C & 0x0f0fu) | ((A & 0xc0c0u) >> 2));
     const uint32_t mnp = j < 2 ? (B & 0x3f3fu) : (((C >> 4) & 0x0f0fu) | ((B & 0xc0c0u) >> 2));
-    // (s_lo, s_hi) as an int16 pair for the packed dots below; m_lo, m_hi as bytes
-    const uint32_t sc2 = __builtin_amdgcn_perm(0u, scp, 0x0C010C00u);
-    const int m_lo = (int)(mnp & 0x3F), m_hi = (int)((mnp >> 8) & 0x3F);
-    // min term m_2j (bs[4j] + bs[4j+1]) + m_2j+1 (bs[4j+2] + bs[4j+3]): two packed int16 dots on
-    // the activation sums as stored (all values fit int16)
-    const uint2 bq = *(const uint2 *)(c.abs16 + 16 * b + 4 * j);
-    const int mterm = dot2_i16((uint32_t)m_lo | ((uint32_t)m_lo << 16), bq.x,
-                               dot2_i16((uint32_t)m_hi | ((uint32_t)m_hi << 16), bq.y, 0));
-    const float yd = c.ad[b];
-    const float fd = fp16_bits_to_f32(st.m.x & 0xFFFF) * yd;
-    const float fdm = fp16_bits_to_f32(st.m.x >> 16) * yd;
-    if (ORDER == 1) {
-        // integer dots of the low / high nibbles in two halves of 16 values each: every partial is
-        // at most 16 * 15 * 127 = 30480 in magnitude, so fits int16, and the scale products are
-        // two packed int16 dots
-        int il0 = 0, il1 = 0, ih0 = 0, ih1 = 0;
+    in.sc2 = __builtin_amdgcn_perm(0u, scp, 0x0C010C00u);
+    const uint32_t m_lo = mnp & 0x3Fu, m_hi = (mnp >> 8) & 0x3Fu;
+    const uint2 bq = *(const uint2 *)((const int16_t *)(act + q4_off_s(nb)) + 16 * b + 4 * j);
+    in.mt = dot2_i16(m_lo | (m_lo << 16), bq.x, dot2_i16(m_hi | (m_hi << 16), bq.y, 0));
+    in.yd = ((const float *)(act + q4_off_d(nb)))[b];
+}
+__device__ __forceinline__ uint32_t nib_lo(uint32_t q) { return q & 0x0F0F0F0Fu; }
+__device__ __forceinline__ uint32_t nib_hi(uint32_t q) { return (q >> 4) & 0x0F0F0F0Fu; }
+
+// the chunk's share of the block's sumi (sum_g sc_g sum q y over its two sub-blocks): the dots of
+// 16 values each fit int16 (|.| <= 16 * 15 * 127), so the scale products are two packed dots
+__device__ __forceinline__ int rb_sumi_part(const RbW &w, const RbIn &in) {
+    const uint32_t qd[8] = {w.p0.x, w.p0.y, w.p0.z, w.p0.w, w.p1.x, w.p1.y, w.p1.z, w.p1.w};
+    int il0 = 0, il1 = 0, ih0 = 0, ih1 = 0;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            il0 = dot4((int)(qd[d] & 0x0F0F0F0Fu), (int)ylo[d], il0);
-            ih0 = dot4((int)((qd[d] >> 4) & 0x0F0F0F0Fu), (int)yhi[d], ih0);
-            il1 = dot4((int)(qd[d + 4] & 0x0F0F0F0Fu), (int)ylo[d + 4], il1);
-            ih1 = dot4((int)((qd[d + 4] >> 4) & 0x0F0F0F0Fu), (int)yhi[d + 4], ih1);
-        }
-        const int sumi = sum4_i32(dot2_i16(sc2, pack_i16(il0, ih0), dot2_i16(sc2, pack_i16(il1, ih1), 0)));
-        const int msum = sum4_i32(mterm);
-        if (live && j == 0) {
-            *(float4 *)(c.rec + 4 * q) = make_float4(fd, (float)sumi, fdm, (float)msum);
-            if (DUMP && r2 < dump.left) {
-                dump.s[(dump.base + r2) * nb + b] = sumi;
-                dump.m[(dump.base + r2) * nb + b] = msum;
-            }
-        }
-    } else {
-        // the reference's lane i sums bytes 4i..4i+3 of every chunk: dword i here
-        int lv[8];
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            // each dot4 is at most 4 * 15 * 127 = 7620 in magnitude: an int16 pair
-            lv[d] = dot2_i16(sc2, pack_i16(dot4((int)(qd[d] & 0x0F0F0F0Fu), (int)ylo[d], 0),
-                                           dot4((int)((qd[d] >> 4) & 0x0F0F0F0Fu), (int)yhi[d], 0)), 0);
-            lv[d] = sum4_i32(lv[d]);
-        }
-        float *rq = c.rec + 16 * q;
-        if (live) {
-            rq[8 + j] = (float)mterm;  // min lane p = j
-            if (j == 0) {
-#pragma unroll
-                for (int d = 0; d < 8; ++d) rq[d] = (float)lv[d];
-                rq[12] = fd;
-                rq[13] = fdm;
-            }
-        }
-        if (DUMP) {
-            int ts = 0;
-#pragma unroll
-            for (int d = 0; d < 8; ++d) ts += lv[d];
-            const int tm = sum4_i32(mterm);
-            if (live && j == 0 && r2 < dump.left) {
-                dump.s[(dump.base + r2) * nb + b] = ts;
-                dump.m[(dump.base + r2) * nb + b] = tm;
-            }
-        }
+    for (int d = 0; d < 4; ++d) {
+        il0 = dot4((int)nib_lo(qd[d]), (int)in.ylo[d], il0);
+        ih0 = dot4((int)nib_hi(qd[d]), (int)in.yhi[d], ih0);
+        il1 = dot4((int)nib_lo(qd[d + 4]), (int)in.ylo[d + 4], il1);
+        ih1 = dot4((int)nib_hi(qd[d + 4]), (int)in.yhi[d + 4], ih1);
     }
+    return dot2_i16(in.sc2, pack_i16(il0, ih0), dot2_i16(in.sc2, pack_i16(il1, ih1), 0));
 }
 
-// The reference's fp32 chain over the wavefront's records, in ascending block order, and its
-// final combination; rows ybase[0], ybase[1] (if r2 < left). Call after a wave_sync.
-template <int ORDER>
-__device__ __forceinline__ void q4_chain(const Q4Ctx &c, int lane, float *__restrict__ ybase, int64_t left) {
-    const int nb = c.nb;
-    if (ORDER == 1) {
-        if (lane < 2) {
-            const float *rr = c.rec + 4 * (size_t)lane * nb;
-            float acc = 0.0f, macc = 0.0f;
-            int b = 0;
-            for (; b + 4 <= nb; b += 4) {
-                float4 p[4];
+// Row order: the reference's lane partials 2j and 2j+1 of the block (each summed over the row's
+// four chunks), for lane j. Register k of a lane holds lane k (j < 2) or 4 + k (j >= 2) of its
+// chunk: one exchange with lane j ^ 2 leaves lanes 0..3 (j < 2) or 4..7 summed over two chunks,
+// one exchange with lane j ^ 1 the lane's own pair summed over all four.
+__device__ __forceinline__ void rb_row_lanes(const RbW &w, const RbIn &in, int j, int &u0, int &u1) {
+    const uint32_t qd[8] = {w.p0.x, w.p0.y, w.p0.z, w.p0.w, w.p1.x, w.p1.y, w.p1.z, w.p1.w};
+    int lv[8];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) p[u] = *(const float4 *)(rr + 4 * (b + u));
+    for (int d = 0; d < 8; ++d)  // each dot4 is at most 4 * 15 * 127 = 7620 in magnitude: an int16 pair
+        lv[d] = dot2_i16(in.sc2, pack_i16(dot4((int)nib_lo(qd[d]), (int)in.ylo[d], 0),
+                                          dot4((int)nib_hi(qd[d]), (int)in.yhi[d], 0)), 0);
+    int t[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    acc = __builtin_fmaf(p[u].x, p[u].y, acc);
-                    macc = __builtin_fmaf(p[u].z, p[u].w, macc);
-                }
-            }
-            for (; b < nb; ++b) {
-                const float4 p = *(const float4 *)(rr + 4 * b);
-                acc = __builtin_fmaf(p.x, p.y, acc);
-                macc = __builtin_fmaf(p.z, p.w, macc);
-            }
-            if (lane < left) ybase[lane] = acc - macc;
-        }
-    } else {
-        float *fin = c.rec + (size_t)2 * nb * 16;
-        if (lane < 16) {
-            const int r2 = lane >> 3, i = lane & 7;
-            const float *rr = c.rec + 16 * (size_t)r2 * nb;
-            float acc = 0.0f, macc = 0.0f;
-            for (int b = 0; b < nb; ++b) {
-                const float *p = rr + 16 * b;
-                acc = __builtin_fmaf(p[12], p[i], acc);
-                macc = __builtin_fmaf(p[13], p[8 + (i & 3)], macc);
-            }
-            fin[12 * r2 + i] = acc;
-            if (i < 4) fin[12 * r2 + 8 + i] = macc;
-        }
-        wave_sync();
-        if (lane < 2 && lane < left) {
-            const float *v = fin + 12 * lane;
-            const float h8 = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
-            ybase[lane] = h8 - ((v[8] + v[9]) + (v[10] + v[11]));
-        }
-    }
+    for (int k = 0; k < 4; ++k) t[k] = lv[k] + dpp_xor2(lv[4 + k]);
+    const bool odd = (j & 1) != 0;
+    const int k0 = odd ? t[2] : t[0], k1 = odd ? t[3] : t[1];
+    const int s0 = odd ? t[0] : t[2], s1 = odd ? t[1] : t[3];
+    u0 = k0 + dpp_xor1(s0);
+    u1 = k1 + dpp_xor1(s1);
 }
 
-// the tensor of global group g in a multi-tensor launch
+// Row order's final combination over the row's four lanes (lane j holds chains 2j, 2j+1 and min
+// chain j): hsum8(acc) - hsum4(macc), fastgguf.c:797-806 and 1089-1095; valid in lane j == 0
+__device__ __forceinline__ float rb_row_final(float acc_a, float acc_b, float macc) {
+    const float ea = acc_a + dppf_xor2(acc_a), eb = acc_b + dppf_xor2(acc_b);  // (v0+v4), (v1+v5) | (v2+v6), (v3+v7)
+    const float f = ea + eb;
+    const float h8 = f + dppf_xor1(f);
+    const float g = macc + dppf_xor1(macc);  // (m0+m1) | (m2+m3)
+    const float h4 = g + dppf_xor2(g);
+    return h8 - h4;
+}
+
+// the tensor of global tile g in a multi-tensor launch
 __device__ __forceinline__ int q4_tensor_of(const MvArgs &a, int64_t g) {
     int ti = 0;
 #pragma unroll
@@ -282,124 +231,154 @@ __device__ __forceinline__ int q4_tensor_of(const MvArgs &a, int64_t g) {
     return ti;
 }
 
-template <int ORDER, int MAXS, int GPW, bool DUMP>
-__global__ __launch_bounds__(256 * GPW) void q4k_mv_kernel(MvArgs a) {
+// Decode matvec. Workgroup = TPW tiles x S wavefronts per tile (wavefront ks of a tile takes its
+// ks-th run of ceil(nb / S) blocks); grid = (tiles over all tensors / TPW, tokens).
+template <int ORDER, int R, int TPW, int S, bool DUMP>
+__global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
+    static_assert(ORDER == 1 || S == 1, "the row order keeps its chains in registers: no block split");
+    constexpr int WPG = TPW * S;
     extern __shared__ __align__(16) uint8_t smem[];
-    // wave-uniform indices in scalar registers: the tensor selection below then reads the kernel
-    // arguments with scalar loads instead of per-lane memory loads ahead of the weight stream
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
-    const int gsub = __builtin_amdgcn_readfirstlane(tid >> 8);
-    const int j = lane & 3, pl = lane >> 2;  // chunk, pair within the step
-    const int nb = a.nb, P = 2 * nb;
-    const int nsteps = (P + 15) >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ts = wave / S, ks = wave - ts * S;
+    const int j = lane & 3, rr = lane >> 2;
+    const int nb = a.nb;
     const int tok = blockIdx.y;
-    const int64_t g = (int64_t)blockIdx.x * GPW + gsub;
-    if (g >= a.groups) {  // a trailing workgroup's spare group: only help quantize
-        const float *xs = a.x + (size_t)(blockIdx.y / a.xdiv) * a.ldx;
-        for (int rb = 0; rb < nb; rb += 16 * GPW) {
-            XRound xr;
-            q8k_load(xs, nb, rb, xr);
-            q8k_store(nb, rb, xr, smem);
-        }
-        __syncthreads();
-        return;
-    }
-    const int ti = q4_tensor_of(a, g);
-    const int64_t lg = g - a.t[ti].gfirst;
-    const int64_t mg = a.sel ? (int64_t)a.sel[tok] * a.t[ti].gpm : 0;  // selected matrix (MoE)
-    const uint8_t *G = a.t[ti].W + (size_t)(mg + lg) * 1152 * nb;
-    const uint8_t *meta = G + (size_t)16 * P * wave;
-    const uint8_t *quant = G + (size_t)128 * nb + (size_t)256 * nb * wave;
+    const int64_t tile = (int64_t)blockIdx.x * TPW + ts;
+    const bool live = tile < a.groups;
+    const int64_t tc = live ? tile : a.groups - 1;
+    const int ti = q4_tensor_of(a, tc);
+    const uint32_t lt = (uint32_t)(tc - a.t[ti].gfirst), gpm = (uint32_t)a.t[ti].gpm;
+    const int64_t mg = a.sel ? (int64_t)a.sel[tok] * gpm : 0;  // selected matrix (MoE)
+    const int nbw = (nb + S - 1) / S, bb0 = ks * nbw;
+    const int nbl = max(0, min(nb, bb0 + nbw) - bb0), bl = max(nbl - 1, 0);
+    const uint8_t *T0 = a.t[ti].W + ((size_t)(mg + lt) * nb + min(bb0, nb - 1)) * RB_BYTES;
 
-    uint8_t *act = smem;
-    Q4Ctx c;
-    c.act = act;
-    c.ad = (const float *)(act + q4_off_d(nb));
-    c.abs16 = (const int16_t *)(act + q4_off_s(nb));
-    c.rec = (float *)(smem + q4_act_bytes(nb) + (size_t)(4 * gsub + wave) * q4_wave_bytes(ORDER, nb));
-    c.nb = nb;
-    c.P = P;
-    c.j = j;
-    c.pl = pl;
-    const int64_t lr0 = (lg % a.t[ti].gpm) * 8 + 2 * wave;
-    const int64_t obase = (lg / a.t[ti].gpm) * a.t[ti].rows;
-    Q4Dump dump{a.dump_s, a.dump_m, obase + lr0, a.t[ti].rows - lr0};
-
-    // (1) x for the first quantization round, then (2) every weight load of the first chunk
+    // (1) x for the first quantization rounds, then (2) the ring's first R steps
     const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
-    XRound xr;
-    q8k_load(x, nb, 0, xr);
-    Q4Step st[MAXS];
-    auto load_steps = [&](int s0) {
+    XQuant<WPG> xq;
+    q8k_begin(xq, x, nb);
+    RbW ring[R];
 #pragma unroll
-        for (int k = 0; k < MAXS; ++k) {
-            const int s = s0 + k;
-            if (s < nsteps) {  // uniform
-                const int np = min(16, P - 16 * s);
-                const int pc = min(pl, np - 1);  // lanes past the last pair re-read a live one
-                const uint8_t *qb = quant + (size_t)2048 * s + 16 * (4 * pc + j);
-                st[k].p0 = ld16(qb);
-                st[k].p1 = ld16(qb + 64 * np);
-                st[k].m = ld16(meta + 16 * (16 * s + pc));
-            }
-        }
-    };
-    load_steps(0);
-    // (3) quantize x into LDS while the weights are in flight (16 * GPW blocks per round)
-    for (int rb = 0; rb < nb; rb += 16 * GPW) {
-        if (rb > 0) q8k_load(x, nb, rb, xr);
-        q8k_store(nb, rb, xr, act);
-    }
+    for (int r = 0; r < R; ++r) rb_load(T0 + (size_t)min(r, bl) * RB_BYTES, lane, ring[r]);
+    // (3) quantize x into LDS while the weights are in flight
+    uint8_t *act = smem;
+    q8k_finish(xq, x, nb, act);
     __syncthreads();
 
-    for (int s0 = 0; s0 < nsteps; s0 += MAXS) {
-        if (s0 > 0) load_steps(s0);
+    const int64_t mrow = (int64_t)(lt % gpm) * RB_ROWS;  // first row of the tile in its matrix
+    const int64_t obase = (int64_t)(lt / gpm) * a.t[ti].rows;
+    const int64_t rows = a.t[ti].rows;
+    float4 *rec = (float4 *)(smem + q4_act_bytes(nb)) + (size_t)ts * RB_ROWS * nb;  // [b][row], S > 1
+    float acc = 0.0f, acc2 = 0.0f, macc = 0.0f;
+    for (int b0 = 0; b0 < nbl; b0 += R) {
 #pragma unroll
-        for (int k = 0; k < MAXS; ++k) {
-            const int s = s0 + k;
-            if (s >= nsteps) break;  // uniform
-            q4_step<ORDER, DUMP>(st[k], s, c, dump);
+        for (int r = 0; r < R; ++r) {
+            const int bi = b0 + r, b = bb0 + bi;
+            if (bi < nbl) {  // uniform
+                RbIn in;
+                rb_in(ring[r], act, nb, b, j, in);
+                const float fd = fp16_bits_to_f32(ring[r].m.x & 0xFFFF) * in.yd;
+                const float fdm = fp16_bits_to_f32(ring[r].m.x >> 16) * in.yd;
+                int sumi = 0, msum = 0;
+                if (ORDER == 1 || DUMP) {
+                    sumi = sum4_i32(rb_sumi_part(ring[r], in));
+                    msum = sum4_i32(in.mt);
+                }
+                if (ORDER == 1) {
+                    if (S == 1) {
+                        acc = __builtin_fmaf(fd, (float)sumi, acc);
+                        macc = __builtin_fmaf(fdm, (float)msum, macc);
+                    } else if (j == 0) {
+                        rec[(size_t)b * RB_ROWS + rr] = make_float4(fd, (float)sumi, fdm, (float)msum);
+                    }
+                } else {
+                    int u0, u1;
+                    rb_row_lanes(ring[r], in, j, u0, u1);
+                    acc = __builtin_fmaf(fd, (float)u0, acc);
+                    acc2 = __builtin_fmaf(fd, (float)u1, acc2);
+                    macc = __builtin_fmaf(fdm, (float)in.mt, macc);
+                }
+                if (DUMP && live && j == 0 && mrow + rr < rows) {
+                    const size_t di = (size_t)(obase + mrow + rr) * nb + b;
+                    a.dump_s[di] = sumi;
+                    a.dump_m[di] = msum;
+                }
+            }
+            rb_load(T0 + (size_t)min(bi + R, bl) * RB_BYTES, lane, ring[r]);
         }
     }
-    wave_sync();
-    q4_chain<ORDER>(c, lane, a.t[ti].y + (size_t)tok * a.ldy + obase + lr0, a.t[ti].rows - lr0);
+    float *y = a.t[ti].y + (size_t)tok * a.ldy + obase + mrow;
+    if (S > 1) {
+        __syncthreads();
+        if (ks == 0 && lane < RB_ROWS) {
+            const float4 *rr4 = rec + lane;
+            int b = 0;
+            for (; b + 4 <= nb; b += 4) {
+                float4 p[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) p[u] = rr4[(size_t)(b + u) * RB_ROWS];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    acc = __builtin_fmaf(p[u].x, p[u].y, acc);
+                    macc = __builtin_fmaf(p[u].z, p[u].w, macc);
+                }
+            }
+            for (; b < nb; ++b) {
+                const float4 p = rr4[(size_t)b * RB_ROWS];
+                acc = __builtin_fmaf(p.x, p.y, acc);
+                macc = __builtin_fmaf(p.z, p.w, macc);
+            }
+            if (live && mrow + lane < rows) y[lane] = acc - macc;
+        }
+    } else if (ORDER == 1) {
+        if (live && j == 0 && mrow + rr < rows) y[rr] = acc - macc;
+    } else {
+        const float out = rb_row_final(acc, acc2, macc);
+        if (live && j == 0 && mrow + rr < rows) y[rr] = out;
+    }
 }
 
-#ifndef FGH_Q4_GPW
-#define FGH_Q4_GPW 2
-#endif
-constexpr int Q4_GPW = FGH_Q4_GPW;  // 8-row groups per workgroup (sharing one quantization of x)
+constexpr int Q4_R = 4;  // ring depth (steps in flight per wavefront)
 
-// groups per workgroup for a row length: Q4_GPW when its LDS fits 64 KiB, else 1
-static int q4_gpw(int order, int nb) { return q4k_lds_bytes(order, nb, Q4_GPW) <= 65536 ? Q4_GPW : 1; }
-
-template <int ORDER, int MAXS, int GPW>
+template <int ORDER, int TPW, int S>
 static hipError_t q4_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
-    const unsigned wg = (unsigned)((a.groups + GPW - 1) / GPW);
-    if (a.dump_s) q4k_mv_kernel<ORDER, MAXS, GPW, true><<<dim3(wg, ntok), 256 * GPW, lds, s>>>(a);
-    else q4k_mv_kernel<ORDER, MAXS, GPW, false><<<dim3(wg, ntok), 256 * GPW, lds, s>>>(a);
+    const unsigned wg = (unsigned)((a.groups + TPW - 1) / TPW);
+    if (a.dump_s) q4k_mv_kernel<ORDER, Q4_R, TPW, S, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    else q4k_mv_kernel<ORDER, Q4_R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     return hipGetLastError();
 }
 
-template <int ORDER, int GPW>
-static hipError_t q4_launch_steps(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
-    // registers sized to the step count; longer rows loop over chunks of Q4_MAXS steps
-    const int nsteps = (2 * a.nb + 15) / 16;
-    if (nsteps <= 1) return q4_launch<ORDER, 1, GPW>(a, ntok, lds, s);
-    if (nsteps <= 2) return q4_launch<ORDER, 2, GPW>(a, ntok, lds, s);
-    if (nsteps <= 4) return q4_launch<ORDER, 4, GPW>(a, ntok, lds, s);
-    return q4_launch<ORDER, Q4_MAXS, GPW>(a, ntok, lds, s);
+// LDS of a launch: the activations, and with a block split the records of TPW tiles
+static size_t q4_lds(int nb, int tpw, int s) {
+    return q4_act_bytes(nb) + (s > 1 ? (size_t)tpw * RB_ROWS * nb * 16 : 0);
 }
+static int q4_tpw(int s) { return s == 1 ? 4 : s == 2 ? 2 : 1; }
 
-size_t q4k_lds_bytes(int order, int nb) { return q4k_lds_bytes(order, nb, q4_gpw(order, nb)); }
+size_t q4k_lds_bytes(int, int nb) { return q4_lds(nb, 4, 1); }
 
+// Wavefronts per tile: the repacked order splits the blocks of short matrices so that a launch
+// has about 1024 wavefronts (2048 for rows of 32 blocks or more), keeping at least 4 blocks per
+// wavefront; one wavefront per tile otherwise (and always in row order). Tiles per workgroup: 4, 2
+// or 1 for 1, 2 or more wavefronts per tile.
 hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int, hipStream_t s) {
-    const int gpw = q4_gpw(order, a.nb);
-    const size_t lds = q4k_lds_bytes(order, a.nb, gpw);
+    const int nb = a.nb;
+    if (order == 0) {
+        const size_t lds = q4_lds(nb, 4, 1);
+        if (lds > 65536) return hipErrorInvalidValue;
+        return q4_launch<0, 4, 1>(a, ntok, lds, s);
+    }
+    const int64_t tiles = a.groups * ntok, target = nb >= 32 ? 2048 : 1024;
+    int S = 1;
+    while (S < 8 && tiles * 2 * S <= target && nb >= 8 * S && q4_lds(nb, q4_tpw(2 * S), 2 * S) <= 65536) S *= 2;
+    const size_t lds = q4_lds(nb, q4_tpw(S), S);
     if (lds > 65536) return hipErrorInvalidValue;
-    if (order == 1) return gpw == 1 ? q4_launch_steps<1, 1>(a, ntok, lds, s) : q4_launch_steps<1, Q4_GPW>(a, ntok, lds, s);
-    return gpw == 1 ? q4_launch_steps<0, 1>(a, ntok, lds, s) : q4_launch_steps<0, Q4_GPW>(a, ntok, lds, s);
+    switch (S) {
+    case 1: return q4_launch<1, 4, 1>(a, ntok, lds, s);
+    case 2: return q4_launch<1, 2, 2>(a, ntok, lds, s);
+    case 4: return q4_launch<1, 1, 4>(a, ntok, lds, s);
+    default: return q4_launch<1, 1, 8>(a, ntok, lds, s);
+    }
 }
 
 // Q8_K images of activation rows, in the kernels' LDS layout (q4_act_bytes(nb) bytes per row): row
@@ -440,48 +419,38 @@ hipError_t launch_q4_image(const float *x, const float *u, int64_t ldx, int nb, 
 }
 size_t q4_image_bytes(int nb) { return q4_act_bytes(nb); }
 
-// MoE expert matvecs grouped by expert (row order, dot_q4_K_q8k): workgroup (x, y) takes 8-row group
-// x of the matrix of segment y (one selected expert with its token slots, from moe_group_kernel)
-// and every slot of that segment. Each wavefront loads its two rows' weights into registers once,
-// then for every chunk of MOE_TC slots copies their activation images (q4_image_kernel, row
-// slot / a.xdiv) into LDS and runs the same steps and chain as q4k_mv_kernel, once per slot.
-// Tensor i of a.t: output rows y_i[slot * ldy]. seg: [0] = number of segments, then per segment
-// {expert, first, count}.
+// MoE expert matvecs grouped by expert (row order, dot_q4_K_q8k): workgroup (x, y) takes tiles
+// 4x..4x+3 (one per wavefront, over the launch's tensors) of the matrix of segment y (one selected
+// expert with its token slots, from moe_group_kernel) and every slot of that segment. Each
+// wavefront loads all blocks of its tile into registers once (NB >= nb); for every chunk of MOE_TC
+// slots the workgroup copies their activation images (q4_image_kernel, row slot / a.xdiv) into LDS
+// and runs the decode kernel's row-order steps and chains once per slot. Tensor i of a.t: output
+// rows y_i[slot * ldy]. seg: [0] = number of segments, then per segment {expert, first, count}.
 constexpr int MOE_TC = 4;
-template <int MAXS>
+template <int NB>
 __global__ __launch_bounds__(256) void q4k_moe_kernel(MvArgs a, const int32_t *__restrict__ seg,
                                                       const int32_t *__restrict__ slots, const uint8_t *__restrict__ img) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j = lane & 3, pl = lane >> 2;
-    const int nb = a.nb, P = 2 * nb;
-    const int nsteps = (P + 15) >> 4;
+    const int j = lane & 3, rr = lane >> 2;
+    const int nb = a.nb;
     const int sidx = blockIdx.y;
     if (sidx >= seg[0]) return;  // whole workgroup: fewer segments than the grid allows
     const int expert = seg[1 + 3 * sidx], first = seg[2 + 3 * sidx], count = seg[3 + 3 * sidx];
-    const int64_t g = blockIdx.x;
-    const int ti = q4_tensor_of(a, g);
-    const int64_t lg = g - a.t[ti].gfirst;  // group within the matrix
-    const uint8_t *G = a.t[ti].W + (size_t)((int64_t)expert * a.t[ti].gpm + lg) * 1152 * nb;
-    const uint8_t *meta = G + (size_t)16 * P * wave;
-    const uint8_t *quant = G + (size_t)128 * nb + (size_t)256 * nb * wave;
-    Q4Step st[MAXS];
+    const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+    const bool live = tile < a.groups;
+    const int64_t tc = live ? tile : a.groups - 1;
+    const int ti = q4_tensor_of(a, tc);
+    const int64_t lt = tc - a.t[ti].gfirst;  // tile within the matrix
+    const uint8_t *T0 = a.t[ti].W + (size_t)((int64_t)expert * a.t[ti].gpm + lt) * nb * RB_BYTES;
+    RbW w[NB];
 #pragma unroll
-    for (int k = 0; k < MAXS; ++k) {
-        const int s = k < nsteps ? k : nsteps - 1;
-        const int np = min(16, P - 16 * s);
-        const int pc = min(pl, np - 1);
-        const uint8_t *qb = quant + (size_t)2048 * s + 16 * (4 * pc + j);
-        st[k].p0 = ld16(qb);
-        st[k].p1 = ld16(qb + 64 * np);
-        st[k].m = ld16(meta + 16 * (16 * s + pc));
-    }
-    const size_t actb = q4_act_bytes(nb), waveb = q4_wave_bytes(0, nb);
+    for (int b = 0; b < NB; ++b) rb_load(T0 + (size_t)min(b, nb - 1) * RB_BYTES, lane, w[b]);
+    const size_t actb = q4_act_bytes(nb);
     const int units = (int)(actb / 16);
-    const int64_t lr0 = lg * 8 + 2 * wave;
-    const int64_t left = a.t[ti].rows - lr0;
-    float *rec0 = (float *)(smem + MOE_TC * actb + (size_t)wave * waveb);
+    const int64_t row = lt * RB_ROWS + rr;
+    const bool store = live && j == 0 && row < a.t[ti].rows;
     for (int c0 = 0; c0 < count; c0 += MOE_TC) {
         const int nc = min(MOE_TC, count - c0);
         // the chunk's activation images (rows slot / xdiv) into LDS
@@ -493,78 +462,70 @@ __global__ __launch_bounds__(256) void q4k_moe_kernel(MvArgs a, const int32_t *_
         __syncthreads();
         for (int c = 0; c < nc; ++c) {
             const uint8_t *act = smem + (size_t)c * actb;
-            Q4Ctx cx;
-            cx.act = act;
-            cx.ad = (const float *)(act + q4_off_d(nb));
-            cx.abs16 = (const int16_t *)(act + q4_off_s(nb));
-            cx.rec = rec0;
-            cx.nb = nb;
-            cx.P = P;
-            cx.j = j;
-            cx.pl = pl;
-            Q4Dump none{nullptr, nullptr, 0, 0};
+            float acc = 0.0f, acc2 = 0.0f, macc = 0.0f;
 #pragma unroll
-            for (int k = 0; k < MAXS; ++k)
-                if (k < nsteps) q4_step<0, false>(st[k], k, cx, none);
-            wave_sync();
-            q4_chain<0>(cx, lane, a.t[ti].y + (size_t)slots[first + c0 + c] * a.ldy + lr0, left);
-            wave_sync();  // the next slot's records reuse the area
+            for (int b = 0; b < NB; ++b) {
+                if (b < nb) {  // uniform
+                    RbIn in;
+                    rb_in(w[b], act, nb, b, j, in);
+                    const float fd = fp16_bits_to_f32(w[b].m.x & 0xFFFF) * in.yd;
+                    const float fdm = fp16_bits_to_f32(w[b].m.x >> 16) * in.yd;
+                    int u0, u1;
+                    rb_row_lanes(w[b], in, j, u0, u1);
+                    acc = __builtin_fmaf(fd, (float)u0, acc);
+                    acc2 = __builtin_fmaf(fd, (float)u1, acc2);
+                    macc = __builtin_fmaf(fdm, (float)in.mt, macc);
+                }
+            }
+            const float out = rb_row_final(acc, acc2, macc);
+            if (store) a.t[ti].y[(size_t)slots[first + c0 + c] * a.ldy + row] = out;
         }
         __syncthreads();  // the next chunk reuses the activations
     }
 }
 
-size_t q4k_moe_lds_bytes(int nb) { return MOE_TC * q4_act_bytes(nb) + 4 * q4_wave_bytes(0, nb); }
+size_t q4k_moe_lds_bytes(int nb) { return MOE_TC * q4_act_bytes(nb); }
+int q4k_moe_max_blocks() { return 8; }
 
-// a.groups = groups of one matrix over all tensors (the launch's x extent); grid.y = max_segments
+// a.groups = tiles of one matrix over all tensors; grid.y = max_segments
 hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *seg, const int32_t *slots, const uint8_t *img,
                           int max_segments, hipStream_t s) {
-    const int nsteps = (2 * a.nb + 15) / 16;
     const size_t lds = q4k_moe_lds_bytes(a.nb);
-    if (nsteps > 4 || lds > 65536) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)a.groups, (unsigned)max_segments);
-    if (nsteps <= 1) q4k_moe_kernel<1><<<grid, 256, lds, s>>>(a, seg, slots, img);
-    else if (nsteps <= 2) q4k_moe_kernel<2><<<grid, 256, lds, s>>>(a, seg, slots, img);
-    else q4k_moe_kernel<4><<<grid, 256, lds, s>>>(a, seg, slots, img);
+    if (a.nb > q4k_moe_max_blocks() || lds > 65536) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.groups + 3) / 4), (unsigned)max_segments);
+    if (a.nb <= 4) q4k_moe_kernel<4><<<grid, 256, lds, s>>>(a, seg, slots, img);
+    else q4k_moe_kernel<8><<<grid, 256, lds, s>>>(a, seg, slots, img);
     return hipGetLastError();
 }
 
-// upload-time re-layout of Q4_K rows into the group layout above; one thread per destination byte
+// upload-time re-layout of Q4_K rows into the tile layout above; one thread per destination byte
 __global__ void q4k_relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int64_t rows,
-                                    int nb, int64_t gpm, int64_t total, int64_t row_bytes) {
-    const int64_t gbytes = (int64_t)1152 * nb;
-    const int P = 2 * nb;
+                                    int nb, int64_t tpm, int64_t total, int64_t row_bytes) {
     for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t g = o / gbytes;
-        const int64_t ob = o - g * gbytes;
-        const int64_t m = g / gpm, gl = g - m * gpm;
-        int w, q, byte;
-        if (ob < (int64_t)128 * nb) {
-            const int idx = (int)(ob >> 4);
-            w = idx / P;
-            q = idx - w * P;
-            byte = (int)(ob & 15);
+        const int64_t tb = o / RB_BYTES;
+        const int ob = (int)(o - tb * RB_BYTES);
+        const int64_t t = tb / nb;
+        const int b = (int)(tb - t * nb);
+        const int64_t m = t / tpm, tl = t - m * tpm;
+        int r, byte;
+        if (ob < 256) {
+            r = ob >> 4;
+            byte = ob & 15;
         } else {
-            const int64_t o2 = ob - (int64_t)128 * nb;
-            w = (int)(o2 / (256 * (int64_t)nb));
-            const int o3 = (int)(o2 - (int64_t)w * 256 * nb);
-            const int s = o3 >> 11, np = min(16, P - 16 * s);
-            const int u = o3 - 2048 * s, h = u / (64 * np), v = u - h * 64 * np;
-            const int L = v >> 4, jj = L & 3;
-            q = 16 * s + (L >> 2);
-            byte = 16 + 32 * jj + 16 * h + (v & 15);
+            const int u = ob - 256, hh = u >> 10, L = (u >> 4) & 63, jj = L & 3;
+            r = L >> 2;
+            byte = 16 + 32 * jj + 16 * (hh ^ (jj >> 1)) + (u & 15);
         }
-        const int r = 2 * w + (q >= nb), b = q - (q >= nb) * nb;
-        const int64_t row = gl * 8 + r;
+        const int64_t row = tl * RB_ROWS + r;
         dst[o] = row < rows ? src[(m * rows + row) * row_bytes + (int64_t)b * 144 + byte] : (uint8_t)0;
     }
 }
 
-hipError_t launch_q4k_relayout(const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t gpm, int64_t total,
+hipError_t launch_q4k_relayout(const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t tpm, int64_t total,
                                int64_t row_bytes, hipStream_t s) {
     const int64_t want = (total + 255) / 256;
     const int grid = (int)(want < 65536 ? want : 65536);
-    q4k_relayout_kernel<<<grid, 256, 0, s>>>(src, dst, rows, nb, gpm, total, row_bytes);
+    q4k_relayout_kernel<<<grid, 256, 0, s>>>(src, dst, rows, nb, tpm, total, row_bytes);
     return hipGetLastError();
 }
 
