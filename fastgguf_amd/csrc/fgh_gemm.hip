@@ -108,11 +108,12 @@ __device__ __forceinline__ int gq_slot(int blk, int j, int h, int row) {
 __device__ __forceinline__ int gm_slot(int blk, int row) { return 1024 + blk * 64 + (row ^ (blk << 2)); }
 
 // the tile-layout address of (row R over all matrices, block 0): its tile and its row in the tile
+// (block b is b * gpm * 2304 further)
 __device__ __forceinline__ const uint8_t *gemm_tile(const GemmArgs &a, int64_t R, int &rr) {
     R = R < a.nrows ? R : a.nrows - 1;
     const int64_t mat = R / a.rows, r = R - mat * a.rows;
     rr = (int)(r & 15);
-    return a.W + (size_t)(mat * a.gpm + (r >> 4)) * a.nb * 2304;
+    return a.W + ((size_t)mat * a.nb * a.gpm + (size_t)(r >> 4)) * 2304;
 }
 
 template <int NT>
@@ -133,13 +134,13 @@ __device__ __forceinline__ void wstage_init(WStage<NT> &w, const GemmArgs &a, in
 }
 
 template <int NT>
-__device__ __forceinline__ void wstage_load(WStage<NT> &w, int nb, int s, int tid) {
+__device__ __forceinline__ void wstage_load(WStage<NT> &w, int nb, size_t bstride, int s, int tid) {
 #pragma unroll
     for (int k = 0; k < WStage<NT>::NU; ++k) {
         const int blk = (tid + k * NT) >> 9;
-        w.q[k] = ld16(w.src[k] + (size_t)min(2 * s + blk, nb - 1) * 2304);
+        w.q[k] = ld16(w.src[k] + (size_t)min(2 * s + blk, nb - 1) * bstride);
     }
-    if (tid < 128) w.m = ld16(w.msrc + (size_t)min(2 * s + (tid >> 6), nb - 1) * 2304);
+    if (tid < 128) w.m = ld16(w.msrc + (size_t)min(2 * s + (tid >> 6), nb - 1) * bstride);
 }
 
 template <int NT>
@@ -270,9 +271,10 @@ __global__ __launch_bounds__(256 * NTW) void q4k_gemm_kernel(GemmArgs a) {
     const int64_t row = row0 + 32 * rs + n;
     const int tok = 32 * tt + n;
 
+    const size_t bstride = (size_t)a.gpm * 2304;  // one block further in the tile layout
     WStage<NT> ws;
     wstage_init(ws, a, row0, tid);
-    wstage_load(ws, nb, 0, tid);
+    wstage_load(ws, nb, bstride, 0, tid);
     ActOps A, B;
     act_load(A, a, min(kh, nb - 1), tok, h);
     for (int i = tid; i < nb * a.Tp / 4; i += NT) ((float4 *)yds)[i] = ((const float4 *)a.ydT)[i];
@@ -284,7 +286,7 @@ __global__ __launch_bounds__(256 * NTW) void q4k_gemm_kernel(GemmArgs a) {
     for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
     for (int s = 0; s < nsteps; s += 2) {
         // step s: stage0, set A; loads of step s + 1 (stage1, set B) in flight
-        wstage_load(ws, nb, min(s + 1, nsteps - 1), tid);
+        wstage_load(ws, nb, bstride, min(s + 1, nsteps - 1), tid);
         act_load(B, a, min(2 * (s + 1) + kh, nb - 1), tok, h);
         __builtin_amdgcn_sched_barrier(0);
         gemm_block<DUMP>(A, stage0, kh, rs, n, h, tt, acc, yds, min(2 * s + kh, nb - 1), 2 * s + kh < nb, row, a);
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(256 * NTW) void q4k_gemm_kernel(GemmArgs a) {
         __syncthreads();
         if (s + 1 < nsteps) {  // uniform
             // step s + 1: stage1, set B; loads of step s + 2 (stage0, set A) in flight
-            wstage_load(ws, nb, min(s + 2, nsteps - 1), tid);
+            wstage_load(ws, nb, bstride, min(s + 2, nsteps - 1), tid);
             act_load(A, a, min(2 * (s + 2) + kh, nb - 1), tok, h);
             __builtin_amdgcn_sched_barrier(0);
             gemm_block<DUMP>(B, stage1, kh, rs, n, h, tt, acc, yds, min(2 * (s + 1) + kh, nb - 1),

@@ -3,7 +3,9 @@
 //
 // Device layout of a Q4_K tensor (written at upload by q4k_relayout_kernel): rows in tiles of 16
 // per matrix (tpm = ceil(rows / 16) tiles, the last one zero-padded). Tile t of matrix m, block b,
-// is 2304 bytes (the file's 16 x 144 bytes, rearranged) at ((m * tpm + t) * nb + b) * 2304:
+// is 2304 bytes (the file's 16 x 144 bytes, rearranged) at ((m * nb + b) * tpm + t) * 2304: block-
+// major, so the wavefronts of a launch, all at about the same block, read one contiguous stretch
+// of HBM at a time (DRAM pages stay open) rather than one stretch per tile:
 //   [0, 256)     meta: row r at 16 r, the block's first 16 bytes (fp16 d, fp16 dmin, 12 bytes of
 //                6-bit scales and mins)
 //   [256, 2304)  quants: slot (h, L) at 256 + 1024 h + 16 L, L = 4 r + j, holds 16-byte piece
@@ -34,11 +36,12 @@ namespace fgh {
 constexpr int RB_ROWS = 16;     // rows per tile
 constexpr int RB_BYTES = 2304;  // one (tile, block): 16 x 144
 
-// LDS activations: natural-order Q8_K blocks: qs [nb][256] at 0, d [nb] at 256 nb, bsums [nb][16]
-// at align16(260 nb)
+// LDS activations: natural-order Q8_K blocks: qs [nb][256] at 0, d [nb] at 256 nb, and the sums of
+// each 32 values, bs32 [nb][8] int16 at align16(260 nb) (bs32[g] = bsums[2g] + bsums[2g+1] of the
+// reference's q8k_blk_t: the min terms only ever use these pairs)
 __host__ __device__ constexpr size_t q4_off_d(int nb) { return (size_t)nb * 256; }
 __host__ __device__ constexpr size_t q4_off_s(int nb) { return ((size_t)nb * 260 + 15) & ~(size_t)15; }
-__host__ __device__ constexpr size_t q4_act_bytes(int nb) { return (q4_off_s(nb) + (size_t)nb * 32 + 15) & ~(size_t)15; }
+__host__ __device__ constexpr size_t q4_act_bytes(int nb) { return (q4_off_s(nb) + (size_t)nb * 16 + 15) & ~(size_t)15; }
 
 // 16 threads per 256-value block; thread tl holds values 16tl..16tl+15 (4 float4 loads)
 struct XRound {
@@ -96,9 +99,10 @@ __device__ __forceinline__ void q8k_store_b(int nb, int b, bool live, const XRou
         s += q0 + q1 + q2 + q3;
         w[u] = pack_q(q0, q1, q2, q3);
     }
+    s += dpp_xor1(s);  // threads 2g, 2g+1: the 32 values of sub-block g
     if (live) {
         *(uint4 *)(act + (size_t)b * 256 + 16 * tl) = make_uint4(w[0], w[1], w[2], w[3]);
-        ((int16_t *)(act + q4_off_s(nb)))[16 * b + tl] = (int16_t)s;
+        if ((tl & 1) == 0) ((int16_t *)(act + q4_off_s(nb)))[8 * b + (tl >> 1)] = (int16_t)s;
         if (tl == 0) ((float *)(act + q4_off_d(nb)))[b] = d;
     }
 }
@@ -140,18 +144,29 @@ __device__ __forceinline__ void rb_load(const uint8_t *T, int lane, RbW &w) {
     w.m = ld16(T + 16 * (lane >> 2));
 }
 
+// Per-lane constants of the scale extraction: chunk j, the shift selecting bytes 2(j & 1) and
+// 2(j & 1) + 1 of the scale words, and an all-ones mask for lanes j >= 2.
+struct RbLane {
+    int j, sh;
+    uint32_t hm;
+};
+__device__ __forceinline__ RbLane rb_lane(int lane) {
+    const int j = lane & 3;
+    return RbLane{j, 16 * (j & 1), j >= 2 ? 0xFFFFFFFFu : 0u};
+}
+
 // What every order needs of one lane's chunk j of one block: its activations (register order),
-// the chunk's two sub-block scales as an int16 pair, the min partial of chunk j,
-// m_2j (bs_4j + bs_4j+1) + m_2j+1 (bs_4j+2 + bs_4j+3) (the reference's min lane p = j), and yd.
+// the chunk's two 6-bit sub-block scales (bytes 0 and 1 of scp), the min partial of chunk j,
+// m_2j bs32_2j + m_2j+1 bs32_2j+1 (the reference's min lane p = j), and yd.
 struct RbIn {
     uint32_t ylo[8], yhi[8];
-    uint32_t sc2;
+    uint32_t scp;
     int mt;
     float yd;
 };
-__device__ __forceinline__ void rb_in(const RbW &w, const uint8_t *act, int nb, int b, int j, RbIn &in) {
-    const int hs = 16 * (j >> 1);  // lanes j >= 2: second half first
-    const uint8_t *yb = act + (size_t)b * 256 + 64 * j;
+__device__ __forceinline__ void rb_in(const RbW &w, const uint8_t *act, int nb, int b, const RbLane &ln, RbIn &in) {
+    const int hs = 16 * (ln.j >> 1);  // lanes j >= 2: second half first
+    const uint8_t *yb = act + (size_t)b * 256 + 64 * ln.j;
     const uint4 l0 = *(const uint4 *)(yb + hs), l1 = *(const uint4 *)(yb + 16 - hs);
     const uint4 h0 = *(const uint4 *)(yb + 32 + hs), h1 = *(const uint4 *)(yb + 48 - hs);
     in.ylo[0] = l0.x; in.ylo[1] = l0.y; in.ylo[2] = l0.z; in.ylo[3] = l0.w;
@@ -161,33 +176,30 @@ __device__ __forceinline__ void rb_in(const RbW &w, const uint8_t *act, int nb, 
     // scales and mins of sub-blocks 2j (low nibbles) and 2j+1 (high nibbles) straight from the
     // packed words u0..u2 (scale_min_k4, fastgguf.c:466-472): for j < 2 the low 6 bits of bytes 2j,
     // 2j+1 of u0 (scales) and u1 (mins); for j >= 2 the nibbles of bytes 2j-4, 2j-3 of u2 with the
-    // top 2 bits of the same bytes of u0 / u1
-    const int sh = 16 * (j & 1);
-    const uint32_t A = w.m.y >> sh, B = w.m.z >> sh, C = w.m.w >> sh;
-    const uint32_t scp = j < 2 ? (A & 0x3f3fu) : ((C & 0x0f0fu) | ((A & 0xc0c0u) >> 2));
-    const uint32_t mnp = j < 2 ? (B & 0x3f3fu) : (((C >> 4) & 0x0f0fu) | ((B & 0xc0c0u) >> 2));
-    in.sc2 = __builtin_amdgcn_perm(0u, scp, 0x0C010C00u);
-    const uint32_t m_lo = mnp & 0x3Fu, m_hi = (mnp >> 8) & 0x3Fu;
-    const uint2 bq = *(const uint2 *)((const int16_t *)(act + q4_off_s(nb)) + 16 * b + 4 * j);
-    in.mt = dot2_i16(m_lo | (m_lo << 16), bq.x, dot2_i16(m_hi | (m_hi << 16), bq.y, 0));
+    // top 2 bits of the same bytes of u0 / u1 (both formed, the lane's one selected bitwise)
+    const uint32_t A = w.m.y >> ln.sh, B = w.m.z >> ln.sh, C = w.m.w >> ln.sh;
+    const uint32_t sc_lo = A & 0x3f3fu, sc_hi = (C & 0x0f0fu) | ((A >> 2) & 0x3030u);
+    const uint32_t mn_lo = B & 0x3f3fu, mn_hi = ((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u);
+    in.scp = (sc_hi & ln.hm) | (sc_lo & ~ln.hm);
+    const uint32_t mnp = (mn_hi & ln.hm) | (mn_lo & ~ln.hm);
+    const uint32_t bq = *(const uint32_t *)((const int16_t *)(act + q4_off_s(nb)) + 8 * b + 2 * ln.j);
+    in.mt = dot2_i16(__builtin_amdgcn_perm(0u, mnp, 0x0C010C00u), bq, 0);
     in.yd = ((const float *)(act + q4_off_d(nb)))[b];
 }
 __device__ __forceinline__ uint32_t nib_lo(uint32_t q) { return q & 0x0F0F0F0Fu; }
 __device__ __forceinline__ uint32_t nib_hi(uint32_t q) { return (q >> 4) & 0x0F0F0F0Fu; }
 
-// the chunk's share of the block's sumi (sum_g sc_g sum q y over its two sub-blocks): the dots of
-// 16 values each fit int16 (|.| <= 16 * 15 * 127), so the scale products are two packed dots
+// the chunk's share of the block's sumi: sc_2j sum(lo q y) + sc_2j+1 sum(hi q y) over its 32 + 32
+// values (each dot sum |.| <= 32 * 15 * 127 < 2^23: 24-bit multiplies)
 __device__ __forceinline__ int rb_sumi_part(const RbW &w, const RbIn &in) {
     const uint32_t qd[8] = {w.p0.x, w.p0.y, w.p0.z, w.p0.w, w.p1.x, w.p1.y, w.p1.z, w.p1.w};
-    int il0 = 0, il1 = 0, ih0 = 0, ih1 = 0;
+    int il = 0, ih = 0;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        il0 = dot4((int)nib_lo(qd[d]), (int)in.ylo[d], il0);
-        ih0 = dot4((int)nib_hi(qd[d]), (int)in.yhi[d], ih0);
-        il1 = dot4((int)nib_lo(qd[d + 4]), (int)in.ylo[d + 4], il1);
-        ih1 = dot4((int)nib_hi(qd[d + 4]), (int)in.yhi[d + 4], ih1);
+    for (int d = 0; d < 8; ++d) {
+        il = dot4((int)nib_lo(qd[d]), (int)in.ylo[d], il);
+        ih = dot4((int)nib_hi(qd[d]), (int)in.yhi[d], ih);
     }
-    return dot2_i16(in.sc2, pack_i16(il0, ih0), dot2_i16(in.sc2, pack_i16(il1, ih1), 0));
+    return __mul24((int)(in.scp & 0xFFu), il) + __mul24((int)(in.scp >> 8), ih);
 }
 
 // Row order: the reference's lane partials 2j and 2j+1 of the block (each summed over the row's
@@ -196,10 +208,11 @@ __device__ __forceinline__ int rb_sumi_part(const RbW &w, const RbIn &in) {
 // one exchange with lane j ^ 1 the lane's own pair summed over all four.
 __device__ __forceinline__ void rb_row_lanes(const RbW &w, const RbIn &in, int j, int &u0, int &u1) {
     const uint32_t qd[8] = {w.p0.x, w.p0.y, w.p0.z, w.p0.w, w.p1.x, w.p1.y, w.p1.z, w.p1.w};
+    const uint32_t sc2 = __builtin_amdgcn_perm(0u, in.scp, 0x0C010C00u);  // (sc_2j, sc_2j+1) as int16
     int lv[8];
 #pragma unroll
     for (int d = 0; d < 8; ++d)  // each dot4 is at most 4 * 15 * 127 = 7620 in magnitude: an int16 pair
-        lv[d] = dot2_i16(in.sc2, pack_i16(dot4((int)nib_lo(qd[d]), (int)in.ylo[d], 0),
+        lv[d] = dot2_i16(sc2, pack_i16(dot4((int)nib_lo(qd[d]), (int)in.ylo[d], 0),
                                           dot4((int)nib_hi(qd[d]), (int)in.yhi[d], 0)), 0);
     int t[4];
 #pragma unroll
@@ -249,10 +262,11 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     const int64_t tc = live ? tile : a.groups - 1;
     const int ti = q4_tensor_of(a, tc);
     const uint32_t lt = (uint32_t)(tc - a.t[ti].gfirst), gpm = (uint32_t)a.t[ti].gpm;
-    const int64_t mg = a.sel ? (int64_t)a.sel[tok] * gpm : 0;  // selected matrix (MoE)
+    const uint32_t mi = (a.sel ? (uint32_t)a.sel[tok] : 0u) + lt / gpm, tt = lt % gpm;  // matrix (MoE: selected), tile
     const int nbw = (nb + S - 1) / S, bb0 = ks * nbw;
     const int nbl = max(0, min(nb, bb0 + nbw) - bb0), bl = max(nbl - 1, 0);
-    const uint8_t *T0 = a.t[ti].W + ((size_t)(mg + lt) * nb + min(bb0, nb - 1)) * RB_BYTES;
+    const size_t bstride = (size_t)gpm * RB_BYTES;
+    const uint8_t *T0 = a.t[ti].W + (((size_t)mi * nb + min(bb0, nb - 1)) * gpm + tt) * RB_BYTES;
 
     // (1) x for the first quantization rounds, then (2) the ring's first R steps
     const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
@@ -260,54 +274,62 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     q8k_begin(xq, x, nb);
     RbW ring[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) rb_load(T0 + (size_t)min(r, bl) * RB_BYTES, lane, ring[r]);
+    for (int r = 0; r < R; ++r) rb_load(T0 + (size_t)min(r, bl) * bstride, lane, ring[r]);
     // (3) quantize x into LDS while the weights are in flight
     uint8_t *act = smem;
     q8k_finish(xq, x, nb, act);
     __syncthreads();
 
-    const int64_t mrow = (int64_t)(lt % gpm) * RB_ROWS;  // first row of the tile in its matrix
+    const int64_t mrow = (int64_t)tt * RB_ROWS;  // first row of the tile in its matrix
     const int64_t obase = (int64_t)(lt / gpm) * a.t[ti].rows;
     const int64_t rows = a.t[ti].rows;
     float4 *rec = (float4 *)(smem + q4_act_bytes(nb)) + (size_t)ts * RB_ROWS * nb;  // [b][row], S > 1
+    const RbLane ln = rb_lane(lane);
     float acc = 0.0f, acc2 = 0.0f, macc = 0.0f;
-    for (int b0 = 0; b0 < nbl; b0 += R) {
+    // one block b from ring slot r
+    auto step = [&](const RbW &w, int b) {
+        RbIn in;
+        rb_in(w, act, nb, b, ln, in);
+        const float fd = fp16_bits_to_f32(w.m.x & 0xFFFF) * in.yd;
+        const float fdm = fp16_bits_to_f32(w.m.x >> 16) * in.yd;
+        int sumi = 0, msum = 0;
+        if (ORDER == 1 || DUMP) {
+            sumi = sum4_i32(rb_sumi_part(w, in));
+            msum = sum4_i32(in.mt);
+        }
+        if (ORDER == 1) {
+            if (S == 1) {
+                acc = __builtin_fmaf(fd, (float)sumi, acc);
+                macc = __builtin_fmaf(fdm, (float)msum, macc);
+            } else if (j == 0) {
+                rec[(size_t)b * RB_ROWS + rr] = make_float4(fd, (float)sumi, fdm, (float)msum);
+            }
+        } else {
+            int u0, u1;
+            rb_row_lanes(w, in, j, u0, u1);
+            acc = __builtin_fmaf(fd, (float)u0, acc);
+            acc2 = __builtin_fmaf(fd, (float)u1, acc2);
+            macc = __builtin_fmaf(fdm, (float)in.mt, macc);
+        }
+        if (DUMP && live && j == 0 && mrow + rr < rows) {
+            const size_t di = (size_t)(obase + mrow + rr) * nb + b;
+            a.dump_s[di] = sumi;
+            a.dump_m[di] = msum;
+        }
+    };
+    // whole rounds of R blocks as straight-line code (the steps interleave), refilling the ring;
+    // then the last nbl % R blocks already in the ring
+    int b0 = 0;
+    for (; b0 + R <= nbl; b0 += R) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int bi = b0 + r, b = bb0 + bi;
-            if (bi < nbl) {  // uniform
-                RbIn in;
-                rb_in(ring[r], act, nb, b, j, in);
-                const float fd = fp16_bits_to_f32(ring[r].m.x & 0xFFFF) * in.yd;
-                const float fdm = fp16_bits_to_f32(ring[r].m.x >> 16) * in.yd;
-                int sumi = 0, msum = 0;
-                if (ORDER == 1 || DUMP) {
-                    sumi = sum4_i32(rb_sumi_part(ring[r], in));
-                    msum = sum4_i32(in.mt);
-                }
-                if (ORDER == 1) {
-                    if (S == 1) {
-                        acc = __builtin_fmaf(fd, (float)sumi, acc);
-                        macc = __builtin_fmaf(fdm, (float)msum, macc);
-                    } else if (j == 0) {
-                        rec[(size_t)b * RB_ROWS + rr] = make_float4(fd, (float)sumi, fdm, (float)msum);
-                    }
-                } else {
-                    int u0, u1;
-                    rb_row_lanes(ring[r], in, j, u0, u1);
-                    acc = __builtin_fmaf(fd, (float)u0, acc);
-                    acc2 = __builtin_fmaf(fd, (float)u1, acc2);
-                    macc = __builtin_fmaf(fdm, (float)in.mt, macc);
-                }
-                if (DUMP && live && j == 0 && mrow + rr < rows) {
-                    const size_t di = (size_t)(obase + mrow + rr) * nb + b;
-                    a.dump_s[di] = sumi;
-                    a.dump_m[di] = msum;
-                }
-            }
-            rb_load(T0 + (size_t)min(bi + R, bl) * RB_BYTES, lane, ring[r]);
+            step(ring[r], bb0 + b0 + r);
+            rb_load(T0 + (size_t)min(b0 + r + R, bl) * bstride, lane, ring[r]);
         }
     }
+#pragma unroll
+    for (int r = 0; r < R - 1; ++r)
+        if (b0 + r < nbl) step(ring[r], bb0 + b0 + r);  // uniform
     float *y = a.t[ti].y + (size_t)tok * a.ldy + obase + mrow;
     if (S > 1) {
         __syncthreads();
@@ -339,14 +361,16 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     }
 }
 
-constexpr int Q4_R = 4;  // ring depth (steps in flight per wavefront)
-
-template <int ORDER, int TPW, int S>
+template <int ORDER, int R, int TPW, int S>
 static hipError_t q4_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
     const unsigned wg = (unsigned)((a.groups + TPW - 1) / TPW);
-    if (a.dump_s) q4k_mv_kernel<ORDER, Q4_R, TPW, S, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
-    else q4k_mv_kernel<ORDER, Q4_R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    if (a.dump_s) q4k_mv_kernel<ORDER, R, TPW, S, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    else q4k_mv_kernel<ORDER, R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     return hipGetLastError();
+}
+template <int ORDER, int TPW, int S>
+static hipError_t q4_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
+    return R == 2 ? q4_launch<ORDER, 2, TPW, S>(a, ntok, lds, s) : q4_launch<ORDER, 4, TPW, S>(a, ntok, lds, s);
 }
 
 // LDS of a launch: the activations, and with a block split the records of TPW tiles
@@ -357,27 +381,28 @@ static int q4_tpw(int s) { return s == 1 ? 4 : s == 2 ? 2 : 1; }
 
 size_t q4k_lds_bytes(int, int nb) { return q4_lds(nb, 4, 1); }
 
-// Wavefronts per tile: the repacked order splits the blocks of short matrices so that a launch
-// has about 1024 wavefronts (2048 for rows of 32 blocks or more), keeping at least 4 blocks per
-// wavefront; one wavefront per tile otherwise (and always in row order). Tiles per workgroup: 4, 2
-// or 1 for 1, 2 or more wavefronts per tile.
+// Launch shape (measured on MI355X at the decode-layer shapes). Wavefronts per tile S: launches of
+// fewer than 768 tiles (tiles x tokens) split the blocks of a tile over up to 8 wavefronts
+// (repacked order), as many as keep the launch within 2048 wavefronts and each wavefront at 4
+// blocks or more; larger launches keep one wavefront per tile (the row order always does). Tiles
+// per workgroup: 4, 2 or 1 for S = 1, 2 or more. Ring depth R: 2 steps when the launch has 1024
+// wavefronts or more over rows shorter than 32 blocks (enough loads in flight across the chip), 4
+// otherwise.
 hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int, hipStream_t s) {
     const int nb = a.nb;
-    if (order == 0) {
-        const size_t lds = q4_lds(nb, 4, 1);
-        if (lds > 65536) return hipErrorInvalidValue;
-        return q4_launch<0, 4, 1>(a, ntok, lds, s);
-    }
-    const int64_t tiles = a.groups * ntok, target = nb >= 32 ? 2048 : 1024;
+    const int64_t tiles = a.groups * ntok;
     int S = 1;
-    while (S < 8 && tiles * 2 * S <= target && nb >= 8 * S && q4_lds(nb, q4_tpw(2 * S), 2 * S) <= 65536) S *= 2;
+    if (order == 1 && tiles < 768)
+        while (S < 8 && tiles * 2 * S <= 2048 && nb >= 8 * S && q4_lds(nb, q4_tpw(2 * S), 2 * S) <= 65536) S *= 2;
+    const int R = nb < 32 && tiles * S >= 1024 ? 2 : 4;
     const size_t lds = q4_lds(nb, q4_tpw(S), S);
     if (lds > 65536) return hipErrorInvalidValue;
+    if (order == 0) return q4_launch_r<0, 4, 1>(R, a, ntok, lds, s);
     switch (S) {
-    case 1: return q4_launch<1, 4, 1>(a, ntok, lds, s);
-    case 2: return q4_launch<1, 2, 2>(a, ntok, lds, s);
-    case 4: return q4_launch<1, 1, 4>(a, ntok, lds, s);
-    default: return q4_launch<1, 1, 8>(a, ntok, lds, s);
+    case 1: return q4_launch_r<1, 4, 1>(R, a, ntok, lds, s);
+    case 2: return q4_launch_r<1, 2, 2>(R, a, ntok, lds, s);
+    case 4: return q4_launch_r<1, 1, 4>(R, a, ntok, lds, s);
+    default: return q4_launch_r<1, 1, 8>(R, a, ntok, lds, s);
     }
 }
 
@@ -443,14 +468,16 @@ __global__ __launch_bounds__(256) void q4k_moe_kernel(MvArgs a, const int32_t *_
     const int64_t tc = live ? tile : a.groups - 1;
     const int ti = q4_tensor_of(a, tc);
     const int64_t lt = tc - a.t[ti].gfirst;  // tile within the matrix
-    const uint8_t *T0 = a.t[ti].W + (size_t)((int64_t)expert * a.t[ti].gpm + lt) * nb * RB_BYTES;
+    const size_t bstride = (size_t)a.t[ti].gpm * RB_BYTES;
+    const uint8_t *T0 = a.t[ti].W + (size_t)expert * nb * bstride + (size_t)lt * RB_BYTES;
     RbW w[NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) rb_load(T0 + (size_t)min(b, nb - 1) * RB_BYTES, lane, w[b]);
+    for (int b = 0; b < NB; ++b) rb_load(T0 + (size_t)min(b, nb - 1) * bstride, lane, w[b]);
     const size_t actb = q4_act_bytes(nb);
     const int units = (int)(actb / 16);
     const int64_t row = lt * RB_ROWS + rr;
     const bool store = live && j == 0 && row < a.t[ti].rows;
+    const RbLane ln = rb_lane(lane);
     for (int c0 = 0; c0 < count; c0 += MOE_TC) {
         const int nc = min(MOE_TC, count - c0);
         // the chunk's activation images (rows slot / xdiv) into LDS
@@ -467,7 +494,7 @@ __global__ __launch_bounds__(256) void q4k_moe_kernel(MvArgs a, const int32_t *_
             for (int b = 0; b < NB; ++b) {
                 if (b < nb) {  // uniform
                     RbIn in;
-                    rb_in(w[b], act, nb, b, j, in);
+                    rb_in(w[b], act, nb, b, ln, in);
                     const float fd = fp16_bits_to_f32(w[b].m.x & 0xFFFF) * in.yd;
                     const float fdm = fp16_bits_to_f32(w[b].m.x >> 16) * in.yd;
                     int u0, u1;
@@ -504,9 +531,9 @@ __global__ void q4k_relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__
     for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += (int64_t)gridDim.x * blockDim.x) {
         const int64_t tb = o / RB_BYTES;
         const int ob = (int)(o - tb * RB_BYTES);
-        const int64_t t = tb / nb;
-        const int b = (int)(tb - t * nb);
-        const int64_t m = t / tpm, tl = t - m * tpm;
+        const int64_t mb = tb / tpm, tl = tb - mb * tpm;  // (matrix, block), tile
+        const int64_t m = mb / nb;
+        const int b = (int)(mb - m * nb);
         int r, byte;
         if (ob < 256) {
             r = ob >> 4;
