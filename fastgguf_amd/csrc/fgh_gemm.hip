@@ -37,17 +37,21 @@ namespace fgh {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------------------------
 // Activation quantizer for the GEMM (quantize_q8k, fastgguf.c:773-793, bit-exact): one wavefront
-// per (token, 256-block); lane l holds values 4l..4l+3. Writes
-//   qs  [nb][Tp/32][8][32][32] int8: group g of block b of token t = 32 tt + n at
-//                    (((b Tp/32 + tt) 8 + g) 32 + n) 32, so one MFMA fragment (32 tokens x 32
-//                    values) is 1 KB contiguous and a block's 8 fragments of one token tile 8 KB
+// per (token, 256-block); lane l holds values 4l..4l+3 (group g = l / 8, half h = (l / 4) % 2).
+// Writes, with NTT = Tp / 32 token tiles and token t = 32 tt + n:
+//   qs  [nb][NTT][8][2][32][16] int8: values 32 g + 16 h .. + 15 of token t at
+//                    ((((b NTT + tt) 8 + g) 2 + h) 32 + n) 16, so the MFMA fragment of (tt, g) is
+//                    1 KB contiguous in lane order (lane = 32 h + n)
 //   ydT [nb][Tp]     fp32 block scales, token-minor (one float4 = 4 consecutive tokens)
-//   bsp [nb][Tp][16] int8: the 32-value sums bs_g = bsums[2g] + bsums[2g+1] as bl_g (bytes 0..7,
-//                    bs & 127) and bh_g (bytes 8..15, bs >> 7)
-// Tokens T..Tp-1 are written as zeros.
+//   bsp [nb][2][32][NTT][8] int8: the 32-value sums bs_g = bsums[2g] + bsums[2g+1] of token t as
+//                    bl_g = bs & 127 at [0][n][tt][g] and bh_g = bs >> 7 at [1][n][tt][g]: MFMA
+//                    lane (n, h) reads its 8 bytes of every token tile at once, lanes contiguous
+// Tokens T..Tp-1 are written as zeros. The block maximum is a DPP reduction within each row of
+// 16 lanes and then across the four rows; the group sums a DPP reduction over 8 lanes.
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict__ x, int64_t ldx, int nb, int T,
                                                          int Tp, int8_t *__restrict__ qs, float *__restrict__ ydT,
@@ -58,23 +62,29 @@ __global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict
     if (b >= nb) return;  // whole wavefront leaves together
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (tok < T) v = *(const float4 *)(x + (size_t)tok * ldx + (size_t)b * 256 + 4 * lane);
+    // the block maximum as the reference forms it (a NaN never replaces the running maximum:
+    // fmaxf keeps the other operand)
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+#define FGH_ROR(f, ctrl) __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, f), ctrl, 0xF, 0xF, false))
+    amax = fmaxf(amax, FGH_ROR(amax, 0x128));  // row_ror 8, 4, 2, 1: every lane of a row of 16
+    amax = fmaxf(amax, FGH_ROR(amax, 0x124));
+    amax = fmaxf(amax, FGH_ROR(amax, 0x122));
+    amax = fmaxf(amax, FGH_ROR(amax, 0x121));
+#undef FGH_ROR
+    auto lane_f = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, amax), l)); };
+    amax = fmaxf(fmaxf(lane_f(0), lane_f(16)), fmaxf(lane_f(32), lane_f(48)));
     const float d = amax / 127.0f;
     const float id = d > 0.0f ? 1.0f / d : 0.0f;
     const int q0 = q8_round(v.x * id), q1 = q8_round(v.y * id);
     const int q2 = q8_round(v.z * id), q3 = q8_round(v.w * id);
-    *(uint32_t *)(qs + ((((size_t)b * (Tp >> 5) + (tok >> 5)) * 8 + (lane >> 3)) * 32 + (tok & 31)) * 32 +
-                  4 * (lane & 7)) = pack_q(q0, q1, q2, q3);
-    int s = q0 + q1 + q2 + q3;  // 32-value group g = lanes 8g..8g+7
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
+    const int ntt = Tp >> 5, n = tok & 31, tt = tok >> 5, g = lane >> 3, h = (lane >> 2) & 1;
+    *(uint32_t *)(qs + (((((size_t)b * ntt + tt) * 8 + g) * 2 + h) * 32 + n) * 16 + 4 * (lane & 3)) =
+        pack_q(q0, q1, q2, q3);
+    const int s = sum8_i32(q0 + q1 + q2 + q3);  // 32-value group g = lanes 8g..8g+7
     if ((lane & 7) == 0) {
-        int8_t *p = bsp + ((size_t)b * Tp + tok) * 16;
-        p[lane >> 3] = (int8_t)(s & 127);
-        p[8 + (lane >> 3)] = (int8_t)(s >> 7);
+        int8_t *p = bsp + (size_t)b * Tp * 16 + (n * ntt + tt) * 8 + g;
+        p[0] = (int8_t)(s & 127);
+        p[32 * ntt * 8] = (int8_t)(s >> 7);
     }
     if (lane == 0) ydT[(size_t)b * Tp + tok] = d;
 }
@@ -82,30 +92,13 @@ __global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict
 // ---------------------------------------------------------------------------------------------
 // The GEMM kernel
 // ---------------------------------------------------------------------------------------------
-constexpr int GW_STAGE = 18432;  // LDS bytes of one weight stage: quants 16 KB + meta 2 KB
-
-// One workgroup's share of a weight stage (blocks 2s and 2s+1 of its 64 rows = 4 tiles), held by
-// thread tid: quant units u = tid + k * NT, u = ((blk * 4 + tile) * 2 + hh) * 64 + L, i.e. slot
-// (hh, L) of the tile layout (64 consecutive units read 1 KB contiguous), and for tid < 128 the
-// meta of (row tid % 64, blk tid / 64).
-template <int NT>
-struct WStage {
-    static constexpr int NU = 1024 / NT;
-    const uint8_t *src[NU];  // per unit: its address in block 0 of its tile
-    int slot[NU];            // per unit: its LDS slot
-    const uint8_t *msrc;     // the meta row's address in block 0 of its tile
-    uint4 q[NU], m;
-};
-
-// LDS stage layout: quants [blk][j][h][row 0..63] x 16 B (a fragment = 512 B contiguous per h),
-// meta at 16 KB: [blk][row] x 16 B. Row slots are XOR-swizzled with 2j (quants) and 4 blk (meta):
-// the eight threads of one 128-byte write phase hold rows 2m, 2m+1 x chunks j = 0..3 of one tile,
-// and the swizzle sends them to eight different bank quads; a fragment read stays a permutation
-// of 32 consecutive slots.
-__device__ __forceinline__ int gq_slot(int blk, int j, int h, int row) {
-    return ((blk * 4 + j) * 2 + h) * 64 + (row ^ (2 * j));
-}
-__device__ __forceinline__ int gm_slot(int blk, int row) { return 1024 + blk * 64 + (row ^ (blk << 2)); }
+// LDS stage of one step (blocks KQ s .. KQ s + KQ - 1), copied from the quantizer's output, where
+// those blocks are adjacent: the quants qs [KQ][NTT][8][32][32], and apart from them bsp [KQ][Tp][16]
+// followed by ydT [KQ][Tp] (each stage part its own LDS array, so the compiler can tell the stage
+// being read from the one being filled)
+__host__ __device__ constexpr int gs_q(int Tp, int KQ) { return KQ * Tp * 256; }
+__host__ __device__ constexpr int gs_e(int Tp, int KQ) { return KQ * Tp * 20; }
+__host__ __device__ constexpr int gs_yd(int Tp, int KQ) { return KQ * Tp * 16; }  // in the e part
 
 // the tile-layout address of (row R over all matrices, block 0): its tile and its row in the tile
 // (block b is b * gpm * 2304 further)
@@ -116,54 +109,63 @@ __device__ __forceinline__ const uint8_t *gemm_tile(const GemmArgs &a, int64_t R
     return a.W + ((size_t)mat * a.nb * a.gpm + (size_t)(r >> 4)) * 2304;
 }
 
-template <int NT>
-__device__ __forceinline__ void wstage_init(WStage<NT> &w, const GemmArgs &a, int64_t row0, int tid) {
-#pragma unroll
-    for (int k = 0; k < WStage<NT>::NU; ++k) {
-        const int u = tid + k * NT;
-        const int L = u & 63, hh = (u >> 6) & 1, tl = (u >> 7) & 3, blk = u >> 9, j = L & 3;
-        const int row = 16 * tl + (L >> 2);
-        int rr;
-        const uint8_t *T = gemm_tile(a, row0 + row, rr);
-        w.src[k] = T + 256 + 1024 * hh + 16 * (4 * rr + j);
-        w.slot[k] = gq_slot(blk, j, hh ^ (j >> 1), row);  // slot hh holds piece hh ^ (j >> 1)
-    }
-    int rr;
-    const uint8_t *T = gemm_tile(a, row0 + (tid & 63), rr);
-    w.msrc = T + 16 * rr;
-}
-
-template <int NT>
-__device__ __forceinline__ void wstage_load(WStage<NT> &w, int nb, size_t bstride, int s, int tid) {
-#pragma unroll
-    for (int k = 0; k < WStage<NT>::NU; ++k) {
-        const int blk = (tid + k * NT) >> 9;
-        w.q[k] = ld16(w.src[k] + (size_t)min(2 * s + blk, nb - 1) * bstride);
-    }
-    if (tid < 128) w.m = ld16(w.msrc + (size_t)min(2 * s + (tid >> 6), nb - 1) * bstride);
-}
-
-template <int NT>
-__device__ __forceinline__ void wstage_store(const WStage<NT> &w, uint8_t *buf, int tid) {
-#pragma unroll
-    for (int k = 0; k < WStage<NT>::NU; ++k) *(uint4 *)(buf + 16 * w.slot[k]) = w.q[k];
-    if (tid < 128) *(uint4 *)(buf + 16 * gm_slot(tid >> 6, tid & 63)) = w.m;
-}
-
-// one lane's activation operands of one block: group g (16 values of token 32 tt + l % 32) and
-// the token's 32-value sums as bytes (bl_0..7 or bh_0..7)
-struct ActOps {
-    uint4 av[8];
-    uint2 am;
+// one lane's weights of one block: pieces h (= lane / 32) of the four chunks of its row, and the
+// row's meta
+struct WOps {
+    uint4 q[4], m;
 };
-
-__device__ __forceinline__ void act_load(ActOps &o, const GemmArgs &a, int b, int tok, int h) {
-    // the block's 8 fragments of this token tile are 8 KB contiguous: two bases, immediate offsets
-    const int8_t *p = a.qs + (((size_t)b * (a.Tp >> 5) + (tok >> 5)) * 8 * 32 + (tok & 31)) * 32 + 16 * h;
+__device__ __forceinline__ void w_load(WOps &w, const uint8_t *T, size_t boff, int rr, int h) {
+    const uint8_t *p = T + boff;
 #pragma unroll
-    for (int g = 0; g < 8; ++g) o.av[g] = *(const uint4 *)(p + 1024 * g);
-    o.am = *(const uint2 *)(a.bsp + ((size_t)b * a.Tp + tok) * 16 + 8 * h);
+    for (int j = 0; j < 4; ++j) w.q[j] = ld16(p + 256 + 1024 * (h ^ (j >> 1)) + 16 * (4 * rr + j));
+    w.m = ld16(p + 16 * rr);
 }
+
+// The workgroup's copy of step s into an LDS stage: three contiguous runs of the quantizer's
+// output, moved by direct-to-LDS loads (global_load_lds_dwordx4: each lane's 16 bytes land at the
+// wavefront's LDS base + 16 * lane, so the stage takes no registers). Completion: vmcnt, then a
+// workgroup barrier. Tp tokens, KQ blocks, NT threads.
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+// One direct-to-LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane i's bytes land at
+// dst + 16 i; dst must be the same in every lane (it goes to M0). Written as inline assembly so
+// that the compiler does not treat the stage being filled as aliasing the stage being read (it
+// would wait for the loads before every LDS read); completion is awaited explicitly (s_dma_wait)
+// before the workgroup barrier that publishes the stage. Nothing else in these kernels uses M0.
+__device__ __forceinline__ void dma16(const void *src, uint8_t *dst) {
+    const unsigned base = (unsigned)(size_t)(lds_u8 *)dst;
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory");
+}
+template <int NT, int Tp, int KQ>
+__device__ __forceinline__ void s_dma(const GemmArgs &a, uint8_t *sq, uint8_t *se, int s, int tid, int wave) {
+    constexpr int QB = Tp * 16;               // 16-byte units of qs per block
+    constexpr int NQ = KQ * QB / NT;          // rounds for the step's blocks
+    constexpr int NE = KQ * Tp + KQ * Tp / 4;  // units of bsp (Tp per block) then ydT (Tp / 4)
+    static_assert(KQ * QB % NT == 0 && NE <= NT, "stage copy shape");
+    const int nb = a.nb;
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int u = tid + k * NT, blk = u / QB;
+        const int b = min(KQ * s + blk, nb - 1);  // blocks past the end: the last again (padding)
+        const int8_t *src = a.qs + (size_t)b * Tp * 256 + 16 * (u - blk * QB);
+        dma16(src, sq + 16 * (k * NT + 64 * wave));
+    }
+    if (64 * wave < NE) {  // uniform: wavefronts holding bsp / ydT units
+        const int e = tid;
+        if (e < NE) {
+            const void *src;
+            if (e < KQ * Tp) {
+                const int blk = e / Tp, b = min(KQ * s + blk, nb - 1);
+                src = a.bsp + ((size_t)b * Tp + (e - blk * Tp)) * 16;
+            } else {
+                const int e2 = e - KQ * Tp, blk = e2 / (Tp / 4), b = min(KQ * s + blk, nb - 1);
+                src = a.ydT + (size_t)b * Tp + 4 * (e2 - blk * (Tp / 4));
+            }
+            dma16(src, se + 1024 * wave);
+        }
+    }
+}
+// every direct-to-LDS load of this wavefront has landed (s_waitcnt vmcnt(0))
+__device__ __forceinline__ void s_dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 __device__ __forceinline__ v4i u4v(uint4 u) { return v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w}; }
 
@@ -173,152 +175,170 @@ __device__ __forceinline__ uint32_t bmul(uint32_t q, uint32_t f2) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// One 256-block of one wavefront: weights from the LDS stage (slice blk of the step), activations
-// from registers. live == false: a padding block (odd block counts): computed, weighted by zero,
-// not dumped.
-template <bool DUMP>
-__device__ __forceinline__ void gemm_block(const ActOps &o, const uint8_t *stage, int blk, int rs, int n, int h,
-                                           int tt, float (&acc)[16], const float *__restrict__ yds, int b, bool live,
-                                           int64_t row, const GemmArgs &a) {
-    const int row32 = rs * 32 + n;
-    const uint4 meta = *(const uint4 *)(stage + 16 * gm_slot(blk, row32));
-    uint4 pc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pc[j] = *(const uint4 *)(stage + 16 * gq_slot(blk, j, h, row32));
-    const Q4KScales sc = q4k_scales(meta.y, meta.z, meta.w);
+// One 256-block of one wavefront for all its NTT token tiles: weights from registers (prepared
+// once per group for every tile), activations from the LDS stage (slice blk). live == false: a
+// padding block (odd block counts): computed, weighted by zero, not dumped.
+template <int NTT, int KQ, bool DUMP>
+__device__ __forceinline__ void gemm_block(const WOps &w, const uint8_t *sq, const uint8_t *se, int blk, int n, int h,
+                                           float (&acc)[NTT][16], int b, bool live, int64_t row, const GemmArgs &a) {
+    const int Tp = NTT * 32;
+    const Q4KScales sc = q4k_scales(w.m.y, w.m.z, w.m.w);
     // a padding block contributes zero: its scales are zeroed once here
-    const float d = live ? fp16_bits_to_f32(meta.x & 0xFFFF) : 0.0f;
-    const float dmin = live ? fp16_bits_to_f32(meta.x >> 16) : 0.0f;
+    const float d = live ? fp16_bits_to_f32(w.m.x & 0xFFFF) : 0.0f;
+    const float dmin = live ? fp16_bits_to_f32(w.m.x >> 16) : 0.0f;
     // the split scale factors of the 8 groups as bytes: sh = sc >> 3, sl = sc & 7
     const uint32_t shb[2] = {(sc.sc_lo >> 3) & 0x07070707u, (sc.sc_hi >> 3) & 0x07070707u};
     const uint32_t slb[2] = {sc.sc_lo & 0x07070707u, sc.sc_hi & 0x07070707u};
-    // pass 0: q * sh over the block's 8 groups; pass 1 continues from 8 * Chi with q * sl
-    v16i ai;
+    // per group g (32 values, sub-block g): the lane's 16 nibbles (chunk g / 2, low or high) times
+    // sh (into Ch) and times sl (into Cl) against the activation fragment of every token tile
+    // (group g of tile tt: 1 KB contiguous per wavefront in the stage); isum = 8 Ch + Cl
+    const uint8_t *qs = sq + (size_t)blk * Tp * 256;
+    v16i ch[NTT], cl[NTT];
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
+    for (int g = 0; g < 8; ++g) {
+        const uint4 pc = w.q[g >> 1];
+        const uint32_t P[4] = {pc.x, pc.y, pc.z, pc.w};
+        // byte g of the factors into both 16-bit lanes (v_perm_b32; selector 0x0C = zero)
+        const uint32_t sel = 0x0C000C00u | (uint32_t)((g & 3) * 0x00010001);
+        const uint32_t fh = __builtin_amdgcn_perm(0u, shb[g >> 2], sel), fl = __builtin_amdgcn_perm(0u, slb[g >> 2], sel);
+        v4i bh, bl;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t P[4] = {pc[j].x, pc[j].y, pc[j].z, pc[j].w};
-#pragma unroll
-            for (int hn = 0; hn < 2; ++hn) {
-                const int g = 2 * j + hn;
-                // byte g of the factors into both 16-bit lanes (v_perm_b32; selector 0x0C = zero)
-                const uint32_t f = __builtin_amdgcn_perm(0u, pass == 0 ? shb[g >> 2] : slb[g >> 2],
-                                                         0x0C000C00u | (uint32_t)((g & 3) * 0x00010001));
-                v4i bw;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) bw[k] = (int)bmul(hn ? ((P[k] >> 4) & 0x0F0F0F0Fu) : (P[k] & 0x0F0F0F0Fu), f);
-                if (pass == 0 && g == 0) {
-                    const v16i z = {};
-                    ai = __builtin_amdgcn_mfma_i32_32x32x32_i8(u4v(o.av[g]), bw, z, 0, 0, 0);
-                } else {
-                    ai = __builtin_amdgcn_mfma_i32_32x32x32_i8(u4v(o.av[g]), bw, ai, 0, 0, 0);
-                }
-            }
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = (g & 1) ? ((P[k] >> 4) & 0x0F0F0F0Fu) : (P[k] & 0x0F0F0F0Fu);
+            bh[k] = (int)bmul(q, fh);
+            bl[k] = (int)bmul(q, fl);
         }
-        if (pass == 0) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) ai[v] <<= 3;
+        for (int tt = 0; tt < NTT; ++tt) {
+            const v4i av = u4v(*(const uint4 *)(qs + (((tt * 8 + g) * 2 + h) * 32 + n) * 16));
+            if (g == 0) {
+                const v16i z = {};
+                ch[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bh, z, 0, 0, 0);
+                cl[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bl, z, 0, 0, 0);
+            } else {
+                ch[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bh, ch[tt], 0, 0, 0);
+                cl[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bl, cl[tt], 0, 0, 0);
+            }
         }
     }
     // the row's eight mins as bytes; lanes 0-31 feed K slots 0..7 (bl), lanes 32-63 slots 8..15 (bh)
     const long mp = (long)(((uint64_t)sc.mn_hi << 32) | sc.mn_lo);
     const long b1 = h == 0 ? mp : 0L, b2 = h == 0 ? 0L : mp;
-    const v16i z = {};
-    const long ab = (long)(((uint64_t)o.am.y << 32) | o.am.x);
-    v16i ms = __builtin_amdgcn_mfma_i32_32x32x16_i8(ab, b2, z, 0, 0, 0);
+    // the lane's activation-sum bytes of every token tile in one read (8 bytes per tile)
+    const uint8_t *bsp = se + (size_t)blk * Tp * 16 + (h * 32 + n) * NTT * 8;
+    uint32_t amw[2 * NTT];
+    if (NTT == 2) {
+        const uint4 t = *(const uint4 *)bsp;
+        amw[0] = t.x; amw[1] = t.y; amw[2 % (2 * NTT)] = t.z; amw[3 % (2 * NTT)] = t.w;
+    } else {
+        const uint2 t = *(const uint2 *)bsp;
+        amw[0] = t.x; amw[1] = t.y;
+    }
+    const float *yds = (const float *)(se + gs_yd(Tp, KQ)) + blk * Tp;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) ms[v] <<= 7;
-    ms = __builtin_amdgcn_mfma_i32_32x32x16_i8(ab, b1, ms, 0, 0, 0);
-    float4 yd[4];
+    for (int tt = 0; tt < NTT; ++tt) {
+        const v16i z = {};
+        const long ab = (long)(((uint64_t)amw[2 * tt + 1] << 32) | amw[2 * tt]);
+        v16i ms = __builtin_amdgcn_mfma_i32_32x32x16_i8(ab, b2, z, 0, 0, 0);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) yd[k] = *(const float4 *)(yds + b * a.Tp + 32 * tt + 8 * k + 4 * h);
+        for (int v = 0; v < 16; ++v) ms[v] <<= 7;
+        ms = __builtin_amdgcn_mfma_i32_32x32x16_i8(ab, b1, ms, 0, 0, 0);
+        float4 yd[4];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int isum = ai[v], msum = ms[v];
-        const float4 q4 = yd[v >> 2];
-        const float ydv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
-        const float t = __builtin_fmaf(-dmin, (float)msum, d * (float)isum);
-        acc[v] = __builtin_fmaf(ydv, t, acc[v]);
-        if (DUMP) {
-            const int tok = 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3);
-            if (live && tok < a.T && row < a.nrows) {
-                const size_t i = ((size_t)tok * a.nrows + row) * a.nb + b;
-                a.dump_s[i] = isum;
-                a.dump_m[i] = msum;
+        for (int k = 0; k < 4; ++k) yd[k] = *(const float4 *)(yds + 32 * tt + 8 * k + 4 * h);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int isum = (ch[tt][v] << 3) + cl[tt][v], msum = ms[v];
+            const float4 q4 = yd[v >> 2];
+            const float ydv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+            const float t = __builtin_fmaf(-dmin, (float)msum, d * (float)isum);
+            acc[tt][v] = __builtin_fmaf(ydv, t, acc[tt][v]);
+            if (DUMP) {
+                const int tok = 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (live && tok < a.T && row < a.nrows) {
+                    const size_t i = ((size_t)tok * a.nrows + row) * a.nb + b;
+                    a.dump_s[i] = isum;
+                    a.dump_m[i] = msum;
+                }
             }
         }
     }
 }
 
-// NTW = token tiles (1 or 2). Wavefront w: rs = w & 1 (32-row slice), kh = (w >> 1) & 1 (even /
-// odd blocks), tt = w >> 2 (32-token tile). Step s covers blocks 2s (kh 0) and 2s + 1 (kh 1).
-template <int NTW, bool DUMP>
-__global__ __launch_bounds__(256 * NTW) void q4k_gemm_kernel(GemmArgs a) {
-    constexpr int NT = 256 * NTW;
-    // LDS: the block scales of every token (ydT, nb x Tp floats), then two weight stages (the
-    // reduction area reuses the first after the loop)
-    extern __shared__ __align__(16) float lds_g[];
-    float *yds = lds_g;
-    uint8_t *stage0 = (uint8_t *)(lds_g + (size_t)a.nb * a.Tp);
-    uint8_t *stage1 = stage0 + GW_STAGE;
+// NTT = token tiles (1 or 2), KQ = parts of the blocks (2 or 4). Wavefront w: rs = w & 1 (32-row
+// slice), kq = w >> 1 (blocks b = kq mod KQ); it computes its 32 rows for every token. Step s
+// covers blocks KQ s .. KQ s + KQ - 1: the weights go straight to registers (each wavefront its
+// own rows, one step ahead), the activations of the step's blocks by direct-to-LDS loads to an LDS
+// stage shared by the two row slices (double-buffered, one step ahead). The KQ partial sums are added at the end through LDS, in order.
+template <int NTT, int KQ, bool DUMP>
+__global__ __launch_bounds__(128 * KQ) void q4k_gemm_kernel(GemmArgs a) {
+    constexpr int NT = 128 * KQ, Tp = 32 * NTT;
+    __shared__ __align__(16) uint8_t q0[gs_q(Tp, KQ)], q1[gs_q(Tp, KQ)];
+    __shared__ __align__(16) uint8_t e0[gs_e(Tp, KQ)], e1[gs_e(Tp, KQ)];
     const int tid = threadIdx.x, l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rs = wave & 1, kh = (wave >> 1) & 1, tt = wave >> 2;
+    const int rs = wave & 1, kq = wave >> 1;
     const int n = l & 31, h = l >> 5;
-    const int nb = a.nb, nsteps = (nb + 1) >> 1;
+    const int nb = a.nb, nsteps = (nb + KQ - 1) / KQ;
     const int64_t row0 = (int64_t)blockIdx.x * 64;
     const int64_t row = row0 + 32 * rs + n;
-    const int tok = 32 * tt + n;
-
     const size_t bstride = (size_t)a.gpm * 2304;  // one block further in the tile layout
-    WStage<NT> ws;
-    wstage_init(ws, a, row0, tid);
-    wstage_load(ws, nb, bstride, 0, tid);
-    ActOps A, B;
-    act_load(A, a, min(kh, nb - 1), tok, h);
-    for (int i = tid; i < nb * a.Tp / 4; i += NT) ((float4 *)yds)[i] = ((const float4 *)a.ydT)[i];
-    wstage_store(ws, stage0, tid);
+    int rr;
+    const uint8_t *T = gemm_tile(a, row, rr);
+
+    WOps wa, wb;
+    w_load(wa, T, (size_t)min(kq, nb - 1) * bstride, rr, h);
+    s_dma<NT, Tp, KQ>(a, q0, e0, 0, tid, wave);
+    s_dma_wait();
     __syncthreads();
 
-    float acc[16];
+    float acc[NTT][16];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[tt][v] = 0.0f;
     for (int s = 0; s < nsteps; s += 2) {
-        // step s: stage0, set A; loads of step s + 1 (stage1, set B) in flight
-        wstage_load(ws, nb, bstride, min(s + 1, nsteps - 1), tid);
-        act_load(B, a, min(2 * (s + 1) + kh, nb - 1), tok, h);
+        // step s: stage0, weights wa; step s + 1 loads (stage1, wb) in flight
+        w_load(wb, T, (size_t)min(KQ * (s + 1) + kq, nb - 1) * bstride, rr, h);
+        s_dma<NT, Tp, KQ>(a, q1, e1, min(s + 1, nsteps - 1), tid, wave);
         __builtin_amdgcn_sched_barrier(0);
-        gemm_block<DUMP>(A, stage0, kh, rs, n, h, tt, acc, yds, min(2 * s + kh, nb - 1), 2 * s + kh < nb, row, a);
+        gemm_block<NTT, KQ, DUMP>(wa, q0, e0, kq, n, h, acc, min(KQ * s + kq, nb - 1), KQ * s + kq < nb, row, a);
         __builtin_amdgcn_sched_barrier(0);
-        wstage_store(ws, stage1, tid);
+        s_dma_wait();
         __syncthreads();
         if (s + 1 < nsteps) {  // uniform
-            // step s + 1: stage1, set B; loads of step s + 2 (stage0, set A) in flight
-            wstage_load(ws, nb, bstride, min(s + 2, nsteps - 1), tid);
-            act_load(A, a, min(2 * (s + 2) + kh, nb - 1), tok, h);
+            // step s + 1: stage1, weights wb; step s + 2 loads (stage0, wa) in flight
+            w_load(wa, T, (size_t)min(KQ * (s + 2) + kq, nb - 1) * bstride, rr, h);
+            s_dma<NT, Tp, KQ>(a, q0, e0, min(s + 2, nsteps - 1), tid, wave);
             __builtin_amdgcn_sched_barrier(0);
-            gemm_block<DUMP>(B, stage1, kh, rs, n, h, tt, acc, yds, min(2 * (s + 1) + kh, nb - 1),
-                             2 * (s + 1) + kh < nb, row, a);
+            gemm_block<NTT, KQ, DUMP>(wb, q1, e1, kq, n, h, acc, min(KQ * (s + 1) + kq, nb - 1),
+                                      KQ * (s + 1) + kq < nb, row, a);
             __builtin_amdgcn_sched_barrier(0);
-            wstage_store(ws, stage0, tid);
+            s_dma_wait();
             __syncthreads();
         }
     }
-    // odd-block half -> LDS (over the first stage: every wavefront is past its last read of it);
-    // the even half adds it (fixed order) and stores
-    float(*red)[2][16][64] = (float(*)[2][16][64])stage0;
-    if (kh == 1) {
+    // parts kq > 0 -> LDS (over the first stage: every wavefront is past its last read of it);
+    // part 0 adds them in order and stores
+    float(*red)[2][NTT][16][64] = (float(*)[2][NTT][16][64])q0;
+    if (kq > 0) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) red[tt][rs][v][l] = acc[v];
+        for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) red[kq - 1][rs][tt][v][l] = acc[tt][v];
     }
     __syncthreads();
-    if (kh == 0 && row < a.nrows) {
+    if (kq == 0 && row < a.nrows) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int tk = 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3);
-            if (tk < a.T) a.Y[(size_t)tk * a.ldy + row] = acc[v] + red[tt][rs][v][l];
-        }
+        for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int tk = 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3);
+                float y = acc[tt][v];
+#pragma unroll
+                for (int k = 1; k < KQ; ++k) y += red[k - 1][rs][tt][v][l];
+                if (tk < a.T) a.Y[(size_t)tk * a.ldy + row] = y;
+            }
     }
 }
 
@@ -329,20 +349,24 @@ hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp,
     return hipGetLastError();
 }
 
-size_t q4k_gemm_lds_bytes(int nb, int Tp) { return (size_t)nb * Tp * 4 + 2 * (size_t)GW_STAGE; }
+static int gemm_kq(int nb) { return nb >= 8 ? 4 : 2; }  // parts of the blocks per workgroup
+
+// the kernel's (static) LDS: two stages
+size_t q4k_gemm_lds_bytes(int nb, int Tp) { return 2 * (size_t)(gs_q(Tp, gemm_kq(nb)) + gs_e(Tp, gemm_kq(nb))); }
+
+template <int NTT, int KQ>
+static void gemm_launch(const GemmArgs &a, hipStream_t s) {
+    const dim3 grid((unsigned)((a.nrows + 63) / 64));
+    if (a.dump_s) q4k_gemm_kernel<NTT, KQ, true><<<grid, 128 * KQ, 0, s>>>(a);
+    else q4k_gemm_kernel<NTT, KQ, false><<<grid, 128 * KQ, 0, s>>>(a);
+}
 
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > 64 || a.Tp != (a.T > 32 ? 64 : 32) || a.nb < 1 || a.nrows < 1) return hipErrorInvalidValue;
-    const size_t lds = q4k_gemm_lds_bytes(a.nb, a.Tp);
-    if (lds > GEMM_LDS_MAX) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((a.nrows + 63) / 64));
-    if (a.Tp == 64) {
-        if (a.dump_s) q4k_gemm_kernel<2, true><<<grid, 512, lds, s>>>(a);
-        else q4k_gemm_kernel<2, false><<<grid, 512, lds, s>>>(a);
-    } else {
-        if (a.dump_s) q4k_gemm_kernel<1, true><<<grid, 256, lds, s>>>(a);
-        else q4k_gemm_kernel<1, false><<<grid, 256, lds, s>>>(a);
-    }
+    if (q4k_gemm_lds_bytes(a.nb, a.Tp) > GEMM_LDS_MAX) return hipErrorInvalidValue;
+    const int kq = gemm_kq(a.nb);
+    if (a.Tp == 64) kq == 4 ? gemm_launch<2, 4>(a, s) : gemm_launch<2, 2>(a, s);
+    else kq == 4 ? gemm_launch<1, 4>(a, s) : gemm_launch<1, 2>(a, s);
     return hipGetLastError();
 }
 
