@@ -9,10 +9,11 @@ fp32 N(0,1) vectors already resident in HBM. To measure HBM and not the 256 MB I
 steps rotate over COPIES distinct device copies of the layer (>= 512 MB in total).
 
 value  = whole-layer algorithmic bytes (weights + fp32 x in + fp32 y out) / step time, in GB/s.
-roofline: the dominant kernel is the Q4_K decode matvec at the gate shape (4096->14336); its
-         duration is the mean over back-to-back launches captured in one HIP graph and timed with
-         HIP events on the library's stream. A step replays one HIP graph of the layer's launches
-         (one per weight copy).
+roofline: the dominant kernel of the step is the Q4_K decode matvec launch of the FFN gate and up
+         projections together (4096->2x14336, one matvec_multi launch as the reference's forward
+         issues it); its duration is the mean over back-to-back launches captured in one HIP graph
+         and timed with HIP events on the library's stream. A step replays one HIP graph of the
+         layer's launches (one per weight copy).
 prefill: BASELINE config 4 (64 tokens x 4096 -> 14336, Q4_K) on the int8 MFMA GEMM, timed the
          same way, cold (rotating weights) and Infinity-Cache hot, as TOPS and fraction of 5 POPS.
 cpu_baseline: the reference's own CPU kernels (oracle/_ref, compiled from fastgguf.c) on the same
@@ -47,10 +48,14 @@ def algo_bytes(rows: int, cols: int) -> int:
     return rows * (cols // 256) * 144 + 4 * cols + 4 * rows
 
 
+# the gate and up projections in one launch: both matrices, x read once, both outputs
+GATE_UP_BYTES = 2 * algo_bytes(14336, 4096) - 4 * 4096
+
+
 def counted_traffic(kernel: str):
     """HBM bytes per launch measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
     profiles/ (scaled by a plain copy kernel of known size), or None if not recorded."""
-    path = os.path.join(ROOT, "profiles", "q4k_gate_decode_prefill_gemm_hbm_counters.md")
+    path = os.path.join(ROOT, "profiles", "q4k_gate_up_decode_prefill_gemm_hbm_counters.md")
     try:
         for line in open(path):
             f = line.split()
@@ -208,20 +213,21 @@ def main() -> int:
     yd = {n: be.dev_alloc(4 * r) for n, r, c in LAYER}
 
     if args.profile_kernels:
-        gate_bytes = algo_bytes(14336, 4096)
-        cbytes = (gate_bytes + 15) // 16 * 16
+        gu_bytes = GATE_UP_BYTES
+        cbytes = (gu_bytes + 15) // 16 * 16
         src, dst = be.dev_alloc(cbytes), be.dev_alloc(cbytes)
         Xp = S.activations(4096, 5, rows=64)
         xpd, ypd = be.dev_alloc(Xp.nbytes), be.dev_alloc(4 * 64 * 14336)
         be.h2d(xpd, Xp)
         for i in range(20):
-            be.matvec_dev(tensors[i % args.copies]["gate"], xd["x2"], yd["gate"])
+            t = tensors[i % args.copies]
+            be.matvec_multi_dev([t["gate"], t["up"]], xd["x2"], [yd["gate"], yd["up"]])
         for i in range(20):
             be.d2d(dst, src, cbytes)
         for i in range(20):
             be.matmul_dev(tensors[i % args.copies]["up"], xpd, ypd, 64)
         be.sync()
-        print(json.dumps({"profile_kernels": True, "gate_bytes": gate_bytes, "copy_bytes": cbytes,
+        print(json.dumps({"profile_kernels": True, "gate_up_bytes": gu_bytes, "copy_bytes": cbytes,
                           "gemm_ops": 2 * 64 * 4096 * 14336}), flush=True)
         be.close()
         return 0
@@ -290,7 +296,7 @@ def main() -> int:
         "o": (lambda i: be.matvec_dev(tensors[i % nc]["o"], xd["a"], yd["o"]), algo_bytes(4096, 4096)),
         "gate": (lambda i: be.matvec_dev(tensors[i % nc]["gate"], xd["x2"], yd["gate"]), algo_bytes(14336, 4096)),
         "gate+up": (lambda i: be.matvec_multi_dev([tensors[i % nc]["gate"], tensors[i % nc]["up"]], xd["x2"],
-                                                 [yd["gate"], yd["up"]]), 2 * algo_bytes(14336, 4096) - 4 * 4096),
+                                                 [yd["gate"], yd["up"]]), GATE_UP_BYTES),
         "down": (lambda i: be.matvec_dev(tensors[i % nc]["down"], xd["h"], yd["down"]), algo_bytes(4096, 14336)),
     }
     kernels = {}
@@ -298,11 +304,12 @@ def main() -> int:
         us = kernel_time(fn, args.kernel_reps)
         gbs = nbytes / (us * 1e-6) / 1e9
         kernels[n] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
-    g = kernels["gate"]
+    g = kernels["gate+up"]
     roofline = {"bound": "hbm", "achieved": g["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g["frac"],
-                "traffic": counted_traffic("gate"),
-                "kernel": "q4k_mv_kernel<repacked> (Q4_K decode matvec, gate 4096->14336)",
-                "bytes_per_launch": algo_bytes(14336, 4096), "us_per_launch": g["us"]}
+                "traffic": counted_traffic("gate_up"),
+                "kernel": "q4k_mv_kernel<repacked, 1 wavefront per 16-row tile> (Q4_K decode matvec, FFN gate + up "
+                          "4096->2x14336 in one launch)",
+                "bytes_per_launch": GATE_UP_BYTES, "us_per_launch": g["us"]}
 
     # prefill: 64 tokens x 4096 -> 14336 Q4_K on the int8 MFMA GEMM; one launch
     # = device Q8_K quantization of X + the GEMM. Cold: rotating over the 2 * COPIES distinct

@@ -152,14 +152,30 @@ def test_upload_refusals(backend):
     with pytest.raises(BackendError) as e:
         backend.upload(2, 256, np.zeros(8 * 144, np.uint8), rows=8)  # Q4_0: not on this path
     assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:  # 238 blocks: the quantized x no longer fits 64 KiB of LDS
+        backend.upload(S.T_Q4_K, 238 * 256, np.zeros(16 * 238 * 144, np.uint8), rows=16)
+    assert e.value.status == SKIP_TYPE
     info1 = backend.info()
-    assert info1["n_skip_type"] == info0["n_skip_type"] + 2
+    assert info1["n_skip_type"] == info0["n_skip_type"] + 3
     from fastgguf_amd.backend import Backend
     small = Backend(0, budget_bytes=1 << 20)
     with pytest.raises(BackendError) as e:
         small.upload(S.T_Q4_K, 4096, S.weights(S.T_Q4_K, 512, 4096, 1))  # 1.2 MB > 1 MB budget
     assert e.value.status == SKIP_MEM and small.info()["n_skip_mem"] == 1
     small.close()
+
+
+@pytest.mark.parametrize("order", [ORDER_REPACKED, ORDER_ROW])
+def test_widest_q4k_rows(backend, oracle, order):
+    """237 blocks (K = 60672), the widest Q4_K row the decode kernel accepts, in both orders."""
+    rows, cols = 24, 237 * 256
+    w = S.random_bytes_weights(S.T_Q4_K, rows, cols, 131)
+    x = S.activations(cols, 132)
+    tt = backend.upload(S.T_Q4_K, cols, w, order=order)
+    y = backend.matvec(tt, x)
+    yo = oracle.matvec(S.T_Q4_K, w, cols, x, O_RP if order == ORDER_REPACKED else O_ROW)
+    assert bits_equal(y, yo)
+    tt.free()
 
 
 def test_graph_replay_matches_eager(backend, oracle):
