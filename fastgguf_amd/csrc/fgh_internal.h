@@ -14,7 +14,9 @@ namespace fgh {
 // r; slice i of a 256-weight block is exactly the part of the block the reference's AVX2 fp32
 // accumulator lane i sums (its bytes 4i..4i+3 of every 32-byte chunk), so the per-lane integer
 // partials are the reference's lane partials, and the fp32 chains can follow its order.
-// Rows past the end of a matrix are zero-filled (d = 0) and never stored.
+// Rows past the end of a matrix are zero-filled (d = 0) and never stored. Tiles lie step-major:
+// step s (a block, or 4 blocks for Q8_0) of row tile t of matrix m is tile (m * steps + s) * tpm + t,
+// tpm = row tiles per matrix.
 //
 //   (Q4_K uses its own layout of 16-row tiles, 2304 B per (tile, block), described in fgh_q4k.hip)
 //   Q6_K tile, one block of 8 rows, 1680 B (= 8 x 210):
@@ -106,6 +108,24 @@ __device__ __forceinline__ int ubyte(uint32_t w, int k) { return (int)((w >> (8 
 
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *(const uint4 *)p; }
 __device__ __forceinline__ uint2 ld8(const uint8_t *p) { return *(const uint2 *)p; }
+
+// Loads from a wavefront-uniform base through a buffer resource: the base lives in scalar
+// registers and each lane adds its own 32-bit offset, so a walk that moves the base costs no
+// vector instructions per load; reads at or past nbytes return 0 (0x00020000: the gfx9 resource
+// word 3, 32-bit data format).
+typedef __amdgpu_buffer_rsrc_t BufRes;
+__device__ __forceinline__ BufRes buf_res(const uint8_t *base, uint32_t nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, (int)nbytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bld16(BufRes r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 bld8(BufRes r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t bld2(BufRes r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0); }
 
 // Q4_K 12-byte scales -> sc (4 bytes each in lo/hi words) and mins, the word form of
 // scale_min_k4 (fastgguf.c:466-472) that unpack_scales_k4 (1057-1067) also uses

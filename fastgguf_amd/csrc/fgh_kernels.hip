@@ -78,20 +78,20 @@ __global__ __launch_bounds__(256) void quant_q8_kernel(const float *__restrict__
 }
 
 // =============================================================================================
-// Upload-time re-layout of Q6_K / Q8_0: file-layout rows (n_mats x rows x row_bytes) -> tiles (Q4_K
-// has its own, fgh_q4k.hip). One thread per destination byte; padding rows and padding blocks are
-// zero.
+// Upload-time re-layout of Q6_K / Q8_0: file-layout rows (n_mats x rows x row_bytes) -> tiles in
+// step-major order, step tb of row tile gl of matrix m at (m * ntile + tb) * gpm + gl (Q4_K has its
+// own, fgh_q4k.hip). One thread per destination byte; padding rows and padding blocks are zero.
 // =============================================================================================
 __global__ void relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int type,
                                 int64_t rows, int nb, int ntile, int64_t gpm, int64_t total, int64_t row_bytes) {
     const int tile_bytes = type == T_Q6_K ? Q6K_TILE : Q80_TILE;
     for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
          o += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t t = o / tile_bytes;
+        const int64_t t = o / tile_bytes;  // = (m * ntile + tb) * gpm + gl
         const int ob = (int)(o - t * tile_bytes);
-        const int64_t g = t / ntile;
-        const int tb = (int)(t - g * ntile);
-        const int64_t m = g / gpm, gl = g - m * gpm;
+        const int64_t mt = t / gpm, gl = t - mt * gpm;
+        const int64_t m = mt / ntile;
+        const int tb = (int)(mt - m * ntile);
         int r, blk, byte;  // source row in group, block in row, byte in block
         if (type == T_Q6_K) {
             blk = tb;

@@ -1,52 +1,51 @@
 // fgh_matvec.hip - the decode matvec for Q6_K / Q8_0 on gfx950 (Q4_K has its own kernel in
-// fgh_q4k.hip): one persistent kernel per call that quantizes x itself and streams the weights.
+// fgh_q4k.hip, on the same plan).
 //
-//  * Quantization (once per workgroup and token): x (fp32, device) -> Q8_K or Q8 blocks in LDS,
-//    bit-exact with the reference's quantize_q8k / quantize_q8 (fastgguf.c:746-793). 16 lanes
-//    share one 256-value block (Q8_K) or 2 lanes one 32-value block (Q8); the block maximum is a
-//    DPP reduction, d = amax/127 and id = 1/d are IEEE divisions, q = round-half-even(x * id).
-//  * Matvec: workgroups loop over 8-row groups (the tile layout of fgh_internal.h); wavefront w
-//    owns rows 2w and 2w+1 of a group. A "step" is one 16-byte load per lane covering 4 tiles x
-//    2 rows x 8 slices (lane = slot*16 + row*8 + slice). Weight loads for the next chunk of steps
-//    are issued before the current chunk is computed, so each wavefront keeps several KB in
-//    flight. Lanes compute the exact integer partials of the reference's fp32 accumulator lanes
-//    (v_dot4_i32_i8) and park them, converted to fp32 (exact), in wavefront-private LDS; then 2
-//    or 16 lanes walk the tiles in ascending order applying the reference kernel's fused
-//    multiply-adds, so outputs are bit-identical to it. No workgroup barrier after quantization.
-//  * Up to 4 tensors of one type and width share one launch (matvec_multi, fastgguf.c:2552).
+// Tiles (fgh_internal.h) are 8 rows of one step: one block (Q6_K, 1680 B) or four blocks (Q8_0,
+// 1088 B). They lie step-major: step s of row tile t of matrix m at ((m * steps + s) * tpm + t) *
+// tile bytes (tpm = row tiles per matrix), so the wavefronts of a launch, all at about the same
+// step, read one contiguous stretch of HBM at a time.
+//
+// A wavefront owns one row tile; lane L = 8 r + i holds slice i of row r, which is exactly what
+// the reference's AVX2 fp32 accumulator lane i of that row sums. Every workgroup quantizes x into
+// LDS (bit-exact with quantize_q8k / quantize_q8, fastgguf.c:746-793) while the first steps of its
+// wavefronts' rings of R steps are in flight; activations are LDS broadcasts. Per step a lane
+// forms its exact integer lane partial (v_dot4_i32_i8, 16-bit scale products by v_dot2_i32_i16)
+// and advances its fp32 chain in registers in block order:
+//   Q8_0, dot_q8_0_q8 (fastgguf.c:891-902):   acc_i = fma(d * xd, s_i, acc_i), out = hsum8(acc)
+//   Q6_K, dot_q6_K_q8k (fastgguf.c:1232-1264): acc_i = fma(d * yd, lane_i, acc_i),
+//        cacc_p = fma(32 d yd, corr_p, cacc_p) in lanes i = p < 4, out = hsum8(acc) - hsum4(cacc)
+// so the outputs are bit-identical to the reference's row kernels. Short matrices split the steps
+// of a tile over S wavefronts: wavefront 0 runs its chains as it streams, the others park their
+// fp32 step records {d * yd, lane partials} in LDS, and wavefront 0 continues the chains over them.
+// Up to 4 tensors of one type and width share one launch (matvec_multi, fastgguf.c:2552).
 #include "fgh_internal.h"
 
 namespace fgh {
 
-constexpr int WAVES = 4;         // wavefronts per workgroup (256 threads)
-constexpr int CS = 4;            // steps per pipelined chunk
-constexpr int CT = 4 * CS;       // tiles per chunk
-
-// per (row, tile) record in wavefront LDS, in floats
-template <int TYPE, int ORDER>
-struct Rec {
-    // Q6_K: 8 lane partials, 4 correction lanes, d*yd (16 with padding); Q8_0: 4 blocks x 8 lane
-    // partials + 4 d*xd
-    static constexpr int N = TYPE == T_Q8_0 ? 36 : 16;
-};
-
-// LDS activation region, each array 16-byte aligned: qs at 0, d at act_off_d, sums at act_off_s
+// ---- LDS activations --------------------------------------------------------------------------
+// Q8_K (Q6_K): qs [nb][256] lane-permuted (position 32 i + 4 c holds element 32 c + 4 i, so lane
+//   i's 32 bytes are contiguous), d [nb] fp32, bs [nb][16] int16.
+// Q8 (Q8_0): per group of 4 blocks g, qs at 128 g: dword i of block 4 g + k at 128 g + 16 i + 4 k
+//   (a lane's 4 blocks in one 16-byte read); d [4 * groups] fp32.
 __host__ __device__ constexpr size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
-__host__ __device__ constexpr size_t act_off_d(int type, int nb) { return (size_t)nb * (type == T_Q8_0 ? 32 : 256); }
-__host__ __device__ constexpr size_t act_off_s(int type, int nb) { return align16(act_off_d(type, nb) + 4 * (size_t)nb); }
+__host__ __device__ constexpr int mv_steps(int type, int nb) { return type == T_Q8_0 ? (nb + 3) / 4 : nb; }
+__host__ __device__ constexpr size_t act_off_d(int type, int nb) {
+    return type == T_Q8_0 ? (size_t)128 * mv_steps(type, nb) : (size_t)256 * nb;
+}
+__host__ __device__ constexpr size_t act_off_s(int type, int nb) {
+    return align16(act_off_d(type, nb) + 4 * (size_t)(type == T_Q8_0 ? 4 * mv_steps(type, nb) : nb));
+}
 __host__ __device__ constexpr size_t act_lds_bytes(int type, int nb) {
-    return align16(act_off_s(type, nb) + (size_t)nb * (type == T_Q8_0 ? 4 : 32));
+    return type == T_Q8_0 ? act_off_s(type, nb) : align16(act_off_s(type, nb) + (size_t)nb * 32);
 }
+// fp32 records of one step of one tile (block split): lane partials, then d * yd per row
+__host__ __device__ constexpr size_t rec_bytes(int type) { return type == T_Q8_0 ? 64 * 16 + 8 * 16 : 64 * 8 + 8 * 4; }
 
-template <int TYPE, int ORDER>
-__host__ __device__ constexpr int wave_lds_bytes() {
-    return 2 * CT * Rec<TYPE, ORDER>::N * 4 + 2 * 12 * 4;  // records + final-combine scratch
-}
-
-__device__ __forceinline__ float dpp_ror_f(float v, int n) {
+__device__ __forceinline__ float ror_f32(float v, int n) {  // DPP row_ror:n within 16 lanes
     const int iv = __builtin_bit_cast(int, v);
     int r;
-    switch (n) {  // row_ror:n (rotate within a row of 16 lanes)
+    switch (n) {
     case 8: r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false); break;
     case 4: r = __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false); break;
     case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x122, 0xF, 0xF, false); break;
@@ -54,383 +53,385 @@ __device__ __forceinline__ float dpp_ror_f(float v, int n) {
     }
     return __builtin_bit_cast(float, r);
 }
+__device__ __forceinline__ float xor1_f32(float v) { return __builtin_bit_cast(float, dpp_xor1(__builtin_bit_cast(int, v))); }
+__device__ __forceinline__ float xor2_f32(float v) { return __builtin_bit_cast(float, dpp_xor2(__builtin_bit_cast(int, v))); }
 
-__device__ __forceinline__ int q_round(float v) {  // (int)lrintf(v) on x86 (see fgh_kernels.hip)
-    return fabsf(v) < 2147483648.0f ? (int)rintf(v) : 0;
-}
-__device__ __forceinline__ uint32_t pack4q(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);
-}
-
-// LDS activation region (offsets above). Q8_K: qs [nb][256] (lane-permuted as in
-// fgh_internal.h), d [nb], bs [nb][16] int16. Q8: qs [nb][32], d [nb], s16 [nb][2].
-template <int TYPE>
-__device__ void quantize_to_lds(const float *__restrict__ x, int nb, uint8_t *smem) {
-    const int tid = threadIdx.x;
-    if (TYPE == T_Q8_0) {
-        int8_t *qs = (int8_t *)smem;
-        float *dd = (float *)(smem + act_off_d(T_Q8_0, nb));
-        int16_t *s16 = (int16_t *)(smem + act_off_s(T_Q8_0, nb));
-        // 2 threads per 32-value block, 128 blocks per round
-        for (int rb = 0; rb < nb; rb += 128) {
-            const int b = rb + (tid >> 1), h = tid & 1;
-            const bool live = b < nb;
-            float v[16];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                float4 f = live ? *(const float4 *)(x + (size_t)b * 32 + 16 * h + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
-                v[4 * u] = f.x; v[4 * u + 1] = f.y; v[4 * u + 2] = f.z; v[4 * u + 3] = f.w;
-            }
-            float amax = 0.0f;
-#pragma unroll
-            for (int u = 0; u < 16; ++u) amax = fmaxf(amax, fabsf(v[u]));
-            amax = fmaxf(amax, __builtin_bit_cast(float, dpp_xor1(__builtin_bit_cast(int, amax))));
-            const float d = amax / 127.0f;
-            const float id = d > 0.0f ? 1.0f / d : 0.0f;
-            int s = 0;
-            uint32_t w[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int q0 = q_round(v[4 * u] * id), q1 = q_round(v[4 * u + 1] * id);
-                const int q2 = q_round(v[4 * u + 2] * id), q3 = q_round(v[4 * u + 3] * id);
-                s += q0 + q1 + q2 + q3;
-                w[u] = pack4q(q0, q1, q2, q3);
-            }
-            if (live) {
-                *(uint4 *)(qs + (size_t)b * 32 + 16 * h) = make_uint4(w[0], w[1], w[2], w[3]);
-                s16[2 * b + h] = (int16_t)s;
-                if (h == 0) dd[b] = d;
-            }
-        }
-    } else {
-        int8_t *qs = (int8_t *)smem;
-        float *dd = (float *)(smem + act_off_d(TYPE, nb));
-        int16_t *bs = (int16_t *)(smem + act_off_s(TYPE, nb));
-        // 16 threads per 256-value block, 16 blocks per round; thread tl holds values 16tl..16tl+15
-        for (int rb = 0; rb < nb; rb += 16) {
-            const int b = rb + (tid >> 4), tl = tid & 15;
-            const bool live = b < nb;
-            float v[16];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                float4 f = live ? *(const float4 *)(x + (size_t)b * 256 + 16 * tl + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
-                v[4 * u] = f.x; v[4 * u + 1] = f.y; v[4 * u + 2] = f.z; v[4 * u + 3] = f.w;
-            }
-            float amax = 0.0f;
-#pragma unroll
-            for (int u = 0; u < 16; ++u) amax = fmaxf(amax, fabsf(v[u]));
-            amax = fmaxf(amax, dpp_ror_f(amax, 8));
-            amax = fmaxf(amax, dpp_ror_f(amax, 4));
-            amax = fmaxf(amax, dpp_ror_f(amax, 2));
-            amax = fmaxf(amax, dpp_ror_f(amax, 1));
-            const float d = amax / 127.0f;
-            const float id = d > 0.0f ? 1.0f / d : 0.0f;
-            int s = 0;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int q0 = q_round(v[4 * u] * id), q1 = q_round(v[4 * u + 1] * id);
-                const int q2 = q_round(v[4 * u + 2] * id), q3 = q_round(v[4 * u + 3] * id);
-                s += q0 + q1 + q2 + q3;
-                // value 16tl + 4u = 32c + 4i (c = tl/2, i = 4(tl%2) + u) goes to position 32i + 4c
-                const int c = tl >> 1, i = 4 * (tl & 1) + u;
-                if (live) *(uint32_t *)(qs + (size_t)b * 256 + 32 * i + 4 * c) = pack4q(q0, q1, q2, q3);
-            }
-            if (live) {
-                bs[16 * b + tl] = (int16_t)s;
-                if (tl == 0) dd[b] = d;
-            }
-        }
-    }
-}
-
-// weights of one step for one lane: q = 16 quant bytes of its slice; m = the row's 16 meta bytes
-// (Q6_K: int8 scales); h = Q6_K qh words, or the row's 4 fp16 d (Q8_0);
-// e = Q6_K fp16 d of the row
-struct StepW {
-    uint4 q, m;
-    uint2 h;
-    uint32_t e;
+// Quantization in rounds over all 64 * WPG threads, 16 values per thread: Q8_K 16 threads per
+// 256-value block (4 WPG blocks a round), Q8 2 threads per 32-value block (32 WPG a round).
+// xq_load issues a round's loads (the first one before the weight loads, so that waiting for x
+// never waits for weights); xq_finish quantizes and stores the first round, then the rest.
+struct XVals {
+    float4 v[4];
 };
-
-template <int TYPE>
-__device__ __forceinline__ void load_step(const uint8_t *__restrict__ Wg, int tile, int slice, int r, StepW &s) {
-    constexpr int TILE = TYPE == T_Q6_K ? Q6K_TILE : Q80_TILE;
-    const uint8_t *t = Wg + (size_t)tile * TILE;
-    if (TYPE == T_Q6_K) {
-        s.q = ld16(t + 144 + 16 * slice);
-        s.h = ld8(t + 1168 + 8 * slice);
-        s.m = ld16(t + 16 * r);
-        s.e = *(const uint16_t *)(t + 128 + 2 * r);
-    } else {
-        s.q = ld16(t + 64 + 16 * slice);
-        s.h = ld8(t + 8 * r);
+template <int TYPE, int WPG>
+struct XQ {
+    static constexpr int TPB = TYPE == T_Q8_0 ? 2 : 16;           // threads per block
+    static constexpr int BPR = 64 * WPG / TPB;                     // blocks per round
+    static constexpr int BV = TYPE == T_Q8_0 ? 32 : 256;           // values per block
+};
+template <int TYPE, int WPG>
+__device__ __forceinline__ void xq_load(const float *__restrict__ x, int nb, int rb, XVals &xv) {
+    using Q = XQ<TYPE, WPG>;
+    const int b = rb + (int)threadIdx.x / Q::TPB, tl = (int)threadIdx.x % Q::TPB;
+    const float *p = x + (size_t)(b < nb ? b : 0) * Q::BV + 16 * tl;  // past the end: block 0, unused
+#pragma unroll
+    for (int u = 0; u < 4; ++u) xv.v[u] = *(const float4 *)(p + 4 * u);
+}
+template <int TYPE, int WPG>
+__device__ __forceinline__ void xq_store(int nb, int rb, const XVals &xv, uint8_t *act) {
+    using Q = XQ<TYPE, WPG>;
+    const int b = rb + (int)threadIdx.x / Q::TPB, tl = (int)threadIdx.x % Q::TPB;
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        v[4 * u] = xv.v[u].x; v[4 * u + 1] = xv.v[u].y; v[4 * u + 2] = xv.v[u].z; v[4 * u + 3] = xv.v[u].w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) amax = fmaxf(amax, fabsf(v[u]));
+    if (TYPE == T_Q8_0) {
+        amax = fmaxf(amax, xor1_f32(amax));
+    } else {  // the block's 16 threads are one DPP row
+        amax = fmaxf(amax, ror_f32(amax, 8));
+        amax = fmaxf(amax, ror_f32(amax, 4));
+        amax = fmaxf(amax, ror_f32(amax, 2));
+        amax = fmaxf(amax, ror_f32(amax, 1));
+    }
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    uint32_t w[4];
+    int s = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int q0 = q8_round(v[4 * u] * id), q1 = q8_round(v[4 * u + 1] * id);
+        const int q2 = q8_round(v[4 * u + 2] * id), q3 = q8_round(v[4 * u + 3] * id);
+        s += q0 + q1 + q2 + q3;
+        w[u] = pack_q(q0, q1, q2, q3);
+    }
+    if (b >= nb) return;
+    if (TYPE == T_Q8_0) {  // dwords 4 tl .. 4 tl + 3 of block b
+        uint8_t *g = act + (size_t)128 * (b >> 2) + 4 * (b & 3);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) *(uint32_t *)(g + 16 * (4 * tl + u)) = w[u];
+        if (tl == 0) ((float *)(act + act_off_d(TYPE, nb)))[b] = d;
+    } else {  // value 16 tl + 4 u = 32 c + 4 i (c = tl / 2, i = 4 (tl % 2) + u) -> position 32 i + 4 c
+        const int c = tl >> 1;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) *(uint32_t *)(act + (size_t)b * 256 + 32 * (4 * (tl & 1) + u) + 4 * c) = w[u];
+        ((int16_t *)(act + act_off_s(TYPE, nb)))[16 * b + tl] = (int16_t)s;
+        if (tl == 0) ((float *)(act + act_off_d(TYPE, nb)))[b] = d;
+    }
+}
+template <int TYPE, int WPG>
+__device__ __forceinline__ void xq_finish(const float *__restrict__ x, int nb, XVals &xv, uint8_t *act) {
+    using Q = XQ<TYPE, WPG>;
+    xq_store<TYPE, WPG>(nb, 0, xv, act);
+    for (int rb = Q::BPR; rb < nb; rb += Q::BPR) {
+        xq_load<TYPE, WPG>(x, nb, rb, xv);
+        xq_store<TYPE, WPG>(nb, rb, xv, act);
     }
 }
 
-template <int TYPE, int ORDER, bool DUMP>
-__global__ __launch_bounds__(256) void mv_kernel(MvArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int RN = Rec<TYPE, ORDER>::N;
-    constexpr int TILE = TYPE == T_Q6_K ? Q6K_TILE : Q80_TILE;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int slot = lane >> 4, r2 = (lane >> 3) & 1, i = lane & 7;
-    const int r = 2 * wave + r2;  // row within the 8-row group
-    const int tok = blockIdx.y;
-    const int nb = a.nb, ntile = a.ntile;
-    uint8_t *act = smem;
-    float *wrec = (float *)(smem + act_lds_bytes(TYPE, nb) + (size_t)wave * wave_lds_bytes<TYPE, ORDER>());
-    float *wfin = wrec + 2 * CT * RN;
+// ---- one step of one lane -----------------------------------------------------------------------
+// Q8_0: q = the lane's dword of each of the 4 blocks, d = its row's 4 fp16 scales.
+// Q6_K: q = 4 ql dwords (2 h + s), h = 2 qh dwords, sc = its row's 16 int8 scales, d = fp16 d.
+template <int TYPE>
+struct StepW;
+template <>
+struct StepW<T_Q8_0> {
+    uint4 q;
+    uint2 d;
+};
+template <>
+struct StepW<T_Q6_K> {
+    uint4 q, sc;
+    uint2 h;
+    uint32_t d;
+};
+// T: the tile (wavefront-uniform)
+__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q8_0> &w) {
+    const BufRes r = buf_res(T, Q80_TILE);
+    w.q = bld16(r, 64 + 16 * lane);
+    w.d = bld8(r, 8 * (lane >> 3));
+}
+__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q6_K> &w) {
+    const BufRes r = buf_res(T, Q6K_TILE);
+    w.q = bld16(r, 144 + 16 * lane);
+    w.h = bld8(r, 1168 + 8 * lane);
+    w.sc = bld16(r, 16 * (lane >> 3));
+    w.d = bld2(r, 128 + 2 * (lane >> 3));
+}
 
-    // groups of this workgroup: g = blockIdx.x + n * gridDim.x
-    const int64_t ng = a.groups > blockIdx.x ? (a.groups - 1 - blockIdx.x) / gridDim.x + 1 : 0;
-    const int nchunk = (ntile + CT - 1) / CT;
-    const int64_t nitems = ng * nchunk;
+// int16 pair (sext byte 1, sext byte 3) of x (v_perm_b32 selectors 8, 9: sign of bytes 1, 3)
+__device__ __forceinline__ uint32_t sx_b13(uint32_t x) { return __builtin_amdgcn_perm(x, x, 0x09030801u); }
+// int16 pair (sext byte 0, sext byte 1) of x (selector 10: the sign of byte 1 of x << 8)
+__device__ __forceinline__ uint32_t sx_b01(uint32_t x) { return __builtin_amdgcn_perm(x << 8, x, 0x08010A00u); }
 
-    auto tensor_of = [&](int64_t g, int &ti) {
-        ti = 0;
-        while (ti + 1 < a.nt && g >= a.t[ti + 1].gfirst) ++ti;
-        return g - a.t[ti].gfirst;
-    };
-    auto load_item = [&](int64_t it, StepW (&sw)[CS]) {
-        const int64_t g = blockIdx.x + (it / nchunk) * gridDim.x;
-        const int c = (int)(it % nchunk);
-        int ti;
-        const int64_t lg = tensor_of(g, ti);
-        const int64_t mg = a.sel ? (int64_t)a.sel[tok] * a.t[ti].gpm : 0;  // selected matrix (MoE)
-        const uint8_t *Wg = a.t[ti].W + (size_t)(mg + lg) * ntile * TILE;
-        // unconditional loads (slots past the end re-read the last tile and are not used), so
-        // the compiler can count outstanding loads and wait only for the chunk it computes
+// Q6_K lane partial of one block (lane i): sum over (h, k) of sc[8h + 2k + (i >= 4)] times the dot
+// of its 4 values (0..63, offset not removed) of chunk (h, k) with the activations; and the
+// correction partial of p = i & 3, (sc_2p bs_2p + sc_2p+1 bs_2p+1) + (sc_2p+8 bs_2p+8 +
+// sc_2p+9 bs_2p+9) (q6_corr_vec, fastgguf.c:1085-1088). Each 4-value dot is at most
+// 4 * 63 * 127 < 2^15 in magnitude: int16 pairs for v_dot2_i32_i16.
+__device__ __forceinline__ void q6_ints(const StepW<T_Q6_K> &w, const uint8_t *act, int nb, int b, int i, int &sum,
+                                        int &corr) {
+    const uint8_t *yb = act + (size_t)b * 256 + 32 * i;
+    const uint4 y0 = *(const uint4 *)yb, y1 = *(const uint4 *)(yb + 16);
+    const uint32_t yv[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+    const uint32_t A[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+    const uint32_t H[2] = {w.h.x, w.h.y};
+    const uint32_t S[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
+    const uint32_t M4 = 0x0F0F0F0Fu, M2 = 0x30303030u;
+    const int shl = i >= 4 ? 0 : 8;  // the lane's scales: bytes 1, 3 of (S_k << shl)
+    int s = 0;
 #pragma unroll
-        for (int k = 0; k < CS; ++k) {
-            const int tile = min(c * CT + 4 * k + slot, ntile - 1);
-            load_step<TYPE>(Wg, tile, 8 * r + i, r, sw[k]);
-        }
-    };
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t A0 = A[2 * h], A1 = A[2 * h + 1], Hh = H[h];
+        const uint32_t q0 = (A0 & M4) | ((Hh << 4) & M2), q1 = (A1 & M4) | ((Hh << 2) & M2);
+        const uint32_t q2 = ((A0 >> 4) & M4) | (Hh & M2), q3 = ((A1 >> 4) & M4) | ((Hh >> 2) & M2);
+        const int d0 = dot4((int)q0, (int)yv[4 * h], 0), d1 = dot4((int)q1, (int)yv[4 * h + 1], 0);
+        const int d2 = dot4((int)q2, (int)yv[4 * h + 2], 0), d3 = dot4((int)q3, (int)yv[4 * h + 3], 0);
+        s = dot2_i16(sx_b13(S[2 * h] << shl), pack_i16(d0, d1), s);
+        s = dot2_i16(sx_b13(S[2 * h + 1] << shl), pack_i16(d2, d3), s);
+    }
+    sum = s;
+    const int p = i & 3;
+    const int cs = 16 * (p & 1);
+    const uint32_t lo = ((p >> 1) ? S[1] : S[0]) >> cs, hi = ((p >> 1) ? S[3] : S[2]) >> cs;
+    const uint32_t *bq = (const uint32_t *)((const int16_t *)(act + act_off_s(T_Q6_K, nb)) + 16 * b + 2 * p);
+    corr = dot2_i16(sx_b01(lo), bq[0], 0) + dot2_i16(sx_b01(hi), bq[4], 0);
+}
 
-    StepW bufA[CS], bufB[CS];
-    if (nitems > 0) load_item(0, bufA);  // first weights in flight during quantization
+// the tensor of global tile g in a multi-tensor launch
+__device__ __forceinline__ int mv_tensor_of(const MvArgs &a, int64_t g) {
+    int ti = 0;
+#pragma unroll
+    for (int k = 1; k < 4; ++k)
+        if (k < a.nt && g >= a.t[k].gfirst) ti = k;
+    return ti;
+}
 
-    quantize_to_lds<TYPE>(a.x + (size_t)(tok / a.xdiv) * a.ldx, nb, act);
+// Workgroup = TPW tiles x S wavefronts per tile (wavefront ks of a tile takes its ks-th run of
+// ceil(steps / S) steps); grid = (tiles over all tensors / TPW, tokens).
+template <int TYPE, int R, int TPW, int S, bool DUMP>
+__global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
+    constexpr int WPG = TPW * S;
+    constexpr int TB = TYPE == T_Q6_K ? Q6K_TILE : Q80_TILE;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ts = wave / S, ks = wave - ts * S;
+    const int r = lane >> 3, i = lane & 7;
+    const int nb = a.nb, nst = a.ntile;
+    const int tok = blockIdx.y;
+    const int64_t tile = (int64_t)blockIdx.x * TPW + ts;
+    const bool live = tile < a.groups;
+    const int64_t tc = live ? tile : a.groups - 1;
+    const int ti = mv_tensor_of(a, tc);
+    const uint32_t lt = (uint32_t)(tc - a.t[ti].gfirst), tpm = (uint32_t)a.t[ti].gpm;
+    const uint32_t mi = (a.sel ? (uint32_t)a.sel[tok] : 0u) + lt / tpm, tt = lt % tpm;
+    const int nsw = (nst + S - 1) / S, s0 = ks * nsw;
+    const int nsl = max(0, min(nst, s0 + nsw) - s0), sl = max(nsl - 1, 0);
+    const size_t sstride = (size_t)tpm * TB;
+    const uint8_t *T0 = a.t[ti].W + (((size_t)mi * nst + min(s0, nst - 1)) * tpm + tt) * TB;
+
+    const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
+    XVals xv;
+    xq_load<TYPE, WPG>(x, nb, 0, xv);
+    StepW<TYPE> ring[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) step_load(T0 + (size_t)min(k, sl) * sstride, (uint32_t)lane, ring[k]);
+    uint8_t *act = smem;
+    xq_finish<TYPE, WPG>(x, nb, xv, act);
     __syncthreads();
 
-    const int8_t *aqs = (const int8_t *)act;
     const float *ad = (const float *)(act + act_off_d(TYPE, nb));
-    const int16_t *abs16 = (const int16_t *)(act + act_off_s(TYPE, nb));
+    const int64_t rows = a.t[ti].rows, mrow = (int64_t)tt * 8;
+    const int64_t obase = (int64_t)(lt / tpm) * rows;
+    const bool row_ok = live && mrow + r < rows;
+    // records of the wavefronts ks >= 1 (step s of the tile at s - nsw): lane partials, then fd
+    uint8_t *rec = smem + act_lds_bytes(TYPE, nb) + (size_t)ts * (nst - nsw) * rec_bytes(TYPE);
+    float acc = 0.0f, cacc = 0.0f;
 
-    // chain state: lanes 0..15 (r2, i)
-    float acc = 0.0f, macc = 0.0f;
-
-    auto process = [&](int64_t it, const StepW (&cur)[CS]) {
-        const int c = (int)(it % nchunk);
-        const int64_t g = blockIdx.x + (it / nchunk) * gridDim.x;
-        int ti;
-        const int64_t lg = tensor_of(g, ti);
-        const int64_t lrow = (lg % a.t[ti].gpm) * 8 + r;
-        const int64_t orow = (lg / a.t[ti].gpm) * a.t[ti].rows + lrow;
-        const bool row_ok = lrow < a.t[ti].rows;
-
-        // ---- integer phase: CS steps ----
+    auto step = [&](const StepW<TYPE> &w, int st) {
+        const bool chain = S == 1 || ks == 0;
+        uint8_t *rs = rec + (size_t)(st - nsw) * rec_bytes(TYPE);
+        if constexpr (TYPE == T_Q8_0) {
+            const uint4 y = *(const uint4 *)(act + (size_t)128 * st + 16 * i);
+            const float4 yd = *(const float4 *)(ad + 4 * st);
+            const int sd[4] = {dot4((int)w.q.x, (int)y.x, 0), dot4((int)w.q.y, (int)y.y, 0),
+                               dot4((int)w.q.z, (int)y.z, 0), dot4((int)w.q.w, (int)y.w, 0)};
+            const float fd[4] = {fp16_bits_to_f32(w.d.x & 0xFFFF) * yd.x, fp16_bits_to_f32(w.d.x >> 16) * yd.y,
+                                 fp16_bits_to_f32(w.d.y & 0xFFFF) * yd.z, fp16_bits_to_f32(w.d.y >> 16) * yd.w};
+            const int nbs = nb - 4 * st;  // blocks of this step (the last one may have fewer)
+            if (chain) {
+                if (nbs >= 4) {  // uniform
 #pragma unroll
-        for (int k = 0; k < CS; ++k) {
-            const int tile = c * CT + 4 * k + slot;
-            const int tl = 4 * k + slot;  // tile within the chunk
-            float *rec = wrec + ((size_t)r2 * CT + tl) * RN;
-            if (TYPE == T_Q6_K) {
-                if (c * CT + 4 * k < ntile) {
-                    const bool live = tile < ntile;
-                    const int b = live ? tile : 0;
-                    const uint4 yv0 = *(const uint4 *)(aqs + (size_t)b * 256 + 32 * i);
-                    const uint4 yv1 = *(const uint4 *)(aqs + (size_t)b * 256 + 32 * i + 16);
-                    const int yv[8] = {(int)yv0.x, (int)yv0.y, (int)yv0.z, (int)yv0.w,
-                                       (int)yv1.x, (int)yv1.y, (int)yv1.z, (int)yv1.w};
-                    const StepW &s = cur[k];
-                    const uint32_t sw[4] = {s.m.x, s.m.y, s.m.z, s.m.w};
-                    const uint32_t A[4] = {s.q.x, s.q.y, s.q.z, s.q.w};
-                    const uint32_t H[2] = {s.h.x, s.h.y};
-                    const int hi4 = i >= 4;
-                    int sum = 0;
+                    for (int k = 0; k < 4; ++k) acc = __builtin_fmaf(fd[k], (float)sd[k], acc);
+                } else {
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const uint32_t A0 = A[2 * h], A1 = A[2 * h + 1], Hh = H[h];
-                        const uint32_t M4 = 0x0F0F0F0Fu, M2 = 0x03030303u;
-                        const uint32_t qv[4] = {(A0 & M4) | ((Hh & M2) << 4), (A1 & M4) | (((Hh >> 2) & M2) << 4),
-                                                ((A0 >> 4) & M4) | (((Hh >> 4) & M2) << 4),
-                                                ((A1 >> 4) & M4) | (((Hh >> 6) & M2) << 4)};
-#pragma unroll
-                        for (int kk = 0; kk < 4; ++kk) {
-                            const int si = 8 * h + 2 * kk + hi4;
-                            sum += sbyte(sw[si >> 2], si & 3) * dot4((int)qv[kk], yv[4 * h + kk], 0);
-                        }
-                    }
-                    const int p = i & 3;
-                    const uint32_t *bp = (const uint32_t *)(abs16 + 16 * b);
-                    const uint32_t b01 = bp[p], b89 = bp[p + 4];
-                    const int s0 = sbyte(sw[(2 * p) >> 2], (2 * p) & 3), s1 = sbyte(sw[(2 * p + 1) >> 2], (2 * p + 1) & 3);
-                    const int s8 = sbyte(sw[(2 * p + 8) >> 2], (2 * p + 8) & 3), s9 = sbyte(sw[(2 * p + 9) >> 2], (2 * p + 9) & 3);
-                    const int mterm = (s0 * (int)(int16_t)(b01 & 0xFFFF) + s1 * (int)(int16_t)(b01 >> 16)) +
-                                      (s8 * (int)(int16_t)(b89 & 0xFFFF) + s9 * (int)(int16_t)(b89 >> 16));
-                    const float fd = fp16_bits_to_f32(s.e) * ad[b];
-                    if (live) {
-                        rec[i] = (float)sum;
-                        if (i < 4) rec[8 + i] = (float)mterm;
-                        if (i == 0) { rec[12] = fd; rec[13] = fd * 32.0f; }
-                    }
-                    if (DUMP) {
-                        const int ts = sum8_i32(sum), tm = sum4_i32(mterm);
-                        if (live && i == 0 && row_ok) {
-                            a.dump_s[orow * nb + b] = ts;
-                            a.dump_m[orow * nb + b] = tm;
-                        }
-                    }
+                    for (int k = 0; k < 3; ++k)
+                        if (k < nbs) acc = __builtin_fmaf(fd[k], (float)sd[k], acc);
                 }
-            } else {  // Q8_0: a tile is 4 blocks
-                if (c * CT + 4 * k < ntile) {
-                    const bool live = tile < ntile;
-                    const StepW &s = cur[k];
-                    const uint32_t qw[4] = {s.q.x, s.q.y, s.q.z, s.q.w};
-                    const uint32_t dw[4] = {s.h.x & 0xFFFF, s.h.x >> 16, s.h.y & 0xFFFF, s.h.y >> 16};
-#pragma unroll
-                    for (int bb = 0; bb < 4; ++bb) {
-                        const int b = 4 * tile + bb;
-                        const bool bl = live && b < nb;
-                        const int bsafe = bl ? b : 0;
-                        const int yw = *(const int *)(aqs + (size_t)bsafe * 32 + 4 * i);
-                        const int sdot = dot4((int)qw[bb], yw, 0);
-                        if (bl) {
-                            rec[8 * bb + i] = (float)sdot;
-                            if (i == 0) rec[32 + bb] = fp16_bits_to_f32(dw[bb]) * ad[bsafe];
-                        }
-                        if (DUMP) {
-                            const int ts = sum8_i32(sdot);
-                            if (bl && i == 0 && row_ok) {
-                                a.dump_s[orow * nb + b] = ts;
-                                a.dump_m[orow * nb + b] = 0;
-                            }
-                        }
-                    }
-                }
+            } else {
+                ((float4 *)rs)[lane] = make_float4((float)sd[0], (float)sd[1], (float)sd[2], (float)sd[3]);
+                if (i == 0) ((float4 *)(rs + 1024))[r] = make_float4(fd[0], fd[1], fd[2], fd[3]);
             }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // ---- chain phase: ascending tiles of this chunk ----
-        const int nct = min(CT, ntile - c * CT);
-        // (all reads first, then the ordered fused multiply-adds; records past nct are skipped)
-        if (TYPE == T_Q8_0) {
-            if (slot == 0) {
-                const float *rec = wrec + (size_t)r2 * CT * RN;
-                const int nblk = min(4 * nct, nb - 4 * c * CT);
+            if (DUMP) {
 #pragma unroll
-                for (int tl = 0; tl < CT; ++tl) {
-                    float lv[4], dv[4];
-#pragma unroll
-                    for (int bb = 0; bb < 4; ++bb) {
-                        lv[bb] = rec[tl * RN + 8 * bb + i];
-                        dv[bb] = rec[tl * RN + 32 + bb];
+                for (int k = 0; k < 4; ++k) {
+                    const int tsum = sum8_i32(sd[k]);
+                    if (row_ok && i == 0 && k < nbs) {
+                        const size_t di = (size_t)(obase + mrow + r) * nb + 4 * st + k;
+                        a.dump_s[di] = tsum;
+                        a.dump_m[di] = 0;
                     }
-#pragma unroll
-                    for (int bb = 0; bb < 4; ++bb)
-                        if (4 * tl + bb < nblk) acc = __builtin_fmaf(dv[bb], lv[bb], acc);
                 }
             }
         } else {
-            if (slot == 0) {
-                const float *rec = wrec + (size_t)r2 * CT * RN;
-#pragma unroll
-                for (int t0 = 0; t0 < CT; t0 += 4) {
-                    float lv[4], mv[4], dv[4], mdv[4];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        lv[u] = rec[(t0 + u) * RN + i];
-                        mv[u] = rec[(t0 + u) * RN + 8 + (i & 3)];
-                        dv[u] = rec[(t0 + u) * RN + 12];
-                        mdv[u] = rec[(t0 + u) * RN + 13];
-                    }
-#pragma unroll
-                    for (int u = 0; u < 4; ++u)
-                        if (t0 + u < nct) {
-                            acc = __builtin_fmaf(dv[u], lv[u], acc);
-                            macc = __builtin_fmaf(mdv[u], mv[u], macc);
-                        }
+            int sum, corr;
+            q6_ints(w, act, nb, st, i, sum, corr);
+            const float fd = fp16_bits_to_f32(w.d) * ad[st];
+            if (chain) {
+                acc = __builtin_fmaf(fd, (float)sum, acc);
+                cacc = __builtin_fmaf(fd * 32.0f, (float)corr, cacc);
+            } else {
+                ((float2 *)rs)[lane] = make_float2((float)sum, (float)corr);
+                if (i == 0) ((float *)(rs + 512))[r] = fd;
+            }
+            if (DUMP) {
+                const int tsum = sum8_i32(sum), tcorr = sum4_i32(corr);
+                if (row_ok && i == 0) {
+                    const size_t di = (size_t)(obase + mrow + r) * nb + st;
+                    a.dump_s[di] = tsum;
+                    a.dump_m[di] = tcorr;
                 }
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // ---- end of a group: combine the lanes in the reference's order and store ----
-        if (c == nchunk - 1) {
-            float *y = a.t[ti].y + (size_t)tok * a.ldy;
-            if (slot == 0) {
-                wfin[12 * r2 + i] = acc;
-                if (i < 4) wfin[12 * r2 + 8 + i] = macc;
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (slot == 0 && i == 0 && row_ok) {
-                const float *v = wfin + 12 * r2;
-                const float h8 = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
-                y[orow] = TYPE == T_Q8_0 ? h8 : h8 - ((v[8] + v[9]) + (v[10] + v[11]));
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            acc = 0.0f;
-            macc = 0.0f;
-        }
     };
-
-    // two register buffers, swapped by unrolling: the next item's loads are in flight while the
-    // current one is computed
-    for (int64_t it = 0; it < nitems; it += 2) {
-        if (it + 1 < nitems) load_item(it + 1, bufB);
-        process(it, bufA);
-        if (it + 1 >= nitems) break;
-        if (it + 2 < nitems) load_item(it + 2, bufA);
-        process(it + 1, bufB);
+    // whole rounds of R steps as straight-line code, refilling the ring; then the last nsl % R
+    int b0 = 0;
+    for (; b0 + R <= nsl; b0 += R) {
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            step(ring[k], s0 + b0 + k);
+            step_load(T0 + (size_t)min(b0 + k + R, sl) * sstride, (uint32_t)lane, ring[k]);
+        }
     }
+#pragma unroll
+    for (int k = 0; k < R - 1; ++k)
+        if (b0 + k < nsl) step(ring[k], s0 + b0 + k);  // uniform
+
+    if (S > 1) {
+        __syncthreads();
+        if (ks != 0) return;
+        // the chains over the other wavefronts' steps, CH steps at a time (all reads first)
+        constexpr int CH = TYPE == T_Q8_0 ? 4 : 8;
+        for (int st0 = nsw; st0 < nst; st0 += CH) {
+            const uint8_t *rs = rec + (size_t)(st0 - nsw) * rec_bytes(TYPE);
+            if constexpr (TYPE == T_Q8_0) {
+                float4 sv[CH], fv[CH];
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {  // records past the end are read but not used
+                    sv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE)))[lane];
+                    fv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE) + 1024))[r];
+                }
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    const int nbs = nb - 4 * (st0 + c);  // uniform
+                    if (nbs >= 4) {
+                        acc = __builtin_fmaf(fv[c].x, sv[c].x, acc);
+                        acc = __builtin_fmaf(fv[c].y, sv[c].y, acc);
+                        acc = __builtin_fmaf(fv[c].z, sv[c].z, acc);
+                        acc = __builtin_fmaf(fv[c].w, sv[c].w, acc);
+                    } else {
+                        if (nbs > 0) acc = __builtin_fmaf(fv[c].x, sv[c].x, acc);
+                        if (nbs > 1) acc = __builtin_fmaf(fv[c].y, sv[c].y, acc);
+                        if (nbs > 2) acc = __builtin_fmaf(fv[c].z, sv[c].z, acc);
+                    }
+                }
+            } else {
+                float2 sv[CH];
+                float fd[CH];
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    sv[c] = ((const float2 *)(rs + c * rec_bytes(TYPE)))[lane];
+                    fd[c] = ((const float *)(rs + c * rec_bytes(TYPE) + 512))[r];
+                }
+#pragma unroll
+                for (int c = 0; c < CH; ++c)
+                    if (st0 + c < nst) {  // uniform
+                        acc = __builtin_fmaf(fd[c], sv[c].x, acc);
+                        cacc = __builtin_fmaf(fd[c] * 32.0f, sv[c].y, cacc);
+                    }
+            }
+        }
+    }
+    // hsum8(acc) - hsum4(cacc) over the row's 8 lanes (fastgguf.c:797-806, 1089-1095), in lane i = 0
+    const float e = acc + __shfl_xor(acc, 4);  // v_i + v_i+4
+    const float f = e + xor1_f32(e);
+    const float h8 = f + xor2_f32(f);
+    float out = h8;
+    if (TYPE == T_Q6_K) {
+        const float g = cacc + xor1_f32(cacc);
+        out = h8 - (g + xor2_f32(g));
+    }
+    if (row_ok && i == 0) a.t[ti].y[(size_t)tok * a.ldy + obase + mrow + r] = out;
 }
 
-template <int TYPE, int ORDER>
-static size_t mv_lds_bytes(int nb) {
-    return act_lds_bytes(TYPE, nb) + (size_t)WAVES * wave_lds_bytes<TYPE, ORDER>();
+// LDS of a launch: the activations and, with a block split, the records of TPW tiles (plus the
+// steps that the last batch of the chain loop reads past the end)
+static size_t mv_lds(int type, int nb, int tpw, int s) {
+    const int nst = mv_steps(type, nb), nsw = (nst + s - 1) / s;
+    const int pad = type == T_Q8_0 ? 3 : 7;
+    return act_lds_bytes(type, nb) + (s > 1 ? ((size_t)tpw * (nst - nsw) + pad) * rec_bytes(type) : 0);
 }
+static int mv_tpw(int s) { return s == 1 ? 4 : s == 2 ? 2 : 1; }
 
 size_t matvec_lds_bytes(int type, int order, int nb) {
     if (type == T_Q4_K) return q4k_lds_bytes(order, nb);
-    if (type == T_Q6_K) return mv_lds_bytes<T_Q6_K, 0>(nb);
-    return mv_lds_bytes<T_Q8_0, 0>(nb);
+    return mv_lds(type, nb, 4, 1);
 }
 
-// persistent grid: as many workgroups as fit on the device at once (occupancy of this variant at
-// this LDS size), balanced so that every workgroup gets the same number of row groups (+-1)
-template <int TYPE, int ORDER, bool DUMP>
-static hipError_t launch_t(const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
-    const size_t lds = matvec_lds_bytes(TYPE, ORDER, a.nb);
-    if (lds > 65536) return hipErrorInvalidValue;
-    int per_cu = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mv_kernel<TYPE, ORDER, DUMP>, 256, lds);
-    if (e != hipSuccess) return e;
-    const int64_t max_wg = (int64_t)num_cu * (per_cu > 0 ? per_cu : 1);
-    int64_t wg = a.groups;
-    if (wg > max_wg) {
-        const int64_t per = (a.groups + max_wg - 1) / max_wg;
-        wg = (a.groups + per - 1) / per;
-    }
-    mv_kernel<TYPE, ORDER, DUMP><<<dim3((unsigned)wg, ntok), 256, lds, s>>>(a);
+template <int TYPE, int R, int TPW, int S>
+static hipError_t mv_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
+    const unsigned wg = (unsigned)((a.groups + TPW - 1) / TPW);
+    if (a.dump_s) mv_kernel<TYPE, R, TPW, S, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    else mv_kernel<TYPE, R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     return hipGetLastError();
+}
+template <int TYPE, int TPW, int S>
+static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
+    return R == 2 ? mv_launch<TYPE, 2, TPW, S>(a, ntok, lds, s) : mv_launch<TYPE, 4, TPW, S>(a, ntok, lds, s);
+}
+
+// Launch shape: launches of fewer than 768 tiles (tiles x tokens) split the steps of a tile over up
+// to 8 wavefronts, as many as keep the launch within 2048 wavefronts, each wavefront at 4 steps or
+// more (Q6_K: 2) and the records within LDS; tiles per workgroup 4, 2 or 1 for S = 1, 2 or more. Ring depth:
+// 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps, 4 otherwise.
+template <int TYPE>
+static hipError_t mv_launch_type(const MvArgs &a, int ntok, hipStream_t s) {
+    const int nb = a.nb, nst = mv_steps(TYPE, nb);
+    constexpr int SPW = TYPE == T_Q6_K ? 2 : 1;  // Q6_K steps are 4x the bytes of Q8_0's per row
+    const int64_t tiles = a.groups * ntok;
+    int S = 1;
+    if (tiles < 768)
+        while (S < 8 && tiles * 2 * S <= 2048 && nst >= 8 * S / SPW && mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S) <= 65536)
+            S *= 2;
+    const int R = nst < 32 && tiles * S >= 1024 ? 2 : 4;
+    const size_t lds = mv_lds(TYPE, nb, mv_tpw(S), S);
+    if (lds > 65536) return hipErrorInvalidValue;
+    switch (S) {
+    case 1: return mv_launch_r<TYPE, 4, 1>(R, a, ntok, lds, s);
+    case 2: return mv_launch_r<TYPE, 2, 2>(R, a, ntok, lds, s);
+    case 4: return mv_launch_r<TYPE, 1, 4>(R, a, ntok, lds, s);
+    default: return mv_launch_r<TYPE, 1, 8>(R, a, ntok, lds, s);
+    }
 }
 
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
-    const bool dump = a.dump_s != nullptr;
     if (type == T_Q4_K) return launch_q4k_matvec(order, a, ntok, num_cu, s);
-    if (type == T_Q6_K)
-        return dump ? launch_t<T_Q6_K, 0, true>(a, ntok, num_cu, s) : launch_t<T_Q6_K, 0, false>(a, ntok, num_cu, s);
-    if (type == T_Q8_0)
-        return dump ? launch_t<T_Q8_0, 0, true>(a, ntok, num_cu, s) : launch_t<T_Q8_0, 0, false>(a, ntok, num_cu, s);
+    if (type == T_Q6_K) return mv_launch_type<T_Q6_K>(a, ntok, s);
+    if (type == T_Q8_0) return mv_launch_type<T_Q8_0>(a, ntok, s);
     return hipErrorInvalidValue;
 }
 

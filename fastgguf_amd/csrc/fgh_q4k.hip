@@ -138,10 +138,12 @@ __device__ __forceinline__ void q8k_finish(XQuant<WPG> &q, const float *x, int n
 struct RbW {
     uint4 p0, p1, m;
 };
-__device__ __forceinline__ void rb_load(const uint8_t *T, int lane, RbW &w) {
-    w.p0 = ld16(T + 256 + 16 * lane);
-    w.p1 = ld16(T + 1280 + 16 * lane);
-    w.m = ld16(T + 16 * (lane >> 2));
+// T: the (tile, block), wavefront-uniform
+__device__ __forceinline__ void rb_load(const uint8_t *T, uint32_t lane, RbW &w) {
+    const BufRes r = buf_res(T, RB_BYTES);
+    w.p0 = bld16(r, 256 + 16 * lane);
+    w.p1 = bld16(r, 1280 + 16 * lane);
+    w.m = bld16(r, 16 * (lane >> 2));
 }
 
 // Per-lane constants of the scale extraction: chunk j, the shift selecting bytes 2(j & 1) and
