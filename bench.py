@@ -304,12 +304,25 @@ def main() -> int:
         us = kernel_time(fn, args.kernel_reps)
         gbs = nbytes / (us * 1e-6) / 1e9
         kernels[n] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    # the same byte count read by a plain streaming kernel (fgh_checksum_dev: 16-byte loads, four in
+    # flight per thread, a sum and nothing else), rotating over as many buffers as weight copies:
+    # the read rate this box delivers to a simple stream, beside the 8 TB/s peak
+    rbytes = (GATE_UP_BYTES + 15) // 16 * 16
+    rbufs = [be.dev_alloc(rbytes) for _ in range(nc)]
+    rus = kernel_time(lambda i: be.checksum_dev(rbufs[i % nc], rbytes, 0), args.kernel_reps)  # streaming pass only
+    for p in rbufs:
+        be.dev_free(p)
+    rgbs = rbytes / (rus * 1e-6) / 1e9
+    read_reference = {"kernel": "checksum_kernel (plain streaming read of the gate+up byte count)", "bytes": rbytes,
+                      "us": round(rus, 3), "GB/s": round(rgbs, 1), "frac": round(rgbs / HBM_PEAK_GBS, 4)}
+
     g = kernels["gate+up"]
     roofline = {"bound": "hbm", "achieved": g["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g["frac"],
                 "traffic": counted_traffic("gate_up"),
                 "kernel": "q4k_mv_kernel<repacked, 1 wavefront per 16-row tile> (Q4_K decode matvec, FFN gate + up "
                           "4096->2x14336 in one launch)",
-                "bytes_per_launch": GATE_UP_BYTES, "us_per_launch": g["us"]}
+                "bytes_per_launch": GATE_UP_BYTES, "us_per_launch": g["us"],
+                "frac_of_read_reference": round(g["GB/s"] / rgbs, 4)}
 
     # prefill: 64 tokens x 4096 -> 14336 Q4_K on the int8 MFMA GEMM; one launch
     # = device Q8_K quantization of X + the GEMM. Cold: rotating over the 2 * COPIES distinct
@@ -349,6 +362,7 @@ def main() -> int:
                    "weight_set_MB": round(args.copies * sum(r * (c // 256) * 144 for _, r, c in LAYER) / 1e6, 1),
                    "device": info["name"], "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
+        "read_reference": read_reference,
         "cpu_baseline": cpu,
         "kernels": kernels,
         "prefill": prefill,

@@ -28,7 +28,7 @@ EXPORTS = (
     "fgh_matvec", "fgh_matvec_multi", "fgh_matmul", "fgh_moe_ffn",
     "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matmul_dev", "fgh_moe_ffn_dev",
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
-    "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_sync",
+    "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
     "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_expf", "fgh_fp16_to_f32",
 )
@@ -82,6 +82,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_copy_h2d": (i32, [vp, vp, vp, u64]),
         "fgh_copy_d2h": (i32, [vp, vp, vp, u64]),
         "fgh_copy_d2d": (i32, [vp, vp, vp, u64]),
+        "fgh_checksum_dev": (i32, [vp, vp, u64, vp]),
         "fgh_sync": (i32, [vp]),
         "fgh_event_create": (i32, [vp, C.POINTER(vp)]),
         "fgh_event_record": (i32, [vp, vp]),
@@ -266,6 +267,20 @@ class Backend:
 
     def d2d(self, dst: int, src: int, nbytes: int):
         self._check(self.lib.fgh_copy_d2d(self.ctx, dst, src, nbytes))
+
+    def checksum_dev(self, src: int, nbytes: int, out: int):
+        """Wrapping 32-bit word sum of nbytes at src, into the device word at out (asynchronous)."""
+        self._check(self.lib.fgh_checksum_dev(self.ctx, src, nbytes, out))
+
+    def checksum(self, src: int, nbytes: int) -> int:
+        out = self.dev_alloc(16)
+        try:
+            self.checksum_dev(src, nbytes, out)
+            v = np.zeros(4, dtype=np.uint32)
+            self.d2h(v, out)
+            return int(v[0])
+        finally:
+            self.dev_free(out)
 
     def sync(self):
         self._check(self.lib.fgh_sync(self.ctx))

@@ -33,6 +33,7 @@ struct fgh_ctx {
     DevBuf gq, gy, gb;  // prompt-GEMM activations (launch_gemm_quant layout)
     DevBuf msel, mw, mg, mu, mh, md, mlog;  // MoE: selection, weights, gate / up / h / down outputs
     DevBuf mseg, mslot, mimx, mimh;         // MoE: slots grouped by expert, Q8_K images of x and h
+    DevBuf ck;                              // fgh_checksum_dev: per-workgroup partial sums
     int num_cu = 256;         // compute units (sizes the persistent decode grid)
     bool capturing = false;   // inside fgh_graph_begin / fgh_graph_end
 };
@@ -220,7 +221,7 @@ void fgh_close(fgh_ctx *c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->gy, &c->gb, &c->msel, &c->mw, &c->mg,
-                      &c->mu, &c->mh, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh})
+                      &c->mu, &c->mh, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck})
         if (b->p) (void)hipFree(b->p);
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -559,6 +560,17 @@ int fgh_copy_d2d(fgh_ctx *c, void *dst, const void *src, uint64_t bytes) {
     if (bytes) HIP_TRY(c, fgh::launch_copy16(src, dst, (int64_t)(bytes / 16), c->stream));
     return FGH_OK;
 }
+int fgh_checksum_dev(fgh_ctx *c, const void *src, uint64_t bytes, uint32_t *out) {
+    if (!c) return FGH_ERR_ARG;
+    if ((bytes && !src) || bytes % 16 != 0) return fail(c, FGH_ERR_ARG, "checksum_dev: null source or bytes % 16 != 0");
+    HIP_TRY(c, hipSetDevice(c->device));
+    const int np = fgh::checksum_parts(c->num_cu);
+    int rc;
+    if ((rc = grow(c, c->ck, (size_t)np * 4))) return rc;
+    HIP_TRY(c, fgh::launch_checksum(src, (int64_t)(bytes / 16), (uint32_t *)c->ck.p, np, out, c->stream));
+    return FGH_OK;
+}
+
 int fgh_sync(fgh_ctx *c) {
     if (!c) return FGH_ERR_ARG;
     NO_CAPTURE(c);

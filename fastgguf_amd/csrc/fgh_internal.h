@@ -156,6 +156,8 @@ hipError_t launch_relayout(const uint8_t *src, uint8_t *dst, int type, int64_t r
                            int64_t gpm, int64_t total, int64_t row_bytes, hipStream_t s);
 hipError_t launch_fp16(const uint16_t *h, float *out, int n, hipStream_t s);
 hipError_t launch_copy16(const void *src, void *dst, int64_t n16, hipStream_t s);
+int checksum_parts(int num_cu);  // workgroups of launch_checksum (words of its part buffer)
+hipError_t launch_checksum(const void *src, int64_t n16, uint32_t *part, int nparts, uint32_t *out, hipStream_t s);
 
 // decode matvec (fgh_matvec.hip): up to 4 tensors of one type, order and width in one launch
 struct MvT {

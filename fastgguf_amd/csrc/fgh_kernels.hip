@@ -169,6 +169,59 @@ hipError_t launch_copy16(const void *src, void *dst, int64_t n16, hipStream_t s)
     return hipGetLastError();
 }
 
+// Wrapping 32-bit sum of the little-endian words of n16 16-byte units in two launches: each
+// thread of the first (16 workgroups per CU) streams its grid-stride share eight units at a time
+// (eight 16-byte loads in flight) and each workgroup writes its part; the second adds the parts (integer wrapping addition
+// is associative: the result does not depend on the launch shape). The kernel boundary makes the
+// parts visible across the XCDs (a release inside the first kernel would write back L2 once per
+// workgroup).
+__device__ __forceinline__ uint32_t wg_sum256(uint32_t v, uint32_t *red) {
+    v += __shfl_xor(v, 32);
+    v += __shfl_xor(v, 16);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);  // row_ror 8, 4, 2, 1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xF, 0xF, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xF, 0xF, false);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+__global__ __launch_bounds__(256) void checksum_part_kernel(const uint4 *__restrict__ src, int64_t n16,
+                                                            uint32_t *__restrict__ part) {
+    __shared__ uint32_t red[4];
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t sum = 0;
+    for (; i + 7 * stride < n16; i += 8 * stride) {
+        uint4 a[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a[u] = src[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sum += (a[u].x + a[u].y) + (a[u].z + a[u].w);
+    }
+    for (; i < n16; i += stride) {
+        const uint4 a = src[i];
+        sum += (a.x + a.y) + (a.z + a.w);
+    }
+    const uint32_t ws = wg_sum256(sum, red);
+    if (threadIdx.x == 0) part[blockIdx.x] = ws;
+}
+__global__ __launch_bounds__(256) void checksum_final_kernel(const uint32_t *__restrict__ part, int n,
+                                                             uint32_t *__restrict__ out) {
+    __shared__ uint32_t red[4];
+    uint32_t v = 0;
+    for (int k = threadIdx.x; k < n; k += blockDim.x) v += part[k];
+    const uint32_t total = wg_sum256(v, red);
+    if (threadIdx.x == 0) *out = total;
+}
+int checksum_parts(int num_cu) { return 16 * num_cu; }  // (measured: the best plain stream at 66 MB)
+// out == nullptr: the streaming part only
+hipError_t launch_checksum(const void *src, int64_t n16, uint32_t *part, int nparts, uint32_t *out, hipStream_t s) {
+    checksum_part_kernel<<<nparts, 256, 0, s>>>((const uint4 *)src, n16, part);
+    if (out) checksum_final_kernel<<<1, 256, 0, s>>>(part, nparts, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_fp16(const uint16_t *h, float *out, int n, hipStream_t s) {
     fp16_kernel<<<(n + 255) / 256, 256, 0, s>>>(h, out, n);
     return hipGetLastError();

@@ -153,6 +153,13 @@ FGH_API int fgh_copy_d2h(fgh_ctx *ctx, void *dst_host, const void *src_dev, uint
 /* device-to-device copy by a plain streaming kernel (16-byte loads and stores), asynchronous on
  * the context stream; bytes % 16 == 0. Also the known-size kernel that calibrates HBM counters. */
 FGH_API int fgh_copy_d2d(fgh_ctx *ctx, void *dst_dev, const void *src_dev, uint64_t bytes);
+/* wrapping 32-bit sum of the little-endian 32-bit words of a device buffer (bytes % 16 == 0),
+ * written to *out_dev (device memory), asynchronous on the context stream: an integrity check of
+ * uploaded or copied data, and the plain streaming-read kernel that gives the read rate a
+ * matvec's weight stream is compared against (out_dev == NULL: only the streaming pass runs, its
+ * per-workgroup parts stay in the context). No counterpart in the reference (device-side helper).
+ * The first call allocates a small part buffer: make it once before graph capture. */
+FGH_API int fgh_checksum_dev(fgh_ctx *ctx, const void *src_dev, uint64_t bytes, uint32_t *out_dev);
 FGH_API int fgh_sync(fgh_ctx *ctx);
 /* HIP events recorded on the context stream */
 FGH_API int fgh_event_create(fgh_ctx *ctx, void **ev);

@@ -155,8 +155,14 @@ def test_upload_refusals(backend):
     with pytest.raises(BackendError) as e:  # 238 blocks: the quantized x no longer fits 64 KiB of LDS
         backend.upload(S.T_Q4_K, 238 * 256, np.zeros(16 * 238 * 144, np.uint8), rows=16)
     assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:  # the same for Q6_K past 224 blocks and Q8_0 past 1820
+        backend.upload(S.T_Q6_K, 225 * 256, np.zeros(8 * 225 * 210, np.uint8), rows=8)
+    assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:
+        backend.upload(S.T_Q8_0, 1821 * 32, np.zeros(8 * 1821 * 34, np.uint8), rows=8)
+    assert e.value.status == SKIP_TYPE
     info1 = backend.info()
-    assert info1["n_skip_type"] == info0["n_skip_type"] + 3
+    assert info1["n_skip_type"] == info0["n_skip_type"] + 5
     from fastgguf_amd.backend import Backend
     small = Backend(0, budget_bytes=1 << 20)
     with pytest.raises(BackendError) as e:
@@ -175,6 +181,18 @@ def test_widest_q4k_rows(backend, oracle, order):
     y = backend.matvec(tt, x)
     yo = oracle.matvec(S.T_Q4_K, w, cols, x, O_RP if order == ORDER_REPACKED else O_ROW)
     assert bits_equal(y, yo)
+    tt.free()
+
+
+@pytest.mark.parametrize("t,nb", [(S.T_Q6_K, 224), (S.T_Q8_0, 1820), (S.T_Q8_0, 1819)])
+def test_widest_q6k_q80_rows(backend, oracle, t, nb):
+    """The widest Q6_K (K = 57344) and Q8_0 (K = 58240) rows the decode kernel accepts, and a
+    Q8_0 width whose last 4-block step is ragged."""
+    rows, cols = 20, nb * (256 if t == S.T_Q6_K else 32)
+    w = S.random_bytes_weights(t, rows, cols, 133 + nb)
+    x = S.activations(cols, 134)
+    tt = backend.upload(t, cols, w)
+    assert bits_equal(backend.matvec(tt, x), oracle.matvec(t, w, cols, x, O_ROW))
     tt.free()
 
 
@@ -214,6 +232,18 @@ def test_graph_replay_matches_eager(backend, oracle):
         backend.dev_free(p)
     for t in ts.values():
         t.free()
+
+
+@pytest.mark.parametrize("nbytes", [0, 16, 4096 + 48, (1 << 24) + 16 * 7])
+def test_checksum_dev(backend, nbytes):
+    """The streaming checksum: the wrapping sum of the buffer's 32-bit words, against numpy."""
+    a = np.random.default_rng(nbytes).integers(0, 1 << 32, nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    src = backend.dev_alloc(max(nbytes, 16))
+    if nbytes:
+        backend.h2d(src, a)
+    want = int(np.sum(a, dtype=np.uint64) & 0xFFFFFFFF)
+    assert backend.checksum(src, nbytes) == want
+    backend.dev_free(src)
 
 
 def test_copy_d2d(backend):
