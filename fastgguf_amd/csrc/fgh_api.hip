@@ -123,7 +123,7 @@ static int quantize_dev(fgh_ctx *c, uint32_t type, int64_t cols, const float *x,
 // (device, stride ldx); y[i]: outputs of tensor i (token stride ldy)
 static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const float *x, int64_t ldx,
                          float *const *y, int64_t ldy, int ntok, int32_t *ds, int32_t *dm,
-                         const int32_t *sel = nullptr, int xdiv = 1) {
+                         const int32_t *sel = nullptr, int xdiv = 1, const float *xu = nullptr) {
     fgh::MvArgs a;
     memset(&a, 0, sizeof(a));
     int64_t g = 0;
@@ -133,6 +133,7 @@ static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const fl
     }
     a.sel = sel;
     a.xdiv = xdiv;
+    a.xu = xu;
     a.nt = n;
     a.groups = g;
     a.x = x;
@@ -442,9 +443,14 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
             (rc = matvec_launch(c, 1, &up, X, n_embd, yu, ff, (int)np, nullptr, nullptr, sel, k)))
             return rc;
     }
-    HIP_TRY(c, fgh::launch_moe_silu_mul(G, U, H, np * ff, c->stream));
     float *yd[1] = {D};
-    if ((rc = matvec_launch(c, 1, &down, H, ff, yd, n_embd, (int)np, nullptr, nullptr, sel, 1))) return rc;
+    if (down->type == FGH_T_Q4_K && down->order == FGH_ORDER_ROW) {
+        // h = silu(g) * u formed inside the down launch while it quantizes its input
+        if ((rc = matvec_launch(c, 1, &down, G, ff, yd, n_embd, (int)np, nullptr, nullptr, sel, 1, U))) return rc;
+    } else {
+        HIP_TRY(c, fgh::launch_moe_silu_mul(G, U, H, np * ff, c->stream));
+        if ((rc = matvec_launch(c, 1, &down, H, ff, yd, n_embd, (int)np, nullptr, nullptr, sel, 1))) return rc;
+    }
     HIP_TRY(c, fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, c->stream));
     return FGH_OK;
 }

@@ -179,6 +179,9 @@ struct MvArgs {
     // every tensor (launched with the tiles of one matrix) and activation row y / xdiv
     const int32_t *sel;
     int xdiv;
+    // Q4_K only: when set, the activation row is silu(x) * xu (silu_f, fastgguf.c:3118), formed
+    // while quantizing (the MoE down projection's input, never stored)
+    const float *xu;
 };
 size_t matvec_lds_bytes(int type, int order, int nb);  // Q6_K / Q8_0 (fgh_matvec.hip)
 // Q4_K (fgh_q4k.hip): its own tile layout and kernel

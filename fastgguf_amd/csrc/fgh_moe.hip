@@ -12,67 +12,114 @@
 
 namespace fgh {
 
-// one wavefront per token; n_expert <= 64 * MOE_EPL
+// one wavefront per token; n_expert <= 64 * MOE_EPL. Lane l holds experts 64 s + l (slot s) in
+// registers; the maxima are DPP / lane-read reductions (no LDS, no barrier) and only the
+// reference's sequential softmax sum goes through LDS (read back four floats at a time).
 constexpr int MOE_EPL = 8;
+
+// an int whose signed order is the float order (for non-NaN floats)
+__device__ __forceinline__ int f32_ord(float f) {
+    const int b = __builtin_bit_cast(int, f);
+    return b < 0 ? b ^ 0x7FFFFFFF : b;
+}
+// maximum over the 64 lanes, in every lane: within rows of 16 by DPP, then the four row results
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));  // row_mirror
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+__device__ __forceinline__ float wave_fmax(float v) {  // fmaxf over the lanes (a NaN lane loses)
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+    auto rl = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+    return fmaxf(fmaxf(rl(0), rl(16)), fmaxf(rl(32), rl(48)));
+}
 
 __global__ __launch_bounds__(64) void moe_route_kernel(const float *__restrict__ logits, int n_expert, int k,
                                                        int32_t *__restrict__ sel, float *__restrict__ w) {
-    __shared__ float p[64 * MOE_EPL];
-    __shared__ float wl[64];
+    __shared__ __align__(16) float ps[64 * MOE_EPL];
     const int t = blockIdx.x, lane = threadIdx.x;
+    const int ns = (n_expert + 63) >> 6;  // slots in use (uniform)
     const float *lg = logits + (size_t)t * n_expert;
-    // max (order-independent, exact)
+    float pv[MOE_EPL];
+    // max: the reference keeps the larger of each value and the running max (starting at -inf),
+    // which fmaxf does, NaN never winning; the same value in every lane
     float mx = -INFINITY;
-    for (int i = lane; i < n_expert; i += 64) mx = fmaxf(mx, lg[i]);
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    for (int i = lane; i < n_expert; i += 64) p[i] = expf_ref(lg[i] - mx);
-    __syncthreads();
-    // the reference's sequential sum, then its scaling by the reciprocal
-    __shared__ float inv_s;
-    if (lane == 0) {
-        float sum = 0.0f;
-        for (int i = 0; i < n_expert; ++i) sum += p[i];
-        inv_s = sum > 0.0f ? 1.0f / sum : 0.0f;
-        if (!(sum > 0.0f)) inv_s = -1.0f;  // marker: leave p unscaled
+    for (int s = 0; s < MOE_EPL; ++s) {
+        const int i = 64 * s + lane;
+        pv[s] = s < ns && i < n_expert ? lg[i] : -INFINITY;
+        mx = fmaxf(mx, pv[s]);
     }
-    __syncthreads();
-    const float inv = inv_s;
-    if (inv >= 0.0f)
-        for (int i = lane; i < n_expert; i += 64) p[i] *= inv;
-    __syncthreads();
-    // top-k by repeated argmax: the first index holding the largest value (v > best, scanning up)
-    float wsum = 0.0f;
-    for (int j = 0; j < k; ++j) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int i = lane; i < n_expert; i += 64)
-            if (p[i] > bv) {  // per lane: ascending indices, so the first maximum is kept
-                bv = p[i];
-                bi = i;
-            }
+    mx = wave_fmax(mx);
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
+    for (int s = 0; s < MOE_EPL; ++s)
+        if (s < ns) {
+            pv[s] = expf_ref(pv[s] - mx);
+            ps[64 * s + lane] = pv[s];
+        }
+    __syncthreads();
+    // the reference's sequential sum, then its scaling by the reciprocal (skipped unless sum > 0)
+    float sum = 0.0f;
+    if (lane == 0) {
+        const float4 *p4 = (const float4 *)ps;
+        int i = 0;
+        for (; i + 4 <= n_expert; i += 4) {
+            const float4 q = p4[i >> 2];
+            sum += q.x;
+            sum += q.y;
+            sum += q.z;
+            sum += q.w;
+        }
+        for (; i < n_expert; ++i) sum += ps[i];
+    }
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 0));
+    if (sum > 0.0f) {
+        const float inv = 1.0f / sum;
+#pragma unroll
+        for (int s = 0; s < MOE_EPL; ++s) pv[s] *= inv;
+    }
+    // top-k by repeated argmax: candidates are values > -inf (a NaN never is), the first index of
+    // the largest wins, and with no candidate index 0 is taken; the chosen value becomes -1
+    float wsum = 0.0f, wl = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        int key[MOE_EPL], m = INT_MIN;
+#pragma unroll
+        for (int s = 0; s < MOE_EPL; ++s) {
+            const bool cand = s < ns && 64 * s + lane < n_expert && pv[s] > -INFINITY;
+            key[s] = cand ? f32_ord(pv[s]) : INT_MIN;
+            m = max(m, key[s]);
+        }
+        m = wave_max_i32(m);
+        int bi = m == INT_MIN ? 0 : -1;  // uniform
+#pragma unroll
+        for (int s = 0; s < MOE_EPL; ++s)
+            if (bi < 0 && s < ns) {  // uniform: the lowest slot holding the maximum
+                const uint64_t hit = __ballot(key[s] == m);
+                if (hit) bi = 64 * s + (int)__builtin_ctzll(hit);
             }
+        const int bl = bi & 63, bs = bi >> 6;
+        float pick = 0.0f;
+#pragma unroll
+        for (int s = 0; s < MOE_EPL; ++s)
+            if (s == bs) pick = pv[s];
+        const float pvj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pick), bl));
+        if (lane == bl) {
+#pragma unroll
+            for (int s = 0; s < MOE_EPL; ++s)
+                if (s == bs) pv[s] = -1.0f;
         }
-        if (bi == 0x7fffffff) bi = 0;  // every value -inf or NaN: argmax_f returns 0
-        const float pv = p[bi];
-        __syncthreads();
-        if (lane == 0) {
-            sel[(size_t)t * k + j] = bi;
-            wl[j] = pv;
-            p[bi] = -1.0f;
-        }
-        wsum += pv;  // every lane keeps the same sequential sum
-        __syncthreads();
+        if (lane == j) wl = pvj;
+        if (lane == 0) sel[(size_t)t * k + j] = bi;
+        wsum += pvj;  // every lane keeps the same sequential sum
     }
     if (wsum < 6.103515625e-5f) wsum = 6.103515625e-5f;
-    if (lane < k) w[(size_t)t * k + lane] = wl[lane] / wsum;
+    if (lane < k) w[(size_t)t * k + lane] = wl / wsum;
 }
 
 // Groups the n_tok * k (token, selected expert) slots by expert, for the grouped expert kernels:
@@ -142,7 +189,18 @@ __global__ void moe_combine_kernel(const float *__restrict__ d, const float *__r
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_embd) return;
     float s = 0.0f;
-    for (int j = 0; j < k; ++j) s = __builtin_fmaf(w[(size_t)t * k + j], d[((size_t)t * k + j) * n_embd + i], s);
+    for (int j0 = 0; j0 < k; j0 += 8) {  // 8 experts' loads in flight, then their fmas in order
+        float dv[8], wv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int jj = min(j0 + u, k - 1);
+            wv[u] = w[(size_t)t * k + jj];
+            dv[u] = d[((size_t)t * k + jj) * n_embd + i];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (j0 + u < k) s = __builtin_fmaf(wv[u], dv[u], s);
+    }
     y[(size_t)t * ldy + i] = s;
 }
 

@@ -113,23 +113,50 @@ __device__ __forceinline__ void q8k_store(int nb, int rb, const XRound &xr, uint
 
 // Quantizes x (nb blocks) into act with all 64 * WPG threads: q8k_begin issues the loads of the
 // first two rounds (before the caller's weight loads), q8k_finish the rest and the stores.
-template <int WPG>
+// x = silu(x) * u, value by value (silu_f, fastgguf.c:3118: x / (1 + expf(-x)))
+__device__ __forceinline__ void xr_silu_mul(XRound &xr, const XRound &ur) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float4 &g = xr.v[q];
+        const float4 uu = ur.v[q];
+        g.x = g.x / (1.0f + expf_ref(-g.x)) * uu.x;
+        g.y = g.y / (1.0f + expf_ref(-g.y)) * uu.y;
+        g.z = g.z / (1.0f + expf_ref(-g.z)) * uu.z;
+        g.w = g.w / (1.0f + expf_ref(-g.w)) * uu.w;
+    }
+}
+
+// SILU: the row quantized is silu(x) * u (u: a second row of the same shape)
+template <int WPG, bool SILU = false>
 struct XQuant {
     static constexpr int XB = 4 * WPG;  // blocks per round
     XRound r0, r1;
+    XRound u0, u1;  // SILU only (unused registers otherwise are removed by the compiler)
 };
-template <int WPG>
-__device__ __forceinline__ void q8k_begin(XQuant<WPG> &q, const float *x, int nb) {
+template <int WPG, bool SILU>
+__device__ __forceinline__ void q8k_begin(XQuant<WPG, SILU> &q, const float *x, const float *u, int nb) {
     q8k_load(x, nb, 0, q.r0);
-    if (nb > XQuant<WPG>::XB) q8k_load(x, nb, XQuant<WPG>::XB, q.r1);  // uniform
+    if (SILU) q8k_load(u, nb, 0, q.u0);
+    if (nb > XQuant<WPG, SILU>::XB) {  // uniform
+        q8k_load(x, nb, XQuant<WPG, SILU>::XB, q.r1);
+        if (SILU) q8k_load(u, nb, XQuant<WPG, SILU>::XB, q.u1);
+    }
 }
-template <int WPG>
-__device__ __forceinline__ void q8k_finish(XQuant<WPG> &q, const float *x, int nb, uint8_t *act) {
-    constexpr int XB = XQuant<WPG>::XB;
+template <int WPG, bool SILU>
+__device__ __forceinline__ void q8k_finish(XQuant<WPG, SILU> &q, const float *x, const float *u, int nb, uint8_t *act) {
+    constexpr int XB = XQuant<WPG, SILU>::XB;
+    if (SILU) xr_silu_mul(q.r0, q.u0);
     q8k_store(nb, 0, q.r0, act);
-    if (nb > XB) q8k_store(nb, XB, q.r1, act);
+    if (nb > XB) {
+        if (SILU) xr_silu_mul(q.r1, q.u1);
+        q8k_store(nb, XB, q.r1, act);
+    }
     for (int rb = 2 * XB; rb < nb; rb += XB) {  // rows longer than 2 * XB blocks
         q8k_load(x, nb, rb, q.r0);
+        if (SILU) {
+            q8k_load(u, nb, rb, q.u0);
+            xr_silu_mul(q.r0, q.u0);
+        }
         q8k_store(nb, rb, q.r0, act);
     }
 }
@@ -248,7 +275,7 @@ __device__ __forceinline__ int q4_tensor_of(const MvArgs &a, int64_t g) {
 
 // Decode matvec. Workgroup = TPW tiles x S wavefronts per tile (wavefront ks of a tile takes its
 // ks-th run of ceil(nb / S) blocks); grid = (tiles over all tensors / TPW, tokens).
-template <int ORDER, int R, int TPW, int S, bool DUMP>
+template <int ORDER, int R, int TPW, int S, bool DUMP, bool SILU = false>
 __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     static_assert(ORDER == 1 || S == 1, "the row order keeps its chains in registers: no block split");
     constexpr int WPG = TPW * S;
@@ -272,14 +299,15 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
 
     // (1) x for the first quantization rounds, then (2) the ring's first R steps
     const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
-    XQuant<WPG> xq;
-    q8k_begin(xq, x, nb);
+    const float *xu = SILU ? a.xu + (size_t)(tok / a.xdiv) * a.ldx : nullptr;
+    XQuant<WPG, SILU> xq;
+    q8k_begin(xq, x, xu, nb);
     RbW ring[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) rb_load(T0 + (size_t)min(r, bl) * bstride, lane, ring[r]);
     // (3) quantize x into LDS while the weights are in flight
     uint8_t *act = smem;
-    q8k_finish(xq, x, nb, act);
+    q8k_finish(xq, x, xu, nb, act);
     __syncthreads();
 
     const int64_t mrow = (int64_t)tt * RB_ROWS;  // first row of the tile in its matrix
@@ -366,8 +394,17 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
 template <int ORDER, int R, int TPW, int S>
 static hipError_t q4_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
     const unsigned wg = (unsigned)((a.groups + TPW - 1) / TPW);
-    if (a.dump_s) q4k_mv_kernel<ORDER, R, TPW, S, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
-    else q4k_mv_kernel<ORDER, R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    if (a.dump_s) {
+        q4k_mv_kernel<ORDER, R, TPW, S, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+        return hipGetLastError();
+    }
+    if constexpr (ORDER == 0 && S == 1) {
+        if (a.xu) {
+            q4k_mv_kernel<ORDER, R, TPW, S, false, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+            return hipGetLastError();
+        }
+    }
+    q4k_mv_kernel<ORDER, R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     return hipGetLastError();
 }
 template <int ORDER, int TPW, int S>
@@ -392,6 +429,7 @@ size_t q4k_lds_bytes(int, int nb) { return q4_lds(nb, 4, 1); }
 // otherwise.
 hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int, hipStream_t s) {
     const int nb = a.nb;
+    if (a.xu && (order != 0 || a.dump_s)) return hipErrorInvalidValue;  // the fused silu: row order only
     const int64_t tiles = a.groups * ntok;
     int S = 1;
     if (order == 1 && tiles < 768)
@@ -448,13 +486,39 @@ size_t q4_image_bytes(int nb) { return q4_act_bytes(nb); }
 
 // MoE expert matvecs grouped by expert (row order, dot_q4_K_q8k): workgroup (x, y) takes tiles
 // 4x..4x+3 (one per wavefront, over the launch's tensors) of the matrix of segment y (one selected
-// expert with its token slots, from moe_group_kernel) and every slot of that segment. Each
-// wavefront loads all blocks of its tile into registers once (NB >= nb); for every chunk of MOE_TC
-// slots the workgroup copies their activation images (q4_image_kernel, row slot / a.xdiv) into LDS
-// and runs the decode kernel's row-order steps and chains once per slot. Tensor i of a.t: output
-// rows y_i[slot * ldy]. seg: [0] = number of segments, then per segment {expert, first, count}.
-constexpr int MOE_TC = 4;
-template <int NB>
+// expert with its token slots, from moe_group_kernel) and every slot of that segment. For every
+// chunk of MOE_TC slots the workgroup copies their activation images (q4_image_kernel, row
+// slot / a.xdiv) into LDS; each wavefront then walks the blocks of its tile through a ring of
+// MOE_R steps, forms a block's weight-side values once (nibbles, scale and min pairs, d, dmin) and
+// runs the decode kernel's row-order lane sums and fp32 chains for every slot of the chunk (the
+// chains of a slot in block order, as the per-token matvec does). Tensor i of a.t: output rows
+// y_i[slot * ldy]. seg: [0] = number of segments, then per segment {expert, first, count}.
+constexpr int MOE_TC = 8, MOE_R = 2;
+
+// the weight side of one (tile, block) for the row order: chunk j's nibbles, its (sc_2j, sc_2j+1)
+// and (m_2j, m_2j+1) as int16 pairs, d and dmin
+struct RbWSide {
+    uint32_t lo[8], hi[8];
+    uint32_t sc2, mn2;
+    float d, dmin;
+};
+__device__ __forceinline__ void rb_wside(const RbW &w, const RbLane &ln, RbWSide &ws) {
+    const uint32_t qd[8] = {w.p0.x, w.p0.y, w.p0.z, w.p0.w, w.p1.x, w.p1.y, w.p1.z, w.p1.w};
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        ws.lo[d] = nib_lo(qd[d]);
+        ws.hi[d] = nib_hi(qd[d]);
+    }
+    const uint32_t A = w.m.y >> ln.sh, B = w.m.z >> ln.sh, C = w.m.w >> ln.sh;  // as rb_in
+    const uint32_t sc_lo = A & 0x3f3fu, sc_hi = (C & 0x0f0fu) | ((A >> 2) & 0x3030u);
+    const uint32_t mn_lo = B & 0x3f3fu, mn_hi = ((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u);
+    ws.sc2 = __builtin_amdgcn_perm(0u, (sc_hi & ln.hm) | (sc_lo & ~ln.hm), 0x0C010C00u);
+    ws.mn2 = __builtin_amdgcn_perm(0u, (mn_hi & ln.hm) | (mn_lo & ~ln.hm), 0x0C010C00u);
+    ws.d = fp16_bits_to_f32(w.m.x & 0xFFFF);
+    ws.dmin = fp16_bits_to_f32(w.m.x >> 16);
+}
+
+template <int TC>
 __global__ __launch_bounds__(256) void q4k_moe_kernel(MvArgs a, const int32_t *__restrict__ seg,
                                                       const int32_t *__restrict__ slots, const uint8_t *__restrict__ img) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -472,16 +536,18 @@ __global__ __launch_bounds__(256) void q4k_moe_kernel(MvArgs a, const int32_t *_
     const int64_t lt = tc - a.t[ti].gfirst;  // tile within the matrix
     const size_t bstride = (size_t)a.t[ti].gpm * RB_BYTES;
     const uint8_t *T0 = a.t[ti].W + (size_t)expert * nb * bstride + (size_t)lt * RB_BYTES;
-    RbW w[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) rb_load(T0 + (size_t)min(b, nb - 1) * bstride, lane, w[b]);
+    const int bl = nb - 1;
     const size_t actb = q4_act_bytes(nb);
     const int units = (int)(actb / 16);
     const int64_t row = lt * RB_ROWS + rr;
     const bool store = live && j == 0 && row < a.t[ti].rows;
     const RbLane ln = rb_lane(lane);
-    for (int c0 = 0; c0 < count; c0 += MOE_TC) {
-        const int nc = min(MOE_TC, count - c0);
+    const int hs = 16 * (j >> 1);  // lanes j >= 2: second half of their activations first (as rb_in)
+    RbW ring[MOE_R];
+    for (int c0 = 0; c0 < count; c0 += TC) {
+        const int nc = min(TC, count - c0);
+#pragma unroll
+        for (int r = 0; r < MOE_R; ++r) rb_load(T0 + (size_t)min(r, bl) * bstride, lane, ring[r]);
         // the chunk's activation images (rows slot / xdiv) into LDS
         for (int i = tid; i < nc * units; i += 256) {
             const int c = i / units, o = i - c * units;
@@ -489,41 +555,81 @@ __global__ __launch_bounds__(256) void q4k_moe_kernel(MvArgs a, const int32_t *_
             ((uint4 *)(smem + (size_t)c * actb))[o] = ((const uint4 *)(img + (size_t)(slot / a.xdiv) * actb))[o];
         }
         __syncthreads();
-        for (int c = 0; c < nc; ++c) {
-            const uint8_t *act = smem + (size_t)c * actb;
-            float acc = 0.0f, acc2 = 0.0f, macc = 0.0f;
+        float acc[TC], acc2[TC], macc[TC];
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                if (b < nb) {  // uniform
-                    RbIn in;
-                    rb_in(w[b], act, nb, b, ln, in);
-                    const float fd = fp16_bits_to_f32(w[b].m.x & 0xFFFF) * in.yd;
-                    const float fdm = fp16_bits_to_f32(w[b].m.x >> 16) * in.yd;
-                    int u0, u1;
-                    rb_row_lanes(w[b], in, j, u0, u1);
-                    acc = __builtin_fmaf(fd, (float)u0, acc);
-                    acc2 = __builtin_fmaf(fd, (float)u1, acc2);
-                    macc = __builtin_fmaf(fdm, (float)in.mt, macc);
+        for (int c = 0; c < TC; ++c) acc[c] = acc2[c] = macc[c] = 0.0f;
+        auto blk = [&](const RbW &w, int b) {
+            RbWSide ws;
+            rb_wside(w, ln, ws);
+#pragma unroll
+            for (int c = 0; c < TC; ++c) {
+                if (c < nc) {  // uniform
+                    const uint8_t *act = smem + (size_t)c * actb;
+                    const uint8_t *yb = act + (size_t)b * 256 + 64 * j;
+                    const uint4 l0 = *(const uint4 *)(yb + hs), l1 = *(const uint4 *)(yb + 16 - hs);
+                    const uint4 h0 = *(const uint4 *)(yb + 32 + hs), h1 = *(const uint4 *)(yb + 48 - hs);
+                    const uint32_t ylo[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+                    const uint32_t yhi[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+                    const uint32_t bq = *(const uint32_t *)((const int16_t *)(act + q4_off_s(nb)) + 8 * b + 2 * j);
+                    const float yd = ((const float *)(act + q4_off_d(nb)))[b];
+                    int lv[8];
+#pragma unroll
+                    for (int d = 0; d < 8; ++d)
+                        lv[d] = dot2_i16(ws.sc2, pack_i16(dot4((int)ws.lo[d], (int)ylo[d], 0),
+                                                          dot4((int)ws.hi[d], (int)yhi[d], 0)), 0);
+                    // the row order's lane pairs (as rb_row_lanes)
+                    int t4[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) t4[k] = lv[k] + dpp_xor2(lv[4 + k]);
+                    const bool odd = (j & 1) != 0;
+                    const int k0 = odd ? t4[2] : t4[0], k1 = odd ? t4[3] : t4[1];
+                    const int s0 = odd ? t4[0] : t4[2], s1 = odd ? t4[1] : t4[3];
+                    const int u0 = k0 + dpp_xor1(s0), u1 = k1 + dpp_xor1(s1);
+                    const int mt = dot2_i16(ws.mn2, bq, 0);
+                    const float fd = ws.d * yd, fdm = ws.dmin * yd;
+                    acc[c] = __builtin_fmaf(fd, (float)u0, acc[c]);
+                    acc2[c] = __builtin_fmaf(fd, (float)u1, acc2[c]);
+                    macc[c] = __builtin_fmaf(fdm, (float)mt, macc[c]);
                 }
             }
-            const float out = rb_row_final(acc, acc2, macc);
-            if (store) a.t[ti].y[(size_t)slots[first + c0 + c] * a.ldy + row] = out;
+        };
+        int b0 = 0;
+        for (; b0 + MOE_R <= nb; b0 += MOE_R) {
+#pragma unroll
+            for (int r = 0; r < MOE_R; ++r) {
+                blk(ring[r], b0 + r);
+                rb_load(T0 + (size_t)min(b0 + r + MOE_R, bl) * bstride, lane, ring[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < MOE_R - 1; ++r)
+            if (b0 + r < nb) blk(ring[r], b0 + r);  // uniform
+#pragma unroll
+        for (int c = 0; c < TC; ++c) {
+            if (c < nc) {  // uniform
+                const float out = rb_row_final(acc[c], acc2[c], macc[c]);
+                if (store) a.t[ti].y[(size_t)slots[first + c0 + c] * a.ldy + row] = out;
+            }
         }
         __syncthreads();  // the next chunk reuses the activations
     }
 }
 
 size_t q4k_moe_lds_bytes(int nb) { return MOE_TC * q4_act_bytes(nb); }
-int q4k_moe_max_blocks() { return 8; }
+// the widest rows whose chunk of activation images fits 64 KiB of LDS
+int q4k_moe_max_blocks() {
+    int nb = 1;
+    while (q4k_moe_lds_bytes(nb + 1) <= 65536) ++nb;
+    return nb;
+}
 
 // a.groups = tiles of one matrix over all tensors; grid.y = max_segments
 hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *seg, const int32_t *slots, const uint8_t *img,
                           int max_segments, hipStream_t s) {
     const size_t lds = q4k_moe_lds_bytes(a.nb);
-    if (a.nb > q4k_moe_max_blocks() || lds > 65536) return hipErrorInvalidValue;
+    if (a.nb < 1 || lds > 65536) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.groups + 3) / 4), (unsigned)max_segments);
-    if (a.nb <= 4) q4k_moe_kernel<4><<<grid, 256, lds, s>>>(a, seg, slots, img);
-    else q4k_moe_kernel<8><<<grid, 256, lds, s>>>(a, seg, slots, img);
+    q4k_moe_kernel<MOE_TC><<<grid, 256, lds, s>>>(a, seg, slots, img);
     return hipGetLastError();
 }
 
