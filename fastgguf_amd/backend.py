@@ -26,7 +26,7 @@ ACT_Q8, ACT_Q8K = 1, 2
 EXPORTS = (
     "fgh_open", "fgh_close", "fgh_info", "fgh_last_error", "fgh_upload", "fgh_tensor_free",
     "fgh_matvec", "fgh_matvec_multi", "fgh_matmul", "fgh_moe_ffn",
-    "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matmul_dev", "fgh_moe_ffn_dev",
+    "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matvec_silu_dev", "fgh_matmul_dev", "fgh_moe_ffn_dev",
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
@@ -71,6 +71,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_moe_ffn": (i32, [vp, vp, vp, vp, i32, f32p, f32p, f32p, i32, vp, vp]),
         "fgh_matvec_dev": (i32, [vp, vp, vp, vp]),
         "fgh_matvec_multi_dev": (i32, [vp, i32, vp, vp, vp]),
+        "fgh_matvec_silu_dev": (i32, [vp, vp, vp, vp, vp]),
         "fgh_matmul_dev": (i32, [vp, vp, vp, i32, vp, i32, i32]),
         "fgh_moe_ffn_dev": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, i32]),
         "fgh_graph_begin": (i32, [vp]),
@@ -303,6 +304,27 @@ class Backend:
 
     def matvec_dev(self, t: Tensor, x_dev: int, y_dev: int):
         self._check(self.lib.fgh_matvec_dev(self.ctx, t.handle, x_dev, y_dev))
+
+    def matvec_silu_dev(self, t: Tensor, g_dev: int, u_dev: int, y_dev: int):
+        """y = t * Q8(silu(g) * u), the dense FFN's down projection (device pointers)."""
+        self._check(self.lib.fgh_matvec_silu_dev(self.ctx, t.handle, g_dev, u_dev, y_dev))
+
+    def matvec_silu(self, t: Tensor, g: np.ndarray, u: np.ndarray) -> np.ndarray:
+        """The same from host arrays (copies in and out; for tests)."""
+        g = np.ascontiguousarray(g, dtype=np.float32)
+        u = np.ascontiguousarray(u, dtype=np.float32)
+        nout = t.rows * t.n_mats
+        gd, ud, yd = self.dev_alloc(g.nbytes), self.dev_alloc(u.nbytes), self.dev_alloc(4 * nout)
+        try:
+            self.h2d(gd, g)
+            self.h2d(ud, u)
+            self.matvec_silu_dev(t, gd, ud, yd)
+            y = np.empty(nout, dtype=np.float32)
+            self.d2h(y, yd)
+            return y
+        finally:
+            for p in (gd, ud, yd):
+                self.dev_free(p)
 
     def matvec_multi_dev(self, ts: list[Tensor], x_dev: int, y_devs: list[int]):
         th = (C.c_void_p * len(ts))(*[t.handle for t in ts])

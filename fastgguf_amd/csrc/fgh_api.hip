@@ -31,7 +31,7 @@ struct fgh_ctx {
     // scratch, grown on demand (gpu_grow_buf, fastgguf.c:2083-2091)
     DevBuf x, y, aqs, ad, abs;
     DevBuf gq, gy, gb;  // prompt-GEMM activations (launch_gemm_quant layout)
-    DevBuf msel, mw, mg, mu, mh, md, mlog;  // MoE: selection, weights, gate / up / h / down outputs
+    DevBuf msel, mw, mg, mu, md, mlog;  // MoE: selection, weights, gate / up / down outputs
     DevBuf mseg, mslot, mimx, mimh;         // MoE: slots grouped by expert, Q8_K images of x and h
     DevBuf ck;                              // fgh_checksum_dev: per-workgroup partial sums
     int num_cu = 256;         // compute units (sizes the persistent decode grid)
@@ -222,7 +222,7 @@ void fgh_close(fgh_ctx *c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->gy, &c->gb, &c->msel, &c->mw, &c->mg,
-                      &c->mu, &c->mh, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck})
+                      &c->mu, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck})
         if (b->p) (void)hipFree(b->p);
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -358,6 +358,15 @@ int fgh_matvec_dev(fgh_ctx *c, const fgh_tensor *t, const float *x, float *y) {
     return fgh_matvec_multi_dev(c, 1, tt, x, yy);
 }
 
+int fgh_matvec_silu_dev(fgh_ctx *c, const fgh_tensor *t, const float *g, const float *u, float *y) {
+    int rc = check_tensor(c, t);
+    if (rc) return rc;
+    if (!g || !u || !y) return fail(c, FGH_ERR_ARG, "matvec_silu: null pointer");
+    HIP_TRY(c, hipSetDevice(c->device));
+    float *yy[1] = {y};
+    return matvec_launch(c, 1, &t, g, t->cols, yy, t->rows * t->n_mats, 1, nullptr, nullptr, nullptr, 1, u);
+}
+
 int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, float *Y, int ldy, int nb) {
     int rc = check_tensor(c, t);
     if (rc) return rc;
@@ -386,10 +395,10 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
     const int64_t np = (int64_t)n_tok * k;  // (token, selected expert) slots
     if ((rc = grow(c, c->msel, (size_t)np * 4)) || (rc = grow(c, c->mw, (size_t)np * 4)) ||
         (rc = grow(c, c->mg, (size_t)np * ff * 4)) || (rc = grow(c, c->mu, (size_t)np * ff * 4)) ||
-        (rc = grow(c, c->mh, (size_t)np * ff * 4)) || (rc = grow(c, c->md, (size_t)np * n_embd * 4)))
+        (rc = grow(c, c->md, (size_t)np * n_embd * 4)))
         return rc;
     int32_t *sel = (int32_t *)c->msel.p;
-    float *w = (float *)c->mw.p, *G = (float *)c->mg.p, *U = (float *)c->mu.p, *H = (float *)c->mh.p,
+    float *w = (float *)c->mw.p, *G = (float *)c->mg.p, *U = (float *)c->mu.p,
           *D = (float *)c->md.p;
     HIP_TRY(c, fgh::launch_moe_route(logits, (int)E, k, n_tok, sel, w, c->stream));
     // several tokens, Q4_K experts: the slots grouped by expert, each expert's rows read once
@@ -443,14 +452,9 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
             (rc = matvec_launch(c, 1, &up, X, n_embd, yu, ff, (int)np, nullptr, nullptr, sel, k)))
             return rc;
     }
+    // down, with h = silu(g) * u formed inside the launch while it quantizes its input
     float *yd[1] = {D};
-    if (down->type == FGH_T_Q4_K && down->order == FGH_ORDER_ROW) {
-        // h = silu(g) * u formed inside the down launch while it quantizes its input
-        if ((rc = matvec_launch(c, 1, &down, G, ff, yd, n_embd, (int)np, nullptr, nullptr, sel, 1, U))) return rc;
-    } else {
-        HIP_TRY(c, fgh::launch_moe_silu_mul(G, U, H, np * ff, c->stream));
-        if ((rc = matvec_launch(c, 1, &down, H, ff, yd, n_embd, (int)np, nullptr, nullptr, sel, 1))) return rc;
-    }
+    if ((rc = matvec_launch(c, 1, &down, G, ff, yd, n_embd, (int)np, nullptr, nullptr, sel, 1, U))) return rc;
     HIP_TRY(c, fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, c->stream));
     return FGH_OK;
 }

@@ -179,8 +179,8 @@ struct MvArgs {
     // every tensor (launched with the tiles of one matrix) and activation row y / xdiv
     const int32_t *sel;
     int xdiv;
-    // Q4_K only: when set, the activation row is silu(x) * xu (silu_f, fastgguf.c:3118), formed
-    // while quantizing (the MoE down projection's input, never stored)
+    // when set, the activation row is silu(x) * xu (silu_f, fastgguf.c:3118), formed while
+    // quantizing (an FFN down projection's input, never stored)
     const float *xu;
 };
 size_t matvec_lds_bytes(int type, int order, int nb);  // Q6_K / Q8_0 (fgh_matvec.hip)
@@ -244,7 +244,6 @@ hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *seg, const int32_t *sl
 size_t q4_image_bytes(int nb);
 hipError_t launch_q4_image(const float *x, const float *u, int64_t ldx, int nb, int64_t rows, uint8_t *img,
                            hipStream_t s);
-hipError_t launch_moe_silu_mul(const float *g, const float *u, float *h, int64_t n, hipStream_t s);
 hipError_t launch_moe_combine(const float *d, const float *w, float *y, int n_embd, int k, int n_tok, int64_t ldy,
                               hipStream_t s);
 

@@ -77,6 +77,18 @@ __device__ __forceinline__ void xq_load(const float *__restrict__ x, int nb, int
 #pragma unroll
     for (int u = 0; u < 4; ++u) xv.v[u] = *(const float4 *)(p + 4 * u);
 }
+// x = silu(x) * u, value by value (silu_f, fastgguf.c:3118: x / (1 + expf(-x)))
+__device__ __forceinline__ void xv_silu_mul(XVals &xv, const XVals &uv) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float4 &g = xv.v[q];
+        const float4 u = uv.v[q];
+        g.x = g.x / (1.0f + expf_ref(-g.x)) * u.x;
+        g.y = g.y / (1.0f + expf_ref(-g.y)) * u.y;
+        g.z = g.z / (1.0f + expf_ref(-g.z)) * u.z;
+        g.w = g.w / (1.0f + expf_ref(-g.w)) * u.w;
+    }
+}
 template <int TYPE, int WPG>
 __device__ __forceinline__ void xq_store(int nb, int rb, const XVals &xv, uint8_t *act) {
     using Q = XQ<TYPE, WPG>;
@@ -122,12 +134,19 @@ __device__ __forceinline__ void xq_store(int nb, int rb, const XVals &xv, uint8_
         if (tl == 0) ((float *)(act + act_off_d(TYPE, nb)))[b] = d;
     }
 }
-template <int TYPE, int WPG>
-__device__ __forceinline__ void xq_finish(const float *__restrict__ x, int nb, XVals &xv, uint8_t *act) {
+// SILU: the row quantized is silu(x) * u (uv: the first round of u, loaded with xv)
+template <int TYPE, int WPG, bool SILU>
+__device__ __forceinline__ void xq_finish(const float *__restrict__ x, const float *__restrict__ u, int nb, XVals &xv,
+                                          XVals &uv, uint8_t *act) {
     using Q = XQ<TYPE, WPG>;
+    if (SILU) xv_silu_mul(xv, uv);
     xq_store<TYPE, WPG>(nb, 0, xv, act);
     for (int rb = Q::BPR; rb < nb; rb += Q::BPR) {
         xq_load<TYPE, WPG>(x, nb, rb, xv);
+        if (SILU) {
+            xq_load<TYPE, WPG>(u, nb, rb, uv);
+            xv_silu_mul(xv, uv);
+        }
         xq_store<TYPE, WPG>(nb, rb, xv, act);
     }
 }
@@ -212,7 +231,7 @@ __device__ __forceinline__ int mv_tensor_of(const MvArgs &a, int64_t g) {
 
 // Workgroup = TPW tiles x S wavefronts per tile (wavefront ks of a tile takes its ks-th run of
 // ceil(steps / S) steps); grid = (tiles over all tensors / TPW, tokens).
-template <int TYPE, int R, int TPW, int S, bool DUMP>
+template <int TYPE, int R, int TPW, int S, bool DUMP, bool SILU = false>
 __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
     constexpr int WPG = TPW * S;
     constexpr int TB = TYPE == T_Q6_K ? Q6K_TILE : Q80_TILE;
@@ -235,13 +254,15 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
     const uint8_t *T0 = a.t[ti].W + (((size_t)mi * nst + min(s0, nst - 1)) * tpm + tt) * TB;
 
     const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
-    XVals xv;
+    const float *xu = SILU ? a.xu + (size_t)(tok / a.xdiv) * a.ldx : nullptr;
+    XVals xv, uv;
     xq_load<TYPE, WPG>(x, nb, 0, xv);
+    if (SILU) xq_load<TYPE, WPG>(xu, nb, 0, uv);
     StepW<TYPE> ring[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) step_load(T0 + (size_t)min(k, sl) * sstride, (uint32_t)lane, ring[k]);
     uint8_t *act = smem;
-    xq_finish<TYPE, WPG>(x, nb, xv, act);
+    xq_finish<TYPE, WPG, SILU>(x, xu, nb, xv, uv, act);
     __syncthreads();
 
     const float *ad = (const float *)(act + act_off_d(TYPE, nb));
@@ -396,6 +417,7 @@ template <int TYPE, int R, int TPW, int S>
 static hipError_t mv_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
     const unsigned wg = (unsigned)((a.groups + TPW - 1) / TPW);
     if (a.dump_s) mv_kernel<TYPE, R, TPW, S, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    else if (a.xu) mv_kernel<TYPE, R, TPW, S, false, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     else mv_kernel<TYPE, R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     return hipGetLastError();
 }
@@ -410,6 +432,7 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 // 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps, 4 otherwise.
 template <int TYPE>
 static hipError_t mv_launch_type(const MvArgs &a, int ntok, hipStream_t s) {
+    if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
     const int nb = a.nb, nst = mv_steps(TYPE, nb);
     constexpr int SPW = TYPE == T_Q6_K ? 2 : 1;  // Q6_K steps are 4x the bytes of Q8_0's per row
     const int64_t tiles = a.groups * ntok;

@@ -3,7 +3,8 @@
 //             first index on ties), w_j = p_j / max(sum_j p_j, 2^-14) (4594-4604)
 //   gate, up: expert sel_j's rows of gate / up times Q8_K(x) (the decode kernels with an expert
 //             index read on the device)
-//   h_j     = silu(g_j) * u_j, silu(x) = x / (1 + expf(-x)) (silu_f 3118)
+//   h_j     = silu(g_j) * u_j, silu(x) = x / (1 + expf(-x)) (silu_f 3118), formed by the down
+//             launch while it quantizes its input (fgh_q4k.hip, fgh_matvec.hip)
 //   down:     d_j = expert sel_j's rows of down times Q8_K(h_j)
 //   y_i     = sum over j in order of fma(w_j, d_j[i], s)  (4626-4635; gcc contracts s += w*dot)
 // Every dot product runs the reference's own per-row order (dot_q4_K_q8k and friends), so the
@@ -174,14 +175,6 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const int32_t *__restric
     for (int i = tid; i < np; i += 256) slots[atomicAdd(&fill[sel[i]], 1)] = i;
 }
 
-__global__ void moe_silu_mul_kernel(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ h,
-                                    int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        const float x = g[i];
-        h[i] = x / (1.0f + expf_ref(-x)) * u[i];
-    }
-}
-
 // y[t][i] = sum_j fma(w[t][j], d[t k + j][i], s), j ascending
 __global__ void moe_combine_kernel(const float *__restrict__ d, const float *__restrict__ w, float *__restrict__ y,
                                    int n_embd, int k, int64_t ldy) {
@@ -224,12 +217,6 @@ hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok,
 hipError_t launch_moe_group(const int32_t *sel, int np, int n_expert, int32_t *seg, int32_t *slots, hipStream_t s) {
     if (np < 1 || np > 64 * 64 || n_expert < 1 || n_expert > 64 * MOE_EPL) return hipErrorInvalidValue;
     moe_group_kernel<<<1, 256, 0, s>>>(sel, np, n_expert, seg, slots);
-    return hipGetLastError();
-}
-
-hipError_t launch_moe_silu_mul(const float *g, const float *u, float *h, int64_t n, hipStream_t s) {
-    const int64_t want = (n + 255) / 256;
-    moe_silu_mul_kernel<<<(unsigned)(want < 4096 ? want : 4096), 256, 0, s>>>(g, u, h, n);
     return hipGetLastError();
 }
 

@@ -398,13 +398,8 @@ static hipError_t q4_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s
         q4k_mv_kernel<ORDER, R, TPW, S, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
         return hipGetLastError();
     }
-    if constexpr (ORDER == 0 && S == 1) {
-        if (a.xu) {
-            q4k_mv_kernel<ORDER, R, TPW, S, false, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
-            return hipGetLastError();
-        }
-    }
-    q4k_mv_kernel<ORDER, R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    if (a.xu) q4k_mv_kernel<ORDER, R, TPW, S, false, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    else q4k_mv_kernel<ORDER, R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     return hipGetLastError();
 }
 template <int ORDER, int TPW, int S>
@@ -429,7 +424,7 @@ size_t q4k_lds_bytes(int, int nb) { return q4_lds(nb, 4, 1); }
 // otherwise.
 hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int, hipStream_t s) {
     const int nb = a.nb;
-    if (a.xu && (order != 0 || a.dump_s)) return hipErrorInvalidValue;  // the fused silu: row order only
+    if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
     const int64_t tiles = a.groups * ntok;
     int S = 1;
     if (order == 1 && tiles < 768)

@@ -196,6 +196,31 @@ def test_widest_q6k_q80_rows(backend, oracle, t, nb):
     tt.free()
 
 
+SILU_CASES = [  # (type, rows, cols, order): split launches (S > 1) and one-wavefront tiles
+    (S.T_Q4_K, 48, 14336, ORDER_REPACKED),
+    (S.T_Q4_K, 4096, 14336, ORDER_REPACKED),  # the Llama-3-8B down projection
+    (S.T_Q4_K, 40, 2048, ORDER_ROW),
+    (S.T_Q6_K, 13, 4608, ORDER_ROW),
+    (S.T_Q8_0, 37, 4128, ORDER_ROW),
+]
+
+
+@pytest.mark.parametrize("case", SILU_CASES, ids=lambda c: f"t{c[0]}_{c[1]}x{c[2]}_o{c[3]}")
+def test_matvec_silu_fused(backend, oracle, case):
+    """fgh_matvec_silu_dev: y = W * Q8(silu(g) * u) equals the reference's loop (silu_f with
+    libm expf, times up, in fp32) followed by the matvec, bit for bit."""
+    t, rows, cols, order = case
+    w = S.random_bytes_weights(t, rows, cols, 141 + rows)
+    g = S.activations(cols, 142) * np.float32(3.0)
+    u = S.activations(cols, 143)
+    h = (g / (np.float32(1.0) + oracle.libm_expf(-g)) * u).astype(np.float32)
+    tt = backend.upload(t, cols, w, order=order)
+    y = backend.matvec_silu(tt, g, u)
+    assert bits_equal(y, backend.matvec(tt, h))
+    assert bits_equal(y, oracle.matvec(t, w, cols, h, O_RP if order == ORDER_REPACKED else O_ROW))
+    tt.free()
+
+
 def test_graph_replay_matches_eager(backend, oracle):
     """A captured layer (QKV, gate+up in one launch) replayed several times, with eager work and
     synchronizations between replays: every replay equals the eager result and the oracle."""
