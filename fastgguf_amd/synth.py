@@ -6,9 +6,14 @@ Byte layouts follow fastgguf.c (lawnak/FastGGUF):
                             (fastgguf.c:622-643; scale unpack scale_min_k4 466-472)
   Q6_K 210 B / 256 weights  ql[128] @0, qh[64] @128, int8 sc[16] @192, fp16 d @208
                             (fastgguf.c:669-693)
+  Q5_0  22 B / 32 weights   fp16 d @0, u32 qh @2 (bit j = bit 4 of element j), nibbles qs[16] @6
+                            (fastgguf.c:518-532, element order q5_elem 939-942)
+  Q5_K 176 B / 256 weights  fp16 d @0, fp16 dmin @2, 12 B scales @4, qh[32] @16, ql[128] @48
+                            (fastgguf.c:644-667)
 Value distributions are the benchmark's: Q4_K nibbles uniform, 6-bit scales and mins uniform in
 [0, 63], d and dmin = fp16(|N(0,1)| * 0.005); Q6_K quant bytes uniform, int8 scales uniform in
-[-64, 63], d = fp16(|N(0,1)| * 0.002); Q8_0 quants uniform in [-127, 127], d = fp16(|N(0,1)| * 0.01).
+[-64, 63], d = fp16(|N(0,1)| * 0.002); Q8_0 quants uniform in [-127, 127], d = fp16(|N(0,1)| * 0.01);
+Q5_0 and Q5_K quant bytes uniform, d = fp16(|N(0,1)| * 0.01) (Q5_0) or as Q4_K (Q5_K).
 fp16 conversion rounds to nearest even (numpy astype).
 """
 from __future__ import annotations
@@ -16,13 +21,21 @@ from __future__ import annotations
 import numpy as np
 
 T_F32 = 0
+T_Q5_0 = 6
 T_Q8_0 = 8
 T_Q4_K = 12
+T_Q5_K = 13
 T_Q6_K = 14
 
 #: (elements per block, bytes per block), block_size_of (fastgguf.c:235-253)
-BLOCK = {T_Q8_0: (32, 34), T_Q4_K: (256, 144), T_Q6_K: (256, 210)}
-TYPE_NAME = {T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q6_K: "Q6_K"}
+BLOCK = {T_Q8_0: (32, 34), T_Q4_K: (256, 144), T_Q6_K: (256, 210), T_Q5_0: (32, 22), T_Q5_K: (256, 176)}
+TYPE_NAME = {T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q6_K: "Q6_K", T_Q5_0: "Q5_0", T_Q5_K: "Q5_K"}
+
+
+def uses_q8(type_: int) -> bool:
+    """Activation kind (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for Q8_0 / Q5_0, Q8_K
+    blocks of 256 for the K-quants."""
+    return type_ in (T_Q8_0, T_Q5_0)
 
 #: activation blocks, the reference's structs q8_blk_t (743) and q8k_blk_t (771)
 Q8_BLK = np.dtype([("d", "<f4"), ("qs", "i1", 32), ("s16", "<i2", 2)])
@@ -94,7 +107,39 @@ def q8_0_weights(rows: int, cols: int, seed: int) -> np.ndarray:
     return blk.reshape(rows, -1)
 
 
+def q5_0_weights(rows: int, cols: int, seed: int) -> np.ndarray:
+    """rows x cols Q5_0 matrix, returned as uint8 [rows, cols/32*22]."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    if cols % 32:
+        raise ValueError("Q5_0 needs cols % 32 == 0")
+    nb = rows * (cols // 32)
+    blk = np.empty((nb, 22), np.uint8)
+    blk[:, 0:2] = _fp16_abs_normal(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)
+    blk[:, 2:22] = rng.integers(0, 256, size=(nb, 20), dtype=np.uint8)
+    return blk.reshape(rows, -1)
+
+
+def q5_k_weights(rows: int, cols: int, seed: int) -> np.ndarray:
+    """rows x cols Q5_K matrix, returned as uint8 [rows, cols/256*176]."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    if cols % 256:
+        raise ValueError("Q5_K needs cols % 256 == 0")
+    nb = rows * (cols // 256)
+    blk = np.empty((nb, 176), np.uint8)
+    blk[:, 0:2] = _fp16_abs_normal(rng, nb, 0.005).view(np.uint8).reshape(nb, 2)
+    blk[:, 2:4] = _fp16_abs_normal(rng, nb, 0.005).view(np.uint8).reshape(nb, 2)
+    sc = rng.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+    mn = rng.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+    blk[:, 4:16] = pack_q4k_scales(sc, mn)
+    blk[:, 16:176] = rng.integers(0, 256, size=(nb, 160), dtype=np.uint8)
+    return blk.reshape(rows, -1)
+
+
 def weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    if type_ == T_Q5_0:
+        return q5_0_weights(rows, cols, seed)
+    if type_ == T_Q5_K:
+        return q5_k_weights(rows, cols, seed)
     if type_ == T_Q4_K:
         return q4_k_weights(rows, cols, seed)
     if type_ == T_Q6_K:
@@ -117,7 +162,7 @@ def random_bytes_weights(type_: int, rows: int, cols: int, seed: int) -> np.ndar
         blk[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
     else:
         blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
-        if type_ == T_Q4_K:
+        if type_ in (T_Q4_K, T_Q5_K):
             blk[:, 2:4] = dm.view(np.uint8).reshape(nb, 2)
     return blk.reshape(rows, -1)
 

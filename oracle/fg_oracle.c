@@ -46,6 +46,11 @@ float fgo_fp16(uint16_t h) {
 }
 
 static inline uint16_t rd16(const uint8_t *p) { uint16_t v; memcpy(&v, p, 2); return v; }
+static inline uint32_t rd32(const uint8_t *p) { uint32_t v; memcpy(&v, p, 4); return v; }
+
+/* the activation kind of a weight type (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for
+ * Q8_0 / Q5_0, Q8_K blocks of 256 for the K-quants */
+static inline int uses_q8(uint32_t type) { return type == FGO_T_Q8_0 || type == FGO_T_Q5_0; }
 
 /* FGO_MUTATE (tests only, tests/test_oracle.py) builds a copy of this oracle with one planted
  * mistake, to show that the golden vectors catch it. 0 = the real oracle. */
@@ -137,6 +142,33 @@ static inline int q6k_val(const uint8_t *p, int e) {
     return lo | (hi << 4);
 }
 
+/* Q5_0 element j (0..31) of a block, offset 16 not removed (q5_elem, fastgguf.c:939-942): nibble j
+ * (low nibbles of qs[0..15] first, then their high nibbles) with bit j of qh as bit 4 */
+static inline int q5_0_val(const uint8_t *p, int j) {
+    uint32_t qh = rd32(p + 2);
+    const uint8_t *qs = p + 6;
+    int nib = j < 16 ? (qs[j] & 0x0F) : (qs[j - 16] >> 4);
+#if FGO_MUTATE == 7 /* the fifth bit taken from the wrong half of qh */
+    return nib | (int)(((qh >> ((j + 16) & 31)) & 1u) << 4);
+#else
+    return nib | (int)(((qh >> j) & 1u) << 4);
+#endif
+}
+
+/* Q5_K element e (0..255) of a block (fastgguf.c:1195-1210, scalar form 1216-1221): chunk j = e / 64
+ * of ql (bytes 48 + 32 j ..), low nibbles for e % 64 < 32, high nibbles above; bit 2 j (low) or
+ * 2 j + 1 (high) of qh[e % 32] as bit 4 */
+static inline int q5k_val(const uint8_t *p, int e) {
+    int j = e >> 6, hi = (e >> 5) & 1, l = e & 31;
+    uint8_t q = p[48 + 32 * j + l];
+    int nib = hi ? (q >> 4) : (q & 0x0F);
+#if FGO_MUTATE == 8 /* the qh bits of a chunk paired as (j, j + 4) instead of (2j, 2j + 1) */
+    return nib | (((p[16 + l] >> (j + 4 * hi)) & 1) << 4);
+#else
+    return nib | (((p[16 + l] >> (2 * j + hi)) & 1) << 4);
+#endif
+}
+
 /* ---- B-1: dot_q8_0_q8 (fastgguf.c:891-902) ----
  * lane i of block b: s_i = sum_{t=4i}^{4i+3} w_t x_t;  acc_i = fma(FP16(d)*xd, s_i, acc_i) */
 float fgo_dot_q8_0(const uint8_t *row, const fgo_q8_blk *xq, int nb) {
@@ -148,6 +180,23 @@ float fgo_dot_q8_0(const uint8_t *row, const fgo_q8_blk *xq, int nb) {
         for (int i = 0; i < 8; i++) {
             int s = 0;
             for (int t = 4 * i; t < 4 * i + 4; t++) s += (int)w[t] * xq[b].qs[t];
+            acc[i] = fmaf(d, (float)s, acc[i]);
+        }
+    }
+    return hsum8(acc);
+}
+
+/* ---- B-6: dot_q5_0_q8 (fastgguf.c:944-959), the same lanes as B-1 over the int8 values q5 - 16
+ * (bx = nibble | 0xF0 where the fifth bit is clear); the x4 tile dot_q32_q8_x4 (1400-1419) equals
+ * it bit for bit (same d * yd, same lanes) */
+float fgo_dot_q5_0(const uint8_t *row, const fgo_q8_blk *xq, int nb) {
+    float acc[8] = {0};
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *p = row + (size_t)b * 22;
+        float d = fgo_fp16(rd16(p)) * xq[b].d;
+        for (int i = 0; i < 8; i++) {
+            int s = 0;
+            for (int t = 4 * i; t < 4 * i + 4; t++) s += (q5_0_val(p, t) - 16) * xq[b].qs[t];
             acc[i] = fmaf(d, (float)s, acc[i]);
         }
     }
@@ -183,6 +232,39 @@ float fgo_dot_q4_K(const uint8_t *row, const fgo_q8k_blk *y, int nb) {
             int s0 = bs[4 * pp] + bs[4 * pp + 1], s1 = bs[4 * pp + 2] + bs[4 * pp + 3];
             int ml = mn[2 * pp] * s0 + mn[2 * pp + 1] * s1;
             macc[pp] = fmaf(dm, (float)ml, macc[pp]);
+        }
+    }
+    return hsum8(acc) - hsum4(macc);
+}
+
+/* ---- B-7: dot_q5_K_q8k (fastgguf.c:1178-1230): the lanes, min lanes and final combination of B-2
+ * with five-bit values (maddubs pairs, madd with the sub-block scale: lane i sums elements 4i..4i+3
+ * of each 32-value sub-block) */
+float fgo_dot_q5_K(const uint8_t *row, const fgo_q8k_blk *y, int nb) {
+    float acc[8] = {0}, macc[4] = {0};
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *p = row + (size_t)b * 176;
+        const int8_t *q8 = y[b].qs;
+        uint8_t sc[8], mn[8];
+        q4k_scales(p + 4, sc, mn);
+        float yd = y[b].d;
+        float dd = fgo_fp16(rd16(p)) * yd, dm = fgo_fp16(rd16(p + 2)) * yd;
+        for (int i = 0; i < 8; i++) {
+            int lane = 0;
+            for (int j = 0; j < 4; j++) {
+                int il = 0, ih = 0;
+                for (int t = 4 * i; t < 4 * i + 4; t++) {
+                    il += q5k_val(p, 64 * j + t) * q8[64 * j + t];
+                    ih += q5k_val(p, 64 * j + 32 + t) * q8[64 * j + 32 + t];
+                }
+                lane += sc[2 * j] * il + sc[2 * j + 1] * ih;
+            }
+            acc[i] = fmaf(dd, (float)lane, acc[i]);
+        }
+        for (int pp = 0; pp < 4; pp++) {
+            const int16_t *bs = y[b].bsums;
+            int s0 = bs[4 * pp] + bs[4 * pp + 1], s1 = bs[4 * pp + 2] + bs[4 * pp + 3];
+            macc[pp] = fmaf(dm, (float)(mn[2 * pp] * s0 + mn[2 * pp + 1] * s1), macc[pp]);
         }
     }
     return hsum8(acc) - hsum4(macc);
@@ -285,6 +367,27 @@ void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
             }
             sumi[b] = s;
             msum[b] = m;
+        } else if (type == FGO_T_Q5_K) {
+            const uint8_t *p = row + (size_t)b * 176;
+            const fgo_q8k_blk *yb = (const fgo_q8k_blk *)act + b;
+            uint8_t sc[8], mn[8];
+            q4k_scales(p + 4, sc, mn);
+            int s = 0, m = 0;
+            for (int g = 0; g < 8; g++) {
+                int ig = 0;
+                for (int l = 0; l < 32; l++) ig += q5k_val(p, 32 * g + l) * yb->qs[32 * g + l];
+                s += sc[g] * ig;
+                m += mn[g] * (yb->bsums[2 * g] + yb->bsums[2 * g + 1]);
+            }
+            sumi[b] = s;
+            msum[b] = m;
+        } else if (type == FGO_T_Q5_0) {
+            const uint8_t *p = row + (size_t)b * 22;
+            const fgo_q8_blk *xb = (const fgo_q8_blk *)act + b;
+            int s = 0;
+            for (int t = 0; t < 32; t++) s += (q5_0_val(p, t) - 16) * xb->qs[t];
+            sumi[b] = s;
+            msum[b] = 0;
         } else { /* Q8_0 */
             const uint8_t *p = row + (size_t)b * 34;
             const fgo_q8_blk *xb = (const fgo_q8_blk *)act + b;
@@ -296,8 +399,27 @@ void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
     }
 }
 
-/* ---- dequantize_row (fastgguf.c:552-562, 622-643, 669-693) ---- */
+/* ---- dequantize_row (fastgguf.c:518-532, 552-562, 622-667, 669-693) ---- */
 int fgo_dequantize_row(uint32_t type, const uint8_t *raw, float *out, int n) {
+    if (type == FGO_T_Q5_0) {
+        for (int b = 0; b < n / 32; b++) {
+            const uint8_t *p = raw + (size_t)b * 22;
+            float d = fgo_fp16(rd16(p));
+            for (int j = 0; j < 32; j++) out[32 * b + j] = d * (float)(q5_0_val(p, j) - 16);
+        }
+        return 0;
+    }
+    if (type == FGO_T_Q5_K) {
+        for (int b = 0; b < n / 256; b++) {
+            const uint8_t *p = raw + (size_t)b * 176;
+            float d = fgo_fp16(rd16(p)), dmin = fgo_fp16(rd16(p + 2));
+            uint8_t sc[8], mn[8];
+            q4k_scales(p + 4, sc, mn);
+            for (int e = 0; e < 256; e++)
+                out[256 * b + e] = d * (float)sc[e / 32] * (float)q5k_val(p, e) - dmin * (float)mn[e / 32];
+        }
+        return 0;
+    }
     if (type == FGO_T_Q8_0) {
         for (int b = 0; b < n / 32; b++) {
             const uint8_t *p = raw + (size_t)b * 34;
@@ -342,29 +464,33 @@ int fgo_block_size(uint32_t type, int *elems, int *bytes) {
     case FGO_T_Q8_0: *elems = 32; *bytes = 34; return 0;
     case FGO_T_Q4_K: *elems = 256; *bytes = 144; return 0;
     case FGO_T_Q6_K: *elems = 256; *bytes = 210; return 0;
+    case FGO_T_Q5_0: *elems = 32; *bytes = 22; return 0;
+    case FGO_T_Q5_K: *elems = 256; *bytes = 176; return 0;
     default: return -1;
     }
 }
 
-/* ---- dot_row dispatch for the three types (fastgguf.c:2183-2201) ---- */
+/* ---- dot_row dispatch for the five types (fastgguf.c:2183-2201) ---- */
 static float dot_row3(uint32_t type, int order, const uint8_t *rb, const void *act, int cols) {
     if (type == FGO_T_Q4_K)
         return order == FGO_ORDER_REPACKED ? fgo_dot_q4_K_rp(rb, (const fgo_q8k_blk *)act, cols / 256)
                                            : fgo_dot_q4_K(rb, (const fgo_q8k_blk *)act, cols / 256);
     if (type == FGO_T_Q6_K) return fgo_dot_q6_K(rb, (const fgo_q8k_blk *)act, cols / 256);
+    if (type == FGO_T_Q5_K) return fgo_dot_q5_K(rb, (const fgo_q8k_blk *)act, cols / 256);
+    if (type == FGO_T_Q5_0) return fgo_dot_q5_0(rb, (const fgo_q8_blk *)act, cols / 32);
     return fgo_dot_q8_0(rb, (const fgo_q8_blk *)act, cols / 32);
 }
 
 static int type_ok(uint32_t type, int cols) {
-    if (type == FGO_T_Q4_K || type == FGO_T_Q6_K) return cols > 0 && cols % 256 == 0;
-    if (type == FGO_T_Q8_0) return cols > 0 && cols % 32 == 0;
+    if (type == FGO_T_Q4_K || type == FGO_T_Q5_K || type == FGO_T_Q6_K) return cols > 0 && cols % 256 == 0;
+    if (type == FGO_T_Q8_0 || type == FGO_T_Q5_0) return cols > 0 && cols % 32 == 0;
     return 0;
 }
 
 /* quantize one activation vector for the type (type_uses_q8 2167 + quantize_act 2176);
  * returns a malloc'd buffer, NULL on failure */
 static void *quantize_for(uint32_t type, const float *x, int cols) {
-    if (type == FGO_T_Q8_0) {
+    if (uses_q8(type)) {
         fgo_q8_blk *q = (fgo_q8_blk *)malloc((size_t)(cols / 32) * sizeof(fgo_q8_blk));
         if (q) fgo_quantize_q8(x, q, cols);
         return q;
@@ -375,8 +501,7 @@ static void *quantize_for(uint32_t type, const float *x, int cols) {
 }
 
 static size_t act_bytes(uint32_t type, int cols) {
-    return type == FGO_T_Q8_0 ? (size_t)(cols / 32) * sizeof(fgo_q8_blk)
-                              : (size_t)(cols / 256) * sizeof(fgo_q8k_blk);
+    return uses_q8(type) ? (size_t)(cols / 32) * sizeof(fgo_q8_blk) : (size_t)(cols / 256) * sizeof(fgo_q8k_blk);
 }
 
 /* matvec (fastgguf.c:2575-2622) and matvec_rp (2540-2545): rows are independent, so the row
@@ -400,22 +525,25 @@ int fgo_matvec(uint32_t type, int order, const uint8_t *w, int64_t rows, int col
  *   for g: a = fma(wsc_g, ia_g, a)          wsc_g = FP16(d)*sc_g  (Q6_K: FP16(d)*sc_g)
  *   for g: a = fnmadd(wmn_g, bs_g, a)       wmn_g = FP16(dmin)*m_g (Q6_K: 32*FP16(d)*sc_g)
  *   f = fma(a, yd_b, f)
- * ---- and gemm32_kern (2909-2937) for Q8_0 (unpack_row_q32 2876-2894, gemm_pack_q8 2897-2913):
- *   per 32-block g: a = fma(d*xd, ia'_g, a); a = fnmadd(128*d, xd*(s16_0+s16_1), a)
- *   with ia' = sum (w+128)*x (the unsigned weight the VNNI kernel multiplies) */
+ * ---- and gemm32_kern (2909-2937) for Q8_0 / Q5_0 (unpack_row_q32 2876-2894, gemm_pack_q8 2897-2913):
+ *   per 32-block g: a = fma(d*xd, ia'_g, a); a = fnmadd(m, xd*(s16_0+s16_1), a)
+ *   with ia' = sum u*x over the unsigned weights the VNNI kernel multiplies: Q8_0 u = w + 128,
+ *   m = 128 d; Q5_0 u = q5 (0..31), m = 16 d */
 static void gemm_row_token(uint32_t type, const uint8_t *rb, const void *act, int cols, float *out) {
-    if (type == FGO_T_Q8_0) {
+    if (uses_q8(type)) {
         const fgo_q8_blk *xq = (const fgo_q8_blk *)act;
+        const int q5 = type == FGO_T_Q5_0, bb = q5 ? 22 : 34;
         float acc = 0.0f;
         for (int g = 0; g < cols / 32; g++) {
-            const uint8_t *p = rb + (size_t)g * 34;
+            const uint8_t *p = rb + (size_t)g * bb;
             float d = fgo_fp16(rd16(p));
             int ia = 0;
-            for (int t = 0; t < 32; t++) ia += ((int)(int8_t)p[2 + t] + 128) * xq[g].qs[t];
+            for (int t = 0; t < 32; t++)
+                ia += (q5 ? q5_0_val(p, t) : (int)(int8_t)p[2 + t] + 128) * xq[g].qs[t];
             float ws = d * xq[g].d;
             float ys = xq[g].d * (float)(xq[g].s16[0] + xq[g].s16[1]);
             acc = fmaf(ws, (float)ia, acc);
-            acc = fmaf(-(128.0f * d), ys, acc);
+            acc = fmaf(-((q5 ? 16.0f : 128.0f) * d), ys, acc);
         }
         *out = acc;
         return;
@@ -482,7 +610,8 @@ int fgo_gemm(uint32_t type, const uint8_t *w, int64_t rows, int cols, const void
     int eb, bb;
     fgo_block_size(type, &eb, &bb);
     size_t stride = (size_t)(cols / eb) * bb;
-    size_t ablk = type == FGO_T_Q8_0 ? sizeof(fgo_q8_blk) : sizeof(fgo_q8k_blk);
+    if (type == FGO_T_Q5_K) return -1; /* no prompt GEMM: matmul runs the row kernel per token */
+    size_t ablk = uses_q8(type) ? sizeof(fgo_q8_blk) : sizeof(fgo_q8k_blk);
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; r++)
         for (int t = 0; t < nb; t++)
@@ -492,9 +621,11 @@ int fgo_gemm(uint32_t type, const uint8_t *w, int64_t rows, int cols, const void
     return 0;
 }
 
-/* matmul (fastgguf.c:3004-3093) restricted to Q4_K / Q6_K / Q8_0, as built for a VNNI CPU:
+/* matmul (fastgguf.c:3004-3093) restricted to Q4_K / Q5_K / Q6_K / Q5_0 / Q8_0, as built for a VNNI
+ * CPU:
  *   nb == 1: matvec;  repacked and nb < 8: per-token matvec;  nb >= 8: the prompt GEMM
- *   (gemm_kquant, or gemm_q32 for Q8_0 - VNNI builds only, GEMM_Q8_0 at 2864-2868);
+ *   (gemm_kquant for Q4_K / Q6_K, gemm_q32 for Q5_0 and, VNNI builds only, Q8_0 - GEMM_Q8_0 at
+ *   2864-2868; Q5_K has no GEMM and no x4 tile: the row kernel per token);
  *   otherwise the x4 tiles, which equal the single-row kernels bit for bit (selftest 5871-5916). */
 int fgo_matmul(uint32_t type, int order, const uint8_t *w, int64_t rows, int cols,
                const float *X, int ldx, float *Y, int ldy, int nb) {
@@ -511,13 +642,13 @@ int fgo_matmul(uint32_t type, int order, const uint8_t *w, int64_t rows, int col
     uint8_t *act = (uint8_t *)malloc(ab * (size_t)nb);
     if (!act) return -1;
     for (int t = 0; t < nb; t++) {
-        if (type == FGO_T_Q8_0) fgo_quantize_q8(X + (size_t)t * ldx, (fgo_q8_blk *)(act + ab * t), cols);
+        if (uses_q8(type)) fgo_quantize_q8(X + (size_t)t * ldx, (fgo_q8_blk *)(act + ab * t), cols);
         else fgo_quantize_q8k(X + (size_t)t * ldx, (fgo_q8k_blk *)(act + ab * t), cols);
     }
     int eb, bb;
     fgo_block_size(type, &eb, &bb);
     int sblocks = cols / eb;
-    if (nb >= 8) {
+    if (nb >= 8 && type != FGO_T_Q5_K) {
         int rc = fgo_gemm(type, w, rows, cols, act, sblocks, Y, ldy, nb);
         free(act);
         return rc;
@@ -649,7 +780,7 @@ int fgo_moe_down(uint32_t type_down, const uint8_t *down, int n_embd, int ff, in
     uint8_t *act = (uint8_t *)malloc(ab * (size_t)k);
     if (!act) return -1;
     for (int j = 0; j < k; j++) {
-        if (type_down == FGO_T_Q8_0) fgo_quantize_q8(h + (size_t)j * ff, (fgo_q8_blk *)(act + ab * j), ff);
+        if (uses_q8(type_down)) fgo_quantize_q8(h + (size_t)j * ff, (fgo_q8_blk *)(act + ab * j), ff);
         else fgo_quantize_q8k(h + (size_t)j * ff, (fgo_q8k_blk *)(act + ab * j), ff);
     }
 #pragma omp parallel for schedule(static)

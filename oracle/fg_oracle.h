@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-enum { FGO_T_F32 = 0, FGO_T_Q8_0 = 8, FGO_T_Q4_K = 12, FGO_T_Q6_K = 14 };
+enum { FGO_T_F32 = 0, FGO_T_Q5_0 = 6, FGO_T_Q8_0 = 8, FGO_T_Q4_K = 12, FGO_T_Q5_K = 13, FGO_T_Q6_K = 14 };
 
 /* fp32 evaluation order a kernel follows (which reference kernel the call restates) */
 enum {
@@ -40,11 +40,13 @@ float fgo_dot_q8_0(const uint8_t *row, const fgo_q8_blk *xq, int nb);
 float fgo_dot_q4_K(const uint8_t *row, const fgo_q8k_blk *y, int nb);
 float fgo_dot_q4_K_rp(const uint8_t *row, const fgo_q8k_blk *y, int nb);
 float fgo_dot_q6_K(const uint8_t *row, const fgo_q8k_blk *y, int nb);
+float fgo_dot_q5_0(const uint8_t *row, const fgo_q8_blk *xq, int nb);
+float fgo_dot_q5_K(const uint8_t *row, const fgo_q8k_blk *y, int nb);
 
 /* per-block integer parts (the bit-exact targets):
- *   Q4_K: sumi[b] = sum_s sc_s * sum_32 q*y,   msum[b] = sum_s m_s * (bs_2s + bs_2s+1)
- *   Q6_K: sumi[b] = sum_g sc_g * sum_16 q*y,   msum[b] = sum_g sc_g * bs_g      (q in 0..63)
- *   Q8_0: sumi[b] = sum_32 w*x,                msum[b] = 0                    */
+ *   Q4_K, Q5_K: sumi[b] = sum_s sc_s * sum_32 q*y,   msum[b] = sum_s m_s * (bs_2s + bs_2s+1)
+ *   Q6_K:       sumi[b] = sum_g sc_g * sum_16 q*y,   msum[b] = sum_g sc_g * bs_g  (q in 0..63)
+ *   Q8_0, Q5_0: sumi[b] = sum_32 w*x,                msum[b] = 0        (Q5_0: w = q5 - 16) */
 void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
                     int32_t *sumi, int32_t *msum);
 

@@ -15,7 +15,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
-from fastgguf_amd.synth import BLOCK, Q8_BLK, Q8K_BLK, T_Q8_0  # noqa: E402
+from fastgguf_amd.synth import BLOCK, Q8_BLK, Q8K_BLK, uses_q8  # noqa: E402
 
 ORDER_ROW = 0
 ORDER_REPACKED = 1
@@ -30,7 +30,7 @@ def _ptr(a: np.ndarray):
 
 
 def act_dtype(type_: int):
-    return Q8_BLK if type_ == T_Q8_0 else Q8K_BLK
+    return Q8_BLK if uses_q8(type_) else Q8K_BLK
 
 
 class Oracle:
@@ -46,7 +46,7 @@ class Oracle:
         for n in ("fgo_quantize_q8", "fgo_quantize_q8k"):
             getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
             getattr(L, n).restype = None
-        for n in ("fgo_dot_q8_0", "fgo_dot_q4_K", "fgo_dot_q4_K_rp", "fgo_dot_q6_K"):
+        for n in ("fgo_dot_q8_0", "fgo_dot_q4_K", "fgo_dot_q4_K_rp", "fgo_dot_q6_K", "fgo_dot_q5_0", "fgo_dot_q5_K"):
             getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
             getattr(L, n).restype = C.c_float
         L.fgo_block_ints.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
@@ -83,7 +83,7 @@ class Oracle:
         return out
 
     def quantize_for(self, type_: int, x: np.ndarray) -> np.ndarray:
-        return self.quantize_q8(x) if type_ == T_Q8_0 else self.quantize_q8k(x)
+        return self.quantize_q8(x) if uses_q8(type_) else self.quantize_q8k(x)
 
     # -- row kernels
     def dot(self, type_: int, row: np.ndarray, act: np.ndarray, order: int = ORDER_ROW) -> float:
@@ -91,7 +91,7 @@ class Oracle:
         eb, _ = BLOCK[type_]
         nb = act.size
         name = {8: "fgo_dot_q8_0", 12: "fgo_dot_q4_K_rp" if order == ORDER_REPACKED else "fgo_dot_q4_K",
-                14: "fgo_dot_q6_K"}[type_]
+                14: "fgo_dot_q6_K", 6: "fgo_dot_q5_0", 13: "fgo_dot_q5_K"}[type_]
         return getattr(self.lib, name)(_ptr(row), _ptr(act), nb)
 
     def block_ints(self, type_: int, row: np.ndarray, act: np.ndarray):
@@ -218,7 +218,7 @@ class Reference:
         for n in ("fgr_quantize_q8", "fgr_quantize_q8k"):
             getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
             getattr(L, n).restype = None
-        for n in ("fgr_dot_q8_0", "fgr_dot_q4_K", "fgr_dot_q6_K"):
+        for n in ("fgr_dot_q8_0", "fgr_dot_q4_K", "fgr_dot_q6_K", "fgr_dot_q5_0", "fgr_dot_q5_K"):
             getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
             getattr(L, n).restype = C.c_float
         L.fgr_matvec.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
@@ -256,7 +256,7 @@ class Reference:
 
     def dot(self, type_, row, act):
         row = np.ascontiguousarray(row, np.uint8)
-        name = {8: "fgr_dot_q8_0", 12: "fgr_dot_q4_K", 14: "fgr_dot_q6_K"}[type_]
+        name = {8: "fgr_dot_q8_0", 12: "fgr_dot_q4_K", 14: "fgr_dot_q6_K", 6: "fgr_dot_q5_0", 13: "fgr_dot_q5_K"}[type_]
         return getattr(self.lib, name)(_ptr(row), _ptr(act), act.size)
 
     def matvec(self, type_, w, cols, x, repack=False):

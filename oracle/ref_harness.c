@@ -29,6 +29,8 @@ FGR_EXPORT void fgr_quantize_q8k(const float *x, void *out, int n) { quantize_q8
 FGR_EXPORT float fgr_dot_q8_0(const uint8_t *row, const void *xq, int nb) { return dot_q8_0_q8(row, (const q8_blk_t *)xq, nb); }
 FGR_EXPORT float fgr_dot_q4_K(const uint8_t *row, const void *y, int nb) { return dot_q4_K_q8k(row, (const q8k_blk_t *)y, nb); }
 FGR_EXPORT float fgr_dot_q6_K(const uint8_t *row, const void *y, int nb) { return dot_q6_K_q8k(row, (const q8k_blk_t *)y, nb); }
+FGR_EXPORT float fgr_dot_q5_0(const uint8_t *row, const void *xq, int nb) { return dot_q5_0_q8(row, (const q8_blk_t *)xq, nb); }
+FGR_EXPORT float fgr_dot_q5_K(const uint8_t *row, const void *y, int nb) { return dot_q5_K_q8k(row, (const q8k_blk_t *)y, nb); }
 
 /* a tensor view over caller memory; `repack` asks for the 8-row layout the reference builds at
  * load time (repack_tensor, 2486). repack_tensor drops the source pages with MADV_DONTNEED, so

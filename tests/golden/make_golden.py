@@ -60,7 +60,8 @@ def main() -> None:
 
     # single-token matvecs: per type, synthetic (benchmark distributions) and random-byte rows
     mv = {}
-    cases = [("q8_0", S.T_Q8_0, 24, 512), ("q4_k", S.T_Q4_K, 24, 768), ("q6_k", S.T_Q6_K, 24, 512)]
+    cases = [("q8_0", S.T_Q8_0, 24, 512), ("q4_k", S.T_Q4_K, 24, 768), ("q6_k", S.T_Q6_K, 24, 512),
+             ("q5_0", S.T_Q5_0, 24, 544), ("q5_k", S.T_Q5_K, 24, 768)]
     for name, t, rows, cols in cases:
         for gname, gen in (("synth", S.weights), ("bytes", S.random_bytes_weights)):
             w = gen(t, rows, cols, 200 + t)
@@ -75,7 +76,8 @@ def main() -> None:
 
     # prompt batches through matmul: 3 tokens (x4 tiles / repacked per-token) and 8, 45 (GEMM)
     mm = {}
-    for name, t, rows, cols in [("q8_0", S.T_Q8_0, 20, 512), ("q4_k", S.T_Q4_K, 24, 512), ("q6_k", S.T_Q6_K, 20, 512)]:
+    for name, t, rows, cols in [("q8_0", S.T_Q8_0, 20, 512), ("q4_k", S.T_Q4_K, 24, 512), ("q6_k", S.T_Q6_K, 20, 512),
+                                ("q5_0", S.T_Q5_0, 20, 544), ("q5_k", S.T_Q5_K, 20, 512)]:
         w = S.weights(t, rows, cols, 400 + t)
         mm[f"{name}_w"] = w
         for nb in (3, 8, 45):
@@ -101,6 +103,20 @@ def main() -> None:
     Y, sel, w = ref.moe_ffn((S.T_Q4_K,) * 3, g, u, d, E, K, D, F, L, X)
     np.savez_compressed(os.path.join(HERE, "moe.npz"), gate=g, up=u, down=d, X=X, logits=L, Y=Y, sel=sel, w=w,
                         dims=np.array([E, K, D, F, T]))
+
+    # MoE with the fallback types of a K-quant file: Q5_K gate / up, Q5_0 down over ff = 160
+    # (5 blocks of 32: not a multiple of 256, the reason a file falls back to Q5_0)
+    E, K, D, F, T = 4, 2, 256, 160, 4
+    types = (S.T_Q5_K, S.T_Q5_K, S.T_Q5_0)
+    g = S.weights(types[0], E * F, D, 611)
+    u = S.weights(types[1], E * F, D, 612)
+    d = S.weights(types[2], E * D, F, 613)
+    X = S.activations(D, 614, rows=T)
+    X[:, 0] = 1.0
+    L = S.router_logits(T, E, 615)
+    Y, sel, w = ref.moe_ffn(types, g, u, d, E, K, D, F, L, X)
+    np.savez_compressed(os.path.join(HERE, "moe_q5.npz"), gate=g, up=u, down=d, X=X, logits=L, Y=Y, sel=sel, w=w,
+                        dims=np.array([E, K, D, F, T]), types=np.array(types))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

@@ -19,7 +19,8 @@ from conftest import ROOT, bits_equal, golden, rel_err
 from fastgguf_amd import synth as S
 from oracle import ORDER_REPACKED, ORDER_ROW, Oracle
 
-TYPES = {"q8_0": S.T_Q8_0, "q4_k": S.T_Q4_K, "q6_k": S.T_Q6_K}
+TYPES = {"q8_0": S.T_Q8_0, "q4_k": S.T_Q4_K, "q6_k": S.T_Q6_K, "q5_0": S.T_Q5_0, "q5_k": S.T_Q5_K}
+ALL = [S.T_Q8_0, S.T_Q4_K, S.T_Q6_K, S.T_Q5_0, S.T_Q5_K]
 
 
 # ---------------------------------------------------------------- golden vectors (reference)
@@ -31,7 +32,7 @@ def test_quantizers_match_golden(oracle):
         assert oracle.quantize_q8k(x).view(np.uint8).tobytes() == g["quant_q8k"][r].tobytes(), f"q8k row {r}"
 
 
-@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("gen", ["synth", "bytes"])
 def test_matvec_matches_golden(oracle, name, gen):
     g = golden("matvec.npz")
@@ -43,7 +44,7 @@ def test_matvec_matches_golden(oracle, name, gen):
         assert bits_equal(oracle.matvec(t, w, cols, x, ORDER_REPACKED), g[f"{name}_{gen}_y_rp"])
 
 
-@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("nb", [3, 8, 45])
 def test_matmul_matches_golden(oracle, name, nb):
     g = golden("matmul.npz")
@@ -64,6 +65,18 @@ def test_moe_matches_golden(oracle):
     assert bits_equal(Y, g["Y"])
     assert list(g["sel"][2][:2]) == [3, 7]      # tie on top keeps the lower index first
     assert list(g["sel"][3]) == [0, 1, 2]       # all-equal logits
+
+
+def test_moe_q5_matches_golden(oracle):
+    """Q5_K gate / up with a Q5_0 down projection over ff = 160 (a K-quant file's fallback types)."""
+    g = golden("moe_q5.npz")
+    E, K, D, F, T = (int(v) for v in g["dims"])
+    types = tuple(int(v) for v in g["types"])
+    assert types == (S.T_Q5_K, S.T_Q5_K, S.T_Q5_0)
+    Y, sel, w = oracle.moe_ffn(types, g["gate"], g["up"], g["down"], E, K, D, F, g["logits"], g["X"])
+    assert np.array_equal(sel, g["sel"])
+    assert bits_equal(w, g["w"])
+    assert bits_equal(Y, g["Y"])
 
 
 # expf inputs where a separately rounded r = x N / ln 2 - k gives another float than glibc's
@@ -89,8 +102,8 @@ def test_expf_restatement_matches_libm(oracle):
 def test_oracle_matches_compiled_reference_random(oracle, reference):
     """Fresh random shapes and seeds against the reference's kernels (where oracle/_ref is built)."""
     rng = np.random.Generator(np.random.PCG64(7))
-    for case in range(6):
-        t = [S.T_Q8_0, S.T_Q4_K, S.T_Q6_K][case % 3]
+    for case in range(10):
+        t = ALL[case % 5]
         cols = int(rng.integers(1, 5)) * 256
         rows = 8 * int(rng.integers(1, 5))
         w = (S.weights if case % 2 else S.random_bytes_weights)(t, rows, cols, 1000 + case)
@@ -102,6 +115,11 @@ def test_oracle_matches_compiled_reference_random(oracle, reference):
         X = S.activations(cols, 3000 + case, rows=nb)
         if reference.variant == "vnni" or t != S.T_Q8_0:  # AVX2 builds have no Q8_0 GEMM
             assert bits_equal(oracle.matmul(t, w, cols, X), reference.matmul(t, w, cols, X))
+        if S.uses_q8(t):  # rows of 32-blocks that are not 256-multiples (a tail step of 1..3 blocks)
+            c2 = 32 * int(rng.integers(1, 40))
+            w2 = S.weights(t, rows, c2, 4000 + case)
+            x2 = S.activations(c2, 5000 + case)
+            assert bits_equal(oracle.matvec(t, w2, c2, x2), reference.matvec(t, w2, c2, x2))
 
 
 # ---------------------------------------------------------------- what the mathematics fixes
@@ -147,7 +165,14 @@ def _decode_codes(t, w_row, cols):
     if t == S.T_Q8_0:
         q = blk[:, 2:34].view(np.int8).astype(np.int64).reshape(-1)
         return q, np.ones_like(q), np.zeros_like(q)
-    if t == S.T_Q4_K:
+    if t == S.T_Q5_0:  # element j: nibble j of qs (low nibbles, then high), bit j of qh as bit 4; minus 16
+        qh = blk[:, 2:6].copy().view("<u4").astype(np.int64)  # [nb, 1]
+        qs = blk[:, 6:22].astype(np.int64)
+        nib = np.concatenate([qs & 15, qs >> 4], axis=1)
+        bit = (qh >> np.arange(32)) & 1
+        q = (nib | (bit << 4)) - 16
+        return q.reshape(-1), np.ones(nb * 32, np.int64), np.zeros(nb * 32, np.int64)
+    if t in (S.T_Q4_K, S.T_Q5_K):
         s12 = blk[:, 4:16].astype(np.int64)
         sc = np.zeros((nb, 8), np.int64)
         mn = np.zeros((nb, 8), np.int64)
@@ -156,8 +181,15 @@ def _decode_codes(t, w_row, cols):
             mn[:, j] = s12[:, j + 4] & 63
             sc[:, j + 4] = (s12[:, j + 8] & 15) | ((s12[:, j] >> 6) << 4)
             mn[:, j + 4] = (s12[:, j + 8] >> 4) | ((s12[:, j + 4] >> 6) << 4)
-        qs = blk[:, 16:144].astype(np.int64).reshape(nb, 4, 32)
-        q = np.stack([qs & 15, qs >> 4], axis=2).reshape(nb, 256)  # [j][lo/hi][32]
+        qs = blk[:, 16:144] if t == S.T_Q4_K else blk[:, 48:176]
+        qs = qs.astype(np.int64).reshape(nb, 4, 32)
+        q = np.stack([qs & 15, qs >> 4], axis=2)  # [nb][j][lo/hi][32]
+        if t == S.T_Q5_K:  # chunk j, half h: bit 2j + h of qh[l] is bit 4 of element l
+            qh = blk[:, 16:48].astype(np.int64)
+            for j in range(4):
+                for h in range(2):
+                    q[:, j, h] |= ((qh >> (2 * j + h)) & 1) << 4
+        q = q.reshape(nb, 256)
         sub = np.arange(256) // 32
         return q.reshape(-1), sc[:, sub].reshape(-1), mn[:, sub].reshape(-1)
     ql = blk[:, 0:128].astype(np.int64).reshape(nb, 2, 64)
@@ -171,7 +203,7 @@ def _decode_codes(t, w_row, cols):
     return q.reshape(-1), sc[:, np.arange(256) // 16].reshape(-1), np.zeros(nb * 256, np.int64)
 
 
-@pytest.mark.parametrize("t", [S.T_Q8_0, S.T_Q4_K, S.T_Q6_K])
+@pytest.mark.parametrize("t", ALL)
 def test_block_ints_brute_force(oracle, t):
     cols = 1024
     w = S.random_bytes_weights(t, 4, cols, 77)
@@ -191,7 +223,7 @@ def test_block_ints_brute_force(oracle, t):
         assert np.array_equal(s, want_s) and np.array_equal(m, want_m)
 
 
-@pytest.mark.parametrize("t", [S.T_Q4_K, S.T_Q6_K, S.T_Q8_0])
+@pytest.mark.parametrize("t", ALL)
 def test_dot_vs_dequantized_double(oracle, t):
     """test_kquant (fastgguf.c:5379-5411): kernel vs double sum of dequantized weights times
     dequantized activations, relative to sum |term| < 1e-4."""
@@ -207,7 +239,7 @@ def test_dot_vs_dequantized_double(oracle, t):
         assert abs(fast - terms.sum()) / (np.abs(terms).sum() + 1e-9) < 1e-4
 
 
-@pytest.mark.parametrize("t", [S.T_Q4_K, S.T_Q6_K, S.T_Q8_0])
+@pytest.mark.parametrize("t", ALL)
 def test_selftest_relations(oracle, t):
     """matmul vs the single-row kernel and repacked vs row (fastgguf.c:5690-5785): < 1e-5."""
     cols, rows, nbt = 512, 37, 45
@@ -227,7 +259,8 @@ def test_selftest_relations(oracle, t):
 # ---------------------------------------------------------------- planted mistakes
 
 MUTANTS = {1: "hsum8 order", 2: "MoE accumulate without fma", 3: "reciprocal instead of division",
-           4: "Q6_K half-lane scale", 5: "Q4_K repacked single chain", 6: "Q4_K GEMM integer epilogue"}
+           4: "Q6_K half-lane scale", 5: "Q4_K repacked single chain", 6: "Q4_K GEMM integer epilogue",
+           7: "Q5_0 fifth bit from the wrong half of qh", 8: "Q5_K qh bit pairing"}
 
 
 @pytest.fixture(scope="module")
@@ -255,6 +288,11 @@ def _golden_failures(o: Oracle) -> int:
     g = golden("moe.npz")
     E, K, D, F, T = (int(v) for v in g["dims"])
     Y, _, _ = o.moe_ffn((S.T_Q4_K,) * 3, g["gate"], g["up"], g["down"], E, K, D, F, g["logits"], g["X"])
+    fails += not bits_equal(Y, g["Y"])
+    g = golden("moe_q5.npz")
+    E, K, D, F, T = (int(v) for v in g["dims"])
+    Y, _, _ = o.moe_ffn(tuple(int(v) for v in g["types"]), g["gate"], g["up"], g["down"], E, K, D, F,
+                        g["logits"], g["X"])
     fails += not bits_equal(Y, g["Y"])
     return fails
 
