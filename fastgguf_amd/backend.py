@@ -13,7 +13,7 @@ import os
 
 import numpy as np
 
-from .synth import BLOCK, Q8_BLK, Q8K_BLK, T_Q4_K, T_Q6_K, T_Q8_0, row_bytes
+from .synth import BLOCK, Q8_BLK, Q8K_BLK, T_Q4_K, T_Q5_0, T_Q5_K, T_Q6_K, T_Q8_0, row_bytes
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfastgguf_hip.so")
@@ -354,5 +354,5 @@ class Backend:
                                              Y_dev, n_tok))
 
 
-__all__ = ["Backend", "BackendError", "Tensor", "load_library", "EXPORTS", "T_Q4_K", "T_Q6_K", "T_Q8_0",
+__all__ = ["Backend", "BackendError", "Tensor", "load_library", "EXPORTS", "T_Q4_K", "T_Q5_0", "T_Q5_K", "T_Q6_K", "T_Q8_0",
            "ORDER_AUTO", "ORDER_ROW", "ORDER_REPACKED"]

@@ -84,16 +84,35 @@ static int grow(fgh_ctx *c, DevBuf &b, size_t need) {
     return FGH_OK;
 }
 
-static bool type_supported(uint32_t t) { return t == FGH_T_Q8_0 || t == FGH_T_Q4_K || t == FGH_T_Q6_K; }
-static int block_elems(uint32_t t) { return t == FGH_T_Q8_0 ? 32 : 256; }
-static int block_bytes(uint32_t t) { return t == FGH_T_Q8_0 ? 34 : t == FGH_T_Q4_K ? 144 : 210; }
-static int tile_bytes(uint32_t t) { return t == FGH_T_Q8_0 ? fgh::Q80_TILE : t == FGH_T_Q4_K ? fgh::Q4K_TILE : fgh::Q6K_TILE; }
+static bool type_supported(uint32_t t) {
+    return t == FGH_T_Q8_0 || t == FGH_T_Q4_K || t == FGH_T_Q6_K || t == FGH_T_Q5_0 || t == FGH_T_Q5_K;
+}
+static bool q16_rows(uint32_t t) { return t == FGH_T_Q4_K || t == FGH_T_Q5_K; }  // 16-row tiles
+static int block_elems(uint32_t t) { return fgh::q8_kind((int)t) ? 32 : 256; }
+static int block_bytes(uint32_t t) {
+    switch (t) {
+    case FGH_T_Q8_0: return 34;
+    case FGH_T_Q5_0: return 22;
+    case FGH_T_Q4_K: return 144;
+    case FGH_T_Q5_K: return 176;
+    default: return 210;
+    }
+}
+static int tile_bytes(uint32_t t) {
+    switch (t) {
+    case FGH_T_Q8_0: return fgh::Q80_TILE;
+    case FGH_T_Q5_0: return fgh::Q50_TILE;
+    case FGH_T_Q4_K: return fgh::Q4K_TILE;
+    case FGH_T_Q5_K: return fgh::Q5K_TILE;
+    default: return fgh::Q6K_TILE;
+    }
+}
 
 // activation buffers for ntok tokens of `cols` values, for the tensor's type
 static int ensure_act(fgh_ctx *c, uint32_t type, int64_t cols, int ntok) {
     const int64_t nbk = cols / block_elems(type);
     int rc;
-    if (type == FGH_T_Q8_0) {
+    if (fgh::q8_kind((int)type)) {
         if ((rc = grow(c, c->aqs, (size_t)ntok * nbk * 32)) || (rc = grow(c, c->ad, (size_t)ntok * nbk * 4)) ||
             (rc = grow(c, c->abs, (size_t)ntok * nbk * 4)))
             return rc;
@@ -109,7 +128,7 @@ static int ensure_act(fgh_ctx *c, uint32_t type, int64_t cols, int ntok) {
 static int quantize_dev(fgh_ctx *c, uint32_t type, int64_t cols, const float *x, int64_t ldx, int ntok) {
     int rc = ensure_act(c, type, cols, ntok);
     if (rc) return rc;
-    if (type == FGH_T_Q8_0) {
+    if (fgh::q8_kind((int)type)) {
         fgh::ActQ8 a{(int8_t *)c->aqs.p, (float *)c->ad.p, (int16_t *)c->abs.p};
         HIP_TRY(c, fgh::launch_quant_q8(x, ldx, (int)(cols / 32), ntok, a, c->stream));
     } else {
@@ -273,8 +292,8 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     t->rows = rows;
     t->n_mats = n_mats;
     t->nb = (int)(cols / block_elems(type));
-    t->ntile = type == FGH_T_Q8_0 ? (t->nb + 3) / 4 : t->nb;
-    const int tile_rows = type == FGH_T_Q4_K ? fgh::Q4K_TILE_ROWS : 8;
+    t->ntile = fgh::q8_kind((int)type) ? (t->nb + 3) / 4 : t->nb;
+    const int tile_rows = q16_rows(type) ? fgh::Q4K_TILE_ROWS : 8;
     t->gpm = (rows + tile_rows - 1) / tile_rows;
     t->groups = t->gpm * n_mats;
     t->order = ord;
@@ -294,9 +313,9 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     }
     hipError_t e = hipMemcpy(stage, host, nbytes, hipMemcpyHostToDevice);
     if (e == hipSuccess)
-        e = type == FGH_T_Q4_K
-                ? fgh::launch_q4k_relayout((const uint8_t *)stage, t->dev, rows, t->nb, t->gpm, (int64_t)t->dev_bytes,
-                                           row_bytes, c->stream)
+        e = q16_rows(type)
+                ? fgh::launch_q4k_relayout((int)type, (const uint8_t *)stage, t->dev, rows, t->nb, t->gpm,
+                                           (int64_t)t->dev_bytes, row_bytes, c->stream)
                 : fgh::launch_relayout((const uint8_t *)stage, t->dev, (int)type, rows, t->nb, t->ntile, t->gpm,
                                        (int64_t)t->dev_bytes, row_bytes, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);

@@ -15,10 +15,10 @@ namespace fgh {
 // accumulator lane i sums (its bytes 4i..4i+3 of every 32-byte chunk), so the per-lane integer
 // partials are the reference's lane partials, and the fp32 chains can follow its order.
 // Rows past the end of a matrix are zero-filled (d = 0) and never stored. Tiles lie step-major:
-// step s (a block, or 4 blocks for Q8_0) of row tile t of matrix m is tile (m * steps + s) * tpm + t,
-// tpm = row tiles per matrix.
+// step s (a block, or 4 blocks for Q8_0 / Q5_0) of row tile t of matrix m is tile
+// (m * steps + s) * tpm + t, tpm = row tiles per matrix.
 //
-//   (Q4_K uses its own layout of 16-row tiles, 2304 B per (tile, block), described in fgh_q4k.hip)
+//   (Q4_K and Q5_K use their own layout of 16-row tiles, described in fgh_q4k.hip)
 //   Q6_K tile, one block of 8 rows, 1680 B (= 8 x 210):
 //     [0, 128)     int8 scales, row r at 16r (file bytes 192..207)
 //     [128, 144)   fp16 d, row r at 128 + 2r (file bytes 208..209)
@@ -27,16 +27,28 @@ namespace fgh {
 //   Q8_0 tile, 4 blocks of 8 rows, 1088 B (= 8 x 4 x 34):
 //     [0, 64)      fp16 d of row r, block bb at 8r + 2bb
 //     [64, 1088)   quants: slice (r, i) at 64 + 16(8r + i); dword bb = block bb's bytes 2+4i..+3
+//   Q5_0 tile, 4 blocks of 8 rows, 704 B (= 8 x 4 x 22); slice (r, i) = elements 4i..4i+3 of each
+//   block (element e: nibble e of the block's qs, low nibbles first, with bit e of qh as bit 4):
+//     [0, 64)      fp16 d of row r, block bb at 8r + 2bb
+//     [64, 576)    nibbles: slice (r, i) at 64 + 8(8r + i): byte 4w + t holds element 4i + t of
+//                  block 2w in its low nibble and of block 2w + 1 in its high nibble
+//     [576, 704)   fifth bits: slice (r, i) at 576 + 2(8r + i), 16 bits n0 | n2 << 4 | n1 << 8 |
+//                  n3 << 12, where bit bb of the nibble n_t is the fifth bit of element 4i + t
+//                  of block bb
+//   (Q5_K shares the Q4_K layout with 512 B of fifth bits per (tile, block), fgh_q4k.hip)
 // ---------------------------------------------------------------------------------------------
-constexpr int T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14;
-constexpr int Q4K_TILE = 2304, Q6K_TILE = 1680, Q80_TILE = 1088;
-constexpr int Q4K_TILE_ROWS = 16;  // rows per Q4_K tile (8 for the other types)
+constexpr int T_Q5_0 = 6, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14;
+constexpr int Q4K_TILE = 2304, Q5K_TILE = 2816, Q6K_TILE = 1680, Q80_TILE = 1088, Q50_TILE = 704;
+constexpr int Q4K_TILE_ROWS = 16;  // rows per Q4_K / Q5_K tile (8 for the other types)
+// the activation kind of a weight type (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for
+// Q8_0 / Q5_0, Q8_K blocks of 256 for the K-quants
+__host__ __device__ constexpr bool q8_kind(int type) { return type == T_Q8_0 || type == T_Q5_0; }
 
-// Device activation layouts. Q8_K (for Q4_K / Q6_K): per token, nb blocks of
+// Device activation layouts. Q8_K (for the K-quants): per token, nb blocks of
 //   qs [nb][256] int8, permuted so lane i's 32 bytes are contiguous: position 32i + 4c + k holds
 //                 element 32c + 4i + k (an 8x8 transpose of the block's dwords)
 //   d  [nb] fp32, bs [nb][16] int16 (the reference's bsums)
-// Q8 (for Q8_0): per token, nb32 blocks of qs [nb32][32] int8 (natural order), d [nb32] fp32,
+// Q8 (for Q8_0 / Q5_0): per token, nb32 blocks of qs [nb32][32] int8 (natural order), d [nb32] fp32,
 //   s16 [nb32][2] int16.
 struct ActQ8K {
     int8_t *qs;
@@ -164,7 +176,7 @@ struct MvT {
     const uint8_t *W;
     float *y;
     int64_t rows;    // rows per matrix
-    int64_t gpm;     // row tiles per matrix (16 rows for Q4_K, 8 otherwise)
+    int64_t gpm;     // row tiles per matrix (16 rows for Q4_K / Q5_K, 8 otherwise)
     int64_t gfirst;  // first global tile index of this tensor
 };
 struct MvArgs {
@@ -183,12 +195,12 @@ struct MvArgs {
     // quantizing (an FFN down projection's input, never stored)
     const float *xu;
 };
-size_t matvec_lds_bytes(int type, int order, int nb);  // Q6_K / Q8_0 (fgh_matvec.hip)
-// Q4_K (fgh_q4k.hip): its own tile layout and kernel
+size_t matvec_lds_bytes(int type, int order, int nb);  // every type (fgh_matvec.hip)
+// Q4_K / Q5_K (fgh_q4k.hip): their own tile layout and kernel
 size_t q4k_lds_bytes(int order, int nb);
-hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
-hipError_t launch_q4k_relayout(const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t tpm, int64_t total,
-                               int64_t row_bytes, hipStream_t s);
+hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
+hipError_t launch_q4k_relayout(int type, const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t tpm,
+                               int64_t total, int64_t row_bytes, hipStream_t s);
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
 
 // MoE around the expert matvecs (fgh_moe.hip)

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void quant_q8_kernel(const float *__restrict__
 }
 
 // =============================================================================================
-// Upload-time re-layout of Q6_K / Q8_0: file-layout rows (n_mats x rows x row_bytes) -> tiles in
+// Upload-time re-layout of Q6_K / Q8_0 / Q5_0: file-layout rows (n_mats x rows x row_bytes) -> tiles in
 // step-major order, step tb of row tile gl of matrix m at (m * ntile + tb) * gpm + gl (Q4_K has its
 // own, fgh_q4k.hip). One thread per destination byte; padding rows and padding blocks are zero.
 // =============================================================================================
@@ -130,6 +130,48 @@ __global__ void relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__rest
     }
 }
 
+// Q5_0 (tile of 4 blocks, 704 B, fgh_internal.h): one thread per destination byte, gathering the
+// nibbles and fifth bits it packs from the file's blocks {fp16 d, u32 qh, qs[16]} (fastgguf.c:
+// 518-532); element e of a block is nibble e of qs (low nibbles of qs[0..15], then their high
+// nibbles) with bit e of qh above it (q5_elem, 939-942)
+__device__ __forceinline__ int q5_nib(const uint8_t *p, int e) { return e < 16 ? (p[6 + e] & 15) : (p[e - 10] >> 4); }
+__device__ __forceinline__ int q5_bit(const uint8_t *p, int e) { return (p[2 + (e >> 3)] >> (e & 7)) & 1; }
+__global__ void relayout_q5_0_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int64_t rows, int nb,
+                                     int ntile, int64_t gpm, int64_t total, int64_t row_bytes) {
+    for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
+         o += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = o / Q50_TILE;  // = (m * ntile + tb) * gpm + gl
+        const int ob = (int)(o - t * Q50_TILE);
+        const int64_t mt = t / gpm, gl = t - mt * gpm;
+        const int64_t m = mt / ntile;
+        const int tb = (int)(mt - m * ntile);
+        const int r = ob < 64 ? ob >> 3 : ob < 576 ? (ob - 64) >> 6 : (ob - 576) >> 4;
+        const int64_t row = gl * 8 + r;
+        // block bb of the step in this row, or null past the row's end
+        auto blk = [&](int bb) -> const uint8_t * {
+            const int b = 4 * tb + bb;
+            return row < rows && b < nb ? src + (m * rows + row) * row_bytes + (int64_t)b * 22 : nullptr;
+        };
+        int v = 0;
+        if (ob < 64) {  // fp16 d of block (ob & 7) >> 1
+            const uint8_t *p = blk((ob & 7) >> 1);
+            v = p ? p[ob & 1] : 0;
+        } else if (ob < 576) {  // byte 4w + t of slice i: element 4i + t of blocks 2w (low), 2w + 1 (high)
+            const int q = ob - 64, i = (q >> 3) & 7, w = (q >> 2) & 1, e = 4 * i + (q & 3);
+            const uint8_t *p0 = blk(2 * w), *p1 = blk(2 * w + 1);
+            v = (p0 ? q5_nib(p0, e) : 0) | (p1 ? q5_nib(p1, e) << 4 : 0);
+        } else {  // byte hb of slice i's fifth bits: nibbles n_hb (low) and n_hb+2 (high)
+            const int q = ob - 576, i = (q >> 1) & 7, hb = q & 1;
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                const uint8_t *p = blk(bb);
+                if (p) v |= (q5_bit(p, 4 * i + hb) << bb) | (q5_bit(p, 4 * i + hb + 2) << (4 + bb));
+            }
+        }
+        dst[o] = (uint8_t)v;
+    }
+}
+
 __global__ void fp16_kernel(const uint16_t *__restrict__ h, float *__restrict__ out, int n) {
     const int k = blockIdx.x * blockDim.x + threadIdx.x;
     if (k < n) out[k] = fp16_bits_to_f32(h[k]);
@@ -154,7 +196,8 @@ hipError_t launch_relayout(const uint8_t *src, uint8_t *dst, int type, int64_t r
                            int64_t gpm, int64_t total, int64_t row_bytes, hipStream_t s) {
     const int64_t want = (total + 255) / 256;
     const int grid = (int)(want < 65536 ? want : 65536);
-    relayout_kernel<<<grid, 256, 0, s>>>(src, dst, type, rows, nb, ntile, gpm, total, row_bytes);
+    if (type == T_Q5_0) relayout_q5_0_kernel<<<grid, 256, 0, s>>>(src, dst, rows, nb, ntile, gpm, total, row_bytes);
+    else relayout_kernel<<<grid, 256, 0, s>>>(src, dst, type, rows, nb, ntile, gpm, total, row_bytes);
     return hipGetLastError();
 }
 

@@ -1,10 +1,10 @@
-// fgh_matvec.hip - the decode matvec for Q6_K / Q8_0 on gfx950 (Q4_K has its own kernel in
-// fgh_q4k.hip, on the same plan).
+// fgh_matvec.hip - the decode matvec for Q6_K / Q8_0 / Q5_0 on gfx950 (Q4_K and Q5_K have their
+// own kernel in fgh_q4k.hip, on the same plan).
 //
 // Tiles (fgh_internal.h) are 8 rows of one step: one block (Q6_K, 1680 B) or four blocks (Q8_0,
-// 1088 B). They lie step-major: step s of row tile t of matrix m at ((m * steps + s) * tpm + t) *
-// tile bytes (tpm = row tiles per matrix), so the wavefronts of a launch, all at about the same
-// step, read one contiguous stretch of HBM at a time.
+// 1088 B; Q5_0, 704 B). They lie step-major: step s of row tile t of matrix m at
+// ((m * steps + s) * tpm + t) * tile bytes (tpm = row tiles per matrix), so the wavefronts of a
+// launch, all at about the same step, read one contiguous stretch of HBM at a time.
 //
 // A wavefront owns one row tile; lane L = 8 r + i holds slice i of row r, which is exactly what
 // the reference's AVX2 fp32 accumulator lane i of that row sums. Every workgroup quantizes x into
@@ -13,6 +13,7 @@
 // forms its exact integer lane partial (v_dot4_i32_i8, 16-bit scale products by v_dot2_i32_i16)
 // and advances its fp32 chain in registers in block order:
 //   Q8_0, dot_q8_0_q8 (fastgguf.c:891-902):   acc_i = fma(d * xd, s_i, acc_i), out = hsum8(acc)
+//   Q5_0, dot_q5_0_q8 (fastgguf.c:944-959):   the same, s_i over the values q5 - 16
 //   Q6_K, dot_q6_K_q8k (fastgguf.c:1232-1264): acc_i = fma(d * yd, lane_i, acc_i),
 //        cacc_p = fma(32 d yd, corr_p, cacc_p) in lanes i = p < 4, out = hsum8(acc) - hsum4(cacc)
 // so the outputs are bit-identical to the reference's row kernels. Short matrices split the steps
@@ -26,21 +27,24 @@ namespace fgh {
 // ---- LDS activations --------------------------------------------------------------------------
 // Q8_K (Q6_K): qs [nb][256] lane-permuted (position 32 i + 4 c holds element 32 c + 4 i, so lane
 //   i's 32 bytes are contiguous), d [nb] fp32, bs [nb][16] int16.
-// Q8 (Q8_0): per group of 4 blocks g, qs at 128 g: dword i of block 4 g + k at 128 g + 16 i + 4 k
+// Q8 (Q8_0 / Q5_0): per group of 4 blocks g, qs at 128 g: dword i of block 4 g + k at 128 g + 16 i + 4 k
 //   (a lane's 4 blocks in one 16-byte read); d [4 * groups] fp32.
 __host__ __device__ constexpr size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
-__host__ __device__ constexpr int mv_steps(int type, int nb) { return type == T_Q8_0 ? (nb + 3) / 4 : nb; }
+__host__ __device__ constexpr int mv_steps(int type, int nb) { return q8_kind(type) ? (nb + 3) / 4 : nb; }
 __host__ __device__ constexpr size_t act_off_d(int type, int nb) {
-    return type == T_Q8_0 ? (size_t)128 * mv_steps(type, nb) : (size_t)256 * nb;
+    return q8_kind(type) ? (size_t)128 * mv_steps(type, nb) : (size_t)256 * nb;
 }
 __host__ __device__ constexpr size_t act_off_s(int type, int nb) {
-    return align16(act_off_d(type, nb) + 4 * (size_t)(type == T_Q8_0 ? 4 * mv_steps(type, nb) : nb));
+    return align16(act_off_d(type, nb) + 4 * (size_t)(q8_kind(type) ? 4 * mv_steps(type, nb) : nb));
 }
 __host__ __device__ constexpr size_t act_lds_bytes(int type, int nb) {
-    return type == T_Q8_0 ? act_off_s(type, nb) : align16(act_off_s(type, nb) + (size_t)nb * 32);
+    return q8_kind(type) ? act_off_s(type, nb) : align16(act_off_s(type, nb) + (size_t)nb * 32);
 }
 // fp32 records of one step of one tile (block split): lane partials, then d * yd per row
-__host__ __device__ constexpr size_t rec_bytes(int type) { return type == T_Q8_0 ? 64 * 16 + 8 * 16 : 64 * 8 + 8 * 4; }
+__host__ __device__ constexpr size_t rec_bytes(int type) { return q8_kind(type) ? 64 * 16 + 8 * 16 : 64 * 8 + 8 * 4; }
+__host__ __device__ constexpr int mv_tile_bytes(int type) {
+    return type == T_Q6_K ? Q6K_TILE : type == T_Q5_0 ? Q50_TILE : Q80_TILE;
+}
 
 __device__ __forceinline__ float ror_f32(float v, int n) {  // DPP row_ror:n within 16 lanes
     const int iv = __builtin_bit_cast(int, v);
@@ -65,9 +69,9 @@ struct XVals {
 };
 template <int TYPE, int WPG>
 struct XQ {
-    static constexpr int TPB = TYPE == T_Q8_0 ? 2 : 16;           // threads per block
+    static constexpr int TPB = q8_kind(TYPE) ? 2 : 16;            // threads per block
     static constexpr int BPR = 64 * WPG / TPB;                     // blocks per round
-    static constexpr int BV = TYPE == T_Q8_0 ? 32 : 256;           // values per block
+    static constexpr int BV = q8_kind(TYPE) ? 32 : 256;            // values per block
 };
 template <int TYPE, int WPG>
 __device__ __forceinline__ void xq_load(const float *__restrict__ x, int nb, int rb, XVals &xv) {
@@ -101,7 +105,7 @@ __device__ __forceinline__ void xq_store(int nb, int rb, const XVals &xv, uint8_
     float amax = 0.0f;
 #pragma unroll
     for (int u = 0; u < 16; ++u) amax = fmaxf(amax, fabsf(v[u]));
-    if (TYPE == T_Q8_0) {
+    if (q8_kind(TYPE)) {
         amax = fmaxf(amax, xor1_f32(amax));
     } else {  // the block's 16 threads are one DPP row
         amax = fmaxf(amax, ror_f32(amax, 8));
@@ -121,7 +125,7 @@ __device__ __forceinline__ void xq_store(int nb, int rb, const XVals &xv, uint8_
         w[u] = pack_q(q0, q1, q2, q3);
     }
     if (b >= nb) return;
-    if (TYPE == T_Q8_0) {  // dwords 4 tl .. 4 tl + 3 of block b
+    if (q8_kind(TYPE)) {  // dwords 4 tl .. 4 tl + 3 of block b
         uint8_t *g = act + (size_t)128 * (b >> 2) + 4 * (b & 3);
 #pragma unroll
         for (int u = 0; u < 4; ++u) *(uint32_t *)(g + 16 * (4 * tl + u)) = w[u];
@@ -153,6 +157,7 @@ __device__ __forceinline__ void xq_finish(const float *__restrict__ x, const flo
 
 // ---- one step of one lane -----------------------------------------------------------------------
 // Q8_0: q = the lane's dword of each of the 4 blocks, d = its row's 4 fp16 scales.
+// Q5_0: n = the lane's nibble bytes of the 4 blocks, h = its 16 fifth bits, d as Q8_0.
 // Q6_K: q = 4 ql dwords (2 h + s), h = 2 qh dwords, sc = its row's 16 int8 scales, d = fp16 d.
 template <int TYPE>
 struct StepW;
@@ -160,6 +165,11 @@ template <>
 struct StepW<T_Q8_0> {
     uint4 q;
     uint2 d;
+};
+template <>
+struct StepW<T_Q5_0> {
+    uint2 n, d;
+    uint32_t h;
 };
 template <>
 struct StepW<T_Q6_K> {
@@ -173,12 +183,40 @@ __device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW
     w.q = bld16(r, 64 + 16 * lane);
     w.d = bld8(r, 8 * (lane >> 3));
 }
+__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q5_0> &w) {
+    const BufRes r = buf_res(T, Q50_TILE);
+    w.n = bld8(r, 64 + 8 * lane);
+    w.h = bld2(r, 576 + 2 * lane);
+    w.d = bld8(r, 8 * (lane >> 3));
+}
 __device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q6_K> &w) {
     const BufRes r = buf_res(T, Q6K_TILE);
     w.q = bld16(r, 144 + 16 * lane);
     w.h = bld8(r, 1168 + 8 * lane);
     w.sc = bld16(r, 16 * (lane >> 3));
     w.d = bld2(r, 128 + 2 * (lane >> 3));
+}
+
+// the lane's partial s_i of each of the step's 4 blocks (y: the lane's activation dword of each)
+__device__ __forceinline__ void q32_sums(const StepW<T_Q8_0> &w, uint4 y, int sd[4]) {
+    sd[0] = dot4((int)w.q.x, (int)y.x, 0);
+    sd[1] = dot4((int)w.q.y, (int)y.y, 0);
+    sd[2] = dot4((int)w.q.z, (int)y.z, 0);
+    sd[3] = dot4((int)w.q.w, (int)y.w, 0);
+}
+// Q5_0: q5 of element 4i + t of block k is nibble byte t of n (blocks 2w / 2w + 1 in the low / high
+// nibbles of dword w) with bit 4 from the fifth bits spread to one nibble per byte; the offset
+// -16 (the reference's bx = q5 - 16) enters as a second dot with -16 in every byte
+__device__ __forceinline__ void q32_sums(const StepW<T_Q5_0> &w, uint4 y, int sd[4]) {
+    const uint32_t e = (w.h & 0x0F0Fu) | ((w.h << 12) & 0x0F0F0000u);  // byte t: bit k = block k
+    const uint32_t Y[4] = {y.x, y.y, y.z, y.w};
+    const uint32_t N[2] = {w.n.x, w.n.y};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t nib = ((k & 1) ? N[k >> 1] >> 4 : N[k >> 1]) & 0x0F0F0F0Fu;
+        const uint32_t q5 = nib | ((e << (4 - k)) & 0x10101010u);
+        sd[k] = dot4((int)q5, (int)Y[k], dot4((int)0xF0F0F0F0u, (int)Y[k], 0));
+    }
 }
 
 // int16 pair (sext byte 1, sext byte 3) of x (v_perm_b32 selectors 8, 9: sign of bytes 1, 3)
@@ -234,7 +272,7 @@ __device__ __forceinline__ int mv_tensor_of(const MvArgs &a, int64_t g) {
 template <int TYPE, int R, int TPW, int S, bool DUMP, bool SILU = false>
 __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
     constexpr int WPG = TPW * S;
-    constexpr int TB = TYPE == T_Q6_K ? Q6K_TILE : Q80_TILE;
+    constexpr int TB = mv_tile_bytes(TYPE);
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -276,11 +314,11 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
     auto step = [&](const StepW<TYPE> &w, int st) {
         const bool chain = S == 1 || ks == 0;
         uint8_t *rs = rec + (size_t)(st - nsw) * rec_bytes(TYPE);
-        if constexpr (TYPE == T_Q8_0) {
+        if constexpr (q8_kind(TYPE)) {
             const uint4 y = *(const uint4 *)(act + (size_t)128 * st + 16 * i);
             const float4 yd = *(const float4 *)(ad + 4 * st);
-            const int sd[4] = {dot4((int)w.q.x, (int)y.x, 0), dot4((int)w.q.y, (int)y.y, 0),
-                               dot4((int)w.q.z, (int)y.z, 0), dot4((int)w.q.w, (int)y.w, 0)};
+            int sd[4];
+            q32_sums(w, y, sd);
             const float fd[4] = {fp16_bits_to_f32(w.d.x & 0xFFFF) * yd.x, fp16_bits_to_f32(w.d.x >> 16) * yd.y,
                                  fp16_bits_to_f32(w.d.y & 0xFFFF) * yd.z, fp16_bits_to_f32(w.d.y >> 16) * yd.w};
             const int nbs = nb - 4 * st;  // blocks of this step (the last one may have fewer)
@@ -346,10 +384,10 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
         __syncthreads();
         if (ks != 0) return;
         // the chains over the other wavefronts' steps, CH steps at a time (all reads first)
-        constexpr int CH = TYPE == T_Q8_0 ? 4 : 8;
+        constexpr int CH = q8_kind(TYPE) ? 4 : 8;
         for (int st0 = nsw; st0 < nst; st0 += CH) {
             const uint8_t *rs = rec + (size_t)(st0 - nsw) * rec_bytes(TYPE);
-            if constexpr (TYPE == T_Q8_0) {
+            if constexpr (q8_kind(TYPE)) {
                 float4 sv[CH], fv[CH];
 #pragma unroll
                 for (int c = 0; c < CH; ++c) {  // records past the end are read but not used
@@ -403,13 +441,13 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
 // steps that the last batch of the chain loop reads past the end)
 static size_t mv_lds(int type, int nb, int tpw, int s) {
     const int nst = mv_steps(type, nb), nsw = (nst + s - 1) / s;
-    const int pad = type == T_Q8_0 ? 3 : 7;
+    const int pad = q8_kind(type) ? 3 : 7;
     return act_lds_bytes(type, nb) + (s > 1 ? ((size_t)tpw * (nst - nsw) + pad) * rec_bytes(type) : 0);
 }
 static int mv_tpw(int s) { return s == 1 ? 4 : s == 2 ? 2 : 1; }
 
 size_t matvec_lds_bytes(int type, int order, int nb) {
-    if (type == T_Q4_K) return q4k_lds_bytes(order, nb);
+    if (type == T_Q4_K || type == T_Q5_K) return q4k_lds_bytes(order, nb);
     return mv_lds(type, nb, 4, 1);
 }
 
@@ -428,7 +466,8 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 
 // Launch shape: launches of fewer than 768 tiles (tiles x tokens) split the steps of a tile over up
 // to 8 wavefronts, as many as keep the launch within 2048 wavefronts, each wavefront at 4 steps or
-// more (Q6_K: 2) and the records within LDS; tiles per workgroup 4, 2 or 1 for S = 1, 2 or more. Ring depth:
+// more (Q6_K: 2) and the records within the 160 KiB of LDS of a workgroup; tiles per workgroup 4, 2
+// or 1 for S = 1, 2 or more. Ring depth:
 // 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps, 4 otherwise.
 template <int TYPE>
 static hipError_t mv_launch_type(const MvArgs &a, int ntok, hipStream_t s) {
@@ -438,11 +477,12 @@ static hipError_t mv_launch_type(const MvArgs &a, int ntok, hipStream_t s) {
     const int64_t tiles = a.groups * ntok;
     int S = 1;
     if (tiles < 768)
-        while (S < 8 && tiles * 2 * S <= 2048 && nst >= 8 * S / SPW && mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S) <= 65536)
+        while (S < 8 && tiles * 2 * S <= 2048 && nst >= 8 * S / SPW &&
+               mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX)
             S *= 2;
     const int R = nst < 32 && tiles * S >= 1024 ? 2 : 4;
     const size_t lds = mv_lds(TYPE, nb, mv_tpw(S), S);
-    if (lds > 65536) return hipErrorInvalidValue;
+    if (lds > (S == 1 ? (size_t)65536 : GEMM_LDS_MAX)) return hipErrorInvalidValue;
     switch (S) {
     case 1: return mv_launch_r<TYPE, 4, 1>(R, a, ntok, lds, s);
     case 2: return mv_launch_r<TYPE, 2, 2>(R, a, ntok, lds, s);
@@ -452,9 +492,10 @@ static hipError_t mv_launch_type(const MvArgs &a, int ntok, hipStream_t s) {
 }
 
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
-    if (type == T_Q4_K) return launch_q4k_matvec(order, a, ntok, num_cu, s);
+    if (type == T_Q4_K || type == T_Q5_K) return launch_q4k_matvec(type, order, a, ntok, num_cu, s);
     if (type == T_Q6_K) return mv_launch_type<T_Q6_K>(a, ntok, s);
     if (type == T_Q8_0) return mv_launch_type<T_Q8_0>(a, ntok, s);
+    if (type == T_Q5_0) return mv_launch_type<T_Q5_0>(a, ntok, s);
     return hipErrorInvalidValue;
 }
 

@@ -1,5 +1,6 @@
 // fgh_q4k.hip - Q4_K decode matvec for gfx950 (the dominant kernel of a Q4_K_M decode layer), the
-// MoE expert kernel over the same layout, and the layout's upload transform.
+// MoE expert kernel over the same layout, and the layout's upload transform; Q5_K on the same
+// layout and kernel (row order).
 //
 // Device layout of a Q4_K tensor (written at upload by q4k_relayout_kernel): rows in tiles of 16
 // per matrix (tpm = ceil(rows / 16) tiles, the last one zero-padded). Tile t of matrix m, block b,
@@ -27,14 +28,26 @@
 //                   macc = fma(dmin*yd, msum, macc), out = acc - macc
 //   row order, dot_q4_K_q8k (fastgguf.c:1118-1153): lane j of a row carries the reference's lane
 //                   chains 2j, 2j+1 and min chain j; out = hsum8(acc) - hsum4(macc)
-// Short matrices split the blocks of a tile over S wavefronts (repacked order): each writes fp32
-// records {d*yd, sumi, dmin*yd, msum} to LDS and one wavefront runs the chain.
+// Short matrices split the blocks of a tile over S wavefronts, which write fp32 records of their
+// blocks to LDS; one wavefront then runs the chains over them in block order. Repacked order:
+// every wavefront records {d*yd, sumi, dmin*yd, msum} per row. Row order: wavefront 0 runs its
+// chains over the first run of blocks while it streams them, the others record each lane's two
+// lane partials and min partial with d*yd (and dmin*yd per row), and wavefront 0 continues.
+//
+// Q5_K (file block {fp16 d, fp16 dmin, 12 B scales, qh[32], ql[128]}, fastgguf.c:644-667) has the
+// Q4_K block's meta and nibbles plus one fifth bit per value: bit 2j (low nibble) or 2j + 1 (high
+// nibble) of qh[l] for byte l of chunk j. Its (tile, block) is 2816 bytes: [0, 2304) as Q4_K's
+// (nibbles from ql), then [2304, 2816) the fifth bits, lane L = 4 r + j at 2304 + 8 L: word 0 (low
+// values) and word 1 (high values), bit 8 t + d = the bit of byte t of the lane's register d. It
+// runs the row order of dot_q5_K_q8k (fastgguf.c:1178-1230), whose lanes, min lanes and final
+// combination are those of dot_q4_K_q8k with five-bit values.
 #include "fgh_internal.h"
 
 namespace fgh {
 
 constexpr int RB_ROWS = 16;     // rows per tile
-constexpr int RB_BYTES = 2304;  // one (tile, block): 16 x 144
+constexpr int RB_BYTES = 2304;  // one Q4_K (tile, block): 16 x 144
+__host__ __device__ constexpr int rb_bytes(int type) { return type == T_Q5_K ? Q5K_TILE : RB_BYTES; }
 
 // LDS activations: natural-order Q8_K blocks: qs [nb][256] at 0, d [nb] at 256 nb, and the sums of
 // each 32 values, bs32 [nb][8] int16 at align16(260 nb) (bs32[g] = bsums[2g] + bsums[2g+1] of the
@@ -42,6 +55,12 @@ constexpr int RB_BYTES = 2304;  // one (tile, block): 16 x 144
 __host__ __device__ constexpr size_t q4_off_d(int nb) { return (size_t)nb * 256; }
 __host__ __device__ constexpr size_t q4_off_s(int nb) { return ((size_t)nb * 260 + 15) & ~(size_t)15; }
 __host__ __device__ constexpr size_t q4_act_bytes(int nb) { return (q4_off_s(nb) + (size_t)nb * 16 + 15) & ~(size_t)15; }
+// LDS records of one tile in a launch that splits its blocks over s wavefronts: repacked order,
+// a float4 per (block, row); row order, for the blocks after the first wavefront's ceil(nb / s),
+// a float4 per (block, lane) and a float per (block, row)
+__host__ __device__ constexpr size_t q4_rec_bytes(int order, int nb, int s) {
+    return s == 1 ? 0 : order == 1 ? (size_t)16 * 16 * nb : (size_t)(nb - (nb + s - 1) / s) * (64 * 16 + 16 * 4);
+}
 
 // 16 threads per 256-value block; thread tl holds values 16tl..16tl+15 (4 float4 loads)
 struct XRound {
@@ -161,16 +180,20 @@ __device__ __forceinline__ void q8k_finish(XQuant<WPG, SILU> &q, const float *x,
     }
 }
 
-// one step of a lane: two 16-byte pieces of its chunk (register order) and its row's meta
+// one step of a lane: two 16-byte pieces of its chunk (register order), its row's meta and, Q5_K
+// only, the fifth bits of its low and high values
 struct RbW {
     uint4 p0, p1, m;
+    uint2 h;
 };
 // T: the (tile, block), wavefront-uniform
+template <int TYPE = T_Q4_K>
 __device__ __forceinline__ void rb_load(const uint8_t *T, uint32_t lane, RbW &w) {
-    const BufRes r = buf_res(T, RB_BYTES);
+    const BufRes r = buf_res(T, rb_bytes(TYPE));
     w.p0 = bld16(r, 256 + 16 * lane);
     w.p1 = bld16(r, 1280 + 16 * lane);
     w.m = bld16(r, 16 * (lane >> 2));
+    if (TYPE == T_Q5_K) w.h = bld8(r, 2304 + 8 * lane);
 }
 
 // Per-lane constants of the scale extraction: chunk j, the shift selecting bytes 2(j & 1) and
@@ -217,16 +240,30 @@ __device__ __forceinline__ void rb_in(const RbW &w, const uint8_t *act, int nb, 
 }
 __device__ __forceinline__ uint32_t nib_lo(uint32_t q) { return q & 0x0F0F0F0Fu; }
 __device__ __forceinline__ uint32_t nib_hi(uint32_t q) { return (q >> 4) & 0x0F0F0F0Fu; }
+// the values of register d of a lane: nibbles, with (Q5_K) bit 8 t + d of the fifth-bit word moved
+// to bit 4 of byte t
+__device__ __forceinline__ uint32_t fifth(uint32_t h, int d) {
+    return (d <= 4 ? h << (4 - d) : h >> (d - 4)) & 0x10101010u;
+}
+template <int TYPE>
+__device__ __forceinline__ uint32_t val_lo(const RbW &w, uint32_t q, int d) {
+    return TYPE == T_Q5_K ? nib_lo(q) | fifth(w.h.x, d) : nib_lo(q);
+}
+template <int TYPE>
+__device__ __forceinline__ uint32_t val_hi(const RbW &w, uint32_t q, int d) {
+    return TYPE == T_Q5_K ? nib_hi(q) | fifth(w.h.y, d) : nib_hi(q);
+}
 
 // the chunk's share of the block's sumi: sc_2j sum(lo q y) + sc_2j+1 sum(hi q y) over its 32 + 32
-// values (each dot sum |.| <= 32 * 15 * 127 < 2^23: 24-bit multiplies)
+// values (each dot sum |.| <= 32 * 31 * 127 < 2^23: 24-bit multiplies)
+template <int TYPE = T_Q4_K>
 __device__ __forceinline__ int rb_sumi_part(const RbW &w, const RbIn &in) {
     const uint32_t qd[8] = {w.p0.x, w.p0.y, w.p0.z, w.p0.w, w.p1.x, w.p1.y, w.p1.z, w.p1.w};
     int il = 0, ih = 0;
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-        il = dot4((int)nib_lo(qd[d]), (int)in.ylo[d], il);
-        ih = dot4((int)nib_hi(qd[d]), (int)in.yhi[d], ih);
+        il = dot4((int)val_lo<TYPE>(w, qd[d], d), (int)in.ylo[d], il);
+        ih = dot4((int)val_hi<TYPE>(w, qd[d], d), (int)in.yhi[d], ih);
     }
     return __mul24((int)(in.scp & 0xFFu), il) + __mul24((int)(in.scp >> 8), ih);
 }
@@ -235,14 +272,15 @@ __device__ __forceinline__ int rb_sumi_part(const RbW &w, const RbIn &in) {
 // four chunks), for lane j. Register k of a lane holds lane k (j < 2) or 4 + k (j >= 2) of its
 // chunk: one exchange with lane j ^ 2 leaves lanes 0..3 (j < 2) or 4..7 summed over two chunks,
 // one exchange with lane j ^ 1 the lane's own pair summed over all four.
+template <int TYPE = T_Q4_K>
 __device__ __forceinline__ void rb_row_lanes(const RbW &w, const RbIn &in, int j, int &u0, int &u1) {
     const uint32_t qd[8] = {w.p0.x, w.p0.y, w.p0.z, w.p0.w, w.p1.x, w.p1.y, w.p1.z, w.p1.w};
     const uint32_t sc2 = __builtin_amdgcn_perm(0u, in.scp, 0x0C010C00u);  // (sc_2j, sc_2j+1) as int16
     int lv[8];
 #pragma unroll
-    for (int d = 0; d < 8; ++d)  // each dot4 is at most 4 * 15 * 127 = 7620 in magnitude: an int16 pair
-        lv[d] = dot2_i16(sc2, pack_i16(dot4((int)nib_lo(qd[d]), (int)in.ylo[d], 0),
-                                          dot4((int)nib_hi(qd[d]), (int)in.yhi[d], 0)), 0);
+    for (int d = 0; d < 8; ++d)  // each dot4 is at most 4 * 31 * 127 = 15748 in magnitude: an int16 pair
+        lv[d] = dot2_i16(sc2, pack_i16(dot4((int)val_lo<TYPE>(w, qd[d], d), (int)in.ylo[d], 0),
+                                          dot4((int)val_hi<TYPE>(w, qd[d], d), (int)in.yhi[d], 0)), 0);
     int t[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) t[k] = lv[k] + dpp_xor2(lv[4 + k]);
@@ -275,9 +313,9 @@ __device__ __forceinline__ int q4_tensor_of(const MvArgs &a, int64_t g) {
 
 // Decode matvec. Workgroup = TPW tiles x S wavefronts per tile (wavefront ks of a tile takes its
 // ks-th run of ceil(nb / S) blocks); grid = (tiles over all tensors / TPW, tokens).
-template <int ORDER, int R, int TPW, int S, bool DUMP, bool SILU = false>
+template <int ORDER, int R, int TPW, int S, bool DUMP, bool SILU = false, int TYPE = T_Q4_K>
 __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
-    static_assert(ORDER == 1 || S == 1, "the row order keeps its chains in registers: no block split");
+    static_assert(TYPE == T_Q4_K || ORDER == 0, "Q5_K runs the row order");
     constexpr int WPG = TPW * S;
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -294,8 +332,8 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     const uint32_t mi = (a.sel ? (uint32_t)a.sel[tok] : 0u) + lt / gpm, tt = lt % gpm;  // matrix (MoE: selected), tile
     const int nbw = (nb + S - 1) / S, bb0 = ks * nbw;
     const int nbl = max(0, min(nb, bb0 + nbw) - bb0), bl = max(nbl - 1, 0);
-    const size_t bstride = (size_t)gpm * RB_BYTES;
-    const uint8_t *T0 = a.t[ti].W + (((size_t)mi * nb + min(bb0, nb - 1)) * gpm + tt) * RB_BYTES;
+    const size_t bstride = (size_t)gpm * rb_bytes(TYPE);
+    const uint8_t *T0 = a.t[ti].W + (((size_t)mi * nb + min(bb0, nb - 1)) * gpm + tt) * rb_bytes(TYPE);
 
     // (1) x for the first quantization rounds, then (2) the ring's first R steps
     const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
@@ -304,7 +342,7 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     q8k_begin(xq, x, xu, nb);
     RbW ring[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) rb_load(T0 + (size_t)min(r, bl) * bstride, lane, ring[r]);
+    for (int r = 0; r < R; ++r) rb_load<TYPE>(T0 + (size_t)min(r, bl) * bstride, lane, ring[r]);
     // (3) quantize x into LDS while the weights are in flight
     uint8_t *act = smem;
     q8k_finish(xq, x, xu, nb, act);
@@ -313,7 +351,11 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     const int64_t mrow = (int64_t)tt * RB_ROWS;  // first row of the tile in its matrix
     const int64_t obase = (int64_t)(lt / gpm) * a.t[ti].rows;
     const int64_t rows = a.t[ti].rows;
-    float4 *rec = (float4 *)(smem + q4_act_bytes(nb)) + (size_t)ts * RB_ROWS * nb;  // [b][row], S > 1
+    // S > 1: records of this tile after the activations; repacked order [b][row] float4, row order
+    // [b - nbw][lane] float4 {u0, u1, mt, d*yd} then [b - nbw][row] dmin*yd
+    uint8_t *recb = smem + q4_act_bytes(nb) + (size_t)ts * q4_rec_bytes(ORDER, nb, S);
+    float4 *rec = (float4 *)recb;
+    float *recm = (float *)(recb + (size_t)(nb - nbw) * 1024);
     const RbLane ln = rb_lane(lane);
     float acc = 0.0f, acc2 = 0.0f, macc = 0.0f;
     // one block b from ring slot r
@@ -324,7 +366,7 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
         const float fdm = fp16_bits_to_f32(w.m.x >> 16) * in.yd;
         int sumi = 0, msum = 0;
         if (ORDER == 1 || DUMP) {
-            sumi = sum4_i32(rb_sumi_part(w, in));
+            sumi = sum4_i32(rb_sumi_part<TYPE>(w, in));
             msum = sum4_i32(in.mt);
         }
         if (ORDER == 1) {
@@ -336,10 +378,15 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
             }
         } else {
             int u0, u1;
-            rb_row_lanes(w, in, j, u0, u1);
-            acc = __builtin_fmaf(fd, (float)u0, acc);
-            acc2 = __builtin_fmaf(fd, (float)u1, acc2);
-            macc = __builtin_fmaf(fdm, (float)in.mt, macc);
+            rb_row_lanes<TYPE>(w, in, j, u0, u1);
+            if (S == 1 || ks == 0) {
+                acc = __builtin_fmaf(fd, (float)u0, acc);
+                acc2 = __builtin_fmaf(fd, (float)u1, acc2);
+                macc = __builtin_fmaf(fdm, (float)in.mt, macc);
+            } else {
+                rec[(size_t)(b - nbw) * 64 + lane] = make_float4((float)u0, (float)u1, (float)in.mt, fd);
+                if (j == 0) recm[(size_t)(b - nbw) * RB_ROWS + rr] = fdm;
+            }
         }
         if (DUMP && live && j == 0 && mrow + rr < rows) {
             const size_t di = (size_t)(obase + mrow + rr) * nb + b;
@@ -354,7 +401,7 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             step(ring[r], bb0 + b0 + r);
-            rb_load(T0 + (size_t)min(b0 + r + R, bl) * bstride, lane, ring[r]);
+            rb_load<TYPE>(T0 + (size_t)min(b0 + r + R, bl) * bstride, lane, ring[r]);
         }
     }
 #pragma unroll
@@ -363,7 +410,7 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     float *y = a.t[ti].y + (size_t)tok * a.ldy + obase + mrow;
     if (S > 1) {
         __syncthreads();
-        if (ks == 0 && lane < RB_ROWS) {
+        if (ORDER == 1 && ks == 0 && lane < RB_ROWS) {
             const float4 *rr4 = rec + lane;
             int b = 0;
             for (; b + 4 <= nb; b += 4) {
@@ -382,6 +429,32 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
                 macc = __builtin_fmaf(p.z, p.w, macc);
             }
             if (live && mrow + lane < rows) y[lane] = acc - macc;
+        } else if (ORDER == 0 && ks == 0) {  // the row chains over the other wavefronts' blocks
+            int b = nbw;
+            for (; b + 4 <= nb; b += 4) {
+                float4 p[4];
+                float m[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    p[u] = rec[(size_t)(b + u - nbw) * 64 + lane];
+                    m[u] = recm[(size_t)(b + u - nbw) * RB_ROWS + rr];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    acc = __builtin_fmaf(p[u].w, p[u].x, acc);
+                    acc2 = __builtin_fmaf(p[u].w, p[u].y, acc2);
+                    macc = __builtin_fmaf(m[u], p[u].z, macc);
+                }
+            }
+            for (; b < nb; ++b) {
+                const float4 p = rec[(size_t)(b - nbw) * 64 + lane];
+                const float m = recm[(size_t)(b - nbw) * RB_ROWS + rr];
+                acc = __builtin_fmaf(p.w, p.x, acc);
+                acc2 = __builtin_fmaf(p.w, p.y, acc2);
+                macc = __builtin_fmaf(m, p.z, macc);
+            }
+            const float out = rb_row_final(acc, acc2, macc);
+            if (live && j == 0 && mrow + rr < rows) y[rr] = out;
         }
     } else if (ORDER == 1) {
         if (live && j == 0 && mrow + rr < rows) y[rr] = acc - macc;
@@ -391,54 +464,60 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     }
 }
 
-template <int ORDER, int R, int TPW, int S>
+template <int ORDER, int R, int TPW, int S, int TYPE>
 static hipError_t q4_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
     const unsigned wg = (unsigned)((a.groups + TPW - 1) / TPW);
     if (a.dump_s) {
-        q4k_mv_kernel<ORDER, R, TPW, S, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+        q4k_mv_kernel<ORDER, R, TPW, S, true, false, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
         return hipGetLastError();
     }
-    if (a.xu) q4k_mv_kernel<ORDER, R, TPW, S, false, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
-    else q4k_mv_kernel<ORDER, R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    if (a.xu) q4k_mv_kernel<ORDER, R, TPW, S, false, true, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    else q4k_mv_kernel<ORDER, R, TPW, S, false, false, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     return hipGetLastError();
 }
-template <int ORDER, int TPW, int S>
+template <int ORDER, int TPW, int S, int TYPE = T_Q4_K>
 static hipError_t q4_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
-    return R == 2 ? q4_launch<ORDER, 2, TPW, S>(a, ntok, lds, s) : q4_launch<ORDER, 4, TPW, S>(a, ntok, lds, s);
+    return R == 2 ? q4_launch<ORDER, 2, TPW, S, TYPE>(a, ntok, lds, s) : q4_launch<ORDER, 4, TPW, S, TYPE>(a, ntok, lds, s);
 }
 
 // LDS of a launch: the activations, and with a block split the records of TPW tiles
-static size_t q4_lds(int nb, int tpw, int s) {
-    return q4_act_bytes(nb) + (s > 1 ? (size_t)tpw * RB_ROWS * nb * 16 : 0);
-}
+static size_t q4_lds(int order, int nb, int tpw, int s) { return q4_act_bytes(nb) + (size_t)tpw * q4_rec_bytes(order, nb, s); }
 static int q4_tpw(int s) { return s == 1 ? 4 : s == 2 ? 2 : 1; }
 
-size_t q4k_lds_bytes(int, int nb) { return q4_lds(nb, 4, 1); }
+size_t q4k_lds_bytes(int order, int nb) { return q4_lds(order, nb, 4, 1); }
 
 // Launch shape (measured on MI355X at the decode-layer shapes). Wavefronts per tile S: launches of
-// fewer than 768 tiles (tiles x tokens) split the blocks of a tile over up to 8 wavefronts
-// (repacked order), as many as keep the launch within 2048 wavefronts and each wavefront at 4
-// blocks or more; larger launches keep one wavefront per tile (the row order always does). Tiles
-// per workgroup: 4, 2 or 1 for S = 1, 2 or more. Ring depth R: 2 steps when the launch has 1024
+// fewer than 768 tiles (tiles x tokens) split the blocks of a tile over up to 8 wavefronts, as many
+// as keep the launch within 2048 wavefronts, each wavefront at 4 blocks or more and the LDS within
+// the 160 KiB of a workgroup; larger launches keep one wavefront per tile. Tiles per workgroup: 4,
+// 2 or 1 for S = 1, 2 or more. Ring depth R: 2 steps when the launch has 1024
 // wavefronts or more over rows shorter than 32 blocks (enough loads in flight across the chip), 4
 // otherwise.
-hipError_t launch_q4k_matvec(int order, const MvArgs &a, int ntok, int, hipStream_t s) {
+template <int ORDER, int TYPE>
+static hipError_t q4_launch_s(int S, int R, const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
+    switch (S) {
+    case 1: return q4_launch_r<ORDER, 4, 1, TYPE>(R, a, ntok, lds, s);
+    case 2: return q4_launch_r<ORDER, 2, 2, TYPE>(R, a, ntok, lds, s);
+    case 4: return q4_launch_r<ORDER, 1, 4, TYPE>(R, a, ntok, lds, s);
+    default: return q4_launch_r<ORDER, 1, 8, TYPE>(R, a, ntok, lds, s);
+    }
+}
+hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int, hipStream_t s) {
     const int nb = a.nb;
     if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
+    if (type == T_Q5_K) order = 0;  // no repacked order for Q5_K
     const int64_t tiles = a.groups * ntok;
     int S = 1;
-    if (order == 1 && tiles < 768)
-        while (S < 8 && tiles * 2 * S <= 2048 && nb >= 8 * S && q4_lds(nb, q4_tpw(2 * S), 2 * S) <= 65536) S *= 2;
+    if (tiles < 768)
+        while (S < 8 && tiles * 2 * S <= 2048 && nb >= 8 * S &&
+               q4_lds(order, nb, q4_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX)
+            S *= 2;
     const int R = nb < 32 && tiles * S >= 1024 ? 2 : 4;
-    const size_t lds = q4_lds(nb, q4_tpw(S), S);
-    if (lds > 65536) return hipErrorInvalidValue;
-    if (order == 0) return q4_launch_r<0, 4, 1>(R, a, ntok, lds, s);
-    switch (S) {
-    case 1: return q4_launch_r<1, 4, 1>(R, a, ntok, lds, s);
-    case 2: return q4_launch_r<1, 2, 2>(R, a, ntok, lds, s);
-    case 4: return q4_launch_r<1, 1, 4>(R, a, ntok, lds, s);
-    default: return q4_launch_r<1, 1, 8>(R, a, ntok, lds, s);
-    }
+    const size_t lds = q4_lds(order, nb, q4_tpw(S), S);
+    if (lds > (S == 1 ? (size_t)65536 : GEMM_LDS_MAX)) return hipErrorInvalidValue;
+    if (type == T_Q5_K) return q4_launch_s<0, T_Q5_K>(S, R, a, ntok, lds, s);
+    if (order == 0) return q4_launch_s<0, T_Q4_K>(S, R, a, ntok, lds, s);
+    return q4_launch_s<1, T_Q4_K>(S, R, a, ntok, lds, s);
 }
 
 // Q8_K images of activation rows, in the kernels' LDS layout (q4_act_bytes(nb) bytes per row): row
@@ -628,34 +707,53 @@ hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *seg, const int32_t *sl
     return hipGetLastError();
 }
 
-// upload-time re-layout of Q4_K rows into the tile layout above; one thread per destination byte
-__global__ void q4k_relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int64_t rows,
+// upload-time re-layout of Q4_K / Q5_K rows into the tile layout above; one thread per destination
+// byte (a Q5_K fifth-bit byte gathers bit 2j or 2j + 1 of 8 bytes of the block's qh)
+__global__ void q4k_relayout_kernel(int type, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int64_t rows,
                                     int nb, int64_t tpm, int64_t total, int64_t row_bytes) {
+    const int TB = rb_bytes(type), BB = type == T_Q5_K ? 176 : 144, QOFF = type == T_Q5_K ? 48 : 16;
     for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t tb = o / RB_BYTES;
-        const int ob = (int)(o - tb * RB_BYTES);
+        const int64_t tb = o / TB;
+        const int ob = (int)(o - tb * TB);
         const int64_t mb = tb / tpm, tl = tb - mb * tpm;  // (matrix, block), tile
         const int64_t m = mb / nb;
         const int b = (int)(mb - m * nb);
-        int r, byte;
+        int r, byte = -1, jj = 0, bi = 0;
         if (ob < 256) {
             r = ob >> 4;
             byte = ob & 15;
-        } else {
-            const int u = ob - 256, hh = u >> 10, L = (u >> 4) & 63, jj = L & 3;
+        } else if (ob < 2304) {
+            const int u = ob - 256, hh = u >> 10, L = (u >> 4) & 63;
+            jj = L & 3;
             r = L >> 2;
-            byte = 16 + 32 * jj + 16 * (hh ^ (jj >> 1)) + (u & 15);
+            byte = QOFF + 32 * jj + 16 * (hh ^ (jj >> 1)) + (u & 15);
+        } else {  // Q5_K: byte bi of lane L's fifth bits (word bi >> 2: low / high values, byte t = bi & 3)
+            const int u = ob - 2304, L = u >> 3;
+            jj = L & 3;
+            r = L >> 2;
+            bi = u & 7;
         }
         const int64_t row = tl * RB_ROWS + r;
-        dst[o] = row < rows ? src[(m * rows + row) * row_bytes + (int64_t)b * 144 + byte] : (uint8_t)0;
+        int v = 0;
+        if (row < rows) {
+            const uint8_t *p = src + (m * rows + row) * row_bytes + (int64_t)b * BB;
+            if (byte >= 0) {
+                v = p[byte];
+            } else {  // bit d: the fifth bit of byte t of register d, chunk byte 16 ((d >> 2) ^ (j >> 1)) + 4 (d & 3) + t
+                const int sh = 2 * jj + (bi >> 2), t = bi & 3;
+#pragma unroll
+                for (int d = 0; d < 8; ++d) v |= ((p[16 + 16 * ((d >> 2) ^ (jj >> 1)) + 4 * (d & 3) + t] >> sh) & 1) << d;
+            }
+        }
+        dst[o] = (uint8_t)v;
     }
 }
 
-hipError_t launch_q4k_relayout(const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t tpm, int64_t total,
-                               int64_t row_bytes, hipStream_t s) {
+hipError_t launch_q4k_relayout(int type, const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t tpm,
+                               int64_t total, int64_t row_bytes, hipStream_t s) {
     const int64_t want = (total + 255) / 256;
     const int grid = (int)(want < 65536 ? want : 65536);
-    q4k_relayout_kernel<<<grid, 256, 0, s>>>(src, dst, rows, nb, tpm, total, row_bytes);
+    q4k_relayout_kernel<<<grid, 256, 0, s>>>(type, src, dst, rows, nb, tpm, total, row_bytes);
     return hipGetLastError();
 }
 

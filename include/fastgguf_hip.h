@@ -1,8 +1,9 @@
 /*
  * fastgguf_hip.h - C ABI of the MI355X (gfx950) backend for fastgguf's quantized
- * weight x Q8-activation hot path: GGUF Q4_K / Q6_K / Q8_0 weights multiplied by activations
- * quantized to the reference's Q8 / Q8_K blocks, as a decode matvec, a <=64-token prompt matmul
- * and a mixture-of-experts FFN over the router-selected experts.
+ * weight x Q8-activation hot path: GGUF Q4_K / Q6_K / Q8_0 weights, and the Q5_K / Q5_0 of
+ * Q5_K_M files and of K-quant files' fallback tensors, multiplied by activations quantized to the
+ * reference's Q8 / Q8_K blocks, as a decode matvec, a <=64-token prompt matmul and a
+ * mixture-of-experts FFN over the router-selected experts.
  *
  * The ABI is plain C: fixed-width integers, plain pointers and sizes, opaque handles, no
  * callbacks, no varargs, no C++ or torch types. A Rust `extern "C"` block or a C caller binds it
@@ -14,7 +15,8 @@
  * its OpenCL kernels: activations are quantized exactly as quantize_q8 / quantize_q8k
  * (fastgguf.c:746-793) do, per-block integer dot products are exact, and the fp32 outputs follow
  * the reference's accumulation order for matvec and MoE (bit-identical) and agree to within
- * 1e-5 relative per output vector for the MFMA prompt GEMM.
+ * 1e-5 relative per output vector for the MFMA prompt GEMM (and for the per-token kernels that
+ * stand in for the reference's CPU prompt GEMM of Q6_K, Q8_0 and Q5_0 tensors).
  *
  * Threading: a context is used by one host thread at a time, like the reference's g_gpu state
  * (fastgguf.c:1845-1857). Host-pointer calls are synchronous: outputs are valid on return, as
@@ -40,8 +42,10 @@ extern "C" {
 #endif
 
 /* GGML tensor types handled here (the reference's enum, fastgguf.c:215-221) */
+#define FGH_T_Q5_0 6u
 #define FGH_T_Q8_0 8u
 #define FGH_T_Q4_K 12u
+#define FGH_T_Q5_K 13u
 #define FGH_T_Q6_K 14u
 
 /* status codes */

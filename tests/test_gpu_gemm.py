@@ -7,12 +7,15 @@ Bar:
     outputs use a different summation order from gemmk_kern, so they are compared with the
     reference's own tolerance: max|y - y_ref| / max|y_ref| <= 1e-5 per token (fastgguf.c:5723-5733),
     against the oracle's restatement of gemm_kquant and against the reference's golden outputs.
-  - Q6_K and Q8_0 run the per-token decode kernels (dot_q6_K_q8k / dot_q8_0_q8 orders): compared
-    with the same tolerance against the GEMM orders.
+  - Q6_K, Q8_0 and Q5_0 run the per-token decode kernels (dot_q6_K_q8k / dot_q8_0_q8 /
+    dot_q5_0_q8 orders): compared with the same tolerance against the GEMM orders (gemm_kquant,
+    gemm_q32).
+  - Q5_K has no prompt GEMM in the reference: its matmul is the row kernel per token there and here,
+    so it is compared bit for bit.
 """
 import numpy as np
 import pytest
-from conftest import golden, rel_err
+from conftest import bits_equal, golden, rel_err
 
 from fastgguf_amd import synth as S
 from fastgguf_amd.backend import ORDER_REPACKED, ORDER_ROW
@@ -31,7 +34,8 @@ def check_tokens(Y, Yref):
         assert e <= TOL, f"token {t}: rel err {e:.3e}"
 
 
-@pytest.mark.parametrize("name,t", [("q8_0", S.T_Q8_0), ("q4_k", S.T_Q4_K), ("q6_k", S.T_Q6_K)])
+@pytest.mark.parametrize("name,t", [("q8_0", S.T_Q8_0), ("q4_k", S.T_Q4_K), ("q6_k", S.T_Q6_K),
+                                    ("q5_0", S.T_Q5_0), ("q5_k", S.T_Q5_K)])
 @pytest.mark.parametrize("nb", [8, 45])
 def test_matmul_matches_golden(backend, name, t, nb):
     g = golden("matmul.npz")
@@ -40,7 +44,10 @@ def test_matmul_matches_golden(backend, name, t, nb):
         if order == ORDER_REPACKED and t != S.T_Q4_K:
             continue
         tt = backend.upload(t, X.shape[1], w, order=order)
-        check_tokens(backend.matmul(tt, X), g[key])
+        Y = backend.matmul(tt, X)
+        check_tokens(Y, g[key])
+        if t == S.T_Q5_K:
+            assert bits_equal(Y, g[key])
         tt.free()
 
 
@@ -74,7 +81,7 @@ def test_gemm_block_ints_exact(backend, oracle, case):
     tt.free()
 
 
-@pytest.mark.parametrize("t", [S.T_Q8_0, S.T_Q6_K])
+@pytest.mark.parametrize("t", [S.T_Q8_0, S.T_Q6_K, S.T_Q5_0, S.T_Q5_K])
 @pytest.mark.parametrize("nb", [8, 64])
 def test_matmul_other_types(backend, oracle, t, nb):
     cols, rows = 2048, 200

@@ -3,7 +3,8 @@ the oracle (and the reference's golden vectors), through the C ABI.
 
 Bar: bit-exact. Activation quants, scales and sums, and per-block integer dot products are
 integer work; the fp32 matvec outputs reproduce the reference kernels' accumulation order
-(dot_q8_0_q8 / dot_q4_K_q8k / dot_q4Kx8 / dot_q6_K_q8k), so they are compared bit for bit too
+(dot_q8_0_q8 / dot_q4_K_q8k / dot_q4Kx8 / dot_q6_K_q8k / dot_q5_0_q8 / dot_q5_K_q8k), so they are
+compared bit for bit too
 (stronger than the 1e-5 per-vector tolerance the north star allows, which is also checked).
 """
 import numpy as np
@@ -49,7 +50,10 @@ def test_quantizers_bit_exact(backend, oracle, n):
     assert backend.quantize_q8k(x).tobytes() == oracle.quantize_q8k(x).tobytes()
 
 
-@pytest.mark.parametrize("name,t", [("q8_0", S.T_Q8_0), ("q4_k", S.T_Q4_K), ("q6_k", S.T_Q6_K)])
+NAMED = [("q8_0", S.T_Q8_0), ("q4_k", S.T_Q4_K), ("q6_k", S.T_Q6_K), ("q5_0", S.T_Q5_0), ("q5_k", S.T_Q5_K)]
+
+
+@pytest.mark.parametrize("name,t", NAMED)
 @pytest.mark.parametrize("gen", ["synth", "bytes"])
 def test_matvec_matches_golden(backend, name, t, gen):
     g = golden("matvec.npz")
@@ -74,6 +78,14 @@ CASES = [  # (type, rows, cols, n_mats, order)
     (S.T_Q4_K, 16, 14336, 1, ORDER_ROW),
     (S.T_Q6_K, 64, 512, 1, ORDER_ROW),
     (S.T_Q6_K, 13, 4608, 2, ORDER_ROW),        # ragged rows, 18 blocks (2 chunks)
+    (S.T_Q5_0, 64, 544, 1, ORDER_ROW),         # 17 blocks: a last step of one block
+    (S.T_Q5_0, 20, 96, 1, ORDER_ROW),          # 3 blocks: one step with a padding block
+    (S.T_Q5_0, 37, 4096 + 64, 2, ORDER_ROW),   # ragged rows, 3-D, a last step of two blocks
+    (S.T_Q5_K, 64, 768, 1, ORDER_ROW),
+    (S.T_Q5_K, 21, 256, 3, ORDER_ROW),         # ragged rows, 3-D, one block
+    (S.T_Q5_K, 16, 14336, 1, ORDER_ROW),       # many blocks (row-order block split over 8 wavefronts)
+    (S.T_Q4_K, 21, 4096, 3, ORDER_ROW),        # row-order split over 4 wavefronts, 3-D, ragged rows
+    (S.T_Q5_K, 40, 2304, 1, ORDER_ROW),        # row-order split of 9 blocks: runs of 5 and 4
 ]
 
 
@@ -93,15 +105,22 @@ def test_block_ints_and_matvec_exact(backend, oracle, case):
     tt.free()
 
 
-@pytest.mark.parametrize("cfg", ["cfg1_q8_0", "gate_q4k_rp", "gate_q4k_row", "down_q4k_rp", "lmhead_q6k"])
+@pytest.mark.parametrize("cfg", ["cfg1_q8_0", "gate_q4k_rp", "gate_q4k_row", "down_q4k_rp", "lmhead_q6k",
+                                 "gate_q5k", "down_q5_0", "down_q5k", "down_q4k_row", "down_q8_0"])
 def test_matvec_config_shapes(backend, oracle, cfg):
-    """BASELINE.json shapes with the benchmark's weight distributions."""
+    """BASELINE.json shapes with the benchmark's weight distributions (and the same FFN shapes
+    for Q5_K and Q5_0)."""
     t, rows, cols, order = {
         "cfg1_q8_0": (S.T_Q8_0, 4096, 4096, ORDER_ROW),
         "gate_q4k_rp": (S.T_Q4_K, 14336, 4096, ORDER_REPACKED),
         "gate_q4k_row": (S.T_Q4_K, 14336, 4096, ORDER_ROW),
         "down_q4k_rp": (S.T_Q4_K, 4096, 14336, ORDER_REPACKED),
         "lmhead_q6k": (S.T_Q6_K, 128256, 4096, ORDER_ROW),
+        "gate_q5k": (S.T_Q5_K, 14336, 4096, ORDER_ROW),
+        "down_q5_0": (S.T_Q5_0, 4096, 14336, ORDER_ROW),
+        "down_q5k": (S.T_Q5_K, 4096, 14336, ORDER_ROW),
+        "down_q4k_row": (S.T_Q4_K, 4096, 14336, ORDER_ROW),
+        "down_q8_0": (S.T_Q8_0, 4096, 14336, ORDER_ROW),
     }[cfg]
     w = S.weights(t, rows, cols, 11)
     x = S.activations(cols, 12)
@@ -127,7 +146,7 @@ def test_matvec_multi_qkv(backend, oracle):
         t.free()
 
 
-@pytest.mark.parametrize("t", [S.T_Q8_0, S.T_Q4_K, S.T_Q6_K])
+@pytest.mark.parametrize("t", [S.T_Q8_0, S.T_Q4_K, S.T_Q6_K, S.T_Q5_0, S.T_Q5_K])
 @pytest.mark.parametrize("nb", [2, 3, 7])
 def test_matmul_small_batch(backend, oracle, t, nb):
     """nb < 8: the per-token decode kernel (matmul 3006-3009 for repacked tensors; the x4 tiles
@@ -161,8 +180,17 @@ def test_upload_refusals(backend):
     with pytest.raises(BackendError) as e:
         backend.upload(S.T_Q8_0, 1821 * 32, np.zeros(8 * 1821 * 34, np.uint8), rows=8)
     assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:  # Q5_K as Q4_K (238 blocks), Q5_0 as Q8_0 (1821)
+        backend.upload(S.T_Q5_K, 238 * 256, np.zeros(16 * 238 * 176, np.uint8), rows=16)
+    assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:
+        backend.upload(S.T_Q5_0, 1821 * 32, np.zeros(8 * 1821 * 22, np.uint8), rows=8)
+    assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:  # Q5_0 cols % 32 != 0
+        backend.upload(S.T_Q5_0, 48, np.zeros(8 * 22, np.uint8), rows=8)
+    assert e.value.status == SKIP_TYPE
     info1 = backend.info()
-    assert info1["n_skip_type"] == info0["n_skip_type"] + 5
+    assert info1["n_skip_type"] == info0["n_skip_type"] + 8
     from fastgguf_amd.backend import Backend
     small = Backend(0, budget_bytes=1 << 20)
     with pytest.raises(BackendError) as e:
@@ -184,11 +212,12 @@ def test_widest_q4k_rows(backend, oracle, order):
     tt.free()
 
 
-@pytest.mark.parametrize("t,nb", [(S.T_Q6_K, 224), (S.T_Q8_0, 1820), (S.T_Q8_0, 1819)])
+@pytest.mark.parametrize("t,nb", [(S.T_Q6_K, 224), (S.T_Q8_0, 1820), (S.T_Q8_0, 1819), (S.T_Q5_0, 1820),
+                                  (S.T_Q5_0, 1817), (S.T_Q5_K, 237)])
 def test_widest_q6k_q80_rows(backend, oracle, t, nb):
-    """The widest Q6_K (K = 57344) and Q8_0 (K = 58240) rows the decode kernel accepts, and a
-    Q8_0 width whose last 4-block step is ragged."""
-    rows, cols = 20, nb * (256 if t == S.T_Q6_K else 32)
+    """The widest Q6_K (K = 57344), Q8_0 / Q5_0 (K = 58240) and Q5_K (K = 60672) rows the decode
+    kernels accept, and Q8_0 / Q5_0 widths whose last 4-block step is ragged."""
+    rows, cols = 20, nb * (32 if S.uses_q8(t) else 256)
     w = S.random_bytes_weights(t, rows, cols, 133 + nb)
     x = S.activations(cols, 134)
     tt = backend.upload(t, cols, w)
@@ -202,6 +231,8 @@ SILU_CASES = [  # (type, rows, cols, order): split launches (S > 1) and one-wave
     (S.T_Q4_K, 40, 2048, ORDER_ROW),
     (S.T_Q6_K, 13, 4608, ORDER_ROW),
     (S.T_Q8_0, 37, 4128, ORDER_ROW),
+    (S.T_Q5_K, 40, 2048, ORDER_ROW),
+    (S.T_Q5_0, 37, 4128, ORDER_ROW),
 ]
 
 

@@ -49,6 +49,47 @@ def test_moe_matches_golden(backend):
         t.free()
 
 
+def test_moe_q5_matches_golden(backend):
+    """Q5_K gate / up and a Q5_0 down projection over ff = 160 (a K-quant file's fallback types):
+    the generic expert path (decode kernels with an expert index), bit for bit."""
+    g = golden("moe_q5.npz")
+    E, K, D, F, T = (int(v) for v in g["dims"])
+    tg, tu, td = (int(v) for v in g["types"])
+    gate = backend.upload(tg, D, g["gate"], rows=F, n_mats=E)
+    up = backend.upload(tu, D, g["up"], rows=F, n_mats=E)
+    down = backend.upload(td, F, g["down"], rows=D, n_mats=E)
+    for n in (1, T):  # one token, and every token in one call
+        Y, sel, w = backend.moe_ffn(gate, up, down, K, g["logits"][:n], g["X"][:n])
+        assert np.array_equal(sel, g["sel"][:n])
+        assert bits_equal(w, g["w"][:n])
+        assert bits_equal(Y, g["Y"][:n])
+    for t in (gate, up, down):
+        t.free()
+
+
+@pytest.mark.parametrize("types", [(S.T_Q5_K, S.T_Q5_K, S.T_Q5_K), (S.T_Q4_K, S.T_Q4_K, S.T_Q5_0),
+                                   (S.T_Q5_0, S.T_Q5_0, S.T_Q6_K)])
+def test_moe_mixed_types_match_oracle(backend, oracle, types):
+    # ff = 352 (11 blocks of 32, a last step of 3 blocks) where the down projection takes Q8
+    # activations; a K-quant down projection needs ff % 256 == 0
+    E, K, D, F, T = 16, 4, 512, 352 if S.uses_q8(types[2]) else 512, 6
+    gw = S.random_bytes_weights(types[0], E * F, D, 230)
+    uw = S.random_bytes_weights(types[1], E * F, D, 231)
+    dw = S.random_bytes_weights(types[2], E * D, F, 232)
+    X = S.activations(D, 233, rows=T)
+    logits = S.router_logits(T, E, 234)
+    Yo, so, wo = oracle.moe_ffn(types, gw, uw, dw, E, K, D, F, logits, X)
+    gate = backend.upload(types[0], D, gw, rows=F, n_mats=E)
+    up = backend.upload(types[1], D, uw, rows=F, n_mats=E)
+    down = backend.upload(types[2], F, dw, rows=D, n_mats=E)
+    Y, sel, w = backend.moe_ffn(gate, up, down, K, logits, X)
+    assert np.array_equal(sel, so)
+    assert bits_equal(w, wo)
+    assert bits_equal(Y, Yo)
+    for t in (gate, up, down):
+        t.free()
+
+
 @pytest.mark.parametrize("E,K,D,F,T", [(16, 4, 512, 256, 1), (16, 4, 512, 256, 5), (32, 8, 768, 512, 9)])
 def test_moe_matches_oracle(backend, oracle, E, K, D, F, T):
     gw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 200 + E)
