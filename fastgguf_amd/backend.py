@@ -31,6 +31,8 @@ EXPORTS = (
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
     "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_expf", "fgh_fp16_to_f32",
+    "fgh_gguf_open", "fgh_gguf_close", "fgh_gguf_summary", "fgh_gguf_tensor", "fgh_gguf_find",
+    "fgh_gguf_kv_num", "fgh_gguf_kv_str", "fgh_gguf_data", "fgh_upload_gguf",
 )
 
 
@@ -38,6 +40,11 @@ class BackendError(RuntimeError):
     def __init__(self, status: int, msg: str):
         super().__init__(f"fastgguf_hip status {status}: {msg}")
         self.status = status
+
+
+class GgufTensorT(C.Structure):
+    _fields_ = [("name", C.c_char * 128), ("type", C.c_uint32), ("n_dims", C.c_int32), ("ne", C.c_uint64 * 4),
+                ("offset", C.c_uint64), ("nbytes", C.c_uint64)]
 
 
 class InfoT(C.Structure):
@@ -94,6 +101,15 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_gemm_block_ints": (i32, [vp, vp, f32p, i32, i32, vp, vp]),
         "fgh_fp16_to_f32": (i32, [vp, vp, i32, vp]),
         "fgh_expf": (i32, [vp, f32p, i32, vp]),
+        "fgh_gguf_open": (i32, [C.c_char_p, C.POINTER(vp), C.c_char_p, C.c_size_t]),
+        "fgh_gguf_close": (None, [vp]),
+        "fgh_gguf_summary": (i32, [vp, C.POINTER(u32), C.POINTER(u64), C.POINTER(i64), C.POINTER(i64)]),
+        "fgh_gguf_tensor": (i32, [vp, i64, C.POINTER(GgufTensorT)]),
+        "fgh_gguf_find": (i64, [vp, C.c_char_p]),
+        "fgh_gguf_kv_num": (i32, [vp, C.c_char_p, C.c_double, C.POINTER(C.c_double)]),
+        "fgh_gguf_kv_str": (C.c_char_p, [vp, C.c_char_p]),
+        "fgh_gguf_data": (vp, [vp, i64]),
+        "fgh_upload_gguf": (i32, [vp, vp, i64, i32, C.POINTER(vp)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -126,6 +142,63 @@ class Tensor:
         if self.handle:
             self.backend.lib.fgh_tensor_free(self.handle)
             self.handle = None
+
+
+class Gguf:
+    """A mapped GGUF file (gguf_open, fastgguf.c:342-440); needs no device."""
+
+    def __init__(self, path: str):
+        self.lib = load_library()
+        h = C.c_void_p()
+        err = C.create_string_buffer(256)
+        rc = self.lib.fgh_gguf_open(os.fsencode(path), C.byref(h), err, len(err))
+        if rc != OK:
+            raise BackendError(rc, err.value.decode(errors="replace"))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            self.lib.fgh_gguf_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def summary(self) -> dict:
+        v, a, nk, nt = C.c_uint32(), C.c_uint64(), C.c_int64(), C.c_int64()
+        self.lib.fgh_gguf_summary(self.handle, C.byref(v), C.byref(a), C.byref(nk), C.byref(nt))
+        return {"version": v.value, "alignment": a.value, "n_kvs": nk.value, "n_tensors": nt.value}
+
+    def tensor(self, i: int) -> dict:
+        t = GgufTensorT()
+        if self.lib.fgh_gguf_tensor(self.handle, i, C.byref(t)) != OK:
+            raise IndexError(i)
+        return {"name": t.name.decode(errors="replace"), "type": t.type, "n_dims": t.n_dims, "ne": list(t.ne)[: t.n_dims],
+                "offset": t.offset, "nbytes": t.nbytes}
+
+    def tensors(self) -> list[dict]:
+        return [self.tensor(i) for i in range(self.summary()["n_tensors"])]
+
+    def find(self, name: str) -> int:
+        return self.lib.fgh_gguf_find(self.handle, name.encode())
+
+    def kv_num(self, key: str, default: float = 0.0) -> float:
+        out = C.c_double()
+        self.lib.fgh_gguf_kv_num(self.handle, key.encode(), default, C.byref(out))
+        return out.value
+
+    def kv_str(self, key: str) -> str | None:
+        v = self.lib.fgh_gguf_kv_str(self.handle, key.encode())
+        return None if v is None else v.decode()
+
+    def data(self, i: int) -> np.ndarray:
+        """A tensor's bytes, read from the mapping (a copy)."""
+        info = self.tensor(i)
+        p = self.lib.fgh_gguf_data(self.handle, i)
+        return np.ctypeslib.as_array((C.c_uint8 * info["nbytes"]).from_address(p)).copy()
 
 
 class Backend:
@@ -169,6 +242,17 @@ class Backend:
         self._check(self.lib.fgh_upload(self.ctx, type_, cols, rows, n_mats, order, _p(data), data.size,
                                         C.byref(h)))
         return Tensor(self, h.value, type_, cols, rows, n_mats)
+
+    # -- gpu_upload_tensor (2060) on a tensor of a mapped GGUF file
+    def upload_gguf(self, g: Gguf, name_or_index, order: int = ORDER_AUTO) -> Tensor:
+        i = g.find(name_or_index) if isinstance(name_or_index, str) else int(name_or_index)
+        if i < 0:
+            raise KeyError(name_or_index)
+        info = g.tensor(i)
+        ne = info["ne"] + [1] * (4 - len(info["ne"]))
+        h = C.c_void_p()
+        self._check(self.lib.fgh_upload_gguf(self.ctx, g.handle, i, order, C.byref(h)))
+        return Tensor(self, h.value, info["type"], ne[0], ne[1], ne[2] * ne[3])
 
     # -- matvec (2575)
     def matvec(self, t: Tensor, x: np.ndarray) -> np.ndarray:
@@ -354,5 +438,5 @@ class Backend:
                                              Y_dev, n_tok))
 
 
-__all__ = ["Backend", "BackendError", "Tensor", "load_library", "EXPORTS", "T_Q4_K", "T_Q5_0", "T_Q5_K", "T_Q6_K", "T_Q8_0",
+__all__ = ["Backend", "BackendError", "Gguf", "Tensor", "load_library", "EXPORTS", "T_Q4_K", "T_Q5_0", "T_Q5_K", "T_Q6_K", "T_Q8_0",
            "ORDER_AUTO", "ORDER_ROW", "ORDER_REPACKED"]

@@ -26,6 +26,7 @@
 #ifndef FASTGGUF_HIP_H
 #define FASTGGUF_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -101,6 +102,38 @@ FGH_API const char *fgh_last_error(const fgh_ctx *ctx);
 FGH_API int fgh_upload(fgh_ctx *ctx, uint32_t ggml_type, int64_t cols, int64_t rows, int64_t n_mats,
                int order, const void *host_data, uint64_t nbytes, fgh_tensor **out);
 FGH_API void fgh_tensor_free(fgh_tensor *t);
+
+/* ---- GGUF files: replaces gguf_open (fastgguf.c:342-440), kv_num (441-448) and tensor_find
+ * (450-454); fgh_upload_gguf is gpu_upload_tensor (2060-2081) on a tensor of the mapped file ----
+ * fgh_gguf_open maps the file read-only and parses its header, metadata and tensor table with the
+ * reference's rules (magic, general.alignment, block sizes, bounds); it needs no device. On
+ * failure it returns a negative status, *out = NULL, and a message in err (err_len bytes; err may
+ * be NULL). A tensor info holds the reference's tensor_t fields: name, type, dims (ne[0] = cols,
+ * the reduction; ne[1] = rows; ne[2] = experts of a 3-D MoE tensor), the byte offset of its data
+ * from the start of the file, and its byte count. fgh_gguf_find returns a tensor's index or -1;
+ * fgh_gguf_kv_num gives a numeric entry (or the first element of an integer array), else def;
+ * fgh_gguf_kv_str a string entry or NULL; fgh_gguf_data a tensor's bytes in the mapping (valid
+ * until fgh_gguf_close). fgh_upload_gguf uploads tensor `index` as fgh_upload would its bytes,
+ * with cols = ne[0], rows = ne[1] and n_mats = the product of the higher dims. */
+typedef struct fgh_gguf fgh_gguf;
+typedef struct {
+    char name[128];
+    uint32_t type;
+    int32_t n_dims;
+    uint64_t ne[4];
+    uint64_t offset;
+    uint64_t nbytes;
+} fgh_gguf_tensor_info;
+FGH_API int fgh_gguf_open(const char *path, fgh_gguf **out, char *err, size_t err_len);
+FGH_API void fgh_gguf_close(fgh_gguf *g);
+FGH_API int fgh_gguf_summary(const fgh_gguf *g, uint32_t *version, uint64_t *alignment, int64_t *n_kvs,
+                             int64_t *n_tensors);
+FGH_API int fgh_gguf_tensor(const fgh_gguf *g, int64_t index, fgh_gguf_tensor_info *out);
+FGH_API int64_t fgh_gguf_find(const fgh_gguf *g, const char *name);
+FGH_API int fgh_gguf_kv_num(const fgh_gguf *g, const char *key, double def, double *out);
+FGH_API const char *fgh_gguf_kv_str(const fgh_gguf *g, const char *key);
+FGH_API const void *fgh_gguf_data(const fgh_gguf *g, int64_t index);
+FGH_API int fgh_upload_gguf(fgh_ctx *ctx, const fgh_gguf *g, int64_t index, int order, fgh_tensor **out);
 
 /* ---- matvec: replaces fg_gpu_matvec (fastgguf.c:2114) and the CPU matvec (2575) ----
  * y[r] = dot(W[r], Q8(x)) for all rows of all matrices (rows * n_mats outputs); x has cols

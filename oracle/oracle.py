@@ -233,6 +233,7 @@ class Reference:
         L.fgr_tensor_free.argtypes = [C.c_void_p]
         L.fgr_tensor_free.restype = None
         L.fgr_tensor_matvec_multi.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.fgr_gguf_table.argtypes = [C.c_char_p] + [C.c_void_p] * 10 + [C.c_int64, C.c_char_p, C.c_int, C.c_void_p]
         L.fgr_init(256)
 
     @property
@@ -292,6 +293,24 @@ class Reference:
         yp = (C.c_void_p * len(ys))(*[y.ctypes.data for y in ys])
         if self.lib.fgr_tensor_matvec_multi(len(hs), arr, _ptr(x), yp) != 0:
             raise ValueError("fgr_tensor_matvec_multi failed")
+
+    def gguf_table(self, path, keys, cap=64):
+        """gguf_open on a file: its summary, tensor table and kv_num(key, -1) answers, or None if the
+        reference refuses the file."""
+        v, a, nk, nt = (np.zeros(1, t) for t in (np.uint32, np.uint64, np.int64, np.int64))
+        names = np.zeros((cap, 128), np.uint8)
+        types, nd = np.zeros(cap, np.uint32), np.zeros(cap, np.int32)
+        ne, off, nb = np.zeros((cap, 4), np.uint64), np.zeros(cap, np.uint64), np.zeros(cap, np.uint64)
+        kv = np.zeros(len(keys), np.float64)
+        kb = b"".join(k.encode() + b"\0" for k in keys)
+        rc = self.lib.fgr_gguf_table(os.fsencode(path), *(_ptr(x) for x in (v, a, nk, nt, names, types, nd, ne, off, nb)),
+                                     cap, kb, len(keys), _ptr(kv))
+        if rc != 0:
+            return None
+        n = int(nt[0])
+        return {"version": v, "alignment": a, "n_kvs": nk, "n_tensors": nt, "names": names[:n], "types": types[:n],
+                "n_dims": nd[:n], "ne": ne[:n], "offsets": off[:n], "nbytes": nb[:n], "kv_keys": np.array(keys),
+                "kv_vals": kv}
 
     def moe_ffn(self, types, gate, up, down, n_expert, k, n_embd, ff, logits, X):
         X = np.ascontiguousarray(X, np.float32)

@@ -173,3 +173,33 @@ FGR_EXPORT int fgr_tensor_matvec_multi(int n, void *const *hs, const float *x, f
     for (int i = 0; i < n; i++) tp[i] = &((fgr_tensor *)hs[i])->t;
     return n == 1 ? matvec(tp[0], x, y[0]) : matvec_multi(n, tp, x, y);
 }
+
+/* gguf_open (342-440) on a file: 0 and its summary and tensor table (up to cap tensors: names
+ * [cap][128], dims [cap][4], offsets from the start of the file), kv_num (441-448) of n_keys
+ * NUL-separated keys with default -1; or gguf_open's -1 */
+FGR_EXPORT int fgr_gguf_table(const char *path, uint32_t *version, uint64_t *alignment, int64_t *n_kvs,
+                              int64_t *n_tensors, char *names, uint32_t *types, int32_t *n_dims, uint64_t *ne,
+                              uint64_t *offsets, uint64_t *nbytes, int64_t cap, const char *keys, int n_keys,
+                              double *kv_vals) {
+    gguf_t g;
+    if (gguf_open(&g, path) != 0) return -1;
+    *version = g.version;
+    *alignment = g.alignment;
+    *n_kvs = (int64_t)g.n_kvs;
+    *n_tensors = (int64_t)g.n_tensors;
+    for (size_t i = 0; i < g.n_tensors && (int64_t)i < cap; i++) {
+        tensor_t *t = &g.tensors[i];
+        memcpy(names + 128 * i, t->name, 128);
+        types[i] = t->type;
+        n_dims[i] = t->n_dims;
+        for (int j = 0; j < 4; j++) ne[4 * i + j] = t->ne[j];
+        offsets[i] = (uint64_t)(t->data - g.map.data);
+        nbytes[i] = t->nbytes;
+    }
+    for (int k = 0; k < n_keys; k++) {
+        kv_vals[k] = kv_num(&g, keys, -1.0);
+        keys += strlen(keys) + 1;
+    }
+    mmap_close(&g.map);
+    return 0;
+}

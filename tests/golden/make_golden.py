@@ -21,6 +21,9 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
+sys.path.insert(0, os.path.dirname(HERE))
+
+import gguf_write as GW  # noqa: E402
 from fastgguf_amd import synth as S  # noqa: E402
 from oracle import Reference  # noqa: E402
 
@@ -117,8 +120,25 @@ def main() -> None:
     Y, sel, w = ref.moe_ffn(types, g, u, d, E, K, D, F, L, X)
     np.savez_compressed(os.path.join(HERE, "moe_q5.npz"), gate=g, up=u, down=d, X=X, logits=L, Y=Y, sel=sel, w=w,
                         dims=np.array([E, K, D, F, T]), types=np.array(types))
+    # GGUF ingestion: tiny.gguf (tests/gguf_write.py's tiny model) and the reference's gguf_open of
+    # it (summary, tensor table, kv_num answers), and its outcome on each broken variant
+    kvs, tensors = GW.tiny_model()
+    good = GW.gguf_bytes(kvs, tensors, alignment=64)
+    path = os.path.join(HERE, "tiny.gguf")
+    with open(path, "wb") as f:
+        f.write(good)
+    tab = ref.gguf_table(path, GW.KV_QUERIES)
+    rcs = {}
+    for name, data in GW.variants(good).items():
+        vp = os.path.join(HERE, f"_variant_{name}.gguf")
+        with open(vp, "wb") as f:
+            f.write(data)
+        rcs[name] = 0 if ref.gguf_table(vp, GW.KV_QUERIES) is not None else -1
+        os.remove(vp)
+    np.savez_compressed(os.path.join(HERE, "gguf.npz"), **tab, variant_names=np.array(list(rcs)),
+                        variant_rc=np.array(list(rcs.values()), np.int32))
     for f in sorted(os.listdir(HERE)):
-        if f.endswith(".npz"):
+        if f.endswith(".npz") or f.endswith(".gguf"):
             print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
 
 
