@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <string>
+#include <vector>
 
 #include "../../include/fastgguf_hip.h"
 #include "fgh_internal.h"
@@ -211,6 +212,8 @@ static int check_tensor(fgh_ctx *c, const fgh_tensor *t) {
 
 extern "C" {
 
+static int selfcheck(fgh_ctx *c);
+
 int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out) {
     if (!out) return FGH_ERR_ARG;
     *out = nullptr;
@@ -230,6 +233,10 @@ int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out) {
     c->num_cu = std::max(1, prop.multiProcessorCount);
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
+        return FGH_ERR_DEVICE;
+    }
+    if (selfcheck(c) != FGH_OK) {  // gpu_selfcheck gates use (fastgguf.c:2048-2052)
+        fgh_close(c);
         return FGH_ERR_DEVICE;
     }
     *out = c;
@@ -798,3 +805,79 @@ int fgh_fp16_to_f32(fgh_ctx *c, const uint16_t *h, int n, float *out) {
 }
 
 }  // extern "C"
+
+// ---- self-check at open (the role of gpu_selfcheck, fastgguf.c:1898-1965) ----
+// Every weight type goes through upload and matvec (Q4_K in both orders, and the prompt GEMM)
+// on cases whose results are exact integers in fp32 whatever the order of the sums: x = 127
+// everywhere (quantized to d = 1, q = 127 exactly), unit fp16 scales, and row r of a 16 x 512
+// tensor holding one code c = 1 + r % 15 in every element. Then y_r = 65024 (v - m): v the
+// element value (Q8_0, Q5_0, Q6_K: c; Q4_K: c; Q5_K: c + 16) and m the min term (1 for Q4_K and
+// Q5_K, whose mins are 1). Rows differ, so a row or tile mix-up shows as well as a dead kernel.
+static void selfcheck_block(uint32_t type, int c, uint8_t *p) {
+    const uint8_t nib2 = (uint8_t)(c | c << 4);
+    const uint16_t one = 0x3C00;  // fp16 1.0
+    switch (type) {
+    case FGH_T_Q8_0:
+        memcpy(p, &one, 2);
+        memset(p + 2, c, 32);
+        break;
+    case FGH_T_Q5_0:  // nibble c with the fifth bit set: q5 - 16 = c
+        memcpy(p, &one, 2);
+        memset(p + 2, 0xFF, 4);
+        memset(p + 6, nib2, 16);
+        break;
+    case FGH_T_Q6_K:  // q = c + 32 (low nibble c, high bits 2): q - 32 = c
+        memset(p, nib2, 128);
+        memset(p + 128, 0xAA, 64);
+        memset(p + 192, 1, 16);
+        memcpy(p + 208, &one, 2);
+        break;
+    default: {  // Q4_K / Q5_K: d = dmin = 1, the 8 scales and 8 mins all 1
+        memcpy(p, &one, 2);
+        memcpy(p + 2, &one, 2);
+        memset(p + 4, 1, 8);
+        memset(p + 12, 0x11, 4);
+        if (type == FGH_T_Q5_K) {
+            memset(p + 16, 0xFF, 32);
+            memset(p + 48, nib2, 128);
+        } else {
+            memset(p + 16, nib2, 128);
+        }
+    }
+    }
+}
+
+static int selfcheck(fgh_ctx *c) {
+    const int cols = 512, rows = 16, ntok = 8;
+    const struct { uint32_t type; int order, be, bb, v16, m; } cases[] = {
+        {FGH_T_Q8_0, FGH_ORDER_ROW, 32, 34, 0, 0},        {FGH_T_Q5_0, FGH_ORDER_ROW, 32, 22, 0, 0},
+        {FGH_T_Q4_K, FGH_ORDER_ROW, 256, 144, 0, 1},      {FGH_T_Q4_K, FGH_ORDER_REPACKED, 256, 144, 0, 1},
+        {FGH_T_Q5_K, FGH_ORDER_ROW, 256, 176, 16, 1},     {FGH_T_Q6_K, FGH_ORDER_ROW, 256, 210, 0, 0},
+    };
+    std::vector<float> x((size_t)ntok * cols, 127.0f), y((size_t)ntok * rows);
+    int rc = FGH_OK;
+    for (const auto &k : cases) {
+        const int nb = cols / k.be;
+        std::vector<uint8_t> w((size_t)rows * nb * k.bb);
+        for (int r = 0; r < rows; r++)
+            for (int b = 0; b < nb; b++) selfcheck_block(k.type, 1 + r % 15, w.data() + ((size_t)r * nb + b) * k.bb);
+        fgh_tensor *t = nullptr;
+        if ((rc = fgh_upload(c, k.type, cols, rows, 1, k.order, w.data(), w.size(), &t)) != FGH_OK) break;
+        // one token through matvec; for Q4_K also 8 tokens through matmul (the prompt GEMM)
+        const int nt = k.type == FGH_T_Q4_K ? ntok : 1;
+        rc = nt == 1 ? fgh_matvec(c, t, x.data(), y.data()) : fgh_matmul(c, t, x.data(), cols, y.data(), rows, nt);
+        fgh_tensor_free(t);
+        if (rc != FGH_OK) break;
+        for (int i = 0; i < nt * rows && rc == FGH_OK; i++) {
+            const float want = 65024.0f * (float)(1 + (i % rows) % 15 + k.v16 - k.m);
+            if (y[(size_t)i] != want) {
+                fprintf(stderr, "[fastgguf_hip] self-check type %u order %d row %d: %g, want %g\n", k.type, k.order,
+                        i % rows, (double)y[(size_t)i], (double)want);
+                rc = FGH_ERR_DEVICE;
+            }
+        }
+        if (rc != FGH_OK) break;
+    }
+    c->n_offloaded = c->n_skip_type = c->n_skip_mem = 0;
+    return rc;
+}

@@ -26,6 +26,16 @@ def check_vec(y, ref):
     assert bits_equal(y, ref), f"not bit-exact: rel {rel_err(y, ref):.3e}"
 
 
+def test_open_self_check_leaves_no_trace():
+    """fgh_open runs the closed-form self-check of every type (the role of gpu_selfcheck,
+    fastgguf.c:1898-1965) and hands over a context with nothing allocated or counted."""
+    from fastgguf_amd.backend import Backend
+    b = Backend(0)
+    i = b.info()
+    assert (i["used"], i["n_offloaded"], i["n_skip_type"], i["n_skip_mem"]) == (0, 0, 0, 0)
+    b.close()
+
+
 def test_fp16_decode_exhaustive(backend, oracle):
     """fp16 -> fp32 of all 65536 codes (the reference selftest's table check, fastgguf.c:6022-6031)."""
     h = np.arange(65536, dtype=np.uint16)
