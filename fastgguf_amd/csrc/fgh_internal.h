@@ -276,6 +276,13 @@ struct GemmArgs {
 hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, int8_t *qs, float *ydT, int8_t *bsp,
                              hipStream_t s);
 constexpr size_t GEMM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
+// true when all wg workgroups of a launch (waves wavefronts and lds bytes each) can be resident
+// on num_cu CUs at once: a split launch whose workgroups need a second round is slower than a
+// smaller split (measured: Q8_0 4096 x 14336 with 4-way splits in two rounds 26 us, 2-way 18 us)
+inline bool all_resident(int64_t wg, int waves, size_t lds, int num_cu) {
+    const int64_t by_lds = lds ? (int64_t)(GEMM_LDS_MAX / lds) : 64, by_waves = 32 / waves;
+    return wg <= (int64_t)num_cu * (by_lds < by_waves ? by_lds : by_waves);
+}
 size_t q4k_gemm_lds_bytes(int nb, int Tp);  // <= GEMM_LDS_MAX for the GEMM to run
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s);
 

@@ -466,11 +466,11 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 
 // Launch shape: launches of fewer than 768 tiles (tiles x tokens) split the steps of a tile over up
 // to 8 wavefronts, as many as keep the launch within 2048 wavefronts, each wavefront at 4 steps or
-// more (Q6_K: 2) and the records within the 160 KiB of LDS of a workgroup; tiles per workgroup 4, 2
-// or 1 for S = 1, 2 or more. Ring depth:
+// more (Q6_K: 2), the records within the 160 KiB of LDS of a workgroup and every workgroup of the
+// launch resident at once; tiles per workgroup 4, 2 or 1 for S = 1, 2 or more. Ring depth:
 // 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps, 4 otherwise.
 template <int TYPE>
-static hipError_t mv_launch_type(const MvArgs &a, int ntok, hipStream_t s) {
+static hipError_t mv_launch_type(const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
     if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
     const int nb = a.nb, nst = mv_steps(TYPE, nb);
     constexpr int SPW = TYPE == T_Q6_K ? 2 : 1;  // Q6_K steps are 4x the bytes of Q8_0's per row
@@ -478,7 +478,9 @@ static hipError_t mv_launch_type(const MvArgs &a, int ntok, hipStream_t s) {
     int S = 1;
     if (tiles < 768)
         while (S < 8 && tiles * 2 * S <= 2048 && nst >= 8 * S / SPW &&
-               mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX)
+               mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX &&
+               all_resident((tiles + mv_tpw(2 * S) - 1) / mv_tpw(2 * S), 2 * S * mv_tpw(2 * S),
+                            mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S), num_cu))
             S *= 2;
     const int R = nst < 32 && tiles * S >= 1024 ? 2 : 4;
     const size_t lds = mv_lds(TYPE, nb, mv_tpw(S), S);
@@ -493,9 +495,9 @@ static hipError_t mv_launch_type(const MvArgs &a, int ntok, hipStream_t s) {
 
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
     if (type == T_Q4_K || type == T_Q5_K) return launch_q4k_matvec(type, order, a, ntok, num_cu, s);
-    if (type == T_Q6_K) return mv_launch_type<T_Q6_K>(a, ntok, s);
-    if (type == T_Q8_0) return mv_launch_type<T_Q8_0>(a, ntok, s);
-    if (type == T_Q5_0) return mv_launch_type<T_Q5_0>(a, ntok, s);
+    if (type == T_Q6_K) return mv_launch_type<T_Q6_K>(a, ntok, num_cu, s);
+    if (type == T_Q8_0) return mv_launch_type<T_Q8_0>(a, ntok, num_cu, s);
+    if (type == T_Q5_0) return mv_launch_type<T_Q5_0>(a, ntok, num_cu, s);
     return hipErrorInvalidValue;
 }
 

@@ -488,8 +488,9 @@ size_t q4k_lds_bytes(int order, int nb) { return q4_lds(order, nb, 4, 1); }
 
 // Launch shape (measured on MI355X at the decode-layer shapes). Wavefronts per tile S: launches of
 // fewer than 768 tiles (tiles x tokens) split the blocks of a tile over up to 8 wavefronts, as many
-// as keep the launch within 2048 wavefronts, each wavefront at 4 blocks or more and the LDS within
-// the 160 KiB of a workgroup; larger launches keep one wavefront per tile. Tiles per workgroup: 4,
+// as keep the launch within 2048 wavefronts, each wavefront at 4 blocks or more, the LDS within
+// the 160 KiB of a workgroup and every workgroup resident at once; larger launches keep one
+// wavefront per tile. Tiles per workgroup: 4,
 // 2 or 1 for S = 1, 2 or more. Ring depth R: 2 steps when the launch has 1024
 // wavefronts or more over rows shorter than 32 blocks (enough loads in flight across the chip), 4
 // otherwise.
@@ -502,7 +503,7 @@ static hipError_t q4_launch_s(int S, int R, const MvArgs &a, int ntok, size_t ld
     default: return q4_launch_r<ORDER, 1, 8, TYPE>(R, a, ntok, lds, s);
     }
 }
-hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int, hipStream_t s) {
+hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
     const int nb = a.nb;
     if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
     if (type == T_Q5_K) order = 0;  // no repacked order for Q5_K
@@ -510,7 +511,9 @@ hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int
     int S = 1;
     if (tiles < 768)
         while (S < 8 && tiles * 2 * S <= 2048 && nb >= 8 * S &&
-               q4_lds(order, nb, q4_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX)
+               q4_lds(order, nb, q4_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX &&
+               all_resident((tiles + q4_tpw(2 * S) - 1) / q4_tpw(2 * S), 2 * S * q4_tpw(2 * S),
+                            q4_lds(order, nb, q4_tpw(2 * S), 2 * S), num_cu))
             S *= 2;
     const int R = nb < 32 && tiles * S >= 1024 ? 2 : 4;
     const size_t lds = q4_lds(order, nb, q4_tpw(S), S);
