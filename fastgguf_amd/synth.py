@@ -10,10 +10,16 @@ Byte layouts follow fastgguf.c (lawnak/FastGGUF):
                             (fastgguf.c:518-532, element order q5_elem 939-942)
   Q5_K 176 B / 256 weights  fp16 d @0, fp16 dmin @2, 12 B scales @4, qh[32] @16, ql[128] @48
                             (fastgguf.c:644-667)
+  Q4_0  18 B / 32 weights   fp16 d @0, nibbles qs[16] @2; value d (q - 8)    (fastgguf.c:485-497)
+  Q4_1  20 B / 32 weights   fp16 d @0, fp16 m @2, nibbles @4; value d q + m  (fastgguf.c:499-516)
+  Q5_1  24 B / 32 weights   fp16 d @0, fp16 m @2, u32 qh @4, nibbles @8      (fastgguf.c:534-550)
+  IQ4_NL 18 B / 32 weights  fp16 d @0, nibbles @2; value d kvalues[q]        (fastgguf.c:694-706)
+  (32-value types: element j is nibble j of qs, low nibbles of qs[0..15] first, then the high ones)
 Value distributions are the benchmark's: Q4_K nibbles uniform, 6-bit scales and mins uniform in
 [0, 63], d and dmin = fp16(|N(0,1)| * 0.005); Q6_K quant bytes uniform, int8 scales uniform in
 [-64, 63], d = fp16(|N(0,1)| * 0.002); Q8_0 quants uniform in [-127, 127], d = fp16(|N(0,1)| * 0.01);
-Q5_0 and Q5_K quant bytes uniform, d = fp16(|N(0,1)| * 0.01) (Q5_0) or as Q4_K (Q5_K).
+Q5_0 and Q5_K quant bytes uniform, d = fp16(|N(0,1)| * 0.01) (Q5_0) or as Q4_K (Q5_K); the other
+32-value types quant bytes uniform, d = fp16(|N(0,1)| * 0.01), m = fp16(N(0,1) * 0.05).
 fp16 conversion rounds to nearest even (numpy astype).
 """
 from __future__ import annotations
@@ -21,21 +27,28 @@ from __future__ import annotations
 import numpy as np
 
 T_F32 = 0
+T_Q4_0 = 2
+T_Q4_1 = 3
 T_Q5_0 = 6
+T_Q5_1 = 7
 T_Q8_0 = 8
 T_Q4_K = 12
 T_Q5_K = 13
 T_Q6_K = 14
+T_IQ4_NL = 20
 
 #: (elements per block, bytes per block), block_size_of (fastgguf.c:235-253)
-BLOCK = {T_Q8_0: (32, 34), T_Q4_K: (256, 144), T_Q6_K: (256, 210), T_Q5_0: (32, 22), T_Q5_K: (256, 176)}
-TYPE_NAME = {T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q6_K: "Q6_K", T_Q5_0: "Q5_0", T_Q5_K: "Q5_K"}
+BLOCK = {T_Q8_0: (32, 34), T_Q4_K: (256, 144), T_Q6_K: (256, 210), T_Q5_0: (32, 22), T_Q5_K: (256, 176),
+         T_Q4_0: (32, 18), T_Q4_1: (32, 20), T_Q5_1: (32, 24), T_IQ4_NL: (32, 18)}
+TYPE_NAME = {T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q6_K: "Q6_K", T_Q5_0: "Q5_0", T_Q5_K: "Q5_K", T_Q4_0: "Q4_0",
+             T_Q4_1: "Q4_1", T_Q5_1: "Q5_1", T_IQ4_NL: "IQ4_NL"}
+Q32_TYPES = (T_Q8_0, T_Q5_0, T_Q4_0, T_Q4_1, T_Q5_1, T_IQ4_NL)
 
 
 def uses_q8(type_: int) -> bool:
-    """Activation kind (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for Q8_0 / Q5_0, Q8_K
-    blocks of 256 for the K-quants."""
-    return type_ in (T_Q8_0, T_Q5_0)
+    """Activation kind (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for the 32-value
+    types, Q8_K blocks of 256 for the K-quants."""
+    return type_ in Q32_TYPES
 
 #: activation blocks, the reference's structs q8_blk_t (743) and q8k_blk_t (771)
 Q8_BLK = np.dtype([("d", "<f4"), ("qs", "i1", 32), ("s16", "<i2", 2)])
@@ -135,7 +148,23 @@ def q5_k_weights(rows: int, cols: int, seed: int) -> np.ndarray:
     return blk.reshape(rows, -1)
 
 
+def q32_weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """rows x cols of Q4_0 / Q4_1 / Q5_1 / IQ4_NL: fp16 d (and m), uniform quant bytes."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    if cols % 32:
+        raise ValueError(f"{TYPE_NAME[type_]} needs cols % 32 == 0")
+    nb = rows * (cols // 32)
+    bb = BLOCK[type_][1]
+    blk = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    blk[:, 0:2] = _fp16_abs_normal(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)
+    if type_ in (T_Q4_1, T_Q5_1):
+        blk[:, 2:4] = (rng.standard_normal(nb) * 0.05).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return blk.reshape(rows, -1)
+
+
 def weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    if type_ in (T_Q4_0, T_Q4_1, T_Q5_1, T_IQ4_NL):
+        return q32_weights(type_, rows, cols, seed)
     if type_ == T_Q5_0:
         return q5_0_weights(rows, cols, seed)
     if type_ == T_Q5_K:
@@ -162,7 +191,7 @@ def random_bytes_weights(type_: int, rows: int, cols: int, seed: int) -> np.ndar
         blk[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
     else:
         blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
-        if type_ in (T_Q4_K, T_Q5_K):
+        if type_ in (T_Q4_K, T_Q5_K, T_Q4_1, T_Q5_1):
             blk[:, 2:4] = dm.view(np.uint8).reshape(nb, 2)
     return blk.reshape(rows, -1)
 

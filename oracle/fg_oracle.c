@@ -50,7 +50,12 @@ static inline uint32_t rd32(const uint8_t *p) { uint32_t v; memcpy(&v, p, 4); re
 
 /* the activation kind of a weight type (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for
  * Q8_0 / Q5_0, Q8_K blocks of 256 for the K-quants */
-static inline int uses_q8(uint32_t type) { return type == FGO_T_Q8_0 || type == FGO_T_Q5_0; }
+static inline int uses_q8(uint32_t type) {
+    return type == FGO_T_Q8_0 || type == FGO_T_Q5_0 || type == FGO_T_Q4_0 || type == FGO_T_Q4_1 ||
+           type == FGO_T_Q5_1 || type == FGO_T_IQ4_NL;
+}
+/* the 32-value block types with a min term (d * q + m): Q4_1 / Q5_1 */
+static inline int has_min32(uint32_t type) { return type == FGO_T_Q4_1 || type == FGO_T_Q5_1; }
 
 /* FGO_MUTATE (tests only, tests/test_oracle.py) builds a copy of this oracle with one planted
  * mistake, to show that the golden vectors catch it. 0 = the real oracle. */
@@ -155,6 +160,36 @@ static inline int q5_0_val(const uint8_t *p, int j) {
 #endif
 }
 
+/* the non-linear values of IQ4_NL (kvalues_iq4nl, fastgguf.c:475-477) */
+static const int8_t IQ4NL[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* nibble j of a 16-byte nibble array in the element order of the 32-value types (nibbles32,
+ * fastgguf.c:809-814): low nibbles of qs[0..15], then their high nibbles */
+static inline int nib32(const uint8_t *qs, int j) { return j < 16 ? (qs[j] & 0x0F) : (qs[j - 16] >> 4); }
+
+/* element j of a 32-value block as the int8 value the reference's row kernel multiplies (bx):
+ * Q4_0 nib - 8 (833-857), Q4_1 nib (1020-1031), Q5_0 q5 - 16 (944-959), Q5_1 q5 (973-989),
+ * IQ4_NL kvalues[nib] (1547-1562), Q8_0 q (891-902); the block's bytes per type in bb */
+static inline int val32(uint32_t type, const uint8_t *p, int j) {
+    switch (type) {
+    case FGO_T_Q4_0: return nib32(p + 2, j) - 8;
+    case FGO_T_Q4_1: return nib32(p + 4, j);
+    case FGO_T_Q5_0: return q5_0_val(p, j) - 16;
+    case FGO_T_Q5_1: return nib32(p + 8, j) | (int)(((rd32(p + 4) >> j) & 1u) << 4);
+    case FGO_T_IQ4_NL: return IQ4NL[nib32(p + 2, j)];
+    default: return (int)(int8_t)p[2 + j];
+    }
+}
+static inline int bytes32(uint32_t type) {
+    switch (type) {
+    case FGO_T_Q4_0: case FGO_T_IQ4_NL: return 18;
+    case FGO_T_Q4_1: return 20;
+    case FGO_T_Q5_0: return 22;
+    case FGO_T_Q5_1: return 24;
+    default: return 34;
+    }
+}
+
 /* Q5_K element e (0..255) of a block (fastgguf.c:1195-1210, scalar form 1216-1221): chunk j = e / 64
  * of ql (bytes 48 + 32 j ..), low nibbles for e % 64 < 32, high nibbles above; bit 2 j (low) or
  * 2 j + 1 (high) of qh[e % 32] as bit 4 */
@@ -201,6 +236,53 @@ float fgo_dot_q5_0(const uint8_t *row, const fgo_q8_blk *xq, int nb) {
         }
     }
     return hsum8(acc);
+}
+
+/* ---- B-8: the other 32-value row kernels, lanes as B-1 over val32:
+ *   dot_q4_0_q8 (833-857; its two-row form dot_q4_0_q8_x2 864-889 computes the same per row),
+ *   dot_iq4_nl_q8 (1547-1562): acc_i = fma(FP16(d) * xd, s_i, acc_i), out = hsum8(acc);
+ *   dot_q4_1_q8 (1020-1031), dot_q5_1_q8 (973-989): the same lanes over the unsigned values plus
+ *   one scalar min chain, macc = fma(FP16(m) * xd, s16_0 + s16_1, macc) (the statement
+ *   `macc += FP16(m) * xd * (float)(...)`, which gcc contracts to a fused multiply-add at -O3:
+ *   the golden vectors of the compiled reference fix it), out = hsum8(acc) + macc */
+float fgo_dot_q32(uint32_t type, const uint8_t *row, const fgo_q8_blk *xq, int nb) {
+    if (type == FGO_T_Q8_0) return fgo_dot_q8_0(row, xq, nb);
+    if (type == FGO_T_Q5_0) return fgo_dot_q5_0(row, xq, nb);
+    const int bb = bytes32(type), mn = has_min32(type);
+    float acc[8] = {0}, macc = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *p = row + (size_t)b * bb;
+        float d = fgo_fp16(rd16(p)) * xq[b].d;
+        for (int i = 0; i < 8; i++) {
+            int s = 0;
+            for (int t = 4 * i; t < 4 * i + 4; t++) s += val32(type, p, t) * xq[b].qs[t];
+            acc[i] = fmaf(d, (float)s, acc[i]);
+        }
+        if (mn) {
+#if FGO_MUTATE == 9 /* the min term added without the fused multiply-add */
+            volatile float pm = fgo_fp16(rd16(p + 2)) * xq[b].d * (float)(xq[b].s16[0] + xq[b].s16[1]);
+            macc = macc + pm;
+#else
+            macc = fmaf(fgo_fp16(rd16(p + 2)) * xq[b].d, (float)(xq[b].s16[0] + xq[b].s16[1]), macc);
+#endif
+        }
+    }
+    return hsum8(acc) + macc;
+}
+
+/* ---- B-9: dot_q40x8 (fastgguf.c:2424-2467), the 8-row repacked Q4_0 kernel, one row of it ----
+ * per block the whole-block integer isum = sum (nib - 8) y (computed as sum nib y - 8 (s16_0 +
+ * s16_1), the same integer); acc = fma(FP16(d) * yd, isum, acc); out = acc. The repack
+ * (repack_q40_group 2390-2398) moves bytes only. */
+float fgo_dot_q4_0_rp(const uint8_t *row, const fgo_q8_blk *xq, int nb) {
+    float acc = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *p = row + (size_t)b * 18;
+        int isum = 0;
+        for (int t = 0; t < 32; t++) isum += (nib32(p + 2, t) - 8) * xq[b].qs[t];
+        acc = fmaf(fgo_fp16(rd16(p)) * xq[b].d, (float)isum, acc);
+    }
+    return acc;
 }
 
 /* ---- B-2: dot_q4_K_q8k (fastgguf.c:1118-1153) ----
@@ -381,11 +463,11 @@ void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
             }
             sumi[b] = s;
             msum[b] = m;
-        } else if (type == FGO_T_Q5_0) {
-            const uint8_t *p = row + (size_t)b * 22;
+        } else if (uses_q8(type) && type != FGO_T_Q8_0) {
+            const uint8_t *p = row + (size_t)b * bytes32(type);
             const fgo_q8_blk *xb = (const fgo_q8_blk *)act + b;
             int s = 0;
-            for (int t = 0; t < 32; t++) s += (q5_0_val(p, t) - 16) * xb->qs[t];
+            for (int t = 0; t < 32; t++) s += val32(type, p, t) * xb->qs[t];
             sumi[b] = s;
             msum[b] = 0;
         } else { /* Q8_0 */
@@ -401,11 +483,12 @@ void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
 
 /* ---- dequantize_row (fastgguf.c:518-532, 552-562, 622-667, 669-693) ---- */
 int fgo_dequantize_row(uint32_t type, const uint8_t *raw, float *out, int n) {
-    if (type == FGO_T_Q5_0) {
+    if (uses_q8(type) && type != FGO_T_Q8_0) { /* d * value (+ m for Q4_1 / Q5_1) */
+        const int bb = bytes32(type);
         for (int b = 0; b < n / 32; b++) {
-            const uint8_t *p = raw + (size_t)b * 22;
-            float d = fgo_fp16(rd16(p));
-            for (int j = 0; j < 32; j++) out[32 * b + j] = d * (float)(q5_0_val(p, j) - 16);
+            const uint8_t *p = raw + (size_t)b * bb;
+            float d = fgo_fp16(rd16(p)), m = has_min32(type) ? fgo_fp16(rd16(p + 2)) : 0.0f;
+            for (int j = 0; j < 32; j++) out[32 * b + j] = d * (float)val32(type, p, j) + m;
         }
         return 0;
     }
@@ -464,26 +547,27 @@ int fgo_block_size(uint32_t type, int *elems, int *bytes) {
     case FGO_T_Q8_0: *elems = 32; *bytes = 34; return 0;
     case FGO_T_Q4_K: *elems = 256; *bytes = 144; return 0;
     case FGO_T_Q6_K: *elems = 256; *bytes = 210; return 0;
-    case FGO_T_Q5_0: *elems = 32; *bytes = 22; return 0;
+    case FGO_T_Q5_0: case FGO_T_Q4_0: case FGO_T_Q4_1: case FGO_T_Q5_1: case FGO_T_IQ4_NL:
+        *elems = 32; *bytes = bytes32(type); return 0;
     case FGO_T_Q5_K: *elems = 256; *bytes = 176; return 0;
     default: return -1;
     }
 }
 
-/* ---- dot_row dispatch for the five types (fastgguf.c:2183-2201) ---- */
+/* ---- dot_row dispatch (fastgguf.c:2183-2201), and the repacked kernels of matvec_rp ---- */
 static float dot_row3(uint32_t type, int order, const uint8_t *rb, const void *act, int cols) {
     if (type == FGO_T_Q4_K)
         return order == FGO_ORDER_REPACKED ? fgo_dot_q4_K_rp(rb, (const fgo_q8k_blk *)act, cols / 256)
                                            : fgo_dot_q4_K(rb, (const fgo_q8k_blk *)act, cols / 256);
     if (type == FGO_T_Q6_K) return fgo_dot_q6_K(rb, (const fgo_q8k_blk *)act, cols / 256);
     if (type == FGO_T_Q5_K) return fgo_dot_q5_K(rb, (const fgo_q8k_blk *)act, cols / 256);
-    if (type == FGO_T_Q5_0) return fgo_dot_q5_0(rb, (const fgo_q8_blk *)act, cols / 32);
-    return fgo_dot_q8_0(rb, (const fgo_q8_blk *)act, cols / 32);
+    if (type == FGO_T_Q4_0 && order == FGO_ORDER_REPACKED) return fgo_dot_q4_0_rp(rb, (const fgo_q8_blk *)act, cols / 32);
+    return fgo_dot_q32(type, rb, (const fgo_q8_blk *)act, cols / 32);
 }
 
 static int type_ok(uint32_t type, int cols) {
     if (type == FGO_T_Q4_K || type == FGO_T_Q5_K || type == FGO_T_Q6_K) return cols > 0 && cols % 256 == 0;
-    if (type == FGO_T_Q8_0 || type == FGO_T_Q5_0) return cols > 0 && cols % 32 == 0;
+    if (uses_q8(type)) return cols > 0 && cols % 32 == 0;
     return 0;
 }
 
@@ -525,25 +609,33 @@ int fgo_matvec(uint32_t type, int order, const uint8_t *w, int64_t rows, int col
  *   for g: a = fma(wsc_g, ia_g, a)          wsc_g = FP16(d)*sc_g  (Q6_K: FP16(d)*sc_g)
  *   for g: a = fnmadd(wmn_g, bs_g, a)       wmn_g = FP16(dmin)*m_g (Q6_K: 32*FP16(d)*sc_g)
  *   f = fma(a, yd_b, f)
- * ---- and gemm32_kern (2909-2937) for Q8_0 / Q5_0 (unpack_row_q32 2876-2894, gemm_pack_q8 2897-2913):
+ * ---- and gemm32_kern (2909-2937) for the 32-value types (unpack_row_q32 2876-2894, gemm_pack_q8
+ * 2897-2913; Q4_0 repacked: unpack_row_q40x8 2400-2421, the same values):
  *   per 32-block g: a = fma(d*xd, ia'_g, a); a = fnmadd(m, xd*(s16_0+s16_1), a)
  *   with ia' = sum u*x over the unsigned weights the VNNI kernel multiplies: Q8_0 u = w + 128,
- *   m = 128 d; Q5_0 u = q5 (0..31), m = 16 d */
+ *   m = 128 d; Q5_0 u = q5, m = 16 d; Q4_0 u = nib, m = 8 d; Q4_1 / Q5_1 u = nib / q5, m = -FP16(m) */
+static int has_gemm(uint32_t type) { return type != FGO_T_Q5_K && type != FGO_T_IQ4_NL; }
 static void gemm_row_token(uint32_t type, const uint8_t *rb, const void *act, int cols, float *out) {
     if (uses_q8(type)) {
         const fgo_q8_blk *xq = (const fgo_q8_blk *)act;
-        const int q5 = type == FGO_T_Q5_0, bb = q5 ? 22 : 34;
+        const int bb = bytes32(type);
         float acc = 0.0f;
         for (int g = 0; g < cols / 32; g++) {
             const uint8_t *p = rb + (size_t)g * bb;
-            float d = fgo_fp16(rd16(p));
+            float d = fgo_fp16(rd16(p)), m;
+            int off;  /* u = value + off */
+            switch (type) {
+            case FGO_T_Q8_0: m = 128.0f * d; off = 128; break;
+            case FGO_T_Q5_0: m = 16.0f * d; off = 16; break;
+            case FGO_T_Q4_0: m = 8.0f * d; off = 8; break;
+            default: m = -fgo_fp16(rd16(p + 2)); off = 0; break; /* Q4_1, Q5_1 */
+            }
             int ia = 0;
-            for (int t = 0; t < 32; t++)
-                ia += (q5 ? q5_0_val(p, t) : (int)(int8_t)p[2 + t] + 128) * xq[g].qs[t];
+            for (int t = 0; t < 32; t++) ia += (val32(type, p, t) + off) * xq[g].qs[t];
             float ws = d * xq[g].d;
             float ys = xq[g].d * (float)(xq[g].s16[0] + xq[g].s16[1]);
             acc = fmaf(ws, (float)ia, acc);
-            acc = fmaf(-((q5 ? 16.0f : 128.0f) * d), ys, acc);
+            acc = fmaf(-m, ys, acc);
         }
         *out = acc;
         return;
@@ -610,7 +702,7 @@ int fgo_gemm(uint32_t type, const uint8_t *w, int64_t rows, int cols, const void
     int eb, bb;
     fgo_block_size(type, &eb, &bb);
     size_t stride = (size_t)(cols / eb) * bb;
-    if (type == FGO_T_Q5_K) return -1; /* no prompt GEMM: matmul runs the row kernel per token */
+    if (!has_gemm(type)) return -1; /* no prompt GEMM: matmul runs the row kernel per token */
     size_t ablk = uses_q8(type) ? sizeof(fgo_q8_blk) : sizeof(fgo_q8k_blk);
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; r++)
@@ -621,17 +713,16 @@ int fgo_gemm(uint32_t type, const uint8_t *w, int64_t rows, int cols, const void
     return 0;
 }
 
-/* matmul (fastgguf.c:3004-3093) restricted to Q4_K / Q5_K / Q6_K / Q5_0 / Q8_0, as built for a VNNI
- * CPU:
- *   nb == 1: matvec;  repacked and nb < 8: per-token matvec;  nb >= 8: the prompt GEMM
- *   (gemm_kquant for Q4_K / Q6_K, gemm_q32 for Q5_0 and, VNNI builds only, Q8_0 - GEMM_Q8_0 at
- *   2864-2868; Q5_K has no GEMM and no x4 tile: the row kernel per token);
+/* matmul (fastgguf.c:3004-3093) for the types here, as built for a VNNI CPU:
+ *   nb == 1: matvec;  repacked (Q4_K, Q4_0) and nb < 8: per-token matvec;  nb >= 8: the prompt
+ *   GEMM (gemm_kquant for Q4_K / Q6_K, gemm_q32 for Q4_0 / Q4_1 / Q5_0 / Q5_1 and, VNNI builds
+ *   only, Q8_0 - GEMM_Q8_0 at 2864-2868; Q5_K and IQ4_NL have no GEMM: the row kernel per token);
  *   otherwise the x4 tiles, which equal the single-row kernels bit for bit (selftest 5871-5916). */
 int fgo_matmul(uint32_t type, int order, const uint8_t *w, int64_t rows, int cols,
                const float *X, int ldx, float *Y, int ldy, int nb) {
     if (!type_ok(type, cols) || nb < 1) return -1;
     if (nb == 1) return fgo_matvec(type, order, w, rows, cols, X, Y);
-    int repacked = type == FGO_T_Q4_K && order == FGO_ORDER_REPACKED;
+    int repacked = (type == FGO_T_Q4_K || type == FGO_T_Q4_0) && order == FGO_ORDER_REPACKED;
     if (repacked && nb < 8) {
         for (int t = 0; t < nb; t++)
             if (fgo_matvec(type, order, w, rows, cols, X + (size_t)t * ldx, Y + (size_t)t * ldy) != 0)
@@ -648,7 +739,7 @@ int fgo_matmul(uint32_t type, int order, const uint8_t *w, int64_t rows, int col
     int eb, bb;
     fgo_block_size(type, &eb, &bb);
     int sblocks = cols / eb;
-    if (nb >= 8 && type != FGO_T_Q5_K) {
+    if (nb >= 8 && has_gemm(type)) {
         int rc = fgo_gemm(type, w, rows, cols, act, sblocks, Y, ldy, nb);
         free(act);
         return rc;

@@ -21,12 +21,15 @@
 extern "C" {
 #endif
 
-enum { FGO_T_F32 = 0, FGO_T_Q5_0 = 6, FGO_T_Q8_0 = 8, FGO_T_Q4_K = 12, FGO_T_Q5_K = 13, FGO_T_Q6_K = 14 };
+enum {
+    FGO_T_F32 = 0, FGO_T_Q4_0 = 2, FGO_T_Q4_1 = 3, FGO_T_Q5_0 = 6, FGO_T_Q5_1 = 7, FGO_T_Q8_0 = 8,
+    FGO_T_Q4_K = 12, FGO_T_Q5_K = 13, FGO_T_Q6_K = 14, FGO_T_IQ4_NL = 20
+};
 
 /* fp32 evaluation order a kernel follows (which reference kernel the call restates) */
 enum {
     FGO_ORDER_ROW = 0,      /* dot_q4_K_q8k / dot_q6_K_q8k / dot_q8_0_q8 (file layout) */
-    FGO_ORDER_REPACKED = 1, /* dot_q4Kx8 (8-row repacked Q4_K, fastgguf.c:2322) */
+    FGO_ORDER_REPACKED = 1, /* dot_q4Kx8 / dot_q40x8 (8-row repacked Q4_K / Q4_0, fastgguf.c:2322, 2424) */
 };
 
 typedef struct { float d; int8_t qs[32]; int16_t s16[2]; } fgo_q8_blk;
@@ -42,11 +45,15 @@ float fgo_dot_q4_K_rp(const uint8_t *row, const fgo_q8k_blk *y, int nb);
 float fgo_dot_q6_K(const uint8_t *row, const fgo_q8k_blk *y, int nb);
 float fgo_dot_q5_0(const uint8_t *row, const fgo_q8_blk *xq, int nb);
 float fgo_dot_q5_K(const uint8_t *row, const fgo_q8k_blk *y, int nb);
+/* any 32-value type (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, IQ4_NL) in its row kernel's order */
+float fgo_dot_q32(uint32_t type, const uint8_t *row, const fgo_q8_blk *xq, int nb);
+float fgo_dot_q4_0_rp(const uint8_t *row, const fgo_q8_blk *xq, int nb);
 
 /* per-block integer parts (the bit-exact targets):
  *   Q4_K, Q5_K: sumi[b] = sum_s sc_s * sum_32 q*y,   msum[b] = sum_s m_s * (bs_2s + bs_2s+1)
  *   Q6_K:       sumi[b] = sum_g sc_g * sum_16 q*y,   msum[b] = sum_g sc_g * bs_g  (q in 0..63)
- *   Q8_0, Q5_0: sumi[b] = sum_32 w*x,                msum[b] = 0        (Q5_0: w = q5 - 16) */
+ *   32-value types: sumi[b] = sum_32 w*x, msum[b] = 0, with w the int8 value the row kernel
+ *   multiplies (Q5_0: q5 - 16, Q4_0: nib - 8, Q4_1: nib, Q5_1: q5, IQ4_NL: kvalues[nib]) */
 void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
                     int32_t *sumi, int32_t *msum);
 

@@ -46,9 +46,12 @@ class Oracle:
         for n in ("fgo_quantize_q8", "fgo_quantize_q8k"):
             getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
             getattr(L, n).restype = None
-        for n in ("fgo_dot_q8_0", "fgo_dot_q4_K", "fgo_dot_q4_K_rp", "fgo_dot_q6_K", "fgo_dot_q5_0", "fgo_dot_q5_K"):
+        for n in ("fgo_dot_q8_0", "fgo_dot_q4_K", "fgo_dot_q4_K_rp", "fgo_dot_q6_K", "fgo_dot_q5_0", "fgo_dot_q5_K",
+                  "fgo_dot_q4_0_rp"):
             getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
             getattr(L, n).restype = C.c_float
+        L.fgo_dot_q32.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
+        L.fgo_dot_q32.restype = C.c_float
         L.fgo_block_ints.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
         L.fgo_matvec.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
         L.fgo_matmul.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_int,
@@ -90,8 +93,12 @@ class Oracle:
         row = np.ascontiguousarray(row, np.uint8)
         eb, _ = BLOCK[type_]
         nb = act.size
-        name = {8: "fgo_dot_q8_0", 12: "fgo_dot_q4_K_rp" if order == ORDER_REPACKED else "fgo_dot_q4_K",
-                14: "fgo_dot_q6_K", 6: "fgo_dot_q5_0", 13: "fgo_dot_q5_K"}[type_]
+        if type_ == 2 and order == ORDER_REPACKED:
+            return self.lib.fgo_dot_q4_0_rp(_ptr(row), _ptr(act), nb)
+        if uses_q8(type_):
+            return self.lib.fgo_dot_q32(type_, _ptr(row), _ptr(act), nb)
+        name = {12: "fgo_dot_q4_K_rp" if order == ORDER_REPACKED else "fgo_dot_q4_K",
+                14: "fgo_dot_q6_K", 13: "fgo_dot_q5_K"}[type_]
         return getattr(self.lib, name)(_ptr(row), _ptr(act), nb)
 
     def block_ints(self, type_: int, row: np.ndarray, act: np.ndarray):
@@ -221,6 +228,8 @@ class Reference:
         for n in ("fgr_dot_q8_0", "fgr_dot_q4_K", "fgr_dot_q6_K", "fgr_dot_q5_0", "fgr_dot_q5_K"):
             getattr(L, n).argtypes = [C.c_void_p, C.c_void_p, C.c_int]
             getattr(L, n).restype = C.c_float
+        L.fgr_dot_q32.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
+        L.fgr_dot_q32.restype = C.c_float
         L.fgr_matvec.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
         L.fgr_matvec_multi.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
                                        C.c_void_p, C.c_void_p]
@@ -257,7 +266,9 @@ class Reference:
 
     def dot(self, type_, row, act):
         row = np.ascontiguousarray(row, np.uint8)
-        name = {8: "fgr_dot_q8_0", 12: "fgr_dot_q4_K", 14: "fgr_dot_q6_K", 6: "fgr_dot_q5_0", 13: "fgr_dot_q5_K"}[type_]
+        if uses_q8(type_):
+            return self.lib.fgr_dot_q32(type_, _ptr(row), _ptr(act), act.size)
+        name = {12: "fgr_dot_q4_K", 14: "fgr_dot_q6_K", 13: "fgr_dot_q5_K"}[type_]
         return getattr(self.lib, name)(_ptr(row), _ptr(act), act.size)
 
     def matvec(self, type_, w, cols, x, repack=False):

@@ -31,6 +31,11 @@ FGR_EXPORT float fgr_dot_q4_K(const uint8_t *row, const void *y, int nb) { retur
 FGR_EXPORT float fgr_dot_q6_K(const uint8_t *row, const void *y, int nb) { return dot_q6_K_q8k(row, (const q8k_blk_t *)y, nb); }
 FGR_EXPORT float fgr_dot_q5_0(const uint8_t *row, const void *xq, int nb) { return dot_q5_0_q8(row, (const q8_blk_t *)xq, nb); }
 FGR_EXPORT float fgr_dot_q5_K(const uint8_t *row, const void *y, int nb) { return dot_q5_K_q8k(row, (const q8k_blk_t *)y, nb); }
+/* dot_row (2183-2201) for a 32-value type on Q8 activations */
+FGR_EXPORT float fgr_dot_q32(uint32_t type, const uint8_t *row, const void *xq, int nb) {
+    int fail = 0;
+    return dot_row(type, ACT_Q8, row, (const q8_blk_t *)xq, NULL, NULL, 32 * nb, &fail);
+}
 
 /* a tensor view over caller memory; `repack` asks for the 8-row layout the reference builds at
  * load time (repack_tensor, 2486). repack_tensor drops the source pages with MADV_DONTNEED, so

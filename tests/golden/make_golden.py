@@ -64,7 +64,8 @@ def main() -> None:
     # single-token matvecs: per type, synthetic (benchmark distributions) and random-byte rows
     mv = {}
     cases = [("q8_0", S.T_Q8_0, 24, 512), ("q4_k", S.T_Q4_K, 24, 768), ("q6_k", S.T_Q6_K, 24, 512),
-             ("q5_0", S.T_Q5_0, 24, 544), ("q5_k", S.T_Q5_K, 24, 768)]
+             ("q5_0", S.T_Q5_0, 24, 544), ("q5_k", S.T_Q5_K, 24, 768), ("q4_0", S.T_Q4_0, 24, 544),
+             ("q4_1", S.T_Q4_1, 24, 544), ("q5_1", S.T_Q5_1, 24, 544), ("iq4_nl", S.T_IQ4_NL, 24, 544)]
     for name, t, rows, cols in cases:
         for gname, gen in (("synth", S.weights), ("bytes", S.random_bytes_weights)):
             w = gen(t, rows, cols, 200 + t)
@@ -73,21 +74,23 @@ def main() -> None:
             mv[f"{key}_w"] = w
             mv[f"{key}_x"] = xv
             mv[f"{key}_y"] = ref.matvec(t, w, cols, xv)
-            if t == S.T_Q4_K:
+            if t in (S.T_Q4_K, S.T_Q4_0):
                 mv[f"{key}_y_rp"] = ref.matvec(t, w, cols, xv, repack=True)
     np.savez_compressed(os.path.join(HERE, "matvec.npz"), **mv)
 
     # prompt batches through matmul: 3 tokens (x4 tiles / repacked per-token) and 8, 45 (GEMM)
     mm = {}
     for name, t, rows, cols in [("q8_0", S.T_Q8_0, 20, 512), ("q4_k", S.T_Q4_K, 24, 512), ("q6_k", S.T_Q6_K, 20, 512),
-                                ("q5_0", S.T_Q5_0, 20, 544), ("q5_k", S.T_Q5_K, 20, 512)]:
+                                ("q5_0", S.T_Q5_0, 20, 544), ("q5_k", S.T_Q5_K, 20, 512),
+                                ("q4_0", S.T_Q4_0, 24, 544), ("q4_1", S.T_Q4_1, 20, 544),
+                                ("q5_1", S.T_Q5_1, 20, 544), ("iq4_nl", S.T_IQ4_NL, 20, 544)]:
         w = S.weights(t, rows, cols, 400 + t)
         mm[f"{name}_w"] = w
         for nb in (3, 8, 45):
             X = S.activations(cols, 500 + nb, rows=nb)
             mm[f"{name}_X{nb}"] = X
             mm[f"{name}_Y{nb}"] = ref.matmul(t, w, cols, X)
-            if t == S.T_Q4_K:
+            if t in (S.T_Q4_K, S.T_Q4_0):
                 mm[f"{name}_Y{nb}_rp"] = ref.matmul(t, w, cols, X, repack=True)
     np.savez_compressed(os.path.join(HERE, "matmul.npz"), **mm)
 

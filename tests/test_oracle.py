@@ -19,8 +19,10 @@ from conftest import ROOT, bits_equal, golden, rel_err
 from fastgguf_amd import synth as S
 from oracle import ORDER_REPACKED, ORDER_ROW, Oracle
 
-TYPES = {"q8_0": S.T_Q8_0, "q4_k": S.T_Q4_K, "q6_k": S.T_Q6_K, "q5_0": S.T_Q5_0, "q5_k": S.T_Q5_K}
-ALL = [S.T_Q8_0, S.T_Q4_K, S.T_Q6_K, S.T_Q5_0, S.T_Q5_K]
+TYPES = {"q8_0": S.T_Q8_0, "q4_k": S.T_Q4_K, "q6_k": S.T_Q6_K, "q5_0": S.T_Q5_0, "q5_k": S.T_Q5_K,
+         "q4_0": S.T_Q4_0, "q4_1": S.T_Q4_1, "q5_1": S.T_Q5_1, "iq4_nl": S.T_IQ4_NL}
+ALL = list(TYPES.values())
+REPACKABLE = (S.T_Q4_K, S.T_Q4_0)  # the types the reference repacks (repack_tensor, fastgguf.c:2486)
 
 
 # ---------------------------------------------------------------- golden vectors (reference)
@@ -40,7 +42,7 @@ def test_matvec_matches_golden(oracle, name, gen):
     w, x = g[f"{name}_{gen}_w"], g[f"{name}_{gen}_x"]
     cols = x.size
     assert bits_equal(oracle.matvec(t, w, cols, x, ORDER_ROW), g[f"{name}_{gen}_y"])
-    if t == S.T_Q4_K:
+    if t in REPACKABLE:
         assert bits_equal(oracle.matvec(t, w, cols, x, ORDER_REPACKED), g[f"{name}_{gen}_y_rp"])
 
 
@@ -52,7 +54,7 @@ def test_matmul_matches_golden(oracle, name, nb):
     w, X = g[f"{name}_w"], g[f"{name}_X{nb}"]
     cols = X.shape[1]
     assert bits_equal(oracle.matmul(t, w, cols, X, ORDER_ROW), g[f"{name}_Y{nb}"])
-    if t == S.T_Q4_K:
+    if t in REPACKABLE:
         assert bits_equal(oracle.matmul(t, w, cols, X, ORDER_REPACKED), g[f"{name}_Y{nb}_rp"])
 
 
@@ -102,14 +104,14 @@ def test_expf_restatement_matches_libm(oracle):
 def test_oracle_matches_compiled_reference_random(oracle, reference):
     """Fresh random shapes and seeds against the reference's kernels (where oracle/_ref is built)."""
     rng = np.random.Generator(np.random.PCG64(7))
-    for case in range(10):
-        t = ALL[case % 5]
+    for case in range(18):
+        t = ALL[case % len(ALL)]
         cols = int(rng.integers(1, 5)) * 256
         rows = 8 * int(rng.integers(1, 5))
         w = (S.weights if case % 2 else S.random_bytes_weights)(t, rows, cols, 1000 + case)
         x = S.activations(cols, 2000 + case)
         assert bits_equal(oracle.matvec(t, w, cols, x), reference.matvec(t, w, cols, x))
-        if t == S.T_Q4_K:
+        if t in REPACKABLE:
             assert bits_equal(oracle.matvec(t, w, cols, x, ORDER_REPACKED), reference.matvec(t, w, cols, x, True))
         nb = int(rng.integers(8, 20))
         X = S.activations(cols, 3000 + case, rows=nb)
@@ -165,12 +167,18 @@ def _decode_codes(t, w_row, cols):
     if t == S.T_Q8_0:
         q = blk[:, 2:34].view(np.int8).astype(np.int64).reshape(-1)
         return q, np.ones_like(q), np.zeros_like(q)
-    if t == S.T_Q5_0:  # element j: nibble j of qs (low nibbles, then high), bit j of qh as bit 4; minus 16
-        qh = blk[:, 2:6].copy().view("<u4").astype(np.int64)  # [nb, 1]
-        qs = blk[:, 6:22].astype(np.int64)
-        nib = np.concatenate([qs & 15, qs >> 4], axis=1)
-        bit = (qh >> np.arange(32)) & 1
-        q = (nib | (bit << 4)) - 16
+    if t in (S.T_Q5_0, S.T_Q5_1, S.T_Q4_0, S.T_Q4_1, S.T_IQ4_NL):
+        # element j: nibble j of qs (low nibbles, then high), with bit j of qh as bit 4 (Q5)
+        qoff = {S.T_Q5_0: 6, S.T_Q5_1: 8, S.T_Q4_0: 2, S.T_Q4_1: 4, S.T_IQ4_NL: 2}[t]
+        qs = blk[:, qoff:qoff + 16].astype(np.int64)
+        q = np.concatenate([qs & 15, qs >> 4], axis=1)
+        if t in (S.T_Q5_0, S.T_Q5_1):
+            h = 2 if t == S.T_Q5_0 else 4
+            qh = blk[:, h:h + 4].copy().view("<u4").astype(np.int64)  # [nb, 1]
+            q = q | (((qh >> np.arange(32)) & 1) << 4)
+        if t == S.T_IQ4_NL:  # the published IQ4_NL values (llama.cpp's kvalues_iq4nl)
+            q = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113])[q]
+        q = q - {S.T_Q5_0: 16, S.T_Q4_0: 8}.get(t, 0)
         return q.reshape(-1), np.ones(nb * 32, np.int64), np.zeros(nb * 32, np.int64)
     if t in (S.T_Q4_K, S.T_Q5_K):
         s12 = blk[:, 4:16].astype(np.int64)
@@ -250,7 +258,7 @@ def test_selftest_relations(oracle, t):
         act = oracle.quantize_for(t, X[b])
         ref = np.array([oracle.dot(t, w[r], act) for r in range(rows)], np.float32)
         assert rel_err(Y[b], ref) < 1e-5
-    if t == S.T_Q4_K:
+    if t in REPACKABLE:
         w = S.random_bytes_weights(t, 16, 768, 57)
         x = S.activations(768, 58)
         assert rel_err(oracle.matvec(t, w, 768, x, ORDER_REPACKED), oracle.matvec(t, w, 768, x, ORDER_ROW)) < 1e-5
@@ -260,7 +268,8 @@ def test_selftest_relations(oracle, t):
 
 MUTANTS = {1: "hsum8 order", 2: "MoE accumulate without fma", 3: "reciprocal instead of division",
            4: "Q6_K half-lane scale", 5: "Q4_K repacked single chain", 6: "Q4_K GEMM integer epilogue",
-           7: "Q5_0 fifth bit from the wrong half of qh", 8: "Q5_K qh bit pairing"}
+           7: "Q5_0 fifth bit from the wrong half of qh", 8: "Q5_K qh bit pairing",
+           9: "Q4_1 / Q5_1 min term without the fused multiply-add"}
 
 
 @pytest.fixture(scope="module")
@@ -278,7 +287,7 @@ def _golden_failures(o: Oracle) -> int:
         for gen in ("synth", "bytes"):
             x = g[f"{name}_{gen}_x"]
             fails += not bits_equal(o.matvec(t, g[f"{name}_{gen}_w"], x.size, x), g[f"{name}_{gen}_y"])
-            if t == S.T_Q4_K:
+            if t in REPACKABLE:
                 fails += not bits_equal(o.matvec(t, g[f"{name}_{gen}_w"], x.size, x, ORDER_REPACKED),
                                         g[f"{name}_{gen}_y_rp"])
     g = golden("matmul.npz")
