@@ -86,7 +86,7 @@ static int grow(fgh_ctx *c, DevBuf &b, size_t need) {
 }
 
 static bool type_supported(uint32_t t) {
-    return t == FGH_T_Q8_0 || t == FGH_T_Q4_K || t == FGH_T_Q6_K || t == FGH_T_Q5_0 || t == FGH_T_Q5_K;
+    return fgh::q8_kind((int)t) || t == FGH_T_Q4_K || t == FGH_T_Q6_K || t == FGH_T_Q5_K;
 }
 static bool q16_rows(uint32_t t) { return t == FGH_T_Q4_K || t == FGH_T_Q5_K; }  // 16-row tiles
 static int block_elems(uint32_t t) { return fgh::q8_kind((int)t) ? 32 : 256; }
@@ -94,6 +94,9 @@ static int block_bytes(uint32_t t) {
     switch (t) {
     case FGH_T_Q8_0: return 34;
     case FGH_T_Q5_0: return 22;
+    case FGH_T_Q4_0: case FGH_T_IQ4_NL: return 18;
+    case FGH_T_Q4_1: return 20;
+    case FGH_T_Q5_1: return 24;
     case FGH_T_Q4_K: return 144;
     case FGH_T_Q5_K: return 176;
     default: return 210;
@@ -102,10 +105,10 @@ static int block_bytes(uint32_t t) {
 static int tile_bytes(uint32_t t) {
     switch (t) {
     case FGH_T_Q8_0: return fgh::Q80_TILE;
-    case FGH_T_Q5_0: return fgh::Q50_TILE;
     case FGH_T_Q4_K: return fgh::Q4K_TILE;
     case FGH_T_Q5_K: return fgh::Q5K_TILE;
-    default: return fgh::Q6K_TILE;
+    case FGH_T_Q6_K: return fgh::Q6K_TILE;
+    default: return fgh::q32_layout((int)t).tile;  // the nibble types
     }
 }
 
@@ -276,10 +279,10 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     NO_CAPTURE(c);
     *out = nullptr;
     if (!host || rows <= 0 || n_mats <= 0 || cols <= 0) return fail(c, FGH_ERR_ARG, "upload: bad shape");
-    // the order the tensor will use: the reference repacks 2-D Q4_K matrices with rows % 8 == 0
-    // (repack_tensor, 2486-2488)
-    const int ord = type == FGH_T_Q4_K && (order == FGH_ORDER_REPACKED ||
-                                           (order == FGH_ORDER_AUTO && n_mats == 1 && rows % 8 == 0))
+    // the order the tensor will use: the reference repacks 2-D Q4_K and Q4_0 matrices with
+    // rows % 8 == 0 (repack_tensor, 2486-2489)
+    const int ord = (type == FGH_T_Q4_K || type == FGH_T_Q4_0) &&
+                            (order == FGH_ORDER_REPACKED || (order == FGH_ORDER_AUTO && n_mats == 1 && rows % 8 == 0))
                         ? FGH_ORDER_REPACKED
                         : FGH_ORDER_ROW;
     if (!type_supported(type) || cols % block_elems(type) != 0 ||

@@ -35,14 +35,32 @@ namespace fgh {
 //     [576, 704)   fifth bits: slice (r, i) at 576 + 2(8r + i), 16 bits n0 | n2 << 4 | n1 << 8 |
 //                  n3 << 12, where bit bb of the nibble n_t is the fifth bit of element 4i + t
 //                  of block bb
+//   Q4_0 / IQ4_NL tile (4 blocks of 8 rows, 576 B), Q4_1 (640 B), Q5_1 (768 B): Q5_0's regions
+//     in the order d [64 B], m [64 B, Q4_1 / Q5_1: fp16 m of row r, block bb at 8r + 2bb],
+//     nibbles [512 B], fifth bits [128 B, Q5_1] (q32_layout gives the offsets)
 //   (Q5_K shares the Q4_K layout with 512 B of fifth bits per (tile, block), fgh_q4k.hip)
 // ---------------------------------------------------------------------------------------------
-constexpr int T_Q5_0 = 6, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14;
+constexpr int T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
+              T_IQ4_NL = 20;
 constexpr int Q4K_TILE = 2304, Q5K_TILE = 2816, Q6K_TILE = 1680, Q80_TILE = 1088, Q50_TILE = 704;
 constexpr int Q4K_TILE_ROWS = 16;  // rows per Q4_K / Q5_K tile (8 for the other types)
 // the activation kind of a weight type (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for
-// Q8_0 / Q5_0, Q8_K blocks of 256 for the K-quants
-__host__ __device__ constexpr bool q8_kind(int type) { return type == T_Q8_0 || type == T_Q5_0; }
+// the 32-value types, Q8_K blocks of 256 for the K-quants
+__host__ __device__ constexpr bool q8_kind(int type) {
+    return type == T_Q8_0 || type == T_Q5_0 || type == T_Q4_0 || type == T_Q4_1 || type == T_Q5_1 ||
+           type == T_IQ4_NL;
+}
+// 32-value nibble types: tile bytes and region offsets (-1: absent) of a 4-block step
+struct Q32Layout {
+    int tile, m, n, h;
+};
+__host__ __device__ constexpr Q32Layout q32_layout(int type) {
+    return type == T_Q5_0 ? Q32Layout{704, -1, 64, 576}
+         : type == T_Q4_1 ? Q32Layout{640, 64, 128, -1}
+         : type == T_Q5_1 ? Q32Layout{768, 64, 128, 640}
+                          : Q32Layout{576, -1, 64, -1};  // Q4_0, IQ4_NL
+}
+__host__ __device__ constexpr bool q32_min(int type) { return type == T_Q4_1 || type == T_Q5_1; }
 
 // Device activation layouts. Q8_K (for the K-quants): per token, nb blocks of
 //   qs [nb][256] int8, permuted so lane i's 32 bytes are contiguous: position 32i + 4c + k holds

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void quant_q8_kernel(const float *__restrict__
 }
 
 // =============================================================================================
-// Upload-time re-layout of Q6_K / Q8_0 / Q5_0: file-layout rows (n_mats x rows x row_bytes) -> tiles in
+// Upload-time re-layout of Q6_K / Q8_0 / the nibble types: file-layout rows (n_mats x rows x row_bytes) -> tiles in
 // step-major order, step tb of row tile gl of matrix m at (m * ntile + tb) * gpm + gl (Q4_K has its
 // own, fgh_q4k.hip). One thread per destination byte; padding rows and padding blocks are zero.
 // =============================================================================================
@@ -130,42 +130,59 @@ __global__ void relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__rest
     }
 }
 
-// Q5_0 (tile of 4 blocks, 704 B, fgh_internal.h): one thread per destination byte, gathering the
-// nibbles and fifth bits it packs from the file's blocks {fp16 d, u32 qh, qs[16]} (fastgguf.c:
-// 518-532); element e of a block is nibble e of qs (low nibbles of qs[0..15], then their high
-// nibbles) with bit e of qh above it (q5_elem, 939-942)
-__device__ __forceinline__ int q5_nib(const uint8_t *p, int e) { return e < 16 ? (p[6 + e] & 15) : (p[e - 10] >> 4); }
-__device__ __forceinline__ int q5_bit(const uint8_t *p, int e) { return (p[2 + (e >> 3)] >> (e & 7)) & 1; }
-__global__ void relayout_q5_0_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int64_t rows, int nb,
-                                     int ntile, int64_t gpm, int64_t total, int64_t row_bytes) {
+// The nibble types (tile of 4 blocks: Q5_0 704 B, Q4_0 / IQ4_NL 576 B, Q4_1 640 B, Q5_1 768 B,
+// regions at q32_layout's offsets, fgh_internal.h): one thread per destination byte, gathering the
+// nibbles and fifth bits it packs from the file's blocks (Q4_0 / IQ4_NL {d, qs[16]}, Q4_1 {d, m,
+// qs}, Q5_0 {d, qh, qs}, Q5_1 {d, m, qh, qs}; fastgguf.c:485-550, 694-706); element e of a block
+// is nibble e of qs (low nibbles of qs[0..15], then their high nibbles) with bit e of qh above it
+// (nibbles32 809-814, q5_elem 939-942)
+struct Q32Src {
+    int bytes, qs, qh;  // block bytes, offsets of qs and qh (-1: none)
+};
+__device__ __forceinline__ Q32Src q32_src(int type) {
+    switch (type) {
+    case T_Q5_0: return {22, 6, 2};
+    case T_Q4_1: return {20, 4, -1};
+    case T_Q5_1: return {24, 8, 4};
+    default: return {18, 2, -1};  // Q4_0, IQ4_NL
+    }
+}
+__global__ void relayout_q32_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int type, int64_t rows,
+                                    int nb, int ntile, int64_t gpm, int64_t total, int64_t row_bytes) {
+    const Q32Layout L = q32_layout(type);
+    const Q32Src B = q32_src(type);
     for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
          o += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t t = o / Q50_TILE;  // = (m * ntile + tb) * gpm + gl
-        const int ob = (int)(o - t * Q50_TILE);
+        const int64_t t = o / L.tile;  // = (m * ntile + tb) * gpm + gl
+        const int ob = (int)(o - t * L.tile);
         const int64_t mt = t / gpm, gl = t - mt * gpm;
         const int64_t m = mt / ntile;
         const int tb = (int)(mt - m * ntile);
-        const int r = ob < 64 ? ob >> 3 : ob < 576 ? (ob - 64) >> 6 : (ob - 576) >> 4;
+        const bool in_m = L.m >= 0 && ob >= L.m && ob < L.m + 64;
+        const bool in_h = L.h >= 0 && ob >= L.h;
+        const int r = ob < 64 || in_m ? (ob & 63) >> 3 : in_h ? (ob - L.h) >> 4 : (ob - L.n) >> 6;
         const int64_t row = gl * 8 + r;
         // block bb of the step in this row, or null past the row's end
         auto blk = [&](int bb) -> const uint8_t * {
             const int b = 4 * tb + bb;
-            return row < rows && b < nb ? src + (m * rows + row) * row_bytes + (int64_t)b * 22 : nullptr;
+            return row < rows && b < nb ? src + (m * rows + row) * row_bytes + (int64_t)b * B.bytes : nullptr;
         };
+        auto nib = [&](const uint8_t *p, int e) { return e < 16 ? (p[B.qs + e] & 15) : (p[B.qs + e - 16] >> 4); };
+        auto bit = [&](const uint8_t *p, int e) { return (p[B.qh + (e >> 3)] >> (e & 7)) & 1; };
         int v = 0;
-        if (ob < 64) {  // fp16 d of block (ob & 7) >> 1
+        if (ob < 64 || in_m) {  // fp16 d (or m) of block (ob & 7) >> 1
             const uint8_t *p = blk((ob & 7) >> 1);
-            v = p ? p[ob & 1] : 0;
-        } else if (ob < 576) {  // byte 4w + t of slice i: element 4i + t of blocks 2w (low), 2w + 1 (high)
-            const int q = ob - 64, i = (q >> 3) & 7, w = (q >> 2) & 1, e = 4 * i + (q & 3);
+            v = p ? p[(in_m ? 2 : 0) + (ob & 1)] : 0;
+        } else if (!in_h) {  // byte 4w + t of slice i: element 4i + t of blocks 2w (low), 2w + 1 (high)
+            const int q = ob - L.n, i = (q >> 3) & 7, w = (q >> 2) & 1, e = 4 * i + (q & 3);
             const uint8_t *p0 = blk(2 * w), *p1 = blk(2 * w + 1);
-            v = (p0 ? q5_nib(p0, e) : 0) | (p1 ? q5_nib(p1, e) << 4 : 0);
+            v = (p0 ? nib(p0, e) : 0) | (p1 ? nib(p1, e) << 4 : 0);
         } else {  // byte hb of slice i's fifth bits: nibbles n_hb (low) and n_hb+2 (high)
-            const int q = ob - 576, i = (q >> 1) & 7, hb = q & 1;
+            const int q = ob - L.h, i = (q >> 1) & 7, hb = q & 1;
 #pragma unroll
             for (int bb = 0; bb < 4; ++bb) {
                 const uint8_t *p = blk(bb);
-                if (p) v |= (q5_bit(p, 4 * i + hb) << bb) | (q5_bit(p, 4 * i + hb + 2) << (4 + bb));
+                if (p) v |= (bit(p, 4 * i + hb) << bb) | (bit(p, 4 * i + hb + 2) << (4 + bb));
             }
         }
         dst[o] = (uint8_t)v;
@@ -196,7 +213,8 @@ hipError_t launch_relayout(const uint8_t *src, uint8_t *dst, int type, int64_t r
                            int64_t gpm, int64_t total, int64_t row_bytes, hipStream_t s) {
     const int64_t want = (total + 255) / 256;
     const int grid = (int)(want < 65536 ? want : 65536);
-    if (type == T_Q5_0) relayout_q5_0_kernel<<<grid, 256, 0, s>>>(src, dst, rows, nb, ntile, gpm, total, row_bytes);
+    if (q8_kind(type) && type != T_Q8_0)
+        relayout_q32_kernel<<<grid, 256, 0, s>>>(src, dst, type, rows, nb, ntile, gpm, total, row_bytes);
     else relayout_kernel<<<grid, 256, 0, s>>>(src, dst, type, rows, nb, ntile, gpm, total, row_bytes);
     return hipGetLastError();
 }

@@ -1,8 +1,8 @@
-// fgh_matvec.hip - the decode matvec for Q6_K / Q8_0 / Q5_0 on gfx950 (Q4_K and Q5_K have their
-// own kernel in fgh_q4k.hip, on the same plan).
+// fgh_matvec.hip - the decode matvec for Q6_K and the 32-value types (Q8_0, Q5_0, Q4_0, Q4_1, Q5_1,
+// IQ4_NL) on gfx950 (Q4_K and Q5_K have their own kernel in fgh_q4k.hip, on the same plan).
 //
 // Tiles (fgh_internal.h) are 8 rows of one step: one block (Q6_K, 1680 B) or four blocks (Q8_0,
-// 1088 B; Q5_0, 704 B). They lie step-major: step s of row tile t of matrix m at
+// 1088 B; Q5_0 704 B, Q4_0 / IQ4_NL 576 B, Q4_1 640 B, Q5_1 768 B). They lie step-major: step s of row tile t of matrix m at
 // ((m * steps + s) * tpm + t) * tile bytes (tpm = row tiles per matrix), so the wavefronts of a
 // launch, all at about the same step, read one contiguous stretch of HBM at a time.
 //
@@ -13,7 +13,10 @@
 // forms its exact integer lane partial (v_dot4_i32_i8, 16-bit scale products by v_dot2_i32_i16)
 // and advances its fp32 chain in registers in block order:
 //   Q8_0, dot_q8_0_q8 (fastgguf.c:891-902):   acc_i = fma(d * xd, s_i, acc_i), out = hsum8(acc)
-//   Q5_0, dot_q5_0_q8 (fastgguf.c:944-959):   the same, s_i over the values q5 - 16
+//   Q5_0, Q4_0, IQ4_NL (944-959, 833-857, 1547-1562): the same, s_i over q5 - 16, q - 8, kvalues[q]
+//   Q4_1, Q5_1 (1020-1031, 973-989): the same over q, plus one min chain per row,
+//        macc = fma(m * xd, s16_0 + s16_1, macc), out = hsum8(acc) + macc
+//   Q4_0 repacked, dot_q40x8 (2424-2467): acc = fma(d * xd, isum, acc) per row over whole blocks
 //   Q6_K, dot_q6_K_q8k (fastgguf.c:1232-1264): acc_i = fma(d * yd, lane_i, acc_i),
 //        cacc_p = fma(32 d yd, corr_p, cacc_p) in lanes i = p < 4, out = hsum8(acc) - hsum4(cacc)
 // so the outputs are bit-identical to the reference's row kernels. Short matrices split the steps
@@ -37,13 +40,19 @@ __host__ __device__ constexpr size_t act_off_d(int type, int nb) {
 __host__ __device__ constexpr size_t act_off_s(int type, int nb) {
     return align16(act_off_d(type, nb) + 4 * (size_t)(q8_kind(type) ? 4 * mv_steps(type, nb) : nb));
 }
+// Q8: after d, for Q4_1 / Q5_1 only, the int32 sum of each block's 32 quants (s16[0] + s16[1], the
+// min term) [4 * steps]; Q8_K: bs [nb][16] int16
 __host__ __device__ constexpr size_t act_lds_bytes(int type, int nb) {
-    return q8_kind(type) ? act_off_s(type, nb) : align16(act_off_s(type, nb) + (size_t)nb * 32);
+    return q8_kind(type) ? act_off_s(type, nb) + (q32_min(type) ? (size_t)16 * mv_steps(type, nb) : 0)
+                         : align16(act_off_s(type, nb) + (size_t)nb * 32);
 }
-// fp32 records of one step of one tile (block split): lane partials, then d * yd per row
-__host__ __device__ constexpr size_t rec_bytes(int type) { return q8_kind(type) ? 64 * 16 + 8 * 16 : 64 * 8 + 8 * 4; }
+// fp32 records of one step of one tile (block split): lane partials, then d * yd per row (and
+// m * yd per row for Q4_1 / Q5_1)
+__host__ __device__ constexpr size_t rec_bytes(int type) {
+    return q8_kind(type) ? 64 * 16 + 8 * 16 + (q32_min(type) ? 8 * 16 : 0) : 64 * 8 + 8 * 4;
+}
 __host__ __device__ constexpr int mv_tile_bytes(int type) {
-    return type == T_Q6_K ? Q6K_TILE : type == T_Q5_0 ? Q50_TILE : Q80_TILE;
+    return type == T_Q6_K ? Q6K_TILE : type == T_Q8_0 ? Q80_TILE : q32_layout(type).tile;
 }
 
 __device__ __forceinline__ float ror_f32(float v, int n) {  // DPP row_ror:n within 16 lanes
@@ -124,12 +133,16 @@ __device__ __forceinline__ void xq_store(int nb, int rb, const XVals &xv, uint8_
         s += q0 + q1 + q2 + q3;
         w[u] = pack_q(q0, q1, q2, q3);
     }
+    if (q32_min(TYPE)) s += dpp_xor1(s);  // the block's two threads: its 32 quants
     if (b >= nb) return;
     if (q8_kind(TYPE)) {  // dwords 4 tl .. 4 tl + 3 of block b
         uint8_t *g = act + (size_t)128 * (b >> 2) + 4 * (b & 3);
 #pragma unroll
         for (int u = 0; u < 4; ++u) *(uint32_t *)(g + 16 * (4 * tl + u)) = w[u];
-        if (tl == 0) ((float *)(act + act_off_d(TYPE, nb)))[b] = d;
+        if (tl == 0) {
+            ((float *)(act + act_off_d(TYPE, nb)))[b] = d;
+            if (q32_min(TYPE)) ((int32_t *)(act + act_off_s(TYPE, nb)))[b] = s;
+        }
     } else {  // value 16 tl + 4 u = 32 c + 4 i (c = tl / 2, i = 4 (tl % 2) + u) -> position 32 i + 4 c
         const int c = tl >> 1;
 #pragma unroll
@@ -159,17 +172,17 @@ __device__ __forceinline__ void xq_finish(const float *__restrict__ x, const flo
 // Q8_0: q = the lane's dword of each of the 4 blocks, d = its row's 4 fp16 scales.
 // Q5_0: n = the lane's nibble bytes of the 4 blocks, h = its 16 fifth bits, d as Q8_0.
 // Q6_K: q = 4 ql dwords (2 h + s), h = 2 qh dwords, sc = its row's 16 int8 scales, d = fp16 d.
+// nibble types (Q4_0, Q4_1, Q5_0, Q5_1, IQ4_NL): n = the lane's nibble bytes of the 4 blocks,
+// d (and m) = its row's 4 fp16 scales (and mins), h = its 16 fifth bits
 template <int TYPE>
-struct StepW;
+struct StepW {
+    uint2 n, d, m;
+    uint32_t h;
+};
 template <>
 struct StepW<T_Q8_0> {
     uint4 q;
     uint2 d;
-};
-template <>
-struct StepW<T_Q5_0> {
-    uint2 n, d;
-    uint32_t h;
 };
 template <>
 struct StepW<T_Q6_K> {
@@ -183,11 +196,14 @@ __device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW
     w.q = bld16(r, 64 + 16 * lane);
     w.d = bld8(r, 8 * (lane >> 3));
 }
-__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q5_0> &w) {
-    const BufRes r = buf_res(T, Q50_TILE);
-    w.n = bld8(r, 64 + 8 * lane);
-    w.h = bld2(r, 576 + 2 * lane);
+template <int TYPE>
+__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<TYPE> &w) {
+    constexpr Q32Layout L = q32_layout(TYPE);
+    const BufRes r = buf_res(T, L.tile);
+    w.n = bld8(r, L.n + 8 * lane);
     w.d = bld8(r, 8 * (lane >> 3));
+    if (L.m >= 0) w.m = bld8(r, L.m + 8 * (lane >> 3));
+    if (L.h >= 0) w.h = bld2(r, L.h + 2 * lane);
 }
 __device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q6_K> &w) {
     const BufRes r = buf_res(T, Q6K_TILE);
@@ -204,18 +220,33 @@ __device__ __forceinline__ void q32_sums(const StepW<T_Q8_0> &w, uint4 y, int sd
     sd[2] = dot4((int)w.q.z, (int)y.z, 0);
     sd[3] = dot4((int)w.q.w, (int)y.w, 0);
 }
-// Q5_0: q5 of element 4i + t of block k is nibble byte t of n (blocks 2w / 2w + 1 in the low / high
-// nibbles of dword w) with bit 4 from the fifth bits spread to one nibble per byte; the offset
-// -16 (the reference's bx = q5 - 16) enters as a second dot with -16 in every byte
-__device__ __forceinline__ void q32_sums(const StepW<T_Q5_0> &w, uint4 y, int sd[4]) {
-    const uint32_t e = (w.h & 0x0F0Fu) | ((w.h << 12) & 0x0F0F0000u);  // byte t: bit k = block k
+// IQ4_NL: the value kvalues_iq4nl[q] (fastgguf.c:475-477) of each nibble byte, by two byte
+// permutes over the table's halves and a third that picks, per byte, the half by bit 3
+__device__ __forceinline__ uint32_t iq4nl_values(uint32_t nib) {
+    constexpr uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;  // -127 .. 113
+    const uint32_t sel = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
+    return __builtin_amdgcn_perm(hi, lo, ((nib >> 1) & 0x04040404u) | 0x03020100u);
+}
+// Nibble types: the value of element 4i + t of block k is nibble byte t of n (blocks 2w / 2w + 1
+// in the low / high nibbles of dword w), with (Q5_0 / Q5_1) bit 4 from the fifth bits spread to
+// one nibble per byte. The offsets of Q4_0 (-8) and Q5_0 (-16), the reference's bx = q - 8 and
+// q5 - 16, enter as a second dot with the offset in every byte.
+template <int TYPE>
+__device__ __forceinline__ void q32_sums(const StepW<TYPE> &w, uint4 y, int sd[4]) {
+    constexpr bool Q5 = TYPE == T_Q5_0 || TYPE == T_Q5_1;
+    const uint32_t e = Q5 ? (w.h & 0x0F0Fu) | ((w.h << 12) & 0x0F0F0000u) : 0u;  // byte t: bit k = block k
     const uint32_t Y[4] = {y.x, y.y, y.z, y.w};
     const uint32_t N[2] = {w.n.x, w.n.y};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint32_t nib = ((k & 1) ? N[k >> 1] >> 4 : N[k >> 1]) & 0x0F0F0F0Fu;
-        const uint32_t q5 = nib | ((e << (4 - k)) & 0x10101010u);
-        sd[k] = dot4((int)q5, (int)Y[k], dot4((int)0xF0F0F0F0u, (int)Y[k], 0));
+        uint32_t q = ((k & 1) ? N[k >> 1] >> 4 : N[k >> 1]) & 0x0F0F0F0Fu;
+        if (Q5) q |= (e << (4 - k)) & 0x10101010u;
+        if (TYPE == T_IQ4_NL) q = iq4nl_values(q);
+        const int off = TYPE == T_Q5_0 ? dot4((int)0xF0F0F0F0u, (int)Y[k], 0)
+                      : TYPE == T_Q4_0 ? dot4((int)0xF8F8F8F8u, (int)Y[k], 0)
+                                       : 0;
+        sd[k] = dot4((int)q, (int)Y[k], off);
     }
 }
 
@@ -269,8 +300,11 @@ __device__ __forceinline__ int mv_tensor_of(const MvArgs &a, int64_t g) {
 
 // Workgroup = TPW tiles x S wavefronts per tile (wavefront ks of a tile takes its ks-th run of
 // ceil(steps / S) steps); grid = (tiles over all tensors / TPW, tokens).
-template <int TYPE, int R, int TPW, int S, bool DUMP, bool SILU = false>
+// ORDER 1 (Q4_0 only): the repacked order of dot_q40x8 (fastgguf.c:2424-2467), one chain per row
+// over whole-block integers, acc = fma(d * yd, isum, acc), out = acc.
+template <int TYPE, int R, int TPW, int S, bool DUMP, bool SILU = false, int ORDER = 0>
 __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
+    static_assert(ORDER == 0 || TYPE == T_Q4_0, "only Q4_0 has a repacked order here");
     constexpr int WPG = TPW * S;
     constexpr int TB = mv_tile_bytes(TYPE);
     extern __shared__ __align__(16) uint8_t smem[];
@@ -309,7 +343,8 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
     const bool row_ok = live && mrow + r < rows;
     // records of the wavefronts ks >= 1 (step s of the tile at s - nsw): lane partials, then fd
     uint8_t *rec = smem + act_lds_bytes(TYPE, nb) + (size_t)ts * (nst - nsw) * rec_bytes(TYPE);
-    float acc = 0.0f, cacc = 0.0f;
+    const int32_t *abs = (const int32_t *)(act + act_off_s(TYPE, nb));  // Q4_1 / Q5_1: block sums
+    float acc = 0.0f, cacc = 0.0f;  // cacc: Q6_K's correction chain, or Q4_1 / Q5_1's min chain
 
     auto step = [&](const StepW<TYPE> &w, int st) {
         const bool chain = S == 1 || ks == 0;
@@ -321,24 +356,39 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
             q32_sums(w, y, sd);
             const float fd[4] = {fp16_bits_to_f32(w.d.x & 0xFFFF) * yd.x, fp16_bits_to_f32(w.d.x >> 16) * yd.y,
                                  fp16_bits_to_f32(w.d.y & 0xFFFF) * yd.z, fp16_bits_to_f32(w.d.y >> 16) * yd.w};
+            float fm[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // Q4_1 / Q5_1: FP16(m) * xd of the min chain
+            if constexpr (q32_min(TYPE)) {
+                fm[0] = fp16_bits_to_f32(w.m.x & 0xFFFF) * yd.x;
+                fm[1] = fp16_bits_to_f32(w.m.x >> 16) * yd.y;
+                fm[2] = fp16_bits_to_f32(w.m.y & 0xFFFF) * yd.z;
+                fm[3] = fp16_bits_to_f32(w.m.y >> 16) * yd.w;
+            }
+            if (ORDER == 1) {  // whole-block integers in every lane of the row
+#pragma unroll
+                for (int k = 0; k < 4; ++k) sd[k] = sum8_i32(sd[k]);
+            }
             const int nbs = nb - 4 * st;  // blocks of this step (the last one may have fewer)
             if (chain) {
-                if (nbs >= 4) {  // uniform
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) acc = __builtin_fmaf(fd[k], (float)sd[k], acc);
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 3; ++k)
-                        if (k < nbs) acc = __builtin_fmaf(fd[k], (float)sd[k], acc);
+                int bsv[4] = {0, 0, 0, 0};
+                if constexpr (q32_min(TYPE)) {
+                    const int4 bs = *(const int4 *)(abs + 4 * st);
+                    bsv[0] = bs.x; bsv[1] = bs.y; bsv[2] = bs.z; bsv[3] = bs.w;
                 }
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (nbs >= 4 || k < nbs) {  // uniform
+                        acc = __builtin_fmaf(fd[k], (float)sd[k], acc);
+                        if (q32_min(TYPE)) cacc = __builtin_fmaf(fm[k], (float)bsv[k], cacc);
+                    }
             } else {
                 ((float4 *)rs)[lane] = make_float4((float)sd[0], (float)sd[1], (float)sd[2], (float)sd[3]);
                 if (i == 0) ((float4 *)(rs + 1024))[r] = make_float4(fd[0], fd[1], fd[2], fd[3]);
+                if (q32_min(TYPE) && i == 0) ((float4 *)(rs + 1152))[r] = make_float4(fm[0], fm[1], fm[2], fm[3]);
             }
             if (DUMP) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const int tsum = sum8_i32(sd[k]);
+                    const int tsum = ORDER == 1 ? sd[k] : sum8_i32(sd[k]);
                     if (row_ok && i == 0 && k < nbs) {
                         const size_t di = (size_t)(obase + mrow + r) * nb + 4 * st + k;
                         a.dump_s[di] = tsum;
@@ -388,25 +438,29 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
         for (int st0 = nsw; st0 < nst; st0 += CH) {
             const uint8_t *rs = rec + (size_t)(st0 - nsw) * rec_bytes(TYPE);
             if constexpr (q8_kind(TYPE)) {
-                float4 sv[CH], fv[CH];
+                float4 sv[CH], fv[CH], mv[CH];
+                int4 bv[CH];
 #pragma unroll
                 for (int c = 0; c < CH; ++c) {  // records past the end are read but not used
                     sv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE)))[lane];
                     fv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE) + 1024))[r];
+                    if (q32_min(TYPE)) {
+                        mv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE) + 1152))[r];
+                        bv[c] = *(const int4 *)(abs + 4 * (st0 + c));
+                    }
                 }
 #pragma unroll
                 for (int c = 0; c < CH; ++c) {
                     const int nbs = nb - 4 * (st0 + c);  // uniform
-                    if (nbs >= 4) {
-                        acc = __builtin_fmaf(fv[c].x, sv[c].x, acc);
-                        acc = __builtin_fmaf(fv[c].y, sv[c].y, acc);
-                        acc = __builtin_fmaf(fv[c].z, sv[c].z, acc);
-                        acc = __builtin_fmaf(fv[c].w, sv[c].w, acc);
-                    } else {
-                        if (nbs > 0) acc = __builtin_fmaf(fv[c].x, sv[c].x, acc);
-                        if (nbs > 1) acc = __builtin_fmaf(fv[c].y, sv[c].y, acc);
-                        if (nbs > 2) acc = __builtin_fmaf(fv[c].z, sv[c].z, acc);
-                    }
+                    const float sk[4] = {sv[c].x, sv[c].y, sv[c].z, sv[c].w}, fk[4] = {fv[c].x, fv[c].y, fv[c].z, fv[c].w};
+                    const float mk[4] = {mv[c].x, mv[c].y, mv[c].z, mv[c].w};
+                    const int bk[4] = {bv[c].x, bv[c].y, bv[c].z, bv[c].w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (nbs >= 4 || k < nbs) {
+                            acc = __builtin_fmaf(fk[k], sk[k], acc);
+                            if (q32_min(TYPE)) cacc = __builtin_fmaf(mk[k], (float)bk[k], cacc);
+                        }
                 }
             } else {
                 float2 sv[CH];
@@ -425,15 +479,17 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
             }
         }
     }
-    // hsum8(acc) - hsum4(cacc) over the row's 8 lanes (fastgguf.c:797-806, 1089-1095), in lane i = 0
+    // hsum8(acc) - hsum4(cacc) over the row's 8 lanes (fastgguf.c:797-806, 1089-1095), in lane i = 0;
+    // Q4_1 / Q5_1: hsum8(acc) + macc (973-989, 1020-1031); repacked Q4_0: the row chain itself
     const float e = acc + __shfl_xor(acc, 4);  // v_i + v_i+4
     const float f = e + xor1_f32(e);
     const float h8 = f + xor2_f32(f);
-    float out = h8;
+    float out = ORDER == 1 ? acc : h8;
     if (TYPE == T_Q6_K) {
         const float g = cacc + xor1_f32(cacc);
         out = h8 - (g + xor2_f32(g));
     }
+    if (q32_min(TYPE)) out = h8 + cacc;
     if (row_ok && i == 0) a.t[ti].y[(size_t)tok * a.ldy + obase + mrow + r] = out;
 }
 
@@ -451,17 +507,17 @@ size_t matvec_lds_bytes(int type, int order, int nb) {
     return mv_lds(type, nb, 4, 1);
 }
 
-template <int TYPE, int R, int TPW, int S>
+template <int TYPE, int ORDER, int R, int TPW, int S>
 static hipError_t mv_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
     const unsigned wg = (unsigned)((a.groups + TPW - 1) / TPW);
-    if (a.dump_s) mv_kernel<TYPE, R, TPW, S, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
-    else if (a.xu) mv_kernel<TYPE, R, TPW, S, false, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
-    else mv_kernel<TYPE, R, TPW, S, false><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    if (a.dump_s) mv_kernel<TYPE, R, TPW, S, true, false, ORDER><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    else if (a.xu) mv_kernel<TYPE, R, TPW, S, false, true, ORDER><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    else mv_kernel<TYPE, R, TPW, S, false, false, ORDER><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     return hipGetLastError();
 }
-template <int TYPE, int TPW, int S>
+template <int TYPE, int ORDER, int TPW, int S>
 static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
-    return R == 2 ? mv_launch<TYPE, 2, TPW, S>(a, ntok, lds, s) : mv_launch<TYPE, 4, TPW, S>(a, ntok, lds, s);
+    return R == 2 ? mv_launch<TYPE, ORDER, 2, TPW, S>(a, ntok, lds, s) : mv_launch<TYPE, ORDER, 4, TPW, S>(a, ntok, lds, s);
 }
 
 // Launch shape: launches of fewer than 768 tiles (tiles x tokens) split the steps of a tile over up
@@ -469,7 +525,7 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 // more (Q6_K: 2), the records within the 160 KiB of LDS of a workgroup and every workgroup of the
 // launch resident at once; tiles per workgroup 4, 2 or 1 for S = 1, 2 or more. Ring depth:
 // 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps, 4 otherwise.
-template <int TYPE>
+template <int TYPE, int ORDER = 0>
 static hipError_t mv_launch_type(const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
     if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
     const int nb = a.nb, nst = mv_steps(TYPE, nb);
@@ -486,10 +542,10 @@ static hipError_t mv_launch_type(const MvArgs &a, int ntok, int num_cu, hipStrea
     const size_t lds = mv_lds(TYPE, nb, mv_tpw(S), S);
     if (lds > (S == 1 ? (size_t)65536 : GEMM_LDS_MAX)) return hipErrorInvalidValue;
     switch (S) {
-    case 1: return mv_launch_r<TYPE, 4, 1>(R, a, ntok, lds, s);
-    case 2: return mv_launch_r<TYPE, 2, 2>(R, a, ntok, lds, s);
-    case 4: return mv_launch_r<TYPE, 1, 4>(R, a, ntok, lds, s);
-    default: return mv_launch_r<TYPE, 1, 8>(R, a, ntok, lds, s);
+    case 1: return mv_launch_r<TYPE, ORDER, 4, 1>(R, a, ntok, lds, s);
+    case 2: return mv_launch_r<TYPE, ORDER, 2, 2>(R, a, ntok, lds, s);
+    case 4: return mv_launch_r<TYPE, ORDER, 1, 4>(R, a, ntok, lds, s);
+    default: return mv_launch_r<TYPE, ORDER, 1, 8>(R, a, ntok, lds, s);
     }
 }
 
@@ -498,6 +554,11 @@ hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int nu
     if (type == T_Q6_K) return mv_launch_type<T_Q6_K>(a, ntok, num_cu, s);
     if (type == T_Q8_0) return mv_launch_type<T_Q8_0>(a, ntok, num_cu, s);
     if (type == T_Q5_0) return mv_launch_type<T_Q5_0>(a, ntok, num_cu, s);
+    if (type == T_Q5_1) return mv_launch_type<T_Q5_1>(a, ntok, num_cu, s);
+    if (type == T_Q4_1) return mv_launch_type<T_Q4_1>(a, ntok, num_cu, s);
+    if (type == T_IQ4_NL) return mv_launch_type<T_IQ4_NL>(a, ntok, num_cu, s);
+    if (type == T_Q4_0)
+        return order == 1 ? mv_launch_type<T_Q4_0, 1>(a, ntok, num_cu, s) : mv_launch_type<T_Q4_0, 0>(a, ntok, num_cu, s);
     return hipErrorInvalidValue;
 }
 

@@ -1,8 +1,8 @@
 /*
  * fastgguf_hip.h - C ABI of the MI355X (gfx950) backend for fastgguf's quantized
- * weight x Q8-activation hot path: GGUF Q4_K / Q6_K / Q8_0 weights, and the Q5_K / Q5_0 of
- * Q5_K_M files and of K-quant files' fallback tensors, multiplied by activations quantized to the
- * reference's Q8 / Q8_K blocks, as a decode matvec, a <=64-token prompt matmul and a
+ * weight x Q8-activation hot path: GGUF Q4_K / Q6_K / Q8_0 weights, and Q5_K, Q5_0, Q4_0, Q4_1,
+ * Q5_1 and IQ4_NL (the other block types of the reference's integer kernels), multiplied by
+ * activations quantized to the reference's Q8 / Q8_K blocks, as a decode matvec, a <=64-token prompt matmul and a
  * mixture-of-experts FFN over the router-selected experts.
  *
  * The ABI is plain C: fixed-width integers, plain pointers and sizes, opaque handles, no
@@ -16,7 +16,7 @@
  * (fastgguf.c:746-793) do, per-block integer dot products are exact, and the fp32 outputs follow
  * the reference's accumulation order for matvec and MoE (bit-identical) and agree to within
  * 1e-5 relative per output vector for the MFMA prompt GEMM (and for the per-token kernels that
- * stand in for the reference's CPU prompt GEMM of Q6_K, Q8_0 and Q5_0 tensors).
+ * stand in for the reference's CPU prompt GEMM of Q6_K tensors and the 32-value types).
  *
  * Threading: a context is used by one host thread at a time, like the reference's g_gpu state
  * (fastgguf.c:1845-1857). Host-pointer calls are synchronous: outputs are valid on return, as
@@ -43,11 +43,15 @@ extern "C" {
 #endif
 
 /* GGML tensor types handled here (the reference's enum, fastgguf.c:215-221) */
+#define FGH_T_Q4_0 2u
+#define FGH_T_Q4_1 3u
 #define FGH_T_Q5_0 6u
+#define FGH_T_Q5_1 7u
 #define FGH_T_Q8_0 8u
 #define FGH_T_Q4_K 12u
 #define FGH_T_Q5_K 13u
 #define FGH_T_Q6_K 14u
+#define FGH_T_IQ4_NL 20u
 
 /* status codes */
 #define FGH_OK 0
@@ -57,10 +61,11 @@ extern "C" {
 #define FGH_SKIP_MEM (-4)      /* upload: over the memory budget, or device allocation failed */
 #define FGH_ERR_DEVICE (-5)    /* no usable device, or a HIP runtime error */
 
-/* fp32 accumulation order of a Q4_K tensor's matvec: which reference kernel it reproduces */
+/* fp32 accumulation order of a Q4_K / Q4_0 tensor's matvec: which reference kernel it reproduces
+ * (the other types have one order) */
 #define FGH_ORDER_AUTO (-1)    /* what the reference CPU path would pick (repack_tensor, 2486) */
-#define FGH_ORDER_ROW 0        /* dot_q4_K_q8k (fastgguf.c:1118), file-layout rows */
-#define FGH_ORDER_REPACKED 1   /* dot_q4Kx8 (fastgguf.c:2322), the 8-row repacked layout */
+#define FGH_ORDER_ROW 0        /* dot_q4_K_q8k / dot_q4_0_q8 (fastgguf.c:1118, 833), file-layout rows */
+#define FGH_ORDER_REPACKED 1   /* dot_q4Kx8 / dot_q40x8 (fastgguf.c:2322, 2424), the 8-row repacked layout */
 
 /* activation block kinds for the quantizer test hook (type_uses_q8, fastgguf.c:2167) */
 #define FGH_ACT_Q8 1           /* q8_blk_t  {f32 d; i8 qs[32];  i16 s16[2];}    40 bytes */

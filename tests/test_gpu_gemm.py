@@ -10,8 +10,9 @@ Bar:
   - Q6_K, Q8_0 and Q5_0 run the per-token decode kernels (dot_q6_K_q8k / dot_q8_0_q8 /
     dot_q5_0_q8 orders): compared with the same tolerance against the GEMM orders (gemm_kquant,
     gemm_q32).
-  - Q5_K has no prompt GEMM in the reference: its matmul is the row kernel per token there and here,
-    so it is compared bit for bit.
+  - Q4_0, Q4_1 and Q5_1 run the decode kernels per token too, against gemm_q32 with the same tolerance.
+  - Q5_K and IQ4_NL have no prompt GEMM in the reference: their matmul is the row kernel per token
+    there and here, so they are compared bit for bit.
 """
 import numpy as np
 import pytest
@@ -35,18 +36,19 @@ def check_tokens(Y, Yref):
 
 
 @pytest.mark.parametrize("name,t", [("q8_0", S.T_Q8_0), ("q4_k", S.T_Q4_K), ("q6_k", S.T_Q6_K),
-                                    ("q5_0", S.T_Q5_0), ("q5_k", S.T_Q5_K)])
+                                    ("q5_0", S.T_Q5_0), ("q5_k", S.T_Q5_K), ("q4_0", S.T_Q4_0),
+                                    ("q4_1", S.T_Q4_1), ("q5_1", S.T_Q5_1), ("iq4_nl", S.T_IQ4_NL)])
 @pytest.mark.parametrize("nb", [8, 45])
 def test_matmul_matches_golden(backend, name, t, nb):
     g = golden("matmul.npz")
     w, X = g[f"{name}_w"], g[f"{name}_X{nb}"]
     for order, key in ((ORDER_ROW, f"{name}_Y{nb}"), (ORDER_REPACKED, f"{name}_Y{nb}_rp")):
-        if order == ORDER_REPACKED and t != S.T_Q4_K:
+        if order == ORDER_REPACKED and t not in (S.T_Q4_K, S.T_Q4_0):
             continue
         tt = backend.upload(t, X.shape[1], w, order=order)
         Y = backend.matmul(tt, X)
         check_tokens(Y, g[key])
-        if t == S.T_Q5_K:
+        if t in (S.T_Q5_K, S.T_IQ4_NL):  # no prompt GEMM in the reference: its row kernel per token
             assert bits_equal(Y, g[key])
         tt.free()
 
@@ -81,14 +83,14 @@ def test_gemm_block_ints_exact(backend, oracle, case):
     tt.free()
 
 
-@pytest.mark.parametrize("t", [S.T_Q8_0, S.T_Q6_K, S.T_Q5_0, S.T_Q5_K])
+@pytest.mark.parametrize("t", [S.T_Q8_0, S.T_Q6_K, S.T_Q5_0, S.T_Q5_K, S.T_Q4_0, S.T_Q4_1, S.T_Q5_1, S.T_IQ4_NL])
 @pytest.mark.parametrize("nb", [8, 64])
 def test_matmul_other_types(backend, oracle, t, nb):
     cols, rows = 2048, 200
     w = S.weights(t, rows, cols, 80 + nb)
     X = S.activations(cols, 81 + nb, rows=nb)
     tt = backend.upload(t, cols, w)
-    check_tokens(backend.matmul(tt, X), oracle.matmul(t, w, cols, X, O_ROW))
+    check_tokens(backend.matmul(tt, X), oracle.matmul(t, w, cols, X, O_RP if t == S.T_Q4_0 else O_ROW))
     tt.free()
 
 

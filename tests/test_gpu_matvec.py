@@ -60,7 +60,9 @@ def test_quantizers_bit_exact(backend, oracle, n):
     assert backend.quantize_q8k(x).tobytes() == oracle.quantize_q8k(x).tobytes()
 
 
-NAMED = [("q8_0", S.T_Q8_0), ("q4_k", S.T_Q4_K), ("q6_k", S.T_Q6_K), ("q5_0", S.T_Q5_0), ("q5_k", S.T_Q5_K)]
+NAMED = [("q8_0", S.T_Q8_0), ("q4_k", S.T_Q4_K), ("q6_k", S.T_Q6_K), ("q5_0", S.T_Q5_0), ("q5_k", S.T_Q5_K),
+         ("q4_0", S.T_Q4_0), ("q4_1", S.T_Q4_1), ("q5_1", S.T_Q5_1), ("iq4_nl", S.T_IQ4_NL)]
+REPACKABLE = (S.T_Q4_K, S.T_Q4_0)  # the types the reference repacks (repack_tensor, fastgguf.c:2486)
 
 
 @pytest.mark.parametrize("name,t", NAMED)
@@ -71,7 +73,7 @@ def test_matvec_matches_golden(backend, name, t, gen):
     tt = backend.upload(t, x.size, w, order=ORDER_ROW)
     check_vec(backend.matvec(tt, x), g[f"{name}_{gen}_y"])
     tt.free()
-    if t == S.T_Q4_K:
+    if t in REPACKABLE:
         tt = backend.upload(t, x.size, w, order=ORDER_REPACKED)
         check_vec(backend.matvec(tt, x), g[f"{name}_{gen}_y_rp"])
         tt.free()
@@ -96,6 +98,17 @@ CASES = [  # (type, rows, cols, n_mats, order)
     (S.T_Q5_K, 16, 14336, 1, ORDER_ROW),       # many blocks (row-order block split over 8 wavefronts)
     (S.T_Q4_K, 21, 4096, 3, ORDER_ROW),        # row-order split over 4 wavefronts, 3-D, ragged rows
     (S.T_Q5_K, 40, 2304, 1, ORDER_ROW),        # row-order split of 9 blocks: runs of 5 and 4
+    (S.T_Q4_0, 64, 544, 1, ORDER_REPACKED),    # dot_q40x8's order, a last step of one block
+    (S.T_Q4_0, 64, 544, 1, ORDER_ROW),
+    (S.T_Q4_0, 37, 4096 + 64, 2, ORDER_ROW),   # 3-D, ragged rows, split launch
+    (S.T_Q4_0, 16, 4096 + 96, 1, ORDER_REPACKED),  # repacked order through a split launch
+    (S.T_Q4_1, 64, 544, 1, ORDER_ROW),
+    (S.T_Q4_1, 20, 96, 1, ORDER_ROW),          # 3 blocks: the min chain over a padding block
+    (S.T_Q4_1, 37, 4096 + 64, 2, ORDER_ROW),   # the min chain through split records
+    (S.T_Q5_1, 64, 544, 1, ORDER_ROW),
+    (S.T_Q5_1, 37, 4096 + 96, 2, ORDER_ROW),
+    (S.T_IQ4_NL, 64, 544, 1, ORDER_ROW),
+    (S.T_IQ4_NL, 37, 4096 + 32, 2, ORDER_ROW),
 ]
 
 
@@ -116,7 +129,8 @@ def test_block_ints_and_matvec_exact(backend, oracle, case):
 
 
 @pytest.mark.parametrize("cfg", ["cfg1_q8_0", "gate_q4k_rp", "gate_q4k_row", "down_q4k_rp", "lmhead_q6k",
-                                 "gate_q5k", "down_q5_0", "down_q5k", "down_q4k_row", "down_q8_0"])
+                                 "gate_q5k", "down_q5_0", "down_q5k", "down_q4k_row", "down_q8_0", "gate_q4_0_rp",
+                                 "down_q4_1", "gate_iq4_nl"])
 def test_matvec_config_shapes(backend, oracle, cfg):
     """BASELINE.json shapes with the benchmark's weight distributions (and the same FFN shapes
     for Q5_K and Q5_0)."""
@@ -131,6 +145,9 @@ def test_matvec_config_shapes(backend, oracle, cfg):
         "down_q5k": (S.T_Q5_K, 4096, 14336, ORDER_ROW),
         "down_q4k_row": (S.T_Q4_K, 4096, 14336, ORDER_ROW),
         "down_q8_0": (S.T_Q8_0, 4096, 14336, ORDER_ROW),
+        "gate_q4_0_rp": (S.T_Q4_0, 14336, 4096, ORDER_REPACKED),
+        "down_q4_1": (S.T_Q4_1, 4096, 14336, ORDER_ROW),
+        "gate_iq4_nl": (S.T_IQ4_NL, 14336, 4096, ORDER_ROW),
     }[cfg]
     w = S.weights(t, rows, cols, 11)
     x = S.activations(cols, 12)
@@ -156,7 +173,7 @@ def test_matvec_multi_qkv(backend, oracle):
         t.free()
 
 
-@pytest.mark.parametrize("t", [S.T_Q8_0, S.T_Q4_K, S.T_Q6_K, S.T_Q5_0, S.T_Q5_K])
+@pytest.mark.parametrize("t", [v for _, v in NAMED])
 @pytest.mark.parametrize("nb", [2, 3, 7])
 def test_matmul_small_batch(backend, oracle, t, nb):
     """nb < 8: the per-token decode kernel (matmul 3006-3009 for repacked tensors; the x4 tiles
@@ -166,7 +183,7 @@ def test_matmul_small_batch(backend, oracle, t, nb):
     X = S.activations(cols, 31 + nb, rows=nb)
     tt = backend.upload(t, cols, w)
     Y = backend.matmul(tt, X)
-    order = O_RP if t == S.T_Q4_K else O_ROW
+    order = O_RP if t in REPACKABLE else O_ROW
     Yo = oracle.matmul(t, w, cols, X, order)
     for b in range(nb):
         check_vec(Y[b], Yo[b])
@@ -179,7 +196,7 @@ def test_upload_refusals(backend):
         backend.upload(S.T_Q4_K, 300, np.zeros(8 * 144 * 2, np.uint8), rows=8)  # cols % 256 != 0
     assert e.value.status == SKIP_TYPE
     with pytest.raises(BackendError) as e:
-        backend.upload(2, 256, np.zeros(8 * 144, np.uint8), rows=8)  # Q4_0: not on this path
+        backend.upload(10, 256, np.zeros(8 * 84, np.uint8), rows=8)  # Q2_K: not on this path
     assert e.value.status == SKIP_TYPE
     with pytest.raises(BackendError) as e:  # 238 blocks: the quantized x no longer fits 64 KiB of LDS
         backend.upload(S.T_Q4_K, 238 * 256, np.zeros(16 * 238 * 144, np.uint8), rows=16)
@@ -196,11 +213,14 @@ def test_upload_refusals(backend):
     with pytest.raises(BackendError) as e:
         backend.upload(S.T_Q5_0, 1821 * 32, np.zeros(8 * 1821 * 22, np.uint8), rows=8)
     assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:  # Q4_1 past 1636 blocks (its block sums share the LDS)
+        backend.upload(S.T_Q4_1, 1637 * 32, np.zeros(8 * 1637 * 20, np.uint8), rows=8)
+    assert e.value.status == SKIP_TYPE
     with pytest.raises(BackendError) as e:  # Q5_0 cols % 32 != 0
         backend.upload(S.T_Q5_0, 48, np.zeros(8 * 22, np.uint8), rows=8)
     assert e.value.status == SKIP_TYPE
     info1 = backend.info()
-    assert info1["n_skip_type"] == info0["n_skip_type"] + 8
+    assert info1["n_skip_type"] == info0["n_skip_type"] + 9
     from fastgguf_amd.backend import Backend
     small = Backend(0, budget_bytes=1 << 20)
     with pytest.raises(BackendError) as e:
@@ -223,14 +243,16 @@ def test_widest_q4k_rows(backend, oracle, order):
 
 
 @pytest.mark.parametrize("t,nb", [(S.T_Q6_K, 224), (S.T_Q8_0, 1820), (S.T_Q8_0, 1819), (S.T_Q5_0, 1820),
-                                  (S.T_Q5_0, 1817), (S.T_Q5_K, 237)])
+                                  (S.T_Q5_0, 1817), (S.T_Q5_K, 237), (S.T_Q4_1, 1636), (S.T_Q4_0, 1818)])
 def test_widest_q6k_q80_rows(backend, oracle, t, nb):
-    """The widest Q6_K (K = 57344), Q8_0 / Q5_0 (K = 58240) and Q5_K (K = 60672) rows the decode
-    kernels accept, and Q8_0 / Q5_0 widths whose last 4-block step is ragged."""
+    """The widest Q6_K (K = 57344), Q8_0 / Q5_0 / Q4_0 (K = 58240), Q4_1 (K = 52352, its block sums
+    beside the quantized x) and Q5_K (K = 60672) rows the decode kernels accept, and widths whose
+    last 4-block step is ragged."""
     rows, cols = 20, nb * (32 if S.uses_q8(t) else 256)
     w = S.random_bytes_weights(t, rows, cols, 133 + nb)
     x = S.activations(cols, 134)
     tt = backend.upload(t, cols, w)
+    # AUTO keeps the row order here: 20 rows are not a multiple of 8 (repack_tensor, fastgguf.c:2487)
     assert bits_equal(backend.matvec(tt, x), oracle.matvec(t, w, cols, x, O_ROW))
     tt.free()
 
@@ -243,6 +265,9 @@ SILU_CASES = [  # (type, rows, cols, order): split launches (S > 1) and one-wave
     (S.T_Q8_0, 37, 4128, ORDER_ROW),
     (S.T_Q5_K, 40, 2048, ORDER_ROW),
     (S.T_Q5_0, 37, 4128, ORDER_ROW),
+    (S.T_Q4_0, 48, 4128, ORDER_REPACKED),
+    (S.T_Q4_1, 37, 4128, ORDER_ROW),
+    (S.T_IQ4_NL, 37, 4128, ORDER_ROW),
 ]
 
 

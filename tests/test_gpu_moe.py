@@ -68,7 +68,8 @@ def test_moe_q5_matches_golden(backend):
 
 
 @pytest.mark.parametrize("types", [(S.T_Q5_K, S.T_Q5_K, S.T_Q5_K), (S.T_Q4_K, S.T_Q4_K, S.T_Q5_0),
-                                   (S.T_Q5_0, S.T_Q5_0, S.T_Q6_K)])
+                                   (S.T_Q5_0, S.T_Q5_0, S.T_Q6_K), (S.T_Q4_0, S.T_Q4_1, S.T_Q5_1),
+                                   (S.T_IQ4_NL, S.T_IQ4_NL, S.T_Q4_1)])
 def test_moe_mixed_types_match_oracle(backend, oracle, types):
     # ff = 352 (11 blocks of 32, a last step of 3 blocks) where the down projection takes Q8
     # activations; a K-quant down projection needs ff % 256 == 0
