@@ -25,8 +25,9 @@ ACT_Q8, ACT_Q8K = 1, 2
 #: every symbol include/fastgguf_hip.h declares
 EXPORTS = (
     "fgh_open", "fgh_close", "fgh_info", "fgh_last_error", "fgh_upload", "fgh_tensor_free",
-    "fgh_matvec", "fgh_matvec_multi", "fgh_matmul", "fgh_moe_ffn",
+    "fgh_matvec", "fgh_matvec_multi", "fgh_matmul", "fgh_moe_ffn", "fgh_attention",
     "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matvec_silu_dev", "fgh_matmul_dev", "fgh_moe_ffn_dev",
+    "fgh_attention_dev",
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
@@ -81,6 +82,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_matvec_silu_dev": (i32, [vp, vp, vp, vp, vp]),
         "fgh_matmul_dev": (i32, [vp, vp, vp, i32, vp, i32, i32]),
         "fgh_moe_ffn_dev": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, i32]),
+        "fgh_attention": (i32, [vp, i32, i32, i32, i32, vp, vp, vp, vp, i32, i32, vp, vp, C.c_float]),
+        "fgh_attention_dev": (i32, [vp, i32, i32, i32, i32, vp, vp, vp, vp, i32, i32, vp, vp, i32, C.c_float]),
         "fgh_graph_begin": (i32, [vp]),
         "fgh_graph_end": (i32, [vp, C.POINTER(vp)]),
         "fgh_graph_launch": (i32, [vp, vp]),
@@ -436,6 +439,32 @@ class Backend:
                     Y_dev: int, n_tok: int):
         self._check(self.lib.fgh_moe_ffn_dev(self.ctx, gate.handle, up.handle, down.handle, k, logits_dev, X_dev,
                                              Y_dev, n_tok))
+
+    def attention(self, q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, st, en, n_head_kv: int,
+                  scale: float) -> np.ndarray:
+        """attn_rows over every (token, head): q [n_tok][n_head][hd], caches [cap][kv_dim], st / en
+        position ranges per token (slot = position % cap). Returns o shaped like q."""
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        k_cache = np.ascontiguousarray(k_cache, dtype=np.float32)
+        v_cache = np.ascontiguousarray(v_cache, dtype=np.float32)
+        if q.ndim != 3 or k_cache.ndim != 2 or k_cache.shape != v_cache.shape:
+            raise ValueError("attention: q is [n_tok][n_head][hd], caches are [cap][kv_dim]")
+        n_tok, n_head, hd = q.shape
+        st = np.ascontiguousarray(st, dtype=np.int32)
+        en = np.ascontiguousarray(en, dtype=np.int32)
+        if st.shape != (n_tok,) or en.shape != (n_tok,):
+            raise ValueError("attention: st and en hold one position per token")
+        o = np.empty_like(q)
+        self._check(self.lib.fgh_attention(self.ctx, n_tok, n_head, n_head_kv, hd, q.ctypes.data, o.ctypes.data,
+                                           k_cache.ctypes.data, v_cache.ctypes.data, k_cache.shape[1],
+                                           k_cache.shape[0], st.ctypes.data, en.ctypes.data, scale))
+        return o
+
+    def attention_dev(self, n_tok: int, n_head: int, n_head_kv: int, hd: int, q_dev: int, o_dev: int,
+                      k_dev: int, v_dev: int, kv_dim: int, cap: int, st_dev: int, en_dev: int, max_len: int,
+                      scale: float):
+        self._check(self.lib.fgh_attention_dev(self.ctx, n_tok, n_head, n_head_kv, hd, q_dev, o_dev, k_dev, v_dev,
+                                               kv_dim, cap, st_dev, en_dev, max_len, scale))
 
 
 __all__ = ["Backend", "BackendError", "Gguf", "Tensor", "load_library", "EXPORTS", "T_Q4_K", "T_Q5_0", "T_Q5_K", "T_Q6_K", "T_Q8_0",

@@ -32,6 +32,7 @@ struct fgh_ctx {
     // scratch, grown on demand (gpu_grow_buf, fastgguf.c:2083-2091)
     DevBuf x, y, aqs, ad, abs;
     DevBuf gq, gy, gb;  // prompt-GEMM activations (launch_gemm_quant layout)
+    DevBuf as;          // attention scores / weights
     DevBuf msel, mw, mg, mu, md, mlog;  // MoE: selection, weights, gate / up / down outputs
     DevBuf mseg, mslot, mimx, mimh;         // MoE: slots grouped by expert, Q8_K images of x and h
     DevBuf ck;                              // fgh_checksum_dev: per-workgroup partial sums
@@ -251,7 +252,7 @@ void fgh_close(fgh_ctx *c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->gy, &c->gb, &c->msel, &c->mw, &c->mg,
-                      &c->mu, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck})
+                      &c->mu, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck, &c->as})
         if (b->p) (void)hipFree(b->p);
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -488,6 +489,27 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
     return FGH_OK;
 }
 
+int fgh_attention_dev(fgh_ctx *c, int n_tok, int n_head, int n_head_kv, int hd, const float *q, float *o,
+                      const float *k_cache, const float *v_cache, int kv_dim, int cap, const int32_t *st,
+                      const int32_t *en, int max_len, float scale) {
+    if (!c) return FGH_ERR_ARG;
+    if (!q || !o || !k_cache || !v_cache || !st || !en || n_tok < 1 || n_head < 1 || n_head_kv < 1 ||
+        n_head % n_head_kv != 0 || hd < 32 || hd > 256 || hd % 32 != 0 || (int64_t)n_head_kv * hd > kv_dim ||
+        kv_dim % 4 != 0 || cap < 1 || max_len < 1)
+        return fail(c, FGH_ERR_ARG, "attention: bad arguments");
+    if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 != 0)
+        return fail(c, FGH_ERR_ARG, "attention: q and the caches must be 16-byte aligned");
+    if ((n_tok * (n_head / n_head_kv) + 3) / 4 > 65535 || n_head_kv > 65535 || (int64_t)n_tok * n_head > INT32_MAX / 2)
+        return fail(c, FGH_ERR_ARG, "attention: too many rows");
+    HIP_TRY(c, hipSetDevice(c->device));
+    int rc;
+    if ((rc = grow(c, c->as, (size_t)n_tok * n_head * max_len * 4))) return rc;
+    fgh::AttnArgs a{q, o, k_cache, v_cache, (float *)c->as.p, st, en, n_head, n_head_kv, hd, kv_dim, cap, max_len,
+                    scale};
+    HIP_TRY(c, fgh::launch_attention(a, n_tok, c->stream));
+    return FGH_OK;
+}
+
 // ---- host-pointer entry points (synchronous) ----
 
 int fgh_matvec_multi(fgh_ctx *c, int n, const fgh_tensor *const *t, const float *x, float *const *y) {
@@ -536,6 +558,47 @@ int fgh_matmul(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, float *
     HIP_TRY(c, hipMemcpy2DAsync(Y, (size_t)ldy * 4, c->y.p, (size_t)nout * 4, (size_t)nout * 4, nb,
                                 hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return FGH_OK;
+}
+
+int fgh_attention(fgh_ctx *c, int n_tok, int n_head, int n_head_kv, int hd, const float *q, float *o,
+                  const float *k_cache, const float *v_cache, int kv_dim, int cap, const int32_t *st, const int32_t *en,
+                  float scale) {
+    if (!c) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
+    if (!q || !o || !k_cache || !v_cache || !st || !en || n_tok < 1 || n_head < 1 || cap < 1 || kv_dim < 1)
+        return fail(c, FGH_ERR_ARG, "attention: bad arguments");
+    int max_len = 1;
+    for (int t = 0; t < n_tok; t++) {
+        const int n = en[t] - st[t] + 1;
+        if (n < 1 || n > cap) return fail(c, FGH_ERR_ARG, "attention: token %d range %d..%d", t, st[t], en[t]);
+        max_len = std::max(max_len, n);
+    }
+    HIP_TRY(c, hipSetDevice(c->device));
+    const size_t nq = (size_t)n_tok * n_head * hd * 4, nc = (size_t)cap * kv_dim * 4, nr = (size_t)n_tok * 4;
+    void *dq = nullptr, *dk = nullptr, *dv = nullptr, *dr = nullptr;
+    int rc = FGH_OK;
+    hipError_t e = hipMalloc(&dq, 2 * nq);
+    if (e == hipSuccess) e = hipMalloc(&dk, nc);
+    if (e == hipSuccess) e = hipMalloc(&dv, nc);
+    if (e == hipSuccess) e = hipMalloc(&dr, 2 * nr);
+    if (e == hipSuccess) e = hipMemcpyAsync(dq, q, nq, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dk, k_cache, nc, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dv, v_cache, nc, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dr, st, nr, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync((char *)dr + nr, en, nr, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        rc = fgh_attention_dev(c, n_tok, n_head, n_head_kv, hd, (const float *)dq, (float *)((char *)dq + nq),
+                               (const float *)dk, (const float *)dv, kv_dim, cap, (const int32_t *)dr,
+                               (const int32_t *)((char *)dr + nr), max_len, scale);
+        if (rc == FGH_OK) e = hipMemcpyAsync(o, (char *)dq + nq, nq, hipMemcpyDeviceToHost, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    }
+    (void)hipStreamSynchronize(c->stream);
+    for (void *p : {dq, dk, dv, dr})
+        if (p) (void)hipFree(p);
+    if (rc) return rc;
+    if (e != hipSuccess) return fail(c, FGH_ERR_DEVICE, "attention: %s", hipGetErrorString(e));
     return FGH_OK;
 }
 

@@ -277,6 +277,18 @@ hipError_t launch_q4_image(const float *x, const float *u, int64_t ldx, int nb, 
 hipError_t launch_moe_combine(const float *d, const float *w, float *y, int n_embd, int k, int n_tok, int64_t ldy,
                               hipStream_t s);
 
+// attention over an fp32 KV ring cache (fgh_attn.hip): rows (token, head), row t * n_head + h
+struct AttnArgs {
+    const float *q;           // [rows][hd]
+    float *o;                 // [rows][hd]
+    const float *k, *v;       // [cap][kv_dim] ring caches (slot = position % cap)
+    float *s;                 // [rows][max_len] scores, then weights
+    const int32_t *st, *en;   // [tokens] position ranges
+    int n_head, n_head_kv, hd, kv_dim, cap, max_len;
+    float scale;
+};
+hipError_t launch_attention(const AttnArgs &a, int n_tok, hipStream_t s);
+
 // prompt-batch Q4_K GEMM (fgh_gemm.hip): 1..64 tokens, weights in the Q4_K decode layout
 struct GemmArgs {
     const uint8_t *W;   // Q4_K tensor (tile layout)

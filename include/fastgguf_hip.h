@@ -166,6 +166,20 @@ FGH_API int fgh_moe_ffn(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tensor *
                 int k, const float *logits, const float *X, float *Y, int n_tok,
                 int32_t *sel_out, float *w_out);
 
+/* ---- attention: replaces attn_rows (fastgguf.c:3273-3326), its vector path (hd % 32 == 0) ----
+ * Rows are (token, head) pairs, row t * n_head + h: q and o are [n_tok][n_head][hd]; the K and V
+ * caches are rings of cap rows of kv_dim floats (position p in row p % cap), head h reading the
+ * cache columns (h / (n_head / n_head_kv)) * hd .. + hd (the GQA grouping of forward, 4770-4790).
+ * Token t attends to positions st[t]..en[t] (1 <= en - st + 1 <= cap). Every output equals the
+ * reference's bit for bit: scores as att_qk_kern's lane chains and hsum4_ps (3227-3246), softmax
+ * as softmax_vec (3194-3219, exp_neg_ps 3168-3184 on whole groups of 8, libm expf on the tail),
+ * value sums as att_v_kern's chain over the positions in order (3249-3270). scale is the
+ * reference's 1/sqrt(hd). Requires hd % 32 == 0 and hd <= 256, n_head % n_head_kv == 0,
+ * n_head_kv * hd <= kv_dim, kv_dim % 4 == 0 (device pointers 16-byte aligned). */
+FGH_API int fgh_attention(fgh_ctx *ctx, int n_tok, int n_head, int n_head_kv, int hd, const float *q, float *o,
+                  const float *k_cache, const float *v_cache, int kv_dim, int cap, const int32_t *st,
+                  const int32_t *en, float scale);
+
 /* ---- device-resident variants: device pointers, asynchronous on the context stream ----
  * These skip the host<->device copies of the synchronous calls above (the copies fastgguf.c
  * makes at 2102 and 2110), for callers that keep activations in device memory. */
@@ -184,6 +198,13 @@ FGH_API int fgh_matmul_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *X_dev
 FGH_API int fgh_moe_ffn_dev(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tensor *up,
                     const fgh_tensor *down, int k, const float *logits_dev, const float *X_dev,
                     float *Y_dev, int n_tok);
+/* fgh_attention on device pointers (st_dev, en_dev: int32 [n_tok] in device memory). max_len
+ * bounds every row's length en - st + 1 (it sizes the score buffer): a row whose range is empty,
+ * longer than cap or than max_len gets NaN outputs, not an error, since the ranges stay on the
+ * device. */
+FGH_API int fgh_attention_dev(fgh_ctx *ctx, int n_tok, int n_head, int n_head_kv, int hd, const float *q_dev,
+                      float *o_dev, const float *k_cache_dev, const float *v_cache_dev, int kv_dim, int cap,
+                      const int32_t *st_dev, const int32_t *en_dev, int max_len, float scale);
 
 /* ---- HIP graphs of device-resident calls (launch-bound decode loops) ----
  * fgh_graph_begin starts capturing the context stream; the *_dev calls that follow are recorded,

@@ -925,3 +925,92 @@ int fgo_moe_ffn(uint32_t type_gate, uint32_t type_up, uint32_t type_down,
     free(sel); free(w); free(h);
     return rc;
 }
+
+/* ---- B-10: attention, attn_rows (fastgguf.c:3273-3326), its vector path (hd % 32 == 0) ----
+ * Per query row, over positions st..en of the ring cache (slot p % cap, head offset kvo):
+ *   score_p = scale * (((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7))), a_l = fma chain over
+ *            m of q[8m + l] * k_p[8m + l]   (att_qk_kern 3227-3246 with hsum4_ps 3187-3190)
+ *   softmax_vec (3194-3219): max; e = exp_neg_ps(s - max) over whole groups of 8 (lane l of the
+ *            8-wide sum takes e[8g + l] in order), hsum8 of the lanes, then the tail with libm
+ *            expf added in order; every value times 1 / sum
+ *   o[c] = fma chain over the positions in order of w_p * v_p[c]   (att_v_kern 3249-3270)
+ * A row of several rows' call sees zeros outside its own range, fma(0, v, acc) = acc: the
+ * result is the row's own range's. */
+static float exp_neg(float x) { /* exp_neg_ps (3168-3184), one lane */
+    int keep = x > -87.0f;
+    x = x > -87.0f ? x : -87.0f; /* max_ps(x, -87): -87 for a NaN */
+    float fx = floorf(fmaf(x, 1.44269504088896341f, 0.5f));
+    x = fmaf(-fx, 0.693359375f, x);
+    x = fmaf(-fx, -2.12194440e-4f, x);
+    float y = 1.9875691500E-4f;
+    y = fmaf(y, x, 1.3981999507E-3f);
+    y = fmaf(y, x, 8.3334519073E-3f);
+    y = fmaf(y, x, 4.1665795894E-2f);
+    y = fmaf(y, x, 1.6666665459E-1f);
+    y = fmaf(y, x, 5.0000001201E-1f);
+    float xx = x * x, x1 = x + 1.0f;
+    y = fmaf(y, xx, x1);
+    uint32_t eb = (uint32_t)((int32_t)fx + 127) << 23;
+    float e;
+    memcpy(&e, &eb, 4);
+    float r = y * e;
+    return keep ? r : 0.0f;
+}
+
+float fgo_exp_neg(float x) { return exp_neg(x); }
+
+static void softmax_vec_row(float *s, int n) {
+    float mx = -INFINITY;
+    for (int i = 0; i < n; i++) if (s[i] > mx) mx = s[i];
+    float vs[8] = {0};
+    int i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) {
+            s[i + l] = exp_neg(s[i + l] - mx);
+            vs[l] += s[i + l];
+        }
+    float sum = hsum8(vs);
+#if FGO_MUTATE == 11 /* the tail through exp_neg_ps instead of libm's expf */
+    for (; i < n; i++) { s[i] = exp_neg(s[i] - mx); sum += s[i]; }
+#else
+    for (; i < n; i++) { s[i] = expf(s[i] - mx); sum += s[i]; }
+#endif
+    if (sum > 0.0f) {
+        float inv = 1.0f / sum;
+        for (int j = 0; j < n; j++) s[j] = s[j] * inv;
+    }
+}
+
+int fgo_attn_rows(int nr, const float *q, float *o, const int *st, const int *en, const float *ck, const float *cv,
+                  int kv_dim, const int *kvo, int cap, int hd, float scale) {
+    if (hd % 32 != 0 || hd <= 0) return -1;
+    for (int r = 0; r < nr; r++) {
+        int n = en[r] - st[r] + 1;
+        if (n < 1 || n > cap) return -1;
+        float *s = (float *)malloc((size_t)n * sizeof(float));
+        if (!s) return -1;
+        const float *qr = q + (size_t)r * hd;
+        for (int p = st[r]; p <= en[r]; p++) {
+            const float *k = ck + (size_t)(p % cap) * kv_dim + kvo[r];
+            float a[8] = {0};
+            for (int m = 0; m < hd / 8; m++)
+                for (int l = 0; l < 8; l++) a[l] = fmaf(qr[8 * m + l], k[8 * m + l], a[l]);
+#if FGO_MUTATE == 10 /* the 8 score lanes added in sequence instead of hsum4_ps's tree */
+            float t = a[0];
+            for (int l = 1; l < 8; l++) t += a[l];
+#else
+            float t = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+#endif
+            s[p - st[r]] = t * scale;
+        }
+        softmax_vec_row(s, n);
+        float *orow = o + (size_t)r * hd;
+        for (int c = 0; c < hd; c++) {
+            float acc = 0.0f;
+            for (int p = st[r]; p <= en[r]; p++) acc = fmaf(s[p - st[r]], cv[(size_t)(p % cap) * kv_dim + kvo[r] + c], acc);
+            orow[c] = acc;
+        }
+        free(s);
+    }
+    return 0;
+}

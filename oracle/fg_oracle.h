@@ -84,6 +84,14 @@ int fgo_moe_ffn(uint32_t type_gate, uint32_t type_up, uint32_t type_down,
 int fgo_moe_down(uint32_t type_down, const uint8_t *down, int n_embd, int ff, int k,
                  const int32_t *sel, const float *w, const float *h, float *out);
 
+/* attention over an fp32 ring cache, attn_rows (fastgguf.c:3273-3326) restated row by row: row r
+ * (q + r*hd -> o + r*hd) over positions st[r]..en[r] (slot p % cap) of the cache rows of kv_dim
+ * floats at offset kvo[r]; hd % 32 == 0 (the reference's vector path). fgo_exp_neg is its
+ * exp_neg_ps (3168-3184) on one value. */
+int fgo_attn_rows(int nr, const float *q, float *o, const int *st, const int *en, const float *ck, const float *cv,
+                  int kv_dim, const int *kvo, int cap, int hd, float scale);
+float fgo_exp_neg(float x);
+
 /* reference order for the router: softmax (3147), top-k by argmax (3328), renormalise (4603) */
 void fgo_moe_route(const float *logits, int n_expert, int k, int32_t *sel, float *w);
 

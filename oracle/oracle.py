@@ -71,6 +71,9 @@ class Oracle:
         L.fgo_expf_compare.argtypes = [C.c_float, C.c_float, C.c_uint32, C.POINTER(C.c_uint64), C.POINTER(C.c_int)]
         L.fgo_expf_compare.restype = C.c_uint64
         L.fgo_dequantize_row.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
+        L.fgo_attn_rows.argtypes = [C.c_int] + [C.c_void_p] * 6 + [C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_float]
+        L.fgo_exp_neg.argtypes = [C.c_float]
+        L.fgo_exp_neg.restype = C.c_float
 
     # -- quantizers
     def quantize_q8(self, x: np.ndarray) -> np.ndarray:
@@ -155,6 +158,10 @@ class Oracle:
     def silu(self, x: float) -> float:
         return self.lib.fgo_silu(x)
 
+    def exp_neg(self, x: float) -> float:
+        """exp_neg_ps (fastgguf.c:3168-3184) on one value."""
+        return float(self.lib.fgo_exp_neg(float(x)))
+
     def expf(self, x: float) -> float:
         return self.lib.fgo_expf_restated(x)
 
@@ -186,6 +193,19 @@ class Oracle:
         if rc != 0:
             raise ValueError("fgo_moe_ffn failed")
         return (Y, sel, w, h) if want_h else (Y, sel, w)
+
+    def attn_rows(self, q, st, en, ck, cv, kvo, hd, scale):
+        """attn_rows restated: q [nr][hd] rows over positions st[r]..en[r] of the ring caches ck / cv
+        [cap][kv_dim] at head offsets kvo[r]; returns o [nr][hd]."""
+        q = np.ascontiguousarray(q, np.float32).reshape(-1, hd)
+        ck = np.ascontiguousarray(ck, np.float32)
+        cv = np.ascontiguousarray(cv, np.float32)
+        st, en, kvo = (np.ascontiguousarray(a, np.int32) for a in (st, en, kvo))
+        o = np.zeros_like(q)
+        if self.lib.fgo_attn_rows(q.shape[0], _ptr(q), _ptr(o), _ptr(st), _ptr(en), _ptr(ck), _ptr(cv), ck.shape[1],
+                                  _ptr(kvo), ck.shape[0], hd, scale) != 0:
+            raise ValueError("fgo_attn_rows failed")
+        return o
 
     def moe_down(self, type_down, down, n_embd, ff, sel, w, h):
         sel = np.ascontiguousarray(sel, np.int32)
@@ -242,6 +262,7 @@ class Reference:
         L.fgr_tensor_free.argtypes = [C.c_void_p]
         L.fgr_tensor_free.restype = None
         L.fgr_tensor_matvec_multi.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.fgr_attn_rows.argtypes = [C.c_int] + [C.c_void_p] * 6 + [C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
         L.fgr_gguf_table.argtypes = [C.c_char_p] + [C.c_void_p] * 10 + [C.c_int64, C.c_char_p, C.c_int, C.c_void_p]
         L.fgr_init(256)
 
@@ -304,6 +325,18 @@ class Reference:
         yp = (C.c_void_p * len(ys))(*[y.ctypes.data for y in ys])
         if self.lib.fgr_tensor_matvec_multi(len(hs), arr, _ptr(x), yp) != 0:
             raise ValueError("fgr_tensor_matvec_multi failed")
+
+    def attn_rows(self, q, st, en, ck, cv, kvo, hd, scale):
+        """The reference's attn_rows on up to 4 rows sharing the head offset kvo."""
+        q = np.ascontiguousarray(q, np.float32).reshape(-1, hd)
+        ck = np.ascontiguousarray(ck, np.float32)
+        cv = np.ascontiguousarray(cv, np.float32)
+        st, en = (np.ascontiguousarray(a, np.int32) for a in (st, en))
+        o = np.zeros_like(q)
+        if self.lib.fgr_attn_rows(q.shape[0], _ptr(q), _ptr(o), _ptr(st), _ptr(en), _ptr(ck), _ptr(cv), ck.shape[1],
+                                  int(kvo), ck.shape[0], hd, scale) != 0:
+            raise ValueError("fgr_attn_rows failed")
+        return o
 
     def gguf_table(self, path, keys, cap=64):
         """gguf_open on a file: its summary, tensor table and kv_num(key, -1) answers, or None if the

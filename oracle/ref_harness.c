@@ -208,3 +208,20 @@ FGR_EXPORT int fgr_gguf_table(const char *path, uint32_t *version, uint64_t *ali
     mmap_close(&g.map);
     return 0;
 }
+
+/* attn_rows (3273-3326) for nr <= 4 query rows sharing one KV head: q [nr][hd], o [nr][hd] */
+FGR_EXPORT int fgr_attn_rows(int nr, const float *q, float *o, const int *st, const int *en, const float *ck,
+                             const float *cv, int kv_dim, int kvo, int cap, int hd, float scale) {
+    if (nr < 1 || nr > 4) return -1;
+    int lo = st[0], hi = en[0];
+    for (int r = 1; r < nr; r++) { if (st[r] < lo) lo = st[r]; if (en[r] > hi) hi = en[r]; }
+    int sld = hi - lo + 1 + 8;
+    float *sb = (float *)calloc((size_t)4 * sld, sizeof(float));
+    if (!sb) return -1;
+    const float *qr[4];
+    float *orow[4];
+    for (int r = 0; r < nr; r++) { qr[r] = q + (size_t)r * hd; orow[r] = o + (size_t)r * hd; }
+    attn_rows(nr, qr, orow, st, en, ck, cv, kv_dim, kvo, cap, hd, scale, sb, sld);
+    free(sb);
+    return 0;
+}

@@ -50,6 +50,35 @@ def quant_inputs() -> np.ndarray:
     return x
 
 
+#: (hd, kv_dim, kvo, cap, st, en, q magnitude): one position, a tail of 7, whole groups of 8 plus
+#: tails, causal prefill rows over a wrapped ring, a full cache, hd 32 .. 256, and scores spread
+#: past exp_neg_ps's -87 cut-off
+ATTN_CASES = [
+    (32, 64, 32, 40, [0], [0], 1.0),
+    (64, 128, 0, 40, [3], [9], 1.0),
+    (64, 128, 64, 40, [30, 30, 30, 30], [45, 46, 47, 48], 1.0),
+    (128, 128, 0, 64, [50, 52, 10, 37], [100, 101, 73, 100], 1.0),
+    (256, 256, 0, 24, [5, 7], [28, 20], 1.0),
+    (32, 32, 0, 40, [2], [34], 30.0),
+]
+
+
+def attn_cases(ref) -> dict:
+    rng = np.random.default_rng(77)
+    out = {}
+    for i, (hd, kv_dim, kvo, cap, st, en, mag) in enumerate(ATTN_CASES):
+        q = (rng.standard_normal((len(st), hd)) * mag).astype(np.float32)
+        ck = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+        cv = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+        scale = np.float32(1.0 / np.sqrt(hd))
+        o = ref.attn_rows(q, st, en, ck, cv, kvo, hd, float(scale))
+        out.update({f"c{i}_q": q, f"c{i}_ck": ck, f"c{i}_cv": cv, f"c{i}_st": np.array(st, np.int32),
+                    f"c{i}_en": np.array(en, np.int32), f"c{i}_o": o,
+                    f"c{i}_meta": np.array([hd, kvo], np.int32), f"c{i}_scale": np.array([scale], np.float32)})
+    out["n_cases"] = np.array([len(ATTN_CASES)], np.int32)
+    return out
+
+
 def main() -> None:
     ref = Reference("vnni")
     print("reference build:", ref.build, "threads:", ref.threads())
@@ -140,6 +169,8 @@ def main() -> None:
         os.remove(vp)
     np.savez_compressed(os.path.join(HERE, "gguf.npz"), **tab, variant_names=np.array(list(rcs)),
                         variant_rc=np.array(list(rcs.values()), np.int32))
+    # attention: the reference's attn_rows on up to 4 rows sharing one head offset, over ring caches
+    np.savez_compressed(os.path.join(HERE, "attn.npz"), **attn_cases(ref))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz") or f.endswith(".gguf"):
             print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

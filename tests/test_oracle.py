@@ -17,7 +17,7 @@ import pytest
 from conftest import ROOT, bits_equal, golden, rel_err
 
 from fastgguf_amd import synth as S
-from oracle import ORDER_REPACKED, ORDER_ROW, Oracle
+from oracle import ORDER_REPACKED, ORDER_ROW, Oracle, Reference
 
 TYPES = {"q8_0": S.T_Q8_0, "q4_k": S.T_Q4_K, "q6_k": S.T_Q6_K, "q5_0": S.T_Q5_0, "q5_k": S.T_Q5_K,
          "q4_0": S.T_Q4_0, "q4_1": S.T_Q4_1, "q5_1": S.T_Q5_1, "iq4_nl": S.T_IQ4_NL}
@@ -269,7 +269,8 @@ def test_selftest_relations(oracle, t):
 MUTANTS = {1: "hsum8 order", 2: "MoE accumulate without fma", 3: "reciprocal instead of division",
            4: "Q6_K half-lane scale", 5: "Q4_K repacked single chain", 6: "Q4_K GEMM integer epilogue",
            7: "Q5_0 fifth bit from the wrong half of qh", 8: "Q5_K qh bit pairing",
-           9: "Q4_1 / Q5_1 min term without the fused multiply-add"}
+           9: "Q4_1 / Q5_1 min term without the fused multiply-add",
+           10: "attention score lanes added in sequence", 11: "softmax tail through exp_neg_ps"}
 
 
 @pytest.fixture(scope="module")
@@ -303,7 +304,84 @@ def _golden_failures(o: Oracle) -> int:
     Y, _, _ = o.moe_ffn(tuple(int(v) for v in g["types"]), g["gate"], g["up"], g["down"], E, K, D, F,
                         g["logits"], g["X"])
     fails += not bits_equal(Y, g["Y"])
+    for c in attn_golden():
+        fails += not bits_equal(o.attn_rows(c["q"], c["st"], c["en"], c["ck"], c["cv"], [c["kvo"]] * len(c["st"]),
+                                            c["hd"], c["scale"]), c["o"])
     return fails
+
+
+def attn_golden() -> list[dict]:
+    g = golden("attn.npz")
+    out = []
+    for i in range(int(g["n_cases"][0])):
+        hd, kvo = (int(v) for v in g[f"c{i}_meta"])
+        out.append(dict(q=g[f"c{i}_q"], ck=g[f"c{i}_ck"], cv=g[f"c{i}_cv"], st=g[f"c{i}_st"], en=g[f"c{i}_en"],
+                        o=g[f"c{i}_o"], hd=hd, kvo=kvo, scale=float(g[f"c{i}_scale"][0])))
+    return out
+
+
+def test_attention_golden(oracle):
+    """attn_rows restated, bit for bit against the compiled reference's outputs."""
+    for c in attn_golden():
+        o = oracle.attn_rows(c["q"], c["st"], c["en"], c["ck"], c["cv"], [c["kvo"]] * len(c["st"]), c["hd"],
+                             c["scale"])
+        assert bits_equal(o, c["o"])
+
+
+def test_exp_neg_against_the_mathematics(oracle):
+    """exp_neg_ps restated: exactly 1 at 0, exactly 0 at and below -87, within 3e-7 relative of
+    e^x (float64) over (-87, 0], and never above 1."""
+    x = np.concatenate([-np.logspace(-8, np.log10(86.999), 20000), -np.linspace(0, 86.99, 20000)]).astype(np.float32)
+    e = np.array([oracle.exp_neg(v) for v in x[::7]], np.float64)
+    ref = np.exp(x[::7].astype(np.float64))
+    assert np.max(np.abs(e - ref) / ref) < 3e-7
+    assert oracle.exp_neg(0.0) == 1.0 and oracle.exp_neg(-87.0) == 0.0 and oracle.exp_neg(-1000.0) == 0.0
+    assert np.all(e <= 1.0)
+
+
+def test_attention_against_float64(oracle):
+    """The restated attention is softmax(q k^T * scale) v within fp32 rounding (float64 math),
+    per row, with GQA head offsets and ring wrap."""
+    rng = np.random.default_rng(5)
+    hd, kv_dim, cap = 64, 256, 50
+    ck = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+    cv = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+    q = rng.standard_normal((6, hd)).astype(np.float32)
+    st, en, kvo = [0, 10, 40, 45, 3, 20], [0, 17, 70, 94, 52, 20], [0, 64, 128, 192, 64, 0]
+    o = oracle.attn_rows(q, st, en, ck, cv, kvo, hd, 0.125)
+    for r in range(6):
+        pos = np.arange(st[r], en[r] + 1) % cap
+        k = ck[pos, kvo[r]:kvo[r] + hd].astype(np.float64)
+        v = cv[pos, kvo[r]:kvo[r] + hd].astype(np.float64)
+        s = k @ q[r].astype(np.float64) * 0.125
+        w = np.exp(s - s.max())
+        ref = (w / w.sum()) @ v
+        assert np.max(np.abs(o[r] - ref)) < 1e-5 * max(1.0, np.abs(ref).max())
+
+
+def test_attention_matches_compiled_reference(oracle):
+    """Random cases against the compiled reference (where it is built): 4-row calls sharing a
+    head offset, ranges of every length mod 8, ring wrap, hd 32 .. 256."""
+    try:
+        ref = Reference()
+    except (OSError, FileNotFoundError):
+        pytest.skip("reference build absent")
+    rng = np.random.default_rng(9)
+    for case in range(24):
+        hd = int(rng.choice([32, 64, 96, 128, 256]))
+        cap = int(rng.integers(8, 80))
+        kv_dim = hd * int(rng.integers(1, 3))
+        kvo = int(rng.integers(0, kv_dim // hd)) * hd
+        nr = int(rng.integers(1, 5))
+        st = rng.integers(0, 200, nr)
+        en = st + rng.integers(0, cap, nr)
+        ck = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+        cv = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+        q = (rng.standard_normal((nr, hd)) * (1 + 10 * (case % 3 == 2))).astype(np.float32)
+        scale = float(np.float32(1 / np.sqrt(hd)))
+        a = ref.attn_rows(q, st, en, ck, cv, kvo, hd, scale)
+        b = oracle.attn_rows(q, st, en, ck, cv, [kvo] * nr, hd, scale)
+        assert bits_equal(a, b), (case, hd, cap, st, en)
 
 
 @pytest.mark.parametrize("mutant", sorted(MUTANTS))
