@@ -54,16 +54,16 @@ __device__ __forceinline__ int row_len(const AttnArgs &a, int tok) {
 }
 __device__ __forceinline__ int64_t kv_slot(int p, int cap) { return (int64_t)(((p % cap) + cap) % cap); }
 
-// A group is 4 rows that read the same K / V head kh: group q of head kh holds j = 4q .. 4q + 3 of
-// the head's n_tok * G rows, j = t * G + g (token t, query head kh * G + g). The scores and the
+// A group is R rows that read the same K / V head kh: group q of head kh holds j = R q .. R q + R - 1
+// of the head's n_tok * G rows, j = t * G + g (token t, query head kh * G + g). The scores and the
 // value sums of a group run over the union lo..hi of its rows' ranges, as attn_rows runs its 4-row
 // calls; a position outside a row's own range has weight 0, and fma(0, v, acc) = acc, so every
 // row's sums are those of its own range.
 struct GroupRow {
     int row, st, en;  // row = -1: no such row; en < st: no valid range
 };
-__device__ __forceinline__ GroupRow group_row(const AttnArgs &a, int n_tok, int grp, int kh, int r) {
-    const int G = a.n_head / a.n_head_kv, j = grp * 4 + r;
+__device__ __forceinline__ GroupRow group_row(const AttnArgs &a, int n_tok, int R, int grp, int kh, int r) {
+    const int G = a.n_head / a.n_head_kv, j = grp * R + r;
     GroupRow g{-1, 0, -1};
     if (j < n_tok * G) {
         const int t = j / G;
@@ -75,11 +75,11 @@ __device__ __forceinline__ GroupRow group_row(const AttnArgs &a, int n_tok, int 
     }
     return g;
 }
-__device__ __forceinline__ bool group_span(const AttnArgs &a, int n_tok, int grp, int kh, int &lo, int &hi) {
+__device__ __forceinline__ bool group_span(const AttnArgs &a, int n_tok, int R, int grp, int kh, int &lo, int &hi) {
     lo = 0x7fffffff;
     hi = -0x7fffffff;
-    for (int r = 0; r < 4; ++r) {
-        const GroupRow g = group_row(a, n_tok, grp, kh, r);
+    for (int r = 0; r < R; ++r) {
+        const GroupRow g = group_row(a, n_tok, R, grp, kh, r);
         if (g.en >= g.st) {
             lo = min(lo, g.st);
             hi = max(hi, g.en);
@@ -88,37 +88,36 @@ __device__ __forceinline__ bool group_span(const AttnArgs &a, int n_tok, int grp
     return hi >= lo;
 }
 
-// scores: grid (key blocks, groups, K heads), 256 threads; thread = one key of the union for the
-// group's 4 rows, 8 lane chains per row over the head's values (2 x float4 of K per step), the q
-// rows from LDS (one address for the whole wavefront: a broadcast read)
+// scores: grid (key blocks, groups of R rows, K heads), 256 threads; thread = one key of the union
+// for the group's R rows, 8 lane chains per row over the head's values (2 x float4 of K per step),
+// the q rows from LDS (one address for the whole wavefront: a broadcast read). R = 16 for prompt
+// batches: each K row loaded serves 16 rows.
+template <int R>
 __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a, int n_tok) {
-    __shared__ float4 qs[4][64];
+    __shared__ float4 qs[R][64];
     const int grp = blockIdx.y, kh = blockIdx.z, tid = threadIdx.x;
     int lo, hi;
-    if (!group_span(a, n_tok, grp, kh, lo, hi)) return;
-    GroupRow gr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) gr[r] = group_row(a, n_tok, grp, kh, r);
+    if (!group_span(a, n_tok, R, grp, kh, lo, hi)) return;
     const int h4 = a.hd / 4;
-    for (int i = tid; i < 4 * h4; i += 256) {
+    for (int i = tid; i < R * h4; i += 256) {
         const int r = i / h4, x = i - r * h4;
-        const GroupRow g = group_row(a, n_tok, grp, kh, r);
+        const GroupRow g = group_row(a, n_tok, R, grp, kh, r);
         qs[r][x] = g.en >= g.st ? ((const float4 *)(a.q + (size_t)g.row * a.hd))[x] : make_float4(0, 0, 0, 0);
     }
     __syncthreads();
     const int64_t kvo = (int64_t)kh * a.hd;
     for (int p = lo + (int)blockIdx.x * 256 + tid; p <= hi; p += (int)gridDim.x * 256) {
         const float4 *kp = (const float4 *)(a.k + kv_slot(p, a.cap) * a.kv_dim + kvo);
-        float acc[4][8];
+        float acc[R][8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int l = 0; l < 8; ++l) acc[r][l] = 0.0f;
-#pragma unroll 4
+#pragma unroll(R == 4 ? 4 : 1)
         for (int m = 0; m < a.hd / 8; ++m) {
             const float4 k0 = kp[2 * m], k1 = kp[2 * m + 1];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+            for (int r = 0; r < R; ++r) {
                 const float4 q0 = qs[r][2 * m], q1 = qs[r][2 * m + 1];
                 acc[r][0] = __builtin_fmaf(q0.x, k0.x, acc[r][0]);
                 acc[r][1] = __builtin_fmaf(q0.y, k0.y, acc[r][1]);
@@ -131,37 +130,83 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a, int n_tok)
             }
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if (p >= gr[r].st && p <= gr[r].en) {
+        for (int r = 0; r < R; ++r) {
+            const GroupRow g = group_row(a, n_tok, R, grp, kh, r);
+            if (p >= g.st && p <= g.en) {
                 const float t = ((acc[r][0] + acc[r][1]) + (acc[r][2] + acc[r][3])) +
                                 ((acc[r][4] + acc[r][5]) + (acc[r][6] + acc[r][7]));
-                a.s[(size_t)gr[r].row * a.max_len + (p - gr[r].st)] = t * a.scale;
+                a.s[(size_t)g.row * a.max_len + (p - g.st)] = t * a.scale;
             }
         }
     }
 }
 
-// softmax: one workgroup per row, in place over the row's scores, the exponentials staged in LDS
-// 4096 at a time; lanes 0..7 of wavefront 0 carry the 8 ordered sums across the chunks
-constexpr int SM_CHUNK = 4096;
+// softmax: one workgroup per row, in place over the row's scores. A row of up to SM_RES positions
+// stays in LDS from its one load to its one store: maximum, exponentials, lanes 0..7 of
+// wavefront 0 running the 8 ordered sums, then every value times 1 / sum. Longer rows go
+// through LDS SM_RES positions at a time, the 8 sums carried across the chunks.
+constexpr int SM_RES = 12288;
+__device__ __forceinline__ float sum8_tree(float v) {  // lanes 0..7: hsum_ps's tree
+    v = v + __shfl_xor(v, 4, 8);                       // (v0 + v4), (v1 + v5), ...
+    v = v + __shfl_xor(v, 1, 8);
+    return v + __shfl_xor(v, 2, 8);  // ((v0 + v4) + (v1 + v5)) + ((v2 + v6) + (v3 + v7))
+}
+__device__ __forceinline__ float lane_sum(const float *e, int ng, int l, float v) {  // v += e[8g + l], g < ng
+    int g = 0;
+    for (; g + 8 <= ng; g += 8) {
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = e[8 * (g + u) + l];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v += t[u];
+    }
+    for (; g < ng; ++g) v += e[8 * g + l];
+    return v;
+}
 __global__ __launch_bounds__(256) void attn_softmax_kernel(AttnArgs a) {
-    __shared__ float e[SM_CHUNK];
+    __shared__ float e[SM_RES];
     __shared__ float red[4];
     __shared__ float total;
     const int row = blockIdx.x, tok = row / a.n_head, tid = threadIdx.x;
     const int n = row_len(a, tok);
     if (n == 0) return;
     float *s = a.s + (size_t)row * a.max_len;
+    const int nv = n & ~7;  // whole groups of 8
+    const bool resident = n <= SM_RES;
     float mx = -__builtin_inff();
-    for (int i = tid; i < n; i += 256) mx = fmaxf(mx, s[i]);
+    if (resident) {
+#pragma unroll 8
+        for (int i = tid; i < n; i += 256) {
+            const float x = s[i];
+            e[i] = x;
+            mx = fmaxf(mx, x);
+        }
+    } else {
+        for (int i = tid; i < n; i += 256) mx = fmaxf(mx, s[i]);
+    }
     for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const int nv = n & ~7;  // whole groups of 8
+    if (resident) {
+        for (int i = tid; i < n; i += 256) e[i] = i < nv ? exp_neg_ref(e[i] - mx) : expf_ref(e[i] - mx);
+        __syncthreads();
+        if (tid < 8) {
+            float v = sum8_tree(lane_sum(e, nv / 8, tid, 0.0f));
+            if (tid == 0) {
+                for (int i = nv; i < n; ++i) v += e[i];  // the tail, in order
+                total = v;
+            }
+        }
+        __syncthreads();
+        const float sum = total;
+        const float inv = 1.0f / sum;
+        for (int i = tid; i < n; i += 256) s[i] = sum > 0.0f ? e[i] * inv : e[i];
+        return;
+    }
     float v = 0.0f;
-    for (int c0 = 0; c0 < n; c0 += SM_CHUNK) {
-        const int cn = min(SM_CHUNK, n - c0);
+    for (int c0 = 0; c0 < n; c0 += SM_RES) {
+        const int cn = min(SM_RES, n - c0);
         for (int i = tid; i < cn; i += 256) {
             const float x = s[c0 + i] - mx;
             const float ev = c0 + i < nv ? exp_neg_ref(x) : expf_ref(x);
@@ -170,20 +215,9 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(AttnArgs a) {
         }
         __syncthreads();
         if (tid < 8) {
-            const int ng = (min(c0 + cn, nv) - c0) / 8;
-            int g = 0;
-            for (; g + 8 <= ng; g += 8) {
-                float t[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) t[u] = e[8 * (g + u) + tid];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) v += t[u];
-            }
-            for (; g < ng; ++g) v += e[8 * g + tid];
+            v = lane_sum(e, (min(c0 + cn, nv) - c0) / 8, tid, v);
             if (c0 + cn == n) {  // the last chunk holds the tail
-                v = v + __shfl_xor(v, 4, 8);  // (v0 + v4), (v1 + v5), ...
-                v = v + __shfl_xor(v, 1, 8);
-                v = v + __shfl_xor(v, 2, 8);  // ((v0 + v4) + (v1 + v5)) + ((v2 + v6) + (v3 + v7))
+                v = sum8_tree(v);
                 if (tid == 0) {
                     for (int i = nv; i < n; ++i) v += e[i - c0];
                     total = v;
@@ -199,92 +233,182 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(AttnArgs a) {
     }
 }
 
-// values: grid (64-column chunks, groups, K heads), 256 threads. Lane (r, c) of wavefront w runs
-// row r's chain for column 16 w + c of the chunk: acc = fma(w_p, v_p, acc) over the union in
-// order. Tiles of 64 positions (V: 64 x 64 floats, weights: 4 x 64) are loaded by all 256
-// threads S tiles ahead into registers, then stored to a double-buffered LDS tile (one barrier
-// per tile): each chain takes its operands from LDS while S tiles of loads are in flight.
-constexpr int AV_S = 6;
-__global__ __launch_bounds__(256) void attn_values_kernel(AttnArgs a, int n_tok) {
-    __shared__ float4 vt[2][64][16];
-    __shared__ float4 wt[2][4][16];
+// values: grid (64-column chunks, groups of 4 CH rows, K heads), 256 threads. Lane c of wavefront w
+// runs the chains of rows CH w .. CH w + CH - 1 for column c of the chunk: acc_r = fma(w_rp, v_p,
+// acc_r) over the union in order, one LDS read of v_p serving the CH chains. CH = 1 for decode
+// (few rows: every wavefront gets a row of its own), CH = 4 for prompt batches (fewer LDS reads
+// per fma). Tiles of 64 positions (V: 64 x 64 floats; weights: CH = 1 row-major 4 x 64, so one
+// 16-byte read gives 4 positions, CH = 4 position-major 64 x 16, so one 16-byte read gives a
+// wavefront's 4 rows) are loaded by all 256 threads AV_S tiles ahead into registers, then stored
+// to a double-buffered LDS tile (one barrier per tile). Every load is unconditional (clamped
+// addresses, the range mask applied at the store, the loop padded to whole rounds of AV_S
+// tiles) and the stages' loads keep their order, so the wait before a tile's store covers that
+// tile's loads only while AV_S - 1 tiles stay in flight.
+typedef float av4 __attribute__((ext_vector_type(4)));  // a native vector: kept in registers when staged
+template <int CH>
+struct AvStage {
+    av4 v0, v1, v2, v3;
+    av4 w;  // CH = 4: 4 positions of one row; CH = 1: .x only
+};
+template <int CH, int AV_S>  // AV_S: tiles in flight, 4 or 8 (the named stages below)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_values_kernel(AttnArgs a,
+                                                                                                     int n_tok) {
+    constexpr int GR = 4 * CH;  // rows per group
+    __shared__ av4 vt[2][64][16];
+    __shared__ __attribute__((aligned(16))) float wt[2][64 * GR];
     const int grp = blockIdx.y, kh = blockIdx.z, cc = (int)blockIdx.x * 64, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int r = lane >> 4, c = wave * 16 + (lane & 15);
-    const GroupRow me = group_row(a, n_tok, grp, kh, r);
     int lo, hi;
-    if (!group_span(a, n_tok, grp, kh, lo, hi)) {
-        if (me.row >= 0 && cc + c < a.hd) a.o[(size_t)me.row * a.hd + cc + c] = __builtin_nanf("");
+    if (!group_span(a, n_tok, GR, grp, kh, lo, hi)) {
+        for (int r = 0; r < CH; ++r) {
+            const GroupRow g = group_row(a, n_tok, GR, grp, kh, CH * wave + r);
+            if (g.row >= 0 && cc + lane < a.hd) a.o[(size_t)g.row * a.hd + cc + lane] = __builtin_nanf("");
+        }
         return;
     }
     const int span = hi - lo + 1, ns = (span + 63) / 64;
-    // loader: V rows lp + 16 m, columns lc .. lc + 3 of the chunk; weight of row wr at position wj
-    const int lp = tid >> 4, lc = (tid & 15) * 4, wr = tid >> 6, wj = tid & 63;
-    const bool lcol = cc + lc < a.hd;
-    const float *vb = a.v + (int64_t)kh * a.hd + cc + lc;
-    const GroupRow wg = group_row(a, n_tok, grp, kh, wr);
+    // loader: V positions lp + 16 m, columns lc .. lc + 3 of the chunk (columns past hd read
+    // column 0 instead: always a valid address; those outputs are not stored); weights: CH = 4,
+    // row wr at positions wp .. wp + 3; CH = 1, row wr1 at position wp1
+    const int lp = tid >> 4, lc = (tid & 15) * 4;
+    const int wr = CH == 4 ? tid >> 4 : tid >> 6, wp = CH == 4 ? (tid & 15) * 4 : tid & 63;
+    const float *vb = a.v + (int64_t)kh * a.hd + (cc + lc < a.hd ? cc + lc : 0);
+    const GroupRow wg = group_row(a, n_tok, GR, grp, kh, wr);
     const float *wrow = a.s + (size_t)(wg.row < 0 ? 0 : wg.row) * a.max_len;
-    auto load = [&](int k, float4(&v)[4], float &w) {
-        const int p0 = lo + k * 64;
+    // the loads walk the tiles in order, so the positions and ring slots advance by 64 per load
+    // (slot + 64 % cap, one conditional subtract) with no division in the loop; a position past
+    // hi reads hi's slot (a valid address; its weight is masked)
+    const int step64 = 64 % a.cap, slot_hi = (int)kv_slot(hi, a.cap);
+    int vpos[4], vslot[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        vpos[m] = lo + lp + 16 * m;
+        vslot[m] = (int)kv_slot(vpos[m], a.cap);
+    }
+    int wx = lo + wp - wg.st;  // score index of the next weight load
+    auto load = [&](AvStage<CH> &t) {
+        av4 *dst[4] = {&t.v0, &t.v1, &t.v2, &t.v3};
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const int p = min(p0 + lp + 16 * m, hi);
-            v[m] = lcol ? *(const float4 *)(vb + kv_slot(p, a.cap) * a.kv_dim) : make_float4(0, 0, 0, 0);
+            const int sl = vpos[m] <= hi ? vslot[m] : slot_hi;
+            *dst[m] = *(const av4 *)(vb + (int64_t)sl * a.kv_dim);
+            vpos[m] += 64;
+            vslot[m] += step64;
+            if (vslot[m] >= a.cap) vslot[m] -= a.cap;
         }
-        const int p = p0 + wj;
-        w = p >= wg.st && p <= wg.en ? wrow[p - wg.st] : 0.0f;
+        // raw loads only: the range mask is applied at the store
+        if constexpr (CH == 4)
+            t.w = (av4){wrow[min(max(wx, 0), a.max_len - 1)], wrow[min(max(wx + 1, 0), a.max_len - 1)],
+                        wrow[min(max(wx + 2, 0), a.max_len - 1)], wrow[min(max(wx + 3, 0), a.max_len - 1)]};
+        else
+            t.w.x = wrow[min(max(wx, 0), a.max_len - 1)];
+        wx += 64;
     };
-    float4 rv[AV_S][4];
-    float rw[AV_S];
+    auto in_range = [&](int p) { return p >= wg.st && p <= wg.en; };
+    float acc[CH];
 #pragma unroll
-    for (int u = 0; u < AV_S; ++u)
-        if (u < ns) load(u, rv[u], rw[u]);
-    float acc = 0.0f;
-    for (int k0 = 0; k0 < ns; k0 += AV_S) {
+    for (int r = 0; r < CH; ++r) acc[r] = 0.0f;
+    const float *vcol = (const float *)vt + lane;
+    // one tile: store the staged registers, barrier, reload them AV_S tiles ahead, run the chains
+    auto step = [&](int k, AvStage<CH> &t) {
+        const int b = k & 1;
+        vt[b][lp][tid & 15] = t.v0;
+        vt[b][lp + 16][tid & 15] = t.v1;
+        vt[b][lp + 32][tid & 15] = t.v2;
+        vt[b][lp + 48][tid & 15] = t.v3;
+        const int p = lo + k * 64 + wp;
+        if constexpr (CH == 4) {
+            float *wf = wt[b];
+            wf[(wp + 0) * GR + wr] = in_range(p) ? t.w.x : 0.0f;
+            wf[(wp + 1) * GR + wr] = in_range(p + 1) ? t.w.y : 0.0f;
+            wf[(wp + 2) * GR + wr] = in_range(p + 2) ? t.w.z : 0.0f;
+            wf[(wp + 3) * GR + wr] = in_range(p + 3) ? t.w.w : 0.0f;
+        } else {
+            wt[b][wr * 64 + wp] = in_range(p) ? t.w.x : 0.0f;
+        }
+        __syncthreads();
+        load(t);  // tile k + AV_S
+        const float *vs = vcol + b * 64 * 64;
+        const int cnt = min(64, span - k * 64);  // <= 0 past the end
+        if constexpr (CH == 4) {
+            const av4 *ws = (const av4 *)wt[b] + wave;  // [pos][16 rows]: this wavefront's 4
+            auto chain = [&](int j) {
+                const float x = vs[j * 64];
+                const av4 w4 = ws[j * 4];
+                acc[0] = __builtin_fmaf(w4.x, x, acc[0]);
+                acc[1] = __builtin_fmaf(w4.y, x, acc[1]);
+                acc[2] = __builtin_fmaf(w4.z, x, acc[2]);
+                acc[3] = __builtin_fmaf(w4.w, x, acc[3]);
+            };
+            if (cnt == 64) {
+#pragma unroll 8
+                for (int j = 0; j < 64; ++j) chain(j);
+            } else {
+                for (int j = 0; j < cnt; ++j) chain(j);
+            }
+        } else {
+            const float *wf = wt[b] + wave * 64;  // [4 rows][pos]: this wavefront's row
+            if (cnt == 64) {
 #pragma unroll
-        for (int u = 0; u < AV_S; ++u) {
-            const int k = k0 + u;
-            if (k < ns) {
-                const int b = k & 1;
-#pragma unroll
-                for (int m = 0; m < 4; ++m) vt[b][lp + 16 * m][tid & 15] = rv[u][m];
-                ((float *)wt[b])[wr * 64 + wj] = rw[u];
-                __syncthreads();
-                if (k + AV_S < ns) load(k + AV_S, rv[u], rw[u]);
-                const float *vs = (const float *)vt[b] + c;
-                const float4 *ws = wt[b][r];
-                const int cnt = min(64, span - k * 64);
-                if (cnt == 64) {
-#pragma unroll
-                    for (int j4 = 0; j4 < 16; ++j4) {
-                        const float4 w4 = ws[j4];
-                        acc = __builtin_fmaf(w4.x, vs[(4 * j4 + 0) * 64], acc);
-                        acc = __builtin_fmaf(w4.y, vs[(4 * j4 + 1) * 64], acc);
-                        acc = __builtin_fmaf(w4.z, vs[(4 * j4 + 2) * 64], acc);
-                        acc = __builtin_fmaf(w4.w, vs[(4 * j4 + 3) * 64], acc);
-                    }
-                } else {
-                    const float *wf = (const float *)ws;
-                    for (int j = 0; j < cnt; ++j) acc = __builtin_fmaf(wf[j], vs[j * 64], acc);
+                for (int j4 = 0; j4 < 16; ++j4) {
+                    const av4 w4 = *(const av4 *)(wf + 4 * j4);
+                    acc[0] = __builtin_fmaf(w4.x, vs[(4 * j4 + 0) * 64], acc[0]);
+                    acc[0] = __builtin_fmaf(w4.y, vs[(4 * j4 + 1) * 64], acc[0]);
+                    acc[0] = __builtin_fmaf(w4.z, vs[(4 * j4 + 2) * 64], acc[0]);
+                    acc[0] = __builtin_fmaf(w4.w, vs[(4 * j4 + 3) * 64], acc[0]);
                 }
+            } else {
+                for (int j = 0; j < cnt; ++j) acc[0] = __builtin_fmaf(wf[j], vs[j * 64], acc[0]);
             }
         }
+    };
+    // the stages' loads are issued strictly in order (scheduling barriers), so the loop head
+    // waits for the oldest stage only
+    AvStage<CH> t0, t1, t2, t3, t4, t5, t6, t7;
+#define AV_LOAD(i) \
+    load(t##i); \
+    __builtin_amdgcn_sched_barrier(0);
+#define AV_STEP(i) \
+    step(k0 + i, t##i); \
+    __builtin_amdgcn_sched_barrier(0);
+    AV_LOAD(0) AV_LOAD(1) AV_LOAD(2) AV_LOAD(3)
+    if constexpr (AV_S == 8) {
+        AV_LOAD(4) AV_LOAD(5) AV_LOAD(6) AV_LOAD(7)
     }
-    if (me.row >= 0 && cc + c < a.hd)
-        a.o[(size_t)me.row * a.hd + cc + c] = me.en >= me.st ? acc : __builtin_nanf("");
+    for (int k0 = 0; k0 < ns; k0 += AV_S) {
+        AV_STEP(0) AV_STEP(1) AV_STEP(2) AV_STEP(3)
+        if constexpr (AV_S == 8) {
+            AV_STEP(4) AV_STEP(5) AV_STEP(6) AV_STEP(7)
+        }
+    }
+#undef AV_LOAD
+#undef AV_STEP
+#pragma unroll
+    for (int r = 0; r < CH; ++r) {
+        const GroupRow g = group_row(a, n_tok, GR, grp, kh, CH * wave + r);
+        if (g.row >= 0 && cc + lane < a.hd)
+            a.o[(size_t)g.row * a.hd + cc + lane] = g.en >= g.st ? acc[r] : __builtin_nanf("");
+    }
 }
 
 hipError_t launch_attention(const AttnArgs &a, int n_tok, hipStream_t s) {
     if (n_tok < 1 || a.hd < 32 || a.hd > 256 || a.hd % 32 != 0 || a.n_head_kv < 1 || a.n_head % a.n_head_kv != 0 ||
         a.max_len < 1 || a.kv_dim % 4 != 0)
         return hipErrorInvalidValue;
-    const int groups = (n_tok * (a.n_head / a.n_head_kv) + 3) / 4;
-    if (groups > 65535 || a.n_head_kv > 65535) return hipErrorInvalidValue;
+    const int rows_kv = n_tok * (a.n_head / a.n_head_kv);  // rows per K / V head
+    if ((rows_kv + 3) / 4 > 65535 || a.n_head_kv > 65535) return hipErrorInvalidValue;
     const unsigned kb = (unsigned)std::min((a.max_len + 255) / 256, 1024);
-    attn_scores_kernel<<<dim3(kb, (unsigned)groups, (unsigned)a.n_head_kv), 256, 0, s>>>(a, n_tok);
+    const dim3 kvh(1, 1, (unsigned)a.n_head_kv);
+    if (rows_kv >= 16)
+        attn_scores_kernel<16><<<dim3(kb, (unsigned)((rows_kv + 15) / 16), kvh.z), 256, 0, s>>>(a, n_tok);
+    else
+        attn_scores_kernel<4><<<dim3(kb, (unsigned)((rows_kv + 3) / 4), kvh.z), 256, 0, s>>>(a, n_tok);
     attn_softmax_kernel<<<n_tok * a.n_head, 256, 0, s>>>(a);
-    attn_values_kernel<<<dim3((unsigned)((a.hd + 63) / 64), (unsigned)groups, (unsigned)a.n_head_kv), 256, 0, s>>>(
-        a, n_tok);
+    const unsigned cch = (unsigned)((a.hd + 63) / 64);
+    if (rows_kv >= 64)  // enough groups of 16 to fill the chip: 4 chains per lane
+        attn_values_kernel<4, 4><<<dim3(cch, (unsigned)((rows_kv + 15) / 16), kvh.z), 256, 0, s>>>(a, n_tok);
+    else
+        attn_values_kernel<1, 8><<<dim3(cch, (unsigned)((rows_kv + 3) / 4), kvh.z), 256, 0, s>>>(a, n_tok);
     return hipGetLastError();
 }
 
