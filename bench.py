@@ -132,6 +132,59 @@ def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
     return out
 
 
+def attention_config(be, kernel_time, enabled: int, cpu: bool) -> dict | None:
+    """Attention over the fp32 KV ring cache (attn_rows, fastgguf.c:3273-3326) at Llama-3-8B's shape
+    (32 query heads over 8 K / V heads, hd 128): one decode token over 4096 positions, and a 64-token
+    prompt batch at the end of a 4096-position context. With cpu, the reference's attn_rows (oracle/_ref,
+    one thread) on the decode case, its 4-row calls per K / V head as the reference's forward makes."""
+    if not enabled:
+        return None
+    import numpy as np
+    rng = np.random.default_rng(400)
+    cap, hd, nh, nkv = 4096, 128, 32, 8
+    kv_dim = nkv * hd
+    ck = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+    cv = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+    kd, vd = be.dev_alloc(ck.nbytes), be.dev_alloc(cv.nbytes)
+    be.h2d(kd, ck)
+    be.h2d(vd, cv)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    out = {"shape": "32 heads over 8 K/V heads, hd 128, fp32 cache of 4096 positions"}
+    for name, nt in (("decode_4096", 1), ("prefill_64_at_4096", 64)):
+        q = rng.standard_normal((nt, nh, hd)).astype(np.float32)
+        en = (10000 + np.arange(nt)).astype(np.int32)
+        st = (en[-1] - cap + 1) * np.ones(nt, np.int32)
+        bufs = [be.dev_alloc(a.nbytes) for a in (q, q, st, en)]
+        for b, a in zip(bufs, (q, q, st, en)):
+            be.h2d(b, a)
+        n_max = int((en - st).max()) + 1
+        us = kernel_time(lambda i: be.attention_dev(nt, nh, nkv, hd, bufs[0], bufs[1], kd, vd, kv_dim, cap, bufs[2],
+                                                    bufs[3], n_max, scale), 100)
+        kv_bytes = 2 * n_max * kv_dim * 4
+        fmas = 2 * int((en - st + 1).sum()) * nh * hd
+        out[name] = {"us": round(us, 2), "kv_bytes": kv_bytes, "kv_GB/s": round(kv_bytes / us / 1e3, 1),
+                     "fma_G/s": round(fmas / us / 1e3, 1)}
+        if cpu and nt == 1:
+            try:
+                sys.path.insert(0, os.path.join(ROOT, "oracle"))
+                from oracle import Reference
+                ref = Reference()
+                t0 = time.perf_counter()
+                reps = 5
+                for _ in range(reps):
+                    for h in range(nkv):
+                        ref.attn_rows(q[0, 4 * h:4 * h + 4], np.repeat(st, 4), np.repeat(en, 4), ck, cv, h * hd, hd,
+                                      scale)
+                out[name]["cpu_reference_1thread_us"] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+            except (FileNotFoundError, OSError) as e:
+                print(f"[bench] attention cpu reference skipped: {e}", file=sys.stderr)
+        for b in bufs:
+            be.dev_free(b)
+    be.dev_free(kd)
+    be.dev_free(vd)
+    return out
+
+
 def cpu_baseline(layer_w: dict, xs: dict, budget_s: float) -> dict | None:
     """The reference's CPU path on the same layer (oracle/_ref), median over a bounded sample."""
     try:
@@ -347,6 +400,7 @@ def main() -> int:
     be.dev_free(ypd)
 
     others = other_configs(be, S, kernel_time, args.configs)
+    attention = attention_config(be, kernel_time, args.configs, args.cpu_seconds > 0)
 
     cpu = cpu_baseline(layer_w, xs, args.cpu_seconds) if args.cpu_seconds > 0 else None
     info = be.info()
@@ -367,6 +421,7 @@ def main() -> int:
         "kernels": kernels,
         "prefill": prefill,
         "other_configs": others,
+        "attention": attention,
     }
     print(json.dumps(out), flush=True)
     return 0
