@@ -27,7 +27,7 @@ EXPORTS = (
     "fgh_open", "fgh_close", "fgh_info", "fgh_last_error", "fgh_upload", "fgh_tensor_free",
     "fgh_matvec", "fgh_matvec_multi", "fgh_matmul", "fgh_moe_ffn", "fgh_attention",
     "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matvec_silu_dev", "fgh_matmul_dev", "fgh_moe_ffn_dev",
-    "fgh_attention_dev",
+    "fgh_attention_dev", "fgh_kvq_store_dev", "fgh_kvq_attention_dev",
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
@@ -84,6 +84,9 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_moe_ffn_dev": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, i32]),
         "fgh_attention": (i32, [vp, i32, i32, i32, i32, vp, vp, vp, vp, i32, i32, vp, vp, C.c_float]),
         "fgh_attention_dev": (i32, [vp, i32, i32, i32, i32, vp, vp, vp, vp, i32, i32, vp, vp, i32, C.c_float]),
+        "fgh_kvq_store_dev": (i32, [vp, i32, i32, i32, i32, i32, vp, vp, i32, vp, vp, i32, vp]),
+        "fgh_kvq_attention_dev": (i32, [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp, vp, i32,
+                                        C.c_float]),
         "fgh_graph_begin": (i32, [vp]),
         "fgh_graph_end": (i32, [vp, C.POINTER(vp)]),
         "fgh_graph_launch": (i32, [vp, vp]),
@@ -465,6 +468,60 @@ class Backend:
                       scale: float):
         self._check(self.lib.fgh_attention_dev(self.ctx, n_tok, n_head, n_head_kv, hd, q_dev, o_dev, k_dev, v_dev,
                                                kv_dim, cap, st_dev, en_dev, max_len, scale))
+
+    def kvq_store_dev(self, n_tok, n_head_kv, hd, kbits, vbits, k_dev, v_dev, stride, kq_dev, vq_dev, cap, pos_dev):
+        self._check(self.lib.fgh_kvq_store_dev(self.ctx, n_tok, n_head_kv, hd, kbits, vbits, k_dev, v_dev, stride,
+                                               kq_dev, vq_dev, cap, pos_dev))
+
+    def kvq_attention_dev(self, n_tok, n_head, n_head_kv, hd, kbits, vbits, q_dev, o_dev, kq_dev, vq_dev, cap,
+                          st_dev, en_dev, max_len, scale):
+        self._check(self.lib.fgh_kvq_attention_dev(self.ctx, n_tok, n_head, n_head_kv, hd, kbits, vbits, q_dev,
+                                                   o_dev, kq_dev, vq_dev, cap, st_dev, en_dev, max_len, scale))
+
+    def kvq_store(self, k, v, pos, kq, vq, kbits: int, vbits: int):
+        """Writes rows k / v ([n_tok][n_head_kv][hd]) at positions pos into host copies of the
+        quantized caches kq / vq ([cap][slot bytes]), on the device; returns the new caches."""
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        n_tok, nkv, hd = k.shape
+        pos = np.ascontiguousarray(pos, np.int32)
+        kq = np.ascontiguousarray(kq, np.uint8)
+        vq = np.ascontiguousarray(vq, np.uint8)
+        bufs = [self.dev_alloc(a.nbytes) for a in (k, v, pos, kq, vq)]
+        try:
+            for b, a in zip(bufs, (k, v, pos, kq, vq)):
+                self.h2d(b, a)
+            self.kvq_store_dev(n_tok, nkv, hd, kbits, vbits, bufs[0], bufs[1], nkv * hd, bufs[3], bufs[4],
+                               kq.shape[0], bufs[2])
+            kq2, vq2 = np.empty_like(kq), np.empty_like(vq)
+            self.d2h(kq2, bufs[3])
+            self.d2h(vq2, bufs[4])
+            return kq2, vq2
+        finally:
+            for b in bufs:
+                self.dev_free(b)
+
+    def kvq_attention(self, q, kq, vq, st, en, n_head_kv: int, kbits: int, vbits: int, scale: float):
+        """TurboQuant attention over host copies of the quantized caches: q [n_tok][n_head][hd]."""
+        q = np.ascontiguousarray(q, np.float32)
+        n_tok, n_head, hd = q.shape
+        st = np.ascontiguousarray(st, np.int32)
+        en = np.ascontiguousarray(en, np.int32)
+        kq = np.ascontiguousarray(kq, np.uint8)
+        vq = np.ascontiguousarray(vq, np.uint8)
+        max_len = int(max(1, (en - st).max() + 1))
+        bufs = [self.dev_alloc(a.nbytes) for a in (q, q, kq, vq, st, en)]
+        try:
+            for b, a in zip(bufs, (q, q, kq, vq, st, en)):
+                self.h2d(b, a)
+            self.kvq_attention_dev(n_tok, n_head, n_head_kv, hd, kbits, vbits, bufs[0], bufs[1], bufs[2], bufs[3],
+                                   kq.shape[0], bufs[4], bufs[5], max_len, scale)
+            o = np.empty_like(q)
+            self.d2h(o, bufs[1])
+            return o
+        finally:
+            for b in bufs:
+                self.dev_free(b)
 
 
 __all__ = ["Backend", "BackendError", "Gguf", "Tensor", "load_library", "EXPORTS", "T_Q4_K", "T_Q5_0", "T_Q5_K", "T_Q6_K", "T_Q8_0",

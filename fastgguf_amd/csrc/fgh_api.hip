@@ -33,6 +33,7 @@ struct fgh_ctx {
     DevBuf x, y, aqs, ad, abs;
     DevBuf gq, gy, gb;  // prompt-GEMM activations (launch_gemm_quant layout)
     DevBuf as;          // attention scores / weights
+    DevBuf kqr, kor, kvc;  // TurboQuant attention: rotated queries, rotated outputs, V centroids
     DevBuf msel, mw, mg, mu, md, mlog;  // MoE: selection, weights, gate / up / down outputs
     DevBuf mseg, mslot, mimx, mimh;         // MoE: slots grouped by expert, Q8_K images of x and h
     DevBuf ck;                              // fgh_checksum_dev: per-workgroup partial sums
@@ -252,7 +253,8 @@ void fgh_close(fgh_ctx *c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->gy, &c->gb, &c->msel, &c->mw, &c->mg,
-                      &c->mu, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck, &c->as})
+                      &c->mu, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck, &c->as, &c->kqr,
+                      &c->kor, &c->kvc})
         if (b->p) (void)hipFree(b->p);
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -507,6 +509,47 @@ int fgh_attention_dev(fgh_ctx *c, int n_tok, int n_head, int n_head_kv, int hd, 
     fgh::AttnArgs a{q, o, k_cache, v_cache, (float *)c->as.p, st, en, n_head, n_head_kv, hd, kv_dim, cap, max_len,
                     scale};
     HIP_TRY(c, fgh::launch_attention(a, n_tok, c->stream));
+    return FGH_OK;
+}
+
+static bool kvq_shape_ok(int hd, int kbits, int vbits) {
+    return hd >= 32 && hd <= 256 && (hd & (hd - 1)) == 0 && (kbits == 4 || kbits == 8) &&
+           (vbits == 2 || vbits == 4 || vbits == 8);
+}
+
+int fgh_kvq_store_dev(fgh_ctx *c, int n_tok, int n_head_kv, int hd, int kbits, int vbits, const float *k,
+                      const float *v, int stride, uint8_t *kq, uint8_t *vq, int cap, const int32_t *pos) {
+    if (!c) return FGH_ERR_ARG;
+    if (!k || !v || !kq || !vq || !pos || n_tok < 1 || n_tok > 65535 || n_head_kv < 1 || n_head_kv > 65535 ||
+        cap < 1 || !kvq_shape_ok(hd, kbits, vbits) || (int64_t)n_head_kv * hd > stride)
+        return fail(c, FGH_ERR_ARG, "kvq_store: bad arguments");
+    if (((uintptr_t)kq | (uintptr_t)vq) % 16 != 0)
+        return fail(c, FGH_ERR_ARG, "kvq_store: the caches must be 16-byte aligned");
+    HIP_TRY(c, hipSetDevice(c->device));
+    fgh::KvqStoreArgs a{k, v, kq, vq, pos, stride, n_head_kv, hd, kbits, vbits, cap};
+    HIP_TRY(c, fgh::launch_kvq_store(a, n_tok, c->stream));
+    return FGH_OK;
+}
+
+int fgh_kvq_attention_dev(fgh_ctx *c, int n_tok, int n_head, int n_head_kv, int hd, int kbits, int vbits,
+                          const float *q, float *o, const uint8_t *kq, const uint8_t *vq, int cap, const int32_t *st,
+                          const int32_t *en, int max_len, float scale) {
+    if (!c) return FGH_ERR_ARG;
+    if (!q || !o || !kq || !vq || !st || !en || n_tok < 1 || n_head < 1 || n_head_kv < 1 ||
+        n_head % n_head_kv != 0 || cap < 1 || max_len < 1 || !kvq_shape_ok(hd, kbits, vbits) ||
+        (int64_t)n_tok * n_head > 65535)
+        return fail(c, FGH_ERR_ARG, "kvq_attention: bad arguments");
+    if (((uintptr_t)q | (uintptr_t)kq | (uintptr_t)vq) % 16 != 0)
+        return fail(c, FGH_ERR_ARG, "kvq_attention: q and the caches must be 16-byte aligned");
+    HIP_TRY(c, hipSetDevice(c->device));
+    const size_t rows = (size_t)n_tok * n_head;
+    int rc;
+    if ((rc = grow(c, c->as, rows * max_len * 4)) || (rc = grow(c, c->kqr, rows * hd * 4)) ||
+        (rc = grow(c, c->kor, rows * hd * 4)) || (rc = grow(c, c->kvc, (size_t)cap * n_head_kv * hd * 4)))
+        return rc;
+    fgh::KvqAttnArgs a{q,  o,  (float *)c->kqr.p, (float *)c->kor.p, (float *)c->as.p, (float *)c->kvc.p, kq, vq, st,
+                       en, n_head, n_head_kv, hd, kbits, vbits, cap, max_len, scale};
+    HIP_TRY(c, fgh::launch_kvq_attention(a, n_tok, c->stream));
     return FGH_OK;
 }
 

@@ -391,6 +391,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     }
 }
 
+hipError_t launch_attention_values(const AttnArgs &a, int n_tok, hipStream_t s) {
+    if (n_tok < 1 || a.hd < 32 || a.hd > 256 || a.hd % 32 != 0 || a.n_head_kv < 1 || a.n_head % a.n_head_kv != 0 ||
+        a.max_len < 1 || a.kv_dim % 4 != 0)
+        return hipErrorInvalidValue;
+    const int rows_kv = n_tok * (a.n_head / a.n_head_kv);
+    if ((rows_kv + 3) / 4 > 65535 || a.n_head_kv > 65535) return hipErrorInvalidValue;
+    const unsigned cch = (unsigned)((a.hd + 63) / 64);
+    if (rows_kv >= 64)
+        attn_values_kernel<4, 4><<<dim3(cch, (unsigned)((rows_kv + 15) / 16), (unsigned)a.n_head_kv), 256, 0, s>>>(
+            a, n_tok);
+    else
+        attn_values_kernel<1, 8><<<dim3(cch, (unsigned)((rows_kv + 3) / 4), (unsigned)a.n_head_kv), 256, 0, s>>>(a,
+                                                                                                              n_tok);
+    return hipGetLastError();
+}
+
 hipError_t launch_attention(const AttnArgs &a, int n_tok, hipStream_t s) {
     if (n_tok < 1 || a.hd < 32 || a.hd > 256 || a.hd % 32 != 0 || a.n_head_kv < 1 || a.n_head % a.n_head_kv != 0 ||
         a.max_len < 1 || a.kv_dim % 4 != 0)

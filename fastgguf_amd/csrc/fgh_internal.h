@@ -288,6 +288,28 @@ struct AttnArgs {
     float scale;
 };
 hipError_t launch_attention(const AttnArgs &a, int n_tok, hipStream_t s);
+hipError_t launch_attention_values(const AttnArgs &a, int n_tok, hipStream_t s);  // the value chains only
+
+// TurboQuant KV cache (fgh_kvq.hip): records of 4 + hd * bits / 8 bytes per (slot, K / V head)
+struct KvqStoreArgs {
+    const float *k, *v;  // [tokens][stride] new K / V rows (n_head_kv * hd values each)
+    uint8_t *kq, *vq;    // [cap][n_head_kv records]
+    const int32_t *pos;  // [tokens] positions (slot = pos % cap)
+    int stride, n_head_kv, hd, kbits, vbits, cap;
+};
+hipError_t launch_kvq_store(const KvqStoreArgs &a, int n_tok, hipStream_t s);
+struct KvqAttnArgs {
+    const float *q;           // [rows][hd] unrotated queries
+    float *o;                 // [rows][hd] outputs, rotated back
+    float *qr, *orot;         // [rows][hd] scratch: rotated queries, rotated outputs
+    float *s;                 // [rows][max_len] scores, then weights
+    float *vc;                // [cap][n_head_kv * hd] scratch: V centroids
+    const uint8_t *kq, *vq;   // quantized caches
+    const int32_t *st, *en;   // [tokens] position ranges
+    int n_head, n_head_kv, hd, kbits, vbits, cap, max_len;
+    float scale;
+};
+hipError_t launch_kvq_attention(const KvqAttnArgs &a, int n_tok, hipStream_t s);
 
 // prompt-batch Q4_K GEMM (fgh_gemm.hip): 1..64 tokens, weights in the Q4_K decode layout
 struct GemmArgs {

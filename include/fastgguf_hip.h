@@ -206,6 +206,22 @@ FGH_API int fgh_attention_dev(fgh_ctx *ctx, int n_tok, int n_head, int n_head_kv
                       float *o_dev, const float *k_cache_dev, const float *v_cache_dev, int kv_dim, int cap,
                       const int32_t *st_dev, const int32_t *en_dev, int max_len, float scale);
 
+/* ---- TurboQuant KV cache: replaces kvq_rotate / kvq_quant_slice (fastgguf.c:3341-3444) at the
+ * cache write (forward 4726-4735) and the attention step over the quantized cache (4760-4846:
+ * q rotated, kvq_dot_k 3447-3462, softmax_inplace 3147-3156, kvq_axpy_v 3465-3489, the output
+ * rotated back). A cache is cap slots; slot p % cap holds n_head_kv records of
+ * 4 + hd * bits / 8 bytes (float scale, then the codes) back to back, the reference's layout
+ * (KVQ_REC, 3361). hd a power of 2 from 32 to 256; K bits 4 or 8, V bits 2, 4 or 8. Outputs equal
+ * the reference's bit for bit. */
+/* k_dev, v_dev: [n_tok][stride] new K / V rows; pos_dev: int32 [n_tok] their positions. */
+FGH_API int fgh_kvq_store_dev(fgh_ctx *ctx, int n_tok, int n_head_kv, int hd, int kbits, int vbits,
+                      const float *k_dev, const float *v_dev, int stride, uint8_t *kq_dev, uint8_t *vq_dev,
+                      int cap, const int32_t *pos_dev);
+/* q_dev, o_dev: [n_tok][n_head][hd], unrotated; ranges and NaN rows as fgh_attention_dev. */
+FGH_API int fgh_kvq_attention_dev(fgh_ctx *ctx, int n_tok, int n_head, int n_head_kv, int hd, int kbits, int vbits,
+                          const float *q_dev, float *o_dev, const uint8_t *kq_dev, const uint8_t *vq_dev,
+                          int cap, const int32_t *st_dev, const int32_t *en_dev, int max_len, float scale);
+
 /* ---- HIP graphs of device-resident calls (launch-bound decode loops) ----
  * fgh_graph_begin starts capturing the context stream; the *_dev calls that follow are recorded,
  * not run; fgh_graph_end instantiates them as one executable graph that fgh_graph_launch replays

@@ -1014,3 +1014,163 @@ int fgo_attn_rows(int nr, const float *q, float *o, const int *st, const int *en
     }
     return 0;
 }
+
+/* ---- B-11: TurboQuant KV cache (fastgguf.c:3341-3513) and its attention step (4760-4846) ----
+ * Rotation R x = H(D x) / sqrt(n): D the signs of xorshift64* (rng_next 3333-3338) from seed
+ * 0x243F6A8885A308D3, bit 63 set -> +1 (kvq_init 3363-3372); H the in-place Walsh-Hadamard
+ * butterflies (a + b, a - b), then every value times 1 / sqrtf(n) (kvq_fwht 3375-3386). Inverse:
+ * the same transform, then the signs (kvq_unrotate 3396-3400).
+ * Slice records (kvq_quant_slice 3415-3444): a float scale, then the codes.
+ *   bits 8: s = amax / 127, q = lrintf(x * (1 / s)) (round half to even)
+ *   bits 4 / 2: ss = sum in order of the rounded x_i * x_i, s = sqrtf(ss / hd), code = the first c with
+ *     u <= (c_c + c_{c+1}) * 0.5 over the Lloyd-Max centroids (kvq_enc4 / kvq_enc2 3403-3412),
+ *     u = x * (1 / s); 4-bit codes low nibble first, 2-bit codes low bits first
+ * Scores (kvq_dot_k 3447-3462): 4-bit acc = acc + fma(q_i, c[lo], q_{i+1} * c[hi]) per byte (the
+ *   contraction of `acc += q_i c_lo + q_{i+1} c_hi` the compiled reference makes: the golden
+ *   vectors fix it), 8-bit acc = fma(q_i, code_i, acc); times s, then times scale.
+ * Softmax: softmax_inplace (3147-3156): max, e = expf(s - max), the sum in order, times 1 / sum.
+ * Values (kvq_axpy_v 3465-3489 from forward 4829-4836): for each position with w != 0, in order,
+ *   o_i = fma(w * s, value_i, o_i) with value_i the centroid (4 / 2 bits) or the int8 code. */
+static const float KVQ_C4[16] = {-2.7326f, -2.0690f, -1.6181f, -1.2562f, -0.9424f, -0.6568f, -0.3881f, -0.1284f,
+                                 0.1284f,  0.3881f,  0.6568f,  0.9424f,  1.2562f,  1.6181f,  2.0690f,  2.7326f};
+static const float KVQ_C2[4] = {-1.5104f, -0.4528f, 0.4528f, 1.5104f};
+
+void fgo_kvq_signs(float *out, int n) {
+    uint64_t s = 0x243F6A8885A308D3ULL;
+    for (int i = 0; i < n; i++) {
+        uint64_t x = s;
+        x ^= x >> 12;
+        x ^= x << 25;
+        x ^= x >> 27;
+        s = x;
+        out[i] = ((x * 0x2545F4914F6CDD1DULL) >> 63) ? 1.0f : -1.0f;
+    }
+}
+
+static void kvq_hadamard(float *x, int n) {
+    for (int len = 1; len < n; len <<= 1)
+        for (int i = 0; i < n; i += 2 * len)
+            for (int j = i; j < i + len; j++) {
+                float a = x[j], b = x[j + len];
+                x[j] = a + b;
+                x[j + len] = a - b;
+            }
+    float inv = 1.0f / sqrtf((float)n);
+    for (int i = 0; i < n; i++) x[i] = x[i] * inv;
+}
+
+int fgo_kvq_rotate(float *x, int n, int inverse) {
+    if (n < 2 || n > 1024 || (n & (n - 1))) return -1;
+    float sg[1024];
+    fgo_kvq_signs(sg, n);
+    if (!inverse)
+        for (int i = 0; i < n; i++) x[i] = x[i] * sg[i];
+    kvq_hadamard(x, n);
+    if (inverse)
+        for (int i = 0; i < n; i++) x[i] = x[i] * sg[i];
+    return 0;
+}
+
+int fgo_kvq_rec_bytes(int hd, int bits) { return 4 + hd * bits / 8; }
+
+static int kvq_code(float u, const float *c, int nc) {
+    int k = 0;
+    while (k < nc - 1 && u > (c[k] + c[k + 1]) * 0.5f) k++;
+    return k;
+}
+
+int fgo_kvq_quant(const float *x, int hd, uint8_t *rec, int bits) {
+    if (bits != 8 && bits != 4 && bits != 2) return -1;
+    uint8_t *q = rec + 4;
+    float s;
+    if (bits == 8) {
+        float amax = 0.0f;
+        for (int i = 0; i < hd; i++) if (fabsf(x[i]) > amax) amax = fabsf(x[i]);
+        s = amax / 127.0f;
+        float inv = s > 0.0f ? 1.0f / s : 0.0f;
+        for (int i = 0; i < hd; i++) q[i] = (uint8_t)(int8_t)lrintf(x[i] * inv);
+    } else {
+        float ss = 0.0f;
+#if FGO_MUTATE == 13 /* the sum of squares as an fma chain */
+        for (int i = 0; i < hd; i++) ss = fmaf(x[i], x[i], ss);
+#else
+        for (int i = 0; i < hd; i++) ss = ss + x[i] * x[i]; /* not contracted by the compiled reference */
+#endif
+        s = sqrtf(ss / (float)hd);
+        float inv = s > 0.0f ? 1.0f / s : 0.0f;
+        if (bits == 4)
+            for (int i = 0; i < hd; i += 2)
+                q[i / 2] = (uint8_t)(kvq_code(x[i] * inv, KVQ_C4, 16) | kvq_code(x[i + 1] * inv, KVQ_C4, 16) << 4);
+        else
+            for (int i = 0; i < hd; i += 4)
+                q[i / 4] = (uint8_t)(kvq_code(x[i] * inv, KVQ_C2, 4) | kvq_code(x[i + 1] * inv, KVQ_C2, 4) << 2 |
+                                     kvq_code(x[i + 2] * inv, KVQ_C2, 4) << 4 | kvq_code(x[i + 3] * inv, KVQ_C2, 4) << 6);
+    }
+    memcpy(rec, &s, 4);
+    return 0;
+}
+
+static float kvq_value(const uint8_t *q, int i, int bits) {
+    if (bits == 8) return (float)(int8_t)q[i];
+    if (bits == 4) return KVQ_C4[(q[i / 2] >> (4 * (i & 1))) & 15];
+    return KVQ_C2[(q[i / 4] >> (2 * (i & 3))) & 3];
+}
+
+static float kvq_dot(const float *qh, const uint8_t *rec, int hd, int bits) {
+    float s, acc = 0.0f;
+    memcpy(&s, rec, 4);
+    const uint8_t *q = rec + 4;
+    if (bits == 8) {
+        for (int i = 0; i < hd; i++) acc = fmaf(qh[i], (float)(int8_t)q[i], acc);
+    } else {
+        for (int i = 0; i < hd; i += 2) {
+#if FGO_MUTATE == 12 /* the pair's products rounded separately, no contraction */
+            acc = acc + (qh[i] * KVQ_C4[q[i / 2] & 15] + qh[i + 1] * KVQ_C4[q[i / 2] >> 4]);
+#else
+            acc = acc + fmaf(qh[i], KVQ_C4[q[i / 2] & 15], qh[i + 1] * KVQ_C4[q[i / 2] >> 4]);
+#endif
+        }
+    }
+    return acc * s;
+}
+
+int fgo_kvq_attn_rows(int nr, const float *q, float *o, const int *st, const int *en, const uint8_t *kq,
+                      const uint8_t *vq, int kqs, int vqs, const int *kvh, int cap, int hd, int kbits, int vbits,
+                      float scale) {
+    if (hd < 2 || hd > 1024 || (hd & (hd - 1)) || (kbits != 4 && kbits != 8) ||
+        (vbits != 2 && vbits != 4 && vbits != 8))
+        return -1;
+    for (int r = 0; r < nr; r++) {
+        int n = en[r] - st[r] + 1;
+        if (n < 1 || n > cap) return -1;
+        float qh[1024];
+        memcpy(qh, q + (size_t)r * hd, (size_t)hd * sizeof(float));
+        fgo_kvq_rotate(qh, hd, 0);
+        float *sc = (float *)malloc((size_t)n * sizeof(float));
+        if (!sc) return -1;
+        for (int p = st[r]; p <= en[r]; p++)
+            sc[p - st[r]] = kvq_dot(qh, kq + (size_t)(p % cap) * kqs + (size_t)kvh[r] * fgo_kvq_rec_bytes(hd, kbits),
+                                    hd, kbits) * scale;
+        float mx = -INFINITY, sum = 0.0f;
+        for (int i = 0; i < n; i++) if (sc[i] > mx) mx = sc[i];
+        for (int i = 0; i < n; i++) { sc[i] = expf(sc[i] - mx); sum += sc[i]; }
+        if (sum > 0.0f) {
+            float inv = 1.0f / sum;
+            for (int i = 0; i < n; i++) sc[i] = sc[i] * inv;
+        }
+        float *oh = o + (size_t)r * hd;
+        for (int i = 0; i < hd; i++) oh[i] = 0.0f;
+        for (int p = st[r]; p <= en[r]; p++) {
+            float w = sc[p - st[r]];
+            if (w == 0.0f) continue;
+            const uint8_t *rec = vq + (size_t)(p % cap) * vqs + (size_t)kvh[r] * fgo_kvq_rec_bytes(hd, vbits);
+            float s;
+            memcpy(&s, rec, 4);
+            float ws = w * s;
+            for (int i = 0; i < hd; i++) oh[i] = fmaf(ws, kvq_value(rec + 4, i, vbits), oh[i]);
+        }
+        fgo_kvq_rotate(oh, hd, 1);
+        free(sc);
+    }
+    return 0;
+}

@@ -92,6 +92,18 @@ int fgo_attn_rows(int nr, const float *q, float *o, const int *st, const int *en
                   int kv_dim, const int *kvo, int cap, int hd, float scale);
 float fgo_exp_neg(float x);
 
+/* TurboQuant KV cache (fastgguf.c:3341-3513, forward 4760-4846): the rotation's signs, the
+ * rotation (inverse = 1: its inverse), slice records of fgo_kvq_rec_bytes(hd, bits) bytes, and
+ * attention rows over quantized ring caches (kq / vq: cap slots of kqs / vqs bytes; row r reads
+ * K / V head kvh[r]; q unrotated, o unrotated). hd a power of 2 up to 1024. */
+void fgo_kvq_signs(float *out, int n);
+int fgo_kvq_rotate(float *x, int n, int inverse);
+int fgo_kvq_rec_bytes(int hd, int bits);
+int fgo_kvq_quant(const float *x, int hd, uint8_t *rec, int bits);
+int fgo_kvq_attn_rows(int nr, const float *q, float *o, const int *st, const int *en, const uint8_t *kq,
+                      const uint8_t *vq, int kqs, int vqs, const int *kvh, int cap, int hd, int kbits, int vbits,
+                      float scale);
+
 /* reference order for the router: softmax (3147), top-k by argmax (3328), renormalise (4603) */
 void fgo_moe_route(const float *logits, int n_expert, int k, int32_t *sel, float *w);
 

@@ -72,6 +72,11 @@ class Oracle:
         L.fgo_expf_compare.restype = C.c_uint64
         L.fgo_dequantize_row.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
         L.fgo_attn_rows.argtypes = [C.c_int] + [C.c_void_p] * 6 + [C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_float]
+        L.fgo_kvq_signs.argtypes = [C.c_void_p, C.c_int]
+        L.fgo_kvq_rotate.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        L.fgo_kvq_quant.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int]
+        L.fgo_kvq_attn_rows.argtypes = [C.c_int] + [C.c_void_p] * 6 + [C.c_int, C.c_int, C.c_void_p] + \
+            [C.c_int] * 4 + [C.c_float]
         L.fgo_exp_neg.argtypes = [C.c_float]
         L.fgo_exp_neg.restype = C.c_float
 
@@ -207,6 +212,38 @@ class Oracle:
             raise ValueError("fgo_attn_rows failed")
         return o
 
+    def kvq_signs(self, n: int) -> np.ndarray:
+        out = np.zeros(n, np.float32)
+        self.lib.fgo_kvq_signs(_ptr(out), n)
+        return out
+
+    def kvq_rotate(self, x, inverse: bool = False) -> np.ndarray:
+        x = np.array(x, np.float32, copy=True)
+        if self.lib.fgo_kvq_rotate(_ptr(x), x.size, int(inverse)) != 0:
+            raise ValueError("fgo_kvq_rotate failed")
+        return x
+
+    def kvq_quant(self, x, bits: int) -> np.ndarray:
+        """One head slice (already rotated) as a TurboQuant record."""
+        x = np.ascontiguousarray(x, np.float32)
+        rec = np.zeros(4 + x.size * bits // 8, np.uint8)
+        if self.lib.fgo_kvq_quant(_ptr(x), x.size, _ptr(rec), bits) != 0:
+            raise ValueError("fgo_kvq_quant failed")
+        return rec
+
+    def kvq_attn_rows(self, q, st, en, kq, vq, kvh, hd, kbits, vbits, scale):
+        """TurboQuant attention rows: q [nr][hd] unrotated; kq / vq [cap][slot bytes]."""
+        q = np.ascontiguousarray(q, np.float32).reshape(-1, hd)
+        kq = np.ascontiguousarray(kq, np.uint8)
+        vq = np.ascontiguousarray(vq, np.uint8)
+        st, en, kvh = (np.ascontiguousarray(a, np.int32) for a in (st, en, kvh))
+        o = np.zeros_like(q)
+        if self.lib.fgo_kvq_attn_rows(q.shape[0], _ptr(q), _ptr(o), _ptr(st), _ptr(en), _ptr(kq), _ptr(vq),
+                                      kq.shape[1], vq.shape[1], _ptr(kvh), kq.shape[0], hd, kbits, vbits,
+                                      scale) != 0:
+            raise ValueError("fgo_kvq_attn_rows failed")
+        return o
+
     def moe_down(self, type_down, down, n_embd, ff, sel, w, h):
         sel = np.ascontiguousarray(sel, np.int32)
         w = np.ascontiguousarray(w, np.float32)
@@ -263,6 +300,12 @@ class Reference:
         L.fgr_tensor_free.restype = None
         L.fgr_tensor_matvec_multi.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
         L.fgr_attn_rows.argtypes = [C.c_int] + [C.c_void_p] * 6 + [C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
+        L.fgr_kvq_signs.argtypes = [C.c_void_p, C.c_int]
+        L.fgr_kvq_rotate.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        L.fgr_kvq_quant.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int]
+        L.fgr_kvq_dequant.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+        L.fgr_kvq_attn_rows.argtypes = [C.c_int] + [C.c_void_p] * 6 + [C.c_int, C.c_int, C.c_void_p] + \
+            [C.c_int] * 4 + [C.c_float]
         L.fgr_gguf_table.argtypes = [C.c_char_p] + [C.c_void_p] * 10 + [C.c_int64, C.c_char_p, C.c_int, C.c_void_p]
         L.fgr_init(256)
 
@@ -336,6 +379,40 @@ class Reference:
         if self.lib.fgr_attn_rows(q.shape[0], _ptr(q), _ptr(o), _ptr(st), _ptr(en), _ptr(ck), _ptr(cv), ck.shape[1],
                                   int(kvo), ck.shape[0], hd, scale) != 0:
             raise ValueError("fgr_attn_rows failed")
+        return o
+
+    def kvq_signs(self, n: int) -> np.ndarray:
+        out = np.zeros(n, np.float32)
+        self.lib.fgr_kvq_signs(_ptr(out), n)
+        return out
+
+    def kvq_rotate(self, x, inverse: bool = False) -> np.ndarray:
+        x = np.array(x, np.float32, copy=True)
+        self.lib.fgr_kvq_rotate(_ptr(x), x.size, int(inverse))
+        return x
+
+    def kvq_quant(self, x, bits: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        rec = np.zeros(4 + x.size * bits // 8, np.uint8)
+        self.lib.fgr_kvq_quant(_ptr(x), x.size, _ptr(rec), bits)
+        return rec
+
+    def kvq_dequant(self, rec, hd: int, bits: int) -> np.ndarray:
+        rec = np.ascontiguousarray(rec, np.uint8)
+        out = np.zeros(hd, np.float32)
+        self.lib.fgr_kvq_dequant(_ptr(rec), _ptr(out), hd, bits)
+        return out
+
+    def kvq_attn_rows(self, q, st, en, kq, vq, kvh, hd, kbits, vbits, scale):
+        q = np.ascontiguousarray(q, np.float32).reshape(-1, hd)
+        kq = np.ascontiguousarray(kq, np.uint8)
+        vq = np.ascontiguousarray(vq, np.uint8)
+        st, en, kvh = (np.ascontiguousarray(a, np.int32) for a in (st, en, kvh))
+        o = np.zeros_like(q)
+        if self.lib.fgr_kvq_attn_rows(q.shape[0], _ptr(q), _ptr(o), _ptr(st), _ptr(en), _ptr(kq), _ptr(vq),
+                                      kq.shape[1], vq.shape[1], _ptr(kvh), kq.shape[0], hd, kbits, vbits,
+                                      scale) != 0:
+            raise ValueError("fgr_kvq_attn_rows failed")
         return o
 
     def gguf_table(self, path, keys, cap=64):

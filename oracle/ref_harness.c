@@ -225,3 +225,48 @@ FGR_EXPORT int fgr_attn_rows(int nr, const float *q, float *o, const int *st, co
     free(sb);
     return 0;
 }
+
+/* TurboQuant KV cache (fastgguf.c:3341-3513): the reference's own rotation, slice quantizer and
+ * the per-head attention step of forward (4760-4846) over a quantized ring cache, one row at a
+ * time. kq / vq: [cap] slots of kqs / vqs bytes; row r reads head kvh[r]'s record. q is the
+ * unrotated query; o receives the unrotated output. */
+FGR_EXPORT void fgr_kvq_signs(float *out, int n) {
+    kvq_init();
+    for (int i = 0; i < n && i < KVQ_MAX_HD; i++) out[i] = g_kvq_sign[i];
+}
+FGR_EXPORT void fgr_kvq_rotate(float *x, int n, int inverse) {
+    kvq_init();
+    if (inverse) kvq_unrotate(x, n);
+    else kvq_rotate(x, n);
+}
+FGR_EXPORT void fgr_kvq_quant(const float *x, int hd, uint8_t *rec, int bits) { kvq_quant_slice(x, hd, rec, bits); }
+FGR_EXPORT void fgr_kvq_dequant(const uint8_t *rec, float *out, int hd, int bits) { kvq_dequant_slice(rec, out, hd, bits); }
+FGR_EXPORT int fgr_kvq_attn_rows(int nr, const float *q, float *o, const int *st, const int *en, const uint8_t *kq,
+                                 const uint8_t *vq, int kqs, int vqs, const int *kvh, int cap, int hd, int kbits,
+                                 int vbits, float scale) {
+    kvq_init();
+    for (int r = 0; r < nr; r++) {
+        int n = en[r] - st[r] + 1;
+        if (n < 1 || n > cap) return -1;
+        float *qh = (float *)malloc((size_t)hd * sizeof(float));
+        float *scores = (float *)malloc((size_t)n * sizeof(float));
+        if (!qh || !scores) { free(qh); free(scores); return -1; }
+        memcpy(qh, q + (size_t)r * hd, (size_t)hd * sizeof(float));
+        kvq_rotate(qh, hd);
+        for (int p = st[r]; p <= en[r]; p++)
+            scores[p - st[r]] = kvq_dot_k(qh, kq + (size_t)(p % cap) * kqs + (size_t)kvh[r] * KVQ_REC(hd, kbits), hd,
+                                          kbits) * scale;
+        softmax_inplace(scores, n);
+        float *oh = o + (size_t)r * hd;
+        memset(oh, 0, (size_t)hd * sizeof(float));
+        for (int p = st[r]; p <= en[r]; p++) {
+            float w = scores[p - st[r]];
+            if (w == 0.0f) continue;
+            kvq_axpy_v(oh, w, vq + (size_t)(p % cap) * vqs + (size_t)kvh[r] * KVQ_REC(hd, vbits), hd, vbits);
+        }
+        kvq_unrotate(oh, hd);
+        free(qh);
+        free(scores);
+    }
+    return 0;
+}

@@ -79,6 +79,51 @@ def attn_cases(ref) -> dict:
     return out
 
 
+#: (hd, K / V heads, cap, K bits, V bits, st, en, K / V head of each row)
+KVQ_ATTN = [
+    (64, 2, 24, 4, 4, [3, 3, 10], [20, 25, 10], [0, 1, 1]),
+    (128, 1, 40, 8, 4, [30, 31], [60, 69], [0, 0]),
+    (128, 2, 17, 4, 2, [0, 5], [16, 9], [1, 0]),
+]
+
+
+def kvq_slot_bytes(hd, nkv, bits):
+    return nkv * (4 + hd * bits // 8)
+
+
+def kvq_cases(ref) -> dict:
+    rng = np.random.default_rng(88)
+    out = {"signs": ref.kvq_signs(1024).astype(np.int8)}
+    for hd in (64, 128, 256):
+        x = (rng.standard_normal(hd) * 3).astype(np.float32)
+        out[f"rot{hd}_x"] = x
+        out[f"rot{hd}_y"] = ref.kvq_rotate(x)
+        out[f"rot{hd}_inv"] = ref.kvq_rotate(x, inverse=True)
+    xs = [ref.kvq_rotate((rng.standard_normal(128) * s).astype(np.float32)) for s in (0.01, 1.0, 40.0)]
+    xs += [np.zeros(128, np.float32), (np.eye(1, 128, 7, dtype=np.float32)[0] * -5.0)]
+    xs += [ref.kvq_rotate((rng.standard_normal(128) * (1 + k)).astype(np.float32)) for k in range(40)]
+    out["quant_x"] = np.stack(xs)
+    for bits in (8, 4, 2):
+        out[f"quant_rec{bits}"] = np.stack([ref.kvq_quant(x, bits) for x in xs])
+    for i, (hd, nkv, cap, kb, vb, st, en, kvh) in enumerate(KVQ_ATTN):
+        kq = np.zeros((cap, kvq_slot_bytes(hd, nkv, kb)), np.uint8)
+        vq = np.zeros((cap, kvq_slot_bytes(hd, nkv, vb)), np.uint8)
+        for sl in range(cap):
+            for h in range(nkv):
+                k = ref.kvq_rotate(rng.standard_normal(hd).astype(np.float32))
+                v = ref.kvq_rotate(rng.standard_normal(hd).astype(np.float32))
+                kq[sl, h * (4 + hd * kb // 8):(h + 1) * (4 + hd * kb // 8)] = ref.kvq_quant(k, kb)
+                vq[sl, h * (4 + hd * vb // 8):(h + 1) * (4 + hd * vb // 8)] = ref.kvq_quant(v, vb)
+        q = (rng.standard_normal((len(st), hd)) * 2).astype(np.float32)
+        scale = np.float32(1.0 / np.sqrt(hd))
+        o = ref.kvq_attn_rows(q, st, en, kq, vq, kvh, hd, kb, vb, float(scale))
+        out.update({f"a{i}_q": q, f"a{i}_kq": kq, f"a{i}_vq": vq, f"a{i}_st": np.array(st, np.int32),
+                    f"a{i}_en": np.array(en, np.int32), f"a{i}_kvh": np.array(kvh, np.int32), f"a{i}_o": o,
+                    f"a{i}_meta": np.array([hd, nkv, kb, vb], np.int32), f"a{i}_scale": np.array([scale])})
+    out["n_attn"] = np.array([len(KVQ_ATTN)], np.int32)
+    return out
+
+
 def main() -> None:
     ref = Reference("vnni")
     print("reference build:", ref.build, "threads:", ref.threads())
@@ -171,6 +216,9 @@ def main() -> None:
                         variant_rc=np.array(list(rcs.values()), np.int32))
     # attention: the reference's attn_rows on up to 4 rows sharing one head offset, over ring caches
     np.savez_compressed(os.path.join(HERE, "attn.npz"), **attn_cases(ref))
+    # TurboQuant KV cache: the reference's rotation signs, rotations, slice records and its
+    # attention step over quantized ring caches
+    np.savez_compressed(os.path.join(HERE, "kvq.npz"), **kvq_cases(ref))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz") or f.endswith(".gguf"):
             print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

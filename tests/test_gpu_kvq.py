@@ -1,0 +1,135 @@
+"""GPU parity of the TurboQuant KV cache (fastgguf.c:3341-3513; forward's cache write 4726-4735
+and attention step 4760-4846) through the C ABI.
+
+Records and outputs are compared bit for bit: records written on the device against the
+oracle's rotation + slice quantizer (pinned to the compiled reference), the attention step
+against the reference's golden outputs and against the oracle on decode and prompt-batch ranges,
+GQA head groups, ring wrap, hd 32 .. 256 and every K / V bit width.
+"""
+import numpy as np
+import pytest
+from conftest import bits_equal
+
+from fastgguf_amd.backend import BackendError
+
+pytestmark = pytest.mark.gpu
+
+
+def rec_bytes(hd, bits):
+    return 4 + hd * bits // 8
+
+
+def oracle_cache(oracle, k, v, pos, cap, kbits, vbits):
+    """Caches written by the oracle: rows k / v [n][n_kv][hd] at positions pos."""
+    n, nkv, hd = k.shape
+    kq = np.zeros((cap, nkv * rec_bytes(hd, kbits)), np.uint8)
+    vq = np.zeros((cap, nkv * rec_bytes(hd, vbits)), np.uint8)
+    for t in range(n):
+        for h in range(nkv):
+            rk, rv = rec_bytes(hd, kbits), rec_bytes(hd, vbits)
+            kq[pos[t] % cap, h * rk:(h + 1) * rk] = oracle.kvq_quant(oracle.kvq_rotate(k[t, h]), kbits)
+            vq[pos[t] % cap, h * rv:(h + 1) * rv] = oracle.kvq_quant(oracle.kvq_rotate(v[t, h]), vbits)
+    return kq, vq
+
+
+def oracle_attention(oracle, q, kq, vq, st, en, n_kv, kbits, vbits, scale):
+    n_tok, n_head, hd = q.shape
+    g = n_head // n_kv
+    kvh = np.tile(np.arange(n_head) // g, n_tok)
+    return oracle.kvq_attn_rows(q.reshape(-1, hd), np.repeat(st, n_head), np.repeat(en, n_head), kq, vq, kvh, hd,
+                                kbits, vbits, scale).reshape(q.shape)
+
+
+@pytest.mark.parametrize("hd,kbits,vbits", [(32, 4, 4), (64, 8, 4), (128, 4, 2), (256, 8, 8), (128, 4, 4)])
+def test_store_matches_oracle(backend, oracle, hd, kbits, vbits):
+    rng = np.random.default_rng(hd + kbits + vbits)
+    nkv, cap, n = 3, 20, 7
+    k = (rng.standard_normal((n, nkv, hd)) * rng.uniform(0.01, 50, (n, nkv, 1))).astype(np.float32)
+    v = (rng.standard_normal((n, nkv, hd)) * rng.uniform(0.01, 50, (n, nkv, 1))).astype(np.float32)
+    k[0, 0] = 0.0  # a zero slice: scale 0, every code the one for 0
+    pos = np.array([0, 1, 5, 19, 20, 33, 58], np.int32)  # slots 0, 1, 5, 19, 0 (overwrite), 13, 18
+    kq0 = np.zeros((cap, nkv * rec_bytes(hd, kbits)), np.uint8)
+    vq0 = np.zeros((cap, nkv * rec_bytes(hd, vbits)), np.uint8)
+    kq, vq = backend.kvq_store(k, v, pos, kq0, vq0, kbits, vbits)
+    # the oracle writes in token order too: token 4 overwrites token 0's slot
+    wk, wv = oracle_cache(oracle, k, v, pos, cap, kbits, vbits)
+    assert np.array_equal(kq, wk)
+    assert np.array_equal(vq, wv)
+
+
+def test_attention_matches_golden(backend):
+    """The reference's own attention step over its own quantized caches: row r as a token whose
+    head kvh[r] carries the golden query."""
+    from test_oracle import kvq_attn_golden
+    rng = np.random.default_rng(4)
+    for c in kvq_attn_golden():
+        hd, nkv = c["hd"], c["nkv"]
+        nr = len(c["st"])
+        q = rng.standard_normal((nr, nkv, hd)).astype(np.float32)
+        for r in range(nr):
+            q[r, c["kvh"][r]] = c["q"][r]
+        o = backend.kvq_attention(q, c["kq"], c["vq"], c["st"], c["en"], nkv, c["kbits"], c["vbits"], c["scale"])
+        got = np.stack([o[r, c["kvh"][r]] for r in range(nr)])
+        assert bits_equal(got, c["o"]), (hd, c["kbits"], c["vbits"])
+
+
+CASES = [  # (n_tok, n_head, n_head_kv, hd, cap, first position, kbits, vbits)
+    (1, 4, 4, 32, 64, 0, 4, 4),
+    (1, 8, 2, 64, 100, 90, 8, 4),
+    (9, 8, 2, 128, 200, 180, 4, 2),
+    (3, 4, 1, 256, 70, 60, 4, 4),
+    (5, 6, 3, 128, 40, 33, 8, 8),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"t{c[0]}h{c[1]}kv{c[2]}d{c[3]}k{c[6]}v{c[7]}")
+def test_attention_matches_oracle(backend, oracle, case):
+    """Caches written on the device (checked against the oracle's), then the attention step."""
+    n_tok, n_head, n_kv, hd, cap, p0, kbits, vbits = case
+    rng = np.random.default_rng(hd + cap + kbits)
+    n_fill = cap
+    k = rng.standard_normal((n_fill, n_kv, hd)).astype(np.float32)
+    v = rng.standard_normal((n_fill, n_kv, hd)).astype(np.float32)
+    pos = np.arange(p0, p0 + n_fill, dtype=np.int32)
+    kq0 = np.zeros((cap, n_kv * rec_bytes(hd, kbits)), np.uint8)
+    vq0 = np.zeros((cap, n_kv * rec_bytes(hd, vbits)), np.uint8)
+    kq, vq = backend.kvq_store(k, v, pos, kq0, vq0, kbits, vbits)
+    wk, wv = oracle_cache(oracle, k, v, pos, cap, kbits, vbits)
+    assert np.array_equal(kq, wk) and np.array_equal(vq, wv)
+    q = (rng.standard_normal((n_tok, n_head, hd)) * 3).astype(np.float32)
+    en = (p0 + n_fill - n_tok + np.arange(n_tok)).astype(np.int32)
+    st = np.maximum(en - (cap - 1), p0).astype(np.int32)
+    if n_tok > 1:
+        st[:] = st[0]
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    o = backend.kvq_attention(q, kq, vq, st, en, n_kv, kbits, vbits, scale)
+    assert bits_equal(o, oracle_attention(oracle, q, kq, vq, st, en, n_kv, kbits, vbits, scale))
+
+
+def test_attention_long_decode(backend, oracle):
+    """Llama-3-8B shape (32 heads over 8 K / V heads, hd 128), K4 / V4 over a full 2048-slot ring,
+    and an 8-token prompt batch at its end."""
+    rng = np.random.default_rng(31)
+    cap, hd, n_head, n_kv, kb, vb = 2048, 128, 32, 8, 4, 4
+    kq = rng.integers(0, 256, (cap, n_kv * rec_bytes(hd, kb)), dtype=np.uint8)
+    vq = rng.integers(0, 256, (cap, n_kv * rec_bytes(hd, vb)), dtype=np.uint8)
+    for cache in (kq, vq):  # positive finite scales
+        for h in range(n_kv):
+            cache[:, h * 68:h * 68 + 4] = rng.uniform(0.5, 2.0, (cap, 1)).astype(np.float32).view(np.uint8)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    for n_tok in (1, 8):
+        q = rng.standard_normal((n_tok, n_head, hd)).astype(np.float32)
+        en = (5000 + np.arange(n_tok)).astype(np.int32)
+        st = np.full(n_tok, en[-1] - cap + 1, np.int32)
+        o = backend.kvq_attention(q, kq, vq, st, en, n_kv, kb, vb, scale)
+        assert bits_equal(o, oracle_attention(oracle, q, kq, vq, st, en, n_kv, kb, vb, scale))
+
+
+def test_refusals(backend):
+    rng = np.random.default_rng(5)
+    k = rng.standard_normal((1, 1, 96)).astype(np.float32)
+    with pytest.raises(BackendError):  # hd not a power of 2
+        backend.kvq_store(k, k, [0], np.zeros((4, 52), np.uint8), np.zeros((4, 52), np.uint8), 4, 4)
+    k = rng.standard_normal((1, 1, 64)).astype(np.float32)
+    with pytest.raises(BackendError):  # 2-bit keys: the reference has none
+        backend.kvq_store(k, k, [0], np.zeros((4, 20), np.uint8), np.zeros((4, 20), np.uint8), 2, 2)

@@ -270,7 +270,8 @@ MUTANTS = {1: "hsum8 order", 2: "MoE accumulate without fma", 3: "reciprocal ins
            4: "Q6_K half-lane scale", 5: "Q4_K repacked single chain", 6: "Q4_K GEMM integer epilogue",
            7: "Q5_0 fifth bit from the wrong half of qh", 8: "Q5_K qh bit pairing",
            9: "Q4_1 / Q5_1 min term without the fused multiply-add",
-           10: "attention score lanes added in sequence", 11: "softmax tail through exp_neg_ps"}
+           10: "attention score lanes added in sequence", 11: "softmax tail through exp_neg_ps",
+           12: "TurboQuant key dot without the contraction", 13: "TurboQuant scale from an fma chain"}
 
 
 @pytest.fixture(scope="module")
@@ -307,7 +308,80 @@ def _golden_failures(o: Oracle) -> int:
     for c in attn_golden():
         fails += not bits_equal(o.attn_rows(c["q"], c["st"], c["en"], c["ck"], c["cv"], [c["kvo"]] * len(c["st"]),
                                             c["hd"], c["scale"]), c["o"])
+    fails += kvq_golden_failures(o)
     return fails
+
+
+def kvq_attn_golden() -> list[dict]:
+    g = golden("kvq.npz")
+    out = []
+    for i in range(int(g["n_attn"][0])):
+        hd, nkv, kb, vb = (int(v) for v in g[f"a{i}_meta"])
+        out.append(dict(q=g[f"a{i}_q"], kq=g[f"a{i}_kq"], vq=g[f"a{i}_vq"], st=g[f"a{i}_st"], en=g[f"a{i}_en"],
+                        kvh=g[f"a{i}_kvh"], o=g[f"a{i}_o"], hd=hd, nkv=nkv, kbits=kb, vbits=vb,
+                        scale=float(g[f"a{i}_scale"][0])))
+    return out
+
+
+def kvq_golden_failures(o: Oracle) -> int:
+    g = golden("kvq.npz")
+    fails = int(not np.array_equal(o.kvq_signs(1024), g["signs"].astype(np.float32)))
+    for hd in (64, 128, 256):
+        fails += not bits_equal(o.kvq_rotate(g[f"rot{hd}_x"]), g[f"rot{hd}_y"])
+        fails += not bits_equal(o.kvq_rotate(g[f"rot{hd}_x"], inverse=True), g[f"rot{hd}_inv"])
+    for bits in (8, 4, 2):
+        for x, rec in zip(g["quant_x"], g[f"quant_rec{bits}"]):
+            fails += not np.array_equal(o.kvq_quant(x, bits), rec)
+    for c in kvq_attn_golden():
+        fails += not bits_equal(o.kvq_attn_rows(c["q"], c["st"], c["en"], c["kq"], c["vq"], c["kvh"], c["hd"],
+                                                c["kbits"], c["vbits"], c["scale"]), c["o"])
+    return fails
+
+
+def test_kvq_golden(oracle):
+    """TurboQuant restated (signs, rotation, slice records, attention step), bit for bit against
+    the compiled reference's outputs."""
+    assert kvq_golden_failures(oracle) == 0
+
+
+def test_kvq_against_the_mathematics(oracle):
+    """The reference's own selftest relations (fastgguf.c:6035-6105) and what the mathematics
+    fixes: the rotation is orthogonal (norms and dot products kept, the inverse undoes it within
+    1e-5), the signs are +-1, K4 / V2 / K8 reconstruction errors stay within the selftest's
+    bounds (0.15 / 0.45 / 0.01), and a record decodes to the scale times the centroid of each code."""
+    rng = np.random.default_rng(21)
+    assert set(np.unique(oracle.kvq_signs(1024))) == {-1.0, 1.0}
+    for hd in (32, 128, 1024):
+        x, y = (rng.standard_normal(hd).astype(np.float32) for _ in range(2))
+        rx, ry = oracle.kvq_rotate(x), oracle.kvq_rotate(y)
+        assert abs(np.linalg.norm(rx) - np.linalg.norm(x)) < 1e-5 * np.linalg.norm(x)
+        assert abs(float(rx @ ry) - float(x @ y)) < 1e-4 * np.linalg.norm(x) * np.linalg.norm(y)
+        back = oracle.kvq_rotate(rx, inverse=True)
+        assert np.linalg.norm(back - x) < 1e-5 * np.linalg.norm(x)
+        # one basis vector: R e_j = sign_j * (column j of H) / sqrt(n), every entry +-1/sqrt(n)
+        e = np.zeros(hd, np.float32)
+        e[3] = 1.0
+        assert np.allclose(np.abs(oracle.kvq_rotate(e)), 1 / np.sqrt(hd), rtol=1e-6)
+    c4 = np.array([-2.7326, -2.0690, -1.6181, -1.2562, -0.9424, -0.6568, -0.3881, -0.1284,
+                   0.1284, 0.3881, 0.6568, 0.9424, 1.2562, 1.6181, 2.0690, 2.7326], np.float32)
+    c2 = np.array([-1.5104, -0.4528, 0.4528, 1.5104], np.float32)
+    for bits, bound in ((4, 0.15), (2, 0.45), (8, 0.01)):
+        x = oracle.kvq_rotate(rng.standard_normal(128).astype(np.float32))
+        rec = oracle.kvq_quant(x, bits)
+        s = rec[:4].view(np.float32)[0]
+        q = rec[4:]
+        if bits == 8:
+            dq = s * q.view(np.int8).astype(np.float32)
+        elif bits == 4:
+            dq = s * c4[np.stack([q & 15, q >> 4], 1).reshape(-1)]
+        else:
+            dq = s * c2[np.stack([(q >> (2 * k)) & 3 for k in range(4)], 1).reshape(-1)]
+            # every code is the nearest centroid of x / s
+            assert np.all(np.abs(x / s - dq / s) <= np.min(np.abs((x / s)[:, None] - c2[None, :]), 1) + 1e-6)
+        assert np.linalg.norm(dq - x) / np.linalg.norm(x) < bound
+
+
+@pytest.mark.parametrize("mutant", sorted(MUTANTS))
 
 
 def attn_golden() -> list[dict]:
