@@ -135,8 +135,10 @@ def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
 def attention_config(be, kernel_time, enabled: int, cpu: bool) -> dict | None:
     """Attention over the fp32 KV ring cache (attn_rows, fastgguf.c:3273-3326) at Llama-3-8B's shape
     (32 query heads over 8 K / V heads, hd 128): one decode token over 4096 positions, and a 64-token
-    prompt batch at the end of a 4096-position context. With cpu, the reference's attn_rows (oracle/_ref,
-    one thread) on the decode case, its 4-row calls per K / V head as the reference's forward makes."""
+    prompt batch at the end of a 4096-position context; then the same over TurboQuant K4 / V4 caches
+    (fastgguf.c:3341-3513) written from the same rows. With cpu, the reference (oracle/_ref, one
+    thread) on each decode case: attn_rows in 4-row calls per K / V head as its forward makes,
+    and its TurboQuant attention step per head."""
     if not enabled:
         return None
     import numpy as np
@@ -180,8 +182,48 @@ def attention_config(be, kernel_time, enabled: int, cpu: bool) -> dict | None:
                 print(f"[bench] attention cpu reference skipped: {e}", file=sys.stderr)
         for b in bufs:
             be.dev_free(b)
-    be.dev_free(kd)
-    be.dev_free(vd)
+    # TurboQuant K4 / V4 caches written from the same K / V rows (the cache write timed per token
+    # and per 64-token batch), then the same two attention calls over them
+    kb, vb = 4, 4
+    kqs, vqs = nkv * (4 + hd * kb // 8), nkv * (4 + hd * vb // 8)
+    kqd, vqd = be.dev_alloc(cap * kqs), be.dev_alloc(cap * vqs)
+    posd = be.dev_alloc(4 * cap)
+    be.h2d(posd, np.arange(cap, dtype=np.int32))
+    be.kvq_store_dev(cap, nkv, hd, kb, vb, kd, vd, kv_dim, kqd, vqd, cap, posd)
+    for nt in (1, 64):
+        us = kernel_time(lambda i: be.kvq_store_dev(nt, nkv, hd, kb, vb, kd, vd, kv_dim, kqd, vqd, cap, posd), 100)
+        out[f"turbo_k4v4_store_{nt}tok"] = {"us": round(us, 2)}
+    for name, nt in (("turbo_k4v4_decode_4096", 1), ("turbo_k4v4_prefill_64_at_4096", 64)):
+        q = rng.standard_normal((nt, nh, hd)).astype(np.float32)
+        en = (10000 + np.arange(nt)).astype(np.int32)
+        st = (en[-1] - cap + 1) * np.ones(nt, np.int32)
+        bufs = [be.dev_alloc(a.nbytes) for a in (q, q, st, en)]
+        for b, a in zip(bufs, (q, q, st, en)):
+            be.h2d(b, a)
+        n_max = int((en - st).max()) + 1
+        us = kernel_time(lambda i: be.kvq_attention_dev(nt, nh, nkv, hd, kb, vb, bufs[0], bufs[1], kqd, vqd, cap,
+                                                        bufs[2], bufs[3], n_max, scale), 100)
+        out[name] = {"us": round(us, 2), "cache_bytes": n_max * (kqs + vqs)}
+        if cpu and nt == 1:
+            try:
+                sys.path.insert(0, os.path.join(ROOT, "oracle"))
+                from oracle import Reference
+                ref = Reference()
+                kq, vq = np.zeros((cap, kqs), np.uint8), np.zeros((cap, vqs), np.uint8)
+                be.d2h(kq, kqd)
+                be.d2h(vq, vqd)
+                kvh = np.arange(nh) // (nh // nkv)
+                t0 = time.perf_counter()
+                reps = 3
+                for _ in range(reps):
+                    ref.kvq_attn_rows(q[0], np.repeat(st, nh), np.repeat(en, nh), kq, vq, kvh, hd, kb, vb, scale)
+                out[name]["cpu_reference_1thread_us"] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+            except (FileNotFoundError, OSError) as e:
+                print(f"[bench] turbo cpu reference skipped: {e}", file=sys.stderr)
+        for b in bufs:
+            be.dev_free(b)
+    for b in (kqd, vqd, posd, kd, vd):
+        be.dev_free(b)
     return out
 
 

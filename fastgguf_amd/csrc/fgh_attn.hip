@@ -142,7 +142,8 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a, int n_tok)
 }
 
 // softmax: one workgroup per row, in place over the row's scores. A row of up to SM_RES positions
-// stays in LDS from its one load to its one store: maximum, exponentials, lanes 0..7 of
+// stays in LDS (sized min(max_len, SM_RES) at launch, so short rows leave room for more
+// workgroups per CU) from its one load to its one store: maximum, exponentials, lanes 0..7 of
 // wavefront 0 running the 8 ordered sums, then every value times 1 / sum. Longer rows go
 // through LDS SM_RES positions at a time, the 8 sums carried across the chunks.
 constexpr int SM_RES = 12288;
@@ -164,7 +165,7 @@ __device__ __forceinline__ float lane_sum(const float *e, int ng, int l, float v
     return v;
 }
 __global__ __launch_bounds__(256) void attn_softmax_kernel(AttnArgs a) {
-    __shared__ float e[SM_RES];
+    extern __shared__ float e[];  // min(max_len, SM_RES) values
     __shared__ float red[4];
     __shared__ float total;
     const int row = blockIdx.x, tok = row / a.n_head, tid = threadIdx.x;
@@ -419,7 +420,7 @@ hipError_t launch_attention(const AttnArgs &a, int n_tok, hipStream_t s) {
         attn_scores_kernel<16><<<dim3(kb, (unsigned)((rows_kv + 15) / 16), kvh.z), 256, 0, s>>>(a, n_tok);
     else
         attn_scores_kernel<4><<<dim3(kb, (unsigned)((rows_kv + 3) / 4), kvh.z), 256, 0, s>>>(a, n_tok);
-    attn_softmax_kernel<<<n_tok * a.n_head, 256, 0, s>>>(a);
+    attn_softmax_kernel<<<n_tok * a.n_head, 256, (size_t)std::min(a.max_len, SM_RES) * 4, s>>>(a);
     const unsigned cch = (unsigned)((a.hd + 63) / 64);
     if (rows_kv >= 64)  // enough groups of 16 to fill the chip: 4 chains per lane
         attn_values_kernel<4, 4><<<dim3(cch, (unsigned)((rows_kv + 15) / 16), kvh.z), 256, 0, s>>>(a, n_tok);

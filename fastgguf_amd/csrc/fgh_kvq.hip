@@ -89,8 +89,9 @@ __global__ __launch_bounds__(256) void kvq_store_kernel(KvqStoreArgs a, int n_to
     __shared__ float sc[2];
     const int tok = blockIdx.x, kh = blockIdx.y, isv = blockIdx.z, tid = threadIdx.x, hd = a.hd;
     const int64_t my_slot = slot_of(a.pos[tok], a.cap);
-    for (int t = tok + 1; t < n_tok; ++t)
-        if (slot_of(a.pos[t], a.cap) == my_slot) return;  // the whole workgroup
+    bool later = false;
+    for (int t = tok + 1 + tid; t < n_tok; t += 256) later |= slot_of(a.pos[t], a.cap) == my_slot;
+    if (__syncthreads_or(later)) return;  // the whole workgroup
     const int bits = isv ? a.vbits : a.kbits;
     const float *src = (isv ? a.v : a.k) + (size_t)tok * a.stride + (size_t)kh * hd;
     for (int i = tid; i < hd; i += 256) x[i] = src[i];
@@ -143,47 +144,92 @@ __device__ __forceinline__ int kvq_row_len(const KvqAttnArgs &a, int tok) {
     return n >= 1 && n <= a.cap && n <= a.max_len ? n : 0;
 }
 
-// scores: grid (key blocks, rows), 256 threads; thread = one key: kvq_dot_k's order, times s,
-// times scale
-__global__ __launch_bounds__(256) void kvq_scores_kernel(KvqAttnArgs a) {
-    __shared__ float q[256];
-    __shared__ float c4[16];
-    const int row = blockIdx.y, tok = row / a.n_head, h = row - tok * a.n_head, tid = threadIdx.x;
-    const int n = kvq_row_len(a, tok);
-    if ((int)blockIdx.x * 256 >= n) return;
-    for (int i = tid; i < a.hd; i += 256) q[i] = a.qr[(size_t)row * a.hd + i];
-    if (tid < 16) c4[tid] = kvq_c4[tid];
-    __syncthreads();
-    const int k = (int)blockIdx.x * 256 + tid;
-    if (k >= n) return;
-    const int kvh = h / (a.n_head / a.n_head_kv), rec = 4 + a.hd * a.kbits / 8;
-    const uint8_t *r = a.kq + slot_of(a.st[tok] + k, a.cap) * (int64_t)(a.n_head_kv * rec) + (int64_t)kvh * rec;
-    const float s = *(const float *)r;
-    const uint32_t *w = (const uint32_t *)(r + 4);
-    float acc = 0.0f;
-    if (a.kbits == 8) {
-        for (int i = 0; i < a.hd; i += 4) {
-            const uint32_t v = w[i / 4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc = __builtin_fmaf(q[i + j], (float)(int8_t)(v >> (8 * j)), acc);
-        }
-    } else {
-        for (int i = 0; i < a.hd; i += 8) {
-            const uint32_t v = w[i / 8];
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                const float hi = q[i + j + 1] * c4[(v >> (4 * j + 4)) & 15];
-                acc = acc + __builtin_fmaf(q[i + j], c4[(v >> (4 * j)) & 15], hi);
-            }
+// Groups of R rows that read one K / V head kh: j = R q .. R q + R - 1 of the head's n_tok * G
+// rows, j = t * G + g (token t, query head kh * G + g); the scores of a group run over the union
+// of its rows' ranges and are stored for each row's own range.
+struct KvqRow {
+    int row, st, en;  // row = -1: no such row; en < st: no valid range
+};
+__device__ __forceinline__ KvqRow kvq_group_row(const KvqAttnArgs &a, int n_tok, int R, int grp, int kh, int r) {
+    const int G = a.n_head / a.n_head_kv, j = grp * R + r;
+    KvqRow g{-1, 0, -1};
+    if (j < n_tok * G) {
+        const int t = j / G;
+        g.row = t * a.n_head + kh * G + (j - t * G);
+        if (kvq_row_len(a, t) > 0) {
+            g.st = a.st[t];
+            g.en = a.en[t];
         }
     }
-    a.s[(size_t)row * a.max_len + k] = acc * s * a.scale;
+    return g;
+}
+
+// scores: grid (key blocks, groups of R rows, K / V heads), 256 threads; thread = one key of the
+// group's union for its R rows: each record's codes are loaded and looked up once for R chains
+// in kvq_dot_k's order, then times s, times scale. R = 16 for prompt batches.
+template <int R>
+__global__ __launch_bounds__(256) void kvq_scores_kernel(KvqAttnArgs a, int n_tok) {
+    __shared__ float q[R][256];
+    __shared__ float c4[16];
+    const int grp = blockIdx.y, kh = blockIdx.z, tid = threadIdx.x, hd = a.hd;
+    int lo = 0x7fffffff, hi = -0x7fffffff;
+    for (int r = 0; r < R; ++r) {
+        const KvqRow g = kvq_group_row(a, n_tok, R, grp, kh, r);
+        if (g.en >= g.st) {
+            lo = min(lo, g.st);
+            hi = max(hi, g.en);
+        }
+    }
+    if (hi < lo) return;
+    for (int i = tid; i < R * hd; i += 256) {
+        const int r = i / hd, x = i - r * hd;
+        const KvqRow g = kvq_group_row(a, n_tok, R, grp, kh, r);
+        q[r][x] = g.en >= g.st ? a.qr[(size_t)g.row * hd + x] : 0.0f;
+    }
+    if (tid < 16) c4[tid] = kvq_c4[tid];
+    __syncthreads();
+    const int rec = 4 + hd * a.kbits / 8;
+    for (int p = lo + (int)blockIdx.x * 256 + tid; p <= hi; p += (int)gridDim.x * 256) {
+        const uint8_t *rp = a.kq + slot_of(p, a.cap) * (int64_t)(a.n_head_kv * rec) + (int64_t)kh * rec;
+        const float s = *(const float *)rp;
+        const uint32_t *w = (const uint32_t *)(rp + 4);
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        if (a.kbits == 8) {
+            for (int i = 0; i < hd; i += 4) {
+                const uint32_t v = w[i / 4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float c = (float)(int8_t)(v >> (8 * j));
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[r] = __builtin_fmaf(q[r][i + j], c, acc[r]);
+                }
+            }
+        } else {
+            for (int i = 0; i < hd; i += 8) {
+                const uint32_t v = w[i / 8];
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const float clo = c4[(v >> (4 * j)) & 15], chi = c4[(v >> (4 * j + 4)) & 15];
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        acc[r] = acc[r] + __builtin_fmaf(q[r][i + j], clo, q[r][i + j + 1] * chi);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const KvqRow g = kvq_group_row(a, n_tok, R, grp, kh, r);
+            if (p >= g.st && p <= g.en) a.s[(size_t)g.row * a.max_len + (p - g.st)] = acc[r] * s * a.scale;
+        }
+    }
 }
 
 // softmax_inplace over each row's scores, then each weight times its position's V scale
 constexpr int KVQ_RES = 12288;
 __global__ __launch_bounds__(256) void kvq_softmax_kernel(KvqAttnArgs a) {
-    __shared__ float e[KVQ_RES];
+    extern __shared__ float e[];  // min(max_len, KVQ_RES) values: rows up to that length stay in LDS
     __shared__ float red[4];
     __shared__ float total;
     const int row = blockIdx.x, tok = row / a.n_head, h = row - tok * a.n_head, tid = threadIdx.x;
@@ -203,16 +249,16 @@ __global__ __launch_bounds__(256) void kvq_softmax_kernel(KvqAttnArgs a) {
         else s[i] = ev;
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0) {  // the sum in order: 32 values loaded ahead of their adds
         float sum = 0.0f;
         const float *src = resident ? e : s;
         int i = 0;
-        for (; i + 8 <= n; i += 8) {
-            float t[8];
+        for (; i + 32 <= n; i += 32) {
+            float t[32];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) t[u] = src[i + u];
+            for (int u = 0; u < 32; ++u) t[u] = src[i + u];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) sum += t[u];
+            for (int u = 0; u < 32; ++u) sum += t[u];
         }
         for (; i < n; ++i) sum += src[i];
         total = sum;
@@ -230,33 +276,48 @@ __global__ __launch_bounds__(256) void kvq_softmax_kernel(KvqAttnArgs a) {
 }
 
 // V codes of the positions min st .. max en (every K / V head) as their centroids, unscaled,
-// into vc[slot][kvh * hd + i]; grid-stride over positions, one thread per 4 values
+// into vc[slot][kvh * hd + i]: a workgroup per position (grid-stride), a thread per 4 values
 __global__ __launch_bounds__(256) void kvq_expand_kernel(KvqAttnArgs a, int n_tok) {
-    int lo = 0x7fffffff, hi = -0x7fffffff;
-    for (int t = 0; t < n_tok; ++t)
+    __shared__ int span[2][4];
+    int lo = 0x7fffffff, hi = -0x7fffffff;  // the tokens' ranges, scanned by all the threads
+    for (int t = threadIdx.x; t < n_tok; t += 256)
         if (kvq_row_len(a, t) > 0) {
             lo = min(lo, a.st[t]);
             hi = max(hi, a.en[t]);
         }
-    if (hi < lo) return;
-    const int hd = a.hd, rec = 4 + hd * a.vbits / 8, kv_dim = a.n_head_kv * hd, per_pos = kv_dim / 4;
-    const int64_t total = (int64_t)(hi - lo + 1) * per_pos;
-    for (int64_t w = (int64_t)blockIdx.x * 256 + threadIdx.x; w < total; w += (int64_t)gridDim.x * 256) {
-        const int p = lo + (int)(w / per_pos), c = (int)(w % per_pos) * 4, kvh = c / hd, i = c - kvh * hd;
+    for (int o = 1; o < 64; o <<= 1) {
+        lo = min(lo, __shfl_xor(lo, o, 64));
+        hi = max(hi, __shfl_xor(hi, o, 64));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        span[0][threadIdx.x >> 6] = lo;
+        span[1][threadIdx.x >> 6] = hi;
+    }
+    __syncthreads();
+    lo = min(min(span[0][0], span[0][1]), min(span[0][2], span[0][3]));
+    hi = max(max(span[1][0], span[1][1]), max(span[1][2], span[1][3]));
+    const int hd = a.hd, rec = 4 + hd * a.vbits / 8, kv_dim = a.n_head_kv * hd;
+    for (int p = lo + (int)blockIdx.x; p <= hi; p += (int)gridDim.x) {
         const int64_t slot = slot_of(p, a.cap);
-        const uint8_t *codes = a.vq + slot * (int64_t)(a.n_head_kv * rec) + (int64_t)kvh * rec + 4;
-        float4 o;
-        if (a.vbits == 8) {
-            const uint32_t v = *(const uint32_t *)(codes + i);
-            o = make_float4((float)(int8_t)v, (float)(int8_t)(v >> 8), (float)(int8_t)(v >> 16), (float)(int8_t)(v >> 24));
-        } else if (a.vbits == 4) {
-            const uint32_t v = codes[i / 2] | (uint32_t)codes[i / 2 + 1] << 8;
-            o = make_float4(kvq_c4[v & 15], kvq_c4[(v >> 4) & 15], kvq_c4[(v >> 8) & 15], kvq_c4[(v >> 12) & 15]);
-        } else {
-            const uint32_t v = codes[i / 4];
-            o = make_float4(kvq_c2[v & 3], kvq_c2[(v >> 2) & 3], kvq_c2[(v >> 4) & 3], kvq_c2[(v >> 6) & 3]);
+        const uint8_t *srec = a.vq + slot * (int64_t)(a.n_head_kv * rec);
+        float *dst = a.vc + slot * (int64_t)kv_dim;
+        for (int c = threadIdx.x * 4; c < kv_dim; c += 1024) {
+            const int kvh = c / hd, i = c - kvh * hd;
+            const uint8_t *codes = srec + kvh * rec + 4;
+            float4 o;
+            if (a.vbits == 8) {
+                const uint32_t v = *(const uint32_t *)(codes + i);
+                o = make_float4((float)(int8_t)v, (float)(int8_t)(v >> 8), (float)(int8_t)(v >> 16),
+                                (float)(int8_t)(v >> 24));
+            } else if (a.vbits == 4) {
+                const uint32_t v = *(const uint16_t *)(codes + i / 2);
+                o = make_float4(kvq_c4[v & 15], kvq_c4[(v >> 4) & 15], kvq_c4[(v >> 8) & 15], kvq_c4[(v >> 12) & 15]);
+            } else {
+                const uint32_t v = codes[i / 4];
+                o = make_float4(kvq_c2[v & 3], kvq_c2[(v >> 2) & 3], kvq_c2[(v >> 4) & 3], kvq_c2[(v >> 6) & 3]);
+            }
+            *(float4 *)(dst + c) = o;
         }
-        *(float4 *)(a.vc + slot * (int64_t)kv_dim + c) = o;
     }
 }
 
@@ -277,10 +338,14 @@ hipError_t launch_kvq_attention(const KvqAttnArgs &a, int n_tok, hipStream_t s) 
         a.max_len < 1 || rows > 65535)
         return hipErrorInvalidValue;
     kvq_rotate_kernel<<<rows, 256, 0, s>>>(a.q, a.qr, a.hd, false);
-    kvq_scores_kernel<<<dim3((unsigned)((a.max_len + 255) / 256), (unsigned)rows), 256, 0, s>>>(a);
-    kvq_softmax_kernel<<<rows, 256, 0, s>>>(a);
-    kvq_expand_kernel<<<(unsigned)std::min<int64_t>(4096, ((int64_t)(a.max_len + n_tok) * a.n_head_kv * a.hd / 4 + 255) / 256),
-                        256, 0, s>>>(a, n_tok);
+    const int rows_kv = n_tok * (a.n_head / a.n_head_kv);
+    const unsigned kb = (unsigned)std::min((a.max_len + 255) / 256, 1024);
+    if (rows_kv >= 16)
+        kvq_scores_kernel<16><<<dim3(kb, (unsigned)((rows_kv + 15) / 16), (unsigned)a.n_head_kv), 256, 0, s>>>(a, n_tok);
+    else
+        kvq_scores_kernel<4><<<dim3(kb, (unsigned)((rows_kv + 3) / 4), (unsigned)a.n_head_kv), 256, 0, s>>>(a, n_tok);
+    kvq_softmax_kernel<<<rows, 256, (size_t)std::min(a.max_len, KVQ_RES) * 4, s>>>(a);
+    kvq_expand_kernel<<<(unsigned)std::min(4096, a.max_len + n_tok), 256, 0, s>>>(a, n_tok);
     AttnArgs v{nullptr, a.orot, nullptr, a.vc, a.s, a.st, a.en, a.n_head, a.n_head_kv, a.hd,
                a.n_head_kv * a.hd, a.cap, a.max_len, 1.0f};
     hipError_t e = launch_attention_values(v, n_tok, s);
