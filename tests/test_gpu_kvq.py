@@ -125,6 +125,34 @@ def test_attention_long_decode(backend, oracle):
         assert bits_equal(o, oracle_attention(oracle, q, kq, vq, st, en, n_kv, kb, vb, scale))
 
 
+def test_attention_dev_bad_rows_are_nan(backend, oracle):
+    """On device pointers a token whose range is empty or longer than max_len gets NaN outputs;
+    the other tokens are unaffected."""
+    rng = np.random.default_rng(41)
+    cap, hd, n_head, n_kv, kb, vb = 64, 64, 4, 2, 4, 4
+    k = rng.standard_normal((cap, n_kv, hd)).astype(np.float32)
+    kq0 = np.zeros((cap, n_kv * rec_bytes(hd, kb)), np.uint8)
+    kq, vq = backend.kvq_store(k, k[::-1].copy(), np.arange(cap, dtype=np.int32), kq0, kq0.copy(), kb, vb)
+    q = rng.standard_normal((4, n_head, hd)).astype(np.float32)
+    st = np.array([0, 10, 20, 5], np.int32)
+    en = np.array([9, 9, 60, 30], np.int32)  # token 1 empty, token 2 longer than max_len 32
+    bufs = [backend.dev_alloc(a.nbytes) for a in (q, q, kq, vq, st, en)]
+    try:
+        for b, a in zip(bufs, (q, q, kq, vq, st, en)):
+            backend.h2d(b, a)
+        backend.kvq_attention_dev(4, n_head, n_kv, hd, kb, vb, bufs[0], bufs[1], bufs[2], bufs[3], cap, bufs[4],
+                                  bufs[5], 32, 0.125)
+        o = np.empty_like(q)
+        backend.d2h(o, bufs[1])
+    finally:
+        for b in bufs:
+            backend.dev_free(b)
+    assert np.all(np.isnan(o[1])) and np.all(np.isnan(o[2]))
+    for t in (0, 3):
+        want = oracle_attention(oracle, q[t:t + 1], kq, vq, st[t:t + 1], en[t:t + 1], n_kv, kb, vb, 0.125)
+        assert bits_equal(o[t:t + 1], want)
+
+
 def test_refusals(backend):
     rng = np.random.default_rng(5)
     k = rng.standard_normal((1, 1, 96)).astype(np.float32)
