@@ -161,3 +161,67 @@ def test_refusals(backend):
     k = rng.standard_normal((1, 1, 64)).astype(np.float32)
     with pytest.raises(BackendError):  # 2-bit keys: the reference has none
         backend.kvq_store(k, k, [0], np.zeros((4, 20), np.uint8), np.zeros((4, 20), np.uint8), 2, 2)
+
+
+def test_attention_graph_replays(backend, oracle):
+    """fp32 and TurboQuant attention captured in one HIP graph: every replay, with eager calls in
+    between, equals the eager result bit for bit (no entry point records a memset)."""
+    rng = np.random.default_rng(51)
+    cap, hd, n_head, n_kv, kb, vb = 256, 64, 8, 2, 4, 2
+    kv_dim = n_kv * hd
+    ck = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+    cv = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+    q = rng.standard_normal((3, n_head, hd)).astype(np.float32)
+    st = np.array([100, 100, 100], np.int32)
+    en = np.array([300, 301, 302], np.int32)
+    pos = np.arange(103, 103 + cap, dtype=np.int32)
+    kq0 = np.zeros((cap, n_kv * rec_bytes(hd, kb)), np.uint8)
+    vq0 = np.zeros((cap, n_kv * rec_bytes(hd, vb)), np.uint8)
+    kq, vq = backend.kvq_store(ck.reshape(cap, n_kv, hd), cv.reshape(cap, n_kv, hd), pos, kq0, vq0, kb, vb)
+    arrays = (q, q, q, ck, cv, kq, vq, st, en)
+    b = [backend.dev_alloc(a.nbytes) for a in arrays]
+    try:
+        for d, a in zip(b, arrays):
+            backend.h2d(d, a)
+        max_len = int((en - st).max()) + 1
+
+        def calls():
+            backend.attention_dev(3, n_head, n_kv, hd, b[0], b[1], b[3], b[4], kv_dim, cap, b[7], b[8], max_len, 0.125)
+            backend.kvq_attention_dev(3, n_head, n_kv, hd, kb, vb, b[0], b[2], b[5], b[6], cap, b[7], b[8], max_len,
+                                      0.125)
+
+        calls()  # eager: grows the scratch buffers before capture
+        backend.sync()
+        want1, want2 = np.empty_like(q), np.empty_like(q)
+        backend.d2h(want1, b[1])
+        backend.d2h(want2, b[2])
+        assert bits_equal(want1, oracle_attention_fp32(oracle, q, ck, cv, st, en, n_kv, 0.125))
+        assert bits_equal(want2, oracle_attention(oracle, q, kq, vq, st, en, n_kv, kb, vb, 0.125))
+        backend.graph_begin()
+        calls()
+        g = backend.graph_end()
+        try:
+            for _ in range(3):
+                zero = np.zeros_like(q)
+                backend.h2d(b[1], zero)
+                backend.h2d(b[2], zero)
+                backend.graph_launch(g)
+                backend.sync()
+                got1, got2 = np.empty_like(q), np.empty_like(q)
+                backend.d2h(got1, b[1])
+                backend.d2h(got2, b[2])
+                assert bits_equal(got1, want1) and bits_equal(got2, want2)
+                calls()  # eager work between replays
+                backend.sync()
+        finally:
+            backend.graph_destroy(g)
+    finally:
+        for d in b:
+            backend.dev_free(d)
+
+
+def oracle_attention_fp32(oracle, q, ck, cv, st, en, n_kv, scale):
+    n_tok, n_head, hd = q.shape
+    kvo = np.tile(np.arange(n_head) // (n_head // n_kv) * hd, n_tok)
+    return oracle.attn_rows(q.reshape(-1, hd), np.repeat(st, n_head), np.repeat(en, n_head), ck, cv, kvo, hd,
+                            scale).reshape(q.shape)
