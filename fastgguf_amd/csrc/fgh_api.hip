@@ -33,7 +33,7 @@ struct fgh_ctx {
     DevBuf x, y, aqs, ad, abs;
     DevBuf gq, gy, gb;  // prompt-GEMM activations (launch_gemm_quant layout)
     DevBuf as;          // attention scores / weights
-    DevBuf kqr, kor, kvc;  // TurboQuant attention: rotated queries, rotated outputs, V centroids
+    DevBuf kqr, kor;    // TurboQuant attention: rotated queries, rotated outputs
     DevBuf msel, mw, mg, mu, md, mlog;  // MoE: selection, weights, gate / up / down outputs
     DevBuf mseg, mslot, mimx, mimh;         // MoE: slots grouped by expert, Q8_K images of x and h
     DevBuf ck;                              // fgh_checksum_dev: per-workgroup partial sums
@@ -254,7 +254,7 @@ void fgh_close(fgh_ctx *c) {
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->gy, &c->gb, &c->msel, &c->mw, &c->mg,
                       &c->mu, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck, &c->as, &c->kqr,
-                      &c->kor, &c->kvc})
+                      &c->kor})
         if (b->p) (void)hipFree(b->p);
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -545,10 +545,10 @@ int fgh_kvq_attention_dev(fgh_ctx *c, int n_tok, int n_head, int n_head_kv, int 
     const size_t rows = (size_t)n_tok * n_head;
     int rc;
     if ((rc = grow(c, c->as, rows * max_len * 4)) || (rc = grow(c, c->kqr, rows * hd * 4)) ||
-        (rc = grow(c, c->kor, rows * hd * 4)) || (rc = grow(c, c->kvc, (size_t)cap * n_head_kv * hd * 4)))
+        (rc = grow(c, c->kor, rows * hd * 4)))
         return rc;
-    fgh::KvqAttnArgs a{q,  o,  (float *)c->kqr.p, (float *)c->kor.p, (float *)c->as.p, (float *)c->kvc.p, kq, vq, st,
-                       en, n_head, n_head_kv, hd, kbits, vbits, cap, max_len, scale};
+    fgh::KvqAttnArgs a{q,  o,  (float *)c->kqr.p, (float *)c->kor.p, (float *)c->as.p, kq, vq, st, en,
+                       n_head, n_head_kv, hd, kbits, vbits, cap, max_len, scale};
     HIP_TRY(c, fgh::launch_kvq_attention(a, n_tok, c->stream));
     return FGH_OK;
 }

@@ -248,15 +248,19 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(AttnArgs a) {
 typedef float av4 __attribute__((ext_vector_type(4)));  // a native vector: kept in registers when staged
 template <int CH>
 struct AvStage {
-    av4 v0, v1, v2, v3;
+    av4 v0, v1, v2, v3;  // fp32 V: 4 columns at each of the thread's 4 positions
+    uint32_t k0, k1, k2, k3;  // TurboQuant V: the same values' raw codes
     av4 w;  // CH = 4: 4 positions of one row; CH = 1: .x only
 };
-template <int CH, int AV_S>  // AV_S: tiles in flight, 4 or 8 (the named stages below)
+// VB = 0: V in fp32 (a.v); VB = 2, 4, 8: V as TurboQuant records (a.vq), decoded to centroids
+// (int8 codes for VB = 8) through an LDS table when a tile is stored
+template <int CH, int AV_S, int VB>  // AV_S: tiles in flight, 4 or 8 (the named stages below)
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_values_kernel(AttnArgs a,
                                                                                                      int n_tok) {
     constexpr int GR = 4 * CH;  // rows per group
     __shared__ av4 vt[2][64][16];
     __shared__ __attribute__((aligned(16))) float wt[2][64 * GR];
+    __shared__ float ctab[16];
     const int grp = blockIdx.y, kh = blockIdx.z, cc = (int)blockIdx.x * 64, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     int lo, hi;
@@ -273,7 +277,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     // row wr at positions wp .. wp + 3; CH = 1, row wr1 at position wp1
     const int lp = tid >> 4, lc = (tid & 15) * 4;
     const int wr = CH == 4 ? tid >> 4 : tid >> 6, wp = CH == 4 ? (tid & 15) * 4 : tid & 63;
-    const float *vb = a.v + (int64_t)kh * a.hd + (cc + lc < a.hd ? cc + lc : 0);
+    const int lcol = cc + lc < a.hd ? cc + lc : 0;
+    const float *vb = VB ? nullptr : a.v + (int64_t)kh * a.hd + lcol;
+    const int vrec = 4 + a.hd * VB / 8;  // TurboQuant: record bytes, the slot's records back to back
+    const uint8_t *qb = VB ? a.vq + (int64_t)kh * vrec + 4 + (int64_t)lcol * VB / 8 : nullptr;
+    const int64_t qstride = (int64_t)a.n_head_kv * vrec;
+    if (VB == 4 && tid < 16) ctab[tid] = kvq_centroid4(tid);
+    if (VB == 2 && tid < 4) ctab[tid] = kvq_centroid2(tid);
+    if constexpr (VB == 2 || VB == 4) __syncthreads();  // the table is read by the first tile's store
     const GroupRow wg = group_row(a, n_tok, GR, grp, kh, wr);
     const float *wrow = a.s + (size_t)(wg.row < 0 ? 0 : wg.row) * a.max_len;
     // the loads walk the tiles in order, so the positions and ring slots advance by 64 per load
@@ -289,10 +300,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     int wx = lo + wp - wg.st;  // score index of the next weight load
     auto load = [&](AvStage<CH> &t) {
         av4 *dst[4] = {&t.v0, &t.v1, &t.v2, &t.v3};
+        uint32_t *kdst[4] = {&t.k0, &t.k1, &t.k2, &t.k3};
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int sl = vpos[m] <= hi ? vslot[m] : slot_hi;
-            *dst[m] = *(const av4 *)(vb + (int64_t)sl * a.kv_dim);
+            if constexpr (VB == 0)
+                *dst[m] = *(const av4 *)(vb + (int64_t)sl * a.kv_dim);
+            else if constexpr (VB == 8)
+                *kdst[m] = *(const uint32_t *)(qb + sl * qstride);
+            else if constexpr (VB == 4)
+                *kdst[m] = *(const uint16_t *)(qb + sl * qstride);
+            else
+                *kdst[m] = *(qb + sl * qstride);
             vpos[m] += 64;
             vslot[m] += step64;
             if (vslot[m] >= a.cap) vslot[m] -= a.cap;
@@ -311,12 +330,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     for (int r = 0; r < CH; ++r) acc[r] = 0.0f;
     const float *vcol = (const float *)vt + lane;
     // one tile: store the staged registers, barrier, reload them AV_S tiles ahead, run the chains
+    auto decode = [&](uint32_t c) -> av4 {  // 4 values of TurboQuant codes
+        if constexpr (VB == 8)
+            return (av4){(float)(int8_t)c, (float)(int8_t)(c >> 8), (float)(int8_t)(c >> 16), (float)(int8_t)(c >> 24)};
+        else if constexpr (VB == 4)
+            return (av4){ctab[c & 15], ctab[(c >> 4) & 15], ctab[(c >> 8) & 15], ctab[(c >> 12) & 15]};
+        else
+            return (av4){ctab[c & 3], ctab[(c >> 2) & 3], ctab[(c >> 4) & 3], ctab[(c >> 6) & 3]};
+    };
     auto step = [&](int k, AvStage<CH> &t) {
         const int b = k & 1;
-        vt[b][lp][tid & 15] = t.v0;
-        vt[b][lp + 16][tid & 15] = t.v1;
-        vt[b][lp + 32][tid & 15] = t.v2;
-        vt[b][lp + 48][tid & 15] = t.v3;
+        if constexpr (VB == 0) {
+            vt[b][lp][tid & 15] = t.v0;
+            vt[b][lp + 16][tid & 15] = t.v1;
+            vt[b][lp + 32][tid & 15] = t.v2;
+            vt[b][lp + 48][tid & 15] = t.v3;
+        } else {
+            vt[b][lp][tid & 15] = decode(t.k0);
+            vt[b][lp + 16][tid & 15] = decode(t.k1);
+            vt[b][lp + 32][tid & 15] = decode(t.k2);
+            vt[b][lp + 48][tid & 15] = decode(t.k3);
+        }
         const int p = lo + k * 64 + wp;
         if constexpr (CH == 4) {
             float *wf = wt[b];
@@ -398,13 +432,21 @@ hipError_t launch_attention_values(const AttnArgs &a, int n_tok, hipStream_t s) 
         return hipErrorInvalidValue;
     const int rows_kv = n_tok * (a.n_head / a.n_head_kv);
     if ((rows_kv + 3) / 4 > 65535 || a.n_head_kv > 65535) return hipErrorInvalidValue;
-    const unsigned cch = (unsigned)((a.hd + 63) / 64);
-    if (rows_kv >= 64)
-        attn_values_kernel<4, 4><<<dim3(cch, (unsigned)((rows_kv + 15) / 16), (unsigned)a.n_head_kv), 256, 0, s>>>(
-            a, n_tok);
-    else
-        attn_values_kernel<1, 8><<<dim3(cch, (unsigned)((rows_kv + 3) / 4), (unsigned)a.n_head_kv), 256, 0, s>>>(a,
-                                                                                                              n_tok);
+    if (a.vq ? (a.vbits != 2 && a.vbits != 4 && a.vbits != 8) : !a.v) return hipErrorInvalidValue;
+    const unsigned cch = (unsigned)((a.hd + 63) / 64), kvh = (unsigned)a.n_head_kv;
+    const dim3 g16(cch, (unsigned)((rows_kv + 15) / 16), kvh), g4(cch, (unsigned)((rows_kv + 3) / 4), kvh);
+    const int vb = a.vq ? a.vbits : 0;
+    if (rows_kv >= 64) {
+        if (vb == 0) attn_values_kernel<4, 4, 0><<<g16, 256, 0, s>>>(a, n_tok);
+        else if (vb == 8) attn_values_kernel<4, 4, 8><<<g16, 256, 0, s>>>(a, n_tok);
+        else if (vb == 4) attn_values_kernel<4, 4, 4><<<g16, 256, 0, s>>>(a, n_tok);
+        else attn_values_kernel<4, 4, 2><<<g16, 256, 0, s>>>(a, n_tok);
+    } else {
+        if (vb == 0) attn_values_kernel<1, 8, 0><<<g4, 256, 0, s>>>(a, n_tok);
+        else if (vb == 8) attn_values_kernel<1, 8, 8><<<g4, 256, 0, s>>>(a, n_tok);
+        else if (vb == 4) attn_values_kernel<1, 8, 4><<<g4, 256, 0, s>>>(a, n_tok);
+        else attn_values_kernel<1, 8, 2><<<g4, 256, 0, s>>>(a, n_tok);
+    }
     return hipGetLastError();
 }
 
@@ -421,12 +463,9 @@ hipError_t launch_attention(const AttnArgs &a, int n_tok, hipStream_t s) {
     else
         attn_scores_kernel<4><<<dim3(kb, (unsigned)((rows_kv + 3) / 4), kvh.z), 256, 0, s>>>(a, n_tok);
     attn_softmax_kernel<<<n_tok * a.n_head, 256, (size_t)std::min(a.max_len, SM_RES) * 4, s>>>(a);
-    const unsigned cch = (unsigned)((a.hd + 63) / 64);
-    if (rows_kv >= 64)  // enough groups of 16 to fill the chip: 4 chains per lane
-        attn_values_kernel<4, 4><<<dim3(cch, (unsigned)((rows_kv + 15) / 16), kvh.z), 256, 0, s>>>(a, n_tok);
-    else
-        attn_values_kernel<1, 8><<<dim3(cch, (unsigned)((rows_kv + 3) / 4), kvh.z), 256, 0, s>>>(a, n_tok);
-    return hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_attention_values(a, n_tok, s);  // 4 chains per lane from 64 rows per K / V head
 }
 
 }  // namespace fgh

@@ -286,8 +286,27 @@ struct AttnArgs {
     const int32_t *st, *en;   // [tokens] position ranges
     int n_head, n_head_kv, hd, kv_dim, cap, max_len;
     float scale;
+    // the value chains only: V as TurboQuant records instead of v (vbits 2, 4 or 8; the records'
+    // scales already folded into the weights), each value its centroid or int8 code
+    const uint8_t *vq = nullptr;
+    int vbits = 0;
 };
 hipError_t launch_attention(const AttnArgs &a, int n_tok, hipStream_t s);
+
+// the Lloyd-Max centroids of N(0, 1) of the TurboQuant cache (fastgguf.c:3356-3359)
+__host__ __device__ inline float kvq_centroid4(int i) {
+    switch (i & 15) {
+    case 0: return -2.7326f;  case 1: return -2.0690f;  case 2: return -1.6181f;  case 3: return -1.2562f;
+    case 4: return -0.9424f;  case 5: return -0.6568f;  case 6: return -0.3881f;  case 7: return -0.1284f;
+    case 8: return 0.1284f;   case 9: return 0.3881f;   case 10: return 0.6568f;  case 11: return 0.9424f;
+    case 12: return 1.2562f;  case 13: return 1.6181f;  case 14: return 2.0690f;  default: return 2.7326f;
+    }
+}
+__host__ __device__ inline float kvq_centroid2(int i) {
+    switch (i & 3) {
+    case 0: return -1.5104f;  case 1: return -0.4528f;  case 2: return 0.4528f;  default: return 1.5104f;
+    }
+}
 hipError_t launch_attention_values(const AttnArgs &a, int n_tok, hipStream_t s);  // the value chains only
 
 // TurboQuant KV cache (fgh_kvq.hip): records of 4 + hd * bits / 8 bytes per (slot, K / V head)
@@ -303,7 +322,6 @@ struct KvqAttnArgs {
     float *o;                 // [rows][hd] outputs, rotated back
     float *qr, *orot;         // [rows][hd] scratch: rotated queries, rotated outputs
     float *s;                 // [rows][max_len] scores, then weights
-    float *vc;                // [cap][n_head_kv * hd] scratch: V centroids
     const uint8_t *kq, *vq;   // quantized caches
     const int32_t *st, *en;   // [tokens] position ranges
     int n_head, n_head_kv, hd, kbits, vbits, cap, max_len;

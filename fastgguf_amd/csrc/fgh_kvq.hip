@@ -11,12 +11,12 @@
 //   q rows rotated (4763)                                    kvq_rotate_kernel
 //   scores: kvq_dot_k (3447-3462) times scale, per key       kvq_scores_kernel
 //   softmax_inplace (3147-3156), then w' = w * s_V(p)         kvq_softmax_kernel
-//   V codes expanded to their centroids (unscaled)            kvq_expand_kernel
-//   o = fma(w', centroid, o) over the positions in order     attn_values (fgh_attn.hip)
+//   o = fma(w', centroid, o) over the positions in order     attn_values (fgh_attn.hip), which
+//                                                            decodes the V codes as it stages them
 //   output rows rotated back (4846)                           kvq_rotate_kernel
 // kvq_axpy_v (3465-3489) adds fma(w * s, value, o) for each position with w != 0; w' = w * s is
 // that product, and a position with w = 0 adds fma(0, value, o) = o, so the value chains of the
-// fp32 attention give its sums.
+// fp32 attention give its sums. No fp32 copy of the cache is made.
 #include <hip/hip_runtime.h>
 
 #include "fgh_internal.h"
@@ -275,52 +275,6 @@ __global__ __launch_bounds__(256) void kvq_softmax_kernel(KvqAttnArgs a) {
     }
 }
 
-// V codes of the positions min st .. max en (every K / V head) as their centroids, unscaled,
-// into vc[slot][kvh * hd + i]: a workgroup per position (grid-stride), a thread per 4 values
-__global__ __launch_bounds__(256) void kvq_expand_kernel(KvqAttnArgs a, int n_tok) {
-    __shared__ int span[2][4];
-    int lo = 0x7fffffff, hi = -0x7fffffff;  // the tokens' ranges, scanned by all the threads
-    for (int t = threadIdx.x; t < n_tok; t += 256)
-        if (kvq_row_len(a, t) > 0) {
-            lo = min(lo, a.st[t]);
-            hi = max(hi, a.en[t]);
-        }
-    for (int o = 1; o < 64; o <<= 1) {
-        lo = min(lo, __shfl_xor(lo, o, 64));
-        hi = max(hi, __shfl_xor(hi, o, 64));
-    }
-    if ((threadIdx.x & 63) == 0) {
-        span[0][threadIdx.x >> 6] = lo;
-        span[1][threadIdx.x >> 6] = hi;
-    }
-    __syncthreads();
-    lo = min(min(span[0][0], span[0][1]), min(span[0][2], span[0][3]));
-    hi = max(max(span[1][0], span[1][1]), max(span[1][2], span[1][3]));
-    const int hd = a.hd, rec = 4 + hd * a.vbits / 8, kv_dim = a.n_head_kv * hd;
-    for (int p = lo + (int)blockIdx.x; p <= hi; p += (int)gridDim.x) {
-        const int64_t slot = slot_of(p, a.cap);
-        const uint8_t *srec = a.vq + slot * (int64_t)(a.n_head_kv * rec);
-        float *dst = a.vc + slot * (int64_t)kv_dim;
-        for (int c = threadIdx.x * 4; c < kv_dim; c += 1024) {
-            const int kvh = c / hd, i = c - kvh * hd;
-            const uint8_t *codes = srec + kvh * rec + 4;
-            float4 o;
-            if (a.vbits == 8) {
-                const uint32_t v = *(const uint32_t *)(codes + i);
-                o = make_float4((float)(int8_t)v, (float)(int8_t)(v >> 8), (float)(int8_t)(v >> 16),
-                                (float)(int8_t)(v >> 24));
-            } else if (a.vbits == 4) {
-                const uint32_t v = *(const uint16_t *)(codes + i / 2);
-                o = make_float4(kvq_c4[v & 15], kvq_c4[(v >> 4) & 15], kvq_c4[(v >> 8) & 15], kvq_c4[(v >> 12) & 15]);
-            } else {
-                const uint32_t v = codes[i / 4];
-                o = make_float4(kvq_c2[v & 3], kvq_c2[(v >> 2) & 3], kvq_c2[(v >> 4) & 3], kvq_c2[(v >> 6) & 3]);
-            }
-            *(float4 *)(dst + c) = o;
-        }
-    }
-}
-
 }  // namespace
 
 hipError_t launch_kvq_store(const KvqStoreArgs &a, int n_tok, hipStream_t s) {
@@ -345,9 +299,10 @@ hipError_t launch_kvq_attention(const KvqAttnArgs &a, int n_tok, hipStream_t s) 
     else
         kvq_scores_kernel<4><<<dim3(kb, (unsigned)((rows_kv + 3) / 4), (unsigned)a.n_head_kv), 256, 0, s>>>(a, n_tok);
     kvq_softmax_kernel<<<rows, 256, (size_t)std::min(a.max_len, KVQ_RES) * 4, s>>>(a);
-    kvq_expand_kernel<<<(unsigned)std::min(4096, a.max_len + n_tok), 256, 0, s>>>(a, n_tok);
-    AttnArgs v{nullptr, a.orot, nullptr, a.vc, a.s, a.st, a.en, a.n_head, a.n_head_kv, a.hd,
+    AttnArgs v{nullptr, a.orot, nullptr, nullptr, a.s, a.st, a.en, a.n_head, a.n_head_kv, a.hd,
                a.n_head_kv * a.hd, a.cap, a.max_len, 1.0f};
+    v.vq = a.vq;  // the value chains decode the V records' codes themselves
+    v.vbits = a.vbits;
     hipError_t e = launch_attention_values(v, n_tok, s);
     if (e != hipSuccess) return e;
     kvq_rotate_kernel<<<rows, 256, 0, s>>>(a.orot, a.o, a.hd, true);
