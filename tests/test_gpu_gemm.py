@@ -95,7 +95,7 @@ def test_matmul_other_types(backend, oracle, t, nb):
 
 
 def test_prefill_config_shape(backend, oracle):
-    """64 tokens x K=4096 -> N=14336, Q4_K (benchmark distributions)."""
+    """Benchmark config 4: 64 tokens x K=4096 -> N=14336, Q4_K (benchmark distributions)."""
     rows, cols, T = 14336, 4096, 64
     w = S.weights(S.T_Q4_K, rows, cols, 90)
     X = S.activations(cols, 91, rows=T)

@@ -132,7 +132,7 @@ def test_block_ints_and_matvec_exact(backend, oracle, case):
                                  "gate_q5k", "down_q5_0", "down_q5k", "down_q4k_row", "down_q8_0", "gate_q4_0_rp",
                                  "down_q4_1", "gate_iq4_nl"])
 def test_matvec_config_shapes(backend, oracle, cfg):
-    """BASELINE.json shapes with the benchmark's weight distributions (and the same FFN shapes
+    """The benchmark configs' shapes with the benchmark's weight distributions (and the same FFN shapes
     for Q5_K and Q5_0)."""
     t, rows, cols, order = {
         "cfg1_q8_0": (S.T_Q8_0, 4096, 4096, ORDER_ROW),

@@ -2,7 +2,7 @@
 
 Every dot product runs the reference's own per-row order, so expert selection, weights and outputs
 are compared bit for bit: against the reference's golden outputs (including tied router logits)
-and against the oracle on random and BASELINE config-5 shapes. The one function outside the
+and against the oracle on random and benchmark config-5 shapes. The one function outside the
 integer and IEEE-basic arithmetic is expf (softmax and silu): the device restates glibc's expf
 method, checked bit for bit against the host libm here and over every float in test_oracle.
 """
@@ -112,7 +112,7 @@ def test_moe_matches_oracle(backend, oracle, E, K, D, F, T):
 
 @pytest.mark.parametrize("T", [1, 64])
 def test_moe_config5(backend, oracle, T):
-    """Qwen3-30B-A3B-shaped layer, 128 experts, top-8, hidden 2048, ff 768."""
+    """Benchmark config 5: Qwen3-30B-A3B-shaped layer, 128 experts, top-8, hidden 2048, ff 768."""
     E, K, D, F = 128, 8, 2048, 768
     gw = S.q4_k_weights(E * F, D, seed=300)
     uw = S.q4_k_weights(E * F, D, seed=301)
