@@ -258,8 +258,12 @@ template <int CH, int AV_S, int VB>  // AV_S: tiles in flight, 4 or 8 (the named
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_values_kernel(AttnArgs a,
                                                                                                      int n_tok) {
     constexpr int GR = 4 * CH;  // rows per group
-    __shared__ av4 vt[2][64][16];
-    __shared__ __attribute__((aligned(16))) float wt[2][64 * GR];
+    // CH = 1: two tiles per barrier over a ring of 4 LDS tiles (a wavefront overwrites a pair's
+    // tiles only after the next pair's barrier, which every wavefront reaches after consuming it)
+    constexpr bool PAIR = CH == 1;
+    constexpr int NB = PAIR ? 4 : 2;
+    __shared__ av4 vt[NB][64][16];
+    __shared__ __attribute__((aligned(16))) float wt[NB][64 * GR];
     __shared__ float ctab[16];
     const int grp = blockIdx.y, kh = blockIdx.z, cc = (int)blockIdx.x * 64, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -329,7 +333,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
     for (int r = 0; r < CH; ++r) acc[r] = 0.0f;
     const float *vcol = (const float *)vt + lane;
-    // one tile: store the staged registers, barrier, reload them AV_S tiles ahead, run the chains
     auto decode = [&](uint32_t c) -> av4 {  // 4 values of TurboQuant codes
         if constexpr (VB == 8)
             return (av4){(float)(int8_t)c, (float)(int8_t)(c >> 8), (float)(int8_t)(c >> 16), (float)(int8_t)(c >> 24)};
@@ -338,8 +341,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         else
             return (av4){ctab[c & 3], ctab[(c >> 2) & 3], ctab[(c >> 4) & 3], ctab[(c >> 6) & 3]};
     };
-    auto step = [&](int k, AvStage<CH> &t) {
-        const int b = k & 1;
+    auto store = [&](int k, AvStage<CH> &t) {
+        const int b = k & (NB - 1);
         if constexpr (VB == 0) {
             vt[b][lp][tid & 15] = t.v0;
             vt[b][lp + 16][tid & 15] = t.v1;
@@ -361,8 +364,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         } else {
             wt[b][wr * 64 + wp] = in_range(p) ? t.w.x : 0.0f;
         }
-        __syncthreads();
-        load(t);  // tile k + AV_S
+    };
+    auto consume = [&](int k) {
+        const int b = k & (NB - 1);
         const float *vs = vcol + b * 64 * 64;
         const int cnt = min(64, span - k * 64);  // <= 0 past the end
         if constexpr (CH == 4) {
@@ -397,6 +401,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             }
         }
     };
+    // one tile: store the staged registers, barrier, reload them AV_S tiles ahead, run the chains
+    auto step = [&](int k, AvStage<CH> &t) {
+        store(k, t);
+        __syncthreads();
+        load(t);  // tile k + AV_S
+        consume(k);
+    };
+    auto step2 = [&](int k, AvStage<CH> &ta, AvStage<CH> &tb) {  // tiles k and k + 1, one barrier
+        store(k, ta);
+        store(k + 1, tb);
+        __syncthreads();
+        load(ta);  // tile k + AV_S
+        load(tb);  // tile k + 1 + AV_S
+        consume(k);
+        consume(k + 1);
+    };
     // the stages' loads are issued strictly in order (scheduling barriers), so the loop head
     // waits for the oldest stage only
     AvStage<CH> t0, t1, t2, t3, t4, t5, t6, t7;
@@ -410,12 +430,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     if constexpr (AV_S == 8) {
         AV_LOAD(4) AV_LOAD(5) AV_LOAD(6) AV_LOAD(7)
     }
+#define AV_STEP2(i, j) \
+    step2(k0 + i, t##i, t##j); \
+    __builtin_amdgcn_sched_barrier(0);
     for (int k0 = 0; k0 < ns; k0 += AV_S) {
-        AV_STEP(0) AV_STEP(1) AV_STEP(2) AV_STEP(3)
-        if constexpr (AV_S == 8) {
-            AV_STEP(4) AV_STEP(5) AV_STEP(6) AV_STEP(7)
+        if constexpr (PAIR) {
+            AV_STEP2(0, 1) AV_STEP2(2, 3)
+            if constexpr (AV_S == 8) {
+                AV_STEP2(4, 5) AV_STEP2(6, 7)
+            }
+        } else {
+            AV_STEP(0) AV_STEP(1) AV_STEP(2) AV_STEP(3)
+            if constexpr (AV_S == 8) {
+                AV_STEP(4) AV_STEP(5) AV_STEP(6) AV_STEP(7)
+            }
         }
     }
+#undef AV_STEP2
 #undef AV_LOAD
 #undef AV_STEP
 #pragma unroll
