@@ -132,13 +132,12 @@ def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
     return out
 
 
-def attention_config(be, kernel_time, enabled: int, cpu: bool) -> dict | None:
+def attention_config(be, kernel_time, enabled: int, cpu_in: dict) -> dict | None:
     """Attention over the fp32 KV ring cache (attn_rows, fastgguf.c:3273-3326) at Llama-3-8B's shape
     (32 query heads over 8 K / V heads, hd 128): one decode token over 4096 positions, and a 64-token
     prompt batch at the end of a 4096-position context; then the same over TurboQuant K4 / V4 caches
-    (fastgguf.c:3341-3513) written from the same rows. With cpu, the reference (oracle/_ref, one
-    thread) on each decode case: attn_rows in 4-row calls per K / V head as its forward makes,
-    and its TurboQuant attention step per head."""
+    (fastgguf.c:3341-3513) written from the same rows. cpu_in receives the decode cases' host
+    inputs, for the reference's CPU timing in cpu_baseline."""
     if not enabled:
         return None
     import numpy as np
@@ -166,20 +165,8 @@ def attention_config(be, kernel_time, enabled: int, cpu: bool) -> dict | None:
         fmas = 2 * int((en - st + 1).sum()) * nh * hd
         out[name] = {"us": round(us, 2), "kv_bytes": kv_bytes, "kv_GB/s": round(kv_bytes / us / 1e3, 1),
                      "fma_G/s": round(fmas / us / 1e3, 1)}
-        if cpu and nt == 1:
-            try:
-                sys.path.insert(0, os.path.join(ROOT, "oracle"))
-                from oracle import Reference
-                ref = Reference()
-                t0 = time.perf_counter()
-                reps = 5
-                for _ in range(reps):
-                    for h in range(nkv):
-                        ref.attn_rows(q[0, 4 * h:4 * h + 4], np.repeat(st, 4), np.repeat(en, 4), ck, cv, h * hd, hd,
-                                      scale)
-                out[name]["cpu_reference_1thread_us"] = round((time.perf_counter() - t0) / reps * 1e6, 1)
-            except (FileNotFoundError, OSError) as e:
-                print(f"[bench] attention cpu reference skipped: {e}", file=sys.stderr)
+        if nt == 1:
+            cpu_in.update(q=q[0], st=st, en=en, ck=ck, cv=cv, hd=hd, nh=nh, nkv=nkv, scale=scale)
         for b in bufs:
             be.dev_free(b)
     # TurboQuant K4 / V4 caches written from the same K / V rows (the cache write timed per token
@@ -204,22 +191,11 @@ def attention_config(be, kernel_time, enabled: int, cpu: bool) -> dict | None:
         us = kernel_time(lambda i: be.kvq_attention_dev(nt, nh, nkv, hd, kb, vb, bufs[0], bufs[1], kqd, vqd, cap,
                                                         bufs[2], bufs[3], n_max, scale), 100)
         out[name] = {"us": round(us, 2), "cache_bytes": n_max * (kqs + vqs)}
-        if cpu and nt == 1:
-            try:
-                sys.path.insert(0, os.path.join(ROOT, "oracle"))
-                from oracle import Reference
-                ref = Reference()
-                kq, vq = np.zeros((cap, kqs), np.uint8), np.zeros((cap, vqs), np.uint8)
-                be.d2h(kq, kqd)
-                be.d2h(vq, vqd)
-                kvh = np.arange(nh) // (nh // nkv)
-                t0 = time.perf_counter()
-                reps = 3
-                for _ in range(reps):
-                    ref.kvq_attn_rows(q[0], np.repeat(st, nh), np.repeat(en, nh), kq, vq, kvh, hd, kb, vb, scale)
-                out[name]["cpu_reference_1thread_us"] = round((time.perf_counter() - t0) / reps * 1e6, 1)
-            except (FileNotFoundError, OSError) as e:
-                print(f"[bench] turbo cpu reference skipped: {e}", file=sys.stderr)
+        if nt == 1:
+            kq, vq = np.zeros((cap, kqs), np.uint8), np.zeros((cap, vqs), np.uint8)
+            be.d2h(kq, kqd)
+            be.d2h(vq, vqd)
+            cpu_in.update(tq=q[0], kq=kq, vq=vq, kbits=kb, vbits=vb)
         for b in bufs:
             be.dev_free(b)
     for b in (kqd, vqd, posd, kd, vd):
@@ -227,8 +203,32 @@ def attention_config(be, kernel_time, enabled: int, cpu: bool) -> dict | None:
     return out
 
 
-def cpu_baseline(layer_w: dict, xs: dict, budget_s: float) -> dict | None:
-    """The reference's CPU path on the same layer (oracle/_ref), median over a bounded sample."""
+def cpu_attention(ref, a: dict) -> dict:
+    """The reference's attention on the bench's decode cases, one thread: attn_rows in 4-row calls
+    per K / V head as its forward makes, and its TurboQuant attention step per head."""
+    import numpy as np
+    out = {}
+    if "q" in a:
+        t0 = time.perf_counter()
+        for _ in range(5):
+            for h in range(a["nkv"]):
+                ref.attn_rows(a["q"][4 * h:4 * h + 4], np.repeat(a["st"], 4), np.repeat(a["en"], 4), a["ck"], a["cv"],
+                              h * a["hd"], a["hd"], a["scale"])
+        out["attention_decode_4096_1thread_us"] = round((time.perf_counter() - t0) / 5 * 1e6, 1)
+    if "tq" in a:
+        nh = a["nh"]
+        kvh = np.arange(nh) // (nh // a["nkv"])
+        t0 = time.perf_counter()
+        for _ in range(3):
+            ref.kvq_attn_rows(a["tq"], np.repeat(a["st"], nh), np.repeat(a["en"], nh), a["kq"], a["vq"], kvh, a["hd"],
+                              a["kbits"], a["vbits"], a["scale"])
+        out["turbo_k4v4_decode_4096_1thread_us"] = round((time.perf_counter() - t0) / 3 * 1e6, 1)
+    return out
+
+
+def cpu_baseline(layer_w: dict, xs: dict, budget_s: float, attn_in: dict | None = None) -> dict | None:
+    """The reference's CPU path on the same layer (oracle/_ref), median over a bounded sample; and
+    on the bench's attention decode cases (attn_in, from attention_config)."""
     try:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         from oracle import Reference
@@ -268,7 +268,7 @@ def cpu_baseline(layer_w: dict, xs: dict, budget_s: float) -> dict | None:
     return {"value": round(total / med / 1e9, 2), "unit": "GB/s", "cores": ref.threads(), "kind": "reference",
             "sample": f"{len(times)} decode layers (median {med * 1e6:.0f} us/layer), fastgguf.c matvec/"
                       f"matvec_multi on repacked Q4_K, {ref.build} build, {copies} rotating weight copies",
-            "ms_per_step": round(med * 1e3, 3)}
+            "ms_per_step": round(med * 1e3, 3), **cpu_attention(ref, attn_in or {})}
 
 
 def main() -> int:
@@ -442,9 +442,10 @@ def main() -> int:
     be.dev_free(ypd)
 
     others = other_configs(be, S, kernel_time, args.configs)
-    attention = attention_config(be, kernel_time, args.configs, args.cpu_seconds > 0)
+    attn_in = {}
+    attention = attention_config(be, kernel_time, args.configs, attn_in)
 
-    cpu = cpu_baseline(layer_w, xs, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    cpu = cpu_baseline(layer_w, xs, args.cpu_seconds, attn_in) if args.cpu_seconds > 0 else None
     info = be.info()
     be.close()
     out = {
