@@ -31,7 +31,7 @@ EXPORTS = (
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
-    "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_expf", "fgh_fp16_to_f32",
+    "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_expf", "fgh_fp16_to_f32", "fgh_matvec_shape",
     "fgh_gguf_open", "fgh_gguf_close", "fgh_gguf_summary", "fgh_gguf_tensor", "fgh_gguf_find",
     "fgh_gguf_kv_num", "fgh_gguf_kv_str", "fgh_gguf_data", "fgh_upload_gguf",
 )
@@ -107,6 +107,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_gemm_block_ints": (i32, [vp, vp, f32p, i32, i32, vp, vp]),
         "fgh_fp16_to_f32": (i32, [vp, vp, i32, vp]),
         "fgh_expf": (i32, [vp, f32p, i32, vp]),
+        "fgh_matvec_shape": (i32, [vp, u32, i32, i64, i64, i32, vp]),
         "fgh_gguf_open": (i32, [C.c_char_p, C.POINTER(vp), C.c_char_p, C.c_size_t]),
         "fgh_gguf_close": (None, [vp]),
         "fgh_gguf_summary": (i32, [vp, C.POINTER(u32), C.POINTER(u64), C.POINTER(i64), C.POINTER(i64)]),
@@ -333,6 +334,13 @@ class Backend:
         out = np.empty(x.size, np.float32)
         self._check(self.lib.fgh_expf(self.ctx, _p(x), x.size, _p(out)))
         return out
+
+    def matvec_shape(self, ggml_type: int, order: int, cols: int, row_tiles: int, ntok: int = 1) -> tuple:
+        """(wavefronts per tile, ring depth, tiles per workgroup, LDS bytes) of the decode launch over
+        row_tiles row tiles (all tensors of the launch) and ntok tokens."""
+        out = np.zeros(4, np.int32)
+        self._check(self.lib.fgh_matvec_shape(self.ctx, ggml_type, order, cols, row_tiles, ntok, _p(out)))
+        return tuple(int(v) for v in out)
 
     def fp16_to_f32(self, h: np.ndarray) -> np.ndarray:
         h = np.ascontiguousarray(h, np.uint16)

@@ -33,27 +33,47 @@ SOURCES = ["fgh_api.hip", "fgh_kernels.hip", "fgh_matvec.hip", "fgh_q4k.hip", "f
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 
+HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+             "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Xclang", "-target-feature", "-Xclang", "-dot6-insts", "-Xclang", "-target-feature", "-Xclang",
+             "-dot4-insts", "-Wall", "-Wno-unused-function", "-fvisibility=hidden",
+             "-I", os.path.join(ROOT, "include")]
+_NOISE = ("packed-fp32-ops", "dot6-insts", "dot4-insts")
+
+
 def hipcc_cmd(out: str = LIB) -> list[str]:
-    return [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
-            "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            "-Xclang", "-target-feature", "-Xclang", "-dot6-insts", "-Xclang", "-target-feature", "-Xclang", "-dot4-insts",
-            "-Wall", "-Wno-unused-function", "-fvisibility=hidden", "-Wl,-z,defs",
-            "-I", os.path.join(ROOT, "include"),
-            "-o", out] + [os.path.join(CSRC, s) for s in SOURCES]
+    """The whole library in one hipcc call (the same flags as build()'s per-file compiles)."""
+    return [HIPCC] + HIP_FLAGS + ["-shared", "-Wl,-z,defs", "-o", out] + [os.path.join(CSRC, s) for s in SOURCES]
 
 
-def build(verbose: bool = True) -> str:
-    tmp = LIB + ".tmp"
-    cmd = hipcc_cmd(tmp)
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def _run(cmd: list[str]) -> tuple[int, str]:
     r = subprocess.run(cmd, capture_output=True, text=True)
-    err = "\n".join(l for l in r.stderr.splitlines()
-                     if not any(f in l for f in ("packed-fp32-ops", "dot6-insts", "dot4-insts")) and l.strip())
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
-    if verbose and err:
-        print(err, file=sys.stderr)
+    err = "\n".join(l for l in r.stderr.splitlines() if not any(f in l for f in _NOISE) and l.strip())
+    return r.returncode, err
+
+
+def build(verbose: bool = True, jobs: int | None = None) -> str:
+    """Compiles each source to an object in parallel (every kernel is launched from its own
+    translation unit, so no device code crosses files), then links the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+    odir = os.path.join(HERE, "_build")
+    os.makedirs(odir, exist_ok=True)
+    objs = [os.path.join(odir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    cmds = [[HIPCC] + HIP_FLAGS + ["-c", "-o", o, os.path.join(CSRC, s)] for s, o in zip(SOURCES, objs)]
+    if verbose:
+        print(" ".join(cmds[0][:-3]) + " -c <each source>", flush=True)
+    jobs = jobs or min(len(cmds), max(1, int(os.environ.get("MAX_JOBS", "0")) or (os.cpu_count() or 4)))
+    with ThreadPoolExecutor(jobs) as ex:
+        results = list(ex.map(_run, cmds))
+    for (rc, err), s in zip(results, SOURCES):
+        if rc != 0:
+            raise RuntimeError(f"hipcc failed on {s} ({rc}):\n{err}")
+        if verbose and err:
+            print(err, file=sys.stderr)
+    tmp = LIB + ".tmp"
+    rc, err = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp] + objs)
+    if rc != 0:
+        raise RuntimeError(f"link failed ({rc}):\n{err}")
     os.replace(tmp, LIB)
     return LIB
 

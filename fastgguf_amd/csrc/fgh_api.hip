@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -39,7 +40,25 @@ struct fgh_ctx {
     DevBuf ck;                              // fgh_checksum_dev: per-workgroup partial sums
     int num_cu = 256;         // compute units (sizes the persistent decode grid)
     bool capturing = false;   // inside fgh_graph_begin / fgh_graph_end
+    // Instantiated graphs not yet destroyed hold the scratch addresses they were captured with:
+    // while any is alive, a buffer that grows keeps its old allocation here, freed when the last
+    // graph is destroyed or the context closes.
+    int live_graphs = 0;
+    std::vector<void *> retired;
+    // failure injection (FGH_FAIL_AT=n at fgh_open): the n-th compute call on this context fails
+    // with FGH_ERR before it launches anything, so a caller's CPU fallback can be tested
+    int64_t calls = 0, fail_at = 0;
 };
+
+// counts one compute call; true (with the context's message set) when it is the injected failure
+static bool injected_failure(fgh_ctx *c);
+
+static void free_retired(fgh_ctx *c) {
+    if (c->retired.empty()) return;
+    (void)hipStreamSynchronize(c->stream);
+    for (void *p : c->retired) (void)hipFree(p);
+    c->retired.clear();
+}
 
 struct fgh_tensor {
     fgh_ctx *ctx;
@@ -76,8 +95,12 @@ static int grow(fgh_ctx *c, DevBuf &b, size_t need) {
     if (need <= b.cap) return FGH_OK;
     if (c->capturing) return fail(c, FGH_ERR, "a scratch buffer would grow during graph capture");
     if (b.p) {
-        HIP_TRY(c, hipStreamSynchronize(c->stream));
-        HIP_TRY(c, hipFree(b.p));
+        if (c->live_graphs > 0) {
+            c->retired.push_back(b.p);  // a live graph may still read or write it
+        } else {
+            HIP_TRY(c, hipStreamSynchronize(c->stream));
+            HIP_TRY(c, hipFree(b.p));
+        }
         b.p = nullptr;
         b.cap = 0;
     }
@@ -209,6 +232,18 @@ static int gemm_q4k(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx
         if ((c)->capturing) return fail((c), FGH_ERR, "%s: not allowed while capturing a graph", __func__); \
     } while (0)
 
+static bool injected_failure(fgh_ctx *c) {
+    if (c->fail_at <= 0 || ++c->calls != c->fail_at) return false;
+    char buf[96];
+    snprintf(buf, sizeof(buf), "injected failure at compute call %lld (FGH_FAIL_AT)", (long long)c->fail_at);
+    c->err = buf;
+    return true;
+}
+#define INJECT(c) \
+    do { \
+        if (injected_failure(c)) return FGH_ERR; \
+    } while (0)
+
 static int check_tensor(fgh_ctx *c, const fgh_tensor *t) {
     if (!c) return FGH_ERR_ARG;
     if (!t || t->ctx != c || !t->dev) return fail(c, FGH_ERR_ARG, "invalid tensor handle");
@@ -222,6 +257,14 @@ static int selfcheck(fgh_ctx *c);
 int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out) {
     if (!out) return FGH_ERR_ARG;
     *out = nullptr;
+    // FASTGGUF_GPU=off / 0 / cpu / none keeps the caller on its CPU path without touching a
+    // device, and FASTGGUF_GPU_DEVICE picks the device when the caller passes device < 0
+    // (fg_gpu_init_ex, fastgguf.c:1972-1982)
+    if (const char *env = getenv("FASTGGUF_GPU"))
+        if (!strcmp(env, "off") || !strcmp(env, "0") || !strcmp(env, "cpu") || !strcmp(env, "none"))
+            return FGH_ERR_DEVICE;
+    if (device < 0)
+        if (const char *dev = getenv("FASTGGUF_GPU_DEVICE")) device = atoi(dev);
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return FGH_ERR_DEVICE;
     if (device < 0) device = 0;
@@ -244,6 +287,7 @@ int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out) {
         fgh_close(c);
         return FGH_ERR_DEVICE;
     }
+    if (const char *f = getenv("FGH_FAIL_AT")) c->fail_at = atoll(f);
     *out = c;
     return FGH_OK;
 }
@@ -256,6 +300,7 @@ void fgh_close(fgh_ctx *c) {
                       &c->mu, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck, &c->as, &c->kqr,
                       &c->kor})
         if (b->p) (void)hipFree(b->p);
+    free_retired(c);
     (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -294,9 +339,11 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
         return fail(c, FGH_SKIP_TYPE, "upload: type %u with %lld cols is not supported", type, (long long)cols);
     }
     const int64_t row_bytes = cols / block_elems(type) * block_bytes(type);
-    if ((uint64_t)(row_bytes * rows * n_mats) != nbytes)
-        return fail(c, FGH_ERR_ARG, "upload: nbytes %llu != %lld", (unsigned long long)nbytes,
-                    (long long)(row_bytes * rows * n_mats));
+    int64_t want = 0;
+    if (__builtin_mul_overflow(row_bytes, rows, &want) || __builtin_mul_overflow(want, n_mats, &want))
+        return fail(c, FGH_ERR_ARG, "upload: the tensor's byte count overflows");
+    if ((uint64_t)want != nbytes)
+        return fail(c, FGH_ERR_ARG, "upload: nbytes %llu != %lld", (unsigned long long)nbytes, (long long)want);
     HIP_TRY(c, hipSetDevice(c->device));
     fgh_tensor *t = new fgh_tensor();
     t->ctx = c;
@@ -310,8 +357,13 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     t->gpm = (rows + tile_rows - 1) / tile_rows;
     t->groups = t->gpm * n_mats;
     t->order = ord;
-    t->dev_bytes = (uint64_t)t->groups * t->ntile * tile_bytes(type);
-    if (c->used + t->dev_bytes > c->budget) {
+    int64_t dev_bytes = 0;
+    if (__builtin_mul_overflow(t->groups, (int64_t)t->ntile * tile_bytes(type), &dev_bytes)) {
+        delete t;
+        return fail(c, FGH_ERR_ARG, "upload: the device copy's byte count overflows");
+    }
+    t->dev_bytes = (uint64_t)dev_bytes;
+    if (t->dev_bytes > c->budget || c->used + t->dev_bytes > c->budget) {
         delete t;
         c->n_skip_mem++;
         return fail(c, FGH_SKIP_MEM, "upload: budget exceeded");
@@ -365,6 +417,7 @@ int fgh_matvec_multi_dev(fgh_ctx *c, int n, const fgh_tensor *const *t, const fl
         if (!y[i]) return fail(c, FGH_ERR_ARG, "matvec_multi: null output");
         if (t[i]->cols != t[0]->cols) return fail(c, FGH_ERR_ARG, "matvec_multi: tensors differ in cols");
     }
+    INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
     // tensors of the same type and order run in one launch (matvec_multi, fastgguf.c:2552-2572)
     bool done[4] = {false, false, false, false};
@@ -394,6 +447,7 @@ int fgh_matvec_silu_dev(fgh_ctx *c, const fgh_tensor *t, const float *g, const f
     int rc = check_tensor(c, t);
     if (rc) return rc;
     if (!g || !u || !y) return fail(c, FGH_ERR_ARG, "matvec_silu: null pointer");
+    INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
     float *yy[1] = {y};
     return matvec_launch(c, 1, &t, g, t->cols, yy, t->rows * t->n_mats, 1, nullptr, nullptr, nullptr, 1, u);
@@ -404,6 +458,7 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
     if (rc) return rc;
     if (!X || !Y || nb < 1 || nb > FG_BATCH || ldx < t->cols || ldy < t->rows * t->n_mats)
         return fail(c, FGH_ERR_ARG, "matmul: bad arguments");
+    INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
     // nb >= 8: the prompt GEMM (matmul 3018-3031) on int8 MFMA for Q4_K; Q6_K and Q8_0 run the
     // per-token decode kernels (their fp32 orders differ from gemm_kquant's only by rounding)
@@ -423,6 +478,7 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
         return fail(c, FGH_ERR_ARG, "moe_ffn: gate/up must be [E][ff][n_embd] and down [E][n_embd][ff]");
     if (!logits || !X || !Y || n_tok < 1 || n_tok > FG_BATCH || k < 1 || k > E || k > 64 || E > 512)
         return fail(c, FGH_ERR_ARG, "moe_ffn: bad arguments (k %d, experts %lld, tokens %d)", k, (long long)E, n_tok);
+    INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
     const int64_t np = (int64_t)n_tok * k;  // (token, selected expert) slots
     if ((rc = grow(c, c->msel, (size_t)np * 4)) || (rc = grow(c, c->mw, (size_t)np * 4)) ||
@@ -503,6 +559,7 @@ int fgh_attention_dev(fgh_ctx *c, int n_tok, int n_head, int n_head_kv, int hd, 
         return fail(c, FGH_ERR_ARG, "attention: q and the caches must be 16-byte aligned");
     if ((n_tok * (n_head / n_head_kv) + 3) / 4 > 65535 || n_head_kv > 65535 || (int64_t)n_tok * n_head > INT32_MAX / 2)
         return fail(c, FGH_ERR_ARG, "attention: too many rows");
+    INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
     int rc;
     if ((rc = grow(c, c->as, (size_t)n_tok * n_head * max_len * 4))) return rc;
@@ -525,6 +582,7 @@ int fgh_kvq_store_dev(fgh_ctx *c, int n_tok, int n_head_kv, int hd, int kbits, i
         return fail(c, FGH_ERR_ARG, "kvq_store: bad arguments");
     if (((uintptr_t)kq | (uintptr_t)vq) % 16 != 0)
         return fail(c, FGH_ERR_ARG, "kvq_store: the caches must be 16-byte aligned");
+    INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
     fgh::KvqStoreArgs a{k, v, kq, vq, pos, stride, n_head_kv, hd, kbits, vbits, cap};
     HIP_TRY(c, fgh::launch_kvq_store(a, n_tok, c->stream));
@@ -541,6 +599,7 @@ int fgh_kvq_attention_dev(fgh_ctx *c, int n_tok, int n_head, int n_head_kv, int 
         return fail(c, FGH_ERR_ARG, "kvq_attention: bad arguments");
     if (((uintptr_t)q | (uintptr_t)kq | (uintptr_t)vq) % 16 != 0)
         return fail(c, FGH_ERR_ARG, "kvq_attention: q and the caches must be 16-byte aligned");
+    INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
     const size_t rows = (size_t)n_tok * n_head;
     int rc;
@@ -768,6 +827,7 @@ int fgh_graph_end(fgh_ctx *c, void **graph) {
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) return fail(c, FGH_ERR_DEVICE, "graph instantiate: %s", hipGetErrorString(e));
     *graph = ge;
+    c->live_graphs++;
     return FGH_OK;
 }
 
@@ -780,7 +840,11 @@ int fgh_graph_launch(fgh_ctx *c, void *graph) {
 
 int fgh_graph_destroy(fgh_ctx *c, void *graph) {
     if (!c || !graph) return FGH_ERR_ARG;
+    NO_CAPTURE(c);
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));  // no replay of it is still running
     HIP_TRY(c, hipGraphExecDestroy((hipGraphExec_t)graph));
+    if (c->live_graphs > 0 && --c->live_graphs == 0) free_retired(c);
     return FGH_OK;
 }
 
@@ -884,6 +948,21 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     (void)hipFree(ds);
     if (rc) return rc;
     if (e != hipSuccess) return fail(c, FGH_ERR_DEVICE, "gemm_block_ints: %s", hipGetErrorString(e));
+    return FGH_OK;
+}
+
+int fgh_matvec_shape(fgh_ctx *c, uint32_t type, int order, int64_t cols, int64_t row_tiles, int ntok,
+                     int32_t *shape) {
+    if (!c || !shape || row_tiles < 1 || ntok < 1 || cols < 1 || !type_supported(type) ||
+        cols % block_elems(type) != 0)
+        return fail(c, FGH_ERR_ARG, "matvec_shape: bad arguments");
+    const int ord = (type == FGH_T_Q4_K || type == FGH_T_Q4_0) && order == FGH_ORDER_REPACKED ? 1 : 0;
+    const fgh::MvShape sh = fgh::matvec_shape((int)type, ord, row_tiles * ntok, (int)(cols / block_elems(type)),
+                                              c->num_cu);
+    shape[0] = sh.S;
+    shape[1] = sh.R;
+    shape[2] = sh.TPW;
+    shape[3] = (int32_t)sh.lds;
     return FGH_OK;
 }
 

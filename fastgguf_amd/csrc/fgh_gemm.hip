@@ -127,13 +127,11 @@ __device__ __forceinline__ void w_load(WOps &w, const uint8_t *T, size_t boff, i
 // workgroup barrier. Tp tokens, KQ blocks, NT threads.
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 // One direct-to-LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane i's bytes land at
-// dst + 16 i; dst must be the same in every lane (it goes to M0). Written as inline assembly so
-// that the compiler does not treat the stage being filled as aliasing the stage being read (it
-// would wait for the loads before every LDS read); completion is awaited explicitly (s_dma_wait)
-// before the workgroup barrier that publishes the stage. Nothing else in these kernels uses M0.
+// dst + 16 i; dst must be the same in every lane. The compiler builtin sets M0 itself (M0 is a
+// register the compiler reserves, so inline assembly that writes it is not safe); completion is
+// awaited explicitly (s_dma_wait) before the workgroup barrier that publishes the stage.
 __device__ __forceinline__ void dma16(const void *src, uint8_t *dst) {
-    const unsigned base = (unsigned)(size_t)(lds_u8 *)dst;
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory");
+    __builtin_amdgcn_global_load_lds(src, (lds_u8 *)dst, 16, 0, 0);
 }
 template <int NT, int Tp, int KQ>
 __device__ __forceinline__ void s_dma(const GemmArgs &a, uint8_t *sq, uint8_t *se, int s, int tid, int wave) {

@@ -202,7 +202,12 @@ int fgh_gguf_open(const char *path, fgh_gguf **out, char *err, size_t err_len) {
     }
     if (r.err) return bail("%s: metadata parse error", path);
     for (const Kv &kv : g->kvs)
-        if (kv.key == "general.alignment" && kv.kind == 0 && kv.num > 0) g->alignment = (uint64_t)kv.num;
+        if (kv.key == "general.alignment" && kv.kind == 0 && kv.num > 0) {
+            // the reference divides by (uint64_t)kv_num: a value below 1 would be a division by
+            // zero there, and one past 2^32 makes the data start overflow; both are refused
+            if (!(kv.num >= 1.0 && kv.num <= 4294967296.0)) return bail("%s: bad general.alignment", path);
+            g->alignment = (uint64_t)kv.num;
+        }
 
     g->tensors.resize((size_t)n_tensors);
     std::vector<uint64_t> offsets((size_t)n_tensors);
@@ -216,10 +221,12 @@ int fgh_gguf_open(const char *path, fgh_gguf **out, char *err, size_t err_len) {
         if (nd > 4) return bail("tensor %s: more than 4 dimensions", t.name);
         t.n_dims = (int32_t)nd;
         uint64_t elems = 1;
+        bool wraps = false;
         for (uint32_t j = 0; j < nd; j++) {
             t.ne[j] = r.get<uint64_t>();
-            elems *= t.ne[j];
+            wraps |= __builtin_mul_overflow(elems, t.ne[j], &elems);
         }
+        if (wraps && !r.err) return bail("tensor %s: element count overflows", t.name);
         t.type = r.get<uint32_t>();
         offsets[(size_t)i] = r.get<uint64_t>();
         if (r.err) break;
@@ -230,7 +237,8 @@ int fgh_gguf_open(const char *path, fgh_gguf **out, char *err, size_t err_len) {
             delete g;
             return gguf_fail(err, err_len, FGH_ERR_ARG, "tensor %s: %s", name.c_str(), m2);
         }
-        t.nbytes = (elems + be - 1) / be * bb;
+        if (__builtin_mul_overflow(elems / be + (elems % be != 0), bb, &t.nbytes))
+            return bail("tensor %s: byte count overflows", t.name);
     }
     if (r.err) return bail("%s: tensor header parse error", path);
 

@@ -214,6 +214,14 @@ struct MvArgs {
     const float *xu;
 };
 size_t matvec_lds_bytes(int type, int order, int nb);  // every type (fgh_matvec.hip)
+// the launch shape a decode launch of `tiles` row tiles (over all tokens) picks: S wavefronts per
+// tile, ring depth R, TPW tiles per workgroup, its dynamic LDS bytes (S == 0: no kernel)
+struct MvShape {
+    int S, R, TPW;
+    size_t lds;
+};
+MvShape matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu);
+MvShape q4k_matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu);
 // Q4_K / Q5_K (fgh_q4k.hip): their own tile layout and kernel
 size_t q4k_lds_bytes(int order, int nb);
 hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);

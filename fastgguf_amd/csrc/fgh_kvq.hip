@@ -15,8 +15,9 @@
 //                                                            decodes the V codes as it stages them
 //   output rows rotated back (4846)                           kvq_rotate_kernel
 // kvq_axpy_v (3465-3489) adds fma(w * s, value, o) for each position with w != 0; w' = w * s is
-// that product, and a position with w = 0 adds fma(0, value, o) = o, so the value chains of the
-// fp32 attention give its sums. No fp32 copy of the cache is made.
+// that product, and a position with w = 0 gets w' = 0 (not 0 * s, which an inf or NaN scale would
+// turn into NaN) and adds fma(0, centroid, o) = o, so the value chains of the fp32 attention give
+// its sums. No fp32 copy of the cache is made.
 #include <hip/hip_runtime.h>
 
 #include "fgh_internal.h"
@@ -271,7 +272,9 @@ __global__ __launch_bounds__(256) void kvq_softmax_kernel(KvqAttnArgs a) {
         const float w = sum > 0.0f ? ev * inv : ev;
         const float sv =
             *(const float *)(a.vq + slot_of(a.st[tok] + i, a.cap) * (int64_t)(a.n_head_kv * rec) + (int64_t)kvh * rec);
-        s[i] = w * sv;
+        // kvq_axpy_v skips a zero weight (fastgguf.c:4829-4831): stored as 0, never 0 * s_V, so a V
+        // record whose scale is inf or NaN adds nothing where the reference adds nothing
+        s[i] = w == 0.0f ? 0.0f : w * sv;
     }
 }
 

@@ -525,12 +525,10 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 // more (Q6_K: 2), the records within the 160 KiB of LDS of a workgroup and every workgroup of the
 // launch resident at once; tiles per workgroup 4, 2 or 1 for S = 1, 2 or more. Ring depth:
 // 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps, 4 otherwise.
-template <int TYPE, int ORDER = 0>
-static hipError_t mv_launch_type(const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
-    if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
-    const int nb = a.nb, nst = mv_steps(TYPE, nb);
+template <int TYPE>
+static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
+    const int nst = mv_steps(TYPE, nb);
     constexpr int SPW = TYPE == T_Q6_K ? 2 : 1;  // Q6_K steps are 4x the bytes of Q8_0's per row
-    const int64_t tiles = a.groups * ntok;
     int S = 1;
     if (tiles < 768)
         while (S < 8 && tiles * 2 * S <= 2048 && nst >= 8 * S / SPW &&
@@ -539,13 +537,32 @@ static hipError_t mv_launch_type(const MvArgs &a, int ntok, int num_cu, hipStrea
                             mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S), num_cu))
             S *= 2;
     const int R = nst < 32 && tiles * S >= 1024 ? 2 : 4;
-    const size_t lds = mv_lds(TYPE, nb, mv_tpw(S), S);
-    if (lds > (S == 1 ? (size_t)65536 : GEMM_LDS_MAX)) return hipErrorInvalidValue;
-    switch (S) {
-    case 1: return mv_launch_r<TYPE, ORDER, 4, 1>(R, a, ntok, lds, s);
-    case 2: return mv_launch_r<TYPE, ORDER, 2, 2>(R, a, ntok, lds, s);
-    case 4: return mv_launch_r<TYPE, ORDER, 1, 4>(R, a, ntok, lds, s);
-    default: return mv_launch_r<TYPE, ORDER, 1, 8>(R, a, ntok, lds, s);
+    return MvShape{S, R, mv_tpw(S), mv_lds(TYPE, nb, mv_tpw(S), S)};
+}
+template <int TYPE, int ORDER = 0>
+static hipError_t mv_launch_type(const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
+    if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
+    const MvShape sh = mv_shape<TYPE>(a.groups * ntok, a.nb, num_cu);
+    if (sh.lds > (sh.S == 1 ? (size_t)65536 : GEMM_LDS_MAX)) return hipErrorInvalidValue;
+    switch (sh.S) {
+    case 1: return mv_launch_r<TYPE, ORDER, 4, 1>(sh.R, a, ntok, sh.lds, s);
+    case 2: return mv_launch_r<TYPE, ORDER, 2, 2>(sh.R, a, ntok, sh.lds, s);
+    case 4: return mv_launch_r<TYPE, ORDER, 1, 4>(sh.R, a, ntok, sh.lds, s);
+    default: return mv_launch_r<TYPE, ORDER, 1, 8>(sh.R, a, ntok, sh.lds, s);
+    }
+}
+
+MvShape matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu) {
+    switch (type) {
+    case T_Q4_K: case T_Q5_K: return q4k_matvec_shape(type, order, tiles, nb, num_cu);
+    case T_Q6_K: return mv_shape<T_Q6_K>(tiles, nb, num_cu);
+    case T_Q8_0: return mv_shape<T_Q8_0>(tiles, nb, num_cu);
+    case T_Q5_0: return mv_shape<T_Q5_0>(tiles, nb, num_cu);
+    case T_Q5_1: return mv_shape<T_Q5_1>(tiles, nb, num_cu);
+    case T_Q4_1: return mv_shape<T_Q4_1>(tiles, nb, num_cu);
+    case T_IQ4_NL: return mv_shape<T_IQ4_NL>(tiles, nb, num_cu);
+    case T_Q4_0: return mv_shape<T_Q4_0>(tiles, nb, num_cu);
+    default: return MvShape{0, 0, 0, 0};
     }
 }
 

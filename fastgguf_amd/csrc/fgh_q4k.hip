@@ -503,11 +503,8 @@ static hipError_t q4_launch_s(int S, int R, const MvArgs &a, int ntok, size_t ld
     default: return q4_launch_r<ORDER, 1, 8, TYPE>(R, a, ntok, lds, s);
     }
 }
-hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
-    const int nb = a.nb;
-    if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
+MvShape q4k_matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu) {
     if (type == T_Q5_K) order = 0;  // no repacked order for Q5_K
-    const int64_t tiles = a.groups * ntok;
     int S = 1;
     if (tiles < 768)
         while (S < 8 && tiles * 2 * S <= 2048 && nb >= 8 * S &&
@@ -516,11 +513,17 @@ hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int
                             q4_lds(order, nb, q4_tpw(2 * S), 2 * S), num_cu))
             S *= 2;
     const int R = nb < 32 && tiles * S >= 1024 ? 2 : 4;
-    const size_t lds = q4_lds(order, nb, q4_tpw(S), S);
-    if (lds > (S == 1 ? (size_t)65536 : GEMM_LDS_MAX)) return hipErrorInvalidValue;
-    if (type == T_Q5_K) return q4_launch_s<0, T_Q5_K>(S, R, a, ntok, lds, s);
-    if (order == 0) return q4_launch_s<0, T_Q4_K>(S, R, a, ntok, lds, s);
-    return q4_launch_s<1, T_Q4_K>(S, R, a, ntok, lds, s);
+    return MvShape{S, R, q4_tpw(S), q4_lds(order, nb, q4_tpw(S), S)};
+}
+
+hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
+    if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
+    if (type == T_Q5_K) order = 0;
+    const MvShape sh = q4k_matvec_shape(type, order, a.groups * ntok, a.nb, num_cu);
+    if (sh.lds > (sh.S == 1 ? (size_t)65536 : GEMM_LDS_MAX)) return hipErrorInvalidValue;
+    if (type == T_Q5_K) return q4_launch_s<0, T_Q5_K>(sh.S, sh.R, a, ntok, sh.lds, s);
+    if (order == 0) return q4_launch_s<0, T_Q4_K>(sh.S, sh.R, a, ntok, sh.lds, s);
+    return q4_launch_s<1, T_Q4_K>(sh.S, sh.R, a, ntok, sh.lds, s);
 }
 
 // Q8_K images of activation rows, in the kernels' LDS layout (q4_act_bytes(nb) bytes per row): row

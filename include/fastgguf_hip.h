@@ -262,13 +262,19 @@ FGH_API int fgh_event_destroy(fgh_ctx *ctx, void *ev);
  * fgh_gemm_block_ints: the same integers as the prompt GEMM (Q4_K, nb tokens, 1..64) computes
  * them: sumi / msum [nb][rows * n_mats][blocks per row], token t from row t of X (stride ldx).
  * fgh_fp16_to_f32: the device's fp16 -> fp32 decode of n codes.
- * fgh_expf: the device's expf (the MoE softmax and silu) of n values. */
+ * fgh_expf: the device's expf (the MoE softmax and silu) of n values.
+ * fgh_matvec_shape: the launch shape a decode launch of `type` (order as fgh_upload resolved it)
+ * over row_tiles row tiles of all its tensors (16 rows per tile for Q4_K / Q5_K, 8 otherwise) and
+ * ntok tokens picks: shape[0] wavefronts per tile, [1] ring depth, [2] tiles per workgroup, [3]
+ * LDS bytes. Lets the tests run every kernel instantiation the launchers can choose. */
 FGH_API int fgh_quantize(fgh_ctx *ctx, int kind, const float *x, int n, void *out_blocks);
 FGH_API int fgh_block_ints(fgh_ctx *ctx, const fgh_tensor *t, const float *x, int32_t *sumi, int32_t *msum);
 FGH_API int fgh_gemm_block_ints(fgh_ctx *ctx, const fgh_tensor *t, const float *X, int ldx, int nb,
                                 int32_t *sumi, int32_t *msum);
 FGH_API int fgh_expf(fgh_ctx *ctx, const float *x, int n, float *out);
 FGH_API int fgh_fp16_to_f32(fgh_ctx *ctx, const uint16_t *h, int n, float *out);
+FGH_API int fgh_matvec_shape(fgh_ctx *ctx, uint32_t type, int order, int64_t cols, int64_t row_tiles, int ntok,
+                             int32_t *shape);
 
 #ifdef __cplusplus
 }

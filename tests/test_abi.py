@@ -62,3 +62,32 @@ def test_open_without_device_fails_cleanly():
     assert rc == B.ERR_DEVICE and not h.value
     with pytest.raises(B.BackendError):
         B.Backend(0)
+
+
+def test_gpu_off_env_keeps_the_caller_on_cpu(monkeypatch):
+    """FASTGGUF_GPU=off (or 0, cpu, none) makes fgh_open fail without touching a device, as
+    fg_gpu_init_ex returns with g_gpu.state = -1 (fastgguf.c:1972-1976)."""
+    lib = B.load_library()
+    for v in ("off", "0", "cpu", "none"):
+        monkeypatch.setenv("FASTGGUF_GPU", v)
+        h = C.c_void_p(1234)
+        assert lib.fgh_open(0, 0, C.byref(h)) == B.ERR_DEVICE and not h.value
+
+
+def test_c_caller_compiles_links_and_runs(tmp_path):
+    """A C program built with gcc against include/fastgguf_hip.h and linked with the library: the
+    header is valid C99, the exports resolve, and the program runs (GGUF parse; without a device
+    fgh_open fails cleanly and it stays on its CPU path)."""
+    import subprocess
+    exe = tmp_path / "abi_smoke"
+    src = os.path.join(ROOT, "tests", "c_abi", "abi_smoke.c")
+    libdir = os.path.dirname(B.LIB_PATH)
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), src, "-o",
+                        str(exe), "-L", libdir, "-lfastgguf_hip", f"-Wl,-rpath,{libdir}"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe), os.path.join(ROOT, "tests", "golden", "tiny.gguf")], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "output.weight 32 x 64 Q8_0" in r.stdout
+    assert ("staying on the CPU path" in r.stdout) != ("matvec: ok" in r.stdout)

@@ -10,6 +10,7 @@ import pytest
 from conftest import ROOT, golden
 
 import gguf_write as GW
+from fastgguf_amd import synth as S
 from fastgguf_amd.backend import BackendError, Gguf
 
 TINY = os.path.join(ROOT, "tests", "golden", "tiny.gguf")
@@ -94,3 +95,30 @@ def test_corrupted_headers_never_crash(tmp_path):
         for t in f.tensors():
             assert t["offset"] + t["nbytes"] <= len(b)
         f.close()
+
+
+def test_overflowing_dims_and_alignment_refused(tmp_path):
+    """Headers the reference would mis-read: dims whose element product wraps a u64 (here
+    256 x 2^60 x 16 = 2^72, which wraps to 0 and would pass the end-of-file check with a 0-byte
+    tensor), a byte count that wraps after the block division, and general.alignment values
+    below 1 (a division by zero in the reference) or past 2^32. Each is refused with a status."""
+    blk = bytes(144)
+    cases = {
+        "dims_wrap": GW.gguf_bytes([("general.alignment", GW.U32, 32)],
+                                   [("w", S.T_Q4_K, [256, 1 << 60, 16], blk)]),
+        "bytes_wrap": GW.gguf_bytes([("general.alignment", GW.U32, 32)],
+                                    [("w", S.T_Q4_K, [1 << 62, 2], blk)]),
+        "align_half": GW.gguf_bytes([("general.alignment", GW.F32, 0.5)], [("w", S.T_Q4_K, [256, 1], blk)]),
+        "align_huge": GW.gguf_bytes([("general.alignment", GW.U64, 1 << 40)], [("w", S.T_Q4_K, [256, 1], blk)]),
+    }
+    for name, data in cases.items():
+        p = tmp_path / f"{name}.gguf"
+        p.write_bytes(data)
+        with pytest.raises(BackendError):
+            Gguf(str(p)).close()
+    # the same files with sane values open
+    ok = GW.gguf_bytes([("general.alignment", GW.U32, 32)], [("w", S.T_Q4_K, [256, 1], blk)])
+    p = tmp_path / "ok.gguf"
+    p.write_bytes(ok)
+    with Gguf(str(p)) as f:
+        assert f.tensors()[0]["nbytes"] == 144

@@ -125,3 +125,43 @@ def test_matmul_wide_q4k(backend, oracle):
             os_, om = oracle.block_ints(S.T_Q4_K, w[r], act)
             assert np.array_equal(s_[tok, r], os_) and np.array_equal(m_[tok, r], om), f"token {tok} row {r}"
     tt.free()
+
+
+def test_graph_keeps_scratch_across_a_larger_eager_call(oracle):
+    """A graph captured with the prompt GEMM's activation scratch at one size, then an eager call
+    that needs more (the scratch grows), then replays: the graph still owns the buffers it was
+    captured with (the context retires, not frees, a grown buffer while a graph is alive), so
+    every replay equals the eager result bit for bit. A fresh context starts with no scratch."""
+    from fastgguf_amd.backend import Backend
+    be = Backend(0)
+    try:
+        cols, rows = 2048, 128
+        w = S.weights(S.T_Q4_K, rows, cols, 501)
+        t = be.upload(S.T_Q4_K, cols, w)
+        wide = be.upload(S.T_Q4_K, 8192, S.weights(S.T_Q4_K, 64, 8192, 502))
+        X = S.activations(cols, 503, rows=9)
+        Xw = S.activations(8192, 504, rows=64)
+        xd, yd = be.dev_alloc(X.nbytes), be.dev_alloc(4 * 9 * rows)
+        xwd, ywd = be.dev_alloc(Xw.nbytes), be.dev_alloc(4 * 64 * 64)
+        be.h2d(xd, X)
+        be.h2d(xwd, Xw)
+        want = be.matmul(t, X)  # grows the scratch to this call's size before capture
+        be.graph_begin()
+        be.matmul_dev(t, xd, yd, 9)
+        g = be.graph_end()
+        for rep in range(3):
+            be.matmul_dev(wide, xwd, ywd, 64)  # 64 tokens x 8192: every GEMM scratch buffer grows
+            be.h2d(yd, np.full(9 * rows, np.nan, np.float32))
+            be.graph_launch(g)
+            be.sync()
+            got = np.empty((9, rows), np.float32)
+            be.d2h(got, yd)
+            assert bits_equal(got, want), f"replay {rep}"
+            check_tokens(got, oracle.matmul(S.T_Q4_K, w, cols, X, O_RP))
+        be.graph_destroy(g)
+        for p in (xd, yd, xwd, ywd):
+            be.dev_free(p)
+        t.free()
+        wide.free()
+    finally:
+        be.close()

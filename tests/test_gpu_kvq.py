@@ -225,3 +225,27 @@ def oracle_attention_fp32(oracle, q, ck, cv, st, en, n_kv, scale):
     kvo = np.tile(np.arange(n_head) // (n_head // n_kv) * hd, n_tok)
     return oracle.attn_rows(q.reshape(-1, hd), np.repeat(st, n_head), np.repeat(en, n_head), ck, cv, kvo, hd,
                             scale).reshape(q.shape)
+
+
+def test_attention_zero_weight_inf_v_scale(backend, oracle):
+    """kvq_axpy_v skips a position whose weight is 0 (fastgguf.c:4829-4831): a V record with an
+    infinite scale at such a position leaves the output finite. Position 0's key record scale is
+    +1e6 and position 1's -1e6 (same codes), so one score dominates and every other weight
+    underflows to exactly 0; every V record but those two has scale +inf."""
+    rng = np.random.default_rng(77)
+    cap, hd, n_kv, kb, vb = 16, 64, 1, 4, 4
+    rk, rv = rec_bytes(hd, kb), rec_bytes(hd, vb)
+    kq = rng.integers(0, 256, (cap, rk), dtype=np.uint8)
+    vq = rng.integers(0, 256, (cap, rv), dtype=np.uint8)
+    kq[:, :4] = np.full((cap, 1), 1.0, np.float32).view(np.uint8)
+    kq[1, 4:] = kq[0, 4:]
+    kq[0, :4] = np.array([1e6], np.float32).view(np.uint8)
+    kq[1, :4] = np.array([-1e6], np.float32).view(np.uint8)
+    vq[:, :4] = np.full((cap, 1), np.inf, np.float32).view(np.uint8)
+    vq[0:2, :4] = np.full((2, 1), 0.75, np.float32).view(np.uint8)
+    q = rng.standard_normal((1, 2, hd)).astype(np.float32)
+    st, en = np.array([0], np.int32), np.array([cap - 1], np.int32)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    want = oracle_attention(oracle, q, kq, vq, st, en, n_kv, kb, vb, scale)
+    assert np.isfinite(want).all()  # the oracle (the reference's skip) stays finite
+    assert bits_equal(backend.kvq_attention(q, kq, vq, st, en, n_kv, kb, vb, scale), want)

@@ -1,0 +1,117 @@
+"""Every decode-kernel instantiation the launchers can pick runs, bit-exact against the oracle.
+
+The decode launchers choose a launch shape per call from the row tiles of the launch, the row
+width and the device's compute units: S wavefronts per tile (a block split for short matrices),
+a register ring of R steps, TPW tiles per workgroup. Each (type, order, S, R) is a separate kernel
+instantiation, and so are its integer-dump and fused-silu forms. fgh_matvec_shape reports the
+shape a call would take (the same function the launchers call), so these tests
+
+  1. scan row widths and tile counts to find every shape each weight type and order can take, and
+  2. run, for each reachable shape, the smallest tensor that takes it: the matvec bit for bit
+     against the oracle's restatement of the reference kernel (dot_q4Kx8 / dot_q4_K_q8k /
+     dot_q6_K_q8k / dot_q8_0_q8 / ... orders), its per-block integers (the dump form) against the
+     oracle's, and the fused silu form bit for bit against the same matvec of silu(g) * u.
+
+The benchmark's dominant launch (gate and up 4096 -> 14336 in one matvec_multi, both orders) is
+tested at its own size as well.
+"""
+import numpy as np
+import pytest
+from conftest import bits_equal
+
+from fastgguf_amd import synth as S
+from fastgguf_amd.backend import ORDER_REPACKED, ORDER_ROW
+from oracle import ORDER_REPACKED as O_RP
+from oracle import ORDER_ROW as O_ROW
+
+pytestmark = pytest.mark.gpu
+
+FAMILIES = [(S.T_Q4_K, ORDER_REPACKED), (S.T_Q4_K, ORDER_ROW), (S.T_Q5_K, ORDER_ROW), (S.T_Q6_K, ORDER_ROW),
+            (S.T_Q8_0, ORDER_ROW), (S.T_Q5_0, ORDER_ROW), (S.T_Q4_0, ORDER_REPACKED), (S.T_Q4_0, ORDER_ROW),
+            (S.T_Q4_1, ORDER_ROW), (S.T_Q5_1, ORDER_ROW), (S.T_IQ4_NL, ORDER_ROW)]
+TILES = [1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 100, 128, 160, 192, 200, 256, 257, 300, 384, 448, 511, 512,
+         513, 600, 700, 767, 768, 900, 1000, 1023, 1024, 1100, 1536, 1792, 2048]
+NB_K = [1, 2, 3, 4, 7, 8, 12, 15, 16, 17, 24, 31, 32, 33, 40, 56, 64, 100, 128, 200, 237]
+NB_32 = [1, 3, 4, 8, 12, 16, 28, 29, 32, 60, 64, 96, 124, 125, 128, 160, 200, 256, 448, 800, 1600, 1820]
+
+
+def tile_rows(t):
+    return 16 if t in (S.T_Q4_K, S.T_Q5_K) else 8
+
+
+def block_elems(t):
+    return 32 if S.uses_q8(t) else 256
+
+
+def reachable(backend, t, order):
+    """{(S, R): (nb, tiles)} over the scan, the case with the fewest weight bytes for each shape"""
+    found = {}
+    for nb in (NB_32 if S.uses_q8(t) else NB_K):
+        for tiles in TILES:
+            s, r, tpw, lds = backend.matvec_shape(t, order, nb * block_elems(t), tiles)
+            if s == 0 or lds > (65536 if s == 1 else 163840):
+                continue  # such a tensor is refused at upload, or the launch refuses it
+            key = (s, r)
+            if key not in found or nb * tiles < found[key][0] * found[key][1]:
+                found[key] = (nb, tiles)
+    return found
+
+
+def family_id(f):
+    return f"{S.TYPE_NAME[f[0]]}_{'rp' if f[1] == ORDER_REPACKED else 'row'}"
+
+
+@pytest.mark.parametrize("fam", FAMILIES, ids=family_id)
+def test_every_launch_shape_bit_exact(backend, oracle, fam):
+    t, order = fam
+    shapes = reachable(backend, t, order)
+    # the forms the launchers are written for: one wavefront per tile at ring depth 4, and block
+    # splits; Q4_K and the 32-value types also reach ring depth 2 on large launches
+    assert (1, 4) in shapes and any(s > 1 for s, _ in shapes), shapes
+    o_order = O_RP if order == ORDER_REPACKED else O_ROW
+    for (s, r), (nb, tiles) in sorted(shapes.items()):
+        rows = tiles * tile_rows(t)
+        cols = nb * block_elems(t)
+        seed = 1000 + 13 * s + r + nb
+        w = S.random_bytes_weights(t, rows, cols, seed)
+        x = S.activations(cols, seed + 1)
+        tt = backend.upload(t, cols, w, order=order)
+        assert backend.matvec_shape(t, order, cols, tiles)[:2] == (s, r)
+        y = backend.matvec(tt, x)
+        assert bits_equal(y, oracle.matvec(t, w, cols, x, o_order)), f"matvec S={s} R={r} nb={nb} tiles={tiles}"
+        # the integer-dump form of the same shape: a sample of rows against the oracle
+        si, mi = backend.block_ints(tt, x)
+        act = oracle.quantize_for(t, x)
+        for row in sorted({0, 1, rows // 2, rows - 1}):
+            os_, om = oracle.block_ints(t, w[row], act)
+            assert np.array_equal(si[row], os_) and np.array_equal(mi[row], om), f"ints S={s} R={r} row {row}"
+        # the fused silu form of the same shape
+        g = S.activations(cols, seed + 2) * np.float32(2.0)
+        u = S.activations(cols, seed + 3)
+        h = (g / (np.float32(1.0) + oracle.libm_expf(-g)) * u).astype(np.float32)
+        assert bits_equal(backend.matvec_silu(tt, g, u), oracle.matvec(t, w, cols, h, o_order)), \
+            f"silu S={s} R={r} nb={nb} tiles={tiles}"
+        tt.free()
+
+
+@pytest.mark.parametrize("order", [ORDER_REPACKED, ORDER_ROW], ids=["rp", "row"])
+def test_gate_up_one_launch_at_benchmark_size(backend, oracle, order):
+    """The benchmark's dominant launch: gate and up (4096 -> 14336 each, benchmark distributions)
+    in one matvec_multi (the reference's forward, fastgguf.c:4870-4872; matvec_multi 2552-2572),
+    both outputs bit for bit against the oracle (dot_q4Kx8, fastgguf.c:2322-2358, or
+    dot_q4_K_q8k, 1118-1176)."""
+    rows, cols = 14336, 4096
+    wg = S.weights(S.T_Q4_K, rows, cols, 901)
+    wu = S.weights(S.T_Q4_K, rows, cols, 902)
+    tg = backend.upload(S.T_Q4_K, cols, wg, order=order)
+    tu = backend.upload(S.T_Q4_K, cols, wu, order=order)
+    # one launch over both tensors' 2 x 896 tiles of 16 rows: one wavefront per tile, ring depth 2
+    assert backend.matvec_shape(S.T_Q4_K, order, cols, 2 * rows // 16)[:3] == (1, 2, 4)
+    o_order = O_RP if order == ORDER_REPACKED else O_ROW
+    for seed in (903, 904):
+        x = S.activations(cols, seed)
+        yg, yu = backend.matvec_multi([tg, tu], x)
+        assert bits_equal(yg, oracle.matvec(S.T_Q4_K, wg, cols, x, o_order))
+        assert bits_equal(yu, oracle.matvec(S.T_Q4_K, wu, cols, x, o_order))
+    tg.free()
+    tu.free()

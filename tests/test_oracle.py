@@ -381,7 +381,16 @@ def test_kvq_against_the_mathematics(oracle):
         assert np.linalg.norm(dq - x) / np.linalg.norm(x) < bound
 
 
-@pytest.mark.parametrize("mutant", sorted(MUTANTS))
+def test_fp16_against_numpy_exhaustive(oracle):
+    """fgo_fp16 (the reference's FP16() table, fastgguf.c:94-122) against numpy's IEEE half ->
+    float over all 65536 codes: normals, subnormals, signed zeros, infinities and NaNs (any NaN
+    code gives a NaN; the others must match bit for bit)."""
+    h = np.arange(65536, dtype=np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([oracle.lib.fgo_fp16(int(v)) for v in h], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
 
 
 def attn_golden() -> list[dict]:
