@@ -32,7 +32,7 @@ struct fgh_ctx {
     std::string err = "ok";
     // scratch, grown on demand (gpu_grow_buf, fastgguf.c:2083-2091)
     DevBuf x, y, aqs, ad, abs;
-    DevBuf gq, gy, gb;  // prompt-GEMM activations (launch_gemm_quant layout)
+    DevBuf gq;          // prompt-GEMM activation records (launch_gemm_quant layout)
     DevBuf as;          // attention scores / weights
     DevBuf kqr, kor;    // TurboQuant attention: rotated queries, rotated outputs
     DevBuf msel, mw, mg, mu, md, mlog;  // MoE: selection, weights, gate / up / down outputs
@@ -195,28 +195,23 @@ static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const fl
     return FGH_OK;
 }
 
-// the prompt GEMM for a Q4_K tensor: quantize T tokens (device X, stride ldx) into the GEMM
-// layout, then one MFMA launch; ds / dm: optional [T][rows * n_mats][nb] integer dump
-static int gemm_q4k(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
-                    int32_t *ds, int32_t *dm) {
-    const int Tp = T > 32 ? 64 : 32;
-    int rc;
-    if ((rc = grow(c, c->gq, (size_t)Tp * t->cols)) || (rc = grow(c, c->gy, (size_t)Tp * t->nb * 4)) ||
-        (rc = grow(c, c->gb, (size_t)Tp * t->nb * 16)))
-        return rc;
-    HIP_TRY(c, fgh::launch_gemm_quant(X, ldx, t->nb, T, Tp, (int8_t *)c->gq.p, (float *)c->gy.p, (int8_t *)c->gb.p,
-                                      c->stream));
+// the prompt GEMM for a Q4_K tensor: quantize T tokens (device X, stride ldx) into the GEMM's
+// activation records (buffer act, at least gemm_act_bytes), then one MFMA launch; ds / dm:
+// optional [T][rows * n_mats][nb] integer dump
+static int gemm_q4k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
+                         uint8_t *act, int32_t *ds, int32_t *dm) {
+    const int Tp = (T + 15) / 16 * 16;
+    HIP_TRY(c, fgh::launch_gemm_quant(X, ldx, t->nb, T, Tp, act, c->stream));
     fgh::GemmArgs a;
     memset(&a, 0, sizeof(a));
     a.W = t->dev;
     a.Y = Y;
     a.rows = t->rows;
     a.gpm = t->gpm;
+    a.groups = t->groups;
     a.nrows = t->rows * t->n_mats;
     a.nb = t->nb;
-    a.qs = (const int8_t *)c->gq.p;
-    a.ydT = (const float *)c->gy.p;
-    a.bsp = (const int8_t *)c->gb.p;
+    a.act = act;
     a.Tp = Tp;
     a.T = T;
     a.ldy = ldy;
@@ -224,6 +219,12 @@ static int gemm_q4k(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx
     a.dump_m = dm;
     HIP_TRY(c, fgh::launch_q4k_gemm(a, c->stream));
     return FGH_OK;
+}
+static int gemm_q4k(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
+                    int32_t *ds, int32_t *dm) {
+    int rc;
+    if ((rc = grow(c, c->gq, fgh::gemm_act_bytes(t->nb, (T + 15) / 16 * 16)))) return rc;
+    return gemm_q4k_into(c, t, X, ldx, Y, ldy, T, (uint8_t *)c->gq.p, ds, dm);
 }
 
 // host-synchronous and allocating calls cannot be recorded into a graph
@@ -296,7 +297,7 @@ void fgh_close(fgh_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
-    for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->gy, &c->gb, &c->msel, &c->mw, &c->mg,
+    for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->msel, &c->mw, &c->mg,
                       &c->mu, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck, &c->as, &c->kqr,
                       &c->kor})
         if (b->p) (void)hipFree(b->p);
@@ -462,7 +463,7 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
     HIP_TRY(c, hipSetDevice(c->device));
     // nb >= 8: the prompt GEMM (matmul 3018-3031) on int8 MFMA for Q4_K; Q6_K and Q8_0 run the
     // per-token decode kernels (their fp32 orders differ from gemm_kquant's only by rounding)
-    if (nb >= 8 && t->type == FGH_T_Q4_K && fgh::q4k_gemm_lds_bytes(t->nb, nb > 32 ? 64 : 32) <= fgh::GEMM_LDS_MAX)
+    if (nb >= 8 && t->type == FGH_T_Q4_K)
         return gemm_q4k(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
     float *ys[1] = {Y};
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
@@ -925,8 +926,7 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     NO_CAPTURE(c);
     if (!X || !sumi || !msum || nb < 1 || nb > FG_BATCH || ldx < t->cols)
         return fail(c, FGH_ERR_ARG, "gemm_block_ints: bad arguments");
-    if (t->type != FGH_T_Q4_K || fgh::q4k_gemm_lds_bytes(t->nb, nb > 32 ? 64 : 32) > fgh::GEMM_LDS_MAX)
-        return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMM's LDS does not fit this K");
+    if (t->type != FGH_T_Q4_K) return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMM takes Q4_K tensors");
     const int64_t nout = t->rows * t->n_mats;
     const size_t nint = (size_t)nb * nout * t->nb;
     HIP_TRY(c, hipSetDevice(c->device));

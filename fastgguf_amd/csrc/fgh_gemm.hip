@@ -1,370 +1,429 @@
-// fgh_gemm.hip - the prompt-batch (8..64 tokens) Q4_K x Q8_K matmul on gfx950 int8 MFMA
-// (the reference's matmul -> gemm_kquant path, fastgguf.c:2818-2854 and 3004-3031).
+// fgh_gemm.hip - the prompt-batch (8..64 tokens) Q4_K x Q8_K matmul on gfx950 MFMA (the role of
+// the reference's matmul -> gemm_kquant path, fastgguf.c:2756-2854 and 3004-3031).
 //
 // Y[tok * ldy + row] = sum_b yd[tok][b] * (d[row][b] * isum - dmin[row][b] * msum), with the exact
-// per-block integers of the reference (dot_q4_K_q8k, fastgguf.c:1118-1176):
-//   isum = sum_g sc_g * sum_{32 values of g} q * y        msum = sum_g m_g * (bs_2g + bs_2g+1)
+// per-block integers of dot_q4_K_q8k (fastgguf.c:1118-1176):
+//   isum = sum_g sc_g * sum_{32 values of g} q * y        msum = sum_g m_g * bs_g
+// (bs_g = bsums[2g] + bsums[2g+1], the sum of sub-block g's 32 quantized activations).
 //
-// The 6-bit sub-block scale does not fit an int8 operand together with the 4-bit quant
-// (q * sc <= 945), so it is split, sc = 8 sh + sl with sh, sl <= 7, and two v_mfma_i32_32x32x32_i8
-// passes run per 32-value group on pre-scaled weights q*sh and q*sl (both <= 105): every group of
-// a block accumulates into the same two accumulators, and isum = 8 Chi + Clo exactly, with no
-// per-group vector work. msum comes from two v_mfma_i32_32x32x16_i8 on the block's eight 32-value
-// activation sums split into bytes (bs = bl + 128 bh, bl in [0,127], bh in [-32,31]) against the
-// row's eight 6-bit mins: msum = C1 + 128 C2.
+// isum on int8 MFMA (v_mfma_i32_16x16x64_i8). The 6-bit sub-block scale times a 4-bit quant does
+// not fit an int8 operand (q * sc <= 945), so sc = 8 sh + sl (sh, sl <= 7) and two chains run on
+// pre-scaled weights q * sh and q * sl (both <= 105; one packed 16-bit multiply per 4 values):
+// isum = 8 Ch + Cl exactly.
+// msum on f16 MFMA (v_mfma_f32_16x16x16_f16), exact: bs in [-4064, 4064] is split bs = 64 bh + bl
+// (bl in [0, 63], bh in [-64, 63]); the 16 K-slots hold bl_g against m_g and bh_g against 64 m_g,
+// all exact in f16, every product and partial sum an integer below 2^24 in magnitude, so the
+// fp32 result is msum exactly, already a float.
 //
-// MFMA roles: A = activations (M = 32 tokens), B = weights (N = 32 rows). Lane l holds row
-// l % 32 of the output tile and 16 tokens 8 (v / 4) + 4 (l / 32) + v % 4, v = 0..15, so a row's
-// d, dmin, scales and mins are per-lane constants. Both operands give lane l the 16 consecutive
-// values 32 g + 16 (l / 32) + i of a group, so the products pair up whatever order the hardware
-// uses inside one K step.
+// MFMA roles: A = activations (M = 16 tokens), B = weights (N = 16 rows of one Q4_K tile). A lane
+// l = 16 kg + n holds output row n and tokens 4 kg .. 4 kg + 3 of its token tile, so a row's d,
+// dmin, scales and mins are per-lane constants. The weights come straight from the decode layout
+// (fgh_q4k.hip): lane (kg, n) loads chunk kg of row n as the decode kernel's lane 4 n + kg does
+// (two 16-byte slots and the row's 16-byte meta; each load instruction reads 1 KB contiguous),
+// so the GEMM needs no second copy of the weights. In K-step i (0..3) of a block the lane feeds
+// the low (i < 2) or high (i >= 2) nibbles of its slot i & 1: 16 values of sub-block 2 kg or
+// 2 kg + 1. The activation record feeds lane (kg, m) the same 16 K positions of token m, so the
+// products pair up whatever order the hardware uses inside one K step.
 //
-// Weights are read in the decode layout (fgh_q4k.hip): the GEMM needs no second copy. A
-// workgroup owns 64 rows (4 tiles) and all tokens: 4 * NTW wavefronts = 2 slices of 32 rows x 2
-// halves of the blocks (even / odd) x NTW tiles of 32 tokens. It walks the blocks in steps of two:
-// the step's weights for all 64 rows (18 KB) are staged in LDS by the whole workgroup with
-// coalesced loads (1 KB contiguous per wavefront load) and read back as MFMA fragments; activations are read
-// straight from global memory in a fragment-ordered layout (1 KB contiguous per load). Both are
-// double-buffered one step ahead. The two halves of the blocks are added at the end through LDS.
+// Workgroup: 4 tiles (64 rows) x KH K-halves, one wavefront each (KH = 2: two per SIMD). Block b
+// is walked by K-half b % KH. Each step the workgroup loads the next step's activation records
+// (launch_gemm_quant's layout, 1 KB contiguous per wavefront load) into registers while it
+// computes, and writes them to the other of two LDS stages before the step's barrier; each
+// wavefront keeps a ring of 4 blocks of its weights in registers (three steps ahead).
 //
-// fp32 order: per (row, token) and block t = d * float(isum) - dmin * float(msum) (one fma),
-// acc = fma(yd, t, acc) over the wavefront's blocks, out = acc_even + acc_odd. The integers are
+// fp32 order: per (row, token) and block t = fma(-dmin, msum, d * float(isum)),
+// acc = fma(yd, t, acc) over the wavefront's blocks; out = acc_half0 + acc_half1. The integers are
 // exact; the fp32 result differs from gemmk_kern's order (fastgguf.c:2765-2797) only by rounding.
+#include <type_traits>
+
 #include "fgh_internal.h"
 
 namespace fgh {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------------------------
-// Activation quantizer for the GEMM (quantize_q8k, fastgguf.c:773-793, bit-exact): one wavefront
-// per (token, 256-block); lane l holds values 4l..4l+3 (group g = l / 8, half h = (l / 4) % 2).
-// Writes, with NTT = Tp / 32 token tiles and token t = 32 tt + n:
-//   qs  [nb][NTT][8][2][32][16] int8: values 32 g + 16 h .. + 15 of token t at
-//                    ((((b NTT + tt) 8 + g) 2 + h) 32 + n) 16, so the MFMA fragment of (tt, g) is
-//                    1 KB contiguous in lane order (lane = 32 h + n)
-//   ydT [nb][Tp]     fp32 block scales, token-minor (one float4 = 4 consecutive tokens)
-//   bsp [nb][2][32][NTT][8] int8: the 32-value sums bs_g = bsums[2g] + bsums[2g+1] of token t as
-//                    bl_g = bs & 127 at [0][n][tt][g] and bh_g = bs >> 7 at [1][n][tt][g]: MFMA
-//                    lane (n, h) reads its 8 bytes of every token tile at once, lanes contiguous
-// Tokens T..Tp-1 are written as zeros. The block maximum is a DPP reduction within each row of
-// 16 lanes and then across the four rows; the group sums a DPP reduction over 8 lanes.
+// Activation records. Per 256-block b, at b * gemm_rec_bytes(Tp), for Tp = 16 NT tokens (token
+// tiles tt of 16, token t = 16 tt + m):
+//   [0, 256 Tp)        int8 fragments (tt, i), i = 0..3, 1 KB each at (4 tt + i) KB: lane
+//                      l = 16 kg + m holds the 16 quants of token t at K positions
+//                      32 (2 kg + (i >> 1)) + 16 ((i & 1) ^ (kg >> 1)) + 0..15 of the block
+//   [256 Tp, 288 Tp)   f16 min fragments tt, 512 B each: lane (kg, m) holds bl of sub-blocks
+//                      4 kg .. 4 kg + 3 (kg < 2) or bh of sub-blocks 4 (kg - 2) .. + 3 (kg >= 2)
+//   [288 Tp, 292 Tp)   fp32 yd [Tp]
+// Tokens T..Tp-1 are zeros.
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict__ x, int64_t ldx, int nb, int T,
-                                                         int Tp, int8_t *__restrict__ qs, float *__restrict__ ydT,
-                                                         int8_t *__restrict__ bsp) {
-    const int lane = threadIdx.x & 63;
-    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int tok = blockIdx.y;
-    if (b >= nb) return;  // whole wavefront leaves together
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tok < T) v = *(const float4 *)(x + (size_t)tok * ldx + (size_t)b * 256 + 4 * lane);
-    // the block maximum as the reference forms it (a NaN never replaces the running maximum:
-    // fmaxf keeps the other operand)
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#define FGH_ROR(f, ctrl) __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, f), ctrl, 0xF, 0xF, false))
-    amax = fmaxf(amax, FGH_ROR(amax, 0x128));  // row_ror 8, 4, 2, 1: every lane of a row of 16
-    amax = fmaxf(amax, FGH_ROR(amax, 0x124));
-    amax = fmaxf(amax, FGH_ROR(amax, 0x122));
-    amax = fmaxf(amax, FGH_ROR(amax, 0x121));
-#undef FGH_ROR
-    auto lane_f = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, amax), l)); };
-    amax = fmaxf(fmaxf(lane_f(0), lane_f(16)), fmaxf(lane_f(32), lane_f(48)));
+__host__ __device__ constexpr int gemm_rec_bytes(int Tp) { return Tp * 292; }
+
+// quantize_q8k (fastgguf.c:773-793, bit-exact) into the records: workgroup (block b, token tile
+// tt) of 4 wavefronts; wavefront w takes elements 64 w .. 64 w + 63 (sub-blocks 2 w, 2 w + 1) of
+// the 16 tokens, lane (q, m) = (l / 16, l % 16) the 16 values 64 w + 16 q .. + 15 of token m.
+// The block maximum combines the 4 lanes of a token (lane exchanges) and the 4 wavefronts (LDS);
+// fmaxf ignores NaN, so any order gives the reference's maximum.
+__global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict__ x, int64_t ldx, int T, int Tp,
+                                                         uint8_t *__restrict__ rec) {
+    __shared__ float red[4][16];
+    const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int m = l & 15, q = l >> 4;
+    const int b = blockIdx.x, tt = blockIdx.y, tok = 16 * tt + m;
+    float v[16];
+    if (tok < T) {
+        const float *p = x + (size_t)tok * ldx + (size_t)b * 256 + 64 * w + 16 * q;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float4 f = *(const float4 *)(p + 4 * u);
+            v[4 * u] = f.x; v[4 * u + 1] = f.y; v[4 * u + 2] = f.z; v[4 * u + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) amax = fmaxf(amax, fabsf(v[u]));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    if (q == 0) red[w][m] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0][m], red[1][m]), fmaxf(red[2][m], red[3][m]));
     const float d = amax / 127.0f;
     const float id = d > 0.0f ? 1.0f / d : 0.0f;
-    const int q0 = q8_round(v.x * id), q1 = q8_round(v.y * id);
-    const int q2 = q8_round(v.z * id), q3 = q8_round(v.w * id);
-    const int ntt = Tp >> 5, n = tok & 31, tt = tok >> 5, g = lane >> 3, h = (lane >> 2) & 1;
-    *(uint32_t *)(qs + (((((size_t)b * ntt + tt) * 8 + g) * 2 + h) * 32 + n) * 16 + 4 * (lane & 3)) =
-        pack_q(q0, q1, q2, q3);
-    const int s = sum8_i32(q0 + q1 + q2 + q3);  // 32-value group g = lanes 8g..8g+7
-    if ((lane & 7) == 0) {
-        int8_t *p = bsp + (size_t)b * Tp * 16 + (n * ntt + tt) * 8 + g;
-        p[0] = (int8_t)(s & 127);
-        p[32 * ntt * 8] = (int8_t)(s >> 7);
+    uint32_t pk[4];
+    int s = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int q0 = q8_round(v[4 * u] * id), q1 = q8_round(v[4 * u + 1] * id);
+        const int q2 = q8_round(v[4 * u + 2] * id), q3 = q8_round(v[4 * u + 3] * id);
+        s += q0 + q1 + q2 + q3;
+        pk[u] = pack_q(q0, q1, q2, q3);
     }
-    if (lane == 0) ydT[(size_t)b * Tp + tok] = d;
+    uint8_t *r = rec + (size_t)b * gemm_rec_bytes(Tp);
+    // sub-block g = 2 w + (q >> 1), piece q & 1: fragment i = (q & 2) | ((q & 1) ^ (w >> 1)), lane 16 w + m
+    const int i = (q & 2) | ((q & 1) ^ (w >> 1));
+    *(uint4 *)(r + ((size_t)(4 * tt + i) * 64 + 16 * w + m) * 16) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    // the 32-value sums: lanes q and q ^ 1 hold the two halves of one sub-block
+    s += __shfl_xor(s, 16, 64);
+    if ((q & 1) == 0) {
+        const int g = 2 * w + (q >> 1);
+        const int bl = s & 63, bh = s >> 6;  // s = 64 bh + bl
+        _Float16 *mn = (_Float16 *)(r + 256 * Tp + (size_t)tt * 512);
+        mn[(16 * (g >> 2) + m) * 4 + (g & 3)] = (_Float16)bl;
+        mn[(16 * (2 + (g >> 2)) + m) * 4 + (g & 3)] = (_Float16)bh;
+    }
+    if (w == 0 && q == 0) ((float *)(r + 288 * Tp))[tok] = d;
+}
+
+hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s) {
+    if (T < 1 || T > Tp || Tp % 16 || Tp > 64 || nb < 1) return hipErrorInvalidValue;
+    gemm_quant_kernel<<<dim3((unsigned)nb, (unsigned)(Tp / 16)), 256, 0, s>>>(x, ldx, T, Tp, rec);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------------------
 // The GEMM kernel
 // ---------------------------------------------------------------------------------------------
-// LDS stage of one step (blocks KQ s .. KQ s + KQ - 1), copied from the quantizer's output, where
-// those blocks are adjacent: the quants qs [KQ][NTT][8][32][32], and apart from them bsp [KQ][Tp][16]
-// followed by ydT [KQ][Tp] (each stage part its own LDS array, so the compiler can tell the stage
-// being read from the one being filled)
-__host__ __device__ constexpr int gs_q(int Tp, int KQ) { return KQ * Tp * 256; }
-__host__ __device__ constexpr int gs_e(int Tp, int KQ) { return KQ * Tp * 20; }
-__host__ __device__ constexpr int gs_yd(int Tp, int KQ) { return KQ * Tp * 16; }  // in the e part
+constexpr int GEMM_NBUF = 2;  // LDS stages: the step computed and the next one being written
 
-// the tile-layout address of (row R over all matrices, block 0): its tile and its row in the tile
-// (block b is b * gpm * 2304 further)
-__device__ __forceinline__ const uint8_t *gemm_tile(const GemmArgs &a, int64_t R, int &rr) {
-    R = R < a.nrows ? R : a.nrows - 1;
-    const int64_t mat = R / a.rows, r = R - mat * a.rows;
-    rr = (int)(r & 15);
-    return a.W + ((size_t)mat * a.nb * a.gpm + (size_t)(r >> 4)) * 2304;
-}
-
-// one lane's weights of one block: pieces h (= lane / 32) of the four chunks of its row, and the
-// row's meta
-struct WOps {
-    uint4 q[4], m;
+// one lane's weights of one block: slots 0 and 1 of its chunk and its row's meta (rb_load's loads)
+struct GW {
+    uint4 p0, p1, m;
 };
-__device__ __forceinline__ void w_load(WOps &w, const uint8_t *T, size_t boff, int rr, int h) {
-    const uint8_t *p = T + boff;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w.q[j] = ld16(p + 256 + 1024 * (h ^ (j >> 1)) + 16 * (4 * rr + j));
-    w.m = ld16(p + 16 * rr);
+__device__ __forceinline__ void gw_load(const uint8_t *blk, int L, int n, GW &w) {
+    const BufRes r = buf_res(blk, 2304);
+    w.p0 = bld16(r, 256 + 16 * L);
+    w.p1 = bld16(r, 1280 + 16 * L);
+    w.m = bld16(r, 16 * n);
 }
 
-// The workgroup's copy of step s into an LDS stage: three contiguous runs of the quantizer's
-// output, moved by direct-to-LDS loads (global_load_lds_dwordx4: each lane's 16 bytes land at the
-// wavefront's LDS base + 16 * lane, so the stage takes no registers). Completion: vmcnt, then a
-// workgroup barrier. Tp tokens, KQ blocks, NT threads.
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-// One direct-to-LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane i's bytes land at
-// dst + 16 i; dst must be the same in every lane. The compiler builtin sets M0 itself (M0 is a
-// register the compiler reserves, so inline assembly that writes it is not safe); completion is
-// awaited explicitly (s_dma_wait) before the workgroup barrier that publishes the stage.
-__device__ __forceinline__ void dma16(const void *src, uint8_t *dst) {
-    __builtin_amdgcn_global_load_lds(src, (lds_u8 *)dst, 16, 0, 0);
-}
-template <int NT, int Tp, int KQ>
-__device__ __forceinline__ void s_dma(const GemmArgs &a, uint8_t *sq, uint8_t *se, int s, int tid, int wave) {
-    constexpr int QB = Tp * 16;               // 16-byte units of qs per block
-    constexpr int NQ = KQ * QB / NT;          // rounds for the step's blocks
-    constexpr int NE = KQ * Tp + KQ * Tp / 4;  // units of bsp (Tp per block) then ydT (Tp / 4)
-    static_assert(KQ * QB % NT == 0 && NE <= NT, "stage copy shape");
-    const int nb = a.nb;
-#pragma unroll
-    for (int k = 0; k < NQ; ++k) {
-        const int u = tid + k * NT, blk = u / QB;
-        const int b = min(KQ * s + blk, nb - 1);  // blocks past the end: the last again (padding)
-        const int8_t *src = a.qs + (size_t)b * Tp * 256 + 16 * (u - blk * QB);
-        dma16(src, sq + 16 * (k * NT + 64 * wave));
-    }
-    if (64 * wave < NE) {  // uniform: wavefronts holding bsp / ydT units
-        const int e = tid;
-        if (e < NE) {
-            const void *src;
-            if (e < KQ * Tp) {
-                const int blk = e / Tp, b = min(KQ * s + blk, nb - 1);
-                src = a.bsp + ((size_t)b * Tp + (e - blk * Tp)) * 16;
-            } else {
-                const int e2 = e - KQ * Tp, blk = e2 / (Tp / 4), b = min(KQ * s + blk, nb - 1);
-                src = a.ydT + (size_t)b * Tp + 4 * (e2 - blk * (Tp / 4));
-            }
-            dma16(src, se + 1024 * wave);
-        }
-    }
-}
-// every direct-to-LDS load of this wavefront has landed (s_waitcnt vmcnt(0))
-__device__ __forceinline__ void s_dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// one step's activation records held by a thread between their load and their LDS write (named
+// registers, not an array: an array is kept in scratch memory); up to 10 rounds of 16 bytes
+struct ARec {
+    uint4 v0, v1, v2, v3, v4, v5, v6, v7, v8, v9;
+};
 
-__device__ __forceinline__ v4i u4v(uint4 u) { return v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w}; }
+// the integer results of one block of a wavefront
+template <int NT>
+struct GAcc {
+    v4i ch[NT], cl[NT];
+    v4f ms[NT];
+    float d, dmin;
+};
 
-// bytes of q (each <= 15) times a small factor (<= 7): no carry between bytes, two 16-bit lanes
+// bytes of q (each <= 15) times a small factor (<= 7) in both 16-bit lanes: no carry between bytes
 __device__ __forceinline__ uint32_t bmul(uint32_t q, uint32_t f2) {
     const u16x2 r = __builtin_bit_cast(u16x2, q) * __builtin_bit_cast(u16x2, f2);
     return __builtin_bit_cast(uint32_t, r);
 }
+__device__ __forceinline__ v4i u4v(uint4 u) { return v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w}; }
 
-// One 256-block of one wavefront for all its NTT token tiles: weights from registers (prepared
-// once per group for every tile), activations from the LDS stage (slice blk). live == false: a
-// padding block (odd block counts): computed, weighted by zero, not dumped.
-template <int NTT, int KQ, bool DUMP>
-__device__ __forceinline__ void gemm_block(const WOps &w, const uint8_t *sq, const uint8_t *se, int blk, int n, int h,
-                                           float (&acc)[NTT][16], int b, bool live, int64_t row, const GemmArgs &a) {
-    const int Tp = NTT * 32;
-    const Q4KScales sc = q4k_scales(w.m.y, w.m.z, w.m.w);
-    // a padding block contributes zero: its scales are zeroed once here
-    const float d = live ? fp16_bits_to_f32(w.m.x & 0xFFFF) : 0.0f;
-    const float dmin = live ? fp16_bits_to_f32(w.m.x >> 16) : 0.0f;
-    // the split scale factors of the 8 groups as bytes: sh = sc >> 3, sl = sc & 7
-    const uint32_t shb[2] = {(sc.sc_lo >> 3) & 0x07070707u, (sc.sc_hi >> 3) & 0x07070707u};
-    const uint32_t slb[2] = {sc.sc_lo & 0x07070707u, sc.sc_hi & 0x07070707u};
-    // per group g (32 values, sub-block g): the lane's 16 nibbles (chunk g / 2, low or high) times
-    // sh (into Ch) and times sl (into Cl) against the activation fragment of every token tile
-    // (group g of tile tt: 1 KB contiguous per wavefront in the stage); isum = 8 Ch + Cl
-    const uint8_t *qs = sq + (size_t)blk * Tp * 256;
-    v16i ch[NTT], cl[NTT];
+// TPW tiles x KH K-halves per workgroup, one wavefront each; with at most 2 wavefronts per SIMD
+// the compiler may use up to 256 VGPRs per wavefront (all of them VGPRs, so the epilogue reads
+// the MFMA results without moves).
+template <int NT, int KH, int TPW, bool DUMP>
+__global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4k_gemm_kernel(GemmArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int Tp = 16 * NT, REC = gemm_rec_bytes(Tp), NTH = 64 * TPW * KH;
+    constexpr int R = (KH * REC + 16 * NTH - 1) / (16 * NTH), SB = R * 16 * NTH;
+    const int tid = threadIdx.x, l = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tw = wave % TPW, kh = wave / TPW;
+    const int n = l & 15, kg = l >> 4, L = 4 * n + kg;
+    const int nb = a.nb, nsteps = (nb + KH - 1) / KH;
+    const int64_t tile = (int64_t)blockIdx.x * TPW + tw;
+    const bool live = tile < a.groups;
+    const int64_t tc = live ? tile : a.groups - 1;
+    const int64_t mi = tc / a.gpm, ti = tc - mi * a.gpm;
+    const size_t bstride = (size_t)a.gpm * 2304;
+    const uint8_t *W0 = a.W + ((size_t)mi * nb * a.gpm + (size_t)ti) * 2304;
+
+    // the step's records: a linear copy of KH records from block KH s (the quantizer's buffer
+    // holds a record of slack past the last block); round k of thread t copies unit k * NTH + t,
+    // so each wavefront load reads 1 KB contiguous and each LDS write is conflict-free
+    static_assert(R >= 1 && R <= 10, "one step's records take 1..10 rounds per thread");
+    auto aload = [&](int s, ARec &ar) {
+        // the base moves in scalar registers; reads past the step's KH records return 0
+        const BufRes src = buf_res(a.act + (size_t)min(s, nsteps - 1) * KH * REC, KH * REC);
+        auto ld = [&](int k) { return bld16(src, 16 * (k * NTH + tid)); };
+        ar.v0 = ld(0);
+        if (R > 1) ar.v1 = ld(1);
+        if (R > 2) ar.v2 = ld(2);
+        if (R > 3) ar.v3 = ld(3);
+        if (R > 4) ar.v4 = ld(4);
+        if (R > 5) ar.v5 = ld(5);
+        if (R > 6) ar.v6 = ld(6);
+        if (R > 7) ar.v7 = ld(7);
+        if (R > 8) ar.v8 = ld(8);
+        if (R > 9) ar.v9 = ld(9);
+    };
+    auto astore = [&](uint8_t *st, const ARec &ar) {
+        uint4 *dst = (uint4 *)st + tid;
+        dst[0] = ar.v0;
+        if (R > 1) dst[NTH] = ar.v1;
+        if (R > 2) dst[2 * NTH] = ar.v2;
+        if (R > 3) dst[3 * NTH] = ar.v3;
+        if (R > 4) dst[4 * NTH] = ar.v4;
+        if (R > 5) dst[5 * NTH] = ar.v5;
+        if (R > 6) dst[6 * NTH] = ar.v6;
+        if (R > 7) dst[7 * NTH] = ar.v7;
+        if (R > 8) dst[8 * NTH] = ar.v8;
+        if (R > 9) dst[9 * NTH] = ar.v9;
+    };
+    auto wload = [&](int s, GW &w) {
+gw_load(W0 + (size_t)min(KH * s + kh, nb - 1) * bstride, L, n, w); };
+
+    v4f acc[NT];
 #pragma unroll
-    for (int g = 0; g < 8; ++g) {
-        const uint4 pc = w.q[g >> 1];
-        const uint32_t P[4] = {pc.x, pc.y, pc.z, pc.w};
-        // byte g of the factors into both 16-bit lanes (v_perm_b32; selector 0x0C = zero)
-        const uint32_t sel = 0x0C000C00u | (uint32_t)((g & 3) * 0x00010001);
-        const uint32_t fh = __builtin_amdgcn_perm(0u, shb[g >> 2], sel), fl = __builtin_amdgcn_perm(0u, slb[g >> 2], sel);
-        v4i bh, bl;
+    for (int t = 0; t < NT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int64_t rows = a.rows, row = ti * 16 + n;
+    const bool store = live && row < rows;
+    const int64_t orow = mi * rows + row;
+
+    // one block of this wavefront from stage st with weights w
+    auto block = [&](const GW &w, const uint8_t *st, GAcc<NT> &g, auto &&issue) {
+        const uint8_t *rec = st + kh * REC;
+        // sub-block scales 2 kg and 2 kg + 1 as bytes 0 and 1 of scp (scale_min_k4, fastgguf.c:466-472)
+        const int sh = 16 * (kg & 1);
+        const uint32_t A = w.m.y >> sh, C = w.m.w >> sh;
+        const uint32_t sc_lo = A & 0x3f3fu, sc_hi = (C & 0x0f0fu) | ((A >> 2) & 0x3030u);
+        const uint32_t scp = kg >= 2 ? sc_hi : sc_lo;
+        // split factors of the two sub-blocks in both 16-bit lanes
+        const uint32_t fh0 = ((scp >> 3) & 7u) * 0x10001u, fl0 = (scp & 7u) * 0x10001u;
+        const uint32_t fh1 = ((scp >> 11) & 7u) * 0x10001u, fl1 = ((scp >> 8) & 7u) * 0x10001u;
+        // the eight 6-bit mins: m0..m3 in the bytes of u1 & 0x3f3f3f3f, m4..m7 of the nibbles of u2
+        // with u1's top bits; lanes kg & 1 take the second four, as f16 (1024 + m) - 1024, times 64
+        // for kg >= 2
+        const uint32_t mlo = w.m.z & 0x3f3f3f3fu;
+        const uint32_t mhi = ((w.m.w >> 4) & 0x0f0f0f0fu) | (((w.m.z >> 6) & 0x03030303u) << 4);
+        const uint32_t mw = (kg & 1) ? mhi : mlo;
+        const h2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const h2v msc = kg >= 2 ? h2v{(_Float16)64.0f, (_Float16)64.0f} : h2v{(_Float16)1.0f, (_Float16)1.0f};
+        const h2v m01 = (__builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u)) - k1024) * msc;
+        const h2v m23 = (__builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u)) - k1024) * msc;
+        const v4h bmin = {m01[0], m01[1], m23[0], m23[1]};
+        g.d = fp16_bits_to_f32(w.m.x & 0xFFFF);
+        g.dmin = fp16_bits_to_f32(w.m.x >> 16);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t q = (g & 1) ? ((P[k] >> 4) & 0x0F0F0F0Fu) : (P[k] & 0x0F0F0F0Fu);
-            bh[k] = (int)bmul(q, fh);
-            bl[k] = (int)bmul(q, fl);
+        for (int t = 0; t < NT; ++t) {
+            const uint2 am = *(const uint2 *)(rec + 256 * Tp + (size_t)t * 512 + 8 * l);
+            g.ms[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, am), bmin, v4f{0.f, 0.f, 0.f, 0.f},
+                                                          0, 0, 0);
         }
+        const uint32_t P0[4] = {w.p0.x, w.p0.y, w.p0.z, w.p0.w}, P1[4] = {w.p1.x, w.p1.y, w.p1.z, w.p1.w};
+        // the A fragments of K-step i are read from LDS during K-step i - 1
+        auto afrag = [&](int t, int i) { return u4v(*(const uint4 *)(rec + ((size_t)(4 * t + i) * 64 + l) * 16)); };
+        v4i av[NT], an[NT];
 #pragma unroll
-        for (int tt = 0; tt < NTT; ++tt) {
-            const v4i av = u4v(*(const uint4 *)(qs + (((tt * 8 + g) * 2 + h) * 32 + n) * 16));
-            if (g == 0) {
-                const v16i z = {};
-                ch[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bh, z, 0, 0, 0);
-                cl[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bl, z, 0, 0, 0);
-            } else {
-                ch[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bh, ch[tt], 0, 0, 0);
-                cl[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bl, cl[tt], 0, 0, 0);
+        for (int t = 0; t < NT; ++t) av[t] = afrag(t, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i < 3) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) an[t] = afrag(t, i + 1);
             }
+            const uint32_t fh = i < 2 ? fh0 : fh1, fl = i < 2 ? fl0 : fl1;
+            v4i bh, bl;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t p = (i & 1) ? P1[k] : P0[k];
+                const uint32_t v = i < 2 ? (p & 0x0F0F0F0Fu) : ((p >> 4) & 0x0F0F0F0Fu);
+                bh[k] = (int)bmul(v, fh);
+                bl[k] = (int)bmul(v, fl);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (i == 0) {
+                    g.ch[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[t], bh, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    g.cl[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[t], bl, v4i{0, 0, 0, 0}, 0, 0, 0);
+                } else {
+                    g.ch[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[t], bh, g.ch[t], 0, 0, 0);
+                    g.cl[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[t], bl, g.cl[t], 0, 0, 0);
+                }
+            }
+            if (i < 3) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) av[t] = an[t];
+            }
+            issue(i);
         }
-    }
-    // the row's eight mins as bytes; lanes 0-31 feed K slots 0..7 (bl), lanes 32-63 slots 8..15 (bh)
-    const long mp = (long)(((uint64_t)sc.mn_hi << 32) | sc.mn_lo);
-    const long b1 = h == 0 ? mp : 0L, b2 = h == 0 ? 0L : mp;
-    // the lane's activation-sum bytes of every token tile in one read (8 bytes per tile)
-    const uint8_t *bsp = se + (size_t)blk * Tp * 16 + (h * 32 + n) * NTT * 8;
-    uint32_t amw[2 * NTT];
-    if (NTT == 2) {
-        const uint4 t = *(const uint4 *)bsp;
-        amw[0] = t.x; amw[1] = t.y; amw[2 % (2 * NTT)] = t.z; amw[3 % (2 * NTT)] = t.w;
-    } else {
-        const uint2 t = *(const uint2 *)bsp;
-        amw[0] = t.x; amw[1] = t.y;
-    }
-    const float *yds = (const float *)(se + gs_yd(Tp, KQ)) + blk * Tp;
+    };
+    // block b's fp32 epilogue from its integers and its stage's yd
+    auto epilogue = [&](const GAcc<NT> &g, const uint8_t *st, int b) {
+        const float *yds = (const float *)(st + kh * REC + 288 * Tp);
 #pragma unroll
-    for (int tt = 0; tt < NTT; ++tt) {
-        const v16i z = {};
-        const long ab = (long)(((uint64_t)amw[2 * tt + 1] << 32) | amw[2 * tt]);
-        v16i ms = __builtin_amdgcn_mfma_i32_32x32x16_i8(ab, b2, z, 0, 0, 0);
+        for (int t = 0; t < NT; ++t) {
+            const float4 yd = *(const float4 *)(yds + 16 * t + 4 * kg);
+            const float ydv[4] = {yd.x, yd.y, yd.z, yd.w};
 #pragma unroll
-        for (int v = 0; v < 16; ++v) ms[v] <<= 7;
-        ms = __builtin_amdgcn_mfma_i32_32x32x16_i8(ab, b1, ms, 0, 0, 0);
-        float4 yd[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) yd[k] = *(const float4 *)(yds + 32 * tt + 8 * k + 4 * h);
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int isum = (ch[tt][v] << 3) + cl[tt][v], msum = ms[v];
-            const float4 q4 = yd[v >> 2];
-            const float ydv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
-            const float t = __builtin_fmaf(-dmin, (float)msum, d * (float)isum);
-            acc[tt][v] = __builtin_fmaf(ydv, t, acc[tt][v]);
-            if (DUMP) {
-                const int tok = 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (live && tok < a.T && row < a.nrows) {
-                    const size_t i = ((size_t)tok * a.nrows + row) * a.nb + b;
-                    a.dump_s[i] = isum;
-                    a.dump_m[i] = msum;
+            for (int r = 0; r < 4; ++r) {
+                const int isum = (g.ch[t][r] << 3) + g.cl[t][r];
+                const float tt = __builtin_fmaf(-g.dmin, g.ms[t][r], g.d * (float)isum);
+                acc[t][r] = __builtin_fmaf(ydv[r], tt, acc[t][r]);
+                if (DUMP) {
+                    const int tok = 16 * t + 4 * kg + r;
+                    if (store && tok < a.T) {
+                        const size_t di = ((size_t)tok * a.nrows + orow) * nb + b;
+                        a.dump_s[di] = isum;
+                        a.dump_m[di] = (int)g.ms[t][r];
+                    }
                 }
             }
         }
-    }
-}
+    };
 
-// NTT = token tiles (1 or 2), KQ = parts of the blocks (2 or 4). Wavefront w: rs = w & 1 (32-row
-// slice), kq = w >> 1 (blocks b = kq mod KQ); it computes its 32 rows for every token. Step s
-// covers blocks KQ s .. KQ s + KQ - 1: the weights go straight to registers (each wavefront its
-// own rows, one step ahead), the activations of the step's blocks by direct-to-LDS loads to an LDS
-// stage shared by the two row slices (double-buffered, one step ahead). The KQ partial sums are added at the end through LDS, in order.
-template <int NTT, int KQ, bool DUMP>
-__global__ __launch_bounds__(128 * KQ) void q4k_gemm_kernel(GemmArgs a) {
-    constexpr int NT = 128 * KQ, Tp = 32 * NTT;
-    __shared__ __align__(16) uint8_t q0[gs_q(Tp, KQ)], q1[gs_q(Tp, KQ)];
-    __shared__ __align__(16) uint8_t e0[gs_e(Tp, KQ)], e1[gs_e(Tp, KQ)];
-    const int tid = threadIdx.x, l = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rs = wave & 1, kq = wave >> 1;
-    const int n = l & 31, h = l >> 5;
-    const int nb = a.nb, nsteps = (nb + KQ - 1) / KQ;
-    const int64_t row0 = (int64_t)blockIdx.x * 64;
-    const int64_t row = row0 + 32 * rs + n;
-    const size_t bstride = (size_t)a.gpm * 2304;  // one block further in the tile layout
-    int rr;
-    const uint8_t *T = gemm_tile(a, row, rr);
-
-    WOps wa, wb;
-    w_load(wa, T, (size_t)min(kq, nb - 1) * bstride, rr, h);
-    s_dma<NT, Tp, KQ>(a, q0, e0, 0, tid, wave);
-    s_dma_wait();
+    // prologue: step 0's records in LDS, the weights of steps 0..2 in flight
+    GW w0, w1, w2, w3;
+    ARec rr;
+    GAcc<NT> g;
+    uint8_t *st0 = smem, *st1 = smem + SB;
+    aload(0, rr);
+    __builtin_amdgcn_sched_barrier(0);
+    wload(0, w0);
+    wload(1, w1);
+    wload(2, w2);
+    __builtin_amdgcn_sched_barrier(0);
+    astore(st0, rr);
     __syncthreads();
-
-    float acc[NTT][16];
-#pragma unroll
-    for (int tt = 0; tt < NTT; ++tt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[tt][v] = 0.0f;
-    for (int s = 0; s < nsteps; s += 2) {
-        // step s: stage0, weights wa; step s + 1 loads (stage1, wb) in flight
-        w_load(wb, T, (size_t)min(KQ * (s + 1) + kq, nb - 1) * bstride, rr, h);
-        s_dma<NT, Tp, KQ>(a, q1, e1, min(s + 1, nsteps - 1), tid, wave);
-        __builtin_amdgcn_sched_barrier(0);
-        gemm_block<NTT, KQ, DUMP>(wa, q0, e0, kq, n, h, acc, min(KQ * s + kq, nb - 1), KQ * s + kq < nb, row, a);
-        __builtin_amdgcn_sched_barrier(0);
-        s_dma_wait();
-        __syncthreads();
-        if (s + 1 < nsteps) {  // uniform
-            // step s + 1: stage1, weights wb; step s + 2 loads (stage0, wa) in flight
-            w_load(wa, T, (size_t)min(KQ * (s + 2) + kq, nb - 1) * bstride, rr, h);
-            s_dma<NT, Tp, KQ>(a, q0, e0, min(s + 2, nsteps - 1), tid, wave);
+    // step s: compute step s from its stage and weights; between its K-steps load step s + 1's
+    // records (after K-step 0) and step s + 3's weights (after K-step 2, into the ring slot step
+    // s - 1 used); then the epilogue, the records to the other stage, barrier. Issued at the top
+    // of the step instead, the workgroup's loads fill the address queue and every wavefront waits
+    // to issue them before computing. The main loop's steps have a block for every K-half and no
+    // branch, so the compiler's load counters stay exact across them (a branch makes it wait for
+    // every outstanding load, the prefetches included, at the next block); the last steps test.
+    auto step = [&](auto full, int s, GW &wc, GW &wn3, const uint8_t *stc, uint8_t *stn) {
+        const int b = KH * s + kh;
+        auto issue = [&](int i) {
             __builtin_amdgcn_sched_barrier(0);
-            gemm_block<NTT, KQ, DUMP>(wb, q1, e1, kq, n, h, acc, min(KQ * (s + 1) + kq, nb - 1),
-                                      KQ * (s + 1) + kq < nb, row, a);
+            if (i == 0) aload(s + 1, rr);
+            if (i == 2) wload(s + 3, wn3);
             __builtin_amdgcn_sched_barrier(0);
-            s_dma_wait();
-            __syncthreads();
+        };
+        if (decltype(full)::value || b < nb) {  // uniform per wavefront
+            block(wc, stc, g, issue);
+            epilogue(g, stc, b);
+        } else {
+            issue(0);
+            issue(2);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        astore(stn, rr);
+        __syncthreads();
+    };
+    using Full = std::true_type;
+    using Edge = std::false_type;
+    const int nfull = nb / KH;  // steps with a block for every K-half
+    int s = 0;
+    for (; s + 4 <= nfull; s += 4) {
+        step(Full(), s, w0, w3, st0, st1);
+        step(Full(), s + 1, w1, w0, st1, st0);
+        step(Full(), s + 2, w2, w1, st0, st1);
+        step(Full(), s + 3, w3, w2, st1, st0);
     }
-    // parts kq > 0 -> LDS (over the first stage: every wavefront is past its last read of it);
-    // part 0 adds them in order and stores
-    float(*red)[2][NTT][16][64] = (float(*)[2][NTT][16][64])q0;
-    if (kq > 0) {
+    // the remaining steps (at most 4), with the same rings and stage parities
+    if (s < nsteps) step(Edge(), s, w0, w3, st0, st1);
+    if (s + 1 < nsteps) step(Edge(), s + 1, w1, w0, st1, st0);
+    if (s + 2 < nsteps) step(Edge(), s + 2, w2, w1, st0, st1);
+    if (s + 3 < nsteps) step(Edge(), s + 3, w3, w2, st1, st0);
+    __syncthreads();  // every wavefront is past its reads of the stages (the reduction reuses them)
+    if (KH == 2) {  // half 1 -> LDS, half 0 adds it in order and stores
+        float *red = (float *)smem + (size_t)tw * 64 * 4 * NT;  // TPW * 4 KB * NT <= one stage
+        if (kh == 1) {
 #pragma unroll
-        for (int tt = 0; tt < NTT; ++tt)
+            for (int t = 0; t < NT; ++t) *(v4f *)(red + (size_t)(t * 64 + l) * 4) = acc[t];
+        }
+        __syncthreads();
+        if (kh == 1) return;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) red[kq - 1][rs][tt][v][l] = acc[tt][v];
+        for (int t = 0; t < NT; ++t) acc[t] += *(const v4f *)(red + (size_t)(t * 64 + l) * 4);
     }
-    __syncthreads();
-    if (kq == 0 && row < a.nrows) {
+    if (store) {
 #pragma unroll
-        for (int tt = 0; tt < NTT; ++tt)
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int tk = 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3);
-                float y = acc[tt][v];
-#pragma unroll
-                for (int k = 1; k < KQ; ++k) y += red[k - 1][rs][tt][v][l];
-                if (tk < a.T) a.Y[(size_t)tk * a.ldy + row] = y;
+            for (int r = 0; r < 4; ++r) {
+                const int tok = 16 * t + 4 * kg + r;
+                if (tok < a.T) a.Y[(size_t)tok * a.ldy + orow] = acc[t][r];
             }
     }
 }
 
-hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, int8_t *qs, float *ydT, int8_t *bsp,
-                             hipStream_t s) {
-    dim3 grid((nb + 3) / 4, Tp);
-    gemm_quant_kernel<<<grid, 256, 0, s>>>(x, ldx, nb, T, Tp, qs, ydT, bsp);
-    return hipGetLastError();
+static int gemm_kh(int nb) { return nb >= 2 ? 2 : 1; }  // wavefronts per tile (K-halves)
+constexpr int GEMM_TPW = 4;                              // tiles per workgroup
+template <int NT, int KH>
+static size_t gemm_lds(int TPW) {
+    const int nth = 64 * TPW * KH, r = (KH * gemm_rec_bytes(16 * NT) + 16 * nth - 1) / (16 * nth);
+    return (size_t)GEMM_NBUF * r * 16 * nth;
 }
 
-static int gemm_kq(int nb) { return nb >= 8 ? 4 : 2; }  // parts of the blocks per workgroup
+size_t gemm_act_bytes(int nb, int Tp) { return (size_t)(nb + 1) * gemm_rec_bytes(Tp); }
 
-// the kernel's (static) LDS: two stages
-size_t q4k_gemm_lds_bytes(int nb, int Tp) { return 2 * (size_t)(gs_q(Tp, gemm_kq(nb)) + gs_e(Tp, gemm_kq(nb))); }
-
-template <int NTT, int KQ>
+template <int NT, int KH>
 static void gemm_launch(const GemmArgs &a, hipStream_t s) {
-    const dim3 grid((unsigned)((a.nrows + 63) / 64));
-    if (a.dump_s) q4k_gemm_kernel<NTT, KQ, true><<<grid, 128 * KQ, 0, s>>>(a);
-    else q4k_gemm_kernel<NTT, KQ, false><<<grid, 128 * KQ, 0, s>>>(a);
+    constexpr int TPW = GEMM_TPW;
+    const dim3 grid((unsigned)((a.groups + TPW - 1) / TPW));
+    const size_t lds = gemm_lds<NT, KH>(TPW);
+    if (a.dump_s) q4k_gemm_kernel<NT, KH, TPW, true><<<grid, 64 * TPW * KH, lds, s>>>(a);
+    else q4k_gemm_kernel<NT, KH, TPW, false><<<grid, 64 * TPW * KH, lds, s>>>(a);
+}
+template <int NT>
+static void gemm_launch_kh(const GemmArgs &a, hipStream_t s) {
+    if (gemm_kh(a.nb) == 2) gemm_launch<NT, 2>(a, s);
+    else gemm_launch<NT, 1>(a, s);
 }
 
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s) {
-    if (a.T < 1 || a.T > 64 || a.Tp != (a.T > 32 ? 64 : 32) || a.nb < 1 || a.nrows < 1) return hipErrorInvalidValue;
-    if (q4k_gemm_lds_bytes(a.nb, a.Tp) > GEMM_LDS_MAX) return hipErrorInvalidValue;
-    const int kq = gemm_kq(a.nb);
-    if (a.Tp == 64) kq == 4 ? gemm_launch<2, 4>(a, s) : gemm_launch<2, 2>(a, s);
-    else kq == 4 ? gemm_launch<1, 4>(a, s) : gemm_launch<1, 2>(a, s);
+    if (a.T < 1 || a.T > a.Tp || a.Tp % 16 || a.Tp > 64 || a.Tp - a.T >= 16 || a.nb < 1 || a.groups < 1)
+        return hipErrorInvalidValue;
+    switch (a.Tp / 16) {
+    case 1: gemm_launch_kh<1>(a, s); break;
+    case 2: gemm_launch_kh<2>(a, s); break;
+    case 3: gemm_launch_kh<3>(a, s); break;
+    default: gemm_launch_kh<4>(a, s); break;
+    }
     return hipGetLastError();
 }
 

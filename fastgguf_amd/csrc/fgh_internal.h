@@ -339,20 +339,20 @@ hipError_t launch_kvq_attention(const KvqAttnArgs &a, int n_tok, hipStream_t s);
 
 // prompt-batch Q4_K GEMM (fgh_gemm.hip): 1..64 tokens, weights in the Q4_K decode layout
 struct GemmArgs {
-    const uint8_t *W;   // Q4_K tensor (tile layout)
-    float *Y;           // Y[tok * ldy + row]
-    int64_t rows, gpm;  // rows and 16-row tiles per matrix
-    int64_t nrows;      // rows over all matrices (outputs per token)
-    int nb;             // 256-blocks per row
-    const int8_t *qs;   // activations from launch_gemm_quant
-    const float *ydT;
-    const int8_t *bsp;
-    int Tp, T;          // padded token count (32 or 64), tokens
+    const uint8_t *W;      // Q4_K tensor (tile layout)
+    float *Y;              // Y[tok * ldy + row]
+    int64_t rows, gpm;     // rows and 16-row tiles per matrix
+    int64_t groups;        // tiles over all matrices
+    int64_t nrows;         // rows over all matrices (outputs per token)
+    int nb;                // 256-blocks per row
+    const uint8_t *act;    // activation records from launch_gemm_quant
+    int Tp, T;             // padded token count (a multiple of 16, Tp - T < 16), tokens
     int64_t ldy;
     int32_t *dump_s, *dump_m;  // test hook: [T][nrows][nb] integers, or null
 };
-hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, int8_t *qs, float *ydT, int8_t *bsp,
-                             hipStream_t s);
+// quantizes T rows of x (stride ldx) into the GEMM's activation records (gemm_act_bytes(nb, Tp))
+hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s);
+size_t gemm_act_bytes(int nb, int Tp);
 constexpr size_t GEMM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
 // true when all wg workgroups of a launch (waves wavefronts and lds bytes each) can be resident
 // on num_cu CUs at once: a split launch whose workgroups need a second round is slower than a
@@ -361,7 +361,6 @@ inline bool all_resident(int64_t wg, int waves, size_t lds, int num_cu) {
     const int64_t by_lds = lds ? (int64_t)(GEMM_LDS_MAX / lds) : 64, by_waves = 32 / waves;
     return wg <= (int64_t)num_cu * (by_lds < by_waves ? by_lds : by_waves);
 }
-size_t q4k_gemm_lds_bytes(int nb, int Tp);  // <= GEMM_LDS_MAX for the GEMM to run
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s);
 
 }  // namespace fgh
