@@ -59,23 +59,21 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 // ---------------------------------------------------------------------------------------------
 __host__ __device__ constexpr int gemm_rec_bytes(int Tp) { return Tp * 292; }
 
-// quantize_q8k (fastgguf.c:773-793, bit-exact) into the records: workgroup (block b, token tile
-// tt) of 4 wavefronts; wavefront w takes elements 64 w .. 64 w + 63 (sub-blocks 2 w, 2 w + 1) of
-// the 16 tokens, lane (q, m) = (l / 16, l % 16) the 16 values 64 w + 16 q .. + 15 of token m.
-// The block maximum combines the 4 lanes of a token (lane exchanges) and the 4 wavefronts (LDS);
-// fmaxf ignores NaN, so any order gives the reference's maximum.
-__global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict__ x, int64_t ldx, int T, int Tp,
-                                                         uint8_t *__restrict__ rec) {
-    __shared__ float red[4][16];
-    const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int m = l & 15, q = l >> 4;
-    const int b = blockIdx.x, tt = blockIdx.y, tok = 16 * tt + m;
+// quantize_q8k (fastgguf.c:773-793, bit-exact) into the records: one wavefront per (block b,
+// 4 tokens); lane l = 16 u + p takes token 4 blockIdx.y + u and the 16 values 16 p .. 16 p + 15 of
+// the block (piece p of sub-block g = p / 2). The block maximum and the 32-value sums combine
+// lanes of one token by lane exchanges (no LDS, no barrier); fmaxf ignores NaN, so any order
+// gives the reference's maximum.
+__global__ __launch_bounds__(64) void gemm_quant_kernel(const float *__restrict__ x, int64_t ldx, int T, int Tp,
+                                                        uint8_t *__restrict__ rec) {
+    const int l = threadIdx.x, p = l & 15;
+    const int b = blockIdx.x, tok = 4 * blockIdx.y + (l >> 4);
     float v[16];
     if (tok < T) {
-        const float *p = x + (size_t)tok * ldx + (size_t)b * 256 + 64 * w + 16 * q;
+        const float *src = x + (size_t)tok * ldx + (size_t)b * 256 + 16 * p;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const float4 f = *(const float4 *)(p + 4 * u);
+            const float4 f = *(const float4 *)(src + 4 * u);
             v[4 * u] = f.x; v[4 * u + 1] = f.y; v[4 * u + 2] = f.z; v[4 * u + 3] = f.w;
         }
     } else {
@@ -85,11 +83,8 @@ __global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict
     float amax = 0.0f;
 #pragma unroll
     for (int u = 0; u < 16; ++u) amax = fmaxf(amax, fabsf(v[u]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    if (q == 0) red[w][m] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red[0][m], red[1][m]), fmaxf(red[2][m], red[3][m]));
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
     const float d = amax / 127.0f;
     const float id = d > 0.0f ? 1.0f / d : 0.0f;
     uint32_t pk[4];
@@ -102,24 +97,23 @@ __global__ __launch_bounds__(256) void gemm_quant_kernel(const float *__restrict
         pk[u] = pack_q(q0, q1, q2, q3);
     }
     uint8_t *r = rec + (size_t)b * gemm_rec_bytes(Tp);
-    // sub-block g = 2 w + (q >> 1), piece q & 1: fragment i = (q & 2) | ((q & 1) ^ (w >> 1)), lane 16 w + m
-    const int i = (q & 2) | ((q & 1) ^ (w >> 1));
-    *(uint4 *)(r + ((size_t)(4 * tt + i) * 64 + 16 * w + m) * 16) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    // the 32-value sums: lanes q and q ^ 1 hold the two halves of one sub-block
-    s += __shfl_xor(s, 16, 64);
-    if ((q & 1) == 0) {
-        const int g = 2 * w + (q >> 1);
+    const int tt = tok >> 4, m = tok & 15, g = p >> 1, kg = g >> 1;
+    // piece p = 2 g + h lands in fragment i = 2 (g & 1) + (h ^ (kg >> 1)) of lane 16 kg + m
+    const int i = 2 * (g & 1) + ((p & 1) ^ (kg >> 1));
+    *(uint4 *)(r + ((size_t)(4 * tt + i) * 64 + 16 * kg + m) * 16) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    s += __shfl_xor(s, 1, 64);  // the sub-block's two pieces
+    if ((p & 1) == 0) {
         const int bl = s & 63, bh = s >> 6;  // s = 64 bh + bl
         _Float16 *mn = (_Float16 *)(r + 256 * Tp + (size_t)tt * 512);
         mn[(16 * (g >> 2) + m) * 4 + (g & 3)] = (_Float16)bl;
         mn[(16 * (2 + (g >> 2)) + m) * 4 + (g & 3)] = (_Float16)bh;
     }
-    if (w == 0 && q == 0) ((float *)(r + 288 * Tp))[tok] = d;
+    if (p == 0) ((float *)(r + 288 * Tp))[tok] = d;
 }
 
 hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s) {
     if (T < 1 || T > Tp || Tp % 16 || Tp > 64 || nb < 1) return hipErrorInvalidValue;
-    gemm_quant_kernel<<<dim3((unsigned)nb, (unsigned)(Tp / 16)), 256, 0, s>>>(x, ldx, T, Tp, rec);
+    gemm_quant_kernel<<<dim3((unsigned)nb, (unsigned)(Tp / 4)), 64, 0, s>>>(x, ldx, T, Tp, rec);
     return hipGetLastError();
 }
 
