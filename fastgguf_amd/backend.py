@@ -26,7 +26,7 @@ ACT_Q8, ACT_Q8K = 1, 2
 EXPORTS = (
     "fgh_open", "fgh_close", "fgh_info", "fgh_last_error", "fgh_upload", "fgh_tensor_free",
     "fgh_matvec", "fgh_matvec_multi", "fgh_matmul", "fgh_moe_ffn", "fgh_attention",
-    "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matvec_silu_dev", "fgh_matmul_dev", "fgh_moe_ffn_dev",
+    "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matvec_silu_dev", "fgh_matmul_dev", "fgh_matmul_dev_noalloc", "fgh_moe_ffn_dev",
     "fgh_attention_dev", "fgh_kvq_store_dev", "fgh_kvq_attention_dev",
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_sync",
@@ -81,6 +81,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_matvec_multi_dev": (i32, [vp, i32, vp, vp, vp]),
         "fgh_matvec_silu_dev": (i32, [vp, vp, vp, vp, vp]),
         "fgh_matmul_dev": (i32, [vp, vp, vp, i32, vp, i32, i32]),
+        "fgh_matmul_dev_noalloc": (i32, [vp, vp, vp, i32, vp, i32, i32]),
         "fgh_moe_ffn_dev": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, i32]),
         "fgh_attention": (i32, [vp, i32, i32, i32, i32, vp, vp, vp, vp, i32, i32, vp, vp, C.c_float]),
         "fgh_attention_dev": (i32, [vp, i32, i32, i32, i32, vp, vp, vp, vp, i32, i32, vp, vp, i32, C.c_float]),
@@ -445,6 +446,10 @@ class Backend:
 
     def matmul_dev(self, t: Tensor, X_dev: int, Y_dev: int, nb: int):
         self._check(self.lib.fgh_matmul_dev(self.ctx, t.handle, X_dev, t.cols, Y_dev, t.nout, nb))
+
+    def matmul_dev_noalloc(self, t: Tensor, X_dev: int, Y_dev: int, nb: int):
+        """matmul_dev with the prompt GEMM's scratch in the library's static per-device array"""
+        self._check(self.lib.fgh_matmul_dev_noalloc(self.ctx, t.handle, X_dev, t.cols, Y_dev, t.nout, nb))
 
     def moe_ffn_dev(self, gate: Tensor, up: Tensor, down: Tensor, k: int, logits_dev: int, X_dev: int,
                     Y_dev: int, n_tok: int):

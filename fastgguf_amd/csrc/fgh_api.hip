@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -48,7 +49,30 @@ struct fgh_ctx {
     // failure injection (FGH_FAIL_AT=n at fgh_open): the n-th compute call on this context fails
     // with FGH_ERR before it launches anything, so a caller's CPU fallback can be tested
     int64_t calls = 0, fail_at = 0;
+    void *noalloc = nullptr;  // this device's address of the static scratch (null: unavailable)
 };
+
+// fgh_matmul_dev_noalloc's scratch: a static array, one copy per device. In host code its name
+// is only a host-side stand-in; kernels get the device address that hipGetSymbolAddress returns
+// with the device current, taken once per device at its first fgh_open and kept here.
+static __device__ __align__(256) uint8_t scratch[FGH_NOALLOC_SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+static std::mutex scratch_mu;
+static void *scratch_addr[MAX_DEVICES];
+static bool scratch_tried[MAX_DEVICES];
+
+// the device address of scratch on the current device (null if it cannot be had)
+static void *scratch_on(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_tried[device]) {
+        scratch_tried[device] = true;
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess) scratch_addr[device] = p;
+        else (void)hipGetLastError();
+    }
+    return scratch_addr[device];
+}
 
 // counts one compute call; true (with the context's message set) when it is the injected failure
 static bool injected_failure(fgh_ctx *c);
@@ -284,6 +308,7 @@ int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out) {
         delete c;
         return FGH_ERR_DEVICE;
     }
+    c->noalloc = scratch_on(device);  // the device is current
     if (selfcheck(c) != FGH_OK) {  // gpu_selfcheck gates use (fastgguf.c:2048-2052)
         fgh_close(c);
         return FGH_ERR_DEVICE;
@@ -465,6 +490,28 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
     // per-token decode kernels (their fp32 orders differ from gemm_kquant's only by rounding)
     if (nb >= 8 && t->type == FGH_T_Q4_K)
         return gemm_q4k(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
+    float *ys[1] = {Y};
+    return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
+}
+
+int fgh_matmul_dev_noalloc(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, float *Y, int ldy, int nb) {
+    int rc = check_tensor(c, t);
+    if (rc) return rc;
+    if (!X || !Y || nb < 1 || nb > FG_BATCH || ldx < t->cols || ldy < t->rows * t->n_mats)
+        return fail(c, FGH_ERR_ARG, "matmul_dev_noalloc: bad arguments");
+    const bool gemm = nb >= 8 && t->type == FGH_T_Q4_K;  // the one path of fgh_matmul_dev with scratch
+    if (gemm) {
+        const size_t need = fgh::gemm_act_bytes(t->nb, (nb + 15) / 16 * 16);
+        if (need > FGH_NOALLOC_SCRATCH_BYTES)
+            return fail(c, FGH_ERR_ARG,
+                        "matmul_dev_noalloc: %d tokens x %lld columns need %zu bytes of scratch, more than its %u",
+                        nb, (long long)t->cols, need, FGH_NOALLOC_SCRATCH_BYTES);
+        if (!c->noalloc)
+            return fail(c, FGH_ERR_DEVICE, "matmul_dev_noalloc: no device address for the static scratch");
+    }
+    INJECT(c);
+    HIP_TRY(c, hipSetDevice(c->device));
+    if (gemm) return gemm_q4k_into(c, t, X, ldx, Y, ldy, nb, (uint8_t *)c->noalloc, nullptr, nullptr);
     float *ys[1] = {Y};
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
 }

@@ -1,0 +1,83 @@
+"""fgh_matmul_dev_noalloc: the prompt matmul with its GEMM scratch in the library's static
+per-device array instead of context buffers. Through the C ABI, its outputs equal fgh_matmul_dev's
+bit for bit (the same kernels on the same inputs), over two calls in a row with the second one
+smaller, on a fresh context as well as on one that has already run other work; a call whose
+scratch would exceed FGH_NOALLOC_SCRATCH_BYTES fails with FGH_ERR_ARG before launching anything."""
+import numpy as np
+import pytest
+from conftest import bits_equal
+
+from fastgguf_amd import synth as S
+from fastgguf_amd.backend import Backend, BackendError
+
+pytestmark = pytest.mark.gpu
+
+FGH_ERR_ARG = -2
+SCRATCH_BYTES = 4 << 20  # FGH_NOALLOC_SCRATCH_BYTES
+
+
+def run_both(be, t, X):
+    """(noalloc output, matmul_dev output) for the tokens X on tensor t, both on the device"""
+    T = X.shape[0]
+    xd = be.dev_alloc(X.nbytes)
+    ya, yb = be.dev_alloc(4 * T * t.nout), be.dev_alloc(4 * T * t.nout)
+    be.h2d(xd, X)
+    poison = np.full(T * t.nout, np.nan, np.float32)
+    be.h2d(ya, poison)
+    be.h2d(yb, poison)
+    be.matmul_dev_noalloc(t, xd, ya, T)
+    be.matmul_dev(t, xd, yb, T)
+    be.sync()
+    got, want = np.empty((T, t.nout), np.float32), np.empty((T, t.nout), np.float32)
+    be.d2h(got, ya)
+    be.d2h(want, yb)
+    for p in (xd, ya, yb):
+        be.dev_free(p)
+    return got, want
+
+
+# (type, rows, cols, tokens): the first two take the prompt GEMM (Q4_K, >= 8 tokens), the larger
+# one first, so the second call reuses the array with a smaller input; the others run the decode
+# kernels, which need no scratch
+CALLS = [(S.T_Q4_K, 1024, 8192, 64), (S.T_Q4_K, 272, 2048, 9), (S.T_Q4_K, 128, 2048, 5), (S.T_Q6_K, 96, 1024, 12)]
+
+
+@pytest.mark.parametrize("fresh", [True, False], ids=["fresh_context", "shared_context"])
+def test_noalloc_matches_matmul_dev(backend, fresh):
+    be = Backend(0) if fresh else backend
+    try:
+        for i, (ty, rows, cols, T) in enumerate(CALLS):
+            w = S.weights(ty, rows, cols, 700 + i)
+            X = S.activations(cols, 710 + i, rows=T)
+            t = be.upload(ty, cols, w)
+            got, want = run_both(be, t, X)
+            assert not np.isnan(want).any()
+            assert bits_equal(got, want), f"call {i}: {S.TYPE_NAME[ty]} {rows}x{cols}, {T} tokens"
+            t.free()
+    finally:
+        if fresh:
+            be.close()
+
+
+def test_noalloc_refuses_more_than_its_scratch(backend):
+    """224 blocks x 64 tokens need (224 + 1) * 292 * 64 bytes > 4 MiB: refused, nothing launched;
+    223 blocks fit and run"""
+    for nbk, ok in ((223, True), (224, False)):
+        cols = 256 * nbk
+        assert ((nbk + 1) * 292 * 64 <= SCRATCH_BYTES) == ok
+        t = backend.upload(S.T_Q4_K, cols, S.weights(S.T_Q4_K, 16, cols, 720 + nbk))
+        X = S.activations(cols, 730, rows=64)
+        if ok:
+            got, want = run_both(backend, t, X)
+            assert bits_equal(got, want)
+        else:
+            xd, yd = backend.dev_alloc(X.nbytes), backend.dev_alloc(4 * 64 * 16)
+            with pytest.raises(BackendError) as e:
+                backend.matmul_dev_noalloc(t, xd, yd, 64)
+            assert e.value.status == FGH_ERR_ARG and "scratch" in str(e.value)
+            backend.dev_free(xd)
+            backend.dev_free(yd)
+            # the context still works after the refusal
+            got, want = run_both(backend, t, X[:8])
+            assert bits_equal(got, want)
+        t.free()
