@@ -244,11 +244,51 @@ static int gemm_q4k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_
     HIP_TRY(c, fgh::launch_q4k_gemm(a, c->stream));
     return FGH_OK;
 }
-static int gemm_q4k(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
-                    int32_t *ds, int32_t *dm) {
+// the prompt GEMM for a Q8_0 tensor (gemm_q32, fastgguf.c:2856-2999): Q8 records of T tokens, then
+// one MFMA launch on the decode tiles; ds: optional [T][rows * n_mats][nb] integer dump
+static int gemm_q80_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
+                         uint8_t *act, int32_t *ds) {
+    const int Tp = T <= 32 ? 32 : 64;
+    HIP_TRY(c, fgh::launch_gemm32_quant(X, ldx, t->nb, T, Tp, act, c->stream));
+    fgh::Gemm32Args a;
+    memset(&a, 0, sizeof(a));
+    a.W = t->dev;
+    a.Y = Y;
+    a.rows = t->rows;
+    a.tpm = t->gpm;
+    a.gpm32 = (t->gpm + 3) / 4;
+    a.groups = a.gpm32 * t->n_mats;
+    a.nrows = t->rows * t->n_mats;
+    a.nb = t->nb;
+    a.nsteps = t->ntile;
+    a.act = act;
+    a.Tp = Tp;
+    a.T = T;
+    a.ldy = ldy;
+    a.dump_s = ds;
+    HIP_TRY(c, fgh::launch_q80_gemm(a, c->stream));
+    return FGH_OK;
+}
+
+// the types and token counts that take a prompt GEMM (matmul, fastgguf.c:3018-3031), and the
+// activation-record bytes it needs (0: the per-token decode kernels, which need no scratch)
+static size_t prompt_gemm_bytes(const fgh_tensor *t, int T) {
+    if (T < 8) return 0;
+    if (t->type == FGH_T_Q4_K) return fgh::gemm_act_bytes(t->nb, (T + 15) / 16 * 16);
+    if (t->type == FGH_T_Q8_0) return fgh::gemm32_act_bytes(t->nb, T <= 32 ? 32 : 64);
+    return 0;
+}
+// the prompt GEMM with its records in act (at least prompt_gemm_bytes)
+static int prompt_gemm_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy,
+                            int T, uint8_t *act, int32_t *ds, int32_t *dm) {
+    if (t->type == FGH_T_Q8_0) return gemm_q80_into(c, t, X, ldx, Y, ldy, T, act, ds);
+    return gemm_q4k_into(c, t, X, ldx, Y, ldy, T, act, ds, dm);
+}
+static int prompt_gemm(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
+                       int32_t *ds, int32_t *dm) {
     int rc;
-    if ((rc = grow(c, c->gq, fgh::gemm_act_bytes(t->nb, (T + 15) / 16 * 16)))) return rc;
-    return gemm_q4k_into(c, t, X, ldx, Y, ldy, T, (uint8_t *)c->gq.p, ds, dm);
+    if ((rc = grow(c, c->gq, prompt_gemm_bytes(t, T)))) return rc;
+    return prompt_gemm_into(c, t, X, ldx, Y, ldy, T, (uint8_t *)c->gq.p, ds, dm);
 }
 
 // host-synchronous and allocating calls cannot be recorded into a graph
@@ -486,10 +526,10 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
         return fail(c, FGH_ERR_ARG, "matmul: bad arguments");
     INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
-    // nb >= 8: the prompt GEMM (matmul 3018-3031) on int8 MFMA for Q4_K; Q6_K and Q8_0 run the
-    // per-token decode kernels (their fp32 orders differ from gemm_kquant's only by rounding)
-    if (nb >= 8 && t->type == FGH_T_Q4_K)
-        return gemm_q4k(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
+    // nb >= 8: the prompt GEMM (matmul 3018-3031) on int8 MFMA for Q4_K and Q8_0; the other types
+    // run the per-token decode kernels (their fp32 orders differ from the reference's GEMM orders
+    // only by rounding)
+    if (prompt_gemm_bytes(t, nb)) return prompt_gemm(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
     float *ys[1] = {Y};
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
 }
@@ -499,9 +539,9 @@ int fgh_matmul_dev_noalloc(fgh_ctx *c, const fgh_tensor *t, const float *X, int 
     if (rc) return rc;
     if (!X || !Y || nb < 1 || nb > FG_BATCH || ldx < t->cols || ldy < t->rows * t->n_mats)
         return fail(c, FGH_ERR_ARG, "matmul_dev_noalloc: bad arguments");
-    const bool gemm = nb >= 8 && t->type == FGH_T_Q4_K;  // the one path of fgh_matmul_dev with scratch
+    const size_t need = prompt_gemm_bytes(t, nb);  // the prompt GEMMs are the paths with scratch
+    const bool gemm = need > 0;
     if (gemm) {
-        const size_t need = fgh::gemm_act_bytes(t->nb, (nb + 15) / 16 * 16);
         if (need > FGH_NOALLOC_SCRATCH_BYTES)
             return fail(c, FGH_ERR_ARG,
                         "matmul_dev_noalloc: %d tokens x %lld columns need %zu bytes of scratch, more than its %u",
@@ -511,7 +551,7 @@ int fgh_matmul_dev_noalloc(fgh_ctx *c, const fgh_tensor *t, const float *X, int 
     }
     INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
-    if (gemm) return gemm_q4k_into(c, t, X, ldx, Y, ldy, nb, (uint8_t *)c->noalloc, nullptr, nullptr);
+    if (gemm) return prompt_gemm_into(c, t, X, ldx, Y, ldy, nb, (uint8_t *)c->noalloc, nullptr, nullptr);
     float *ys[1] = {Y};
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
 }
@@ -973,7 +1013,9 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     NO_CAPTURE(c);
     if (!X || !sumi || !msum || nb < 1 || nb > FG_BATCH || ldx < t->cols)
         return fail(c, FGH_ERR_ARG, "gemm_block_ints: bad arguments");
-    if (t->type != FGH_T_Q4_K) return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMM takes Q4_K tensors");
+    if (t->type != FGH_T_Q4_K && t->type != FGH_T_Q8_0)
+        return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMMs take Q4_K and Q8_0 tensors");
+    if (nb < 8) return fail(c, FGH_ERR_ARG, "gemm_block_ints: the prompt GEMM runs 8..64 tokens");
     const int64_t nout = t->rows * t->n_mats;
     const size_t nint = (size_t)nb * nout * t->nb;
     HIP_TRY(c, hipSetDevice(c->device));
@@ -984,7 +1026,9 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     hipError_t e = hipMemcpy2DAsync(c->x.p, (size_t)t->cols * 4, X, (size_t)ldx * 4, (size_t)t->cols * 4, nb,
                                     hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) {
-        rc = gemm_q4k(c, t, (const float *)c->x.p, t->cols, (float *)c->y.p, nout, nb, dsi, dmi);
+        // Q8_0 has no min term: its msum are zeros, as the oracle's
+        if (t->type == FGH_T_Q8_0) e = hipMemsetAsync(dmi, 0, nint * 4, c->stream);
+        if (e == hipSuccess) rc = prompt_gemm(c, t, (const float *)c->x.p, t->cols, (float *)c->y.p, nout, nb, dsi, dmi);
         if (!rc) {
             e = hipMemcpyAsync(sumi, dsi, nint * 4, hipMemcpyDeviceToHost, c->stream);
             if (e == hipSuccess) e = hipMemcpyAsync(msum, dmi, nint * 4, hipMemcpyDeviceToHost, c->stream);

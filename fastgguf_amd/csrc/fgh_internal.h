@@ -350,6 +350,25 @@ struct GemmArgs {
     int64_t ldy;
     int32_t *dump_s, *dump_m;  // test hook: [T][nrows][nb] integers, or null
 };
+// the Q8_0 prompt GEMM (fgh_gemm32.hip) on the decode tiles (8-row tiles, 4 blocks per tile step)
+struct Gemm32Args {
+    const uint8_t *W;      // Q8_0 tensor (tile layout)
+    float *Y;              // Y[tok * ldy + row]
+    int64_t rows;          // rows per matrix
+    int64_t tpm;           // 8-row tiles per matrix
+    int64_t gpm32;         // 32-row groups per matrix, (tpm + 3) / 4
+    int64_t groups;        // 32-row groups over all matrices
+    int64_t nrows;         // rows over all matrices (outputs per token)
+    int nb, nsteps;        // 32-blocks per row, tile steps per row ((nb + 3) / 4)
+    const uint8_t *act;    // activation records from launch_gemm32_quant
+    int Tp, T;             // padded token count (32 or 64, Tp - T < 32), tokens
+    int64_t ldy;
+    int32_t *dump_s;       // test hook: [T][nrows][nb] integers, or null
+};
+hipError_t launch_gemm32_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s);
+size_t gemm32_act_bytes(int nb, int Tp);
+hipError_t launch_q80_gemm(const Gemm32Args &a, hipStream_t s);
+
 // quantizes T rows of x (stride ldx) into the GEMM's activation records (gemm_act_bytes(nb, Tp))
 hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s);
 size_t gemm_act_bytes(int nb, int Tp);

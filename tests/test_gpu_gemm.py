@@ -7,9 +7,11 @@ Bar:
     outputs use a different summation order from gemmk_kern, so they are compared with the
     reference's own tolerance: max|y - y_ref| / max|y_ref| <= 1e-5 per token (fastgguf.c:5723-5733),
     against the oracle's restatement of gemm_kquant and against the reference's golden outputs.
-  - Q6_K, Q8_0 and Q5_0 run the per-token decode kernels (dot_q6_K_q8k / dot_q8_0_q8 /
-    dot_q5_0_q8 orders): compared with the same tolerance against the GEMM orders (gemm_kquant,
-    gemm_q32).
+  - Q8_0 runs its int8 MFMA GEMM (one 32-value block per v_mfma_i32_32x32x32_i8): its per-block
+    integers (dot_q8_0_q8's sum of q * xq) bit for bit against the oracle's, its fp32 outputs within
+    the same tolerance of the oracle's GEMM order (gemm_q32).
+  - Q6_K and Q5_0 run the per-token decode kernels (dot_q6_K_q8k / dot_q5_0_q8 orders): compared
+    with the same tolerance against the GEMM orders (gemm_kquant, gemm_q32).
   - Q4_0, Q4_1 and Q5_1 run the decode kernels per token too, against gemm_q32 with the same tolerance.
   - Q5_K and IQ4_NL have no prompt GEMM in the reference: their matmul is the row kernel per token
     there and here, so they are compared bit for bit.
@@ -80,6 +82,47 @@ def test_gemm_block_ints_exact(backend, oracle, case):
     Y = backend.matmul(tt, X)
     order = O_RP if (n_mats == 1 and rows % 8 == 0) else O_ROW
     check_tokens(Y, oracle.matmul(S.T_Q4_K, w, cols, X, order))
+    tt.free()
+
+
+Q80_CASES = [  # (rows, cols, n_mats, tokens): K-parts 1 (1 tile step), 2 (2-3 steps, one with an
+    # Edge step), 4; partial last steps (blocks % 4 != 0); ragged rows; 3-D; both token tiles
+    (64, 128, 1, 8),
+    (40, 256, 1, 32),
+    (100, 416, 1, 31),      # 13 blocks: 4 tile steps, the last with one block
+    (72, 384, 3, 45),       # 3 steps (K-parts 2, one idle in the last step), 9 tiles per matrix
+    (256, 4096, 1, 64),
+    (24, 14336, 1, 33),     # 448 blocks
+    (8, 2080, 2, 9),        # 65 blocks, one 8-row tile per matrix
+]
+
+
+@pytest.mark.parametrize("case", Q80_CASES, ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}_T{c[3]}")
+def test_q80_gemm_block_ints_exact(backend, oracle, case):
+    rows, cols, n_mats, T = case
+    w = S.random_bytes_weights(S.T_Q8_0, rows * n_mats, cols, 170 + rows)
+    X = S.activations(cols, 171 + T, rows=T) * np.float32(2.0)
+    tt = backend.upload(S.T_Q8_0, cols, w, rows=rows, n_mats=n_mats)
+    s, m = backend.gemm_block_ints(tt, X)
+    assert not m.any()  # no min term
+    for tok in (0, T // 2, T - 1):
+        act = oracle.quantize_for(S.T_Q8_0, X[tok])
+        for r in range(rows * n_mats):
+            os_, _ = oracle.block_ints(S.T_Q8_0, w[r], act)
+            assert np.array_equal(s[tok, r], os_), f"sumi token {tok} row {r}"
+    check_tokens(backend.matmul(tt, X), oracle.matmul(S.T_Q8_0, w, cols, X, O_ROW))
+    tt.free()
+
+
+def test_q80_prefill_config_shape(backend, oracle):
+    """64 tokens x K=4096 -> N=14336, Q8_0 (benchmark distributions), then 9 tokens (one token
+    tile) reusing the buffers"""
+    rows, cols = 14336, 4096
+    w = S.weights(S.T_Q8_0, rows, cols, 190)
+    X = S.activations(cols, 191, rows=64)
+    tt = backend.upload(S.T_Q8_0, cols, w)
+    check_tokens(backend.matmul(tt, X), oracle.matmul(S.T_Q8_0, w, cols, X, O_ROW))
+    check_tokens(backend.matmul(tt, X[:9]), oracle.matmul(S.T_Q8_0, w, cols, X[:9], O_ROW))
     tt.free()
 
 
