@@ -321,7 +321,7 @@ class Backend:
         return s, m
 
     def gemm_block_ints(self, t: Tensor, X: np.ndarray):
-        """Per (token, row, block) integers of the prompt GEMM (Q4_K or Q8_0, 8..64 tokens): sumi, msum
+        """Per (token, row, block) integers of the prompt GEMM (Q4_K, Q6_K or Q8_0, 8..64 tokens): sumi, msum
         [nb][nout][blocks] (msum zeros for Q8_0)."""
         X = np.ascontiguousarray(X, np.float32)
         nb = X.shape[0]

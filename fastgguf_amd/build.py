@@ -28,7 +28,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libfastgguf_hip.so")
-SOURCES = ["fgh_api.hip", "fgh_kernels.hip", "fgh_matvec.hip", "fgh_q4k.hip", "fgh_gemm.hip", "fgh_gemm32.hip", "fgh_moe.hip",
+SOURCES = ["fgh_api.hip", "fgh_kernels.hip", "fgh_matvec.hip", "fgh_q4k.hip", "fgh_gemm.hip", "fgh_gemm32.hip", "fgh_gemm6.hip", "fgh_moe.hip",
            "fgh_gguf.hip", "fgh_attn.hip", "fgh_kvq.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

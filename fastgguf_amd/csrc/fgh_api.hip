@@ -270,18 +270,47 @@ static int gemm_q80_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_
     return FGH_OK;
 }
 
+// the prompt GEMM for a Q6_K tensor (gemm_kquant's Q6_K branch, fastgguf.c:2704-2725, 2818-2854):
+// Q8_K records of T tokens, then one MFMA launch on the decode tiles; ds / dm: optional
+// [T][rows * n_mats][nb] integer dump
+static int gemm_q6k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
+                         uint8_t *act, int32_t *ds, int32_t *dm) {
+    const int Tp = (T + 15) / 16 * 16;
+    HIP_TRY(c, fgh::launch_gemm6_quant(X, ldx, t->nb, T, Tp, act, c->stream));
+    fgh::Gemm6Args a;
+    memset(&a, 0, sizeof(a));
+    a.W = t->dev;
+    a.Y = Y;
+    a.rows = t->rows;
+    a.tpm = t->gpm;
+    a.gpm16 = (t->gpm + 1) / 2;
+    a.groups = a.gpm16 * t->n_mats;
+    a.nrows = t->rows * t->n_mats;
+    a.nb = t->nb;
+    a.act = act;
+    a.Tp = Tp;
+    a.T = T;
+    a.ldy = ldy;
+    a.dump_s = ds;
+    a.dump_m = dm;
+    HIP_TRY(c, fgh::launch_q6k_gemm(a, c->stream));
+    return FGH_OK;
+}
+
 // the types and token counts that take a prompt GEMM (matmul, fastgguf.c:3018-3031), and the
 // activation-record bytes it needs (0: the per-token decode kernels, which need no scratch)
 static size_t prompt_gemm_bytes(const fgh_tensor *t, int T) {
     if (T < 8) return 0;
     if (t->type == FGH_T_Q4_K) return fgh::gemm_act_bytes(t->nb, (T + 15) / 16 * 16);
     if (t->type == FGH_T_Q8_0) return fgh::gemm32_act_bytes(t->nb, T <= 32 ? 32 : 64);
+    if (t->type == FGH_T_Q6_K) return fgh::gemm6_act_bytes(t->nb, (T + 15) / 16 * 16);
     return 0;
 }
 // the prompt GEMM with its records in act (at least prompt_gemm_bytes)
 static int prompt_gemm_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy,
                             int T, uint8_t *act, int32_t *ds, int32_t *dm) {
     if (t->type == FGH_T_Q8_0) return gemm_q80_into(c, t, X, ldx, Y, ldy, T, act, ds);
+    if (t->type == FGH_T_Q6_K) return gemm_q6k_into(c, t, X, ldx, Y, ldy, T, act, ds, dm);
     return gemm_q4k_into(c, t, X, ldx, Y, ldy, T, act, ds, dm);
 }
 static int prompt_gemm(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
@@ -526,7 +555,7 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
         return fail(c, FGH_ERR_ARG, "matmul: bad arguments");
     INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
-    // nb >= 8: the prompt GEMM (matmul 3018-3031) on int8 MFMA for Q4_K and Q8_0; the other types
+    // nb >= 8: the prompt GEMM (matmul 3018-3031) on int8 MFMA for Q4_K, Q6_K and Q8_0; the other types
     // run the per-token decode kernels (their fp32 orders differ from the reference's GEMM orders
     // only by rounding)
     if (prompt_gemm_bytes(t, nb)) return prompt_gemm(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
@@ -1013,8 +1042,8 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     NO_CAPTURE(c);
     if (!X || !sumi || !msum || nb < 1 || nb > FG_BATCH || ldx < t->cols)
         return fail(c, FGH_ERR_ARG, "gemm_block_ints: bad arguments");
-    if (t->type != FGH_T_Q4_K && t->type != FGH_T_Q8_0)
-        return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMMs take Q4_K and Q8_0 tensors");
+    if (t->type != FGH_T_Q4_K && t->type != FGH_T_Q6_K && t->type != FGH_T_Q8_0)
+        return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMMs take Q4_K, Q6_K and Q8_0 tensors");
     if (nb < 8) return fail(c, FGH_ERR_ARG, "gemm_block_ints: the prompt GEMM runs 8..64 tokens");
     const int64_t nout = t->rows * t->n_mats;
     const size_t nint = (size_t)nb * nout * t->nb;

@@ -369,6 +369,25 @@ hipError_t launch_gemm32_quant(const float *x, int64_t ldx, int nb, int T, int T
 size_t gemm32_act_bytes(int nb, int Tp);
 hipError_t launch_q80_gemm(const Gemm32Args &a, hipStream_t s);
 
+// the Q6_K prompt GEMM (fgh_gemm6.hip) on the decode tiles (8-row tiles, one block per tile step)
+struct Gemm6Args {
+    const uint8_t *W;      // Q6_K tensor (tile layout)
+    float *Y;              // Y[tok * ldy + row]
+    int64_t rows;          // rows per matrix
+    int64_t tpm;           // 8-row tiles per matrix
+    int64_t gpm16;         // 16-row tiles (pairs of decode tiles) per matrix, (tpm + 1) / 2
+    int64_t groups;        // 16-row tiles over all matrices
+    int64_t nrows;         // rows over all matrices (outputs per token)
+    int nb;                // 256-blocks per row
+    const uint8_t *act;    // activation records from launch_gemm6_quant
+    int Tp, T;             // padded token count (a multiple of 16, Tp - T < 16), tokens
+    int64_t ldy;
+    int32_t *dump_s, *dump_m;  // test hook: [T][nrows][nb] sumi / msum, or null
+};
+hipError_t launch_gemm6_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s);
+size_t gemm6_act_bytes(int nb, int Tp);
+hipError_t launch_q6k_gemm(const Gemm6Args &a, hipStream_t s);
+
 // quantizes T rows of x (stride ldx) into the GEMM's activation records (gemm_act_bytes(nb, Tp))
 hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s);
 size_t gemm_act_bytes(int nb, int Tp);

@@ -271,8 +271,8 @@ FGH_API int fgh_event_destroy(fgh_ctx *ctx, void *ev);
  * n/32 blocks of 40 bytes; FGH_ACT_Q8K: n/256 blocks of 292 bytes), from host x.
  * fgh_block_ints: per (row, block) integer parts of dot(W[r], Q8(x)) as the device kernels
  * compute them: sumi / msum [rows * n_mats][blocks per row] (see the oracle's fgo_block_ints).
- * fgh_gemm_block_ints: the same integers as the prompt GEMMs (Q4_K or Q8_0, nb tokens, 8..64)
- * compute them: sumi / msum [nb][rows * n_mats][blocks per row] (msum zeros for Q8_0), token t
+ * fgh_gemm_block_ints: the same integers as the prompt GEMMs (Q4_K, Q6_K or Q8_0, nb tokens,
+ * 8..64) compute them: sumi / msum [nb][rows * n_mats][blocks per row] (msum zeros for Q8_0), token t
  * from row t of X (stride ldx).
  * fgh_fp16_to_f32: the device's fp16 -> fp32 decode of n codes.
  * fgh_expf: the device's expf (the MoE softmax and silu) of n values.

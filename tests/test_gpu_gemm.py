@@ -10,8 +10,11 @@ Bar:
   - Q8_0 runs its int8 MFMA GEMM (one 32-value block per v_mfma_i32_32x32x32_i8): its per-block
     integers (dot_q8_0_q8's sum of q * xq) bit for bit against the oracle's, its fp32 outputs within
     the same tolerance of the oracle's GEMM order (gemm_q32).
-  - Q6_K and Q5_0 run the per-token decode kernels (dot_q6_K_q8k / dot_q5_0_q8 orders): compared
-    with the same tolerance against the GEMM orders (gemm_kquant, gemm_q32).
+  - Q6_K runs its int8 MFMA GEMM (three chains over balanced base-8 digits of the scales): its
+    per-block integers (dot_q6_K_q8k's sumi over the unsigned quants, and msum) bit for bit
+    against the oracle's, its fp32 outputs within the same tolerance of gemm_kquant's order.
+  - Q5_0 runs the per-token decode kernels (dot_q5_0_q8 order): compared with the same tolerance
+    against the GEMM order (gemm_q32).
   - Q4_0, Q4_1 and Q5_1 run the decode kernels per token too, against gemm_q32 with the same tolerance.
   - Q5_K and IQ4_NL have no prompt GEMM in the reference: their matmul is the row kernel per token
     there and here, so they are compared bit for bit.
@@ -123,6 +126,45 @@ def test_q80_prefill_config_shape(backend, oracle):
     tt = backend.upload(S.T_Q8_0, cols, w)
     check_tokens(backend.matmul(tt, X), oracle.matmul(S.T_Q8_0, w, cols, X, O_ROW))
     check_tokens(backend.matmul(tt, X[:9]), oracle.matmul(S.T_Q8_0, w, cols, X[:9], O_ROW))
+    tt.free()
+
+
+Q6K_CASES = [  # (rows, cols, n_mats, tokens): K-halves 1 (one block) and 2 (odd and even block
+    # counts); an odd number of 8-row tiles (a half-empty last pair); ragged rows; 3-D; 1..4 token tiles
+    (16, 256, 1, 8),
+    (40, 512, 1, 16),
+    (100, 768, 1, 31),      # 13 tiles: the last pair has one tile
+    (24, 2048, 3, 45),      # 3 tiles per matrix
+    (64, 4096, 1, 64),
+    (8, 14336, 1, 33),      # 56 blocks, one tile
+]
+
+
+@pytest.mark.parametrize("case", Q6K_CASES, ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}_T{c[3]}")
+def test_q6k_gemm_block_ints_exact(backend, oracle, case):
+    rows, cols, n_mats, T = case
+    w = S.random_bytes_weights(S.T_Q6_K, rows * n_mats, cols, 270 + rows)
+    X = S.activations(cols, 271 + T, rows=T) * np.float32(2.0)
+    tt = backend.upload(S.T_Q6_K, cols, w, rows=rows, n_mats=n_mats)
+    s, m = backend.gemm_block_ints(tt, X)
+    for tok in (0, T // 2, T - 1):
+        act = oracle.quantize_for(S.T_Q6_K, X[tok])
+        for r in range(rows * n_mats):
+            os_, om = oracle.block_ints(S.T_Q6_K, w[r], act)
+            assert np.array_equal(s[tok, r], os_), f"sumi token {tok} row {r}"
+            assert np.array_equal(m[tok, r], om), f"msum token {tok} row {r}"
+    check_tokens(backend.matmul(tt, X), oracle.matmul(S.T_Q6_K, w, cols, X, O_ROW))
+    tt.free()
+
+
+def test_q6k_prefill_config_shape(backend, oracle):
+    """64 tokens x K=4096 -> N=14336, Q6_K (benchmark distributions), then 9 tokens"""
+    rows, cols = 14336, 4096
+    w = S.weights(S.T_Q6_K, rows, cols, 290)
+    X = S.activations(cols, 291, rows=64)
+    tt = backend.upload(S.T_Q6_K, cols, w)
+    check_tokens(backend.matmul(tt, X), oracle.matmul(S.T_Q6_K, w, cols, X, O_ROW))
+    check_tokens(backend.matmul(tt, X[:9]), oracle.matmul(S.T_Q6_K, w, cols, X[:9], O_ROW))
     tt.free()
 
 
