@@ -669,11 +669,13 @@ int fgh_attention_dev(fgh_ctx *c, int n_tok, int n_head, int n_head_kv, int hd, 
                       const int32_t *en, int max_len, float scale) {
     if (!c) return FGH_ERR_ARG;
     if (!q || !o || !k_cache || !v_cache || !st || !en || n_tok < 1 || n_head < 1 || n_head_kv < 1 ||
-        n_head % n_head_kv != 0 || hd < 32 || hd > 256 || hd % 32 != 0 || (int64_t)n_head_kv * hd > kv_dim ||
-        kv_dim % 4 != 0 || cap < 1 || max_len < 1)
+        n_head % n_head_kv != 0 || hd < 1 || hd > 256 || (int64_t)n_head_kv * hd > kv_dim || cap < 1 || max_len < 1)
         return fail(c, FGH_ERR_ARG, "attention: bad arguments");
-    if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 != 0)
-        return fail(c, FGH_ERR_ARG, "attention: q and the caches must be 16-byte aligned");
+    // the vector path (hd % 32 == 0) reads q and the caches 16 bytes at a time
+    if (hd % 32 == 0 && (kv_dim % 4 != 0 || ((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 != 0))
+        return fail(c, FGH_ERR_ARG, "attention: for hd %% 32 == 0, kv_dim %% 4 == 0 and 16-byte aligned q and caches");
+    if (((uintptr_t)q | (uintptr_t)o | (uintptr_t)k_cache | (uintptr_t)v_cache) % 4 != 0)
+        return fail(c, FGH_ERR_ARG, "attention: q, o and the caches must be 4-byte aligned");
     if ((n_tok * (n_head / n_head_kv) + 3) / 4 > 65535 || n_head_kv > 65535 || (int64_t)n_tok * n_head > INT32_MAX / 2)
         return fail(c, FGH_ERR_ARG, "attention: too many rows");
     INJECT(c);

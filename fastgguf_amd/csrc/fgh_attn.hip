@@ -1,12 +1,15 @@
-// fgh_attn.hip - attention over an fp32 KV ring cache on gfx950, bit-exact with the vector path of
-// the reference's attn_rows (fastgguf.c:3273-3326; hd % 32 == 0).
+// fgh_attn.hip - attention over an fp32 KV ring cache on gfx950, bit-exact with the reference's
+// attn_rows (fastgguf.c:3273-3326): its vector path (hd % 32 == 0) and its per-row path (any
+// other head size up to 256).
 //
 // Rows are (token, head) pairs: row i = t * n_head + h reads q / writes o at i * hd and the K / V
 // head (h / G) * hd of each cache row (G = n_head / n_head_kv, the GQA grouping of the reference's
 // forward, 4770-4790), over the positions st[t]..en[t] (slot p % cap). Three launches:
 //   scores   8 chains per key: chain l runs fma over q[8m + l] k[8m + l] (att_qk_kern,
 //            3227-3246), then hsum4_ps's tree ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)) (3187-3190),
-//            times scale
+//            times scale; other head sizes dot_f32v's order (1618-1632): 8-lane chains s0 over
+//            values 16 i + l and s1 over 16 i + 8 + l, one more group of 8 into s0, hsum_ps of
+//            s0 + s1, then the last hd % 8 values one fma each, times scale (3313-3315)
 //   softmax  one workgroup per row (softmax_vec, 3194-3219): the maximum, exp_neg_ps (3168-3184)
 //            over whole groups of 8 and libm's expf over the tail, the sum as 8 ordered lane sums
 //            (lane l over e[8g + l]) added in hsum_ps's tree then the tail in order, and every
@@ -16,7 +19,8 @@
 // The value sums are one dependent chain per (row, element) over every position: the
 // reference's order, which no split over positions keeps. What bounds them is the latency of
 // their operands, so the kernel keeps many tiles of V in flight per workgroup and runs the
-// chains out of LDS. Head sizes up to 256; kv_dim and the cache pointers 16-byte aligned.
+// chains out of LDS. Head sizes up to 256; for hd % 32 == 0, kv_dim % 4 == 0 and 16-byte aligned
+// pointers; other head sizes read K and (when a 16-byte read would not be aligned) V value by value.
 #include <hip/hip_runtime.h>
 
 #include "fgh_internal.h"
@@ -141,6 +145,69 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a, int n_tok)
     }
 }
 
+// scores of the per-row path (hd % 32 != 0): as attn_scores_kernel, thread = one key of the group's
+// union, the q rows from LDS, K read value by value (any head size and offset), dot_f32v's order
+template <int R>
+__global__ __launch_bounds__(256) void attn_scores_row_kernel(AttnArgs a, int n_tok) {
+    __shared__ float qs[R][256];
+    const int grp = blockIdx.y, kh = blockIdx.z, tid = threadIdx.x;
+    int lo, hi;
+    if (!group_span(a, n_tok, R, grp, kh, lo, hi)) return;
+    const int hd = a.hd;
+    for (int i = tid; i < R * hd; i += 256) {
+        const int r = i / hd, x = i - r * hd;
+        const GroupRow g = group_row(a, n_tok, R, grp, kh, r);
+        qs[r][x] = g.en >= g.st ? a.q[(size_t)g.row * hd + x] : 0.0f;
+    }
+    __syncthreads();
+    const int64_t kvo = (int64_t)kh * hd;
+    for (int p = lo + (int)blockIdx.x * 256 + tid; p <= hi; p += (int)gridDim.x * 256) {
+        const float *kp = a.k + kv_slot(p, a.cap) * a.kv_dim + kvo;
+        float s0[R][8], s1[R][8];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int l = 0; l < 8; ++l) s0[r][l] = s1[r][l] = 0.0f;
+        int i = 0;
+        for (; i + 16 <= hd; i += 16) {
+            float k0[8], k1[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                k0[l] = kp[i + l];
+                k1[l] = kp[i + 8 + l];
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    s0[r][l] = __builtin_fmaf(qs[r][i + l], k0[l], s0[r][l]);
+                    s1[r][l] = __builtin_fmaf(qs[r][i + 8 + l], k1[l], s1[r][l]);
+                }
+        }
+        if (i + 8 <= hd) {
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                const float k0 = kp[i + l];
+#pragma unroll
+                for (int r = 0; r < R; ++r) s0[r][l] = __builtin_fmaf(qs[r][i + l], k0, s0[r][l]);
+            }
+            i += 8;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const GroupRow g = group_row(a, n_tok, R, grp, kh, r);
+            if (p >= g.st && p <= g.en) {
+                float v[8];
+#pragma unroll
+                for (int l = 0; l < 8; ++l) v[l] = s0[r][l] + s1[r][l];
+                float t = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));  // hsum_ps
+                for (int j = i; j < hd; ++j) t = __builtin_fmaf(qs[r][j], kp[j], t);
+                a.s[(size_t)g.row * a.max_len + (p - g.st)] = t * a.scale;
+            }
+        }
+    }
+}
+
 // softmax: one workgroup per row, in place over the row's scores. A row of up to SM_RES positions
 // stays in LDS (sized min(max_len, SM_RES) at launch, so short rows leave room for more
 // workgroups per CU) from its one load to its one store: maximum, exponentials, lanes 0..7 of
@@ -254,7 +321,9 @@ struct AvStage {
 };
 // VB = 0: V in fp32 (a.v); VB = 2, 4, 8: V as TurboQuant records (a.vq), decoded to centroids
 // (int8 codes for VB = 8) through an LDS table when a tile is stored
-template <int CH, int AV_S, int VB>  // AV_S: tiles in flight, 4 or 8 (the named stages below)
+// SC: V read value by value (hd or kv_dim not a multiple of 4: a 16-byte read would not be aligned),
+// columns past hd reading column 0
+template <int CH, int AV_S, int VB, bool SC = false>  // AV_S: tiles in flight, 4 or 8 (the named stages below)
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_values_kernel(AttnArgs a,
                                                                                                      int n_tok) {
     constexpr int GR = 4 * CH;  // rows per group
@@ -283,6 +352,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int wr = CH == 4 ? tid >> 4 : tid >> 6, wp = CH == 4 ? (tid & 15) * 4 : tid & 63;
     const int lcol = cc + lc < a.hd ? cc + lc : 0;
     const float *vb = VB ? nullptr : a.v + (int64_t)kh * a.hd + lcol;
+    // SC: the offsets of columns lcol + 1 .. + 3 from lcol (0 where a column is past hd: column lcol)
+    const int sc1 = cc + lc + 1 < a.hd ? 1 : 0, sc2 = cc + lc + 2 < a.hd ? 2 : 0, sc3 = cc + lc + 3 < a.hd ? 3 : 0;
     const int vrec = 4 + a.hd * VB / 8;  // TurboQuant: record bytes, the slot's records back to back
     const uint8_t *qb = VB ? a.vq + (int64_t)kh * vrec + 4 + (int64_t)lcol * VB / 8 : nullptr;
     const int64_t qstride = (int64_t)a.n_head_kv * vrec;
@@ -308,7 +379,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int sl = vpos[m] <= hi ? vslot[m] : slot_hi;
-            if constexpr (VB == 0)
+            if constexpr (VB == 0 && SC) {
+                const float *vp = vb + (int64_t)sl * a.kv_dim;
+                *dst[m] = (av4){vp[0], vp[sc1], vp[sc2], vp[sc3]};
+            } else if constexpr (VB == 0)
                 *dst[m] = *(const av4 *)(vb + (int64_t)sl * a.kv_dim);
             else if constexpr (VB == 8)
                 *kdst[m] = *(const uint32_t *)(qb + sl * qstride);
@@ -458,16 +532,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 }
 
 hipError_t launch_attention_values(const AttnArgs &a, int n_tok, hipStream_t s) {
-    if (n_tok < 1 || a.hd < 32 || a.hd > 256 || a.hd % 32 != 0 || a.n_head_kv < 1 || a.n_head % a.n_head_kv != 0 ||
-        a.max_len < 1 || a.kv_dim % 4 != 0)
+    if (n_tok < 1 || a.hd < 1 || a.hd > 256 || a.n_head_kv < 1 || a.n_head % a.n_head_kv != 0 || a.max_len < 1)
         return hipErrorInvalidValue;
+    // 16-byte V reads need 4-value columns and rows; TurboQuant records need a multiple of 32
+    const bool sc = a.hd % 4 != 0 || a.kv_dim % 4 != 0 || (uintptr_t)a.v % 16 != 0;
+    if (a.vq && (a.hd % 32 != 0 || sc)) return hipErrorInvalidValue;
     const int rows_kv = n_tok * (a.n_head / a.n_head_kv);
     if ((rows_kv + 3) / 4 > 65535 || a.n_head_kv > 65535) return hipErrorInvalidValue;
     if (a.vq ? (a.vbits != 2 && a.vbits != 4 && a.vbits != 8) : !a.v) return hipErrorInvalidValue;
     const unsigned cch = (unsigned)((a.hd + 63) / 64), kvh = (unsigned)a.n_head_kv;
     const dim3 g16(cch, (unsigned)((rows_kv + 15) / 16), kvh), g4(cch, (unsigned)((rows_kv + 3) / 4), kvh);
     const int vb = a.vq ? a.vbits : 0;
-    if (rows_kv >= 64) {
+    if (sc) {
+        if (rows_kv >= 64) attn_values_kernel<4, 4, 0, true><<<g16, 256, 0, s>>>(a, n_tok);
+        else attn_values_kernel<1, 8, 0, true><<<g4, 256, 0, s>>>(a, n_tok);
+    } else if (rows_kv >= 64) {
         if (vb == 0) attn_values_kernel<4, 4, 0><<<g16, 256, 0, s>>>(a, n_tok);
         else if (vb == 8) attn_values_kernel<4, 4, 8><<<g16, 256, 0, s>>>(a, n_tok);
         else if (vb == 4) attn_values_kernel<4, 4, 4><<<g16, 256, 0, s>>>(a, n_tok);
@@ -482,14 +561,17 @@ hipError_t launch_attention_values(const AttnArgs &a, int n_tok, hipStream_t s) 
 }
 
 hipError_t launch_attention(const AttnArgs &a, int n_tok, hipStream_t s) {
-    if (n_tok < 1 || a.hd < 32 || a.hd > 256 || a.hd % 32 != 0 || a.n_head_kv < 1 || a.n_head % a.n_head_kv != 0 ||
-        a.max_len < 1 || a.kv_dim % 4 != 0)
+    if (n_tok < 1 || a.hd < 1 || a.hd > 256 || a.n_head_kv < 1 || a.n_head % a.n_head_kv != 0 || a.max_len < 1)
         return hipErrorInvalidValue;
+    const bool vec = a.hd % 32 == 0;  // the reference's vector path: 16-byte reads of q and K
+    if (vec && (a.kv_dim % 4 != 0 || ((uintptr_t)a.q | (uintptr_t)a.k) % 16 != 0)) return hipErrorInvalidValue;
     const int rows_kv = n_tok * (a.n_head / a.n_head_kv);  // rows per K / V head
     if ((rows_kv + 3) / 4 > 65535 || a.n_head_kv > 65535) return hipErrorInvalidValue;
     const unsigned kb = (unsigned)std::min((a.max_len + 255) / 256, 1024);
     const dim3 kvh(1, 1, (unsigned)a.n_head_kv);
-    if (rows_kv >= 16)
+    if (!vec)
+        attn_scores_row_kernel<4><<<dim3(kb, (unsigned)((rows_kv + 3) / 4), kvh.z), 256, 0, s>>>(a, n_tok);
+    else if (rows_kv >= 16)
         attn_scores_kernel<16><<<dim3(kb, (unsigned)((rows_kv + 15) / 16), kvh.z), 256, 0, s>>>(a, n_tok);
     else
         attn_scores_kernel<4><<<dim3(kb, (unsigned)((rows_kv + 3) / 4), kvh.z), 256, 0, s>>>(a, n_tok);

@@ -166,16 +166,18 @@ FGH_API int fgh_moe_ffn(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tensor *
                 int k, const float *logits, const float *X, float *Y, int n_tok,
                 int32_t *sel_out, float *w_out);
 
-/* ---- attention: replaces attn_rows (fastgguf.c:3273-3326), its vector path (hd % 32 == 0) ----
+/* ---- attention: replaces attn_rows (fastgguf.c:3273-3326), both of its paths ----
  * Rows are (token, head) pairs, row t * n_head + h: q and o are [n_tok][n_head][hd]; the K and V
  * caches are rings of cap rows of kv_dim floats (position p in row p % cap), head h reading the
  * cache columns (h / (n_head / n_head_kv)) * hd .. + hd (the GQA grouping of forward, 4770-4790).
  * Token t attends to positions st[t]..en[t] (1 <= en - st + 1 <= cap). Every output equals the
  * reference's bit for bit: scores as att_qk_kern's lane chains and hsum4_ps (3227-3246), softmax
  * as softmax_vec (3194-3219, exp_neg_ps 3168-3184 on whole groups of 8, libm expf on the tail),
- * value sums as att_v_kern's chain over the positions in order (3249-3270). scale is the
- * reference's 1/sqrt(hd). Requires hd % 32 == 0 and hd <= 256, n_head % n_head_kv == 0,
- * n_head_kv * hd <= kv_dim, kv_dim % 4 == 0 (device pointers 16-byte aligned). */
+ * value sums as att_v_kern's chain over the positions in order (3249-3270). Head sizes that are
+ * not a multiple of 32 take the reference's per-row path (3313-3325): scores as dot_f32v
+ * (1618-1632), then the same softmax and value sums. scale is the reference's 1/sqrt(hd).
+ * Requires 1 <= hd <= 256, n_head % n_head_kv == 0, n_head_kv * hd <= kv_dim; for hd % 32 == 0
+ * also kv_dim % 4 == 0 and 16-byte aligned device pointers (4-byte aligned otherwise). */
 FGH_API int fgh_attention(fgh_ctx *ctx, int n_tok, int n_head, int n_head_kv, int hd, const float *q, float *o,
                   const float *k_cache, const float *v_cache, int kv_dim, int cap, const int32_t *st,
                   const int32_t *en, float scale);

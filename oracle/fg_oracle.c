@@ -926,10 +926,15 @@ int fgo_moe_ffn(uint32_t type_gate, uint32_t type_up, uint32_t type_down,
     return rc;
 }
 
-/* ---- B-10: attention, attn_rows (fastgguf.c:3273-3326), its vector path (hd % 32 == 0) ----
+/* ---- B-10: attention, attn_rows (fastgguf.c:3273-3326): its vector path (hd % 32 == 0) and
+ * its per-row path (any other hd, 3313-3325) ----
  * Per query row, over positions st..en of the ring cache (slot p % cap, head offset kvo):
  *   score_p = scale * (((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7))), a_l = fma chain over
- *            m of q[8m + l] * k_p[8m + l]   (att_qk_kern 3227-3246 with hsum4_ps 3187-3190)
+ *            m of q[8m + l] * k_p[8m + l]   (att_qk_kern 3227-3246 with hsum4_ps 3187-3190);
+ *            other hd: score_p = dot_f32v(q, k_p, hd) * scale (1618-1632 in its AVX2 + FMA form:
+ *            8-lane fma chains s0 over values 16 i + l and s1 over 16 i + 8 + l, one more 8-value
+ *            group into s0 when 8 remain, hsum_ps(s0 + s1), then the last hd % 8 values one fma
+ *            each, as gcc contracts `s += a[i] * b[i]` when FMA is available)
  *   softmax_vec (3194-3219): max; e = exp_neg_ps(s - max) over whole groups of 8 (lane l of the
  *            8-wide sum takes e[8g + l] in order), hsum8 of the lanes, then the tail with libm
  *            expf added in order; every value times 1 / sum
@@ -981,9 +986,33 @@ static void softmax_vec_row(float *s, int n) {
     }
 }
 
+/* dot_f32v (fastgguf.c:1618-1632), AVX2 + FMA form */
+static float dot_f32v(const float *a, const float *b, int n) {
+    float s0[8] = {0}, s1[8] = {0};
+    int i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 8; l++) {
+            s0[l] = fmaf(a[i + l], b[i + l], s0[l]);
+            s1[l] = fmaf(a[i + 8 + l], b[i + 8 + l], s1[l]);
+        }
+    if (i + 8 <= n) {
+        for (int l = 0; l < 8; l++) s0[l] = fmaf(a[i + l], b[i + l], s0[l]);
+        i += 8;
+    }
+    float v[8];
+    for (int l = 0; l < 8; l++) v[l] = s0[l] + s1[l];
+    float s = hsum8(v);
+#if FGO_MUTATE == 14 /* the tail multiplied and added in two roundings instead of one fma */
+    for (; i < n; i++) s += a[i] * b[i];
+#else
+    for (; i < n; i++) s = fmaf(a[i], b[i], s);
+#endif
+    return s;
+}
+
 int fgo_attn_rows(int nr, const float *q, float *o, const int *st, const int *en, const float *ck, const float *cv,
                   int kv_dim, const int *kvo, int cap, int hd, float scale) {
-    if (hd % 32 != 0 || hd <= 0) return -1;
+    if (hd <= 0) return -1;
     for (int r = 0; r < nr; r++) {
         int n = en[r] - st[r] + 1;
         if (n < 1 || n > cap) return -1;
@@ -992,6 +1021,10 @@ int fgo_attn_rows(int nr, const float *q, float *o, const int *st, const int *en
         const float *qr = q + (size_t)r * hd;
         for (int p = st[r]; p <= en[r]; p++) {
             const float *k = ck + (size_t)(p % cap) * kv_dim + kvo[r];
+            if (hd % 32 != 0) { /* the per-row path */
+                s[p - st[r]] = dot_f32v(qr, k, hd) * scale;
+                continue;
+            }
             float a[8] = {0};
             for (int m = 0; m < hd / 8; m++)
                 for (int l = 0; l < 8; l++) a[l] = fmaf(qr[8 * m + l], k[8 * m + l], a[l]);

@@ -52,7 +52,9 @@ def quant_inputs() -> np.ndarray:
 
 #: (hd, kv_dim, kvo, cap, st, en, q magnitude): one position, a tail of 7, whole groups of 8 plus
 #: tails, causal prefill rows over a wrapped ring, a full cache, hd 32 .. 256, and scores spread
-#: past exp_neg_ps's -87 cut-off
+#: past exp_neg_ps's -87 cut-off; then head sizes that are not multiples of 32, which take the
+#: per-row path and dot_f32v's order: 16-value chunks only (80), one more group of 8 (72, 120),
+#: a scalar tail (100, 36), and an odd size at an odd offset (13)
 ATTN_CASES = [
     (32, 64, 32, 40, [0], [0], 1.0),
     (64, 128, 0, 40, [3], [9], 1.0),
@@ -60,6 +62,12 @@ ATTN_CASES = [
     (128, 128, 0, 64, [50, 52, 10, 37], [100, 101, 73, 100], 1.0),
     (256, 256, 0, 24, [5, 7], [28, 20], 1.0),
     (32, 32, 0, 40, [2], [34], 30.0),
+    (80, 160, 80, 40, [3, 5], [20, 33], 1.0),
+    (72, 144, 0, 30, [0], [25], 1.0),
+    (100, 200, 100, 24, [1, 2, 3], [23, 10, 15], 1.0),
+    (36, 36, 0, 20, [0], [19], 4.0),
+    (13, 26, 13, 16, [2, 4], [9, 15], 1.0),
+    (120, 240, 0, 50, [10, 11, 12, 13], [40, 41, 42, 43], 1.0),
 ]
 
 
@@ -127,6 +135,9 @@ def kvq_cases(ref) -> dict:
 def main() -> None:
     ref = Reference("vnni")
     print("reference build:", ref.build, "threads:", ref.threads())
+    if sys.argv[1:] == ["attn"]:  # only the attention vectors
+        np.savez_compressed(os.path.join(HERE, "attn.npz"), **attn_cases(ref))
+        return
     out = {}
 
     x = quant_inputs()

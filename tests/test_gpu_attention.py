@@ -3,7 +3,9 @@
 Every output is compared bit for bit: against the compiled reference's golden outputs and against
 the oracle's restatement (pinned to those outputs) on decode and prompt-batch ranges, GQA head
 groups, ring wrap, head sizes 32 .. 256, every range length mod 8 (the softmax tail), and scores
-spread past exp_neg_ps's -87 cut-off.
+spread past exp_neg_ps's -87 cut-off. Head sizes that are not multiples of 32 (the reference's
+per-row path, dot_f32v's score order) run with 16-value chunks only, an extra group of 8, a
+scalar tail, and odd sizes whose rows are not 16-byte aligned.
 """
 import numpy as np
 import pytest
@@ -43,6 +45,12 @@ CASES = [  # (n_tok, n_head, n_head_kv, hd, cap, first position, magnitude)
     (5, 6, 3, 96, 40, 33, 1.0),       # hd 96, ring shorter than the range start
     (3, 4, 1, 256, 70, 60, 1.0),      # hd 256, multi-query
     (4, 2, 2, 32, 50, 10, 30.0),      # scores past the -87 cut-off
+    (1, 32, 32, 80, 300, 250, 1.0),   # per-row path: hd 80 decode (five 16-value chunks)
+    (9, 8, 2, 112, 60, 50, 1.0),      # hd 112: chunks and one group of 8, prompt batch, GQA
+    (5, 6, 3, 100, 40, 33, 1.0),      # hd 100: a scalar tail of 4
+    (70, 4, 2, 72, 100, 20, 1.0),     # hd 72, 70 tokens x 2 heads per K head: the 16-row value kernel
+    (3, 5, 5, 13, 30, 25, 2.0),       # odd hd: unaligned rows, values read one by one
+    (66, 2, 1, 6, 80, 0, 1.0),        # tiny hd: the tail only; 66 rows per K head
 ]
 
 
@@ -113,9 +121,9 @@ def test_attention_dev_bad_rows_are_nan(backend, oracle):
 def test_attention_refusals(backend):
     rng = np.random.default_rng(13)
     ck = rng.standard_normal((16, 96)).astype(np.float32)
-    q = rng.standard_normal((1, 2, 48)).astype(np.float32)
-    with pytest.raises(BackendError):  # hd not a multiple of 32
-        backend.attention(q, ck, ck, [0], [3], 2, 0.1)
+    q = rng.standard_normal((1, 1, 288)).astype(np.float32)
+    with pytest.raises(BackendError):  # hd above 256
+        backend.attention(q, np.zeros((16, 288), np.float32), np.zeros((16, 288), np.float32), [0], [3], 1, 0.1)
     q = rng.standard_normal((1, 3, 32)).astype(np.float32)
     with pytest.raises(BackendError):  # 3 heads over 2 KV heads
         backend.attention(q, ck, ck, [0], [3], 2, 0.1)

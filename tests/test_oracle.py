@@ -271,7 +271,8 @@ MUTANTS = {1: "hsum8 order", 2: "MoE accumulate without fma", 3: "reciprocal ins
            7: "Q5_0 fifth bit from the wrong half of qh", 8: "Q5_K qh bit pairing",
            9: "Q4_1 / Q5_1 min term without the fused multiply-add",
            10: "attention score lanes added in sequence", 11: "softmax tail through exp_neg_ps",
-           12: "TurboQuant key dot without the contraction", 13: "TurboQuant scale from an fma chain"}
+           12: "TurboQuant key dot without the contraction", 13: "TurboQuant scale from an fma chain",
+           14: "per-row attention score tail without the contraction"}
 
 
 @pytest.fixture(scope="module")
