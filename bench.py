@@ -6,18 +6,22 @@ fused QKV 4096->6144, O 4096->4096, gate and up 4096->14336 (one shared activati
 14336->4096. A step quantizes each input vector on the device (bit-exact Q8_K) and runs the five
 matvecs. Weights are seeded synthetic Q4_K blocks with the benchmark's distributions; inputs are
 fp32 N(0,1) vectors already resident in HBM. To measure HBM and not the 256 MB Infinity Cache,
-steps rotate over COPIES distinct device copies of the layer (>= 512 MB in total).
+steps rotate over COPIES distinct device copies of the layer (>= 512 MB in total). Steps are
+recorded as a real decode replays them: one HIP graph holds GRAPH_LAYERS consecutive layers
+(32, Llama-3-8B's depth), so the per-graph launch cost is spread over the layers it holds.
 
 value  = whole-layer algorithmic bytes (weights + fp32 x in + fp32 y out) / step time, in GB/s.
 roofline: the dominant kernel of the step is the Q4_K decode matvec launch of the FFN gate and up
          projections together (4096->2x14336, one matvec_multi launch as the reference's forward
          issues it); its duration is the mean over back-to-back launches captured in one HIP graph
-         and timed with HIP events on the library's stream. A step replays one HIP graph of the
-         layer's launches (one per weight copy).
+         and timed with HIP events on the library's stream. Every per-kernel timing rotates over
+         at least 512 MB of distinct weight copies.
 prefill: BASELINE config 4 (64 tokens x 4096 -> 14336, Q4_K) on the int8 MFMA GEMM, timed the
-         same way, cold (rotating weights) and Infinity-Cache hot, as TOPS and fraction of 5 POPS.
+         same way, cold (rotating weights) and Infinity-Cache hot, as TOPS and fraction of 5 POPS;
+         the same shape in Q8_0 and Q6_K on their MFMA GEMMs, against their HBM floors.
 cpu_baseline: the reference's own CPU kernels (oracle/_ref, compiled from fastgguf.c) on the same
-         layer with its default repacked Q4_K path, on this host's cores, for a bounded sample.
+         layer with its default repacked Q4_K path, on this host's physical cores, over weight
+         copies beyond the host's L3, for a bounded sample.
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -50,6 +54,46 @@ def algo_bytes(rows: int, cols: int) -> int:
 
 # the gate and up projections in one launch: both matrices, x read once, both outputs
 GATE_UP_BYTES = 2 * algo_bytes(14336, 4096) - 4 * 4096
+
+
+ROT_BYTES = 512e6  # a per-kernel timing rotates over at least this many bytes of weights
+
+
+def copies_for(nbytes: int, least: int = 1) -> int:
+    return max(least, -(-int(ROT_BYTES) // nbytes))
+
+
+def host_cpu() -> dict:
+    """This process's CPUs: model, sockets, physical cores and logical CPUs it may run on, and the
+    total L3 over the sockets (sysfs and /proc/cpuinfo). Taken before the GPU is initialised: the
+    runtime may pin the calling thread afterwards."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores, pkgs, l3 = set(), set(), {}
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}"
+        try:
+            pkg = int(open(f"{base}/topology/physical_package_id").read())
+            core = int(open(f"{base}/topology/core_id").read())
+        except OSError:
+            pkg, core = 0, c
+        pkgs.add(pkg)
+        cores.add((pkg, core))
+        try:
+            shared = open(f"{base}/cache/index3/shared_cpu_list").read().strip()
+            size = open(f"{base}/cache/index3/size").read().strip()
+            l3[shared] = int(size[:-1]) * (1024 if size.endswith("K") else 1024 * 1024 if size.endswith("M") else 1)
+        except (OSError, ValueError):
+            pass
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "sockets": len(pkgs), "physical_cores": len(cores), "logical_cpus": len(cpus),
+            "l3_bytes": sum(l3.values()), "l3_instances": len(l3)}
 
 
 def counted_traffic(kernel: str):
@@ -226,7 +270,7 @@ def cpu_attention(ref, a: dict) -> dict:
     return out
 
 
-def cpu_baseline(layer_w: dict, xs: dict, budget_s: float, attn_in: dict | None = None) -> dict | None:
+def cpu_baseline(layer_w: dict, xs: dict, budget_s: float, cpu: dict, attn_in: dict | None = None) -> dict | None:
     """The reference's CPU path on the same layer (oracle/_ref), median over a bounded sample; and
     on the bench's attention decode cases (attn_in, from attention_config)."""
     try:
@@ -239,7 +283,8 @@ def cpu_baseline(layer_w: dict, xs: dict, budget_s: float, attn_in: dict | None 
     import numpy as np
 
     from fastgguf_amd.synth import T_Q4_K
-    copies = 3  # 370 MB of repacked weights: beyond a host L3
+    per_copy = sum(r * (c // 256) * 144 for _, r, c in LAYER)
+    copies = max(3, -(-int(1.5 * cpu["l3_bytes"]) // per_copy))  # the weights stream past the L3
     hs = [{n: ref.tensor(T_Q4_K, layer_w[n], c, repack=True) for n, r, c in LAYER} for _ in range(copies)]
     ys = {n: np.zeros(r, np.float32) for n, r, c in LAYER}
 
@@ -267,8 +312,12 @@ def cpu_baseline(layer_w: dict, xs: dict, budget_s: float, attn_in: dict | None 
     total = sum(algo_bytes(r, c) for _, r, c in LAYER)
     return {"value": round(total / med / 1e9, 2), "unit": "GB/s", "cores": ref.threads(), "kind": "reference",
             "sample": f"{len(times)} decode layers (median {med * 1e6:.0f} us/layer), fastgguf.c matvec/"
-                      f"matvec_multi on repacked Q4_K, {ref.build} build, {copies} rotating weight copies",
-            "ms_per_step": round(med * 1e3, 3), **cpu_attention(ref, attn_in or {})}
+                      f"matvec_multi on repacked Q4_K, {ref.build} build, {copies} rotating weight copies "
+                      f"({copies * per_copy / 1e6:.0f} MB, 1.5x the L3 or more)",
+            "ms_per_step": round(med * 1e3, 3), "cpu": cpu, "omp_places": os.environ.get("OMP_PLACES"),
+            "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
+            "numa": "one process, no numactl in this image (no --interleave=all run)",
+            **cpu_attention(ref, attn_in or {})}
 
 
 def main() -> int:
@@ -277,6 +326,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--copies", type=int, default=5, help="distinct device copies of the layer")
+    ap.add_argument("--graph-layers", type=int, default=32, help="decode layers per replayed HIP graph")
     ap.add_argument("--kernel-reps", type=int, default=200, help="individually timed gate matvecs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget (0 = skip)")
     ap.add_argument("--configs", type=int, default=1, help="also time BASELINE configs 1, 3 and 5 (0 = skip)")
@@ -288,7 +338,9 @@ def main() -> int:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build has no multi-GPU "
               "path: every GPU box here has one GPU)", file=sys.stderr)
         return 2
-    os.environ.setdefault("OMP_NUM_THREADS", str(min(16, os.cpu_count() or 1)))
+    # the CPU leg: one thread per physical core this process may use, pinned to cores
+    host = host_cpu()
+    os.environ.setdefault("OMP_NUM_THREADS", str(max(1, host["physical_cores"])))
     os.environ.setdefault("OMP_PROC_BIND", "close")
     os.environ.setdefault("OMP_PLACES", "cores")
 
@@ -333,29 +385,45 @@ def main() -> int:
         be.matvec_multi_dev([t["gate"], t["up"]], xd["x2"], [yd["gate"], yd["up"]])  # forward 4870-4872
         be.matvec_dev(t["down"], xd["h"], yd["down"])
 
-    # one HIP graph per weight copy: a step is one graph replay (5 matvecs in 4 launches, each
-    # quantizing its input on the device)
-    graphs = []
-    for t in tensors:
+    # a step is one decode layer (5 matvecs in 4 launches, each quantizing its input on the
+    # device); GRAPH_LAYERS consecutive layers (cycling the weight copies) form one HIP graph, as a
+    # whole decode step of the model is one graph; K steps replay K / L graphs plus one graph of
+    # the remaining K % L layers, so exactly K layers are timed
+    L = max(1, args.graph_layers)
+
+    def layer_graph(first: int, n: int):
         be.graph_begin()
-        record_layer(t)
-        graphs.append(be.graph_end())
+        for j in range(n):
+            record_layer(tensors[(first + j) % args.copies])
+        return be.graph_end()
 
-    def step(k: int):
+    graphs = [layer_graph(i * L, L) for i in range(args.copies)]
+    rest = layer_graph(0, args.steps % L) if args.steps % L else None
+    for k in range(max(1, -(-args.warmup // L))):
         be.graph_launch(graphs[k % args.copies])
-
-    for k in range(args.warmup):
-        step(k)
     be.sync()
     e0, e1 = be.event(), be.event()
     be.sync()
     be.record(e0)
-    for k in range(args.steps):
-        step(k)
+    for k in range(args.steps // L):
+        be.graph_launch(graphs[k % args.copies])
+    if rest is not None:
+        be.graph_launch(rest)
     be.record(e1)
     ms = be.elapsed_ms(e0, e1)
     be.sync()
     ms_step = ms / args.steps
+    # the same layers one graph each (the per-graph launch cost included), for comparison
+    g1 = [layer_graph(i, 1) for i in range(args.copies)]
+    n1 = min(args.steps, 100)
+    be.record(e0)
+    for k in range(n1):
+        be.graph_launch(g1[k % args.copies])
+    be.record(e1)
+    be.sync()
+    ms_step_1 = be.elapsed_ms(e0, e1) / n1
+    for g in graphs + g1 + ([rest] if rest is not None else []):
+        be.graph_destroy(g)
     layer_bytes = sum(algo_bytes(r, c) for _, r, c in LAYER)
     value = layer_bytes / (ms_step * 1e-3) / 1e9
 
@@ -386,30 +454,43 @@ def main() -> int:
         return t * 1e3 / (n * GRAPH_LAUNCHES)  # us
 
     nc = args.copies
+    # per-kernel rotations: the layer copies plus more of each matrix, at least ROT_BYTES each
+    rot = {}
+    for n, r, c in LAYER:
+        rot[n] = [t[n] for t in tensors]
+        while len(rot[n]) < copies_for(r * (c // 256) * 144):
+            rot[n].append(be.upload(S.T_Q4_K, c, layer_w[n]))
+    extra = [t for n in rot for t in rot[n][nc:]]
+    ngu = min(len(rot["gate"]), len(rot["up"]))
     launches = {
-        "qkv": (lambda i: be.matvec_dev(tensors[i % nc]["qkv"], xd["x"], yd["qkv"]), algo_bytes(6144, 4096)),
-        "o": (lambda i: be.matvec_dev(tensors[i % nc]["o"], xd["a"], yd["o"]), algo_bytes(4096, 4096)),
-        "gate": (lambda i: be.matvec_dev(tensors[i % nc]["gate"], xd["x2"], yd["gate"]), algo_bytes(14336, 4096)),
-        "gate+up": (lambda i: be.matvec_multi_dev([tensors[i % nc]["gate"], tensors[i % nc]["up"]], xd["x2"],
+        "qkv": (lambda i: be.matvec_dev(rot["qkv"][i % len(rot["qkv"])], xd["x"], yd["qkv"]), algo_bytes(6144, 4096)),
+        "o": (lambda i: be.matvec_dev(rot["o"][i % len(rot["o"])], xd["a"], yd["o"]), algo_bytes(4096, 4096)),
+        "gate": (lambda i: be.matvec_dev(rot["gate"][i % len(rot["gate"])], xd["x2"], yd["gate"]),
+                 algo_bytes(14336, 4096)),
+        "gate+up": (lambda i: be.matvec_multi_dev([rot["gate"][i % ngu], rot["up"][i % ngu]], xd["x2"],
                                                  [yd["gate"], yd["up"]]), GATE_UP_BYTES),
-        "down": (lambda i: be.matvec_dev(tensors[i % nc]["down"], xd["h"], yd["down"]), algo_bytes(4096, 14336)),
+        "down": (lambda i: be.matvec_dev(rot["down"][i % len(rot["down"])], xd["h"], yd["down"]),
+                 algo_bytes(4096, 14336)),
     }
     kernels = {}
     for n, (fn, nbytes) in launches.items():
         us = kernel_time(fn, args.kernel_reps)
         gbs = nbytes / (us * 1e-6) / 1e9
-        kernels[n] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        kernels[n] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                      "rotation_MB": round(nbytes * (ngu if n == "gate+up" else len(rot[n])) / 1e6)}
     # the same byte count read by a plain streaming kernel (fgh_checksum_dev: 16-byte loads, four in
-    # flight per thread, a sum and nothing else), rotating over as many buffers as weight copies:
-    # the read rate this box delivers to a simple stream, beside the 8 TB/s peak
+    # flight per thread, a sum and nothing else), rotating over at least 1 GB of buffers: the read
+    # rate this box delivers to a simple stream, beside the 8 TB/s peak
     rbytes = (GATE_UP_BYTES + 15) // 16 * 16
-    rbufs = [be.dev_alloc(rbytes) for _ in range(nc)]
-    rus = kernel_time(lambda i: be.checksum_dev(rbufs[i % nc], rbytes, 0), args.kernel_reps)  # streaming pass only
+    nr = -(-int(2 * ROT_BYTES) // rbytes)
+    rbufs = [be.dev_alloc(rbytes) for _ in range(nr)]
+    rus = kernel_time(lambda i: be.checksum_dev(rbufs[i % nr], rbytes, 0), args.kernel_reps)  # streaming pass only
     for p in rbufs:
         be.dev_free(p)
     rgbs = rbytes / (rus * 1e-6) / 1e9
     read_reference = {"kernel": "checksum_kernel (plain streaming read of the gate+up byte count)", "bytes": rbytes,
-                      "us": round(rus, 3), "GB/s": round(rgbs, 1), "frac": round(rgbs / HBM_PEAK_GBS, 4)}
+                      "us": round(rus, 3), "GB/s": round(rgbs, 1), "frac": round(rgbs / HBM_PEAK_GBS, 4),
+                      "rotation_MB": round(nr * rbytes / 1e6)}
 
     g = kernels["gate+up"]
     roofline = {"bound": "hbm", "achieved": g["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g["frac"],
@@ -427,17 +508,42 @@ def main() -> int:
     xpd = be.dev_alloc(Xp.nbytes)
     be.h2d(xpd, Xp)
     ypd = be.dev_alloc(4 * T * 14336)
-    mats = [t[n] for t in tensors for n in ("gate", "up")]
+    mats = [m for i in range(ngu) for m in (rot["gate"][i], rot["up"][i])]
     ops = 2.0 * T * 4096 * 14336
     prefill = {}
     for kind, pick in (("cold", lambda i: mats[i % len(mats)]), ("hot", lambda i: mats[0])):
         us = kernel_time(lambda i: be.matmul_dev(pick(i), xpd, ypd, T), args.kernel_reps)
         tops = ops / (us * 1e-6) / 1e12
         prefill[kind] = {"us": round(us, 3), "TOPS": round(tops, 2), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+    wq4 = 14336 * 16 * 144
     prefill.update({"workload": "cfg4: 64 tokens x K=4096 -> N=14336, Q4_K x Q8_K (quantization of X included)",
                     "ops_per_launch": ops, "peak_TOPS": INT8_PEAK_TOPS,
-                    "kernel": "q4k_gemm_kernel (int8 MFMA 32x32x32, split sub-block scales)",
+                    "kernel": "gemm_quant_kernel + q4k_gemm_kernel (int8 MFMA 16x16x64, split sub-block scales)",
+                    "hbm_floor_us": round((wq4 + 4 * T * (4096 + 14336)) / HBM_PEAK_GBS / 1e3, 3),
                     "traffic": counted_traffic("prefill_gemm")})
+    # the same shape in Q8_0 and Q6_K on their MFMA GEMMs (gemm_q32's and gemm_kquant's roles),
+    # cold over >= 512 MB of rotating copies and hot, against the HBM floor of their weights
+    for name, ty, wgen, bpr in (("q8_0", S.T_Q8_0, S.q8_0_weights, 128 * 34), ("q6_k", S.T_Q6_K, S.q6_k_weights, 16 * 210)):
+        wbytes = 14336 * bpr
+        w = wgen(14336, 4096, seed=130)
+        ts = [be.upload(ty, 4096, w) for _ in range(copies_for(wbytes))]
+        del w
+        line = {}
+        for kind, pick in (("cold", lambda i: ts[i % len(ts)]), ("hot", lambda i: ts[0])):
+            us = kernel_time(lambda i: be.matmul_dev(pick(i), xpd, ypd, T), args.kernel_reps)
+            nbytes = wbytes + 4 * T * (4096 + 14336)
+            line[kind] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                          "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "TOPS": round(ops / us / 1e6, 2)}
+        line.update({"workload": f"64 tokens x K=4096 -> N=14336, {name.upper()} (quantization of X included)",
+                     "hbm_floor_us": round((wbytes + 4 * T * (4096 + 14336)) / HBM_PEAK_GBS / 1e3, 3),
+                     "rotation_MB": round(len(ts) * wbytes / 1e6),
+                     "kernel": "q80_gemm_kernel (int8 MFMA 32x32x32, one block per K step)" if name == "q8_0" else
+                               "q6k_gemm_kernel (int8 MFMA 16x16x64, three scale-digit chains)"})
+        prefill[name] = line
+        for t in ts:
+            t.free()
+    for t in extra:
+        t.free()
     be.dev_free(xpd)
     be.dev_free(ypd)
 
@@ -445,12 +551,13 @@ def main() -> int:
     attn_in = {}
     attention = attention_config(be, kernel_time, args.configs, attn_in)
 
-    cpu = cpu_baseline(layer_w, xs, args.cpu_seconds, attn_in) if args.cpu_seconds > 0 else None
+    cpu = cpu_baseline(layer_w, xs, args.cpu_seconds, host, attn_in) if args.cpu_seconds > 0 else None
     info = be.info()
     be.close()
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "ms_per_step_one_layer_graphs": round(ms_step_1, 5), "graph_layers": L, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "cfg2: Llama-3-8B decode layer as Q4_K matvecs at batch 1 (QKV 4096->6144, "
                                "O 4096->4096, gate/up 4096->14336, down 14336->4096), device Q8_K quantization "
