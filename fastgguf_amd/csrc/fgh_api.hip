@@ -605,12 +605,53 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
     int32_t *sel = (int32_t *)c->msel.p;
     float *w = (float *)c->mw.p, *G = (float *)c->mg.p, *U = (float *)c->mu.p,
           *D = (float *)c->md.p;
-    HIP_TRY(c, fgh::launch_moe_route(logits, (int)E, k, n_tok, sel, w, c->stream));
     // several tokens, Q4_K experts: the slots grouped by expert, each expert's rows read once
     const bool grouped = n_tok > 1 && gate->type == FGH_T_Q4_K && up->type == FGH_T_Q4_K && down->type == FGH_T_Q4_K &&
                          gate->order == FGH_ORDER_ROW && up->order == FGH_ORDER_ROW && down->order == FGH_ORDER_ROW &&
                          gate->nb <= fgh::q4k_moe_max_blocks() && down->nb <= fgh::q4k_moe_max_blocks() &&
                          fgh::q4k_moe_lds_bytes(gate->nb) <= 65536 && fgh::q4k_moe_lds_bytes(down->nb) <= 65536;
+    // Q4_K / Q5_K experts otherwise: two launches. Gate and up route each token inside the
+    // launch (every wavefront routes its own token: the weights it streams depend on the choice),
+    // publish sel / w and write h = silu(g) * u (a workgroup holds the gate and up tiles of the
+    // same rows); down quantizes each slot's h and sums the k experts' rows in order (the
+    // combine), so neither the routing nor the down rows take a launch of their own.
+    const bool kq = (gate->type == FGH_T_Q4_K || gate->type == FGH_T_Q5_K) &&
+                    (down->type == FGH_T_Q4_K || down->type == FGH_T_Q5_K);
+    const bool fold = kq && !grouped && gate->type == up->type && gate->order == up->order &&
+                      down->order == FGH_ORDER_ROW && k <= 8 &&
+                      fgh::q4k_moe_down_lds(down->nb, k) <= fgh::GEMM_LDS_MAX &&
+                      fgh::q4k_route_fits((int)gate->type, gate->order, (gate->gpm + up->gpm) * np, gate->nb, c->num_cu);
+    if (fold) {
+        fgh::MvArgs a;
+        memset(&a, 0, sizeof(a));
+        a.t[0] = fgh::MvT{gate->dev, G, gate->rows, gate->gpm, 0};
+        a.t[1] = fgh::MvT{up->dev, U, up->rows, up->gpm, gate->gpm};
+        a.nt = 2;
+        a.groups = gate->gpm + up->gpm;
+        a.x = X;
+        a.ldx = n_embd;
+        a.ldy = ff;
+        a.nb = gate->nb;
+        a.ntile = gate->ntile;
+        a.xdiv = k;
+        a.logits = logits;
+        a.n_expert = (int)E;
+        a.sel_out = sel;
+        a.w_out = w;
+        HIP_TRY(c, fgh::launch_matvec2((int)gate->type, gate->order, a, (int)np, c->num_cu, c->stream));
+        memset(&a, 0, sizeof(a));
+        a.t[0] = fgh::MvT{down->dev, Y, down->rows, down->gpm, 0};
+        a.nt = 1;
+        a.groups = down->gpm;
+        a.x = G;  // h
+        a.ldx = ff;
+        a.ldy = n_embd;
+        a.nb = down->nb;
+        a.sel = sel;
+        HIP_TRY(c, fgh::launch_q4k_moe_down((int)down->type, a, w, k, n_tok, c->stream));
+        return FGH_OK;
+    }
+    HIP_TRY(c, fgh::launch_moe_route(logits, (int)E, k, n_tok, sel, w, c->stream));
     if (grouped) {
         const size_t ibx = fgh::q4_image_bytes(gate->nb), ibh = fgh::q4_image_bytes(down->nb);
         if ((rc = grow(c, c->mseg, (size_t)(1 + 3 * E) * 4)) || (rc = grow(c, c->mslot, (size_t)np * 4)) ||

@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <limits.h>
 #include <stdint.h>
 
 namespace fgh {
@@ -212,6 +213,17 @@ struct MvArgs {
     // when set, the activation row is silu(x) * xu (silu_f, fastgguf.c:3118), formed while
     // quantizing (an FFN down projection's input, never stored)
     const float *xu;
+    // MoE routing inside the launch (Q4_K / Q5_K kernels, instead of sel): token slot y routes
+    // token y / xdiv itself (logits [tokens][n_expert]) and takes its selected expert y % xdiv; the
+    // slot-0 workgroup 0 of each token writes its k = xdiv experts and weights to sel_out / w_out.
+    // Such a launch takes t[0] = gate, t[1] = up of the same shape and writes h = silu(g) * u to
+    // t[0].y (g and u themselves are not stored). route_off: the LDS byte offset of the
+    // wavefronts' routing buffers (set by the launcher)
+    const float *logits;
+    int n_expert;
+    int32_t *sel_out;
+    float *w_out;
+    uint32_t route_off;
 };
 size_t matvec_lds_bytes(int type, int order, int nb);  // every type (fgh_matvec.hip)
 // the launch shape a decode launch of `tiles` row tiles (over all tokens) picks: S wavefronts per
@@ -225,6 +237,13 @@ MvShape q4k_matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu)
 // Q4_K / Q5_K (fgh_q4k.hip): their own tile layout and kernel
 size_t q4k_lds_bytes(int order, int nb);
 hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
+// the MoE down projection and ordered combine of each token in one launch (Q4_K / Q5_K row order):
+// a.t[0] = {down, y}, a.x = the h = silu(g) * u rows of the token slots (stride a.ldx), a.sel the
+// slots' experts, wts their weights, k <= 8 experts per token
+size_t q4k_moe_down_lds(int nb, int k);
+// whether a Q4_K / Q5_K decode launch over `tiles` tiles x tokens has room to route its tokens
+bool q4k_route_fits(int type, int order, int64_t tiles, int nb, int num_cu);
+hipError_t launch_q4k_moe_down(int type, const MvArgs &a, const float *wts, int k, int ntok, hipStream_t s);
 hipError_t launch_q4k_relayout(int type, const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t tpm,
                                int64_t total, int64_t row_bytes, hipStream_t s);
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
@@ -252,9 +271,12 @@ __host__ __device__ inline float expf_ref(float x) {
     const double invln2n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                  c2 = 0x1.62e42ff0c52d6p-1 / 32;
-    if (!(x < 128.0f)) return x > 0.0f ? __builtin_inff() : x;  // +inf, NaN; overflow below
-    if (!(x > -128.0f)) return 0.0f;
-    const double xd = x;
+    // No branch and no select on the result (the compiler would turn either into a branch around
+    // the table read, whose wait then serializes unrolled calls): x is clamped to [-128, 128], where
+    // the method itself gives 0 and +inf (as glibc's early returns do), and a NaN x is added back.
+    const float xc = fminf(fmaxf(x, -128.0f), 128.0f);  // a NaN x becomes -128 (result 0)
+    const float nan_x = x != x ? x : 0.0f;
+    const double xd = xc;
     const double z = invln2n * xd;
     double kd = z + shift;
     uint64_t ki;
@@ -267,8 +289,135 @@ __host__ __device__ inline float expf_ref(float x) {
     const double p = __builtin_fma(c0, r, c1), r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(p, r2, y);
-    return (float)(y * s);
+    return (float)(y * s) + nan_x;
 }
+
+// ---- MoE routing (fgh_moe.hip's route launch, and the decode kernel when it routes itself) ----
+constexpr int MOE_EPL = 8;
+
+// an int whose signed order is the float order (for non-NaN floats)
+__device__ __forceinline__ int f32_ord(float f) {
+    const int b = __builtin_bit_cast(int, f);
+    return b < 0 ? b ^ 0x7FFFFFFF : b;
+}
+// maximum over the 64 lanes, in every lane: within rows of 16 by DPP, then the four row results
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));  // row_mirror
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+__device__ __forceinline__ float wave_fmax(float v) {  // fmaxf over the lanes (a NaN lane loses)
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+    auto rl = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+    return fmaxf(fmaxf(rl(0), rl(16)), fmaxf(rl(32), rl(48)));
+}
+
+// The routing of one token by one wavefront (the reference's moe_ffn routing, fastgguf.c:4594-4604,
+// over softmax_inplace 3147-3156 and argmax_f 3328-3332): lg its n_expert logits (NS = the 64-expert
+// slots a lane holds, n_expert <= 64 NS), ps 64 * MOE_EPL floats of LDS for this wavefront. Writes
+// the k selected experts to sel and their weights to w (either may be null) and returns selected
+// expert number `want` (uniform). Lane l holds experts 64 s + l (slot s) in registers; the maxima
+// are DPP / lane-read reductions (no barrier) and only the reference's sequential softmax sum goes
+// through LDS. Straight-line code over the slots: no branch waits on a memory read.
+template <int NS>
+__device__ __forceinline__ int moe_route_ns(const float *__restrict__ lg, int n_expert, int k, float *ps,
+                                            int32_t *sel, float *w, int want) {
+    const int lane = threadIdx.x & 63;
+    const BufRes lr = buf_res((const uint8_t *)lg, (uint32_t)n_expert * 4);
+    float pv[NS];
+    // max: the reference keeps the larger of each value and the running max (starting at -inf),
+    // which fmaxf does, NaN never winning; the same value in every lane
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lr, 4 * (64 * s + lane), 0, 0));
+        pv[s] = 64 * s + lane < n_expert ? v : -INFINITY;
+        mx = fmaxf(mx, pv[s]);
+    }
+    mx = wave_fmax(mx);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        pv[s] = expf_ref(pv[s] - mx);
+        ps[64 * s + lane] = pv[s];
+    }
+    // one wavefront: its LDS writes above precede lane 0's reads below.
+    // The reference's sequential sum: lane 0 adds 16 values at a time while the next 16 are read.
+    float sum = 0.0f;
+    if (lane == 0) {
+        const float4 *p4 = (const float4 *)ps;
+        const int nf = n_expert >> 4;
+        float4 c0 = p4[0], c1 = p4[1], c2 = p4[2], c3 = p4[3];
+        for (int c = 0; c < nf; ++c) {
+            const int nx = 4 * min(c + 1, nf - 1);
+            const float4 d0 = p4[nx], d1 = p4[nx + 1], d2 = p4[nx + 2], d3 = p4[nx + 3];
+            sum += c0.x; sum += c0.y; sum += c0.z; sum += c0.w;
+            sum += c1.x; sum += c1.y; sum += c1.z; sum += c1.w;
+            sum += c2.x; sum += c2.y; sum += c2.z; sum += c2.w;
+            sum += c3.x; sum += c3.y; sum += c3.z; sum += c3.w;
+            c0 = d0; c1 = d1; c2 = d2; c3 = d3;
+        }
+        for (int i = 16 * nf; i < n_expert; ++i) sum += ps[i];
+    }
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 0));
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) pv[s] = sum > 0.0f ? pv[s] * inv : pv[s];  // skipped unless sum > 0
+    // top-k by repeated argmax: candidates are values > -inf (a NaN never is), the first index of
+    // the largest wins, and with no candidate index 0 is taken; the chosen value becomes -1
+    const int ord_m1 = f32_ord(-1.0f);
+    int key[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) key[s] = 64 * s + lane < n_expert && pv[s] > -INFINITY ? f32_ord(pv[s]) : INT_MIN;
+    float wsum = 0.0f, wl = 0.0f;
+    int sl = 0, pick_want = 0;
+    for (int j = 0; j < k; ++j) {
+        int m = key[0];
+#pragma unroll
+        for (int s = 1; s < NS; ++s) m = max(m, key[s]);
+        m = wave_max_i32(m);
+        int bi = 0;  // the lowest expert holding the maximum (uniform)
+#pragma unroll
+        for (int s = NS - 1; s >= 0; --s) {
+            const uint64_t hit = __ballot(key[s] == m);
+            bi = hit ? 64 * s + (int)__builtin_ctzll(hit) : bi;
+        }
+        bi = m == INT_MIN ? 0 : bi;
+        const int bl = bi & 63, bs = bi >> 6;
+        float pick = pv[0];
+#pragma unroll
+        for (int s = 1; s < NS; ++s) pick = s == bs ? pv[s] : pick;
+        const float pvj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pick), bl));
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const bool hitme = lane == bl && s == bs;
+            pv[s] = hitme ? -1.0f : pv[s];
+            key[s] = hitme ? ord_m1 : key[s];
+        }
+        wl = lane == j ? pvj : wl;
+        sl = lane == j ? bi : sl;
+        pick_want = j == want ? bi : pick_want;
+        wsum += pvj;  // every lane keeps the same sequential sum
+    }
+    if (wsum < 6.103515625e-5f) wsum = 6.103515625e-5f;
+    if (sel && lane < k) sel[lane] = sl;
+    if (w && lane < k) w[lane] = wl / wsum;
+    return pick_want;
+}
+// n_expert <= 64 * MOE_EPL, k <= min(n_expert, 64)
+__device__ __forceinline__ int moe_route_wave(const float *__restrict__ lg, int n_expert, int k, float *ps,
+                                              int32_t *sel, float *w, int want) {
+    if (n_expert <= 64) return moe_route_ns<1>(lg, n_expert, k, ps, sel, w, want);
+    if (n_expert <= 128) return moe_route_ns<2>(lg, n_expert, k, ps, sel, w, want);
+    if (n_expert <= 256) return moe_route_ns<4>(lg, n_expert, k, ps, sel, w, want);
+    return moe_route_ns<MOE_EPL>(lg, n_expert, k, ps, sel, w, want);
+}
+
 hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s);  // test hook
 hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok, int32_t *sel, float *w, hipStream_t s);
 hipError_t launch_moe_group(const int32_t *sel, int np, int n_expert, int32_t *seg, int32_t *slots, hipStream_t s);

@@ -13,114 +13,12 @@
 
 namespace fgh {
 
-// one wavefront per token; n_expert <= 64 * MOE_EPL. Lane l holds experts 64 s + l (slot s) in
-// registers; the maxima are DPP / lane-read reductions (no LDS, no barrier) and only the
-// reference's sequential softmax sum goes through LDS (read back four floats at a time).
-constexpr int MOE_EPL = 8;
-
-// an int whose signed order is the float order (for non-NaN floats)
-__device__ __forceinline__ int f32_ord(float f) {
-    const int b = __builtin_bit_cast(int, f);
-    return b < 0 ? b ^ 0x7FFFFFFF : b;
-}
-// maximum over the 64 lanes, in every lane: within rows of 16 by DPP, then the four row results
-__device__ __forceinline__ int wave_max_i32(int v) {
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));  // row_half_mirror
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));  // row_mirror
-    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
-}
-__device__ __forceinline__ float wave_fmax(float v) {  // fmaxf over the lanes (a NaN lane loses)
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
-    auto rl = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
-    return fmaxf(fmaxf(rl(0), rl(16)), fmaxf(rl(32), rl(48)));
-}
-
+// one wavefront per token (moe_route_wave, fgh_internal.h)
 __global__ __launch_bounds__(64) void moe_route_kernel(const float *__restrict__ logits, int n_expert, int k,
                                                        int32_t *__restrict__ sel, float *__restrict__ w) {
     __shared__ __align__(16) float ps[64 * MOE_EPL];
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const int ns = (n_expert + 63) >> 6;  // slots in use (uniform)
-    const float *lg = logits + (size_t)t * n_expert;
-    float pv[MOE_EPL];
-    // max: the reference keeps the larger of each value and the running max (starting at -inf),
-    // which fmaxf does, NaN never winning; the same value in every lane
-    float mx = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < MOE_EPL; ++s) {
-        const int i = 64 * s + lane;
-        pv[s] = s < ns && i < n_expert ? lg[i] : -INFINITY;
-        mx = fmaxf(mx, pv[s]);
-    }
-    mx = wave_fmax(mx);
-#pragma unroll
-    for (int s = 0; s < MOE_EPL; ++s)
-        if (s < ns) {
-            pv[s] = expf_ref(pv[s] - mx);
-            ps[64 * s + lane] = pv[s];
-        }
-    __syncthreads();
-    // the reference's sequential sum, then its scaling by the reciprocal (skipped unless sum > 0)
-    float sum = 0.0f;
-    if (lane == 0) {
-        const float4 *p4 = (const float4 *)ps;
-        int i = 0;
-        for (; i + 4 <= n_expert; i += 4) {
-            const float4 q = p4[i >> 2];
-            sum += q.x;
-            sum += q.y;
-            sum += q.z;
-            sum += q.w;
-        }
-        for (; i < n_expert; ++i) sum += ps[i];
-    }
-    sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 0));
-    if (sum > 0.0f) {
-        const float inv = 1.0f / sum;
-#pragma unroll
-        for (int s = 0; s < MOE_EPL; ++s) pv[s] *= inv;
-    }
-    // top-k by repeated argmax: candidates are values > -inf (a NaN never is), the first index of
-    // the largest wins, and with no candidate index 0 is taken; the chosen value becomes -1
-    float wsum = 0.0f, wl = 0.0f;
-    for (int j = 0; j < k; ++j) {
-        int key[MOE_EPL], m = INT_MIN;
-#pragma unroll
-        for (int s = 0; s < MOE_EPL; ++s) {
-            const bool cand = s < ns && 64 * s + lane < n_expert && pv[s] > -INFINITY;
-            key[s] = cand ? f32_ord(pv[s]) : INT_MIN;
-            m = max(m, key[s]);
-        }
-        m = wave_max_i32(m);
-        int bi = m == INT_MIN ? 0 : -1;  // uniform
-#pragma unroll
-        for (int s = 0; s < MOE_EPL; ++s)
-            if (bi < 0 && s < ns) {  // uniform: the lowest slot holding the maximum
-                const uint64_t hit = __ballot(key[s] == m);
-                if (hit) bi = 64 * s + (int)__builtin_ctzll(hit);
-            }
-        const int bl = bi & 63, bs = bi >> 6;
-        float pick = 0.0f;
-#pragma unroll
-        for (int s = 0; s < MOE_EPL; ++s)
-            if (s == bs) pick = pv[s];
-        const float pvj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pick), bl));
-        if (lane == bl) {
-#pragma unroll
-            for (int s = 0; s < MOE_EPL; ++s)
-                if (s == bs) pv[s] = -1.0f;
-        }
-        if (lane == j) wl = pvj;
-        if (lane == 0) sel[(size_t)t * k + j] = bi;
-        wsum += pvj;  // every lane keeps the same sequential sum
-    }
-    if (wsum < 6.103515625e-5f) wsum = 6.103515625e-5f;
-    if (lane < k) w[(size_t)t * k + lane] = wl / wsum;
+    const int t = blockIdx.x;
+    moe_route_wave(logits + (size_t)t * n_expert, n_expert, k, ps, sel + (size_t)t * k, w + (size_t)t * k, 0);
 }
 
 // Groups the n_tok * k (token, selected expert) slots by expert, for the grouped expert kernels:

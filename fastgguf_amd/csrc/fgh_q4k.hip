@@ -180,16 +180,53 @@ __device__ __forceinline__ void q8k_finish(XQuant<WPG, SILU> &q, const float *x,
     }
 }
 
+// A wavefront quantizes the blocks b0 .. b0 + n - 1 of its own activation row into its own LDS
+// region (the MoE down launch: one wavefront per selected expert, each with its own row): rounds of
+// 4 blocks, 16 lanes per block. No barrier: the wavefront's LDS reads follow its own writes in
+// order. q8k_wave_begin issues the loads of the first two rounds (before the weight loads).
+template <bool SILU>
+__device__ __forceinline__ void q8k_wave_load(const float *x, const float *u, int nb, int b0, int n, int k, XRound &xr,
+                                              XRound &ur) {
+    const int i = 4 * k + ((threadIdx.x & 63) >> 4), b = b0 + i;
+    const bool live = i < n && b < nb;
+    q8k_load_b(x, b, live, xr);
+    if (SILU) q8k_load_b(u, b, live, ur);
+}
+template <bool SILU>
+__device__ __forceinline__ void q8k_wave_store(int nb, int b0, int n, int k, XRound &xr, const XRound &ur,
+                                               uint8_t *act) {
+    const int i = 4 * k + ((threadIdx.x & 63) >> 4), b = b0 + i;
+    if (SILU) xr_silu_mul(xr, ur);
+    q8k_store_b(nb, b, i < n && b < nb, xr, act);
+}
+template <int WPG, bool SILU>
+__device__ __forceinline__ void q8k_wave_begin(XQuant<WPG, SILU> &q, const float *x, const float *u, int nb, int b0,
+                                               int n) {
+    q8k_wave_load<SILU>(x, u, nb, b0, n, 0, q.r0, q.u0);
+    if (n > 4) q8k_wave_load<SILU>(x, u, nb, b0, n, 1, q.r1, q.u1);  // uniform
+}
+template <int WPG, bool SILU>
+__device__ __forceinline__ void q8k_wave_finish(XQuant<WPG, SILU> &q, const float *x, const float *u, int nb, int b0,
+                                                int n, uint8_t *act) {
+    q8k_wave_store<SILU>(nb, b0, n, 0, q.r0, q.u0, act);
+    if (n > 4) q8k_wave_store<SILU>(nb, b0, n, 1, q.r1, q.u1, act);
+    for (int k = 2; 4 * k < n; ++k) {  // rows longer than 8 blocks
+        q8k_wave_load<SILU>(x, u, nb, b0, n, k, q.r0, q.u0);
+        q8k_wave_store<SILU>(nb, b0, n, k, q.r0, q.u0, act);
+    }
+}
+
 // one step of a lane: two 16-byte pieces of its chunk (register order), its row's meta and, Q5_K
 // only, the fifth bits of its low and high values
 struct RbW {
     uint4 p0, p1, m;
     uint2 h;
 };
-// T: the (tile, block), wavefront-uniform
+// T: the (tile, block), wavefront-uniform; live = false: a ring slot past the wavefront's blocks,
+// whose loads return zeros without reading memory (a buffer of 0 bytes)
 template <int TYPE = T_Q4_K>
-__device__ __forceinline__ void rb_load(const uint8_t *T, uint32_t lane, RbW &w) {
-    const BufRes r = buf_res(T, rb_bytes(TYPE));
+__device__ __forceinline__ void rb_load(const uint8_t *T, uint32_t lane, RbW &w, bool live = true) {
+    const BufRes r = buf_res(T, live ? rb_bytes(TYPE) : 0);
     w.p0 = bld16(r, 256 + 16 * lane);
     w.p1 = bld16(r, 1280 + 16 * lane);
     w.m = bld16(r, 16 * (lane >> 2));
@@ -313,7 +350,7 @@ __device__ __forceinline__ int q4_tensor_of(const MvArgs &a, int64_t g) {
 
 // Decode matvec. Workgroup = TPW tiles x S wavefronts per tile (wavefront ks of a tile takes its
 // ks-th run of ceil(nb / S) blocks); grid = (tiles over all tensors / TPW, tokens).
-template <int ORDER, int R, int TPW, int S, bool DUMP, bool SILU = false, int TYPE = T_Q4_K>
+template <int ORDER, int R, int TPW, int S, bool DUMP, bool SILU = false, int TYPE = T_Q4_K, bool ROUTE = false>
 __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     static_assert(TYPE == T_Q4_K || ORDER == 0, "Q5_K runs the row order");
     constexpr int WPG = TPW * S;
@@ -324,22 +361,53 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     const int j = lane & 3, rr = lane >> 2;
     const int nb = a.nb;
     const int tok = blockIdx.y;
-    const int64_t tile = (int64_t)blockIdx.x * TPW + ts;
-    const bool live = tile < a.groups;
-    const int64_t tc = live ? tile : a.groups - 1;
-    const int ti = q4_tensor_of(a, tc);
-    const uint32_t lt = (uint32_t)(tc - a.t[ti].gfirst), gpm = (uint32_t)a.t[ti].gpm;
-    const uint32_t mi = (a.sel ? (uint32_t)a.sel[tok] : 0u) + lt / gpm, tt = lt % gpm;  // matrix (MoE: selected), tile
+    // ROUTE: the workgroup holds TPW / 2 row tiles of gate (a.t[0]) and up (a.t[1]), tile slots
+    // 2 i (gate) and 2 i + 1 (up) over the same rows, and writes h = silu(g) * u of them
+    int64_t tile;
+    bool live;
+    int ti;
+    uint32_t lt, gpm;
+    if (ROUTE) {
+        gpm = (uint32_t)a.t[0].gpm;
+        const uint32_t rt = blockIdx.x * (TPW / 2) + (ts >> 1);
+        live = rt < gpm;
+        ti = ts & 1;
+        lt = live ? rt : gpm - 1;
+        tile = lt;
+    } else {
+        tile = (int64_t)blockIdx.x * TPW + ts;
+        live = tile < a.groups;
+        const int64_t tc = live ? tile : a.groups - 1;
+        ti = q4_tensor_of(a, tc);
+        lt = (uint32_t)(tc - a.t[ti].gfirst);
+        gpm = (uint32_t)a.t[ti].gpm;
+    }
+    // (1) x for the first quantization rounds (independent of the expert)
+    const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
+    const float *xu = SILU ? a.xu + (size_t)(tok / a.xdiv) * a.ldx : nullptr;
+    XQuant<WPG, SILU> xq;
+    q8k_begin(xq, x, xu, nb);
+    // the expert of this token slot: from sel, or routed here (every wavefront routes its token
+    // itself, in its own LDS buffer: no barrier; workgroup 0 of the token's first slot publishes
+    // the token's experts and weights)
+    int esel = 0;
+    if (ROUTE) {
+        const int t = tok / a.xdiv, jj = tok - t * a.xdiv;
+        const bool pub = blockIdx.x == 0 && jj == 0 && wave == 0 && a.sel_out;
+        float *ps = (float *)(smem + a.route_off) + (size_t)wave * 64 * MOE_EPL;
+        esel = __builtin_amdgcn_readfirstlane(moe_route_wave(a.logits + (size_t)t * a.n_expert, a.n_expert, a.xdiv, ps,
+                                                             pub ? a.sel_out + (size_t)t * a.xdiv : nullptr,
+                                                             pub ? a.w_out + (size_t)t * a.xdiv : nullptr, jj));
+    } else if (a.sel) {
+        esel = a.sel[tok];
+    }
+    const uint32_t mi = (uint32_t)esel + lt / gpm, tt = lt % gpm;  // matrix (MoE: selected), tile
     const int nbw = (nb + S - 1) / S, bb0 = ks * nbw;
     const int nbl = max(0, min(nb, bb0 + nbw) - bb0), bl = max(nbl - 1, 0);
     const size_t bstride = (size_t)gpm * rb_bytes(TYPE);
     const uint8_t *T0 = a.t[ti].W + (((size_t)mi * nb + min(bb0, nb - 1)) * gpm + tt) * rb_bytes(TYPE);
 
-    // (1) x for the first quantization rounds, then (2) the ring's first R steps
-    const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
-    const float *xu = SILU ? a.xu + (size_t)(tok / a.xdiv) * a.ldx : nullptr;
-    XQuant<WPG, SILU> xq;
-    q8k_begin(xq, x, xu, nb);
+    // (2) the ring's first R steps
     RbW ring[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) rb_load<TYPE>(T0 + (size_t)min(r, bl) * bstride, lane, ring[r]);
@@ -407,60 +475,83 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
 #pragma unroll
     for (int r = 0; r < R - 1; ++r)
         if (b0 + r < nbl) step(ring[r], bb0 + b0 + r);  // uniform
-    float *y = a.t[ti].y + (size_t)tok * a.ldy + obase + mrow;
+    // the row results: lane ri(lane) holds row `row` of the tile when has
+    float out = 0.0f;
+    bool has;
+    int row;
     if (S > 1) {
         __syncthreads();
-        if (ORDER == 1 && ks == 0 && lane < RB_ROWS) {
-            const float4 *rr4 = rec + lane;
-            int b = 0;
-            for (; b + 4 <= nb; b += 4) {
-                float4 p[4];
+        if (ORDER == 1) {
+            has = ks == 0 && lane < RB_ROWS;
+            row = lane;
+            if (has) {
+                const float4 *rr4 = rec + lane;
+                int b = 0;
+                for (; b + 4 <= nb; b += 4) {
+                    float4 p[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) p[u] = rr4[(size_t)(b + u) * RB_ROWS];
+                    for (int u = 0; u < 4; ++u) p[u] = rr4[(size_t)(b + u) * RB_ROWS];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    acc = __builtin_fmaf(p[u].x, p[u].y, acc);
-                    macc = __builtin_fmaf(p[u].z, p[u].w, macc);
+                    for (int u = 0; u < 4; ++u) {
+                        acc = __builtin_fmaf(p[u].x, p[u].y, acc);
+                        macc = __builtin_fmaf(p[u].z, p[u].w, macc);
+                    }
                 }
-            }
-            for (; b < nb; ++b) {
-                const float4 p = rr4[(size_t)b * RB_ROWS];
-                acc = __builtin_fmaf(p.x, p.y, acc);
-                macc = __builtin_fmaf(p.z, p.w, macc);
-            }
-            if (live && mrow + lane < rows) y[lane] = acc - macc;
-        } else if (ORDER == 0 && ks == 0) {  // the row chains over the other wavefronts' blocks
-            int b = nbw;
-            for (; b + 4 <= nb; b += 4) {
-                float4 p[4];
-                float m[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    p[u] = rec[(size_t)(b + u - nbw) * 64 + lane];
-                    m[u] = recm[(size_t)(b + u - nbw) * RB_ROWS + rr];
+                for (; b < nb; ++b) {
+                    const float4 p = rr4[(size_t)b * RB_ROWS];
+                    acc = __builtin_fmaf(p.x, p.y, acc);
+                    macc = __builtin_fmaf(p.z, p.w, macc);
                 }
+                out = acc - macc;
+            }
+        } else {  // the row chains over the other wavefronts' blocks
+            has = ks == 0 && j == 0;
+            row = rr;
+            if (ks == 0) {
+                int b = nbw;
+                for (; b + 4 <= nb; b += 4) {
+                    float4 p[4];
+                    float m[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    acc = __builtin_fmaf(p[u].w, p[u].x, acc);
-                    acc2 = __builtin_fmaf(p[u].w, p[u].y, acc2);
-                    macc = __builtin_fmaf(m[u], p[u].z, macc);
+                    for (int u = 0; u < 4; ++u) {
+                        p[u] = rec[(size_t)(b + u - nbw) * 64 + lane];
+                        m[u] = recm[(size_t)(b + u - nbw) * RB_ROWS + rr];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        acc = __builtin_fmaf(p[u].w, p[u].x, acc);
+                        acc2 = __builtin_fmaf(p[u].w, p[u].y, acc2);
+                        macc = __builtin_fmaf(m[u], p[u].z, macc);
+                    }
                 }
+                for (; b < nb; ++b) {
+                    const float4 p = rec[(size_t)(b - nbw) * 64 + lane];
+                    const float m = recm[(size_t)(b - nbw) * RB_ROWS + rr];
+                    acc = __builtin_fmaf(p.w, p.x, acc);
+                    acc2 = __builtin_fmaf(p.w, p.y, acc2);
+                    macc = __builtin_fmaf(m, p.z, macc);
+                }
+                out = rb_row_final(acc, acc2, macc);
             }
-            for (; b < nb; ++b) {
-                const float4 p = rec[(size_t)(b - nbw) * 64 + lane];
-                const float m = recm[(size_t)(b - nbw) * RB_ROWS + rr];
-                acc = __builtin_fmaf(p.w, p.x, acc);
-                acc2 = __builtin_fmaf(p.w, p.y, acc2);
-                macc = __builtin_fmaf(m, p.z, macc);
-            }
-            const float out = rb_row_final(acc, acc2, macc);
-            if (live && j == 0 && mrow + rr < rows) y[rr] = out;
         }
-    } else if (ORDER == 1) {
-        if (live && j == 0 && mrow + rr < rows) y[rr] = acc - macc;
     } else {
-        const float out = rb_row_final(acc, acc2, macc);
-        if (live && j == 0 && mrow + rr < rows) y[rr] = out;
+        has = j == 0;
+        row = rr;
+        out = ORDER == 1 ? acc - macc : rb_row_final(acc, acc2, macc);
+    }
+    const bool store = has && live && mrow + row < rows;
+    if (ROUTE) {
+        // gate tile -> LDS (the routing buffers are free: every wavefront routed before the
+        // barrier after the quantization); up tile: h = silu(g) * u (silu_f, fastgguf.c:3118)
+        float *pg = (float *)(smem + a.route_off) + (ts >> 1) * RB_ROWS;
+        if (ti == 0 && has) pg[row] = out;
+        __syncthreads();
+        if (ti == 1 && store) {
+            const float g = pg[row];
+            a.t[0].y[(size_t)tok * a.ldy + mrow + row] = g / (1.0f + expf_ref(-g)) * out;
+        }
+    } else if (store) {
+        a.t[ti].y[(size_t)tok * a.ldy + obase + mrow + row] = out;
     }
 }
 
@@ -469,6 +560,10 @@ static hipError_t q4_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s
     const unsigned wg = (unsigned)((a.groups + TPW - 1) / TPW);
     if (a.dump_s) {
         q4k_mv_kernel<ORDER, R, TPW, S, true, false, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+        return hipGetLastError();
+    }
+    if (a.logits) {
+        q4k_mv_kernel<ORDER, R, TPW, S, false, false, TYPE, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
         return hipGetLastError();
     }
     if (a.xu) q4k_mv_kernel<ORDER, R, TPW, S, false, true, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
@@ -516,14 +611,121 @@ MvShape q4k_matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu)
     return MvShape{S, R, q4_tpw(S), q4_lds(order, nb, q4_tpw(S), S)};
 }
 
+// with routing: each wavefront's routing buffer after the activations and records
+static uint32_t q4_route_off(const MvShape &sh) { return (uint32_t)((sh.lds + 15) & ~(size_t)15); }
+static size_t q4_route_lds(const MvShape &sh) { return q4_route_off(sh) + (size_t)sh.S * sh.TPW * 64 * MOE_EPL * 4; }
+
+// the routing launch pairs gate and up tiles inside a workgroup: at most 2 wavefronts per tile
+static MvShape q4_route_shape(int type, int order, int64_t tiles, int nb, int num_cu) {
+    MvShape sh = q4k_matvec_shape(type, type == T_Q5_K ? 0 : order, tiles, nb, num_cu);
+    if (sh.S > 2) {
+        sh.S = 2;
+        sh.TPW = q4_tpw(2);
+        sh.lds = q4_lds(type == T_Q5_K ? 0 : order, nb, sh.TPW, sh.S);
+    }
+    return sh;
+}
+
+bool q4k_route_fits(int type, int order, int64_t tiles, int nb, int num_cu) {
+    const MvShape sh = q4_route_shape(type, order, tiles, nb, num_cu);
+    return sh.lds <= (sh.S == 1 ? (size_t)65536 : GEMM_LDS_MAX) && q4_route_lds(sh) <= GEMM_LDS_MAX;
+}
+
 hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
     if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
     if (type == T_Q5_K) order = 0;
-    const MvShape sh = q4k_matvec_shape(type, order, a.groups * ntok, a.nb, num_cu);
+    const MvShape sh = a.logits ? q4_route_shape(type, order, a.groups * ntok, a.nb, num_cu)
+                                : q4k_matvec_shape(type, order, a.groups * ntok, a.nb, num_cu);
     if (sh.lds > (sh.S == 1 ? (size_t)65536 : GEMM_LDS_MAX)) return hipErrorInvalidValue;
-    if (type == T_Q5_K) return q4_launch_s<0, T_Q5_K>(sh.S, sh.R, a, ntok, sh.lds, s);
-    if (order == 0) return q4_launch_s<0, T_Q4_K>(sh.S, sh.R, a, ntok, sh.lds, s);
-    return q4_launch_s<1, T_Q4_K>(sh.S, sh.R, a, ntok, sh.lds, s);
+    MvArgs b = a;
+    size_t lds = sh.lds;
+    if (a.logits) {  // gate and up of the selected experts, h = silu(g) * u into a.t[0].y
+        if (a.sel || !a.sel_out || !a.w_out || a.n_expert < 1 || a.n_expert > 64 * MOE_EPL || a.xdiv < 1 ||
+            a.xdiv > a.n_expert || a.xdiv > 64 || ntok % a.xdiv || q4_route_lds(sh) > GEMM_LDS_MAX || a.nt != 2 ||
+            a.t[0].gpm != a.t[1].gpm || a.t[0].rows != a.t[1].rows || a.dump_s || a.xu)
+            return hipErrorInvalidValue;
+        b.route_off = q4_route_off(sh);
+        b.groups = 2 * a.t[0].gpm;  // TPW / 2 row tiles per workgroup
+        lds = q4_route_lds(sh);
+    }
+    if (type == T_Q5_K) return q4_launch_s<0, T_Q5_K>(sh.S, sh.R, b, ntok, lds, s);
+    if (order == 0) return q4_launch_s<0, T_Q4_K>(sh.S, sh.R, b, ntok, lds, s);
+    return q4_launch_s<1, T_Q4_K>(sh.S, sh.R, b, ntok, lds, s);
+}
+
+// MoE down projection and combine of one token in one launch (moe_ffn, fastgguf.c:4620-4635):
+// workgroup = one 16-row tile of the output x the token's k selected experts, wavefront j = expert
+// sel[t k + j]. Wavefront j quantizes its own row h_j (a.x = the h rows of the token's slots) into
+// its own LDS region, runs the row order of dot_q4_K_q8k (or dot_q5_K_q8k)
+// over the expert's blocks and parks each row's dot product in LDS; wavefront 0 then forms
+// y = fma(w_j, d_j, s) over j in order, the reference's sum (gcc contracts `s += w * dot`).
+// grid = (16-row tiles of one expert matrix, tokens); a.t[0] = {down, y}, a.ldy = y's token stride.
+template <int R, int TYPE>
+__global__ __launch_bounds__(512) void q4k_moe_down_kernel(MvArgs a, const float *__restrict__ wts, int k) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int jw = __builtin_amdgcn_readfirstlane(tid >> 6);  // the selected expert of this wavefront
+    const int j = lane & 3, rr = lane >> 2;
+    const int nb = a.nb, tok = blockIdx.y, slot = tok * k + jw;
+    const uint32_t tt = blockIdx.x, gpm = (uint32_t)a.t[0].gpm;
+    const uint32_t mi = (uint32_t)a.sel[slot];
+    const size_t bstride = (size_t)gpm * rb_bytes(TYPE);
+    const uint8_t *T0 = a.t[0].W + ((size_t)mi * nb * gpm + tt) * rb_bytes(TYPE);
+    uint8_t *act = smem + (size_t)jw * q4_act_bytes(nb);
+    float *dots = (float *)(smem + (size_t)k * q4_act_bytes(nb));  // [k][16]
+    const float *x = a.x + (size_t)slot * a.ldx;
+    XQuant<1, false> xq;
+    q8k_wave_begin(xq, x, nullptr, nb, 0, nb);
+    const int bl = nb - 1;
+    RbW ring[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rb_load<TYPE>(T0 + (size_t)min(r, bl) * bstride, lane, ring[r], r < nb);
+    q8k_wave_finish(xq, x, nullptr, nb, 0, nb, act);
+    const RbLane ln = rb_lane(lane);
+    float acc = 0.0f, acc2 = 0.0f, macc = 0.0f;
+    auto step = [&](const RbW &w, int b) {
+        RbIn in;
+        rb_in(w, act, nb, b, ln, in);
+        const float fd = fp16_bits_to_f32(w.m.x & 0xFFFF) * in.yd;
+        const float fdm = fp16_bits_to_f32(w.m.x >> 16) * in.yd;
+        int u0, u1;
+        rb_row_lanes<TYPE>(w, in, j, u0, u1);
+        acc = __builtin_fmaf(fd, (float)u0, acc);
+        acc2 = __builtin_fmaf(fd, (float)u1, acc2);
+        macc = __builtin_fmaf(fdm, (float)in.mt, macc);
+    };
+    int b0 = 0;
+    for (; b0 + R <= nb; b0 += R) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            step(ring[r], b0 + r);
+            rb_load<TYPE>(T0 + (size_t)min(b0 + r + R, bl) * bstride, lane, ring[r], b0 + r + R < nb);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R - 1; ++r)
+        if (b0 + r < nb) step(ring[r], b0 + r);  // uniform
+    const float out = rb_row_final(acc, acc2, macc);
+    if (j == 0) dots[jw * 16 + rr] = out;
+    __syncthreads();
+    if (jw == 0 && lane < RB_ROWS) {
+        const int64_t row = (int64_t)tt * RB_ROWS + lane;
+        float sum = 0.0f;
+        for (int jj = 0; jj < k; ++jj) sum = __builtin_fmaf(wts[(size_t)tok * k + jj], dots[jj * 16 + lane], sum);
+        if (row < a.t[0].rows) a.t[0].y[(size_t)tok * a.ldy + row] = sum;
+    }
+}
+
+size_t q4k_moe_down_lds(int nb, int k) { return (size_t)k * q4_act_bytes(nb) + (size_t)k * RB_ROWS * 4; }
+
+hipError_t launch_q4k_moe_down(int type, const MvArgs &a, const float *wts, int k, int ntok, hipStream_t s) {
+    const size_t lds = q4k_moe_down_lds(a.nb, k);
+    if (!a.sel || !a.x || a.xu || k < 1 || k > 8 || ntok < 1 || lds > GEMM_LDS_MAX || a.t[0].gpm < 1)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)a.t[0].gpm, (unsigned)ntok);
+    if (type == T_Q5_K) q4k_moe_down_kernel<4, T_Q5_K><<<grid, 64 * k, lds, s>>>(a, wts, k);
+    else q4k_moe_down_kernel<4, T_Q4_K><<<grid, 64 * k, lds, s>>>(a, wts, k);
+    return hipGetLastError();
 }
 
 // Q8_K images of activation rows, in the kernels' LDS layout (q4_act_bytes(nb) bytes per row): row

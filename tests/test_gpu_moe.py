@@ -29,6 +29,7 @@ def test_device_expf_matches_libm(backend, oracle):
     got = backend.expf(xs)
     want = oracle.libm_expf(xs)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.isnan(backend.expf(np.array([np.nan, -np.nan], np.float32))).all()
 
 
 def upload_experts(backend, w, cols, rows, n_exp):
@@ -45,6 +46,12 @@ def test_moe_matches_golden(backend):
     assert np.array_equal(sel, g["sel"])  # ties on token 2 (experts 3, 7) and token 3 (all equal)
     assert bits_equal(w, g["w"])
     assert bits_equal(Y, g["Y"])
+    # one token per call: the launch that routes inside the gate / up matvec
+    for i in range(T):
+        Y1, sel1, w1 = backend.moe_ffn(gate, up, down, K, g["logits"][i:i + 1], g["X"][i:i + 1])
+        assert np.array_equal(sel1, g["sel"][i:i + 1])
+        assert bits_equal(w1, g["w"][i:i + 1])
+        assert bits_equal(Y1, g["Y"][i:i + 1])
     for t in (gate, up, down):
         t.free()
 
@@ -105,6 +112,26 @@ def test_moe_matches_oracle(backend, oracle, E, K, D, F, T):
     assert bits_equal(w, wo)
     for t in range(T):
         assert rel_err(Y[t], Yo[t]) <= 1e-5
+    assert bits_equal(Y, Yo)
+    for t in (gate, up, down):
+        t.free()
+
+
+@pytest.mark.parametrize("E,K,T", [(200, 8, 1), (512, 8, 1), (96, 10, 1), (70, 1, 1), (200, 8, 3)])
+def test_moe_routing_shapes(backend, oracle, E, K, T):
+    """Expert counts that fill several 64-expert slots of a wavefront (and 512, the most), k above
+    the 8 experts the fused down launch takes (the separate routing launch), and k = 1."""
+    D, F = 256, 256
+    gw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 400 + E)
+    uw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 401 + E)
+    dw = S.random_bytes_weights(S.T_Q4_K, E * D, F, 402 + E)
+    X = S.activations(D, 403 + K, rows=T)
+    logits = S.router_logits(T, E, 404 + K)
+    Yo, so, wo = oracle.moe_ffn((S.T_Q4_K,) * 3, gw, uw, dw, E, K, D, F, logits, X)
+    gate, up, down = (upload_experts(backend, a, c, r, E) for a, c, r in ((gw, D, F), (uw, D, F), (dw, F, D)))
+    Y, sel, w = backend.moe_ffn(gate, up, down, K, logits, X)
+    assert np.array_equal(sel, so)
+    assert bits_equal(w, wo)
     assert bits_equal(Y, Yo)
     for t in (gate, up, down):
         t.free()

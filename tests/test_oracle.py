@@ -85,7 +85,8 @@ def test_moe_q5_matches_golden(oracle):
 # fused evaluation (found by sweeping every float); and special values
 EXPF_HARD = [float.fromhex("0x1.04845ep+5"), float.fromhex("-0x1.f8cbb2p+5")]
 EXPF_SPECIAL = [0.0, -0.0, 1.0, -1.0, 88.72283, 88.72284, 100.0, -87.33654, -103.97207, -103.97208, -150.0,
-                float("inf"), float("-inf"), 1e-30, -1e-30]
+                float("inf"), float("-inf"), 1e-30, -1e-30, 127.99999, 128.0, -128.0, -127.99999, 200.0,
+                -200.0, 1e30, -1e30]
 
 
 def test_expf_restatement_matches_libm(oracle):
