@@ -39,6 +39,7 @@ struct fgh_ctx {
     DevBuf msel, mw, mg, mu, md, mlog;  // MoE: selection, weights, gate / up / down outputs
     DevBuf mseg, mslot, mimx, mimh;         // MoE: slots grouped by expert, Q8_K images of x and h
     DevBuf ck;                              // fgh_checksum_dev: per-workgroup partial sums
+    DevBuf h;                               // fgh_matvec_silu_dev: silu(g) * u
     int num_cu = 256;         // compute units (sizes the persistent decode grid)
     bool capturing = false;   // inside fgh_graph_begin / fgh_graph_end
     // Instantiated graphs not yet destroyed hold the scratch addresses they were captured with:
@@ -195,7 +196,7 @@ static int quantize_dev(fgh_ctx *c, uint32_t type, int64_t cols, const float *x,
 // (device, stride ldx); y[i]: outputs of tensor i (token stride ldy)
 static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const float *x, int64_t ldx,
                          float *const *y, int64_t ldy, int ntok, int32_t *ds, int32_t *dm,
-                         const int32_t *sel = nullptr, int xdiv = 1, const float *xu = nullptr) {
+                         const int32_t *sel = nullptr, int xdiv = 1) {
     fgh::MvArgs a;
     memset(&a, 0, sizeof(a));
     int64_t g = 0;
@@ -205,7 +206,6 @@ static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const fl
     }
     a.sel = sel;
     a.xdiv = xdiv;
-    a.xu = xu;
     a.nt = n;
     a.groups = g;
     a.x = x;
@@ -393,7 +393,7 @@ void fgh_close(fgh_ctx *c) {
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf *b : {&c->x, &c->y, &c->aqs, &c->ad, &c->abs, &c->gq, &c->msel, &c->mw, &c->mg,
                       &c->mu, &c->md, &c->mlog, &c->mseg, &c->mslot, &c->mimx, &c->mimh, &c->ck, &c->as, &c->kqr,
-                      &c->kor})
+                      &c->kor, &c->h})
         if (b->p) (void)hipFree(b->p);
     free_retired(c);
     (void)hipStreamDestroy(c->stream);
@@ -544,8 +544,13 @@ int fgh_matvec_silu_dev(fgh_ctx *c, const fgh_tensor *t, const float *g, const f
     if (!g || !u || !y) return fail(c, FGH_ERR_ARG, "matvec_silu: null pointer");
     INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
+    // h once (one short launch), then the plain matvec: forming h inside the matvec's quantization
+    // would repeat its expf in every workgroup
+    if ((rc = grow(c, c->h, (size_t)t->cols * 4))) return rc;
+    float *h = (float *)c->h.p;
+    HIP_TRY(c, fgh::launch_silu_mul(g, u, h, t->cols, c->stream));
     float *yy[1] = {y};
-    return matvec_launch(c, 1, &t, g, t->cols, yy, t->rows * t->n_mats, 1, nullptr, nullptr, nullptr, 1, u);
+    return matvec_launch(c, 1, &t, h, t->cols, yy, t->rows * t->n_mats, 1, nullptr, nullptr);
 }
 
 int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, float *Y, int ldy, int nb) {
@@ -698,9 +703,10 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
             (rc = matvec_launch(c, 1, &up, X, n_embd, yu, ff, (int)np, nullptr, nullptr, sel, k)))
             return rc;
     }
-    // down, with h = silu(g) * u formed inside the launch while it quantizes its input
+    // down on h = silu(g) * u (formed in place of g)
+    HIP_TRY(c, fgh::launch_silu_mul(G, U, G, np * ff, c->stream));
     float *yd[1] = {D};
-    if ((rc = matvec_launch(c, 1, &down, G, ff, yd, n_embd, (int)np, nullptr, nullptr, sel, 1, U))) return rc;
+    if ((rc = matvec_launch(c, 1, &down, G, ff, yd, n_embd, (int)np, nullptr, nullptr, sel, 1))) return rc;
     HIP_TRY(c, fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, c->stream));
     return FGH_OK;
 }

@@ -210,9 +210,6 @@ struct MvArgs {
     // every tensor (launched with the tiles of one matrix) and activation row y / xdiv
     const int32_t *sel;
     int xdiv;
-    // when set, the activation row is silu(x) * xu (silu_f, fastgguf.c:3118), formed while
-    // quantizing (an FFN down projection's input, never stored)
-    const float *xu;
     // MoE routing inside the launch (Q4_K / Q5_K kernels, instead of sel): token slot y routes
     // token y / xdiv itself (logits [tokens][n_expert]) and takes its selected expert y % xdiv; the
     // slot-0 workgroup 0 of each token writes its k = xdiv experts and weights to sel_out / w_out.
@@ -419,6 +416,8 @@ __device__ __forceinline__ int moe_route_wave(const float *__restrict__ lg, int 
 }
 
 hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s);  // test hook
+// h = silu(g) * u over n values (silu_f, fastgguf.c:3118); h may be g
+hipError_t launch_silu_mul(const float *g, const float *u, float *h, int64_t n, hipStream_t s);
 hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok, int32_t *sel, float *w, hipStream_t s);
 hipError_t launch_moe_group(const int32_t *sel, int np, int n_expert, int32_t *seg, int32_t *slots, hipStream_t s);
 // grouped Q4_K row-order expert matvecs (fgh_q4k.hip): a.groups = tiles of one matrix over a.t;

@@ -90,18 +90,6 @@ __device__ __forceinline__ void xq_load(const float *__restrict__ x, int nb, int
 #pragma unroll
     for (int u = 0; u < 4; ++u) xv.v[u] = *(const float4 *)(p + 4 * u);
 }
-// x = silu(x) * u, value by value (silu_f, fastgguf.c:3118: x / (1 + expf(-x)))
-__device__ __forceinline__ void xv_silu_mul(XVals &xv, const XVals &uv) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        float4 &g = xv.v[q];
-        const float4 u = uv.v[q];
-        g.x = g.x / (1.0f + expf_ref(-g.x)) * u.x;
-        g.y = g.y / (1.0f + expf_ref(-g.y)) * u.y;
-        g.z = g.z / (1.0f + expf_ref(-g.z)) * u.z;
-        g.w = g.w / (1.0f + expf_ref(-g.w)) * u.w;
-    }
-}
 template <int TYPE, int WPG>
 __device__ __forceinline__ void xq_store(int nb, int rb, const XVals &xv, uint8_t *act) {
     using Q = XQ<TYPE, WPG>;
@@ -151,19 +139,13 @@ __device__ __forceinline__ void xq_store(int nb, int rb, const XVals &xv, uint8_
         if (tl == 0) ((float *)(act + act_off_d(TYPE, nb)))[b] = d;
     }
 }
-// SILU: the row quantized is silu(x) * u (uv: the first round of u, loaded with xv)
-template <int TYPE, int WPG, bool SILU>
-__device__ __forceinline__ void xq_finish(const float *__restrict__ x, const float *__restrict__ u, int nb, XVals &xv,
-                                          XVals &uv, uint8_t *act) {
+// the rounds after the first (xv: the first round, loaded before the weights)
+template <int TYPE, int WPG>
+__device__ __forceinline__ void xq_finish(const float *__restrict__ x, int nb, XVals &xv, uint8_t *act) {
     using Q = XQ<TYPE, WPG>;
-    if (SILU) xv_silu_mul(xv, uv);
     xq_store<TYPE, WPG>(nb, 0, xv, act);
     for (int rb = Q::BPR; rb < nb; rb += Q::BPR) {
         xq_load<TYPE, WPG>(x, nb, rb, xv);
-        if (SILU) {
-            xq_load<TYPE, WPG>(u, nb, rb, uv);
-            xv_silu_mul(xv, uv);
-        }
         xq_store<TYPE, WPG>(nb, rb, xv, act);
     }
 }
@@ -302,7 +284,7 @@ __device__ __forceinline__ int mv_tensor_of(const MvArgs &a, int64_t g) {
 // ceil(steps / S) steps); grid = (tiles over all tensors / TPW, tokens).
 // ORDER 1 (Q4_0 only): the repacked order of dot_q40x8 (fastgguf.c:2424-2467), one chain per row
 // over whole-block integers, acc = fma(d * yd, isum, acc), out = acc.
-template <int TYPE, int R, int TPW, int S, bool DUMP, bool SILU = false, int ORDER = 0>
+template <int TYPE, int R, int TPW, int S, bool DUMP, int ORDER = 0>
 __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
     static_assert(ORDER == 0 || TYPE == T_Q4_0, "only Q4_0 has a repacked order here");
     constexpr int WPG = TPW * S;
@@ -326,15 +308,13 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
     const uint8_t *T0 = a.t[ti].W + (((size_t)mi * nst + min(s0, nst - 1)) * tpm + tt) * TB;
 
     const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
-    const float *xu = SILU ? a.xu + (size_t)(tok / a.xdiv) * a.ldx : nullptr;
-    XVals xv, uv;
+    XVals xv;
     xq_load<TYPE, WPG>(x, nb, 0, xv);
-    if (SILU) xq_load<TYPE, WPG>(xu, nb, 0, uv);
     StepW<TYPE> ring[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) step_load(T0 + (size_t)min(k, sl) * sstride, (uint32_t)lane, ring[k]);
     uint8_t *act = smem;
-    xq_finish<TYPE, WPG, SILU>(x, xu, nb, xv, uv, act);
+    xq_finish<TYPE, WPG>(x, nb, xv, act);
     __syncthreads();
 
     const float *ad = (const float *)(act + act_off_d(TYPE, nb));
@@ -510,9 +490,8 @@ size_t matvec_lds_bytes(int type, int order, int nb) {
 template <int TYPE, int ORDER, int R, int TPW, int S>
 static hipError_t mv_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
     const unsigned wg = (unsigned)((a.groups + TPW - 1) / TPW);
-    if (a.dump_s) mv_kernel<TYPE, R, TPW, S, true, false, ORDER><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
-    else if (a.xu) mv_kernel<TYPE, R, TPW, S, false, true, ORDER><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
-    else mv_kernel<TYPE, R, TPW, S, false, false, ORDER><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    if (a.dump_s) mv_kernel<TYPE, R, TPW, S, true, ORDER><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    else mv_kernel<TYPE, R, TPW, S, false, ORDER><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     return hipGetLastError();
 }
 template <int TYPE, int ORDER, int TPW, int S>
@@ -541,7 +520,6 @@ static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
 }
 template <int TYPE, int ORDER = 0>
 static hipError_t mv_launch_type(const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
-    if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
     const MvShape sh = mv_shape<TYPE>(a.groups * ntok, a.nb, num_cu);
     if (sh.lds > (sh.S == 1 ? (size_t)65536 : GEMM_LDS_MAX)) return hipErrorInvalidValue;
     switch (sh.S) {

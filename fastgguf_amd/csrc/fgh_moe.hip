@@ -105,6 +105,28 @@ hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s) {
     return hipGetLastError();
 }
 
+// four values per thread, 1024 per workgroup; each value is read before its h is written, so h
+// may be g (or u)
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float *g, const float *u, float *h, int64_t n) {
+    const int64_t i0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    float gv[4], uv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int64_t i = min(i0 + 256 * q, n - 1);
+        gv[q] = g[i];
+        uv[q] = u[i];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (i0 + 256 * q < n) h[i0 + 256 * q] = gv[q] / (1.0f + expf_ref(-gv[q])) * uv[q];
+}
+
+hipError_t launch_silu_mul(const float *g, const float *u, float *h, int64_t n, hipStream_t s) {
+    if (n < 1) return hipErrorInvalidValue;
+    silu_mul_kernel<<<(unsigned)((n + 1023) / 1024), 256, 0, s>>>(g, u, h, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok, int32_t *sel, float *w,
                             hipStream_t s) {
     if (n_expert < 1 || n_expert > 64 * MOE_EPL || k < 1 || k > n_expert || k > 64) return hipErrorInvalidValue;

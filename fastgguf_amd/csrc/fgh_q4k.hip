@@ -130,9 +130,8 @@ __device__ __forceinline__ void q8k_store(int nb, int rb, const XRound &xr, uint
     q8k_store_b(nb, b, b < nb, xr, act);
 }
 
-// Quantizes x (nb blocks) into act with all 64 * WPG threads: q8k_begin issues the loads of the
-// first two rounds (before the caller's weight loads), q8k_finish the rest and the stores.
-// x = silu(x) * u, value by value (silu_f, fastgguf.c:3118: x / (1 + expf(-x)))
+// x = silu(x) * u, value by value (silu_f, fastgguf.c:3118: x / (1 + expf(-x))); the Q8_K
+// images of h rows (q4_image_kernel) form it while they quantize
 __device__ __forceinline__ void xr_silu_mul(XRound &xr, const XRound &ur) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -145,74 +144,51 @@ __device__ __forceinline__ void xr_silu_mul(XRound &xr, const XRound &ur) {
     }
 }
 
-// SILU: the row quantized is silu(x) * u (u: a second row of the same shape)
-template <int WPG, bool SILU = false>
+// Quantizes x (nb blocks) into act with all 64 * WPG threads: q8k_begin issues the loads of the
+// first two rounds (before the caller's weight loads), q8k_finish the rest and the stores.
+template <int WPG>
 struct XQuant {
     static constexpr int XB = 4 * WPG;  // blocks per round
     XRound r0, r1;
-    XRound u0, u1;  // SILU only (unused registers otherwise are removed by the compiler)
 };
-template <int WPG, bool SILU>
-__device__ __forceinline__ void q8k_begin(XQuant<WPG, SILU> &q, const float *x, const float *u, int nb) {
+template <int WPG>
+__device__ __forceinline__ void q8k_begin(XQuant<WPG> &q, const float *x, int nb) {
     q8k_load(x, nb, 0, q.r0);
-    if (SILU) q8k_load(u, nb, 0, q.u0);
-    if (nb > XQuant<WPG, SILU>::XB) {  // uniform
-        q8k_load(x, nb, XQuant<WPG, SILU>::XB, q.r1);
-        if (SILU) q8k_load(u, nb, XQuant<WPG, SILU>::XB, q.u1);
-    }
+    if (nb > XQuant<WPG>::XB) q8k_load(x, nb, XQuant<WPG>::XB, q.r1);  // uniform
 }
-template <int WPG, bool SILU>
-__device__ __forceinline__ void q8k_finish(XQuant<WPG, SILU> &q, const float *x, const float *u, int nb, uint8_t *act) {
-    constexpr int XB = XQuant<WPG, SILU>::XB;
-    if (SILU) xr_silu_mul(q.r0, q.u0);
+template <int WPG>
+__device__ __forceinline__ void q8k_finish(XQuant<WPG> &q, const float *x, int nb, uint8_t *act) {
+    constexpr int XB = XQuant<WPG>::XB;
     q8k_store(nb, 0, q.r0, act);
-    if (nb > XB) {
-        if (SILU) xr_silu_mul(q.r1, q.u1);
-        q8k_store(nb, XB, q.r1, act);
-    }
+    if (nb > XB) q8k_store(nb, XB, q.r1, act);
     for (int rb = 2 * XB; rb < nb; rb += XB) {  // rows longer than 2 * XB blocks
         q8k_load(x, nb, rb, q.r0);
-        if (SILU) {
-            q8k_load(u, nb, rb, q.u0);
-            xr_silu_mul(q.r0, q.u0);
-        }
         q8k_store(nb, rb, q.r0, act);
     }
 }
 
-// A wavefront quantizes the blocks b0 .. b0 + n - 1 of its own activation row into its own LDS
-// region (the MoE down launch: one wavefront per selected expert, each with its own row): rounds of
-// 4 blocks, 16 lanes per block. No barrier: the wavefront's LDS reads follow its own writes in
+// A wavefront quantizes the blocks 0 .. nb - 1 of its own activation row into its own LDS region
+// (the MoE down launch: one wavefront per selected expert, each with its own row): rounds of 4
+// blocks, 16 lanes per block. No barrier: the wavefront's LDS reads follow its own writes in
 // order. q8k_wave_begin issues the loads of the first two rounds (before the weight loads).
-template <bool SILU>
-__device__ __forceinline__ void q8k_wave_load(const float *x, const float *u, int nb, int b0, int n, int k, XRound &xr,
-                                              XRound &ur) {
-    const int i = 4 * k + ((threadIdx.x & 63) >> 4), b = b0 + i;
-    const bool live = i < n && b < nb;
-    q8k_load_b(x, b, live, xr);
-    if (SILU) q8k_load_b(u, b, live, ur);
+__device__ __forceinline__ void q8k_wave_load(const float *x, int nb, int k, XRound &xr) {
+    const int b = 4 * k + ((threadIdx.x & 63) >> 4);
+    q8k_load_b(x, b, b < nb, xr);
 }
-template <bool SILU>
-__device__ __forceinline__ void q8k_wave_store(int nb, int b0, int n, int k, XRound &xr, const XRound &ur,
-                                               uint8_t *act) {
-    const int i = 4 * k + ((threadIdx.x & 63) >> 4), b = b0 + i;
-    if (SILU) xr_silu_mul(xr, ur);
-    q8k_store_b(nb, b, i < n && b < nb, xr, act);
+__device__ __forceinline__ void q8k_wave_store(int nb, int k, const XRound &xr, uint8_t *act) {
+    const int b = 4 * k + ((threadIdx.x & 63) >> 4);
+    q8k_store_b(nb, b, b < nb, xr, act);
 }
-template <int WPG, bool SILU>
-__device__ __forceinline__ void q8k_wave_begin(XQuant<WPG, SILU> &q, const float *x, const float *u, int nb, int b0,
-                                               int n) {
-    q8k_wave_load<SILU>(x, u, nb, b0, n, 0, q.r0, q.u0);
-    if (n > 4) q8k_wave_load<SILU>(x, u, nb, b0, n, 1, q.r1, q.u1);  // uniform
+__device__ __forceinline__ void q8k_wave_begin(XQuant<1> &q, const float *x, int nb) {
+    q8k_wave_load(x, nb, 0, q.r0);
+    if (nb > 4) q8k_wave_load(x, nb, 1, q.r1);  // uniform
 }
-template <int WPG, bool SILU>
-__device__ __forceinline__ void q8k_wave_finish(XQuant<WPG, SILU> &q, const float *x, const float *u, int nb, int b0,
-                                                int n, uint8_t *act) {
-    q8k_wave_store<SILU>(nb, b0, n, 0, q.r0, q.u0, act);
-    if (n > 4) q8k_wave_store<SILU>(nb, b0, n, 1, q.r1, q.u1, act);
-    for (int k = 2; 4 * k < n; ++k) {  // rows longer than 8 blocks
-        q8k_wave_load<SILU>(x, u, nb, b0, n, k, q.r0, q.u0);
-        q8k_wave_store<SILU>(nb, b0, n, k, q.r0, q.u0, act);
+__device__ __forceinline__ void q8k_wave_finish(XQuant<1> &q, const float *x, int nb, uint8_t *act) {
+    q8k_wave_store(nb, 0, q.r0, act);
+    if (nb > 4) q8k_wave_store(nb, 1, q.r1, act);
+    for (int k = 2; 4 * k < nb; ++k) {  // rows longer than 8 blocks
+        q8k_wave_load(x, nb, k, q.r0);
+        q8k_wave_store(nb, k, q.r0, act);
     }
 }
 
@@ -350,7 +326,7 @@ __device__ __forceinline__ int q4_tensor_of(const MvArgs &a, int64_t g) {
 
 // Decode matvec. Workgroup = TPW tiles x S wavefronts per tile (wavefront ks of a tile takes its
 // ks-th run of ceil(nb / S) blocks); grid = (tiles over all tensors / TPW, tokens).
-template <int ORDER, int R, int TPW, int S, bool DUMP, bool SILU = false, int TYPE = T_Q4_K, bool ROUTE = false>
+template <int ORDER, int R, int TPW, int S, bool DUMP, int TYPE = T_Q4_K, bool ROUTE = false>
 __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     static_assert(TYPE == T_Q4_K || ORDER == 0, "Q5_K runs the row order");
     constexpr int WPG = TPW * S;
@@ -384,9 +360,8 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     }
     // (1) x for the first quantization rounds (independent of the expert)
     const float *x = a.x + (size_t)(tok / a.xdiv) * a.ldx;
-    const float *xu = SILU ? a.xu + (size_t)(tok / a.xdiv) * a.ldx : nullptr;
-    XQuant<WPG, SILU> xq;
-    q8k_begin(xq, x, xu, nb);
+    XQuant<WPG> xq;
+    q8k_begin(xq, x, nb);
     // the expert of this token slot: from sel, or routed here (every wavefront routes its token
     // itself, in its own LDS buffer: no barrier; workgroup 0 of the token's first slot publishes
     // the token's experts and weights)
@@ -413,7 +388,7 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     for (int r = 0; r < R; ++r) rb_load<TYPE>(T0 + (size_t)min(r, bl) * bstride, lane, ring[r]);
     // (3) quantize x into LDS while the weights are in flight
     uint8_t *act = smem;
-    q8k_finish(xq, x, xu, nb, act);
+    q8k_finish(xq, x, nb, act);
     __syncthreads();
 
     const int64_t mrow = (int64_t)tt * RB_ROWS;  // first row of the tile in its matrix
@@ -559,15 +534,14 @@ template <int ORDER, int R, int TPW, int S, int TYPE>
 static hipError_t q4_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
     const unsigned wg = (unsigned)((a.groups + TPW - 1) / TPW);
     if (a.dump_s) {
-        q4k_mv_kernel<ORDER, R, TPW, S, true, false, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+        q4k_mv_kernel<ORDER, R, TPW, S, true, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
         return hipGetLastError();
     }
     if (a.logits) {
-        q4k_mv_kernel<ORDER, R, TPW, S, false, false, TYPE, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+        q4k_mv_kernel<ORDER, R, TPW, S, false, TYPE, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
         return hipGetLastError();
     }
-    if (a.xu) q4k_mv_kernel<ORDER, R, TPW, S, false, true, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
-    else q4k_mv_kernel<ORDER, R, TPW, S, false, false, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+    q4k_mv_kernel<ORDER, R, TPW, S, false, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
     return hipGetLastError();
 }
 template <int ORDER, int TPW, int S, int TYPE = T_Q4_K>
@@ -632,7 +606,6 @@ bool q4k_route_fits(int type, int order, int64_t tiles, int nb, int num_cu) {
 }
 
 hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
-    if (a.xu && a.dump_s) return hipErrorInvalidValue;  // the integer dump takes plain x
     if (type == T_Q5_K) order = 0;
     const MvShape sh = a.logits ? q4_route_shape(type, order, a.groups * ntok, a.nb, num_cu)
                                 : q4k_matvec_shape(type, order, a.groups * ntok, a.nb, num_cu);
@@ -642,7 +615,7 @@ hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int
     if (a.logits) {  // gate and up of the selected experts, h = silu(g) * u into a.t[0].y
         if (a.sel || !a.sel_out || !a.w_out || a.n_expert < 1 || a.n_expert > 64 * MOE_EPL || a.xdiv < 1 ||
             a.xdiv > a.n_expert || a.xdiv > 64 || ntok % a.xdiv || q4_route_lds(sh) > GEMM_LDS_MAX || a.nt != 2 ||
-            a.t[0].gpm != a.t[1].gpm || a.t[0].rows != a.t[1].rows || a.dump_s || a.xu)
+            a.t[0].gpm != a.t[1].gpm || a.t[0].rows != a.t[1].rows || a.dump_s)
             return hipErrorInvalidValue;
         b.route_off = q4_route_off(sh);
         b.groups = 2 * a.t[0].gpm;  // TPW / 2 row tiles per workgroup
@@ -674,13 +647,13 @@ __global__ __launch_bounds__(512) void q4k_moe_down_kernel(MvArgs a, const float
     uint8_t *act = smem + (size_t)jw * q4_act_bytes(nb);
     float *dots = (float *)(smem + (size_t)k * q4_act_bytes(nb));  // [k][16]
     const float *x = a.x + (size_t)slot * a.ldx;
-    XQuant<1, false> xq;
-    q8k_wave_begin(xq, x, nullptr, nb, 0, nb);
+    XQuant<1> xq;
+    q8k_wave_begin(xq, x, nb);
     const int bl = nb - 1;
     RbW ring[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) rb_load<TYPE>(T0 + (size_t)min(r, bl) * bstride, lane, ring[r], r < nb);
-    q8k_wave_finish(xq, x, nullptr, nb, 0, nb, act);
+    q8k_wave_finish(xq, x, nb, act);
     const RbLane ln = rb_lane(lane);
     float acc = 0.0f, acc2 = 0.0f, macc = 0.0f;
     auto step = [&](const RbW &w, int b) {
@@ -720,7 +693,7 @@ size_t q4k_moe_down_lds(int nb, int k) { return (size_t)k * q4_act_bytes(nb) + (
 
 hipError_t launch_q4k_moe_down(int type, const MvArgs &a, const float *wts, int k, int ntok, hipStream_t s) {
     const size_t lds = q4k_moe_down_lds(a.nb, k);
-    if (!a.sel || !a.x || a.xu || k < 1 || k > 8 || ntok < 1 || lds > GEMM_LDS_MAX || a.t[0].gpm < 1)
+    if (!a.sel || !a.x || k < 1 || k > 8 || ntok < 1 || lds > GEMM_LDS_MAX || a.t[0].gpm < 1)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)a.t[0].gpm, (unsigned)ntok);
     if (type == T_Q5_K) q4k_moe_down_kernel<4, T_Q5_K><<<grid, 64 * k, lds, s>>>(a, wts, k);

@@ -191,8 +191,9 @@ FGH_API int fgh_matvec_multi_dev(fgh_ctx *ctx, int n, const fgh_tensor *const *t
 /* The dense SiLU FFN's down projection, y = t * Q8(h) with h[i] = silu(g[i]) * u[i] (g, u: the
  * gate and up outputs, t->cols values each): replaces forward's loop
  * `gate[i] = silu_f(gate[i]) * up[i]` followed by matvec(ffn_down, gate) (4874-4877, silu_f
- * 3118), with h formed while the launch quantizes it (never stored). Same results bit for bit as
- * that loop followed by fgh_matvec_dev. */
+ * 3118): one short launch forms h in the context's scratch (t->cols floats; like all scratch, it
+ * must have its size from an eager call before a graph capture uses it), then the matvec. Same
+ * results bit for bit as that loop followed by fgh_matvec_dev. */
 FGH_API int fgh_matvec_silu_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *g_dev, const float *u_dev,
                         float *y_dev);
 FGH_API int fgh_matmul_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *X_dev, int ldx, float *Y_dev,
