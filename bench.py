@@ -471,13 +471,18 @@ def main() -> int:
                                                  [yd["gate"], yd["up"]]), GATE_UP_BYTES),
         "down": (lambda i: be.matvec_dev(rot["down"][i % len(rot["down"])], xd["h"], yd["down"]),
                  algo_bytes(4096, 14336)),
+        # gate and up paired in one launch that writes h = silu(g) * u (the loop between the FFN's
+        # matvecs), for callers that chain the layer on the device; not part of the layer above,
+        # which runs the reference's launches
+        "gate+up+silu": (lambda i: be.matvec_gate_up_silu_dev(rot["gate"][i % ngu], rot["up"][i % ngu], xd["x2"],
+                                                             yd["gate"]), GATE_UP_BYTES),
     }
     kernels = {}
     for n, (fn, nbytes) in launches.items():
         us = kernel_time(fn, args.kernel_reps)
         gbs = nbytes / (us * 1e-6) / 1e9
         kernels[n] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                      "rotation_MB": round(nbytes * (ngu if n == "gate+up" else len(rot[n])) / 1e6)}
+                      "rotation_MB": round(nbytes * (ngu if n.startswith("gate+up") else len(rot[n])) / 1e6)}
     # the same byte count read by a plain streaming kernel (fgh_checksum_dev: 16-byte loads, four in
     # flight per thread, a sum and nothing else), rotating over at least 1 GB of buffers: the read
     # rate this box delivers to a simple stream, beside the 8 TB/s peak

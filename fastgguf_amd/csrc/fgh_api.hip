@@ -553,6 +553,51 @@ int fgh_matvec_silu_dev(fgh_ctx *c, const fgh_tensor *t, const float *g, const f
     return matvec_launch(c, 1, &t, h, t->cols, yy, t->rows * t->n_mats, 1, nullptr, nullptr);
 }
 
+int fgh_matvec_gate_up_silu_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, const float *x, float *h) {
+    int rc;
+    if ((rc = check_tensor(c, gate)) || (rc = check_tensor(c, up))) return rc;
+    if (!x || !h) return fail(c, FGH_ERR_ARG, "matvec_gate_up_silu: null pointer");
+    if (gate->cols != up->cols || gate->rows != up->rows || gate->n_mats != 1 || up->n_mats != 1)
+        return fail(c, FGH_ERR_ARG, "matvec_gate_up_silu: gate and up must be single matrices of one shape");
+    INJECT(c);
+    HIP_TRY(c, hipSetDevice(c->device));
+    const int64_t rows = gate->rows;
+    if (q16_rows(gate->type) && gate->type == up->type && gate->order == up->order) {
+        // one launch: a workgroup holds gate and up tiles of the same rows and writes their h
+        fgh::MvArgs a;
+        memset(&a, 0, sizeof(a));
+        a.t[0] = fgh::MvT{gate->dev, h, rows, gate->gpm, 0};
+        a.t[1] = fgh::MvT{up->dev, nullptr, rows, up->gpm, gate->gpm};
+        a.nt = 2;
+        a.groups = gate->gpm + up->gpm;
+        a.x = x;
+        a.ldx = gate->cols;
+        a.ldy = rows;
+        a.nb = gate->nb;
+        a.ntile = gate->ntile;
+        a.xdiv = 1;
+        a.pair = 1;
+        HIP_TRY(c, fgh::launch_matvec2((int)gate->type, gate->order, a, 1, c->num_cu, c->stream));
+        return FGH_OK;
+    }
+    // other types: g into h and u into scratch (one launch when their type and order agree),
+    // then h = silu(h) * u
+    if ((rc = grow(c, c->h, (size_t)rows * 4))) return rc;
+    float *u = (float *)c->h.p;
+    if (gate->type == up->type && gate->order == up->order) {
+        const fgh_tensor *gu[2] = {gate, up};
+        float *ys[2] = {h, u};
+        if ((rc = matvec_launch(c, 2, gu, x, gate->cols, ys, rows, 1, nullptr, nullptr))) return rc;
+    } else {
+        float *yg[1] = {h}, *yu[1] = {u};
+        if ((rc = matvec_launch(c, 1, &gate, x, gate->cols, yg, rows, 1, nullptr, nullptr)) ||
+            (rc = matvec_launch(c, 1, &up, x, up->cols, yu, rows, 1, nullptr, nullptr)))
+            return rc;
+    }
+    HIP_TRY(c, fgh::launch_silu_mul(h, u, h, rows, c->stream));
+    return FGH_OK;
+}
+
 int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, float *Y, int ldy, int nb) {
     int rc = check_tensor(c, t);
     if (rc) return rc;

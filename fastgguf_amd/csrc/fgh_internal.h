@@ -221,7 +221,10 @@ struct MvArgs {
     int32_t *sel_out;
     float *w_out;
     uint32_t route_off;
+    // the same pairing of gate (t[0]) and up (t[1]) without routing: h = silu(g) * u to t[0].y
+    int pair;
 };
+enum { MV_PLAIN = 0, MV_PAIR = 1, MV_ROUTE = 2 };  // decode kernel forms (Q4_K / Q5_K)
 size_t matvec_lds_bytes(int type, int order, int nb);  // every type (fgh_matvec.hip)
 // the launch shape a decode launch of `tiles` row tiles (over all tokens) picks: S wavefronts per
 // tile, ring depth R, TPW tiles per workgroup, its dynamic LDS bytes (S == 0: no kernel)

@@ -326,8 +326,9 @@ __device__ __forceinline__ int q4_tensor_of(const MvArgs &a, int64_t g) {
 
 // Decode matvec. Workgroup = TPW tiles x S wavefronts per tile (wavefront ks of a tile takes its
 // ks-th run of ceil(nb / S) blocks); grid = (tiles over all tensors / TPW, tokens).
-template <int ORDER, int R, int TPW, int S, bool DUMP, int TYPE = T_Q4_K, bool ROUTE = false>
+template <int ORDER, int R, int TPW, int S, bool DUMP, int TYPE = T_Q4_K, int MODE = MV_PLAIN>
 __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
+    constexpr bool PAIR = MODE != MV_PLAIN, ROUTE = MODE == MV_ROUTE;
     static_assert(TYPE == T_Q4_K || ORDER == 0, "Q5_K runs the row order");
     constexpr int WPG = TPW * S;
     extern __shared__ __align__(16) uint8_t smem[];
@@ -337,13 +338,13 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
     const int j = lane & 3, rr = lane >> 2;
     const int nb = a.nb;
     const int tok = blockIdx.y;
-    // ROUTE: the workgroup holds TPW / 2 row tiles of gate (a.t[0]) and up (a.t[1]), tile slots
+    // PAIR: the workgroup holds TPW / 2 row tiles of gate (a.t[0]) and up (a.t[1]), tile slots
     // 2 i (gate) and 2 i + 1 (up) over the same rows, and writes h = silu(g) * u of them
     int64_t tile;
     bool live;
     int ti;
     uint32_t lt, gpm;
-    if (ROUTE) {
+    if (PAIR) {
         gpm = (uint32_t)a.t[0].gpm;
         const uint32_t rt = blockIdx.x * (TPW / 2) + (ts >> 1);
         live = rt < gpm;
@@ -515,8 +516,8 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
         out = ORDER == 1 ? acc - macc : rb_row_final(acc, acc2, macc);
     }
     const bool store = has && live && mrow + row < rows;
-    if (ROUTE) {
-        // gate tile -> LDS (the routing buffers are free: every wavefront routed before the
+    if (PAIR) {
+        // gate tile -> LDS (with routing, its buffers are free: every wavefront routed before the
         // barrier after the quantization); up tile: h = silu(g) * u (silu_f, fastgguf.c:3118)
         float *pg = (float *)(smem + a.route_off) + (ts >> 1) * RB_ROWS;
         if (ti == 0 && has) pg[row] = out;
@@ -538,7 +539,11 @@ static hipError_t q4_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s
         return hipGetLastError();
     }
     if (a.logits) {
-        q4k_mv_kernel<ORDER, R, TPW, S, false, TYPE, true><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+        q4k_mv_kernel<ORDER, R, TPW, S, false, TYPE, MV_ROUTE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
+        return hipGetLastError();
+    }
+    if (a.pair) {
+        q4k_mv_kernel<ORDER, R, TPW, S, false, TYPE, MV_PAIR><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
         return hipGetLastError();
     }
     q4k_mv_kernel<ORDER, R, TPW, S, false, TYPE><<<dim3(wg, ntok), 64 * TPW * S, lds, s>>>(a);
@@ -585,12 +590,14 @@ MvShape q4k_matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu)
     return MvShape{S, R, q4_tpw(S), q4_lds(order, nb, q4_tpw(S), S)};
 }
 
-// with routing: each wavefront's routing buffer after the activations and records
+// paired launches: after the activations and records, with routing each wavefront's routing
+// buffer, without it the gate tiles' rows
 static uint32_t q4_route_off(const MvShape &sh) { return (uint32_t)((sh.lds + 15) & ~(size_t)15); }
 static size_t q4_route_lds(const MvShape &sh) { return q4_route_off(sh) + (size_t)sh.S * sh.TPW * 64 * MOE_EPL * 4; }
+static size_t q4_pair_lds(const MvShape &sh) { return q4_route_off(sh) + (size_t)sh.TPW / 2 * RB_ROWS * 4; }
 
-// the routing launch pairs gate and up tiles inside a workgroup: at most 2 wavefronts per tile
-static MvShape q4_route_shape(int type, int order, int64_t tiles, int nb, int num_cu) {
+// paired launches hold gate and up tiles in one workgroup: at most 2 wavefronts per tile
+static MvShape q4_pair_shape(int type, int order, int64_t tiles, int nb, int num_cu) {
     MvShape sh = q4k_matvec_shape(type, type == T_Q5_K ? 0 : order, tiles, nb, num_cu);
     if (sh.S > 2) {
         sh.S = 2;
@@ -601,25 +608,28 @@ static MvShape q4_route_shape(int type, int order, int64_t tiles, int nb, int nu
 }
 
 bool q4k_route_fits(int type, int order, int64_t tiles, int nb, int num_cu) {
-    const MvShape sh = q4_route_shape(type, order, tiles, nb, num_cu);
+    const MvShape sh = q4_pair_shape(type, order, tiles, nb, num_cu);
     return sh.lds <= (sh.S == 1 ? (size_t)65536 : GEMM_LDS_MAX) && q4_route_lds(sh) <= GEMM_LDS_MAX;
 }
 
 hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
     if (type == T_Q5_K) order = 0;
-    const MvShape sh = a.logits ? q4_route_shape(type, order, a.groups * ntok, a.nb, num_cu)
-                                : q4k_matvec_shape(type, order, a.groups * ntok, a.nb, num_cu);
+    const bool pair = a.logits || a.pair;
+    const MvShape sh = pair ? q4_pair_shape(type, order, a.groups * ntok, a.nb, num_cu)
+                            : q4k_matvec_shape(type, order, a.groups * ntok, a.nb, num_cu);
     if (sh.lds > (sh.S == 1 ? (size_t)65536 : GEMM_LDS_MAX)) return hipErrorInvalidValue;
     MvArgs b = a;
     size_t lds = sh.lds;
-    if (a.logits) {  // gate and up of the selected experts, h = silu(g) * u into a.t[0].y
-        if (a.sel || !a.sel_out || !a.w_out || a.n_expert < 1 || a.n_expert > 64 * MOE_EPL || a.xdiv < 1 ||
-            a.xdiv > a.n_expert || a.xdiv > 64 || ntok % a.xdiv || q4_route_lds(sh) > GEMM_LDS_MAX || a.nt != 2 ||
-            a.t[0].gpm != a.t[1].gpm || a.t[0].rows != a.t[1].rows || a.dump_s)
+    if (pair) {  // gate and up (of the selected experts), h = silu(g) * u into a.t[0].y
+        if (a.nt != 2 || a.t[0].gpm != a.t[1].gpm || a.t[0].rows != a.t[1].rows || a.dump_s)
+            return hipErrorInvalidValue;
+        if (a.logits && (a.sel || !a.sel_out || !a.w_out || a.n_expert < 1 || a.n_expert > 64 * MOE_EPL ||
+                         a.xdiv < 1 || a.xdiv > a.n_expert || a.xdiv > 64 || ntok % a.xdiv))
             return hipErrorInvalidValue;
         b.route_off = q4_route_off(sh);
         b.groups = 2 * a.t[0].gpm;  // TPW / 2 row tiles per workgroup
-        lds = q4_route_lds(sh);
+        lds = a.logits ? q4_route_lds(sh) : q4_pair_lds(sh);
+        if (lds > GEMM_LDS_MAX) return hipErrorInvalidValue;
     }
     if (type == T_Q5_K) return q4_launch_s<0, T_Q5_K>(sh.S, sh.R, b, ntok, lds, s);
     if (order == 0) return q4_launch_s<0, T_Q4_K>(sh.S, sh.R, b, ntok, lds, s);

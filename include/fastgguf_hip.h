@@ -196,6 +196,16 @@ FGH_API int fgh_matvec_multi_dev(fgh_ctx *ctx, int n, const fgh_tensor *const *t
  * results bit for bit as that loop followed by fgh_matvec_dev. */
 FGH_API int fgh_matvec_silu_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *g_dev, const float *u_dev,
                         float *y_dev);
+/* The dense SiLU FFN's gate and up projections and the loop between them and the down
+ * projection: h[i] = silu_f(gate[i] . Q(x)) * (up[i] . Q(x)) (forward 4870-4876: matvec_multi of
+ * ffn_gate and ffn_up, then `gate[i] = silu_f(gate[i]) * up[i]`), gate->rows values to h_dev;
+ * gate and up: single matrices of one shape. Q4_K / Q5_K tensors of one type and order take one
+ * launch (a workgroup holds gate and up tiles of the same rows, so g and u are never stored);
+ * other types run the matvecs, then a short silu launch (with the context's scratch, which must
+ * have its size from an eager call before a graph capture uses it). Same results bit for bit as
+ * fgh_matvec_multi_dev followed by that loop; h_dev then feeds fgh_matvec_dev(ffn_down). */
+FGH_API int fgh_matvec_gate_up_silu_dev(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tensor *up,
+                                const float *x_dev, float *h_dev);
 FGH_API int fgh_matmul_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *X_dev, int ldx, float *Y_dev,
                    int ldy, int nb);
 /* fgh_matmul_dev without any device allocation. No counterpart in the reference: it is for

@@ -3,17 +3,18 @@
 The decode launchers choose a launch shape per call from the row tiles of the launch, the row
 width and the device's compute units: S wavefronts per tile (a block split for short matrices),
 a register ring of R steps, TPW tiles per workgroup. Each (type, order, S, R) is a separate kernel
-instantiation, and so are its integer-dump and fused-silu forms. fgh_matvec_shape reports the
-shape a call would take (the same function the launchers call), so these tests
+instantiation, and so is its integer-dump form. fgh_matvec_shape reports the shape a call would
+take (the same function the launchers call), so these tests
 
   1. scan row widths and tile counts to find every shape each weight type and order can take, and
   2. run, for each reachable shape, the smallest tensor that takes it: the matvec bit for bit
      against the oracle's restatement of the reference kernel (dot_q4Kx8 / dot_q4_K_q8k /
      dot_q6_K_q8k / dot_q8_0_q8 / ... orders), its per-block integers (the dump form) against the
-     oracle's, and the fused silu form bit for bit against the same matvec of silu(g) * u.
+     oracle's, and the silu entry (a short silu launch, then the same kernel) bit for bit
+     against the same matvec of silu(g) * u.
 
 The benchmark's dominant launch (gate and up 4096 -> 14336 in one matvec_multi, both orders) is
-tested at its own size as well.
+tested at its own size as well, and so is the paired gate / up form that writes h = silu(g) * u.
 """
 import numpy as np
 import pytest
@@ -85,7 +86,7 @@ def test_every_launch_shape_bit_exact(backend, oracle, fam):
         for row in sorted({0, 1, rows // 2, rows - 1}):
             os_, om = oracle.block_ints(t, w[row], act)
             assert np.array_equal(si[row], os_) and np.array_equal(mi[row], om), f"ints S={s} R={r} row {row}"
-        # the fused silu form of the same shape
+        # the silu entry on the same shape
         g = S.activations(cols, seed + 2) * np.float32(2.0)
         u = S.activations(cols, seed + 3)
         h = (g / (np.float32(1.0) + oracle.libm_expf(-g)) * u).astype(np.float32)
@@ -115,3 +116,35 @@ def test_gate_up_one_launch_at_benchmark_size(backend, oracle, order):
         assert bits_equal(yu, oracle.matvec(S.T_Q4_K, wu, cols, x, o_order))
     tg.free()
     tu.free()
+
+
+GATE_UP_CASES = [  # type, order, rows, cols: one tile pair to the benchmark shape, odd tile counts,
+    # the split (2 wavefronts per tile) and unsplit forms; Q6_K / Q8_0: matvecs then the silu launch
+    (S.T_Q4_K, ORDER_REPACKED, 14336, 4096), (S.T_Q4_K, ORDER_ROW, 14336, 4096),
+    (S.T_Q4_K, ORDER_REPACKED, 16, 256), (S.T_Q4_K, ORDER_REPACKED, 48, 4096), (S.T_Q4_K, ORDER_ROW, 208, 14336),
+    (S.T_Q4_K, ORDER_REPACKED, 3200, 512), (S.T_Q5_K, ORDER_ROW, 1040, 2048), (S.T_Q5_K, ORDER_ROW, 7168, 768),
+    (S.T_Q6_K, ORDER_ROW, 1000, 2048), (S.T_Q8_0, ORDER_ROW, 1000, 4096),
+]
+
+
+@pytest.mark.parametrize("case", GATE_UP_CASES, ids=lambda c: f"{S.TYPE_NAME[c[0]]}_{c[1]}_{c[2]}x{c[3]}")
+def test_gate_up_silu_bit_exact(backend, oracle, case):
+    """fgh_matvec_gate_up_silu_dev: h = silu_f(g) * u with g, u the gate and up matvecs (forward,
+    fastgguf.c:4870-4876), bit for bit against the oracle's matvecs followed by the reference's
+    loop (libm expf, fp32), and against fgh_matvec_multi followed by the same loop."""
+    t, order, rows, cols = case
+    wg = S.random_bytes_weights(t, rows, cols, 700 + rows)
+    wu = S.random_bytes_weights(t, rows, cols, 701 + rows)
+    x = S.activations(cols, 702) * np.float32(2.0)
+    tg = backend.upload(t, cols, wg, order=order)
+    tu = backend.upload(t, cols, wu, order=order)
+    o_order = O_RP if order == ORDER_REPACKED else O_ROW
+    g = oracle.matvec(t, wg, cols, x, o_order)
+    u = oracle.matvec(t, wu, cols, x, o_order)
+    want = (g / (np.float32(1.0) + oracle.libm_expf(-g)) * u).astype(np.float32)
+    h = backend.matvec_gate_up_silu(tg, tu, x)
+    assert bits_equal(h, want)
+    gm, um = backend.matvec_multi([tg, tu], x)
+    assert bits_equal(gm, g) and bits_equal(um, u)
+    for tt in (tg, tu):
+        tt.free()
