@@ -497,6 +497,16 @@ def main() -> int:
                       "us": round(rus, 3), "GB/s": round(rgbs, 1), "frac": round(rgbs / HBM_PEAK_GBS, 4),
                       "rotation_MB": round(nr * rbytes / 1e6)}
 
+    # the int8 MFMA rate a kernel that runs nothing but MFMA chains gets on this box: the attainable
+    # peak beside the published 5.0 POPS (fgh_mfma_peak_dev, 2000 rounds per launch)
+    mops = be.mfma_peak_dev(2000)
+    mus = kernel_time(lambda i: be.mfma_peak_dev(2000), 40)
+    mtops = mops / (mus * 1e-6) / 1e12
+    mfma_reference = {"kernel": "mfma_peak_kernel (8 independent v_mfma_i32_16x16x64_i8 chains per wavefront, "
+                                "8 wavefronts per compute unit, no memory traffic)",
+                      "ops": mops, "us": round(mus, 3), "TOPS": round(mtops, 1),
+                      "frac": round(mtops / INT8_PEAK_TOPS, 4)}
+
     g = kernels["gate+up"]
     roofline = {"bound": "hbm", "achieved": g["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g["frac"],
                 "traffic": counted_traffic("gate_up"),
@@ -519,7 +529,8 @@ def main() -> int:
     for kind, pick in (("cold", lambda i: mats[i % len(mats)]), ("hot", lambda i: mats[0])):
         us = kernel_time(lambda i: be.matmul_dev(pick(i), xpd, ypd, T), args.kernel_reps)
         tops = ops / (us * 1e-6) / 1e12
-        prefill[kind] = {"us": round(us, 3), "TOPS": round(tops, 2), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+        prefill[kind] = {"us": round(us, 3), "TOPS": round(tops, 2), "frac": round(tops / INT8_PEAK_TOPS, 4),
+                         "frac_of_mfma_reference": round(tops / mtops, 4)}
     wq4 = 14336 * 16 * 144
     prefill.update({"workload": "cfg4: 64 tokens x K=4096 -> N=14336, Q4_K x Q8_K (quantization of X included)",
                     "ops_per_launch": ops, "peak_TOPS": INT8_PEAK_TOPS,
@@ -572,6 +583,7 @@ def main() -> int:
                    "device": info["name"], "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
         "read_reference": read_reference,
+        "mfma_reference": mfma_reference,
         "cpu_baseline": cpu,
         "kernels": kernels,
         "prefill": prefill,

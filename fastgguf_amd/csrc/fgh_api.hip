@@ -986,6 +986,17 @@ int fgh_checksum_dev(fgh_ctx *c, const void *src, uint64_t bytes, uint32_t *out)
     return FGH_OK;
 }
 
+int fgh_mfma_peak_dev(fgh_ctx *c, int iters, uint64_t *ops) {
+    if (!c) return FGH_ERR_ARG;
+    if (iters < 1 || iters > (1 << 20) || !ops) return fail(c, FGH_ERR_ARG, "mfma_peak_dev: iters 1..2^20 and ops");
+    HIP_TRY(c, hipSetDevice(c->device));
+    int rc;
+    if ((rc = grow(c, c->ck, (size_t)fgh::mfma_peak_blocks(c->num_cu) * 4))) return rc;
+    HIP_TRY(c, fgh::launch_mfma_peak(iters, (uint32_t *)c->ck.p, c->num_cu, c->stream));
+    *ops = fgh::mfma_peak_ops(c->num_cu, iters);
+    return FGH_OK;
+}
+
 int fgh_sync(fgh_ctx *c) {
     if (!c) return FGH_ERR_ARG;
     NO_CAPTURE(c);

@@ -419,6 +419,10 @@ __device__ __forceinline__ int moe_route_wave(const float *__restrict__ lg, int 
 }
 
 hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s);  // test hook
+// the MFMA-only rate probe (fgh_kernels.hip): launch, its workgroups, int8 ops per launch
+int mfma_peak_blocks(int num_cu);
+uint64_t mfma_peak_ops(int num_cu, int iters);
+hipError_t launch_mfma_peak(int iters, uint32_t *sink, int num_cu, hipStream_t s);
 // h = silu(g) * u over n values (silu_f, fastgguf.c:3118); h may be g
 hipError_t launch_silu_mul(const float *g, const float *u, float *h, int64_t n, hipStream_t s);
 hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok, int32_t *sel, float *w, hipStream_t s);

@@ -283,6 +283,36 @@ hipError_t launch_checksum(const void *src, int64_t n16, uint32_t *part, int npa
     return hipGetLastError();
 }
 
+// The int8 MFMA rate the box delivers to a kernel that does nothing else: every wavefront runs
+// `iters` rounds of 8 independent v_mfma_i32_16x16x64_i8 chains (operands in registers, no memory
+// traffic); a result reaches memory only if its sum equals `magic`, so none of the work can be
+// dropped. Two workgroups of 4 wavefronts per compute unit.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, uint32_t magic, uint32_t *__restrict__ sink) {
+    const int t = threadIdx.x;
+    v4i_t a = {t, t + 1, t + 2, (int)magic}, b = {3 * t, 1, 2, 3};
+    v4i_t c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = v4i_t{0, 0, 0, 0};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c[j], 0, 0, 0);
+        a.x += it;
+    }
+    uint32_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += (uint32_t)(c[j][0] + c[j][1] + c[j][2] + c[j][3]);
+    if (sum == magic) sink[blockIdx.x] = sum;
+}
+int mfma_peak_blocks(int num_cu) { return 2 * num_cu; }
+uint64_t mfma_peak_ops(int num_cu, int iters) {
+    return (uint64_t)mfma_peak_blocks(num_cu) * 4 * (uint64_t)iters * 8 * (2 * 16 * 16 * 64);
+}
+hipError_t launch_mfma_peak(int iters, uint32_t *sink, int num_cu, hipStream_t s) {
+    mfma_peak_kernel<<<mfma_peak_blocks(num_cu), 256, 0, s>>>(iters, 0x9E3779B9u, sink);
+    return hipGetLastError();
+}
+
 hipError_t launch_fp16(const uint16_t *h, float *out, int n, hipStream_t s) {
     fp16_kernel<<<(n + 255) / 256, 256, 0, s>>>(h, out, n);
     return hipGetLastError();

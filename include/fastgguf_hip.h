@@ -272,6 +272,14 @@ FGH_API int fgh_copy_d2d(fgh_ctx *ctx, void *dst_dev, const void *src_dev, uint6
  * per-workgroup parts stay in the context). No counterpart in the reference (device-side helper).
  * The first call allocates a small part buffer: make it once before graph capture. */
 FGH_API int fgh_checksum_dev(fgh_ctx *ctx, const void *src_dev, uint64_t bytes, uint32_t *out_dev);
+/* The int8 MFMA rate this device delivers to a kernel that runs nothing but MFMA: one launch, on
+ * the context stream, of 8 independent v_mfma_i32_16x16x64_i8 chains per wavefront for `iters`
+ * rounds over two 4-wavefront workgroups per compute unit (no memory traffic); *ops receives the
+ * int8 operations (2 per multiply-add) the launch performs, to divide by its timed duration. The
+ * attainable peak the prompt GEMM is compared against, beside the published one. No counterpart
+ * in the reference. Shares the small part buffer of fgh_checksum_dev (make one call before a
+ * graph capture). */
+FGH_API int fgh_mfma_peak_dev(fgh_ctx *ctx, int iters, uint64_t *ops);
 FGH_API int fgh_sync(fgh_ctx *ctx);
 /* HIP events recorded on the context stream */
 FGH_API int fgh_event_create(fgh_ctx *ctx, void **ev);
