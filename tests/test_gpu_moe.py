@@ -117,11 +117,13 @@ def test_moe_matches_oracle(backend, oracle, E, K, D, F, T):
         t.free()
 
 
-@pytest.mark.parametrize("E,K,T", [(200, 8, 1), (512, 8, 1), (96, 10, 1), (70, 1, 1), (200, 8, 3)])
-def test_moe_routing_shapes(backend, oracle, E, K, T):
+@pytest.mark.parametrize("E,K,T,D,F", [(200, 8, 1, 256, 256), (512, 8, 1, 256, 256), (96, 10, 1, 256, 256),
+                                       (70, 1, 1, 256, 256), (200, 8, 3, 256, 256), (32, 4, 1, 2048, 256),
+                                       (16, 2, 2, 4096, 512)])
+def test_moe_routing_shapes(backend, oracle, E, K, T, D, F):
     """Expert counts that fill several 64-expert slots of a wavefront (and 512, the most), k above
-    the 8 experts the fused down launch takes (the separate routing launch), and k = 1."""
-    D, F = 256, 256
+    the 8 experts the fused down launch takes (the separate routing launch), k = 1, and long rows
+    over few tiles, where the routing launch splits each tile's blocks over two wavefronts."""
     gw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 400 + E)
     uw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 401 + E)
     dw = S.random_bytes_weights(S.T_Q4_K, E * D, F, 402 + E)
