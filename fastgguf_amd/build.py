@@ -28,8 +28,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libfastgguf_hip.so")
-SOURCES = ["fgh_api.hip", "fgh_kernels.hip", "fgh_matvec.hip", "fgh_q4k.hip", "fgh_gemm.hip", "fgh_gemm32.hip", "fgh_gemm6.hip", "fgh_moe.hip",
-           "fgh_gguf.hip", "fgh_attn.hip", "fgh_kvq.hip"]
+SOURCES = ["fgh_api.hip", "fgh_kernels.hip", "fgh_matvec.hip", "fgh_q4k.hip", "fgh_gemm.hip", "fgh_gemm32.hip",
+           "fgh_gemm32n.hip", "fgh_gemm6.hip", "fgh_moe.hip", "fgh_gguf.hip", "fgh_attn.hip", "fgh_kvq.hip"]
+# per-source additions: the nibble-type GEMM converts every MFMA result with a VALU instruction, so
+# its results go to VGPRs (without the flag the compiler writes them to AGPRs and copies each out)
+FILE_FLAGS = {"fgh_gemm32n.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 
@@ -39,11 +42,6 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
              "-dot4-insts", "-Wall", "-Wno-unused-function", "-fvisibility=hidden",
              "-I", os.path.join(ROOT, "include")]
 _NOISE = ("packed-fp32-ops", "dot6-insts", "dot4-insts")
-
-
-def hipcc_cmd(out: str = LIB) -> list[str]:
-    """The whole library in one hipcc call (the same flags as build()'s per-file compiles)."""
-    return [HIPCC] + HIP_FLAGS + ["-shared", "-Wl,-z,defs", "-o", out] + [os.path.join(CSRC, s) for s in SOURCES]
 
 
 def _run(cmd: list[str]) -> tuple[int, str]:
@@ -59,7 +57,8 @@ def build(verbose: bool = True, jobs: int | None = None) -> str:
     odir = os.path.join(HERE, "_build")
     os.makedirs(odir, exist_ok=True)
     objs = [os.path.join(odir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
-    cmds = [[HIPCC] + HIP_FLAGS + ["-c", "-o", o, os.path.join(CSRC, s)] for s, o in zip(SOURCES, objs)]
+    cmds = [[HIPCC] + HIP_FLAGS + FILE_FLAGS.get(s, []) + ["-c", "-o", o, os.path.join(CSRC, s)]
+            for s, o in zip(SOURCES, objs)]
     if verbose:
         print(" ".join(cmds[0][:-3]) + " -c <each source>", flush=True)
     jobs = jobs or min(len(cmds), max(1, int(os.environ.get("MAX_JOBS", "0")) or (os.cpu_count() or 4)))

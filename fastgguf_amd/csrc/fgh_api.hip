@@ -270,6 +270,37 @@ static int gemm_q80_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_
     return FGH_OK;
 }
 
+// the prompt GEMM for a Q4_0 / Q4_1 / Q5_0 / Q5_1 tensor (gemm_q32, fastgguf.c:2856-2999, in its fp32
+// order): Q8 records of T tokens, then one MFMA launch on the decode tiles; ds: optional
+// [T][rows * n_mats][nb] dump of the unsigned-weight integers sum u * xq
+static int gemm_q32n_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
+                          uint8_t *act, int32_t *ds) {
+    const int Tp = (T + 15) / 16 * 16;
+    HIP_TRY(c, fgh::launch_gemmn_quant(X, ldx, t->nb, T, Tp, act, c->stream));
+    fgh::GemmNArgs a;
+    memset(&a, 0, sizeof(a));
+    a.W = t->dev;
+    a.Y = Y;
+    a.rows = t->rows;
+    a.tpm = t->gpm;
+    a.ppm = (t->gpm + 1) / 2;
+    a.groups = a.ppm * t->n_mats;
+    a.nrows = t->rows * t->n_mats;
+    a.nb = t->nb;
+    a.nsteps = t->ntile;
+    a.act = act;
+    a.Tp = Tp;
+    a.T = T;
+    a.ldy = ldy;
+    a.dump_s = ds;
+    a.type = (int)t->type;
+    HIP_TRY(c, fgh::launch_q32n_gemm(a, c->stream));
+    return FGH_OK;
+}
+static bool q32n_type(uint32_t type) {
+    return type == FGH_T_Q4_0 || type == FGH_T_Q4_1 || type == FGH_T_Q5_0 || type == FGH_T_Q5_1;
+}
+
 // the prompt GEMM for a Q6_K tensor (gemm_kquant's Q6_K branch, fastgguf.c:2704-2725, 2818-2854):
 // Q8_K records of T tokens, then one MFMA launch on the decode tiles; ds / dm: optional
 // [T][rows * n_mats][nb] integer dump
@@ -304,6 +335,7 @@ static size_t prompt_gemm_bytes(const fgh_tensor *t, int T) {
     if (t->type == FGH_T_Q4_K) return fgh::gemm_act_bytes(t->nb, (T + 15) / 16 * 16);
     if (t->type == FGH_T_Q8_0) return fgh::gemm32_act_bytes(t->nb, T <= 32 ? 32 : 64);
     if (t->type == FGH_T_Q6_K) return fgh::gemm6_act_bytes(t->nb, (T + 15) / 16 * 16);
+    if (q32n_type(t->type)) return fgh::gemmn_act_bytes(t->nb, (T + 15) / 16 * 16);
     return 0;
 }
 // the prompt GEMM with its records in act (at least prompt_gemm_bytes)
@@ -311,6 +343,7 @@ static int prompt_gemm_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int
                             int T, uint8_t *act, int32_t *ds, int32_t *dm) {
     if (t->type == FGH_T_Q8_0) return gemm_q80_into(c, t, X, ldx, Y, ldy, T, act, ds);
     if (t->type == FGH_T_Q6_K) return gemm_q6k_into(c, t, X, ldx, Y, ldy, T, act, ds, dm);
+    if (q32n_type(t->type)) return gemm_q32n_into(c, t, X, ldx, Y, ldy, T, act, ds);
     return gemm_q4k_into(c, t, X, ldx, Y, ldy, T, act, ds, dm);
 }
 static int prompt_gemm(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
@@ -605,9 +638,9 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
         return fail(c, FGH_ERR_ARG, "matmul: bad arguments");
     INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
-    // nb >= 8: the prompt GEMM (matmul 3018-3031) on int8 MFMA for Q4_K, Q6_K and Q8_0; the other types
-    // run the per-token decode kernels (their fp32 orders differ from the reference's GEMM orders
-    // only by rounding)
+    // nb >= 8: the prompt GEMMs (matmul 3018-3031) on int8 MFMA for Q4_K, Q6_K, Q8_0 and the nibble
+    // types Q4_0 / Q4_1 / Q5_0 / Q5_1; Q5_K and IQ4_NL, which have no GEMM in the reference, run the
+    // per-token decode kernels as its matmul does
     if (prompt_gemm_bytes(t, nb)) return prompt_gemm(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
     float *ys[1] = {Y};
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
@@ -1147,8 +1180,8 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     NO_CAPTURE(c);
     if (!X || !sumi || !msum || nb < 1 || nb > FG_BATCH || ldx < t->cols)
         return fail(c, FGH_ERR_ARG, "gemm_block_ints: bad arguments");
-    if (t->type != FGH_T_Q4_K && t->type != FGH_T_Q6_K && t->type != FGH_T_Q8_0)
-        return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMMs take Q4_K, Q6_K and Q8_0 tensors");
+    if (!prompt_gemm_bytes(t, 8))
+        return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMMs take Q4_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0 and Q5_1 tensors");
     if (nb < 8) return fail(c, FGH_ERR_ARG, "gemm_block_ints: the prompt GEMM runs 8..64 tokens");
     const int64_t nout = t->rows * t->n_mats;
     const size_t nint = (size_t)nb * nout * t->nb;
@@ -1160,8 +1193,8 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     hipError_t e = hipMemcpy2DAsync(c->x.p, (size_t)t->cols * 4, X, (size_t)ldx * 4, (size_t)t->cols * 4, nb,
                                     hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) {
-        // Q8_0 has no min term: its msum are zeros, as the oracle's
-        if (t->type == FGH_T_Q8_0) e = hipMemsetAsync(dmi, 0, nint * 4, c->stream);
+        // the 32-value types have no min integer: their msum are zeros, as the oracle's
+        if (t->type == FGH_T_Q8_0 || q32n_type(t->type)) e = hipMemsetAsync(dmi, 0, nint * 4, c->stream);
         if (e == hipSuccess) rc = prompt_gemm(c, t, (const float *)c->x.p, t->cols, (float *)c->y.p, nout, nb, dsi, dmi);
         if (!rc) {
             e = hipMemcpyAsync(sumi, dsi, nint * 4, hipMemcpyDeviceToHost, c->stream);

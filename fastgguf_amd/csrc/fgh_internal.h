@@ -524,6 +524,27 @@ hipError_t launch_gemm32_quant(const float *x, int64_t ldx, int nb, int T, int T
 size_t gemm32_act_bytes(int nb, int Tp);
 hipError_t launch_q80_gemm(const Gemm32Args &a, hipStream_t s);
 
+// the prompt GEMM of the nibble types Q4_0 / Q4_1 / Q5_0 / Q5_1 (fgh_gemm32n.hip) on the decode
+// tiles (8-row tiles, 4 blocks per tile step)
+struct GemmNArgs {
+    const uint8_t *W;      // tensor (tile layout)
+    float *Y;              // Y[tok * ldy + row]
+    int64_t rows;          // rows per matrix
+    int64_t tpm;           // 8-row tiles per matrix
+    int64_t ppm;           // 16-row pairs of tiles per matrix, (tpm + 1) / 2
+    int64_t groups;        // pairs over all matrices
+    int64_t nrows;         // rows over all matrices (outputs per token)
+    int nb, nsteps;        // 32-blocks per row, tile steps per row ((nb + 3) / 4)
+    const uint8_t *act;    // activation records from launch_gemmn_quant
+    int Tp, T;             // padded token count (a multiple of 16, Tp - T < 16), tokens
+    int64_t ldy;
+    int32_t *dump_s;       // test hook: [T][nrows][nb] integers sum u * xq, or null
+    int type;
+};
+hipError_t launch_gemmn_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s);
+size_t gemmn_act_bytes(int nb, int Tp);
+hipError_t launch_q32n_gemm(const GemmNArgs &a, hipStream_t s);
+
 // the Q6_K prompt GEMM (fgh_gemm6.hip) on the decode tiles (8-row tiles, one block per tile step)
 struct Gemm6Args {
     const uint8_t *W;      // Q6_K tensor (tile layout)

@@ -292,9 +292,12 @@ FGH_API int fgh_event_destroy(fgh_ctx *ctx, void *ev);
  * n/32 blocks of 40 bytes; FGH_ACT_Q8K: n/256 blocks of 292 bytes), from host x.
  * fgh_block_ints: per (row, block) integer parts of dot(W[r], Q8(x)) as the device kernels
  * compute them: sumi / msum [rows * n_mats][blocks per row] (see the oracle's fgo_block_ints).
- * fgh_gemm_block_ints: the same integers as the prompt GEMMs (Q4_K, Q6_K or Q8_0, nb tokens,
- * 8..64) compute them: sumi / msum [nb][rows * n_mats][blocks per row] (msum zeros for Q8_0), token t
- * from row t of X (stride ldx).
+ * fgh_gemm_block_ints: the same integers as the prompt GEMMs (Q4_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0
+ * or Q5_1, nb tokens, 8..64) compute them: sumi / msum [nb][rows * n_mats][blocks per row], token t
+ * from row t of X (stride ldx). The 32-value types have msum zeros; for Q4_0 / Q4_1 / Q5_0 / Q5_1
+ * sumi is gemm_q32's integer over the unsigned weights (nibble or 5-bit value) times the quants
+ * (fastgguf.c:2876-2894, 2919-2931), i.e. fgh_block_ints' sumi plus 8 (Q4_0) or 16 (Q5_0) times
+ * the block's quant sum.
  * fgh_fp16_to_f32: the device's fp16 -> fp32 decode of n codes.
  * fgh_expf: the device's expf (the MoE softmax and silu) of n values.
  * fgh_matvec_shape: the launch shape a decode launch of `type` (order as fgh_upload resolved it)

@@ -7,15 +7,17 @@ Bar:
     outputs use a different summation order from gemmk_kern, so they are compared with the
     reference's own tolerance: max|y - y_ref| / max|y_ref| <= 1e-5 per token (fastgguf.c:5723-5733),
     against the oracle's restatement of gemm_kquant and against the reference's golden outputs.
-  - Q8_0 runs its int8 MFMA GEMM (one 32-value block per v_mfma_i32_32x32x32_i8): its per-block
-    integers (dot_q8_0_q8's sum of q * xq) bit for bit against the oracle's, its fp32 outputs within
-    the same tolerance of the oracle's GEMM order (gemm_q32).
   - Q6_K runs its int8 MFMA GEMM (three chains over balanced base-8 digits of the scales): its
     per-block integers (dot_q6_K_q8k's sumi over the unsigned quants, and msum) bit for bit
     against the oracle's, its fp32 outputs within the same tolerance of gemm_kquant's order.
-  - Q5_0 runs the per-token decode kernels (dot_q5_0_q8 order): compared with the same tolerance
-    against the GEMM order (gemm_q32).
-  - Q4_0, Q4_1 and Q5_1 run the decode kernels per token too, against gemm_q32 with the same tolerance.
+  - Q8_0 runs its int8 MFMA GEMM (one 32-value block per v_mfma_i32_32x32x32_i8, K split in up to 4
+    parts): its per-block integers (dot_q8_0_q8's sum of q * xq) bit for bit against the oracle's,
+    its fp32 outputs within the same tolerance of the oracle's GEMM order (gemm_q32).
+  - Q4_0, Q4_1, Q5_0 and Q5_1 run the nibble-type MFMA GEMM in gemm_q32's own order (no K split):
+    its per-block integers (gemm_q32's sum of unsigned weight times quant) bit for bit against the
+    oracle's row integers plus offset times the quant sum, and its fp32 outputs bit for bit against
+    the oracle's gemm_q32 and the reference's golden outputs (both orders of Q4_0: the reference's
+    GEMM unpacks the repacked rows to the same values).
   - Q5_K and IQ4_NL have no prompt GEMM in the reference: their matmul is the row kernel per token
     there and here, so they are compared bit for bit.
 """
@@ -53,7 +55,8 @@ def test_matmul_matches_golden(backend, name, t, nb):
         tt = backend.upload(t, X.shape[1], w, order=order)
         Y = backend.matmul(tt, X)
         check_tokens(Y, g[key])
-        if t in (S.T_Q5_K, S.T_IQ4_NL):  # no prompt GEMM in the reference: its row kernel per token
+        # no prompt GEMM in the reference (its row kernel per token), or gemm_q32's own order
+        if t in (S.T_Q5_K, S.T_IQ4_NL, S.T_Q4_0, S.T_Q4_1, S.T_Q5_0, S.T_Q5_1):
             assert bits_equal(Y, g[key])
         tt.free()
 
@@ -127,6 +130,59 @@ def test_q80_prefill_config_shape(backend, oracle):
     check_tokens(backend.matmul(tt, X), oracle.matmul(S.T_Q8_0, w, cols, X, O_ROW))
     check_tokens(backend.matmul(tt, X[:9]), oracle.matmul(S.T_Q8_0, w, cols, X[:9], O_ROW))
     tt.free()
+
+
+# the dumped integer minus the oracle's row integer, in units of the block's quant sum: gemm_q32's
+# unsigned weights are value + 8 (Q4_0) / + 16 (Q5_0)
+Q32N_OFF = {S.T_Q4_0: 8, S.T_Q4_1: 0, S.T_Q5_0: 16, S.T_Q5_1: 0}
+Q32N_CASES = [  # (rows, cols, n_mats, tokens): one token tile (8, 16 tokens), 2 and 3 tiles
+    # (ragged), 4 tiles; a partial last tile step (blocks % 4 != 0); an odd number of 8-row tiles (a
+    # half-empty last pair); ragged rows; 3-D; long rows; launches of ~600 to ~1500 wavefronts, the
+    # last with two token tiles per wavefront
+    (16, 128, 1, 8),
+    (40, 288, 1, 16),       # 9 blocks: 3 tile steps, the last with one block; 5 tiles
+    (100, 416, 1, 31),      # 13 blocks; 13 tiles
+    (21, 1056, 3, 45),      # 33 blocks, 3-D, 3 tiles per matrix
+    (64, 4096, 1, 64),
+    (24, 14336, 1, 33),     # 448 blocks
+    (4792, 160, 1, 32),     # 300 row pairs x 2 token tiles; ragged rows
+    (9600, 96, 1, 32),      # 600 x 2
+    (12288, 256, 1, 64),    # 768 x 2 pairs of token tiles
+]
+
+
+@pytest.mark.parametrize("t", [S.T_Q4_0, S.T_Q4_1, S.T_Q5_0, S.T_Q5_1], ids=["q4_0", "q4_1", "q5_0", "q5_1"])
+@pytest.mark.parametrize("case", Q32N_CASES, ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}_T{c[3]}")
+def test_q32n_gemm_exact(backend, oracle, t, case):
+    rows, cols, n_mats, T = case
+    w = S.random_bytes_weights(t, rows * n_mats, cols, 270 + rows + t)
+    X = S.activations(cols, 271 + T, rows=T) * np.float32(2.0)
+    tt = backend.upload(t, cols, w, rows=rows, n_mats=n_mats)
+    s, m = backend.gemm_block_ints(tt, X)
+    assert not m.any()  # no min integer
+    check_rows = range(rows * n_mats) if rows * n_mats <= 256 else range(0, rows * n_mats, 97)
+    for tok in (0, T // 2, T - 1):
+        act = oracle.quantize_for(t, X[tok])
+        qsum = act["s16"].astype(np.int64).sum(axis=1)
+        for r in check_rows:
+            os_, _ = oracle.block_ints(t, w[r], act)
+            assert np.array_equal(s[tok, r], os_ + Q32N_OFF[t] * qsum), f"sumi token {tok} row {r}"
+    Y = backend.matmul(tt, X)
+    assert bits_equal(Y, oracle.matmul(t, w, cols, X, O_ROW))
+    tt.free()
+
+
+def test_q32n_prefill_config_shape(backend, oracle):
+    """64 tokens x K=4096 -> N=14336 and 14336 -> 4096 (benchmark distributions), Q4_0 and Q5_1,
+    bit for bit with gemm_q32; then 9 tokens (one token tile) reusing the buffers"""
+    for t, seed in ((S.T_Q4_0, 290), (S.T_Q5_1, 291)):
+        for rows, cols in ((14336, 4096), (4096, 14336)):
+            w = S.weights(t, rows, cols, seed)
+            X = S.activations(cols, seed + 1, rows=64)
+            tt = backend.upload(t, cols, w)
+            assert bits_equal(backend.matmul(tt, X), oracle.matmul(t, w, cols, X, O_ROW))
+            assert bits_equal(backend.matmul(tt, X[:9]), oracle.matmul(t, w, cols, X[:9], O_ROW))
+            tt.free()
 
 
 Q6K_CASES = [  # (rows, cols, n_mats, tokens): K-halves 1 (one block) and 2 (odd and even block

@@ -37,9 +37,11 @@ def run_both(be, t, X):
 
 
 # (type, rows, cols, tokens): the first two take the prompt GEMM (Q4_K, >= 8 tokens), the larger
-# one first, so the second call reuses the array with a smaller input; the others run the decode
-# kernels, which need no scratch
-CALLS = [(S.T_Q4_K, 1024, 8192, 64), (S.T_Q4_K, 272, 2048, 9), (S.T_Q4_K, 128, 2048, 5), (S.T_Q6_K, 96, 1024, 12)]
+# one first, so the second call reuses the array with a smaller input; the third runs the decode
+# kernels, which need no scratch; then the Q6_K GEMM and the nibble-type GEMM (Q5_1, then Q4_0
+# smaller)
+CALLS = [(S.T_Q4_K, 1024, 8192, 64), (S.T_Q4_K, 272, 2048, 9), (S.T_Q4_K, 128, 2048, 5), (S.T_Q6_K, 96, 1024, 12),
+         (S.T_Q5_1, 200, 4096, 40), (S.T_Q4_0, 64, 1024, 8)]
 
 
 @pytest.mark.parametrize("fresh", [True, False], ids=["fresh_context", "shared_context"])
