@@ -18,7 +18,7 @@ roofline: the dominant kernel of the step is the Q4_K decode matvec launch of th
          at least 512 MB of distinct weight copies.
 prefill: BASELINE config 4 (64 tokens x 4096 -> 14336, Q4_K) on the int8 MFMA GEMM, timed the
          same way, cold (rotating weights) and Infinity-Cache hot, as TOPS and fraction of 5 POPS;
-         the same shape in Q8_0 and Q6_K on their MFMA GEMMs, against their HBM floors.
+         the same shape in Q8_0, Q6_K and Q4_0 on their MFMA GEMMs, against their HBM floors.
 cpu_baseline: the reference's own CPU kernels (oracle/_ref, compiled from fastgguf.c) on the same
          layer with its default repacked Q4_K path, on this host's physical cores, over weight
          copies beyond the host's L3, for a bounded sample.
@@ -544,9 +544,13 @@ def main() -> int:
                     "kernel": "gemm_quant_kernel + q4k_gemm_kernel (int8 MFMA 16x16x64, split sub-block scales)",
                     "hbm_floor_us": round((wq4 + 4 * T * (4096 + 14336)) / HBM_PEAK_GBS / 1e3, 3),
                     "traffic": counted_traffic("prefill_gemm")})
-    # the same shape in Q8_0 and Q6_K on their MFMA GEMMs (gemm_q32's and gemm_kquant's roles),
+    # the same shape in Q8_0, Q6_K and Q4_0 on their MFMA GEMMs (gemm_q32's and gemm_kquant's roles),
     # cold over >= 512 MB of rotating copies and hot, against the HBM floor of their weights
-    for name, ty, wgen, bpr in (("q8_0", S.T_Q8_0, S.q8_0_weights, 128 * 34), ("q6_k", S.T_Q6_K, S.q6_k_weights, 16 * 210)):
+    kname = {"q8_0": "q80_gemm_kernel (int8 MFMA 32x32x32, one block per K step)",
+             "q6_k": "q6k_gemm_kernel (int8 MFMA 16x16x64, three scale-digit chains)",
+             "q4_0": "q32n_gemm_kernel (int8 MFMA 16x16x32 per block, gemm_q32's fp32 order, bit-exact)"}
+    for name, ty, wgen, bpr in (("q8_0", S.T_Q8_0, S.q8_0_weights, 128 * 34), ("q6_k", S.T_Q6_K, S.q6_k_weights, 16 * 210),
+                                ("q4_0", S.T_Q4_0, lambda r, c, seed: S.weights(S.T_Q4_0, r, c, seed), 128 * 18)):
         wbytes = 14336 * bpr
         w = wgen(14336, 4096, seed=130)
         ts = [be.upload(ty, 4096, w) for _ in range(copies_for(wbytes))]
@@ -560,8 +564,7 @@ def main() -> int:
         line.update({"workload": f"64 tokens x K=4096 -> N=14336, {name.upper()} (quantization of X included)",
                      "hbm_floor_us": round((wbytes + 4 * T * (4096 + 14336)) / HBM_PEAK_GBS / 1e3, 3),
                      "rotation_MB": round(len(ts) * wbytes / 1e6),
-                     "kernel": "q80_gemm_kernel (int8 MFMA 32x32x32, one block per K step)" if name == "q8_0" else
-                               "q6k_gemm_kernel (int8 MFMA 16x16x64, three scale-digit chains)"})
+                     "kernel": kname[name]})
         prefill[name] = line
         for t in ts:
             t.free()
