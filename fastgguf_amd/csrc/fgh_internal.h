@@ -98,7 +98,7 @@ __device__ __forceinline__ int dpp_xor2(int v) {  // quad_perm [2,3,0,1]
     return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
 }
 __device__ __forceinline__ int dpp_half_mirror(int v) {  // lane j <-> 7-j within 8 lanes
-    return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+    return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, true);  // every lane has a source
 }
 // exact integer sum over the 8 lanes of a row group; every lane of the group gets the total
 __device__ __forceinline__ int sum8_i32(int v) {

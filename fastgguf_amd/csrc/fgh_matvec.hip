@@ -23,6 +23,8 @@
 // of a tile over S wavefronts: wavefront 0 runs its chains as it streams, the others park their
 // fp32 step records {d * yd, lane partials} in LDS, and wavefront 0 continues the chains over them.
 // Up to 4 tensors of one type and width share one launch (matvec_multi, fastgguf.c:2552).
+#include <type_traits>
+
 #include "fgh_internal.h"
 
 namespace fgh {
@@ -326,7 +328,9 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
     const int32_t *abs = (const int32_t *)(act + act_off_s(TYPE, nb));  // Q4_1 / Q5_1: block sums
     float acc = 0.0f, cacc = 0.0f;  // cacc: Q6_K's correction chain, or Q4_1 / Q5_1's min chain
 
-    auto step = [&](const StepW<TYPE> &w, int st) {
+    // CHECK: the step may be the tile's last, with fewer than 4 blocks (the checks are uniform)
+    auto step = [&](const StepW<TYPE> &w, int st, auto check) {
+        constexpr bool CHECK = decltype(check)::value;
         const bool chain = S == 1 || ks == 0;
         uint8_t *rs = rec + (size_t)(st - nsw) * rec_bytes(TYPE);
         if constexpr (q8_kind(TYPE)) {
@@ -356,7 +360,7 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
                 }
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
-                    if (nbs >= 4 || k < nbs) {  // uniform
+                    if (!CHECK || nbs >= 4 || k < nbs) {  // uniform
                         acc = __builtin_fmaf(fd[k], (float)sd[k], acc);
                         if (q32_min(TYPE)) cacc = __builtin_fmaf(fm[k], (float)bsv[k], cacc);
                     }
@@ -397,18 +401,31 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
             }
         }
     };
-    // whole rounds of R steps as straight-line code, refilling the ring; then the last nsl % R
+    // whole rounds of R steps as straight-line code, refilling the ring. The rounds that end at
+    // least R steps before the wavefront's last step neither reach a partial step nor refill past
+    // the last (no checks, no clamp on the refill address); the next round may do both; then the
+    // last nsl % R steps.
+    using Check = std::true_type;
+    using NoCheck = std::false_type;
     int b0 = 0;
-    for (; b0 + R <= nsl; b0 += R) {
+    for (; b0 + 2 * R <= nsl; b0 += R) {
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-            step(ring[k], s0 + b0 + k);
+            step(ring[k], s0 + b0 + k, NoCheck());
+            step_load(T0 + (size_t)(b0 + k + R) * sstride, (uint32_t)lane, ring[k]);
+        }
+    }
+    if (b0 + R <= nsl) {
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            step(ring[k], s0 + b0 + k, Check());
             step_load(T0 + (size_t)min(b0 + k + R, sl) * sstride, (uint32_t)lane, ring[k]);
         }
+        b0 += R;
     }
 #pragma unroll
     for (int k = 0; k < R - 1; ++k)
-        if (b0 + k < nsl) step(ring[k], s0 + b0 + k);  // uniform
+        if (b0 + k < nsl) step(ring[k], s0 + b0 + k, Check());  // uniform
 
     if (S > 1) {
         __syncthreads();
