@@ -170,8 +170,8 @@ __global__ __launch_bounds__(256) void q32n_gemm_kernel(GemmNArgs a) {
     const uint8_t *wbase = a.W + ((size_t)mi * ns * a.tpm + 2 * p) * L.tile;
     const size_t wstride = (size_t)a.tpm * L.tile;
     const uint32_t toff = (uint32_t)(n >> 3) * L.tile;
-    const uint32_t noff = toff + L.n + 8 * (8 * r8 + 2 * g), doff = toff + 8 * r8;
-    const uint32_t moff = toff + (MIN ? L.m : 0) + 8 * r8, hoff = toff + (Q5 ? L.h : 0) + 2 * (8 * r8 + 2 * g);
+    const uint32_t noff = toff + L.n + 8 * (8 * r8 + 2 * g), doff = toff + L.ds * r8;
+    const uint32_t hoff = toff + (Q5 ? L.h : 0) + 2 * (8 * r8 + 2 * g);
     const uint32_t soff = 2048 + ((l & 4) ? 256 : 0) + 16 * (4 * g + (l & 3));  // xd or ys of token 4 g + l % 4
     const uint32_t abytes = (uint32_t)ns * GEMMN_REC;
     BufRes ar[NT];
@@ -182,8 +182,13 @@ __global__ __launch_bounds__(256) void q32n_gemm_kernel(GemmNArgs a) {
     auto load = [&](int s, WStepN &w, AStepN (&x)[NT]) __attribute__((always_inline)) {
         const BufRes rw = buf_res(wbase + (size_t)s * wstride, wbytes);
         w.n = bld16(rw, noff);
-        w.d = bld8(rw, doff);
-        if (MIN) w.m = bld8(rw, moff);
+        if (MIN) {  // the row's d and m in one record
+            const uint4 dm = bld16(rw, doff);
+            w.d = make_uint2(dm.x, dm.y);
+            w.m = make_uint2(dm.z, dm.w);
+        } else {
+            w.d = bld8(rw, doff);
+        }
         if (Q5) w.h = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)hoff, 0, 0);
         const int so = s * GEMMN_REC;
 #pragma unroll

@@ -37,8 +37,9 @@ namespace fgh {
 //                  n3 << 12, where bit bb of the nibble n_t is the fifth bit of element 4i + t
 //                  of block bb
 //   Q4_0 / IQ4_NL tile (4 blocks of 8 rows, 576 B), Q4_1 (640 B), Q5_1 (768 B): Q5_0's regions
-//     in the order d [64 B], m [64 B, Q4_1 / Q5_1: fp16 m of row r, block bb at 8r + 2bb],
-//     nibbles [512 B], fifth bits [128 B, Q5_1] (q32_layout gives the offsets)
+//     in the order scales, nibbles [512 B], fifth bits [128 B, Q5_1]; the scales of Q4_1 / Q5_1
+//     are 16-byte row records [128 B]: fp16 d of row r, block bb at 16r + 2bb, then its fp16 m at
+//     16r + 8 + 2bb (one 16-byte load per row and step); q32_layout gives the offsets
 //   (Q5_K shares the Q4_K layout with 512 B of fifth bits per (tile, block), fgh_q4k.hip)
 // ---------------------------------------------------------------------------------------------
 constexpr int T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
@@ -51,15 +52,16 @@ __host__ __device__ constexpr bool q8_kind(int type) {
     return type == T_Q8_0 || type == T_Q5_0 || type == T_Q4_0 || type == T_Q4_1 || type == T_Q5_1 ||
            type == T_IQ4_NL;
 }
-// 32-value nibble types: tile bytes and region offsets (-1: absent) of a 4-block step
+// 32-value nibble types: tile bytes, region offsets (-1: absent) of a 4-block step, and the
+// scale records: row r's at ds r, its fp16 d first, its fp16 m (Q4_1 / Q5_1) at + m
 struct Q32Layout {
-    int tile, m, n, h;
+    int tile, m, n, h, ds;
 };
 __host__ __device__ constexpr Q32Layout q32_layout(int type) {
-    return type == T_Q5_0 ? Q32Layout{704, -1, 64, 576}
-         : type == T_Q4_1 ? Q32Layout{640, 64, 128, -1}
-         : type == T_Q5_1 ? Q32Layout{768, 64, 128, 640}
-                          : Q32Layout{576, -1, 64, -1};  // Q4_0, IQ4_NL
+    return type == T_Q5_0 ? Q32Layout{704, -1, 64, 576, 8}
+         : type == T_Q4_1 ? Q32Layout{640, 8, 128, -1, 16}
+         : type == T_Q5_1 ? Q32Layout{768, 8, 128, 640, 16}
+                          : Q32Layout{576, -1, 64, -1, 8};  // Q4_0, IQ4_NL
 }
 __host__ __device__ constexpr bool q32_min(int type) { return type == T_Q4_1 || type == T_Q5_1; }
 

@@ -158,9 +158,11 @@ __global__ void relayout_q32_kernel(const uint8_t *__restrict__ src, uint8_t *__
         const int64_t mt = t / gpm, gl = t - mt * gpm;
         const int64_t m = mt / ntile;
         const int tb = (int)(mt - m * ntile);
-        const bool in_m = L.m >= 0 && ob >= L.m && ob < L.m + 64;
+        const bool in_sc = ob < 8 * L.ds;  // the scale records, L.ds bytes per row
+        const int sj = ob % L.ds;          // byte of the row's record: d, then m from L.m
+        const bool in_m = in_sc && L.m >= 0 && sj >= L.m;
         const bool in_h = L.h >= 0 && ob >= L.h;
-        const int r = ob < 64 || in_m ? (ob & 63) >> 3 : in_h ? (ob - L.h) >> 4 : (ob - L.n) >> 6;
+        const int r = in_sc ? ob / L.ds : in_h ? (ob - L.h) >> 4 : (ob - L.n) >> 6;
         const int64_t row = gl * 8 + r;
         // block bb of the step in this row, or null past the row's end
         auto blk = [&](int bb) -> const uint8_t * {
@@ -170,9 +172,9 @@ __global__ void relayout_q32_kernel(const uint8_t *__restrict__ src, uint8_t *__
         auto nib = [&](const uint8_t *p, int e) { return e < 16 ? (p[B.qs + e] & 15) : (p[B.qs + e - 16] >> 4); };
         auto bit = [&](const uint8_t *p, int e) { return (p[B.qh + (e >> 3)] >> (e & 7)) & 1; };
         int v = 0;
-        if (ob < 64 || in_m) {  // fp16 d (or m) of block (ob & 7) >> 1
-            const uint8_t *p = blk((ob & 7) >> 1);
-            v = p ? p[(in_m ? 2 : 0) + (ob & 1)] : 0;
+        if (in_sc) {  // fp16 d (or m) of block (sj & 7) >> 1
+            const uint8_t *p = blk((sj & 7) >> 1);
+            v = p ? p[(in_m ? 2 : 0) + (sj & 1)] : 0;
         } else if (!in_h) {  // byte 4w + t of slice i: element 4i + t of blocks 2w (low), 2w + 1 (high)
             const int q = ob - L.n, i = (q >> 3) & 7, w = (q >> 2) & 1, e = 4 * i + (q & 3);
             const uint8_t *p0 = blk(2 * w), *p1 = blk(2 * w + 1);

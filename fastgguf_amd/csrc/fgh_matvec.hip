@@ -42,8 +42,8 @@ __host__ __device__ constexpr size_t act_off_d(int type, int nb) {
 __host__ __device__ constexpr size_t act_off_s(int type, int nb) {
     return align16(act_off_d(type, nb) + 4 * (size_t)(q8_kind(type) ? 4 * mv_steps(type, nb) : nb));
 }
-// Q8: after d, for Q4_1 / Q5_1 only, the int32 sum of each block's 32 quants (s16[0] + s16[1], the
-// min term) [4 * steps]; Q8_K: bs [nb][16] int16
+// Q8: after d, for Q4_1 / Q5_1 only, the sum of each block's 32 quants (s16[0] + s16[1], the min
+// term) as fp32, exact [4 * steps]; Q8_K: bs [nb][16] int16
 __host__ __device__ constexpr size_t act_lds_bytes(int type, int nb) {
     return q8_kind(type) ? act_off_s(type, nb) + (q32_min(type) ? (size_t)16 * mv_steps(type, nb) : 0)
                          : align16(act_off_s(type, nb) + (size_t)nb * 32);
@@ -131,7 +131,7 @@ __device__ __forceinline__ void xq_store(int nb, int rb, const XVals &xv, uint8_
         for (int u = 0; u < 4; ++u) *(uint32_t *)(g + 16 * (4 * tl + u)) = w[u];
         if (tl == 0) {
             ((float *)(act + act_off_d(TYPE, nb)))[b] = d;
-            if (q32_min(TYPE)) ((int32_t *)(act + act_off_s(TYPE, nb)))[b] = s;
+            if (q32_min(TYPE)) ((float *)(act + act_off_s(TYPE, nb)))[b] = (float)s;  // exact: |s| < 2^13
         }
     } else {  // value 16 tl + 4 u = 32 c + 4 i (c = tl / 2, i = 4 (tl % 2) + u) -> position 32 i + 4 c
         const int c = tl >> 1;
@@ -185,8 +185,13 @@ __device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW
     constexpr Q32Layout L = q32_layout(TYPE);
     const BufRes r = buf_res(T, L.tile);
     w.n = bld8(r, L.n + 8 * lane);
-    w.d = bld8(r, 8 * (lane >> 3));
-    if (L.m >= 0) w.m = bld8(r, L.m + 8 * (lane >> 3));
+    if (L.m >= 0) {  // the row's d and m in one record
+        const uint4 dm = bld16(r, L.ds * (lane >> 3));
+        w.d = make_uint2(dm.x, dm.y);
+        w.m = make_uint2(dm.z, dm.w);
+    } else {
+        w.d = bld8(r, L.ds * (lane >> 3));
+    }
     if (L.h >= 0) w.h = bld2(r, L.h + 2 * lane);
 }
 __device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q6_K> &w) {
@@ -325,7 +330,7 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
     const bool row_ok = live && mrow + r < rows;
     // records of the wavefronts ks >= 1 (step s of the tile at s - nsw): lane partials, then fd
     uint8_t *rec = smem + act_lds_bytes(TYPE, nb) + (size_t)ts * (nst - nsw) * rec_bytes(TYPE);
-    const int32_t *abs = (const int32_t *)(act + act_off_s(TYPE, nb));  // Q4_1 / Q5_1: block sums
+    const float *abs = (const float *)(act + act_off_s(TYPE, nb));  // Q4_1 / Q5_1: block sums, as fp32
     float acc = 0.0f, cacc = 0.0f;  // cacc: Q6_K's correction chain, or Q4_1 / Q5_1's min chain
 
     // CHECK: the step may be the tile's last, with fewer than 4 blocks (the checks are uniform)
@@ -353,16 +358,16 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
             }
             const int nbs = nb - 4 * st;  // blocks of this step (the last one may have fewer)
             if (chain) {
-                int bsv[4] = {0, 0, 0, 0};
+                float bsv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
                 if constexpr (q32_min(TYPE)) {
-                    const int4 bs = *(const int4 *)(abs + 4 * st);
+                    const float4 bs = *(const float4 *)(abs + 4 * st);
                     bsv[0] = bs.x; bsv[1] = bs.y; bsv[2] = bs.z; bsv[3] = bs.w;
                 }
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
                     if (!CHECK || nbs >= 4 || k < nbs) {  // uniform
                         acc = __builtin_fmaf(fd[k], (float)sd[k], acc);
-                        if (q32_min(TYPE)) cacc = __builtin_fmaf(fm[k], (float)bsv[k], cacc);
+                        if (q32_min(TYPE)) cacc = __builtin_fmaf(fm[k], bsv[k], cacc);
                     }
             } else {
                 ((float4 *)rs)[lane] = make_float4((float)sd[0], (float)sd[1], (float)sd[2], (float)sd[3]);
@@ -436,14 +441,14 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
             const uint8_t *rs = rec + (size_t)(st0 - nsw) * rec_bytes(TYPE);
             if constexpr (q8_kind(TYPE)) {
                 float4 sv[CH], fv[CH], mv[CH];
-                int4 bv[CH];
+                float4 bv[CH];
 #pragma unroll
                 for (int c = 0; c < CH; ++c) {  // records past the end are read but not used
                     sv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE)))[lane];
                     fv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE) + 1024))[r];
                     if (q32_min(TYPE)) {
                         mv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE) + 1152))[r];
-                        bv[c] = *(const int4 *)(abs + 4 * (st0 + c));
+                        bv[c] = *(const float4 *)(abs + 4 * (st0 + c));
                     }
                 }
 #pragma unroll
@@ -451,12 +456,12 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
                     const int nbs = nb - 4 * (st0 + c);  // uniform
                     const float sk[4] = {sv[c].x, sv[c].y, sv[c].z, sv[c].w}, fk[4] = {fv[c].x, fv[c].y, fv[c].z, fv[c].w};
                     const float mk[4] = {mv[c].x, mv[c].y, mv[c].z, mv[c].w};
-                    const int bk[4] = {bv[c].x, bv[c].y, bv[c].z, bv[c].w};
+                    const float bk[4] = {bv[c].x, bv[c].y, bv[c].z, bv[c].w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
                         if (nbs >= 4 || k < nbs) {
                             acc = __builtin_fmaf(fk[k], sk[k], acc);
-                            if (q32_min(TYPE)) cacc = __builtin_fmaf(mk[k], (float)bk[k], cacc);
+                            if (q32_min(TYPE)) cacc = __builtin_fmaf(mk[k], bk[k], cacc);
                         }
                 }
             } else {
