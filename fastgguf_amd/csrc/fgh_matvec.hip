@@ -48,10 +48,15 @@ __host__ __device__ constexpr size_t act_lds_bytes(int type, int nb) {
     return q8_kind(type) ? act_off_s(type, nb) + (q32_min(type) ? (size_t)16 * mv_steps(type, nb) : 0)
                          : align16(act_off_s(type, nb) + (size_t)nb * 32);
 }
-// fp32 records of one step of one tile (block split): lane partials, then d * yd per row (and
+// records of one step of one tile (block split): lane partials, then fp32 d * yd per row (and
 // m * yd per row for Q4_1 / Q5_1)
+// Q4_0 / Q4_1 / Q5_0 / Q5_1 keep the lane partials as int16 (exact: a lane's 4 products are at most
+// 4 * 31 * 127, repacked Q4_0's whole-block sum at most 32 * 8 * 127 = 32512), half the bytes, so
+// a long row splits further within the LDS; Q8_0 and IQ4_NL need 17 bits and keep fp32
+__host__ __device__ constexpr bool rec_i16(int type) { return q8_kind(type) && type != T_Q8_0 && type != T_IQ4_NL; }
+__host__ __device__ constexpr size_t rec_fd_off(int type) { return q8_kind(type) ? (rec_i16(type) ? 512 : 1024) : 512; }
 __host__ __device__ constexpr size_t rec_bytes(int type) {
-    return q8_kind(type) ? 64 * 16 + 8 * 16 + (q32_min(type) ? 8 * 16 : 0) : 64 * 8 + 8 * 4;
+    return q8_kind(type) ? rec_fd_off(type) + 8 * 16 + (q32_min(type) ? 8 * 16 : 0) : 64 * 8 + 8 * 4;
 }
 __host__ __device__ constexpr int mv_tile_bytes(int type) {
     return type == T_Q6_K ? Q6K_TILE : type == T_Q8_0 ? Q80_TILE : q32_layout(type).tile;
@@ -370,9 +375,13 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
                         if (q32_min(TYPE)) cacc = __builtin_fmaf(fm[k], bsv[k], cacc);
                     }
             } else {
-                ((float4 *)rs)[lane] = make_float4((float)sd[0], (float)sd[1], (float)sd[2], (float)sd[3]);
-                if (i == 0) ((float4 *)(rs + 1024))[r] = make_float4(fd[0], fd[1], fd[2], fd[3]);
-                if (q32_min(TYPE) && i == 0) ((float4 *)(rs + 1152))[r] = make_float4(fm[0], fm[1], fm[2], fm[3]);
+                if (rec_i16(TYPE))
+                    ((uint2 *)rs)[lane] = make_uint2(pack_i16(sd[0], sd[1]), pack_i16(sd[2], sd[3]));
+                else
+                    ((float4 *)rs)[lane] = make_float4((float)sd[0], (float)sd[1], (float)sd[2], (float)sd[3]);
+                constexpr size_t FD = rec_fd_off(TYPE);
+                if (i == 0) ((float4 *)(rs + FD))[r] = make_float4(fd[0], fd[1], fd[2], fd[3]);
+                if (q32_min(TYPE) && i == 0) ((float4 *)(rs + FD + 128))[r] = make_float4(fm[0], fm[1], fm[2], fm[3]);
             }
             if (DUMP) {
 #pragma unroll
@@ -442,12 +451,19 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
             if constexpr (q8_kind(TYPE)) {
                 float4 sv[CH], fv[CH], mv[CH];
                 float4 bv[CH];
+                constexpr size_t FD = rec_fd_off(TYPE);
 #pragma unroll
                 for (int c = 0; c < CH; ++c) {  // records past the end are read but not used
-                    sv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE)))[lane];
-                    fv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE) + 1024))[r];
+                    if (rec_i16(TYPE)) {
+                        const uint2 p = ((const uint2 *)(rs + c * rec_bytes(TYPE)))[lane];
+                        sv[c] = make_float4((float)(int16_t)(p.x & 0xFFFF), (float)((int)p.x >> 16),
+                                            (float)(int16_t)(p.y & 0xFFFF), (float)((int)p.y >> 16));
+                    } else {
+                        sv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE)))[lane];
+                    }
+                    fv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE) + FD))[r];
                     if (q32_min(TYPE)) {
-                        mv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE) + 1152))[r];
+                        mv[c] = ((const float4 *)(rs + c * rec_bytes(TYPE) + FD + 128))[r];
                         bv[c] = *(const float4 *)(abs + 4 * (st0 + c));
                     }
                 }
@@ -502,7 +518,7 @@ static size_t mv_lds(int type, int nb, int tpw, int s) {
     const int pad = q8_kind(type) ? 3 : 7;
     return act_lds_bytes(type, nb) + (s > 1 ? ((size_t)tpw * (nst - nsw) + pad) * rec_bytes(type) : 0);
 }
-static int mv_tpw(int s) { return s == 1 ? 4 : s == 2 ? 2 : 1; }
+static int mv_tpw(int s) { return s == 1 ? 4 : s <= 4 ? 2 : 1; }
 
 size_t matvec_lds_bytes(int type, int order, int nb) {
     if (type == T_Q4_K || type == T_Q5_K) return q4k_lds_bytes(order, nb);
@@ -524,7 +540,8 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 // Launch shape: launches of fewer than 768 tiles (tiles x tokens) split the steps of a tile over up
 // to 8 wavefronts, as many as keep the launch within 2048 wavefronts, each wavefront at 4 steps or
 // more (Q6_K: 2), the records within the 160 KiB of LDS of a workgroup and every workgroup of the
-// launch resident at once; tiles per workgroup 4, 2 or 1 for S = 1, 2 or more. Ring depth:
+// launch resident at once; tiles per workgroup 4 for S = 1, 2 for S = 2 and 4 (halving the
+// workgroups that each quantize x), 1 for S = 8. Ring depth:
 // 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps, 4 otherwise.
 template <int TYPE>
 static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
@@ -547,7 +564,7 @@ static hipError_t mv_launch_type(const MvArgs &a, int ntok, int num_cu, hipStrea
     switch (sh.S) {
     case 1: return mv_launch_r<TYPE, ORDER, 4, 1>(sh.R, a, ntok, sh.lds, s);
     case 2: return mv_launch_r<TYPE, ORDER, 2, 2>(sh.R, a, ntok, sh.lds, s);
-    case 4: return mv_launch_r<TYPE, ORDER, 1, 4>(sh.R, a, ntok, sh.lds, s);
+    case 4: return mv_launch_r<TYPE, ORDER, 2, 4>(sh.R, a, ntok, sh.lds, s);
     default: return mv_launch_r<TYPE, ORDER, 1, 8>(sh.R, a, ntok, sh.lds, s);
     }
 }
