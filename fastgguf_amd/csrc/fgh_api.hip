@@ -37,7 +37,7 @@ struct fgh_ctx {
     DevBuf as;          // attention scores / weights
     DevBuf kqr, kor;    // TurboQuant attention: rotated queries, rotated outputs
     DevBuf msel, mw, mg, mu, md, mlog;  // MoE: selection, weights, gate / up / down outputs
-    DevBuf mseg, mslot, mimx, mimh;         // MoE: slots grouped by expert, Q8_K images of x and h
+    DevBuf mseg, mslot, mimx, mimh;         // MoE: per-expert slot counts and buckets, Q8_K images of x and h
     DevBuf ck;                              // fgh_checksum_dev: per-workgroup partial sums
     DevBuf h;                               // fgh_matvec_silu_dev: silu(g) * u
     int num_cu = 256;         // compute units (sizes the persistent decode grid)
@@ -734,17 +734,19 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
         HIP_TRY(c, fgh::launch_q4k_moe_down((int)down->type, a, w, k, n_tok, c->stream));
         return FGH_OK;
     }
-    HIP_TRY(c, fgh::launch_moe_route(logits, (int)E, k, n_tok, sel, w, c->stream));
     if (grouped) {
+        // one launch for the x images, the routing and the slots filed by expert; the grouped
+        // kernels read the buckets; the combine clears their counts for the next call
         const size_t ibx = fgh::q4_image_bytes(gate->nb), ibh = fgh::q4_image_bytes(down->nb);
-        if ((rc = grow(c, c->mseg, (size_t)(1 + 3 * E) * 4)) || (rc = grow(c, c->mslot, (size_t)np * 4)) ||
+        void *cnt_before = c->mseg.p;
+        if ((rc = grow(c, c->mseg, (size_t)E * 4)) || (rc = grow(c, c->mslot, (size_t)E * n_tok * 4)) ||
             (rc = grow(c, c->mimx, (size_t)n_tok * ibx)) || (rc = grow(c, c->mimh, (size_t)np * ibh)))
             return rc;
-        int32_t *seg = (int32_t *)c->mseg.p, *slots = (int32_t *)c->mslot.p;
+        int32_t *cnt = (int32_t *)c->mseg.p, *buckets = (int32_t *)c->mslot.p;
+        if (c->mseg.p != cnt_before) HIP_TRY(c, hipMemsetAsync(cnt, 0, c->mseg.cap, c->stream));  // new: zero once
         uint8_t *imx = (uint8_t *)c->mimx.p, *imh = (uint8_t *)c->mimh.p;
-        HIP_TRY(c, fgh::launch_moe_group(sel, (int)np, (int)E, seg, slots, c->stream));
-        HIP_TRY(c, fgh::launch_q4_image(X, nullptr, n_embd, gate->nb, n_tok, imx, c->stream));
-        const int maxseg = (int)std::min<int64_t>(E, np);
+        HIP_TRY(c, fgh::launch_moe_prep(X, n_embd, gate->nb, imx, logits, (int)E, k, n_tok, sel, w, cnt, buckets,
+                                        c->stream));
         fgh::MvArgs a;
         memset(&a, 0, sizeof(a));
         a.t[0] = fgh::MvT{gate->dev, G, gate->rows, gate->gpm, 0};
@@ -756,7 +758,7 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
         a.ldy = ff;
         a.nb = gate->nb;
         a.xdiv = k;
-        HIP_TRY(c, fgh::launch_q4k_moe(a, seg, slots, imx, maxseg, c->stream));
+        HIP_TRY(c, fgh::launch_q4k_moe(a, cnt, buckets, n_tok, (int)E, imx, c->stream));
         // h = silu(g) * u, quantized straight into its images (never stored as fp32)
         HIP_TRY(c, fgh::launch_q4_image(G, U, ff, down->nb, np, imh, c->stream));
         a.t[0] = fgh::MvT{down->dev, D, down->rows, down->gpm, 0};
@@ -766,10 +768,11 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
         a.ldy = n_embd;
         a.nb = down->nb;
         a.xdiv = 1;
-        HIP_TRY(c, fgh::launch_q4k_moe(a, seg, slots, imh, maxseg, c->stream));
-        HIP_TRY(c, fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, c->stream));
+        HIP_TRY(c, fgh::launch_q4k_moe(a, cnt, buckets, n_tok, (int)E, imh, c->stream));
+        HIP_TRY(c, fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, cnt, (int)E, c->stream));
         return FGH_OK;
     }
+    HIP_TRY(c, fgh::launch_moe_route(logits, (int)E, k, n_tok, sel, w, c->stream));
     // gate and up: one launch when their type and order agree (both read the same x row)
     if (gate->type == up->type && gate->order == up->order) {
         const fgh_tensor *gu[2] = {gate, up};
@@ -785,7 +788,7 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
     HIP_TRY(c, fgh::launch_silu_mul(G, U, G, np * ff, c->stream));
     float *yd[1] = {D};
     if ((rc = matvec_launch(c, 1, &down, G, ff, yd, n_embd, (int)np, nullptr, nullptr, sel, 1))) return rc;
-    HIP_TRY(c, fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, c->stream));
+    HIP_TRY(c, fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, nullptr, 0, c->stream));
     return FGH_OK;
 }
 

@@ -428,19 +428,24 @@ hipError_t launch_mfma_peak(int iters, uint32_t *sink, int num_cu, hipStream_t s
 // h = silu(g) * u over n values (silu_f, fastgguf.c:3118); h may be g
 hipError_t launch_silu_mul(const float *g, const float *u, float *h, int64_t n, hipStream_t s);
 hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok, int32_t *sel, float *w, hipStream_t s);
-hipError_t launch_moe_group(const int32_t *sel, int np, int n_expert, int32_t *seg, int32_t *slots, hipStream_t s);
+// the grouped path's first launch (fgh_q4k.hip): x images, routing, and the slots filed in
+// per-expert buckets of n_tok entries (cnt[n_expert] zero on entry; moe_combine clears it)
+hipError_t launch_moe_prep(const float *x, int64_t ldx, int nb, uint8_t *img, const float *logits, int n_expert,
+                           int k, int n_tok, int32_t *sel, float *w, int32_t *cnt, int32_t *bucket, hipStream_t s);
 // grouped Q4_K row-order expert matvecs (fgh_q4k.hip): a.groups = tiles of one matrix over a.t;
-// rows of at most q4k_moe_max_blocks() blocks
+// rows of at most q4k_moe_max_blocks() blocks; expert e's slots in buckets[e * cap ..), cnt[e] of them
 size_t q4k_moe_lds_bytes(int nb);
 int q4k_moe_max_blocks();
-hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *seg, const int32_t *slots, const uint8_t *img,
-                          int max_segments, hipStream_t s);
+hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *cnt, const int32_t *buckets, int cap, int n_expert,
+                          const uint8_t *img, hipStream_t s);
 // Q8_K images of rows in the decode kernels' LDS layout; u != null: the rows are silu(x) * u
 size_t q4_image_bytes(int nb);
 hipError_t launch_q4_image(const float *x, const float *u, int64_t ldx, int nb, int64_t rows, uint8_t *img,
                            hipStream_t s);
+// y = the ordered combine of the k experts' rows; cnt != null: also clears cnt[n_expert] (the
+// grouped path's bucket counts, for its next call)
 hipError_t launch_moe_combine(const float *d, const float *w, float *y, int n_embd, int k, int n_tok, int64_t ldy,
-                              hipStream_t s);
+                              int32_t *cnt, int n_expert, hipStream_t s);
 
 // attention over an fp32 KV ring cache (fgh_attn.hip): rows (token, head), row t * n_head + h
 struct AttnArgs {

@@ -21,63 +21,15 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *__restrict__
     moe_route_wave(logits + (size_t)t * n_expert, n_expert, k, ps, sel + (size_t)t * k, w + (size_t)t * k, 0);
 }
 
-// Groups the n_tok * k (token, selected expert) slots by expert, for the grouped expert kernels:
-// seg[0] = number of selected experts; seg[1 + 3 i .. 3 + 3 i] = {expert, first, count} of the
-// i-th of them in ascending expert order; slots[first .. first + count) = its slots. The order of
-// slots inside an expert is whatever the atomics give: each slot's arithmetic is independent of
-// it, so results do not depend on it. One workgroup of 256 threads; n_expert <= 512.
-__global__ __launch_bounds__(256) void moe_group_kernel(const int32_t *__restrict__ sel, int np, int n_expert,
-                                                        int32_t *__restrict__ seg, int32_t *__restrict__ slots) {
-    __shared__ int cnt[64 * MOE_EPL], fill[64 * MOE_EPL], scan[2][256], sscan[2][256];
-    const int tid = threadIdx.x;
-    for (int e = tid; e < 64 * MOE_EPL; e += 256) {
-        cnt[e] = 0;
-        fill[e] = 0;
-    }
-    __syncthreads();
-    for (int i = tid; i < np; i += 256) atomicAdd(&cnt[sel[i]], 1);
-    __syncthreads();
-    // thread t owns experts 2t, 2t + 1: inclusive scans of counts and of non-empty flags
-    const int c0 = cnt[2 * tid], c1 = cnt[2 * tid + 1];
-    int v = c0 + c1, f = (c0 > 0) + (c1 > 0);
-    int buf = 0;
-    scan[0][tid] = v;
-    sscan[0][tid] = f;
-    __syncthreads();
-    for (int o = 1; o < 256; o <<= 1) {
-        if (tid >= o) {
-            v += scan[buf][tid - o];
-            f += sscan[buf][tid - o];
-        }
-        buf ^= 1;
-        scan[buf][tid] = v;
-        sscan[buf][tid] = f;
-        __syncthreads();
-    }
-    const int start0 = v - c0 - c1, sidx0 = f - (c0 > 0) - (c1 > 0);
-    if (2 * tid < n_expert && c0 > 0) {
-        seg[1 + 3 * sidx0] = 2 * tid;
-        seg[2 + 3 * sidx0] = start0;
-        seg[3 + 3 * sidx0] = c0;
-    }
-    if (2 * tid + 1 < n_expert && c1 > 0) {
-        const int si = sidx0 + (c0 > 0);
-        seg[1 + 3 * si] = 2 * tid + 1;
-        seg[2 + 3 * si] = start0 + c0;
-        seg[3 + 3 * si] = c1;
-    }
-    if (tid == 255) seg[0] = f;
-    fill[2 * tid] = start0;
-    fill[2 * tid + 1] = start0 + c0;
-    __syncthreads();
-    for (int i = tid; i < np; i += 256) slots[atomicAdd(&fill[sel[i]], 1)] = i;
-}
-
 // y[t][i] = sum_j fma(w[t][j], d[t k + j][i], s), j ascending
+// (cnt: the grouped path's bucket counts, cleared here for its next call: this launch runs after
+// every kernel that reads them)
 __global__ void moe_combine_kernel(const float *__restrict__ d, const float *__restrict__ w, float *__restrict__ y,
-                                   int n_embd, int k, int64_t ldy) {
+                                   int n_embd, int k, int64_t ldy, int32_t *__restrict__ cnt, int n_expert) {
     const int t = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (cnt && blockIdx.x == 0 && t == 0)
+        for (int e = threadIdx.x; e < n_expert; e += blockDim.x) cnt[e] = 0;
     if (i >= n_embd) return;
     float s = 0.0f;
     for (int j0 = 0; j0 < k; j0 += 8) {  // 8 experts' loads in flight, then their fmas in order
@@ -134,15 +86,9 @@ hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok,
     return hipGetLastError();
 }
 
-hipError_t launch_moe_group(const int32_t *sel, int np, int n_expert, int32_t *seg, int32_t *slots, hipStream_t s) {
-    if (np < 1 || np > 64 * 64 || n_expert < 1 || n_expert > 64 * MOE_EPL) return hipErrorInvalidValue;
-    moe_group_kernel<<<1, 256, 0, s>>>(sel, np, n_expert, seg, slots);
-    return hipGetLastError();
-}
-
 hipError_t launch_moe_combine(const float *d, const float *w, float *y, int n_embd, int k, int n_tok, int64_t ldy,
-                              hipStream_t s) {
-    moe_combine_kernel<<<dim3((n_embd + 255) / 256, n_tok), 256, 0, s>>>(d, w, y, n_embd, k, ldy);
+                              int32_t *cnt, int n_expert, hipStream_t s) {
+    moe_combine_kernel<<<dim3((n_embd + 255) / 256, n_tok), 256, 0, s>>>(d, w, y, n_embd, k, ldy, cnt, n_expert);
     return hipGetLastError();
 }
 

@@ -749,15 +749,52 @@ hipError_t launch_q4_image(const float *x, const float *u, int64_t ldx, int nb, 
 }
 size_t q4_image_bytes(int nb) { return q4_act_bytes(nb); }
 
+// The grouped MoE path's first launch, one wavefront per token t: the Q8_K image of x row t
+// (q4_image_kernel's blocks, 4 at a time), the token's routing (moe_route_wave: sel, w), and each
+// selected slot t k + j filed in its expert's bucket: bucket[e * cap + position], cnt[e] counting
+// (cap = tokens: a token selects an expert at most once). The order inside a bucket is whatever
+// the atomics give; no result depends on it. cnt starts at zero and moe_combine_kernel, the
+// path's last launch, clears it again.
+__global__ __launch_bounds__(64) void moe_prep_kernel(const float *__restrict__ x, int64_t ldx, int nb,
+                                                      uint8_t *__restrict__ img, const float *__restrict__ logits,
+                                                      int n_expert, int k, int32_t *__restrict__ sel,
+                                                      float *__restrict__ w, int32_t *__restrict__ cnt,
+                                                      int32_t *__restrict__ bucket, int cap) {
+    __shared__ __align__(16) float ps[64 * MOE_EPL];
+    const int t = blockIdx.x;
+    const float *xr = x + (size_t)t * ldx;
+    uint8_t *ir = img + (size_t)t * q4_act_bytes(nb);
+    for (int b0 = 0; b0 < nb; b0 += 4) {
+        const int b = b0 + (int)(threadIdx.x >> 4);
+        XRound xv;
+        q8k_load_b(xr, b, b < nb, xv);
+        q8k_store_b(nb, b, b < nb, xv, ir);
+    }
+    moe_route_wave(logits + (size_t)t * n_expert, n_expert, k, ps, sel + (size_t)t * k, w + (size_t)t * k, 0);
+    __syncthreads();  // the wavefront's own sel stores, read back
+    if ((int)threadIdx.x < k) {
+        const int slot = t * k + (int)threadIdx.x, e = sel[slot];
+        bucket[(size_t)e * cap + atomicAdd(&cnt[e], 1)] = slot;
+    }
+}
+
+hipError_t launch_moe_prep(const float *x, int64_t ldx, int nb, uint8_t *img, const float *logits, int n_expert,
+                           int k, int n_tok, int32_t *sel, float *w, int32_t *cnt, int32_t *bucket, hipStream_t s) {
+    if (n_expert < 1 || n_expert > 64 * MOE_EPL || k < 1 || k > n_expert || k > 64 || nb < 1 || n_tok < 1)
+        return hipErrorInvalidValue;
+    moe_prep_kernel<<<n_tok, 64, 0, s>>>(x, ldx, nb, img, logits, n_expert, k, sel, w, cnt, bucket, n_tok);
+    return hipGetLastError();
+}
+
 // MoE expert matvecs grouped by expert (row order, dot_q4_K_q8k): workgroup (x, y) takes tiles
-// 4x..4x+3 (one per wavefront, over the launch's tensors) of the matrix of segment y (one selected
-// expert with its token slots, from moe_group_kernel) and every slot of that segment. For every
+// 4x..4x+3 (one per wavefront, over the launch's tensors) of the matrix of expert y and every
+// slot in its bucket (moe_prep_kernel; a workgroup of an expert no token selected exits). For every
 // chunk of MOE_TC slots the workgroup copies their activation images (q4_image_kernel, row
 // slot / a.xdiv) into LDS; each wavefront then walks the blocks of its tile through a ring of
 // MOE_R steps, forms a block's weight-side values once (nibbles, scale and min pairs, d, dmin) and
 // runs the decode kernel's row-order lane sums and fp32 chains for every slot of the chunk (the
 // chains of a slot in block order, as the per-token matvec does). Tensor i of a.t: output rows
-// y_i[slot * ldy]. seg: [0] = number of segments, then per segment {expert, first, count}.
+// y_i[slot * ldy].
 constexpr int MOE_TC = 8, MOE_R = 2;
 
 // the weight side of one (tile, block) for the row order: chunk j's nibbles, its (sc_2j, sc_2j+1)
@@ -784,16 +821,17 @@ __device__ __forceinline__ void rb_wside(const RbW &w, const RbLane &ln, RbWSide
 }
 
 template <int TC>
-__global__ __launch_bounds__(256) void q4k_moe_kernel(MvArgs a, const int32_t *__restrict__ seg,
-                                                      const int32_t *__restrict__ slots, const uint8_t *__restrict__ img) {
+__global__ __launch_bounds__(256) void q4k_moe_kernel(MvArgs a, const int32_t *__restrict__ cnt,
+                                                      const int32_t *__restrict__ slots, int cap,
+                                                      const uint8_t *__restrict__ img) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 3, rr = lane >> 2;
     const int nb = a.nb;
-    const int sidx = blockIdx.y;
-    if (sidx >= seg[0]) return;  // whole workgroup: fewer segments than the grid allows
-    const int expert = seg[1 + 3 * sidx], first = seg[2 + 3 * sidx], count = seg[3 + 3 * sidx];
+    const int expert = blockIdx.y, count = cnt[expert];
+    if (count == 0) return;  // whole workgroup: no token selected this expert
+    const int first = expert * cap;
     const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
     const bool live = tile < a.groups;
     const int64_t tc = live ? tile : a.groups - 1;
@@ -888,13 +926,13 @@ int q4k_moe_max_blocks() {
     return nb;
 }
 
-// a.groups = tiles of one matrix over all tensors; grid.y = max_segments
-hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *seg, const int32_t *slots, const uint8_t *img,
-                          int max_segments, hipStream_t s) {
+// a.groups = tiles of one matrix over all tensors; grid.y = experts
+hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *cnt, const int32_t *buckets, int cap, int n_expert,
+                          const uint8_t *img, hipStream_t s) {
     const size_t lds = q4k_moe_lds_bytes(a.nb);
-    if (a.nb < 1 || lds > 65536) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((a.groups + 3) / 4), (unsigned)max_segments);
-    q4k_moe_kernel<MOE_TC><<<grid, 256, lds, s>>>(a, seg, slots, img);
+    if (a.nb < 1 || lds > 65536 || n_expert < 1 || cap < 1) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.groups + 3) / 4), (unsigned)n_expert);
+    q4k_moe_kernel<MOE_TC><<<grid, 256, lds, s>>>(a, cnt, buckets, cap, img);
     return hipGetLastError();
 }
 

@@ -161,3 +161,47 @@ def test_moe_config5(backend, oracle, T):
     assert bits_equal(Y2, Y)
     for t in (gate, up, down):
         t.free()
+
+
+def test_moe_grouped_graph_replays(backend, oracle):
+    """The several-token path (the slots filed in per-expert buckets whose counts the path's last
+    launch clears) captured in a graph: every replay, with eager MoE calls of another expert count
+    and token count between them, equals the oracle bit for bit, and so do the eager calls."""
+    E, K, D, F, T = 32, 4, 512, 256, 9
+    gw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 510)
+    uw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 511)
+    dw = S.random_bytes_weights(S.T_Q4_K, E * D, F, 512)
+    X = S.activations(D, 513, rows=T)
+    logits = S.router_logits(T, E, 514)
+    Yo, _, _ = oracle.moe_ffn((S.T_Q4_K,) * 3, gw, uw, dw, E, K, D, F, logits, X)
+    gate, up, down = (upload_experts(backend, a, c, r, E) for a, c, r in ((gw, D, F), (uw, D, F), (dw, F, D)))
+    E2, T2 = 16, 5  # the eager calls between the replays
+    gw2 = S.random_bytes_weights(S.T_Q4_K, E2 * F, D, 520)
+    uw2 = S.random_bytes_weights(S.T_Q4_K, E2 * F, D, 521)
+    dw2 = S.random_bytes_weights(S.T_Q4_K, E2 * D, F, 522)
+    X2 = S.activations(D, 523, rows=T2)
+    logits2 = S.router_logits(T2, E2, 524)
+    Yo2, _, _ = oracle.moe_ffn((S.T_Q4_K,) * 3, gw2, uw2, dw2, E2, K, D, F, logits2, X2)
+    g2, u2, d2 = (upload_experts(backend, a, c, r, E2) for a, c, r in ((gw2, D, F), (uw2, D, F), (dw2, F, D)))
+    xd, ld, yd = backend.dev_alloc(X.nbytes), backend.dev_alloc(logits.nbytes), backend.dev_alloc(4 * T * D)
+    backend.h2d(xd, X)
+    backend.h2d(ld, np.ascontiguousarray(logits, np.float32))
+    backend.moe_ffn_dev(gate, up, down, K, ld, xd, yd, T)  # eager first: the scratch exists
+    backend.sync()
+    backend.graph_begin()
+    backend.moe_ffn_dev(gate, up, down, K, ld, xd, yd, T)
+    g = backend.graph_end()
+    for rep in range(3):
+        backend.h2d(yd, np.full(T * D, np.nan, np.float32))
+        backend.graph_launch(g)
+        backend.sync()
+        Y = np.empty((T, D), np.float32)
+        backend.d2h(Y, yd)
+        assert bits_equal(Y, Yo), f"replay {rep}"
+        Y2, _, _ = backend.moe_ffn(g2, u2, d2, K, logits2, X2)
+        assert bits_equal(Y2, Yo2), f"eager call after replay {rep}"
+    backend.graph_destroy(g)
+    for p in (xd, ld, yd):
+        backend.dev_free(p)
+    for t in (gate, up, down, g2, u2, d2):
+        t.free()
