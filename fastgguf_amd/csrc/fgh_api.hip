@@ -225,9 +225,14 @@ static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const fl
 static int gemm_q4k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
                          uint8_t *act, int32_t *ds, int32_t *dm) {
     const int Tp = (T + 15) / 16 * 16;
-    HIP_TRY(c, fgh::launch_gemm_quant(X, ldx, t->nb, T, Tp, act, c->stream));
+    const fgh::GemmScratch gs = fgh::gemm_scratch(t->groups, t->rows * t->n_mats, t->nb, T, c->num_cu);
+    int32_t *cnt = gs.ks > 1 ? (int32_t *)(act + gs.cnt_off) : nullptr;
+    HIP_TRY(c, fgh::launch_gemm_quant(X, ldx, t->nb, T, Tp, act, cnt, gs.ncnt, c->stream));
     fgh::GemmArgs a;
     memset(&a, 0, sizeof(a));
+    a.ks = gs.ks;
+    a.cnt = cnt;
+    a.part = gs.ks > 1 ? (float *)(act + gs.part_off) : nullptr;
     a.W = t->dev;
     a.Y = Y;
     a.rows = t->rows;
@@ -330,9 +335,9 @@ static int gemm_q6k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_
 
 // the types and token counts that take a prompt GEMM (matmul, fastgguf.c:3018-3031), and the
 // activation-record bytes it needs (0: the per-token decode kernels, which need no scratch)
-static size_t prompt_gemm_bytes(const fgh_tensor *t, int T) {
+static size_t prompt_gemm_bytes(const fgh_ctx *c, const fgh_tensor *t, int T) {
     if (T < 8) return 0;
-    if (t->type == FGH_T_Q4_K) return fgh::gemm_act_bytes(t->nb, (T + 15) / 16 * 16);
+    if (t->type == FGH_T_Q4_K) return fgh::gemm_scratch(t->groups, t->rows * t->n_mats, t->nb, T, c->num_cu).bytes;
     if (t->type == FGH_T_Q8_0) return fgh::gemm32_act_bytes(t->nb, T <= 32 ? 32 : 64);
     if (t->type == FGH_T_Q6_K) return fgh::gemm6_act_bytes(t->nb, (T + 15) / 16 * 16);
     if (q32n_type(t->type)) return fgh::gemmn_act_bytes(t->nb, (T + 15) / 16 * 16);
@@ -349,7 +354,7 @@ static int prompt_gemm_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int
 static int prompt_gemm(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
                        int32_t *ds, int32_t *dm) {
     int rc;
-    if ((rc = grow(c, c->gq, prompt_gemm_bytes(t, T)))) return rc;
+    if ((rc = grow(c, c->gq, prompt_gemm_bytes(c, t, T)))) return rc;
     return prompt_gemm_into(c, t, X, ldx, Y, ldy, T, (uint8_t *)c->gq.p, ds, dm);
 }
 
@@ -641,7 +646,7 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
     // nb >= 8: the prompt GEMMs (matmul 3018-3031) on int8 MFMA for Q4_K, Q6_K, Q8_0 and the nibble
     // types Q4_0 / Q4_1 / Q5_0 / Q5_1; Q5_K and IQ4_NL, which have no GEMM in the reference, run the
     // per-token decode kernels as its matmul does
-    if (prompt_gemm_bytes(t, nb)) return prompt_gemm(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
+    if (prompt_gemm_bytes(c, t, nb)) return prompt_gemm(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
     float *ys[1] = {Y};
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
 }
@@ -651,7 +656,7 @@ int fgh_matmul_dev_noalloc(fgh_ctx *c, const fgh_tensor *t, const float *X, int 
     if (rc) return rc;
     if (!X || !Y || nb < 1 || nb > FG_BATCH || ldx < t->cols || ldy < t->rows * t->n_mats)
         return fail(c, FGH_ERR_ARG, "matmul_dev_noalloc: bad arguments");
-    const size_t need = prompt_gemm_bytes(t, nb);  // the prompt GEMMs are the paths with scratch
+    const size_t need = prompt_gemm_bytes(c, t, nb);  // the prompt GEMMs are the paths with scratch
     const bool gemm = need > 0;
     if (gemm) {
         if (need > FGH_NOALLOC_SCRATCH_BYTES)
@@ -1183,7 +1188,7 @@ int fgh_gemm_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx
     NO_CAPTURE(c);
     if (!X || !sumi || !msum || nb < 1 || nb > FG_BATCH || ldx < t->cols)
         return fail(c, FGH_ERR_ARG, "gemm_block_ints: bad arguments");
-    if (!prompt_gemm_bytes(t, 8))
+    if (!prompt_gemm_bytes(c, t, 8))
         return fail(c, FGH_ERR_ARG, "gemm_block_ints: the MFMA GEMMs take Q4_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0 and Q5_1 tensors");
     if (nb < 8) return fail(c, FGH_ERR_ARG, "gemm_block_ints: the prompt GEMM runs 8..64 tokens");
     const int64_t nout = t->rows * t->n_mats;

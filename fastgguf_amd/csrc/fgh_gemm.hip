@@ -31,9 +31,14 @@
 // computes, and writes them to the other of two LDS stages before the step's barrier; each
 // wavefront keeps a ring of 4 blocks of its weights in registers (three steps ahead).
 //
+// Short output (fewer row groups than compute units): grid.y = ks K splits of consecutive blocks
+// (gemm_splits); each split's workgroup writes its partial and the last of a row group's splits to
+// arrive adds them in split order.
+//
 // fp32 order: per (row, token) and block t = fma(-dmin, msum, d * float(isum)),
-// acc = fma(yd, t, acc) over the wavefront's blocks; out = acc_half0 + acc_half1. The integers are
-// exact; the fp32 result differs from gemmk_kern's order (fastgguf.c:2765-2797) only by rounding.
+// acc = fma(yd, t, acc) over the wavefront's blocks; out = acc_half0 + acc_half1 (then, with a K
+// split, ((part_0 + part_1) + part_2) + part_3). The integers are exact; the fp32 result differs
+// from gemmk_kern's order (fastgguf.c:2765-2797) only by rounding.
 #include <type_traits>
 
 #include "fgh_internal.h"
@@ -65,8 +70,10 @@ __host__ __device__ constexpr int gemm_rec_bytes(int Tp) { return Tp * 292; }
 // lanes of one token by lane exchanges (no LDS, no barrier); fmaxf ignores NaN, so any order
 // gives the reference's maximum.
 __global__ __launch_bounds__(64) void gemm_quant_kernel(const float *__restrict__ x, int64_t ldx, int T, int Tp,
-                                                        uint8_t *__restrict__ rec) {
+                                                        uint8_t *__restrict__ rec, int32_t *__restrict__ cnt, int ncnt) {
     const int l = threadIdx.x, p = l & 15;
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+        for (int i = l; i < ncnt; i += 64) cnt[i] = 0;  // the K split's arrival counters
     const int b = blockIdx.x, tok = 4 * blockIdx.y + (l >> 4);
     float v[16];
     if (tok < T) {
@@ -111,9 +118,10 @@ __global__ __launch_bounds__(64) void gemm_quant_kernel(const float *__restrict_
     if (p == 0) ((float *)(r + 288 * Tp))[tok] = d;
 }
 
-hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s) {
-    if (T < 1 || T > Tp || Tp % 16 || Tp > 64 || nb < 1) return hipErrorInvalidValue;
-    gemm_quant_kernel<<<dim3((unsigned)nb, (unsigned)(Tp / 4)), 64, 0, s>>>(x, ldx, T, Tp, rec);
+hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, int32_t *cnt, int ncnt,
+                             hipStream_t s) {
+    if (T < 1 || T > Tp || Tp % 16 || Tp > 64 || nb < 1 || ncnt < 0) return hipErrorInvalidValue;
+    gemm_quant_kernel<<<dim3((unsigned)nb, (unsigned)(Tp / 4)), 64, 0, s>>>(x, ldx, T, Tp, rec, cnt, ncnt);
     return hipGetLastError();
 }
 
@@ -166,7 +174,10 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tw = wave % TPW, kh = wave / TPW;
     const int n = l & 15, kg = l >> 4, L = 4 * n + kg;
-    const int nb = a.nb, nsteps = (nb + KH - 1) / KH;
+    // K split ksi of a.ks: blocks [b_lo, b_lo + nbk)
+    const int nb = a.nb, ksi = blockIdx.y, nbs = (nb + a.ks - 1) / a.ks;
+    const int b_lo = ksi * nbs, nbk = min(nb - b_lo, nbs);
+    const int nsteps = (nbk + KH - 1) / KH;
     const int64_t tile = (int64_t)blockIdx.x * TPW + tw;
     const bool live = tile < a.groups;
     const int64_t tc = live ? tile : a.groups - 1;
@@ -174,13 +185,14 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     const size_t bstride = (size_t)a.gpm * 2304;
     const uint8_t *W0 = a.W + ((size_t)mi * nb * a.gpm + (size_t)ti) * 2304;
 
-    // the step's records: a linear copy of KH records from block KH s (the quantizer's buffer
-    // holds a record of slack past the last block); round k of thread t copies unit k * NTH + t,
+    // the step's records: a linear copy of KH records from block b_lo + KH s (the quantizer's
+    // buffer holds a record of slack past the last block); round k of thread t copies unit k * NTH + t,
     // so each wavefront load reads 1 KB contiguous and each LDS write is conflict-free
     static_assert(R >= 1 && R <= 10, "one step's records take 1..10 rounds per thread");
     auto aload = [&](int s, ARec &ar) {
         // the base moves in scalar registers; reads past the step's KH records return 0
-        const BufRes src = buf_res(a.act + (size_t)min(s, nsteps - 1) * KH * REC, KH * REC);
+        const int s2 = b_lo + KH * min(s, nsteps - 1), avail = min(KH, nb + 1 - s2);  // >= 2 records
+        const BufRes src = buf_res(a.act + (size_t)s2 * REC, avail * REC);
         auto ld = [&](int k) { return bld16(src, 16 * (k * NTH + tid)); };
         ar.v0 = ld(0);
         if (R > 1) ar.v1 = ld(1);
@@ -207,7 +219,7 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
         if (R > 9) dst[9 * NTH] = ar.v9;
     };
     auto wload = [&](int s, GW &w) {
-gw_load(W0 + (size_t)min(KH * s + kh, nb - 1) * bstride, L, n, w); };
+gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
 
     v4f acc[NT];
 #pragma unroll
@@ -329,14 +341,14 @@ gw_load(W0 + (size_t)min(KH * s + kh, nb - 1) * bstride, L, n, w); };
     // branch, so the compiler's load counters stay exact across them (a branch makes it wait for
     // every outstanding load, the prefetches included, at the next block); the last steps test.
     auto step = [&](auto full, int s, GW &wc, GW &wn3, const uint8_t *stc, uint8_t *stn) {
-        const int b = KH * s + kh;
+        const int b = b_lo + KH * s + kh;
         auto issue = [&](int i) {
             __builtin_amdgcn_sched_barrier(0);
             if (i == 0) aload(s + 1, rr);
             if (i == 2) wload(s + 3, wn3);
             __builtin_amdgcn_sched_barrier(0);
         };
-        if (decltype(full)::value || b < nb) {  // uniform per wavefront
+        if (decltype(full)::value || b < b_lo + nbk) {  // uniform per wavefront
             block(wc, stc, g, issue);
             epilogue(g, stc, b);
         } else {
@@ -349,7 +361,7 @@ gw_load(W0 + (size_t)min(KH * s + kh, nb - 1) * bstride, L, n, w); };
     };
     using Full = std::true_type;
     using Edge = std::false_type;
-    const int nfull = nb / KH;  // steps with a block for every K-half
+    const int nfull = nbk / KH;  // steps with a block for every K-half
     int s = 0;
     for (; s + 4 <= nfull; s += 4) {
         step(Full(), s, w0, w3, st0, st1);
@@ -363,18 +375,79 @@ gw_load(W0 + (size_t)min(KH * s + kh, nb - 1) * bstride, L, n, w); };
     if (s + 2 < nsteps) step(Edge(), s + 2, w2, w1, st0, st1);
     if (s + 3 < nsteps) step(Edge(), s + 3, w3, w2, st1, st0);
     __syncthreads();  // every wavefront is past its reads of the stages (the reduction reuses them)
-    if (KH == 2) {  // half 1 -> LDS, half 0 adds it in order and stores
+    if (KH == 2) {  // half 1 -> LDS, half 0 adds it in order
         float *red = (float *)smem + (size_t)tw * 64 * 4 * NT;  // TPW * 4 KB * NT <= one stage
         if (kh == 1) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) *(v4f *)(red + (size_t)(t * 64 + l) * 4) = acc[t];
         }
         __syncthreads();
-        if (kh == 1) return;
+        if (kh == 0) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t] += *(const v4f *)(red + (size_t)(t * 64 + l) * 4);
+            for (int t = 0; t < NT; ++t) acc[t] += *(const v4f *)(red + (size_t)(t * 64 + l) * 4);
+        }
     }
-    if (store) {
+    if (a.ks > 1) {
+        // K split: publish this split's partial; the tile group's last split to arrive adds all of
+        // them in split order (whichever arrives last, the sum is the same). The partials are
+        // written and read as agent-scope atomics (write-through stores, loads that miss the L2 of
+        // the reading XCD), and each wavefront waits until its stores have completed before the
+        // workgroup's arrival increment, so the last arriver reads every partial from memory. An
+        // agent-scope release instead writes back the whole L2 of the workgroup's XCD (measured
+        // slower: 39.6 us against 36.9 us at 64 x 14336 -> 4096).
+        const size_t pstride = (size_t)a.T * a.nrows;
+        if (kh == 0 && store) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int tok = 16 * t + 4 * kg + r;
+                    if (tok < a.T)
+                        __hip_atomic_store(a.part + ksi * pstride + (size_t)tok * a.nrows + orow, acc[t][r],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+        }
+        // every wavefront's partial stores complete before thread 0's arrival increment
+        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt 0
+        __syncthreads();
+        int *flag = (int *)smem + 4096;  // past the reduction area
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(&a.cnt[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *flag = old == a.ks - 1;
+        }
+        __syncthreads();
+        if (!*flag || kh != 0 || !store) return;
+        // every partial of the lane's outputs loaded first (all in flight together; loading each
+        // just before its add took one memory round trip per output: 36.9 -> 27.4 us), then the sums
+        float pv[4][NT][4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int tok = 16 * t + 4 * kg + r;
+                    pv[k][t][r] = 0.0f;
+                    if (k < a.ks && k != ksi && tok < a.T)
+                        pv[k][t][r] = __hip_atomic_load(a.part + k * pstride + (size_t)tok * a.nrows + orow,
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = 16 * t + 4 * kg + r;
+                if (tok < a.T) {
+                    float v = ksi == 0 ? acc[t][r] : pv[0][t][r];
+#pragma unroll
+                    for (int k = 1; k < 4; ++k)
+                        if (k < a.ks) v += ksi == k ? acc[t][r] : pv[k][t][r];
+                    a.Y[(size_t)tok * a.ldy + orow] = v;
+                }
+            }
+        return;
+    }
+    if (kh == 0 && store) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -398,7 +471,7 @@ size_t gemm_act_bytes(int nb, int Tp) { return (size_t)(nb + 1) * gemm_rec_bytes
 template <int NT, int KH>
 static void gemm_launch(const GemmArgs &a, hipStream_t s) {
     constexpr int TPW = GEMM_TPW;
-    const dim3 grid((unsigned)((a.groups + TPW - 1) / TPW));
+    const dim3 grid((unsigned)((a.groups + TPW - 1) / TPW), (unsigned)a.ks);
     const size_t lds = gemm_lds<NT, KH>(TPW);
     if (a.dump_s) q4k_gemm_kernel<NT, KH, TPW, true><<<grid, 64 * TPW * KH, lds, s>>>(a);
     else q4k_gemm_kernel<NT, KH, TPW, false><<<grid, 64 * TPW * KH, lds, s>>>(a);
@@ -409,9 +482,29 @@ static void gemm_launch_kh(const GemmArgs &a, hipStream_t s) {
     else gemm_launch<NT, 1>(a, s);
 }
 
+// K splits: as many (up to 4) as still give each workgroup its own compute unit, each split at
+// least 4 blocks. Row counts below 64 x the compute units (the down projection 14336 -> 4096: 64
+// workgroups) otherwise leave most units idle.
+int gemm_splits(int64_t groups, int nb, int num_cu) {
+    const int64_t wg = (groups + GEMM_TPW - 1) / GEMM_TPW;
+    int ks = 1;
+    while (ks < 4 && wg * (ks + 1) <= num_cu && nb / (ks + 1) >= 4) ++ks;
+    return ks;
+}
+static size_t up256(size_t n) { return (n + 255) / 256 * 256; }
+GemmScratch gemm_scratch(int64_t groups, int64_t nrows, int nb, int T, int num_cu) {
+    GemmScratch g;
+    g.ks = gemm_splits(groups, nb, num_cu);
+    g.ncnt = g.ks > 1 ? (int)((groups + GEMM_TPW - 1) / GEMM_TPW) : 0;
+    g.cnt_off = up256(gemm_act_bytes(nb, (T + 15) / 16 * 16));
+    g.part_off = g.cnt_off + up256((size_t)g.ncnt * 4);
+    g.bytes = g.ks > 1 ? g.part_off + (size_t)g.ks * T * nrows * 4 : gemm_act_bytes(nb, (T + 15) / 16 * 16);
+    return g;
+}
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > a.Tp || a.Tp % 16 || a.Tp > 64 || a.Tp - a.T >= 16 || a.nb < 1 || a.groups < 1)
         return hipErrorInvalidValue;
+    if (a.ks < 1 || a.ks > 4 || (a.ks > 1 && (!a.part || !a.cnt))) return hipErrorInvalidValue;
     switch (a.Tp / 16) {
     case 1: gemm_launch_kh<1>(a, s); break;
     case 2: gemm_launch_kh<2>(a, s); break;

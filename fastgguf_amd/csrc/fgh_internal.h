@@ -511,6 +511,9 @@ struct GemmArgs {
     int Tp, T;             // padded token count (a multiple of 16, Tp - T < 16), tokens
     int64_t ldy;
     int32_t *dump_s, *dump_m;  // test hook: [T][nrows][nb] integers, or null
+    int ks;                    // K splits (grid.y); ks > 1: partials [ks][T][nrows] and counters
+    float *part;
+    int32_t *cnt;
 };
 // the Q8_0 prompt GEMM (fgh_gemm32.hip) on the decode tiles (8-row tiles, 4 blocks per tile step)
 struct Gemm32Args {
@@ -572,8 +575,16 @@ size_t gemm6_act_bytes(int nb, int Tp);
 hipError_t launch_q6k_gemm(const Gemm6Args &a, hipStream_t s);
 
 // quantizes T rows of x (stride ldx) into the GEMM's activation records (gemm_act_bytes(nb, Tp))
-hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s);
+// and zeroes the K split's ncnt arrival counters (cnt may be null when ncnt is 0)
+hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, int32_t *cnt, int ncnt,
+                             hipStream_t s);
 size_t gemm_act_bytes(int nb, int Tp);
+// the Q4_K prompt GEMM's scratch: records, then (ks > 1) ncnt arrival counters and the partials
+struct GemmScratch {
+    int ks, ncnt;
+    size_t cnt_off, part_off, bytes;
+};
+GemmScratch gemm_scratch(int64_t groups, int64_t nrows, int nb, int T, int num_cu);
 constexpr size_t GEMM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
 // true when all wg workgroups of a launch (waves wavefronts and lds bytes each) can be resident
 // on num_cu CUs at once: a split launch whose workgroups need a second round is slower than a

@@ -210,14 +210,16 @@ FGH_API int fgh_matmul_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *X_dev
                    int ldy, int nb);
 /* fgh_matmul_dev without any device allocation. No counterpart in the reference: it is for
  * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
- * that forbid hipMalloc). The prompt GEMM's activation records (nb >= 8 tokens of a Q4_K tensor:
- * (blocks + 1) * 292 * (nb rounded up to 16) bytes) go to a static device array of
- * FGH_NOALLOC_SCRATCH_BYTES per device, held until the process ends; a call that would need more
- * fails with FGH_ERR_ARG before it launches anything. Every call on a device shares that device's
- * array: calls that overlap on one device (several streams or contexts) race. Nothing in the
- * array needs to start at zero; each call writes what it reads. Same results bit for bit as
- * fgh_matmul_dev. */
-#define FGH_NOALLOC_SCRATCH_BYTES (4u << 20)
+ * that forbid hipMalloc). The prompt GEMM's scratch (nb >= 8 tokens of a Q4_K tensor: the
+ * activation records, (blocks + 1) * 292 * (nb rounded up to 16) bytes, and for a tensor with
+ * fewer 64-row groups than half the compute units the K split's counters and partials, at most
+ * 4 MiB) goes to a static device array of FGH_NOALLOC_SCRATCH_BYTES per device, held until the
+ * process ends; a call that would need more fails with FGH_ERR_ARG before it launches anything.
+ * Every call on a device shares that device's array: calls that overlap on one device (several
+ * streams or contexts) race. Nothing in the array needs to start at zero; each call writes what
+ * it reads (the split's counters are zeroed by the call's own first launch). Same results bit for
+ * bit as fgh_matmul_dev. */
+#define FGH_NOALLOC_SCRATCH_BYTES (8u << 20)
 FGH_API int fgh_matmul_dev_noalloc(fgh_ctx *ctx, const fgh_tensor *t, const float *X_dev, int ldx,
                            float *Y_dev, int ldy, int nb);
 FGH_API int fgh_moe_ffn_dev(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tensor *up,

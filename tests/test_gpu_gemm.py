@@ -61,14 +61,15 @@ def test_matmul_matches_golden(backend, name, t, nb):
         tt.free()
 
 
-GEMM_CASES = [  # (rows, cols, n_mats, tokens)
+GEMM_CASES = [  # (rows, cols, n_mats, tokens); K splits (few row groups) as noted
     (64, 256, 1, 8),        # one block, one workgroup
     (100, 512, 1, 31),      # ragged rows, one token tile
     (128, 1024, 1, 32),
     (72, 768, 1, 33),       # odd block count, two token tiles
-    (21, 2048, 3, 45),      # 3-D, ragged rows per matrix
-    (64, 4096, 1, 64),
-    (16, 14336, 1, 64),     # 56 blocks
+    (21, 2048, 3, 45),      # 3-D, ragged rows per matrix; 2 K splits of 4 blocks
+    (48, 3072, 1, 17),      # 3 K splits of 4 blocks
+    (64, 4096, 1, 64),      # 4 K splits of 4 blocks
+    (16, 14336, 1, 64),     # 56 blocks, 4 K splits of 14
 ]
 
 
@@ -246,6 +247,23 @@ def test_prefill_config_shape(backend, oracle):
     # a second call with fewer tokens reuses the buffers
     Y2 = backend.matmul(tt, X[:9])
     check_tokens(Y2, oracle.matmul(S.T_Q4_K, w, cols, X[:9], O_RP))
+    tt.free()
+
+
+def test_prefill_down_shape(backend, oracle):
+    """The FFN down projection of a 64-token prompt, 64 tokens x K=14336 -> N=4096 (Q4_K): 64 row
+    groups for 256 compute units, so the GEMM runs 4 K splits whose last arriver adds the partials
+    in split order; within tolerance of gemm_kquant, and every call gives the same bits (the
+    arrival order does not enter the sum)."""
+    rows, cols, T = 4096, 14336, 64
+    w = S.weights(S.T_Q4_K, rows, cols, 92)
+    X = S.activations(cols, 93, rows=T)
+    tt = backend.upload(S.T_Q4_K, cols, w)
+    Y = backend.matmul(tt, X)
+    check_tokens(Y, oracle.matmul(S.T_Q4_K, w, cols, X, O_RP))
+    for _ in range(3):
+        assert bits_equal(backend.matmul(tt, X), Y)
+    check_tokens(backend.matmul(tt, X[:9]), oracle.matmul(S.T_Q4_K, w, cols, X[:9], O_RP))
     tt.free()
 
 

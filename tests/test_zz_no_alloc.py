@@ -13,7 +13,7 @@ from fastgguf_amd.backend import Backend, BackendError
 pytestmark = pytest.mark.gpu
 
 FGH_ERR_ARG = -2
-SCRATCH_BYTES = 4 << 20  # FGH_NOALLOC_SCRATCH_BYTES
+SCRATCH_BYTES = 8 << 20  # FGH_NOALLOC_SCRATCH_BYTES
 
 
 def run_both(be, t, X):
@@ -61,19 +61,35 @@ def test_noalloc_matches_matmul_dev(backend, fresh):
             be.close()
 
 
+def q4k_gemm_scratch(rows, nbk, T, num_cu=256):
+    """bytes of the Q4_K prompt GEMM's scratch: (nbk + 1) activation records of 292 * Tp bytes, and
+    with a K split (few row groups) 256 bytes of arrival counters and ks partials of T x rows fp32"""
+    wg = -(-rows // 64)
+    ks = 1
+    while ks < 4 and wg * (ks + 1) <= num_cu and nbk // (ks + 1) >= 4:
+        ks += 1
+    rec = (nbk + 1) * 292 * (-(-T // 16) * 16)
+    if ks == 1:
+        return rec
+    up = lambda n: -(-n // 256) * 256
+    return up(rec) + up(4 * wg) + ks * T * rows * 4
+
+
 def test_noalloc_refuses_more_than_its_scratch(backend):
-    """224 blocks x 64 tokens need (224 + 1) * 292 * 64 bytes > 4 MiB: refused, nothing launched;
-    223 blocks fit and run"""
+    """4096 rows at 64 tokens (the down projection's output width, a 4-way K split): 223 blocks
+    need 224 records of 292 * 64 bytes plus the split's counters and 4 MiB of partials, within
+    8 MiB, and run; 224 blocks exceed it: refused, nothing launched, and the context still works"""
+    rows = 4096
     for nbk, ok in ((223, True), (224, False)):
         cols = 256 * nbk
-        assert ((nbk + 1) * 292 * 64 <= SCRATCH_BYTES) == ok
-        t = backend.upload(S.T_Q4_K, cols, S.weights(S.T_Q4_K, 16, cols, 720 + nbk))
+        assert (q4k_gemm_scratch(rows, nbk, 64) <= SCRATCH_BYTES) == ok
+        t = backend.upload(S.T_Q4_K, cols, S.weights(S.T_Q4_K, rows, cols, 720 + nbk))
         X = S.activations(cols, 730, rows=64)
         if ok:
             got, want = run_both(backend, t, X)
             assert bits_equal(got, want)
         else:
-            xd, yd = backend.dev_alloc(X.nbytes), backend.dev_alloc(4 * 64 * 16)
+            xd, yd = backend.dev_alloc(X.nbytes), backend.dev_alloc(4 * 64 * rows)
             with pytest.raises(BackendError) as e:
                 backend.matmul_dev_noalloc(t, xd, yd, 64)
             assert e.value.status == FGH_ERR_ARG and "scratch" in str(e.value)
