@@ -309,12 +309,23 @@ static bool q32n_type(uint32_t type) {
 // the prompt GEMM for a Q6_K tensor (gemm_kquant's Q6_K branch, fastgguf.c:2704-2725, 2818-2854):
 // Q8_K records of T tokens, then one MFMA launch on the decode tiles; ds / dm: optional
 // [T][rows * n_mats][nb] integer dump
+// the Q6_K GEMM's scratch (16-row tiles: pairs of the decode layout's 8-row tiles)
+static fgh::GemmScratch q6k_scratch(const fgh_ctx *c, const fgh_tensor *t, int T) {
+    const int64_t groups16 = (t->gpm + 1) / 2 * t->n_mats;
+    return fgh::gemm_split_scratch(fgh::gemm6_act_bytes(t->nb, (T + 15) / 16 * 16), groups16, t->rows * t->n_mats,
+                                   t->nb, T, c->num_cu);
+}
 static int gemm_q6k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
                          uint8_t *act, int32_t *ds, int32_t *dm) {
     const int Tp = (T + 15) / 16 * 16;
-    HIP_TRY(c, fgh::launch_gemm6_quant(X, ldx, t->nb, T, Tp, act, c->stream));
+    const fgh::GemmScratch gs = q6k_scratch(c, t, T);
+    int32_t *cnt = gs.ks > 1 ? (int32_t *)(act + gs.cnt_off) : nullptr;
+    HIP_TRY(c, fgh::launch_gemm6_quant(X, ldx, t->nb, T, Tp, act, cnt, gs.ncnt, c->stream));
     fgh::Gemm6Args a;
     memset(&a, 0, sizeof(a));
+    a.ks = gs.ks;
+    a.cnt = cnt;
+    a.part = gs.ks > 1 ? (float *)(act + gs.part_off) : nullptr;
     a.W = t->dev;
     a.Y = Y;
     a.rows = t->rows;
@@ -339,7 +350,7 @@ static size_t prompt_gemm_bytes(const fgh_ctx *c, const fgh_tensor *t, int T) {
     if (T < 8) return 0;
     if (t->type == FGH_T_Q4_K) return fgh::gemm_scratch(t->groups, t->rows * t->n_mats, t->nb, T, c->num_cu).bytes;
     if (t->type == FGH_T_Q8_0) return fgh::gemm32_act_bytes(t->nb, T <= 32 ? 32 : 64);
-    if (t->type == FGH_T_Q6_K) return fgh::gemm6_act_bytes(t->nb, (T + 15) / 16 * 16);
+    if (t->type == FGH_T_Q6_K) return q6k_scratch(c, t, T).bytes;
     if (q32n_type(t->type)) return fgh::gemmn_act_bytes(t->nb, (T + 15) / 16 * 16);
     return 0;
 }

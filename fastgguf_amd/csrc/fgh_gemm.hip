@@ -387,64 +387,9 @@ gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
             for (int t = 0; t < NT; ++t) acc[t] += *(const v4f *)(red + (size_t)(t * 64 + l) * 4);
         }
     }
-    if (a.ks > 1) {
-        // K split: publish this split's partial; the tile group's last split to arrive adds all of
-        // them in split order (whichever arrives last, the sum is the same). The partials are
-        // written and read as agent-scope atomics (write-through stores, loads that miss the L2 of
-        // the reading XCD), and each wavefront waits until its stores have completed before the
-        // workgroup's arrival increment, so the last arriver reads every partial from memory. An
-        // agent-scope release instead writes back the whole L2 of the workgroup's XCD (measured
-        // slower: 39.6 us against 36.9 us at 64 x 14336 -> 4096).
-        const size_t pstride = (size_t)a.T * a.nrows;
-        if (kh == 0 && store) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int tok = 16 * t + 4 * kg + r;
-                    if (tok < a.T)
-                        __hip_atomic_store(a.part + ksi * pstride + (size_t)tok * a.nrows + orow, acc[t][r],
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-        }
-        // every wavefront's partial stores complete before thread 0's arrival increment
-        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt 0
-        __syncthreads();
-        int *flag = (int *)smem + 4096;  // past the reduction area
-        if (tid == 0) {
-            const int old = __hip_atomic_fetch_add(&a.cnt[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *flag = old == a.ks - 1;
-        }
-        __syncthreads();
-        if (!*flag || kh != 0 || !store) return;
-        // every partial of the lane's outputs loaded first (all in flight together; loading each
-        // just before its add took one memory round trip per output: 36.9 -> 27.4 us), then the sums
-        float pv[4][NT][4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int tok = 16 * t + 4 * kg + r;
-                    pv[k][t][r] = 0.0f;
-                    if (k < a.ks && k != ksi && tok < a.T)
-                        pv[k][t][r] = __hip_atomic_load(a.part + k * pstride + (size_t)tok * a.nrows + orow,
-                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tok = 16 * t + 4 * kg + r;
-                if (tok < a.T) {
-                    float v = ksi == 0 ? acc[t][r] : pv[0][t][r];
-#pragma unroll
-                    for (int k = 1; k < 4; ++k)
-                        if (k < a.ks) v += ksi == k ? acc[t][r] : pv[k][t][r];
-                    a.Y[(size_t)tok * a.ldy + orow] = v;
-                }
-            }
+    if (a.ks > 1) {  // the K split's partials (the reduction's LDS area is done with)
+        gemm_split_finish<NT>(acc, kh == 0 && store, tid, kg, orow, a.ks, ksi, a.T, a.nrows, a.ldy, a.part, a.cnt, a.Y,
+                              (int *)smem + 4096);
         return;
     }
     if (kh == 0 && store) {
@@ -492,14 +437,17 @@ int gemm_splits(int64_t groups, int nb, int num_cu) {
     return ks;
 }
 static size_t up256(size_t n) { return (n + 255) / 256 * 256; }
-GemmScratch gemm_scratch(int64_t groups, int64_t nrows, int nb, int T, int num_cu) {
+GemmScratch gemm_split_scratch(size_t rec_bytes, int64_t groups, int64_t nrows, int nb, int T, int num_cu) {
     GemmScratch g;
     g.ks = gemm_splits(groups, nb, num_cu);
     g.ncnt = g.ks > 1 ? (int)((groups + GEMM_TPW - 1) / GEMM_TPW) : 0;
-    g.cnt_off = up256(gemm_act_bytes(nb, (T + 15) / 16 * 16));
+    g.cnt_off = up256(rec_bytes);
     g.part_off = g.cnt_off + up256((size_t)g.ncnt * 4);
-    g.bytes = g.ks > 1 ? g.part_off + (size_t)g.ks * T * nrows * 4 : gemm_act_bytes(nb, (T + 15) / 16 * 16);
+    g.bytes = g.ks > 1 ? g.part_off + (size_t)g.ks * T * nrows * 4 : rec_bytes;
     return g;
+}
+GemmScratch gemm_scratch(int64_t groups, int64_t nrows, int nb, int T, int num_cu) {
+    return gemm_split_scratch(gemm_act_bytes(nb, (T + 15) / 16 * 16), groups, nrows, nb, T, num_cu);
 }
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > a.Tp || a.Tp % 16 || a.Tp > 64 || a.Tp - a.T >= 16 || a.nb < 1 || a.groups < 1)

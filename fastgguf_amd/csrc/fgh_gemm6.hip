@@ -55,8 +55,10 @@ __host__ __device__ constexpr int gemm6_rec_bytes(int Tp) { return Tp * 292; }
 // block (scale group p). The block maximum combines the token's 16 lanes by lane exchanges; fmaxf
 // ignores NaN, so any order gives the reference's maximum.
 __global__ __launch_bounds__(64) void gemm6_quant_kernel(const float *__restrict__ x, int64_t ldx, int T, int Tp,
-                                                         uint8_t *__restrict__ rec) {
+                                                         uint8_t *__restrict__ rec, int32_t *__restrict__ cnt, int ncnt) {
     const int l = threadIdx.x, p = l & 15;
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+        for (int i = l; i < ncnt; i += 64) cnt[i] = 0;  // the K split's arrival counters
     const int b = blockIdx.x, tok = 4 * blockIdx.y + (l >> 4);
     float v[16];
     if (tok < T) {
@@ -98,9 +100,11 @@ __global__ __launch_bounds__(64) void gemm6_quant_kernel(const float *__restrict
     if (p == 0) ((float *)(r + 256 * Tp))[tok] = d;
 }
 
-hipError_t launch_gemm6_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s) {
+hipError_t launch_gemm6_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, int32_t *cnt, int ncnt,
+                              hipStream_t s) {
+    if (ncnt < 0) return hipErrorInvalidValue;
     if (T < 1 || T > Tp || Tp % 16 || Tp > 64 || nb < 1) return hipErrorInvalidValue;
-    gemm6_quant_kernel<<<dim3((unsigned)nb, (unsigned)(Tp / 4)), 64, 0, s>>>(x, ldx, T, Tp, rec);
+    gemm6_quant_kernel<<<dim3((unsigned)nb, (unsigned)(Tp / 4)), 64, 0, s>>>(x, ldx, T, Tp, rec, cnt, ncnt);
     return hipGetLastError();
 }
 
@@ -168,7 +172,10 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tw = wave % TPW, kh = wave / TPW;
     const int n = l & 15, kg = l >> 4, r8 = n & 7, dt = n >> 3;
-    const int nb = a.nb, nsteps = (nb + KH - 1) / KH;
+    // K split ksi of a.ks (grid.y): blocks [b_lo, b_lo + nbk)
+    const int nb = a.nb, ksi = blockIdx.y, nbs = (nb + a.ks - 1) / a.ks;
+    const int b_lo = ksi * nbs, nbk = min(nb - b_lo, nbs);
+    const int nsteps = (nbk + KH - 1) / KH;
     const int64_t tile = (int64_t)blockIdx.x * TPW + tw;
     const bool live = tile < a.groups;
     const int64_t tc = live ? tile : a.groups - 1;
@@ -182,7 +189,9 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     const uint32_t scoff = toff + 16 * r8, doff = toff + 128 + 2 * r8;
 
     auto aload = [&](int s, ARec6 &ar) __attribute__((always_inline)) {
-        const BufRes src = buf_res(a.act + (size_t)min(s, nsteps - 1) * KH * REC, KH * REC);
+        // KH records from block b_lo + KH s (the buffer holds a record of slack past the last block)
+        const int s2 = b_lo + KH * min(s, nsteps - 1), avail = min(KH, nb + 1 - s2);  // >= 2 records
+        const BufRes src = buf_res(a.act + (size_t)s2 * REC, avail * REC);
         auto ld = [&](int k) __attribute__((always_inline)) { return bld16(src, 16 * (k * NTH + tid)); };
         ar.v0 = ld(0);
         if (R > 1) ar.v1 = ld(1);
@@ -208,9 +217,10 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
         if (R > 8) dst[8 * NTH] = ar.v8;
         if (R > 9) dst[9 * NTH] = ar.v9;
     };
-    // block KH s + kh of the tile pair; reads past the valid tiles (a matrix's last pair) return 0
+    // block b_lo + KH s + kh of the tile pair; reads past the valid tiles (a matrix's last pair)
+    // return 0
     auto wload = [&](int s, GW6 &w) __attribute__((always_inline)) {
-        const int b = min(KH * s + kh, nb - 1);
+        const int b = b_lo + min(KH * s + kh, nbk - 1);
         const BufRes r = buf_res(a.W + ((size_t)(mi * nb + b) * a.tpm + 2 * ti) * Q6K_TILE, nvalid * Q6K_TILE);
         w.ql0 = bld16v(r, qloff);
         w.ql1 = bld16v(r, qloff + 16);
@@ -307,14 +317,14 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     // then the epilogue, the records to the other stage, the barrier. Steps with a block for every
     // K-half run without branches (exact load counters); the last may test.
     auto step = [&](auto full, int s, GW6 &wc, GW6 &wn3, const uint8_t *stc, uint8_t *stn) __attribute__((always_inline)) {
-        const int b = KH * s + kh;
+        const int b = b_lo + KH * s + kh;
         auto issue = [&](int i) __attribute__((always_inline)) {
             __builtin_amdgcn_sched_barrier(0);
             if (i == 0) aload(s + 1, rr);
             if (i == 2) wload(s + 3, wn3);
             __builtin_amdgcn_sched_barrier(0);
         };
-        if (decltype(full)::value || b < nb) {  // uniform per wavefront
+        if (decltype(full)::value || b < b_lo + nbk) {  // uniform per wavefront
             block(wc, stc, g, issue);
             epilogue(g, wc, stc, b);
         } else {
@@ -327,7 +337,7 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     };
     using Full = std::true_type;
     using Edge = std::false_type;
-    const int nfull = nb / KH;
+    const int nfull = nbk / KH;
     int s = 0;
     for (; s + 4 <= nfull; s += 4) {
         step(Full(), s, w0, w3, st0, st1);
@@ -340,18 +350,24 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     if (s + 2 < nsteps) step(Edge(), s + 2, w2, w1, st0, st1);
     if (s + 3 < nsteps) step(Edge(), s + 3, w3, w2, st1, st0);
     __syncthreads();  // every wavefront is past its reads of the stages (the reduction reuses them)
-    if (KH == 2) {  // half 1 -> LDS, half 0 adds it in order and stores
-        float *red = (float *)smem + (size_t)tw * 64 * 4 * NT;
+    if (KH == 2) {  // half 1 -> LDS, half 0 adds it in order
+        float *red = (float *)smem + (size_t)tw * 64 * 4 * NT;  // TPW * 4 KB * NT <= one stage
         if (kh == 1) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) *(v4f *)(red + (size_t)(t * 64 + l) * 4) = acc[t];
         }
         __syncthreads();
-        if (kh == 1) return;
+        if (kh == 0) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t] += *(const v4f *)(red + (size_t)(t * 64 + l) * 4);
+            for (int t = 0; t < NT; ++t) acc[t] += *(const v4f *)(red + (size_t)(t * 64 + l) * 4);
+        }
     }
-    if (store) {
+    if (a.ks > 1) {  // the K split's partials (the reduction's LDS area is done with)
+        gemm_split_finish<NT>(acc, kh == 0 && store, tid, kg, orow, a.ks, ksi, a.T, a.nrows, a.ldy, a.part, a.cnt, a.Y,
+                              (int *)smem + 4096);
+        return;
+    }
+    if (kh == 0 && store) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -374,7 +390,7 @@ size_t gemm6_act_bytes(int nb, int Tp) { return (size_t)(nb + 1) * gemm6_rec_byt
 
 template <int NT, int KH>
 static void gemm6_launch(const Gemm6Args &a, hipStream_t s) {
-    const dim3 grid((unsigned)((a.groups + GEMM6_TPW - 1) / GEMM6_TPW));
+    const dim3 grid((unsigned)((a.groups + GEMM6_TPW - 1) / GEMM6_TPW), (unsigned)a.ks);
     const size_t lds = gemm6_lds<NT, KH>();
     if (a.dump_s) q6k_gemm_kernel<NT, KH, GEMM6_TPW, true><<<grid, 64 * GEMM6_TPW * KH, lds, s>>>(a);
     else q6k_gemm_kernel<NT, KH, GEMM6_TPW, false><<<grid, 64 * GEMM6_TPW * KH, lds, s>>>(a);
@@ -389,6 +405,7 @@ hipError_t launch_q6k_gemm(const Gemm6Args &a, hipStream_t s) {
     if (a.T < 1 || a.T > a.Tp || a.Tp % 16 || a.Tp > 64 || a.Tp - a.T >= 16 || a.nb < 1 || a.groups < 1 ||
         a.gpm16 != (a.tpm + 1) / 2)
         return hipErrorInvalidValue;
+    if (a.ks < 1 || a.ks > 4 || (a.ks > 1 && (!a.part || !a.cnt))) return hipErrorInvalidValue;
     switch (a.Tp / 16) {
     case 1: gemm6_launch_kh<1>(a, s); break;
     case 2: gemm6_launch_kh<2>(a, s); break;

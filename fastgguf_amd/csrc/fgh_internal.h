@@ -569,8 +569,13 @@ struct Gemm6Args {
     int Tp, T;             // padded token count (a multiple of 16, Tp - T < 16), tokens
     int64_t ldy;
     int32_t *dump_s, *dump_m;  // test hook: [T][nrows][nb] sumi / msum, or null
+    int ks;                    // K splits (grid.y); ks > 1: partials [ks][T][nrows] and counters
+    float *part;
+    int32_t *cnt;
 };
-hipError_t launch_gemm6_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s);
+// the Q6_K GEMM's records (gemm6_act_bytes(nb, Tp)); zeroes the K split's ncnt counters
+hipError_t launch_gemm6_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, int32_t *cnt, int ncnt,
+                              hipStream_t s);
 size_t gemm6_act_bytes(int nb, int Tp);
 hipError_t launch_q6k_gemm(const Gemm6Args &a, hipStream_t s);
 
@@ -579,12 +584,73 @@ hipError_t launch_q6k_gemm(const Gemm6Args &a, hipStream_t s);
 hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, int32_t *cnt, int ncnt,
                              hipStream_t s);
 size_t gemm_act_bytes(int nb, int Tp);
-// the Q4_K prompt GEMM's scratch: records, then (ks > 1) ncnt arrival counters and the partials
+// the scratch of a prompt GEMM on 16-row tiles, 4 per workgroup (Q4_K, Q6_K): its activation
+// records (rec_bytes), then, when it splits K (ks > 1), ncnt arrival counters and the partials
+// [ks][T][nrows]
 struct GemmScratch {
     int ks, ncnt;
     size_t cnt_off, part_off, bytes;
 };
-GemmScratch gemm_scratch(int64_t groups, int64_t nrows, int nb, int T, int num_cu);
+GemmScratch gemm_split_scratch(size_t rec_bytes, int64_t groups, int64_t nrows, int nb, int T, int num_cu);
+GemmScratch gemm_scratch(int64_t groups, int64_t nrows, int nb, int T, int num_cu);  // Q4_K's
+
+typedef float gemm_v4f __attribute__((ext_vector_type(4)));
+// The end of a K-split prompt GEMM workgroup (grid.y = ks splits of consecutive blocks; blockIdx.x
+// = the row group): lane (kg, n) of a storing wavefront (mine) holds output row orow for tokens
+// 16 t + 4 kg + r in acc[t][r]. The split's partial goes to part as agent-scope atomic stores
+// (write-through); every wavefront waits until its stores have completed, then thread 0 bumps the
+// row group's counter. The last split to arrive loads every other partial (agent-scope loads, all
+// in flight at once) and writes Y = ((p_0 + p_1) + p_2) + p_3, in split order whichever arrives
+// last. Every wavefront of the workgroup calls it (two barriers); flag is one int of LDS.
+template <int NT>
+__device__ __forceinline__ void gemm_split_finish(const gemm_v4f (&acc)[NT], bool mine, int tid, int kg, int64_t orow,
+                                                  int ks, int ksi, int T, int64_t nrows, int64_t ldy, float *part,
+                                                  int32_t *cnt, float *Y, int *flag) {
+    const size_t pstride = (size_t)T * nrows;
+    if (mine) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = 16 * t + 4 * kg + r;
+                if (tok < T)
+                    __hip_atomic_store(part + ksi * pstride + (size_t)tok * nrows + orow, acc[t][r], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+    }
+    __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt 0: this wavefront's partial stores have completed
+    __syncthreads();
+    if (tid == 0)
+        *flag = __hip_atomic_fetch_add(&cnt[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ks - 1;
+    __syncthreads();
+    if (!*flag || !mine) return;
+    float pv[4][NT][4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = 16 * t + 4 * kg + r;
+                pv[k][t][r] = 0.0f;
+                if (k < ks && k != ksi && tok < T)
+                    pv[k][t][r] = __hip_atomic_load(part + k * pstride + (size_t)tok * nrows + orow, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = 16 * t + 4 * kg + r;
+            if (tok < T) {
+                float v = ksi == 0 ? acc[t][r] : pv[0][t][r];
+#pragma unroll
+                for (int k = 1; k < 4; ++k)
+                    if (k < ks) v += ksi == k ? acc[t][r] : pv[k][t][r];
+                Y[(size_t)tok * ldy + orow] = v;
+            }
+        }
+}
 constexpr size_t GEMM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
 // true when all wg workgroups of a launch (waves wavefronts and lds bytes each) can be resident
 // on num_cu CUs at once: a split launch whose workgroups need a second round is slower than a

@@ -191,9 +191,10 @@ Q6K_CASES = [  # (rows, cols, n_mats, tokens): K-halves 1 (one block) and 2 (odd
     (16, 256, 1, 8),
     (40, 512, 1, 16),
     (100, 768, 1, 31),      # 13 tiles: the last pair has one tile
-    (24, 2048, 3, 45),      # 3 tiles per matrix
-    (64, 4096, 1, 64),
-    (8, 14336, 1, 33),      # 56 blocks, one tile
+    (24, 2048, 3, 45),      # 3 tiles per matrix; 2 K splits (few row groups)
+    (48, 3072, 1, 17),      # 3 K splits
+    (64, 4096, 1, 64),      # 4 K splits
+    (8, 14336, 1, 33),      # 56 blocks, one tile, 4 K splits of 14
 ]
 
 
@@ -211,6 +212,20 @@ def test_q6k_gemm_block_ints_exact(backend, oracle, case):
             assert np.array_equal(s[tok, r], os_), f"sumi token {tok} row {r}"
             assert np.array_equal(m[tok, r], om), f"msum token {tok} row {r}"
     check_tokens(backend.matmul(tt, X), oracle.matmul(S.T_Q6_K, w, cols, X, O_ROW))
+    tt.free()
+
+
+def test_q6k_prefill_down_shape(backend, oracle):
+    """The FFN down projection (Q6_K in Q4_K_M files), 64 tokens x K=14336 -> N=4096: 4 K splits,
+    within tolerance of gemm_kquant, the same bits on every call; then 9 tokens."""
+    rows, cols = 4096, 14336
+    w = S.weights(S.T_Q6_K, rows, cols, 292)
+    X = S.activations(cols, 293, rows=64)
+    tt = backend.upload(S.T_Q6_K, cols, w)
+    Y = backend.matmul(tt, X)
+    check_tokens(Y, oracle.matmul(S.T_Q6_K, w, cols, X, O_ROW))
+    assert bits_equal(backend.matmul(tt, X), Y)
+    check_tokens(backend.matmul(tt, X[:9]), oracle.matmul(S.T_Q6_K, w, cols, X[:9], O_ROW))
     tt.free()
 
 
