@@ -251,12 +251,23 @@ static int gemm_q4k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_
 }
 // the prompt GEMM for a Q8_0 tensor (gemm_q32, fastgguf.c:2856-2999): Q8 records of T tokens, then
 // one MFMA launch on the decode tiles; ds: optional [T][rows * n_mats][nb] integer dump
+// the Q8_0 GEMM's scratch: workgroups of 2 groups of 32 rows, splits of at least 8 tile steps
+static fgh::GemmScratch q80_scratch(const fgh_ctx *c, const fgh_tensor *t, int T) {
+    const int64_t groups = (t->gpm + 3) / 4 * t->n_mats;
+    return fgh::gemm_split_scratch(fgh::gemm32_act_bytes(t->nb, T <= 32 ? 32 : 64), fgh::gemm32_workgroups(groups),
+                                   (int)t->ntile, 8, t->rows * t->n_mats, T, c->num_cu);
+}
 static int gemm_q80_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
                          uint8_t *act, int32_t *ds) {
     const int Tp = T <= 32 ? 32 : 64;
-    HIP_TRY(c, fgh::launch_gemm32_quant(X, ldx, t->nb, T, Tp, act, c->stream));
+    const fgh::GemmScratch gs = q80_scratch(c, t, T);
+    int32_t *cnt = gs.ks > 1 ? (int32_t *)(act + gs.cnt_off) : nullptr;
+    HIP_TRY(c, fgh::launch_gemm32_quant(X, ldx, t->nb, T, Tp, act, cnt, gs.ncnt, c->stream));
     fgh::Gemm32Args a;
     memset(&a, 0, sizeof(a));
+    a.ks = gs.ks;
+    a.cnt = cnt;
+    a.part = gs.ks > 1 ? (float *)(act + gs.part_off) : nullptr;
     a.W = t->dev;
     a.Y = Y;
     a.rows = t->rows;
@@ -311,9 +322,9 @@ static bool q32n_type(uint32_t type) {
 // [T][rows * n_mats][nb] integer dump
 // the Q6_K GEMM's scratch (16-row tiles: pairs of the decode layout's 8-row tiles)
 static fgh::GemmScratch q6k_scratch(const fgh_ctx *c, const fgh_tensor *t, int T) {
-    const int64_t groups16 = (t->gpm + 1) / 2 * t->n_mats;
-    return fgh::gemm_split_scratch(fgh::gemm6_act_bytes(t->nb, (T + 15) / 16 * 16), groups16, t->rows * t->n_mats,
-                                   t->nb, T, c->num_cu);
+    const int64_t groups16 = (t->gpm + 1) / 2 * t->n_mats;  // 4 per workgroup, splits of >= 4 blocks
+    return fgh::gemm_split_scratch(fgh::gemm6_act_bytes(t->nb, (T + 15) / 16 * 16), (groups16 + 3) / 4, t->nb, 4,
+                                   t->rows * t->n_mats, T, c->num_cu);
 }
 static int gemm_q6k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
                          uint8_t *act, int32_t *ds, int32_t *dm) {
@@ -349,7 +360,7 @@ static int gemm_q6k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_
 static size_t prompt_gemm_bytes(const fgh_ctx *c, const fgh_tensor *t, int T) {
     if (T < 8) return 0;
     if (t->type == FGH_T_Q4_K) return fgh::gemm_scratch(t->groups, t->rows * t->n_mats, t->nb, T, c->num_cu).bytes;
-    if (t->type == FGH_T_Q8_0) return fgh::gemm32_act_bytes(t->nb, T <= 32 ? 32 : 64);
+    if (t->type == FGH_T_Q8_0) return q80_scratch(c, t, T).bytes;
     if (t->type == FGH_T_Q6_K) return q6k_scratch(c, t, T).bytes;
     if (q32n_type(t->type)) return fgh::gemmn_act_bytes(t->nb, (T + 15) / 16 * 16);
     return 0;

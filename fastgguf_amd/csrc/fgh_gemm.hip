@@ -388,8 +388,9 @@ gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
         }
     }
     if (a.ks > 1) {  // the K split's partials (the reduction's LDS area is done with)
-        gemm_split_finish<NT>(acc, kh == 0 && store, tid, kg, orow, a.ks, ksi, a.T, a.nrows, a.ldy, a.part, a.cnt, a.Y,
-                              (int *)smem + 4096);
+        gemm_split_finish<4 * NT>([&](int e) { return 16 * (e >> 2) + 4 * kg + (e & 3); },
+                                  [&](int e) { return acc[e >> 2][e & 3]; }, kh == 0 && store, tid, orow, a.ks, ksi, a.T,
+                                  a.nrows, a.ldy, a.part, a.cnt, a.Y, (int *)smem + 4096);
         return;
     }
     if (kh == 0 && store) {
@@ -427,27 +428,22 @@ static void gemm_launch_kh(const GemmArgs &a, hipStream_t s) {
     else gemm_launch<NT, 1>(a, s);
 }
 
-// K splits: as many (up to 4) as still give each workgroup its own compute unit, each split at
-// least 4 blocks. Row counts below 64 x the compute units (the down projection 14336 -> 4096: 64
-// workgroups) otherwise leave most units idle.
-int gemm_splits(int64_t groups, int nb, int num_cu) {
-    const int64_t wg = (groups + GEMM_TPW - 1) / GEMM_TPW;
-    int ks = 1;
-    while (ks < 4 && wg * (ks + 1) <= num_cu && nb / (ks + 1) >= 4) ++ks;
-    return ks;
-}
 static size_t up256(size_t n) { return (n + 255) / 256 * 256; }
-GemmScratch gemm_split_scratch(size_t rec_bytes, int64_t groups, int64_t nrows, int nb, int T, int num_cu) {
+GemmScratch gemm_split_scratch(size_t rec_bytes, int64_t wg, int units, int min_units, int64_t nrows, int T,
+                               int num_cu) {
     GemmScratch g;
-    g.ks = gemm_splits(groups, nb, num_cu);
-    g.ncnt = g.ks > 1 ? (int)((groups + GEMM_TPW - 1) / GEMM_TPW) : 0;
+    g.ks = 1;
+    while (g.ks < 4 && wg * (g.ks + 1) <= num_cu && units / (g.ks + 1) >= min_units) ++g.ks;
+    g.ncnt = g.ks > 1 ? (int)wg : 0;
     g.cnt_off = up256(rec_bytes);
     g.part_off = g.cnt_off + up256((size_t)g.ncnt * 4);
     g.bytes = g.ks > 1 ? g.part_off + (size_t)g.ks * T * nrows * 4 : rec_bytes;
     return g;
 }
+// the Q4_K GEMM: workgroups of 4 tiles, splits of at least 4 blocks
 GemmScratch gemm_scratch(int64_t groups, int64_t nrows, int nb, int T, int num_cu) {
-    return gemm_split_scratch(gemm_act_bytes(nb, (T + 15) / 16 * 16), groups, nrows, nb, T, num_cu);
+    return gemm_split_scratch(gemm_act_bytes(nb, (T + 15) / 16 * 16), (groups + GEMM_TPW - 1) / GEMM_TPW, nb, 4, nrows,
+                              T, num_cu);
 }
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > a.Tp || a.Tp % 16 || a.Tp > 64 || a.Tp - a.T >= 16 || a.nb < 1 || a.groups < 1)

@@ -48,8 +48,11 @@ __host__ __device__ constexpr int gemm32_rec_bytes(int Tp) { return Tp * 144; }
 // block. The block maximum combines the lane pair (m, m + 32); fmaxf ignores NaN, as the
 // reference's comparison does.
 __global__ __launch_bounds__(64) void gemm32_quant_kernel(const float *__restrict__ x, int64_t ldx, int nb, int T,
-                                                          int Tp, uint8_t *__restrict__ rec) {
+                                                          int Tp, uint8_t *__restrict__ rec, int32_t *__restrict__ cnt,
+                                                          int ncnt) {
     const int l = threadIdx.x, h = l >> 5, m = l & 31;
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+        for (int i = l; i < ncnt; i += 64) cnt[i] = 0;  // the K split's arrival counters
     const int b = blockIdx.x, tt = blockIdx.y, tok = 32 * tt + m;
     float v[16];
     if (tok < T && b < nb) {
@@ -80,10 +83,13 @@ __global__ __launch_bounds__(64) void gemm32_quant_kernel(const float *__restric
     if (h == 0) ((float *)(r + 128 * Tp))[bb * Tp + tok] = d;
 }
 
-hipError_t launch_gemm32_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s) {
+hipError_t launch_gemm32_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, int32_t *cnt, int ncnt,
+                               hipStream_t s) {
+    if (ncnt < 0) return hipErrorInvalidValue;
     if (T < 1 || T > Tp || Tp % 32 || Tp > 64 || nb < 1) return hipErrorInvalidValue;
     // every block of every tile step, the ones past the row's end as zeros
-    gemm32_quant_kernel<<<dim3((unsigned)((nb + 3) / 4 * 4), (unsigned)(Tp / 32)), 64, 0, s>>>(x, ldx, nb, T, Tp, rec);
+    gemm32_quant_kernel<<<dim3((unsigned)((nb + 3) / 4 * 4), (unsigned)(Tp / 32)), 64, 0, s>>>(x, ldx, nb, T, Tp, rec,
+                                                                                              cnt, ncnt);
     return hipGetLastError();
 }
 
@@ -119,7 +125,10 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tw = wave % TPW, kh = wave / TPW;
     const int n = l & 31, h = l >> 5, r8 = n & 7;
-    const int ns = a.nsteps, nws = (ns + KH - 1) / KH;  // tile steps, workgroup steps
+    // K split ksi of a.ks (grid.y): tile steps [s_lo, s_lo + nsk) of the row's ns
+    const int ns = a.nsteps, ksi = blockIdx.y, nss = (ns + a.ks - 1) / a.ks;
+    const int s_lo = ksi * nss, nsk = min(ns - s_lo, nss);
+    const int nws = (nsk + KH - 1) / KH;  // workgroup steps
     const int64_t grp = (int64_t)blockIdx.x * TPW + tw;
     const bool live = grp < a.groups;
     const int64_t gc = live ? grp : a.groups - 1;
@@ -131,10 +140,10 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     const int64_t orow = mi * rows + row;
     const uint32_t woff = (uint32_t)((n >> 3) * Q80_TILE), qoff = woff + 64 + 16 * (8 * r8 + 4 * h), doff = woff + 8 * r8;
 
-    // the step's records: a linear copy of KH tile-step records from tile step KH j (the
+    // the step's records: a linear copy of KH tile-step records from tile step s_lo + KH j (the
     // quantizer's buffer holds KH records of slack past the last)
     auto aload = [&](int j, ARec32 &ar) __attribute__((always_inline)) {
-        const BufRes src = buf_res(a.act + (size_t)min(j, nws - 1) * KH * REC, KH * REC);
+        const BufRes src = buf_res(a.act + (size_t)(s_lo + KH * min(j, nws - 1)) * REC, KH * REC);
         auto ld = [&](int k) __attribute__((always_inline)) { return bld16(src, 16 * (k * NTH + tid)); };
         ar.v0 = ld(0);
         if (R > 1) ar.v1 = ld(1);
@@ -155,7 +164,7 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     // the group's weights of tile step KH j + kh: its (up to) 4 tiles are contiguous; reads past
     // the valid tiles (a matrix's last group) return zeros
     auto wload = [&](int j, GW32 &w) __attribute__((always_inline)) {
-        const int s = min(KH * j + kh, ns - 1);
+        const int s = s_lo + min(KH * j + kh, nsk - 1);
         const BufRes r = buf_res(a.W + ((size_t)(mi * ns + s) * a.tpm + 4 * gi) * Q80_TILE, nvalid * Q80_TILE);
         w.s0 = bld16v(r, qoff);
         w.s1 = bld16v(r, qoff + 16);
@@ -218,14 +227,14 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     // which every K-part has a tile step run without branches (exact load counters); the last
     // may test.
     auto step = [&](auto full, int j, GW32 &wc, GW32 &wn3, const uint8_t *stc, uint8_t *stn) __attribute__((always_inline)) {
-        const int s = KH * j + kh;
+        const int s = s_lo + KH * j + kh;
         auto issue = [&](int bb) __attribute__((always_inline)) {
             __builtin_amdgcn_sched_barrier(0);
             if (bb == 0) aload(j + 1, rr);
             if (bb == 2) wload(j + 3, wn3);
             __builtin_amdgcn_sched_barrier(0);
         };
-        if (decltype(full)::value || s < ns) {  // uniform per wavefront
+        if (decltype(full)::value || s < s_lo + nsk) {  // uniform per wavefront
             block(wc, stc, s, issue);
         } else {
             issue(0);
@@ -237,7 +246,7 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     };
     using Full = std::true_type;
     using Edge = std::false_type;
-    const int nfull = ns / KH;  // workgroup steps in which every K-part has a tile step
+    const int nfull = nsk / KH;  // workgroup steps in which every K-part has a tile step
     int j = 0;
     for (; j + 4 <= nfull; j += 4) {
         step(Full(), j, w0, w3, st0, st1);
@@ -261,19 +270,26 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
                         v4f{acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]};
         }
         __syncthreads();
-        if (kh > 0) return;
+        if (kh == 0) {
 #pragma unroll
-        for (int k = 1; k < KH; ++k)
+            for (int k = 1; k < KH; ++k)
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
+                for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const v4f o = *(const v4f *)(red + ((size_t)((k - 1) * NT + t) * 4 * 64 + q * 64 + l) * 4);
+                    for (int q = 0; q < 4; ++q) {
+                        const v4f o = *(const v4f *)(red + ((size_t)((k - 1) * NT + t) * 4 * 64 + q * 64 + l) * 4);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[t][4 * q + e] += o[e];
-                }
+                        for (int e = 0; e < 4; ++e) acc[t][4 * q + e] += o[e];
+                    }
+        }
     }
-    if (store) {
+    if (a.ks > 1) {  // the K split's partials; the flag sits past the reduction area
+        gemm_split_finish<16 * NT>([&](int e) { return 32 * (e >> 4) + 8 * ((e & 15) >> 2) + 4 * h + (e & 3); },
+                                   [&](int e) { return acc[e >> 4][e & 15]; }, kh == 0 && store, tid, orow, a.ks, ksi,
+                                   a.T, a.nrows, a.ldy, a.part, a.cnt, a.Y, (int *)smem + TPW * (KH - 1) * 64 * 16 * NT);
+        return;
+    }
+    if (kh == 0 && store) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -290,8 +306,9 @@ template <int NT, int KH>
 static size_t gemm32_lds() {
     const int nth = 64 * GEMM32_TPW * KH, r = (KH * gemm32_rec_bytes(32 * NT) + 16 * nth - 1) / (16 * nth);
     const size_t stages = (size_t)2 * r * 16 * nth, red = (size_t)GEMM32_TPW * (KH - 1) * 64 * 16 * NT * 4;
-    return stages > red ? stages : red;
+    return std::max(stages, red + 4);  // + the K split's flag past the reduction area
 }
+int gemm32_workgroups(int64_t groups) { return (int)((groups + GEMM32_TPW - 1) / GEMM32_TPW); }
 
 size_t gemm32_act_bytes(int nb, int Tp) {
     const int ns = (nb + 3) / 4;
@@ -300,7 +317,7 @@ size_t gemm32_act_bytes(int nb, int Tp) {
 
 template <int NT, int KH>
 static void gemm32_launch(const Gemm32Args &a, hipStream_t s) {
-    const dim3 grid((unsigned)((a.groups + GEMM32_TPW - 1) / GEMM32_TPW));
+    const dim3 grid((unsigned)((a.groups + GEMM32_TPW - 1) / GEMM32_TPW), (unsigned)a.ks);
     const size_t lds = gemm32_lds<NT, KH>();
     if (a.dump_s) q80_gemm_kernel<NT, KH, GEMM32_TPW, true><<<grid, 64 * GEMM32_TPW * KH, lds, s>>>(a);
     else q80_gemm_kernel<NT, KH, GEMM32_TPW, false><<<grid, 64 * GEMM32_TPW * KH, lds, s>>>(a);
@@ -318,6 +335,8 @@ hipError_t launch_q80_gemm(const Gemm32Args &a, hipStream_t s) {
     if (a.T < 1 || a.T > a.Tp || (a.Tp != 32 && a.Tp != 64) || a.Tp - a.T >= 32 || a.nb < 1 ||
         a.nsteps != (a.nb + 3) / 4 || a.groups < 1 || a.gpm32 != (a.tpm + 3) / 4)
         return hipErrorInvalidValue;
+    if (a.ks < 1 || a.ks > 4 || (a.ks > 1 && (!a.part || !a.cnt)) || (a.nsteps + a.ks - 1) / a.ks * (a.ks - 1) >= a.nsteps)
+        return hipErrorInvalidValue;  // every split has a tile step
     if (a.Tp == 32) gemm32_launch_kh<1>(a, s);
     else gemm32_launch_kh<2>(a, s);
     return hipGetLastError();

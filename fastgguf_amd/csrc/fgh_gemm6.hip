@@ -363,8 +363,9 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
         }
     }
     if (a.ks > 1) {  // the K split's partials (the reduction's LDS area is done with)
-        gemm_split_finish<NT>(acc, kh == 0 && store, tid, kg, orow, a.ks, ksi, a.T, a.nrows, a.ldy, a.part, a.cnt, a.Y,
-                              (int *)smem + 4096);
+        gemm_split_finish<4 * NT>([&](int e) { return 16 * (e >> 2) + 4 * kg + (e & 3); },
+                                  [&](int e) { return acc[e >> 2][e & 3]; }, kh == 0 && store, tid, orow, a.ks, ksi, a.T,
+                                  a.nrows, a.ldy, a.part, a.cnt, a.Y, (int *)smem + 4096);
         return;
     }
     if (kh == 0 && store) {

@@ -529,8 +529,14 @@ struct Gemm32Args {
     int Tp, T;             // padded token count (32 or 64, Tp - T < 32), tokens
     int64_t ldy;
     int32_t *dump_s;       // test hook: [T][nrows][nb] integers, or null
+    int ks;                // K splits of the tile steps (grid.y); ks > 1: partials and counters
+    float *part;
+    int32_t *cnt;
 };
-hipError_t launch_gemm32_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, hipStream_t s);
+// the Q8_0 GEMM's records; zeroes the K split's ncnt counters
+hipError_t launch_gemm32_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, int32_t *cnt, int ncnt,
+                               hipStream_t s);
+int gemm32_workgroups(int64_t groups);  // workgroups (row groups of the Q8_0 GEMM) over groups
 size_t gemm32_act_bytes(int nb, int Tp);
 hipError_t launch_q80_gemm(const Gemm32Args &a, hipStream_t s);
 
@@ -584,39 +590,39 @@ hipError_t launch_q6k_gemm(const Gemm6Args &a, hipStream_t s);
 hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp, uint8_t *rec, int32_t *cnt, int ncnt,
                              hipStream_t s);
 size_t gemm_act_bytes(int nb, int Tp);
-// the scratch of a prompt GEMM on 16-row tiles, 4 per workgroup (Q4_K, Q6_K): its activation
-// records (rec_bytes), then, when it splits K (ks > 1), ncnt arrival counters and the partials
-// [ks][T][nrows]
+// The scratch of a prompt GEMM (Q4_K, Q6_K, Q8_0): its activation records (rec_bytes), then, when
+// it splits K (ks > 1), one arrival counter per workgroup of a split (ncnt) and the partials
+// [ks][T][nrows]. ks: as many splits (up to 4) of the units along K (blocks or tile steps) as
+// still give each workgroup its own compute unit, each split at least min_units; short outputs
+// (the down projection 14336 -> 4096: 64 workgroups) otherwise leave most units idle.
 struct GemmScratch {
     int ks, ncnt;
     size_t cnt_off, part_off, bytes;
 };
-GemmScratch gemm_split_scratch(size_t rec_bytes, int64_t groups, int64_t nrows, int nb, int T, int num_cu);
+GemmScratch gemm_split_scratch(size_t rec_bytes, int64_t wg, int units, int min_units, int64_t nrows, int T,
+                               int num_cu);
 GemmScratch gemm_scratch(int64_t groups, int64_t nrows, int nb, int T, int num_cu);  // Q4_K's
 
-typedef float gemm_v4f __attribute__((ext_vector_type(4)));
-// The end of a K-split prompt GEMM workgroup (grid.y = ks splits of consecutive blocks; blockIdx.x
-// = the row group): lane (kg, n) of a storing wavefront (mine) holds output row orow for tokens
-// 16 t + 4 kg + r in acc[t][r]. The split's partial goes to part as agent-scope atomic stores
+// The end of a K-split prompt GEMM workgroup (grid.y = ks splits of consecutive K units;
+// blockIdx.x = the row group): element e < NE of a storing lane (mine) is output row orow, token
+// tok(e), value val(e). The split's partial goes to part as agent-scope atomic stores
 // (write-through); every wavefront waits until its stores have completed, then thread 0 bumps the
 // row group's counter. The last split to arrive loads every other partial (agent-scope loads, all
-// in flight at once) and writes Y = ((p_0 + p_1) + p_2) + p_3, in split order whichever arrives
-// last. Every wavefront of the workgroup calls it (two barriers); flag is one int of LDS.
-template <int NT>
-__device__ __forceinline__ void gemm_split_finish(const gemm_v4f (&acc)[NT], bool mine, int tid, int kg, int64_t orow,
-                                                  int ks, int ksi, int T, int64_t nrows, int64_t ldy, float *part,
-                                                  int32_t *cnt, float *Y, int *flag) {
+// in flight at once: loading each just before its add took a memory round trip per output) and
+// writes Y = ((p_0 + p_1) + p_2) + p_3, in split order whichever arrives last. Every wavefront of
+// the workgroup calls it (two barriers); flag is one int of LDS. An agent-scope release instead of
+// the write-through stores writes back the whole L2 of the workgroup's XCD (measured slower).
+template <int NE, class Tok, class Val>
+__device__ __forceinline__ void gemm_split_finish(Tok tok, Val val, bool mine, int tid, int64_t orow, int ks, int ksi,
+                                                  int T, int64_t nrows, int64_t ldy, float *part, int32_t *cnt,
+                                                  float *Y, int *flag) {
     const size_t pstride = (size_t)T * nrows;
     if (mine) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tok = 16 * t + 4 * kg + r;
-                if (tok < T)
-                    __hip_atomic_store(part + ksi * pstride + (size_t)tok * nrows + orow, acc[t][r], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            }
+        for (int e = 0; e < NE; ++e)
+            if (tok(e) < T)
+                __hip_atomic_store(part + ksi * pstride + (size_t)tok(e) * nrows + orow, val(e), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt 0: this wavefront's partial stores have completed
     __syncthreads();
@@ -624,32 +630,26 @@ __device__ __forceinline__ void gemm_split_finish(const gemm_v4f (&acc)[NT], boo
         *flag = __hip_atomic_fetch_add(&cnt[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ks - 1;
     __syncthreads();
     if (!*flag || !mine) return;
-    float pv[4][NT][4];
+    float pv[4][NE];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tok = 16 * t + 4 * kg + r;
-                pv[k][t][r] = 0.0f;
-                if (k < ks && k != ksi && tok < T)
-                    pv[k][t][r] = __hip_atomic_load(part + k * pstride + (size_t)tok * nrows + orow, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-            }
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tok = 16 * t + 4 * kg + r;
-            if (tok < T) {
-                float v = ksi == 0 ? acc[t][r] : pv[0][t][r];
-#pragma unroll
-                for (int k = 1; k < 4; ++k)
-                    if (k < ks) v += ksi == k ? acc[t][r] : pv[k][t][r];
-                Y[(size_t)tok * ldy + orow] = v;
-            }
+        for (int e = 0; e < NE; ++e) {
+            pv[k][e] = 0.0f;
+            if (k < ks && k != ksi && tok(e) < T)
+                pv[k][e] = __hip_atomic_load(part + k * pstride + (size_t)tok(e) * nrows + orow, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
         }
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+        if (tok(e) < T) {
+            float v = ksi == 0 ? val(e) : pv[0][e];
+#pragma unroll
+            for (int k = 1; k < 4; ++k)
+                if (k < ks) v += ksi == k ? val(e) : pv[k][e];
+            Y[(size_t)tok(e) * ldy + orow] = v;
+        }
+    }
 }
 constexpr size_t GEMM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
 // true when all wg workgroups of a launch (waves wavefronts and lds bytes each) can be resident

@@ -98,9 +98,10 @@ Q80_CASES = [  # (rows, cols, n_mats, tokens): K-parts 1 (1 tile step), 2 (2-3 s
     (40, 256, 1, 32),
     (100, 416, 1, 31),      # 13 blocks: 4 tile steps, the last with one block
     (72, 384, 3, 45),       # 3 steps (K-parts 2, one idle in the last step), 9 tiles per matrix
-    (256, 4096, 1, 64),
-    (24, 14336, 1, 33),     # 448 blocks
-    (8, 2080, 2, 9),        # 65 blocks, one 8-row tile per matrix
+    (256, 4096, 1, 64),     # 4 K splits of 8 tile steps (few row groups)
+    (24, 14336, 1, 33),     # 448 blocks, 4 K splits of 28 tile steps
+    (8, 2080, 2, 9),        # 65 blocks, one 8-row tile per matrix, 2 K splits (9 and 8 steps)
+    (40, 3072, 1, 20),      # 3 K splits of 8 tile steps
 ]
 
 
@@ -118,6 +119,20 @@ def test_q80_gemm_block_ints_exact(backend, oracle, case):
             os_, _ = oracle.block_ints(S.T_Q8_0, w[r], act)
             assert np.array_equal(s[tok, r], os_), f"sumi token {tok} row {r}"
     check_tokens(backend.matmul(tt, X), oracle.matmul(S.T_Q8_0, w, cols, X, O_ROW))
+    tt.free()
+
+
+def test_q80_prefill_down_shape(backend, oracle):
+    """The FFN down projection, 64 tokens x K=14336 -> N=4096, Q8_0: 4 K splits, within tolerance
+    of the oracle's GEMM order, the same bits on every call; then 9 tokens"""
+    rows, cols = 4096, 14336
+    w = S.weights(S.T_Q8_0, rows, cols, 192)
+    X = S.activations(cols, 193, rows=64)
+    tt = backend.upload(S.T_Q8_0, cols, w)
+    Y = backend.matmul(tt, X)
+    check_tokens(Y, oracle.matmul(S.T_Q8_0, w, cols, X, O_ROW))
+    assert bits_equal(backend.matmul(tt, X), Y)
+    check_tokens(backend.matmul(tt, X[:9]), oracle.matmul(S.T_Q8_0, w, cols, X[:9], O_ROW))
     tt.free()
 
 
