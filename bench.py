@@ -18,7 +18,9 @@ roofline: the dominant kernel of the step is the Q4_K decode matvec launch of th
          at least 512 MB of distinct weight copies.
 prefill: BASELINE config 4 (64 tokens x 4096 -> 14336, Q4_K) on the int8 MFMA GEMM, timed the
          same way, cold (rotating weights) and Infinity-Cache hot, as TOPS and fraction of 5 POPS;
-         the same shape in Q8_0, Q6_K and Q4_0 on their MFMA GEMMs, against their HBM floors.
+         the same shape in Q8_0, Q6_K and Q4_0 on their MFMA GEMMs, and the FFN down projection
+         of the same tokens (14336 -> 4096, where the GEMMs split K) in Q4_K, Q6_K and Q8_0,
+         against their HBM floors.
 cpu_baseline: the reference's own CPU kernels (oracle/_ref, compiled from fastgguf.c) on the same
          layer with its default repacked Q4_K path, on this host's physical cores, over weight
          copies beyond the host's L3, for a bounded sample.
@@ -545,29 +547,45 @@ def main() -> int:
                     "hbm_floor_us": round((wq4 + 4 * T * (4096 + 14336)) / HBM_PEAK_GBS / 1e3, 3),
                     "traffic": counted_traffic("prefill_gemm")})
     # the same shape in Q8_0, Q6_K and Q4_0 on their MFMA GEMMs (gemm_q32's and gemm_kquant's roles),
-    # cold over >= 512 MB of rotating copies and hot, against the HBM floor of their weights
+    # and the FFN down projection 14336 -> 4096 of the same 64 tokens (Q4_K on the layer's own down
+    # copies; Q6_K, the down type of Q4_K_M files, and Q8_0: the GEMMs split K there), cold over
+    # >= 512 MB of rotating copies and hot, against the HBM floor of their weights
+    Xd = S.activations(14336, 6, rows=T)
+    xdd = be.dev_alloc(Xd.nbytes)
+    be.h2d(xdd, Xd)
     kname = {"q8_0": "q80_gemm_kernel (int8 MFMA 32x32x32, one block per K step)",
              "q6_k": "q6k_gemm_kernel (int8 MFMA 16x16x64, three scale-digit chains)",
-             "q4_0": "q32n_gemm_kernel (int8 MFMA 16x16x32 per block, gemm_q32's fp32 order, bit-exact)"}
-    for name, ty, wgen, bpr in (("q8_0", S.T_Q8_0, S.q8_0_weights, 128 * 34), ("q6_k", S.T_Q6_K, S.q6_k_weights, 16 * 210),
-                                ("q4_0", S.T_Q4_0, lambda r, c, seed: S.weights(S.T_Q4_0, r, c, seed), 128 * 18)):
-        wbytes = 14336 * bpr
-        w = wgen(14336, 4096, seed=130)
-        ts = [be.upload(ty, 4096, w) for _ in range(copies_for(wbytes))]
-        del w
+             "q4_0": "q32n_gemm_kernel (int8 MFMA 16x16x32 per block, gemm_q32's fp32 order, bit-exact)",
+             "q4_k": "gemm_quant_kernel + q4k_gemm_kernel (int8 MFMA 16x16x64, split sub-block scales)"}
+
+    def prefill_line(name, ts, wbytes, rows, cols, xin):
         line = {}
         for kind, pick in (("cold", lambda i: ts[i % len(ts)]), ("hot", lambda i: ts[0])):
-            us = kernel_time(lambda i: be.matmul_dev(pick(i), xpd, ypd, T), args.kernel_reps)
-            nbytes = wbytes + 4 * T * (4096 + 14336)
+            us = kernel_time(lambda i: be.matmul_dev(pick(i), xin, ypd, T), args.kernel_reps)
+            nbytes = wbytes + 4 * T * (rows + cols)
             line[kind] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
                           "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "TOPS": round(ops / us / 1e6, 2)}
-        line.update({"workload": f"64 tokens x K=4096 -> N=14336, {name.upper()} (quantization of X included)",
-                     "hbm_floor_us": round((wbytes + 4 * T * (4096 + 14336)) / HBM_PEAK_GBS / 1e3, 3),
+        split = " (4 K splits)" if rows == 4096 else ""
+        line.update({"workload": f"64 tokens x K={cols} -> N={rows}, {name.upper()}{split} (quantization of X included)",
+                     "hbm_floor_us": round((wbytes + 4 * T * (rows + cols)) / HBM_PEAK_GBS / 1e3, 3),
                      "rotation_MB": round(len(ts) * wbytes / 1e6),
                      "kernel": kname[name]})
-        prefill[name] = line
-        for t in ts:
-            t.free()
+        return line
+
+    prefill["q4_k_down"] = prefill_line("q4_k", rot["down"], 4096 * 56 * 144, 4096, 14336, xdd)
+    for name, ty, wgen, bpr in (("q8_0", S.T_Q8_0, S.q8_0_weights, 34 / 32), ("q6_k", S.T_Q6_K, S.q6_k_weights, 210 / 256),
+                                ("q4_0", S.T_Q4_0, lambda r, c, seed: S.weights(S.T_Q4_0, r, c, seed), 18 / 32)):
+        for rows, cols, key, xin in ((14336, 4096, name, xpd), (4096, 14336, name + "_down", xdd)):
+            if key == "q4_0_down":
+                continue
+            wbytes = int(rows * cols * bpr)
+            w = wgen(rows, cols, seed=130)
+            ts = [be.upload(ty, cols, w) for _ in range(copies_for(wbytes))]
+            del w
+            prefill[key] = prefill_line(name, ts, wbytes, rows, cols, xin)
+            for t in ts:
+                t.free()
+    be.dev_free(xdd)
     for t in extra:
         t.free()
     be.dev_free(xpd)
