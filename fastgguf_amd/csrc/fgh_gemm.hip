@@ -387,6 +387,7 @@ gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
             for (int t = 0; t < NT; ++t) acc[t] += *(const v4f *)(red + (size_t)(t * 64 + l) * 4);
         }
     }
+    static_assert(2 * SB >= 4 * 4096 + 4, "the K split's flag (LDS int 4096) lies inside the stages");
     if (a.ks > 1) {  // the K split's partials (the reduction's LDS area is done with)
         gemm_split_finish<4 * NT>([&](int e) { return 16 * (e >> 2) + 4 * kg + (e & 3); },
                                   [&](int e) { return acc[e >> 2][e & 3]; }, kh == 0 && store, tid, orow, a.ks, ksi, a.T,
