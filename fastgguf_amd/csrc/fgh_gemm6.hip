@@ -362,7 +362,8 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
             for (int t = 0; t < NT; ++t) acc[t] += *(const v4f *)(red + (size_t)(t * 64 + l) * 4);
         }
     }
-    static_assert(2 * SB >= 4 * 4096 + 4, "the K split's flag (LDS int 4096) lies inside the stages");
+    // a K split (at least 8 blocks, so KH = 2) puts its flag at LDS int 4096, inside the stages
+    static_assert(KH == 1 || 2 * SB >= 4 * 4096 + 4, "the K split's flag lies inside the stages");
     if (a.ks > 1) {  // the K split's partials (the reduction's LDS area is done with)
         gemm_split_finish<4 * NT>([&](int e) { return 16 * (e >> 2) + 4 * kg + (e & 3); },
                                   [&](int e) { return acc[e >> 2][e & 3]; }, kh == 0 && store, tid, orow, a.ks, ksi, a.T,
@@ -407,7 +408,7 @@ hipError_t launch_q6k_gemm(const Gemm6Args &a, hipStream_t s) {
     if (a.T < 1 || a.T > a.Tp || a.Tp % 16 || a.Tp > 64 || a.Tp - a.T >= 16 || a.nb < 1 || a.groups < 1 ||
         a.gpm16 != (a.tpm + 1) / 2)
         return hipErrorInvalidValue;
-    if (a.ks < 1 || a.ks > 4 || (a.ks > 1 && (!a.part || !a.cnt))) return hipErrorInvalidValue;
+    if (a.ks < 1 || a.ks > 4 || (a.ks > 1 && (!a.part || !a.cnt || gemm6_kh(a.nb) == 1))) return hipErrorInvalidValue;
     switch (a.Tp / 16) {
     case 1: gemm6_launch_kh<1>(a, s); break;
     case 2: gemm6_launch_kh<2>(a, s); break;
