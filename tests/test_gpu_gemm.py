@@ -354,3 +354,43 @@ def test_graph_keeps_scratch_across_a_larger_eager_call(oracle):
         wide.free()
     finally:
         be.close()
+
+
+@pytest.mark.parametrize("ty", [S.T_Q4_K, S.T_Q6_K, S.T_Q8_0], ids=["q4_k", "q6_k", "q8_0"])
+def test_split_gemm_graph_replays(oracle, ty):
+    """The K-split GEMMs inside a HIP graph: the arrival counters are zeroed by the call's own
+    quantizer launch (no memset node), so replays with eager calls of another shape in between
+    give the eager result bit for bit, every time."""
+    from fastgguf_amd.backend import Backend
+    be = Backend(0)
+    try:
+        rows, cols, T = 64, 8192, 40  # one workgroup of rows, K split 4 ways
+        w = S.weights(ty, rows, cols, 511)
+        t = be.upload(ty, cols, w)
+        other = be.upload(ty, 2048, S.weights(ty, 256, 2048, 512))
+        X = S.activations(cols, 513, rows=T)
+        Xo = S.activations(2048, 514, rows=64)
+        xd, yd = be.dev_alloc(X.nbytes), be.dev_alloc(4 * T * rows)
+        xod, yod = be.dev_alloc(Xo.nbytes), be.dev_alloc(4 * 64 * 256)
+        be.h2d(xd, X)
+        be.h2d(xod, Xo)
+        want = be.matmul(t, X)
+        check_tokens(want, oracle.matmul(ty, w, cols, X, O_RP if ty == S.T_Q4_K else O_ROW))
+        be.graph_begin()
+        be.matmul_dev(t, xd, yd, T)
+        g = be.graph_end()
+        for rep in range(4):
+            be.h2d(yd, np.full(T * rows, np.nan, np.float32))
+            be.graph_launch(g)
+            be.matmul_dev(other, xod, yod, 64)
+            be.sync()
+            got = np.empty((T, rows), np.float32)
+            be.d2h(got, yd)
+            assert bits_equal(got, want), f"replay {rep}"
+        be.graph_destroy(g)
+        for p in (xd, yd, xod, yod):
+            be.dev_free(p)
+        t.free()
+        other.free()
+    finally:
+        be.close()
