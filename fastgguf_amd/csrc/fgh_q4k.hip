@@ -561,7 +561,7 @@ static int q4_tpw(int s) { return s == 1 ? 4 : s == 2 ? 2 : 1; }
 size_t q4k_lds_bytes(int order, int nb) { return q4_lds(order, nb, 4, 1); }
 
 // Launch shape (measured on MI355X at the decode-layer shapes). Wavefronts per tile S: launches of
-// fewer than 768 tiles (tiles x tokens) split the blocks of a tile over up to 8 wavefronts, as many
+// at most 768 tiles (tiles x tokens) split the blocks of a tile over up to 8 wavefronts, as many
 // as keep the launch within 2048 wavefronts, each wavefront at 4 blocks or more, the LDS within
 // the 160 KiB of a workgroup and every workgroup resident at once; larger launches keep one
 // wavefront per tile. Tiles per workgroup: 4,
@@ -580,7 +580,7 @@ static hipError_t q4_launch_s(int S, int R, const MvArgs &a, int ntok, size_t ld
 MvShape q4k_matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu) {
     if (type == T_Q5_K) order = 0;  // no repacked order for Q5_K
     int S = 1;
-    if (tiles < 768)
+    if (tiles <= 768)  // (the MoE batch-1 gate/up launch has 768: 14.98 -> 14.33 us with S = 2)
         while (S < 8 && tiles * 2 * S <= 2048 && nb >= 8 * S &&
                q4_lds(order, nb, q4_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX &&
                all_resident((tiles + q4_tpw(2 * S) - 1) / q4_tpw(2 * S), 2 * S * q4_tpw(2 * S),
