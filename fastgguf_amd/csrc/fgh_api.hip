@@ -225,7 +225,7 @@ static int matvec_launch(fgh_ctx *c, int n, const fgh_tensor *const *t, const fl
 static int gemm_q4k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
                          uint8_t *act, int32_t *ds, int32_t *dm) {
     const int Tp = (T + 15) / 16 * 16;
-    const fgh::GemmScratch gs = fgh::gemm_scratch(t->groups, t->rows * t->n_mats, t->nb, T, c->num_cu);
+    const fgh::GemmScratch gs = fgh::gemm_scratch(t->groups, t->nb, T, c->num_cu);
     int32_t *cnt = gs.ks > 1 ? (int32_t *)(act + gs.cnt_off) : nullptr;
     HIP_TRY(c, fgh::launch_gemm_quant(X, ldx, t->nb, T, Tp, act, cnt, gs.ncnt, c->stream));
     fgh::GemmArgs a;
@@ -254,8 +254,9 @@ static int gemm_q4k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_
 // the Q8_0 GEMM's scratch: workgroups of 2 groups of 32 rows, splits of at least 8 tile steps
 static fgh::GemmScratch q80_scratch(const fgh_ctx *c, const fgh_tensor *t, int T) {
     const int64_t groups = (t->gpm + 3) / 4 * t->n_mats;
-    return fgh::gemm_split_scratch(fgh::gemm32_act_bytes(t->nb, T <= 32 ? 32 : 64), fgh::gemm32_workgroups(groups),
-                                   (int)t->ntile, 8, t->rows * t->n_mats, T, c->num_cu);
+    const int Tp = T <= 32 ? 32 : 64;
+    return fgh::gemm_split_scratch(fgh::gemm32_act_bytes(t->nb, Tp), fgh::gemm32_workgroups(groups), (int)t->ntile, 8,
+                                   Tp, c->num_cu);
 }
 static int gemm_q80_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
                          uint8_t *act, int32_t *ds) {
@@ -323,8 +324,8 @@ static bool q32n_type(uint32_t type) {
 // the Q6_K GEMM's scratch (16-row tiles: pairs of the decode layout's 8-row tiles)
 static fgh::GemmScratch q6k_scratch(const fgh_ctx *c, const fgh_tensor *t, int T) {
     const int64_t groups16 = (t->gpm + 1) / 2 * t->n_mats;  // 4 per workgroup, splits of >= 4 blocks
-    return fgh::gemm_split_scratch(fgh::gemm6_act_bytes(t->nb, (T + 15) / 16 * 16), (groups16 + 3) / 4, t->nb, 4,
-                                   t->rows * t->n_mats, T, c->num_cu);
+    const int Tp = (T + 15) / 16 * 16;
+    return fgh::gemm_split_scratch(fgh::gemm6_act_bytes(t->nb, Tp), (groups16 + 3) / 4, t->nb, 4, Tp, c->num_cu);
 }
 static int gemm_q6k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_t ldx, float *Y, int64_t ldy, int T,
                          uint8_t *act, int32_t *ds, int32_t *dm) {
@@ -359,7 +360,7 @@ static int gemm_q6k_into(fgh_ctx *c, const fgh_tensor *t, const float *X, int64_
 // activation-record bytes it needs (0: the per-token decode kernels, which need no scratch)
 static size_t prompt_gemm_bytes(const fgh_ctx *c, const fgh_tensor *t, int T) {
     if (T < 8) return 0;
-    if (t->type == FGH_T_Q4_K) return fgh::gemm_scratch(t->groups, t->rows * t->n_mats, t->nb, T, c->num_cu).bytes;
+    if (t->type == FGH_T_Q4_K) return fgh::gemm_scratch(t->groups, t->nb, T, c->num_cu).bytes;
     if (t->type == FGH_T_Q8_0) return q80_scratch(c, t, T).bytes;
     if (t->type == FGH_T_Q6_K) return q6k_scratch(c, t, T).bytes;
     if (q32n_type(t->type)) return fgh::gemmn_act_bytes(t->nb, (T + 15) / 16 * 16);

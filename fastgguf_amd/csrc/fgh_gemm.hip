@@ -391,8 +391,8 @@ gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
     static_assert(KH == 1 || 2 * SB >= 4 * 4096 + 4, "the K split's flag lies inside the stages");
     if (a.ks > 1) {  // the K split's partials (the reduction's LDS area is done with)
         gemm_split_finish<4 * NT>([&](int e) { return 16 * (e >> 2) + 4 * kg + (e & 3); },
-                                  [&](int e) { return acc[e >> 2][e & 3]; }, kh == 0 && store, tid, orow, a.ks, ksi, a.T,
-                                  a.nrows, a.ldy, a.part, a.cnt, a.Y, (int *)smem + 4096);
+                                  [&](int e) { return acc[e >> 2][e & 3]; }, kh == 0, store, tid, tw, TPW, orow, a.ks,
+                                  ksi, a.T, a.ldy, a.part, a.cnt, a.Y, (int *)smem + 4096);
         return;
     }
     if (kh == 0 && store) {
@@ -431,21 +431,20 @@ static void gemm_launch_kh(const GemmArgs &a, hipStream_t s) {
 }
 
 static size_t up256(size_t n) { return (n + 255) / 256 * 256; }
-GemmScratch gemm_split_scratch(size_t rec_bytes, int64_t wg, int units, int min_units, int64_t nrows, int T,
-                               int num_cu) {
+GemmScratch gemm_split_scratch(size_t rec_bytes, int64_t wg, int units, int min_units, int Tp, int num_cu) {
     GemmScratch g;
     g.ks = 1;
     while (g.ks < 4 && wg * (g.ks + 1) <= num_cu && units / (g.ks + 1) >= min_units) ++g.ks;
     g.ncnt = g.ks > 1 ? (int)wg : 0;
     g.cnt_off = up256(rec_bytes);
     g.part_off = g.cnt_off + up256((size_t)g.ncnt * 4);
-    g.bytes = g.ks > 1 ? g.part_off + (size_t)g.ks * T * nrows * 4 : rec_bytes;
+    g.bytes = g.ks > 1 ? g.part_off + (size_t)g.ks * wg * 64 * Tp * 4 : rec_bytes;
     return g;
 }
 // the Q4_K GEMM: workgroups of 4 tiles, splits of at least 4 blocks
-GemmScratch gemm_scratch(int64_t groups, int64_t nrows, int nb, int T, int num_cu) {
-    return gemm_split_scratch(gemm_act_bytes(nb, (T + 15) / 16 * 16), (groups + GEMM_TPW - 1) / GEMM_TPW, nb, 4, nrows,
-                              T, num_cu);
+GemmScratch gemm_scratch(int64_t groups, int nb, int T, int num_cu) {
+    const int Tp = (T + 15) / 16 * 16;
+    return gemm_split_scratch(gemm_act_bytes(nb, Tp), (groups + GEMM_TPW - 1) / GEMM_TPW, nb, 4, Tp, num_cu);
 }
 hipError_t launch_q4k_gemm(const GemmArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > a.Tp || a.Tp % 16 || a.Tp > 64 || a.Tp - a.T >= 16 || a.nb < 1 || a.groups < 1)

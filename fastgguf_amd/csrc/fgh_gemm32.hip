@@ -285,8 +285,8 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     }
     if (a.ks > 1) {  // the K split's partials; the flag sits past the reduction area
         gemm_split_finish<16 * NT>([&](int e) { return 32 * (e >> 4) + 8 * ((e & 15) >> 2) + 4 * h + (e & 3); },
-                                   [&](int e) { return acc[e >> 4][e & 15]; }, kh == 0 && store, tid, orow, a.ks, ksi,
-                                   a.T, a.nrows, a.ldy, a.part, a.cnt, a.Y, (int *)smem + TPW * (KH - 1) * 64 * 16 * NT);
+                                   [&](int e) { return acc[e >> 4][e & 15]; }, kh == 0, store, tid, tw, TPW, orow, a.ks,
+                                   ksi, a.T, a.ldy, a.part, a.cnt, a.Y, (int *)smem + TPW * (KH - 1) * 64 * 16 * NT);
         return;
     }
     if (kh == 0 && store) {

@@ -366,8 +366,8 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     static_assert(KH == 1 || 2 * SB >= 4 * 4096 + 4, "the K split's flag lies inside the stages");
     if (a.ks > 1) {  // the K split's partials (the reduction's LDS area is done with)
         gemm_split_finish<4 * NT>([&](int e) { return 16 * (e >> 2) + 4 * kg + (e & 3); },
-                                  [&](int e) { return acc[e >> 2][e & 3]; }, kh == 0 && store, tid, orow, a.ks, ksi, a.T,
-                                  a.nrows, a.ldy, a.part, a.cnt, a.Y, (int *)smem + 4096);
+                                  [&](int e) { return acc[e >> 2][e & 3]; }, kh == 0, store, tid, tw, TPW, orow, a.ks,
+                                  ksi, a.T, a.ldy, a.part, a.cnt, a.Y, (int *)smem + 4096);
         return;
     }
     if (kh == 0 && store) {

@@ -147,6 +147,7 @@ __device__ __forceinline__ uint2 ld8(const uint8_t *p) { return *(const uint2 *)
 // vector instructions per load; reads at or past nbytes return 0 (0x00020000: the gfx9 resource
 // word 3, 32-bit data format).
 typedef __amdgpu_buffer_rsrc_t BufRes;
+typedef unsigned fgh_u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ BufRes buf_res(const uint8_t *base, uint32_t nbytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, (int)nbytes, 0x00020000);
 }
@@ -591,38 +592,49 @@ hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp,
                              hipStream_t s);
 size_t gemm_act_bytes(int nb, int Tp);
 // The scratch of a prompt GEMM (Q4_K, Q6_K, Q8_0): its activation records (rec_bytes), then, when
-// it splits K (ks > 1), one arrival counter per workgroup of a split (ncnt) and the partials
-// [ks][T][nrows]. ks: as many splits (up to 4) of the units along K (blocks or tile steps) as
-// still give each workgroup its own compute unit, each split at least min_units; short outputs
-// (the down projection 14336 -> 4096: 64 workgroups) otherwise leave most units idle.
+// it splits K (ks > 1), one arrival counter per workgroup of a split (ncnt) and the partials: per
+// split and workgroup 64 rows x Tp tokens of fp32. ks: as many splits (up to 4) of the units
+// along K (blocks or tile steps) as still give each workgroup its own compute unit, each split at
+// least min_units; short outputs (the down projection 14336 -> 4096: 64 workgroups) otherwise
+// leave most units idle.
 struct GemmScratch {
     int ks, ncnt;
     size_t cnt_off, part_off, bytes;
 };
-GemmScratch gemm_split_scratch(size_t rec_bytes, int64_t wg, int units, int min_units, int64_t nrows, int T,
-                               int num_cu);
-GemmScratch gemm_scratch(int64_t groups, int64_t nrows, int nb, int T, int num_cu);  // Q4_K's
+GemmScratch gemm_split_scratch(size_t rec_bytes, int64_t wg, int units, int min_units, int Tp, int num_cu);
+GemmScratch gemm_scratch(int64_t groups, int nb, int T, int num_cu);  // Q4_K's
 
 // The end of a K-split prompt GEMM workgroup (grid.y = ks splits of consecutive K units;
-// blockIdx.x = the row group): element e < NE of a storing lane (mine) is output row orow, token
-// tok(e), value val(e). The split's partial goes to part as agent-scope atomic stores
-// (write-through); every wavefront waits until its stores have completed, then thread 0 bumps the
-// row group's counter. The last split to arrive loads every other partial (agent-scope loads, all
-// in flight at once: loading each just before its add took a memory round trip per output) and
-// writes Y = ((p_0 + p_1) + p_2) + p_3, in split order whichever arrives last. Every wavefront of
-// the workgroup calls it (two barriers); flag is one int of LDS. An agent-scope release instead of
-// the write-through stores writes back the whole L2 of the workgroup's XCD (measured slower).
+// blockIdx.x = the row group; nslot storing wavefronts, this one slot). A storing wavefront
+// (mine: uniform) holds NE outputs per lane: element e is token tok(e) of row orow, value val(e).
+// Its partial goes to its own NE x 64 floats of part, quad q of lane l at 16 (64 q + l) bytes
+// (each store instruction writes 1 KB contiguous), as write-through stores (sc1, agent scope);
+// every wavefront waits until its stores have completed, then thread 0 bumps the row group's
+// counter. The last split to arrive loads the other partials (sc1 loads, which read past the L2 of
+// the reading XCD; all in flight at once) and writes Y = ((p_0 + p_1) + p_2) + p_3 for its lanes
+// with store set, in split order whichever arrives last. Every wavefront of the workgroup calls
+// it (two barriers); flag is one int of LDS. An agent-scope release instead of the write-through
+// stores writes back the whole L2 of the workgroup's XCD; 4-byte stores and loads scattered by
+// token took 10 us more at 64 x 14336 -> 4096.
 template <int NE, class Tok, class Val>
-__device__ __forceinline__ void gemm_split_finish(Tok tok, Val val, bool mine, int tid, int64_t orow, int ks, int ksi,
-                                                  int T, int64_t nrows, int64_t ldy, float *part, int32_t *cnt,
-                                                  float *Y, int *flag) {
-    const size_t pstride = (size_t)T * nrows;
+__device__ __forceinline__ void gemm_split_finish(Tok tok, Val val, bool mine, bool store, int tid, int slot, int nslot,
+                                                  int64_t orow, int ks, int ksi, int T, int64_t ldy, float *part,
+                                                  int32_t *cnt, float *Y, int *flag) {
+    static_assert(NE % 4 == 0, "whole quads");
+    constexpr int NQ = NE / 4, WF = NE * 64;  // quads per lane, floats per wavefront
+    constexpr int SC1 = 16;                    // cache policy: agent-scope coherent (write-through / no L2 hit)
+    const int lane = tid & 63;
+    auto res = [&](int k) {
+        return buf_res((const uint8_t *)(part + (((size_t)k * gridDim.x + blockIdx.x) * nslot + slot) * WF), WF * 4);
+    };
     if (mine) {
+        const BufRes r = res(ksi);
 #pragma unroll
-        for (int e = 0; e < NE; ++e)
-            if (tok(e) < T)
-                __hip_atomic_store(part + ksi * pstride + (size_t)tok(e) * nrows + orow, val(e), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        for (int q = 0; q < NQ; ++q) {
+            const uint4 v = make_uint4(__float_as_uint(val(4 * q)), __float_as_uint(val(4 * q + 1)),
+                                       __float_as_uint(val(4 * q + 2)), __float_as_uint(val(4 * q + 3)));
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(fgh_u32x4, v), r, 16 * (64 * q + lane), 0, SC1);
+        }
     }
     __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt 0: this wavefront's partial stores have completed
     __syncthreads();
@@ -632,14 +644,21 @@ __device__ __forceinline__ void gemm_split_finish(Tok tok, Val val, bool mine, i
     if (!*flag || !mine) return;
     float pv[4][NE];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < 4; ++k) {
+        if (k < ks && k != ksi) {  // uniform
+            const BufRes r = res(k);
 #pragma unroll
-        for (int e = 0; e < NE; ++e) {
-            pv[k][e] = 0.0f;
-            if (k < ks && k != ksi && tok(e) < T)
-                pv[k][e] = __hip_atomic_load(part + k * pstride + (size_t)tok(e) * nrows + orow, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
+            for (int q = 0; q < NQ; ++q) {
+                const fgh_u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(r, 16 * (64 * q + lane), 0, SC1);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) pv[k][4 * q + c] = __uint_as_float(w[c]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < NE; ++e) pv[k][e] = 0.0f;
         }
+    }
+    if (!store) return;
 #pragma unroll
     for (int e = 0; e < NE; ++e) {
         if (tok(e) < T) {

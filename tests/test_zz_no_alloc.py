@@ -63,16 +63,18 @@ def test_noalloc_matches_matmul_dev(backend, fresh):
 
 def q4k_gemm_scratch(rows, nbk, T, num_cu=256):
     """bytes of the Q4_K prompt GEMM's scratch: (nbk + 1) activation records of 292 * Tp bytes, and
-    with a K split (few row groups) 256 bytes of arrival counters and ks partials of T x rows fp32"""
+    with a K split (few row groups) the arrival counters and ks partials of 64 rows x Tp tokens of
+    fp32 per workgroup"""
     wg = -(-rows // 64)
     ks = 1
     while ks < 4 and wg * (ks + 1) <= num_cu and nbk // (ks + 1) >= 4:
         ks += 1
-    rec = (nbk + 1) * 292 * (-(-T // 16) * 16)
+    Tp = -(-T // 16) * 16
+    rec = (nbk + 1) * 292 * Tp
     if ks == 1:
         return rec
     up = lambda n: -(-n // 256) * 256
-    return up(rec) + up(4 * wg) + ks * T * rows * 4
+    return up(rec) + up(4 * wg) + ks * wg * 64 * Tp * 4
 
 
 def test_noalloc_refuses_more_than_its_scratch(backend):
