@@ -112,6 +112,34 @@ def counted_traffic(kernel: str):
     return None
 
 
+GRAPH_LAUNCHES = 50  # back-to-back launches of one kernel per timed HIP graph
+
+
+def kernel_time_on(be, launch, reps: int) -> float:
+    """GRAPH_LAUNCHES back-to-back launches of one call (rotating over weight copies) captured in
+    one HIP graph, replayed and timed with HIP events on the library's stream: us per launch (the
+    kernel's duration plus the in-graph gap between launches)."""
+    launch(0)  # grows any scratch before capture
+    be.graph_begin()
+    for i in range(GRAPH_LAUNCHES):
+        launch(i)
+    gr = be.graph_end()
+    be.graph_launch(gr)
+    be.sync()
+    a, b = be.event(), be.event()
+    n = max(1, reps // GRAPH_LAUNCHES)
+    be.record(a)
+    for _ in range(n):
+        be.graph_launch(gr)
+    be.record(b)
+    be.sync()
+    t = be.elapsed_ms(a, b)
+    be.event_destroy(a)
+    be.event_destroy(b)
+    be.graph_destroy(gr)
+    return t * 1e3 / (n * GRAPH_LAUNCHES)  # us
+
+
 def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
     """BASELINE configs 1 (Q8_0 4096^2 matvec), 3 (Q6_K LM head 128256 x 4096) and 5 (MoE, 128
     experts, top-8, hidden 2048, ff 768: batch 1 and 64 tokens), each timed like the kernels above.
@@ -182,6 +210,37 @@ def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
     for st in sets:
         for t in st:
             t.free()
+    # config 5 at 64 tokens on the grouped path's other expert kernel (the VALU lane chains,
+    # FGH_MOE_KERNEL=valu; same bits), beside the default int8 MFMA kernels above
+    os.environ["FGH_MOE_KERNEL"] = "valu"
+    try:
+        from fastgguf_amd.backend import Backend
+        bv = Backend(0)
+    finally:
+        os.environ.pop("FGH_MOE_KERNEL", None)
+    vsets = [(bv.upload(S.T_Q4_K, D, S.q4_k_weights(E * F, D, seed=300 + 3 * c), rows=F, n_mats=E),
+              bv.upload(S.T_Q4_K, D, S.q4_k_weights(E * F, D, seed=301 + 3 * c), rows=F, n_mats=E),
+              bv.upload(S.T_Q4_K, F, S.q4_k_weights(E * D, F, seed=302 + 3 * c), rows=D, n_mats=E)) for c in range(2)]
+    T = 64
+    X = S.activations(D, 310, rows=T)
+    L = S.router_logits(T, E, 311)
+    xd, ld, yd = bv.dev_alloc(X.nbytes), bv.dev_alloc(L.nbytes), bv.dev_alloc(X.nbytes)
+    bv.h2d(xd, X)
+    bv.h2d(ld, L)
+    us = kernel_time_on(bv, lambda i: bv.moe_ffn_dev(*vsets[i % 2], K, ld, xd, yd, T), 100)
+    m = out["cfg5_moe_64tok"]
+    out["cfg5_moe_64tok_valu_kernel"] = {"us": round(us, 3), "GB/s": round(m["bytes"] / us / 1e3, 1),
+                                         "frac": round(m["bytes"] / us / 1e3 / HBM_PEAK_GBS, 4),
+                                         "TOPS": round(m["TOPS"] * m["us"] / us, 3)}
+    m["kernel"] = "int8 MFMA (default)"
+    m["frac_mfma_peak"] = round(m["TOPS"] / (INT8_PEAK_TOPS), 5)
+    out["cfg5_moe_64tok_valu_kernel"]["frac_mfma_peak"] = round(out["cfg5_moe_64tok_valu_kernel"]["TOPS"] / INT8_PEAK_TOPS, 5)
+    for p_ in (xd, ld, yd):
+        bv.dev_free(p_)
+    for st in vsets:
+        for t in st:
+            t.free()
+    bv.close()
     return out
 
 
@@ -436,31 +495,9 @@ def main() -> int:
     layer_bytes = sum(algo_bytes(r, c) for _, r, c in LAYER)
     value = layer_bytes / (ms_step * 1e-3) / 1e9
 
-    # per-kernel durations: GRAPH_LAUNCHES back-to-back launches of one kernel (rotating over the
-    # weight copies) captured in one HIP graph, replayed and timed with HIP events on the library's
-    # stream; time / launches = the kernel's duration plus the in-graph gap between launches
-    GRAPH_LAUNCHES = 50
-
+    # per-kernel durations (kernel_time_on): graphs of back-to-back launches of one kernel
     def kernel_time(launch, reps: int) -> float:
-        launch(0)  # grows any scratch before capture
-        be.graph_begin()
-        for i in range(GRAPH_LAUNCHES):
-            launch(i)
-        gr = be.graph_end()
-        be.graph_launch(gr)
-        be.sync()
-        a, b = be.event(), be.event()
-        n = max(1, reps // GRAPH_LAUNCHES)
-        be.record(a)
-        for _ in range(n):
-            be.graph_launch(gr)
-        be.record(b)
-        be.sync()
-        t = be.elapsed_ms(a, b)
-        be.event_destroy(a)
-        be.event_destroy(b)
-        be.graph_destroy(gr)
-        return t * 1e3 / (n * GRAPH_LAUNCHES)  # us
+        return kernel_time_on(be, launch, reps)
 
     nc = args.copies
     # per-kernel rotations: the layer copies plus more of each matrix, at least ROT_BYTES each

@@ -31,7 +31,7 @@ EXPORTS = (
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_mfma_peak_dev", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
-    "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_expf", "fgh_fp16_to_f32", "fgh_matvec_shape",
+    "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_moe_block_ints", "fgh_expf", "fgh_fp16_to_f32", "fgh_matvec_shape",
     "fgh_gguf_open", "fgh_gguf_close", "fgh_gguf_summary", "fgh_gguf_tensor", "fgh_gguf_find",
     "fgh_gguf_kv_num", "fgh_gguf_kv_str", "fgh_gguf_data", "fgh_upload_gguf",
 )
@@ -108,6 +108,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_quantize": (i32, [vp, i32, f32p, i32, vp]),
         "fgh_block_ints": (i32, [vp, vp, f32p, vp, vp]),
         "fgh_gemm_block_ints": (i32, [vp, vp, f32p, i32, i32, vp, vp]),
+        "fgh_moe_block_ints": (i32, [vp, vp, vp, vp, i32, f32p, f32p, i32, vp, vp, vp, vp]),
         "fgh_fp16_to_f32": (i32, [vp, vp, i32, vp]),
         "fgh_expf": (i32, [vp, f32p, i32, vp]),
         "fgh_matvec_shape": (i32, [vp, u32, i32, i64, i64, i32, vp]),
@@ -331,6 +332,20 @@ class Backend:
         m = np.empty((nb, t.nout, t.nblocks), np.int32)
         self._check(self.lib.fgh_gemm_block_ints(self.ctx, t.handle, _p(X), t.cols, nb, _p(s), _p(m)))
         return s, m
+
+    def moe_block_ints(self, gate: Tensor, up: Tensor, down: Tensor, k: int, logits: np.ndarray, X: np.ndarray):
+        """The grouped MoE path's per (slot, row, block) integers: gate sumi / msum [n_tok * k][ff][blocks],
+        down sumi / msum [n_tok * k][n_embd][blocks] (slot t * k + j: token t's j-th expert)."""
+        X = np.ascontiguousarray(X, np.float32)
+        logits = np.ascontiguousarray(logits, np.float32)
+        np_ = X.shape[0] * k
+        gs = np.empty((np_, gate.rows, gate.nblocks), np.int32)
+        gm = np.empty_like(gs)
+        ds = np.empty((np_, down.rows, down.nblocks), np.int32)
+        dm = np.empty_like(ds)
+        self._check(self.lib.fgh_moe_block_ints(self.ctx, gate.handle, up.handle, down.handle, k, _p(logits), _p(X),
+                                                X.shape[0], _p(gs), _p(gm), _p(ds), _p(dm)))
+        return gs, gm, ds, dm
 
     def expf(self, x: np.ndarray) -> np.ndarray:
         """The device's expf (MoE softmax and silu) of every value of x."""

@@ -51,6 +51,15 @@ struct fgh_ctx {
     // with FGH_ERR before it launches anything, so a caller's CPU fallback can be tested
     int64_t calls = 0, fail_at = 0;
     void *noalloc = nullptr;  // this device's address of the static scratch (null: unavailable)
+    // the grouped MoE path's expert kernel (FGH_MOE_KERNEL at fgh_open): int8 MFMA (default) or
+    // the VALU lane chains ("valu"); both are bit-identical. moe_nsg: slots per chunk / 4 of the
+    // MFMA kernel (FGH_MOE_NSG: 1, 2 or 4; 0 picks by the slots per expert)
+    bool moe_valu = false;
+    int moe_nsg = 0;
+    fgh::MoeMmShape moe_shape;  // FGH_MOE_R / FGH_MOE_TT at fgh_open (ring depth, tiles per wavefront)
+    // fgh_moe_block_ints: device dumps of the grouped kernels' integers (gate sumi / msum, down
+    // sumi / msum), null otherwise
+    int32_t *moe_dump[4] = {nullptr, nullptr, nullptr, nullptr};
 };
 
 // fgh_matmul_dev_noalloc's scratch: a static array, one copy per device. In host code its name
@@ -444,6 +453,10 @@ int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out) {
         return FGH_ERR_DEVICE;
     }
     if (const char *f = getenv("FGH_FAIL_AT")) c->fail_at = atoll(f);
+    if (const char *m = getenv("FGH_MOE_KERNEL")) c->moe_valu = !strcmp(m, "valu");
+    if (const char *m = getenv("FGH_MOE_NSG")) c->moe_nsg = atoi(m);
+    if (const char *m = getenv("FGH_MOE_R")) c->moe_shape.r = atoi(m);
+    if (const char *m = getenv("FGH_MOE_TT")) c->moe_shape.tt = atoi(m);
     *out = c;
     return FGH_OK;
 }
@@ -716,11 +729,19 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
     int32_t *sel = (int32_t *)c->msel.p;
     float *w = (float *)c->mw.p, *G = (float *)c->mg.p, *U = (float *)c->mu.p,
           *D = (float *)c->md.p;
-    // several tokens, Q4_K experts: the slots grouped by expert, each expert's rows read once
-    const bool grouped = n_tok > 1 && gate->type == FGH_T_Q4_K && up->type == FGH_T_Q4_K && down->type == FGH_T_Q4_K &&
-                         gate->order == FGH_ORDER_ROW && up->order == FGH_ORDER_ROW && down->order == FGH_ORDER_ROW &&
-                         gate->nb <= fgh::q4k_moe_max_blocks() && down->nb <= fgh::q4k_moe_max_blocks() &&
-                         fgh::q4k_moe_lds_bytes(gate->nb) <= 65536 && fgh::q4k_moe_lds_bytes(down->nb) <= 65536;
+    // several tokens, Q4_K experts: the slots grouped by expert, each expert's rows read once, on
+    // int8 MFMA (or, FGH_MOE_KERNEL=valu, the VALU lane chains; same bits)
+    const bool q4row = n_tok > 1 && gate->type == FGH_T_Q4_K && up->type == FGH_T_Q4_K && down->type == FGH_T_Q4_K &&
+                       gate->order == FGH_ORDER_ROW && up->order == FGH_ORDER_ROW && down->order == FGH_ORDER_ROW;
+    // MFMA chunks: 4 slots per group, 2 groups (an expert with more slots gets more workgroups)
+    int nsg = c->moe_nsg == 1 || c->moe_nsg == 2 || c->moe_nsg == 4 ? c->moe_nsg : 2;
+    const int nbx = std::max(gate->nb, down->nb);
+    while (nsg > 1 && fgh::q4k_moe_mfma_lds(nsg, nbx) > fgh::GEMM_LDS_MAX) nsg /= 2;
+    const bool mfma_fits = fgh::q4k_moe_mfma_lds(nsg, nbx) <= fgh::GEMM_LDS_MAX && gate->gpm == up->gpm;
+    const bool valu_fits = gate->nb <= fgh::q4k_moe_max_blocks() && down->nb <= fgh::q4k_moe_max_blocks() &&
+                           fgh::q4k_moe_lds_bytes(gate->nb) <= 65536 && fgh::q4k_moe_lds_bytes(down->nb) <= 65536;
+    const bool use_valu = c->moe_valu ? valu_fits : !mfma_fits;
+    const bool grouped = q4row && (use_valu ? valu_fits : mfma_fits);
     // Q4_K / Q5_K experts otherwise: two launches. Gate and up route each token inside the
     // launch (every wavefront routes its own token: the weights it streams depend on the choice),
     // publish sel / w and write h = silu(g) * u (a workgroup holds the gate and up tiles of the
@@ -767,14 +788,45 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
         // kernels read the buckets; the combine clears their counts for the next call
         const size_t ibx = fgh::q4_image_bytes(gate->nb), ibh = fgh::q4_image_bytes(down->nb);
         void *cnt_before = c->mseg.p;
-        if ((rc = grow(c, c->mseg, (size_t)E * 4)) || (rc = grow(c, c->mslot, (size_t)E * n_tok * 4)) ||
+        // a bucket holds every slot of the call (a token may pick one expert more than once)
+        const int cap = (int)np;
+        if ((rc = grow(c, c->mseg, (size_t)E * 4)) || (rc = grow(c, c->mslot, (size_t)E * cap * 4)) ||
             (rc = grow(c, c->mimx, (size_t)n_tok * ibx)) || (rc = grow(c, c->mimh, (size_t)np * ibh)))
             return rc;
         int32_t *cnt = (int32_t *)c->mseg.p, *buckets = (int32_t *)c->mslot.p;
-        if (c->mseg.p != cnt_before) HIP_TRY(c, hipMemsetAsync(cnt, 0, c->mseg.cap, c->stream));  // new: zero once
+        if (c->mseg.p != cnt_before) HIP_TRY(c, fgh::launch_zero_i32(cnt, (int)(c->mseg.cap / 4), c->stream));  // new: zero once
         uint8_t *imx = (uint8_t *)c->mimx.p, *imh = (uint8_t *)c->mimh.p;
         HIP_TRY(c, fgh::launch_moe_prep(X, n_embd, gate->nb, imx, logits, (int)E, k, n_tok, sel, w, cnt, buckets,
                                         c->stream));
+        // from here the counts are non-zero until the combine clears them: a failed launch clears
+        // them itself, so the next call starts from zero
+        auto fail_reset = [&](const char *what, hipError_t e) {
+            (void)fgh::launch_zero_i32(cnt, (int)E, c->stream);
+            return fail(c, FGH_ERR_DEVICE, "moe_ffn: %s: %s", what, hipGetErrorString(e));
+        };
+        hipError_t e;
+        if (!use_valu) {
+            // gate / up on MFMA, writing the h images; down on MFMA; the ordered combine
+            fgh::MoeMmShape sh = c->moe_shape;
+            sh.nsg = nsg;
+            if ((e = fgh::launch_q4k_moe_mfma(sh, gate->dev, up->dev, ff, gate->gpm, gate->nb, cnt, buckets, cap, (int)E,
+                                               n_tok, imx, k, G, U, ff, c->moe_dump[0], c->moe_dump[1], c->num_cu,
+                                               c->stream)) != hipSuccess)
+                return fail_reset("gate / up experts", e);
+            // h = silu(g) * u, quantized straight into its images (never stored as fp32)
+            if ((e = fgh::launch_q4_image(G, U, ff, down->nb, np, imh, c->stream)) != hipSuccess)
+                return fail_reset("silu images", e);
+            if ((e = fgh::launch_q4k_moe_mfma(sh, down->dev, nullptr, n_embd, down->gpm, down->nb, cnt, buckets, cap,
+                                               (int)E, n_tok, imh, 1, D, nullptr, n_embd, c->moe_dump[2], c->moe_dump[3],
+                                               c->num_cu, c->stream)) != hipSuccess)
+                return fail_reset("down experts", e);
+            if ((e = fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, cnt, (int)E, c->stream)) != hipSuccess)
+                return fail_reset("combine", e);
+            return FGH_OK;
+        }
+        auto experts = [&](const fgh::MvArgs &aa, const uint8_t *img) {
+            return fgh::launch_q4k_moe(aa, cnt, buckets, cap, (int)E, img, c->stream);
+        };
         fgh::MvArgs a;
         memset(&a, 0, sizeof(a));
         a.t[0] = fgh::MvT{gate->dev, G, gate->rows, gate->gpm, 0};
@@ -786,9 +838,10 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
         a.ldy = ff;
         a.nb = gate->nb;
         a.xdiv = k;
-        HIP_TRY(c, fgh::launch_q4k_moe(a, cnt, buckets, n_tok, (int)E, imx, c->stream));
+        if ((e = experts(a, imx)) != hipSuccess) return fail_reset("gate / up experts", e);
         // h = silu(g) * u, quantized straight into its images (never stored as fp32)
-        HIP_TRY(c, fgh::launch_q4_image(G, U, ff, down->nb, np, imh, c->stream));
+        if ((e = fgh::launch_q4_image(G, U, ff, down->nb, np, imh, c->stream)) != hipSuccess)
+            return fail_reset("silu images", e);
         a.t[0] = fgh::MvT{down->dev, D, down->rows, down->gpm, 0};
         a.nt = 1;
         a.groups = down->gpm;
@@ -796,8 +849,9 @@ int fgh_moe_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, co
         a.ldy = n_embd;
         a.nb = down->nb;
         a.xdiv = 1;
-        HIP_TRY(c, fgh::launch_q4k_moe(a, cnt, buckets, n_tok, (int)E, imh, c->stream));
-        HIP_TRY(c, fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, cnt, (int)E, c->stream));
+        if ((e = experts(a, imh)) != hipSuccess) return fail_reset("down experts", e);
+        if ((e = fgh::launch_moe_combine(D, w, Y, (int)n_embd, k, n_tok, n_embd, cnt, (int)E, c->stream)) != hipSuccess)
+            return fail_reset("combine", e);
         return FGH_OK;
     }
     HIP_TRY(c, fgh::launch_moe_route(logits, (int)E, k, n_tok, sel, w, c->stream));
@@ -1201,6 +1255,46 @@ int fgh_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *x, int32_t *sum
     (void)hipFree(ds);
     if (rc) return rc;
     if (e != hipSuccess) return fail(c, FGH_ERR_DEVICE, "block_ints: %s", hipGetErrorString(e));
+    return FGH_OK;
+}
+
+int fgh_moe_block_ints(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, const fgh_tensor *down, int k,
+                       const float *logits, const float *X, int n_tok, int32_t *gate_sumi, int32_t *gate_msum,
+                       int32_t *down_sumi, int32_t *down_msum) {
+    int rc;
+    if ((rc = check_tensor(c, gate)) || (rc = check_tensor(c, up)) || (rc = check_tensor(c, down))) return rc;
+    NO_CAPTURE(c);
+    if (!logits || !X || !gate_sumi || !gate_msum || !down_sumi || !down_msum || n_tok < 2 || n_tok > FG_BATCH ||
+        k < 1 || k > gate->n_mats)
+        return fail(c, FGH_ERR_ARG, "moe_block_ints: bad arguments");
+    if (c->moe_valu || gate->type != FGH_T_Q4_K || up->type != FGH_T_Q4_K || down->type != FGH_T_Q4_K ||
+        gate->order != FGH_ORDER_ROW || up->order != FGH_ORDER_ROW || down->order != FGH_ORDER_ROW)
+        return fail(c, FGH_ERR_ARG, "moe_block_ints: the grouped MFMA path takes Q4_K row-order experts");
+    const int64_t np = (int64_t)n_tok * k;
+    const size_t ng = (size_t)np * gate->rows * gate->nb, nd = (size_t)np * down->rows * down->nb;
+    HIP_TRY(c, hipSetDevice(c->device));
+    void *buf = nullptr;
+    HIP_TRY(c, hipMalloc(&buf, (ng + nd) * 8));
+    int32_t *d0 = (int32_t *)buf;
+    c->moe_dump[0] = d0;
+    c->moe_dump[1] = d0 + ng;
+    c->moe_dump[2] = d0 + 2 * ng;
+    c->moe_dump[3] = d0 + 2 * ng + nd;
+    std::vector<float> Y((size_t)n_tok * down->rows);
+    rc = fgh_moe_ffn(c, gate, up, down, k, logits, X, Y.data(), n_tok, nullptr, nullptr);
+    hipError_t e = hipSuccess;
+    if (!rc) {
+        int32_t *outs[4] = {gate_sumi, gate_msum, down_sumi, down_msum};
+        const size_t cnts[4] = {ng, ng, nd, nd};
+        for (int i = 0; i < 4 && e == hipSuccess; ++i)
+            e = hipMemcpyAsync(outs[i], c->moe_dump[i], cnts[i] * 4, hipMemcpyDeviceToHost, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    }
+    (void)hipStreamSynchronize(c->stream);
+    for (auto &p : c->moe_dump) p = nullptr;
+    (void)hipFree(buf);
+    if (rc) return rc;
+    if (e != hipSuccess) return fail(c, FGH_ERR_DEVICE, "moe_block_ints: %s", hipGetErrorString(e));
     return FGH_OK;
 }
 

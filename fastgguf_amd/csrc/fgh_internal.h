@@ -71,6 +71,13 @@ __host__ __device__ constexpr bool q32_min(int type) { return type == T_Q4_1 || 
 //   d  [nb] fp32, bs [nb][16] int16 (the reference's bsums)
 // Q8 (for Q8_0 / Q5_0): per token, nb32 blocks of qs [nb32][32] int8 (natural order), d [nb32] fp32,
 //   s16 [nb32][2] int16.
+// The Q4_K / Q5_K kernels' activation image (their LDS, and the MoE path's per-row images in
+// HBM): natural-order Q8_K blocks: qs [nb][256] at 0, d [nb] fp32 at 256 nb, and the sums of each
+// 32 values, bs32 [nb][8] int16 at align16(260 nb) (bs32[g] = bsums[2g] + bsums[2g+1] of the
+// reference's q8k_blk_t: the min terms only ever use these pairs)
+__host__ __device__ constexpr size_t q4_off_d(int nb) { return (size_t)nb * 256; }
+__host__ __device__ constexpr size_t q4_off_s(int nb) { return ((size_t)nb * 260 + 15) & ~(size_t)15; }
+__host__ __device__ constexpr size_t q4_act_bytes(int nb) { return (q4_off_s(nb) + (size_t)nb * 16 + 15) & ~(size_t)15; }
 struct ActQ8K {
     int8_t *qs;
     float *d;
@@ -115,6 +122,62 @@ __device__ __forceinline__ int sum4_i32(int v) {
     return v;
 }
 
+// ---- Q8_K quantization of one 256-value block by 16 threads (the Q4_K / Q5_K kernels' images) ----
+// 16 threads per 256-value block; thread tl holds values 16tl..16tl+15 (4 float4 loads)
+struct XRound {
+    float4 v[4];
+};
+// block b of x (thread's 16 values: tl = threadIdx.x % 16); blocks past the end read block 0
+__device__ __forceinline__ void q8k_load_b(const float *__restrict__ x, int b, bool live, XRound &xr) {
+    const float *p = x + (size_t)(live ? b : 0) * 256 + 16 * (threadIdx.x & 15);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) xr.v[u] = *(const float4 *)(p + 4 * u);
+}
+__device__ __forceinline__ float dpp_ror_f32(float v, int ctrl_n) {
+    const int iv = __builtin_bit_cast(int, v);
+    int r;
+    switch (ctrl_n) {
+    case 8: r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false); break;
+    case 4: r = __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false); break;
+    case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x122, 0xF, 0xF, false); break;
+    default: r = __builtin_amdgcn_update_dpp(0, iv, 0x121, 0xF, 0xF, false); break;
+    }
+    return __builtin_bit_cast(float, r);
+}
+// quantizes the 16 threads' block b into act (stored only if live); the 16 threads of a block
+// are one DPP row, so a row is either wholly live or wholly not
+__device__ __forceinline__ void q8k_store_b(int nb, int b, bool live, const XRound &xr, uint8_t *act) {
+    const int tl = threadIdx.x & 15;
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        v[4 * u] = xr.v[u].x; v[4 * u + 1] = xr.v[u].y; v[4 * u + 2] = xr.v[u].z; v[4 * u + 3] = xr.v[u].w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) amax = fmaxf(amax, fabsf(v[u]));
+    amax = fmaxf(amax, dpp_ror_f32(amax, 8));
+    amax = fmaxf(amax, dpp_ror_f32(amax, 4));
+    amax = fmaxf(amax, dpp_ror_f32(amax, 2));
+    amax = fmaxf(amax, dpp_ror_f32(amax, 1));
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    uint32_t w[4];
+    int s = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int q0 = q8_round(v[4 * u] * id), q1 = q8_round(v[4 * u + 1] * id);
+        const int q2 = q8_round(v[4 * u + 2] * id), q3 = q8_round(v[4 * u + 3] * id);
+        s += q0 + q1 + q2 + q3;
+        w[u] = pack_q(q0, q1, q2, q3);
+    }
+    s += dpp_xor1(s);  // threads 2g, 2g+1: the 32 values of sub-block g
+    if (live) {
+        *(uint4 *)(act + (size_t)b * 256 + 16 * tl) = make_uint4(w[0], w[1], w[2], w[3]);
+        if ((tl & 1) == 0) ((int16_t *)(act + q4_off_s(nb)))[8 * b + (tl >> 1)] = (int16_t)s;
+        if (tl == 0) ((float *)(act + q4_off_d(nb)))[b] = d;
+    }
+}
 __device__ __forceinline__ float fp16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
@@ -430,15 +493,32 @@ hipError_t launch_mfma_peak(int iters, uint32_t *sink, int num_cu, hipStream_t s
 hipError_t launch_silu_mul(const float *g, const float *u, float *h, int64_t n, hipStream_t s);
 hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok, int32_t *sel, float *w, hipStream_t s);
 // the grouped path's first launch (fgh_q4k.hip): x images, routing, and the slots filed in
-// per-expert buckets of n_tok entries (cnt[n_expert] zero on entry; moe_combine clears it)
+// per-expert buckets of n_tok * k entries (a token may pick one expert more than once when its
+// probabilities are not finite); cnt[n_expert] zero on entry; moe_combine clears it
 hipError_t launch_moe_prep(const float *x, int64_t ldx, int nb, uint8_t *img, const float *logits, int n_expert,
                            int k, int n_tok, int32_t *sel, float *w, int32_t *cnt, int32_t *bucket, hipStream_t s);
-// grouped Q4_K row-order expert matvecs (fgh_q4k.hip): a.groups = tiles of one matrix over a.t;
-// rows of at most q4k_moe_max_blocks() blocks; expert e's slots in buckets[e * cap ..), cnt[e] of them
+// grouped Q4_K row-order expert matvecs on the VALU (fgh_q4k.hip): a.groups = tiles of one matrix
+// over a.t; rows of at most q4k_moe_max_blocks() blocks; expert e's slots in buckets[e * cap ..),
+// cnt[e] of them
 size_t q4k_moe_lds_bytes(int nb);
 int q4k_moe_max_blocks();
 hipError_t launch_q4k_moe(const MvArgs &a, const int32_t *cnt, const int32_t *buckets, int cap, int n_expert,
                           const uint8_t *img, hipStream_t s);
+// the same on int8 MFMA (fgh_moemm.hip), bit-identical: one launch over w0 (and w1 of the same
+// shape, its tiles after w0's) [E][rows][cols], y0 / y1 [slot * ldy + row], activation image row
+// slot / xdiv; chunks of 4 * nsg slots (1, 2 or 4) side by side, q4k_moe_mfma_lds(nsg, nb) bytes of
+// LDS; r: ring depth (2, 3 or 4 blocks); tt: tiles per wavefront (0: about three wavefronts per
+// SIMD over all experts). dump_s / dump_m (or null): w0's integers [slot][rows][nb].
+struct MoeMmShape {
+    int nsg = 2, r = 3, tt = 0;
+};
+size_t q4k_moe_mfma_lds(int nsg, int nb);
+hipError_t launch_q4k_moe_mfma(const MoeMmShape &sh, const uint8_t *w0, const uint8_t *w1, int64_t rows, int64_t gpm,
+                               int nb, const int32_t *cnt, const int32_t *buckets, int cap, int n_expert, int n_tok,
+                               const uint8_t *img, int xdiv, float *y0, float *y1, int64_t ldy, int32_t *dump_s,
+                               int32_t *dump_m, int num_cu, hipStream_t s);
+// zeroes n ints (a small fill kernel: the grouped path's counts after a failed launch)
+hipError_t launch_zero_i32(int32_t *p, int n, hipStream_t s);
 // Q8_K images of rows in the decode kernels' LDS layout; u != null: the rows are silu(x) * u
 size_t q4_image_bytes(int nb);
 hipError_t launch_q4_image(const float *x, const float *u, int64_t ldx, int nb, int64_t rows, uint8_t *img,

@@ -3,8 +3,9 @@
 //             first index on ties), w_j = p_j / max(sum_j p_j, 2^-14) (4594-4604)
 //   gate, up: expert sel_j's rows of gate / up times Q8_K(x) (the decode kernels with an expert
 //             index read on the device)
-//   h_j     = silu(g_j) * u_j, silu(x) = x / (1 + expf(-x)) (silu_f 3118), formed by the down
-//             launch while it quantizes its input (fgh_q4k.hip, fgh_matvec.hip)
+//   h_j     = silu(g_j) * u_j, silu(x) = x / (1 + expf(-x)) (silu_f 3118): formed inside the
+//             gate / up launch (one token), by the launch that quantizes the down projection's
+//             inputs (the grouped path), or by silu_mul_kernel (the generic path)
 //   down:     d_j = expert sel_j's rows of down times Q8_K(h_j)
 //   y_i     = sum over j in order of fma(w_j, d_j[i], s)  (4626-4635; gcc contracts s += w*dot)
 // Every dot product runs the reference's own per-row order (dot_q4_K_q8k and friends), so the
@@ -83,6 +84,17 @@ hipError_t launch_moe_route(const float *logits, int n_expert, int k, int n_tok,
                             hipStream_t s) {
     if (n_expert < 1 || n_expert > 64 * MOE_EPL || k < 1 || k > n_expert || k > 64) return hipErrorInvalidValue;
     moe_route_kernel<<<n_tok, 64, 0, s>>>(logits, n_expert, k, sel, w);
+    return hipGetLastError();
+}
+
+__global__ void zero_i32_kernel(int32_t *__restrict__ p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+hipError_t launch_zero_i32(int32_t *p, int n, hipStream_t s) {
+    if (n < 1) return hipSuccess;
+    zero_i32_kernel<<<(n + 255) / 256, 256, 0, s>>>(p, n);
     return hipGetLastError();
 }
 

@@ -49,12 +49,6 @@ constexpr int RB_ROWS = 16;     // rows per tile
 constexpr int RB_BYTES = 2304;  // one Q4_K (tile, block): 16 x 144
 __host__ __device__ constexpr int rb_bytes(int type) { return type == T_Q5_K ? Q5K_TILE : RB_BYTES; }
 
-// LDS activations: natural-order Q8_K blocks: qs [nb][256] at 0, d [nb] at 256 nb, and the sums of
-// each 32 values, bs32 [nb][8] int16 at align16(260 nb) (bs32[g] = bsums[2g] + bsums[2g+1] of the
-// reference's q8k_blk_t: the min terms only ever use these pairs)
-__host__ __device__ constexpr size_t q4_off_d(int nb) { return (size_t)nb * 256; }
-__host__ __device__ constexpr size_t q4_off_s(int nb) { return ((size_t)nb * 260 + 15) & ~(size_t)15; }
-__host__ __device__ constexpr size_t q4_act_bytes(int nb) { return (q4_off_s(nb) + (size_t)nb * 16 + 15) & ~(size_t)15; }
 // LDS records of one tile in a launch that splits its blocks over s wavefronts: repacked order,
 // a float4 per (block, row); row order, for the blocks after the first wavefront's ceil(nb / s),
 // a float4 per (block, lane) and a float per (block, row)
@@ -62,69 +56,14 @@ __host__ __device__ constexpr size_t q4_rec_bytes(int order, int nb, int s) {
     return s == 1 ? 0 : order == 1 ? (size_t)16 * 16 * nb : (size_t)(nb - (nb + s - 1) / s) * (64 * 16 + 16 * 4);
 }
 
-// 16 threads per 256-value block; thread tl holds values 16tl..16tl+15 (4 float4 loads)
-struct XRound {
-    float4 v[4];
-};
-// block b of x (thread's 16 values: tl = threadIdx.x % 16); blocks past the end read block 0
-__device__ __forceinline__ void q8k_load_b(const float *__restrict__ x, int b, bool live, XRound &xr) {
-    const float *p = x + (size_t)(live ? b : 0) * 256 + 16 * (threadIdx.x & 15);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) xr.v[u] = *(const float4 *)(p + 4 * u);
-}
 __device__ __forceinline__ void q8k_load(const float *__restrict__ x, int nb, int rb, XRound &xr) {
     const int b = rb + (threadIdx.x >> 4);
     q8k_load_b(x, b, b < nb, xr);
 }
 
-__device__ __forceinline__ float dpp_ror_f32(float v, int ctrl_n) {
-    const int iv = __builtin_bit_cast(int, v);
-    int r;
-    switch (ctrl_n) {
-    case 8: r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false); break;
-    case 4: r = __builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, false); break;
-    case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x122, 0xF, 0xF, false); break;
-    default: r = __builtin_amdgcn_update_dpp(0, iv, 0x121, 0xF, 0xF, false); break;
-    }
-    return __builtin_bit_cast(float, r);
-}
 __device__ __forceinline__ float dppf_xor1(float v) { return __builtin_bit_cast(float, dpp_xor1(__builtin_bit_cast(int, v))); }
 __device__ __forceinline__ float dppf_xor2(float v) { return __builtin_bit_cast(float, dpp_xor2(__builtin_bit_cast(int, v))); }
 
-// quantizes the 16 threads' block b into act (stored only if live); the 16 threads of a block
-// are one DPP row, so a row is either wholly live or wholly not
-__device__ __forceinline__ void q8k_store_b(int nb, int b, bool live, const XRound &xr, uint8_t *act) {
-    const int tl = threadIdx.x & 15;
-    float v[16];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        v[4 * u] = xr.v[u].x; v[4 * u + 1] = xr.v[u].y; v[4 * u + 2] = xr.v[u].z; v[4 * u + 3] = xr.v[u].w;
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int u = 0; u < 16; ++u) amax = fmaxf(amax, fabsf(v[u]));
-    amax = fmaxf(amax, dpp_ror_f32(amax, 8));
-    amax = fmaxf(amax, dpp_ror_f32(amax, 4));
-    amax = fmaxf(amax, dpp_ror_f32(amax, 2));
-    amax = fmaxf(amax, dpp_ror_f32(amax, 1));
-    const float d = amax / 127.0f;
-    const float id = d > 0.0f ? 1.0f / d : 0.0f;
-    uint32_t w[4];
-    int s = 0;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int q0 = q8_round(v[4 * u] * id), q1 = q8_round(v[4 * u + 1] * id);
-        const int q2 = q8_round(v[4 * u + 2] * id), q3 = q8_round(v[4 * u + 3] * id);
-        s += q0 + q1 + q2 + q3;
-        w[u] = pack_q(q0, q1, q2, q3);
-    }
-    s += dpp_xor1(s);  // threads 2g, 2g+1: the 32 values of sub-block g
-    if (live) {
-        *(uint4 *)(act + (size_t)b * 256 + 16 * tl) = make_uint4(w[0], w[1], w[2], w[3]);
-        if ((tl & 1) == 0) ((int16_t *)(act + q4_off_s(nb)))[8 * b + (tl >> 1)] = (int16_t)s;
-        if (tl == 0) ((float *)(act + q4_off_d(nb)))[b] = d;
-    }
-}
 __device__ __forceinline__ void q8k_store(int nb, int rb, const XRound &xr, uint8_t *act) {
     const int b = rb + (threadIdx.x >> 4);
     q8k_store_b(nb, b, b < nb, xr, act);
@@ -751,10 +690,11 @@ size_t q4_image_bytes(int nb) { return q4_act_bytes(nb); }
 
 // The grouped MoE path's first launch, one wavefront per token t: the Q8_K image of x row t
 // (q4_image_kernel's blocks, 4 at a time), the token's routing (moe_route_wave: sel, w), and each
-// selected slot t k + j filed in its expert's bucket: bucket[e * cap + position], cnt[e] counting
-// (cap = tokens: a token selects an expert at most once). The order inside a bucket is whatever
-// the atomics give; no result depends on it. cnt starts at zero and moe_combine_kernel, the
-// path's last launch, clears it again.
+// selected slot t k + j filed in its expert's bucket: bucket[e * cap + position], cnt[e] counting.
+// cap = tokens * k: a token whose probabilities are not all finite (NaN or infinite logits) can
+// select one expert several times, as the reference's repeated argmax does, so a bucket holds up
+// to every slot of the call. The order inside a bucket is whatever the atomics give; no result
+// depends on it. cnt starts at zero and moe_combine_kernel, the path's last launch, clears it.
 __global__ __launch_bounds__(64) void moe_prep_kernel(const float *__restrict__ x, int64_t ldx, int nb,
                                                       uint8_t *__restrict__ img, const float *__restrict__ logits,
                                                       int n_expert, int k, int32_t *__restrict__ sel,
@@ -782,7 +722,7 @@ hipError_t launch_moe_prep(const float *x, int64_t ldx, int nb, uint8_t *img, co
                            int k, int n_tok, int32_t *sel, float *w, int32_t *cnt, int32_t *bucket, hipStream_t s) {
     if (n_expert < 1 || n_expert > 64 * MOE_EPL || k < 1 || k > n_expert || k > 64 || nb < 1 || n_tok < 1)
         return hipErrorInvalidValue;
-    moe_prep_kernel<<<n_tok, 64, 0, s>>>(x, ldx, nb, img, logits, n_expert, k, sel, w, cnt, bucket, n_tok);
+    moe_prep_kernel<<<n_tok, 64, 0, s>>>(x, ldx, nb, img, logits, n_expert, k, sel, w, cnt, bucket, n_tok * k);
     return hipGetLastError();
 }
 

@@ -310,6 +310,14 @@ FGH_API int fgh_quantize(fgh_ctx *ctx, int kind, const float *x, int n, void *ou
 FGH_API int fgh_block_ints(fgh_ctx *ctx, const fgh_tensor *t, const float *x, int32_t *sumi, int32_t *msum);
 FGH_API int fgh_gemm_block_ints(fgh_ctx *ctx, const fgh_tensor *t, const float *X, int ldx, int nb,
                                 int32_t *sumi, int32_t *msum);
+/* fgh_moe_block_ints: fgh_moe_ffn of n_tok >= 2 tokens over Q4_K row-order experts (the grouped
+ * int8 MFMA path), returning the per (slot, row, block) integers its expert kernels formed: slot
+ * t * k + j is token t's j-th selected expert; gate_* [n_tok * k][ff][gate blocks] are gate's
+ * sumi / msum of Q8_K(x_t), down_* [n_tok * k][n_embd][down blocks] down's of Q8_K(h_tj)
+ * (the oracle's fgo_block_ints of those rows and activations). */
+FGH_API int fgh_moe_block_ints(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tensor *up, const fgh_tensor *down,
+                               int k, const float *logits, const float *X, int n_tok, int32_t *gate_sumi,
+                               int32_t *gate_msum, int32_t *down_sumi, int32_t *down_msum);
 FGH_API int fgh_expf(fgh_ctx *ctx, const float *x, int n, float *out);
 FGH_API int fgh_fp16_to_f32(fgh_ctx *ctx, const uint16_t *h, int n, float *out);
 FGH_API int fgh_matvec_shape(fgh_ctx *ctx, uint32_t type, int order, int64_t cols, int64_t row_tiles, int ntok,

@@ -205,3 +205,107 @@ def test_moe_grouped_graph_replays(backend, oracle):
         backend.dev_free(p)
     for t in (gate, up, down, g2, u2, d2):
         t.free()
+
+
+def _backend_with(env):
+    """A second context whose MoE kernel choice comes from the environment at fgh_open."""
+    import os
+
+    from fastgguf_amd.backend import Backend
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return Backend(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("E,K,D,F,T", [(8, 4, 512, 256, 64), (128, 8, 2048, 768, 64), (16, 2, 4096, 512, 33)])
+def test_moe_grouped_kernels_match_oracle(backend, oracle, E, K, D, F, T):
+    """The grouped path's expert kernels: int8 MFMA (the default) with chunks of 4, 8 and 16 slots,
+    ring depths 2, 3 and 4 and other tile counts per wavefront, and the VALU lane chains, each bit
+    for bit equal to the oracle. E = 8 at 64 tokens puts about 32 slots on every expert, so every
+    chunk size runs several chunks per expert side by side; 128 experts is config 5; 4096 columns
+    is 16 blocks per row."""
+    gw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 600 + E)
+    uw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 601 + E)
+    dw = S.random_bytes_weights(S.T_Q4_K, E * D, F, 602 + E)
+    X = S.activations(D, 603 + T, rows=T)
+    logits = S.router_logits(T, E, 604 + T)
+    Yo, so, wo = oracle.moe_ffn((S.T_Q4_K,) * 3, gw, uw, dw, E, K, D, F, logits, X)
+    for env in ({}, {"FGH_MOE_NSG": "1"}, {"FGH_MOE_NSG": "4"}, {"FGH_MOE_R": "2"}, {"FGH_MOE_R": "4", "FGH_MOE_TT": "1"},
+                {"FGH_MOE_NSG": "1", "FGH_MOE_R": "4", "FGH_MOE_TT": "3"}, {"FGH_MOE_KERNEL": "valu"}):
+        be = backend if not env else _backend_with(env)
+        try:
+            gate, up, down = (upload_experts(be, a, c, r, E) for a, c, r in ((gw, D, F), (uw, D, F), (dw, F, D)))
+            Y, sel, w = be.moe_ffn(gate, up, down, K, logits, X)
+            assert np.array_equal(sel, so), env
+            assert bits_equal(w, wo), env
+            assert bits_equal(Y, Yo), env
+            for t in (gate, up, down):
+                t.free()
+        finally:
+            if be is not backend:
+                be.close()
+
+
+def test_moe_grouped_block_ints_match_oracle(backend, oracle):
+    """The MFMA expert kernels' per (slot, row, block) integers: gate's against the oracle's
+    integers of the selected expert's rows and Q8_K(x_t), down's against those of Q8_K(h), h the
+    oracle's silu(g) * u (bit-identical to the device's)."""
+    E, K, D, F, T = 16, 4, 512, 256, 12
+    gw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 700)
+    uw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 701)
+    dw = S.random_bytes_weights(S.T_Q4_K, E * D, F, 702)
+    X = S.activations(D, 703, rows=T)
+    logits = S.router_logits(T, E, 704)
+    Yo, so, wo, ho = oracle.moe_ffn((S.T_Q4_K,) * 3, gw, uw, dw, E, K, D, F, logits, X, want_h=True)
+    gate, up, down = (upload_experts(backend, a, c, r, E) for a, c, r in ((gw, D, F), (uw, D, F), (dw, F, D)))
+    gs, gm, ds, dm = backend.moe_block_ints(gate, up, down, K, logits, X)
+    rbg, rbd = S.row_bytes(S.T_Q4_K, D), S.row_bytes(S.T_Q4_K, F)
+    gw2, dw2 = gw.reshape(E * F, rbg), dw.reshape(E * D, rbd)
+    for t in range(T):
+        ax = oracle.quantize_q8k(X[t])
+        for j in range(K):
+            e, slot = int(so[t, j]), t * K + j
+            ah = oracle.quantize_q8k(ho[t, j])
+            for r in range(F):
+                s, m = oracle.block_ints(S.T_Q4_K, gw2[e * F + r], ax)
+                assert np.array_equal(gs[slot, r], s) and np.array_equal(gm[slot, r], m), (t, j, r)
+            for r in range(D):
+                s, m = oracle.block_ints(S.T_Q4_K, dw2[e * D + r], ah)
+                assert np.array_equal(ds[slot, r], s) and np.array_equal(dm[slot, r], m), (t, j, r)
+    for t_ in (gate, up, down):
+        t_.free()
+
+
+def test_moe_grouped_nonfinite_logits(backend, oracle):
+    """Tokens whose router probabilities are not all finite pick one expert several times, as the
+    reference's repeated argmax does (a picked probability becomes -1 and stays a candidate): one
+    token with only two finite logits for k = 4, one all NaN, one with +inf. The other tokens of the
+    same batch keep their results bit for bit (each expert's bucket holds every slot of the call),
+    and the next call starts from cleared counts."""
+    E, K, D, F, T = 16, 4, 512, 256, 8
+    gw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 710)
+    uw = S.random_bytes_weights(S.T_Q4_K, E * F, D, 711)
+    dw = S.random_bytes_weights(S.T_Q4_K, E * D, F, 712)
+    X = S.activations(D, 713, rows=T)
+    logits = S.router_logits(T, E, 714)
+    logits[2, 2:] = np.nan
+    logits[4, :] = np.nan
+    logits[6, 5] = np.inf
+    Yo, so, wo = oracle.moe_ffn((S.T_Q4_K,) * 3, gw, uw, dw, E, K, D, F, logits, X)
+    gate, up, down = (upload_experts(backend, a, c, r, E) for a, c, r in ((gw, D, F), (uw, D, F), (dw, F, D)))
+    for rep in range(2):
+        Y, sel, w = backend.moe_ffn(gate, up, down, K, logits, X)
+        assert np.array_equal(sel, so), rep
+        assert np.array_equal(np.isnan(w), np.isnan(wo)) and bits_equal(np.nan_to_num(w), np.nan_to_num(wo)), rep
+        assert np.array_equal(np.isnan(Y), np.isnan(Yo)), rep
+        assert bits_equal(np.where(np.isnan(Y), 0, Y), np.where(np.isnan(Yo), 0, Yo)), rep
+    assert (so[2, 2:] == so[2, 1]).all() or len(set(so[2])) < K  # the duplicate picks happened
+    for t_ in (gate, up, down):
+        t_.free()
