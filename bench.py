@@ -529,19 +529,37 @@ def main() -> int:
         gbs = nbytes / (us * 1e-6) / 1e9
         kernels[n] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                       "rotation_MB": round(nbytes * (ngu if n.startswith("gate+up") else len(rot[n])) / 1e6)}
-    # the same byte count read by a plain streaming kernel (fgh_checksum_dev: 16-byte loads, four in
-    # flight per thread, a sum and nothing else), rotating over at least 1 GB of buffers: the read
-    # rate this box delivers to a simple stream, beside the 8 TB/s peak
-    rbytes = (GATE_UP_BYTES + 15) // 16 * 16
-    nr = -(-int(2 * ROT_BYTES) // rbytes)
-    rbufs = [be.dev_alloc(rbytes) for _ in range(nr)]
-    rus = kernel_time(lambda i: be.checksum_dev(rbufs[i % nr], rbytes, 0), args.kernel_reps)  # streaming pass only
-    for p in rbufs:
-        be.dev_free(p)
+    # the HBM rate this box delivers to a plain stream (fgh_checksum_dev: each workgroup reads one
+    # contiguous share with nontemporal 16-byte loads, a sum and nothing else, the fastest read of a
+    # sweep of shapes), at the gate+up byte count and at 1 GB, each rotating over at least 2 GB of
+    # buffers; and the HIP runtime's own device-to-device copy of 1 GB (hipMemcpyAsync, read plus
+    # write bytes), an independent figure
+    def read_rate(nbytes: int, reps: int):
+        nbytes = (nbytes + 15) // 16 * 16
+        n = max(2, -(-int(4 * ROT_BYTES) // nbytes))
+        bufs = [be.dev_alloc(nbytes) for _ in range(n)]
+        us = kernel_time(lambda i: be.checksum_dev(bufs[i % n], nbytes, 0), reps)  # streaming pass only
+        for p in bufs:
+            be.dev_free(p)
+        return nbytes, us, n
+    rbytes, rus, nr = read_rate(GATE_UP_BYTES, args.kernel_reps)
     rgbs = rbytes / (rus * 1e-6) / 1e9
-    read_reference = {"kernel": "checksum_kernel (plain streaming read of the gate+up byte count)", "bytes": rbytes,
-                      "us": round(rus, 3), "GB/s": round(rgbs, 1), "frac": round(rgbs / HBM_PEAK_GBS, 4),
-                      "rotation_MB": round(nr * rbytes / 1e6)}
+    gbytes, gus, ngb = read_rate(1 << 30, 50)
+    ggbs = gbytes / (gus * 1e-6) / 1e9
+    cbytes = 1 << 30
+    cbufs = [be.dev_alloc(cbytes) for _ in range(4)]
+    cus = kernel_time(lambda i: be.memcpy_dev(cbufs[2 * (i % 2) + 1], cbufs[2 * (i % 2)], cbytes), 50)
+    for p in cbufs:
+        be.dev_free(p)
+    cgbs = 2 * cbytes / (cus * 1e-6) / 1e9
+    read_reference = {"kernel": "checksum_part_kernel (plain streaming read: contiguous share per workgroup, "
+                                "nontemporal 16-byte loads)",
+                      "bytes": rbytes, "us": round(rus, 3), "GB/s": round(rgbs, 1), "frac": round(rgbs / HBM_PEAK_GBS, 4),
+                      "rotation_MB": round(nr * rbytes / 1e6),
+                      "at_1GB": {"bytes": gbytes, "us": round(gus, 3), "GB/s": round(ggbs, 1),
+                                 "frac": round(ggbs / HBM_PEAK_GBS, 4), "rotation_MB": round(ngb * gbytes / 1e6)},
+                      "hipMemcpyAsync_1GB": {"bytes_read_plus_written": 2 * cbytes, "us": round(cus, 3),
+                                             "GB/s": round(cgbs, 1), "frac": round(cgbs / HBM_PEAK_GBS, 4)}}
 
     # the int8 MFMA rate a kernel that runs nothing but MFMA chains gets on this box: the attainable
     # peak beside the published 5.0 POPS (fgh_mfma_peak_dev, 2000 rounds per launch)
@@ -559,7 +577,8 @@ def main() -> int:
                 "kernel": "q4k_mv_kernel<repacked, 1 wavefront per 16-row tile> (Q4_K decode matvec, FFN gate + up "
                           "4096->2x14336 in one launch)",
                 "bytes_per_launch": GATE_UP_BYTES, "us_per_launch": g["us"],
-                "frac_of_read_reference": round(g["GB/s"] / rgbs, 4)}
+                "frac_of_read_reference": round(g["GB/s"] / rgbs, 4),
+                "frac_of_read_reference_1GB": round(g["GB/s"] / ggbs, 4)}
 
     # prefill: 64 tokens x 4096 -> 14336 Q4_K on the int8 MFMA GEMM; one launch
     # = device Q8_K quantization of X + the GEMM. Cold: rotating over the 2 * COPIES distinct

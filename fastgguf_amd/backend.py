@@ -29,7 +29,7 @@ EXPORTS = (
     "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matvec_silu_dev", "fgh_matvec_gate_up_silu_dev", "fgh_matmul_dev", "fgh_matmul_dev_noalloc", "fgh_moe_ffn_dev",
     "fgh_attention_dev", "fgh_kvq_store_dev", "fgh_kvq_attention_dev",
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
-    "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_mfma_peak_dev", "fgh_sync",
+    "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_memcpy_dev", "fgh_mfma_peak_dev", "fgh_sync",
     "fgh_event_create", "fgh_event_record", "fgh_event_elapsed_ms", "fgh_event_destroy",
     "fgh_quantize", "fgh_block_ints", "fgh_gemm_block_ints", "fgh_moe_block_ints", "fgh_expf", "fgh_fp16_to_f32", "fgh_matvec_shape",
     "fgh_gguf_open", "fgh_gguf_close", "fgh_gguf_summary", "fgh_gguf_tensor", "fgh_gguf_find",
@@ -99,6 +99,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_copy_d2h": (i32, [vp, vp, vp, u64]),
         "fgh_copy_d2d": (i32, [vp, vp, vp, u64]),
         "fgh_checksum_dev": (i32, [vp, vp, u64, vp]),
+        "fgh_memcpy_dev": (i32, [vp, vp, vp, u64]),
         "fgh_mfma_peak_dev": (i32, [vp, i32, C.POINTER(u64)]),
         "fgh_sync": (i32, [vp]),
         "fgh_event_create": (i32, [vp, C.POINTER(vp)]),
@@ -385,6 +386,10 @@ class Backend:
 
     def d2d(self, dst: int, src: int, nbytes: int):
         self._check(self.lib.fgh_copy_d2d(self.ctx, dst, src, nbytes))
+
+    def memcpy_dev(self, dst: int, src: int, nbytes: int):
+        """hipMemcpyAsync device to device on the context stream (the runtime's copy)."""
+        self._check(self.lib.fgh_memcpy_dev(self.ctx, dst, src, nbytes))
 
     def checksum_dev(self, src: int, nbytes: int, out: int):
         """Wrapping 32-bit word sum of nbytes at src, into the device word at out (asynchronous)."""

@@ -1100,7 +1100,14 @@ int fgh_checksum_dev(fgh_ctx *c, const void *src, uint64_t bytes, uint32_t *out)
     const int np = fgh::checksum_parts(c->num_cu);
     int rc;
     if ((rc = grow(c, c->ck, (size_t)np * 4))) return rc;
-    HIP_TRY(c, fgh::launch_checksum(src, (int64_t)(bytes / 16), (uint32_t *)c->ck.p, np, out, c->stream));
+    HIP_TRY(c, fgh::launch_checksum(src, (int64_t)(bytes / 16), (uint32_t *)c->ck.p, c->num_cu, out, c->stream));
+    return FGH_OK;
+}
+int fgh_memcpy_dev(fgh_ctx *c, void *dst, const void *src, uint64_t bytes) {
+    if (!c) return FGH_ERR_ARG;
+    if (!dst || !src) return fail(c, FGH_ERR_ARG, "memcpy_dev: null pointer");
+    HIP_TRY(c, hipSetDevice(c->device));
+    if (bytes) HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->stream));
     return FGH_OK;
 }
 

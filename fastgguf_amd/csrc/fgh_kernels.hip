@@ -232,12 +232,16 @@ hipError_t launch_copy16(const void *src, void *dst, int64_t n16, hipStream_t s)
     return hipGetLastError();
 }
 
-// Wrapping 32-bit sum of the little-endian words of n16 16-byte units in two launches: each
-// thread of the first (16 workgroups per CU) streams its grid-stride share eight units at a time
-// (eight 16-byte loads in flight) and each workgroup writes its part; the second adds the parts (integer wrapping addition
-// is associative: the result does not depend on the launch shape). The kernel boundary makes the
-// parts visible across the XCDs (a release inside the first kernel would write back L2 once per
-// workgroup).
+// Wrapping 32-bit sum of the little-endian words of n16 16-byte units in two launches: the first
+// gives each workgroup one contiguous share of the buffer, which its threads stream with U
+// nontemporal 16-byte loads in flight each, and writes the share's sum; the second adds the parts
+// (integer wrapping addition is associative: the result does not depend on the launch shape). The
+// kernel boundary makes the parts visible across the XCDs. The shape is the fastest of a sweep on
+// MI355X (workgroups per CU 8 / 16 / 32, loads in flight 4 / 8 / 16, grid-stride or contiguous
+// shares, default or nontemporal loads, 66 MB to 1 GB rotating over 3 GB): contiguous shares with
+// nontemporal loads, 32 workgroups per CU of 4 loads each below 128 MB (66 MB: 5.85 TB/s against
+// 5.10 for the grid-stride form), 16 of 8 loads above (1 GB: 6.98 TB/s against 5.13); hipMemcpyAsync
+// moves 4.9-5.4 TB/s (read plus write) in the same sweep.
 __device__ __forceinline__ uint32_t wg_sum256(uint32_t v, uint32_t *red) {
     v += __shfl_xor(v, 32);
     v += __shfl_xor(v, 16);
@@ -249,22 +253,26 @@ __device__ __forceinline__ uint32_t wg_sum256(uint32_t v, uint32_t *red) {
     __syncthreads();
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
+typedef unsigned ck_u32x4 __attribute__((ext_vector_type(4)));
+template <int U>
 __global__ __launch_bounds__(256) void checksum_part_kernel(const uint4 *__restrict__ src, int64_t n16,
                                                             uint32_t *__restrict__ part) {
     __shared__ uint32_t red[4];
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const int64_t lo = min((int64_t)blockIdx.x * per, n16), hi = min(lo + per, n16);
+    const ck_u32x4 *p = (const ck_u32x4 *)src;
+    int64_t i = lo + threadIdx.x;
     uint32_t sum = 0;
-    for (; i + 7 * stride < n16; i += 8 * stride) {
-        uint4 a[8];
+    for (; i + (U - 1) * 256 < hi; i += U * 256) {
+        ck_u32x4 a[U];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) a[u] = src[i + u * stride];
+        for (int u = 0; u < U; ++u) a[u] = __builtin_nontemporal_load(p + i + u * 256);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) sum += (a[u].x + a[u].y) + (a[u].z + a[u].w);
+        for (int u = 0; u < U; ++u) sum += (a[u][0] + a[u][1]) + (a[u][2] + a[u][3]);
     }
-    for (; i < n16; i += stride) {
-        const uint4 a = src[i];
-        sum += (a.x + a.y) + (a.z + a.w);
+    for (; i < hi; i += 256) {
+        const ck_u32x4 a = __builtin_nontemporal_load(p + i);
+        sum += (a[0] + a[1]) + (a[2] + a[3]);
     }
     const uint32_t ws = wg_sum256(sum, red);
     if (threadIdx.x == 0) part[blockIdx.x] = ws;
@@ -277,11 +285,14 @@ __global__ __launch_bounds__(256) void checksum_final_kernel(const uint32_t *__r
     const uint32_t total = wg_sum256(v, red);
     if (threadIdx.x == 0) *out = total;
 }
-int checksum_parts(int num_cu) { return 16 * num_cu; }  // (measured: the best plain stream at 66 MB)
+int checksum_parts(int num_cu) { return 32 * num_cu; }  // the most workgroups a launch uses
 // out == nullptr: the streaming part only
-hipError_t launch_checksum(const void *src, int64_t n16, uint32_t *part, int nparts, uint32_t *out, hipStream_t s) {
-    checksum_part_kernel<<<nparts, 256, 0, s>>>((const uint4 *)src, n16, part);
-    if (out) checksum_final_kernel<<<1, 256, 0, s>>>(part, nparts, out);
+hipError_t launch_checksum(const void *src, int64_t n16, uint32_t *part, int num_cu, uint32_t *out, hipStream_t s) {
+    const bool small = n16 * 16 < ((int64_t)128 << 20);
+    const int np = small ? 32 * num_cu : 16 * num_cu;
+    if (small) checksum_part_kernel<4><<<np, 256, 0, s>>>((const uint4 *)src, n16, part);
+    else checksum_part_kernel<8><<<np, 256, 0, s>>>((const uint4 *)src, n16, part);
+    if (out) checksum_final_kernel<<<1, 256, 0, s>>>(part, np, out);
     return hipGetLastError();
 }
 

@@ -182,29 +182,29 @@ struct StepW<T_Q6_K> {
 // T: the tile (wavefront-uniform)
 __device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q8_0> &w) {
     const BufRes r = buf_res(T, Q80_TILE);
-    w.q = bld16(r, 64 + 16 * lane);
-    w.d = bld8(r, 8 * (lane >> 3));
+    w.q = bld16<WNT>(r, 64 + 16 * lane);
+    w.d = bld8<WNT>(r, 8 * (lane >> 3));
 }
 template <int TYPE>
 __device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<TYPE> &w) {
     constexpr Q32Layout L = q32_layout(TYPE);
     const BufRes r = buf_res(T, L.tile);
-    w.n = bld8(r, L.n + 8 * lane);
+    w.n = bld8<WNT>(r, L.n + 8 * lane);
     if (L.m >= 0) {  // the row's d and m in one record
-        const uint4 dm = bld16(r, L.ds * (lane >> 3));
+        const uint4 dm = bld16<WNT>(r, L.ds * (lane >> 3));
         w.d = make_uint2(dm.x, dm.y);
         w.m = make_uint2(dm.z, dm.w);
     } else {
-        w.d = bld8(r, L.ds * (lane >> 3));
+        w.d = bld8<WNT>(r, L.ds * (lane >> 3));
     }
-    if (L.h >= 0) w.h = bld2(r, L.h + 2 * lane);
+    if (L.h >= 0) w.h = bld2<WNT>(r, L.h + 2 * lane);
 }
 __device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q6_K> &w) {
     const BufRes r = buf_res(T, Q6K_TILE);
-    w.q = bld16(r, 144 + 16 * lane);
-    w.h = bld8(r, 1168 + 8 * lane);
-    w.sc = bld16(r, 16 * (lane >> 3));
-    w.d = bld2(r, 128 + 2 * (lane >> 3));
+    w.q = bld16<WNT>(r, 144 + 16 * lane);
+    w.h = bld8<WNT>(r, 1168 + 8 * lane);
+    w.sc = bld16<WNT>(r, 16 * (lane >> 3));
+    w.d = bld2<WNT>(r, 128 + 2 * (lane >> 3));
 }
 
 // the lane's partial s_i of each of the step's 4 blocks (y: the lane's activation dword of each)

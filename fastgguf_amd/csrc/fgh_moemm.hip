@@ -82,9 +82,9 @@ struct MmW {
 };
 __device__ __forceinline__ void mm_wload(const uint8_t *blk, uint32_t L, uint32_t n, bool live, MmW &w) {
     const BufRes r = buf_res(blk, live ? Q4K_TILE : 0);
-    w.p0 = bld16(r, 256 + 16 * L);
-    w.p1 = bld16(r, 1280 + 16 * L);
-    w.m = bld16(r, 16 * n);
+    w.p0 = bld16<WNT>(r, 256 + 16 * L);
+    w.p1 = bld16<WNT>(r, 1280 + 16 * L);
+    w.m = bld16<WNT>(r, 16 * n);
 }
 
 struct MmArgs {

@@ -142,10 +142,10 @@ struct RbW {
 template <int TYPE = T_Q4_K>
 __device__ __forceinline__ void rb_load(const uint8_t *T, uint32_t lane, RbW &w, bool live = true) {
     const BufRes r = buf_res(T, live ? rb_bytes(TYPE) : 0);
-    w.p0 = bld16(r, 256 + 16 * lane);
-    w.p1 = bld16(r, 1280 + 16 * lane);
-    w.m = bld16(r, 16 * (lane >> 2));
-    if (TYPE == T_Q5_K) w.h = bld8(r, 2304 + 8 * lane);
+    w.p0 = bld16<WNT>(r, 256 + 16 * lane);
+    w.p1 = bld16<WNT>(r, 1280 + 16 * lane);
+    w.m = bld16<WNT>(r, 16 * (lane >> 2));
+    if (TYPE == T_Q5_K) w.h = bld8<WNT>(r, 2304 + 8 * lane);
 }
 
 // Per-lane constants of the scale extraction: chunk j, the shift selecting bytes 2(j & 1) and

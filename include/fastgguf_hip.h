@@ -270,10 +270,16 @@ FGH_API int fgh_copy_d2d(fgh_ctx *ctx, void *dst_dev, const void *src_dev, uint6
 /* wrapping 32-bit sum of the little-endian 32-bit words of a device buffer (bytes % 16 == 0),
  * written to *out_dev (device memory), asynchronous on the context stream: an integrity check of
  * uploaded or copied data, and the plain streaming-read kernel that gives the read rate a
- * matvec's weight stream is compared against (out_dev == NULL: only the streaming pass runs, its
- * per-workgroup parts stay in the context). No counterpart in the reference (device-side helper).
+ * matvec's weight stream is compared against: each workgroup streams one contiguous share with
+ * nontemporal 16-byte loads, the fastest read form measured on MI355X (out_dev == NULL: only the
+ * streaming pass runs, its per-workgroup parts stay in the context). No counterpart in the
+ * reference (device-side helper).
  * The first call allocates a small part buffer: make it once before graph capture. */
 FGH_API int fgh_checksum_dev(fgh_ctx *ctx, const void *src_dev, uint64_t bytes, uint32_t *out_dev);
+/* device-to-device copy by the HIP runtime (hipMemcpyAsync on the context stream): the runtime's
+ * own copy rate, an independent figure beside fgh_checksum_dev's read rate. No counterpart in the
+ * reference. */
+FGH_API int fgh_memcpy_dev(fgh_ctx *ctx, void *dst_dev, const void *src_dev, uint64_t bytes);
 /* The int8 MFMA rate this device delivers to a kernel that runs nothing but MFMA: one launch, on
  * the context stream, of 8 independent v_mfma_i32_16x16x64_i8 chains per wavefront for `iters`
  * rounds over two 4-wavefront workgroups per compute unit (no memory traffic); *ops receives the
