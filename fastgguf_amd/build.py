@@ -83,7 +83,7 @@ def build_oracle(verbose: bool = True) -> None:
     odir = os.path.join(ROOT, "oracle")
     targets = ["all"]
     if os.path.exists("/root/reference/fastgguf.c"):
-        targets.append("ref")
+        targets += ["ref", "ref-hip"]
     r = subprocess.run(["make", "-C", odir, "-B"] + targets, capture_output=True, text=True)
     if verbose:
         print(r.stdout[-2000:], flush=True)
@@ -91,6 +91,22 @@ def build_oracle(verbose: bool = True) -> None:
         raise RuntimeError(f"oracle build failed:\n{r.stderr[-4000:]}")
 
 
+C_CALLER = os.path.join(ROOT, "tests", "c_abi", "_build", "abi_smoke")
+
+
+def build_c_caller() -> str:
+    """Builds the plain C caller of the ABI (tests/c_abi/abi_smoke.c) with gcc against the header
+    and the library, as fastgguf.c would link it; its device branch runs in the GPU suite."""
+    os.makedirs(os.path.dirname(C_CALLER), exist_ok=True)
+    rc, err = _run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "c_abi", "abi_smoke.c"), "-o", C_CALLER, "-L", HERE,
+                    "-lfastgguf_hip", "-Wl,-rpath,$ORIGIN/../../../fastgguf_amd"])
+    if rc != 0:
+        raise RuntimeError(f"C caller build failed ({rc}):\n{err}")
+    return C_CALLER
+
+
 if __name__ == "__main__":
     build()
     build_oracle()
+    build_c_caller()

@@ -266,7 +266,10 @@ def _cpu_has_vnni() -> bool:
 
 
 class Reference:
-    """The reference's own kernels, compiled from /root/reference (oracle/_ref)."""
+    """The reference's own kernels, compiled from /root/reference (oracle/_ref). Variant "hip" is the
+    harness on the copy of fastgguf.c that include/fastgguf_c_hip.patch patches: its matvec,
+    matvec_multi, matmul and moe_ffn are the reference's call sites, routed to the gfx950 library
+    once hip_init() has opened a device (the drop-in test's caller, not a checker)."""
 
     def __init__(self, variant: str | None = None):
         if variant is None:
@@ -307,7 +310,20 @@ class Reference:
         L.fgr_kvq_attn_rows.argtypes = [C.c_int] + [C.c_void_p] * 6 + [C.c_int, C.c_int, C.c_void_p] + \
             [C.c_int] * 4 + [C.c_float]
         L.fgr_gguf_table.argtypes = [C.c_char_p] + [C.c_void_p] * 10 + [C.c_int64, C.c_char_p, C.c_int, C.c_void_p]
+        if variant == "hip":
+            L.fgr_hip_init.argtypes = [C.c_int]
+            L.fgr_hip_state.argtypes = [C.c_void_p]
         L.fgr_init(256)
+
+    def hip_init(self, mode: int = 0) -> int:
+        """The patched build only (variant "hip"): its fg_gpu_init_ex(mode); 1 = on the device."""
+        return self.lib.fgr_hip_init(mode)
+
+    def hip_state(self):
+        """(g_gpu.state, n_offloaded, n_skip_type, n_skip_mem) of the patched build."""
+        c = np.zeros(3, np.int32)
+        st = self.lib.fgr_hip_state(_ptr(c))
+        return (st, int(c[0]), int(c[1]), int(c[2]))
 
     @property
     def build(self) -> str:

@@ -7,6 +7,11 @@
  * linked into the product library. The reference source is #included, not copied: compiling it
  * with FG_VARIANT set renames its main() functions (fastgguf.c:51-59) so this file can add its own
  * exported wrappers around the `static` kernels.
+ *
+ * Built with FG_HIP on a copy of fastgguf.c that include/fastgguf_c_hip.patch has patched, the same
+ * wrappers run the reference's own call sites (matvec 2575, matvec_multi 2552, matmul 3004,
+ * moe_ffn 4588) with their tensors uploaded by the patched gpu_upload_tensor (2060): the drop-in
+ * test calls them on the GPU box and compares with the unpatched build's CPU results.
  */
 #define FG_VARIANT ref
 #include FG_REF_SOURCE
@@ -22,6 +27,23 @@ FGR_EXPORT void fgr_init(int max_cols) {
 }
 
 FGR_EXPORT int fgr_threads(void) { return omp_get_max_threads(); }
+
+#ifdef FG_HIP
+/* the patched fg_gpu_init_ex (1968; mode 0 honours FASTGGUF_GPU, 1 probes) and what it left in
+ * g_gpu: state 1 ready, -1 on the CPU; counts[3] = n_offloaded, n_skip_type, n_skip_mem */
+FGR_EXPORT int fgr_hip_init(int mode) {
+    fg_gpu_init_ex(mode);
+    return g_gpu.state;
+}
+FGR_EXPORT int fgr_hip_state(int *counts) {
+    if (counts) {
+        counts[0] = g_gpu.n_offloaded;
+        counts[1] = g_gpu.n_skip_type;
+        counts[2] = g_gpu.n_skip_mem;
+    }
+    return g_gpu.state;
+}
+#endif
 
 FGR_EXPORT void fgr_quantize_q8(const float *x, void *out, int n) { quantize_q8(x, (q8_blk_t *)out, n); }
 FGR_EXPORT void fgr_quantize_q8k(const float *x, void *out, int n) { quantize_q8k(x, (q8k_blk_t *)out, n); }
@@ -51,6 +73,10 @@ static int make_tensor(tensor_t *t, uint32_t type, int repack, const uint8_t *w,
     t->data = w;
     t->nbytes = row_stride(type, (uint64_t)cols) * (uint64_t)rows;
     *copy = NULL;
+#ifdef FG_HIP
+    gpu_upload_tensor(t);     /* before the repack, as in model_load (4509-4557) */
+    if (t->gpu) return 0;
+#endif
     if (repack) {
         *copy = (uint8_t *)malloc(t->nbytes);
         if (!*copy) return -1;
@@ -62,6 +88,13 @@ static int make_tensor(tensor_t *t, uint32_t type, int repack, const uint8_t *w,
 }
 
 static void drop_tensor(tensor_t *t, uint8_t *copy) {
+#ifdef FG_HIP
+    if (t->gpu) {
+        fgh_tensor_free((fgh_tensor *)t->gpu);
+        g_gpu.used -= t->nbytes;
+        t->gpu = NULL;
+    }
+#endif
     free((void *)t->rp);
     free(copy);
 }
@@ -138,6 +171,14 @@ FGR_EXPORT int fgr_moe_ffn(uint32_t tg_type, uint32_t tu_type, uint32_t td_type,
     memset(&LL, 0, sizeof(LL));
     LL.ffn_gate_inp = &ti; LL.ffn_gate_exps = &tg; LL.ffn_up_exps = &tu; LL.ffn_down_exps = &td;
     int rc = 0;
+#ifdef FG_HIP
+    tg.nbytes = row_stride(tg_type, (uint64_t)n_embd) * ff * n_expert;
+    tu.nbytes = row_stride(tu_type, (uint64_t)n_embd) * ff * n_expert;
+    td.nbytes = row_stride(td_type, (uint64_t)ff) * n_embd * n_expert;
+    gpu_upload_tensor(&tg);
+    gpu_upload_tensor(&tu);
+    gpu_upload_tensor(&td);
+#endif
     for (int t = 0; t < n_tok && rc == 0; t++) {
         const float *x = X + (size_t)t * n_embd;
         if (x[0] != 1.0f) { rc = -2; break; }
@@ -148,6 +189,11 @@ FGR_EXPORT int fgr_moe_ffn(uint32_t tg_type, uint32_t tu_type, uint32_t td_type,
             if (w_out) w_out[(size_t)t * k + j] = mm->moe_w[j];
         }
     }
+#ifdef FG_HIP
+    drop_tensor(&tg, NULL);
+    drop_tensor(&tu, NULL);
+    drop_tensor(&td, NULL);
+#endif
     free(mm->moe_probs); free(mm->moe_w); free(mm->moe_sel); free(mm->moe_h);
     free(mm->moe_xq); free(mm->moe_xk); free(mm); free(router);
     return rc;

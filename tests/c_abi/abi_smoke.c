@@ -5,7 +5,9 @@
  *
  * argv[1]: a GGUF file (tests/golden/tiny.gguf). Without a usable device fgh_open fails and the
  * program, like fastgguf.c's fg_gpu_init, stays on its CPU path; with one, it runs a closed-form
- * Q8_0 matvec (every weight 3, scale 1, x = 127 -> q = 127, d = 1: y = 3 * 127 * 256 = 97536). */
+ * Q8_0 matvec (every weight 3, scale 1, x = 127 -> q = 127, d = 1: y = 3 * 127 * 256 = 97536),
+ * the same product through the prompt GEMM for 16 tokens (token b's x = 127 - b, so its outputs are
+ * 3 * 256 * (127 - b): q = 127 - b with d = 1), and checks the upload counters. */
 #include <stdio.h>
 #include <string.h>
 
@@ -50,6 +52,18 @@ int main(int argc, char **argv) {
              fgh_matvec(ctx, t, x, y) == FGH_OK;
     for (int r = 0; ok && r < ROWS; r++) ok = y[r] == 97536.0f;
     printf("matvec: %s\n", ok ? "ok" : fgh_last_error(ctx));
+    enum { NB = 16 };
+    static float X[NB * COLS], Y[NB * ROWS];
+    for (int b = 0; b < NB; b++)
+        for (int k = 0; k < COLS; k++) X[b * COLS + k] = (float)(127 - b);
+    int okm = ok && fgh_matmul(ctx, t, X, COLS, Y, ROWS, NB) == FGH_OK;
+    for (int b = 0; okm && b < NB; b++)
+        for (int r = 0; okm && r < ROWS; r++) okm = Y[b * ROWS + r] == 3.0f * 256.0f * (float)(127 - b);
+    printf("matmul: %s\n", okm ? "ok" : fgh_last_error(ctx));
+    fgh_info_t in;
+    int oki = fgh_info(ctx, &in) == FGH_OK && in.n_offloaded == 1 && in.used > 0;
+    printf("info: %s (%s, %llu MB)\n", oki ? "ok" : "wrong counters", in.name, (unsigned long long)(in.vram >> 20));
+    ok = ok && okm && oki;
     fgh_tensor_free(t);
     fgh_close(ctx);
     fgh_gguf_close(g);
