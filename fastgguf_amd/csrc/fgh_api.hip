@@ -62,9 +62,12 @@ struct fgh_ctx {
     int32_t *moe_dump[4] = {nullptr, nullptr, nullptr, nullptr};
 };
 
-// fgh_matmul_dev_noalloc's scratch: a static array, one copy per device. In host code its name
-// is only a host-side stand-in; kernels get the device address that hipGetSymbolAddress returns
-// with the device current, taken once per device at its first fgh_open and kept here.
+// fgh_matmul_dev_noalloc's scratch: a static array, one copy per device. Every prompt GEMM keeps
+// its activation records here (Q4_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1), and the K-split ones
+// (Q4_K, Q6_K, Q8_0) their counters and partials after them (prompt_gemm_bytes sizes both). In
+// host code its name is only a host-side stand-in; kernels get the device address that
+// hipGetSymbolAddress returns with the device current, taken once per device at its first
+// fgh_open and kept here.
 static __device__ __align__(256) uint8_t scratch[FGH_NOALLOC_SCRATCH_BYTES];
 constexpr int MAX_DEVICES = 64;
 static std::mutex scratch_mu;

@@ -323,7 +323,11 @@ struct AvStage {
 // (int8 codes for VB = 8) through an LDS table when a tile is stored
 // SC: V read value by value (hd or kv_dim not a multiple of 4: a 16-byte read would not be aligned),
 // columns past hd reading column 0
-template <int CH, int AV_S, int VB, bool SC = false>  // AV_S: tiles in flight, 4 or 8 (the named stages below)
+// PR: the reference's per-row path (hd % 32 != 0, fastgguf.c:3318-3323): each row's chain walks
+// only its own positions st..en, so a position of another row of the group adds nothing to it (not
+// even fma(0, v, acc), which is NaN for a non-finite v and turns -0 into +0); the vector path's
+// att_v_kern walks the group's whole span with zero weights, as the chains do without PR
+template <int CH, int AV_S, int VB, bool SC = false, bool PR = false>  // AV_S: tiles in flight, 4 or 8 (the named stages below)
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_values_kernel(AttnArgs a,
                                                                                                      int n_tok) {
     constexpr int GR = 4 * CH;  // rows per group
@@ -404,8 +408,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     };
     auto in_range = [&](int p) { return p >= wg.st && p <= wg.en; };
     float acc[CH];
+    int rst[CH], ren[CH];  // PR: the ranges of this wavefront's rows (uniform over its lanes)
 #pragma unroll
-    for (int r = 0; r < CH; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < CH; ++r) {
+        acc[r] = 0.0f;
+        if constexpr (PR) {
+            const GroupRow g = group_row(a, n_tok, GR, grp, kh, CH * wave + r);
+            rst[r] = g.st;
+            ren[r] = g.en;
+        }
+    }
+    // acc = fma(w, v, acc) for a position p of row r's chain (PR: only inside its own range)
+    auto fma_at = [&](int r, int p, float w, float v) {
+        if constexpr (PR)
+            acc[r] = p >= rst[r] && p <= ren[r] ? __builtin_fmaf(w, v, acc[r]) : acc[r];
+        else
+            acc[r] = __builtin_fmaf(w, v, acc[r]);
+    };
     const float *vcol = (const float *)vt + lane;
     auto decode = [&](uint32_t c) -> av4 {  // 4 values of TurboQuant codes
         if constexpr (VB == 8)
@@ -443,15 +462,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         const int b = k & (NB - 1);
         const float *vs = vcol + b * 64 * 64;
         const int cnt = min(64, span - k * 64);  // <= 0 past the end
+        const int p0 = lo + k * 64;              // the tile's first position
         if constexpr (CH == 4) {
             const av4 *ws = (const av4 *)wt[b] + wave;  // [pos][16 rows]: this wavefront's 4
             auto chain = [&](int j) {
                 const float x = vs[j * 64];
                 const av4 w4 = ws[j * 4];
-                acc[0] = __builtin_fmaf(w4.x, x, acc[0]);
-                acc[1] = __builtin_fmaf(w4.y, x, acc[1]);
-                acc[2] = __builtin_fmaf(w4.z, x, acc[2]);
-                acc[3] = __builtin_fmaf(w4.w, x, acc[3]);
+                fma_at(0, p0 + j, w4.x, x);
+                fma_at(1, p0 + j, w4.y, x);
+                fma_at(2, p0 + j, w4.z, x);
+                fma_at(3, p0 + j, w4.w, x);
             };
             if (cnt == 64) {
 #pragma unroll 8
@@ -465,13 +485,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
                 for (int j4 = 0; j4 < 16; ++j4) {
                     const av4 w4 = *(const av4 *)(wf + 4 * j4);
-                    acc[0] = __builtin_fmaf(w4.x, vs[(4 * j4 + 0) * 64], acc[0]);
-                    acc[0] = __builtin_fmaf(w4.y, vs[(4 * j4 + 1) * 64], acc[0]);
-                    acc[0] = __builtin_fmaf(w4.z, vs[(4 * j4 + 2) * 64], acc[0]);
-                    acc[0] = __builtin_fmaf(w4.w, vs[(4 * j4 + 3) * 64], acc[0]);
+                    fma_at(0, p0 + 4 * j4 + 0, w4.x, vs[(4 * j4 + 0) * 64]);
+                    fma_at(0, p0 + 4 * j4 + 1, w4.y, vs[(4 * j4 + 1) * 64]);
+                    fma_at(0, p0 + 4 * j4 + 2, w4.z, vs[(4 * j4 + 2) * 64]);
+                    fma_at(0, p0 + 4 * j4 + 3, w4.w, vs[(4 * j4 + 3) * 64]);
                 }
             } else {
-                for (int j = 0; j < cnt; ++j) acc[0] = __builtin_fmaf(wf[j], vs[j * 64], acc[0]);
+                for (int j = 0; j < cnt; ++j) fma_at(0, p0 + j, wf[j], vs[j * 64]);
             }
         }
     };
@@ -543,7 +563,15 @@ hipError_t launch_attention_values(const AttnArgs &a, int n_tok, hipStream_t s) 
     const unsigned cch = (unsigned)((a.hd + 63) / 64), kvh = (unsigned)a.n_head_kv;
     const dim3 g16(cch, (unsigned)((rows_kv + 15) / 16), kvh), g4(cch, (unsigned)((rows_kv + 3) / 4), kvh);
     const int vb = a.vq ? a.vbits : 0;
-    if (sc) {
+    if (a.hd % 32 != 0) {  // the per-row path (TurboQuant V needs hd % 32 == 0)
+        if (sc) {
+            if (rows_kv >= 64) attn_values_kernel<4, 4, 0, true, true><<<g16, 256, 0, s>>>(a, n_tok);
+            else attn_values_kernel<1, 8, 0, true, true><<<g4, 256, 0, s>>>(a, n_tok);
+        } else {
+            if (rows_kv >= 64) attn_values_kernel<4, 4, 0, false, true><<<g16, 256, 0, s>>>(a, n_tok);
+            else attn_values_kernel<1, 8, 0, false, true><<<g4, 256, 0, s>>>(a, n_tok);
+        }
+    } else if (sc) {
         if (rows_kv >= 64) attn_values_kernel<4, 4, 0, true><<<g16, 256, 0, s>>>(a, n_tok);
         else attn_values_kernel<1, 8, 0, true><<<g4, 256, 0, s>>>(a, n_tok);
     } else if (rows_kv >= 64) {

@@ -210,15 +210,23 @@ FGH_API int fgh_matmul_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *X_dev
                    int ldy, int nb);
 /* fgh_matmul_dev without any device allocation. No counterpart in the reference: it is for
  * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
- * that forbid hipMalloc). The prompt GEMM's scratch (nb >= 8 tokens of a Q4_K tensor: the
- * activation records, (blocks + 1) * 292 * (nb rounded up to 16) bytes, and for a tensor with
- * fewer 64-row groups than half the compute units the K split's counters and partials, at most
- * 4 MiB) goes to a static device array of FGH_NOALLOC_SCRATCH_BYTES per device, held until the
- * process ends; a call that would need more fails with FGH_ERR_ARG before it launches anything.
- * Every call on a device shares that device's array: calls that overlap on one device (several
- * streams or contexts) race. Nothing in the array needs to start at zero; each call writes what
- * it reads (the split's counters are zeroed by the call's own first launch). Same results bit for
- * bit as fgh_matmul_dev. */
+ * that forbid hipMalloc). From nb >= 8 tokens the prompt GEMM's scratch goes to a static device
+ * array of FGH_NOALLOC_SCRATCH_BYTES per device, held until the process ends (under 8 tokens the
+ * decode kernels run and need none). Its size per type, Tp = nb rounded up to 16 (Q8_0: 32 or 64):
+ *   Q4_K, Q6_K  (256-blocks + 1) * 292 * Tp bytes of activation records;
+ *   Q8_0        (steps + KH) * 144 * Tp bytes of records, steps = ceil(32-blocks / 4), KH = 4
+ *               from 4 steps (2 for 2-3 steps, 1 for one);
+ *   Q4_0, Q4_1, Q5_0, Q5_1  (Tp / 16) * ceil(32-blocks / 4) * 2560 bytes of records;
+ * and for Q4_K, Q6_K and Q8_0 tensors with few 64-row groups (ks >= 2 K splits fit beside them on
+ * the compute units, as for a 14336 -> 4096 down projection) the split's counters, 4 bytes per
+ * group rounded to 256, and partials of ks * groups * 64 * Tp * 4 bytes, at most 4 MiB on 256
+ * compute units. At 64 tokens that holds every K the upload accepts when the GEMM does not split,
+ * and, with a split, Q4_K and Q6_K K <= 57088 (223 blocks) and Q8_0 K <= 57728 (1804 blocks). A
+ * call that would need more fails with FGH_ERR_ARG before it launches anything. Every call on a
+ * device shares that device's array: calls that overlap on one device (several streams or
+ * contexts) race. Nothing in the array needs to start at zero; each call writes what it reads
+ * (the split's counters are zeroed by the call's own first launch). Same results bit for bit as
+ * fgh_matmul_dev. */
 #define FGH_NOALLOC_SCRATCH_BYTES (8u << 20)
 FGH_API int fgh_matmul_dev_noalloc(fgh_ctx *ctx, const fgh_tensor *t, const float *X_dev, int ldx,
                            float *Y_dev, int ldy, int nb);

@@ -939,8 +939,10 @@ int fgo_moe_ffn(uint32_t type_gate, uint32_t type_up, uint32_t type_down,
  *            8-wide sum takes e[8g + l] in order), hsum8 of the lanes, then the tail with libm
  *            expf added in order; every value times 1 / sum
  *   o[c] = fma chain over the positions in order of w_p * v_p[c]   (att_v_kern 3249-3270)
- * A row of several rows' call sees zeros outside its own range, fma(0, v, acc) = acc: the
- * result is the row's own range's. */
+ * The vector path's chain walks the union lo..hi of the ranges of the call's rows (here: the rows
+ * with the same kvo) with weight 0 outside the row's own range (3296-3309); for finite V that
+ * adds nothing (fma(0, v, acc) = acc), while a non-finite v there makes the output NaN. The
+ * per-row path's chain walks the row's own range only (3318-3323). */
 static float exp_neg(float x) { /* exp_neg_ps (3168-3184), one lane */
     int keep = x > -87.0f;
     x = x > -87.0f ? x : -87.0f; /* max_ps(x, -87): -87 for a NaN */
@@ -1038,9 +1040,19 @@ int fgo_attn_rows(int nr, const float *q, float *o, const int *st, const int *en
         }
         softmax_vec_row(s, n);
         float *orow = o + (size_t)r * hd;
+        int lo = st[r], hi = en[r];
+        if (hd % 32 == 0)
+            for (int r2 = 0; r2 < nr; r2++)
+                if (kvo[r2] == kvo[r] && en[r2] >= st[r2]) {
+                    lo = st[r2] < lo ? st[r2] : lo;
+                    hi = en[r2] > hi ? en[r2] : hi;
+                }
         for (int c = 0; c < hd; c++) {
             float acc = 0.0f;
-            for (int p = st[r]; p <= en[r]; p++) acc = fmaf(s[p - st[r]], cv[(size_t)(p % cap) * kv_dim + kvo[r] + c], acc);
+            for (int p = lo; p <= hi; p++) {
+                float w = p >= st[r] && p <= en[r] ? s[p - st[r]] : 0.0f;
+                acc = fmaf(w, cv[(size_t)(p % cap) * kv_dim + kvo[r] + c], acc);
+            }
             orow[c] = acc;
         }
         free(s);

@@ -52,6 +52,18 @@ def rel_err(y, ref):
     return float(np.abs(y - ref).max() / (np.abs(ref).max() + 1e-30))
 
 
+def bits_equal_or_nan(a, b):
+    """bits_equal, with any NaN matching any NaN: the CPU's fma(0, inf) gives the x86 default NaN
+    (sign set), the GPU's the positive one."""
+    import numpy as np
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    if a.shape != b.shape:
+        return False
+    na, nb = np.isnan(a), np.isnan(b)
+    return bool(np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32)))
+
+
 def bits_equal(a, b):
     import numpy as np
     a = np.ascontiguousarray(a, np.float32)

@@ -71,19 +71,33 @@ ATTN_CASES = [
 ]
 
 
+#: non-finite V at positions that only one row of the call covers, (position, column of the head,
+#: value) each: the per-row path walks each row's own positions only, so the other row stays finite
+#: (aligned hd 36, and hd 13 read value by value); the vector path walks the call's whole span with
+#: zero weights outside a row's range, so fma(0, inf) makes the other row's column NaN there
+ATTN_NONFINITE = [
+    (36, 36, 0, 20, [0, 8], [5, 15], 1.0, [(12, 3, np.inf), (13, 7, np.nan)]),
+    (13, 26, 13, 16, [2, 9], [6, 14], 1.0, [(11, 0, np.inf), (3, 12, -np.inf)]),
+    (64, 128, 64, 32, [0, 8], [5, 15], 1.0, [(12, 3, np.inf), (2, 9, -np.inf)]),
+]
+
+
 def attn_cases(ref) -> dict:
     rng = np.random.default_rng(77)
     out = {}
-    for i, (hd, kv_dim, kvo, cap, st, en, mag) in enumerate(ATTN_CASES):
+    cases = [c + ([],) for c in ATTN_CASES] + ATTN_NONFINITE
+    for i, (hd, kv_dim, kvo, cap, st, en, mag, plants) in enumerate(cases):
         q = (rng.standard_normal((len(st), hd)) * mag).astype(np.float32)
         ck = rng.standard_normal((cap, kv_dim)).astype(np.float32)
         cv = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+        for p, col, v in plants:
+            cv[p % cap, kvo + col] = v
         scale = np.float32(1.0 / np.sqrt(hd))
         o = ref.attn_rows(q, st, en, ck, cv, kvo, hd, float(scale))
         out.update({f"c{i}_q": q, f"c{i}_ck": ck, f"c{i}_cv": cv, f"c{i}_st": np.array(st, np.int32),
                     f"c{i}_en": np.array(en, np.int32), f"c{i}_o": o,
                     f"c{i}_meta": np.array([hd, kvo], np.int32), f"c{i}_scale": np.array([scale], np.float32)})
-    out["n_cases"] = np.array([len(ATTN_CASES)], np.int32)
+    out["n_cases"] = np.array([len(cases)], np.int32)
     return out
 
 

@@ -9,7 +9,7 @@ scalar tail, and odd sizes whose rows are not 16-byte aligned.
 """
 import numpy as np
 import pytest
-from conftest import bits_equal
+from conftest import bits_equal, bits_equal_or_nan
 
 from fastgguf_amd.backend import BackendError
 
@@ -35,7 +35,7 @@ def test_attention_matches_golden(backend):
         q = rng.standard_normal((len(c["st"]), n_head, hd)).astype(np.float32)
         q[:, kvo // hd] = c["q"]
         o = backend.attention(q, c["ck"], c["cv"], c["st"], c["en"], n_head, c["scale"])
-        assert bits_equal(o[:, kvo // hd], c["o"]), (hd, kvo, c["st"], c["en"])
+        assert bits_equal_or_nan(o[:, kvo // hd], c["o"]), (hd, kvo, c["st"], c["en"])
 
 
 CASES = [  # (n_tok, n_head, n_head_kv, hd, cap, first position, magnitude)
@@ -69,6 +69,32 @@ def test_attention_matches_oracle(backend, oracle, case):
     scale = float(np.float32(1 / np.sqrt(hd)))
     o = backend.attention(q, ck, cv, st, en, n_kv, scale)
     assert bits_equal(o, oracle_attention(oracle, q, ck, cv, st, en, n_kv, scale))
+
+
+@pytest.mark.parametrize("case", [(70, 4, 2, 72, 100, 20), (66, 2, 1, 6, 80, 0), (3, 5, 5, 13, 30, 25)],
+                         ids=["d72_16row", "d6_16row_unaligned", "d13_4row_unaligned"])
+def test_attention_per_row_path_nonfinite_v(backend, oracle, case):
+    """The per-row path (hd % 32 != 0) walks each row's own positions only (fastgguf.c:3318-3323):
+    inf and NaN in V at the last position of a causal batch, which only the last token attends,
+    leave every other token's outputs finite, in the value kernel's 16-row and 4-row groups alike.
+    (The vector path walks its call's whole span, with NaN where fma(0, inf) falls: the golden
+    case with hd 64 covers that.)"""
+    n_tok, n_head, n_kv, hd, cap, p0 = case
+    rng = np.random.default_rng(hd + 7)
+    kv_dim = n_kv * hd
+    ck = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+    cv = rng.standard_normal((cap, kv_dim)).astype(np.float32)
+    q = rng.standard_normal((n_tok, n_head, hd)).astype(np.float32)
+    en = (p0 + 5 + np.arange(n_tok)).astype(np.int32)
+    st = np.full(n_tok, p0, np.int32)
+    last = int(en[-1]) % cap
+    cv[last, 0] = np.inf
+    cv[last, kv_dim - 1] = np.nan
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    o = backend.attention(q, ck, cv, st, en, n_kv, scale)
+    want = oracle_attention(oracle, q, ck, cv, st, en, n_kv, scale)
+    assert np.isfinite(want[:-1]).all() and not np.isfinite(want[-1]).all()
+    assert bits_equal_or_nan(o, want)
 
 
 def test_attention_long_decode(backend, oracle):

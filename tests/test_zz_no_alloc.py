@@ -38,9 +38,12 @@ def run_both(be, t, X):
 
 # (type, rows, cols, tokens): the first two take the prompt GEMM (Q4_K, >= 8 tokens), the larger
 # one first, so the second call reuses the array with a smaller input; the third runs the decode
-# kernels, which need no scratch; then the Q6_K GEMM and the nibble-type GEMM (Q5_1, then Q4_0
-# smaller)
-CALLS = [(S.T_Q4_K, 1024, 8192, 64), (S.T_Q4_K, 272, 2048, 9), (S.T_Q4_K, 128, 2048, 5), (S.T_Q6_K, 96, 1024, 12),
+# kernels, which need no scratch; then the Q6_K GEMM with a 4-way K split (4096 output rows: 64
+# row groups) and without, the Q8_0 GEMM with a K split and without (smaller), and the nibble-type
+# GEMM (Q5_1, then Q4_0 smaller)
+CALLS = [(S.T_Q4_K, 1024, 8192, 64), (S.T_Q4_K, 272, 2048, 9), (S.T_Q4_K, 128, 2048, 5),
+         (S.T_Q6_K, 4096, 14336, 64), (S.T_Q6_K, 96, 1024, 12),
+         (S.T_Q8_0, 4096, 14336, 64), (S.T_Q8_0, 512, 2048, 16),
          (S.T_Q5_1, 200, 4096, 40), (S.T_Q4_0, 64, 1024, 8)]
 
 
@@ -61,31 +64,43 @@ def test_noalloc_matches_matmul_dev(backend, fresh):
             be.close()
 
 
-def q4k_gemm_scratch(rows, nbk, T, num_cu=256):
-    """bytes of the Q4_K prompt GEMM's scratch: (nbk + 1) activation records of 292 * Tp bytes, and
-    with a K split (few row groups) the arrival counters and ks partials of 64 rows x Tp tokens of
-    fp32 per workgroup"""
+def _up(n, m=256):
+    return -(-n // m) * m
+
+
+def gemm_scratch(type_, rows, cols, T, num_cu=256):
+    """bytes of a prompt GEMM's scratch (Q4_K, Q6_K, Q8_0): the activation records, and with a K
+    split (few 64-row groups) the arrival counters and ks partials of 64 rows x Tp tokens of fp32
+    per workgroup"""
     wg = -(-rows // 64)
+    if type_ == S.T_Q8_0:
+        Tp = 32 if T <= 32 else 64
+        steps = -(-(cols // 32) // 4)
+        rec = (steps + (4 if steps >= 4 else 2 if steps >= 2 else 1)) * 144 * Tp
+        units, min_units = steps, 8
+    else:  # Q4_K, Q6_K: one 292-byte Q8_K record per 256-block and token, one of slack
+        Tp = -(-T // 16) * 16
+        rec = (cols // 256 + 1) * 292 * Tp
+        units, min_units = cols // 256, 4
     ks = 1
-    while ks < 4 and wg * (ks + 1) <= num_cu and nbk // (ks + 1) >= 4:
+    while ks < 4 and wg * (ks + 1) <= num_cu and units // (ks + 1) >= min_units:
         ks += 1
-    Tp = -(-T // 16) * 16
-    rec = (nbk + 1) * 292 * Tp
-    if ks == 1:
-        return rec
-    up = lambda n: -(-n // 256) * 256
-    return up(rec) + up(4 * wg) + ks * wg * 64 * Tp * 4
+    return rec if ks == 1 else _up(rec) + _up(4 * wg) + ks * wg * 64 * Tp * 4
 
 
-def test_noalloc_refuses_more_than_its_scratch(backend):
-    """4096 rows at 64 tokens (the down projection's output width, a 4-way K split): 223 blocks
-    need 224 records of 292 * 64 bytes plus the split's counters and 4 MiB of partials, within
-    8 MiB, and run; 224 blocks exceed it: refused, nothing launched, and the context still works"""
+@pytest.mark.parametrize("type_,largest", [(S.T_Q4_K, 223), (S.T_Q6_K, 223), (S.T_Q8_0, 1804)],
+                         ids=["Q4_K", "Q6_K", "Q8_0"])
+def test_noalloc_refuses_more_than_its_scratch(backend, type_, largest):
+    """4096 rows at 64 tokens (the down projection's output width, a 4-way K split): the largest K
+    whose records fit beside the split's counters and 4 MiB of partials within 8 MiB runs; one
+    block more is refused, nothing launched, and the context still works"""
     rows = 4096
-    for nbk, ok in ((223, True), (224, False)):
-        cols = 256 * nbk
-        assert (q4k_gemm_scratch(rows, nbk, 64) <= SCRATCH_BYTES) == ok
-        t = backend.upload(S.T_Q4_K, cols, S.weights(S.T_Q4_K, rows, cols, 720 + nbk))
+    blk = 32 if type_ == S.T_Q8_0 else 256
+    for nbk, ok in ((largest, True), (largest + 1, False)):
+        cols = blk * nbk
+        assert (gemm_scratch(type_, rows, cols, 64) <= SCRATCH_BYTES) == ok
+        print(f"noalloc {S.TYPE_NAME[type_]} {rows}x{cols} 64 tokens ({'fits' if ok else 'refused'})", flush=True)
+        t = backend.upload(type_, cols, S.weights(type_, rows, cols, 720 + nbk))
         X = S.activations(cols, 730, rows=64)
         if ok:
             got, want = run_both(backend, t, X)
