@@ -26,7 +26,7 @@ ACT_Q8, ACT_Q8K = 1, 2
 EXPORTS = (
     "fgh_open", "fgh_close", "fgh_info", "fgh_last_error", "fgh_upload", "fgh_tensor_free",
     "fgh_matvec", "fgh_matvec_multi", "fgh_matmul", "fgh_moe_ffn", "fgh_attention",
-    "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matvec_silu_dev", "fgh_matvec_gate_up_silu_dev", "fgh_matmul_dev", "fgh_matmul_dev_noalloc", "fgh_moe_ffn_dev",
+    "fgh_matvec_dev", "fgh_matvec_multi_dev", "fgh_matvec_silu_dev", "fgh_matvec_gate_up_silu_dev", "fgh_ffn_dev", "fgh_matmul_dev", "fgh_matmul_dev_noalloc", "fgh_moe_ffn_dev",
     "fgh_attention_dev", "fgh_kvq_store_dev", "fgh_kvq_attention_dev",
     "fgh_graph_begin", "fgh_graph_end", "fgh_graph_launch", "fgh_graph_destroy",
     "fgh_dev_alloc", "fgh_dev_free", "fgh_copy_h2d", "fgh_copy_d2h", "fgh_copy_d2d", "fgh_checksum_dev", "fgh_memcpy_dev", "fgh_mfma_peak_dev", "fgh_sync",
@@ -81,6 +81,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fgh_matvec_multi_dev": (i32, [vp, i32, vp, vp, vp]),
         "fgh_matvec_silu_dev": (i32, [vp, vp, vp, vp, vp]),
         "fgh_matvec_gate_up_silu_dev": (i32, [vp, vp, vp, vp, vp]),
+        "fgh_ffn_dev": (i32, [vp, vp, vp, vp, vp, vp, vp]),
         "fgh_matmul_dev": (i32, [vp, vp, vp, i32, vp, i32, i32]),
         "fgh_matmul_dev_noalloc": (i32, [vp, vp, vp, i32, vp, i32, i32]),
         "fgh_moe_ffn_dev": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, i32]),
@@ -458,6 +459,10 @@ class Backend:
         """h = silu(gate * Q(x)) * (up * Q(x)), the dense FFN's gate / up and the loop before
         its down projection (device pointers)."""
         self._check(self.lib.fgh_matvec_gate_up_silu_dev(self.ctx, gate.handle, up.handle, x_dev, h_dev))
+
+    def ffn_dev(self, gate: Tensor, up: Tensor, down: Tensor, x_dev: int, h_dev: int, y_dev: int) -> None:
+        """The dense SiLU FFN of one token (fgh_ffn_dev): h = silu(gate x) * (up x), y = down h."""
+        self._check(self.lib.fgh_ffn_dev(self.ctx, gate.handle, up.handle, down.handle, x_dev, h_dev, y_dev))
 
     def matvec_gate_up_silu(self, gate: Tensor, up: Tensor, x: np.ndarray) -> np.ndarray:
         """The same from a host array (copies in and out; for tests)."""

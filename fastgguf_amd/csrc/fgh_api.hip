@@ -675,6 +675,18 @@ int fgh_matvec_gate_up_silu_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_te
     return FGH_OK;
 }
 
+int fgh_ffn_dev(fgh_ctx *c, const fgh_tensor *gate, const fgh_tensor *up, const fgh_tensor *down, const float *x,
+                float *h, float *y) {
+    int rc;
+    if ((rc = check_tensor(c, gate)) || (rc = check_tensor(c, up)) || (rc = check_tensor(c, down))) return rc;
+    if (!x || !h || !y) return fail(c, FGH_ERR_ARG, "ffn: null pointer");
+    if (down->n_mats != 1 || down->cols != gate->rows)
+        return fail(c, FGH_ERR_ARG, "ffn: down must be one matrix whose columns are gate's rows");
+    // the paired gate / up launch writes h (or the matvecs and the silu launch), then down reads it
+    if ((rc = fgh_matvec_gate_up_silu_dev(c, gate, up, x, h))) return rc;
+    return fgh_matvec_dev(c, down, h, y);
+}
+
 int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, float *Y, int ldy, int nb) {
     int rc = check_tensor(c, t);
     if (rc) return rc;

@@ -206,6 +206,13 @@ FGH_API int fgh_matvec_silu_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *
  * fgh_matvec_multi_dev followed by that loop; h_dev then feeds fgh_matvec_dev(ffn_down). */
 FGH_API int fgh_matvec_gate_up_silu_dev(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tensor *up,
                                 const float *x_dev, float *h_dev);
+/* The dense SiLU FFN of one token: replaces forward's matvec_multi(ffn_gate, ffn_up), the loop
+ * `gate[i] = silu_f(gate[i]) * up[i]` and matvec(ffn_down, gate) (4870-4877): h_dev receives
+ * gate->rows values of h, y_dev down->rows outputs, bit for bit fgh_matvec_gate_up_silu_dev
+ * followed by fgh_matvec_dev(down, h_dev, y_dev), which is what it runs (two launches for Q4_K /
+ * Q5_K gate and up of one type and order). down: one matrix with gate->rows columns. */
+FGH_API int fgh_ffn_dev(fgh_ctx *ctx, const fgh_tensor *gate, const fgh_tensor *up, const fgh_tensor *down,
+                        const float *x_dev, float *h_dev, float *y_dev);
 FGH_API int fgh_matmul_dev(fgh_ctx *ctx, const fgh_tensor *t, const float *X_dev, int ldx, float *Y_dev,
                    int ldy, int nb);
 /* fgh_matmul_dev without any device allocation. No counterpart in the reference: it is for
