@@ -2,28 +2,33 @@
 """Benchmark of the quantized weight x Q8-activation hot path on one MI355X.
 
 Workload: one Llama-3-8B-shaped decode layer as Q4_K matvecs at batch 1:
-fused QKV 4096->6144, O 4096->4096, gate and up 4096->14336 (one shared activation), down
-14336->4096. A step quantizes each input vector on the device (bit-exact Q8_K) and runs the five
-matvecs. Weights are seeded synthetic Q4_K blocks with the benchmark's distributions; inputs are
+fused QKV 4096->6144, O 4096->4096, and the SiLU FFN: gate and up 4096->14336 (one shared
+activation), h = silu(gate) * up, down 14336->h->4096 (forward, fastgguf.c:4870-4877, through
+fgh_ffn_dev: the paired gate / up launch writes h, the down matvec reads it). A step quantizes each
+input vector on the device (bit-exact Q8_K) and runs the five matvecs in four launches. Weights are
+seeded synthetic Q4_K blocks with the benchmark's distributions; inputs are
 fp32 N(0,1) vectors already resident in HBM. To measure HBM and not the 256 MB Infinity Cache,
 steps rotate over COPIES distinct device copies of the layer (>= 512 MB in total). Steps are
 recorded as a real decode replays them: one HIP graph holds GRAPH_LAYERS consecutive layers
 (32, Llama-3-8B's depth), so the per-graph launch cost is spread over the layers it holds.
 
-value  = whole-layer algorithmic bytes (weights + fp32 x in + fp32 y out) / step time, in GB/s.
-roofline: the dominant kernel of the step is the Q4_K decode matvec launch of the FFN gate and up
-         projections together (4096->2x14336, one matvec_multi launch as the reference's forward
-         issues it); its duration is the mean over back-to-back launches captured in one HIP graph
-         and timed with HIP events on the library's stream. Every per-kernel timing rotates over
-         at least 512 MB of distinct weight copies.
+value  = whole-layer algorithmic bytes (weights + fp32 x in + fp32 y out of the five matvecs) /
+         step time, in GB/s.
+roofline: the dominant kernel of the step is the Q4_K decode launch of the FFN gate and up
+         projections paired (4096->2x14336 in one launch that writes h = silu(g) * u); its duration
+         is the mean over back-to-back launches captured in one HIP graph and timed with HIP events
+         on the library's stream. The matvec_multi launch of gate and up (g and u stored) is
+         reported beside it. Every per-kernel timing rotates over at least 512 MB of distinct
+         weight copies.
 prefill: BASELINE config 4 (64 tokens x 4096 -> 14336, Q4_K) on the int8 MFMA GEMM, timed the
          same way, cold (rotating weights) and Infinity-Cache hot, as TOPS and fraction of 5 POPS;
          the same shape in Q8_0, Q6_K and Q4_0 on their MFMA GEMMs, and the FFN down projection
          of the same tokens (14336 -> 4096, where the GEMMs split K) in Q4_K, Q6_K and Q8_0,
          against their HBM floors.
 cpu_baseline: the reference's own CPU kernels (oracle/_ref, compiled from fastgguf.c) on the same
-         layer with its default repacked Q4_K path, on this host's physical cores, over weight
-         copies beyond the host's L3, for a bounded sample.
+         layer's five matvecs with its default repacked Q4_K path (its silu loop, 14336 expf, is
+         not in the sample), on this host's physical cores, over weight copies beyond the host's
+         L3, for a bounded sample.
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -56,6 +61,8 @@ def algo_bytes(rows: int, cols: int) -> int:
 
 # the gate and up projections in one launch: both matrices, x read once, both outputs
 GATE_UP_BYTES = 2 * algo_bytes(14336, 4096) - 4 * 4096
+# the same paired into one launch that writes h = silu(g) * u: one output instead of two
+GATE_UP_SILU_BYTES = GATE_UP_BYTES - 4 * 14336
 
 
 ROT_BYTES = 512e6  # a per-kernel timing rotates over at least this many bytes of weights
@@ -426,6 +433,7 @@ def main() -> int:
     for k, v in xs.items():
         be.h2d(xd[k], v)
     yd = {n: be.dev_alloc(4 * r) for n, r, c in LAYER}
+    yd["h"] = be.dev_alloc(4 * 14336)
 
     if args.profile_kernels:
         gu_bytes = GATE_UP_BYTES
@@ -437,6 +445,9 @@ def main() -> int:
         for i in range(20):
             t = tensors[i % args.copies]
             be.matvec_multi_dev([t["gate"], t["up"]], xd["x2"], [yd["gate"], yd["up"]])
+        for i in range(20):
+            t = tensors[i % args.copies]
+            be.matvec_gate_up_silu_dev(t["gate"], t["up"], xd["x2"], yd["h"])
         for i in range(20):
             be.d2d(dst, src, cbytes)
         for i in range(20):
@@ -450,10 +461,9 @@ def main() -> int:
     def record_layer(t):
         be.matvec_dev(t["qkv"], xd["x"], yd["qkv"])
         be.matvec_dev(t["o"], xd["a"], yd["o"])
-        be.matvec_multi_dev([t["gate"], t["up"]], xd["x2"], [yd["gate"], yd["up"]])  # forward 4870-4872
-        be.matvec_dev(t["down"], xd["h"], yd["down"])
+        be.ffn_dev(t["gate"], t["up"], t["down"], xd["x2"], yd["h"], yd["down"])  # forward 4870-4877
 
-    # a step is one decode layer (5 matvecs in 4 launches, each quantizing its input on the
+    # a step is one decode layer (5 matvecs and the silu loop in 4 launches, each quantizing its input on the
     # device); GRAPH_LAYERS consecutive layers (cycling the weight copies) form one HIP graph, as a
     # whole decode step of the model is one graph; K steps replay K / L graphs plus one graph of
     # the remaining K % L layers, so exactly K layers are timed
@@ -518,17 +528,20 @@ def main() -> int:
         "down": (lambda i: be.matvec_dev(rot["down"][i % len(rot["down"])], xd["h"], yd["down"]),
                  algo_bytes(4096, 14336)),
         # gate and up paired in one launch that writes h = silu(g) * u (the loop between the FFN's
-        # matvecs), for callers that chain the layer on the device; not part of the layer above,
-        # which runs the reference's launches
+        # matvecs): the layer's FFN launch and its dominant kernel
         "gate+up+silu": (lambda i: be.matvec_gate_up_silu_dev(rot["gate"][i % ngu], rot["up"][i % ngu], xd["x2"],
-                                                             yd["gate"]), GATE_UP_BYTES),
+                                                             yd["gate"]), GATE_UP_SILU_BYTES),
+        "ffn": (lambda i: be.ffn_dev(rot["gate"][i % ngu], rot["up"][i % ngu], rot["down"][i % len(rot["down"])],
+                                     xd["x2"], yd["h"], yd["down"]),
+                GATE_UP_SILU_BYTES + algo_bytes(4096, 14336)),
     }
     kernels = {}
     for n, (fn, nbytes) in launches.items():
         us = kernel_time(fn, args.kernel_reps)
         gbs = nbytes / (us * 1e-6) / 1e9
         kernels[n] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                      "rotation_MB": round(nbytes * (ngu if n.startswith("gate+up") else len(rot[n])) / 1e6)}
+                      "rotation_MB": round(nbytes * (ngu if n.startswith("gate+up") else
+                                                     min(ngu, len(rot["down"])) if n == "ffn" else len(rot[n])) / 1e6)}
     # the HBM rate this box delivers to a plain stream (fgh_checksum_dev: each workgroup reads one
     # contiguous share with nontemporal 16-byte loads, a sum and nothing else, the fastest read of a
     # sweep of shapes), at the gate+up byte count and at 1 GB, each rotating over at least 2 GB of
@@ -571,12 +584,12 @@ def main() -> int:
                       "ops": mops, "us": round(mus, 3), "TOPS": round(mtops, 1),
                       "frac": round(mtops / INT8_PEAK_TOPS, 4)}
 
-    g = kernels["gate+up"]
+    g = kernels["gate+up+silu"]
     roofline = {"bound": "hbm", "achieved": g["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g["frac"],
-                "traffic": counted_traffic("gate_up"),
-                "kernel": "q4k_mv_kernel<repacked, 1 wavefront per 16-row tile> (Q4_K decode matvec, FFN gate + up "
-                          "4096->2x14336 in one launch)",
-                "bytes_per_launch": GATE_UP_BYTES, "us_per_launch": g["us"],
+                "traffic": counted_traffic("gate_up_silu"),
+                "kernel": "q4k_mv_kernel<repacked, 1 wavefront per 16-row tile, gate/up paired> (Q4_K decode matvec, "
+                          "FFN gate + up 4096->2x14336 in one launch writing h = silu(g) * u)",
+                "bytes_per_launch": GATE_UP_SILU_BYTES, "us_per_launch": g["us"],
                 "frac_of_read_reference": round(g["GB/s"] / rgbs, 4),
                 "frac_of_read_reference_1GB": round(g["GB/s"] / ggbs, 4)}
 

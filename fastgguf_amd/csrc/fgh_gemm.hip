@@ -136,9 +136,9 @@ struct GW {
 };
 __device__ __forceinline__ void gw_load(const uint8_t *blk, int L, int n, GW &w) {
     const BufRes r = buf_res(blk, 2304);
-    w.p0 = bld16<WNT>(r, 256 + 16 * L);
-    w.p1 = bld16<WNT>(r, 1280 + 16 * L);
-    w.m = bld16<WNT>(r, 16 * n);
+    w.p0 = bld16(r, 256 + 16 * L);
+    w.p1 = bld16(r, 1280 + 16 * L);
+    w.m = bld16(r, 16 * n);
 }
 
 // one step's activation records held by a thread between their load and their LDS write (named

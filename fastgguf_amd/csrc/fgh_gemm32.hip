@@ -104,10 +104,10 @@ struct GW32 {
     v2i d;
 };
 __device__ __forceinline__ v4i bld16v(BufRes r, uint32_t off) {
-    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, WNT));  // weights
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));  // weights
 }
 __device__ __forceinline__ v2i bld8v(BufRes r, uint32_t off) {
-    return __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, WNT));  // weights
+    return __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));  // weights
 }
 
 // one step's activation records held by a thread between their load and their LDS write

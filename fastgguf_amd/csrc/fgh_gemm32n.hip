@@ -181,15 +181,15 @@ __global__ __launch_bounds__(256) void q32n_gemm_kernel(GemmNArgs a) {
     // step s < ns (the callers clamp where a step could pass the end)
     auto load = [&](int s, WStepN &w, AStepN (&x)[NT]) __attribute__((always_inline)) {
         const BufRes rw = buf_res(wbase + (size_t)s * wstride, wbytes);
-        w.n = bld16<WNT>(rw, noff);
+        w.n = bld16(rw, noff);
         if (MIN) {  // the row's d and m in one record
-            const uint4 dm = bld16<WNT>(rw, doff);
+            const uint4 dm = bld16(rw, doff);
             w.d = make_uint2(dm.x, dm.y);
             w.m = make_uint2(dm.z, dm.w);
         } else {
-            w.d = bld8<WNT>(rw, doff);
+            w.d = bld8(rw, doff);
         }
-        if (Q5) w.h = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)hoff, 0, WNT);
+        if (Q5) w.h = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)hoff, 0, 0);
         const int so = s * GEMMN_REC;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {

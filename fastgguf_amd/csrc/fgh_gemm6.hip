@@ -118,7 +118,7 @@ struct GW6 {
     uint32_t d;
 };
 __device__ __forceinline__ v4i bld16v(BufRes r, uint32_t off) {
-    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, WNT));  // weights
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));  // weights
 }
 
 // one step's activation records held by a thread between their load and their LDS write

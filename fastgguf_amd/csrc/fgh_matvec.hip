@@ -179,16 +179,18 @@ struct StepW<T_Q6_K> {
     uint2 h;
     uint32_t d;
 };
-// T: the tile (wavefront-uniform)
-__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q8_0> &w) {
-    const BufRes r = buf_res(T, Q80_TILE);
+// T: the tile (wavefront-uniform); live = false: zeros without a memory access (a refill past the
+// wavefront's last step: re-reading the last step's bytes missed the caches under nontemporal
+// loads, 2 % more HBM traffic)
+__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q8_0> &w, bool live = true) {
+    const BufRes r = buf_res(T, live ? Q80_TILE : 0);
     w.q = bld16<WNT>(r, 64 + 16 * lane);
     w.d = bld8<WNT>(r, 8 * (lane >> 3));
 }
 template <int TYPE>
-__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<TYPE> &w) {
+__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<TYPE> &w, bool live = true) {
     constexpr Q32Layout L = q32_layout(TYPE);
-    const BufRes r = buf_res(T, L.tile);
+    const BufRes r = buf_res(T, live ? L.tile : 0);
     w.n = bld8<WNT>(r, L.n + 8 * lane);
     if (L.m >= 0) {  // the row's d and m in one record
         const uint4 dm = bld16<WNT>(r, L.ds * (lane >> 3));
@@ -199,8 +201,8 @@ __device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW
     }
     if (L.h >= 0) w.h = bld2<WNT>(r, L.h + 2 * lane);
 }
-__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q6_K> &w) {
-    const BufRes r = buf_res(T, Q6K_TILE);
+__device__ __forceinline__ void step_load(const uint8_t *T, uint32_t lane, StepW<T_Q6_K> &w, bool live = true) {
+    const BufRes r = buf_res(T, live ? Q6K_TILE : 0);
     w.q = bld16<WNT>(r, 144 + 16 * lane);
     w.h = bld8<WNT>(r, 1168 + 8 * lane);
     w.sc = bld16<WNT>(r, 16 * (lane >> 3));
@@ -433,7 +435,7 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             step(ring[k], s0 + b0 + k, Check());
-            step_load(T0 + (size_t)min(b0 + k + R, sl) * sstride, (uint32_t)lane, ring[k]);
+            step_load(T0 + (size_t)min(b0 + k + R, sl) * sstride, (uint32_t)lane, ring[k], b0 + k + R <= sl);
         }
         b0 += R;
     }

@@ -75,15 +75,17 @@ __device__ __forceinline__ uint32_t bmul(uint32_t q, uint32_t f2) {
 }
 __device__ __forceinline__ v4i u4v(uint4 u) { return v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w}; }
 
-// one lane's weights of one block: the two 16-byte slots of its chunk and its row's meta;
-// live = false: zeros without a memory access (a ring slot past the wavefront's last step)
+// one lane's weights of one block: pieces 0 and 1 of its chunk and its row's meta; live = false:
+// zeros without a memory access (a ring slot past the wavefront's last step). The decode layout
+// keeps piece h of chunk kg in slot h ^ (kg >> 1) (1024-byte halves from byte 256): o0 / o1, the
+// lane's byte offsets of pieces 0 / 1, undo that swap in the addresses, not in registers.
 struct MmW {
     uint4 p0, p1, m;
 };
-__device__ __forceinline__ void mm_wload(const uint8_t *blk, uint32_t L, uint32_t n, bool live, MmW &w) {
+__device__ __forceinline__ void mm_wload(const uint8_t *blk, uint32_t o0, uint32_t o1, uint32_t n, bool live, MmW &w) {
     const BufRes r = buf_res(blk, live ? Q4K_TILE : 0);
-    w.p0 = bld16<WNT>(r, 256 + 16 * L);
-    w.p1 = bld16<WNT>(r, 1280 + 16 * L);
+    w.p0 = bld16<WNT>(r, o0);
+    w.p1 = bld16<WNT>(r, o1);
     w.m = bld16<WNT>(r, 16 * n);
 }
 
@@ -121,6 +123,7 @@ __global__ __launch_bounds__(64 * MM_TPW) void q4k_moe_mfma_kernel(MmArgs a) {
     const int ntl = (int)max((int64_t)0, min((int64_t)a.tt, ntile - t0));
     const int kg = l >> 4, n = l & 15;  // B operand: chunk kg of row n (decode lane 4 n + kg)
     const uint32_t L = 4 * n + kg;
+    const uint32_t o0 = (kg >= 2 ? 1280u : 256u) + 16 * L, o1 = (kg >= 2 ? 256u : 1280u) + 16 * L;
     const int s = l >> 4;               // output: slot s of a group, row n
     const size_t actb = q4_act_bytes(nb);
     uint8_t *frag = smem;
@@ -140,7 +143,7 @@ __global__ __launch_bounds__(64 * MM_TPW) void q4k_moe_mfma_kernel(MmArgs a) {
         int rj = 0, rb = 0;  // the next step to load: tile t0 + rj, block rb
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            mm_wload(step_ptr(t0 + min(rj, max(ntl - 1, 0)), rb), L, n, rj < ntl, ring[r]);
+            mm_wload(step_ptr(t0 + min(rj, max(ntl - 1, 0)), rb), o0, o1, n, rj < ntl, ring[r]);
             if (++rb == nb) { rb = 0; ++rj; }
         }
         // (2) the chunk's slots, then its fragments, yd and sums
@@ -206,15 +209,9 @@ __global__ __launch_bounds__(64 * MM_TPW) void q4k_moe_mfma_kernel(MmArgs a) {
         for (int e = 0; e < 4; ++e) aoff[e] = (e == aq ? 0u : 256u) + 4u * (uint32_t)l;
         // one block b of launch tile t from ring slot w
         auto blk = [&](const MmW &w, int b, int64_t t) {
-            // piece h of the chunk sits in slot h ^ (kg >> 1) of the decode layout
+            // pieces 0 and 1 of the chunk (the loads undid the layout's swap)
             const bool sw = kg >= 2;
-            const uint32_t P0[4] = {w.p0.x, w.p0.y, w.p0.z, w.p0.w}, P1[4] = {w.p1.x, w.p1.y, w.p1.z, w.p1.w};
-            uint32_t X[2][4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                X[0][e] = sw ? P1[e] : P0[e];
-                X[1][e] = sw ? P0[e] : P1[e];
-            }
+            const uint32_t X[2][4] = {{w.p0.x, w.p0.y, w.p0.z, w.p0.w}, {w.p1.x, w.p1.y, w.p1.z, w.p1.w}};
             // sub-block scales 2 kg and 2 kg + 1 as bytes 0 and 1 of scp (scale_min_k4, fastgguf.c:466-472)
             const int shs = 16 * (kg & 1);
             const uint32_t A = w.m.y >> shs, C = w.m.w >> shs;
@@ -309,7 +306,7 @@ __global__ __launch_bounds__(64 * MM_TPW) void q4k_moe_mfma_kernel(MmArgs a) {
         const int total = ntl * nb;
         auto step = [&](int r) {
             blk(ring[r], b, t0 + j);
-            mm_wload(step_ptr(t0 + min(rj, ntl - 1), rb), L, n, rj < ntl, ring[r]);
+            mm_wload(step_ptr(t0 + min(rj, ntl - 1), rb), o0, o1, n, rj < ntl, ring[r]);
             if (++rb == nb) { rb = 0; ++rj; }
             if (++b == nb) {  // uniform: the tile's last block
                 finish(j);

@@ -377,14 +377,16 @@ __global__ __launch_bounds__(64 * TPW * S) void q4k_mv_kernel(MvArgs a) {
             a.dump_m[di] = msum;
         }
     };
-    // whole rounds of R blocks as straight-line code (the steps interleave), refilling the ring;
-    // then the last nbl % R blocks already in the ring
+    // whole rounds of R blocks as straight-line code (the steps interleave), refilling the ring
+    // (a refill past the wavefront's last block loads nothing: re-reading the last block missed
+    // the caches under nontemporal loads, 2 % more HBM traffic and 1.5-2 % longer launches); then
+    // the last nbl % R blocks already in the ring
     int b0 = 0;
     for (; b0 + R <= nbl; b0 += R) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             step(ring[r], bb0 + b0 + r);
-            rb_load<TYPE>(T0 + (size_t)min(b0 + r + R, bl) * bstride, lane, ring[r]);
+            rb_load<TYPE>(T0 + (size_t)min(b0 + r + R, bl) * bstride, lane, ring[r], b0 + r + R <= bl);
         }
     }
 #pragma unroll
@@ -688,33 +690,50 @@ hipError_t launch_q4_image(const float *x, const float *u, int64_t ldx, int nb, 
 }
 size_t q4_image_bytes(int nb) { return q4_act_bytes(nb); }
 
-// The grouped MoE path's first launch, one wavefront per token t: the Q8_K image of x row t
-// (q4_image_kernel's blocks, 4 at a time), the token's routing (moe_route_wave: sel, w), and each
-// selected slot t k + j filed in its expert's bucket: bucket[e * cap + position], cnt[e] counting.
-// cap = tokens * k: a token whose probabilities are not all finite (NaN or infinite logits) can
-// select one expert several times, as the reference's repeated argmax does, so a bucket holds up
-// to every slot of the call. The order inside a bucket is whatever the atomics give; no result
-// depends on it. cnt starts at zero and moe_combine_kernel, the path's last launch, clears it.
-__global__ __launch_bounds__(64) void moe_prep_kernel(const float *__restrict__ x, int64_t ldx, int nb,
-                                                      uint8_t *__restrict__ img, const float *__restrict__ logits,
-                                                      int n_expert, int k, int32_t *__restrict__ sel,
-                                                      float *__restrict__ w, int32_t *__restrict__ cnt,
-                                                      int32_t *__restrict__ bucket, int cap) {
+// The grouped MoE path's first launch, one workgroup of two wavefronts per token t: wavefront 1
+// forms the Q8_K image of x row t (q4_image_kernel's blocks, 8 at a time: the loads of two rounds
+// in flight before the barrier, so they overlap the routing), wavefront 0 routes the token
+// (moe_route_wave: sel, w) and, after the barrier (which also makes its sel stores visible to its
+// own lanes), files each selected slot t k + j in its expert's bucket: bucket[e * cap + position],
+// cnt[e] counting. cap = tokens * k: a token whose probabilities are not all finite (NaN or
+// infinite logits) can select one expert several times, as the reference's repeated argmax does,
+// so a bucket holds up to every slot of the call. The order inside a bucket is whatever the
+// atomics give; no result depends on it. cnt starts at zero and moe_combine_kernel, the path's
+// last launch, clears it. (One wavefront doing both, its quantization rounds one after another:
+// 7.4 us at config 5.)
+__global__ __launch_bounds__(128) void moe_prep_kernel(const float *__restrict__ x, int64_t ldx, int nb,
+                                                       uint8_t *__restrict__ img, const float *__restrict__ logits,
+                                                       int n_expert, int k, int32_t *__restrict__ sel,
+                                                       float *__restrict__ w, int32_t *__restrict__ cnt,
+                                                       int32_t *__restrict__ bucket, int cap) {
     __shared__ __align__(16) float ps[64 * MOE_EPL];
     const int t = blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = (int)threadIdx.x & 63;
     const float *xr = x + (size_t)t * ldx;
     uint8_t *ir = img + (size_t)t * q4_act_bytes(nb);
-    for (int b0 = 0; b0 < nb; b0 += 4) {
-        const int b = b0 + (int)(threadIdx.x >> 4);
-        XRound xv;
-        q8k_load_b(xr, b, b < nb, xv);
-        q8k_store_b(nb, b, b < nb, xv, ir);
+    const int bl = lane >> 4;  // this lane's block of a round of 4
+    XRound xa, xb;
+    if (wave == 1) {
+        q8k_load_b(xr, bl, bl < nb, xa);
+        q8k_load_b(xr, 4 + bl, 4 + bl < nb, xb);
+    } else {
+        moe_route_wave(logits + (size_t)t * n_expert, n_expert, k, ps, sel + (size_t)t * k, w + (size_t)t * k, 0);
     }
-    moe_route_wave(logits + (size_t)t * n_expert, n_expert, k, ps, sel + (size_t)t * k, w + (size_t)t * k, 0);
-    __syncthreads();  // the wavefront's own sel stores, read back
-    if ((int)threadIdx.x < k) {
-        const int slot = t * k + (int)threadIdx.x, e = sel[slot];
-        bucket[(size_t)e * cap + atomicAdd(&cnt[e], 1)] = slot;
+    __syncthreads();
+    if (wave == 0) {
+        if (lane < k) {
+            const int slot = t * k + lane, e = sel[slot];
+            bucket[(size_t)e * cap + atomicAdd(&cnt[e], 1)] = slot;
+        }
+        return;
+    }
+    q8k_store_b(nb, bl, bl < nb, xa, ir);
+    q8k_store_b(nb, 4 + bl, 4 + bl < nb, xb, ir);
+    for (int b0 = 8; b0 < nb; b0 += 8) {  // rows of more than 8 blocks
+        q8k_load_b(xr, b0 + bl, b0 + bl < nb, xa);
+        q8k_load_b(xr, b0 + 4 + bl, b0 + 4 + bl < nb, xb);
+        q8k_store_b(nb, b0 + bl, b0 + bl < nb, xa, ir);
+        q8k_store_b(nb, b0 + 4 + bl, b0 + 4 + bl < nb, xb, ir);
     }
 }
 
@@ -722,7 +741,7 @@ hipError_t launch_moe_prep(const float *x, int64_t ldx, int nb, uint8_t *img, co
                            int k, int n_tok, int32_t *sel, float *w, int32_t *cnt, int32_t *bucket, hipStream_t s) {
     if (n_expert < 1 || n_expert > 64 * MOE_EPL || k < 1 || k > n_expert || k > 64 || nb < 1 || n_tok < 1)
         return hipErrorInvalidValue;
-    moe_prep_kernel<<<n_tok, 64, 0, s>>>(x, ldx, nb, img, logits, n_expert, k, sel, w, cnt, bucket, n_tok * k);
+    moe_prep_kernel<<<n_tok, 128, 0, s>>>(x, ldx, nb, img, logits, n_expert, k, sel, w, cnt, bucket, n_tok * k);
     return hipGetLastError();
 }
 
