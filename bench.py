@@ -673,8 +673,8 @@ def main() -> int:
         "ms_per_step_one_layer_graphs": round(ms_step_1, 5), "graph_layers": L, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "cfg2: Llama-3-8B decode layer as Q4_K matvecs at batch 1 (QKV 4096->6144, "
-                               "O 4096->4096, gate/up 4096->14336, down 14336->4096), device Q8_K quantization "
-                               "of each input included",
+                               "O 4096->4096, gate/up 4096->14336 in one launch writing h = silu(g) * u, down "
+                               "14336->4096 on h), device Q8_K quantization of each input included",
                    "layer_bytes": layer_bytes, "weight_copies": args.copies,
                    "weight_set_MB": round(args.copies * sum(r * (c // 256) * 144 for _, r, c in LAYER) / 1e6, 1),
                    "device": info["name"], "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
