@@ -32,23 +32,30 @@ T_Q4_1 = 3
 T_Q5_0 = 6
 T_Q5_1 = 7
 T_Q8_0 = 8
+T_Q2_K = 10
+T_Q3_K = 11
 T_Q4_K = 12
 T_Q5_K = 13
 T_Q6_K = 14
 T_IQ4_NL = 20
+T_IQ4_XS = 23
 
 #: (elements per block, bytes per block), block_size_of (fastgguf.c:235-253)
 BLOCK = {T_Q8_0: (32, 34), T_Q4_K: (256, 144), T_Q6_K: (256, 210), T_Q5_0: (32, 22), T_Q5_K: (256, 176),
-         T_Q4_0: (32, 18), T_Q4_1: (32, 20), T_Q5_1: (32, 24), T_IQ4_NL: (32, 18)}
+         T_Q4_0: (32, 18), T_Q4_1: (32, 20), T_Q5_1: (32, 24), T_IQ4_NL: (32, 18),
+         T_Q2_K: (256, 84), T_Q3_K: (256, 110), T_IQ4_XS: (256, 136)}
 TYPE_NAME = {T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q6_K: "Q6_K", T_Q5_0: "Q5_0", T_Q5_K: "Q5_K", T_Q4_0: "Q4_0",
-             T_Q4_1: "Q4_1", T_Q5_1: "Q5_1", T_IQ4_NL: "IQ4_NL"}
+             T_Q4_1: "Q4_1", T_Q5_1: "Q5_1", T_IQ4_NL: "IQ4_NL", T_Q2_K: "Q2_K", T_Q3_K: "Q3_K",
+             T_IQ4_XS: "IQ4_XS"}
 Q32_TYPES = (T_Q8_0, T_Q5_0, T_Q4_0, T_Q4_1, T_Q5_1, T_IQ4_NL)
+#: 256-value blocks whose row kernels take Q8 (32-value) activations
+K256Q8_TYPES = (T_Q2_K, T_Q3_K, T_IQ4_XS)
 
 
 def uses_q8(type_: int) -> bool:
     """Activation kind (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for the 32-value
-    types, Q8_K blocks of 256 for the K-quants."""
-    return type_ in Q32_TYPES
+    types and for Q2_K / Q3_K / IQ4_XS, Q8_K blocks of 256 for the other K-quants."""
+    return type_ in Q32_TYPES or type_ in K256Q8_TYPES
 
 #: activation blocks, the reference's structs q8_blk_t (743) and q8k_blk_t (771)
 Q8_BLK = np.dtype([("d", "<f4"), ("qs", "i1", 32), ("s16", "<i2", 2)])
@@ -162,7 +169,27 @@ def q32_weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
     return blk.reshape(rows, -1)
 
 
+#: byte offsets of the fp16 scales in a 256-value block of the low-bit types: d (and dmin)
+_K256Q8_D = {T_Q2_K: (80, 82), T_Q3_K: (108,), T_IQ4_XS: (0,)}
+
+
+def k256q8_weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """rows x cols of Q2_K / Q3_K / IQ4_XS: uniform quant and scale bytes, fp16 d (Q2_K: and
+    dmin) of the magnitudes the other generators use."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    if cols % 256:
+        raise ValueError(f"{TYPE_NAME[type_]} needs cols % 256 == 0")
+    nb = rows * (cols // 256)
+    bb = BLOCK[type_][1]
+    blk = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    for o, scale in zip(_K256Q8_D[type_], (0.004, 0.002)):
+        blk[:, o:o + 2] = _fp16_abs_normal(rng, nb, scale).view(np.uint8).reshape(nb, 2)
+    return blk.reshape(rows, -1)
+
+
 def weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    if type_ in K256Q8_TYPES:
+        return k256q8_weights(type_, rows, cols, seed)
     if type_ in (T_Q4_0, T_Q4_1, T_Q5_1, T_IQ4_NL):
         return q32_weights(type_, rows, cols, seed)
     if type_ == T_Q5_0:
@@ -189,6 +216,12 @@ def random_bytes_weights(type_: int, rows: int, cols: int, seed: int) -> np.ndar
     dm = (0x2400 + rng.integers(0, 0x400, size=nb)).astype(np.uint16)
     if type_ == T_Q6_K:
         blk[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    elif type_ in K256Q8_TYPES:   # the reference selftest's Q2_K / Q3_K / IQ4_XS rows (5612-5676)
+        o = _K256Q8_D[type_]
+        blk[:, o[0]:o[0] + 2] = d.view(np.uint8).reshape(nb, 2)
+        if len(o) > 1:
+            blk[:, o[1]:o[1] + 2] = (0x2800 + rng.integers(0, 0x400, size=nb)).astype(np.uint16).view(
+                np.uint8).reshape(nb, 2)
     else:
         blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         if type_ in (T_Q4_K, T_Q5_K, T_Q4_1, T_Q5_1):

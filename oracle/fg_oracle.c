@@ -50,10 +50,14 @@ static inline uint32_t rd32(const uint8_t *p) { uint32_t v; memcpy(&v, p, 4); re
 
 /* the activation kind of a weight type (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for
  * Q8_0 / Q5_0, Q8_K blocks of 256 for the K-quants */
+/* the 256-value types whose row kernels take Q8 (32-value) activations: Q2_K, Q3_K, IQ4_XS
+ * (type_uses_q8, 2171) */
+static inline int k256q8(uint32_t type) { return type == FGO_T_Q2_K || type == FGO_T_Q3_K || type == FGO_T_IQ4_XS; }
 static inline int uses_q8(uint32_t type) {
     return type == FGO_T_Q8_0 || type == FGO_T_Q5_0 || type == FGO_T_Q4_0 || type == FGO_T_Q4_1 ||
-           type == FGO_T_Q5_1 || type == FGO_T_IQ4_NL;
+           type == FGO_T_Q5_1 || type == FGO_T_IQ4_NL || k256q8(type);
 }
+static inline int k256q8_bytes(uint32_t type) { return type == FGO_T_Q2_K ? 84 : type == FGO_T_Q3_K ? 110 : 136; }
 /* the 32-value block types with a min term (d * q + m): Q4_1 / Q5_1 */
 static inline int has_min32(uint32_t type) { return type == FGO_T_Q4_1 || type == FGO_T_Q5_1; }
 
@@ -274,6 +278,95 @@ float fgo_dot_q32(uint32_t type, const uint8_t *row, const fgo_q8_blk *xq, int n
  * per block the whole-block integer isum = sum (nib - 8) y (computed as sum nib y - 8 (s16_0 +
  * s16_1), the same integer); acc = fma(FP16(d) * yd, isum, acc); out = acc. The repack
  * (repack_q40_group 2390-2398) moves bytes only. */
+/* ---- the 256-value types on Q8 activations: dot_q2_K_q8 (fastgguf.c:1426-1479), dot_q3_K_q8
+ * (1481-1545), dot_iq4_xs_q8 (1580-1614). One fp32 chain per row over its 32-blocks in order
+ * (block b, then 32-block c = 0..7 of it, c = 4 half + j for the K-quants):
+ *   Q2_K: S = sum_l ((qs[32 half + l] >> 2 j) & 3) * sc(l) * x_l with sc(l) the low nibble of
+ *         scales[8 half + 2 j + (l >= 16)], M = m_0 s16_0 + m_1 s16_1 (the high nibbles);
+ *         sum = fma(xd, fma(d, S, -(dmin * M)), sum)
+ *   Q3_K: qu = lo | 4 hbit (hmask bit 4 half + j of byte l), sc' = 6-bit scale - 32, S = sum
+ *         qu * sc'(l) * x_l, off = 4 (sc'_0 s16_0 + sc'_1 s16_1); sum = fma(d * xd, (float)(S - off), sum)
+ *   IQ4_XS: si = sum kvalues[nib] * x over the 32-block; sum = fma(d * (ls - 32) * xd, (float)si, sum)
+ * These are the contractions gcc makes of the reference's expressions (`sum += xk->d * (d * S -
+ * dmin * M)` and its like); they were fixed against the compiled reference, which every other
+ * form tried disagrees with on a third or more of random rows. The integers are the AVX2 kernels'
+ * (maddubs / madd sums), exact. */
+static void q3k_scales(const uint8_t *p, int8_t *scs) {
+    uint32_t a0 = rd32(p + 96), a1 = rd32(p + 100), tmp = rd32(p + 104), aux[4];
+    aux[0] = (a0 & 0x0f0f0f0fu) | (((tmp >> 0) & 0x03030303u) << 4);
+    aux[1] = (a1 & 0x0f0f0f0fu) | (((tmp >> 2) & 0x03030303u) << 4);
+    aux[2] = ((a0 >> 4) & 0x0f0f0f0fu) | (((tmp >> 4) & 0x03030303u) << 4);
+    aux[3] = ((a1 >> 4) & 0x0f0f0f0fu) | (((tmp >> 6) & 0x03030303u) << 4);
+    memcpy(scs, aux, 16);
+}
+static inline int q2k_q(const uint8_t *p, int c, int l) { return (p[16 + 32 * (c >> 2) + l] >> (2 * (c & 3))) & 3; }
+static inline int q3k_q(const uint8_t *p, int c, int l) {
+#if FGO_MUTATE == 16 /* the hmask bit of the other half */
+    return ((p[32 + 32 * (c >> 2) + l] >> (2 * (c & 3))) & 3) | ((p[l] >> (c ^ 4)) & 1) * 4;
+#else
+    return ((p[32 + 32 * (c >> 2) + l] >> (2 * (c & 3))) & 3) | ((p[l] >> c) & 1) * 4;
+#endif
+}
+static const int8_t IQ4NL_XS[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+static inline int iq4xs_ls(const uint8_t *p, int c) {
+#if FGO_MUTATE == 17 /* the high scale bits of scales_h at bit c instead of 2c */
+    return ((p[4 + c / 2] >> (4 * (c % 2))) & 0xF) | (((rd16(p + 2) >> c) & 3) << 4);
+#else
+    return ((p[4 + c / 2] >> (4 * (c % 2))) & 0xF) | (((rd16(p + 2) >> (2 * c)) & 3) << 4);
+#endif
+}
+static inline int iq4xs_q(const uint8_t *p, int c, int l) {
+    const uint8_t q = p[8 + 16 * c + (l & 15)];
+    return IQ4NL_XS[l < 16 ? (q & 0xF) : (q >> 4)];
+}
+/* the integers of 32-block c of a block: S (the scaled sum; IQ4_XS: si) and the type's second
+ * integer (Q2_K: M; Q3_K: sc'_0 s16_0 + sc'_1 s16_1; IQ4_XS: 0) */
+static void k256q8_ints(uint32_t type, const uint8_t *p, int c, const fgo_q8_blk *xb, int *S, int *M) {
+    int s = 0, m = 0;
+    if (type == FGO_T_Q2_K) {
+        const int a = p[2 * c], b = p[2 * c + 1];
+        for (int l = 0; l < 32; l++) s += q2k_q(p, c, l) * ((l < 16 ? a : b) & 0xF) * xb->qs[l];
+        m = (a >> 4) * xb->s16[0] + (b >> 4) * xb->s16[1];
+    } else if (type == FGO_T_Q3_K) {
+        int8_t scs[16];
+        q3k_scales(p, scs);
+        const int a = scs[2 * c] - 32, b = scs[2 * c + 1] - 32;
+        for (int l = 0; l < 32; l++) s += q3k_q(p, c, l) * (l < 16 ? a : b) * xb->qs[l];
+        m = a * xb->s16[0] + b * xb->s16[1];
+    } else {
+        for (int l = 0; l < 32; l++) s += iq4xs_q(p, c, l) * xb->qs[l];
+    }
+    *S = s;
+    *M = m;
+}
+float fgo_dot_k256q8(uint32_t type, const uint8_t *row, const fgo_q8_blk *xq, int nb256) {
+    const int bb = k256q8_bytes(type);
+    float sum = 0.0f;
+    for (int b = 0; b < nb256; b++) {
+        const uint8_t *p = row + (size_t)b * bb;
+        for (int c = 0; c < 8; c++) {
+            const fgo_q8_blk *xb = xq + 8 * b + c;
+            int S, M;
+            k256q8_ints(type, p, c, xb, &S, &M);
+            if (type == FGO_T_Q2_K) {
+                const float d = fgo_fp16(rd16(p + 80)), dmin = fgo_fp16(rd16(p + 82));
+#if FGO_MUTATE == 15 /* the reference's expression without gcc's contractions */
+                sum += xb->d * (d * (float)S - dmin * (float)M);
+#else
+                sum = fmaf(xb->d, fmaf(d, (float)S, -(dmin * (float)M)), sum);
+#endif
+            } else if (type == FGO_T_Q3_K) {
+                const float d = fgo_fp16(rd16(p + 108));
+                sum = fmaf(d * xb->d, (float)(S - 4 * M), sum);
+            } else {
+                const float d = fgo_fp16(rd16(p));
+                sum = fmaf(d * (float)(iq4xs_ls(p, c) - 32) * xb->d, (float)S, sum);
+            }
+        }
+    }
+    return sum;
+}
+
 float fgo_dot_q4_0_rp(const uint8_t *row, const fgo_q8_blk *xq, int nb) {
     float acc = 0.0f;
     for (int b = 0; b < nb; b++) {
@@ -463,6 +556,9 @@ void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
             }
             sumi[b] = s;
             msum[b] = m;
+        } else if (k256q8(type)) { /* b counts 32-blocks here */
+            const uint8_t *p = row + (size_t)(b / 8) * k256q8_bytes(type);
+            k256q8_ints(type, p, b % 8, (const fgo_q8_blk *)act + b, &sumi[b], &msum[b]);
         } else if (uses_q8(type) && type != FGO_T_Q8_0) {
             const uint8_t *p = row + (size_t)b * bytes32(type);
             const fgo_q8_blk *xb = (const fgo_q8_blk *)act + b;
@@ -483,6 +579,29 @@ void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
 
 /* ---- dequantize_row (fastgguf.c:518-532, 552-562, 622-667, 669-693) ---- */
 int fgo_dequantize_row(uint32_t type, const uint8_t *raw, float *out, int n) {
+    if (k256q8(type)) { /* dequantize_row 563-586 (Q2_K), 587-620 (Q3_K), 709-727 (IQ4_XS) */
+        const int bb = k256q8_bytes(type);
+        for (int b = 0; b < n / 256; b++) {
+            const uint8_t *p = raw + (size_t)b * bb;
+            for (int c = 0; c < 8; c++)
+                for (int l = 0; l < 32; l++) {
+                    float v;
+                    if (type == FGO_T_Q2_K) {
+                        const int s = p[2 * c + (l >= 16)];
+                        v = fgo_fp16(rd16(p + 80)) * (float)(s & 0xF) * (float)q2k_q(p, c, l) -
+                            fgo_fp16(rd16(p + 82)) * (float)(s >> 4);
+                    } else if (type == FGO_T_Q3_K) {
+                        int8_t scs[16];
+                        q3k_scales(p, scs);
+                        v = fgo_fp16(rd16(p + 108)) * (float)(scs[2 * c + (l >= 16)] - 32) * (float)(q3k_q(p, c, l) - 4);
+                    } else {
+                        v = fgo_fp16(rd16(p)) * (float)(iq4xs_ls(p, c) - 32) * (float)iq4xs_q(p, c, l);
+                    }
+                    out[256 * b + 32 * c + l] = v;
+                }
+        }
+        return 0;
+    }
     if (uses_q8(type) && type != FGO_T_Q8_0) { /* d * value (+ m for Q4_1 / Q5_1) */
         const int bb = bytes32(type);
         for (int b = 0; b < n / 32; b++) {
@@ -550,6 +669,7 @@ int fgo_block_size(uint32_t type, int *elems, int *bytes) {
     case FGO_T_Q5_0: case FGO_T_Q4_0: case FGO_T_Q4_1: case FGO_T_Q5_1: case FGO_T_IQ4_NL:
         *elems = 32; *bytes = bytes32(type); return 0;
     case FGO_T_Q5_K: *elems = 256; *bytes = 176; return 0;
+    case FGO_T_Q2_K: case FGO_T_Q3_K: case FGO_T_IQ4_XS: *elems = 256; *bytes = k256q8_bytes(type); return 0;
     default: return -1;
     }
 }
@@ -562,11 +682,12 @@ static float dot_row3(uint32_t type, int order, const uint8_t *rb, const void *a
     if (type == FGO_T_Q6_K) return fgo_dot_q6_K(rb, (const fgo_q8k_blk *)act, cols / 256);
     if (type == FGO_T_Q5_K) return fgo_dot_q5_K(rb, (const fgo_q8k_blk *)act, cols / 256);
     if (type == FGO_T_Q4_0 && order == FGO_ORDER_REPACKED) return fgo_dot_q4_0_rp(rb, (const fgo_q8_blk *)act, cols / 32);
+    if (k256q8(type)) return fgo_dot_k256q8(type, rb, (const fgo_q8_blk *)act, cols / 256);
     return fgo_dot_q32(type, rb, (const fgo_q8_blk *)act, cols / 32);
 }
 
 static int type_ok(uint32_t type, int cols) {
-    if (type == FGO_T_Q4_K || type == FGO_T_Q5_K || type == FGO_T_Q6_K) return cols > 0 && cols % 256 == 0;
+    if (type == FGO_T_Q4_K || type == FGO_T_Q5_K || type == FGO_T_Q6_K || k256q8(type)) return cols > 0 && cols % 256 == 0;
     if (uses_q8(type)) return cols > 0 && cols % 32 == 0;
     return 0;
 }
@@ -614,7 +735,7 @@ int fgo_matvec(uint32_t type, int order, const uint8_t *w, int64_t rows, int col
  *   per 32-block g: a = fma(d*xd, ia'_g, a); a = fnmadd(m, xd*(s16_0+s16_1), a)
  *   with ia' = sum u*x over the unsigned weights the VNNI kernel multiplies: Q8_0 u = w + 128,
  *   m = 128 d; Q5_0 u = q5, m = 16 d; Q4_0 u = nib, m = 8 d; Q4_1 / Q5_1 u = nib / q5, m = -FP16(m) */
-static int has_gemm(uint32_t type) { return type != FGO_T_Q5_K && type != FGO_T_IQ4_NL; }
+static int has_gemm(uint32_t type) { return type != FGO_T_Q5_K && type != FGO_T_IQ4_NL && !k256q8(type); }
 static void gemm_row_token(uint32_t type, const uint8_t *rb, const void *act, int cols, float *out) {
     if (uses_q8(type)) {
         const fgo_q8_blk *xq = (const fgo_q8_blk *)act;
@@ -716,7 +837,8 @@ int fgo_gemm(uint32_t type, const uint8_t *w, int64_t rows, int cols, const void
 /* matmul (fastgguf.c:3004-3093) for the types here, as built for a VNNI CPU:
  *   nb == 1: matvec;  repacked (Q4_K, Q4_0) and nb < 8: per-token matvec;  nb >= 8: the prompt
  *   GEMM (gemm_kquant for Q4_K / Q6_K, gemm_q32 for Q4_0 / Q4_1 / Q5_0 / Q5_1 and, VNNI builds
- *   only, Q8_0 - GEMM_Q8_0 at 2864-2868; Q5_K and IQ4_NL have no GEMM: the row kernel per token);
+ *   only, Q8_0 - GEMM_Q8_0 at 2864-2868; Q5_K, IQ4_NL, Q2_K, Q3_K and IQ4_XS have no GEMM: the
+ *   row kernel per token);
  *   otherwise the x4 tiles, which equal the single-row kernels bit for bit (selftest 5871-5916). */
 int fgo_matmul(uint32_t type, int order, const uint8_t *w, int64_t rows, int cols,
                const float *X, int ldx, float *Y, int ldy, int nb) {

@@ -23,7 +23,8 @@ extern "C" {
 
 enum {
     FGO_T_F32 = 0, FGO_T_Q4_0 = 2, FGO_T_Q4_1 = 3, FGO_T_Q5_0 = 6, FGO_T_Q5_1 = 7, FGO_T_Q8_0 = 8,
-    FGO_T_Q4_K = 12, FGO_T_Q5_K = 13, FGO_T_Q6_K = 14, FGO_T_IQ4_NL = 20
+    FGO_T_Q2_K = 10, FGO_T_Q3_K = 11, FGO_T_Q4_K = 12, FGO_T_Q5_K = 13, FGO_T_Q6_K = 14, FGO_T_IQ4_NL = 20,
+    FGO_T_IQ4_XS = 23
 };
 
 /* fp32 evaluation order a kernel follows (which reference kernel the call restates) */
@@ -47,6 +48,8 @@ float fgo_dot_q5_0(const uint8_t *row, const fgo_q8_blk *xq, int nb);
 float fgo_dot_q5_K(const uint8_t *row, const fgo_q8k_blk *y, int nb);
 /* any 32-value type (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, IQ4_NL) in its row kernel's order */
 float fgo_dot_q32(uint32_t type, const uint8_t *row, const fgo_q8_blk *xq, int nb);
+/* the 256-value types on Q8 activations (Q2_K, Q3_K, IQ4_XS); nb256 blocks of the row */
+float fgo_dot_k256q8(uint32_t type, const uint8_t *row, const fgo_q8_blk *xq, int nb256);
 float fgo_dot_q4_0_rp(const uint8_t *row, const fgo_q8_blk *xq, int nb);
 
 /* per-block integer parts (the bit-exact targets):

@@ -15,7 +15,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
-from fastgguf_amd.synth import BLOCK, Q8_BLK, Q8K_BLK, uses_q8  # noqa: E402
+from fastgguf_amd.synth import BLOCK, K256Q8_TYPES, Q8_BLK, Q8K_BLK, uses_q8  # noqa: E402
 
 ORDER_ROW = 0
 ORDER_REPACKED = 1
@@ -52,6 +52,8 @@ class Oracle:
             getattr(L, n).restype = C.c_float
         L.fgo_dot_q32.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
         L.fgo_dot_q32.restype = C.c_float
+        L.fgo_dot_k256q8.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
+        L.fgo_dot_k256q8.restype = C.c_float
         L.fgo_block_ints.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
         L.fgo_matvec.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
         L.fgo_matmul.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_int,
@@ -103,6 +105,8 @@ class Oracle:
         nb = act.size
         if type_ == 2 and order == ORDER_REPACKED:
             return self.lib.fgo_dot_q4_0_rp(_ptr(row), _ptr(act), nb)
+        if type_ in K256Q8_TYPES:
+            return self.lib.fgo_dot_k256q8(type_, _ptr(row), _ptr(act), nb // 8)
         if uses_q8(type_):
             return self.lib.fgo_dot_q32(type_, _ptr(row), _ptr(act), nb)
         name = {12: "fgo_dot_q4_K_rp" if order == ORDER_REPACKED else "fgo_dot_q4_K",

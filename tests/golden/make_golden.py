@@ -2,7 +2,7 @@
 
 Run in a container where lawnak/FastGGUF is mounted at /root/reference:
 
-    make -C oracle ref && python tests/golden/make_golden.py
+    make -C oracle ref && python tests/golden/make_golden.py [attn | lowbit]
 
 It loads oracle/_ref/libfgref_vnni.so (fastgguf.c compiled from where it lies, AVX-512-VNNI
 build; ref_harness.c exports its static kernels) and records inputs and outputs only: weight
@@ -146,11 +146,35 @@ def kvq_cases(ref) -> dict:
     return out
 
 
+def lowbit_cases(ref) -> dict:
+    """Q2_K / Q3_K / IQ4_XS rows on Q8 activations: matvec on synthetic and selftest-style byte
+    rows (dot_q2_K_q8 1426, dot_q3_K_q8 1481, dot_iq4_xs_q8 1580 through dot_row) and matmul at
+    3, 8 and 45 tokens (no GEMM for these types: the row kernel per token, 3004-3093)."""
+    out = {}
+    for name, t in (("q2_k", S.T_Q2_K), ("q3_k", S.T_Q3_K), ("iq4_xs", S.T_IQ4_XS)):
+        for gname, gen, rows, cols in (("synth", S.weights, 24, 768), ("bytes", S.random_bytes_weights, 24, 1024)):
+            w = gen(t, rows, cols, 700 + t)
+            xv = S.activations(cols, 710 + t)
+            out[f"{name}_{gname}_w"] = w
+            out[f"{name}_{gname}_x"] = xv
+            out[f"{name}_{gname}_y"] = ref.matvec(t, w, cols, xv)
+        w = S.weights(t, 20, 512, 720 + t)
+        out[f"{name}_mm_w"] = w
+        for nb in (3, 8, 45):
+            X = S.activations(512, 730 + nb, rows=nb)
+            out[f"{name}_mm_X{nb}"] = X
+            out[f"{name}_mm_Y{nb}"] = ref.matmul(t, w, 512, X)
+    return out
+
+
 def main() -> None:
     ref = Reference("vnni")
     print("reference build:", ref.build, "threads:", ref.threads())
     if sys.argv[1:] == ["attn"]:  # only the attention vectors
         np.savez_compressed(os.path.join(HERE, "attn.npz"), **attn_cases(ref))
+        return
+    if sys.argv[1:] == ["lowbit"]:  # only the Q2_K / Q3_K / IQ4_XS vectors
+        np.savez_compressed(os.path.join(HERE, "lowbit.npz"), **lowbit_cases(ref))
         return
     out = {}
 
@@ -244,6 +268,7 @@ def main() -> None:
     # TurboQuant KV cache: the reference's rotation signs, rotations, slice records and its
     # attention step over quantized ring caches
     np.savez_compressed(os.path.join(HERE, "kvq.npz"), **kvq_cases(ref))
+    np.savez_compressed(os.path.join(HERE, "lowbit.npz"), **lowbit_cases(ref))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz") or f.endswith(".gguf"):
             print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

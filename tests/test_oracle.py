@@ -22,6 +22,7 @@ from oracle import ORDER_REPACKED, ORDER_ROW, Oracle, Reference
 TYPES = {"q8_0": S.T_Q8_0, "q4_k": S.T_Q4_K, "q6_k": S.T_Q6_K, "q5_0": S.T_Q5_0, "q5_k": S.T_Q5_K,
          "q4_0": S.T_Q4_0, "q4_1": S.T_Q4_1, "q5_1": S.T_Q5_1, "iq4_nl": S.T_IQ4_NL}
 ALL = list(TYPES.values())
+LOWBIT = {"q2_k": S.T_Q2_K, "q3_k": S.T_Q3_K, "iq4_xs": S.T_IQ4_XS}
 REPACKABLE = (S.T_Q4_K, S.T_Q4_0)  # the types the reference repacks (repack_tensor, fastgguf.c:2486)
 
 
@@ -273,7 +274,9 @@ MUTANTS = {1: "hsum8 order", 2: "MoE accumulate without fma", 3: "reciprocal ins
            9: "Q4_1 / Q5_1 min term without the fused multiply-add",
            10: "attention score lanes added in sequence", 11: "softmax tail through exp_neg_ps",
            12: "TurboQuant key dot without the contraction", 13: "TurboQuant scale from an fma chain",
-           14: "per-row attention score tail without the contraction"}
+           14: "per-row attention score tail without the contraction",
+           15: "Q2_K chain without gcc's contractions", 16: "Q3_K hmask bit of the other half",
+           17: "IQ4_XS high scale bits at the wrong shift"}
 
 
 @pytest.fixture(scope="module")
@@ -311,6 +314,11 @@ def _golden_failures(o: Oracle) -> int:
         fails += not bits_equal(o.attn_rows(c["q"], c["st"], c["en"], c["ck"], c["cv"], [c["kvo"]] * len(c["st"]),
                                             c["hd"], c["scale"]), c["o"])
     fails += kvq_golden_failures(o)
+    g = golden("lowbit.npz")
+    for name, t in LOWBIT.items():
+        for gen in ("synth", "bytes"):
+            x = g[f"{name}_{gen}_x"]
+            fails += not bits_equal(o.matvec(t, g[f"{name}_{gen}_w"], x.size, x), g[f"{name}_{gen}_y"])
     return fails
 
 
