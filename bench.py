@@ -25,6 +25,9 @@ prefill: BASELINE config 4 (64 tokens x 4096 -> 14336, Q4_K) on the int8 MFMA GE
          the same shape in Q8_0, Q6_K and Q4_0 on their MFMA GEMMs, and the FFN down projection
          of the same tokens (14336 -> 4096, where the GEMMs split K) in Q4_K, Q6_K and Q8_0,
          against their HBM floors.
+other configs: BASELINE configs 1, 3 and 5 (Q8_0 matvec, Q6_K LM head, the MoE FFN at 1 and 64
+         tokens) and the low-bit types Q2_K, Q3_K and IQ4_XS at the gate shape 4096 -> 14336,
+         against the same HBM peak.
 cpu_baseline: the reference's own CPU kernels (oracle/_ref, compiled from fastgguf.c) on the same
          layer's five matvecs with its default repacked Q4_K path (its silu loop, 14336 expf, is
          not in the sample), on this host's physical cores, over weight copies beyond the host's
@@ -178,6 +181,23 @@ def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
                                 "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes}
     t.free()
     be.dev_free(y)
+    # the low-bit types (Q2_K, Q3_K, IQ4_XS; fgh_kq.hip) at the gate shape 4096 -> 14336, weight
+    # copies rotating past the Infinity Cache
+    for name, ty in (("q2_k", S.T_Q2_K), ("q3_k", S.T_Q3_K), ("iq4_xs", S.T_IQ4_XS)):
+        wb = 14336 * S.row_bytes(ty, 4096)
+        n = copies_for(wb)
+        w = S.weights(ty, 14336, 4096, 130 + ty)
+        ts = [be.upload(ty, 4096, w) for _ in range(n)]
+        del w
+        y = be.dev_alloc(4 * 14336)
+        us = kernel_time(lambda i: be.matvec_dev(ts[i % n], x, y), 200)
+        nbytes = wb + 4 * (4096 + 14336)
+        out[f"lowbit_{name}_gate_matvec"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                                              "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+                                              "copies": n}
+        for t in ts:
+            t.free()
+        be.dev_free(y)
     be.dev_free(x)
     # config 5: MoE FFN, 2 expert sets (531 MB)
     E, K, D, F = 128, 8, 2048, 768

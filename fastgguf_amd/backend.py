@@ -13,7 +13,7 @@ import os
 
 import numpy as np
 
-from .synth import BLOCK, Q8_BLK, Q8K_BLK, T_Q4_K, T_Q5_0, T_Q5_K, T_Q6_K, T_Q8_0, row_bytes
+from .synth import BLOCK, K256Q8_TYPES, Q8_BLK, Q8K_BLK, T_Q4_K, T_Q5_0, T_Q5_K, T_Q6_K, T_Q8_0, row_bytes
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfastgguf_hip.so")
@@ -319,9 +319,12 @@ class Backend:
         return out
 
     def block_ints(self, t: Tensor, x: np.ndarray):
+        """Per (row, block) integers of the decode kernel: sumi, msum [nout][blocks]; Q2_K, Q3_K and
+        IQ4_XS per 32-value block, the units of their chains."""
         x = np.ascontiguousarray(x, np.float32)
-        s = np.empty((t.nout, t.nblocks), np.int32)
-        m = np.empty((t.nout, t.nblocks), np.int32)
+        nbk = t.cols // 32 if t.type in K256Q8_TYPES else t.nblocks
+        s = np.empty((t.nout, nbk), np.int32)
+        m = np.empty((t.nout, nbk), np.int32)
         self._check(self.lib.fgh_block_ints(self.ctx, t.handle, _p(x), _p(s), _p(m)))
         return s, m
 

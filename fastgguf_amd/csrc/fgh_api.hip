@@ -148,7 +148,7 @@ static int grow(fgh_ctx *c, DevBuf &b, size_t need) {
 }
 
 static bool type_supported(uint32_t t) {
-    return fgh::q8_kind((int)t) || t == FGH_T_Q4_K || t == FGH_T_Q6_K || t == FGH_T_Q5_K;
+    return fgh::q8_kind((int)t) || t == FGH_T_Q4_K || t == FGH_T_Q6_K || t == FGH_T_Q5_K || fgh::kq_kind((int)t);
 }
 static bool q16_rows(uint32_t t) { return t == FGH_T_Q4_K || t == FGH_T_Q5_K; }  // 16-row tiles
 static int block_elems(uint32_t t) { return fgh::q8_kind((int)t) ? 32 : 256; }
@@ -161,6 +161,7 @@ static int block_bytes(uint32_t t) {
     case FGH_T_Q5_1: return 24;
     case FGH_T_Q4_K: return 144;
     case FGH_T_Q5_K: return 176;
+    case FGH_T_Q2_K: case FGH_T_Q3_K: case FGH_T_IQ4_XS: return fgh::kq_block_bytes((int)t);
     default: return 210;
     }
 }
@@ -170,6 +171,7 @@ static int tile_bytes(uint32_t t) {
     case FGH_T_Q4_K: return fgh::Q4K_TILE;
     case FGH_T_Q5_K: return fgh::Q5K_TILE;
     case FGH_T_Q6_K: return fgh::Q6K_TILE;
+    case FGH_T_Q2_K: case FGH_T_Q3_K: case FGH_T_IQ4_XS: return fgh::kq_tile((int)t);
     default: return fgh::q32_layout((int)t).tile;  // the nibble types
     }
 }
@@ -553,6 +555,9 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
         e = q16_rows(type)
                 ? fgh::launch_q4k_relayout((int)type, (const uint8_t *)stage, t->dev, rows, t->nb, t->gpm,
                                            (int64_t)t->dev_bytes, row_bytes, c->stream)
+            : fgh::kq_kind((int)type)
+                ? fgh::launch_kq_relayout((int)type, (const uint8_t *)stage, t->dev, rows, t->nb, t->gpm,
+                                          (int64_t)t->dev_bytes, row_bytes, c->stream)
                 : fgh::launch_relayout((const uint8_t *)stage, t->dev, (int)type, rows, t->nb, t->ntile, t->gpm,
                                        (int64_t)t->dev_bytes, row_bytes, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
@@ -695,8 +700,8 @@ int fgh_matmul_dev(fgh_ctx *c, const fgh_tensor *t, const float *X, int ldx, flo
     INJECT(c);
     HIP_TRY(c, hipSetDevice(c->device));
     // nb >= 8: the prompt GEMMs (matmul 3018-3031) on int8 MFMA for Q4_K, Q6_K, Q8_0 and the nibble
-    // types Q4_0 / Q4_1 / Q5_0 / Q5_1; Q5_K and IQ4_NL, which have no GEMM in the reference, run the
-    // per-token decode kernels as its matmul does
+    // types Q4_0 / Q4_1 / Q5_0 / Q5_1; Q5_K, IQ4_NL, Q2_K, Q3_K and IQ4_XS, which have no GEMM in the
+    // reference, run the per-token decode kernels as its matmul does
     if (prompt_gemm_bytes(c, t, nb)) return prompt_gemm(c, t, X, ldx, Y, ldy, nb, nullptr, nullptr);
     float *ys[1] = {Y};
     return matvec_launch(c, 1, &t, X, ldx, ys, ldy, nb, nullptr, nullptr);
@@ -1257,7 +1262,8 @@ int fgh_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *x, int32_t *sum
     NO_CAPTURE(c);
     if (!x || !sumi || !msum) return fail(c, FGH_ERR_ARG, "block_ints: null pointer");
     const int64_t nout = t->rows * t->n_mats;
-    const size_t nint = (size_t)nout * t->nb;
+    // per (row, block); Q2_K / Q3_K / IQ4_XS: per (row, 32-value block), the units of their chains
+    const size_t nint = (size_t)nout * t->nb * (fgh::kq_kind((int)t->type) ? 8 : 1);
     HIP_TRY(c, hipSetDevice(c->device));
     void *ds = nullptr;
     if ((rc = grow(c, c->x, (size_t)t->cols * 4)) || (rc = grow(c, c->y, (size_t)nout * 4))) return rc;

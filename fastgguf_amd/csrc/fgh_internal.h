@@ -42,8 +42,8 @@ namespace fgh {
 //     16r + 8 + 2bb (one 16-byte load per row and step); q32_layout gives the offsets
 //   (Q5_K shares the Q4_K layout with 512 B of fifth bits per (tile, block), fgh_q4k.hip)
 // ---------------------------------------------------------------------------------------------
-constexpr int T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
-              T_IQ4_NL = 20;
+constexpr int T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12,
+              T_Q5_K = 13, T_Q6_K = 14, T_IQ4_NL = 20, T_IQ4_XS = 23;
 constexpr int Q4K_TILE = 2304, Q5K_TILE = 2816, Q6K_TILE = 1680, Q80_TILE = 1088, Q50_TILE = 704;
 constexpr int Q4K_TILE_ROWS = 16;  // rows per Q4_K / Q5_K tile (8 for the other types)
 // the activation kind of a weight type (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for
@@ -64,6 +64,11 @@ __host__ __device__ constexpr Q32Layout q32_layout(int type) {
                           : Q32Layout{576, -1, 64, -1, 8};  // Q4_0, IQ4_NL
 }
 __host__ __device__ constexpr bool q32_min(int type) { return type == T_Q4_1 || type == T_Q5_1; }
+// the 256-value types on Q8 activations (Q2_K, Q3_K, IQ4_XS; their own kernel, fgh_kq.hip):
+// file block bytes and device tile bytes (8 rows of one block)
+__host__ __device__ constexpr bool kq_kind(int type) { return type == T_Q2_K || type == T_Q3_K || type == T_IQ4_XS; }
+__host__ __device__ constexpr int kq_block_bytes(int type) { return type == T_Q2_K ? 84 : type == T_Q3_K ? 110 : 136; }
+__host__ __device__ constexpr int kq_tile(int type) { return 8 * kq_block_bytes(type); }
 
 // Device activation layouts. Q8_K (for the K-quants): per token, nb blocks of
 //   qs [nb][256] int8, permuted so lane i's 32 bytes are contiguous: position 32i + 4c + k holds
@@ -197,6 +202,15 @@ __device__ __forceinline__ int dot2_i16(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot2(__builtin_bit_cast(fgh_short2, a), __builtin_bit_cast(fgh_short2, b), c, false);
 }
 
+// IQ4_NL / IQ4_XS: the value kvalues_iq4nl[q] (fastgguf.c:475-477) of each nibble byte, by two
+// byte permutes over the table's halves and a third that picks, per byte, the half by bit 3
+__device__ __forceinline__ uint32_t iq4nl_values(uint32_t nib) {
+    constexpr uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;  // -127 .. 113
+    const uint32_t sel = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
+    return __builtin_amdgcn_perm(hi, lo, ((nib >> 1) & 0x04040404u) | 0x03020100u);
+}
+
 __device__ __forceinline__ int sbyte(uint32_t w, int k) {  // signed byte k of a dword
     return (int)(int8_t)(w >> (8 * k));
 }
@@ -324,6 +338,12 @@ hipError_t launch_q4k_moe_down(int type, const MvArgs &a, const float *wts, int 
 hipError_t launch_q4k_relayout(int type, const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t tpm,
                                int64_t total, int64_t row_bytes, hipStream_t s);
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
+// Q2_K / Q3_K / IQ4_XS (fgh_kq.hip): tiles, decode kernel, launch shape
+size_t kq_lds_bytes(int nb);
+MvShape kq_matvec_shape(int type, int64_t tiles, int nb, int num_cu);
+hipError_t launch_kq_matvec(int type, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
+hipError_t launch_kq_relayout(int type, const uint8_t *src, uint8_t *dst, int64_t rows, int nb, int64_t gpm,
+                              int64_t total, int64_t row_bytes, hipStream_t s);
 
 // MoE around the expert matvecs (fgh_moe.hip)
 // expf as glibc >= 2.27 computes it (the method of ARM's optimized-routines expf), in double:

@@ -1,5 +1,6 @@
 // fgh_matvec.hip - the decode matvec for Q6_K and the 32-value types (Q8_0, Q5_0, Q4_0, Q4_1, Q5_1,
-// IQ4_NL) on gfx950 (Q4_K and Q5_K have their own kernel in fgh_q4k.hip, on the same plan).
+// IQ4_NL) on gfx950 (Q4_K and Q5_K have their own kernel in fgh_q4k.hip, on the same plan, and so
+// do Q2_K, Q3_K and IQ4_XS in fgh_kq.hip).
 //
 // Tiles (fgh_internal.h) are 8 rows of one step: one block (Q6_K, 1680 B) or four blocks (Q8_0,
 // 1088 B; Q5_0 704 B, Q4_0 / IQ4_NL 576 B, Q4_1 640 B, Q5_1 768 B). They lie step-major: step s of row tile t of matrix m at
@@ -215,14 +216,6 @@ __device__ __forceinline__ void q32_sums(const StepW<T_Q8_0> &w, uint4 y, int sd
     sd[1] = dot4((int)w.q.y, (int)y.y, 0);
     sd[2] = dot4((int)w.q.z, (int)y.z, 0);
     sd[3] = dot4((int)w.q.w, (int)y.w, 0);
-}
-// IQ4_NL: the value kvalues_iq4nl[q] (fastgguf.c:475-477) of each nibble byte, by two byte
-// permutes over the table's halves and a third that picks, per byte, the half by bit 3
-__device__ __forceinline__ uint32_t iq4nl_values(uint32_t nib) {
-    constexpr uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;  // -127 .. 113
-    const uint32_t sel = nib & 0x07070707u;
-    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
-    return __builtin_amdgcn_perm(hi, lo, ((nib >> 1) & 0x04040404u) | 0x03020100u);
 }
 // Nibble types: the value of element 4i + t of block k is nibble byte t of n (blocks 2w / 2w + 1
 // in the low / high nibbles of dword w), with (Q5_0 / Q5_1) bit 4 from the fifth bits spread to
@@ -524,6 +517,7 @@ static int mv_tpw(int s) { return s == 1 ? 4 : s <= 4 ? 2 : 1; }
 
 size_t matvec_lds_bytes(int type, int order, int nb) {
     if (type == T_Q4_K || type == T_Q5_K) return q4k_lds_bytes(order, nb);
+    if (kq_kind(type)) return kq_lds_bytes(nb);
     return mv_lds(type, nb, 4, 1);
 }
 
@@ -574,6 +568,7 @@ static hipError_t mv_launch_type(const MvArgs &a, int ntok, int num_cu, hipStrea
 MvShape matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu) {
     switch (type) {
     case T_Q4_K: case T_Q5_K: return q4k_matvec_shape(type, order, tiles, nb, num_cu);
+    case T_Q2_K: case T_Q3_K: case T_IQ4_XS: return kq_matvec_shape(type, tiles, nb, num_cu);
     case T_Q6_K: return mv_shape<T_Q6_K>(tiles, nb, num_cu);
     case T_Q8_0: return mv_shape<T_Q8_0>(tiles, nb, num_cu);
     case T_Q5_0: return mv_shape<T_Q5_0>(tiles, nb, num_cu);
@@ -587,6 +582,7 @@ MvShape matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu) {
 
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
     if (type == T_Q4_K || type == T_Q5_K) return launch_q4k_matvec(type, order, a, ntok, num_cu, s);
+    if (kq_kind(type)) return launch_kq_matvec(type, a, ntok, num_cu, s);
     if (type == T_Q6_K) return mv_launch_type<T_Q6_K>(a, ntok, num_cu, s);
     if (type == T_Q8_0) return mv_launch_type<T_Q8_0>(a, ntok, num_cu, s);
     if (type == T_Q5_0) return mv_launch_type<T_Q5_0>(a, ntok, num_cu, s);

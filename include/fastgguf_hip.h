@@ -48,10 +48,13 @@ extern "C" {
 #define FGH_T_Q5_0 6u
 #define FGH_T_Q5_1 7u
 #define FGH_T_Q8_0 8u
+#define FGH_T_Q2_K 10u
+#define FGH_T_Q3_K 11u
 #define FGH_T_Q4_K 12u
 #define FGH_T_Q5_K 13u
 #define FGH_T_Q6_K 14u
 #define FGH_T_IQ4_NL 20u
+#define FGH_T_IQ4_XS 23u
 
 /* status codes */
 #define FGH_OK 0

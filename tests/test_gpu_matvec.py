@@ -196,7 +196,13 @@ def test_upload_refusals(backend):
         backend.upload(S.T_Q4_K, 300, np.zeros(8 * 144 * 2, np.uint8), rows=8)  # cols % 256 != 0
     assert e.value.status == SKIP_TYPE
     with pytest.raises(BackendError) as e:
-        backend.upload(10, 256, np.zeros(8 * 84, np.uint8), rows=8)  # Q2_K: not on this path
+        backend.upload(1, 256, np.zeros(8 * 512, np.uint8), rows=8)  # F16: not on this path
+    assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:  # Q2_K needs cols % 256 == 0
+        backend.upload(S.T_Q2_K, 288, np.zeros(8 * 84, np.uint8), rows=8)
+    assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:  # Q2_K / Q3_K / IQ4_XS past 204 blocks: x past 64 KiB of LDS
+        backend.upload(S.T_IQ4_XS, 205 * 256, np.zeros(8 * 205 * 136, np.uint8), rows=8)
     assert e.value.status == SKIP_TYPE
     with pytest.raises(BackendError) as e:  # 238 blocks: the quantized x no longer fits 64 KiB of LDS
         backend.upload(S.T_Q4_K, 238 * 256, np.zeros(16 * 238 * 144, np.uint8), rows=16)
@@ -220,7 +226,7 @@ def test_upload_refusals(backend):
         backend.upload(S.T_Q5_0, 48, np.zeros(8 * 22, np.uint8), rows=8)
     assert e.value.status == SKIP_TYPE
     info1 = backend.info()
-    assert info1["n_skip_type"] == info0["n_skip_type"] + 9
+    assert info1["n_skip_type"] == info0["n_skip_type"] + 11
     from fastgguf_amd.backend import Backend
     small = Backend(0, budget_bytes=1 << 20)
     with pytest.raises(BackendError) as e:
