@@ -425,6 +425,7 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=200, help="individually timed gate matvecs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget (0 = skip)")
     ap.add_argument("--configs", type=int, default=1, help="also time BASELINE configs 1, 3 and 5 (0 = skip)")
+    ap.add_argument("--attention", type=int, default=1, help="also time the attention calls (0 = skip)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run 20 gate matvecs, 20 copies of the same byte count by a plain copy kernel, "
                          "and 20 prefill GEMMs, eagerly (for rocprofv3 --pmc counter passes)")
@@ -682,7 +683,7 @@ def main() -> int:
 
     others = other_configs(be, S, kernel_time, args.configs)
     attn_in = {}
-    attention = attention_config(be, kernel_time, args.configs, attn_in)
+    attention = attention_config(be, kernel_time, args.configs and args.attention, attn_in)
 
     cpu = cpu_baseline(layer_w, xs, args.cpu_seconds, host, attn_in) if args.cpu_seconds > 0 else None
     info = be.info()
