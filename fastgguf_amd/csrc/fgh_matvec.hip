@@ -538,7 +538,11 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 // more (Q6_K: 2), the records within the 160 KiB of LDS of a workgroup and every workgroup of the
 // launch resident at once; tiles per workgroup 4 for S = 1, 2 for S = 2 and 4 (halving the
 // workgroups that each quantize x), 1 for S = 8. Ring depth:
-// 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps, 4 otherwise.
+// 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps, 4 otherwise;
+// Q6_K (steps of 1680 B, 1.5x the others'): 2 for split launches and for the LM-head size (8192
+// tiles or more over rows shorter than 32 steps), 4 otherwise (measured, graph of back-to-back
+// launches: 14336 x 4096 11.9 -> 11.0 us, 8192 x 2048 6.4 -> 5.8, 4096 x 14336 13.4 -> 13.1;
+// the LM head, QKV and the split shapes unchanged).
 template <int TYPE>
 static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
     const int nst = mv_steps(TYPE, nb);
@@ -550,7 +554,8 @@ static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
                all_resident((tiles + mv_tpw(2 * S) - 1) / mv_tpw(2 * S), 2 * S * mv_tpw(2 * S),
                             mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S), num_cu))
             S *= 2;
-    const int R = nst < 32 && tiles * S >= 1024 ? 2 : 4;
+    const int R = TYPE == T_Q6_K ? (S > 1 || (tiles >= 8192 && nst < 32) ? 2 : 4)
+                                 : nst < 32 && tiles * S >= 1024 ? 2 : 4;
     return MvShape{S, R, mv_tpw(S), mv_lds(TYPE, nb, mv_tpw(S), S)};
 }
 template <int TYPE, int ORDER = 0>

@@ -29,7 +29,8 @@ pytestmark = pytest.mark.gpu
 
 FAMILIES = [(S.T_Q4_K, ORDER_REPACKED), (S.T_Q4_K, ORDER_ROW), (S.T_Q5_K, ORDER_ROW), (S.T_Q6_K, ORDER_ROW),
             (S.T_Q8_0, ORDER_ROW), (S.T_Q5_0, ORDER_ROW), (S.T_Q4_0, ORDER_REPACKED), (S.T_Q4_0, ORDER_ROW),
-            (S.T_Q4_1, ORDER_ROW), (S.T_Q5_1, ORDER_ROW), (S.T_IQ4_NL, ORDER_ROW)]
+            (S.T_Q4_1, ORDER_ROW), (S.T_Q5_1, ORDER_ROW), (S.T_IQ4_NL, ORDER_ROW), (S.T_Q2_K, ORDER_ROW),
+            (S.T_Q3_K, ORDER_ROW), (S.T_IQ4_XS, ORDER_ROW)]
 TILES = [1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 100, 128, 160, 192, 200, 256, 257, 300, 384, 448, 511, 512,
          513, 600, 700, 767, 768, 900, 1000, 1023, 1024, 1100, 1536, 1792, 2048]
 NB_K = [1, 2, 3, 4, 7, 8, 12, 15, 16, 17, 24, 31, 32, 33, 40, 56, 64, 100, 128, 200, 237]
@@ -41,13 +42,13 @@ def tile_rows(t):
 
 
 def block_elems(t):
-    return 32 if S.uses_q8(t) else 256
+    return 256 if t in S.K256Q8_TYPES or not S.uses_q8(t) else 32
 
 
 def reachable(backend, t, order):
     """{(S, R): (nb, tiles)} over the scan, the case with the fewest weight bytes for each shape"""
     found = {}
-    for nb in (NB_32 if S.uses_q8(t) else NB_K):
+    for nb in (NB_32 if block_elems(t) == 32 else NB_K):
         for tiles in TILES:
             s, r, tpw, lds = backend.matvec_shape(t, order, nb * block_elems(t), tiles)
             if s == 0 or lds > (65536 if s == 1 else 163840):
