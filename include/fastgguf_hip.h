@@ -1,7 +1,8 @@
 /*
  * fastgguf_hip.h - C ABI of the MI355X (gfx950) backend for fastgguf's quantized
  * weight x Q8-activation hot path: GGUF Q4_K / Q6_K / Q8_0 weights, and Q5_K, Q5_0, Q4_0, Q4_1,
- * Q5_1 and IQ4_NL (the other block types of the reference's integer kernels), multiplied by
+ * Q5_1, IQ4_NL, Q2_K, Q3_K and IQ4_XS (the other block types of the reference's integer kernels;
+ * its own OpenCL offload leaves the last three on the CPU), multiplied by
  * activations quantized to the reference's Q8 / Q8_K blocks, as a decode matvec, a <=64-token prompt matmul and a
  * mixture-of-experts FFN over the router-selected experts.
  *
