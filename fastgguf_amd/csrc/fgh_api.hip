@@ -104,7 +104,7 @@ struct fgh_tensor {
     int order;     // FGH_ORDER_ROW / FGH_ORDER_REPACKED (Q4_K); ROW otherwise
     int nb;        // blocks per row (256-blocks for K-quants, 32-blocks for Q8_0)
     int ntile;     // tiles per row group
-    int64_t gpm;   // row tiles per matrix (16 rows for Q4_K, 8 otherwise)
+    int64_t gpm;   // row tiles per matrix (16 rows for Q4_K, Q5_K, Q2_K, Q3_K and IQ4_XS, 8 otherwise)
     int64_t groups;
     uint8_t *dev;
     uint64_t dev_bytes;
@@ -527,7 +527,7 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     t->n_mats = n_mats;
     t->nb = (int)(cols / block_elems(type));
     t->ntile = fgh::q8_kind((int)type) ? (t->nb + 3) / 4 : t->nb;
-    const int tile_rows = q16_rows(type) ? fgh::Q4K_TILE_ROWS : 8;
+    const int tile_rows = q16_rows(type) ? fgh::Q4K_TILE_ROWS : fgh::kq_kind((int)type) ? fgh::KQ_TILE_ROWS : 8;
     t->gpm = (rows + tile_rows - 1) / tile_rows;
     t->groups = t->gpm * n_mats;
     t->order = ord;

@@ -65,10 +65,11 @@ __host__ __device__ constexpr Q32Layout q32_layout(int type) {
 }
 __host__ __device__ constexpr bool q32_min(int type) { return type == T_Q4_1 || type == T_Q5_1; }
 // the 256-value types on Q8 activations (Q2_K, Q3_K, IQ4_XS; their own kernel, fgh_kq.hip):
-// file block bytes and device tile bytes (8 rows of one block)
+// file block bytes and device tile bytes (16 rows of one block)
 __host__ __device__ constexpr bool kq_kind(int type) { return type == T_Q2_K || type == T_Q3_K || type == T_IQ4_XS; }
 __host__ __device__ constexpr int kq_block_bytes(int type) { return type == T_Q2_K ? 84 : type == T_Q3_K ? 110 : 136; }
-__host__ __device__ constexpr int kq_tile(int type) { return 8 * kq_block_bytes(type); }
+constexpr int KQ_TILE_ROWS = 16;
+__host__ __device__ constexpr int kq_tile(int type) { return KQ_TILE_ROWS * kq_block_bytes(type); }
 
 // Device activation layouts. Q8_K (for the K-quants): per token, nb blocks of
 //   qs [nb][256] int8, permuted so lane i's 32 bytes are contiguous: position 32i + 4c + k holds
@@ -286,7 +287,7 @@ struct MvT {
     const uint8_t *W;
     float *y;
     int64_t rows;    // rows per matrix
-    int64_t gpm;     // row tiles per matrix (16 rows for Q4_K / Q5_K, 8 otherwise)
+    int64_t gpm;     // row tiles per matrix (16 rows for Q4_K / Q5_K / Q2_K / Q3_K / IQ4_XS, 8 otherwise)
     int64_t gfirst;  // first global tile index of this tensor
 };
 struct MvArgs {

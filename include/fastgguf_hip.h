@@ -328,8 +328,9 @@ FGH_API int fgh_event_destroy(fgh_ctx *ctx, void *ev);
  * fgh_fp16_to_f32: the device's fp16 -> fp32 decode of n codes.
  * fgh_expf: the device's expf (the MoE softmax and silu) of n values.
  * fgh_matvec_shape: the launch shape a decode launch of `type` (order as fgh_upload resolved it)
- * over row_tiles row tiles of all its tensors (16 rows per tile for Q4_K / Q5_K, 8 otherwise) and
- * ntok tokens picks: shape[0] wavefronts per tile, [1] ring depth, [2] tiles per workgroup, [3]
+ * over row_tiles row tiles of all its tensors (16 rows per tile for Q4_K / Q5_K / Q2_K / Q3_K /
+ * IQ4_XS, 8 otherwise) and ntok tokens picks: shape[0] wavefronts per tile, [1] ring depth, [2]
+ * tiles per workgroup, [3]
  * LDS bytes. Lets the tests run every kernel instantiation the launchers can choose. */
 FGH_API int fgh_quantize(fgh_ctx *ctx, int kind, const float *x, int n, void *out_blocks);
 FGH_API int fgh_block_ints(fgh_ctx *ctx, const fgh_tensor *t, const float *x, int32_t *sumi, int32_t *msum);

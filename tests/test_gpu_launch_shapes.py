@@ -38,7 +38,7 @@ NB_32 = [1, 3, 4, 8, 12, 16, 28, 29, 32, 60, 64, 96, 124, 125, 128, 160, 200, 25
 
 
 def tile_rows(t):
-    return 16 if t in (S.T_Q4_K, S.T_Q5_K) else 8
+    return 16 if t in (S.T_Q4_K, S.T_Q5_K) or t in S.K256Q8_TYPES else 8
 
 
 def block_elems(t):

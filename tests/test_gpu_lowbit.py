@@ -34,10 +34,11 @@ def test_matvec_matches_golden(backend, name, gen):
     t.free()
 
 
-# shapes that take every launch form: 8 wavefronts per tile (64 rows), 2 and 4 (a few hundred
-# rows), 1 (thousands of rows); ragged row counts (a partly filled last tile); one-block rows
+# shapes that take every launch form: 8 wavefronts per tile (up to a few thousand rows of 16 blocks
+# or more), 4 (8200 rows, or 8 blocks), 2 (20000 rows, or 4 blocks), 1 (rows of 1 block); ragged
+# row counts (a partly filled last tile)
 SHAPES = [(64, 16384), (13, 2048), (512, 4096), (200, 8192), (4096, 4096), (8200, 4096), (9, 256), (1000, 256),
-          (2048, 14336)]
+          (2048, 14336), (100, 1024), (20000, 2048)]
 
 
 @pytest.mark.parametrize("t", list(LOWBIT.values()))
@@ -46,7 +47,7 @@ def test_matvec_matches_oracle(backend, oracle, t, rows, cols):
     gen = S.random_bytes_weights if (rows + cols) % 2 else S.weights
     w = gen(t, rows, cols, rows + 7 * t)
     x = S.activations(cols, cols + t) * np.float32(2.5)
-    print(f"matvec {S.TYPE_NAME[t]} {rows}x{cols} shape {backend.matvec_shape(t, 0, cols, (rows + 7) // 8)}",
+    print(f"matvec {S.TYPE_NAME[t]} {rows}x{cols} shape {backend.matvec_shape(t, 0, cols, (rows + 15) // 16)}",
           flush=True)
     tt = backend.upload(t, cols, w)
     check_vec(backend.matvec(tt, x), oracle.matvec(t, w, cols, x))
@@ -54,10 +55,10 @@ def test_matvec_matches_oracle(backend, oracle, t, rows, cols):
 
 
 def test_launch_forms_are_all_taken(backend):
-    """The shapes above cover 1, 2, 4 and 8 wavefronts per tile (ring depth 4 throughout)."""
-    seen = {backend.matvec_shape(S.T_Q2_K, 0, cols, (rows + 7) // 8)[:2] for rows, cols in SHAPES}
-    assert {s for s, _ in seen} == {1, 2, 4, 8}, seen
-    assert {r for _, r in seen} == {4}, seen
+    """The shapes above cover 1, 2, 4 and 8 wavefronts per tile (ring depth 4 for whole rows, 2
+    for split launches)."""
+    seen = {backend.matvec_shape(S.T_Q2_K, 0, cols, (rows + 15) // 16)[:2] for rows, cols in SHAPES}
+    assert seen == {(1, 4), (2, 2), (4, 2), (8, 2)}, seen
 
 
 @pytest.mark.parametrize("t", list(LOWBIT.values()))
