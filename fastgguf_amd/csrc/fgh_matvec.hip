@@ -534,11 +534,15 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 }
 
 // Launch shape: launches of fewer than 768 tiles (tiles x tokens) split the steps of a tile over up
-// to 8 wavefronts, as many as keep the launch within 2048 wavefronts, each wavefront at 4 steps or
-// more (Q6_K: 2), the records within the 160 KiB of LDS of a workgroup and every workgroup of the
-// launch resident at once; tiles per workgroup 4 for S = 1, 2 for S = 2 and 4 (halving the
-// workgroups that each quantize x), 1 for S = 8. Ring depth:
-// 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps, 4 otherwise;
+// to 8 wavefronts, as many as keep the launch within 2048 wavefronts, each wavefront at 2 steps or
+// more, the records within the 160 KiB of LDS of a workgroup and every workgroup of the launch
+// resident at once; tiles per workgroup 4 for S = 1, 2 for S = 2 and 4 (halving the workgroups
+// that each quantize x), 1 for S = 8. (With 4 steps or more per wavefront, as before for the
+// 32-value types, 2048 x 2048, 1024 x 2048 and 512 x 2048 ran 9-15 % slower, 4096 x 1024 3-8 %;
+// 1024 x 1024 and 2048 x 1024 of Q4_1 / Q5_0 gain 1-3 % with it; larger shapes do not split
+// differently.) Ring depth:
+// 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps and for
+// wavefronts of 2 steps, 4 otherwise;
 // Q6_K (steps of 1680 B, 1.5x the others'): 2 for split launches and for the LM-head size (8192
 // tiles or more over rows shorter than 32 steps), 4 otherwise (measured, graph of back-to-back
 // launches: 14336 x 4096 11.9 -> 11.0 us, 8192 x 2048 6.4 -> 5.8, 4096 x 14336 13.4 -> 13.1;
@@ -546,16 +550,15 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 template <int TYPE>
 static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
     const int nst = mv_steps(TYPE, nb);
-    constexpr int SPW = TYPE == T_Q6_K ? 2 : 1;  // Q6_K steps are 4x the bytes of Q8_0's per row
     int S = 1;
     if (tiles < 768)
-        while (S < 8 && tiles * 2 * S <= 2048 && nst >= 8 * S / SPW &&
+        while (S < 8 && tiles * 2 * S <= 2048 && nst >= 4 * S &&
                mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX &&
                all_resident((tiles + mv_tpw(2 * S) - 1) / mv_tpw(2 * S), 2 * S * mv_tpw(2 * S),
                             mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S), num_cu))
             S *= 2;
     const int R = TYPE == T_Q6_K ? (S > 1 || (tiles >= 8192 && nst < 32) ? 2 : 4)
-                                 : nst < 32 && tiles * S >= 1024 ? 2 : 4;
+                                 : (nst < 32 && tiles * S >= 1024) || (nst + S - 1) / S <= 2 ? 2 : 4;
     return MvShape{S, R, mv_tpw(S), mv_lds(TYPE, nb, mv_tpw(S), S)};
 }
 template <int TYPE, int ORDER = 0>
