@@ -503,12 +503,14 @@ size_t q4k_lds_bytes(int order, int nb) { return q4_lds(order, nb, 4, 1); }
 
 // Launch shape (measured on MI355X at the decode-layer shapes). Wavefronts per tile S: launches of
 // at most 768 tiles (tiles x tokens) split the blocks of a tile over up to 8 wavefronts, as many
-// as keep the launch within 2048 wavefronts, each wavefront at 2 blocks or more, the LDS within
+// as keep the launch within 2048 wavefronts with 2 blocks or more each, or (Q4_K) within 3072 with
+// 4 blocks or more each (repacked 11008 x 4096, 688 tiles: 4 ways, 7.30 -> 6.87 us against 2;
+// 5120 x 13824, 320 tiles: 8 ways, 12.7 -> 11.6 us against 4; Q5_K does better without), the LDS within
 // the 160 KiB of a workgroup and every workgroup resident at once; larger launches keep one
 // wavefront per tile. Tiles per workgroup: 4, 2 or 1 for S = 1, 2 or more. Ring depth R: 2 steps
-// for split launches (but the repacked order over rows of 48 blocks or more: its down projection
-// 14336 -> 4096 runs 9.09 us at depth 4 against 9.19 at 2) and for unsplit ones of 1024 tiles or
-// more over rows shorter than 32 blocks (enough loads in flight across the chip), 4 otherwise.
+// for split launches (the repacked down projection 14336 -> 4096 alone runs 1 % faster at depth 4,
+// 9.09 against 9.19 us, and 5120 x 13824 9 % slower) and for unsplit ones of 1024 tiles or more
+// over rows shorter than 32 blocks (enough loads in flight across the chip), 4 otherwise.
 // (Before, splits kept 4 blocks per
 // wavefront and depth 4 unless the launch had 1024 wavefronts over short rows; measured, graph of
 // back-to-back launches: O 4096 x 4096 4.78 -> 4.59 us, 2048 x 2048 4.41 -> 3.59, 4096 x 8192
@@ -527,12 +529,13 @@ MvShape q4k_matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu)
     if (type == T_Q5_K) order = 0;  // no repacked order for Q5_K
     int S = 1;
     if (tiles <= 768)  // (the MoE batch-1 gate/up launch has 768: 14.98 -> 14.33 us with S = 2)
-        while (S < 8 && tiles * 2 * S <= 2048 && nb >= 4 * S &&
+        while (S < 8 &&
+               ((tiles * 2 * S <= 2048 && nb >= 4 * S) || (type == T_Q4_K && tiles * 2 * S <= 3072 && nb >= 8 * S)) &&
                q4_lds(order, nb, q4_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX &&
                all_resident((tiles + q4_tpw(2 * S) - 1) / q4_tpw(2 * S), 2 * S * q4_tpw(2 * S),
                             q4_lds(order, nb, q4_tpw(2 * S), 2 * S), num_cu))
             S *= 2;
-    const int R = (S > 1 && !(order == 1 && nb >= 48)) || (nb < 32 && tiles >= 1024) ? 2 : 4;
+    const int R = S > 1 || (nb < 32 && tiles >= 1024) ? 2 : 4;
     return MvShape{S, R, q4_tpw(S), q4_lds(order, nb, q4_tpw(S), S)};
 }
 
