@@ -540,7 +540,10 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 // that each quantize x), 1 for S = 8. (With 4 steps or more per wavefront, as before for the
 // 32-value types, 2048 x 2048, 1024 x 2048 and 512 x 2048 ran 9-15 % slower, 4096 x 1024 3-8 %;
 // 1024 x 1024 and 2048 x 1024 of Q4_1 / Q5_0 gain 1-3 % with it; larger shapes do not split
-// differently.) Ring depth:
+// differently.) Q4_0, Q5_0 and IQ4_NL also split 2 ways from 768 to 1536 tiles within 3072
+// wavefronts (11008 x 4096, 8192 x 4096, 6400 x 4096: IQ4_NL 13-15 %, Q4_0 / Q5_0 2-4 % faster;
+// Q8_0 and Q6_K gain at some of these shapes and lose at others, 3-7 %, and Q4_1 / Q5_1 lose up
+// to 5 %: they keep the 768-tile limit). Ring depth:
 // 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps and for
 // wavefronts of 2 steps, 4 otherwise;
 // Q6_K (steps of 1680 B, 1.5x the others'): 2 for split launches and for the LM-head size (8192
@@ -551,8 +554,10 @@ template <int TYPE>
 static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
     const int nst = mv_steps(TYPE, nb);
     int S = 1;
-    if (tiles < 768)
-        while (S < 8 && tiles * 2 * S <= 2048 && nst >= 4 * S &&
+    // Q4_0, Q5_0 and IQ4_NL split 2 ways up to 1536 tiles and 3072 wavefronts too
+    constexpr bool NIB = TYPE == T_Q4_0 || TYPE == T_Q5_0 || TYPE == T_IQ4_NL;
+    if (tiles < (NIB ? 1536 : 768))
+        while (S < 8 && (tiles * 2 * S <= 2048 || (NIB && S == 1 && tiles * 2 <= 3072)) && nst >= 4 * S &&
                mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX &&
                all_resident((tiles + mv_tpw(2 * S) - 1) / mv_tpw(2 * S), 2 * S * mv_tpw(2 * S),
                             mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S), num_cu))
