@@ -543,7 +543,10 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 // differently.) Q4_0, Q5_0 and IQ4_NL also split 2 ways from 768 to 1536 tiles within 3072
 // wavefronts (11008 x 4096, 8192 x 4096, 6400 x 4096: IQ4_NL 13-15 %, Q4_0 / Q5_0 2-4 % faster;
 // Q8_0 and Q6_K gain at some of these shapes and lose at others, 3-7 %, and Q4_1 / Q5_1 lose up
-// to 5 %: they keep the 768-tile limit). Ring depth:
+// to 5 %: they keep the 768-tile limit). Q6_K splits only up to 512 tiles: from 576 to 768
+// (4608 .. 6144 rows) every split leaves some compute units two workgroups (288 .. 384 of them for
+// 256 units) and waits for them, 18.0 - 19.4 us at 14336 columns against 16.7 - 16.9 unsplit, while
+// 512 tiles split 4 ways fill the 256 units once (12.9 us against 16.5). Ring depth:
 // 2 steps for launches of 1024 wavefronts or more over rows shorter than 32 steps and for
 // wavefronts of 2 steps, 4 otherwise;
 // Q6_K (steps of 1680 B, 1.5x the others'): 2 for split launches and for the LM-head size (8192
@@ -554,9 +557,10 @@ template <int TYPE>
 static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
     const int nst = mv_steps(TYPE, nb);
     int S = 1;
-    // Q4_0, Q5_0 and IQ4_NL split 2 ways up to 1536 tiles and 3072 wavefronts too
+    // Q4_0, Q5_0 and IQ4_NL split 2 ways up to 1536 tiles and 3072 wavefronts too; Q6_K splits
+    // only up to 512 tiles
     constexpr bool NIB = TYPE == T_Q4_0 || TYPE == T_Q5_0 || TYPE == T_IQ4_NL;
-    if (tiles < (NIB ? 1536 : 768))
+    if (tiles < (NIB ? 1536 : TYPE == T_Q6_K ? 513 : 768))
         while (S < 8 && (tiles * 2 * S <= 2048 || (NIB && S == 1 && tiles * 2 <= 3072)) && nst >= 4 * S &&
                mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S) <= GEMM_LDS_MAX &&
                all_resident((tiles + mv_tpw(2 * S) - 1) / mv_tpw(2 * S), 2 * S * mv_tpw(2 * S),
