@@ -507,7 +507,8 @@ size_t q4k_lds_bytes(int order, int nb) { return q4_lds(order, nb, 4, 1); }
 // 4 blocks or more each (repacked 11008 x 4096, 688 tiles: 4 ways, 7.30 -> 6.87 us against 2;
 // 5120 x 13824, 320 tiles: 8 ways, 12.7 -> 11.6 us against 4; Q5_K does better without), the LDS within
 // the 160 KiB of a workgroup and every workgroup resident at once; larger launches keep one
-// wavefront per tile. Tiles per workgroup: 4, 2 or 1 for S = 1, 2 or more. Ring depth R: 2 steps
+// wavefront per tile. Tiles per workgroup: 4, 2 or 1 for S = 1, 2 or more, and 2 for a 4-way
+// split of 9/8 to 2 tiles per compute unit. Ring depth R: 2 steps
 // for split launches (the repacked down projection 14336 -> 4096 alone runs 1 % faster at depth 4,
 // 9.09 against 9.19 us, and 5120 x 13824 9 % slower) and for unsplit ones of 1024 tiles or more
 // over rows shorter than 32 blocks (enough loads in flight across the chip), 4 otherwise.
@@ -517,11 +518,13 @@ size_t q4k_lds_bytes(int order, int nb) { return q4_lds(order, nb, 4, 1); }
 // 6.97 -> 6.02, the row order's down 4096 x 14336 10.1 -> 9.6, Q5_K's 11.4 -> 10.7; QKV, gate,
 // the repacked down and the paired launches unchanged.)
 template <int ORDER, int TYPE>
-static hipError_t q4_launch_s(int S, int R, const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
+static hipError_t q4_launch_s(int S, int TPW, int R, const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
     switch (S) {
     case 1: return q4_launch_r<ORDER, 4, 1, TYPE>(R, a, ntok, lds, s);
     case 2: return q4_launch_r<ORDER, 2, 2, TYPE>(R, a, ntok, lds, s);
-    case 4: return q4_launch_r<ORDER, 1, 4, TYPE>(R, a, ntok, lds, s);
+    case 4:
+        return TPW == 2 ? q4_launch_r<ORDER, 2, 4, TYPE>(R, a, ntok, lds, s)
+                        : q4_launch_r<ORDER, 1, 4, TYPE>(R, a, ntok, lds, s);
     default: return q4_launch_r<ORDER, 1, 8, TYPE>(R, a, ntok, lds, s);
     }
 }
@@ -536,7 +539,14 @@ MvShape q4k_matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu)
                             q4_lds(order, nb, q4_tpw(2 * S), 2 * S), num_cu))
             S *= 2;
     const int R = S > 1 || (nb < 32 && tiles >= 1024) ? 2 : 4;
-    return MvShape{S, R, q4_tpw(S), q4_lds(order, nb, q4_tpw(S), S)};
+    // a 4-way split of 9/8 to 2 tiles per compute unit holds 2 tiles per workgroup (Q4_K repacked
+    // 5120 x 5120, 320 tiles: 6.78 -> 5.96 us, Q5_K 7.45 -> 6.76; 4608 x 5120 6.78 -> 5.91; rows
+    // of 16 blocks within 2 % either way from 288 tiles up; 257 tiles 6 % slower)
+    int tpw = q4_tpw(S);
+    if (S == 4 && tiles * 8 >= 9 * (int64_t)num_cu && tiles <= 2 * num_cu &&
+        q4_lds(order, nb, 2, 4) <= GEMM_LDS_MAX && all_resident((tiles + 1) / 2, 8, q4_lds(order, nb, 2, 4), num_cu))
+        tpw = 2;
+    return MvShape{S, R, tpw, q4_lds(order, nb, tpw, S)};
 }
 
 // paired launches: after the activations and records, with routing each wavefront's routing
@@ -580,9 +590,9 @@ hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int
         lds = a.logits ? q4_route_lds(sh) : q4_pair_lds(sh);
         if (lds > GEMM_LDS_MAX) return hipErrorInvalidValue;
     }
-    if (type == T_Q5_K) return q4_launch_s<0, T_Q5_K>(sh.S, sh.R, b, ntok, lds, s);
-    if (order == 0) return q4_launch_s<0, T_Q4_K>(sh.S, sh.R, b, ntok, lds, s);
-    return q4_launch_s<1, T_Q4_K>(sh.S, sh.R, b, ntok, lds, s);
+    if (type == T_Q5_K) return q4_launch_s<0, T_Q5_K>(sh.S, sh.TPW, sh.R, b, ntok, lds, s);
+    if (order == 0) return q4_launch_s<0, T_Q4_K>(sh.S, sh.TPW, sh.R, b, ntok, lds, s);
+    return q4_launch_s<1, T_Q4_K>(sh.S, sh.TPW, sh.R, b, ntok, lds, s);
 }
 
 // MoE down projection and combine of one token in one launch (moe_ffn, fastgguf.c:4620-4635):

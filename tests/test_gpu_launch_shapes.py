@@ -2,7 +2,7 @@
 
 The decode launchers choose a launch shape per call from the row tiles of the launch, the row
 width and the device's compute units: S wavefronts per tile (a block split for short matrices),
-a register ring of R steps, TPW tiles per workgroup. Each (type, order, S, R) is a separate kernel
+a register ring of R steps, TPW tiles per workgroup. Each (type, order, S, R, TPW) is a separate kernel
 instantiation, and so is its integer-dump form. fgh_matvec_shape reports the shape a call would
 take (the same function the launchers call), so these tests
 
@@ -46,14 +46,14 @@ def block_elems(t):
 
 
 def reachable(backend, t, order):
-    """{(S, R): (nb, tiles)} over the scan, the case with the fewest weight bytes for each shape"""
+    """{(S, R, TPW): (nb, tiles)} over the scan, the case with the fewest weight bytes for each shape"""
     found = {}
     for nb in (NB_32 if block_elems(t) == 32 else NB_K):
         for tiles in TILES:
             s, r, tpw, lds = backend.matvec_shape(t, order, nb * block_elems(t), tiles)
             if s == 0 or lds > (65536 if s == 1 else 163840):
                 continue  # such a tensor is refused at upload, or the launch refuses it
-            key = (s, r)
+            key = (s, r, tpw)
             if key not in found or nb * tiles < found[key][0] * found[key][1]:
                 found[key] = (nb, tiles)
     return found
@@ -69,18 +69,19 @@ def test_every_launch_shape_bit_exact(backend, oracle, fam):
     shapes = reachable(backend, t, order)
     # the forms the launchers are written for: one wavefront per tile at ring depth 4, and block
     # splits; Q4_K and the 32-value types also reach ring depth 2 on large launches
-    assert (1, 4) in shapes and any(s > 1 for s, _ in shapes), shapes
+    assert any(k[:2] == (1, 4) for k in shapes) and any(k[0] > 1 for k in shapes), shapes
     o_order = O_RP if order == ORDER_REPACKED else O_ROW
-    for (s, r), (nb, tiles) in sorted(shapes.items()):
+    for (s, r, tpw), (nb, tiles) in sorted(shapes.items()):
         rows = tiles * tile_rows(t)
         cols = nb * block_elems(t)
         seed = 1000 + 13 * s + r + nb
         w = S.random_bytes_weights(t, rows, cols, seed)
         x = S.activations(cols, seed + 1)
         tt = backend.upload(t, cols, w, order=order)
-        assert backend.matvec_shape(t, order, cols, tiles)[:2] == (s, r)
+        assert backend.matvec_shape(t, order, cols, tiles)[:3] == (s, r, tpw)
         y = backend.matvec(tt, x)
-        assert bits_equal(y, oracle.matvec(t, w, cols, x, o_order)), f"matvec S={s} R={r} nb={nb} tiles={tiles}"
+        assert bits_equal(y, oracle.matvec(t, w, cols, x, o_order)), \
+            f"matvec S={s} R={r} TPW={tpw} nb={nb} tiles={tiles}"
         # the integer-dump form of the same shape: a sample of rows against the oracle
         si, mi = backend.block_ints(tt, x)
         act = oracle.quantize_for(t, x)
@@ -94,6 +95,25 @@ def test_every_launch_shape_bit_exact(backend, oracle, fam):
         assert bits_equal(backend.matvec_silu(tt, g, u), oracle.matvec(t, w, cols, h, o_order)), \
             f"silu S={s} R={r} nb={nb} tiles={tiles}"
         tt.free()
+
+
+@pytest.mark.parametrize("fam", FAMILIES[:3], ids=family_id)
+@pytest.mark.parametrize("rows,cols", [(5120, 5120), (6144, 4096), (4616, 4096)])
+def test_two_tiles_per_workgroup_split(backend, oracle, fam, rows, cols):
+    """4-way splits of 9/8 to 2 tiles per compute unit hold 2 tiles per workgroup: 5120 x 5120
+    (320 tiles), QKV 6144 x 4096 (384), 4616 x 4096 (289 tiles: a partly filled last tile and
+    workgroup), bit for bit against the oracle."""
+    t, order = fam
+    tiles = (rows + 15) // 16
+    shape = backend.matvec_shape(t, order, cols, tiles)
+    print(f"{S.TYPE_NAME[t]} order {order} {rows}x{cols} shape {shape}", flush=True)
+    assert shape[:3] == (4, 2, 2), shape  # MI355X: 256 compute units
+    w = S.random_bytes_weights(t, rows, cols, rows + cols + t)
+    x = S.activations(cols, rows + 1)
+    tt = backend.upload(t, cols, w, order=order)
+    o_order = O_RP if order == ORDER_REPACKED else O_ROW
+    assert bits_equal(backend.matvec(tt, x), oracle.matvec(t, w, cols, x, o_order))
+    tt.free()
 
 
 @pytest.mark.parametrize("order", [ORDER_REPACKED, ORDER_ROW], ids=["rp", "row"])
