@@ -26,8 +26,8 @@ prefill: BASELINE config 4 (64 tokens x 4096 -> 14336, Q4_K) on the int8 MFMA GE
          of the same tokens (14336 -> 4096, where the GEMMs split K) in Q4_K, Q6_K and Q8_0,
          against their HBM floors.
 other configs: BASELINE configs 1, 3 and 5 (Q8_0 matvec, Q6_K LM head, the MoE FFN at 1 and 64
-         tokens) and the low-bit types Q2_K, Q3_K and IQ4_XS at the gate shape 4096 -> 14336,
-         against the same HBM peak.
+         tokens), the low-bit types Q2_K, Q3_K and IQ4_XS and the float types F32, F16 and BF16
+         at the gate shape 4096 -> 14336, against the same HBM peak.
 cpu_baseline: the reference's own CPU kernels (oracle/_ref, compiled from fastgguf.c) on the same
          layer's five matvecs with its default repacked Q4_K path (its silu loop, 14336 expf, is
          not in the sample), on this host's physical cores, over weight copies beyond the host's
@@ -195,6 +195,22 @@ def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
         out[f"lowbit_{name}_gate_matvec"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
                                               "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes,
                                               "copies": n}
+        for t in ts:
+            t.free()
+        be.dev_free(y)
+    # the float types (F32, F16, BF16; fgh_float.hip) at the same shape: x in fp32, no quantization
+    for name, ty in (("f32", S.T_F32), ("f16", S.T_F16), ("bf16", S.T_BF16)):
+        wb = 14336 * S.row_bytes(ty, 4096)
+        n = copies_for(wb)
+        w = S.weights(ty, 14336, 4096, 140 + ty)
+        ts = [be.upload(ty, 4096, w) for _ in range(n)]
+        del w
+        y = be.dev_alloc(4 * 14336)
+        us = kernel_time(lambda i: be.matvec_dev(ts[i % n], x, y), 100)
+        nbytes = wb + 4 * (4096 + 14336)
+        out[f"float_{name}_gate_matvec"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                                             "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+                                             "copies": n}
         for t in ts:
             t.free()
         be.dev_free(y)

@@ -30,7 +30,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libfastgguf_hip.so")
 SOURCES = ["fgh_api.hip", "fgh_kernels.hip", "fgh_matvec.hip", "fgh_q4k.hip", "fgh_moemm.hip", "fgh_gemm.hip", "fgh_gemm32.hip",
            "fgh_gemm32n.hip", "fgh_gemm6.hip", "fgh_moe.hip", "fgh_gguf.hip", "fgh_attn.hip", "fgh_kvq.hip",
-           "fgh_kq.hip"]
+           "fgh_kq.hip", "fgh_float.hip"]
 # per-source additions: the nibble-type GEMM converts every MFMA result with a VALU instruction, so
 # its results go to VGPRs (without the flag the compiler writes them to AGPRs and copies each out)
 FILE_FLAGS = {"fgh_gemm32n.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"], "fgh_moemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}

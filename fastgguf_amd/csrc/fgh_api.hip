@@ -148,10 +148,11 @@ static int grow(fgh_ctx *c, DevBuf &b, size_t need) {
 }
 
 static bool type_supported(uint32_t t) {
-    return fgh::q8_kind((int)t) || t == FGH_T_Q4_K || t == FGH_T_Q6_K || t == FGH_T_Q5_K || fgh::kq_kind((int)t);
+    return fgh::q8_kind((int)t) || t == FGH_T_Q4_K || t == FGH_T_Q6_K || t == FGH_T_Q5_K || fgh::kq_kind((int)t) ||
+           fgh::fl_kind((int)t);
 }
 static bool q16_rows(uint32_t t) { return t == FGH_T_Q4_K || t == FGH_T_Q5_K; }  // 16-row tiles
-static int block_elems(uint32_t t) { return fgh::q8_kind((int)t) ? 32 : 256; }
+static int block_elems(uint32_t t) { return fgh::fl_kind((int)t) ? 1 : fgh::q8_kind((int)t) ? 32 : 256; }
 static int block_bytes(uint32_t t) {
     switch (t) {
     case FGH_T_Q8_0: return 34;
@@ -162,6 +163,7 @@ static int block_bytes(uint32_t t) {
     case FGH_T_Q4_K: return 144;
     case FGH_T_Q5_K: return 176;
     case FGH_T_Q2_K: case FGH_T_Q3_K: case FGH_T_IQ4_XS: return fgh::kq_block_bytes((int)t);
+    case FGH_T_F32: case FGH_T_F16: case FGH_T_BF16: return fgh::fl_value_bytes((int)t);
     default: return 210;
     }
 }
@@ -172,6 +174,7 @@ static int tile_bytes(uint32_t t) {
     case FGH_T_Q5_K: return fgh::Q5K_TILE;
     case FGH_T_Q6_K: return fgh::Q6K_TILE;
     case FGH_T_Q2_K: case FGH_T_Q3_K: case FGH_T_IQ4_XS: return fgh::kq_tile((int)t);
+    case FGH_T_F32: case FGH_T_F16: case FGH_T_BF16: return fgh::FL_TILE;
     default: return fgh::q32_layout((int)t).tile;  // the nibble types
     }
 }
@@ -507,8 +510,10 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
                             (order == FGH_ORDER_REPACKED || (order == FGH_ORDER_AUTO && n_mats == 1 && rows % 8 == 0))
                         ? FGH_ORDER_REPACKED
                         : FGH_ORDER_ROW;
+    // the decode kernels stage x in LDS: up to 64 KiB (the float types, whose x stays fp32: 160 KiB)
+    const size_t lds_max = fgh::fl_kind((int)type) ? fgh::GEMM_LDS_MAX : 65536;
     if (!type_supported(type) || cols % block_elems(type) != 0 ||
-        fgh::matvec_lds_bytes((int)type, ord, (int)std::min<int64_t>(cols / block_elems(type), 1 << 20)) > 65536) {
+        fgh::matvec_lds_bytes((int)type, ord, (int)std::min<int64_t>(cols / block_elems(type), 1 << 20)) > lds_max) {
         c->n_skip_type++;
         return fail(c, FGH_SKIP_TYPE, "upload: type %u with %lld cols is not supported", type, (long long)cols);
     }
@@ -526,8 +531,13 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
     t->rows = rows;
     t->n_mats = n_mats;
     t->nb = (int)(cols / block_elems(type));
-    t->ntile = fgh::q8_kind((int)type) ? (t->nb + 3) / 4 : t->nb;
-    const int tile_rows = q16_rows(type) ? fgh::Q4K_TILE_ROWS : fgh::kq_kind((int)type) ? fgh::KQ_TILE_ROWS : 8;
+    t->ntile = fgh::fl_kind((int)type) ? (int)((cols + fgh::fl_step_elems((int)type) - 1) / fgh::fl_step_elems((int)type))
+               : fgh::q8_kind((int)type) ? (t->nb + 3) / 4
+                                          : t->nb;
+    const int tile_rows = q16_rows(type)               ? fgh::Q4K_TILE_ROWS
+                          : fgh::kq_kind((int)type) ? fgh::KQ_TILE_ROWS
+                          : fgh::fl_kind((int)type) ? fgh::fl_tile_rows((int)type)
+                                                    : 8;
     t->gpm = (rows + tile_rows - 1) / tile_rows;
     t->groups = t->gpm * n_mats;
     t->order = ord;
@@ -558,6 +568,9 @@ int fgh_upload(fgh_ctx *c, uint32_t type, int64_t cols, int64_t rows, int64_t n_
             : fgh::kq_kind((int)type)
                 ? fgh::launch_kq_relayout((int)type, (const uint8_t *)stage, t->dev, rows, t->nb, t->gpm,
                                           (int64_t)t->dev_bytes, row_bytes, c->stream)
+            : fgh::fl_kind((int)type)
+                ? fgh::launch_fl_relayout((int)type, (const uint8_t *)stage, t->dev, rows, cols, t->ntile, t->gpm,
+                                          (int64_t)t->dev_bytes, c->stream)
                 : fgh::launch_relayout((const uint8_t *)stage, t->dev, (int)type, rows, t->nb, t->ntile, t->gpm,
                                        (int64_t)t->dev_bytes, row_bytes, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
@@ -1261,6 +1274,7 @@ int fgh_block_ints(fgh_ctx *c, const fgh_tensor *t, const float *x, int32_t *sum
     if (rc) return rc;
     NO_CAPTURE(c);
     if (!x || !sumi || !msum) return fail(c, FGH_ERR_ARG, "block_ints: null pointer");
+    if (fgh::fl_kind((int)t->type)) return fail(c, FGH_ERR_ARG, "block_ints: a float tensor has no integer parts");
     const int64_t nout = t->rows * t->n_mats;
     // per (row, block); Q2_K / Q3_K / IQ4_XS: per (row, 32-value block), the units of their chains
     const size_t nint = (size_t)nout * t->nb * (fgh::kq_kind((int)t->type) ? 8 : 1);

@@ -42,8 +42,8 @@ namespace fgh {
 //     16r + 8 + 2bb (one 16-byte load per row and step); q32_layout gives the offsets
 //   (Q5_K shares the Q4_K layout with 512 B of fifth bits per (tile, block), fgh_q4k.hip)
 // ---------------------------------------------------------------------------------------------
-constexpr int T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12,
-              T_Q5_K = 13, T_Q6_K = 14, T_IQ4_NL = 20, T_IQ4_XS = 23;
+constexpr int T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q2_K = 10,
+              T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_NL = 20, T_IQ4_XS = 23, T_BF16 = 30;
 constexpr int Q4K_TILE = 2304, Q5K_TILE = 2816, Q6K_TILE = 1680, Q80_TILE = 1088, Q50_TILE = 704;
 constexpr int Q4K_TILE_ROWS = 16;  // rows per Q4_K / Q5_K tile (8 for the other types)
 // the activation kind of a weight type (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for
@@ -70,6 +70,13 @@ __host__ __device__ constexpr bool kq_kind(int type) { return type == T_Q2_K || 
 __host__ __device__ constexpr int kq_block_bytes(int type) { return type == T_Q2_K ? 84 : type == T_Q3_K ? 110 : 136; }
 constexpr int KQ_TILE_ROWS = 16;
 __host__ __device__ constexpr int kq_tile(int type) { return KQ_TILE_ROWS * kq_block_bytes(type); }
+// the float types F32, F16, BF16 (fp32 activations, their own kernel, fgh_float.hip): a step of a
+// row tile is 1 KB, 16 bytes per lane: F32 tiles of 4 rows x 64 values, F16 8 x 64, BF16 64 x 8
+__host__ __device__ constexpr bool fl_kind(int type) { return type == T_F32 || type == T_F16 || type == T_BF16; }
+constexpr int FL_TILE = 1024;
+__host__ __device__ constexpr int fl_tile_rows(int type) { return type == T_F32 ? 4 : type == T_F16 ? 8 : 64; }
+__host__ __device__ constexpr int fl_step_elems(int type) { return type == T_BF16 ? 8 : 64; }
+__host__ __device__ constexpr int fl_value_bytes(int type) { return type == T_F32 ? 4 : 2; }
 
 // Device activation layouts. Q8_K (for the K-quants): per token, nb blocks of
 //   qs [nb][256] int8, permuted so lane i's 32 bytes are contiguous: position 32i + 4c + k holds
@@ -329,6 +336,12 @@ MvShape q4k_matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu)
 // Q4_K / Q5_K (fgh_q4k.hip): their own tile layout and kernel
 size_t q4k_lds_bytes(int order, int nb);
 hipError_t launch_q4k_matvec(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
+// F32 / F16 / BF16 (fgh_float.hip): a.nb = the row's values, a.ntile = its steps
+size_t fl_lds_bytes(int type, int64_t cols);
+MvShape fl_matvec_shape(int type, int64_t tiles, int64_t cols, int num_cu);
+hipError_t launch_fl_matvec(int type, const MvArgs &a, int ntok, int num_cu, hipStream_t s);
+hipError_t launch_fl_relayout(int type, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols, int steps,
+                              int64_t gpm, int64_t total, hipStream_t s);
 // the MoE down projection and ordered combine of each token in one launch (Q4_K / Q5_K row order):
 // a.t[0] = {down, y}, a.x = the h = silu(g) * u rows of the token slots (stride a.ldx), a.sel the
 // slots' experts, wts their weights, k <= 8 experts per token

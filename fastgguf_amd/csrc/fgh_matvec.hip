@@ -1,6 +1,6 @@
 // fgh_matvec.hip - the decode matvec for Q6_K and the 32-value types (Q8_0, Q5_0, Q4_0, Q4_1, Q5_1,
 // IQ4_NL) on gfx950 (Q4_K and Q5_K have their own kernel in fgh_q4k.hip, on the same plan, and so
-// do Q2_K, Q3_K and IQ4_XS in fgh_kq.hip).
+// do Q2_K, Q3_K and IQ4_XS in fgh_kq.hip, and F32, F16 and BF16 in fgh_float.hip).
 //
 // Tiles (fgh_internal.h) are 8 rows of one step: one block (Q6_K, 1680 B) or four blocks (Q8_0,
 // 1088 B; Q5_0 704 B, Q4_0 / IQ4_NL 576 B, Q4_1 640 B, Q5_1 768 B). They lie step-major: step s of row tile t of matrix m at
@@ -518,6 +518,7 @@ static int mv_tpw(int s) { return s == 1 ? 4 : s <= 4 ? 2 : 1; }
 size_t matvec_lds_bytes(int type, int order, int nb) {
     if (type == T_Q4_K || type == T_Q5_K) return q4k_lds_bytes(order, nb);
     if (kq_kind(type)) return kq_lds_bytes(nb);
+    if (fl_kind(type)) return fl_lds_bytes(type, nb);  // nb: the row's values
     return mv_lds(type, nb, 4, 1);
 }
 
@@ -586,6 +587,7 @@ MvShape matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu) {
     switch (type) {
     case T_Q4_K: case T_Q5_K: return q4k_matvec_shape(type, order, tiles, nb, num_cu);
     case T_Q2_K: case T_Q3_K: case T_IQ4_XS: return kq_matvec_shape(type, tiles, nb, num_cu);
+    case T_F32: case T_F16: case T_BF16: return fl_matvec_shape(type, tiles, nb, num_cu);
     case T_Q6_K: return mv_shape<T_Q6_K>(tiles, nb, num_cu);
     case T_Q8_0: return mv_shape<T_Q8_0>(tiles, nb, num_cu);
     case T_Q5_0: return mv_shape<T_Q5_0>(tiles, nb, num_cu);
@@ -600,6 +602,7 @@ MvShape matvec_shape(int type, int order, int64_t tiles, int nb, int num_cu) {
 hipError_t launch_matvec2(int type, int order, const MvArgs &a, int ntok, int num_cu, hipStream_t s) {
     if (type == T_Q4_K || type == T_Q5_K) return launch_q4k_matvec(type, order, a, ntok, num_cu, s);
     if (kq_kind(type)) return launch_kq_matvec(type, a, ntok, num_cu, s);
+    if (fl_kind(type)) return launch_fl_matvec(type, a, ntok, num_cu, s);
     if (type == T_Q6_K) return mv_launch_type<T_Q6_K>(a, ntok, num_cu, s);
     if (type == T_Q8_0) return mv_launch_type<T_Q8_0>(a, ntok, num_cu, s);
     if (type == T_Q5_0) return mv_launch_type<T_Q5_0>(a, ntok, num_cu, s);

@@ -15,11 +15,14 @@ Byte layouts follow fastgguf.c (lawnak/FastGGUF):
   Q5_1  24 B / 32 weights   fp16 d @0, fp16 m @2, u32 qh @4, nibbles @8      (fastgguf.c:534-550)
   IQ4_NL 18 B / 32 weights  fp16 d @0, nibbles @2; value d kvalues[q]        (fastgguf.c:694-706)
   (32-value types: element j is nibble j of qs, low nibbles of qs[0..15] first, then the high ones)
+  F32 / F16 / BF16: one value per element, 4 / 2 / 2 bytes; BF16 = the high 16 bits of an fp32
+                            (dequantize_row 481-489, bf16_to_float 124-127)
 Value distributions are the benchmark's: Q4_K nibbles uniform, 6-bit scales and mins uniform in
 [0, 63], d and dmin = fp16(|N(0,1)| * 0.005); Q6_K quant bytes uniform, int8 scales uniform in
 [-64, 63], d = fp16(|N(0,1)| * 0.002); Q8_0 quants uniform in [-127, 127], d = fp16(|N(0,1)| * 0.01);
 Q5_0 and Q5_K quant bytes uniform, d = fp16(|N(0,1)| * 0.01) (Q5_0) or as Q4_K (Q5_K); the other
-32-value types quant bytes uniform, d = fp16(|N(0,1)| * 0.01), m = fp16(N(0,1) * 0.05).
+32-value types quant bytes uniform, d = fp16(|N(0,1)| * 0.01), m = fp16(N(0,1) * 0.05); the float
+types N(0,1) * 0.02 (F16 rounded to nearest even, BF16 rounded to nearest even on the high half).
 fp16 conversion rounds to nearest even (numpy astype).
 """
 from __future__ import annotations
@@ -27,6 +30,8 @@ from __future__ import annotations
 import numpy as np
 
 T_F32 = 0
+T_F16 = 1
+T_BF16 = 30
 T_Q4_0 = 2
 T_Q4_1 = 3
 T_Q5_0 = 6
@@ -43,13 +48,16 @@ T_IQ4_XS = 23
 #: (elements per block, bytes per block), block_size_of (fastgguf.c:235-253)
 BLOCK = {T_Q8_0: (32, 34), T_Q4_K: (256, 144), T_Q6_K: (256, 210), T_Q5_0: (32, 22), T_Q5_K: (256, 176),
          T_Q4_0: (32, 18), T_Q4_1: (32, 20), T_Q5_1: (32, 24), T_IQ4_NL: (32, 18),
-         T_Q2_K: (256, 84), T_Q3_K: (256, 110), T_IQ4_XS: (256, 136)}
+         T_Q2_K: (256, 84), T_Q3_K: (256, 110), T_IQ4_XS: (256, 136), T_F32: (1, 4), T_F16: (1, 2),
+         T_BF16: (1, 2)}
 TYPE_NAME = {T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q6_K: "Q6_K", T_Q5_0: "Q5_0", T_Q5_K: "Q5_K", T_Q4_0: "Q4_0",
              T_Q4_1: "Q4_1", T_Q5_1: "Q5_1", T_IQ4_NL: "IQ4_NL", T_Q2_K: "Q2_K", T_Q3_K: "Q3_K",
-             T_IQ4_XS: "IQ4_XS"}
+             T_IQ4_XS: "IQ4_XS", T_F32: "F32", T_F16: "F16", T_BF16: "BF16"}
 Q32_TYPES = (T_Q8_0, T_Q5_0, T_Q4_0, T_Q4_1, T_Q5_1, T_IQ4_NL)
 #: 256-value blocks whose row kernels take Q8 (32-value) activations
 K256Q8_TYPES = (T_Q2_K, T_Q3_K, T_IQ4_XS)
+#: one value per element; the row kernels take x in fp32 (no quantization)
+FLOAT_TYPES = (T_F32, T_F16, T_BF16)
 
 
 def uses_q8(type_: int) -> bool:
@@ -187,7 +195,46 @@ def k256q8_weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
     return blk.reshape(rows, -1)
 
 
+def _bf16_bits(v: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, rounded to nearest even on the dropped 16 bits (finite inputs)"""
+    u = np.ascontiguousarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def float_weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    rng = np.random.Generator(np.random.PCG64(seed))
+    v = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    if type_ == T_F16:
+        v = v.astype(np.float16)
+    elif type_ == T_BF16:
+        v = _bf16_bits(v)
+    return np.ascontiguousarray(v).view(np.uint8).reshape(rows, -1)
+
+
+def random_float_bits(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """Random finite values of every exponent that keeps products with N(0, 1) activations finite:
+    F16 every exponent (subnormals included, no inf / NaN), F32 and BF16 exponents 2^-40 .. 2^10,
+    and about one value in 16 a zero or a subnormal, with random signs."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    n = rows * cols
+    if type_ == T_F16:
+        b = rng.integers(0, 1 << 16, size=n, dtype=np.uint32)
+        e = (b >> 10) & 31
+        b = np.where(e == 31, b & ~np.uint32(1 << 14), b).astype(np.uint16)  # exponent 31 -> 15
+    else:
+        man = rng.integers(0, 1 << 23, size=n, dtype=np.uint32)
+        ex = rng.integers(127 - 40, 127 + 11, size=n).astype(np.uint32)
+        ex = np.where(rng.integers(0, 16, size=n) == 0, 0, ex).astype(np.uint32)  # zeros / subnormals
+        sg = rng.integers(0, 2, size=n, dtype=np.uint32)
+        b = (sg << 31) | (ex << 23) | man
+        if type_ == T_BF16:
+            b = (b >> 16).astype(np.uint16)
+    return np.ascontiguousarray(b).view(np.uint8).reshape(rows, -1)
+
+
 def weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    if type_ in FLOAT_TYPES:
+        return float_weights(type_, rows, cols, seed)
     if type_ in K256Q8_TYPES:
         return k256q8_weights(type_, rows, cols, seed)
     if type_ in (T_Q4_0, T_Q4_1, T_Q5_1, T_IQ4_NL):
@@ -208,6 +255,8 @@ def weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
 def random_bytes_weights(type_: int, rows: int, cols: int, seed: int) -> np.ndarray:
     """Uniform random bytes with sane fp16 scales, as the reference selftest builds its rows
     (fastgguf.c:5701-5710): d in 0x2C00..0x2FFF, dmin in 0x2400..0x27FF."""
+    if type_ in FLOAT_TYPES:
+        return random_float_bits(type_, rows, cols, seed)
     rng = np.random.Generator(np.random.PCG64(seed))
     eb, bb = BLOCK[type_]
     nb = rows * (cols // eb)

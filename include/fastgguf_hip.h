@@ -4,7 +4,8 @@
  * Q5_1, IQ4_NL, Q2_K, Q3_K and IQ4_XS (the other block types of the reference's integer kernels;
  * its own OpenCL offload leaves the last three on the CPU), multiplied by
  * activations quantized to the reference's Q8 / Q8_K blocks, as a decode matvec, a <=64-token prompt matmul and a
- * mixture-of-experts FFN over the router-selected experts.
+ * mixture-of-experts FFN over the router-selected experts; and the float weight types F32, F16
+ * and BF16, whose row kernels take x in fp32 (dot_row, fastgguf.c:2207-2214).
  *
  * The ABI is plain C: fixed-width integers, plain pointers and sizes, opaque handles, no
  * callbacks, no varargs, no C++ or torch types. A Rust `extern "C"` block or a C caller binds it
@@ -44,6 +45,8 @@ extern "C" {
 #endif
 
 /* GGML tensor types handled here (the reference's enum, fastgguf.c:215-221) */
+#define FGH_T_F32 0u
+#define FGH_T_F16 1u
 #define FGH_T_Q4_0 2u
 #define FGH_T_Q4_1 3u
 #define FGH_T_Q5_0 6u
@@ -56,12 +59,14 @@ extern "C" {
 #define FGH_T_Q6_K 14u
 #define FGH_T_IQ4_NL 20u
 #define FGH_T_IQ4_XS 23u
+#define FGH_T_BF16 30u
 
 /* status codes */
 #define FGH_OK 0
 #define FGH_ERR (-1)           /* operation failed (the reference's -1 from fg_gpu_matvec) */
 #define FGH_ERR_ARG (-2)       /* bad argument or shape mismatch */
-#define FGH_SKIP_TYPE (-3)     /* upload: unsupported type or cols not a block multiple */
+#define FGH_SKIP_TYPE (-3)     /* upload: unsupported type, cols not a block multiple, or too many
+                                  cols for the kernel's LDS copy of x */
 #define FGH_SKIP_MEM (-4)      /* upload: over the memory budget, or device allocation failed */
 #define FGH_ERR_DEVICE (-5)    /* no usable device, or a HIP runtime error */
 
@@ -318,7 +323,8 @@ FGH_API int fgh_event_destroy(fgh_ctx *ctx, void *ev);
  * fgh_quantize: the device quantizer's output in the reference struct layout (kind FGH_ACT_Q8:
  * n/32 blocks of 40 bytes; FGH_ACT_Q8K: n/256 blocks of 292 bytes), from host x.
  * fgh_block_ints: per (row, block) integer parts of dot(W[r], Q8(x)) as the device kernels
- * compute them: sumi / msum [rows * n_mats][blocks per row] (see the oracle's fgo_block_ints).
+ * compute them: sumi / msum [rows * n_mats][blocks per row] (see the oracle's fgo_block_ints);
+ * FGH_ERR_ARG for the float types, which have none.
  * fgh_gemm_block_ints: the same integers as the prompt GEMMs (Q4_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0
  * or Q5_1, nb tokens, 8..64) compute them: sumi / msum [nb][rows * n_mats][blocks per row], token t
  * from row t of X (stride ldx). The 32-value types have msum zeros; for Q4_0 / Q4_1 / Q5_0 / Q5_1
@@ -329,7 +335,8 @@ FGH_API int fgh_event_destroy(fgh_ctx *ctx, void *ev);
  * fgh_expf: the device's expf (the MoE softmax and silu) of n values.
  * fgh_matvec_shape: the launch shape a decode launch of `type` (order as fgh_upload resolved it)
  * over row_tiles row tiles of all its tensors (16 rows per tile for Q4_K / Q5_K / Q2_K / Q3_K /
- * IQ4_XS, 8 otherwise) and ntok tokens picks: shape[0] wavefronts per tile, [1] ring depth, [2]
+ * IQ4_XS, 4 for F32, 8 for F16, 64 for BF16, 8 otherwise) and ntok tokens picks: shape[0]
+ * wavefronts per tile, [1] ring depth, [2]
  * tiles per workgroup, [3]
  * LDS bytes. Lets the tests run every kernel instantiation the launchers can choose. */
 FGH_API int fgh_quantize(fgh_ctx *ctx, int kind, const float *x, int n, void *out_blocks);

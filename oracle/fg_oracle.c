@@ -47,6 +47,13 @@ float fgo_fp16(uint16_t h) {
 
 static inline uint16_t rd16(const uint8_t *p) { uint16_t v; memcpy(&v, p, 2); return v; }
 static inline uint32_t rd32(const uint8_t *p) { uint32_t v; memcpy(&v, p, 4); return v; }
+/* bf16_to_float (fastgguf.c:124-127): the 16 bits above 16 zero bits */
+static inline float bf16_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
 
 /* the activation kind of a weight type (type_uses_q8, fastgguf.c:2167-2173): Q8 blocks of 32 for
  * Q8_0 / Q5_0, Q8_K blocks of 256 for the K-quants */
@@ -57,6 +64,8 @@ static inline int uses_q8(uint32_t type) {
     return type == FGO_T_Q8_0 || type == FGO_T_Q5_0 || type == FGO_T_Q4_0 || type == FGO_T_Q4_1 ||
            type == FGO_T_Q5_1 || type == FGO_T_IQ4_NL || k256q8(type);
 }
+/* the float types, whose row kernels take x itself (ACT_F32, type_uses_q8 2172) */
+static inline int float_type(uint32_t type) { return type == FGO_T_F32 || type == FGO_T_F16 || type == FGO_T_BF16; }
 static inline int k256q8_bytes(uint32_t type) { return type == FGO_T_Q2_K ? 84 : type == FGO_T_Q3_K ? 110 : 136; }
 /* the 32-value block types with a min term (d * q + m): Q4_1 / Q5_1 */
 static inline int has_min32(uint32_t type) { return type == FGO_T_Q4_1 || type == FGO_T_Q5_1; }
@@ -579,6 +588,13 @@ void fgo_block_ints(uint32_t type, const uint8_t *row, const void *act, int nb,
 
 /* ---- dequantize_row (fastgguf.c:518-532, 552-562, 622-667, 669-693) ---- */
 int fgo_dequantize_row(uint32_t type, const uint8_t *raw, float *out, int n) {
+    if (float_type(type)) { /* dequantize_row 481-489 */
+        for (int i = 0; i < n; i++) {
+            if (type == FGO_T_F32) memcpy(&out[i], raw + 4 * (size_t)i, 4);
+            else out[i] = type == FGO_T_F16 ? fgo_fp16(rd16(raw + 2 * (size_t)i)) : bf16_f32(rd16(raw + 2 * (size_t)i));
+        }
+        return 0;
+    }
     if (k256q8(type)) { /* dequantize_row 563-586 (Q2_K), 587-620 (Q3_K), 709-727 (IQ4_XS) */
         const int bb = k256q8_bytes(type);
         for (int b = 0; b < n / 256; b++) {
@@ -663,6 +679,8 @@ int fgo_dequantize_row(uint32_t type, const uint8_t *raw, float *out, int n) {
 
 int fgo_block_size(uint32_t type, int *elems, int *bytes) {
     switch (type) {
+    case FGO_T_F32: *elems = 1; *bytes = 4; return 0;
+    case FGO_T_F16: case FGO_T_BF16: *elems = 1; *bytes = 2; return 0;
     case FGO_T_Q8_0: *elems = 32; *bytes = 34; return 0;
     case FGO_T_Q4_K: *elems = 256; *bytes = 144; return 0;
     case FGO_T_Q6_K: *elems = 256; *bytes = 210; return 0;
@@ -674,8 +692,9 @@ int fgo_block_size(uint32_t type, int *elems, int *bytes) {
     }
 }
 
-/* ---- dot_row dispatch (fastgguf.c:2183-2201), and the repacked kernels of matvec_rp ---- */
+/* ---- dot_row dispatch (fastgguf.c:2183-2214), and the repacked kernels of matvec_rp ---- */
 static float dot_row3(uint32_t type, int order, const uint8_t *rb, const void *act, int cols) {
+    if (float_type(type)) return fgo_dot_float(type, rb, (const float *)act, cols);
     if (type == FGO_T_Q4_K)
         return order == FGO_ORDER_REPACKED ? fgo_dot_q4_K_rp(rb, (const fgo_q8k_blk *)act, cols / 256)
                                            : fgo_dot_q4_K(rb, (const fgo_q8k_blk *)act, cols / 256);
@@ -687,6 +706,7 @@ static float dot_row3(uint32_t type, int order, const uint8_t *rb, const void *a
 }
 
 static int type_ok(uint32_t type, int cols) {
+    if (float_type(type)) return cols > 0;
     if (type == FGO_T_Q4_K || type == FGO_T_Q5_K || type == FGO_T_Q6_K || k256q8(type)) return cols > 0 && cols % 256 == 0;
     if (uses_q8(type)) return cols > 0 && cols % 32 == 0;
     return 0;
@@ -695,6 +715,11 @@ static int type_ok(uint32_t type, int cols) {
 /* quantize one activation vector for the type (type_uses_q8 2167 + quantize_act 2176);
  * returns a malloc'd buffer, NULL on failure */
 static void *quantize_for(uint32_t type, const float *x, int cols) {
+    if (float_type(type)) { /* x itself (ACT_F32) */
+        float *c = (float *)malloc((size_t)cols * sizeof(float));
+        if (c) memcpy(c, x, (size_t)cols * sizeof(float));
+        return c;
+    }
     if (uses_q8(type)) {
         fgo_q8_blk *q = (fgo_q8_blk *)malloc((size_t)(cols / 32) * sizeof(fgo_q8_blk));
         if (q) fgo_quantize_q8(x, q, cols);
@@ -706,6 +731,7 @@ static void *quantize_for(uint32_t type, const float *x, int cols) {
 }
 
 static size_t act_bytes(uint32_t type, int cols) {
+    if (float_type(type)) return (size_t)cols * sizeof(float);
     return uses_q8(type) ? (size_t)(cols / 32) * sizeof(fgo_q8_blk) : (size_t)(cols / 256) * sizeof(fgo_q8k_blk);
 }
 
@@ -735,7 +761,9 @@ int fgo_matvec(uint32_t type, int order, const uint8_t *w, int64_t rows, int col
  *   per 32-block g: a = fma(d*xd, ia'_g, a); a = fnmadd(m, xd*(s16_0+s16_1), a)
  *   with ia' = sum u*x over the unsigned weights the VNNI kernel multiplies: Q8_0 u = w + 128,
  *   m = 128 d; Q5_0 u = q5, m = 16 d; Q4_0 u = nib, m = 8 d; Q4_1 / Q5_1 u = nib / q5, m = -FP16(m) */
-static int has_gemm(uint32_t type) { return type != FGO_T_Q5_K && type != FGO_T_IQ4_NL && !k256q8(type); }
+static int has_gemm(uint32_t type) {
+    return type != FGO_T_Q5_K && type != FGO_T_IQ4_NL && !k256q8(type) && !float_type(type);
+}
 static void gemm_row_token(uint32_t type, const uint8_t *rb, const void *act, int cols, float *out) {
     if (uses_q8(type)) {
         const fgo_q8_blk *xq = (const fgo_q8_blk *)act;
@@ -855,7 +883,8 @@ int fgo_matmul(uint32_t type, int order, const uint8_t *w, int64_t rows, int col
     uint8_t *act = (uint8_t *)malloc(ab * (size_t)nb);
     if (!act) return -1;
     for (int t = 0; t < nb; t++) {
-        if (uses_q8(type)) fgo_quantize_q8(X + (size_t)t * ldx, (fgo_q8_blk *)(act + ab * t), cols);
+        if (float_type(type)) memcpy(act + ab * t, X + (size_t)t * ldx, ab);
+        else if (uses_q8(type)) fgo_quantize_q8(X + (size_t)t * ldx, (fgo_q8_blk *)(act + ab * t), cols);
         else fgo_quantize_q8k(X + (size_t)t * ldx, (fgo_q8k_blk *)(act + ab * t), cols);
     }
     int eb, bb;
@@ -993,7 +1022,8 @@ int fgo_moe_down(uint32_t type_down, const uint8_t *down, int n_embd, int ff, in
     uint8_t *act = (uint8_t *)malloc(ab * (size_t)k);
     if (!act) return -1;
     for (int j = 0; j < k; j++) {
-        if (uses_q8(type_down)) fgo_quantize_q8(h + (size_t)j * ff, (fgo_q8_blk *)(act + ab * j), ff);
+        if (float_type(type_down)) memcpy(act + ab * j, h + (size_t)j * ff, ab);
+        else if (uses_q8(type_down)) fgo_quantize_q8(h + (size_t)j * ff, (fgo_q8_blk *)(act + ab * j), ff);
         else fgo_quantize_q8k(h + (size_t)j * ff, (fgo_q8k_blk *)(act + ab * j), ff);
     }
 #pragma omp parallel for schedule(static)
@@ -1131,6 +1161,54 @@ static float dot_f32v(const float *a, const float *b, int n) {
 #else
     for (; i < n; i++) s = fmaf(a[i], b[i], s);
 #endif
+    return s;
+}
+
+/* ---- the float weight types (dot_row 2207-2214 with x in fp32) ----
+ * F32:  dot_f32v over the row's values (1618-1632, above)
+ * F16:  dot_f16_row (1645-1656), F16C + AVX2 form: 8 fma chains, chain l over values 8 i + l
+ *       (each converted exactly by vcvtph2ps), hsum_ps, then the last n % 8 values one fma each
+ *       (gcc's contraction of `s += FP16(h) * x[i]`)
+ * BF16: the loop `s += bf16_to_float(h) * x[i]` (2209-2213): one contracted fma chain over the
+ *       row in order */
+static float dot_f16_row(const uint8_t *row, const float *x, int n) {
+    float acc[8] = {0};
+    int i = 0;
+#if FGO_MUTATE == 18 /* dot_f32v's two accumulators (values 16 i + l and 16 i + 8 + l) */
+    float acc2[8] = {0};
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 8; l++) {
+            acc[l] = fmaf(fgo_fp16(rd16(row + 2 * (i + l))), x[i + l], acc[l]);
+            acc2[l] = fmaf(fgo_fp16(rd16(row + 2 * (i + 8 + l))), x[i + 8 + l], acc2[l]);
+        }
+    for (int l = 0; l < 8; l++) acc[l] += acc2[l];
+#endif
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(fgo_fp16(rd16(row + 2 * (i + l))), x[i + l], acc[l]);
+    float s = hsum8(acc);
+    for (; i < n; i++) s = fmaf(fgo_fp16(rd16(row + 2 * i)), x[i], s);
+    return s;
+}
+static float dot_bf16_row(const uint8_t *row, const float *x, int n) {
+    float s = 0.0f;
+#if FGO_MUTATE == 19 /* the product rounded before the add (no contraction) */
+    for (int i = 0; i < n; i++) {
+        volatile float p = bf16_f32(rd16(row + 2 * i)) * x[i];
+        s += p;
+    }
+#else
+    for (int i = 0; i < n; i++) s = fmaf(bf16_f32(rd16(row + 2 * i)), x[i], s);
+#endif
+    return s;
+}
+float fgo_dot_float(uint32_t type, const uint8_t *row, const float *x, int n) {
+    if (type == FGO_T_F16) return dot_f16_row(row, x, n);
+    if (type == FGO_T_BF16) return dot_bf16_row(row, x, n);
+    float *w = (float *)malloc((size_t)n * sizeof(float));  /* the row's values (rd_f32, unaligned) */
+    if (!w) return NAN;
+    memcpy(w, row, (size_t)n * sizeof(float));
+    float s = dot_f32v(w, x, n);
+    free(w);
     return s;
 }
 

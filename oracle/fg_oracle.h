@@ -22,7 +22,7 @@ extern "C" {
 #endif
 
 enum {
-    FGO_T_F32 = 0, FGO_T_Q4_0 = 2, FGO_T_Q4_1 = 3, FGO_T_Q5_0 = 6, FGO_T_Q5_1 = 7, FGO_T_Q8_0 = 8,
+    FGO_T_F32 = 0, FGO_T_F16 = 1, FGO_T_BF16 = 30, FGO_T_Q4_0 = 2, FGO_T_Q4_1 = 3, FGO_T_Q5_0 = 6, FGO_T_Q5_1 = 7, FGO_T_Q8_0 = 8,
     FGO_T_Q2_K = 10, FGO_T_Q3_K = 11, FGO_T_Q4_K = 12, FGO_T_Q5_K = 13, FGO_T_Q6_K = 14, FGO_T_IQ4_NL = 20,
     FGO_T_IQ4_XS = 23
 };
@@ -51,6 +51,8 @@ float fgo_dot_q32(uint32_t type, const uint8_t *row, const fgo_q8_blk *xq, int n
 /* the 256-value types on Q8 activations (Q2_K, Q3_K, IQ4_XS); nb256 blocks of the row */
 float fgo_dot_k256q8(uint32_t type, const uint8_t *row, const fgo_q8_blk *xq, int nb256);
 float fgo_dot_q4_0_rp(const uint8_t *row, const fgo_q8_blk *xq, int nb);
+/* the float types (F32, F16, BF16) on fp32 activations, n values of the row (dot_row 2207-2214) */
+float fgo_dot_float(uint32_t type, const uint8_t *row, const float *x, int n);
 
 /* per-block integer parts (the bit-exact targets):
  *   Q4_K, Q5_K: sumi[b] = sum_s sc_s * sum_32 q*y,   msum[b] = sum_s m_s * (bs_2s + bs_2s+1)
@@ -121,7 +123,7 @@ float fgo_expf_restated(float x);
 void fgo_expf_n(const float *x, int n, float *out); /* this libm's expf of n values */
 uint64_t fgo_expf_compare(float lo, float hi, uint32_t stride, uint64_t *n_checked, int *max_ulp);
 
-/* dequantize_row for the three types (fastgguf.c:552, 622, 669): textbook value decode */
+/* dequantize_row (fastgguf.c:475-727) for every type here: textbook value decode */
 int fgo_dequantize_row(uint32_t type, const uint8_t *raw, float *out, int n);
 
 /* block geometry: elements and bytes per block (block_size_of, fastgguf.c:235) */

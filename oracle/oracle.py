@@ -15,7 +15,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
-from fastgguf_amd.synth import BLOCK, K256Q8_TYPES, Q8_BLK, Q8K_BLK, uses_q8  # noqa: E402
+from fastgguf_amd.synth import BLOCK, FLOAT_TYPES, K256Q8_TYPES, Q8_BLK, Q8K_BLK, uses_q8  # noqa: E402
 
 ORDER_ROW = 0
 ORDER_REPACKED = 1
@@ -54,6 +54,8 @@ class Oracle:
         L.fgo_dot_q32.restype = C.c_float
         L.fgo_dot_k256q8.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
         L.fgo_dot_k256q8.restype = C.c_float
+        L.fgo_dot_float.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
+        L.fgo_dot_float.restype = C.c_float
         L.fgo_block_ints.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
         L.fgo_matvec.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
         L.fgo_matmul.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_int,
@@ -96,11 +98,17 @@ class Oracle:
         return out
 
     def quantize_for(self, type_: int, x: np.ndarray) -> np.ndarray:
+        """the activations the type's row kernel reads: x itself for the float types"""
+        if type_ in FLOAT_TYPES:
+            return np.ascontiguousarray(x, np.float32).copy()
         return self.quantize_q8(x) if uses_q8(type_) else self.quantize_q8k(x)
 
     # -- row kernels
     def dot(self, type_: int, row: np.ndarray, act: np.ndarray, order: int = ORDER_ROW) -> float:
         row = np.ascontiguousarray(row, np.uint8)
+        if type_ in FLOAT_TYPES:  # act: x in fp32
+            act = np.ascontiguousarray(act, np.float32)
+            return self.lib.fgo_dot_float(type_, _ptr(row), _ptr(act), act.size)
         eb, _ = BLOCK[type_]
         nb = act.size
         if type_ == 2 and order == ORDER_REPACKED:

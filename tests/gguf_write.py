@@ -54,8 +54,8 @@ LONG_KEY = "llama.a_key_longer_than_the_readers_buffer_" + "x" * 57  # 100 chara
 def tiny_model() -> tuple[list, list]:
     """The metadata and tensors of tests/golden/tiny.gguf: every value kind the reader handles (a
     string, numbers of several types, integer / string / float arrays, a key longer than 95
-    characters), general.alignment = 64, and tensors of the five device types (2-D, 3-D experts)
-    plus F32 tensors the device path does not take."""
+    characters), general.alignment = 64, and tensors of five quantized types (2-D, 3-D experts)
+    plus F32 tensors (2-D and 1-D)."""
     kvs = [("general.architecture", STR, "llama"), ("general.alignment", U32, 64),
            ("llama.block_count", U32, 1), ("llama.embedding_length", U64, 256),
            ("llama.rope.freq_base", F32, 500000.0), ("llama.attention.head_count", I32, -8),

@@ -2,7 +2,7 @@
 
 Run in a container where lawnak/FastGGUF is mounted at /root/reference:
 
-    make -C oracle ref && python tests/golden/make_golden.py [attn | lowbit]
+    make -C oracle ref && python tests/golden/make_golden.py [attn | lowbit | float]
 
 It loads oracle/_ref/libfgref_vnni.so (fastgguf.c compiled from where it lies, AVX-512-VNNI
 build; ref_harness.c exports its static kernels) and records inputs and outputs only: weight
@@ -167,11 +167,37 @@ def lowbit_cases(ref) -> dict:
     return out
 
 
+def float_cases(ref) -> dict:
+    """F32 / F16 / BF16 rows on fp32 activations (dot_row 2207-2214: dot_f32v 1618, dot_f16_row 1645,
+    the BF16 loop 2209): matvec on N(0, 0.02) rows and on random finite bit patterns, at widths
+    with and without a tail (the 16-, 8- and 1-value steps of each kernel), and matmul at 3 and 9
+    tokens (no GEMM for these types: dot_row per token, 3033-3093)."""
+    out = {}
+    for name, t in (("f32", S.T_F32), ("f16", S.T_F16), ("bf16", S.T_BF16)):
+        for cols in (3, 8, 100, 776, 1024):
+            for gname, gen in (("synth", S.weights), ("bytes", S.random_bytes_weights)):
+                w = gen(t, 12, cols, 800 + 3 * t + cols)
+                xv = S.activations(cols, 810 + t + cols) * np.float32(2.5)
+                out[f"{name}_{gname}_{cols}_w"] = w
+                out[f"{name}_{gname}_{cols}_x"] = xv
+                out[f"{name}_{gname}_{cols}_y"] = ref.matvec(t, w, cols, xv)
+        w = S.weights(t, 20, 264, 820 + t)
+        out[f"{name}_mm_w"] = w
+        for nb in (3, 9):
+            X = S.activations(264, 830 + nb, rows=nb)
+            out[f"{name}_mm_X{nb}"] = X
+            out[f"{name}_mm_Y{nb}"] = ref.matmul(t, w, 264, X)
+    return out
+
+
 def main() -> None:
     ref = Reference("vnni")
     print("reference build:", ref.build, "threads:", ref.threads())
     if sys.argv[1:] == ["attn"]:  # only the attention vectors
         np.savez_compressed(os.path.join(HERE, "attn.npz"), **attn_cases(ref))
+        return
+    if sys.argv[1:] == ["float"]:  # only the F32 / F16 / BF16 vectors
+        np.savez_compressed(os.path.join(HERE, "float.npz"), **float_cases(ref))
         return
     if sys.argv[1:] == ["lowbit"]:  # only the Q2_K / Q3_K / IQ4_XS vectors
         np.savez_compressed(os.path.join(HERE, "lowbit.npz"), **lowbit_cases(ref))

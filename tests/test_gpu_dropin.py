@@ -68,12 +68,13 @@ def test_patched_console_program_reports_the_device():
 
 
 @pytest.mark.parametrize("type_", [S.T_Q4_K, S.T_Q4_0, S.T_Q6_K, S.T_Q8_0, S.T_Q5_K, S.T_Q5_0, S.T_Q4_1, S.T_Q5_1,
-                                   S.T_IQ4_NL, S.T_Q2_K, S.T_Q3_K, S.T_IQ4_XS])
+                                   S.T_IQ4_NL, S.T_Q2_K, S.T_Q3_K, S.T_IQ4_XS, S.T_F32, S.T_F16, S.T_BF16])
 def test_matvec_call_site(pair, type_):
     """matvec (2575): the tensor uploaded by gpu_upload_tensor runs on the device in the order the
     CPU path would have used (Q4_K / Q4_0 repacked, as model_load does), bit for bit. Q2_K, Q3_K
     and IQ4_XS, which the reference's own GPU path leaves on the CPU (gpu_kernel_for 1744-1751),
-    are offloaded too."""
+    are offloaded too; F32, F16 and BF16 run there in both (1745), here with the CPU kernels'
+    bits."""
     hip, cpu = pair
     rows, cols = 2048, 4096
     w = S.weights(type_, rows, cols, 100 + type_)
@@ -119,12 +120,12 @@ def test_matvec_multi_call_site(pair):
         assert bits_equal(a, b)
 
 
-@pytest.mark.parametrize("type_", [S.T_Q4_K, S.T_Q6_K, S.T_Q8_0, S.T_Q4_0, S.T_Q3_K])
+@pytest.mark.parametrize("type_", [S.T_Q4_K, S.T_Q6_K, S.T_Q8_0, S.T_Q4_0, S.T_Q3_K, S.T_F16])
 @pytest.mark.parametrize("nb", [4, 64])
 def test_matmul_call_site(pair, type_, nb):
     """matmul (3004): under 8 tokens the reference runs matvec per token (bit-exact); at 64 the
     device's prompt GEMM replaces gemm_kquant / gemm_q32 (Q4_0: bit-exact with gemm_q32's order);
-    Q3_K has no GEMM: the row kernel per token on both sides, bit-exact at every batch."""
+    Q3_K and F16 have no GEMM: the row kernel per token on both sides, bit-exact at every batch."""
     hip, cpu = pair
     rows, cols = 1024, 4096
     w = S.weights(type_, rows, cols, 500 + type_)
@@ -132,7 +133,7 @@ def test_matmul_call_site(pair, type_, nb):
     print(f"matmul {S.TYPE_NAME[type_]} nb={nb}", flush=True)
     Y = hip.matmul(type_, w, cols, X, True)
     Yref = cpu.matmul(type_, w, cols, X, type_ in REPACKS)
-    if nb < 8 or type_ in (S.T_Q4_0, S.T_Q3_K):
+    if nb < 8 or type_ in (S.T_Q4_0, S.T_Q3_K, S.T_F16):
         assert bits_equal(Y, Yref)
     else:
         for t in range(nb):

@@ -196,7 +196,10 @@ def test_upload_refusals(backend):
         backend.upload(S.T_Q4_K, 300, np.zeros(8 * 144 * 2, np.uint8), rows=8)  # cols % 256 != 0
     assert e.value.status == SKIP_TYPE
     with pytest.raises(BackendError) as e:
-        backend.upload(1, 256, np.zeros(8 * 512, np.uint8), rows=8)  # F16: not on this path
+        backend.upload(15, 256, np.zeros(8 * 292, np.uint8), rows=8)  # Q8_K: not a weight type here
+    assert e.value.status == SKIP_TYPE
+    with pytest.raises(BackendError) as e:  # F32 / F16 / BF16 past 40960 values: x past 160 KiB of LDS
+        backend.upload(S.T_F16, 40961, np.zeros(8 * 40961 * 2, np.uint8), rows=8)
     assert e.value.status == SKIP_TYPE
     with pytest.raises(BackendError) as e:  # Q2_K needs cols % 256 == 0
         backend.upload(S.T_Q2_K, 288, np.zeros(8 * 84, np.uint8), rows=8)
@@ -226,7 +229,7 @@ def test_upload_refusals(backend):
         backend.upload(S.T_Q5_0, 48, np.zeros(8 * 22, np.uint8), rows=8)
     assert e.value.status == SKIP_TYPE
     info1 = backend.info()
-    assert info1["n_skip_type"] == info0["n_skip_type"] + 11
+    assert info1["n_skip_type"] == info0["n_skip_type"] + 12
     from fastgguf_amd.backend import Backend
     small = Backend(0, budget_bytes=1 << 20)
     with pytest.raises(BackendError) as e:

@@ -23,6 +23,7 @@ TYPES = {"q8_0": S.T_Q8_0, "q4_k": S.T_Q4_K, "q6_k": S.T_Q6_K, "q5_0": S.T_Q5_0,
          "q4_0": S.T_Q4_0, "q4_1": S.T_Q4_1, "q5_1": S.T_Q5_1, "iq4_nl": S.T_IQ4_NL}
 ALL = list(TYPES.values())
 LOWBIT = {"q2_k": S.T_Q2_K, "q3_k": S.T_Q3_K, "iq4_xs": S.T_IQ4_XS}
+FLOAT = {"f32": S.T_F32, "f16": S.T_F16, "bf16": S.T_BF16}
 REPACKABLE = (S.T_Q4_K, S.T_Q4_0)  # the types the reference repacks (repack_tensor, fastgguf.c:2486)
 
 
@@ -276,7 +277,8 @@ MUTANTS = {1: "hsum8 order", 2: "MoE accumulate without fma", 3: "reciprocal ins
            12: "TurboQuant key dot without the contraction", 13: "TurboQuant scale from an fma chain",
            14: "per-row attention score tail without the contraction",
            15: "Q2_K chain without gcc's contractions", 16: "Q3_K hmask bit of the other half",
-           17: "IQ4_XS high scale bits at the wrong shift"}
+           17: "IQ4_XS high scale bits at the wrong shift", 18: "F16 row in dot_f32v's two accumulators",
+           19: "BF16 chain without the contraction"}
 
 
 @pytest.fixture(scope="module")
@@ -319,6 +321,12 @@ def _golden_failures(o: Oracle) -> int:
         for gen in ("synth", "bytes"):
             x = g[f"{name}_{gen}_x"]
             fails += not bits_equal(o.matvec(t, g[f"{name}_{gen}_w"], x.size, x), g[f"{name}_{gen}_y"])
+    g = golden("float.npz")
+    for name, t in FLOAT.items():
+        for gen in ("synth", "bytes"):
+            for cols in (3, 100, 1024):
+                x = g[f"{name}_{gen}_{cols}_x"]
+                fails += not bits_equal(o.matvec(t, g[f"{name}_{gen}_{cols}_w"], cols, x), g[f"{name}_{gen}_{cols}_y"])
     return fails
 
 
