@@ -1423,9 +1423,12 @@ int fgh_fp16_to_f32(fgh_ctx *c, const uint16_t *h, int n, float *out) {
 // Every weight type goes through upload and matvec (Q4_K in both orders, and the prompt GEMM)
 // on cases whose results are exact integers in fp32 whatever the order of the sums: x = 127
 // everywhere (quantized to d = 1, q = 127 exactly), unit fp16 scales, and row r of a 16 x 512
-// tensor holding one code c = 1 + r % 15 in every element. Then y_r = 65024 (v - m): v the
-// element value (Q8_0, Q5_0, Q6_K: c; Q4_K: c; Q5_K: c + 16) and m the min term (1 for Q4_K and
-// Q5_K, whose mins are 1). Rows differ, so a row or tile mix-up shows as well as a dead kernel.
+// tensor holding one code c = 1 + r % 15 (Q2_K: 1 + r % 3) in every element. Then
+// y_r = 65024 (v - m): v the element value (Q8_0, Q5_0, Q4_1, Q6_K, Q4_K, Q2_K, F16: c; Q5_K:
+// c + 16) and m the min term (1 for Q4_K and Q5_K, whose mins are 1). Rows differ, so a row or
+// tile mix-up shows as well as a dead kernel. One type per kernel family: the 8-row-tile kernel
+// (Q8_0, Q5_0, Q4_1's min chain, Q6_K), the Q4_K / Q5_K kernel in both orders and the prompt
+// GEMM, the low-bit kernel (Q2_K) and the float kernel (F16).
 static void selfcheck_block(uint32_t type, int c, uint8_t *p) {
     const uint8_t nib2 = (uint8_t)(c | c << 4);
     const uint16_t one = 0x3C00;  // fp16 1.0
@@ -1445,6 +1448,24 @@ static void selfcheck_block(uint32_t type, int c, uint8_t *p) {
         memset(p + 192, 1, 16);
         memcpy(p + 208, &one, 2);
         break;
+    case FGH_T_Q4_1:  // d = 1, m = 0, nibble c
+        memcpy(p, &one, 2);
+        memset(p + 2, 0, 2);
+        memset(p + 4, nib2, 16);
+        break;
+    case FGH_T_Q2_K: {  // 16 scale bytes: scale 1, min 0; every 2-bit value c (c <= 3); d = 1, dmin = 0
+        memset(p, 1, 16);
+        memset(p + 16, c * 0x55, 64);
+        memcpy(p + 80, &one, 2);
+        memset(p + 82, 0, 2);
+        break;
+    }
+    case FGH_T_F16: {  // one value: c
+        const uint16_t h = (uint16_t)(0x3C00 + ((31 - __builtin_clz((unsigned)c)) << 10) +
+                                      ((c << (10 - (31 - __builtin_clz((unsigned)c)))) & 0x3FF));
+        memcpy(p, &h, 2);
+        break;
+    }
     default: {  // Q4_K / Q5_K: d = dmin = 1, the 8 scales and 8 mins all 1
         memcpy(p, &one, 2);
         memcpy(p + 2, &one, 2);
@@ -1462,10 +1483,12 @@ static void selfcheck_block(uint32_t type, int c, uint8_t *p) {
 
 static int selfcheck(fgh_ctx *c) {
     const int cols = 512, rows = 16, ntok = 8;
-    const struct { uint32_t type; int order, be, bb, v16, m; } cases[] = {
-        {FGH_T_Q8_0, FGH_ORDER_ROW, 32, 34, 0, 0},        {FGH_T_Q5_0, FGH_ORDER_ROW, 32, 22, 0, 0},
-        {FGH_T_Q4_K, FGH_ORDER_ROW, 256, 144, 0, 1},      {FGH_T_Q4_K, FGH_ORDER_REPACKED, 256, 144, 0, 1},
-        {FGH_T_Q5_K, FGH_ORDER_ROW, 256, 176, 16, 1},     {FGH_T_Q6_K, FGH_ORDER_ROW, 256, 210, 0, 0},
+    const struct { uint32_t type; int order, be, bb, v16, m, mod; } cases[] = {
+        {FGH_T_Q8_0, FGH_ORDER_ROW, 32, 34, 0, 0, 15},    {FGH_T_Q5_0, FGH_ORDER_ROW, 32, 22, 0, 0, 15},
+        {FGH_T_Q4_K, FGH_ORDER_ROW, 256, 144, 0, 1, 15},  {FGH_T_Q4_K, FGH_ORDER_REPACKED, 256, 144, 0, 1, 15},
+        {FGH_T_Q5_K, FGH_ORDER_ROW, 256, 176, 16, 1, 15}, {FGH_T_Q6_K, FGH_ORDER_ROW, 256, 210, 0, 0, 15},
+        {FGH_T_Q4_1, FGH_ORDER_ROW, 32, 20, 0, 0, 15},    {FGH_T_Q2_K, FGH_ORDER_ROW, 256, 84, 0, 0, 3},
+        {FGH_T_F16, FGH_ORDER_ROW, 1, 2, 0, 0, 15},
     };
     std::vector<float> x((size_t)ntok * cols, 127.0f), y((size_t)ntok * rows);
     int rc = FGH_OK;
@@ -1473,7 +1496,7 @@ static int selfcheck(fgh_ctx *c) {
         const int nb = cols / k.be;
         std::vector<uint8_t> w((size_t)rows * nb * k.bb);
         for (int r = 0; r < rows; r++)
-            for (int b = 0; b < nb; b++) selfcheck_block(k.type, 1 + r % 15, w.data() + ((size_t)r * nb + b) * k.bb);
+            for (int b = 0; b < nb; b++) selfcheck_block(k.type, 1 + r % k.mod, w.data() + ((size_t)r * nb + b) * k.bb);
         fgh_tensor *t = nullptr;
         if ((rc = fgh_upload(c, k.type, cols, rows, 1, k.order, w.data(), w.size(), &t)) != FGH_OK) break;
         // one token through matvec; for Q4_K also 8 tokens through matmul (the prompt GEMM)
@@ -1482,7 +1505,7 @@ static int selfcheck(fgh_ctx *c) {
         fgh_tensor_free(t);
         if (rc != FGH_OK) break;
         for (int i = 0; i < nt * rows && rc == FGH_OK; i++) {
-            const float want = 65024.0f * (float)(1 + (i % rows) % 15 + k.v16 - k.m);
+            const float want = 65024.0f * (float)(1 + (i % rows) % k.mod + k.v16 - k.m);
             if (y[(size_t)i] != want) {
                 fprintf(stderr, "[fastgguf_hip] self-check type %u order %d row %d: %g, want %g\n", k.type, k.order,
                         i % rows, (double)y[(size_t)i], (double)want);

@@ -98,8 +98,9 @@ typedef struct {
 /* ---- context: replaces fg_gpu_init / fg_gpu_init_ex (fastgguf.c:1968-2057) ----
  * device < 0 picks device 0 (the reference's FASTGGUF_GPU_DEVICE default is the largest discrete
  * GPU; on a one-GPU MI355X box that is device 0). budget_bytes == 0 means 87.5 % of device memory
- * (fastgguf.c:2045). Runs a self-check (the role of gpu_selfcheck, 1898-1965): every weight type
- * through upload and matvec (Q4_K in both orders and through the prompt GEMM) on small cases
+ * (fastgguf.c:2045). Runs a self-check (the role of gpu_selfcheck, 1898-1965): a weight type of
+ * every kernel family through upload and matvec (Q4_K in both orders and through the prompt
+ * GEMM) on small cases
  * whose outputs are exact integers in closed form; on any failure it prints the case to stderr,
  * returns < 0 with *out = NULL, and the caller stays on the CPU. */
 FGH_API int fgh_open(int device, uint64_t budget_bytes, fgh_ctx **out);
