@@ -26,10 +26,11 @@
 // products pair up whatever order the hardware uses inside one K step.
 //
 // Workgroup: 4 tiles (64 rows) x KH K-halves, one wavefront each (KH = 2: two per SIMD). Block b
-// is walked by K-half b % KH. Each step the workgroup loads the next step's activation records
-// (launch_gemm_quant's layout, 1 KB contiguous per wavefront load) into registers while it
-// computes, and writes them to the other of two LDS stages before the step's barrier; each
-// wavefront keeps a ring of 4 blocks of its weights in registers (three steps ahead).
+// is walked by K-half b % KH. Each step the workgroup loads the activation records of the step
+// three ahead (launch_gemm_quant's layout, 1 KB contiguous per wavefront load) straight into one
+// of four LDS stages (buffer loads to LDS) while it computes, and each wavefront keeps a ring of
+// 4 blocks of its weights in registers (three steps ahead). A step's barrier waits only for the
+// records of the next step, not for the weights loaded after them.
 //
 // Short output (fewer row groups than compute units): grid.y = ks K splits of consecutive blocks
 // (gemm_splits); each split's workgroup writes its partial and the last of a row group's splits to
@@ -128,7 +129,9 @@ hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp,
 // ---------------------------------------------------------------------------------------------
 // The GEMM kernel
 // ---------------------------------------------------------------------------------------------
-constexpr int GEMM_NBUF = 2;  // LDS stages: the step computed and the next one being written
+// LDS stages of activation records: the step computed, and the next three steps' loads landing
+constexpr int GEMM_NST = 4;
+typedef __attribute__((address_space(3))) void *LdsPtr;
 
 // one lane's weights of one block: slots 0 and 1 of its chunk and its row's meta (rb_load's loads)
 struct GW {
@@ -141,11 +144,6 @@ __device__ __forceinline__ void gw_load(const uint8_t *blk, int L, int n, GW &w)
     w.m = bld16(r, 16 * n);
 }
 
-// one step's activation records held by a thread between their load and their LDS write (named
-// registers, not an array: an array is kept in scratch memory); up to 10 rounds of 16 bytes
-struct ARec {
-    uint4 v0, v1, v2, v3, v4, v5, v6, v7, v8, v9;
-};
 
 // the integer results of one block of a wavefront
 template <int NT>
@@ -167,9 +165,15 @@ __device__ __forceinline__ v4i u4v(uint4 u) { return v4i{(int)u.x, (int)u.y, (in
 // the MFMA results without moves).
 template <int NT, int KH, int TPW, bool DUMP>
 __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4k_gemm_kernel(GemmArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
     constexpr int Tp = 16 * NT, REC = gemm_rec_bytes(Tp), NTH = 64 * TPW * KH;
     constexpr int R = (KH * REC + 16 * NTH - 1) / (16 * NTH), SB = R * 16 * NTH;
+    static_assert(GEMM_NST * SB <= 163840, "the record stages fit the workgroup's 160 KiB of LDS");
+    // four separate arrays, so that the compiler sees a stage's LDS reads never meet the loads
+    // landing in the other stages (one array would make it wait for them before every read)
+    __shared__ __align__(16) uint8_t sa0[SB];
+    __shared__ __align__(16) uint8_t sa1[SB];
+    __shared__ __align__(16) uint8_t sa2[SB];
+    __shared__ __align__(16) uint8_t sa3[SB];
     const int tid = threadIdx.x, l = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tw = wave % TPW, kh = wave / TPW;
@@ -186,37 +190,29 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     const uint8_t *W0 = a.W + ((size_t)mi * nb * a.gpm + (size_t)ti) * 2304;
 
     // the step's records: a linear copy of KH records from block b_lo + KH s (the quantizer's
-    // buffer holds a record of slack past the last block); round k of thread t copies unit k * NTH + t,
-    // so each wavefront load reads 1 KB contiguous and each LDS write is conflict-free
+    // buffer holds a record of slack past the last block), loaded straight into a stage of LDS
+    // (buffer loads to LDS: no registers, no LDS writes of their own): round k of thread t
+    // copies unit k * NTH + t, so each wavefront load reads 1 KB contiguous and writes 1 KB
+    // contiguous at 16 bytes per lane; reads past the step's KH records return 0
     static_assert(R >= 1 && R <= 10, "one step's records take 1..10 rounds per thread");
-    auto aload = [&](int s, ARec &ar) {
-        // the base moves in scalar registers; reads past the step's KH records return 0
+    auto adma = [&](int s, uint8_t *st) {
         const int s2 = b_lo + KH * min(s, nsteps - 1), avail = min(KH, nb + 1 - s2);  // >= 2 records
         const BufRes src = buf_res(a.act + (size_t)s2 * REC, avail * REC);
-        auto ld = [&](int k) { return bld16(src, 16 * (k * NTH + tid)); };
-        ar.v0 = ld(0);
-        if (R > 1) ar.v1 = ld(1);
-        if (R > 2) ar.v2 = ld(2);
-        if (R > 3) ar.v3 = ld(3);
-        if (R > 4) ar.v4 = ld(4);
-        if (R > 5) ar.v5 = ld(5);
-        if (R > 6) ar.v6 = ld(6);
-        if (R > 7) ar.v7 = ld(7);
-        if (R > 8) ar.v8 = ld(8);
-        if (R > 9) ar.v9 = ld(9);
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (LdsPtr)(st + (size_t)(k * NTH + 64 * wave) * 16), 16,
+                                                     16 * (k * NTH + tid), 0, 0, 0);
     };
-    auto astore = [&](uint8_t *st, const ARec &ar) {
-        uint4 *dst = (uint4 *)st + tid;
-        dst[0] = ar.v0;
-        if (R > 1) dst[NTH] = ar.v1;
-        if (R > 2) dst[2 * NTH] = ar.v2;
-        if (R > 3) dst[3 * NTH] = ar.v3;
-        if (R > 4) dst[4 * NTH] = ar.v4;
-        if (R > 5) dst[5 * NTH] = ar.v5;
-        if (R > 6) dst[6 * NTH] = ar.v6;
-        if (R > 7) dst[7 * NTH] = ar.v7;
-        if (R > 8) dst[8 * NTH] = ar.v8;
-        if (R > 9) dst[9 * NTH] = ar.v9;
+    // the end of a step: this wavefront's own loads into the next step's stage have landed (the
+    // loads issued after them, at most GEMM_AFTER, may still be in flight) and its LDS reads are
+    // done; then the workgroup's barrier. No fence: a workgroup fence would wait for every load
+    // in flight, the ring's weights and the later stages' records included.
+    auto stage_barrier = [&]() {
+        constexpr int N = 9 + 2 * R;  // weights, records, weights, records, weights (3 + R + 3 + R + 3)
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // vmcnt(N) expcnt(7) lgkmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
     };
     auto wload = [&](int s, GW &w) {
 gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
@@ -320,31 +316,34 @@ gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
         }
     };
 
-    // prologue: step 0's records in LDS, the weights of steps 0..2 in flight
+    // prologue: the records of steps 0..2 into stages 0..2 and the weights of steps 0..2, each
+    // step's records then weights (the order the steps keep); step 0's records landed
     GW w0, w1, w2, w3;
-    ARec rr;
     GAcc<NT> g;
-    uint8_t *st0 = smem, *st1 = smem + SB;
-    aload(0, rr);
+    uint8_t *const st0 = sa0, *const st1 = sa1, *const st2 = sa2, *const st3 = sa3;
     __builtin_amdgcn_sched_barrier(0);
+    adma(0, st0);
     wload(0, w0);
+    adma(1, st1);
     wload(1, w1);
+    adma(2, st2);
     wload(2, w2);
-    __builtin_amdgcn_sched_barrier(0);
-    astore(st0, rr);
-    __syncthreads();
-    // step s: compute step s from its stage and weights; between its K-steps load step s + 1's
-    // records (after K-step 0) and step s + 3's weights (after K-step 2, into the ring slot step
-    // s - 1 used); then the epilogue, the records to the other stage, barrier. Issued at the top
-    // of the step instead, the workgroup's loads fill the address queue and every wavefront waits
-    // to issue them before computing. The main loop's steps have a block for every K-half and no
-    // branch, so the compiler's load counters stay exact across them (a branch makes it wait for
-    // every outstanding load, the prefetches included, at the next block); the last steps test.
-    auto step = [&](auto full, int s, GW &wc, GW &wn3, const uint8_t *stc, uint8_t *stn) {
+    stage_barrier();
+    // step s: compute step s from its stage and weights; between its K-steps load step s + 3's
+    // records (after K-step 0, into the stage step s - 1 used, free since the last barrier) and
+    // step s + 3's weights (after K-step 2, into the ring slot step s - 1 used); then the
+    // epilogue and the barrier, once step s + 1's records have landed. Every step issues the
+    // same loads (the last ones re-read the last step's), so the count the barrier waits for is
+    // the same at every step. Issued at the top of the step instead, the workgroup's loads fill
+    // the address queue and every wavefront waits to issue them before computing. The main
+    // loop's steps have a block for every K-half and no branch, so the compiler's load counters
+    // stay exact across them (a branch makes it wait for every outstanding load, the prefetches
+    // included, at the next block); the last steps test.
+    auto step = [&](auto full, int s, GW &wc, GW &wn3, const uint8_t *stc, uint8_t *st3n) {
         const int b = b_lo + KH * s + kh;
         auto issue = [&](int i) {
             __builtin_amdgcn_sched_barrier(0);
-            if (i == 0) aload(s + 1, rr);
+            if (i == 0) adma(s + 3, st3n);
             if (i == 2) wload(s + 3, wn3);
             __builtin_amdgcn_sched_barrier(0);
         };
@@ -355,28 +354,31 @@ gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
             issue(0);
             issue(2);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        astore(stn, rr);
-        __syncthreads();
+        stage_barrier();
     };
     using Full = std::true_type;
     using Edge = std::false_type;
     const int nfull = nbk / KH;  // steps with a block for every K-half
     int s = 0;
     for (; s + 4 <= nfull; s += 4) {
-        step(Full(), s, w0, w3, st0, st1);
+        step(Full(), s, w0, w3, st0, st3);
         step(Full(), s + 1, w1, w0, st1, st0);
-        step(Full(), s + 2, w2, w1, st0, st1);
-        step(Full(), s + 3, w3, w2, st1, st0);
+        step(Full(), s + 2, w2, w1, st2, st1);
+        step(Full(), s + 3, w3, w2, st3, st2);
     }
-    // the remaining steps (at most 4), with the same rings and stage parities
-    if (s < nsteps) step(Edge(), s, w0, w3, st0, st1);
+    // the remaining steps (at most 4), with the same rings and stages
+    if (s < nsteps) step(Edge(), s, w0, w3, st0, st3);
     if (s + 1 < nsteps) step(Edge(), s + 1, w1, w0, st1, st0);
-    if (s + 2 < nsteps) step(Edge(), s + 2, w2, w1, st0, st1);
-    if (s + 3 < nsteps) step(Edge(), s + 3, w3, w2, st1, st0);
-    __syncthreads();  // every wavefront is past its reads of the stages (the reduction reuses them)
+    if (s + 2 < nsteps) step(Edge(), s + 2, w2, w1, st2, st1);
+    if (s + 3 < nsteps) step(Edge(), s + 3, w3, w2, st3, st2);
+    // every load has landed (the last steps' loads into stages past the last step included) and
+    // every wavefront is past its reads of the stages: the reduction reuses them
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     if (KH == 2) {  // half 1 -> LDS, half 0 adds it in order
-        float *red = (float *)smem + (size_t)tw * 64 * 4 * NT;  // TPW * 4 KB * NT <= one stage
+        // tiles 0, 1 in stage 0, tiles 2, 3 in stage 1: 2 x 4 KB x NT <= one stage
+        static_assert(KH == 1 || (TPW <= 4 && 2 * 4096 * NT <= SB), "the reduction fits two stages");
+        float *red = (float *)(tw < 2 ? st0 : st1) + (size_t)(tw & 1) * 64 * 4 * NT;
         if (kh == 1) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) *(v4f *)(red + (size_t)(t * 64 + l) * 4) = acc[t];
@@ -387,12 +389,11 @@ gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
             for (int t = 0; t < NT; ++t) acc[t] += *(const v4f *)(red + (size_t)(t * 64 + l) * 4);
         }
     }
-    // a K split (at least 8 blocks, so KH = 2) puts its flag at LDS int 4096, inside the stages
-    static_assert(KH == 1 || 2 * SB >= 4 * 4096 + 4, "the K split's flag lies inside the stages");
+    // a K split (at least 8 blocks, so KH = 2) puts its flag in stage 2 (the reduction used 0, 1)
     if (a.ks > 1) {  // the K split's partials (the reduction's LDS area is done with)
         gemm_split_finish<4 * NT>([&](int e) { return 16 * (e >> 2) + 4 * kg + (e & 3); },
                                   [&](int e) { return acc[e >> 2][e & 3]; }, kh == 0, store, tid, tw, TPW, orow, a.ks,
-                                  ksi, a.T, a.ldy, a.part, a.cnt, a.Y, (int *)smem + 4096);
+                                  ksi, a.T, a.ldy, a.part, a.cnt, a.Y, (int *)st2);
         return;
     }
     if (kh == 0 && store) {
@@ -408,21 +409,15 @@ gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
 
 static int gemm_kh(int nb) { return nb >= 2 ? 2 : 1; }  // wavefronts per tile (K-halves)
 constexpr int GEMM_TPW = 4;                              // tiles per workgroup
-template <int NT, int KH>
-static size_t gemm_lds(int TPW) {
-    const int nth = 64 * TPW * KH, r = (KH * gemm_rec_bytes(16 * NT) + 16 * nth - 1) / (16 * nth);
-    return (size_t)GEMM_NBUF * r * 16 * nth;
-}
-
 size_t gemm_act_bytes(int nb, int Tp) { return (size_t)(nb + 1) * gemm_rec_bytes(Tp); }
 
 template <int NT, int KH>
 static void gemm_launch(const GemmArgs &a, hipStream_t s) {
     constexpr int TPW = GEMM_TPW;
     const dim3 grid((unsigned)((a.groups + TPW - 1) / TPW), (unsigned)a.ks);
-    const size_t lds = gemm_lds<NT, KH>(TPW);
-    if (a.dump_s) q4k_gemm_kernel<NT, KH, TPW, true><<<grid, 64 * TPW * KH, lds, s>>>(a);
-    else q4k_gemm_kernel<NT, KH, TPW, false><<<grid, 64 * TPW * KH, lds, s>>>(a);
+    // the record stages are the kernel's static LDS
+    if (a.dump_s) q4k_gemm_kernel<NT, KH, TPW, true><<<grid, 64 * TPW * KH, 0, s>>>(a);
+    else q4k_gemm_kernel<NT, KH, TPW, false><<<grid, 64 * TPW * KH, 0, s>>>(a);
 }
 template <int NT>
 static void gemm_launch_kh(const GemmArgs &a, hipStream_t s) {
