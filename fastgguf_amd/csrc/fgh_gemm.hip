@@ -129,9 +129,7 @@ hipError_t launch_gemm_quant(const float *x, int64_t ldx, int nb, int T, int Tp,
 // ---------------------------------------------------------------------------------------------
 // The GEMM kernel
 // ---------------------------------------------------------------------------------------------
-// LDS stages of activation records: the step computed, and the next three steps' loads landing
-constexpr int GEMM_NST = 4;
-typedef __attribute__((address_space(3))) void *LdsPtr;
+
 
 // one lane's weights of one block: slots 0 and 1 of its chunk and its row's meta (rb_load's loads)
 struct GW {
@@ -190,30 +188,15 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
     const uint8_t *W0 = a.W + ((size_t)mi * nb * a.gpm + (size_t)ti) * 2304;
 
     // the step's records: a linear copy of KH records from block b_lo + KH s (the quantizer's
-    // buffer holds a record of slack past the last block), loaded straight into a stage of LDS
-    // (buffer loads to LDS: no registers, no LDS writes of their own): round k of thread t
-    // copies unit k * NTH + t, so each wavefront load reads 1 KB contiguous and writes 1 KB
-    // contiguous at 16 bytes per lane; reads past the step's KH records return 0
+    // buffer holds a record of slack past the last block) into a stage (gemm_dma)
     static_assert(R >= 1 && R <= 10, "one step's records take 1..10 rounds per thread");
     auto adma = [&](int s, uint8_t *st) {
         const int s2 = b_lo + KH * min(s, nsteps - 1), avail = min(KH, nb + 1 - s2);  // >= 2 records
-        const BufRes src = buf_res(a.act + (size_t)s2 * REC, avail * REC);
-#pragma unroll
-        for (int k = 0; k < R; ++k)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (LdsPtr)(st + (size_t)(k * NTH + 64 * wave) * 16), 16,
-                                                     16 * (k * NTH + tid), 0, 0, 0);
+        gemm_dma<R, NTH>(buf_res(a.act + (size_t)s2 * REC, avail * REC), st, wave, tid);
     };
-    // the end of a step: this wavefront's own loads into the next step's stage have landed (the
-    // loads issued after them, at most GEMM_AFTER, may still be in flight) and its LDS reads are
-    // done; then the workgroup's barrier. No fence: a workgroup fence would wait for every load
-    // in flight, the ring's weights and the later stages' records included.
-    auto stage_barrier = [&]() {
-        constexpr int N = 9 + 2 * R;  // weights, records, weights, records, weights (3 + R + 3 + R + 3)
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // vmcnt(N) expcnt(7) lgkmcnt(0)
-        asm volatile("s_barrier" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-    };
+    // a step ends once step s + 1's records have landed: the loads issued after them are the
+    // weights of s + 1, the records and weights of s + 2 and of s + 3 (3 + R + 3 + R + 3)
+    auto stage_barrier = [&]() { gemm_stage_barrier<9 + 2 * R>(); };
     auto wload = [&](int s, GW &w) {
 gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
 

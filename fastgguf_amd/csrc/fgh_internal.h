@@ -796,6 +796,31 @@ __device__ __forceinline__ void gemm_split_finish(Tok tok, Val val, bool mine, b
     }
 }
 constexpr size_t GEMM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
+// The prompt GEMMs' activation records go straight from memory into one of GEMM_NST LDS stages
+// (buffer loads to LDS: no registers, no LDS writes of their own), three steps ahead: round k of
+// thread t copies 16-byte unit k * NTH + t of the step's records (each wavefront load reads and
+// writes 1 KB contiguous, 16 bytes per lane); reads past src's range return 0.
+constexpr int GEMM_NST = 4;
+typedef __attribute__((address_space(3))) void *LdsPtr;
+template <int R, int NTH>
+__device__ __forceinline__ void gemm_dma(BufRes src, uint8_t *st, int wave, int tid) {
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (LdsPtr)(st + (size_t)(k * NTH + 64 * wave) * 16), 16,
+                                                 16 * (k * NTH + tid), 0, 0, 0);
+}
+// The end of a GEMM step: this wavefront's loads into the next step's stage have landed (the N
+// loads issued after them may still be in flight) and its LDS reads are done; then the
+// workgroup's barrier. No fence: a workgroup fence would wait for every load in flight, the
+// ring's weights and the later stages' records included.
+template <int N>
+__device__ __forceinline__ void gemm_stage_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // vmcnt(N) expcnt(7) lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
 // true when all wg workgroups of a launch (waves wavefronts and lds bytes each) can be resident
 // on num_cu CUs at once: a split launch whose workgroups need a second round is slower than a
 // smaller split (measured: Q8_0 4096 x 14336 with 4-way splits in two rounds 26 us, 2-way 18 us)
