@@ -40,11 +40,11 @@ def run_both(be, t, X):
 # one first, so the second call reuses the array with a smaller input; the third runs the decode
 # kernels, which need no scratch; then the Q6_K GEMM with a 4-way K split (4096 output rows: 64
 # row groups) and without, the Q8_0 GEMM with a K split and without (smaller), and the nibble-type
-# GEMM (Q5_1, then Q4_0 smaller)
+# GEMM (Q5_1, then Q4_0 smaller); last an F16 tensor, whose per-token decode kernel needs no scratch
 CALLS = [(S.T_Q4_K, 1024, 8192, 64), (S.T_Q4_K, 272, 2048, 9), (S.T_Q4_K, 128, 2048, 5),
          (S.T_Q6_K, 4096, 14336, 64), (S.T_Q6_K, 96, 1024, 12),
          (S.T_Q8_0, 4096, 14336, 64), (S.T_Q8_0, 512, 2048, 16),
-         (S.T_Q5_1, 200, 4096, 40), (S.T_Q4_0, 64, 1024, 8)]
+         (S.T_Q5_1, 200, 4096, 40), (S.T_Q4_0, 64, 1024, 8), (S.T_F16, 300, 1000, 24)]
 
 
 @pytest.mark.parametrize("fresh", [True, False], ids=["fresh_context", "shared_context"])
