@@ -54,6 +54,19 @@ def test_matvec_matches_oracle(backend, oracle, t, rows, cols):
     tt.free()
 
 
+@pytest.mark.parametrize("t", list(LOWBIT.values()))
+def test_widest_row(backend, oracle, t):
+    """204 blocks (K = 52224), the widest row the kernel accepts (its quantized x fills 64 KiB of
+    LDS less 256 bytes); one block more is refused at upload (test_gpu_matvec)."""
+    rows, cols = 40, 204 * 256
+    w = S.random_bytes_weights(t, rows, cols, 80 + t)
+    x = S.activations(cols, 81 + t)
+    print(f"widest {S.TYPE_NAME[t]} {rows}x{cols}", flush=True)
+    tt = backend.upload(t, cols, w)
+    check_vec(backend.matvec(tt, x), oracle.matvec(t, w, cols, x))
+    tt.free()
+
+
 def test_launch_forms_are_all_taken(backend):
     """The shapes above cover 1, 2, 4 and 8 wavefronts per tile (ring depth 4 for whole rows, 2
     for split launches)."""
