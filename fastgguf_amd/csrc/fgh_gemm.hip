@@ -195,8 +195,10 @@ __global__ __launch_bounds__(64 * TPW * KH) __attribute__((amdgpu_waves_per_eu(2
         gemm_dma<R, NTH>(buf_res(a.act + (size_t)s2 * REC, avail * REC), st, wave, tid);
     };
     // a step ends once step s + 1's records have landed: the loads issued after them are the
-    // weights of s + 1, the records and weights of s + 2 and of s + 3 (3 + R + 3 + R + 3)
-    auto stage_barrier = [&]() { gemm_stage_barrier<9 + 2 * R>(); };
+    // weights of s + 1, the records and weights of s + 2 and of s + 3 (3 + R + 3 + R + 3). The
+    // dump form's stores are memory operations of the same counter, issued among them: it waits
+    // for everything.
+    auto stage_barrier = [&]() { gemm_stage_barrier<DUMP ? 0 : 9 + 2 * R>(); };
     auto wload = [&](int s, GW &w) {
 gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
 
@@ -304,12 +306,18 @@ gw_load(W0 + (size_t)(b_lo + min(KH * s + kh, nbk - 1)) * bstride, L, n, w); };
     GW w0, w1, w2, w3;
     GAcc<NT> g;
     uint8_t *const st0 = sa0, *const st1 = sa1, *const st2 = sa2, *const st3 = sa3;
+    // (the scheduling barriers keep the loads in this order: the barrier's count relies on it)
     __builtin_amdgcn_sched_barrier(0);
     adma(0, st0);
+    __builtin_amdgcn_sched_barrier(0);
     wload(0, w0);
+    __builtin_amdgcn_sched_barrier(0);
     adma(1, st1);
+    __builtin_amdgcn_sched_barrier(0);
     wload(1, w1);
+    __builtin_amdgcn_sched_barrier(0);
     adma(2, st2);
+    __builtin_amdgcn_sched_barrier(0);
     wload(2, w2);
     stage_barrier();
     // step s: compute step s from its stage and weights; between its K-steps load step s + 3's
