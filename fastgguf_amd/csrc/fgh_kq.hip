@@ -332,18 +332,32 @@ __global__ __launch_bounds__(64 * TPW * S) void kq_mv_kernel(MvArgs a) {
     if (S > 1) {
         __syncthreads();
         if (ks != 0) return;
-        // the chains over the other wavefronts' steps (the row's 8 pairs of a step: 64 B)
-        for (int st = nsw; st < nst; ++st) {
+        // the chains over the other wavefronts' steps (the row's 8 pairs of a step: 64 B), the
+        // records of 4 steps read before their 32 fmas (one LDS round trip per 4 steps), then
+        // the last steps one at a time
+        auto chain8 = [&](const float4 (&v)[4]) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc = __builtin_fmaf(v[q].x, v[q].y, acc);
+                acc = __builtin_fmaf(v[q].z, v[q].w, acc);
+            }
+        };
+        int st = nsw;
+        for (; st + 4 <= nst; st += 4) {
+            float4 v[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float4 *p = (const float4 *)(rec + (size_t)(st + u - nsw) * KQ_REC + 64 * r);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[u][q] = p[q];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) chain8(v[u]);
+        }
+        for (; st < nst; ++st) {
             const float4 *p = (const float4 *)(rec + (size_t)(st - nsw) * KQ_REC + 64 * r);
-            const float4 v0 = p[0], v1 = p[1], v2 = p[2], v3 = p[3];
-            acc = __builtin_fmaf(v0.x, v0.y, acc);
-            acc = __builtin_fmaf(v0.z, v0.w, acc);
-            acc = __builtin_fmaf(v1.x, v1.y, acc);
-            acc = __builtin_fmaf(v1.z, v1.w, acc);
-            acc = __builtin_fmaf(v2.x, v2.y, acc);
-            acc = __builtin_fmaf(v2.z, v2.w, acc);
-            acc = __builtin_fmaf(v3.x, v3.y, acc);
-            acc = __builtin_fmaf(v3.z, v3.w, acc);
+            const float4 v[4] = {p[0], p[1], p[2], p[3]};
+            chain8(v);
         }
     }
     if (row_ok && j == 0) a.t[ti].y[(size_t)tok * a.ldy + obase + mrow + r] = acc;

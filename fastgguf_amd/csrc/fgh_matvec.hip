@@ -439,9 +439,12 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
     if (S > 1) {
         __syncthreads();
         if (ks != 0) return;
-        // the chains over the other wavefronts' steps, CH steps at a time (all reads first)
+        // the chains over the other wavefronts' steps, CH steps at a time (all reads first).
+        // CHECK: the batch may reach the tile's partial last step or past the tile's end (the
+        // tests are uniform; without them the chain is one fma per block, no select)
         constexpr int CH = q8_kind(TYPE) ? 4 : 8;
-        for (int st0 = nsw; st0 < nst; st0 += CH) {
+        auto batch = [&](int st0, auto check) {
+            constexpr bool CHECK = decltype(check)::value;
             const uint8_t *rs = rec + (size_t)(st0 - nsw) * rec_bytes(TYPE);
             if constexpr (q8_kind(TYPE)) {
                 float4 sv[CH], fv[CH], mv[CH];
@@ -470,7 +473,7 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
                     const float bk[4] = {bv[c].x, bv[c].y, bv[c].z, bv[c].w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (nbs >= 4 || k < nbs) {
+                        if (!CHECK || nbs >= 4 || k < nbs) {
                             acc = __builtin_fmaf(fk[k], sk[k], acc);
                             if (q32_min(TYPE)) cacc = __builtin_fmaf(mk[k], bk[k], cacc);
                         }
@@ -485,12 +488,17 @@ __global__ __launch_bounds__(64 * TPW * S) void mv_kernel(MvArgs a) {
                 }
 #pragma unroll
                 for (int c = 0; c < CH; ++c)
-                    if (st0 + c < nst) {  // uniform
+                    if (!CHECK || st0 + c < nst) {  // uniform
                         acc = __builtin_fmaf(fd[c], sv[c].x, acc);
                         cacc = __builtin_fmaf(fd[c] * 32.0f, sv[c].y, cacc);
                     }
             }
-        }
+        };
+        // batches of whole steps (4 blocks each for the 32-value types), then the rest
+        const int nwhole = q8_kind(TYPE) ? nb / 4 : nst;
+        int st0 = nsw;
+        for (; st0 + CH <= nwhole; st0 += CH) batch(st0, NoCheck());
+        for (; st0 < nst; st0 += CH) batch(st0, Check());
     }
     // hsum8(acc) - hsum4(cacc) over the row's 8 lanes (fastgguf.c:797-806, 1089-1095), in lane i = 0;
     // Q4_1 / Q5_1: hsum8(acc) + macc (973-989, 1020-1031); repacked Q4_0: the row chain itself
