@@ -116,6 +116,26 @@ def test_two_tiles_per_workgroup_split(backend, oracle, fam, rows, cols):
     tt.free()
 
 
+@pytest.mark.parametrize("fam", FAMILIES[3:], ids=family_id)
+@pytest.mark.parametrize("rows,nb32,nb256", [(512, 163, 43), (4096, 451, 57)])
+def test_split_chain_long_tail(backend, oracle, fam, rows, nb32, nb256):
+    """Block splits whose final chain runs many whole batches of records before the tested last
+    batch: rows of 163 / 451 32-value blocks (a last step of 3 blocks) or 43 / 57 256-value
+    blocks, 512 rows and the down projection's 4096, bit for bit against the oracle."""
+    t, order = fam
+    nb = nb32 if block_elems(t) == 32 else nb256
+    tiles, cols = rows // tile_rows(t), nb * block_elems(t)
+    shape = backend.matvec_shape(t, order, cols, tiles)
+    print(f"{S.TYPE_NAME[t]} order {order} {rows}x{cols} shape {shape}", flush=True)
+    assert shape[0] > 1, shape
+    w = S.random_bytes_weights(t, rows, cols, rows + nb + t)
+    x = S.activations(cols, rows + 2)
+    tt = backend.upload(t, cols, w, order=order)
+    o_order = O_RP if order == ORDER_REPACKED else O_ROW
+    assert bits_equal(backend.matvec(tt, x), oracle.matvec(t, w, cols, x, o_order))
+    tt.free()
+
+
 @pytest.mark.parametrize("order", [ORDER_REPACKED, ORDER_ROW], ids=["rp", "row"])
 def test_gate_up_one_launch_at_benchmark_size(backend, oracle, order):
     """The benchmark's dominant launch: gate and up (4096 -> 14336 each, benchmark distributions)
