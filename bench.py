@@ -152,7 +152,9 @@ def kernel_time_on(be, launch, reps: int) -> float:
 
 def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
     """BASELINE configs 1 (Q8_0 4096^2 matvec), 3 (Q6_K LM head 128256 x 4096) and 5 (MoE, 128
-    experts, top-8, hidden 2048, ff 768: batch 1 and 64 tokens), each timed like the kernels above.
+    experts, top-8, hidden 2048, ff 768: batch 1 and 64 tokens), each timed like the kernels above,
+    and the other weight types' decode lines (low-bit and float types at the gate shape, Q4_0 and
+    Q8_0 at the down shape).
     Weight sets rotate where one copy would stay in the Infinity Cache."""
     if not enabled:
         return None
@@ -211,6 +213,26 @@ def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
         out[f"float_{name}_gate_matvec"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
                                              "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes,
                                              "copies": n}
+        for t in ts:
+            t.free()
+        be.dev_free(y)
+    be.dev_free(x)
+    # two 32-value types at the down projection's shape 14336 -> 4096 (Q4_0 in its repacked
+    # order): long rows over few tiles, so the launches split each tile's steps over wavefronts
+    x = be.dev_alloc(4 * 14336)
+    be.h2d(x, S.activations(14336, 150))
+    for name, ty in (("q4_0", S.T_Q4_0), ("q8_0", S.T_Q8_0)):
+        wb = 4096 * S.row_bytes(ty, 14336)
+        n = copies_for(wb)
+        w = S.weights(ty, 4096, 14336, 150 + ty)
+        ts = [be.upload(ty, 14336, w) for _ in range(n)]
+        del w
+        y = be.dev_alloc(4 * 4096)
+        us = kernel_time(lambda i: be.matvec_dev(ts[i % n], x, y), 100)
+        nbytes = wb + 4 * (4096 + 14336)
+        out[f"long_rows_{name}_down_matvec"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                                                 "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+                                                 "copies": n}
         for t in ts:
             t.free()
         be.dev_free(y)
