@@ -189,3 +189,44 @@ def test_gate_up_silu_bit_exact(backend, oracle, case):
     assert bits_equal(gm, g) and bits_equal(um, u)
     for tt in (tg, tu):
         tt.free()
+
+
+def test_split_launches_graph_replays(backend, oracle):
+    """Q4_0 (repacked), Q8_0 and Q2_K matvecs over 4096 x 14336 (block splits with long final
+    chains) captured in one HIP graph: every replay, with eager calls and host synchronizations
+    between the replays and the outputs overwritten before each, gives the oracle's bits."""
+    rows, cols = 4096, 14336
+    cases = [(S.T_Q4_0, ORDER_REPACKED, O_RP), (S.T_Q8_0, ORDER_ROW, O_ROW), (S.T_Q2_K, ORDER_ROW, O_ROW)]
+    ws = [S.random_bytes_weights(t, rows, cols, 80 + i) for i, (t, _, _) in enumerate(cases)]
+    x = S.activations(cols, 81)
+    ts = [backend.upload(t, cols, w, order=o) for (t, o, _), w in zip(cases, ws)]
+    for (t, o, _), tt in zip(cases, ts):
+        assert backend.matvec_shape(t, o, cols, rows // tile_rows(t))[0] > 1
+    want = [oracle.matvec(t, w, cols, x, oo) for (t, _, oo), w in zip(cases, ws)]
+    xd = backend.dev_alloc(4 * cols)
+    yds = [backend.dev_alloc(4 * rows) for _ in cases]
+    backend.h2d(xd, x)
+    for tt, yd in zip(ts, yds):  # eager first
+        backend.matvec_dev(tt, xd, yd)
+    backend.sync()
+    backend.graph_begin()
+    for tt, yd in zip(ts, yds):
+        backend.matvec_dev(tt, xd, yd)
+    g = backend.graph_end()
+    try:
+        for rep in range(3):
+            for yd in yds:
+                backend.h2d(yd, np.full(rows, np.nan, np.float32))
+            backend.graph_launch(g)
+            backend.sync()
+            for (t, _, _), yd, yw in zip(cases, yds, want):
+                y = np.empty(rows, np.float32)
+                backend.d2h(y, yd)
+                assert bits_equal(y, yw), f"{S.TYPE_NAME[t]} replay {rep}"
+            assert bits_equal(backend.matvec(ts[1], x), want[1])  # eager work between replays
+    finally:
+        backend.graph_destroy(g)
+    for p in [xd] + yds:
+        backend.dev_free(p)
+    for tt in ts:
+        tt.free()
