@@ -539,6 +539,8 @@ static hipError_t mv_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s
 }
 template <int TYPE, int ORDER, int TPW, int S>
 static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
+    if constexpr (S == 2 && (TYPE == T_Q8_0 || TYPE == T_IQ4_NL))
+        if (R == 8) return mv_launch<TYPE, ORDER, 8, TPW, S>(a, ntok, lds, s);
     return R == 2 ? mv_launch<TYPE, ORDER, 2, TPW, S>(a, ntok, lds, s) : mv_launch<TYPE, ORDER, 4, TPW, S>(a, ntok, lds, s);
 }
 
@@ -561,7 +563,9 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 // Q6_K (steps of 1680 B, 1.5x the others'): 2 for split launches and for the LM-head size (8192
 // tiles or more over rows shorter than 32 steps), 4 otherwise (measured, graph of back-to-back
 // launches: 14336 x 4096 11.9 -> 11.0 us, 8192 x 2048 6.4 -> 5.8, 4096 x 14336 13.4 -> 13.1;
-// the LM head, QKV and the split shapes unchanged).
+// the LM head, QKV and the split shapes unchanged). Q8_0 and IQ4_NL 2-way splits of rows of 64
+// steps or more take ring depth 8 (4096 x 14336: 16.1 -> 15.6 us and 17.0 -> 16.2 us; the 4-way
+// splits of the other types measured no faster with it).
 template <int TYPE>
 static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
     const int nst = mv_steps(TYPE, nb);
@@ -575,8 +579,9 @@ static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
                all_resident((tiles + mv_tpw(2 * S) - 1) / mv_tpw(2 * S), 2 * S * mv_tpw(2 * S),
                             mv_lds(TYPE, nb, mv_tpw(2 * S), 2 * S), num_cu))
             S *= 2;
-    const int R = TYPE == T_Q6_K ? (S > 1 || (tiles >= 8192 && nst < 32) ? 2 : 4)
-                                 : (nst < 32 && tiles * S >= 1024) || (nst + S - 1) / S <= 2 ? 2 : 4;
+    int R = TYPE == T_Q6_K ? (S > 1 || (tiles >= 8192 && nst < 32) ? 2 : 4)
+                           : (nst < 32 && tiles * S >= 1024) || (nst + S - 1) / S <= 2 ? 2 : 4;
+    if ((TYPE == T_Q8_0 || TYPE == T_IQ4_NL) && S == 2 && (nst + 1) / 2 >= 32) R = 8;
     return MvShape{S, R, mv_tpw(S), mv_lds(TYPE, nb, mv_tpw(S), S)};
 }
 template <int TYPE, int ORDER = 0>
