@@ -539,6 +539,8 @@ static hipError_t mv_launch(const MvArgs &a, int ntok, size_t lds, hipStream_t s
 }
 template <int TYPE, int ORDER, int TPW, int S>
 static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipStream_t s) {
+    if constexpr (S == 1 && TPW == 4 && (TYPE == T_Q4_0 || TYPE == T_IQ4_NL))
+        if (R == 16) return mv_launch<TYPE, ORDER, 16, TPW, S>(a, ntok, lds, s);
     if constexpr ((S == 2 && (TYPE == T_Q8_0 || TYPE == T_IQ4_NL)) || (S == 1 && TYPE != T_Q6_K))
         if (R == 8) return mv_launch<TYPE, ORDER, 8, TPW, S>(a, ntok, lds, s);
     return R == 2 ? mv_launch<TYPE, ORDER, 2, TPW, S>(a, ntok, lds, s) : mv_launch<TYPE, ORDER, 4, TPW, S>(a, ntok, lds, s);
@@ -571,7 +573,8 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 // Q8_0 22.6 / 26.3 / 15.6 -> 17.8 / 20.6 / 14.9 us, Q5_0 24.8 / 28.5 -> 18.0 / 20.1, Q5_1
 // 27.4 / 31.6 / 18.1 -> 21.3 / 24.0 / 14.5, Q4_1 23.7 / 27.6 / 15.8 -> 19.2 / 21.5 / 13.2,
 // IQ4_NL 26.9 / 31.1 / 17.4 -> 23.1 / 26.2 / 15.5, Q4_0 22.2 / 25.5 -> 21.6 / 24.6; Q6_K no
-// change).
+// change); Q4_0 and IQ4_NL (the smallest steps, 576 B) ring depth 16 (IQ4_NL 23.1 / 26.1 / 15.6
+// -> 21.3 / 23.0 / 14.5 us, Q4_0 21.7 / 24.6 -> 20.5 / 22.0; 16 was slower for the others).
 template <int TYPE>
 static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
     const int nst = mv_steps(TYPE, nb);
@@ -588,7 +591,7 @@ static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
     int R = TYPE == T_Q6_K ? (S > 1 || (tiles >= 8192 && nst < 32) ? 2 : 4)
                            : (nst < 32 && tiles * S >= 1024) || (nst + S - 1) / S <= 2 ? 2 : 4;
     if ((TYPE == T_Q8_0 || TYPE == T_IQ4_NL) && S == 2 && (nst + 1) / 2 >= 32) R = 8;
-    if (TYPE != T_Q6_K && S == 1 && tiles <= 1024 && nst >= 64) R = 8;
+    if (TYPE != T_Q6_K && S == 1 && tiles <= 1024 && nst >= 64) R = TYPE == T_Q4_0 || TYPE == T_IQ4_NL ? 16 : 8;
     return MvShape{S, R, mv_tpw(S), mv_lds(TYPE, nb, mv_tpw(S), S)};
 }
 template <int TYPE, int ORDER = 0>
