@@ -568,8 +568,11 @@ static hipError_t mv_launch_r(int R, const MvArgs &a, int ntok, size_t lds, hipS
 // the LM head, QKV and the split shapes unchanged). Q8_0 and IQ4_NL 2-way splits of rows of 64
 // steps or more take ring depth 8 (4096 x 14336: 16.1 -> 15.6 us and 17.0 -> 16.2 us; the 4-way
 // splits of the other types measured no faster with it). Unsplit launches of at most 1024 tiles
-// over rows of 64 steps or more (long rows whose split would not stay resident), every type but
-// Q6_K: ring depth 8 (graph of back-to-back launches, 5120 x 13824 / 6144 x 16384 / 8192 x 8192:
+// over rows of 32 steps or more (rows whose split would not stay resident, or launches past the
+// split limit), every type but Q6_K: ring depth 8 (8192 x 4096 / 6144 x 5120 / 7168 x 7168:
+// Q8_0 9.4 / 10.7 / 14.0 -> 8.8 / 9.1 / 11.9 us, Q4_1 9.5 / 11.2 / 14.3 -> 8.1 / 9.8 / 11.8,
+// Q5_1 10.7 / 12.6 / 16.2 -> 9.1 / 10.5 / 12.9; at 14336 x 4096, 1792 tiles, within 7 % either
+// way, so that keeps depth 4; graph of back-to-back launches, 5120 x 13824 / 6144 x 16384 / 8192 x 8192:
 // Q8_0 22.6 / 26.3 / 15.6 -> 17.8 / 20.6 / 14.9 us, Q5_0 24.8 / 28.5 -> 18.0 / 20.1, Q5_1
 // 27.4 / 31.6 / 18.1 -> 21.3 / 24.0 / 14.5, Q4_1 23.7 / 27.6 / 15.8 -> 19.2 / 21.5 / 13.2,
 // IQ4_NL 26.9 / 31.1 / 17.4 -> 23.1 / 26.2 / 15.5, Q4_0 22.2 / 25.5 -> 21.6 / 24.6; Q6_K no
@@ -591,7 +594,8 @@ static MvShape mv_shape(int64_t tiles, int nb, int num_cu) {
     int R = TYPE == T_Q6_K ? (S > 1 || (tiles >= 8192 && nst < 32) ? 2 : 4)
                            : (nst < 32 && tiles * S >= 1024) || (nst + S - 1) / S <= 2 ? 2 : 4;
     if ((TYPE == T_Q8_0 || TYPE == T_IQ4_NL) && S == 2 && (nst + 1) / 2 >= 32) R = 8;
-    if (TYPE != T_Q6_K && S == 1 && tiles <= 1024 && nst >= 64) R = TYPE == T_Q4_0 || TYPE == T_IQ4_NL ? 16 : 8;
+    if (TYPE != T_Q6_K && S == 1 && tiles <= 1024 && nst >= 32)
+        R = (TYPE == T_Q4_0 || TYPE == T_IQ4_NL) && nst >= 64 ? 16 : 8;
     return MvShape{S, R, mv_tpw(S), mv_lds(TYPE, nb, mv_tpw(S), S)};
 }
 template <int TYPE, int ORDER = 0>
