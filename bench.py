@@ -154,7 +154,7 @@ def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
     """BASELINE configs 1 (Q8_0 4096^2 matvec), 3 (Q6_K LM head 128256 x 4096) and 5 (MoE, 128
     experts, top-8, hidden 2048, ff 768: batch 1 and 64 tokens), each timed like the kernels above,
     and the other weight types' decode lines (low-bit and float types at the gate shape, Q4_0 and
-    Q8_0 at the down shape).
+    Q8_0 at two long-row down shapes).
     Weight sets rotate where one copy would stay in the Infinity Cache."""
     if not enabled:
         return None
@@ -217,25 +217,27 @@ def other_configs(be, S, kernel_time, enabled: int) -> dict | None:
             t.free()
         be.dev_free(y)
     be.dev_free(x)
-    # two 32-value types at the down projection's shape 14336 -> 4096 (Q4_0 in its repacked
-    # order): long rows over few tiles, so the launches split each tile's steps over wavefronts
+    # two 32-value types over long rows (Q4_0 in its repacked order): the down projection
+    # 14336 -> 4096 (512 tiles: the launches split each tile's steps over wavefronts) and
+    # Llama-2-13B's down projection 13824 -> 5120 (640 tiles: unsplit, with deep rings)
     x = be.dev_alloc(4 * 14336)
     be.h2d(x, S.activations(14336, 150))
-    for name, ty in (("q4_0", S.T_Q4_0), ("q8_0", S.T_Q8_0)):
-        wb = 4096 * S.row_bytes(ty, 14336)
-        n = copies_for(wb)
-        w = S.weights(ty, 4096, 14336, 150 + ty)
-        ts = [be.upload(ty, 14336, w) for _ in range(n)]
-        del w
-        y = be.dev_alloc(4 * 4096)
-        us = kernel_time(lambda i: be.matvec_dev(ts[i % n], x, y), 100)
-        nbytes = wb + 4 * (4096 + 14336)
-        out[f"long_rows_{name}_down_matvec"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
-                                                 "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes,
-                                                 "copies": n}
-        for t in ts:
-            t.free()
-        be.dev_free(y)
+    for tag, rows, cols in (("down", 4096, 14336), ("13b_down", 5120, 13824)):
+        for name, ty in (("q4_0", S.T_Q4_0), ("q8_0", S.T_Q8_0)):
+            wb = rows * S.row_bytes(ty, cols)
+            n = copies_for(wb)
+            w = S.weights(ty, rows, cols, 150 + ty)
+            ts = [be.upload(ty, cols, w) for _ in range(n)]
+            del w
+            y = be.dev_alloc(4 * rows)
+            us = kernel_time(lambda i: be.matvec_dev(ts[i % n], x, y), 100)
+            nbytes = wb + 4 * (rows + cols)
+            out[f"long_rows_{name}_{tag}_matvec"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                                                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                                                     "bytes": nbytes, "copies": n}
+            for t in ts:
+                t.free()
+            be.dev_free(y)
     be.dev_free(x)
     # config 5: MoE FFN, 2 expert sets (531 MB)
     E, K, D, F = 128, 8, 2048, 768
