@@ -230,3 +230,29 @@ def test_split_launches_graph_replays(backend, oracle):
         backend.dev_free(p)
     for tt in ts:
         tt.free()
+
+
+DEEP = [(S.T_Q4_0, ORDER_REPACKED), (S.T_Q4_0, ORDER_ROW), (S.T_Q8_0, ORDER_ROW), (S.T_Q4_1, ORDER_ROW),
+        (S.T_Q5_0, ORDER_ROW), (S.T_Q5_1, ORDER_ROW), (S.T_IQ4_NL, ORDER_ROW)]
+
+
+@pytest.mark.parametrize("fam", DEEP, ids=family_id)
+@pytest.mark.parametrize("rows,nb", [(5123, 451), (6401, 161)])
+def test_deep_ring_unsplit_ragged(backend, oracle, fam, rows, nb):
+    """Unsplit launches with rings of 8 or 16 steps (at most 1024 tiles over rows of 32 steps or
+    more) on ragged shapes: a partly filled last tile (rows % 8 != 0) and a last step of 3 or 1
+    blocks, bit for bit against the oracle. 6401 rows are 801 tiles, which the types with 2-way
+    splits up to 1536 tiles (Q4_0, Q5_0, IQ4_NL) split instead."""
+    t, order = fam
+    cols, tiles = nb * 32, (rows + 7) // 8
+    shape = backend.matvec_shape(t, order, cols, tiles)
+    print(f"{S.TYPE_NAME[t]} order {order} {rows}x{cols} shape {shape}", flush=True)
+    nib = t in (S.T_Q4_0, S.T_Q5_0, S.T_IQ4_NL)
+    if rows == 5123 or not nib:
+        assert shape[0] == 1 and shape[1] in (8, 16), shape
+    w = S.random_bytes_weights(t, rows, cols, rows + nb + t)
+    x = S.activations(cols, rows + 3)
+    tt = backend.upload(t, cols, w, order=order)
+    o_order = O_RP if order == ORDER_REPACKED else O_ROW
+    assert bits_equal(backend.matvec(tt, x), oracle.matvec(t, w, cols, x, o_order))
+    tt.free()
