@@ -256,3 +256,23 @@ def test_deep_ring_unsplit_ragged(backend, oracle, fam, rows, nb):
     o_order = O_RP if order == ORDER_REPACKED else O_ROW
     assert bits_equal(backend.matvec(tt, x), oracle.matvec(t, w, cols, x, o_order))
     tt.free()
+
+
+@pytest.mark.parametrize("fam", [(S.T_Q8_0, ORDER_ROW), (S.T_Q4_1, ORDER_ROW), (S.T_Q5_1, ORDER_ROW)], ids=family_id)
+def test_deep_ring_per_token_matmul(backend, oracle, fam):
+    """The per-token matmul (3 tokens: the decode kernel with grid.y = tokens) over 256 tiles of
+    rows of 33 steps: 768 tile-token launches, unsplit with a ring of 8, each token's row bit for
+    bit against the oracle."""
+    t, order = fam
+    rows, cols, nt = 2048, 32 * 131, 3
+    shape = backend.matvec_shape(t, order, cols, rows // 8, nt)
+    print(f"{S.TYPE_NAME[t]} {rows}x{cols} x {nt} tokens shape {shape}", flush=True)
+    assert shape[:2] == (1, 8), shape
+    w = S.random_bytes_weights(t, rows, cols, 77 + t)
+    X = S.activations(cols, 78 + t, rows=nt)
+    tt = backend.upload(t, cols, w, order=order)
+    Y = backend.matmul(tt, X)
+    Yo = oracle.matmul(t, w, cols, X, O_ROW)
+    for b in range(nt):
+        assert bits_equal(Y[b], Yo[b]), f"token {b}"
+    tt.free()
